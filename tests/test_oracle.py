@@ -1,0 +1,366 @@
+"""Pins of the CPU oracle (no GPU).
+
+Each test checks an oracle function against something other than its own
+formula: a brute force, a closed form, a special case that reduces to a
+textbook routine, a loop-form restatement of the reference's naive kernel
+references, or finite differences (torch.autograd.gradcheck in float64).
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import oracle as O
+
+
+@pytest.fixture(autouse=True)
+def _float64_default():
+    old = torch.get_default_dtype()
+    torch.set_default_dtype(torch.float64)
+    yield
+    torch.set_default_dtype(old)
+
+
+def _rng(seed):
+    g = torch.Generator().manual_seed(seed)
+    return g
+
+
+# ---------------------------------------------------------------- top-k / router
+
+def test_topk_tie_rule_matches_bruteforce():
+    g = _rng(0)
+    x = torch.randint(0, 7, (9, 50), generator=g).double()   # many ties
+    _, idx = O.topk_desc(x, 13)
+    ref = O.topk_desc_numpy(x.numpy(), 13)
+    assert np.array_equal(idx.numpy(), ref)
+
+
+def test_route_sequence_logits_equals_probs_when_distinct():
+    g = _rng(1)
+    logits = torch.randn(6, 97, generator=g, dtype=torch.float32)
+    for S in (0, 1, 3):
+        i1, w1, p1 = O.route_sequence(logits, 8, S, select_by="logits")
+        i2, w2, p2 = O.route_sequence(logits, 8, S, select_by="probs")
+        assert torch.equal(i1, i2)
+        assert torch.equal(w1, w2)
+        # agrees with torch.topk where there are no ties
+        p = p1.clone()
+        if S:
+            p[:, :S] = 0
+            p = p / p.sum(-1, keepdim=True)
+        assert torch.equal(torch.topk(p, 8, dim=-1).indices, i1)
+
+
+def test_route_sequence_invariants():
+    g = _rng(2)
+    logits = torch.randn(5, 33, generator=g)
+    idx, w, probs = O.route_sequence(logits, 4, 1)
+    assert torch.allclose(w.sum(-1), torch.ones(5))
+    assert (idx >= 1).all() and (idx < 33).all()
+    sel = torch.gather(probs, -1, idx)
+    assert (sel[:, :-1] >= sel[:, 1:]).all()
+    # k = C - S selects every routed chapter
+    idx_all, w_all, _ = O.route_sequence(logits, 32, 1)
+    assert torch.equal(idx_all.sort(-1).values, torch.arange(1, 33).expand(5, -1))
+    # the weights are a softmax over the selected logits (D1 cancels)
+    assert torch.allclose(w, F.softmax(torch.gather(logits, -1, idx), dim=-1))
+
+
+def test_route_token_level_matches_sequence_per_row():
+    g = _rng(3)
+    logits = torch.randn(2, 5, 40, generator=g)
+    idx, w, _ = O.route_token_level(logits, 6, 2)
+    i2, w2, _ = O.route_sequence(logits.reshape(10, 40), 6, 2)
+    assert torch.equal(idx.reshape(10, 6), i2)
+    assert torch.allclose(w.reshape(10, 6), w2)
+
+
+def test_prepend_closed_form():
+    idx = torch.tensor([[5, 9, 2, 7]])
+    w = torch.tensor([[0.4, 0.3, 0.2, 0.1]])
+    ci, cw = O.prepend_shared_chapters(idx, w, num_chapters=33, num_shared_chapters=1,
+                                       routed_scaling_factor=2.5)
+    assert ci.tolist() == [[0, 5, 9, 2, 7]]
+    assert abs(float(cw[0, 0]) - 1.0 / 3.5) < 1e-15
+    assert torch.allclose(cw[0, 1:], 2.5 * w[0] / 3.5)
+
+
+def test_rolling_pool_coefficients_and_special_cases():
+    g = _rng(4)
+    h = torch.randn(3, 11, 5, generator=g)
+    for w in (1, 3, 4, 11, 50):
+        direct = torch.stack([torch.stack([h[b, max(0, t - w + 1):t + 1].mean(0) for t in range(11)]).mean(0)
+                              for b in range(3)])
+        got = O.sequence_pool(h, "sequence-rolling", w)
+        c = O.rolling_pool_coefficients(11, w)
+        assert torch.allclose(got, direct)
+        assert torch.allclose(torch.einsum("l,bld->bd", c, h), direct)
+        assert abs(float(c.sum()) - 1.0) < 1e-12
+    assert torch.allclose(O.sequence_pool(h, "sequence-rolling", 1), h.mean(1))
+    assert torch.allclose(O.sequence_pool(h, "sequence-rolling", 11), O.sequence_pool(h, "sequence-rolling", None))
+
+
+def test_router_losses_closed_forms():
+    C, R, k = 16, 4, 3
+    logits = torch.zeros(R, C)
+    probs = F.softmax(logits, -1)
+    idx = torch.arange(k).expand(R, -1)
+    L = O.router_losses(logits, probs, idx, C)
+    assert abs(float(L["load_balance"]) - k) < 1e-12          # C * sum f * (1/C)
+    assert abs(float(L["z_loss"]) - math.log(C) ** 2) < 1e-12
+    assert abs(float(L["entropy"]) - math.log(C)) < 1e-12
+    assert abs(float(L["auxiliary"]) - (1.0 / C ** 2 - 1.0 / C) ** 2) < 1e-15
+    tot = O.compute_total_router_loss(L, 0.01, 0.0, 0.001)
+    assert abs(float(tot) - (0.01 * k + 0.001 * math.log(C) ** 2)) < 1e-12
+
+
+def test_select_from_probs_equals_route():
+    g = _rng(5)
+    logits = torch.randn(4, 21, generator=g)
+    probs = F.softmax(logits, -1)
+    i1, w1 = O.select_routed_chapters_from_probs(probs, 5, 1)
+    i2, w2, _ = O.route_sequence(logits, 5, 1, select_by="probs")
+    assert torch.equal(i1, i2) and torch.allclose(w1, w2)
+
+
+# ---------------------------------------------------------------- gather / normalise
+
+def test_gather_index_arithmetic():
+    g = _rng(6)
+    bank = torch.randn(7 * 4, 3, generator=g)
+    idx = torch.tensor([[2, 0, 6], [5, 5, 1]])
+    mem, flat = O.gather_chapters(bank, idx, 4)
+    for b in range(2):
+        for s in range(3):
+            for j in range(4):
+                row = int(idx[b, s]) * 4 + j
+                assert int(flat[b, s * 4 + j]) == row
+                assert torch.equal(mem[b, s * 4 + j], bank[row])
+
+
+def test_normalize_noop_cases_and_rms():
+    g = _rng(7)
+    mem = torch.randn(2, 12, 8, generator=g)
+    assert torch.equal(O.normalize_shared_routed(mem, num_shared_chapters=0, tokens_per_chapter=4,
+                                                 norm_type="rms", eps=1e-6), mem)
+    assert torch.equal(O.normalize_shared_routed(mem, num_shared_chapters=3, tokens_per_chapter=4,
+                                                 norm_type="rms", eps=1e-6), mem)
+    out = O.normalize_shared_routed(mem, num_shared_chapters=1, tokens_per_chapter=4,
+                                    norm_type="rms", eps=0.0)
+    assert torch.allclose(out.pow(2).mean(-1), torch.ones(2, 12))
+    ln = O.normalize_shared_routed(mem, num_shared_chapters=1, tokens_per_chapter=4,
+                                   norm_type="layernorm", eps=0.0)
+    assert torch.allclose(ln.mean(-1), torch.zeros(2, 12), atol=1e-12)
+
+
+# ---------------------------------------------------------------- attention
+
+def _weights(g, d, H, HK, dh=None):
+    dh = dh or d // H
+    Wq = torch.randn(H * dh, d, generator=g) * 0.1
+    Wk = torch.randn(HK * dh, d, generator=g) * 0.1
+    Wv = torch.randn(HK * dh, d, generator=g) * 0.1
+    Wo = torch.randn(d, H * dh, generator=g) * 0.1
+    return Wq, Wk, Wv, Wo
+
+
+def test_cross_attention_vs_explicit_loops():
+    g = _rng(8)
+    B, L, N, d, H, HK = 2, 3, 5, 8, 4, 2
+    h = torch.randn(B, L, d, generator=g)
+    mem = torch.randn(B, N, d, generator=g)
+    Wq, Wk, Wv, Wo = _weights(g, d, H, HK)
+    out = O.cross_attention(h, mem, Wq, Wk, Wv, Wo, H, HK)
+    dh = d // H
+    ref = torch.zeros(B, L, d)
+    for b in range(B):
+        heads = []
+        for hq in range(H):
+            hk = hq // (H // HK)
+            q = h[b] @ Wq[hq * dh:(hq + 1) * dh].T
+            k = mem[b] @ Wk[hk * dh:(hk + 1) * dh].T
+            v = mem[b] @ Wv[hk * dh:(hk + 1) * dh].T
+            s = q @ k.T / math.sqrt(dh)
+            e = torch.exp(s - s.max(-1, keepdim=True).values)
+            heads.append((e / e.sum(-1, keepdim=True)) @ v)
+        ref[b] = torch.cat(heads, -1) @ Wo.T
+    assert torch.allclose(out, ref, atol=1e-12)
+
+
+def _seq_setup(seed=9, B=2, L=6, d=16, H=2, HK=2, C=9, T=4):
+    g = _rng(seed)
+    h = torch.randn(B, L, d, generator=g)
+    bank = torch.randn(C * T, d, generator=g) * 0.5
+    Wr = torch.randn(C, d, generator=g) * 0.5
+    br = torch.zeros(C)
+    Wq, Wk, Wv, Wo = _weights(g, d, H, HK)
+    return h, bank, Wr, br, Wq, Wk, Wv, Wo
+
+
+@pytest.mark.parametrize("normalize", [False, True])
+def test_semantics_A_omega_in_attention_equivalence(normalize):
+    """(omega x) W = omega (x W): scaling logits and values by omega over
+    unweighted projections equals the reference chain that weights rows first."""
+    h, bank, Wr, br, Wq, Wk, Wv, Wo = _seq_setup()
+    H, HK, C, T, S, k, s = 2, 2, 9, 4, 1, 3, 2.5
+    out, det = O.sequence_memory_layer(h, bank, Wr, br, Wq, Wk, Wv, Wo, H=H, HK=HK, C=C, T=T,
+                                       S=S, top_k=k, routed_scale=s, normalize=normalize,
+                                       eps=1e-5, return_details=True)
+    B, L, d = h.shape
+    dh = d // H
+    X, _ = O.gather_chapters(bank, det["idx_star"], T)
+    if normalize:
+        X = O.rms_norm(X, 1e-5)
+    om = det["omega"].repeat_interleave(T, dim=1)          # (B, N)
+    q = (h @ Wq.T).view(B, L, H, dh)
+    kh = (X @ Wk.T).view(B, -1, HK, dh)
+    vh = (X @ Wv.T).view(B, -1, HK, dh)
+    sc = torch.einsum("blhd,bnhd->bhln", q, kh) * om[:, None, None, :] / math.sqrt(dh)
+    p = F.softmax(sc, -1)
+    a = torch.einsum("bhln,bnhd->blhd", p * om[:, None, None, :], vh).reshape(B, L, d)
+    assert torch.allclose(a @ Wo.T, out, atol=1e-12)
+
+
+def test_semantics_A_all_chapters_equal_weight_is_dense():
+    h, bank, Wr, br, Wq, Wk, Wv, Wo = _seq_setup(C=5)
+    # S=0, k=C, router weights forced equal -> omega = 1/C for every chapter
+    C, T = 5, 4
+    idx = torch.arange(C).expand(2, -1)
+    w = torch.full((2, C), 1.0 / C)
+    mem, _ = O.gather_chapters(bank, idx, T)
+    mem = O.weight_memory(mem, w, T)
+    out = O.cross_attention(h, mem, Wq, Wk, Wv, Wo, 2, 2)
+    dense = O.cross_attention(h, bank / C, Wq, Wk, Wv, Wo, 2, 2)
+    assert torch.allclose(out, dense, atol=1e-12)
+
+
+def test_sequence_layer_gradcheck():
+    """Finite differences pin the autograd of the whole routed layer (selection fixed)."""
+    h, bank, Wr, br, Wq, Wk, Wv, Wo = _seq_setup(seed=10, B=2, L=3, d=8, H=2, HK=1, C=6, T=2)
+    args = [t.clone().requires_grad_(True) for t in (h, bank, Wr, br, Wq, Wk, Wv, Wo)]
+
+    def f(*a):
+        return O.sequence_memory_layer(*a, H=2, HK=1, C=6, T=2, S=1, top_k=2, routed_scale=2.5,
+                                       normalize=True, eps=1e-5)
+    assert torch.autograd.gradcheck(f, args, eps=1e-6, atol=1e-7)
+
+
+def test_router_weight_grad_closed_form():
+    """d(logits) of omega(logits) equals the restricted softmax Jacobian."""
+    g = _rng(11)
+    R, C, S, k, s = 3, 12, 1, 4, 2.5
+    z = torch.randn(R, C, generator=g, requires_grad=True)
+    idx, w, _ = O.route_sequence(z, k, S)
+    _, om = O.prepend_shared_chapters(idx, w, num_chapters=C, num_shared_chapters=S,
+                                      routed_scaling_factor=s)
+    gom = torch.randn(R, S + k, generator=g)
+    (om * gom).sum().backward()
+    gw = gom[:, S:] * s / (S + s)
+    what = w.detach()
+    dz = torch.zeros(R, C)
+    dz.scatter_(1, idx, what * (gw - (what * gw).sum(-1, keepdim=True)))
+    assert torch.allclose(z.grad, dz, atol=1e-12)
+
+
+# ---------------------------------------------------------------- token-level kernels
+
+def _sparse_inputs(seed, B=1, TQ=5, HQ=4, HK=2, D=8, M=6, BS=4, S=3):
+    g = _rng(seed)
+    q = torch.randn(B, TQ, HQ, D, generator=g)
+    k = torch.randn(B, M * BS, HK, D, generator=g)
+    v = torch.randn(B, M * BS, HK, D, generator=g)
+    idx = torch.stack([torch.stack([torch.randperm(M, generator=g)[:S] for _ in range(HK)])
+                       for _ in range(B * TQ)]).view(B, TQ, HK, S)
+    w = torch.rand(B, TQ, S, generator=g)
+    w = w / w.sum(-1, keepdim=True)
+    return q, k, v, idx, w, BS
+
+
+def test_sparse_weighted_vs_naive_loop():
+    q, k, v, idx, w, BS = _sparse_inputs(12)
+    sc = 0.3
+    assert torch.allclose(O.sparse_attention_weighted(q, k, v, idx, w, BS, sc),
+                          O.naive_reference_weighted(q, k, v, idx, w, BS, sc), atol=1e-12)
+
+
+def test_sparse_unweighted_vs_naive_loop():
+    q, k, v, idx, w, BS = _sparse_inputs(13)
+    assert torch.allclose(O.sparse_attention_unweighted(q, k, v, idx, BS, 0.3),
+                          O.naive_reference_unweighted(q, k, v, idx, BS, 0.3), atol=1e-12)
+
+
+def test_sparse_joint_bias_vs_naive_and_equal_weight_case():
+    q, k, v, idx, w, BS = _sparse_inputs(14)
+    assert torch.allclose(O.sparse_attention_joint_bias(q, k, v, idx, w, BS, 0.3),
+                          O.naive_reference_weighted_joint_bias(q, k, v, idx, w, BS, 0.3), atol=1e-12)
+    eq = torch.full_like(w, 1.0 / w.shape[-1])
+    assert torch.allclose(O.sparse_attention_joint_bias(q, k, v, idx, eq, BS, 0.3),
+                          O.sparse_attention_unweighted(q, k, v, idx, BS, 0.3), atol=1e-12)
+
+
+def test_sparse_block_weighted_vs_loop_and_ones():
+    q, k, v, idx, w, BS = _sparse_inputs(15)
+    g = _rng(16)
+    bw = torch.rand(idx.shape, generator=g)
+    assert torch.allclose(O.sparse_attention_block_weighted(q, k, v, idx, bw, BS, 0.3),
+                          O.naive_reference_block_weighted(q, k, v, idx, bw, BS, 0.3), atol=1e-12)
+    assert torch.allclose(O.sparse_attention_block_weighted(q, k, v, idx, torch.ones_like(bw), BS, 0.3),
+                          O.sparse_attention_unweighted(q, k, v, idx, BS, 0.3), atol=1e-12)
+
+
+def test_weighted_single_chapter_is_plain_attention():
+    q, k, v, idx, w, BS = _sparse_inputs(17, S=1)
+    out = O.sparse_attention_weighted(q, k, v, idx, torch.ones_like(w), BS, 0.125)
+    ref = torch.zeros_like(out)
+    for t in range(q.shape[1]):
+        for hq in range(q.shape[2]):
+            hk = hq // 2
+            c0 = int(idx[0, t, hk, 0]) * BS
+            kk, vv = k[0, c0:c0 + BS, hk], v[0, c0:c0 + BS, hk]
+            p = F.softmax(q[0, t, hq] @ kk.T * 0.125, -1)
+            ref[0, t, hq] = p @ vv
+    assert torch.allclose(out, ref, atol=1e-12)
+
+
+def test_token_layer_shared_branch_is_dense_attention():
+    g = _rng(18)
+    B, L, d, H, C, T = 1, 4, 8, 2, 5, 4
+    h = torch.randn(B, L, d, generator=g)
+    bank = torch.randn(C * T, d, generator=g)
+    Wq, Wk, Wv, Wo = _weights(g, d, H, H)
+    pre = O.token_routed_preproj(h, bank[:T], None, torch.zeros(B, L, 0, dtype=torch.long), None,
+                                 T, 2.5, Wq, Wk, Wv, H, H)
+    dense = O.cross_attention(h, bank[:T], Wq, Wk, Wv, None, H, H, return_preproj=True)
+    assert torch.allclose(pre, dense, atol=1e-12)
+
+
+def test_token_layer_gradcheck():
+    g = _rng(19)
+    B, L, d, H, C, T = 1, 3, 8, 2, 5, 2
+    args = [torch.randn(B, L, d, generator=g), torch.randn(C * T, d, generator=g),
+            torch.randn(C, d, generator=g), torch.zeros(C)] + list(_weights(g, d, H, H))
+    args = [a.requires_grad_(True) for a in args]
+
+    def f(*a):
+        return O.token_memory_layer(*a, H=H, HK=H, C=C, T=T, S=1, top_k=2, routed_scale=2.5)
+    assert torch.autograd.gradcheck(f, args, eps=1e-6, atol=1e-7)
+
+
+def test_decode_is_L1_sequence_layer():
+    h, bank, Wr, br, Wq, Wk, Wv, Wo = _seq_setup(seed=20, L=1)
+    out, det = O.sequence_memory_layer(h, bank, Wr, br, Wq, Wk, Wv, Wo, H=2, HK=2, C=9, T=4, S=1,
+                                       top_k=3, routed_scale=2.5, return_details=True)
+    dec = O.decode_step(h, bank, det["idx_star"], det["omega"], Wq, Wk, Wv, Wo, H=2, HK=2, T=4)
+    assert torch.allclose(out, dec, atol=1e-12)
+
+
+def test_moe_with_routing_single_chapter_equals_cross_attention():
+    h, bank, Wr, br, Wq, Wk, Wv, Wo = _seq_setup(seed=21)
+    idx = torch.tensor([[3], [7]])
+    out = O.moe_with_routing(h, bank, idx, torch.ones(2, 1), 4, Wq, Wk, Wv, Wo, 2, 2)
+    mem, _ = O.gather_chapters(bank, idx, 4)
+    assert torch.allclose(out, O.cross_attention(h, mem, Wq, Wk, Wv, Wo, 2, 2), atol=1e-12)
