@@ -1,0 +1,139 @@
+/*
+ * libmoc -- MI355X (gfx950) Mixture-of-Chapters memory cross-attention.
+ *
+ * C ABI: plain pointers, int64 sizes and a HIP stream.  Every pointer argument
+ * is DEVICE memory unless stated otherwise.  Entry points never allocate,
+ * never synchronise the host, and launch asynchronously on `stream`.  They
+ * return MOC_OK (0) or an error code; moc_last_error() returns the message of
+ * the last failure on the calling thread.  Shape/argument errors are reported
+ * before anything is launched.
+ *
+ * Citations name the reference interface each entry point replaces
+ * (paths relative to the Tasmay-Tibrewal/Memory repository root).
+ *
+ * Layouts used below:
+ *   chapter-head tiles  K[u][hk][t][dh], V[u][hk][t][dh]   (u = de-duplicated chapter,
+ *                        t < T tokens of the chapter, dh < Dh); every (u, hk) block is
+ *                        contiguous.
+ *   edge                 e = row * NS + slot of a (rows, NS) chapter-selection matrix.
+ */
+#ifndef MOC_H
+#define MOC_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* hipStream_t;
+
+#define MOC_ABI_VERSION 1
+
+/* status codes */
+#define MOC_OK 0
+#define MOC_ERR_ARG 1         /* bad pointer / shape / value (Python: ValueError) */
+#define MOC_ERR_UNSUPPORTED 2 /* valid but not implemented for this shape/dtype  */
+#define MOC_ERR_LAUNCH 3      /* HIP runtime error                               */
+
+/* element types */
+#define MOC_F32 0
+#define MOC_BF16 1
+
+/* row normalisation of gathered bank rows */
+#define MOC_NORM_NONE 0
+#define MOC_NORM_RMS 1
+#define MOC_NORM_LAYERNORM 2
+
+const char* moc_last_error(void);
+int moc_abi_version(void);
+
+/* ------------------------------------------------------------------ router */
+
+/* Replaces the top-k block of ChapterRouter.forward (memory_transformer/router.py:114-149)
+ * and of route_token_level (router.py:293-329): p = softmax(logits); when S > 0 the first S
+ * chapters are zeroed and p renormalised; the k largest are selected (order: logit
+ * descending, equal logits by ascending chapter id) and their weights renormalised.
+ * logits f32 [R, C]; idx i32 [R, k] (global chapter ids); w f32 [R, k];
+ * probs f32 [R, C] (optional, NULL to skip) receives softmax(logits).  k <= 1024. */
+int moc_router_topk(const float* logits, int64_t R, int64_t C, int S, int k, int32_t* idx, float* w,
+                    float* probs, hipStream_t stream);
+
+/* Gradient of the chain above w.r.t. logits, given dw = dL/dw (f32 [R, k]).
+ * Writes every element of dlogits f32 [R, C].  Same clamp_min(1e-12) gating as autograd. */
+int moc_router_topk_bwd(const float* logits, const int32_t* idx, const float* dw, int64_t R, int64_t C, int S,
+                        int k, float* dlogits, hipStream_t stream);
+
+/* Replaces MemoryTransformer._prepend_shared_chapters (memory_transformer/model.py:356-391):
+ * idx_star = [0..S-1, idx], omega = [1 (S times), scale * w] / sum.  S > 0.
+ * idx i32 [R, k], w f32 [R, k] -> idx_star i32 [R, S+k], omega f32 [R, S+k]. */
+int moc_prepend_shared(const int32_t* idx, const float* w, int64_t R, int k, int S, float scale, int32_t* idx_star,
+                       float* omega, hipStream_t stream);
+/* dw f32 [R, k] = d omega / d w applied to domega f32 [R, S+k] (overwrites dw). */
+int moc_prepend_shared_bwd(const float* w, const float* domega, int64_t R, int k, int S, float scale, float* dw,
+                           hipStream_t stream);
+
+/* Replaces the pooling of ChapterRouter.forward (router.py:96-107 mean; :158-195 rolling
+ * mean given as per-position coefficients coef f32 [L], NULL = mean).
+ * h [B, L, d] of dtype; pooled f32 [B, d]; workspace from moc_router_pool_workspace. */
+size_t moc_router_pool_workspace(int64_t B, int64_t L, int64_t d);
+int moc_router_pool(const void* h, int dtype, int64_t B, int64_t L, int64_t d, const float* coef, float* pooled,
+                    void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* Replaces ChapterRouter.router (nn.Linear(d, C, bias=True), router.py:64) for few rows:
+ * logits f32 [R, C] = x f32 [R, d] . W[C, d]^T + bias f32 [C] (bias may be NULL). */
+int moc_router_linear(const float* x, int64_t R, int64_t d, const void* W, int w_dtype, const float* bias, int64_t C,
+                      float* logits, hipStream_t stream);
+/* Backward of moc_router_linear: dx f32 [R, d], dW f32 [C, d], db f32 [C]; any may be NULL. */
+size_t moc_router_linear_bwd_workspace(int64_t R, int64_t d, int64_t C);
+int moc_router_linear_bwd(const float* dz, const float* x, int64_t R, int64_t d, const void* W, int w_dtype,
+                          int64_t C, float* dx, float* dW, float* db, void* workspace, size_t workspace_bytes,
+                          hipStream_t stream);
+
+/* ------------------------------------------------------------- chapter plan */
+
+/* De-duplicates the chapters of E edges and builds the chapter -> edges inverted index
+ * (a stable counting sort; the reference builds it with argsort + searchsorted,
+ * kernels-final/kernel_v4.py:213-257).  chap i32 [E] in [0, C) (others are skipped).
+ * uniq i32 [min(E, C)], n_uniq i32 [2] = {distinct chapters, skipped edges},
+ * edge_u i32 [E] (-1 for skipped), csr_off i32 [min(E, C) + 1], csr_edge i32 [E].
+ * C <= 16384. */
+size_t moc_chapter_plan_workspace(int64_t E, int64_t C);
+int moc_chapter_plan(const int32_t* chap, int64_t E, int64_t C, void* workspace, size_t workspace_bytes,
+                     int32_t* uniq, int32_t* n_uniq, int32_t* edge_u, int32_t* csr_off, int32_t* csr_edge,
+                     hipStream_t stream);
+
+/* --------------------------------------------------- gather + K/V projection */
+
+/* Per-row statistics of the gathered rows for MemoryTransformer._normalize_shared_routed_memory_vectors
+ * (memory_transformer/model.py:393-432): mean f32 and rstd f32 [max_u * T]. */
+int moc_row_stats(const void* bank, int bank_dtype, int64_t d, int T, const int32_t* uniq, const int32_t* n_uniq,
+                  int64_t max_u, int norm, float eps, float* mean, float* rstd, hipStream_t stream);
+
+/* Replaces ChapteredMemoryBank.get_chapters_batched (memory_transformer/memory_bank.py:244-293)
+ * followed by k_proj/v_proj of MemoryCrossAttention._compute_qkv (memory_attention.py:241-243),
+ * computed once per distinct chapter.  bank [N_m, d] (bf16 or f32), wkv [2*HK*Dh, d] of dtype
+ * (= [Wk; Wv]); row_mean/row_rstd from moc_row_stats or both NULL.  Outputs chapter-head
+ * tiles k_tiles, v_tiles [max_u][HK][T][Dh] of dtype.  d % 64 == 0, (2*HK*Dh) % 128 == 0. */
+int moc_kv_project(int dtype, const void* bank, int bank_dtype, int64_t d, int T, const int32_t* uniq,
+                   const int32_t* n_uniq, int64_t max_u, const float* row_mean, const float* row_rstd,
+                   const void* wkv, int HK, int Dh, void* k_tiles, void* v_tiles, hipStream_t stream);
+
+/* ------------------------------------------------- routed attention forward */
+
+/* Replaces MemoryCrossAttention._attention on omega-weighted gathered memory
+ * (memory_transformer/model.py:689-692 + memory_attention.py:458-478, :269-318) for the
+ * sequence-level path: one joint softmax over the NS selected chapters of each sequence,
+ * with omega scaling both logits and values.  q [B, L, H, Dh]; slot_u i32 [B, NS] (the
+ * plan's edge_u); omega f32 [B, NS]; out [B, L, H, Dh]; lse f32 [B, H, L] (log2 domain,
+ * consumed by the backward).  Dh == 64, T == 64. */
+int moc_xattn_fwd(int dtype, const void* q, const void* k_tiles, const void* v_tiles, const int32_t* slot_u,
+                  const float* omega, int64_t B, int64_t L, int H, int HK, int Dh, int T, int NS, float scale,
+                  void* out, float* lse, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MOC_H */

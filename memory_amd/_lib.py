@@ -1,0 +1,120 @@
+"""ctypes binding of libmoc.so (the C ABI declared in include/moc.h).
+
+There is no CPU or PyTorch fallback: every op of this package runs the HIP
+kernels of libmoc.so on a ROCm device and raises if the library is missing or
+a tensor is not on the GPU.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+import threading
+
+import torch
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "_lib", "libmoc.so")
+HEADER = os.path.join(os.path.dirname(HERE), "include", "moc.h")
+
+MOC_OK, MOC_ERR_ARG, MOC_ERR_UNSUPPORTED, MOC_ERR_LAUNCH = 0, 1, 2, 3
+MOC_F32, MOC_BF16 = 0, 1
+MOC_NORM_NONE, MOC_NORM_RMS, MOC_NORM_LAYERNORM = 0, 1, 2
+
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_I = ctypes.c_int
+_F = ctypes.c_float
+_SZ = ctypes.c_size_t
+
+# name -> (restype, argtypes)
+_SIGS = {
+    "moc_last_error": (ctypes.c_char_p, []),
+    "moc_abi_version": (_I, []),
+    "moc_router_topk": (_I, [_P, _I64, _I64, _I, _I, _P, _P, _P, _P]),
+    "moc_router_topk_bwd": (_I, [_P, _P, _P, _I64, _I64, _I, _I, _P, _P]),
+    "moc_prepend_shared": (_I, [_P, _P, _I64, _I, _I, _F, _P, _P, _P]),
+    "moc_prepend_shared_bwd": (_I, [_P, _P, _I64, _I, _I, _F, _P, _P]),
+    "moc_router_pool_workspace": (_SZ, [_I64, _I64, _I64]),
+    "moc_router_pool": (_I, [_P, _I, _I64, _I64, _I64, _P, _P, _P, _SZ, _P]),
+    "moc_router_linear": (_I, [_P, _I64, _I64, _P, _I, _P, _I64, _P, _P]),
+    "moc_router_linear_bwd_workspace": (_SZ, [_I64, _I64, _I64]),
+    "moc_router_linear_bwd": (_I, [_P, _P, _I64, _I64, _P, _I, _I64, _P, _P, _P, _P, _SZ, _P]),
+    "moc_chapter_plan_workspace": (_SZ, [_I64, _I64]),
+    "moc_chapter_plan": (_I, [_P, _I64, _I64, _P, _SZ, _P, _P, _P, _P, _P, _P]),
+    "moc_row_stats": (_I, [_P, _I, _I64, _I, _P, _P, _I64, _I, _F, _P, _P, _P]),
+    "moc_kv_project": (_I, [_I, _P, _I, _I64, _I, _P, _P, _I64, _P, _P, _P, _I, _I, _P, _P, _P]),
+    "moc_xattn_fwd": (_I, [_I, _P, _P, _P, _P, _P, _I64, _I64, _I, _I, _I, _I, _I, _F, _P, _P, _P]),
+}
+
+_lib = None
+_lock = threading.Lock()
+
+
+class MocError(RuntimeError):
+    pass
+
+
+def declared_symbols(header: str = HEADER):
+    """Function names declared in include/moc.h."""
+    text = open(header).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(moc_[a-z0-9_]+)\s*\(", text)))
+
+
+def lib():
+    """Load libmoc.so (once).  Raises if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(LIB_PATH):
+                raise MocError(
+                    f"libmoc.so not found at {LIB_PATH}; build it with `python -m memory_amd.build` "
+                    "(memory_amd has no CPU fallback)")
+            l = ctypes.CDLL(LIB_PATH)
+            for name, (res, args) in _SIGS.items():
+                f = getattr(l, name)
+                f.restype = res
+                f.argtypes = args
+            _lib = l
+    return _lib
+
+
+def call(name: str, *args) -> None:
+    rc = getattr(lib(), name)(*args)
+    if rc != MOC_OK:
+        msg = lib().moc_last_error().decode(errors="replace")
+        if rc in (MOC_ERR_ARG, MOC_ERR_UNSUPPORTED):
+            raise ValueError(f"{name}: {msg}")
+        raise MocError(f"{name} failed ({rc}): {msg}")
+
+
+def query(name: str, *args):
+    return getattr(lib(), name)(*args)
+
+
+def stream_ptr(device: torch.device | None = None) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def ptr(t: torch.Tensor | None):
+    return None if t is None else t.data_ptr()
+
+
+def dtype_code(dt: torch.dtype) -> int:
+    if dt == torch.float32:
+        return MOC_F32
+    if dt == torch.bfloat16:
+        return MOC_BF16
+    raise ValueError(f"memory_amd kernels support float32 and bfloat16 tensors, got {dt}")
+
+
+def require_gpu(*tensors: torch.Tensor) -> None:
+    for t in tensors:
+        if t is not None and not t.is_cuda:
+            raise RuntimeError(
+                "memory_amd runs only on ROCm devices (HIP kernels of libmoc.so); got a tensor on "
+                f"{t.device}. There is no CPU fallback.")

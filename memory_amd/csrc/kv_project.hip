@@ -1,0 +1,275 @@
+// Chapter gather + K/V projection as one MFMA GEMM.
+//
+//   rows r = u * T + j of the de-duplicated chapter list (u < n_uniq, j < T)
+//   X[r, :]  = norm(bank[uniq[u] * T + j, :])        (gather + optional row norm)
+//   Y[r, n]  = sum_k X[r, k] * Wkv[n, k]              Wkv = [Wk; Wv], (2*HK*Dh, d)
+//
+// The output is written as "chapter-head tiles": K[u][hk][j][dh] and
+// V[u][hk][j][dh], i.e. every (chapter, kv head) pair is one contiguous T x Dh
+// block that the attention kernels stream straight into LDS.
+//
+// Reference: the gather is ChapteredMemoryBank.get_chapters_batched
+// (memory_transformer/memory_bank.py:263-293), the optional normalisation is
+// MemoryTransformer._normalize_shared_routed_memory_vectors
+// (memory_transformer/model.py:393-432, applied per row, so shared and routed
+// slices need no separate pass), and the projections are k_proj / v_proj of
+// MemoryCrossAttention._compute_qkv (memory_transformer/memory_attention.py:241-243).
+// The router weight omega (model.py:689-692) is NOT applied here: since
+// (omega * x) W^T = omega * (x W^T), it is applied per chapter inside attention,
+// which lets one projected chapter serve every sequence that selected it.
+#include "moc_common.h"
+
+namespace moc {
+
+// Per-row statistics for the normalisation prologue: mean (layernorm only) and
+// 1/sqrt(var + eps) (layernorm) or 1/sqrt(mean(x^2) + eps) (rms).
+template <typename TB>
+__global__ __launch_bounds__(256) void row_stats_kernel(const TB* __restrict__ bank, int64_t d, int Tc,
+                                                        const int32_t* __restrict__ uniq,
+                                                        const int32_t* __restrict__ n_uniq, int64_t max_u,
+                                                        int norm, float eps, float* __restrict__ mean,
+                                                        float* __restrict__ rstd) {
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int64_t nrows = (int64_t)min((int64_t)n_uniq[0], max_u) * Tc;
+  if (r >= nrows) return;
+  const int64_t src = (int64_t)uniq[r / Tc] * Tc + (r % Tc);
+  const TB* x = bank + src * d;
+  float s = 0.f, s2 = 0.f;
+  for (int64_t j = lane; j < d; j += 64) {
+    float v = to_f(x[j]);
+    s += v;
+    s2 += v * v;
+  }
+  s = wave_sum(s);
+  s2 = wave_sum(s2);
+  if (norm == MOC_NORM_LAYERNORM) {  // biased variance, two-pass, like F.layer_norm
+    const float mu = s / (float)d;
+    float q = 0.f;
+    for (int64_t j = lane; j < d; j += 64) {
+      float v = to_f(x[j]) - mu;
+      q += v * v;
+    }
+    q = wave_sum(q);
+    if (lane == 0) { mean[r] = mu; rstd[r] = rsqrtf(q / (float)d + eps); }
+  } else if (lane == 0) {
+    mean[r] = 0.f;
+    rstd[r] = rsqrtf(s2 / (float)d + eps);
+  }
+}
+
+// EPC consecutive elements of TB as floats (EPC = 16 bytes worth of T).
+template <typename T, typename TB> struct ChunkLoad;
+template <> struct ChunkLoad<bf16, bf16> {
+  static __device__ __forceinline__ void run(const bf16* p, float* o) {
+    bf16x8 v = *reinterpret_cast<const bf16x8*>(p);
+#pragma unroll
+    for (int x = 0; x < 8; ++x) o[x] = (float)v[x];
+  }
+};
+template <> struct ChunkLoad<bf16, float> {
+  static __device__ __forceinline__ void run(const float* p, float* o) {
+    f32x4 a = *reinterpret_cast<const f32x4*>(p), b = *reinterpret_cast<const f32x4*>(p + 4);
+#pragma unroll
+    for (int x = 0; x < 4; ++x) { o[x] = a[x]; o[4 + x] = b[x]; }
+  }
+};
+template <> struct ChunkLoad<float, float> {
+  static __device__ __forceinline__ void run(const float* p, float* o) {
+    f32x4 a = *reinterpret_cast<const f32x4*>(p);
+#pragma unroll
+    for (int x = 0; x < 4; ++x) o[x] = a[x];
+  }
+};
+
+constexpr int kGemmThreads = 256;
+
+// 128 x 128 output tile per workgroup, 4 waves in a 2 x 2 grid of 64 x 64.
+// The k-stage is 128 bytes of each row (64 bf16 / 32 fp32), double-buffered.
+template <typename T, typename TB>
+__global__ __launch_bounds__(kGemmThreads) void kv_project_kernel(
+    const TB* __restrict__ bank, int64_t d, int Tc, const int32_t* __restrict__ uniq,
+    const int32_t* __restrict__ n_uniq, int64_t max_u, const float* __restrict__ row_mean,
+    const float* __restrict__ row_rstd, const T* __restrict__ wkv, int HK, int Dh, T* __restrict__ kout,
+    T* __restrict__ vout) {
+  constexpr int BK = 128 / (int)sizeof(T);  // elements per 128-byte row slice
+  constexpr int EPC = 16 / (int)sizeof(T);  // elements per 16-byte chunk
+  constexpr int KSTEPS = BK / 32;
+  constexpr int TILE_BYTES = 128 * 128;
+  using Tile = SwzTile<T, BK>;
+  __shared__ __attribute__((aligned(16))) char lds[2][2][TILE_BYTES];
+
+  const int64_t nrows = (int64_t)min((int64_t)n_uniq[0], max_u) * Tc;
+  const int64_t m0 = (int64_t)blockIdx.x * 128;
+  if (m0 >= nrows) return;
+  const int n0 = blockIdx.y * 128;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int g = lane >> 4, c16 = lane & 15;
+
+  // Each thread moves 4 chunks of A and 4 chunks of B per stage (8 chunks per row).
+  const TB* a_src[4];
+  float a_mu[4], a_rs[4];
+  bool a_ok[4];
+  const T* b_src[4];
+  int a_row[4], a_cc[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int q = tid + kGemmThreads * i;
+    a_row[i] = q >> 3;
+    a_cc[i] = q & 7;
+    const int64_t r = m0 + a_row[i];
+    a_ok[i] = r < nrows;
+    const int64_t rr = a_ok[i] ? r : 0;
+    const int64_t src = (int64_t)uniq[rr / Tc] * Tc + (rr % Tc);
+    a_src[i] = bank + src * d + a_cc[i] * EPC;
+    a_mu[i] = row_rstd ? row_mean[rr] : 0.f;
+    a_rs[i] = row_rstd ? row_rstd[rr] : 1.f;
+    b_src[i] = wkv + (int64_t)(n0 + a_row[i]) * d + a_cc[i] * EPC;
+  }
+
+  typedef typename Frag<T>::type F8;
+  // Raw global data is held in registers across the MFMA loop and only
+  // converted / normalised when it is written to LDS (stash), so the loads
+  // of stage k+1 overlap the math of stage k.
+  constexpr int NV = (EPC * (int)sizeof(TB)) / 16;  // 16-byte loads per A chunk
+  V16 ra[4][NV], rb[4];
+  auto fetch = [&](int kt) {
+    const int64_t ko = (int64_t)kt * BK;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int x = 0; x < NV; ++x) ra[i][x] = ld16(a_src[i] + ko + x * (16 / (int)sizeof(TB)));
+      rb[i] = ld16(b_src[i] + ko);
+    }
+  };
+  auto stash = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float v[EPC];
+      ChunkLoad<T, TB>::run(reinterpret_cast<const TB*>(ra[i]), v);
+      if (row_rstd) {
+#pragma unroll
+        for (int x = 0; x < EPC; ++x) v[x] = (v[x] - a_mu[i]) * a_rs[i];
+      }
+      if (!a_ok[i]) {
+#pragma unroll
+        for (int x = 0; x < EPC; ++x) v[x] = 0.f;
+      }
+      T t[EPC];
+#pragma unroll
+      for (int x = 0; x < EPC; ++x) t[x] = from_f<T>(v[x]);
+      st16(&lds[buf][0][Tile::off(a_row[i], a_cc[i] * EPC)], *reinterpret_cast<V16*>(t));
+      st16(&lds[buf][1][Tile::off(a_row[i], a_cc[i] * EPC)], rb[i]);
+    }
+  };
+
+  f32x4 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int nk = (int)(d / BK);
+  fetch(0);
+  stash(0);
+  __syncthreads();
+  for (int kt = 0; kt < nk; ++kt) {
+    const int buf = kt & 1;
+    if (kt + 1 < nk) fetch(kt + 1);
+    const char* As = lds[buf][0];
+    const char* Bs = lds[buf][1];
+#pragma unroll
+    for (int ks = 0; ks < KSTEPS; ++ks) {
+      F8 a[4], b[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) a[i] = Tile::frag(As, wm * 64 + 16 * i + c16, ks * 32 + 8 * g);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) b[j] = Tile::frag(Bs, wn * 64 + 16 * j + c16, ks * 32 + 8 * g);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) mma(acc[i][j], a[i], b[j]);
+    }
+    if (kt + 1 < nk) stash(buf ^ 1);
+    __syncthreads();
+  }
+
+  // Epilogue: scatter into chapter-head tiles.
+  const int KV = HK * Dh;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int n = n0 + wn * 64 + 16 * j + c16;
+    const bool is_v = n >= KV;
+    const int nn = is_v ? n - KV : n;
+    const int hk = nn / Dh, dh = nn % Dh;
+    T* dst = is_v ? vout : kout;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int64_t r = m0 + wm * 64 + 16 * i + 4 * g + e;
+        if (r < nrows) {
+          const int64_t u = r / Tc, jj = r % Tc;
+          dst[((u * HK + hk) * Tc + jj) * Dh + dh] = from_f<T>(acc[i][j][e]);
+        }
+      }
+    }
+  }
+}
+
+}  // namespace moc
+
+using namespace moc;
+
+extern "C" {
+
+int moc_row_stats(const void* bank, int bank_dtype, int64_t d, int T, const int32_t* uniq, const int32_t* n_uniq,
+                  int64_t max_u, int norm, float eps, float* mean, float* rstd, hipStream_t stream) {
+  MOC_REQUIRE(bank && uniq && n_uniq && mean && rstd, MOC_ERR_ARG, "moc_row_stats: null pointer");
+  MOC_REQUIRE(norm == MOC_NORM_RMS || norm == MOC_NORM_LAYERNORM, MOC_ERR_ARG, "moc_row_stats: norm=%d", norm);
+  MOC_REQUIRE(d > 0 && T > 0 && max_u >= 0, MOC_ERR_ARG, "moc_row_stats: bad shape");
+  if (max_u == 0) return MOC_OK;
+  const int64_t rows = max_u * T;
+  dim3 grid((unsigned)((rows + 3) / 4));
+  if (bank_dtype == MOC_F32)
+    hipLaunchKernelGGL(row_stats_kernel<float>, grid, dim3(256), 0, stream, (const float*)bank, d, T, uniq, n_uniq, max_u,
+                       norm, eps, mean, rstd);
+  else if (bank_dtype == MOC_BF16)
+    hipLaunchKernelGGL(row_stats_kernel<bf16>, grid, dim3(256), 0, stream, (const bf16*)bank, d, T, uniq, n_uniq, max_u,
+                       norm, eps, mean, rstd);
+  else
+    return set_error(MOC_ERR_UNSUPPORTED, "moc_row_stats: dtype %d", bank_dtype);
+  return check_launch("row_stats_kernel");
+}
+
+int moc_kv_project(int dtype, const void* bank, int bank_dtype, int64_t d, int T, const int32_t* uniq,
+                   const int32_t* n_uniq, int64_t max_u, const float* row_mean, const float* row_rstd,
+                   const void* wkv, int HK, int Dh, void* k_tiles, void* v_tiles, hipStream_t stream) {
+  MOC_REQUIRE(bank && uniq && n_uniq && wkv && k_tiles && v_tiles, MOC_ERR_ARG, "moc_kv_project: null pointer");
+  MOC_REQUIRE((row_mean == nullptr) == (row_rstd == nullptr), MOC_ERR_ARG, "moc_kv_project: mean/rstd must be both set or both null");
+  MOC_REQUIRE(T > 0 && HK > 0 && Dh > 0 && max_u >= 0, MOC_ERR_ARG, "moc_kv_project: bad shape");
+  const int BK = dtype == MOC_BF16 ? 64 : 32;
+  MOC_REQUIRE(d % 64 == 0 && d >= BK, MOC_ERR_UNSUPPORTED, "moc_kv_project: memory_dim %lld must be a multiple of 64",
+              (long long)d);
+  MOC_REQUIRE((2 * HK * Dh) % 128 == 0, MOC_ERR_UNSUPPORTED, "moc_kv_project: 2*HK*Dh=%d must be a multiple of 128",
+              2 * HK * Dh);
+  if (max_u == 0) return MOC_OK;
+  const int64_t rows = max_u * T;
+  dim3 grid((unsigned)((rows + 127) / 128), (unsigned)(2 * HK * Dh / 128));
+  if (dtype == MOC_BF16 && bank_dtype == MOC_BF16)
+    hipLaunchKernelGGL((kv_project_kernel<bf16, bf16>), grid, dim3(kGemmThreads), 0, stream, (const bf16*)bank, d, T, uniq,
+                       n_uniq, max_u, row_mean, row_rstd, (const bf16*)wkv, HK, Dh, (bf16*)k_tiles, (bf16*)v_tiles);
+  else if (dtype == MOC_BF16 && bank_dtype == MOC_F32)
+    hipLaunchKernelGGL((kv_project_kernel<bf16, float>), grid, dim3(kGemmThreads), 0, stream, (const float*)bank, d, T, uniq,
+                       n_uniq, max_u, row_mean, row_rstd, (const bf16*)wkv, HK, Dh, (bf16*)k_tiles, (bf16*)v_tiles);
+  else if (dtype == MOC_F32 && bank_dtype == MOC_F32)
+    hipLaunchKernelGGL((kv_project_kernel<float, float>), grid, dim3(kGemmThreads), 0, stream, (const float*)bank, d, T,
+                       uniq, n_uniq, max_u, row_mean, row_rstd, (const float*)wkv, HK, Dh, (float*)k_tiles,
+                       (float*)v_tiles);
+  else
+    return set_error(MOC_ERR_UNSUPPORTED, "moc_kv_project: dtype %d with bank dtype %d", dtype, bank_dtype);
+  return check_launch("kv_project_kernel");
+}
+
+}  // extern "C"

@@ -1,0 +1,166 @@
+// Shared device/host helpers for libmoc (MI355X / gfx950 only).
+//
+// Conventions used by every kernel in this library:
+//  * Element types: T in {float, __bf16}.  All matrix products accumulate in
+//    fp32 on the matrix cores (v_mfma_f32_16x16x32_bf16 for bf16 operands,
+//    eight v_mfma_f32_16x16x4_f32 for fp32 operands).
+//  * A "fragment" is 8 consecutive reduction-dimension (k) elements held by
+//    one lane.  For the 16x16 MFMA tile, lane l holds row/column (l % 16) and
+//    k-group g = l / 16 of the 32-wide k step.  The order of k inside one MFMA
+//    reduction is free, so both operands only have to agree on it.
+//  * Accumulator layout (16x16 fp32 tile, 4 values per lane):
+//    lane l holds column n = l % 16 and rows m = 4 * (l / 16) + e, e = 0..3.
+//  * Entry points never allocate and never synchronise the host; they return
+//    a status code and keep a thread-local message for moc_last_error().
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+
+#include "../../include/moc.h"
+
+namespace moc {
+
+typedef __bf16 bf16;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x8 __attribute__((ext_vector_type(8)));
+
+// ----------------------------------------------------------------- errors (host)
+int set_error(int code, const char* fmt, ...);
+int check_launch(const char* what);
+
+#define MOC_REQUIRE(cond, code, ...)                                   \
+  do {                                                                 \
+    if (!(cond)) return ::moc::set_error((code), __VA_ARGS__);         \
+  } while (0)
+
+#define MOC_HIP(call)                                                  \
+  do {                                                                 \
+    hipError_t _e = (call);                                            \
+    if (_e != hipSuccess)                                              \
+      return ::moc::set_error(MOC_ERR_LAUNCH, "%s: %s", #call,         \
+                              hipGetErrorString(_e));                  \
+  } while (0)
+
+// ------------------------------------------------------------ element helpers
+template <typename T> struct Frag;
+template <> struct Frag<bf16> { typedef bf16x8 type; };
+template <> struct Frag<float> { typedef f32x8 type; };
+
+__device__ __forceinline__ float to_f(float x) { return x; }
+__device__ __forceinline__ float to_f(bf16 x) { return (float)x; }
+template <typename T> __device__ __forceinline__ T from_f(float x);
+template <> __device__ __forceinline__ float from_f<float>(float x) { return x; }
+template <> __device__ __forceinline__ bf16 from_f<bf16>(float x) { return (bf16)x; }
+
+// c += a * b over one 32-wide k step (see the header comment for layouts).
+__device__ __forceinline__ void mma(f32x4& c, const bf16x8& a, const bf16x8& b) {
+  c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ void mma(f32x4& c, const f32x8& a, const f32x8& b) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j) c = __builtin_amdgcn_mfma_f32_16x16x4f32(a[j], b[j], c, 0, 0, 0);
+}
+
+// 16-byte vector of raw bits.
+struct alignas(16) V16 { uint32_t w[4]; };
+
+__device__ __forceinline__ V16 ld16(const void* p) { return *reinterpret_cast<const V16*>(p); }
+__device__ __forceinline__ void st16(void* p, const V16& v) { *reinterpret_cast<V16*>(p) = v; }
+
+// Load 8 consecutive elements of type TI and return them as 8 elements of T.
+template <typename T, typename TI> struct Load8;
+template <typename T> struct Load8<T, T> {
+  static __device__ __forceinline__ typename Frag<T>::type run(const T* p) {
+    return *reinterpret_cast<const typename Frag<T>::type*>(p);
+  }
+};
+template <> struct Load8<bf16, float> {
+  static __device__ __forceinline__ bf16x8 run(const float* p) {
+    f32x8 v = *reinterpret_cast<const f32x8*>(p);
+    bf16x8 r;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) r[j] = (bf16)v[j];
+    return r;
+  }
+};
+
+template <typename T> __device__ __forceinline__ typename Frag<T>::type zero_frag() {
+  typename Frag<T>::type z;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) z[j] = from_f<T>(0.f);
+  return z;
+}
+
+// ------------------------------------------------------------- LDS tile views
+// A TILE is a square-ish block of ROWS x COLS elements of T stored row-major
+// with the 16-byte chunks of every row XOR-swizzled by (row & 7): a fragment
+// read (16 lanes, 16 consecutive rows, same column chunk) then touches 8
+// distinct chunk slots instead of one bank group.  Requires >= 8 chunks/row.
+template <typename T, int COLS>
+struct SwzTile {
+  static constexpr int kRowBytes = COLS * (int)sizeof(T);
+  static constexpr int kChunks = kRowBytes / 16;
+  static_assert(kChunks >= 8 && (kChunks & (kChunks - 1)) == 0, "row must be >= 8 pow2 chunks");
+  __device__ static __forceinline__ int off(int row, int col) {
+    int byte = col * (int)sizeof(T);
+    int chunk = byte >> 4;
+    return row * kRowBytes + (((chunk ^ (row & 7)) & (kChunks - 1)) << 4) + (byte & 15);
+  }
+  // 8 consecutive elements starting at (row, col), col multiple of 8/4 for bf16/f32 chunk sizes.
+  __device__ static __forceinline__ typename Frag<T>::type frag(const char* base, int row, int col) {
+    typename Frag<T>::type r;
+    if constexpr (sizeof(T) == 2) {
+      r = *reinterpret_cast<const bf16x8*>(base + off(row, col));
+    } else {
+      f32x4 lo = *reinterpret_cast<const f32x4*>(base + off(row, col));
+      f32x4 hi = *reinterpret_cast<const f32x4*>(base + off(row, col + 4));
+      r = f32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    }
+    return r;
+  }
+  // Two groups of 4 consecutive elements: (row, c0..c0+3) and (row, c1..c1+3).
+  __device__ static __forceinline__ typename Frag<T>::type frag44(const char* base, int row, int c0, int c1) {
+    typename Frag<T>::type r;
+    if constexpr (sizeof(T) == 2) {
+      bf16x4 a = *reinterpret_cast<const bf16x4*>(base + off(row, c0));
+      bf16x4 b = *reinterpret_cast<const bf16x4*>(base + off(row, c1));
+      r = bf16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+    } else {
+      f32x4 a = *reinterpret_cast<const f32x4*>(base + off(row, c0));
+      f32x4 b = *reinterpret_cast<const f32x4*>(base + off(row, c1));
+      r = f32x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+    }
+    return r;
+  }
+};
+
+// ------------------------------------------------------------ wave reductions
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+// Reduce over the 4 lanes {l, l^16, l^32, l^48} that share a 16x16 column.
+__device__ __forceinline__ float quad_max(float v) {
+  v = fmaxf(v, __shfl_xor(v, 16, 64));
+  v = fmaxf(v, __shfl_xor(v, 32, 64));
+  return v;
+}
+__device__ __forceinline__ float quad_sum(float v) {
+  v += __shfl_xor(v, 16, 64);
+  v += __shfl_xor(v, 32, 64);
+  return v;
+}
+
+inline int dtype_size(int dt) { return dt == MOC_F32 ? 4 : (dt == MOC_BF16 ? 2 : 0); }
+
+}  // namespace moc

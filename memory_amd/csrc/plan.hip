@@ -1,0 +1,159 @@
+// Chapter plan: de-duplicates the chapters selected across a batch and builds
+// the inverted index (chapter -> list of routing edges) that the
+// chapter-centric kernels walk.
+//
+// An "edge" is one (row, slot) pair of a selection matrix, encoded as
+// e = row * NS + slot.  Given chap[e] in [0, C):
+//   uniq[u]        sorted distinct chapter ids, u < n_uniq
+//   edge_u[e]      u such that uniq[u] == chap[e]
+//   csr_off[u]     first position of chapter uniq[u] in csr_edge (csr_off[n_uniq] =
+//                  number of valid edges)
+//   n_uniq[0..1]   number of distinct chapters, number of edges with an id
+//                  outside [0, C) (those edges get edge_u = -1 and are skipped,
+//                  as the reference kernels skip them: kernels-final/kernel_v4.py:353)
+//   csr_edge[p]    edges sorted by (chapter, e) -- a stable counting sort, so the
+//                  result (and every accumulation that walks it) is deterministic.
+// The reference's inverted index for the weighted kernel does the same with an
+// argsort on (b*H + h)*M + chapter (kernels-final/kernel_v4.py:213-257).
+#include "moc_common.h"
+
+namespace moc {
+
+constexpr int kPlanEdgesPerBlock = 1024;
+constexpr int kPlanMaxC = 16384;  // histogram lives in LDS (64 KB)
+
+// counts[g][c] for the edge range of block g.
+__global__ __launch_bounds__(256) void plan_hist_kernel(const int32_t* __restrict__ chap, int64_t E, int64_t C,
+                                                        int32_t* __restrict__ counts) {
+  extern __shared__ int32_t h[];
+  const int g = blockIdx.x;
+  for (int64_t c = threadIdx.x; c < C; c += 256) h[c] = 0;
+  __syncthreads();
+  const int64_t e0 = (int64_t)g * kPlanEdgesPerBlock;
+  const int64_t e1 = min(E, e0 + kPlanEdgesPerBlock);
+  for (int64_t e = e0 + threadIdx.x; e < e1; e += 256) {
+    int32_t c = chap[e];
+    if (c >= 0 && c < C) atomicAdd(&h[c], 1);  // out-of-range ids are dropped (counted below)
+  }
+  __syncthreads();
+  for (int64_t c = threadIdx.x; c < C; c += 256) counts[(int64_t)g * C + c] = h[c];
+}
+
+// Column prefix over blocks: counts[g][c] <- sum_{g' < g} counts[g'][c]; total[c] = sum.
+__global__ void plan_colscan_kernel(int32_t* __restrict__ counts, int G, int64_t C, int32_t* __restrict__ total) {
+  const int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= C) return;
+  int32_t run = 0;
+  for (int g = 0; g < G; ++g) {
+    int32_t v = counts[(int64_t)g * C + c];
+    counts[(int64_t)g * C + c] = run;
+    run += v;
+  }
+  total[c] = run;
+}
+
+// Single workgroup: exclusive scans of total[c] and of (total[c] > 0).
+//   start[c] = first csr position of chapter c; uid[c] = unique index of c.
+__global__ __launch_bounds__(1024) void plan_scan_kernel(const int32_t* __restrict__ total, int64_t C, int64_t E,
+                                                         int32_t* __restrict__ start, int32_t* __restrict__ uid,
+                                                         int32_t* __restrict__ uniq, int32_t* __restrict__ csr_off,
+                                                         int32_t* __restrict__ n_uniq) {
+  __shared__ int32_t s_tot[1024], s_cnt[1024];
+  __shared__ int32_t carry[2];
+  const int tid = threadIdx.x;
+  if (tid == 0) { carry[0] = 0; carry[1] = 0; }
+  __syncthreads();
+  for (int64_t base = 0; base < C; base += 1024) {
+    const int64_t c = base + tid;
+    const int32_t t = (c < C) ? total[c] : 0;
+    const int32_t f = t > 0 ? 1 : 0;
+    s_tot[tid] = t;
+    s_cnt[tid] = f;
+    __syncthreads();
+    for (int o = 1; o < 1024; o <<= 1) {
+      int32_t a = (tid >= o) ? s_tot[tid - o] : 0;
+      int32_t b = (tid >= o) ? s_cnt[tid - o] : 0;
+      __syncthreads();
+      s_tot[tid] += a;
+      s_cnt[tid] += b;
+      __syncthreads();
+    }
+    const int32_t ex_t = carry[0] + s_tot[tid] - t;
+    const int32_t ex_f = carry[1] + s_cnt[tid] - f;
+    if (c < C) {
+      start[c] = ex_t;
+      uid[c] = f ? ex_f : -1;
+      if (f) { uniq[ex_f] = (int32_t)c; csr_off[ex_f] = ex_t; }
+    }
+    __syncthreads();
+    if (tid == 1023) { carry[0] += s_tot[1023]; carry[1] += s_cnt[1023]; }
+    __syncthreads();
+  }
+  // n_uniq[1] = number of edges whose chapter id was out of range (they are skipped).
+  if (tid == 0) { n_uniq[0] = carry[1]; n_uniq[1] = (int32_t)(E - carry[0]); csr_off[carry[1]] = carry[0]; }
+}
+
+// Stable placement: block g walks its edges in order (one lane), cursor in LDS.
+__global__ __launch_bounds__(256) void plan_place_kernel(const int32_t* __restrict__ chap, int64_t E, int64_t C,
+                                                         const int32_t* __restrict__ counts,
+                                                         const int32_t* __restrict__ start,
+                                                         const int32_t* __restrict__ uid,
+                                                         int32_t* __restrict__ edge_u, int32_t* __restrict__ csr_edge) {
+  extern __shared__ int32_t cur[];
+  const int g = blockIdx.x;
+  const int64_t e0 = (int64_t)g * kPlanEdgesPerBlock;
+  const int64_t e1 = min(E, e0 + kPlanEdgesPerBlock);
+  // Only chapters touched by this block need a cursor; initialise them all (C is LDS-bounded).
+  for (int64_t c = threadIdx.x; c < C; c += 256) cur[c] = start[c] + counts[(int64_t)g * C + c];
+  __syncthreads();
+  for (int64_t e = e0 + threadIdx.x; e < e1; e += 256) {
+    const int32_t c = chap[e];
+    edge_u[e] = (c >= 0 && c < C) ? uid[c] : -1;
+  }
+  if (threadIdx.x == 0) {
+    for (int64_t e = e0; e < e1; ++e) {
+      const int32_t c = chap[e];
+      if (c >= 0 && c < C) csr_edge[cur[c]++] = (int32_t)e;
+    }
+  }
+}
+
+}  // namespace moc
+
+using namespace moc;
+
+extern "C" {
+
+size_t moc_chapter_plan_workspace(int64_t E, int64_t C) {
+  const int64_t G = (E + kPlanEdgesPerBlock - 1) / kPlanEdgesPerBlock;
+  // counts[G][C] + total[C] + start[C] + uid[C]
+  return (size_t)(G * C + 3 * C) * sizeof(int32_t);
+}
+
+int moc_chapter_plan(const int32_t* chap, int64_t E, int64_t C, void* workspace, size_t workspace_bytes,
+                     int32_t* uniq, int32_t* n_uniq, int32_t* edge_u, int32_t* csr_off, int32_t* csr_edge,
+                     hipStream_t stream) {
+  MOC_REQUIRE(chap && workspace && uniq && n_uniq && edge_u && csr_off && csr_edge, MOC_ERR_ARG,
+              "moc_chapter_plan: null pointer");
+  MOC_REQUIRE(E > 0 && E < (int64_t)1 << 31, MOC_ERR_ARG, "moc_chapter_plan: E=%lld out of range", (long long)E);
+  MOC_REQUIRE(C > 0 && C <= kPlanMaxC, MOC_ERR_UNSUPPORTED, "moc_chapter_plan: C=%lld not in [1, %d]", (long long)C,
+              kPlanMaxC);
+  MOC_REQUIRE(workspace_bytes >= moc_chapter_plan_workspace(E, C), MOC_ERR_ARG, "moc_chapter_plan: workspace too small");
+  const int G = (int)((E + kPlanEdgesPerBlock - 1) / kPlanEdgesPerBlock);
+  int32_t* counts = (int32_t*)workspace;
+  int32_t* total = counts + (int64_t)G * C;
+  int32_t* start = total + C;
+  int32_t* uid = start + C;
+  const size_t lds = (size_t)C * sizeof(int32_t);
+  hipLaunchKernelGGL(plan_hist_kernel, dim3(G), dim3(256), lds, stream, chap, E, C, counts);
+  int rc = check_launch("plan_hist_kernel");
+  if (rc) return rc;
+  hipLaunchKernelGGL(plan_colscan_kernel, dim3((unsigned)((C + 255) / 256)), dim3(256), 0, stream, counts, G, C, total);
+  if ((rc = check_launch("plan_colscan_kernel"))) return rc;
+  hipLaunchKernelGGL(plan_scan_kernel, dim3(1), dim3(1024), 0, stream, total, C, E, start, uid, uniq, csr_off, n_uniq);
+  if ((rc = check_launch("plan_scan_kernel"))) return rc;
+  hipLaunchKernelGGL(plan_place_kernel, dim3(G), dim3(256), lds, stream, chap, E, C, counts, start, uid, edge_u, csr_edge);
+  return check_launch("plan_place_kernel");
+}
+
+}  // extern "C"

@@ -1,0 +1,238 @@
+// Sequence-routed memory cross-attention, forward ("joint" combine).
+//
+// For sequence b, query i, query head h (kv head hk = h / (H / HK)) and the
+// NS selected chapters c with router weights omega[b, c]:
+//   s_ij  = omega_c * scale * q_i . k_j           (j ranges over chapter c's T keys)
+//   o_i   = sum_j softmax_j(s_ij) * omega_c * v_j
+// which is exactly MemoryCrossAttention over the omega-weighted gathered rows
+// (memory_transformer/model.py:689-692 then memory_attention.py:458-478 /
+// :269-318): (omega x) W^T = omega (x W^T), so the key and the value of every
+// row of chapter c carry the factor omega_c.  k_j / v_j come from the
+// chapter-head tiles written by kv_project.hip; slot_u[b, c] says which
+// de-duplicated chapter holds slot c of sequence b (negative = skip the slot).
+//
+// Work decomposition (Dh = T = 64): one workgroup = 128 queries of one
+// (sequence, head); 4 waves x 32 queries.  Every chapter is one 64-key tile,
+// so omega is a scalar per tile and folds into the exp2 argument.  Each wave
+// computes S^T = K Q^T (lane = one query, 16 keys), keeps the running max and
+// a lane-partial row sum, and accumulates O^T = V^T P^T, whose accumulator
+// layout is again "lane = one query", so the online-softmax rescale needs no
+// data movement.  K and V^T tiles are double-buffered in LDS.
+#include "moc_common.h"
+
+namespace moc {
+
+constexpr int kFwdThreads = 256;
+constexpr int kDh = 64;
+constexpr int kTch = 64;
+
+// Load one 64x64 chapter-head tile of T from global into registers (each
+// thread owns NCHUNK 16-byte chunks), then store it to LDS either as-is
+// (row = key) or transposed (row = dim).
+template <typename T>
+struct TileIO {
+  static constexpr int EPC = 16 / (int)sizeof(T);
+  static constexpr int CPR = kDh / EPC;                       // chunks per row
+  static constexpr int NCHUNK = (kTch * CPR) / kFwdThreads;   // per thread (2 or 4)
+  using Tile = SwzTile<T, 64>;
+  V16 r[NCHUNK];
+  __device__ __forceinline__ void load(const T* src, int tid) {
+#pragma unroll
+    for (int i = 0; i < NCHUNK; ++i) r[i] = ld16(src + (size_t)(tid + kFwdThreads * i) * EPC);
+  }
+  __device__ __forceinline__ void store(char* dst, int tid) const {
+#pragma unroll
+    for (int i = 0; i < NCHUNK; ++i) {
+      const int q = tid + kFwdThreads * i;
+      st16(dst + Tile::off(q / CPR, (q % CPR) * EPC), r[i]);
+    }
+  }
+  __device__ __forceinline__ void store_t(char* dst, int tid) const {
+#pragma unroll
+    for (int i = 0; i < NCHUNK; ++i) {
+      const int q = tid + kFwdThreads * i;
+      const int key = q / CPR, d0 = (q % CPR) * EPC;
+      const T* v = reinterpret_cast<const T*>(&r[i]);
+#pragma unroll
+      for (int x = 0; x < EPC; ++x) *reinterpret_cast<T*>(dst + Tile::off(d0 + x, key)) = v[x];
+    }
+  }
+};
+
+template <typename T>
+__global__ __launch_bounds__(kFwdThreads) void xattn_fwd_kernel(
+    const T* __restrict__ q, const T* __restrict__ ktiles, const T* __restrict__ vtiles,
+    const int32_t* __restrict__ slot_u, const float* __restrict__ omega, int L, int H, int HK, int NS,
+    float scale_log2, T* __restrict__ out, float* __restrict__ lse) {
+  typedef typename Frag<T>::type F8;
+  using Tile = SwzTile<T, 64>;
+  constexpr int TB = kTch * kDh * (int)sizeof(T);
+  __shared__ __attribute__((aligned(16))) char sK[2][TB];
+  __shared__ __attribute__((aligned(16))) char sV[2][TB];
+
+  const int b = blockIdx.z, h = blockIdx.y;
+  const int hk = h / (H / HK);
+  const int q0 = blockIdx.x * 128;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 4, c16 = lane & 15;
+
+  // Q^T fragments (B operand): query = q0 + 32*wave + 16*qb + c16, dims 32*ks + 8*g ..
+  F8 qf[2][2];
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb) {
+    const int qi = q0 + 32 * wave + 16 * qb + c16;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      if (qi < L)
+        qf[qb][ks] = Load8<T, T>::run(q + ((size_t)(b * (size_t)L + qi) * H + h) * kDh + 32 * ks + 8 * g);
+      else
+        qf[qb][ks] = zero_frag<T>();
+    }
+  }
+
+  float m[2] = {-INFINITY, -INFINITY};
+  float lpart[2] = {0.f, 0.f};
+  f32x4 o[4][2];
+#pragma unroll
+  for (int db = 0; db < 4; ++db)
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) o[db][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int32_t* su = slot_u + (size_t)b * NS;
+  const float* om = omega + (size_t)b * NS;
+  TileIO<T> kio, vio;
+  auto tile_ptr = [&](const T* base, int u) { return base + ((size_t)u * HK + hk) * (kTch * kDh); };
+
+  int u_cur = su[0];
+  if (u_cur >= 0) {
+    kio.load(tile_ptr(ktiles, u_cur), tid);
+    vio.load(tile_ptr(vtiles, u_cur), tid);
+    kio.store(sK[0], tid);
+    vio.store_t(sV[0], tid);
+  }
+  __syncthreads();
+
+  for (int s = 0; s < NS; ++s) {
+    const int buf = s & 1;
+    const int u_next = (s + 1 < NS) ? su[s + 1] : -1;
+    if (u_next >= 0) {
+      kio.load(tile_ptr(ktiles, u_next), tid);
+      vio.load(tile_ptr(vtiles, u_next), tid);
+    }
+    if (u_cur >= 0) {
+      const float w = om[s];
+      const float c = w * scale_log2;
+      const char* Ks = sK[buf];
+      const char* Vs = sV[buf];
+      // S^T[kb][qb]: rows = keys 16*kb + 4*g + e, column = query c16 of block qb
+      f32x4 st[4][2];
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) st[kb][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+          F8 a = Tile::frag(Ks, 16 * kb + c16, 32 * ks + 8 * g);
+#pragma unroll
+          for (int qb = 0; qb < 2; ++qb) mma(st[kb][qb], a, qf[qb][ks]);
+        }
+      }
+      F8 pf[2][2];
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb) {
+        float mx = -INFINITY;
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) mx = fmaxf(mx, st[kb][qb][e]);
+        mx = quad_max(mx);
+        const float mnew = fmaxf(m[qb], mx * c);  // c >= 0 (router weights are non-negative)
+        const float alpha = exp2f(m[qb] - mnew);
+        m[qb] = mnew;
+        float ps = 0.f;
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float p = exp2f(st[kb][qb][e] * c - mnew);
+            ps += p;
+            st[kb][qb][e] = p * w;
+          }
+        lpart[qb] = lpart[qb] * alpha + ps;
+#pragma unroll
+        for (int db = 0; db < 4; ++db) o[db][qb] *= alpha;
+#pragma unroll
+        for (int ks2 = 0; ks2 < 2; ++ks2)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            pf[qb][ks2][e] = from_f<T>(st[2 * ks2][qb][e]);
+            pf[qb][ks2][4 + e] = from_f<T>(st[2 * ks2 + 1][qb][e]);
+          }
+      }
+      // O^T[db][qb] += V^T(dims 16*db + c16, keys) * P^T
+#pragma unroll
+      for (int ks2 = 0; ks2 < 2; ++ks2) {
+#pragma unroll
+        for (int db = 0; db < 4; ++db) {
+          F8 a = Tile::frag44(Vs, 16 * db + c16, 32 * ks2 + 4 * g, 32 * ks2 + 16 + 4 * g);
+#pragma unroll
+          for (int qb = 0; qb < 2; ++qb) mma(o[db][qb], a, pf[qb][ks2]);
+        }
+      }
+    }
+    if (u_next >= 0) {
+      kio.store(sK[buf ^ 1], tid);
+      vio.store_t(sV[buf ^ 1], tid);
+    }
+    u_cur = u_next;
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb) {
+    const float l = quad_sum(lpart[qb]);
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+    const int qi = q0 + 32 * wave + 16 * qb + c16;
+    if (qi < L) {
+      T* op = out + ((size_t)(b * (size_t)L + qi) * H + h) * kDh;
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) op[16 * db + 4 * g + e] = from_f<T>(o[db][qb][e] * inv);
+      if (g == 0) lse[((size_t)b * H + h) * L + qi] = l > 0.f ? m[qb] + log2f(l) : -INFINITY;
+    }
+  }
+}
+
+}  // namespace moc
+
+using namespace moc;
+
+extern "C" {
+
+int moc_xattn_fwd(int dtype, const void* q, const void* k_tiles, const void* v_tiles, const int32_t* slot_u,
+                  const float* omega, int64_t B, int64_t L, int H, int HK, int Dh, int T, int NS, float scale,
+                  void* out, float* lse, hipStream_t stream) {
+  MOC_REQUIRE(q && k_tiles && v_tiles && slot_u && omega && out && lse, MOC_ERR_ARG, "moc_xattn_fwd: null pointer");
+  MOC_REQUIRE(Dh == kDh && T == kTch, MOC_ERR_UNSUPPORTED, "moc_xattn_fwd: needs head_dim 64 and 64 tokens per chapter (got %d, %d)", Dh, T);
+  MOC_REQUIRE(H > 0 && HK > 0 && H % HK == 0, MOC_ERR_ARG, "moc_xattn_fwd: H=%d HK=%d", H, HK);
+  MOC_REQUIRE(NS > 0 && B >= 0 && L >= 0, MOC_ERR_ARG, "moc_xattn_fwd: bad shape");
+  MOC_REQUIRE(B < 65536 && H < 65536, MOC_ERR_UNSUPPORTED, "moc_xattn_fwd: grid too large");
+  if (B == 0 || L == 0) return MOC_OK;
+  dim3 grid((unsigned)((L + 127) / 128), (unsigned)H, (unsigned)B);
+  const float sl2 = scale * 1.4426950408889634f;
+  if (dtype == MOC_BF16)
+    hipLaunchKernelGGL(xattn_fwd_kernel<bf16>, grid, dim3(kFwdThreads), 0, stream, (const bf16*)q, (const bf16*)k_tiles,
+                       (const bf16*)v_tiles, slot_u, omega, (int)L, H, HK, NS, sl2, (bf16*)out, lse);
+  else if (dtype == MOC_F32)
+    hipLaunchKernelGGL(xattn_fwd_kernel<float>, grid, dim3(kFwdThreads), 0, stream, (const float*)q,
+                       (const float*)k_tiles, (const float*)v_tiles, slot_u, omega, (int)L, H, HK, NS, sl2, (float*)out,
+                       lse);
+  else
+    return set_error(MOC_ERR_UNSUPPORTED, "moc_xattn_fwd: dtype %d", dtype);
+  return check_launch("xattn_fwd_kernel");
+}
+
+}  // extern "C"

@@ -1,0 +1,276 @@
+"""Autograd functions over the libmoc kernels.
+
+Every function here runs HIP kernels through the C ABI (memory_amd/_lib.py);
+tensors must live on a ROCm device.  PyTorch provides device memory (caching
+allocator), the current stream and autograd bookkeeping only.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Optional
+
+import torch
+
+from . import _lib as L
+from ._lib import call, ptr, stream_ptr
+
+
+# --------------------------------------------------------------------------- router
+
+class _RouterPool(torch.autograd.Function):
+    """Mean (or coefficient-weighted) pooling over the sequence, fp32 output.
+
+    Reference: memory_transformer/router.py:96-107 (mean) and :158-195 (rolling
+    mean, which is a fixed linear combination of positions)."""
+
+    @staticmethod
+    def forward(ctx, h: torch.Tensor, coef: Optional[torch.Tensor]):
+        L.require_gpu(h)
+        h = h.contiguous()
+        B, Lq, d = h.shape
+        pooled = torch.empty(B, d, device=h.device, dtype=torch.float32)
+        ws_bytes = L.query("moc_router_pool_workspace", B, Lq, d)
+        ws = torch.empty(max(1, ws_bytes), device=h.device, dtype=torch.uint8)
+        cf = None if coef is None else coef.to(device=h.device, dtype=torch.float32).contiguous()
+        call("moc_router_pool", ptr(h), L.dtype_code(h.dtype), B, Lq, d, ptr(cf), ptr(pooled), ptr(ws), ws_bytes,
+             stream_ptr(h.device))
+        ctx.save_for_backward(cf)
+        ctx.shape, ctx.dtype = (B, Lq, d), h.dtype
+        return pooled
+
+    @staticmethod
+    def backward(ctx, dpooled):
+        (cf,) = ctx.saved_tensors
+        B, Lq, d = ctx.shape
+        if cf is None:
+            dh = (dpooled * (1.0 / Lq)).to(ctx.dtype).unsqueeze(1).expand(B, Lq, d)
+        else:
+            dh = (dpooled.unsqueeze(1) * cf.view(1, Lq, 1)).to(ctx.dtype)
+        return dh, None
+
+
+def router_pool(h: torch.Tensor, coef: Optional[torch.Tensor] = None) -> torch.Tensor:
+    return _RouterPool.apply(h, coef)
+
+
+class _RouterLinear(torch.autograd.Function):
+    """logits = x W^T + b in fp32 for a few rows (sequence-level routing)."""
+
+    @staticmethod
+    def forward(ctx, x: torch.Tensor, W: torch.Tensor, b: Optional[torch.Tensor]):
+        L.require_gpu(x, W, b)
+        x = x.float().contiguous()
+        Wc = W.contiguous()
+        bc = None if b is None else b.float().contiguous()
+        R, d = x.shape
+        C = W.shape[0]
+        logits = torch.empty(R, C, device=x.device, dtype=torch.float32)
+        call("moc_router_linear", ptr(x), R, d, ptr(Wc), L.dtype_code(Wc.dtype), ptr(bc), C, ptr(logits),
+             stream_ptr(x.device))
+        ctx.save_for_backward(x, Wc)
+        ctx.has_b = b is not None
+        ctx.b_dtype = None if b is None else b.dtype
+        return logits
+
+    @staticmethod
+    def backward(ctx, dz):
+        x, Wc = ctx.saved_tensors
+        dz = dz.float().contiguous()
+        R, d = x.shape
+        C = Wc.shape[0]
+        need_x, need_w, need_b = ctx.needs_input_grad
+        dx = torch.empty(R, d, device=x.device, dtype=torch.float32) if need_x else None
+        dW = torch.empty(C, d, device=x.device, dtype=torch.float32) if need_w else None
+        db = torch.empty(C, device=x.device, dtype=torch.float32) if (need_b and ctx.has_b) else None
+        if dW is None and db is not None:
+            dW_tmp = torch.empty(C, d, device=x.device, dtype=torch.float32)
+        else:
+            dW_tmp = dW
+        ws_bytes = L.query("moc_router_linear_bwd_workspace", R, d, C)
+        ws = torch.empty(max(1, ws_bytes), device=x.device, dtype=torch.uint8)
+        call("moc_router_linear_bwd", ptr(dz), ptr(x), R, d, ptr(Wc), L.dtype_code(Wc.dtype), C, ptr(dx), ptr(dW_tmp),
+             ptr(db), ptr(ws), ws_bytes, stream_ptr(x.device))
+        if dW is not None:
+            dW = dW.to(Wc.dtype)
+        if db is not None:
+            db = db.to(ctx.b_dtype)
+        return dx, dW, db
+
+
+def router_linear(x: torch.Tensor, W: torch.Tensor, b: Optional[torch.Tensor]) -> torch.Tensor:
+    return _RouterLinear.apply(x, W, b)
+
+
+class _RouterTopK(torch.autograd.Function):
+    """softmax -> shared-prefix mask -> renorm -> top-k -> renorm (router.py:114-149)."""
+
+    @staticmethod
+    def forward(ctx, logits: torch.Tensor, k: int, S: int):
+        L.require_gpu(logits)
+        logits = logits.float().contiguous()
+        R, C = logits.shape
+        idx = torch.empty(R, k, device=logits.device, dtype=torch.int32)
+        w = torch.empty(R, k, device=logits.device, dtype=torch.float32)
+        call("moc_router_topk", ptr(logits), R, C, S, k, ptr(idx), ptr(w), None, stream_ptr(logits.device))
+        ctx.save_for_backward(logits, idx)
+        ctx.k, ctx.S = k, S
+        ctx.mark_non_differentiable(idx)
+        return idx, w
+
+    @staticmethod
+    def backward(ctx, _didx, dw):
+        logits, idx = ctx.saved_tensors
+        R, C = logits.shape
+        dz = torch.empty_like(logits)
+        if dw is None:
+            return None, None, None
+        dw = dw.float().contiguous()
+        call("moc_router_topk_bwd", ptr(logits), ptr(idx), ptr(dw), R, C, ctx.S, ctx.k, ptr(dz),
+             stream_ptr(logits.device))
+        return dz, None, None
+
+
+def router_topk(logits: torch.Tensor, k: int, exclude_prefix_chapters: int = 0):
+    """Returns (idx int32 (R, k) global chapter ids, weights fp32 (R, k))."""
+    return _RouterTopK.apply(logits, int(k), int(exclude_prefix_chapters))
+
+
+class _PrependShared(torch.autograd.Function):
+    """MemoryTransformer._prepend_shared_chapters (memory_transformer/model.py:356-391)."""
+
+    @staticmethod
+    def forward(ctx, idx: torch.Tensor, w: torch.Tensor, S: int, scale: float):
+        L.require_gpu(idx, w)
+        idx = idx.to(torch.int32).contiguous()
+        w = w.float().contiguous()
+        R, k = idx.shape
+        idx_star = torch.empty(R, S + k, device=idx.device, dtype=torch.int32)
+        omega = torch.empty(R, S + k, device=idx.device, dtype=torch.float32)
+        call("moc_prepend_shared", ptr(idx), ptr(w), R, k, S, float(scale), ptr(idx_star), ptr(omega),
+             stream_ptr(idx.device))
+        ctx.save_for_backward(w)
+        ctx.S, ctx.scale = S, float(scale)
+        ctx.mark_non_differentiable(idx_star)
+        return idx_star, omega
+
+    @staticmethod
+    def backward(ctx, _di, domega):
+        (w,) = ctx.saved_tensors
+        R, k = w.shape
+        if domega is None or k == 0:
+            return None, None, None, None
+        dw = torch.empty_like(w)
+        call("moc_prepend_shared_bwd", ptr(w), ptr(domega.float().contiguous()), R, k, ctx.S, ctx.scale, ptr(dw),
+             stream_ptr(w.device))
+        return None, dw, None, None
+
+
+def prepend_shared(idx: torch.Tensor, w: torch.Tensor, num_shared: int, routed_scale: float):
+    return _PrependShared.apply(idx, w, int(num_shared), float(routed_scale))
+
+
+# ----------------------------------------------------------------------- chapter plan
+
+@dataclass
+class ChapterPlan:
+    uniq: torch.Tensor      # int32 [max_u]
+    n_uniq: torch.Tensor    # int32 [2]  (distinct chapters, skipped edges)
+    edge_u: torch.Tensor    # int32 [E]
+    csr_off: torch.Tensor   # int32 [max_u + 1]
+    csr_edge: torch.Tensor  # int32 [E]
+    max_u: int
+    num_chapters: int
+
+
+def chapter_plan(chap: torch.Tensor, num_chapters: int) -> ChapterPlan:
+    """De-duplicate the selected chapters (any shape, flattened row-major into edges)."""
+    L.require_gpu(chap)
+    flat = chap.reshape(-1).to(torch.int32).contiguous()
+    E = flat.numel()
+    C = int(num_chapters)
+    max_u = min(E, C)
+    dev = flat.device
+    uniq = torch.empty(max_u, device=dev, dtype=torch.int32)
+    n_uniq = torch.empty(2, device=dev, dtype=torch.int32)
+    edge_u = torch.empty(E, device=dev, dtype=torch.int32)
+    csr_off = torch.empty(max_u + 1, device=dev, dtype=torch.int32)
+    csr_edge = torch.empty(E, device=dev, dtype=torch.int32)
+    ws_bytes = L.query("moc_chapter_plan_workspace", E, C)
+    ws = torch.empty(max(1, ws_bytes), device=dev, dtype=torch.uint8)
+    call("moc_chapter_plan", ptr(flat), E, C, ptr(ws), ws_bytes, ptr(uniq), ptr(n_uniq), ptr(edge_u), ptr(csr_off),
+         ptr(csr_edge), stream_ptr(dev))
+    return ChapterPlan(uniq, n_uniq, edge_u, csr_off, csr_edge, max_u, C)
+
+
+_NORM = {None: L.MOC_NORM_NONE, "none": L.MOC_NORM_NONE, "rms": L.MOC_NORM_RMS, "layernorm": L.MOC_NORM_LAYERNORM}
+
+
+def norm_code(norm_type: Optional[str]) -> int:
+    if norm_type not in _NORM:
+        raise ValueError(f"Unsupported norm_type: {norm_type}")
+    return _NORM[norm_type]
+
+
+def row_stats(bank: torch.Tensor, plan: ChapterPlan, T: int, norm: int, eps: float):
+    rows = plan.max_u * T
+    mean = torch.empty(rows, device=bank.device, dtype=torch.float32)
+    rstd = torch.empty(rows, device=bank.device, dtype=torch.float32)
+    call("moc_row_stats", ptr(bank), L.dtype_code(bank.dtype), bank.shape[1], T, ptr(plan.uniq), ptr(plan.n_uniq),
+         plan.max_u, norm, float(eps), ptr(mean), ptr(rstd), stream_ptr(bank.device))
+    return mean, rstd
+
+
+def kv_project(bank: torch.Tensor, plan: ChapterPlan, T: int, wkv: torch.Tensor, HK: int, Dh: int,
+               mean: Optional[torch.Tensor], rstd: Optional[torch.Tensor], dtype: torch.dtype):
+    kt = torch.empty(plan.max_u, HK, T, Dh, device=bank.device, dtype=dtype)
+    vt = torch.empty_like(kt)
+    call("moc_kv_project", L.dtype_code(dtype), ptr(bank), L.dtype_code(bank.dtype), bank.shape[1], T, ptr(plan.uniq),
+         ptr(plan.n_uniq), plan.max_u, ptr(mean), ptr(rstd), ptr(wkv), HK, Dh, ptr(kt), ptr(vt),
+         stream_ptr(bank.device))
+    return kt, vt
+
+
+# ------------------------------------------------------------- routed attention (A)
+
+class _RoutedAttention(torch.autograd.Function):
+    """Gather + K/V projection + joint routed attention (sequence level).
+
+    Inputs: q (B, L, H, Dh) [compute dtype]; bank (N_m, d); wk/wv (HK*Dh, d);
+    omega (B, NS) fp32 chapter weights; idx_star (B, NS) chapter ids.
+    Output: attention output (B, L, H, Dh) before o_proj."""
+
+    @staticmethod
+    def forward(ctx, q, bank, wk, wv, omega, idx_star, num_chapters, T, norm, eps, HK):
+        L.require_gpu(q, bank, wk, wv, omega, idx_star)
+        dtype = q.dtype
+        B, Lq, H, Dh = q.shape
+        NS = idx_star.shape[1]
+        q = q.contiguous()
+        bank = bank.contiguous()
+        plan = chapter_plan(idx_star, num_chapters)
+        mean = rstd = None
+        if norm != L.MOC_NORM_NONE:
+            mean, rstd = row_stats(bank, plan, T, norm, eps)
+        wkv = torch.cat([wk, wv], 0).to(dtype).contiguous()
+        kt, vt = kv_project(bank, plan, T, wkv, HK, Dh, mean, rstd, dtype)
+        om = omega.float().contiguous()
+        out = torch.empty(B, Lq, H, Dh, device=q.device, dtype=dtype)
+        lse = torch.empty(B, H, Lq, device=q.device, dtype=torch.float32)
+        call("moc_xattn_fwd", L.dtype_code(dtype), ptr(q), ptr(kt), ptr(vt), ptr(plan.edge_u), ptr(om), B, Lq, H, HK,
+             Dh, T, NS, float(Dh) ** -0.5, ptr(out), ptr(lse), stream_ptr(q.device))
+        ctx.save_for_backward(q, bank, wkv, om, out, lse, kt, vt, mean, rstd, plan.uniq, plan.n_uniq, plan.edge_u,
+                              plan.csr_off, plan.csr_edge)
+        ctx.cfg = (num_chapters, T, norm, eps, HK, plan.max_u, wk.dtype, wv.dtype, bank.dtype)
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        raise NotImplementedError("backward lands with xattn_bwd.hip")
+
+
+def routed_attention(q, bank, wk, wv, omega, idx_star, *, num_chapters: int, tokens_per_chapter: int,
+                     norm_type: Optional[str] = None, eps: float = 1e-6, num_kv_heads: Optional[int] = None):
+    HK = q.shape[2] if num_kv_heads is None else int(num_kv_heads)
+    return _RoutedAttention.apply(q, bank, wk, wv, omega, idx_star, int(num_chapters), int(tokens_per_chapter),
+                                  norm_code(norm_type), float(eps), HK)
