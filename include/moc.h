@@ -132,6 +132,42 @@ int moc_xattn_fwd(int dtype, const void* q, const void* k_tiles, const void* v_t
                   const float* omega, int64_t B, int64_t L, int H, int HK, int Dh, int T, int NS, float scale,
                   void* out, float* lse, hipStream_t stream);
 
+/* ------------------------------------------------ routed attention backward */
+
+/* Backward of moc_xattn_fwd (autograd of memory_transformer/memory_attention.py:301-316 through
+ * the omega weighting of model.py:689-692).  prep: delta f32 [B, H, L] = rowsum(dout * out). */
+int moc_xattn_bwd_prep(int dtype, const void* out, const void* dout, int64_t B, int64_t L, int H, int Dh,
+                       float* delta, hipStream_t stream);
+/* dq [B, L, H, Dh] (dtype). */
+int moc_xattn_bwd_dq(int dtype, const void* q, const void* k_tiles, const void* v_tiles, const int32_t* slot_u,
+                     const float* omega, const void* dout, const float* lse, const float* delta, int64_t B, int64_t L,
+                     int H, int HK, int Dh, int T, int NS, float scale, void* dq, hipStream_t stream);
+/* Chapter-centric dK/dV over the plan's inverted index (the reference's
+ * mem_xattn_weighted_bwd_dkv_invidx_kernel design, kernels-final/kernel_v4.py:534-671, applied
+ * to the joint combine): dkv [max_u * T][2 * HK * Dh] (dtype) holds, per distinct chapter row,
+ * [dL/dk (all kv heads) | dL/dv]; rows of unused plan slots are written as zero.
+ * domega_part f32 [B * NS][H]: per (edge, query head) partial of dL/domega (caller sums over H;
+ * entries of skipped edges are not written). */
+int moc_xattn_bwd_dkv(int dtype, const void* q, const void* k_tiles, const void* v_tiles, const float* omega,
+                      const void* dout, const float* lse, const float* delta, const int32_t* n_uniq,
+                      const int32_t* csr_off, const int32_t* csr_edge, int64_t max_u, int64_t B, int64_t L, int H,
+                      int HK, int Dh, int T, int NS, float scale, void* dkv, float* domega_part,
+                      hipStream_t stream);
+
+/* Gathered (and normalised) rows X [max_u * T][d] in dtype for the weight-gradient GEMM
+ * dWkv = dkv^T X; rows of unused plan slots are zero. */
+int moc_gather_rows(int dtype, const void* bank, int bank_dtype, int64_t d, int T, const int32_t* uniq,
+                    const int32_t* n_uniq, int64_t max_u, const float* row_mean, const float* row_rstd, void* out,
+                    hipStream_t stream);
+
+/* Backward of the gather (memory_bank.py:287-291, a scatter-add into the bank gradient) through
+ * the optional row normalisation: grad_bank[uniq[u]*T + t, :] = norm_bwd(dX[u*T + t, :]).
+ * Distinct chapters own distinct rows, so the rows are stored, not added; grad_bank must be
+ * zero elsewhere.  dX [max_u * T][d] of dx_dtype, grad_bank of bank_dtype. */
+int moc_bank_scatter(int dx_dtype, const void* dX, const void* bank, int bank_dtype, int64_t d, int T,
+                     const int32_t* uniq, const int32_t* n_uniq, int64_t max_u, const float* row_mean,
+                     const float* row_rstd, int norm, void* grad_bank, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -138,6 +138,40 @@ struct SwzTile {
   }
 };
 
+// ------------------------------------------------------ 64x64 tile movement
+// One contiguous 64 x 64 tile of T (e.g. a chapter-head K or V block) moved
+// global -> registers -> LDS by NT threads; each thread owns NCHUNK 16-byte
+// chunks.  store() keeps row = first index, store_t() writes the transpose.
+template <typename T, int NT>
+struct TileIO {
+  static constexpr int EPC = 16 / (int)sizeof(T);
+  static constexpr int CPR = 64 / EPC;             // chunks per row
+  static constexpr int NCHUNK = (64 * CPR) / NT;   // per thread
+  using Tile = SwzTile<T, 64>;
+  V16 r[NCHUNK];
+  __device__ __forceinline__ void load(const T* src, int tid) {
+#pragma unroll
+    for (int i = 0; i < NCHUNK; ++i) r[i] = ld16(src + (size_t)(tid + NT * i) * EPC);
+  }
+  __device__ __forceinline__ void store(char* dst, int tid) const {
+#pragma unroll
+    for (int i = 0; i < NCHUNK; ++i) {
+      const int q = tid + NT * i;
+      st16(dst + Tile::off(q / CPR, (q % CPR) * EPC), r[i]);
+    }
+  }
+  __device__ __forceinline__ void store_t(char* dst, int tid) const {
+#pragma unroll
+    for (int i = 0; i < NCHUNK; ++i) {
+      const int q = tid + NT * i;
+      const int row = q / CPR, c0 = (q % CPR) * EPC;
+      const T* v = reinterpret_cast<const T*>(&r[i]);
+#pragma unroll
+      for (int x = 0; x < EPC; ++x) *reinterpret_cast<T*>(dst + Tile::off(c0 + x, row)) = v[x];
+    }
+  }
+};
+
 // ------------------------------------------------------------ wave reductions
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll

@@ -26,39 +26,6 @@ constexpr int kFwdThreads = 256;
 constexpr int kDh = 64;
 constexpr int kTch = 64;
 
-// Load one 64x64 chapter-head tile of T from global into registers (each
-// thread owns NCHUNK 16-byte chunks), then store it to LDS either as-is
-// (row = key) or transposed (row = dim).
-template <typename T>
-struct TileIO {
-  static constexpr int EPC = 16 / (int)sizeof(T);
-  static constexpr int CPR = kDh / EPC;                       // chunks per row
-  static constexpr int NCHUNK = (kTch * CPR) / kFwdThreads;   // per thread (2 or 4)
-  using Tile = SwzTile<T, 64>;
-  V16 r[NCHUNK];
-  __device__ __forceinline__ void load(const T* src, int tid) {
-#pragma unroll
-    for (int i = 0; i < NCHUNK; ++i) r[i] = ld16(src + (size_t)(tid + kFwdThreads * i) * EPC);
-  }
-  __device__ __forceinline__ void store(char* dst, int tid) const {
-#pragma unroll
-    for (int i = 0; i < NCHUNK; ++i) {
-      const int q = tid + kFwdThreads * i;
-      st16(dst + Tile::off(q / CPR, (q % CPR) * EPC), r[i]);
-    }
-  }
-  __device__ __forceinline__ void store_t(char* dst, int tid) const {
-#pragma unroll
-    for (int i = 0; i < NCHUNK; ++i) {
-      const int q = tid + kFwdThreads * i;
-      const int key = q / CPR, d0 = (q % CPR) * EPC;
-      const T* v = reinterpret_cast<const T*>(&r[i]);
-#pragma unroll
-      for (int x = 0; x < EPC; ++x) *reinterpret_cast<T*>(dst + Tile::off(d0 + x, key)) = v[x];
-    }
-  }
-};
-
 template <typename T>
 __global__ __launch_bounds__(kFwdThreads) void xattn_fwd_kernel(
     const T* __restrict__ q, const T* __restrict__ ktiles, const T* __restrict__ vtiles,
@@ -100,7 +67,7 @@ __global__ __launch_bounds__(kFwdThreads) void xattn_fwd_kernel(
 
   const int32_t* su = slot_u + (size_t)b * NS;
   const float* om = omega + (size_t)b * NS;
-  TileIO<T> kio, vio;
+  TileIO<T, kFwdThreads> kio, vio;
   auto tile_ptr = [&](const T* base, int u) { return base + ((size_t)u * HK + hk) * (kTch * kDh); };
 
   int u_cur = su[0];

@@ -266,7 +266,45 @@ class _RoutedAttention(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, dout):
-        raise NotImplementedError("backward lands with xattn_bwd.hip")
+        (q, bank, wkv, om, out, lse, kt, vt, mean, rstd, uniq, n_uniq, edge_u, csr_off,
+         csr_edge) = ctx.saved_tensors
+        C, T, norm, eps, HK, max_u, wk_dtype, wv_dtype, bank_dtype = ctx.cfg
+        dtype = q.dtype
+        dt = L.dtype_code(dtype)
+        B, Lq, H, Dh = q.shape
+        NS = om.shape[1]
+        KV = HK * Dh
+        d = bank.shape[1]
+        dev = q.device
+        st = stream_ptr(dev)
+        scale = float(Dh) ** -0.5
+        dout = dout.to(dtype).contiguous()
+        delta = torch.empty(B, H, Lq, device=dev, dtype=torch.float32)
+        call("moc_xattn_bwd_prep", dt, ptr(out), ptr(dout), B, Lq, H, Dh, ptr(delta), st)
+        dq = torch.empty_like(q)
+        call("moc_xattn_bwd_dq", dt, ptr(q), ptr(kt), ptr(vt), ptr(edge_u), ptr(om), ptr(dout), ptr(lse), ptr(delta),
+             B, Lq, H, HK, Dh, T, NS, scale, ptr(dq), st)
+        dkv = torch.empty(max_u * T, 2 * KV, device=dev, dtype=dtype)
+        dom_part = torch.zeros(B * NS, H, device=dev, dtype=torch.float32)
+        call("moc_xattn_bwd_dkv", dt, ptr(q), ptr(kt), ptr(vt), ptr(om), ptr(dout), ptr(lse), ptr(delta),
+             ptr(n_uniq), ptr(csr_off), ptr(csr_edge), max_u, B, Lq, H, HK, Dh, T, NS, scale, ptr(dkv),
+             ptr(dom_part), st)
+        domega = dom_part.sum(-1).view(B, NS)
+        need_bank, need_wk, need_wv = ctx.needs_input_grad[1:4]
+        dbank = dwk = dwv = None
+        if need_wk or need_wv:
+            X = torch.empty(max_u * T, d, device=dev, dtype=dtype)
+            call("moc_gather_rows", dt, ptr(bank), L.dtype_code(bank.dtype), d, T, ptr(uniq), ptr(n_uniq), max_u,
+                 ptr(mean), ptr(rstd), ptr(X), st)
+            dwkv = torch.matmul(dkv.t(), X)
+            dwk = dwkv[:KV].to(wk_dtype) if need_wk else None
+            dwv = dwkv[KV:].to(wv_dtype) if need_wv else None
+        if need_bank:
+            dX = torch.matmul(dkv, wkv)
+            dbank = torch.zeros(bank.shape, device=dev, dtype=bank_dtype)
+            call("moc_bank_scatter", L.dtype_code(dX.dtype), ptr(dX), ptr(bank), L.dtype_code(bank.dtype), d, T,
+                 ptr(uniq), ptr(n_uniq), max_u, ptr(mean), ptr(rstd), norm, ptr(dbank), st)
+        return dq, dbank, dwk, dwv, domega, None, None, None, None, None, None
 
 
 def routed_attention(q, bank, wk, wv, omega, idx_star, *, num_chapters: int, tokens_per_chapter: int,
