@@ -126,8 +126,8 @@ int moc_kv_project(int dtype, const void* bank, int bank_dtype, int64_t d, int T
  * (memory_transformer/model.py:689-692 + memory_attention.py:458-478, :269-318) for the
  * sequence-level path: one joint softmax over the NS selected chapters of each sequence,
  * with omega scaling both logits and values.  q [B, L, H, Dh]; slot_u i32 [B, NS] (the
- * plan's edge_u); omega f32 [B, NS]; out [B, L, H, Dh]; lse f32 [B, H, L] (log2 domain,
- * consumed by the backward).  Dh == 64, T == 64. */
+ * plan's edge_u); omega f32 [B, NS]; out [B, L, H, Dh]; lse f32 [B, H, round_up(L, 128)] (log2
+ * domain, +inf in the padding; consumed by the backward).  Dh == 64, T == 64. */
 int moc_xattn_fwd(int dtype, const void* q, const void* k_tiles, const void* v_tiles, const int32_t* slot_u,
                   const float* omega, int64_t B, int64_t L, int H, int HK, int Dh, int T, int NS, float scale,
                   void* out, float* lse, hipStream_t stream);
@@ -135,24 +135,31 @@ int moc_xattn_fwd(int dtype, const void* q, const void* k_tiles, const void* v_t
 /* ------------------------------------------------ routed attention backward */
 
 /* Backward of moc_xattn_fwd (autograd of memory_transformer/memory_attention.py:301-316 through
- * the omega weighting of model.py:689-692).  prep: delta f32 [B, H, L] = rowsum(dout * out). */
-int moc_xattn_bwd_prep(int dtype, const void* out, const void* dout, int64_t B, int64_t L, int H, int Dh,
-                       float* delta, hipStream_t stream);
+ * the omega weighting of model.py:689-692).  Rows of lse / delta / qt / dot have stride
+ * Lp = round_up(L, 128) (moc_xattn_fwd writes lse that way, padded with +inf).
+ * prep: delta f32 [B, H, Lp] = rowsum(dout * out); qt, dot [B, H, Dh, Lp] (dtype) = q and dout
+ * transposed per (sequence, head), zero-padded. */
+int moc_xattn_bwd_prep(int dtype, const void* q, const void* out, const void* dout, int64_t B, int64_t L, int H,
+                       int Dh, float* delta, void* qt, void* dot, hipStream_t stream);
 /* dq [B, L, H, Dh] (dtype). */
 int moc_xattn_bwd_dq(int dtype, const void* q, const void* k_tiles, const void* v_tiles, const int32_t* slot_u,
                      const float* omega, const void* dout, const float* lse, const float* delta, int64_t B, int64_t L,
                      int H, int HK, int Dh, int T, int NS, float scale, void* dq, hipStream_t stream);
-/* Chapter-centric dK/dV over the plan's inverted index (the reference's
- * mem_xattn_weighted_bwd_dkv_invidx_kernel design, kernels-final/kernel_v4.py:534-671, applied
- * to the joint combine): dkv [max_u * T][2 * HK * Dh] (dtype) holds, per distinct chapter row,
- * [dL/dk (all kv heads) | dL/dv]; rows of unused plan slots are written as zero.
- * domega_part f32 [B * NS][H]: per (edge, query head) partial of dL/domega (caller sums over H;
- * entries of skipped edges are not written). */
-int moc_xattn_bwd_dkv(int dtype, const void* q, const void* k_tiles, const void* v_tiles, const float* omega,
-                      const void* dout, const float* lse, const float* delta, const int32_t* n_uniq,
-                      const int32_t* csr_off, const int32_t* csr_edge, int64_t max_u, int64_t B, int64_t L, int H,
-                      int HK, int Dh, int T, int NS, float scale, void* dkv, float* domega_part,
-                      hipStream_t stream);
+/* dK/dV per edge (edge e = b * NS + slot): dkv_edge [B * NS * T][2 * HK * Dh] (dtype) holds for
+ * the chapter in slot `slot` of sequence b the rows [dL/dk (all kv heads) | dL/dv], where
+ * dL/dk, dL/dv are gradients w.r.t. the unweighted projected keys/values (omega folded in).
+ * Rows of skipped slots are not written.  domega_part f32 [B * NS][H]: per (edge, query head)
+ * parts of dL/domega (caller sums over H; skipped edges are not written). */
+int moc_xattn_bwd_dkv(int dtype, const void* q, const void* qt, const void* dout, const void* dot,
+                      const void* k_tiles, const void* v_tiles, const int32_t* slot_u, const float* omega,
+                      const float* lse, const float* delta, int64_t B, int64_t L, int H, int HK, int Dh, int T,
+                      int NS, float scale, void* dkv_edge, float* domega_part, hipStream_t stream);
+/* Sums the per-edge rows per distinct chapter following the plan's inverted index (the
+ * reference accumulates per chapter with its inverted-index kernel,
+ * kernels-final/kernel_v4.py:534-671): dkv [max_u * 64][row_elems] (dtype); rows of unused
+ * plan slots are written as zero.  Fixed summation order (deterministic). */
+int moc_dkv_reduce(int dtype, const void* dkv_edge, const int32_t* n_uniq, const int32_t* csr_off,
+                   const int32_t* csr_edge, int64_t max_u, int64_t row_elems, void* dkv, hipStream_t stream);
 
 /* Gathered (and normalised) rows X [max_u * T][d] in dtype for the weight-gradient GEMM
  * dWkv = dkv^T X; rows of unused plan slots are zero. */

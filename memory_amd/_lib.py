@@ -46,10 +46,11 @@ _SIGS = {
     "moc_row_stats": (_I, [_P, _I, _I64, _I, _P, _P, _I64, _I, _F, _P, _P, _P]),
     "moc_kv_project": (_I, [_I, _P, _I, _I64, _I, _P, _P, _I64, _P, _P, _P, _I, _I, _P, _P, _P]),
     "moc_xattn_fwd": (_I, [_I, _P, _P, _P, _P, _P, _I64, _I64, _I, _I, _I, _I, _I, _F, _P, _P, _P]),
-    "moc_xattn_bwd_prep": (_I, [_I, _P, _P, _I64, _I64, _I, _I, _P, _P]),
+    "moc_xattn_bwd_prep": (_I, [_I, _P, _P, _P, _I64, _I64, _I, _I, _P, _P, _P, _P]),
     "moc_xattn_bwd_dq": (_I, [_I, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I, _I, _I, _I, _I, _F, _P, _P]),
-    "moc_xattn_bwd_dkv": (_I, [_I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I, _I, _I, _I, _I, _F,
+    "moc_xattn_bwd_dkv": (_I, [_I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I, _I, _I, _I, _I, _F,
                                _P, _P, _P]),
+    "moc_dkv_reduce": (_I, [_I, _P, _P, _P, _P, _I64, _I64, _P, _P]),
     "moc_gather_rows": (_I, [_I, _P, _I, _I64, _I, _P, _P, _I64, _P, _P, _P, _P]),
     "moc_bank_scatter": (_I, [_I, _P, _P, _I, _I64, _I, _P, _P, _I64, _P, _P, _I, _P, _P]),
 }
@@ -89,8 +90,22 @@ def lib():
     return _lib
 
 
+# Optional per-entry-point GPU timing: when set to a dict, every call records a
+# pair of events on the current stream, appended to KERNEL_EVENTS[name].
+KERNEL_EVENTS = None
+
+
 def call(name: str, *args) -> None:
-    rc = getattr(lib(), name)(*args)
+    ev = KERNEL_EVENTS
+    if ev is not None:
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        rc = getattr(lib(), name)(*args)
+        e1.record()
+        ev.setdefault(name, []).append((e0, e1))
+    else:
+        rc = getattr(lib(), name)(*args)
     if rc != MOC_OK:
         msg = lib().moc_last_error().decode(errors="replace")
         if rc in (MOC_ERR_ARG, MOC_ERR_UNSUPPORTED):

@@ -93,28 +93,28 @@ __global__ __launch_bounds__(1024) void plan_scan_kernel(const int32_t* __restri
   if (tid == 0) { n_uniq[0] = carry[1]; n_uniq[1] = (int32_t)(E - carry[0]); csr_off[carry[1]] = carry[0]; }
 }
 
-// Stable placement: block g walks its edges in order (one lane), cursor in LDS.
+// Stable placement: an edge's position is its chapter's start, plus the
+// edges of that chapter in earlier blocks, plus the edges of that chapter
+// earlier in this block (counted from an LDS copy of the block's ids).
 __global__ __launch_bounds__(256) void plan_place_kernel(const int32_t* __restrict__ chap, int64_t E, int64_t C,
                                                          const int32_t* __restrict__ counts,
                                                          const int32_t* __restrict__ start,
                                                          const int32_t* __restrict__ uid,
                                                          int32_t* __restrict__ edge_u, int32_t* __restrict__ csr_edge) {
-  extern __shared__ int32_t cur[];
+  __shared__ int32_t ids[kPlanEdgesPerBlock];
   const int g = blockIdx.x;
   const int64_t e0 = (int64_t)g * kPlanEdgesPerBlock;
-  const int64_t e1 = min(E, e0 + kPlanEdgesPerBlock);
-  // Only chapters touched by this block need a cursor; initialise them all (C is LDS-bounded).
-  for (int64_t c = threadIdx.x; c < C; c += 256) cur[c] = start[c] + counts[(int64_t)g * C + c];
+  const int n = (int)min((int64_t)kPlanEdgesPerBlock, E - e0);
+  for (int i = threadIdx.x; i < n; i += 256) ids[i] = chap[e0 + i];
   __syncthreads();
-  for (int64_t e = e0 + threadIdx.x; e < e1; e += 256) {
-    const int32_t c = chap[e];
-    edge_u[e] = (c >= 0 && c < C) ? uid[c] : -1;
-  }
-  if (threadIdx.x == 0) {
-    for (int64_t e = e0; e < e1; ++e) {
-      const int32_t c = chap[e];
-      if (c >= 0 && c < C) csr_edge[cur[c]++] = (int32_t)e;
-    }
+  for (int i = threadIdx.x; i < n; i += 256) {
+    const int32_t c = ids[i];
+    const bool ok = c >= 0 && c < C;
+    edge_u[e0 + i] = ok ? uid[c] : -1;
+    if (!ok) continue;
+    int before = 0;
+    for (int j = 0; j < i; ++j) before += ids[j] == c;
+    csr_edge[start[c] + counts[(int64_t)g * C + c] + before] = (int32_t)(e0 + i);
   }
 }
 
@@ -144,7 +144,7 @@ int moc_chapter_plan(const int32_t* chap, int64_t E, int64_t C, void* workspace,
   int32_t* total = counts + (int64_t)G * C;
   int32_t* start = total + C;
   int32_t* uid = start + C;
-  const size_t lds = (size_t)C * sizeof(int32_t);
+  const size_t lds = (size_t)C * sizeof(int32_t);  // histogram of plan_hist_kernel
   hipLaunchKernelGGL(plan_hist_kernel, dim3(G), dim3(256), lds, stream, chap, E, C, counts);
   int rc = check_launch("plan_hist_kernel");
   if (rc) return rc;
@@ -152,7 +152,7 @@ int moc_chapter_plan(const int32_t* chap, int64_t E, int64_t C, void* workspace,
   if ((rc = check_launch("plan_colscan_kernel"))) return rc;
   hipLaunchKernelGGL(plan_scan_kernel, dim3(1), dim3(1024), 0, stream, total, C, E, start, uid, uniq, csr_off, n_uniq);
   if ((rc = check_launch("plan_scan_kernel"))) return rc;
-  hipLaunchKernelGGL(plan_place_kernel, dim3(G), dim3(256), lds, stream, chap, E, C, counts, start, uid, edge_u, csr_edge);
+  hipLaunchKernelGGL(plan_place_kernel, dim3(G), dim3(256), 0, stream, chap, E, C, counts, start, uid, edge_u, csr_edge);
   return check_launch("plan_place_kernel");
 }
 

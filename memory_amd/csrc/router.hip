@@ -360,19 +360,32 @@ __global__ __launch_bounds__(256) void router_linear_dw_kernel(const float* __re
   }
 }
 
+// dx partials: each thread owns one column j and up to kDxRows rows; W is read
+// once per row-chunk.  grid (ceil(d/256), nsplit over C, ceil(R/kDxRows)).
+constexpr int kDxRows = 16;
 template <typename TW>
 __global__ __launch_bounds__(256) void router_linear_dx_partial_kernel(const float* __restrict__ dz, const TW* __restrict__ W,
                                                                        int64_t R, int64_t d, int64_t C, int c_per_split,
                                                                        float* __restrict__ part) {
   const int64_t j = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const int64_t r = blockIdx.y;
-  const int split = blockIdx.z;
+  const int split = blockIdx.y;
+  const int64_t r0 = (int64_t)blockIdx.z * kDxRows;
+  const int nr = (int)min((int64_t)kDxRows, R - r0);
   if (j >= d) return;
   const int64_t c0 = (int64_t)split * c_per_split;
   const int64_t c1 = min(C, c0 + c_per_split);
-  float acc = 0.f;
-  for (int64_t c = c0; c < c1; ++c) acc += dz[r * C + c] * to_f(W[c * d + j]);
-  part[((int64_t)split * R + r) * d + j] = acc;
+  float acc[kDxRows];
+#pragma unroll
+  for (int r = 0; r < kDxRows; ++r) acc[r] = 0.f;
+  for (int64_t c = c0; c < c1; ++c) {
+    const float wv = to_f(W[c * d + j]);
+#pragma unroll
+    for (int r = 0; r < kDxRows; ++r)
+      if (r < nr) acc[r] += dz[(r0 + r) * C + c] * wv;
+  }
+#pragma unroll
+  for (int r = 0; r < kDxRows; ++r)
+    if (r < nr) part[((int64_t)split * R + r0 + r) * d + j] = acc[r];
 }
 
 }  // namespace moc
@@ -487,7 +500,7 @@ int moc_router_linear_bwd(const float* dz, const float* x, int64_t R, int64_t d,
     MOC_REQUIRE(workspace && workspace_bytes >= moc_router_linear_bwd_workspace(R, d, C), MOC_ERR_ARG,
                 "moc_router_linear_bwd: workspace too small");
     int nsplit = (int)((C + 127) / 128);
-    dim3 grid((unsigned)((d + 255) / 256), (unsigned)R, (unsigned)nsplit);
+    dim3 grid((unsigned)((d + 255) / 256), (unsigned)nsplit, (unsigned)((R + kDxRows - 1) / kDxRows));
     float* part = (float*)workspace;
     if (w_dtype == MOC_F32)
       hipLaunchKernelGGL(router_linear_dx_partial_kernel<float>, grid, dim3(256), 0, stream, dz, (const float*)W, R, d, C, 128, part);

@@ -24,25 +24,54 @@ constexpr int kBThreads = 256;
 constexpr int kBDh = 64;
 constexpr int kBT = 64;
 
-// delta[b, h, i] = sum_d dO[b, i, h, d] * O[b, i, h, d]; 16 lanes per row.
+// Backward pre-pass, one workgroup per (64-query block, head, sequence):
+//   delta[b, h, i] = dO_i . O_i
+//   qt[b, h, :, i] = Q[b, i, h, :]     dot[b, h, :, i] = dO[b, i, h, :]
+// Rows of delta / qt / dot have stride Lp = round_up(L, 128); padded entries are 0.
+// The transposed copies give the dK/dV kernel its query-major MFMA operands as
+// plain 8-byte loads.
 template <typename T>
-__global__ __launch_bounds__(256) void xattn_bwd_prep_kernel(const T* __restrict__ out, const T* __restrict__ dout,
-                                                             int64_t rows, int L, int H, float* __restrict__ delta) {
-  const int64_t r = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
-  const int sub = threadIdx.x & 15;
-  float acc = 0.f;
-  if (r < rows) {
-    const T* o = out + r * kBDh + 4 * sub;
-    const T* d = dout + r * kBDh + 4 * sub;
-#pragma unroll
-    for (int x = 0; x < 4; ++x) acc += to_f(o[x]) * to_f(d[x]);
+__global__ __launch_bounds__(256) void xattn_bwd_prep_kernel(const T* __restrict__ q, const T* __restrict__ out,
+                                                             const T* __restrict__ dout, int L, int Lp, int H,
+                                                             float* __restrict__ delta, T* __restrict__ qt,
+                                                             T* __restrict__ dot) {
+  __shared__ T tq[64][66];
+  __shared__ T td[64][66];
+  const int q0 = blockIdx.x * 64, h = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x;
+  for (int i = tid; i < 64 * 64; i += 256) {
+    const int qq = i >> 6, dd = i & 63;
+    const int qi = q0 + qq;
+    T vq = from_f<T>(0.f), vd = from_f<T>(0.f);
+    if (qi < L) {
+      const size_t off = ((size_t)(b * (size_t)L + qi) * H + h) * kBDh + dd;
+      vq = q[off];
+      vd = dout[off];
+    }
+    tq[qq][dd] = vq;
+    td[qq][dd] = vd;
   }
+  // delta: 4 threads per query, 16 dims each
+  {
+    const int qq = tid >> 2, part = tid & 3;
+    const int qi = q0 + qq;
+    float acc = 0.f;
+    if (qi < L) {
+      const T* o = out + ((size_t)(b * (size_t)L + qi) * H + h) * kBDh + 16 * part;
+      const T* d = dout + ((size_t)(b * (size_t)L + qi) * H + h) * kBDh + 16 * part;
 #pragma unroll
-  for (int s = 8; s >= 1; s >>= 1) acc += __shfl_xor(acc, s, 16);
-  if (r < rows && sub == 0) {
-    const int64_t h = r % H, bi = r / H;
-    const int64_t i = bi % L, b = bi / L;
-    delta[(b * H + h) * L + i] = acc;
+      for (int x = 0; x < 16; ++x) acc += to_f(o[x]) * to_f(d[x]);
+    }
+    acc += __shfl_xor(acc, 1, 4);
+    acc += __shfl_xor(acc, 2, 4);
+    if (part == 0) delta[((size_t)b * H + h) * Lp + qi] = acc;
+  }
+  __syncthreads();
+  const size_t base = ((size_t)b * H + h) * kBDh;
+  for (int i = tid; i < 64 * 64; i += 256) {
+    const int dd = i >> 6, qq = i & 63;
+    qt[(base + dd) * Lp + q0 + qq] = tq[qq][dd];
+    dot[(base + dd) * Lp + q0 + qq] = td[qq][dd];
   }
 }
 
@@ -63,6 +92,7 @@ __global__ __launch_bounds__(kBThreads) void xattn_bwd_dq_kernel(
   const int b = blockIdx.z, h = blockIdx.y;
   const int hk = h / (H / HK);
   const int q0 = blockIdx.x * 128;
+  const int Lp = (int)gridDim.x * 128;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 4, c16 = lane & 15;
 
@@ -78,8 +108,8 @@ __global__ __launch_bounds__(kBThreads) void xattn_bwd_dq_kernel(
       qf[qb][ks] = ok ? Load8<T, T>::run(q + row + 32 * ks + 8 * g) : zero_frag<T>();
       dof[qb][ks] = ok ? Load8<T, T>::run(dout + row + 32 * ks + 8 * g) : zero_frag<T>();
     }
-    lse2[qb] = ok ? lse[((size_t)b * H + h) * L + qi] : INFINITY;
-    dl[qb] = ok ? delta[((size_t)b * H + h) * L + qi] : 0.f;
+    lse2[qb] = ok ? lse[((size_t)b * H + h) * Lp + qi] : INFINITY;
+    dl[qb] = ok ? delta[((size_t)b * H + h) * Lp + qi] : 0.f;
   }
   f32x4 acc[2][4];
 #pragma unroll
@@ -170,54 +200,60 @@ __global__ __launch_bounds__(kBThreads) void xattn_bwd_dq_kernel(
     }
 }
 
-// dk/dv: one workgroup per (distinct chapter u, kv head hk); walks the edges of
-// u in csr order and, for each, the G query heads of hk and all L queries of
-// the edge's sequence in steps of 128 (4 waves x 32 queries).  K and V of the
-// chapter stay in registers; Q^T and dO^T of the step are staged in LDS.
-template <typename T>
-__global__ __launch_bounds__(kBThreads, 1) void xattn_bwd_dkv_kernel(
-    const T* __restrict__ q, const T* __restrict__ ktiles, const T* __restrict__ vtiles,
-    const float* __restrict__ omega, const T* __restrict__ dout, const float* __restrict__ lse,
-    const float* __restrict__ delta, const int32_t* __restrict__ n_uniq, const int32_t* __restrict__ csr_off,
-    const int32_t* __restrict__ csr_edge, int L, int H, int HK, int NS, float scale_log2, float scale,
-    T* __restrict__ dkv, float* __restrict__ domega_part) {
-  typedef typename Frag<T>::type F8;
-  constexpr int QS = 128;
-  using TileQ = SwzTile<T, QS>;             // [64 dims][128 queries]
-  constexpr int STAGE = kBDh * QS * (int)sizeof(T);
-  constexpr int SMEM = 2 * STAGE > 32768 ? 2 * STAGE : 32768;
-  __shared__ __attribute__((aligned(16))) char smem[SMEM];
-  __shared__ float red[kBThreads / 64];
-  char* sQt = smem;
-  char* sDt = smem + STAGE;
+// dk/dv, slot-group decomposition.  One workgroup = one (sequence b, kv head
+// hk, group of SG consecutive slots); wave w owns slot SG*blockIdx.x + w, i.e.
+// the 64 keys of one selected chapter, whose K and V tiles sit in LDS.  All
+// slots of a sequence attend the same queries, so the query-side tiles of a
+// step (Q and dO row-major, Q^T and dO^T, QS queries each) are staged in LDS
+// once and shared by the SG waves.  Global loads of step n+1 are issued before
+// the math of step n.  Output: per-edge dk / dv rows (edge e = b*NS + slot),
+// summed per distinct chapter by dkv_reduce_kernel.
+template <typename T> struct DkvCfg;
+template <> struct DkvCfg<bf16> { static constexpr int SG = 4, QS = 64; };
+template <> struct DkvCfg<float> { static constexpr int SG = 2, QS = 32; };
 
-  const int u = blockIdx.x, hk = blockIdx.y;
+template <typename T>
+__global__ __launch_bounds__(64 * DkvCfg<T>::SG, 1) void xattn_bwd_dkv_kernel(
+    const T* __restrict__ q, const T* __restrict__ qt, const T* __restrict__ dout, const T* __restrict__ dot,
+    const T* __restrict__ ktiles, const T* __restrict__ vtiles, const int32_t* __restrict__ slot_u,
+    const float* __restrict__ omega, const float* __restrict__ lse, const float* __restrict__ delta, int L, int Lp,
+    int H, int HK, int NS, float scale_log2, float scale, T* __restrict__ dkv_edge, float* __restrict__ domega_part) {
+  typedef typename Frag<T>::type F8;
+  constexpr int SG = DkvCfg<T>::SG, QS = DkvCfg<T>::QS, NT = 64 * SG;
+  constexpr int EPC = 16 / (int)sizeof(T);
+  using TileK = SwzTile<T, 64>;   // [key][dim] and [query][dim]
+  using TileT = SwzTile<T, QS>;   // [dim][query]
+  constexpr int KVB = 64 * 64 * (int)sizeof(T);
+  constexpr int STB = 64 * QS * (int)sizeof(T);  // one staged tile (always 8 KB)
+  constexpr int NCH = 4 * STB / 16 / NT;         // staged chunks per thread per step
+  __shared__ __attribute__((aligned(16))) char sKV[SG][2][KVB];
+  __shared__ __attribute__((aligned(16))) char sQ[STB], sD[STB], sQt[STB], sDt[STB];
+  __shared__ float sL[QS], sDl[QS];
+
+  const int b = blockIdx.z, hk = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 4, c16 = lane & 15;
-  const int KV = HK * kBDh;
-  const size_t row_stride = 2 * (size_t)KV;
-  if (u >= n_uniq[0]) {
-    // rows of unused plan slots are zero so that GEMMs over all slots stay exact
-    for (int i = tid; i < kBT * kBDh; i += kBThreads) {
-      const int key = i / kBDh, dim = i % kBDh;
-      T* rowp = dkv + ((size_t)u * kBT + key) * row_stride;
-      rowp[hk * kBDh + dim] = from_f<T>(0.f);
-      rowp[KV + hk * kBDh + dim] = from_f<T>(0.f);
-    }
-    return;
-  }
+  const int slot = SG * blockIdx.x + wave;
+  const int e = b * NS + slot;
+  const int u = slot < NS ? slot_u[e] : -1;
+  const bool active = u >= 0;
   const int G = H / HK;
+  const int KV = HK * 64;
+  const size_t row_stride = 2 * (size_t)KV;
 
-  const T* Kt = ktiles + ((size_t)u * HK + hk) * (kBT * kBDh);
-  const T* Vt = vtiles + ((size_t)u * HK + hk) * (kBT * kBDh);
-  F8 kf[4][2], vf[4][2];
-#pragma unroll
-  for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      kf[kb][ks] = Load8<T, T>::run(Kt + (16 * kb + c16) * kBDh + 32 * ks + 8 * g);
-      vf[kb][ks] = Load8<T, T>::run(Vt + (16 * kb + c16) * kBDh + 32 * ks + 8 * g);
+  // K and V of this wave's chapter -> LDS (each wave loads its own pair)
+  if (active) {
+    const T* kp = ktiles + ((size_t)u * HK + hk) * 4096;
+    const T* vp = vtiles + ((size_t)u * HK + hk) * 4096;
+    for (int i = lane; i < 64 * (64 / EPC); i += 64) {
+      const int row = i / (64 / EPC), cc = (i % (64 / EPC)) * EPC;
+      st16(sKV[wave][0] + TileK::off(row, cc), ld16(kp + (size_t)i * EPC));
+      st16(sKV[wave][1] + TileK::off(row, cc), ld16(vp + (size_t)i * EPC));
     }
+  }
+  const float w = active ? omega[e] : 0.f;
+  const float c = w * scale_log2, dsc = w * scale;
+
   f32x4 dk[4][4], dv[4][4];
 #pragma unroll
   for (int kb = 0; kb < 4; ++kb)
@@ -227,174 +263,209 @@ __global__ __launch_bounds__(kBThreads, 1) void xattn_bwd_dkv_kernel(
       dv[kb][db] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
 
-  constexpr int EPC = 16 / (int)sizeof(T);
-  constexpr int CPR = kBDh / EPC;
-  constexpr int NCH = (QS * CPR) / kBThreads;  // chunks of each of Q and dO per thread per step
-
-  const int p0 = csr_off[u], p1 = csr_off[u + 1];
-  for (int p = p0; p < p1; ++p) {
-    const int e = csr_edge[p];
-    const int b = e / NS;
-    const float w = omega[e];
-    const float c = w * scale_log2;
-    const float dsc = w * scale;
-    for (int hq = hk * G; hq < hk * G + G; ++hq) {
-      float dwp = 0.f;
-      const size_t lrow = ((size_t)b * H + hq) * L;
-      for (int q0 = 0; q0 < L; q0 += QS) {
-        // stage Q^T and dO^T (transposed) for queries q0 .. q0+127
+  const int nstep = (L + QS - 1) / QS;
+  for (int hq = hk * G; hq < hk * G + G; ++hq) {
+    const size_t bh = (size_t)b * H + hq;
+    // staged chunk c of a step: tile = c / (STB/16); within tile: row / col chunk
+    V16 pre[NCH];
+    float preL = 0.f, preD = 0.f;
+    auto fetch = [&](int st) {
+      const int q0 = st * QS;
 #pragma unroll
-        for (int i = 0; i < NCH; ++i) {
-          const int ch = tid + kBThreads * i;
-          const int qq = ch / CPR, d0 = (ch % CPR) * EPC;
+      for (int i = 0; i < NCH; ++i) {
+        const int ch = tid + NT * i;
+        const int tile = ch / (STB / 16), r = ch % (STB / 16);
+        if (tile < 2) {  // Q / dO rows: [query][dim], 64/EPC chunks per row
+          const int qq = r / (64 / EPC), cc = (r % (64 / EPC)) * EPC;
           const int qi = q0 + qq;
-          V16 vq, vd;
-          if (qi < L) {
-            const size_t off = ((size_t)(b * (size_t)L + qi) * H + hq) * kBDh + d0;
-            vq = ld16(q + off);
-            vd = ld16(dout + off);
-          } else {
-            vq = V16{{0u, 0u, 0u, 0u}};
-            vd = vq;
-          }
-          const T* tq = reinterpret_cast<const T*>(&vq);
-          const T* td = reinterpret_cast<const T*>(&vd);
-#pragma unroll
-          for (int x = 0; x < EPC; ++x) {
-            *reinterpret_cast<T*>(sQt + TileQ::off(d0 + x, qq)) = tq[x];
-            *reinterpret_cast<T*>(sDt + TileQ::off(d0 + x, qq)) = td[x];
-          }
+          const T* src = tile == 0 ? q : dout;
+          pre[i] = qi < L ? ld16(src + ((size_t)(b * (size_t)L + qi) * H + hq) * 64 + cc) : V16{{0u, 0u, 0u, 0u}};
+        } else {         // Q^T / dO^T: [dim][query], QS/EPC chunks per row
+          const int dd = r / (QS / EPC), cc = (r % (QS / EPC)) * EPC;
+          const T* src = tile == 2 ? qt : dot;
+          pre[i] = ld16(src + (bh * 64 + dd) * Lp + q0 + cc);
         }
-        // A-operand fragments (row = query) straight from global
-        F8 qa[2][2], da[2][2];
-        float l2[2][4], dl[2][4];
+      }
+      if (tid < QS) {
+        preL = lse[bh * Lp + q0 + tid];
+        preD = delta[bh * Lp + q0 + tid];
+      }
+    };
+    auto stash = [&]() {
 #pragma unroll
-        for (int qb = 0; qb < 2; ++qb) {
-          const int qi = q0 + 32 * wave + 16 * qb + c16;
-          const bool ok = qi < L;
-          const size_t off = ((size_t)(b * (size_t)L + qi) * H + hq) * kBDh;
-#pragma unroll
-          for (int ks = 0; ks < 2; ++ks) {
-            qa[qb][ks] = ok ? Load8<T, T>::run(q + off + 32 * ks + 8 * g) : zero_frag<T>();
-            da[qb][ks] = ok ? Load8<T, T>::run(dout + off + 32 * ks + 8 * g) : zero_frag<T>();
-          }
-#pragma unroll
-          for (int x = 0; x < 4; ++x) {
-            const int qr = q0 + 32 * wave + 16 * qb + 4 * g + x;
-            l2[qb][x] = qr < L ? lse[lrow + qr] : INFINITY;
-            dl[qb][x] = qr < L ? delta[lrow + qr] : 0.f;
-          }
+      for (int i = 0; i < NCH; ++i) {
+        const int ch = tid + NT * i;
+        const int tile = ch / (STB / 16), r = ch % (STB / 16);
+        if (tile < 2) {
+          const int qq = r / (64 / EPC), cc = (r % (64 / EPC)) * EPC;
+          st16((tile == 0 ? sQ : sD) + TileK::off(qq, cc), pre[i]);
+        } else {
+          const int dd = r / (QS / EPC), cc = (r % (QS / EPC)) * EPC;
+          st16((tile == 2 ? sQt : sDt) + TileT::off(dd, cc), pre[i]);
         }
-        // S = Q K^T and dPu = dO V^T: rows = queries 4g+x of block qb, column = key 16kb + c16
-        f32x4 sc[2][4], dp[2][4];
+      }
+      if (tid < QS) { sL[tid] = preL; sDl[tid] = preD; }
+    };
+    float dwp = 0.f;
+    fetch(0);
+    for (int st = 0; st < nstep; ++st) {
+      __syncthreads();  // previous step's readers are done (and K/V visible on the first step)
+      stash();
+      __syncthreads();
+      if (st + 1 < nstep) fetch(st + 1);
+      if (active) {
 #pragma unroll
-        for (int qb = 0; qb < 2; ++qb)
-#pragma unroll
-          for (int kb = 0; kb < 4; ++kb) {
-            sc[qb][kb] = f32x4{0.f, 0.f, 0.f, 0.f};
-            dp[qb][kb] = f32x4{0.f, 0.f, 0.f, 0.f};
-          }
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks)
+        for (int half = 0; half < QS / 32; ++half) {
+          const int qb0 = 32 * half;
+          f32x4 sc[2][4], dp[2][4];
 #pragma unroll
           for (int qb = 0; qb < 2; ++qb)
 #pragma unroll
             for (int kb = 0; kb < 4; ++kb) {
-              mma(sc[qb][kb], qa[qb][ks], kf[kb][ks]);
-              mma(dp[qb][kb], da[qb][ks], vf[kb][ks]);
+              sc[qb][kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+              dp[qb][kb] = f32x4{0.f, 0.f, 0.f, 0.f};
             }
-        // P^T (scaled by omega) and dS^T (scaled by omega*scale) as A operands: row = key
-        F8 pa[4], sa[4];
 #pragma unroll
-        for (int qb = 0; qb < 2; ++qb)
+          for (int ks = 0; ks < 2; ++ks) {
+            F8 qa[2], da[2];
 #pragma unroll
-          for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-            for (int x = 0; x < 4; ++x) {
-              const float sraw = sc[qb][kb][x];
-              const float pr = exp2f(sraw * c - l2[qb][x]);
-              const float dpu = dp[qb][kb][x];
-              const float ds = pr * (w * dpu - dl[qb][x]);
-              dwp += ds * sraw * scale + pr * dpu;
-              pa[kb][4 * qb + x] = from_f<T>(pr * w);
-              sa[kb][4 * qb + x] = from_f<T>(ds * dsc);
+            for (int qb = 0; qb < 2; ++qb) {
+              qa[qb] = TileK::frag(sQ, qb0 + 16 * qb + c16, 32 * ks + 8 * g);
+              da[qb] = TileK::frag(sD, qb0 + 16 * qb + c16, 32 * ks + 8 * g);
             }
-        __syncthreads();  // staged Q^T / dO^T visible
 #pragma unroll
-        for (int db = 0; db < 4; ++db) {
-          F8 bq = TileQ::frag44(sQt, 16 * db + c16, 32 * wave + 4 * g, 32 * wave + 16 + 4 * g);
-          F8 bd = TileQ::frag44(sDt, 16 * db + c16, 32 * wave + 4 * g, 32 * wave + 16 + 4 * g);
+            for (int kb = 0; kb < 4; ++kb) {
+              F8 kf = TileK::frag(sKV[wave][0], 16 * kb + c16, 32 * ks + 8 * g);
+              F8 vf = TileK::frag(sKV[wave][1], 16 * kb + c16, 32 * ks + 8 * g);
 #pragma unroll
-          for (int kb = 0; kb < 4; ++kb) {
-            mma(dv[kb][db], pa[kb], bd);
-            mma(dk[kb][db], sa[kb], bq);
+              for (int qb = 0; qb < 2; ++qb) {
+                mma(sc[qb][kb], qa[qb], kf);
+                mma(dp[qb][kb], da[qb], vf);
+              }
+            }
+          }
+          F8 pa[4], sa[4];
+#pragma unroll
+          for (int qb = 0; qb < 2; ++qb) {
+            const f32x4 l2 = *reinterpret_cast<const f32x4*>(&sL[qb0 + 16 * qb + 4 * g]);
+            const f32x4 dl = *reinterpret_cast<const f32x4*>(&sDl[qb0 + 16 * qb + 4 * g]);
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+              for (int x = 0; x < 4; ++x) {
+                const float sraw = sc[qb][kb][x];
+                const float pr = exp2f(sraw * c - l2[x]);
+                const float dpu = dp[qb][kb][x];
+                const float ds = pr * (w * dpu - dl[x]);
+                dwp += ds * sraw * scale + pr * dpu;
+                pa[kb][4 * qb + x] = from_f<T>(pr * w);
+                sa[kb][4 * qb + x] = from_f<T>(ds * dsc);
+              }
+          }
+#pragma unroll
+          for (int db = 0; db < 4; ++db) {
+            F8 bq = TileT::frag44(sQt, 16 * db + c16, qb0 + 4 * g, qb0 + 16 + 4 * g);
+            F8 bd = TileT::frag44(sDt, 16 * db + c16, qb0 + 4 * g, qb0 + 16 + 4 * g);
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb) {
+              mma(dv[kb][db], pa[kb], bd);
+              mma(dk[kb][db], sa[kb], bq);
+            }
           }
         }
-        __syncthreads();  // before the next step overwrites the stage
       }
-      // domega partial of (edge, query head)
+    }
+    if (active) {
       dwp = wave_sum(dwp);
-      if (lane == 0) red[wave] = dwp;
-      __syncthreads();
-      if (tid == 0) domega_part[(size_t)e * H + hq] = red[0] + red[1] + red[2] + red[3];
-      __syncthreads();
+      if (lane == 0) domega_part[(size_t)e * H + hq] = dwp;
     }
   }
+  if (!active) return;
+  T* rows = dkv_edge + (size_t)e * 64 * row_stride;
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int x = 0; x < 4; ++x) {
+        const int key = 16 * kb + 4 * g + x, dim = 16 * db + c16;
+        rows[(size_t)key * row_stride + hk * 64 + dim] = from_f<T>(dk[kb][db][x]);
+        rows[(size_t)key * row_stride + KV + hk * 64 + dim] = from_f<T>(dv[kb][db][x]);
+      }
+}
 
-  // Cross-wave reduction of dk, dv (4 partial 64x64 fp32 tiles each) through LDS.
-  float* buf = reinterpret_cast<float*>(smem);  // holds 2 tiles (32 KB)
-  T* rows = dkv + (size_t)u * kBT * row_stride;
-  auto reduce_store = [&](f32x4 (&acc)[4][4], int col0) {
-    // round 1: waves 2,3 publish; waves 0,1 add
-    if (wave >= 2) {
-      float* t = buf + (wave - 2) * 4096;
+// dkv[u*T + t, :] = sum over the edges of distinct chapter u (csr order) of
+// dkv_edge[e*T + t, :]; zero rows for unused plan slots.  grid (max_u, kRedSplit):
+// each workgroup sums one slice of the chapter block in 16-byte chunks.
+constexpr int kRedSplit = 16;
+template <typename T>
+__global__ __launch_bounds__(256) void dkv_reduce_kernel(const T* __restrict__ dkv_edge,
+                                                         const int32_t* __restrict__ n_uniq,
+                                                         const int32_t* __restrict__ csr_off,
+                                                         const int32_t* __restrict__ csr_edge, int64_t row_elems,
+                                                         T* __restrict__ dkv) {
+  constexpr int EPC = 16 / (int)sizeof(T);
+  const int u = blockIdx.x;
+  const int64_t n = 64 * row_elems;     // elements of one chapter block
+  const int64_t nch = n / EPC;          // 16-byte chunks
+  const int64_t per = (nch + kRedSplit - 1) / kRedSplit;
+  const int64_t c0 = (int64_t)blockIdx.y * per, c1 = min(nch, c0 + per);
+  T* dst = dkv + (size_t)u * n;
+  if (u >= n_uniq[0]) {
+    for (int64_t i = c0 + threadIdx.x; i < c1; i += 256) st16(dst + i * EPC, V16{{0u, 0u, 0u, 0u}});
+    return;
+  }
+  const int p0 = csr_off[u], p1 = csr_off[u + 1];
+  if (p1 - p0 == 1) {
+    const T* src = dkv_edge + (size_t)csr_edge[p0] * n;
+    for (int64_t i = c0 + threadIdx.x; i < c1; i += 256) st16(dst + i * EPC, ld16(src + i * EPC));
+    return;
+  }
+  for (int64_t i = c0 + threadIdx.x; i < c1; i += 256) {
+    float acc[EPC];
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb)
+    for (int x = 0; x < EPC; ++x) acc[x] = 0.f;
+    for (int p = p0; p < p1; ++p) {
+      V16 v = ld16(dkv_edge + (size_t)csr_edge[p] * n + i * EPC);
+      const T* t = reinterpret_cast<const T*>(&v);
 #pragma unroll
-        for (int db = 0; db < 4; ++db)
-#pragma unroll
-          for (int x = 0; x < 4; ++x) t[(16 * kb + 4 * g + x) * 64 + 16 * db + c16] = acc[kb][db][x];
+      for (int x = 0; x < EPC; ++x) acc[x] += to_f(t[x]);
     }
-    __syncthreads();
-    if (wave < 2) {
-      const float* t = buf + wave * 4096;
+    T o[EPC];
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-        for (int db = 0; db < 4; ++db)
-#pragma unroll
-          for (int x = 0; x < 4; ++x) acc[kb][db][x] += t[(16 * kb + 4 * g + x) * 64 + 16 * db + c16];
-    }
-    __syncthreads();
-    // round 2: wave 1 publishes, wave 0 adds and writes the rows
-    if (wave == 1) {
-#pragma unroll
-      for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-        for (int db = 0; db < 4; ++db)
-#pragma unroll
-          for (int x = 0; x < 4; ++x) buf[(16 * kb + 4 * g + x) * 64 + 16 * db + c16] = acc[kb][db][x];
-    }
-    __syncthreads();
-    if (wave == 0) {
-#pragma unroll
-      for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-        for (int db = 0; db < 4; ++db)
-#pragma unroll
-          for (int x = 0; x < 4; ++x) {
-            const int key = 16 * kb + 4 * g + x, dim = 16 * db + c16;
-            rows[(size_t)key * row_stride + col0 + dim] = from_f<T>(acc[kb][db][x] + buf[key * 64 + dim]);
-          }
-    }
-    __syncthreads();
-  };
-  reduce_store(dk, hk * kBDh);
-  reduce_store(dv, KV + hk * kBDh);
+    for (int x = 0; x < EPC; ++x) o[x] = from_f<T>(acc[x]);
+    st16(dst + i * EPC, *reinterpret_cast<V16*>(o));
+  }
 }
 
 // X[r, :] = norm(bank[uniq[r / T] * T + r % T, :]) in the compute dtype; rows of
-// unused plan slots (r >= n_uniq * T) are zero.
+// unused plan slots (r >= n_uniq * T) are zero.  One wave per row, 16-byte chunks
+// (d % 8 == 0).
+template <typename TO, typename TI>
+__device__ __forceinline__ void load8f(const TI* p, float* o) {
+  if constexpr (sizeof(TI) == 2) {
+    bf16x8 v = *reinterpret_cast<const bf16x8*>(p);
+#pragma unroll
+    for (int x = 0; x < 8; ++x) o[x] = (float)v[x];
+  } else {
+    f32x4 a = *reinterpret_cast<const f32x4*>(p), c = *reinterpret_cast<const f32x4*>(p + 4);
+#pragma unroll
+    for (int x = 0; x < 4; ++x) { o[x] = a[x]; o[4 + x] = c[x]; }
+  }
+}
+template <typename TO>
+__device__ __forceinline__ void store8f(TO* p, const float* v) {
+  if constexpr (sizeof(TO) == 2) {
+    bf16x8 r;
+#pragma unroll
+    for (int x = 0; x < 8; ++x) r[x] = (bf16)v[x];
+    *reinterpret_cast<bf16x8*>(p) = r;
+  } else {
+    *reinterpret_cast<f32x4*>(p) = f32x4{v[0], v[1], v[2], v[3]};
+    *reinterpret_cast<f32x4*>(p + 4) = f32x4{v[4], v[5], v[6], v[7]};
+  }
+}
+
 template <typename T, typename TB>
 __global__ __launch_bounds__(256) void gather_rows_kernel(const TB* __restrict__ bank, int64_t d, int Tc,
                                                           const int32_t* __restrict__ uniq,
@@ -406,13 +477,21 @@ __global__ __launch_bounds__(256) void gather_rows_kernel(const TB* __restrict__
   if (r >= rows) return;
   const int64_t valid = (int64_t)n_uniq[0] * Tc;
   T* o = out + r * d;
+  float v[8];
   if (r >= valid) {
-    for (int64_t j = lane; j < d; j += 64) o[j] = from_f<T>(0.f);
+#pragma unroll
+    for (int x = 0; x < 8; ++x) v[x] = 0.f;
+    for (int64_t j = 8 * lane; j < d; j += 512) store8f<T>(o + j, v);
     return;
   }
-  const TB* x = bank + ((int64_t)uniq[r / Tc] * Tc + r % Tc) * d;
+  const TB* xr = bank + ((int64_t)uniq[r / Tc] * Tc + r % Tc) * d;
   const float mu = rstd ? mean[r] : 0.f, rs = rstd ? rstd[r] : 1.f;
-  for (int64_t j = lane; j < d; j += 64) o[j] = from_f<T>((to_f(x[j]) - mu) * rs);
+  for (int64_t j = 8 * lane; j < d; j += 512) {
+    load8f<T, TB>(xr + j, v);
+#pragma unroll
+    for (int x = 0; x < 8; ++x) v[x] = (v[x] - mu) * rs;
+    store8f<T>(o + j, v);
+  }
 }
 
 // grad_bank[src(r), :] = norm_bwd(dX[r, :]) for r < n_uniq * T.  Distinct
@@ -429,27 +508,36 @@ __global__ __launch_bounds__(256) void bank_scatter_kernel(const TX* __restrict_
   const int lane = threadIdx.x & 63;
   if (r >= rows || r >= (int64_t)n_uniq[0] * Tc) return;
   const int64_t src = (int64_t)uniq[r / Tc] * Tc + r % Tc;
-  const TX* g = dX + r * d;
+  const TX* gr = dX + r * d;
   TG* o = grad + src * d;
+  float gv[8];
   if (!rstd) {
-    for (int64_t j = lane; j < d; j += 64) o[j] = (TG)to_f(g[j]);
+    for (int64_t j = 8 * lane; j < d; j += 512) {
+      load8f<TG, TX>(gr + j, gv);
+      store8f<TG>(o + j, gv);
+    }
     return;
   }
-  const TB* x = bank + src * d;
+  const TB* xr = bank + src * d;
   const float mu = mean[r], rs = rstd[r];
-  float sg = 0.f, sgx = 0.f;
-  for (int64_t j = lane; j < d; j += 64) {
-    const float gv = to_f(g[j]);
-    const float xh = (to_f(x[j]) - mu) * rs;
-    sg += gv;
-    sgx += gv * xh;
+  float sg = 0.f, sgx = 0.f, xv[8];
+  for (int64_t j = 8 * lane; j < d; j += 512) {
+    load8f<TG, TX>(gr + j, gv);
+    load8f<TG, TB>(xr + j, xv);
+#pragma unroll
+    for (int x = 0; x < 8; ++x) {
+      sg += gv[x];
+      sgx += gv[x] * (xv[x] - mu) * rs;
+    }
   }
   sg = wave_sum(sg) / (float)d;
   sgx = wave_sum(sgx) / (float)d;
-  for (int64_t j = lane; j < d; j += 64) {
-    const float gv = to_f(g[j]);
-    const float xh = (to_f(x[j]) - mu) * rs;
-    o[j] = (TG)(rs * (gv - (layernorm ? sg : 0.f) - xh * sgx));
+  for (int64_t j = 8 * lane; j < d; j += 512) {
+    load8f<TG, TX>(gr + j, gv);
+    load8f<TG, TB>(xr + j, xv);
+#pragma unroll
+    for (int x = 0; x < 8; ++x) gv[x] = rs * (gv[x] - (layernorm ? sg : 0.f) - (xv[x] - mu) * rs * sgx);
+    store8f<TG>(o + j, gv);
   }
 }
 
@@ -459,19 +547,20 @@ using namespace moc;
 
 extern "C" {
 
-int moc_xattn_bwd_prep(int dtype, const void* out, const void* dout, int64_t B, int64_t L, int H, int Dh,
-                       float* delta, hipStream_t stream) {
-  MOC_REQUIRE(out && dout && delta, MOC_ERR_ARG, "moc_xattn_bwd_prep: null pointer");
+int moc_xattn_bwd_prep(int dtype, const void* q, const void* out, const void* dout, int64_t B, int64_t L, int H,
+                       int Dh, float* delta, void* qt, void* dot, hipStream_t stream) {
+  MOC_REQUIRE(q && out && dout && delta && qt && dot, MOC_ERR_ARG, "moc_xattn_bwd_prep: null pointer");
   MOC_REQUIRE(Dh == kBDh, MOC_ERR_UNSUPPORTED, "moc_xattn_bwd_prep: head_dim %d (needs 64)", Dh);
-  const int64_t rows = B * L * H;
-  if (rows == 0) return MOC_OK;
-  dim3 grid((unsigned)((rows + 15) / 16));
+  MOC_REQUIRE(B >= 0 && L >= 0 && H > 0 && B < 65536, MOC_ERR_ARG, "moc_xattn_bwd_prep: bad shape");
+  if (B == 0 || L == 0) return MOC_OK;
+  const int Lp = (int)((L + 127) / 128 * 128);
+  dim3 grid((unsigned)(Lp / 64), (unsigned)H, (unsigned)B);
   if (dtype == MOC_BF16)
-    hipLaunchKernelGGL(xattn_bwd_prep_kernel<bf16>, grid, dim3(256), 0, stream, (const bf16*)out, (const bf16*)dout,
-                       rows, (int)L, H, delta);
+    hipLaunchKernelGGL(xattn_bwd_prep_kernel<bf16>, grid, dim3(256), 0, stream, (const bf16*)q, (const bf16*)out,
+                       (const bf16*)dout, (int)L, Lp, H, delta, (bf16*)qt, (bf16*)dot);
   else if (dtype == MOC_F32)
-    hipLaunchKernelGGL(xattn_bwd_prep_kernel<float>, grid, dim3(256), 0, stream, (const float*)out, (const float*)dout,
-                       rows, (int)L, H, delta);
+    hipLaunchKernelGGL(xattn_bwd_prep_kernel<float>, grid, dim3(256), 0, stream, (const float*)q, (const float*)out,
+                       (const float*)dout, (int)L, Lp, H, delta, (float*)qt, (float*)dot);
   else
     return set_error(MOC_ERR_UNSUPPORTED, "moc_xattn_bwd_prep: dtype %d", dtype);
   return check_launch("xattn_bwd_prep_kernel");
@@ -500,36 +589,59 @@ int moc_xattn_bwd_dq(int dtype, const void* q, const void* k_tiles, const void* 
   return check_launch("xattn_bwd_dq_kernel");
 }
 
-int moc_xattn_bwd_dkv(int dtype, const void* q, const void* k_tiles, const void* v_tiles, const float* omega,
-                      const void* dout, const float* lse, const float* delta, const int32_t* n_uniq,
-                      const int32_t* csr_off, const int32_t* csr_edge, int64_t max_u, int64_t B, int64_t L, int H,
-                      int HK, int Dh, int T, int NS, float scale, void* dkv, float* domega_part,
-                      hipStream_t stream) {
-  MOC_REQUIRE(q && k_tiles && v_tiles && omega && dout && lse && delta && n_uniq && csr_off && csr_edge && dkv &&
+int moc_xattn_bwd_dkv(int dtype, const void* q, const void* qt, const void* dout, const void* dot,
+                      const void* k_tiles, const void* v_tiles, const int32_t* slot_u, const float* omega,
+                      const float* lse, const float* delta, int64_t B, int64_t L, int H, int HK, int Dh, int T,
+                      int NS, float scale, void* dkv_edge, float* domega_part, hipStream_t stream) {
+  MOC_REQUIRE(q && qt && dout && dot && k_tiles && v_tiles && slot_u && omega && lse && delta && dkv_edge &&
                   domega_part,
               MOC_ERR_ARG, "moc_xattn_bwd_dkv: null pointer");
   MOC_REQUIRE(Dh == kBDh && T == kBT, MOC_ERR_UNSUPPORTED, "moc_xattn_bwd_dkv: needs head_dim 64 and T 64");
-  MOC_REQUIRE(H > 0 && HK > 0 && H % HK == 0 && NS > 0 && max_u >= 0, MOC_ERR_ARG, "moc_xattn_bwd_dkv: bad shape");
-  if (max_u == 0) return MOC_OK;
-  dim3 grid((unsigned)max_u, (unsigned)HK);
+  MOC_REQUIRE(H > 0 && HK > 0 && H % HK == 0 && NS > 0 && B >= 0 && B < 65536, MOC_ERR_ARG,
+              "moc_xattn_bwd_dkv: bad shape");
+  if (B == 0 || L == 0) return MOC_OK;
+  const int Lp = (int)((L + 127) / 128 * 128);
   const float sl2 = scale * 1.4426950408889634f;
-  if (dtype == MOC_BF16)
-    hipLaunchKernelGGL(xattn_bwd_dkv_kernel<bf16>, grid, dim3(kBThreads), 0, stream, (const bf16*)q,
-                       (const bf16*)k_tiles, (const bf16*)v_tiles, omega, (const bf16*)dout, lse, delta, n_uniq, csr_off,
-                       csr_edge, (int)L, H, HK, NS, sl2, scale, (bf16*)dkv, domega_part);
-  else if (dtype == MOC_F32)
-    hipLaunchKernelGGL(xattn_bwd_dkv_kernel<float>, grid, dim3(kBThreads), 0, stream, (const float*)q,
-                       (const float*)k_tiles, (const float*)v_tiles, omega, (const float*)dout, lse, delta, n_uniq,
-                       csr_off, csr_edge, (int)L, H, HK, NS, sl2, scale, (float*)dkv, domega_part);
-  else
+  if (dtype == MOC_BF16) {
+    constexpr int SG = DkvCfg<bf16>::SG;
+    dim3 grid((unsigned)((NS + SG - 1) / SG), (unsigned)HK, (unsigned)B);
+    hipLaunchKernelGGL(xattn_bwd_dkv_kernel<bf16>, grid, dim3(64 * SG), 0, stream, (const bf16*)q, (const bf16*)qt,
+                       (const bf16*)dout, (const bf16*)dot, (const bf16*)k_tiles, (const bf16*)v_tiles, slot_u,
+                       omega, lse, delta, (int)L, Lp, H, HK, NS, sl2, scale, (bf16*)dkv_edge, domega_part);
+  } else if (dtype == MOC_F32) {
+    constexpr int SG = DkvCfg<float>::SG;
+    dim3 grid((unsigned)((NS + SG - 1) / SG), (unsigned)HK, (unsigned)B);
+    hipLaunchKernelGGL(xattn_bwd_dkv_kernel<float>, grid, dim3(64 * SG), 0, stream, (const float*)q,
+                       (const float*)qt, (const float*)dout, (const float*)dot, (const float*)k_tiles,
+                       (const float*)v_tiles, slot_u, omega, lse, delta, (int)L, Lp, H, HK, NS, sl2, scale,
+                       (float*)dkv_edge, domega_part);
+  } else {
     return set_error(MOC_ERR_UNSUPPORTED, "moc_xattn_bwd_dkv: dtype %d", dtype);
+  }
   return check_launch("xattn_bwd_dkv_kernel");
+}
+
+int moc_dkv_reduce(int dtype, const void* dkv_edge, const int32_t* n_uniq, const int32_t* csr_off,
+                   const int32_t* csr_edge, int64_t max_u, int64_t row_elems, void* dkv, hipStream_t stream) {
+  MOC_REQUIRE(dkv_edge && n_uniq && csr_off && csr_edge && dkv, MOC_ERR_ARG, "moc_dkv_reduce: null pointer");
+  MOC_REQUIRE(row_elems > 0 && row_elems % 8 == 0, MOC_ERR_ARG, "moc_dkv_reduce: row_elems %lld", (long long)row_elems);
+  if (max_u == 0) return MOC_OK;
+  if (dtype == MOC_BF16)
+    hipLaunchKernelGGL(dkv_reduce_kernel<bf16>, dim3((unsigned)max_u, kRedSplit), dim3(256), 0, stream, (const bf16*)dkv_edge,
+                       n_uniq, csr_off, csr_edge, row_elems, (bf16*)dkv);
+  else if (dtype == MOC_F32)
+    hipLaunchKernelGGL(dkv_reduce_kernel<float>, dim3((unsigned)max_u, kRedSplit), dim3(256), 0, stream, (const float*)dkv_edge,
+                       n_uniq, csr_off, csr_edge, row_elems, (float*)dkv);
+  else
+    return set_error(MOC_ERR_UNSUPPORTED, "moc_dkv_reduce: dtype %d", dtype);
+  return check_launch("dkv_reduce_kernel");
 }
 
 int moc_gather_rows(int dtype, const void* bank, int bank_dtype, int64_t d, int T, const int32_t* uniq,
                     const int32_t* n_uniq, int64_t max_u, const float* row_mean, const float* row_rstd, void* out,
                     hipStream_t stream) {
   MOC_REQUIRE(bank && uniq && n_uniq && out, MOC_ERR_ARG, "moc_gather_rows: null pointer");
+  MOC_REQUIRE(d % 8 == 0, MOC_ERR_UNSUPPORTED, "moc_gather_rows: d=%lld must be a multiple of 8", (long long)d);
   const int64_t rows = max_u * T;
   if (rows == 0) return MOC_OK;
   dim3 grid((unsigned)((rows + 3) / 4));
@@ -548,6 +660,7 @@ int moc_bank_scatter(int dx_dtype, const void* dX, const void* bank, int bank_dt
                      const int32_t* uniq, const int32_t* n_uniq, int64_t max_u, const float* row_mean,
                      const float* row_rstd, int norm, void* grad_bank, hipStream_t stream) {
   MOC_REQUIRE(dX && bank && uniq && n_uniq && grad_bank, MOC_ERR_ARG, "moc_bank_scatter: null pointer");
+  MOC_REQUIRE(d % 8 == 0, MOC_ERR_UNSUPPORTED, "moc_bank_scatter: d=%lld must be a multiple of 8", (long long)d);
   MOC_REQUIRE((norm == MOC_NORM_NONE) == (row_rstd == nullptr), MOC_ERR_ARG, "moc_bank_scatter: norm/stats mismatch");
   const int64_t rows = max_u * T;
   if (rows == 0) return MOC_OK;

@@ -157,6 +157,10 @@ __global__ __launch_bounds__(kFwdThreads) void xattn_fwd_kernel(
     __syncthreads();
   }
 
+  // lse rows have stride Lp = round_up(L, 128); padded entries hold +inf so
+  // that the backward's exp2(s - lse) is exactly 0 there (also for a row
+  // whose every slot was skipped).
+  const int Lp = (int)gridDim.x * 128;
 #pragma unroll
   for (int qb = 0; qb < 2; ++qb) {
     const float l = quad_sum(lpart[qb]);
@@ -168,8 +172,8 @@ __global__ __launch_bounds__(kFwdThreads) void xattn_fwd_kernel(
       for (int db = 0; db < 4; ++db)
 #pragma unroll
         for (int e = 0; e < 4; ++e) op[16 * db + 4 * g + e] = from_f<T>(o[db][qb][e] * inv);
-      if (g == 0) lse[((size_t)b * H + h) * L + qi] = l > 0.f ? m[qb] + log2f(l) : -INFINITY;
     }
+    if (g == 0) lse[((size_t)b * H + h) * Lp + qi] = (qi < L && l > 0.f) ? m[qb] + log2f(l) : INFINITY;
   }
 }
 

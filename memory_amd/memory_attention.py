@@ -1,0 +1,183 @@
+"""MemoryCrossAttention with the reference's module API, on libmoc kernels.
+
+Mirrors memory_transformer/memory_attention.py:45-898 for full-rank
+projections (q_proj/k_proj/v_proj/o_proj, bias-free, GQA-capable).  The
+projections of the query side and the output are plain GEMMs (nn.Linear); the
+memory side (gather, optional row norm, K/V projection of each distinct
+chapter, routed attention and its backward) runs in the HIP kernels.
+
+Three ways to call forward, all with the reference's return value
+``(output (B, L, hidden_dim), None)``:
+  * ``memory=`` a (N, d) or (B, N, d) tensor, N a multiple of 64: dense
+    attention over it (memory_attention.py:402-478).  The rows are treated as
+    64-row chapters of weight 1; a 2-D memory is projected once for the batch.
+  * ``routed_memory_state=`` the fused sequence-level path: the bank, the
+    selected chapters (shared prefix included) and their weights omega.  It
+    computes exactly the reference's gather -> (normalise) -> x omega ->
+    attention chain of memory_transformer/model.py:674-692 without
+    materialising the gathered memory.
+  * ``token_routing_state=`` the token-level path (memory_attention.py:480-716):
+    dense shared chapters plus routed chapters per token, combined MoE-style
+    (per-chapter softmax mixed by the router weights) or jointly.
+"""
+
+from __future__ import annotations
+
+from typing import Any, Dict, Optional, Tuple
+
+import torch
+import torch.nn as nn
+
+from . import ops
+from .token_routing_kernel import normalize_kernel_version
+
+try:
+    from torch.utils.checkpoint import checkpoint as torch_checkpoint
+except Exception:  # pragma: no cover
+    torch_checkpoint = None
+
+CHAPTER_TOKENS = 64  # chapter tile height of the kernels
+
+
+class MemoryCrossAttention(nn.Module):
+    def __init__(self, hidden_dim: int, num_heads: int, num_kv_heads: Optional[int] = None,
+                 memory_dim: Optional[int] = None, use_low_rank_projections: bool = False,
+                 projection_rank: Optional[int] = None, reduced_dim_mode: bool = False,
+                 reduced_dim: Optional[int] = None, wo_init_zero: bool = True, dropout: float = 0.0,
+                 use_flash_attention: bool = True, gradient_checkpointing: bool = False):
+        super().__init__()
+        self.hidden_dim = hidden_dim
+        self.memory_dim = memory_dim if memory_dim is not None else hidden_dim
+        self.num_heads = num_heads
+        self.num_kv_heads = num_heads if num_kv_heads is None else num_kv_heads
+        if self.num_heads <= 0:
+            raise ValueError(f"num_heads must be > 0, got {self.num_heads}")
+        if hidden_dim % num_heads != 0:
+            raise ValueError(f"hidden_dim ({hidden_dim}) must be divisible by num_heads ({num_heads})")
+        if self.num_kv_heads <= 0:
+            raise ValueError(f"num_kv_heads must be > 0, got {self.num_kv_heads}")
+        if self.num_heads % self.num_kv_heads != 0:
+            raise ValueError(f"num_heads ({self.num_heads}) must be divisible by num_kv_heads ({self.num_kv_heads})")
+        if use_low_rank_projections or reduced_dim_mode:
+            raise NotImplementedError(
+                "memory_amd implements the full-rank projections of MemoryCrossAttention; low-rank and "
+                "reduced-dim modes (memory_attention.py:150-207) are outside this build's scope")
+        if dropout and dropout > 0:
+            raise NotImplementedError("attention dropout is not implemented by the HIP kernels")
+        self.head_dim = hidden_dim // num_heads
+        self.kv_hidden_dim = self.num_kv_heads * self.head_dim
+        self.num_kv_groups = self.num_heads // self.num_kv_heads
+        self.scale = self.head_dim ** -0.5
+        self.dropout = dropout
+        self.use_flash_attention = use_flash_attention  # kept for API parity; the HIP path is always used
+        self.gradient_checkpointing = gradient_checkpointing
+        self.reduced_dim_mode = False
+        self.use_low_rank_projections = False
+        self.q_proj = nn.Linear(self.hidden_dim, self.hidden_dim, bias=False)
+        self.k_proj = nn.Linear(self.memory_dim, self.kv_hidden_dim, bias=False)
+        self.v_proj = nn.Linear(self.memory_dim, self.kv_hidden_dim, bias=False)
+        self.o_proj = nn.Linear(self.hidden_dim, self.hidden_dim, bias=False)
+        if wo_init_zero:
+            nn.init.zeros_(self.o_proj.weight)
+
+    # ------------------------------------------------------------------ helpers
+    def _project_output(self, attn_output: torch.Tensor) -> torch.Tensor:
+        return self.o_proj(attn_output)
+
+    def _queries(self, hidden_states: torch.Tensor) -> torch.Tensor:
+        B, L, _ = hidden_states.shape
+        return self.q_proj(hidden_states).view(B, L, self.num_heads, self.head_dim)
+
+    def _routed(self, hidden_states, bank, idx_star, omega, num_chapters, T, norm_type, eps):
+        B, L, _ = hidden_states.shape
+
+        def run(h):
+            q = self._queries(h)
+            a = ops.routed_attention(q, bank, self.k_proj.weight, self.v_proj.weight, omega, idx_star,
+                                     num_chapters=num_chapters, tokens_per_chapter=T, norm_type=norm_type, eps=eps,
+                                     num_kv_heads=self.num_kv_heads)
+            return a.reshape(B, L, self.hidden_dim)
+
+        if self.gradient_checkpointing and self.training and torch.is_grad_enabled() and torch_checkpoint:
+            return torch_checkpoint(run, hidden_states, use_reentrant=False)
+        return run(hidden_states)
+
+    def _dense_as_chapters(self, hidden_states: torch.Tensor, memory: torch.Tensor) -> torch.Tensor:
+        """Dense attention over `memory` via the routed kernels (64-row chapters, weight 1)."""
+        B = hidden_states.shape[0]
+        if memory.dim() not in (2, 3):
+            raise ValueError(f"memory must be (N, d) or (B, N, d), got {tuple(memory.shape)}")
+        N = memory.shape[-2]
+        if N % CHAPTER_TOKENS != 0:
+            raise ValueError(f"memory length {N} must be a multiple of {CHAPTER_TOKENS} for the HIP kernels")
+        per = N // CHAPTER_TOKENS
+        dev = hidden_states.device
+        if memory.dim() == 2:
+            bank = memory
+            idx = torch.arange(per, device=dev, dtype=torch.int32).expand(B, per)
+            C = per
+        else:
+            if memory.shape[0] != B:
+                raise ValueError("batched memory must have the batch size of hidden_states")
+            bank = memory.reshape(B * N, memory.shape[-1])
+            idx = (torch.arange(B, device=dev, dtype=torch.int32).view(B, 1) * per
+                   + torch.arange(per, device=dev, dtype=torch.int32).view(1, per))
+            C = B * per
+        omega = torch.ones(B, per, device=dev, dtype=torch.float32)
+        return self._routed(hidden_states, bank, idx, omega, C, CHAPTER_TOKENS, None, 0.0)
+
+    # ------------------------------------------------------------------ forward
+    def forward(self, hidden_states: torch.Tensor, memory: Optional[torch.Tensor] = None,
+                token_routing_state: Optional[Dict[str, Any]] = None, token_routing_kernel_version: str = "v2",
+                return_attn_weights: bool = False,
+                routed_memory_state: Optional[Dict[str, Any]] = None) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
+        if return_attn_weights:
+            raise NotImplementedError("return_attn_weights is not supported by the fused HIP attention")
+        if token_routing_state is not None:
+            preproj = self._forward_token_routed_attention(hidden_states, token_routing_state,
+                                                           token_routing_kernel_version)
+            return self._project_output(preproj), None
+        if routed_memory_state is not None:
+            st = routed_memory_state
+            norm_type = st.get("norm_type") if st.get("normalize", False) else None
+            attn = self._routed(hidden_states, st["bank"], st["chapter_indices"], st["chapter_weights"],
+                                int(st["num_chapters"]), int(st["tokens_per_chapter"]), norm_type,
+                                float(st.get("eps", 1e-6)))
+            return self._project_output(attn), None
+        if memory is None:
+            raise ValueError("memory must be provided when token_routing_state is None.")
+        return self._project_output(self._dense_as_chapters(hidden_states, memory)), None
+
+    def _forward_token_routed_attention(self, hidden_states: torch.Tensor, token_routing_state: Dict[str, Any],
+                                        token_routing_kernel_version: str = "v2") -> torch.Tensor:
+        """Token-level routed memory attention (memory_attention.py:480-716), pre o_proj."""
+        st = token_routing_state
+        shared_memory = st.get("shared_memory")
+        routed_memory = st.get("routed_memory")
+        idx = st.get("token_chapter_indices", None)
+        T = int(st.get("tokens_per_chapter", 0))
+        routed_scale = float(st.get("routed_scale", 1.0))
+        chapter_weights = st.get("chapter_weights", None)
+        version = normalize_kernel_version(st.get("kernel_version", token_routing_kernel_version))
+        if idx is None:
+            raise ValueError("token_routing_state must include token_chapter_indices.")
+        if idx.dim() != 3:
+            raise ValueError(f"token_chapter_indices must be rank-3 [B, T, topk], got shape {tuple(idx.shape)}.")
+        if idx.shape[0] != hidden_states.shape[0] or idx.shape[1] != hidden_states.shape[1]:
+            raise ValueError(
+                "token_chapter_indices shape prefix must match hidden_states [B, T, ...]. "
+                f"got hidden_states={tuple(hidden_states.shape)}, token_chapter_indices={tuple(idx.shape)}")
+        B, L, _ = hidden_states.shape
+        combined = None
+        if shared_memory is not None and shared_memory.numel() > 0:
+            combined = self._dense_as_chapters(hidden_states, shared_memory)
+        if routed_memory is not None and routed_memory.numel() > 0 and idx.shape[-1] > 0 and T > 0:
+            q = self._queries(hidden_states)
+            routed = ops.token_routed_attention(q, routed_memory, self.k_proj.weight, self.v_proj.weight, idx,
+                                                chapter_weights, tokens_per_chapter=T, version=version,
+                                                num_kv_heads=self.num_kv_heads)
+            routed = routed.reshape(B, L, self.hidden_dim) * routed_scale
+            combined = routed if combined is None else combined + routed
+        if combined is None:
+            combined = hidden_states.new_zeros((B, L, self.hidden_dim))
+        return combined

@@ -1,0 +1,120 @@
+"""Routing glue of MemoryTransformer for the memory layers, on libmoc kernels.
+
+Mirrors the static helpers of memory_transformer/model.py (:331-432) and the
+per-memory-layer routing block of MemoryTransformer.forward (:527-692), plus
+the memory sublayer call of MemoryTransformerBlock (memory_block.py:549-558,
+without the caller-owned RMSNorm and residual).
+
+``RoutedMemoryLayer`` is the fused sequence-level memory layer: router ->
+shared-chapter prepend -> [gather -> optional row norm -> x omega -> K/V
+projection -> joint attention] -> o_proj, where the bracket never
+materialises the (B, (S+k)*T, d) gathered memory.  ``TokenRoutedMemoryLayer``
+is the token-level variant (model.py:543-607 + memory_attention.py:480-716).
+"""
+
+from __future__ import annotations
+
+from typing import Dict, Optional, Tuple
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from . import ops
+from .memory_attention import MemoryCrossAttention
+from .router import ChapterRouter
+
+
+def select_routed_chapters_from_probs(probs: torch.Tensor, top_k: int, num_shared_chapters: int):
+    """model.py:331-354: mask the shared prefix, renormalise, top-k, renormalise.
+
+    Selection runs the router top-k kernel on log(probs) (same order as probs;
+    the kernel's softmax of log(probs) is probs / sum(probs))."""
+    B, C = probs.shape
+    S = max(0, min(int(num_shared_chapters), C))
+    k = min(int(top_k), C - S)
+    if k <= 0:
+        return (torch.empty((B, 0), dtype=torch.long, device=probs.device),
+                torch.empty((B, 0), dtype=probs.dtype, device=probs.device))
+    logits = torch.log(probs.float().clamp_min(torch.finfo(torch.float32).tiny))
+    idx, w = ops.router_topk(logits, k, S)
+    return idx.long(), w
+
+
+def prepend_shared_chapters(chapter_indices: torch.Tensor, chapter_weights: torch.Tensor, *, num_chapters: int,
+                            num_shared_chapters: int, routed_scaling_factor: float):
+    """model.py:356-391 (prepend kernel + its backward)."""
+    S = max(0, min(int(num_shared_chapters), int(num_chapters)))
+    if S <= 0:
+        return chapter_indices, chapter_weights
+    idx_star, omega = ops.prepend_shared(chapter_indices, chapter_weights, S, routed_scaling_factor)
+    return idx_star.long(), omega
+
+
+def normalize_shared_routed_memory_vectors(memory: torch.Tensor, *, num_shared_chapters: int,
+                                           tokens_per_chapter: int, norm_type: str, eps: float) -> torch.Tensor:
+    """model.py:393-432 on a materialised (B, N, d) memory (the unfused glue).
+
+    The fused path applies the same per-row normalisation inside the gather
+    prologue of the K/V projection kernel."""
+    if memory.dim() != 3:
+        raise ValueError(f"memory must be 3D (B, T, D), got shape {tuple(memory.shape)}")
+    if tokens_per_chapter <= 0:
+        return memory
+    st = min(max(0, int(num_shared_chapters)) * int(tokens_per_chapter), int(memory.shape[1]))
+    if st <= 0 or st >= int(memory.shape[1]):
+        return memory
+    if norm_type == "rms":
+        return memory / memory.pow(2).mean(dim=-1, keepdim=True).add(eps).sqrt()
+    if norm_type == "layernorm":
+        return F.layer_norm(memory, (memory.shape[-1],), eps=eps)
+    raise ValueError(f"Unsupported norm_type: {norm_type}")
+
+
+class RoutedMemoryLayer(nn.Module):
+    """One sequence-routed memory sublayer (router + memory cross-attention).
+
+    Parameter names follow the reference state dict: ``router.router.{weight,bias}``
+    (model.py:314 / router.py:64) and ``memory_attn.{q,k,v,o}_proj.weight``
+    (memory_block.py:476 / memory_attention.py:140-143).  The bank is passed to
+    forward (the reference shares one bank between memory layers)."""
+
+    def __init__(self, hidden_dim: int, num_heads: int, num_chapters: int, tokens_per_chapter: int, top_k: int,
+                 num_shared_chapters: int = 1, routed_scaling_factor: float = 2.5, num_kv_heads: Optional[int] = None,
+                 normalize_shared_routed_before_mixing: bool = False, shared_routed_norm_type: str = "rms",
+                 shared_routed_norm_eps: float = 1e-6, routing_strategy: str = "sequence",
+                 routing_window_size: Optional[int] = None, wo_init_zero: bool = True,
+                 gradient_checkpointing: bool = False):
+        super().__init__()
+        self.num_chapters = int(num_chapters)
+        self.tokens_per_chapter = int(tokens_per_chapter)
+        self.num_shared_chapters = int(num_shared_chapters)
+        self.routed_scaling_factor = float(routed_scaling_factor)
+        self.normalize = bool(normalize_shared_routed_before_mixing)
+        self.norm_type = shared_routed_norm_type
+        self.norm_eps = float(shared_routed_norm_eps)
+        self.routing_window_size = routing_window_size
+        self.router = ChapterRouter(hidden_dim, num_chapters, top_k, routing_strategy)
+        self.memory_attn = MemoryCrossAttention(hidden_dim, num_heads, num_kv_heads, wo_init_zero=wo_init_zero,
+                                                gradient_checkpointing=gradient_checkpointing)
+
+    def route(self, hidden_states: torch.Tensor, return_losses: bool = True):
+        idx, w, losses = self.router(hidden_states, return_losses=return_losses,
+                                     exclude_prefix_chapters=self.num_shared_chapters,
+                                     rolling_window_size=self.routing_window_size)
+        idx_star, omega = prepend_shared_chapters(idx, w, num_chapters=self.num_chapters,
+                                                  num_shared_chapters=self.num_shared_chapters,
+                                                  routed_scaling_factor=self.routed_scaling_factor)
+        return idx_star, omega, losses
+
+    def forward(self, hidden_states: torch.Tensor, bank: torch.Tensor,
+                return_losses: bool = True) -> Tuple[torch.Tensor, Dict[str, torch.Tensor]]:
+        idx_star, omega, losses = self.route(hidden_states, return_losses)
+        NS = idx_star.shape[1]
+        # model.py:402-405: normalisation only mixes when both the shared and routed slices are non-empty
+        normalize = self.normalize and 0 < self.num_shared_chapters < NS
+        state = {"bank": bank, "chapter_indices": idx_star, "chapter_weights": omega,
+                 "num_chapters": self.num_chapters, "tokens_per_chapter": self.tokens_per_chapter,
+                 "normalize": normalize, "norm_type": self.norm_type, "eps": self.norm_eps}
+        out, _ = self.memory_attn(hidden_states, routed_memory_state=state)
+        return out, losses

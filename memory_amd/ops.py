@@ -87,10 +87,12 @@ class _RouterLinear(torch.autograd.Function):
             dW_tmp = torch.empty(C, d, device=x.device, dtype=torch.float32)
         else:
             dW_tmp = dW
-        ws_bytes = L.query("moc_router_linear_bwd_workspace", R, d, C)
-        ws = torch.empty(max(1, ws_bytes), device=x.device, dtype=torch.uint8)
-        call("moc_router_linear_bwd", ptr(dz), ptr(x), R, d, ptr(Wc), L.dtype_code(Wc.dtype), C, ptr(dx), ptr(dW_tmp),
-             ptr(db), ptr(ws), ws_bytes, stream_ptr(x.device))
+        if dW_tmp is not None or db is not None:
+            call("moc_router_linear_bwd", ptr(dz), ptr(x), R, d, ptr(Wc), L.dtype_code(Wc.dtype), C, None,
+                 ptr(dW_tmp), ptr(db), None, 0, stream_ptr(x.device))
+        if dx is not None:
+            # dx = dz W: a plain (R, C) x (C, d) GEMM (hipBLASLt)
+            torch.matmul(dz, Wc.float(), out=dx)
         if dW is not None:
             dW = dW.to(Wc.dtype)
         if db is not None:
@@ -256,7 +258,8 @@ class _RoutedAttention(torch.autograd.Function):
         kt, vt = kv_project(bank, plan, T, wkv, HK, Dh, mean, rstd, dtype)
         om = omega.float().contiguous()
         out = torch.empty(B, Lq, H, Dh, device=q.device, dtype=dtype)
-        lse = torch.empty(B, H, Lq, device=q.device, dtype=torch.float32)
+        Lp = (Lq + 127) // 128 * 128
+        lse = torch.empty(B, H, Lp, device=q.device, dtype=torch.float32)
         call("moc_xattn_fwd", L.dtype_code(dtype), ptr(q), ptr(kt), ptr(vt), ptr(plan.edge_u), ptr(om), B, Lq, H, HK,
              Dh, T, NS, float(Dh) ** -0.5, ptr(out), ptr(lse), stream_ptr(q.device))
         ctx.save_for_backward(q, bank, wkv, om, out, lse, kt, vt, mean, rstd, plan.uniq, plan.n_uniq, plan.edge_u,
@@ -279,16 +282,21 @@ class _RoutedAttention(torch.autograd.Function):
         st = stream_ptr(dev)
         scale = float(Dh) ** -0.5
         dout = dout.to(dtype).contiguous()
-        delta = torch.empty(B, H, Lq, device=dev, dtype=torch.float32)
-        call("moc_xattn_bwd_prep", dt, ptr(out), ptr(dout), B, Lq, H, Dh, ptr(delta), st)
+        Lp = lse.shape[2]
+        delta = torch.empty(B, H, Lp, device=dev, dtype=torch.float32)
+        qt = torch.empty(B, H, Dh, Lp, device=dev, dtype=dtype)
+        dot = torch.empty_like(qt)
+        call("moc_xattn_bwd_prep", dt, ptr(q), ptr(out), ptr(dout), B, Lq, H, Dh, ptr(delta), ptr(qt), ptr(dot), st)
         dq = torch.empty_like(q)
         call("moc_xattn_bwd_dq", dt, ptr(q), ptr(kt), ptr(vt), ptr(edge_u), ptr(om), ptr(dout), ptr(lse), ptr(delta),
              B, Lq, H, HK, Dh, T, NS, scale, ptr(dq), st)
-        dkv = torch.empty(max_u * T, 2 * KV, device=dev, dtype=dtype)
+        dkv_edge = torch.empty(B * NS * T, 2 * KV, device=dev, dtype=dtype)
         dom_part = torch.zeros(B * NS, H, device=dev, dtype=torch.float32)
-        call("moc_xattn_bwd_dkv", dt, ptr(q), ptr(kt), ptr(vt), ptr(om), ptr(dout), ptr(lse), ptr(delta),
-             ptr(n_uniq), ptr(csr_off), ptr(csr_edge), max_u, B, Lq, H, HK, Dh, T, NS, scale, ptr(dkv),
-             ptr(dom_part), st)
+        call("moc_xattn_bwd_dkv", dt, ptr(q), ptr(qt), ptr(dout), ptr(dot), ptr(kt), ptr(vt), ptr(edge_u), ptr(om),
+             ptr(lse), ptr(delta), B, Lq, H, HK, Dh, T, NS, scale, ptr(dkv_edge), ptr(dom_part), st)
+        dkv = torch.empty(max_u * T, 2 * KV, device=dev, dtype=dtype)
+        call("moc_dkv_reduce", dt, ptr(dkv_edge), ptr(n_uniq), ptr(csr_off), ptr(csr_edge), max_u, 2 * KV, ptr(dkv),
+             st)
         domega = dom_part.sum(-1).view(B, NS)
         need_bank, need_wk, need_wv = ctx.needs_input_grad[1:4]
         dbank = dwk = dwv = None
@@ -312,3 +320,14 @@ def routed_attention(q, bank, wk, wv, omega, idx_star, *, num_chapters: int, tok
     HK = q.shape[2] if num_kv_heads is None else int(num_kv_heads)
     return _RoutedAttention.apply(q, bank, wk, wv, omega, idx_star, int(num_chapters), int(tokens_per_chapter),
                                   norm_code(norm_type), float(eps), HK)
+
+
+def router_token_logits(h: torch.Tensor, W: torch.Tensor, b: Optional[torch.Tensor]) -> torch.Tensor:
+    """Per-token router logits (B*T, C) as fp32 (router.py:294, ``self.router(hidden_states)``).
+
+    A plain (B*T, d) x (d, C) GEMM in the activations' dtype (hipBLASLt through
+    torch.matmul), as the reference's nn.Linear under autocast; returned as fp32."""
+    L.require_gpu(h, W)
+    x = h.reshape(-1, h.shape[-1])
+    z = torch.nn.functional.linear(x, W.to(x.dtype), None if b is None else b.to(x.dtype))
+    return z.float()
