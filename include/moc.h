@@ -175,6 +175,46 @@ int moc_bank_scatter(int dx_dtype, const void* dX, const void* bank, int bank_dt
                      const int32_t* uniq, const int32_t* n_uniq, int64_t max_u, const float* row_mean,
                      const float* row_rstd, int norm, void* grad_bank, hipStream_t stream);
 
+/* -------------------------------------------- token-routed sparse attention */
+
+/* Token-level routing (every query token picks its own chapters): the per-chapter
+ * MoE combine of kernels-final/kernel_v4.py (FSA_topk_sparse_attention_weighted_bthd,
+ * :1313-1340, and the per-chapter loop of memory_attention.py:596-688), the joint softmax
+ * of kernel_v2.py (FSA_topk_sparse_attention_bthd, :3181-3315, optional block weights,
+ * :765-773) and the joint log-bias of kernel_v5.py (:819-846).  Chapter-centric over a
+ * chapter plan of the edges e = token * S + slot (token = b * Tq + t).
+ * q [tokens][HQ][64]; K/V addressed by element strides (chapter cs, kv head hs, row rs).
+ * Heads hk0 .. hk0+nhk-1 are processed; each edge serves rpe rows (query heads
+ * hq_off .. hq_off+rpe-1).  Partials: o_part f32 [E * rpe][64], lse_part f32 [E * rpe]. */
+int moc_sparse_fwd(int dtype, const void* q, int64_t ntok, int HQ, const void* k, const void* v, int64_t cs,
+                   int64_t hs, int64_t rs, int HK, int Dh, const int32_t* uniq, const int32_t* n_uniq,
+                   const int32_t* csr_off, const int32_t* csr_edge, int64_t max_u, int S, int hk0, int nhk,
+                   int hq_off, int rpe, float scale, float* o_part, float* lse_part, hipStream_t stream);
+/* Combine of the slot partials: mode 0 MoE sum_s w_s o_s; 1 joint; 2 joint with block weights
+ * max(w, 0); 3 joint with log(max(w, 1e-20)) bias.  w f32 [E] (per edge), edge_u from the plan
+ * (negative = skipped slot).  out [tokens][HQ][64]; lse_joint f32 [tokens * rpe] (modes 1-3). */
+int moc_sparse_combine(int dtype, const float* o_part, const float* lse_part, const int32_t* edge_u, const float* w,
+                       int mode, int S, int rpe, int64_t ntok, int HQ, int hq_off, void* out, float* lse_joint,
+                       hipStream_t stream);
+/* Backward prep: mode 0 -> dst f32 [E * rpe] = dout . o_part; else dst f32 [tokens * rpe] = dout . out. */
+int moc_sparse_bwd_prep(int dtype, const void* dout, const void* out, const float* o_part, const int32_t* edge_u,
+                        int mode, int S, int rpe, int64_t ntok, int HQ, int hq_off, float* dst, hipStream_t stream);
+/* Chapter-centric backward: dK/dV of every (chapter, kv head) stored with element strides
+ * (ocs, ohs, ors) into dk / dv (rows of untouched chapters are left as they are); per-edge
+ * dq parts f32 [E * rpe][64]; dlog f32 [E * rpe] (modes 2-3, d loss / d log weight). */
+int moc_sparse_bwd(int dtype, const void* q, const void* dout, int64_t ntok, int HQ, const void* k, const void* v,
+                   int64_t cs, int64_t hs, int64_t rs, int HK, int Dh, const int32_t* uniq, const int32_t* n_uniq,
+                   const int32_t* csr_off, const int32_t* csr_edge, int64_t max_u, int S, int hk0, int nhk,
+                   int hq_off, int rpe, int mode, const float* lse_row, const float* delta_row, const float* w,
+                   float scale, void* dk, void* dv, int64_t ocs, int64_t ohs, int64_t ors, float* dq_part,
+                   float* dlog, hipStream_t stream);
+/* dq [tokens][HQ][64] rows hq_off .. hq_off+rpe-1 = sum over valid slots of dq_part. */
+int moc_sparse_dq_combine(int dtype, const float* dq_part, const int32_t* edge_u, int S, int rpe, int64_t ntok,
+                          int HQ, int hq_off, void* dq, hipStream_t stream);
+/* dw f32 [E]: mode 0 sum of dst rows; modes 2/3 sum of dlog rows / w (0 where the clamp is active). */
+int moc_sparse_dw(const float* src, const float* w, const int32_t* edge_u, int mode, int rpe, int64_t E, float* dw,
+                  hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -51,6 +51,14 @@ _SIGS = {
     "moc_xattn_bwd_dkv": (_I, [_I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I, _I, _I, _I, _I, _F,
                                _P, _P, _P]),
     "moc_dkv_reduce": (_I, [_I, _P, _P, _P, _P, _I64, _I64, _P, _P]),
+    "moc_sparse_fwd": (_I, [_I, _P, _I64, _I, _P, _P, _I64, _I64, _I64, _I, _I, _P, _P, _P, _P, _I64, _I, _I, _I,
+                            _I, _I, _F, _P, _P, _P]),
+    "moc_sparse_combine": (_I, [_I, _P, _P, _P, _P, _I, _I, _I, _I64, _I, _I, _P, _P, _P]),
+    "moc_sparse_bwd_prep": (_I, [_I, _P, _P, _P, _P, _I, _I, _I, _I64, _I, _I, _P, _P]),
+    "moc_sparse_bwd": (_I, [_I, _P, _P, _I64, _I, _P, _P, _I64, _I64, _I64, _I, _I, _P, _P, _P, _P, _I64, _I, _I,
+                            _I, _I, _I, _I, _P, _P, _P, _F, _P, _P, _I64, _I64, _I64, _P, _P, _P]),
+    "moc_sparse_dq_combine": (_I, [_I, _P, _P, _I, _I, _I64, _I, _I, _P, _P]),
+    "moc_sparse_dw": (_I, [_P, _P, _P, _I, _I, _I64, _P, _P]),
     "moc_gather_rows": (_I, [_I, _P, _I, _I64, _I, _P, _P, _I64, _P, _P, _P, _P]),
     "moc_bank_scatter": (_I, [_I, _P, _P, _I, _I64, _I, _P, _P, _I64, _P, _P, _I, _P, _P]),
 }

@@ -1,0 +1,705 @@
+// Token-routed sparse memory attention (every query token picks its own
+// chapters), forward and backward, chapter-centric.
+//
+// Inputs: q [tokens][HQ][64] (token = b * Tq + t), K / V addressed by element
+// strides (chapter cs, kv-head hs, row rs) so both the per-batch natural layout
+// [B*Tk][HK][64] of the reference's FSA entry points and the chapter-head tiles
+// of kv_project work.  An edge e = token * S + slot selects chapter gid; the
+// chapter plan (plan.hip) groups edges per distinct chapter.  Rows of an edge
+// are the query heads hq it serves: rpe rows per edge, row r <-> hq = hq_off + r.
+//
+// Forward = two kernels:
+//   sparse_fwd_kernel      per (chapter, kv head): for every row of every edge of
+//                          the chapter, the softmax over the chapter's 64 keys is
+//                          complete inside the tile -> o_part (normalised) and
+//                          lse_part (log2 domain).
+//   sparse_combine_kernel  per (token, head) over its S slots:
+//     mode 0 (MoE, kernels-final/kernel_v4.py:1-15 / naive_reference_weighted,
+//             benchmark_kernels_final.py:239-294):  o = sum_s w_s o_s
+//     mode 1 (joint, kernel_v2.py / naive_reference_unweighted :206-236):
+//             o = sum_s a_s o_s / sum_s a_s,  a_s = exp2(lse_s)
+//     mode 2 (block weights, kernel_v2.py:765-773): a_s = max(w_s, 0) exp2(lse_s)
+//     mode 3 (joint log-bias, kernel_v5.py:1-9, :218-220): a_s = max(w_s, 1e-20) exp2(lse_s)
+//     and the joint log-sum-exp of the row for the backward (modes 1-3).
+// Backward: prep (per-slot dw for mode 0, row delta for modes 1-3), the
+// chapter-centric kernel (dK / dV accumulated in registers over all edges of the
+// chapter -- deterministic, no atomics --, per-edge dQ parts, per-edge
+// d log(weight) for modes 2-3), then per-token reductions of dQ and dw.
+#include "moc_common.h"
+
+namespace moc {
+
+constexpr int kSpDh = 64;
+
+template <typename T> struct SpCfg;
+template <> struct SpCfg<bf16> { static constexpr int NW = 4; };
+template <> struct SpCfg<float> { static constexpr int NW = 2; };
+template <typename T> constexpr int sp_threads() { return 64 * SpCfg<T>::NW; }
+
+// Load a 64x64 K or V tile at (chapter gid, head hk) into LDS as [key][dim]
+// (transpose = false) or [dim][key] (transpose = true).
+template <typename T, int NT>
+__device__ __forceinline__ void sp_load_tile(char* dst, const T* base, int64_t rs, int tid, bool transpose) {
+  using Tile = SwzTile<T, 64>;
+  constexpr int EPC = 16 / (int)sizeof(T);
+  constexpr int CPR = 64 / EPC;
+  for (int i = tid; i < 64 * CPR; i += NT) {
+    const int row = i / CPR, c0 = (i % CPR) * EPC;
+    V16 v = ld16(base + row * rs + c0);
+    if (!transpose) {
+      st16(dst + Tile::off(row, c0), v);
+    } else {
+      const T* t = reinterpret_cast<const T*>(&v);
+#pragma unroll
+      for (int x = 0; x < EPC; ++x) *reinterpret_cast<T*>(dst + Tile::off(c0 + x, row)) = t[x];
+    }
+  }
+}
+
+// ------------------------------------------------------------------ forward
+template <typename T>
+__global__ __launch_bounds__(64 * SpCfg<T>::NW) void sparse_fwd_kernel(
+    const T* __restrict__ q, int HQ, const T* __restrict__ k, const T* __restrict__ v, int64_t cs, int64_t hs,
+    int64_t rs, int HK, const int32_t* __restrict__ uniq, const int32_t* __restrict__ n_uniq,
+    const int32_t* __restrict__ csr_off, const int32_t* __restrict__ csr_edge, int S, int hk0, int hq_off, int rpe,
+    float scale_log2, float* __restrict__ o_part, float* __restrict__ lse_part) {
+  typedef typename Frag<T>::type F8;
+  constexpr int NW = SpCfg<T>::NW, NT = 64 * NW;
+  using Tile = SwzTile<T, 64>;
+  constexpr int TB = 64 * 64 * (int)sizeof(T);
+  __shared__ __attribute__((aligned(16))) char sK[TB];
+  __shared__ __attribute__((aligned(16))) char sVt[TB];
+  const int u = blockIdx.x, hk = hk0 + blockIdx.y;
+  if (u >= n_uniq[0]) return;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 4, c16 = lane & 15;
+  const int gid = uniq[u];
+  sp_load_tile<T, NT>(sK, k + gid * cs + hk * hs, rs, tid, false);
+  sp_load_tile<T, NT>(sVt, v + gid * cs + hk * hs, rs, tid, true);
+  __syncthreads();
+  const int G = HQ / HK;
+  const int p0 = csr_off[u], p1 = csr_off[u + 1];
+  const int nrows = (p1 - p0) * G;
+  for (int r0 = 32 * wave; r0 < nrows; r0 += 32 * NW) {
+    F8 qf[2][2];
+    int erow[2];  // e * rpe + row, or -1
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+      const int r = r0 + 16 * qb + c16;
+      erow[qb] = -1;
+      if (r < nrows) {
+        const int e = csr_edge[p0 + r / G];
+        const int hq = hk * G + r % G;
+        const int64_t tok = e / S;
+        erow[qb] = e * rpe + (hq - hq_off);
+        const T* qp = q + ((size_t)tok * HQ + hq) * kSpDh;
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) qf[qb][ks] = Load8<T, T>::run(qp + 32 * ks + 8 * g);
+      } else {
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) qf[qb][ks] = zero_frag<T>();
+      }
+    }
+    f32x4 st[4][2];
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb) st[kb][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) {
+        F8 a = Tile::frag(sK, 16 * kb + c16, 32 * ks + 8 * g);
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) mma(st[kb][qb], a, qf[qb][ks]);
+      }
+    F8 pf[2][2];
+    float m[2], l[2];
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+      float mx = -INFINITY;
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int x = 0; x < 4; ++x) mx = fmaxf(mx, st[kb][qb][x]);
+      m[qb] = quad_max(mx) * scale_log2;
+      float ps = 0.f;
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int x = 0; x < 4; ++x) {
+          const float p = exp2f(st[kb][qb][x] * scale_log2 - m[qb]);
+          ps += p;
+          st[kb][qb][x] = p;
+        }
+      l[qb] = quad_sum(ps);
+#pragma unroll
+      for (int ks2 = 0; ks2 < 2; ++ks2)
+#pragma unroll
+        for (int x = 0; x < 4; ++x) {
+          pf[qb][ks2][x] = from_f<T>(st[2 * ks2][qb][x]);
+          pf[qb][ks2][4 + x] = from_f<T>(st[2 * ks2 + 1][qb][x]);
+        }
+    }
+    f32x4 o[4][2];
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb) o[db][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks2 = 0; ks2 < 2; ++ks2)
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+        F8 a = Tile::frag44(sVt, 16 * db + c16, 32 * ks2 + 4 * g, 32 * ks2 + 16 + 4 * g);
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) mma(o[db][qb], a, pf[qb][ks2]);
+      }
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+      if (erow[qb] < 0) continue;
+      const float inv = 1.f / l[qb];
+      float* op = o_part + (size_t)erow[qb] * kSpDh;
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+        *reinterpret_cast<f32x4*>(op + 16 * db + 4 * g) = o[db][qb] * inv;
+      if (g == 0) lse_part[erow[qb]] = m[qb] + log2f(l[qb]);
+    }
+  }
+}
+
+// Per (token, row): combine the slot partials.  16 lanes per row, 4 dims each.
+__device__ __forceinline__ float sp_logw(int mode, float w) {
+  if (mode == 2) return w > 0.f ? log2f(w) : -INFINITY;
+  if (mode == 3) return log2f(fmaxf(w, 1e-20f));
+  return 0.f;
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void sparse_combine_kernel(const float* __restrict__ o_part,
+                                                             const float* __restrict__ lse_part,
+                                                             const int32_t* __restrict__ edge_u,
+                                                             const float* __restrict__ w, int mode, int S, int rpe,
+                                                             int64_t ntok, int HQ, int hq_off, T* __restrict__ out,
+                                                             float* __restrict__ lse_joint) {
+  const int64_t row = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+  const int sub = threadIdx.x & 15;
+  if (row >= ntok * rpe) return;
+  const int64_t tok = row / rpe;
+  const int r = (int)(row % rpe);
+  f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+  if (mode == 0) {
+    for (int s = 0; s < S; ++s) {
+      const int64_t e = tok * S + s;
+      if (edge_u[e] < 0) continue;
+      const float ws = w[e];
+      acc += ws * *reinterpret_cast<const f32x4*>(o_part + ((size_t)e * rpe + r) * kSpDh + 4 * sub);
+    }
+  } else {
+    float M = -INFINITY;
+    for (int s = 0; s < S; ++s) {
+      const int64_t e = tok * S + s;
+      if (edge_u[e] < 0) continue;
+      M = fmaxf(M, lse_part[(size_t)e * rpe + r] + sp_logw(mode, w ? w[e] : 1.f));
+    }
+    float den = 0.f;
+    if (M > -INFINITY) {
+      for (int s = 0; s < S; ++s) {
+        const int64_t e = tok * S + s;
+        if (edge_u[e] < 0) continue;
+        const float a = exp2f(lse_part[(size_t)e * rpe + r] + sp_logw(mode, w ? w[e] : 1.f) - M);
+        den += a;
+        acc += a * *reinterpret_cast<const f32x4*>(o_part + ((size_t)e * rpe + r) * kSpDh + 4 * sub);
+      }
+    }
+    const float inv = den > 0.f ? 1.f / den : 0.f;
+    acc *= inv;
+    if (sub == 0) lse_joint[row] = den > 0.f ? M + log2f(den) : INFINITY;
+  }
+  T* op = out + ((size_t)tok * HQ + hq_off + r) * kSpDh + 4 * sub;
+#pragma unroll
+  for (int x = 0; x < 4; ++x) op[x] = from_f<T>(acc[x]);
+}
+
+// ----------------------------------------------------------------- backward
+// mode 0: dwe[e*rpe + r] = dO_row . o_part[e, r]      (dL/dw_s partial per head)
+// else:   delta[row]     = dO_row . out_row
+template <typename T>
+__global__ __launch_bounds__(256) void sparse_bwd_prep_kernel(const T* __restrict__ dout, const T* __restrict__ out,
+                                                              const float* __restrict__ o_part,
+                                                              const int32_t* __restrict__ edge_u, int mode, int S,
+                                                              int rpe, int64_t ntok, int HQ, int hq_off,
+                                                              float* __restrict__ dst) {
+  const int64_t row = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+  const int sub = threadIdx.x & 15;
+  if (row >= ntok * rpe) return;
+  const int64_t tok = row / rpe;
+  const int r = (int)(row % rpe);
+  const size_t off = ((size_t)tok * HQ + hq_off + r) * kSpDh + 4 * sub;
+  float d[4];
+#pragma unroll
+  for (int x = 0; x < 4; ++x) d[x] = to_f(dout[off + x]);
+  if (mode == 0) {
+    for (int s = 0; s < S; ++s) {
+      const int64_t e = tok * S + s;
+      float acc = 0.f;
+      if (edge_u[e] >= 0) {
+        const f32x4 o = *reinterpret_cast<const f32x4*>(o_part + ((size_t)e * rpe + r) * kSpDh + 4 * sub);
+        acc = d[0] * o[0] + d[1] * o[1] + d[2] * o[2] + d[3] * o[3];
+      }
+#pragma unroll
+      for (int sh = 8; sh >= 1; sh >>= 1) acc += __shfl_xor(acc, sh, 16);
+      if (sub == 0) dst[(size_t)e * rpe + r] = acc;
+    }
+  } else {
+    float acc = 0.f;
+#pragma unroll
+    for (int x = 0; x < 4; ++x) acc += d[x] * to_f(out[off + x]);
+#pragma unroll
+    for (int sh = 8; sh >= 1; sh >>= 1) acc += __shfl_xor(acc, sh, 16);
+    if (sub == 0) dst[row] = acc;
+  }
+}
+
+// Chapter-centric backward.  Per 32-row block of a wave: S = Q K^T and dPu = dO V^T
+// (lane = key column), P from the saved log-sum-exp, dS, then
+//   dV += P'^T dO, dK += scale dS^T Q         (A = row-key fragments, B = [dim][row] LDS)
+//   dq_part = scale dS K                     (dS transposed through LDS)
+//   dlog (modes 2-3) = row sums of dS
+template <typename T>
+__global__ __launch_bounds__(64 * SpCfg<T>::NW, 1) void sparse_bwd_kernel(
+    const T* __restrict__ q, const T* __restrict__ dout, int HQ, const T* __restrict__ k, const T* __restrict__ v,
+    int64_t cs, int64_t hs, int64_t rs, int HK, const int32_t* __restrict__ uniq, const int32_t* __restrict__ n_uniq,
+    const int32_t* __restrict__ csr_off, const int32_t* __restrict__ csr_edge, int S, int hk0, int hq_off, int rpe,
+    int mode, const float* __restrict__ lse_row, const float* __restrict__ delta_row, const float* __restrict__ w,
+    float scale_log2, float scale, T* __restrict__ dk, T* __restrict__ dv, int64_t ocs, int64_t ohs, int64_t ors,
+    float* __restrict__ dq_part, float* __restrict__ dlog) {
+  typedef typename Frag<T>::type F8;
+  constexpr int NW = SpCfg<T>::NW, NT = 64 * NW;
+  using Tile = SwzTile<T, 64>;   // [key][dim] and [dim][key] tiles
+  constexpr int TB = 64 * 64 * (int)sizeof(T);
+  __shared__ __attribute__((aligned(16))) char sK[TB];
+  __shared__ __attribute__((aligned(16))) char sV[TB];
+  __shared__ __attribute__((aligned(16))) char sKt[TB];
+  // per wave: Q^T, dO^T as [64 dims][32 rows] (row pitch P32) and dS as [32 rows][64 keys] (pitch PK)
+  constexpr int P32 = 36, PK = 72;
+  constexpr int WB = (64 * P32 > 32 * PK ? 64 * P32 : 32 * PK) * (int)sizeof(T);
+  __shared__ __attribute__((aligned(16))) char sW[NW][3][WB];
+  const int u = blockIdx.x, hk = hk0 + blockIdx.y;
+  if (u >= n_uniq[0]) return;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 4, c16 = lane & 15;
+  const int gid = uniq[u];
+  sp_load_tile<T, NT>(sK, k + gid * cs + hk * hs, rs, tid, false);
+  sp_load_tile<T, NT>(sKt, k + gid * cs + hk * hs, rs, tid, true);
+  sp_load_tile<T, NT>(sV, v + gid * cs + hk * hs, rs, tid, false);
+  __syncthreads();
+  T* sQt = reinterpret_cast<T*>(sW[wave][0]);
+  T* sDt = reinterpret_cast<T*>(sW[wave][1]);
+  T* sDS = reinterpret_cast<T*>(sW[wave][2]);
+  static_assert(NW * 3 * WB >= 64 * 64 * 4, "reduction buffer");
+
+  f32x4 dka[4][4], dva[4][4];
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+      dka[kb][db] = f32x4{0.f, 0.f, 0.f, 0.f};
+      dva[kb][db] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  const int G = HQ / HK;
+  const int p0 = csr_off[u], p1 = csr_off[u + 1];
+  const int nrows = (p1 - p0) * G;
+  for (int r0 = 32 * wave; r0 < nrows; r0 += 32 * NW) {
+    // ---- row bookkeeping (A-operand rows: lane row 16*qb + c16)
+    F8 qa[2][2], da[2][2];
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+      const int r = r0 + 16 * qb + c16;
+      if (r < nrows) {
+        const int e = csr_edge[p0 + r / G];
+        const int hq = hk * G + r % G;
+        const size_t off = ((size_t)(e / S) * HQ + hq) * kSpDh;
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+          qa[qb][ks] = Load8<T, T>::run(q + off + 32 * ks + 8 * g);
+          da[qb][ks] = Load8<T, T>::run(dout + off + 32 * ks + 8 * g);
+        }
+      } else {
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) { qa[qb][ks] = zero_frag<T>(); da[qb][ks] = zero_frag<T>(); }
+      }
+    }
+    // ---- stage Q^T and dO^T of the 32 rows: lane -> row (lane & 31), dims 32*(lane>>5) ..
+    {
+      const int rr = lane & 31, half = lane >> 5;
+      const int r = r0 + rr;
+      const bool ok = r < nrows;
+      size_t off = 0;
+      if (ok) {
+        const int e = csr_edge[p0 + r / G];
+        off = ((size_t)(e / S) * HQ + hk * G + r % G) * kSpDh + 32 * half;
+      }
+      constexpr int EPC = 16 / (int)sizeof(T);
+#pragma unroll
+      for (int c = 0; c < 32 / EPC; ++c) {
+        V16 vq = ok ? ld16(q + off + c * EPC) : V16{{0u, 0u, 0u, 0u}};
+        V16 vd = ok ? ld16(dout + off + c * EPC) : V16{{0u, 0u, 0u, 0u}};
+        const T* tq = reinterpret_cast<const T*>(&vq);
+        const T* td = reinterpret_cast<const T*>(&vd);
+#pragma unroll
+        for (int x = 0; x < EPC; ++x) {
+          const int dd = 32 * half + c * EPC + x;
+          sQt[dd * P32 + rr] = tq[x];
+          sDt[dd * P32 + rr] = td[x];
+        }
+      }
+    }
+    // ---- per-lane row stats for rows 4g + x of block qb (C-layout rows)
+    float lr[2][4], dr[2][4], wr[2][4], lw[2][4];
+    int er[2][4];
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+      for (int x = 0; x < 4; ++x) {
+        const int r = r0 + 16 * qb + 4 * g + x;
+        er[qb][x] = -1;
+        lr[qb][x] = INFINITY;
+        dr[qb][x] = 0.f;
+        wr[qb][x] = 1.f;
+        lw[qb][x] = 0.f;
+        if (r < nrows) {
+          const int e = csr_edge[p0 + r / G];
+          const int hq = hk * G + r % G;
+          const int erw = e * rpe + (hq - hq_off);
+          er[qb][x] = erw;
+          if (mode == 0) {
+            lr[qb][x] = lse_row[erw];
+            wr[qb][x] = w[e];
+            dr[qb][x] = delta_row[erw];
+          } else {
+            const int64_t trow = (int64_t)(e / S) * rpe + (hq - hq_off);
+            lr[qb][x] = lse_row[trow];
+            dr[qb][x] = delta_row[trow];
+            lw[qb][x] = sp_logw(mode, w ? w[e] : 1.f);
+          }
+        }
+      }
+    // ---- S and dPu
+    f32x4 sc[2][4], dp[2][4];
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) {
+        sc[qb][kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+        dp[qb][kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        F8 kf = Tile::frag(sK, 16 * kb + c16, 32 * ks + 8 * g);
+        F8 vf = Tile::frag(sV, 16 * kb + c16, 32 * ks + 8 * g);
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) {
+          mma(sc[qb][kb], qa[qb][ks], kf);
+          mma(dp[qb][kb], da[qb][ks], vf);
+        }
+      }
+    F8 pa[4], sa[4];
+    float rowsum[2][4];
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+      for (int x = 0; x < 4; ++x) rowsum[qb][x] = 0.f;
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int x = 0; x < 4; ++x) {
+          const float p = exp2f(sc[qb][kb][x] * scale_log2 + lw[qb][x] - lr[qb][x]);
+          float ds, pv;
+          if (mode == 0) {
+            ds = wr[qb][x] * p * (dp[qb][kb][x] - dr[qb][x]);
+            pv = wr[qb][x] * p;
+          } else {
+            ds = p * (dp[qb][kb][x] - dr[qb][x]);
+            pv = p;
+          }
+          rowsum[qb][x] += ds;
+          pa[kb][4 * qb + x] = from_f<T>(pv);
+          sa[kb][4 * qb + x] = from_f<T>(ds * scale);
+          sDS[(16 * qb + 4 * g + x) * PK + 16 * kb + c16] = from_f<T>(ds);
+        }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // ---- dV, dK
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+      F8 bq, bd;
+      const int dd = 16 * db + c16;
+#pragma unroll
+      for (int x = 0; x < 4; ++x) {
+        bq[x] = sQt[dd * P32 + 4 * g + x];
+        bq[4 + x] = sQt[dd * P32 + 16 + 4 * g + x];
+        bd[x] = sDt[dd * P32 + 4 * g + x];
+        bd[4 + x] = sDt[dd * P32 + 16 + 4 * g + x];
+      }
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) {
+        mma(dva[kb][db], pa[kb], bd);
+        mma(dka[kb][db], sa[kb], bq);
+      }
+    }
+    // ---- dq_part = scale * dS K : A = dS rows from LDS (row = 16*qb + c16, keys 32*ks + 8*g ..)
+    f32x4 dqa[2][4];
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+      for (int db = 0; db < 4; ++db) dqa[qb][db] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      F8 as[2];
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+        for (int x = 0; x < 8; ++x) as[qb][x] = sDS[(16 * qb + c16) * PK + 32 * ks + 8 * g + x];
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+        F8 bk = Tile::frag(sKt, 16 * db + c16, 32 * ks + 8 * g);
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) mma(dqa[qb][db], as[qb], bk);
+      }
+    }
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+      for (int x = 0; x < 4; ++x) {
+        if (er[qb][x] < 0) continue;
+        float* dst = dq_part + (size_t)er[qb][x] * kSpDh;
+#pragma unroll
+        for (int db = 0; db < 4; ++db) dst[16 * db + c16] = dqa[qb][db][x] * scale;
+      }
+    if (dlog) {
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+        for (int x = 0; x < 4; ++x) {
+          float s = rowsum[qb][x];
+          s += __shfl_xor(s, 1, 16);
+          s += __shfl_xor(s, 2, 16);
+          s += __shfl_xor(s, 4, 16);
+          s += __shfl_xor(s, 8, 16);
+          if (c16 == 0 && er[qb][x] >= 0) dlog[er[qb][x]] = s;
+        }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+  // ---- cross-wave reduction of dK / dV and strided store
+  __syncthreads();
+  float* buf = reinterpret_cast<float*>(&sW[0][0][0]);  // NW * 3 * TB/2 bytes >= 16 KB
+  T* dkb = dk + gid * ocs + hk * ohs;
+  T* dvb = dv + gid * ocs + hk * ohs;
+  auto reduce_store = [&](f32x4 (&acc)[4][4], T* dst) {
+    for (int src = 1; src < NW; ++src) {
+      if (wave == src) {
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+          for (int db = 0; db < 4; ++db)
+#pragma unroll
+            for (int x = 0; x < 4; ++x) buf[(16 * kb + 4 * g + x) * 64 + 16 * db + c16] = acc[kb][db][x];
+      }
+      __syncthreads();
+      if (wave == 0) {
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+          for (int db = 0; db < 4; ++db)
+#pragma unroll
+            for (int x = 0; x < 4; ++x) acc[kb][db][x] += buf[(16 * kb + 4 * g + x) * 64 + 16 * db + c16];
+      }
+      __syncthreads();
+    }
+    if (wave == 0) {
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+#pragma unroll
+          for (int x = 0; x < 4; ++x) dst[(16 * kb + 4 * g + x) * ors + 16 * db + c16] = from_f<T>(acc[kb][db][x]);
+    }
+  };
+  reduce_store(dka, dkb);
+  reduce_store(dva, dvb);
+}
+
+// dq[token, hq_off + r] = sum over valid slots of dq_part[e, r]
+template <typename T>
+__global__ __launch_bounds__(256) void sparse_dq_combine_kernel(const float* __restrict__ dq_part,
+                                                                const int32_t* __restrict__ edge_u, int S, int rpe,
+                                                                int64_t ntok, int HQ, int hq_off,
+                                                                T* __restrict__ dq) {
+  const int64_t row = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+  const int sub = threadIdx.x & 15;
+  if (row >= ntok * rpe) return;
+  const int64_t tok = row / rpe;
+  const int r = (int)(row % rpe);
+  f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int s = 0; s < S; ++s) {
+    const int64_t e = tok * S + s;
+    if (edge_u[e] < 0) continue;
+    acc += *reinterpret_cast<const f32x4*>(dq_part + ((size_t)e * rpe + r) * kSpDh + 4 * sub);
+  }
+  T* op = dq + ((size_t)tok * HQ + hq_off + r) * kSpDh + 4 * sub;
+#pragma unroll
+  for (int x = 0; x < 4; ++x) op[x] = from_f<T>(acc[x]);
+}
+
+// dw[e] for an edge e = token * S + s, summed over its rpe rows:
+//   mode 0: sum_r dwe[e, r]; modes 2/3: sum_r dlog[e, r] * d log(w) / dw.
+__global__ void sparse_dw_kernel(const float* __restrict__ src, const float* __restrict__ w,
+                                 const int32_t* __restrict__ edge_u, int mode, int rpe, int64_t E,
+                                 float* __restrict__ dw) {
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= E) return;
+  float s = 0.f;
+  if (edge_u[e] >= 0)
+    for (int r = 0; r < rpe; ++r) s += src[(size_t)e * rpe + r];
+  if (mode == 2) s = w[e] > 0.f ? s / w[e] : 0.f;
+  if (mode == 3) s = w[e] > 1e-20f ? s / w[e] : 0.f;
+  dw[e] = s;
+}
+
+}  // namespace moc
+
+using namespace moc;
+
+extern "C" {
+
+
+int moc_sparse_fwd(int dtype, const void* q, int64_t ntok, int HQ, const void* k, const void* v, int64_t cs,
+                   int64_t hs, int64_t rs, int HK, int Dh, const int32_t* uniq, const int32_t* n_uniq,
+                   const int32_t* csr_off, const int32_t* csr_edge, int64_t max_u, int S, int hk0, int nhk,
+                   int hq_off, int rpe, float scale, float* o_part, float* lse_part, hipStream_t stream) {
+  MOC_REQUIRE(q && k && v && uniq && n_uniq && csr_off && csr_edge && o_part && lse_part, MOC_ERR_ARG,
+              "moc_sparse_fwd: null pointer");
+  MOC_REQUIRE(Dh == kSpDh, MOC_ERR_UNSUPPORTED, "moc_sparse_fwd: head_dim %d (needs 64)", Dh);
+  MOC_REQUIRE(HQ > 0 && HK > 0 && HQ % HK == 0 && nhk > 0 && hk0 >= 0 && hk0 + nhk <= HK && S > 0, MOC_ERR_ARG,
+              "moc_sparse_fwd: bad heads HQ=%d HK=%d hk0=%d nhk=%d", HQ, HK, hk0, nhk);
+  if (max_u == 0 || ntok == 0) return MOC_OK;
+  dim3 grid((unsigned)max_u, (unsigned)nhk);
+  const float sl2 = scale * 1.4426950408889634f;
+  if (dtype == MOC_BF16)
+    hipLaunchKernelGGL(sparse_fwd_kernel<bf16>, grid, dim3(sp_threads<bf16>()), 0, stream, (const bf16*)q, HQ,
+                       (const bf16*)k, (const bf16*)v, cs, hs, rs, HK, uniq, n_uniq, csr_off, csr_edge, S, hk0, hq_off,
+                       rpe, sl2, o_part, lse_part);
+  else if (dtype == MOC_F32)
+    hipLaunchKernelGGL(sparse_fwd_kernel<float>, grid, dim3(sp_threads<float>()), 0, stream, (const float*)q, HQ,
+                       (const float*)k, (const float*)v, cs, hs, rs, HK, uniq, n_uniq, csr_off, csr_edge, S, hk0,
+                       hq_off, rpe, sl2, o_part, lse_part);
+  else
+    return set_error(MOC_ERR_UNSUPPORTED, "moc_sparse_fwd: dtype %d", dtype);
+  return check_launch("sparse_fwd_kernel");
+}
+
+int moc_sparse_combine(int dtype, const float* o_part, const float* lse_part, const int32_t* edge_u, const float* w,
+                       int mode, int S, int rpe, int64_t ntok, int HQ, int hq_off, void* out, float* lse_joint,
+                       hipStream_t stream) {
+  MOC_REQUIRE(o_part && lse_part && edge_u && out, MOC_ERR_ARG, "moc_sparse_combine: null pointer");
+  MOC_REQUIRE(mode >= 0 && mode <= 3, MOC_ERR_ARG, "moc_sparse_combine: mode %d", mode);
+  MOC_REQUIRE((mode == 0 || mode >= 2) ? w != nullptr : true, MOC_ERR_ARG, "moc_sparse_combine: mode %d needs weights", mode);
+  MOC_REQUIRE(mode == 0 || lse_joint, MOC_ERR_ARG, "moc_sparse_combine: joint modes need lse_joint");
+  const int64_t rows = ntok * rpe;
+  if (rows == 0) return MOC_OK;
+  dim3 grid((unsigned)((rows + 15) / 16));
+  if (dtype == MOC_BF16)
+    hipLaunchKernelGGL(sparse_combine_kernel<bf16>, grid, dim3(256), 0, stream, o_part, lse_part, edge_u, w, mode, S,
+                       rpe, ntok, HQ, hq_off, (bf16*)out, lse_joint);
+  else if (dtype == MOC_F32)
+    hipLaunchKernelGGL(sparse_combine_kernel<float>, grid, dim3(256), 0, stream, o_part, lse_part, edge_u, w, mode, S,
+                       rpe, ntok, HQ, hq_off, (float*)out, lse_joint);
+  else
+    return set_error(MOC_ERR_UNSUPPORTED, "moc_sparse_combine: dtype %d", dtype);
+  return check_launch("sparse_combine_kernel");
+}
+
+int moc_sparse_bwd_prep(int dtype, const void* dout, const void* out, const float* o_part, const int32_t* edge_u,
+                        int mode, int S, int rpe, int64_t ntok, int HQ, int hq_off, float* dst, hipStream_t stream) {
+  MOC_REQUIRE(dout && out && edge_u && dst && (mode != 0 || o_part), MOC_ERR_ARG, "moc_sparse_bwd_prep: null pointer");
+  const int64_t rows = ntok * rpe;
+  if (rows == 0) return MOC_OK;
+  dim3 grid((unsigned)((rows + 15) / 16));
+  if (dtype == MOC_BF16)
+    hipLaunchKernelGGL(sparse_bwd_prep_kernel<bf16>, grid, dim3(256), 0, stream, (const bf16*)dout, (const bf16*)out,
+                       o_part, edge_u, mode, S, rpe, ntok, HQ, hq_off, dst);
+  else if (dtype == MOC_F32)
+    hipLaunchKernelGGL(sparse_bwd_prep_kernel<float>, grid, dim3(256), 0, stream, (const float*)dout,
+                       (const float*)out, o_part, edge_u, mode, S, rpe, ntok, HQ, hq_off, dst);
+  else
+    return set_error(MOC_ERR_UNSUPPORTED, "moc_sparse_bwd_prep: dtype %d", dtype);
+  return check_launch("sparse_bwd_prep_kernel");
+}
+
+int moc_sparse_bwd(int dtype, const void* q, const void* dout, int64_t ntok, int HQ, const void* k, const void* v,
+                   int64_t cs, int64_t hs, int64_t rs, int HK, int Dh, const int32_t* uniq, const int32_t* n_uniq,
+                   const int32_t* csr_off, const int32_t* csr_edge, int64_t max_u, int S, int hk0, int nhk,
+                   int hq_off, int rpe, int mode, const float* lse_row, const float* delta_row, const float* w,
+                   float scale, void* dk, void* dv, int64_t ocs, int64_t ohs, int64_t ors, float* dq_part,
+                   float* dlog, hipStream_t stream) {
+  MOC_REQUIRE(q && dout && k && v && uniq && n_uniq && csr_off && csr_edge && lse_row && delta_row && dk && dv &&
+                  dq_part,
+              MOC_ERR_ARG, "moc_sparse_bwd: null pointer");
+  MOC_REQUIRE(Dh == kSpDh, MOC_ERR_UNSUPPORTED, "moc_sparse_bwd: head_dim %d (needs 64)", Dh);
+  MOC_REQUIRE(mode >= 0 && mode <= 3 && (mode == 1 || w), MOC_ERR_ARG, "moc_sparse_bwd: mode %d / weights", mode);
+  MOC_REQUIRE(HQ > 0 && HK > 0 && HQ % HK == 0 && nhk > 0 && hk0 >= 0 && hk0 + nhk <= HK && S > 0, MOC_ERR_ARG,
+              "moc_sparse_bwd: bad heads");
+  if (max_u == 0 || ntok == 0) return MOC_OK;
+  dim3 grid((unsigned)max_u, (unsigned)nhk);
+  const float sl2 = scale * 1.4426950408889634f;
+  if (dtype == MOC_BF16)
+    hipLaunchKernelGGL(sparse_bwd_kernel<bf16>, grid, dim3(sp_threads<bf16>()), 0, stream, (const bf16*)q,
+                       (const bf16*)dout, HQ, (const bf16*)k, (const bf16*)v, cs, hs, rs, HK, uniq, n_uniq, csr_off,
+                       csr_edge, S, hk0, hq_off, rpe, mode, lse_row, delta_row, w, sl2, scale, (bf16*)dk, (bf16*)dv,
+                       ocs, ohs, ors, dq_part, dlog);
+  else if (dtype == MOC_F32)
+    hipLaunchKernelGGL(sparse_bwd_kernel<float>, grid, dim3(sp_threads<float>()), 0, stream, (const float*)q,
+                       (const float*)dout, HQ, (const float*)k, (const float*)v, cs, hs, rs, HK, uniq, n_uniq,
+                       csr_off, csr_edge, S, hk0, hq_off, rpe, mode, lse_row, delta_row, w, sl2, scale, (float*)dk,
+                       (float*)dv, ocs, ohs, ors, dq_part, dlog);
+  else
+    return set_error(MOC_ERR_UNSUPPORTED, "moc_sparse_bwd: dtype %d", dtype);
+  return check_launch("sparse_bwd_kernel");
+}
+
+int moc_sparse_dq_combine(int dtype, const float* dq_part, const int32_t* edge_u, int S, int rpe, int64_t ntok,
+                          int HQ, int hq_off, void* dq, hipStream_t stream) {
+  MOC_REQUIRE(dq_part && edge_u && dq, MOC_ERR_ARG, "moc_sparse_dq_combine: null pointer");
+  const int64_t rows = ntok * rpe;
+  if (rows == 0) return MOC_OK;
+  dim3 grid((unsigned)((rows + 15) / 16));
+  if (dtype == MOC_BF16)
+    hipLaunchKernelGGL(sparse_dq_combine_kernel<bf16>, grid, dim3(256), 0, stream, dq_part, edge_u, S, rpe, ntok, HQ,
+                       hq_off, (bf16*)dq);
+  else if (dtype == MOC_F32)
+    hipLaunchKernelGGL(sparse_dq_combine_kernel<float>, grid, dim3(256), 0, stream, dq_part, edge_u, S, rpe, ntok, HQ,
+                       hq_off, (float*)dq);
+  else
+    return set_error(MOC_ERR_UNSUPPORTED, "moc_sparse_dq_combine: dtype %d", dtype);
+  return check_launch("sparse_dq_combine_kernel");
+}
+
+int moc_sparse_dw(const float* src, const float* w, const int32_t* edge_u, int mode, int rpe, int64_t E, float* dw,
+                  hipStream_t stream) {
+  MOC_REQUIRE(src && edge_u && dw && (mode == 0 || w), MOC_ERR_ARG, "moc_sparse_dw: null pointer");
+  MOC_REQUIRE(mode == 0 || mode == 2 || mode == 3, MOC_ERR_ARG, "moc_sparse_dw: mode %d has no weight gradient", mode);
+  if (E == 0) return MOC_OK;
+  hipLaunchKernelGGL(sparse_dw_kernel, dim3((unsigned)((E + 255) / 256)), dim3(256), 0, stream, src, w, edge_u, mode,
+                     rpe, E, dw);
+  return check_launch("sparse_dw_kernel");
+}
+
+}  // extern "C"

@@ -118,3 +118,50 @@ class RoutedMemoryLayer(nn.Module):
                  "normalize": normalize, "norm_type": self.norm_type, "eps": self.norm_eps}
         out, _ = self.memory_attn(hidden_states, routed_memory_state=state)
         return out, losses
+
+
+class TokenRoutedMemoryLayer(nn.Module):
+    """Token-level memory sublayer (model.py:543-607 + memory_attention.py:480-716).
+
+    Every token routes to its own top-k routed chapters; the shared prefix is attended
+    densely; routed chapters are combined MoE-style (per-chapter softmax mixed by the
+    router weights, the reference's default since its glue always passes
+    ``chapter_weights``) or jointly when ``weighted`` is False."""
+
+    def __init__(self, hidden_dim: int, num_heads: int, num_chapters: int, tokens_per_chapter: int, top_k: int,
+                 num_shared_chapters: int = 1, routed_scaling_factor: float = 2.5, num_kv_heads: Optional[int] = None,
+                 normalize_shared_routed_before_mixing: bool = False, shared_routed_norm_type: str = "rms",
+                 shared_routed_norm_eps: float = 1e-6, weighted: bool = True, kernel_version: str = "v4",
+                 wo_init_zero: bool = True):
+        super().__init__()
+        self.num_chapters = int(num_chapters)
+        self.tokens_per_chapter = int(tokens_per_chapter)
+        self.num_shared_chapters = max(0, min(int(num_shared_chapters), int(num_chapters)))
+        self.routed_scaling_factor = float(routed_scaling_factor)
+        self.normalize = bool(normalize_shared_routed_before_mixing)
+        self.norm_type = shared_routed_norm_type
+        self.norm_eps = float(shared_routed_norm_eps)
+        self.weighted = bool(weighted)
+        self.kernel_version = kernel_version
+        self.router = ChapterRouter(hidden_dim, num_chapters, top_k, "token")
+        self.memory_attn = MemoryCrossAttention(hidden_dim, num_heads, num_kv_heads, wo_init_zero=wo_init_zero)
+
+    def forward(self, hidden_states: torch.Tensor, bank: torch.Tensor,
+                return_losses: bool = True) -> Tuple[torch.Tensor, Dict[str, torch.Tensor]]:
+        S, T = self.num_shared_chapters, self.tokens_per_chapter
+        idx, w, losses = self.router.route_token_level(hidden_states, return_losses=return_losses,
+                                                       exclude_prefix_chapters=S)
+        st = S * T
+        shared = bank[:st] if st > 0 else None
+        routed = bank[st:] if st < bank.shape[0] else None
+        if self.normalize and shared is not None and routed is not None and shared.numel() and routed.numel():
+            merged = normalize_shared_routed_memory_vectors(bank.unsqueeze(0), num_shared_chapters=S,
+                                                            tokens_per_chapter=T, norm_type=self.norm_type,
+                                                            eps=self.norm_eps).squeeze(0)
+            shared, routed = merged[:st], merged[st:]
+        state = {"shared_memory": shared, "routed_memory": routed,
+                 "token_chapter_indices": (idx - S).to(torch.int32), "tokens_per_chapter": T,
+                 "routed_scale": self.routed_scaling_factor, "kernel_version": self.kernel_version,
+                 "chapter_weights": w if self.weighted else None}
+        out, _ = self.memory_attn(hidden_states, token_routing_state=state)
+        return out, losses

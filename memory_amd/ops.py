@@ -323,11 +323,18 @@ def routed_attention(q, bank, wk, wv, omega, idx_star, *, num_chapters: int, tok
 
 
 def router_token_logits(h: torch.Tensor, W: torch.Tensor, b: Optional[torch.Tensor]) -> torch.Tensor:
-    """Per-token router logits (B*T, C) as fp32 (router.py:294, ``self.router(hidden_states)``).
+    """Per-token router logits (B*T, C) in fp32 (router.py:294, ``self.router(hidden_states)``).
 
-    A plain (B*T, d) x (d, C) GEMM in the activations' dtype (hipBLASLt through
-    torch.matmul), as the reference's nn.Linear under autocast; returned as fp32."""
+    A plain (B*T, d) x (d, C) fp32 GEMM (hipBLASLt through torch.matmul).  fp32, not the
+    reference's autocast bf16, so that the top-k selection sees distinct logits."""
     L.require_gpu(h, W)
-    x = h.reshape(-1, h.shape[-1])
-    z = torch.nn.functional.linear(x, W.to(x.dtype), None if b is None else b.to(x.dtype))
-    return z.float()
+    x = h.reshape(-1, h.shape[-1]).float()
+    return torch.nn.functional.linear(x, W.float(), None if b is None else b.float())
+
+
+def token_routed_attention(q, routed_memory, wk, wv, idx, chapter_weights, *, tokens_per_chapter: int,
+                           version: str = "v2", num_kv_heads: Optional[int] = None):
+    """Routed branch of the token-level memory layer (see memory_amd.sparse_attention)."""
+    from .sparse_attention import token_routed_attention as _tra
+    return _tra(q, routed_memory, wk, wv, idx, chapter_weights, tokens_per_chapter=tokens_per_chapter,
+                version=version, num_kv_heads=num_kv_heads)

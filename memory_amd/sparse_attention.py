@@ -1,0 +1,321 @@
+"""Token-routed sparse memory attention on libmoc's chapter-centric kernels.
+
+Entry points with the reference's signatures:
+  * FSA_topk_sparse_attention_bthd            (kernels-final/kernel_v2.py:3181-3195; v1-v3)
+  * FSA_topk_sparse_attention_weighted_bthd   (kernels-final/kernel_v4.py:1313-1326; v4)
+  * FSA_topk_sparse_attention_weighted_joint_bias_bthd
+                                              (kernels-final/kernel_v5.py:819; v5, same signature)
+and ``token_routed_attention`` for MemoryCrossAttention's token path
+(memory_attention.py:480-716), which projects the routed bank once per call
+instead of once per batch element.
+
+Combine modes (see csrc/sparse_xattn.hip): 0 = exact per-chapter MoE
+(sum_s w_s softmax_s V_s); 1 = joint softmax over all selected keys;
+2 = joint softmax with block weights p ~ max(w, 0) e^s (v1-v3 block_weights_bths);
+3 = joint softmax with a log(max(w, 1e-20)) logit bias (v5).
+Chapters are 64 tokens (block_size 64); head_dim 64.
+"""
+
+from __future__ import annotations
+
+from typing import List, Optional
+
+import torch
+
+from . import _lib as L
+from ._lib import call, ptr, stream_ptr
+from . import ops
+
+BLOCK = 64
+
+
+class _Segment:
+    """One plan over the edges of a set of kv heads (all heads when the chapter
+    choice is the same for every head, else one kv head)."""
+
+    def __init__(self, chap_flat: torch.Tensor, num_chapters: int, hk0: int, nhk: int, hq_off: int, rpe: int,
+                 w_flat: Optional[torch.Tensor]):
+        self.plan = ops.chapter_plan(chap_flat, num_chapters)
+        self.hk0, self.nhk, self.hq_off, self.rpe = hk0, nhk, hq_off, rpe
+        self.w = w_flat
+        self.E = chap_flat.numel()
+
+
+def _kv_strides(layout: str, HK: int):
+    """Element strides (chapter, kv head, row) of a K/V buffer."""
+    if layout == "natural":   # [chapters*64][HK][64]
+        return 64 * HK * 64, 64, HK * 64
+    if layout == "tiles":     # [chapters][HK][64][64]
+        return HK * 64 * 64, 64 * 64, 64
+    raise ValueError(layout)
+
+
+def _forward(q, k, v, layout, segments: List[_Segment], mode: int, S: int, scale: float):
+    B, Tq, HQ, D = q.shape
+    HK = k.shape[-2] if layout == "natural" else k.shape[1]
+    dt = L.dtype_code(q.dtype)
+    st = stream_ptr(q.device)
+    cs, hs, rs = _kv_strides(layout, HK)
+    ntok = B * Tq
+    out = torch.empty(B, Tq, HQ, D, device=q.device, dtype=q.dtype)
+    saved = []
+    for sg in segments:
+        o_part = torch.empty(sg.E * sg.rpe, D, device=q.device, dtype=torch.float32)
+        lse_part = torch.empty(sg.E * sg.rpe, device=q.device, dtype=torch.float32)
+        call("moc_sparse_fwd", dt, ptr(q), ntok, HQ, ptr(k), ptr(v), cs, hs, rs, HK, D, ptr(sg.plan.uniq),
+             ptr(sg.plan.n_uniq), ptr(sg.plan.csr_off), ptr(sg.plan.csr_edge), sg.plan.max_u, S, sg.hk0, sg.nhk,
+             sg.hq_off, sg.rpe, float(scale), ptr(o_part), ptr(lse_part), st)
+        lse_joint = None if mode == 0 else torch.empty(ntok * sg.rpe, device=q.device, dtype=torch.float32)
+        call("moc_sparse_combine", dt, ptr(o_part), ptr(lse_part), ptr(sg.plan.edge_u), ptr(sg.w), mode, S, sg.rpe,
+             ntok, HQ, sg.hq_off, ptr(out), ptr(lse_joint), st)
+        saved.append((o_part, lse_part, lse_joint))
+    return out, saved
+
+
+def _backward(q, k, v, layout, out, dout, segments, saved, mode, S, scale, dk, dv, dk_layout):
+    """Fills dk/dv (pre-zeroed, layout dk_layout), returns dq and the per-edge dw (or None)."""
+    B, Tq, HQ, D = q.shape
+    HK = k.shape[-2] if layout == "natural" else k.shape[1]
+    dt = L.dtype_code(q.dtype)
+    st = stream_ptr(q.device)
+    cs, hs, rs = _kv_strides(layout, HK)
+    ntok = B * Tq
+    dq = torch.empty_like(q)
+    dws = []
+    dout = dout.to(q.dtype).contiguous()
+    ocs, ohs, ors, dv_off = dk_layout
+    for sg, (o_part, lse_part, lse_joint) in zip(segments, saved):
+        if mode == 0:
+            drow = torch.empty(sg.E * sg.rpe, device=q.device, dtype=torch.float32)
+            lrow = lse_part
+        else:
+            drow = torch.empty(ntok * sg.rpe, device=q.device, dtype=torch.float32)
+            lrow = lse_joint
+        call("moc_sparse_bwd_prep", dt, ptr(dout), ptr(out), ptr(o_part), ptr(sg.plan.edge_u), mode, S, sg.rpe, ntok,
+             HQ, sg.hq_off, ptr(drow), st)
+        dq_part = torch.empty(sg.E * sg.rpe, D, device=q.device, dtype=torch.float32)
+        dlog = torch.empty(sg.E * sg.rpe, device=q.device, dtype=torch.float32) if mode in (2, 3) else None
+        call("moc_sparse_bwd", dt, ptr(q), ptr(dout), ntok, HQ, ptr(k), ptr(v), cs, hs, rs, HK, D,
+             ptr(sg.plan.uniq), ptr(sg.plan.n_uniq), ptr(sg.plan.csr_off), ptr(sg.plan.csr_edge), sg.plan.max_u, S,
+             sg.hk0, sg.nhk, sg.hq_off, sg.rpe, mode, ptr(lrow), ptr(drow), ptr(sg.w), float(scale), ptr(dk),
+             dv.data_ptr() if dv is not None else dk.data_ptr() + dv_off, ocs, ohs, ors, ptr(dq_part), ptr(dlog), st)
+        call("moc_sparse_dq_combine", dt, ptr(dq_part), ptr(sg.plan.edge_u), S, sg.rpe, ntok, HQ, sg.hq_off, ptr(dq),
+             st)
+        if mode != 1:
+            dw = torch.empty(sg.E, device=q.device, dtype=torch.float32)
+            call("moc_sparse_dw", ptr(drow if mode == 0 else dlog), ptr(sg.w), ptr(sg.plan.edge_u), mode, sg.rpe,
+                 sg.E, ptr(dw), st)
+            dws.append(dw)
+    return dq, dws
+
+
+def _global_chapters(idx: torch.Tensor, M: int, per_batch: bool) -> torch.Tensor:
+    """Chapter ids in the plan's id space: b * M + c for per-batch K/V; -1 when c is out of range."""
+    c = idx.to(torch.int32)
+    bad = (c < 0) | (c >= M)
+    if per_batch:
+        B = c.shape[0]
+        shape = (B,) + (1,) * (c.dim() - 1)
+        c = c + torch.arange(B, device=c.device, dtype=torch.int32).view(shape) * M
+    return torch.where(bad, torch.full_like(c, -1), c)
+
+
+def _segments(idx: torch.Tensor, w: Optional[torch.Tensor], mode: int, M: int, per_batch: bool, HQ: int, HK: int,
+              num_chapters: int) -> List[_Segment]:
+    """idx (B, T, S) -> one segment for all heads; (B, T, HK, S) -> one segment per kv head."""
+    G = HQ // HK
+    if idx.dim() == 3:
+        chap = _global_chapters(idx, M, per_batch).contiguous()
+        wf = None if w is None else w.float().contiguous()
+        return [_Segment(chap.reshape(-1), num_chapters, 0, HK, 0, HQ, wf)]
+    segs = []
+    for hk in range(HK):
+        chap = _global_chapters(idx[:, :, hk, :], M, per_batch).contiguous()
+        if w is None:
+            wf = None
+        elif w.dim() == 4:
+            wf = w[:, :, hk, :].float().contiguous()
+        else:
+            wf = w.float().contiguous()
+        segs.append(_Segment(chap.reshape(-1), num_chapters, hk, 1, hk * G, G, wf))
+    return segs
+
+
+class _FSAFunction(torch.autograd.Function):
+    """Sparse attention over per-batch K/V [B, Tk, HK, D] (the FSA entry points)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, w, idx, mode, scale):
+        L.require_gpu(q, k, v, idx, w)
+        B, Tq, HQ, D = q.shape
+        Bk, Tk, HK, Dk = k.shape
+        if D != 64 or Dk != 64:
+            raise ValueError(f"head_dim must be 64 for the HIP kernels, got {D}/{Dk}")
+        if Tk % BLOCK != 0:
+            raise ValueError(f"Tk={Tk} must be a multiple of block_size {BLOCK}")
+        if HQ % HK != 0:
+            raise ValueError(f"HQ ({HQ}) must be a multiple of HK ({HK})")
+        if Bk not in (1, B):
+            raise ValueError(f"k/v batch {Bk} must be 1 or {B}")
+        M = Tk // BLOCK
+        q, k, v = q.contiguous(), k.to(q.dtype).contiguous(), v.to(q.dtype).contiguous()
+        S = idx.shape[-1]
+        segs = _segments(idx, w, mode, M, Bk > 1, HQ, HK, Bk * M)
+        out, saved = _forward(q, k, v, "natural", segs, mode, S, scale)
+        ctx.segs, ctx.saved_parts = segs, saved
+        ctx.save_for_backward(q, k, v, out)
+        ctx.mode, ctx.S, ctx.scale = mode, S, scale
+        ctx.w_shape = None if w is None else w.shape
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        q, k, v, out = ctx.saved_tensors
+        HK = k.shape[2]
+        dk = torch.zeros_like(k)
+        dv = torch.zeros_like(v)
+        cs, hs, rs = _kv_strides("natural", HK)
+        dq, dws = _backward(q, k, v, "natural", out, dout, ctx.segs, ctx.saved_parts, ctx.mode, ctx.S, ctx.scale,
+                            dk, dv, (cs, hs, rs, 0))
+        dw = None
+        if ctx.w_shape is not None and dws:
+            if len(dws) == 1:
+                dw = dws[0].view(ctx.w_shape)
+            elif len(ctx.w_shape) == 4:      # per-head weights: one segment per kv head
+                dw = torch.stack([x.view(ctx.w_shape[0], ctx.w_shape[1], ctx.w_shape[3]) for x in dws], dim=2)
+            else:                            # per-token weights shared by every kv head
+                dw = torch.stack(dws, 0).sum(0).view(ctx.w_shape)
+        return dq, dk, dv, dw, None, None, None
+
+
+def _check_common(cu_seqlens_q, cu_seqlens_k, disable_causal_mask, block_size):
+    if cu_seqlens_q is not None or cu_seqlens_k is not None:
+        raise NotImplementedError("variable-length (cu_seqlens) inputs are not supported by the HIP kernels")
+    if not disable_causal_mask:
+        raise NotImplementedError(
+            "causal memory masking is not implemented; memory cross-attention is non-causal "
+            "(MemoryCrossAttention passes disable_causal_mask=True, memory_attention.py:816)")
+    if int(block_size) != BLOCK:
+        raise ValueError(f"block_size must be {BLOCK} (the chapter tile of the HIP kernels), got {block_size}")
+
+
+def _indices(block_indices_bths, topk_idx_hns, q):
+    if block_indices_bths is not None:
+        return block_indices_bths
+    if topk_idx_hns is None:
+        raise ValueError("block_indices_bths or topk_idx_hns is required")
+    H, N, S = topk_idx_hns.shape
+    B, Tq = q.shape[0], q.shape[1]
+    return topk_idx_hns.permute(1, 0, 2).reshape(B, Tq, H, S)
+
+
+def FSA_topk_sparse_attention_bthd(q_bthd, k_bthd, v_bthd, block_indices_bths, block_size, block_weights_bths=None,
+                                   softmax_scale=None, cu_seqlens_q=None, cu_seqlens_k=None, topk_idx_hns=None,
+                                   topk_w_hns=None, assume_sorted_topk=False, disable_causal_mask=False):
+    """Joint softmax over each query's selected chapters (optionally block-weighted)."""
+    _check_common(cu_seqlens_q, cu_seqlens_k, disable_causal_mask, block_size)
+    idx = _indices(block_indices_bths, topk_idx_hns, q_bthd)
+    w = block_weights_bths
+    if w is None and topk_w_hns is not None:
+        H, N, S = topk_w_hns.shape
+        w = topk_w_hns.permute(1, 0, 2).reshape(q_bthd.shape[0], q_bthd.shape[1], H, S)
+    scale = float(softmax_scale) if softmax_scale is not None else q_bthd.shape[-1] ** -0.5
+    return _FSAFunction.apply(q_bthd, k_bthd, v_bthd, w, idx, 1 if w is None else 2, scale)
+
+
+def FSA_topk_sparse_attention_weighted_bthd(q_bthd, k_bthd, v_bthd, block_indices_bths, chapter_weights_bts,
+                                            block_size, softmax_scale=None, cu_seqlens_q=None, cu_seqlens_k=None,
+                                            topk_idx_hns=None, assume_sorted_topk=False, disable_causal_mask=False):
+    """Exact per-chapter MoE combine: sum_s w_s softmax(q K_s^T) V_s (kernel_v4 semantics)."""
+    _check_common(cu_seqlens_q, cu_seqlens_k, disable_causal_mask, block_size)
+    idx = _indices(block_indices_bths, topk_idx_hns, q_bthd)
+    scale = float(softmax_scale) if softmax_scale is not None else q_bthd.shape[-1] ** -0.5
+    return _FSAFunction.apply(q_bthd, k_bthd, v_bthd, chapter_weights_bts, idx, 0, scale)
+
+
+def FSA_topk_sparse_attention_weighted_joint_bias_bthd(q_bthd, k_bthd, v_bthd, block_indices_bths,
+                                                       chapter_weights_bts, block_size, softmax_scale=None,
+                                                       cu_seqlens_q=None, cu_seqlens_k=None, topk_idx_hns=None,
+                                                       assume_sorted_topk=False, disable_causal_mask=False):
+    """Joint softmax with a log(max(w, 1e-20)) logit bias per chapter (kernel_v5 semantics)."""
+    _check_common(cu_seqlens_q, cu_seqlens_k, disable_causal_mask, block_size)
+    idx = _indices(block_indices_bths, topk_idx_hns, q_bthd)
+    scale = float(softmax_scale) if softmax_scale is not None else q_bthd.shape[-1] ** -0.5
+    return _FSAFunction.apply(q_bthd, k_bthd, v_bthd, chapter_weights_bts, idx, 3, scale)
+
+
+# ------------------------------------------------------------------ model path
+
+class _TokenRouted(torch.autograd.Function):
+    """Routed branch of the token-level memory layer: K/V of the routed bank are
+    projected once (kv_project over every routed chapter), then sparse attention.
+
+    q (B, L, H, 64); routed (N_r, d); wk/wv (HK*64, d); idx (B, L, k) local chapter
+    ids; w (B, L, k) or None.  Returns (B, L, H, 64)."""
+
+    @staticmethod
+    def forward(ctx, q, routed, wk, wv, w, idx, mode, HK):
+        L.require_gpu(q, routed, wk, wv, idx, w)
+        dtype = q.dtype
+        B, Lq, HQ, D = q.shape
+        Nr, d = routed.shape
+        if Nr % BLOCK != 0:
+            raise ValueError(f"routed memory length {Nr} must be a multiple of {BLOCK}")
+        C = Nr // BLOCK
+        q = q.contiguous()
+        routed = routed.contiguous()
+        all_plan = ops.chapter_plan(torch.arange(C, device=q.device, dtype=torch.int32), C)
+        wkv = torch.cat([wk, wv], 0).to(dtype).contiguous()
+        kt, vt = ops.kv_project(routed, all_plan, BLOCK, wkv, HK, D, None, None, dtype)
+        S = idx.shape[-1]
+        segs = _segments(idx, w, mode, C, False, HQ, HK, C)
+        out, saved = _forward(q, kt, vt, "tiles", segs, mode, S, D ** -0.5)
+        ctx.segs, ctx.saved_parts, ctx.all_plan = segs, saved, all_plan
+        ctx.save_for_backward(q, routed, wkv, kt, vt, out)
+        ctx.cfg = (mode, S, HK, wk.dtype, wv.dtype, None if w is None else w.shape)
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        q, routed, wkv, kt, vt, out = ctx.saved_tensors
+        mode, S, HK, wk_dtype, wv_dtype, w_shape = ctx.cfg
+        dtype = q.dtype
+        D = q.shape[-1]
+        KV = HK * D
+        Nr, d = routed.shape
+        dkv = torch.zeros(Nr, 2 * KV, device=q.device, dtype=dtype)
+        # dk / dv written as rows [chapter*64 + key][hk*64 + dim] (dv at column offset KV)
+        elem = dkv.element_size()
+        dq, dws = _backward(q, kt, vt, "tiles", out, dout, ctx.segs, ctx.saved_parts, mode, S, D ** -0.5, dkv, None,
+                            (64 * 2 * KV, 64, 2 * KV, KV * elem))
+        need_r, need_wk, need_wv = ctx.needs_input_grad[1:4]
+        dr = dwk = dwv = None
+        if need_wk or need_wv:
+            dwkv = torch.matmul(dkv.t(), routed.to(dtype))
+            dwk = dwkv[:KV].to(wk_dtype) if need_wk else None
+            dwv = dwkv[KV:].to(wv_dtype) if need_wv else None
+        if need_r:
+            dr = torch.matmul(dkv, wkv).to(routed.dtype)
+        dw = None
+        if w_shape is not None and dws:
+            dw = dws[0].view(w_shape) if len(dws) == 1 else torch.stack(dws, 0).sum(0).view(w_shape)
+        return dq, dr, dwk, dwv, dw, None, None, None
+
+
+def token_routed_attention(q, routed_memory, wk, wv, idx, chapter_weights, *, tokens_per_chapter: int,
+                           version: str = "v2", num_kv_heads: Optional[int] = None):
+    """The routed branch of MemoryCrossAttention._forward_token_routed_attention
+    (memory_attention.py:553-707), before routed_scale and o_proj.
+
+    Dispatch mirrors the reference: weights given -> exact MoE combine (v1-v4),
+    or the joint log-bias approximation when the version is v5; no weights ->
+    joint softmax over the selected chapters."""
+    if int(tokens_per_chapter) != BLOCK:
+        raise ValueError(f"tokens_per_chapter must be {BLOCK} for the HIP kernels, got {tokens_per_chapter}")
+    HK = q.shape[2] if num_kv_heads is None else int(num_kv_heads)
+    if chapter_weights is None:
+        mode = 1
+    else:
+        mode = 3 if version == "v5" else 0
+    w = None if chapter_weights is None else chapter_weights.float()
+    return _TokenRouted.apply(q, routed_memory, wk, wv, w, idx, mode, HK)

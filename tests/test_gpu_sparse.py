@@ -1,0 +1,180 @@
+"""GPU parity of the token-routed sparse attention (the FSA entry points of the
+reference's kernels v1-v5 and MemoryCrossAttention's token path) against the
+oracle's vectorised restatements of benchmark_kernels_final.py's naive
+references, forward and backward (float64 autograd).
+
+fp32: 1e-4 relative max error; bf16: 2e-2 (3e-2 for weight gradients, the
+reference harness's bf16 backward tolerance, benchmark_kernels_final.py:676-682)."""
+
+import pytest
+import torch
+
+import oracle as O
+from helpers import assert_rel, gen
+
+pytestmark = pytest.mark.gpu
+
+REF = {1: O.sparse_attention_unweighted, 2: O.sparse_attention_block_weighted, 0: O.sparse_attention_weighted,
+       3: O.sparse_attention_joint_bias}
+
+
+def _inputs(seed, B, Tq, HQ, HK, M, S, per_head, mode):
+    g = gen(seed)
+    D = 64
+    q = torch.randn(B, Tq, HQ, D, generator=g)
+    k = torch.randn(B, M * 64, HK, D, generator=g)
+    v = torch.randn(B, M * 64, HK, D, generator=g)
+    if per_head:
+        idx = torch.stack([torch.stack([torch.randperm(M, generator=g)[:S] for _ in range(HK)])
+                           for _ in range(B * Tq)]).view(B, Tq, HK, S)
+    else:
+        idx = torch.stack([torch.randperm(M, generator=g)[:S] for _ in range(B * Tq)]).view(B, Tq, 1, S)
+        idx = idx.expand(B, Tq, HK, S).contiguous()
+    if mode == 2:
+        w = torch.rand(B, Tq, HK, S, generator=g) + 0.05
+    elif mode in (0, 3):
+        w = torch.rand(B, Tq, S, generator=g) + 0.05
+        w = w / w.sum(-1, keepdim=True)
+    else:
+        w = None
+    dO = torch.randn(B, Tq, HQ, D, generator=g)
+    return q, k, v, idx, w, dO
+
+
+def _ref(mode, q, k, v, idx, w, scale):
+    f = REF[mode]
+    if mode == 1:
+        return f(q, k, v, idx, 64, scale)
+    return f(q, k, v, idx, w, 64, scale)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("mode", [0, 1, 2, 3])
+@pytest.mark.parametrize("B,Tq,HQ,HK,M,S,per_head", [(2, 40, 2, 2, 6, 3, False), (1, 70, 4, 2, 5, 2, True)])
+def test_fsa_modes_forward_backward(gpu_device, dtype, mode, B, Tq, HQ, HK, M, S, per_head):
+    print(f"fsa mode={mode} dtype={dtype} B={B} Tq={Tq} HQ={HQ} HK={HK} M={M} S={S} per_head={per_head}", flush=True)
+    from memory_amd import sparse_attention as SA
+    dev = gpu_device
+    q, k, v, idx, w, dO = _inputs(31 + mode + 7 * per_head, B, Tq, HQ, HK, M, S, per_head, mode)
+    scale = 0.125
+    rq, rk, rv = (t.to(dtype).double().requires_grad_(True) for t in (q, k, v))
+    rw = None if w is None else w.double().requires_grad_(True)
+    ref = _ref(mode, rq, rk, rv, idx, rw, scale)
+    (ref * dO.to(dtype).double()).sum().backward()
+
+    gq, gk, gv = (t.to(dev, dtype).requires_grad_(True) for t in (q, k, v))
+    gw = None if w is None else w.to(dev).requires_grad_(True)
+    idx_d = idx.to(dev, torch.int32)
+    kw = dict(softmax_scale=scale, disable_causal_mask=True)
+    if mode == 0:
+        out = SA.FSA_topk_sparse_attention_weighted_bthd(gq, gk, gv, idx_d, gw, 64, **kw)
+    elif mode == 3:
+        out = SA.FSA_topk_sparse_attention_weighted_joint_bias_bthd(gq, gk, gv, idx_d, gw, 64, **kw)
+    else:
+        out = SA.FSA_topk_sparse_attention_bthd(gq, gk, gv, idx_d, 64, block_weights_bths=gw, **kw)
+    (out.float() * dO.to(dev)).sum().backward()
+    tol = 1e-4 if dtype == torch.float32 else 2e-2
+    assert_rel(out, ref, tol, "out")
+    assert_rel(gq.grad, rq.grad, tol, "dq")
+    assert_rel(gk.grad, rk.grad, tol, "dk")
+    assert_rel(gv.grad, rv.grad, tol, "dv")
+    if w is not None:
+        assert_rel(gw.grad, rw.grad, 1e-4 if dtype == torch.float32 else 3e-2, "dw")
+
+
+def test_fsa_out_of_range_chapters_are_skipped(gpu_device):
+    """The reference's kernels skip chapter ids outside [0, M) (kernels-final/kernel_v4.py:353):
+    for the MoE combine that equals giving the slot weight 0."""
+    from memory_amd import sparse_attention as SA
+    dev = gpu_device
+    q, k, v, idx, w, dO = _inputs(77, 1, 20, 2, 2, 4, 3, False, 0)
+    bad = idx.clone()
+    bad[0, ::3, :, 1] = 9          # out of range
+    bad[0, 1::5, :, 2] = -1
+    ref_idx = torch.where((bad < 0) | (bad >= 4), torch.zeros_like(bad), bad)
+    ref_w = w.clone()
+    ref_w[(bad[:, :, 0, :] < 0) | (bad[:, :, 0, :] >= 4)] = 0.0
+    ref = O.sparse_attention_weighted(q.double(), k.double(), v.double(), ref_idx, ref_w.double(), 64, 0.125)
+    out = SA.FSA_topk_sparse_attention_weighted_bthd(q.to(dev), k.to(dev), v.to(dev), bad.to(dev, torch.int32),
+                                                     w.to(dev), 64, softmax_scale=0.125, disable_causal_mask=True)
+    assert_rel(out, ref, 1e-4, "out with skipped slots")
+
+
+def test_fsa_rejects_unsupported(gpu_device):
+    from memory_amd import sparse_attention as SA
+    dev = gpu_device
+    q = torch.randn(1, 4, 2, 64, device=dev)
+    k = torch.randn(1, 128, 2, 64, device=dev)
+    idx = torch.zeros(1, 4, 2, 1, dtype=torch.int32, device=dev)
+    with pytest.raises(NotImplementedError, match="causal"):
+        SA.FSA_topk_sparse_attention_bthd(q, k, k, idx, 64)
+    with pytest.raises(ValueError, match="block_size"):
+        SA.FSA_topk_sparse_attention_bthd(q, k, k, idx, 32, disable_causal_mask=True)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("weighted,version", [(True, "v4"), (False, "v2"), (True, "v5")])
+def test_token_layer_matches_oracle(gpu_device, dtype, weighted, version):
+    """MemoryCrossAttention's token-routing path (shared dense + routed MoE) vs the oracle's
+    token_memory_layer, including gradients of h, the bank and every projection."""
+    print(f"token layer dtype={dtype} weighted={weighted} version={version}", flush=True)
+    from memory_amd.memory_attention import MemoryCrossAttention
+    from memory_amd.model import TokenRoutedMemoryLayer
+    dev = gpu_device
+    g = gen(55)
+    B, Lq, d, H, C, T, S, k = 2, 48, 128, 2, 9, 64, 1, 3
+    h = torch.randn(B, Lq, d, generator=g)
+    bank = torch.randn(C * T, d, generator=g)
+    Wr = torch.randn(C, d, generator=g) * 0.3
+    br = torch.zeros(C)
+    Wq, Wk, Wv, Wo = (torch.randn(d, d, generator=g) / d ** 0.5 for _ in range(4))
+    layer = TokenRoutedMemoryLayer(d, H, C, T, k, num_shared_chapters=S, routed_scaling_factor=2.5,
+                                   weighted=weighted, kernel_version=version, wo_init_zero=False)
+    with torch.no_grad():
+        layer.router.router.weight.copy_(Wr)
+        layer.router.router.bias.copy_(br)
+        for lin, W in zip((layer.memory_attn.q_proj, layer.memory_attn.k_proj, layer.memory_attn.v_proj,
+                           layer.memory_attn.o_proj), (Wq, Wk, Wv, Wo)):
+            lin.weight.copy_(W)
+    layer = layer.to(dev)
+    for m in (layer.memory_attn.q_proj, layer.memory_attn.k_proj, layer.memory_attn.v_proj, layer.memory_attn.o_proj):
+        m.to(dtype)
+    hg = h.to(dev, dtype).requires_grad_(True)
+    bg = bank.to(dev, dtype).requires_grad_(True)
+    out, _ = layer(hg, bg, return_losses=False)
+    dO = torch.randn(out.shape, generator=gen(56))
+    (out.float() * dO.to(dev)).sum().backward()
+
+    leaves = [t.double().clone().requires_grad_(True) for t in (h, bank, Wr, br, Wq, Wk, Wv, Wo)]
+    if dtype != torch.float32:
+        for i in (0, 1, 4, 5, 6, 7):
+            leaves[i] = leaves[i].detach().to(dtype).double().requires_grad_(True)
+    if version == "v5" and weighted:
+        ref = _token_layer_v5(*leaves, H=H, C=C, T=T, S=S, top_k=k)
+    else:
+        ref = O.token_memory_layer(*leaves, H=H, HK=H, C=C, T=T, S=S, top_k=k, routed_scale=2.5, weighted=weighted)
+    (ref * dO.double()).sum().backward()
+    tol = 1e-4 if dtype == torch.float32 else 2e-2
+    assert_rel(out, ref, tol, "out")
+    names = ["dh", "dbank", "dWr", "dbr", "dWq", "dWk", "dWv", "dWo"]
+    got = [hg.grad, bg.grad, layer.router.router.weight.grad, layer.router.router.bias.grad,
+           layer.memory_attn.q_proj.weight.grad, layer.memory_attn.k_proj.weight.grad,
+           layer.memory_attn.v_proj.weight.grad, layer.memory_attn.o_proj.weight.grad]
+    for n, gr, r in zip(names, got, leaves):
+        if r.grad is None or (not weighted and n in ("dWr", "dbr")):
+            continue
+        t = tol if n not in ("dWr", "dbr") else (1e-4 if dtype == torch.float32 else 5e-2)
+        assert_rel(gr, r.grad, t, n)
+
+
+def _token_layer_v5(h, bank, Wr, br, Wq, Wk, Wv, Wo, *, H, C, T, S, top_k):
+    """Token layer with the v5 joint log-bias combine for the routed branch (the reference
+    dispatches to kernel_v5 for weighted routing when the kernel version is v5)."""
+    logits = O.linear(h, Wr, br)
+    idx, w, _ = O.route_token_level(logits, top_k, S)
+    B, Lq, d = h.shape
+    shared = O.cross_attention(h, bank[:S * T], Wq, Wk, Wv, None, H, H, return_preproj=True)
+    q, k, v = O.compute_qkv(h, bank[S * T:], Wq, Wk, Wv, H, H)
+    idx4 = (idx - S).unsqueeze(2).expand(B, Lq, H, top_k)
+    r = O.sparse_attention_joint_bias(q, k, v, idx4, w, T, q.shape[-1] ** -0.5)
+    return O.linear(shared + r.reshape(B, Lq, -1) * 2.5, Wo)
