@@ -134,8 +134,162 @@ def cpu_baseline(cfg, budget_s=20.0):
                       f"({med * 1e3:.0f} ms each)"}
 
 
+def kernel_table(events, steps):
+    per = {}
+    for name, pairs in events.items():
+        durs = [a.elapsed_time(b) for a, b in pairs]
+        per[name] = {"calls_per_step": len(pairs) / steps, "avg_ms": sum(durs) / len(durs),
+                     "ms_per_step": sum(durs) / steps}
+    return per
+
+
+def timed(fn, steps, warmup):
+    """Run fn warmup + steps times; returns (ms per step, per-entry-point event table)."""
+    import torch
+    from memory_amd import _lib
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    _lib.KERNEL_EVENTS = {}
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        fn()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ev = _lib.KERNEL_EVENTS
+    _lib.KERNEL_EVENTS = None
+    return wall * 1e3 / steps, kernel_table(ev, steps)
+
+
+C4 = dict(B=4, L=2048, d=768, H=12, HK=12, C=4097, T=64, S=1, k=16, scale=2.5)
+
+
+def c4_flops(cfg):
+    B, L, d, H, HK, C, T, S, k = (cfg[x] for x in ("B", "L", "d", "H", "HK", "C", "T", "S", "k"))
+    ntok, Dh = B * L, d // H
+    router = 2.0 * ntok * d * C
+    q = o = 2.0 * ntok * d * d
+    attn = 4.0 * ntok * H * (S + k) * T * Dh
+    kv = 2.0 * (C - S) * T * d * (2 * HK * Dh) + 2.0 * S * T * d * (2 * HK * Dh)
+    fwd = router + q + o + attn + kv
+    return dict(router=router, q=q, o=o, attn=attn, kv=kv, fwd=fwd, step=3.0 * fwd)
+
+
+def run_c4(args):
+    import torch
+    from memory_amd.model import TokenRoutedMemoryLayer
+    cfg = dict(C4)
+    dev = torch.device("cuda", 0)
+    dtype = torch.bfloat16
+    torch.manual_seed(0)
+    B, L, d, H, C, T = (cfg[x] for x in ("B", "L", "d", "H", "C", "T"))
+    h = torch.randn(B, L, d, device=dev, dtype=dtype, requires_grad=True)
+    bank = (torch.randn(C * T, d, device=dev) * 0.02).to(dtype).requires_grad_(True)
+    layer = TokenRoutedMemoryLayer(d, H, C, T, cfg["k"], num_shared_chapters=cfg["S"],
+                                   routed_scaling_factor=cfg["scale"], weighted=True, kernel_version="v4",
+                                   wo_init_zero=False).to(dev)
+    with torch.no_grad():
+        for lin in (layer.memory_attn.q_proj, layer.memory_attn.k_proj, layer.memory_attn.v_proj,
+                    layer.memory_attn.o_proj):
+            lin.weight.normal_(0.0, 0.02)
+            lin.to(dtype)
+        layer.router.router.weight.normal_(0.0, 0.02)
+    torch.manual_seed(1)
+    dout = torch.randn(B, L, d, device=dev, dtype=dtype)
+
+    def step():
+        h.grad = None
+        bank.grad = None
+        for p in layer.parameters():
+            p.grad = None
+        out, _ = layer(h, bank, return_losses=False)
+        out.backward(dout)
+
+    ms, per = timed(step, args.steps, args.warmup)
+    fl = c4_flops(cfg)
+    tflops = fl["step"] / (ms * 1e-3) / 1e12
+    kernels = {n: {"avg_ms": round(v["avg_ms"], 4), "calls": v["calls_per_step"]}
+               for n, v in sorted(per.items(), key=lambda kv: -kv[1]["ms_per_step"])}
+    return {
+        "metric": "token-level memory-xattn fwd+bwd tokens/s (B=4,L=2048,d=768,k=16,T=64)",
+        "value": round(B * L / (ms * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": "c4: token-level routed memory layer fwd+bwd (v4 MoE combine)", **cfg},
+        "tflops": round(tflops, 2), "mfma_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
+        "algorithmic_gflop_per_step": round(fl["step"] / 1e9, 1), "kernels": kernels,
+    }
+
+
+C5 = dict(B=64, d=768, H=12, HK=12, C=4097, T=64, S=1, k=64, scale=2.5, layers=4, prompt=512)
+
+
+def run_c5(args):
+    import torch
+    from memory_amd.decode import DecodeRouting, MemoryDecodeCache, decode_attention
+    from memory_amd.model import RoutedMemoryLayer
+    cfg = dict(C5)
+    dev = torch.device("cuda", 0)
+    dtype = torch.bfloat16
+    torch.manual_seed(0)
+    B, d, H, HK, C, T = (cfg[x] for x in ("B", "d", "H", "HK", "C", "T"))
+    bank = (torch.randn(C * T, d, device=dev) * 0.02).to(dtype)
+    layers = []
+    with torch.no_grad():
+        prompt = torch.randn(B, cfg["prompt"], d, device=dev, dtype=dtype)
+        for _ in range(cfg["layers"]):
+            lay = RoutedMemoryLayer(d, H, C, T, cfg["k"], num_shared_chapters=cfg["S"],
+                                    routed_scaling_factor=cfg["scale"], num_kv_heads=HK, wo_init_zero=False).to(dev)
+            for lin in (lay.memory_attn.q_proj, lay.memory_attn.k_proj, lay.memory_attn.v_proj,
+                        lay.memory_attn.o_proj):
+                lin.weight.normal_(0.0, 0.02)
+                lin.to(dtype)
+            lay.router.router.weight.normal_(0.0, 0.02)
+            idx_star, omega, _ = lay.route(prompt, return_losses=False)
+            cache = MemoryDecodeCache(bank, lay.memory_attn.k_proj.weight, lay.memory_attn.v_proj.weight,
+                                      num_chapters=C, tokens_per_chapter=T, num_kv_heads=HK, dtype=dtype)
+            layers.append((lay, cache, DecodeRouting(idx_star, omega, C)))
+        h_t = torch.randn(B, 1, d, device=dev, dtype=dtype)
+    uniq = [r.unique_chapters() for _, _, r in layers]
+    tile_bytes = 64 * 64 * 2 * HK * 2          # K + V of one chapter, all kv heads, bf16
+    unique_bytes = sum(uniq) * tile_bytes
+    per_seq_bytes = cfg["layers"] * B * (cfg["S"] + cfg["k"]) * tile_bytes
+
+    def step():
+        with torch.no_grad():
+            for lay, cache, routing in layers:
+                q = lay.memory_attn.q_proj(h_t.reshape(B, d)).view(B, H, 64)
+                a = decode_attention(q, cache, routing)
+                lay.memory_attn.o_proj(a.reshape(B, 1, d))
+
+    ms, per = timed(step, args.steps, args.warmup)
+    dec = per.get("moc_decode_partial")
+    roofline = None
+    if dec:
+        ach = (unique_bytes / cfg["layers"]) / (dec["avg_ms"] * 1e-3) / 1e9
+        roofline = {"kernel": "moc_decode_partial", "bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS,
+                    "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
+                    "avg_ms": round(dec["avg_ms"], 4), "algorithmic_bytes": unique_bytes / cfg["layers"]}
+    kernels = {n: {"avg_ms": round(v["avg_ms"], 4), "calls": v["calls_per_step"]}
+               for n, v in sorted(per.items(), key=lambda kv: -kv[1]["ms_per_step"])}
+    return {
+        "metric": "memory-layer decode HBM GB/s (4 layers, B=64, k=64, T=64; unique selected K/V bytes)",
+        "value": round(unique_bytes / (ms * 1e-3) / 1e9, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": "c5: decode step through 4 memory layers sharing one bank", **cfg,
+                   "unique_chapters_per_layer": uniq},
+        "hbm_frac": round(unique_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "per_sequence_gbs": round(per_seq_bytes / (ms * 1e-3) / 1e9, 1),
+        "tokens_per_s": round(B / (ms * 1e-3), 1),
+        "roofline": roofline, "kernels": kernels,
+    }
+
+
 def main():
     ap = argparse.ArgumentParser()
+    ap.add_argument("--workload", choices=["c3", "c4", "c5"], default="c3")
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
@@ -146,6 +300,11 @@ def main():
         print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); "
               "the path shards by sequence with no exchange in the forward, see DESIGN.md", file=sys.stderr)
         sys.exit(2)
+
+    if args.workload != "c3":
+        line = run_c4(args) if args.workload == "c4" else run_c5(args)
+        print(json.dumps(line), flush=True)
+        return
 
     import torch
     from memory_amd import _lib

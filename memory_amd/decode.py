@@ -1,0 +1,94 @@
+"""Single-token decode through sequence-routed memory layers.
+
+For generation with the chapters and weights fixed by the prompt (the decode
+use of memory_transformer/model.py:612-692 through
+MemoryCrossAttention.forward with L = 1), the K/V projection of every chapter
+is computed once per layer (``MemoryDecodeCache``, 0.8 GB per layer at the
+paper shape) and each step only reads the tiles of the selected chapters:
+q = q_proj(h_t) -> chapter-centric partial attention (each selected tile read
+once per step for all sequences that chose it) -> joint merge over the
+sequence's slots -> o_proj.  Inference only (no autograd).
+"""
+
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from . import _lib as L
+from . import ops
+from ._lib import call, ptr, stream_ptr
+
+
+class MemoryDecodeCache:
+    """Per-layer K/V chapter tiles [C][HK][64][64] of the whole bank (optionally row-normalised)."""
+
+    def __init__(self, bank: torch.Tensor, wk: torch.Tensor, wv: torch.Tensor, *, num_chapters: int,
+                 tokens_per_chapter: int, num_kv_heads: int, norm_type: Optional[str] = None, eps: float = 1e-6,
+                 dtype: torch.dtype = torch.bfloat16):
+        L.require_gpu(bank, wk, wv)
+        C, T = int(num_chapters), int(tokens_per_chapter)
+        self.num_chapters, self.T, self.HK, self.dtype = C, T, int(num_kv_heads), dtype
+        with torch.no_grad():
+            plan = ops.chapter_plan(torch.arange(C, device=bank.device, dtype=torch.int32), C)
+            code = ops.norm_code(norm_type)
+            mean = rstd = None
+            if code:
+                mean, rstd = ops.row_stats(bank.contiguous(), plan, T, code, eps)
+            wkv = torch.cat([wk, wv], 0).to(dtype).contiguous()
+            self.k_tiles, self.v_tiles = ops.kv_project(bank.contiguous(), plan, T, wkv, self.HK, 64, mean, rstd,
+                                                        dtype)
+
+    @property
+    def nbytes(self) -> int:
+        return self.k_tiles.numel() * self.k_tiles.element_size() * 2
+
+
+class DecodeRouting:
+    """Fixed (chapter ids incl. the shared prefix, omega) of a batch of sequences and their plan."""
+
+    def __init__(self, chapter_indices: torch.Tensor, chapter_weights: torch.Tensor, num_chapters: int):
+        L.require_gpu(chapter_indices, chapter_weights)
+        self.idx = chapter_indices.to(torch.int32).contiguous()
+        self.omega = chapter_weights.float().contiguous()
+        self.B, self.NS = self.idx.shape
+        self.plan = ops.chapter_plan(self.idx, num_chapters)
+
+    def unique_chapters(self) -> int:
+        return int(self.plan.n_uniq[0].item())
+
+
+def decode_attention(q: torch.Tensor, cache: MemoryDecodeCache, routing: DecodeRouting) -> torch.Tensor:
+    """q (B, H, 64) -> attention output (B, H, 64) over the routed chapters (joint softmax, omega-weighted)."""
+    L.require_gpu(q)
+    B, H, D = q.shape
+    if q.dtype != cache.dtype:
+        q = q.to(cache.dtype)
+    q = q.contiguous()
+    dt = L.dtype_code(cache.dtype)
+    st = stream_ptr(q.device)
+    NS = routing.NS
+    E = B * NS
+    o_part = torch.empty(E * H, D, device=q.device, dtype=torch.float32)
+    lse_part = torch.empty(E * H, device=q.device, dtype=torch.float32)
+    pl = routing.plan
+    call("moc_decode_partial", dt, ptr(q), B, H, ptr(cache.k_tiles), ptr(cache.v_tiles), cache.HK, D, cache.T,
+         ptr(pl.uniq), ptr(pl.n_uniq), ptr(pl.csr_off), ptr(pl.csr_edge), pl.max_u, ptr(routing.omega), NS,
+         float(D) ** -0.5, ptr(o_part), ptr(lse_part), st)
+    out = torch.empty(B, H, D, device=q.device, dtype=cache.dtype)
+    lse = torch.empty(B * H, device=q.device, dtype=torch.float32)
+    call("moc_sparse_combine", dt, ptr(o_part), ptr(lse_part), ptr(pl.edge_u), None, 1, NS, H, B, H, 0, ptr(out),
+         ptr(lse), st)
+    return out
+
+
+def memory_decode_step(memory_attn, hidden: torch.Tensor, cache: MemoryDecodeCache,
+                       routing: DecodeRouting) -> torch.Tensor:
+    """One decode step of a memory sublayer: hidden (B, 1, d) -> (B, 1, d) (before the residual)."""
+    B = hidden.shape[0]
+    H = memory_attn.num_heads
+    with torch.no_grad():
+        q = memory_attn.q_proj(hidden.reshape(B, -1)).view(B, H, memory_attn.head_dim)
+        a = decode_attention(q, cache, routing)
+        return memory_attn.o_proj(a.reshape(B, 1, -1).to(memory_attn.o_proj.weight.dtype))
