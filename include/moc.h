@@ -114,23 +114,27 @@ int moc_row_stats(const void* bank, int bank_dtype, int64_t d, int T, const int3
 /* Replaces ChapteredMemoryBank.get_chapters_batched (memory_transformer/memory_bank.py:244-293)
  * followed by k_proj/v_proj of MemoryCrossAttention._compute_qkv (memory_attention.py:241-243),
  * computed once per distinct chapter.  bank [N_m, d] (bf16 or f32), wkv [2*HK*Dh, d] of dtype
- * (= [Wk; Wv]); row_mean/row_rstd from moc_row_stats or both NULL.  Outputs chapter-head
- * tiles k_tiles, v_tiles [max_u][HK][T][Dh] of dtype.  d % 64 == 0, (2*HK*Dh) % 128 == 0. */
+ * (= [Wk; Wv]); row_mean/row_rstd from moc_row_stats or both NULL.  Outputs (each may be NULL,
+ * but K and V each need one form): chapter-head tiles k_tiles, v_tiles [max_u][HK][T][Dh] and
+ * their transposes kt_tiles, vt_tiles [max_u][HK][Dh][T], of dtype.  d % 64 == 0,
+ * (2*HK*Dh) % 128 == 0. */
 int moc_kv_project(int dtype, const void* bank, int bank_dtype, int64_t d, int T, const int32_t* uniq,
                    const int32_t* n_uniq, int64_t max_u, const float* row_mean, const float* row_rstd,
-                   const void* wkv, int HK, int Dh, void* k_tiles, void* v_tiles, hipStream_t stream);
+                   const void* wkv, int HK, int Dh, void* k_tiles, void* v_tiles, void* kt_tiles, void* vt_tiles,
+                   hipStream_t stream);
 
 /* ------------------------------------------------- routed attention forward */
 
 /* Replaces MemoryCrossAttention._attention on omega-weighted gathered memory
  * (memory_transformer/model.py:689-692 + memory_attention.py:458-478, :269-318) for the
  * sequence-level path: one joint softmax over the NS selected chapters of each sequence,
- * with omega scaling both logits and values.  q [B, L, H, Dh]; slot_u i32 [B, NS] (the
- * plan's edge_u); omega f32 [B, NS]; out [B, L, H, Dh]; lse f32 [B, H, round_up(L, 128)] (log2
- * domain, +inf in the padding; consumed by the backward).  Dh == 64, T == 64. */
-int moc_xattn_fwd(int dtype, const void* q, const void* k_tiles, const void* v_tiles, const int32_t* slot_u,
-                  const float* omega, int64_t B, int64_t L, int H, int HK, int Dh, int T, int NS, float scale,
-                  void* out, float* lse, hipStream_t stream);
+ * with omega scaling both logits and values.  q [B, L, H, Dh]; k_tiles and vt_tiles (V transposed)
+ * from moc_kv_project, n_tiles = max_u * HK tiles each (< 4 GiB per buffer); slot_u i32 [B, NS] (the plan's edge_u); omega f32 [B, NS]; out [B, L, H, Dh];
+ * lse f32 [B, H, round_up(L, 128)] (log2 domain, +inf in the padding; consumed by the backward).
+ * Dh == 64, T == 64. */
+int moc_xattn_fwd(int dtype, const void* q, const void* k_tiles, const void* vt_tiles, int64_t n_tiles,
+                  const int32_t* slot_u, const float* omega, int64_t B, int64_t L, int H, int HK, int Dh, int T,
+                  int NS, float scale, void* out, float* lse, hipStream_t stream);
 
 /* ------------------------------------------------ routed attention backward */
 
@@ -141,10 +145,11 @@ int moc_xattn_fwd(int dtype, const void* q, const void* k_tiles, const void* v_t
  * transposed per (sequence, head), zero-padded. */
 int moc_xattn_bwd_prep(int dtype, const void* q, const void* out, const void* dout, int64_t B, int64_t L, int H,
                        int Dh, float* delta, void* qt, void* dot, hipStream_t stream);
-/* dq [B, L, H, Dh] (dtype). */
-int moc_xattn_bwd_dq(int dtype, const void* q, const void* k_tiles, const void* v_tiles, const int32_t* slot_u,
-                     const float* omega, const void* dout, const float* lse, const float* delta, int64_t B, int64_t L,
-                     int H, int HK, int Dh, int T, int NS, float scale, void* dq, hipStream_t stream);
+/* dq [B, L, H, Dh] (dtype); needs K, K^T and V tiles. */
+int moc_xattn_bwd_dq(int dtype, const void* q, const void* k_tiles, const void* kt_tiles, const void* v_tiles,
+                     int64_t n_tiles, const int32_t* slot_u, const float* omega, const void* dout, const float* lse,
+                     const float* delta, int64_t B, int64_t L, int H, int HK, int Dh, int T, int NS, float scale,
+                     void* dq, hipStream_t stream);
 /* dK/dV per edge (edge e = b * NS + slot): dkv_edge [B * NS * T][2 * HK * Dh] (dtype) holds for
  * the chapter in slot `slot` of sequence b the rows [dL/dk (all kv heads) | dL/dv], where
  * dL/dk, dL/dv are gradients w.r.t. the unweighted projected keys/values (omega folded in).
@@ -223,7 +228,7 @@ int moc_sparse_dw(const float* src, const float* w, const int32_t* edge_u, int m
  * Chapter-centric over the plan of the (sequence, slot) edges, so each selected tile is read
  * once per step.  q [B][H][64]; omega f32 [B * NS]; partials o_part f32 [B * NS * H][64] and
  * lse_part f32 [B * NS * H] are merged by moc_sparse_combine in joint mode (rpe = H). */
-int moc_decode_partial(int dtype, const void* q, int64_t B, int H, const void* k_tiles, const void* v_tiles, int HK,
+int moc_decode_partial(int dtype, const void* q, int64_t B, int H, const void* k_tiles, const void* vt_tiles, int HK,
                        int Dh, int T, const int32_t* uniq, const int32_t* n_uniq, const int32_t* csr_off,
                        const int32_t* csr_edge, int64_t max_u, const float* omega, int NS, float scale, float* o_part,
                        float* lse_part, hipStream_t stream);

@@ -32,6 +32,9 @@ CFLAGS = [
     "-I", INCLUDE,
     # Packed fp32 VALU ops (v_pk_add/mul/fma_f32) are kept out of the device code.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # keep MFMA accumulators in architectural VGPRs where they fit (no AGPR<->VGPR copies
+    # around the VALU softmax work); kernels that need more registers still get AGPRs
+    "-mllvm", "-amdgpu-mfma-vgpr-form=true",
     "-Wno-unused-command-line-argument",
 ]
 

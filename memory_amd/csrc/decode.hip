@@ -9,7 +9,7 @@
 // (sequence, slot) edges).
 //
 // decode_partial_kernel: one wave per (distinct chapter u, kv head hk).  Lane j
-// holds key row j; V is transposed through LDS so that lane d holds value column d.
+// holds key row j of the K tile and lane d value column d (row d of the V^T tile).
 // For every edge (b, slot) of u and every query head hq of hk:
 //   s_j = omega * scale * q . k_j  ->  lse (log2), o_d = omega * sum_j p_j v_jd / sum_j p_j
 // written as partials; moc_sparse_combine (joint mode) merges the slots of a sequence.
@@ -21,11 +21,10 @@ constexpr int kDecWaves = 4;
 
 template <typename T>
 __global__ __launch_bounds__(64 * kDecWaves) void decode_partial_kernel(
-    const T* __restrict__ q, int H, const T* __restrict__ ktiles, const T* __restrict__ vtiles, int HK,
+    const T* __restrict__ q, int H, const T* __restrict__ ktiles, const T* __restrict__ vttiles, int HK,
     const int32_t* __restrict__ uniq, const int32_t* __restrict__ n_uniq, const int32_t* __restrict__ csr_off,
     const int32_t* __restrict__ csr_edge, const float* __restrict__ omega, int NS, float scale_log2,
     float* __restrict__ o_part, float* __restrict__ lse_part) {
-  __shared__ T sv[kDecWaves][64][66];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int64_t pair = (int64_t)blockIdx.x * kDecWaves + wave;
   const int nu = n_uniq[0];
@@ -33,12 +32,12 @@ __global__ __launch_bounds__(64 * kDecWaves) void decode_partial_kernel(
   const int u = (int)(pair / HK), hk = (int)(pair % HK);
   const int gid = uniq[u];
   const size_t tile = ((size_t)gid * HK + hk) * 4096;
-  // key row `lane` and value row `lane` (64 elements each)
+  // key row `lane` and value column `lane` (64 elements each)
   constexpr int EPC = 16 / (int)sizeof(T);
-  float kr[64];
+  float kr[64], vc[64];
   {
     const T* kp = ktiles + tile + (size_t)lane * 64;
-    const T* vp = vtiles + tile + (size_t)lane * 64;
+    const T* vp = vttiles + tile + (size_t)lane * 64;
 #pragma unroll
     for (int c = 0; c < 64 / EPC; ++c) {
       V16 a = ld16(kp + c * EPC);
@@ -48,16 +47,10 @@ __global__ __launch_bounds__(64 * kDecWaves) void decode_partial_kernel(
 #pragma unroll
       for (int x = 0; x < EPC; ++x) {
         kr[c * EPC + x] = to_f(ta[x]);
-        sv[wave][lane][c * EPC + x] = tb[x];
+        vc[c * EPC + x] = to_f(tb[x]);
       }
     }
   }
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  float vc[64];  // value column `lane`
-#pragma unroll
-  for (int j = 0; j < 64; ++j) vc[j] = to_f(sv[wave][j][lane]);
 
   const int G = H / HK;
   const int p0 = csr_off[u], p1 = csr_off[u + 1];
@@ -78,11 +71,11 @@ __global__ __launch_bounds__(64 * kDecWaves) void decode_partial_kernel(
       }
       const float s = dot * c;
       const float m = wave_max(s);
-      const float pj = exp2f(s - m);
+      const float pj = __builtin_amdgcn_exp2f(s - m);
       const float l = wave_sum(pj);
       float o = 0.f;
 #pragma unroll
-      for (int j = 0; j < 64; ++j) o += __shfl(pj, j, 64) * vc[j];
+      for (int j = 0; j < 64; ++j) o += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pj), j)) * vc[j];
       const size_t row = (size_t)e * H + hq;
       o_part[row * 64 + lane] = o * (w / l);
       if (lane == 0) lse_part[row] = m + log2f(l);
@@ -96,11 +89,11 @@ using namespace moc;
 
 extern "C" {
 
-int moc_decode_partial(int dtype, const void* q, int64_t B, int H, const void* k_tiles, const void* v_tiles, int HK,
+int moc_decode_partial(int dtype, const void* q, int64_t B, int H, const void* k_tiles, const void* vt_tiles, int HK,
                        int Dh, int T, const int32_t* uniq, const int32_t* n_uniq, const int32_t* csr_off,
                        const int32_t* csr_edge, int64_t max_u, const float* omega, int NS, float scale, float* o_part,
                        float* lse_part, hipStream_t stream) {
-  MOC_REQUIRE(q && k_tiles && v_tiles && uniq && n_uniq && csr_off && csr_edge && omega && o_part && lse_part,
+  MOC_REQUIRE(q && k_tiles && vt_tiles && uniq && n_uniq && csr_off && csr_edge && omega && o_part && lse_part,
               MOC_ERR_ARG, "moc_decode_partial: null pointer");
   MOC_REQUIRE(Dh == 64 && T == 64, MOC_ERR_UNSUPPORTED, "moc_decode_partial: needs head_dim 64 and T 64");
   MOC_REQUIRE(H > 0 && HK > 0 && H % HK == 0 && NS > 0, MOC_ERR_ARG, "moc_decode_partial: bad heads");
@@ -110,11 +103,11 @@ int moc_decode_partial(int dtype, const void* q, int64_t B, int H, const void* k
   const float sl2 = scale * 1.4426950408889634f;
   if (dtype == MOC_BF16)
     hipLaunchKernelGGL(decode_partial_kernel<bf16>, grid, dim3(64 * kDecWaves), 0, stream, (const bf16*)q, H,
-                       (const bf16*)k_tiles, (const bf16*)v_tiles, HK, uniq, n_uniq, csr_off, csr_edge, omega, NS, sl2,
+                       (const bf16*)k_tiles, (const bf16*)vt_tiles, HK, uniq, n_uniq, csr_off, csr_edge, omega, NS, sl2,
                        o_part, lse_part);
   else if (dtype == MOC_F32)
     hipLaunchKernelGGL(decode_partial_kernel<float>, grid, dim3(64 * kDecWaves), 0, stream, (const float*)q, H,
-                       (const float*)k_tiles, (const float*)v_tiles, HK, uniq, n_uniq, csr_off, csr_edge, omega, NS,
+                       (const float*)k_tiles, (const float*)vt_tiles, HK, uniq, n_uniq, csr_off, csr_edge, omega, NS,
                        sl2, o_part, lse_part);
   else
     return set_error(MOC_ERR_UNSUPPORTED, "moc_decode_partial: dtype %d", dtype);

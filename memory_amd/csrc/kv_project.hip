@@ -91,7 +91,7 @@ __global__ __launch_bounds__(kGemmThreads) void kv_project_kernel(
     const TB* __restrict__ bank, int64_t d, int Tc, const int32_t* __restrict__ uniq,
     const int32_t* __restrict__ n_uniq, int64_t max_u, const float* __restrict__ row_mean,
     const float* __restrict__ row_rstd, const T* __restrict__ wkv, int HK, int Dh, T* __restrict__ kout,
-    T* __restrict__ vout) {
+    T* __restrict__ vout, T* __restrict__ kout_t, T* __restrict__ vout_t) {
   constexpr int BK = 128 / (int)sizeof(T);  // elements per 128-byte row slice
   constexpr int EPC = 16 / (int)sizeof(T);  // elements per 16-byte chunk
   constexpr int KSTEPS = BK / 32;
@@ -195,7 +195,8 @@ __global__ __launch_bounds__(kGemmThreads) void kv_project_kernel(
     __syncthreads();
   }
 
-  // Epilogue: scatter into chapter-head tiles.
+  // Epilogue: scatter into chapter-head tiles [u][hk][t][dh]; optionally also the
+  // transposed tiles [u][hk][dh][t] (4 consecutive t per lane -> one vector store).
   const int KV = HK * Dh;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
@@ -204,14 +205,27 @@ __global__ __launch_bounds__(kGemmThreads) void kv_project_kernel(
     const int nn = is_v ? n - KV : n;
     const int hk = nn / Dh, dh = nn % Dh;
     T* dst = is_v ? vout : kout;
+    T* dst_t = is_v ? vout_t : kout_t;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
+      const int64_t r0 = m0 + wm * 64 + 16 * i + 4 * g;
+      T vals[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const int64_t r = m0 + wm * 64 + 16 * i + 4 * g + e;
+        const int64_t r = r0 + e;
+        vals[e] = from_f<T>(acc[i][j][e]);
         if (r < nrows) {
           const int64_t u = r / Tc, jj = r % Tc;
-          dst[((u * HK + hk) * Tc + jj) * Dh + dh] = from_f<T>(acc[i][j][e]);
+          if (dst) dst[((u * HK + hk) * Tc + jj) * Dh + dh] = vals[e];
+        }
+      }
+      if (dst_t && r0 < nrows) {  // Tc % 4 == 0 and nrows % Tc == 0: the 4 rows share a chapter
+        const int64_t u = r0 / Tc, jj = r0 % Tc;
+        T* p = dst_t + ((u * HK + hk) * Dh + dh) * Tc + jj;
+        if constexpr (sizeof(T) == 2) {
+          *reinterpret_cast<bf16x4*>(p) = bf16x4{vals[0], vals[1], vals[2], vals[3]};
+        } else {
+          *reinterpret_cast<f32x4*>(p) = f32x4{vals[0], vals[1], vals[2], vals[3]};
         }
       }
     }
@@ -245,10 +259,14 @@ int moc_row_stats(const void* bank, int bank_dtype, int64_t d, int T, const int3
 
 int moc_kv_project(int dtype, const void* bank, int bank_dtype, int64_t d, int T, const int32_t* uniq,
                    const int32_t* n_uniq, int64_t max_u, const float* row_mean, const float* row_rstd,
-                   const void* wkv, int HK, int Dh, void* k_tiles, void* v_tiles, hipStream_t stream) {
-  MOC_REQUIRE(bank && uniq && n_uniq && wkv && k_tiles && v_tiles, MOC_ERR_ARG, "moc_kv_project: null pointer");
+                   const void* wkv, int HK, int Dh, void* k_tiles, void* v_tiles, void* kt_tiles, void* vt_tiles,
+                   hipStream_t stream) {
+  MOC_REQUIRE(bank && uniq && n_uniq && wkv && (k_tiles || kt_tiles) && (v_tiles || vt_tiles), MOC_ERR_ARG,
+              "moc_kv_project: null pointer");
   MOC_REQUIRE((row_mean == nullptr) == (row_rstd == nullptr), MOC_ERR_ARG, "moc_kv_project: mean/rstd must be both set or both null");
   MOC_REQUIRE(T > 0 && HK > 0 && Dh > 0 && max_u >= 0, MOC_ERR_ARG, "moc_kv_project: bad shape");
+  MOC_REQUIRE((kt_tiles == nullptr && vt_tiles == nullptr) || T % 4 == 0, MOC_ERR_ARG,
+              "moc_kv_project: transposed tiles need T %% 4 == 0");
   const int BK = dtype == MOC_BF16 ? 64 : 32;
   MOC_REQUIRE(d % 64 == 0 && d >= BK, MOC_ERR_UNSUPPORTED, "moc_kv_project: memory_dim %lld must be a multiple of 64",
               (long long)d);
@@ -259,14 +277,14 @@ int moc_kv_project(int dtype, const void* bank, int bank_dtype, int64_t d, int T
   dim3 grid((unsigned)((rows + 127) / 128), (unsigned)(2 * HK * Dh / 128));
   if (dtype == MOC_BF16 && bank_dtype == MOC_BF16)
     hipLaunchKernelGGL((kv_project_kernel<bf16, bf16>), grid, dim3(kGemmThreads), 0, stream, (const bf16*)bank, d, T, uniq,
-                       n_uniq, max_u, row_mean, row_rstd, (const bf16*)wkv, HK, Dh, (bf16*)k_tiles, (bf16*)v_tiles);
+                       n_uniq, max_u, row_mean, row_rstd, (const bf16*)wkv, HK, Dh, (bf16*)k_tiles, (bf16*)v_tiles, (bf16*)kt_tiles, (bf16*)vt_tiles);
   else if (dtype == MOC_BF16 && bank_dtype == MOC_F32)
     hipLaunchKernelGGL((kv_project_kernel<bf16, float>), grid, dim3(kGemmThreads), 0, stream, (const float*)bank, d, T, uniq,
-                       n_uniq, max_u, row_mean, row_rstd, (const bf16*)wkv, HK, Dh, (bf16*)k_tiles, (bf16*)v_tiles);
+                       n_uniq, max_u, row_mean, row_rstd, (const bf16*)wkv, HK, Dh, (bf16*)k_tiles, (bf16*)v_tiles, (bf16*)kt_tiles, (bf16*)vt_tiles);
   else if (dtype == MOC_F32 && bank_dtype == MOC_F32)
     hipLaunchKernelGGL((kv_project_kernel<float, float>), grid, dim3(kGemmThreads), 0, stream, (const float*)bank, d, T,
                        uniq, n_uniq, max_u, row_mean, row_rstd, (const float*)wkv, HK, Dh, (float*)k_tiles,
-                       (float*)v_tiles);
+                       (float*)v_tiles, (float*)kt_tiles, (float*)vt_tiles);
   else
     return set_error(MOC_ERR_UNSUPPORTED, "moc_kv_project: dtype %d with bank dtype %d", dtype, bank_dtype);
   return check_launch("kv_project_kernel");

@@ -138,6 +138,25 @@ struct SwzTile {
   }
 };
 
+// s_waitcnt vmcnt(0) (expcnt / lgkmcnt left open), gfx9 encoding
+__device__ __forceinline__ void vm_wait_all() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// -------------------------------------------------------------- buffer loads
+// Raw buffer loads: SGPR resource + per-thread VGPR offset + uniform SGPR offset.
+// The per-thread offset register is fixed for a kernel's lifetime, so in-flight
+// prefetches never pin address registers that later code wants to reuse, and
+// reads past `bytes` return zero.
+struct Buf {
+  __amdgpu_buffer_rsrc_t r;
+  __device__ __forceinline__ Buf(const void* p, uint32_t bytes)
+      : r(__builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000)) {}
+  __device__ __forceinline__ V16 load16(uint32_t voff, uint32_t soff) const {
+    typedef int i32x4 __attribute__((ext_vector_type(4)));
+    i32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+    return __builtin_bit_cast(V16, v);
+  }
+};
+
 // ------------------------------------------------------ 64x64 tile movement
 // One contiguous 64 x 64 tile of T (e.g. a chapter-head K or V block) moved
 // global -> registers -> LDS by NT threads; each thread owns NCHUNK 16-byte
@@ -152,6 +171,11 @@ struct TileIO {
   __device__ __forceinline__ void load(const T* src, int tid) {
 #pragma unroll
     for (int i = 0; i < NCHUNK; ++i) r[i] = ld16(src + (size_t)(tid + NT * i) * EPC);
+  }
+  // tile at byte offset `tile_off` of buffer `b`
+  __device__ __forceinline__ void load(const Buf& b, uint32_t tile_off, int tid) {
+#pragma unroll
+    for (int i = 0; i < NCHUNK; ++i) r[i] = b.load16((uint32_t)(tid + NT * i) * 16u, tile_off);
   }
   __device__ __forceinline__ void store(char* dst, int tid) const {
 #pragma unroll

@@ -78,16 +78,17 @@ __global__ __launch_bounds__(256) void xattn_bwd_prep_kernel(const T* __restrict
 // dq: one workgroup = 128 queries of one (sequence, head), loop over its slots.
 template <typename T>
 __global__ __launch_bounds__(kBThreads) void xattn_bwd_dq_kernel(
-    const T* __restrict__ q, const T* __restrict__ ktiles, const T* __restrict__ vtiles,
-    const int32_t* __restrict__ slot_u, const float* __restrict__ omega, const T* __restrict__ dout,
-    const float* __restrict__ lse, const float* __restrict__ delta, int L, int H, int HK, int NS, float scale_log2,
-    float scale, T* __restrict__ dq) {
+    const T* __restrict__ q, const T* __restrict__ ktiles, const T* __restrict__ kttiles,
+    const T* __restrict__ vtiles, const int32_t* __restrict__ slot_u, const float* __restrict__ omega,
+    const T* __restrict__ dout, const float* __restrict__ lse, const float* __restrict__ delta, int L, int H, int HK,
+    int NS, int64_t n_tiles, float scale_log2, float scale, T* __restrict__ dq) {
   typedef typename Frag<T>::type F8;
   using Tile = SwzTile<T, 64>;
   constexpr int TB = kBT * kBDh * (int)sizeof(T);
-  __shared__ __attribute__((aligned(16))) char sK[TB];
-  __shared__ __attribute__((aligned(16))) char sKt[TB];
-  __shared__ __attribute__((aligned(16))) char sV[TB];
+  // double-buffered K, K^T and V tiles (48 KB bf16, 96 KB fp32)
+  __shared__ __attribute__((aligned(16))) char sK[2][TB];
+  __shared__ __attribute__((aligned(16))) char sKt[2][TB];
+  __shared__ __attribute__((aligned(16))) char sV[2][TB];
 
   const int b = blockIdx.z, h = blockIdx.y;
   const int hk = h / (H / HK);
@@ -119,26 +120,33 @@ __global__ __launch_bounds__(kBThreads) void xattn_bwd_dq_kernel(
 
   const int32_t* su = slot_u + (size_t)b * NS;
   const float* om = omega + (size_t)b * NS;
-  TileIO<T, kBThreads> kio, vio;
-  auto tile_ptr = [&](const T* base, int u) { return base + ((size_t)u * HK + hk) * (kBT * kBDh); };
+  TileIO<T, kBThreads> kio, ktio, vio;
+  const uint32_t nbytes = (uint32_t)(n_tiles * TB);
+  const Buf kb(ktiles, nbytes), ktb(kttiles, nbytes), vb(vtiles, nbytes);
+  auto tile_off = [&](int u) { return (uint32_t)(((size_t)u * HK + hk) * TB); };
   int u_cur = su[0];
   if (u_cur >= 0) {
-    kio.load(tile_ptr(ktiles, u_cur), tid);
-    vio.load(tile_ptr(vtiles, u_cur), tid);
+    kio.load(kb, tile_off(u_cur), tid);
+    ktio.load(ktb, tile_off(u_cur), tid);
+    vio.load(vb, tile_off(u_cur), tid);
+    kio.store(sK[0], tid);
+    ktio.store(sKt[0], tid);
+    vio.store(sV[0], tid);
   }
+  vm_wait_all();  // Q / dO fragments have landed on every path into the loop
+  __syncthreads();
   for (int s = 0; s < NS; ++s) {
-    if (u_cur >= 0) {
-      kio.store(sK, tid);
-      kio.store_t(sKt, tid);
-      vio.store(sV, tid);
-    }
-    __syncthreads();
+    const int buf = s & 1;
     const int u_next = (s + 1 < NS) ? su[s + 1] : -1;
     if (u_next >= 0) {
-      kio.load(tile_ptr(ktiles, u_next), tid);
-      vio.load(tile_ptr(vtiles, u_next), tid);
+      kio.load(kb, tile_off(u_next), tid);
+      ktio.load(ktb, tile_off(u_next), tid);
+      vio.load(vb, tile_off(u_next), tid);
     }
     if (u_cur >= 0) {
+      const char* sKc = sK[buf];
+      const char* sKtc = sKt[buf];
+      const char* sVc = sV[buf];
       const float w = om[s];
       const float c = w * scale_log2;
       const float dsc = w * scale;
@@ -154,8 +162,8 @@ __global__ __launch_bounds__(kBThreads) void xattn_bwd_dq_kernel(
       for (int ks = 0; ks < 2; ++ks) {
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb) {
-          F8 ak = Tile::frag(sK, 16 * kb + c16, 32 * ks + 8 * g);
-          F8 av = Tile::frag(sV, 16 * kb + c16, 32 * ks + 8 * g);
+          F8 ak = Tile::frag(sKc, 16 * kb + c16, 32 * ks + 8 * g);
+          F8 av = Tile::frag(sVc, 16 * kb + c16, 32 * ks + 8 * g);
 #pragma unroll
           for (int qb = 0; qb < 2; ++qb) {
             mma(st[kb][qb], ak, qf[qb][ks]);
@@ -170,7 +178,7 @@ __global__ __launch_bounds__(kBThreads) void xattn_bwd_dq_kernel(
         for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            const float p = exp2f(st[kb][qb][e] * c - lse2[qb]);
+            const float p = __builtin_amdgcn_exp2f(st[kb][qb][e] * c - lse2[qb]);
             const float ds = p * (w * dp[kb][qb][e] - dl[qb]) * dsc;
             const int ks2 = kb >> 1, half = kb & 1;
             dsf[qb][ks2][4 * half + e] = from_f<T>(ds);
@@ -179,10 +187,15 @@ __global__ __launch_bounds__(kBThreads) void xattn_bwd_dq_kernel(
       for (int ks2 = 0; ks2 < 2; ++ks2)
 #pragma unroll
         for (int db = 0; db < 4; ++db) {
-          F8 bk = Tile::frag44(sKt, 16 * db + c16, 32 * ks2 + 4 * g, 32 * ks2 + 16 + 4 * g);
+          F8 bk = Tile::frag44(sKtc, 16 * db + c16, 32 * ks2 + 4 * g, 32 * ks2 + 16 + 4 * g);
 #pragma unroll
           for (int qb = 0; qb < 2; ++qb) mma(acc[qb][db], dsf[qb][ks2], bk);
         }
+    }
+    if (u_next >= 0) {
+      kio.store(sK[buf ^ 1], tid);
+      ktio.store(sKt[buf ^ 1], tid);
+      vio.store(sV[buf ^ 1], tid);
     }
     u_cur = u_next;
     __syncthreads();
@@ -354,7 +367,7 @@ __global__ __launch_bounds__(64 * DkvCfg<T>::SG, 1) void xattn_bwd_dkv_kernel(
 #pragma unroll
               for (int x = 0; x < 4; ++x) {
                 const float sraw = sc[qb][kb][x];
-                const float pr = exp2f(sraw * c - l2[x]);
+                const float pr = __builtin_amdgcn_exp2f(sraw * c - l2[x]);
                 const float dpu = dp[qb][kb][x];
                 const float ds = pr * (w * dpu - dl[x]);
                 dwp += ds * sraw * scale + pr * dpu;
@@ -566,24 +579,27 @@ int moc_xattn_bwd_prep(int dtype, const void* q, const void* out, const void* do
   return check_launch("xattn_bwd_prep_kernel");
 }
 
-int moc_xattn_bwd_dq(int dtype, const void* q, const void* k_tiles, const void* v_tiles, const int32_t* slot_u,
-                     const float* omega, const void* dout, const float* lse, const float* delta, int64_t B, int64_t L,
-                     int H, int HK, int Dh, int T, int NS, float scale, void* dq, hipStream_t stream) {
-  MOC_REQUIRE(q && k_tiles && v_tiles && slot_u && omega && dout && lse && delta && dq, MOC_ERR_ARG,
+int moc_xattn_bwd_dq(int dtype, const void* q, const void* k_tiles, const void* kt_tiles, const void* v_tiles,
+                     int64_t n_tiles, const int32_t* slot_u, const float* omega, const void* dout, const float* lse,
+                     const float* delta, int64_t B, int64_t L, int H, int HK, int Dh, int T, int NS, float scale,
+                     void* dq, hipStream_t stream) {
+  MOC_REQUIRE(q && k_tiles && kt_tiles && v_tiles && slot_u && omega && dout && lse && delta && dq, MOC_ERR_ARG,
               "moc_xattn_bwd_dq: null pointer");
   MOC_REQUIRE(Dh == kBDh && T == kBT, MOC_ERR_UNSUPPORTED, "moc_xattn_bwd_dq: needs head_dim 64 and T 64");
   MOC_REQUIRE(H > 0 && HK > 0 && H % HK == 0 && NS > 0, MOC_ERR_ARG, "moc_xattn_bwd_dq: bad shape");
+  MOC_REQUIRE(n_tiles > 0 && n_tiles * 64 * 64 * (dtype == MOC_F32 ? 4 : 2) < ((int64_t)1 << 32), MOC_ERR_UNSUPPORTED,
+              "moc_xattn_bwd_dq: tile buffers must be < 4 GiB (n_tiles=%lld)", (long long)n_tiles);
   if (B == 0 || L == 0) return MOC_OK;
   dim3 grid((unsigned)((L + 127) / 128), (unsigned)H, (unsigned)B);
   const float sl2 = scale * 1.4426950408889634f;
   if (dtype == MOC_BF16)
     hipLaunchKernelGGL(xattn_bwd_dq_kernel<bf16>, grid, dim3(kBThreads), 0, stream, (const bf16*)q, (const bf16*)k_tiles,
-                       (const bf16*)v_tiles, slot_u, omega, (const bf16*)dout, lse, delta, (int)L, H, HK, NS, sl2, scale,
-                       (bf16*)dq);
+                       (const bf16*)kt_tiles, (const bf16*)v_tiles, slot_u, omega, (const bf16*)dout, lse, delta, (int)L, H, HK, NS, n_tiles, sl2,
+                       scale, (bf16*)dq);
   else if (dtype == MOC_F32)
     hipLaunchKernelGGL(xattn_bwd_dq_kernel<float>, grid, dim3(kBThreads), 0, stream, (const float*)q,
-                       (const float*)k_tiles, (const float*)v_tiles, slot_u, omega, (const float*)dout, lse, delta,
-                       (int)L, H, HK, NS, sl2, scale, (float*)dq);
+                       (const float*)k_tiles, (const float*)kt_tiles, (const float*)v_tiles, slot_u, omega, (const float*)dout, lse, delta,
+                       (int)L, H, HK, NS, n_tiles, sl2, scale, (float*)dq);
   else
     return set_error(MOC_ERR_UNSUPPORTED, "moc_xattn_bwd_dq: dtype %d", dtype);
   return check_launch("xattn_bwd_dq_kernel");

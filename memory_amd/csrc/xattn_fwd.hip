@@ -26,11 +26,18 @@ constexpr int kFwdThreads = 256;
 constexpr int kDh = 64;
 constexpr int kTch = 64;
 
+// Running-max policy: a row's reference max m only moves up when the chapter
+// max exceeds it by more than kRescaleSlack (log2 units), so most chapters skip
+// the O / l rescale; probabilities stay <= 2^kRescaleSlack, far from overflow.
+constexpr float kRescaleSlack = 8.f;
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
 template <typename T>
 __global__ __launch_bounds__(kFwdThreads) void xattn_fwd_kernel(
-    const T* __restrict__ q, const T* __restrict__ ktiles, const T* __restrict__ vtiles,
+    const T* __restrict__ q, const T* __restrict__ ktiles, const T* __restrict__ vttiles,
     const int32_t* __restrict__ slot_u, const float* __restrict__ omega, int L, int H, int HK, int NS,
-    float scale_log2, T* __restrict__ out, float* __restrict__ lse) {
+    int64_t n_tiles, float scale_log2, T* __restrict__ out, float* __restrict__ lse) {
   typedef typename Frag<T>::type F8;
   using Tile = SwzTile<T, 64>;
   constexpr int TB = kTch * kDh * (int)sizeof(T);
@@ -68,23 +75,29 @@ __global__ __launch_bounds__(kFwdThreads) void xattn_fwd_kernel(
   const int32_t* su = slot_u + (size_t)b * NS;
   const float* om = omega + (size_t)b * NS;
   TileIO<T, kFwdThreads> kio, vio;
-  auto tile_ptr = [&](const T* base, int u) { return base + ((size_t)u * HK + hk) * (kTch * kDh); };
+  // tiles are addressed as byte offsets into two buffers (n_tiles * TB bytes each)
+  const Buf kb(ktiles, (uint32_t)(n_tiles * TB)), vb(vttiles, (uint32_t)(n_tiles * TB));
+  auto tile_off = [&](int u) { return (uint32_t)(((size_t)u * HK + hk) * TB); };
 
   int u_cur = su[0];
   if (u_cur >= 0) {
-    kio.load(tile_ptr(ktiles, u_cur), tid);
-    vio.load(tile_ptr(vtiles, u_cur), tid);
+    kio.load(kb, tile_off(u_cur), tid);
+    vio.load(vb, tile_off(u_cur), tid);
     kio.store(sK[0], tid);
-    vio.store_t(sV[0], tid);
+    vio.store(sV[0], tid);
   }
+  // Q fragments must have landed before the loop on every path (also when slot 0
+  // is skipped); otherwise the wait for them inside the loop can't be told apart
+  // from the prefetch and becomes a full vmcnt(0) ahead of the first MFMA.
+  vm_wait_all();
   __syncthreads();
 
   for (int s = 0; s < NS; ++s) {
     const int buf = s & 1;
     const int u_next = (s + 1 < NS) ? su[s + 1] : -1;
     if (u_next >= 0) {
-      kio.load(tile_ptr(ktiles, u_next), tid);
-      vio.load(tile_ptr(vtiles, u_next), tid);
+      kio.load(kb, tile_off(u_next), tid);
+      vio.load(vb, tile_off(u_next), tid);
     }
     if (u_cur >= 0) {
       const float w = om[s];
@@ -106,52 +119,74 @@ __global__ __launch_bounds__(kFwdThreads) void xattn_fwd_kernel(
           for (int qb = 0; qb < 2; ++qb) mma(st[kb][qb], a, qf[qb][ks]);
         }
       }
-      F8 pf[2][2];
+      // chapter max per row, lazy update of the reference max
+      float cm[2];
+      bool grow = false;
 #pragma unroll
       for (int qb = 0; qb < 2; ++qb) {
-        float mx = -INFINITY;
+        float mx = fmaxf(fmaxf(st[0][qb][0], st[0][qb][1]), fmaxf(st[0][qb][2], st[0][qb][3]));
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) mx = fmaxf(mx, st[kb][qb][e]);
-        mx = quad_max(mx);
-        const float mnew = fmaxf(m[qb], mx * c);  // c >= 0 (router weights are non-negative)
-        const float alpha = exp2f(m[qb] - mnew);
-        m[qb] = mnew;
-        float ps = 0.f;
-#pragma unroll
-        for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const float p = exp2f(st[kb][qb][e] * c - mnew);
-            ps += p;
-            st[kb][qb][e] = p * w;
-          }
-        lpart[qb] = lpart[qb] * alpha + ps;
-#pragma unroll
-        for (int db = 0; db < 4; ++db) o[db][qb] *= alpha;
-#pragma unroll
-        for (int ks2 = 0; ks2 < 2; ++ks2)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            pf[qb][ks2][e] = from_f<T>(st[2 * ks2][qb][e]);
-            pf[qb][ks2][4 + e] = from_f<T>(st[2 * ks2 + 1][qb][e]);
-          }
+        for (int kb = 1; kb < 4; ++kb)
+          mx = fmaxf(mx, fmaxf(fmaxf(st[kb][qb][0], st[kb][qb][1]), fmaxf(st[kb][qb][2], st[kb][qb][3])));
+        cm[qb] = quad_max(mx) * c;  // c >= 0 (router weights are non-negative)
+        grow |= cm[qb] > m[qb] + kRescaleSlack;
       }
-      // O^T[db][qb] += V^T(dims 16*db + c16, keys) * P^T
+      if (__any(grow)) {
 #pragma unroll
-      for (int ks2 = 0; ks2 < 2; ++ks2) {
+        for (int qb = 0; qb < 2; ++qb) {
+          const float mn = cm[qb] > m[qb] + kRescaleSlack ? cm[qb] : m[qb];
+          const float alpha = fast_exp2(m[qb] - mn);
+          m[qb] = mn;
+          lpart[qb] *= alpha;
 #pragma unroll
-        for (int db = 0; db < 4; ++db) {
-          F8 a = Tile::frag44(Vs, 16 * db + c16, 32 * ks2 + 4 * g, 32 * ks2 + 16 + 4 * g);
-#pragma unroll
-          for (int qb = 0; qb < 2; ++qb) mma(o[db][qb], a, pf[qb][ks2]);
+          for (int db = 0; db < 4; ++db) o[db][qb] *= alpha;
         }
+      }
+      F8 pf[2][2];
+      if (w > 0.f) {
+        // p~ = w * exp2(s*c - m): w folded into the exponent; the row sum needs sum(p~) / w
+        const float lw = __log2f(w);
+        const float rw = 1.f / w;
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) {
+          const float off = m[qb] - lw;
+          float ps = 0.f;
+#pragma unroll
+          for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const float p = fast_exp2(st[kb][qb][e] * c - off);
+              ps += p;
+              st[kb][qb][e] = p;
+            }
+          lpart[qb] += ps * rw;
+#pragma unroll
+          for (int ks2 = 0; ks2 < 2; ++ks2)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              pf[qb][ks2][e] = from_f<T>(st[2 * ks2][qb][e]);
+              pf[qb][ks2][4 + e] = from_f<T>(st[2 * ks2 + 1][qb][e]);
+            }
+        }
+        // O^T[db][qb] += V^T(dims 16*db + c16, keys) * P~^T
+#pragma unroll
+        for (int ks2 = 0; ks2 < 2; ++ks2) {
+#pragma unroll
+          for (int db = 0; db < 4; ++db) {
+            F8 a = Tile::frag44(Vs, 16 * db + c16, 32 * ks2 + 4 * g, 32 * ks2 + 16 + 4 * g);
+#pragma unroll
+            for (int qb = 0; qb < 2; ++qb) mma(o[db][qb], a, pf[qb][ks2]);
+          }
+        }
+      } else {
+        // zero weight: keys and values are zero, every logit is 0 -> only the denominator moves
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) lpart[qb] += 16.f * fast_exp2(-m[qb]);
       }
     }
     if (u_next >= 0) {
       kio.store(sK[buf ^ 1], tid);
-      vio.store_t(sV[buf ^ 1], tid);
+      vio.store(sV[buf ^ 1], tid);
     }
     u_cur = u_next;
     __syncthreads();
@@ -183,23 +218,26 @@ using namespace moc;
 
 extern "C" {
 
-int moc_xattn_fwd(int dtype, const void* q, const void* k_tiles, const void* v_tiles, const int32_t* slot_u,
-                  const float* omega, int64_t B, int64_t L, int H, int HK, int Dh, int T, int NS, float scale,
-                  void* out, float* lse, hipStream_t stream) {
-  MOC_REQUIRE(q && k_tiles && v_tiles && slot_u && omega && out && lse, MOC_ERR_ARG, "moc_xattn_fwd: null pointer");
+int moc_xattn_fwd(int dtype, const void* q, const void* k_tiles, const void* vt_tiles, int64_t n_tiles,
+                  const int32_t* slot_u, const float* omega, int64_t B, int64_t L, int H, int HK, int Dh, int T,
+                  int NS, float scale, void* out, float* lse, hipStream_t stream) {
+  MOC_REQUIRE(q && k_tiles && vt_tiles && slot_u && omega && out && lse, MOC_ERR_ARG, "moc_xattn_fwd: null pointer");
   MOC_REQUIRE(Dh == kDh && T == kTch, MOC_ERR_UNSUPPORTED, "moc_xattn_fwd: needs head_dim 64 and 64 tokens per chapter (got %d, %d)", Dh, T);
   MOC_REQUIRE(H > 0 && HK > 0 && H % HK == 0, MOC_ERR_ARG, "moc_xattn_fwd: H=%d HK=%d", H, HK);
   MOC_REQUIRE(NS > 0 && B >= 0 && L >= 0, MOC_ERR_ARG, "moc_xattn_fwd: bad shape");
   MOC_REQUIRE(B < 65536 && H < 65536, MOC_ERR_UNSUPPORTED, "moc_xattn_fwd: grid too large");
+  MOC_REQUIRE(n_tiles > 0 && n_tiles * 64 * 64 * (dtype == MOC_F32 ? 4 : 2) < ((int64_t)1 << 32), MOC_ERR_UNSUPPORTED,
+              "moc_xattn_fwd: tile buffers must be < 4 GiB (n_tiles=%lld)", (long long)n_tiles);
   if (B == 0 || L == 0) return MOC_OK;
   dim3 grid((unsigned)((L + 127) / 128), (unsigned)H, (unsigned)B);
   const float sl2 = scale * 1.4426950408889634f;
   if (dtype == MOC_BF16)
     hipLaunchKernelGGL(xattn_fwd_kernel<bf16>, grid, dim3(kFwdThreads), 0, stream, (const bf16*)q, (const bf16*)k_tiles,
-                       (const bf16*)v_tiles, slot_u, omega, (int)L, H, HK, NS, sl2, (bf16*)out, lse);
+                       (const bf16*)vt_tiles, slot_u, omega, (int)L, H, HK, NS, n_tiles, sl2, (bf16*)out, lse);
   else if (dtype == MOC_F32)
     hipLaunchKernelGGL(xattn_fwd_kernel<float>, grid, dim3(kFwdThreads), 0, stream, (const float*)q,
-                       (const float*)k_tiles, (const float*)v_tiles, slot_u, omega, (int)L, H, HK, NS, sl2, (float*)out,
+                       (const float*)k_tiles, (const float*)vt_tiles, slot_u, omega, (int)L, H, HK, NS, n_tiles, sl2,
+                       (float*)out,
                        lse);
   else
     return set_error(MOC_ERR_UNSUPPORTED, "moc_xattn_fwd: dtype %d", dtype);

@@ -224,13 +224,18 @@ def row_stats(bank: torch.Tensor, plan: ChapterPlan, T: int, norm: int, eps: flo
 
 
 def kv_project(bank: torch.Tensor, plan: ChapterPlan, T: int, wkv: torch.Tensor, HK: int, Dh: int,
-               mean: Optional[torch.Tensor], rstd: Optional[torch.Tensor], dtype: torch.dtype):
-    kt = torch.empty(plan.max_u, HK, T, Dh, device=bank.device, dtype=dtype)
-    vt = torch.empty_like(kt)
+               mean: Optional[torch.Tensor], rstd: Optional[torch.Tensor], dtype: torch.dtype,
+               layouts=("k", "v")):
+    """Chapter-head tiles of the plan's chapters.  ``layouts`` picks the outputs among
+    "k", "v" ([u][hk][t][dh]) and "kt", "vt" (transposed, [u][hk][dh][t])."""
+    out = {}
+    for name in ("k", "v", "kt", "vt"):
+        if name in layouts:
+            out[name] = torch.empty(plan.max_u, HK, T, Dh, device=bank.device, dtype=dtype)
     call("moc_kv_project", L.dtype_code(dtype), ptr(bank), L.dtype_code(bank.dtype), bank.shape[1], T, ptr(plan.uniq),
-         ptr(plan.n_uniq), plan.max_u, ptr(mean), ptr(rstd), ptr(wkv), HK, Dh, ptr(kt), ptr(vt),
-         stream_ptr(bank.device))
-    return kt, vt
+         ptr(plan.n_uniq), plan.max_u, ptr(mean), ptr(rstd), ptr(wkv), HK, Dh, ptr(out.get("k")), ptr(out.get("v")),
+         ptr(out.get("kt")), ptr(out.get("vt")), stream_ptr(bank.device))
+    return tuple(out[n] for n in layouts)
 
 
 # ------------------------------------------------------------- routed attention (A)
@@ -255,21 +260,21 @@ class _RoutedAttention(torch.autograd.Function):
         if norm != L.MOC_NORM_NONE:
             mean, rstd = row_stats(bank, plan, T, norm, eps)
         wkv = torch.cat([wk, wv], 0).to(dtype).contiguous()
-        kt, vt = kv_project(bank, plan, T, wkv, HK, Dh, mean, rstd, dtype)
+        kt, vt, ktt, vtt = kv_project(bank, plan, T, wkv, HK, Dh, mean, rstd, dtype, ("k", "v", "kt", "vt"))
         om = omega.float().contiguous()
         out = torch.empty(B, Lq, H, Dh, device=q.device, dtype=dtype)
         Lp = (Lq + 127) // 128 * 128
         lse = torch.empty(B, H, Lp, device=q.device, dtype=torch.float32)
-        call("moc_xattn_fwd", L.dtype_code(dtype), ptr(q), ptr(kt), ptr(vt), ptr(plan.edge_u), ptr(om), B, Lq, H, HK,
-             Dh, T, NS, float(Dh) ** -0.5, ptr(out), ptr(lse), stream_ptr(q.device))
-        ctx.save_for_backward(q, bank, wkv, om, out, lse, kt, vt, mean, rstd, plan.uniq, plan.n_uniq, plan.edge_u,
-                              plan.csr_off, plan.csr_edge)
+        call("moc_xattn_fwd", L.dtype_code(dtype), ptr(q), ptr(kt), ptr(vtt), plan.max_u * HK, ptr(plan.edge_u),
+             ptr(om), B, Lq, H, HK, Dh, T, NS, float(Dh) ** -0.5, ptr(out), ptr(lse), stream_ptr(q.device))
+        ctx.save_for_backward(q, bank, wkv, om, out, lse, kt, vt, ktt, mean, rstd, plan.uniq, plan.n_uniq,
+                              plan.edge_u, plan.csr_off, plan.csr_edge)
         ctx.cfg = (num_chapters, T, norm, eps, HK, plan.max_u, wk.dtype, wv.dtype, bank.dtype)
         return out
 
     @staticmethod
     def backward(ctx, dout):
-        (q, bank, wkv, om, out, lse, kt, vt, mean, rstd, uniq, n_uniq, edge_u, csr_off,
+        (q, bank, wkv, om, out, lse, kt, vt, ktt, mean, rstd, uniq, n_uniq, edge_u, csr_off,
          csr_edge) = ctx.saved_tensors
         C, T, norm, eps, HK, max_u, wk_dtype, wv_dtype, bank_dtype = ctx.cfg
         dtype = q.dtype
@@ -288,8 +293,8 @@ class _RoutedAttention(torch.autograd.Function):
         dot = torch.empty_like(qt)
         call("moc_xattn_bwd_prep", dt, ptr(q), ptr(out), ptr(dout), B, Lq, H, Dh, ptr(delta), ptr(qt), ptr(dot), st)
         dq = torch.empty_like(q)
-        call("moc_xattn_bwd_dq", dt, ptr(q), ptr(kt), ptr(vt), ptr(edge_u), ptr(om), ptr(dout), ptr(lse), ptr(delta),
-             B, Lq, H, HK, Dh, T, NS, scale, ptr(dq), st)
+        call("moc_xattn_bwd_dq", dt, ptr(q), ptr(kt), ptr(ktt), ptr(vt), kt.shape[0] * HK, ptr(edge_u), ptr(om),
+             ptr(dout), ptr(lse), ptr(delta), B, Lq, H, HK, Dh, T, NS, scale, ptr(dq), st)
         dkv_edge = torch.empty(B * NS * T, 2 * KV, device=dev, dtype=dtype)
         dom_part = torch.zeros(B * NS, H, device=dev, dtype=torch.float32)
         call("moc_xattn_bwd_dkv", dt, ptr(q), ptr(qt), ptr(dout), ptr(dot), ptr(kt), ptr(vt), ptr(edge_u), ptr(om),

@@ -266,7 +266,7 @@ class _TokenRouted(torch.autograd.Function):
         routed = routed.contiguous()
         all_plan = ops.chapter_plan(torch.arange(C, device=q.device, dtype=torch.int32), C)
         wkv = torch.cat([wk, wv], 0).to(dtype).contiguous()
-        kt, vt = ops.kv_project(routed, all_plan, BLOCK, wkv, HK, D, None, None, dtype)
+        kt, vt = ops.kv_project(routed, all_plan, BLOCK, wkv, HK, D, None, None, dtype, ("k", "v"))
         S = idx.shape[-1]
         segs = _segments(idx, w, mode, C, False, HQ, HK, C)
         out, saved = _forward(q, kt, vt, "tiles", segs, mode, S, D ** -0.5)

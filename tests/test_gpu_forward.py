@@ -162,7 +162,7 @@ def test_kv_project_matches_reference(dev, dtype, bank_dtype, norm):
     if code:
         mean, rstd = ops.row_stats(bg, plan, T, code, 1e-5)
     wkv = torch.cat([wk, wv]).to(dev, dtype)
-    kt, vt = ops.kv_project(bg, plan, T, wkv, HK, Dh, mean, rstd, dtype)
+    kt, vt, ktt, vtt = ops.kv_project(bg, plan, T, wkv, HK, Dh, mean, rstd, dtype, ("k", "v", "kt", "vt"))
     n_u = int(plan.n_uniq[0])
     uniq = plan.uniq[:n_u].cpu().long()
     X, _ = O.gather_chapters(bank.to(bank_dtype).double(), uniq.view(1, -1), T)
@@ -176,6 +176,9 @@ def test_kv_project_matches_reference(dev, dtype, bank_dtype, norm):
     tol = 1e-4 if dtype == torch.float32 else 2e-2
     assert_rel(kt[:n_u].cpu(), Kr, tol, "K tiles")
     assert_rel(vt[:n_u].cpu(), Vr, tol, "V tiles")
+    # the transposed tiles are the same values, bit for bit
+    assert torch.equal(ktt[:n_u].transpose(-1, -2).cpu(), kt[:n_u].cpu())
+    assert torch.equal(vtt[:n_u].transpose(-1, -2).cpu(), vt[:n_u].cpu())
 
 
 # --------------------------------------------------- routed attention forward
