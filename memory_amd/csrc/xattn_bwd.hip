@@ -18,6 +18,8 @@
 // order), so the later dX = [dk dv] [Wk; Wv] GEMM runs over distinct chapters.
 #include "moc_common.h"
 
+#include <type_traits>
+
 namespace moc {
 
 constexpr int kBThreads = 256;
@@ -215,15 +217,27 @@ __global__ __launch_bounds__(kBThreads) void xattn_bwd_dq_kernel(
 
 // dk/dv, slot-group decomposition.  One workgroup = one (sequence b, kv head
 // hk, group of SG consecutive slots); wave w owns slot SG*blockIdx.x + w, i.e.
-// the 64 keys of one selected chapter, whose K and V tiles sit in LDS.  All
-// slots of a sequence attend the same queries, so the query-side tiles of a
-// step (Q and dO row-major, Q^T and dO^T, QS queries each) are staged in LDS
-// once and shared by the SG waves.  Global loads of step n+1 are issued before
-// the math of step n.  Output: per-edge dk / dv rows (edge e = b*NS + slot),
-// summed per distinct chapter by dkv_reduce_kernel.
+// the 64 keys of one selected chapter.  All slots of a sequence attend the same
+// queries, so the query-side tiles of a step (Q and dO row-major, Q^T and dO^T,
+// QS queries each) are staged in LDS once and shared by the SG waves; they are
+// double-buffered, the next step's global loads being issued before the math of
+// the current one, so a step costs one barrier.  In bf16 the wave's K and V
+// fragments live in registers for the whole kernel (loaded once from HBM); the
+// fp32 variant keeps them in LDS.  Output: per-edge dk / dv rows (edge e =
+// b*NS + slot), summed per distinct chapter by dkv_reduce_kernel, and
+// d omega per (edge, query head).
+//
+// Per score element (key j, query i) with p = exp2(c s - lse_i) the softmax
+// probability (c = omega * scale * log2 e, s = q_i . k_j):
+//   p~   = omega p                      (A operand of dV = P~^T dO)
+//   ds~  = p~ (omega scale dP - scale delta_i)  (A operand of dK = dS~^T Q)
+//   dw  += p~ (ds~/p~ * s + dP) / omega (summed, divided by omega once at the end)
+// which matches the gradient of softmax(omega s_ij scale) against omega-scaled
+// values; omega == 0 takes the general form (keys and values vanish but the
+// gradient of omega does not).
 template <typename T> struct DkvCfg;
-template <> struct DkvCfg<bf16> { static constexpr int SG = 4, QS = 64; };
-template <> struct DkvCfg<float> { static constexpr int SG = 2, QS = 32; };
+template <> struct DkvCfg<bf16> { static constexpr int SG = 4, QS = 64; static constexpr bool kKVRegs = true; };
+template <> struct DkvCfg<float> { static constexpr int SG = 2, QS = 32; static constexpr bool kKVRegs = false; };
 
 template <typename T>
 __global__ __launch_bounds__(64 * DkvCfg<T>::SG, 1) void xattn_bwd_dkv_kernel(
@@ -233,15 +247,16 @@ __global__ __launch_bounds__(64 * DkvCfg<T>::SG, 1) void xattn_bwd_dkv_kernel(
     int H, int HK, int NS, float scale_log2, float scale, T* __restrict__ dkv_edge, float* __restrict__ domega_part) {
   typedef typename Frag<T>::type F8;
   constexpr int SG = DkvCfg<T>::SG, QS = DkvCfg<T>::QS, NT = 64 * SG;
+  constexpr bool kKVRegs = DkvCfg<T>::kKVRegs;
   constexpr int EPC = 16 / (int)sizeof(T);
   using TileK = SwzTile<T, 64>;   // [key][dim] and [query][dim]
   using TileT = SwzTile<T, QS>;   // [dim][query]
   constexpr int KVB = 64 * 64 * (int)sizeof(T);
   constexpr int STB = 64 * QS * (int)sizeof(T);  // one staged tile (always 8 KB)
   constexpr int NCH = 4 * STB / 16 / NT;         // staged chunks per thread per step
-  __shared__ __attribute__((aligned(16))) char sKV[SG][2][KVB];
-  __shared__ __attribute__((aligned(16))) char sQ[STB], sD[STB], sQt[STB], sDt[STB];
-  __shared__ float sL[QS], sDl[QS];
+  __shared__ __attribute__((aligned(16))) char sKV[kKVRegs ? 1 : SG][2][kKVRegs ? 16 : KVB];
+  __shared__ __attribute__((aligned(16))) char sStage[2][4][STB];  // [buf][Q, dO, Q^T, dO^T]
+  __shared__ float sL[2][QS], sDl[2][QS];
 
   const int b = blockIdx.z, hk = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -254,18 +269,39 @@ __global__ __launch_bounds__(64 * DkvCfg<T>::SG, 1) void xattn_bwd_dkv_kernel(
   const int KV = HK * 64;
   const size_t row_stride = 2 * (size_t)KV;
 
-  // K and V of this wave's chapter -> LDS (each wave loads its own pair)
+  // K / V fragments of this wave's chapter: B operands of S = Q K^T and dP = dO V^T
+  // (key row 16 kb + c16, dims 32 ks + 8 g .. +7)
+  F8 kreg[4][2], vreg[4][2];
   if (active) {
     const T* kp = ktiles + ((size_t)u * HK + hk) * 4096;
     const T* vp = vtiles + ((size_t)u * HK + hk) * 4096;
-    for (int i = lane; i < 64 * (64 / EPC); i += 64) {
-      const int row = i / (64 / EPC), cc = (i % (64 / EPC)) * EPC;
-      st16(sKV[wave][0] + TileK::off(row, cc), ld16(kp + (size_t)i * EPC));
-      st16(sKV[wave][1] + TileK::off(row, cc), ld16(vp + (size_t)i * EPC));
+    if constexpr (kKVRegs) {
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+          kreg[kb][ks] = Load8<T, T>::run(kp + (16 * kb + c16) * 64 + 32 * ks + 8 * g);
+          vreg[kb][ks] = Load8<T, T>::run(vp + (16 * kb + c16) * 64 + 32 * ks + 8 * g);
+        }
+    } else {
+      for (int i = lane; i < 64 * (64 / EPC); i += 64) {
+        const int row = i / (64 / EPC), cc = (i % (64 / EPC)) * EPC;
+        st16(sKV[wave][0] + TileK::off(row, cc), ld16(kp + (size_t)i * EPC));
+        st16(sKV[wave][1] + TileK::off(row, cc), ld16(vp + (size_t)i * EPC));
+      }
     }
   }
+  auto kfrag = [&](int kb, int ks) -> F8 {
+    if constexpr (kKVRegs) return kreg[kb][ks];
+    else return TileK::frag(sKV[wave][0], 16 * kb + c16, 32 * ks + 8 * g);
+  };
+  auto vfrag = [&](int kb, int ks) -> F8 {
+    if constexpr (kKVRegs) return vreg[kb][ks];
+    else return TileK::frag(sKV[wave][1], 16 * kb + c16, 32 * ks + 8 * g);
+  };
   const float w = active ? omega[e] : 0.f;
   const float c = w * scale_log2, dsc = w * scale;
+  const float lw = w > 0.f ? __log2f(w) : 0.f;
 
   f32x4 dk[4][4], dv[4][4];
 #pragma unroll
@@ -279,7 +315,7 @@ __global__ __launch_bounds__(64 * DkvCfg<T>::SG, 1) void xattn_bwd_dkv_kernel(
   const int nstep = (L + QS - 1) / QS;
   for (int hq = hk * G; hq < hk * G + G; ++hq) {
     const size_t bh = (size_t)b * H + hq;
-    // staged chunk c of a step: tile = c / (STB/16); within tile: row / col chunk
+    // staged chunk ch of a step: tile = ch / (STB/16); within a tile: row / column chunk
     V16 pre[NCH];
     float preL = 0.f, preD = 0.f;
     auto fetch = [&](int st) {
@@ -304,29 +340,37 @@ __global__ __launch_bounds__(64 * DkvCfg<T>::SG, 1) void xattn_bwd_dkv_kernel(
         preD = delta[bh * Lp + q0 + tid];
       }
     };
-    auto stash = [&]() {
+    auto stash = [&](int buf) {
 #pragma unroll
       for (int i = 0; i < NCH; ++i) {
         const int ch = tid + NT * i;
         const int tile = ch / (STB / 16), r = ch % (STB / 16);
         if (tile < 2) {
           const int qq = r / (64 / EPC), cc = (r % (64 / EPC)) * EPC;
-          st16((tile == 0 ? sQ : sD) + TileK::off(qq, cc), pre[i]);
+          st16(sStage[buf][tile] + TileK::off(qq, cc), pre[i]);
         } else {
           const int dd = r / (QS / EPC), cc = (r % (QS / EPC)) * EPC;
-          st16((tile == 2 ? sQt : sDt) + TileT::off(dd, cc), pre[i]);
+          st16(sStage[buf][tile] + TileT::off(dd, cc), pre[i]);
         }
       }
-      if (tid < QS) { sL[tid] = preL; sDl[tid] = preD; }
+      if (tid < QS) {
+        // scaled here, not in fetch, so the loads stay in flight across a step's math
+        sL[buf][tid] = preL;
+        sDl[buf][tid] = preD * scale;
+      }
     };
     float dwp = 0.f;
     fetch(0);
+    stash(0);
+    __syncthreads();
     for (int st = 0; st < nstep; ++st) {
-      __syncthreads();  // previous step's readers are done (and K/V visible on the first step)
-      stash();
-      __syncthreads();
+      const int buf = st & 1;
       if (st + 1 < nstep) fetch(st + 1);
       if (active) {
+        const char* sQ = sStage[buf][0];
+        const char* sD = sStage[buf][1];
+        const char* sQt = sStage[buf][2];
+        const char* sDt = sStage[buf][3];
 #pragma unroll
         for (int half = 0; half < QS / 32; ++half) {
           const int qb0 = 32 * half;
@@ -348,8 +392,8 @@ __global__ __launch_bounds__(64 * DkvCfg<T>::SG, 1) void xattn_bwd_dkv_kernel(
             }
 #pragma unroll
             for (int kb = 0; kb < 4; ++kb) {
-              F8 kf = TileK::frag(sKV[wave][0], 16 * kb + c16, 32 * ks + 8 * g);
-              F8 vf = TileK::frag(sKV[wave][1], 16 * kb + c16, 32 * ks + 8 * g);
+              const F8 kf = kfrag(kb, ks);
+              const F8 vf = vfrag(kb, ks);
 #pragma unroll
               for (int qb = 0; qb < 2; ++qb) {
                 mma(sc[qb][kb], qa[qb], kf);
@@ -358,23 +402,39 @@ __global__ __launch_bounds__(64 * DkvCfg<T>::SG, 1) void xattn_bwd_dkv_kernel(
             }
           }
           F8 pa[4], sa[4];
+          // omega is uniform per wave: the branch sits outside the element loop
+          auto grad_elems = [&](auto positive) {
+            constexpr bool kPos = decltype(positive)::value;
 #pragma unroll
-          for (int qb = 0; qb < 2; ++qb) {
-            const f32x4 l2 = *reinterpret_cast<const f32x4*>(&sL[qb0 + 16 * qb + 4 * g]);
-            const f32x4 dl = *reinterpret_cast<const f32x4*>(&sDl[qb0 + 16 * qb + 4 * g]);
+            for (int qb = 0; qb < 2; ++qb) {
+              // l2 - log2(omega): exp2(c s - l2) = omega p;  dl = scale * delta
+              const f32x4 l2 = *reinterpret_cast<const f32x4*>(&sL[buf][qb0 + 16 * qb + 4 * g]) - lw;
+              const f32x4 dl = *reinterpret_cast<const f32x4*>(&sDl[buf][qb0 + 16 * qb + 4 * g]);
 #pragma unroll
-            for (int kb = 0; kb < 4; ++kb)
+              for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-              for (int x = 0; x < 4; ++x) {
-                const float sraw = sc[qb][kb][x];
-                const float pr = __builtin_amdgcn_exp2f(sraw * c - l2[x]);
-                const float dpu = dp[qb][kb][x];
-                const float ds = pr * (w * dpu - dl[x]);
-                dwp += ds * sraw * scale + pr * dpu;
-                pa[kb][4 * qb + x] = from_f<T>(pr * w);
-                sa[kb][4 * qb + x] = from_f<T>(ds * dsc);
-              }
-          }
+                for (int x = 0; x < 4; ++x) {
+                  const float sraw = sc[qb][kb][x];
+                  const float dpu = dp[qb][kb][x];
+                  float pt = 0.f, dst = 0.f;
+                  if constexpr (kPos) {
+                    pt = __builtin_amdgcn_exp2f(sraw * c - l2[x]);  // omega p
+                    const float tq = dpu * dsc - dl[x];              // scale (omega dP - delta)
+                    dst = pt * tq;
+                    dwp += pt * (tq * sraw + dpu);
+                  } else {
+                    const float pr = __builtin_amdgcn_exp2f(-l2[x]);  // every logit is 0
+                    dwp += pr * (dpu - dl[x] * sraw);
+                  }
+                  pa[kb][4 * qb + x] = from_f<T>(pt);
+                  sa[kb][4 * qb + x] = from_f<T>(dst);
+                }
+            }
+          };
+          if (w > 0.f)
+            grad_elems(std::true_type{});
+          else
+            grad_elems(std::false_type{});
 #pragma unroll
           for (int db = 0; db < 4; ++db) {
             F8 bq = TileT::frag44(sQt, 16 * db + c16, qb0 + 4 * g, qb0 + 16 + 4 * g);
@@ -387,9 +447,12 @@ __global__ __launch_bounds__(64 * DkvCfg<T>::SG, 1) void xattn_bwd_dkv_kernel(
           }
         }
       }
+      if (st + 1 < nstep) stash(buf ^ 1);
+      __syncthreads();
     }
     if (active) {
       dwp = wave_sum(dwp);
+      if (w > 0.f) dwp /= w;
       if (lane == 0) domega_part[(size_t)e * H + hq] = dwp;
     }
   }

@@ -31,14 +31,16 @@ def _ref_grads(q, bank, Wk, Wv, ci, cw, dO, T, S, norm, HK):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("B,Lq,H,HK,C,k,norm,dup", [
-    (2, 128, 4, 4, 33, 4, None, False),
-    (3, 100, 4, 2, 12, 5, "rms", True),
-    (2, 130, 2, 1, 20, 3, "layernorm", True),
-    (4, 64, 4, 4, 9, 8, None, True),
+@pytest.mark.parametrize("B,Lq,H,HK,C,k,norm,dup,zero_w", [
+    (2, 128, 4, 4, 33, 4, None, False, False),
+    (3, 100, 4, 2, 12, 5, "rms", True, False),
+    (2, 130, 2, 1, 20, 3, "layernorm", True, False),
+    (4, 64, 4, 4, 9, 8, None, True, False),
+    (3, 96, 4, 2, 16, 6, None, True, True),
 ])
-def test_routed_attention_backward(gpu_device, dtype, B, Lq, H, HK, C, k, norm, dup):
-    print(f"routed_attention bwd dtype={dtype} B={B} L={Lq} H={H} HK={HK} C={C} k={k} norm={norm}", flush=True)
+def test_routed_attention_backward(gpu_device, dtype, B, Lq, H, HK, C, k, norm, dup, zero_w):
+    print(f"routed_attention bwd dtype={dtype} B={B} L={Lq} H={H} HK={HK} C={C} k={k} norm={norm} "
+          f"zero_w={zero_w}", flush=True)
     from memory_amd import ops
     dev = gpu_device
     g = gen(100 + B + Lq)
@@ -54,6 +56,11 @@ def test_routed_attention_backward(gpu_device, dtype, B, Lq, H, HK, C, k, norm, 
         logits = logits[:1].expand(B, C) + 0.01 * torch.randn(B, C, generator=g)
     idx, w, _ = O.route_sequence(logits, k, S)
     ci, cw = O.prepend_shared_chapters(idx, w, num_chapters=C, num_shared_chapters=S, routed_scaling_factor=2.5)
+    if zero_w:
+        # exact-zero chapter weights: keys / values vanish, d omega does not
+        cw = cw.clone()
+        cw[:, 2] = 0.0
+        cw[0, 4] = 0.0
     q = (h @ Wq.T).view(B, Lq, H, Dh)
     dO = torch.randn(B, Lq, H, Dh, generator=g)
 
