@@ -153,8 +153,8 @@ int moc_xattn_bwd_dq(int dtype, const void* q, const void* k_tiles, const void* 
 /* dK/dV per edge (edge e = b * NS + slot): dkv_edge [B * NS * T][2 * HK * Dh] (dtype) holds for
  * the chapter in slot `slot` of sequence b the rows [dL/dk (all kv heads) | dL/dv], where
  * dL/dk, dL/dv are gradients w.r.t. the unweighted projected keys/values (omega folded in).
- * Rows of skipped slots are not written.  domega_part f32 [B * NS][H]: per (edge, query head)
- * parts of dL/domega (caller sums over H; skipped edges are not written). */
+ * Rows of skipped slots are not written.  domega_part f32 [B * NS][HK]: per (edge, kv head)
+ * parts of dL/domega (caller sums over HK; skipped edges are not written). */
 int moc_xattn_bwd_dkv(int dtype, const void* q, const void* qt, const void* dout, const void* dot,
                       const void* k_tiles, const void* v_tiles, const int32_t* slot_u, const float* omega,
                       const float* lse, const float* delta, int64_t B, int64_t L, int H, int HK, int Dh, int T,

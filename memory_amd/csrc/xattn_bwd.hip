@@ -18,8 +18,6 @@
 // order), so the later dX = [dk dv] [Wk; Wv] GEMM runs over distinct chapters.
 #include "moc_common.h"
 
-#include <type_traits>
-
 namespace moc {
 
 constexpr int kBThreads = 256;
@@ -228,13 +226,15 @@ __global__ __launch_bounds__(kBThreads) void xattn_bwd_dq_kernel(
 // d omega per (edge, query head).
 //
 // Per score element (key j, query i) with p = exp2(c s - lse_i) the softmax
-// probability (c = omega * scale * log2 e, s = q_i . k_j):
-//   p~   = omega p                      (A operand of dV = P~^T dO)
-//   ds~  = p~ (omega scale dP - scale delta_i)  (A operand of dK = dS~^T Q)
-//   dw  += p~ (ds~/p~ * s + dP) / omega (summed, divided by omega once at the end)
-// which matches the gradient of softmax(omega s_ij scale) against omega-scaled
-// values; omega == 0 takes the general form (keys and values vanish but the
-// gradient of omega does not).
+// probability (c = omega * scale * log2 e, s = q_i . k_j, dP = dO_i . v_j):
+//   p~   = omega p = exp2(c s - (lse_i - log2 omega))   (A operand of dV = P~^T dO)
+//   t    = scale (omega dP - delta_i)
+//   ds~  = p~ t                                          (A operand of dK = dS~^T Q)
+// which is the gradient of softmax(omega s scale) against omega-scaled values.
+// d omega = sum_ij p~ (t s + dP) / omega is read off the accumulators at the end:
+// sum_j dk_j . k_j + dv_j . v_j.  omega == 0 runs the same loop with p~ = p (log2
+// omega taken as 0): d omega then needs no division, and the chapter's dK / dV
+// (which vanish) are zeroed.
 template <typename T> struct DkvCfg;
 template <> struct DkvCfg<bf16> { static constexpr int SG = 4, QS = 64; static constexpr bool kKVRegs = true; };
 template <> struct DkvCfg<float> { static constexpr int SG = 2, QS = 32; static constexpr bool kKVRegs = false; };
@@ -253,7 +253,7 @@ __global__ __launch_bounds__(64 * DkvCfg<T>::SG, 1) void xattn_bwd_dkv_kernel(
   using TileT = SwzTile<T, QS>;   // [dim][query]
   constexpr int KVB = 64 * 64 * (int)sizeof(T);
   constexpr int STB = 64 * QS * (int)sizeof(T);  // one staged tile (always 8 KB)
-  constexpr int NCH = 4 * STB / 16 / NT;         // staged chunks per thread per step
+  constexpr int CPT = STB / 16 / NT;             // chunks per thread per staged tile
   __shared__ __attribute__((aligned(16))) char sKV[kKVRegs ? 1 : SG][2][kKVRegs ? 16 : KVB];
   __shared__ __attribute__((aligned(16))) char sStage[2][4][STB];  // [buf][Q, dO, Q^T, dO^T]
   __shared__ float sL[2][QS], sDl[2][QS];
@@ -315,25 +315,33 @@ __global__ __launch_bounds__(64 * DkvCfg<T>::SG, 1) void xattn_bwd_dkv_kernel(
   const int nstep = (L + QS - 1) / QS;
   for (int hq = hk * G; hq < hk * G + G; ++hq) {
     const size_t bh = (size_t)b * H + hq;
-    // staged chunk ch of a step: tile = ch / (STB/16); within a tile: row / column chunk
-    V16 pre[NCH];
+    // staged tiles of a step: 0 = Q rows, 1 = dO rows ([query][dim]), 2 = Q^T, 3 = dO^T
+    // ([dim][query]); every thread moves CPT 16-byte chunks of each.  Row tiles read
+    // through a buffer spanning this sequence only, so rows past L come back as zeros.
+    const uint32_t seq_bytes = (uint32_t)((size_t)L * H * 64 * sizeof(T));
+    const uint32_t head_bytes = (uint32_t)((size_t)64 * Lp * sizeof(T));
+    const Buf bq(q + (size_t)b * L * H * 64, seq_bytes), bd(dout + (size_t)b * L * H * 64, seq_bytes);
+    const Buf bqt(qt + bh * 64 * Lp, head_bytes), bdt(dot + bh * 64 * Lp, head_bytes);
+    uint32_t voff_r[CPT], voff_t[CPT];
+#pragma unroll
+    for (int j = 0; j < CPT; ++j) {
+      const int r = tid + NT * j;
+      const int qq = r / (64 / EPC), cc = (r % (64 / EPC)) * EPC;
+      const int dd = r / (QS / EPC), ct = (r % (QS / EPC)) * EPC;
+      voff_r[j] = (uint32_t)(((qq * H + hq) * 64 + cc) * (int)sizeof(T));
+      voff_t[j] = (uint32_t)((dd * Lp + ct) * (int)sizeof(T));
+    }
+    V16 pre[4 * CPT];
     float preL = 0.f, preD = 0.f;
     auto fetch = [&](int st) {
       const int q0 = st * QS;
+      const uint32_t so_r = (uint32_t)((size_t)q0 * H * 64 * sizeof(T)), so_t = (uint32_t)(q0 * sizeof(T));
 #pragma unroll
-      for (int i = 0; i < NCH; ++i) {
-        const int ch = tid + NT * i;
-        const int tile = ch / (STB / 16), r = ch % (STB / 16);
-        if (tile < 2) {  // Q / dO rows: [query][dim], 64/EPC chunks per row
-          const int qq = r / (64 / EPC), cc = (r % (64 / EPC)) * EPC;
-          const int qi = q0 + qq;
-          const T* src = tile == 0 ? q : dout;
-          pre[i] = qi < L ? ld16(src + ((size_t)(b * (size_t)L + qi) * H + hq) * 64 + cc) : V16{{0u, 0u, 0u, 0u}};
-        } else {         // Q^T / dO^T: [dim][query], QS/EPC chunks per row
-          const int dd = r / (QS / EPC), cc = (r % (QS / EPC)) * EPC;
-          const T* src = tile == 2 ? qt : dot;
-          pre[i] = ld16(src + (bh * 64 + dd) * Lp + q0 + cc);
-        }
+      for (int j = 0; j < CPT; ++j) {
+        pre[j] = bq.load16(voff_r[j], so_r);
+        pre[CPT + j] = bd.load16(voff_r[j], so_r);
+        pre[2 * CPT + j] = bqt.load16(voff_t[j], so_t);
+        pre[3 * CPT + j] = bdt.load16(voff_t[j], so_t);
       }
       if (tid < QS) {
         preL = lse[bh * Lp + q0 + tid];
@@ -342,16 +350,14 @@ __global__ __launch_bounds__(64 * DkvCfg<T>::SG, 1) void xattn_bwd_dkv_kernel(
     };
     auto stash = [&](int buf) {
 #pragma unroll
-      for (int i = 0; i < NCH; ++i) {
-        const int ch = tid + NT * i;
-        const int tile = ch / (STB / 16), r = ch % (STB / 16);
-        if (tile < 2) {
-          const int qq = r / (64 / EPC), cc = (r % (64 / EPC)) * EPC;
-          st16(sStage[buf][tile] + TileK::off(qq, cc), pre[i]);
-        } else {
-          const int dd = r / (QS / EPC), cc = (r % (QS / EPC)) * EPC;
-          st16(sStage[buf][tile] + TileT::off(dd, cc), pre[i]);
-        }
+      for (int j = 0; j < CPT; ++j) {
+        const int r = tid + NT * j;
+        const int qq = r / (64 / EPC), cc = (r % (64 / EPC)) * EPC;
+        const int dd = r / (QS / EPC), ct = (r % (QS / EPC)) * EPC;
+        st16(sStage[buf][0] + TileK::off(qq, cc), pre[j]);
+        st16(sStage[buf][1] + TileK::off(qq, cc), pre[CPT + j]);
+        st16(sStage[buf][2] + TileT::off(dd, ct), pre[2 * CPT + j]);
+        st16(sStage[buf][3] + TileT::off(dd, ct), pre[3 * CPT + j]);
       }
       if (tid < QS) {
         // scaled here, not in fetch, so the loads stay in flight across a step's math
@@ -359,7 +365,6 @@ __global__ __launch_bounds__(64 * DkvCfg<T>::SG, 1) void xattn_bwd_dkv_kernel(
         sDl[buf][tid] = preD * scale;
       }
     };
-    float dwp = 0.f;
     fetch(0);
     stash(0);
     __syncthreads();
@@ -402,39 +407,23 @@ __global__ __launch_bounds__(64 * DkvCfg<T>::SG, 1) void xattn_bwd_dkv_kernel(
             }
           }
           F8 pa[4], sa[4];
-          // omega is uniform per wave: the branch sits outside the element loop
-          auto grad_elems = [&](auto positive) {
-            constexpr bool kPos = decltype(positive)::value;
 #pragma unroll
-            for (int qb = 0; qb < 2; ++qb) {
-              // l2 - log2(omega): exp2(c s - l2) = omega p;  dl = scale * delta
-              const f32x4 l2 = *reinterpret_cast<const f32x4*>(&sL[buf][qb0 + 16 * qb + 4 * g]) - lw;
-              const f32x4 dl = *reinterpret_cast<const f32x4*>(&sDl[buf][qb0 + 16 * qb + 4 * g]);
+          for (int qb = 0; qb < 2; ++qb) {
+            // l2 - log2(omega): exp2(c s - l2) = omega p;  dl = scale * delta
+            const f32x4 l2 = *reinterpret_cast<const f32x4*>(&sL[buf][qb0 + 16 * qb + 4 * g]) - lw;
+            const f32x4 dl = *reinterpret_cast<const f32x4*>(&sDl[buf][qb0 + 16 * qb + 4 * g]);
 #pragma unroll
-              for (int kb = 0; kb < 4; ++kb)
+            for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-                for (int x = 0; x < 4; ++x) {
-                  const float sraw = sc[qb][kb][x];
-                  const float dpu = dp[qb][kb][x];
-                  float pt = 0.f, dst = 0.f;
-                  if constexpr (kPos) {
-                    pt = __builtin_amdgcn_exp2f(sraw * c - l2[x]);  // omega p
-                    const float tq = dpu * dsc - dl[x];              // scale (omega dP - delta)
-                    dst = pt * tq;
-                    dwp += pt * (tq * sraw + dpu);
-                  } else {
-                    const float pr = __builtin_amdgcn_exp2f(-l2[x]);  // every logit is 0
-                    dwp += pr * (dpu - dl[x] * sraw);
-                  }
-                  pa[kb][4 * qb + x] = from_f<T>(pt);
-                  sa[kb][4 * qb + x] = from_f<T>(dst);
-                }
-            }
-          };
-          if (w > 0.f)
-            grad_elems(std::true_type{});
-          else
-            grad_elems(std::false_type{});
+              for (int x = 0; x < 4; ++x) {
+                const float sraw = sc[qb][kb][x];
+                const float dpu = dp[qb][kb][x];
+                const float pt = __builtin_amdgcn_exp2f(sraw * c - l2[x]);  // omega p (p if omega = 0)
+                const float tq = dpu * dsc - dl[x];                           // scale (omega dP - delta)
+                pa[kb][4 * qb + x] = from_f<T>(pt);
+                sa[kb][4 * qb + x] = from_f<T>(pt * tq);
+              }
+          }
 #pragma unroll
           for (int db = 0; db < 4; ++db) {
             F8 bq = TileT::frag44(sQt, 16 * db + c16, qb0 + 4 * g, qb0 + 16 + 4 * g);
@@ -450,13 +439,38 @@ __global__ __launch_bounds__(64 * DkvCfg<T>::SG, 1) void xattn_bwd_dkv_kernel(
       if (st + 1 < nstep) stash(buf ^ 1);
       __syncthreads();
     }
-    if (active) {
-      dwp = wave_sum(dwp);
-      if (w > 0.f) dwp /= w;
-      if (lane == 0) domega_part[(size_t)e * H + hq] = dwp;
-    }
   }
   if (!active) return;
+  // omega dL/domega = sum_ij p~ (t s + dP) = sum_j dk_j . k_j + dv_j . v_j (the accumulators
+  // are p~-weighted sums of dS~^T Q and P~^T dO), summed over the query heads of hk
+  {
+    const T* kp = ktiles + ((size_t)u * HK + hk) * 4096;
+    const T* vp = vtiles + ((size_t)u * HK + hk) * 4096;
+    float acc = 0.f;
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int x = 0; x < 4; ++x) {
+          const int off = (16 * kb + 4 * g + x) * 64 + 16 * db + c16;
+          acc += dk[kb][db][x] * to_f(kp[off]) + dv[kb][db][x] * to_f(vp[off]);
+        }
+    acc = wave_sum(acc);
+    if (w > 0.f) acc /= w;
+    if (lane == 0) domega_part[(size_t)e * HK + hk] = acc;
+  }
+  if (w == 0.f) {
+    // the element loop ran with p in place of omega p: keys and values of a zero-weight
+    // chapter carry no gradient
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+        dk[kb][db] = f32x4{0.f, 0.f, 0.f, 0.f};
+        dv[kb][db] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+  }
   T* rows = dkv_edge + (size_t)e * 64 * row_stride;
 #pragma unroll
   for (int kb = 0; kb < 4; ++kb)
@@ -678,6 +692,8 @@ int moc_xattn_bwd_dkv(int dtype, const void* q, const void* qt, const void* dout
   MOC_REQUIRE(Dh == kBDh && T == kBT, MOC_ERR_UNSUPPORTED, "moc_xattn_bwd_dkv: needs head_dim 64 and T 64");
   MOC_REQUIRE(H > 0 && HK > 0 && H % HK == 0 && NS > 0 && B >= 0 && B < 65536, MOC_ERR_ARG,
               "moc_xattn_bwd_dkv: bad shape");
+  MOC_REQUIRE(L * H * 64 * (dtype == MOC_F32 ? 4 : 2) < ((int64_t)1 << 32), MOC_ERR_UNSUPPORTED,
+              "moc_xattn_bwd_dkv: one sequence's q / dout must be < 4 GiB (L=%lld, H=%d)", (long long)L, H);
   if (B == 0 || L == 0) return MOC_OK;
   const int Lp = (int)((L + 127) / 128 * 128);
   const float sl2 = scale * 1.4426950408889634f;

@@ -296,7 +296,7 @@ class _RoutedAttention(torch.autograd.Function):
         call("moc_xattn_bwd_dq", dt, ptr(q), ptr(kt), ptr(ktt), ptr(vt), kt.shape[0] * HK, ptr(edge_u), ptr(om),
              ptr(dout), ptr(lse), ptr(delta), B, Lq, H, HK, Dh, T, NS, scale, ptr(dq), st)
         dkv_edge = torch.empty(B * NS * T, 2 * KV, device=dev, dtype=dtype)
-        dom_part = torch.zeros(B * NS, H, device=dev, dtype=torch.float32)
+        dom_part = torch.zeros(B * NS, HK, device=dev, dtype=torch.float32)
         call("moc_xattn_bwd_dkv", dt, ptr(q), ptr(qt), ptr(dout), ptr(dot), ptr(kt), ptr(vt), ptr(edge_u), ptr(om),
              ptr(lse), ptr(delta), B, Lq, H, HK, Dh, T, NS, scale, ptr(dkv_edge), ptr(dom_part), st)
         dkv = torch.empty(max_u * T, 2 * KV, device=dev, dtype=dtype)
