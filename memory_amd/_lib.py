@@ -101,13 +101,16 @@ def lib():
 
 
 # Optional per-entry-point GPU timing: when set to a dict, every call records a
-# pair of events on the current stream, appended to KERNEL_EVENTS[name].
+# pair of events on the current stream (the one the kernels are launched on),
+# appended to KERNEL_EVENTS[name]; KERNEL_EVENTS_ONLY (a set of names) limits the
+# recording to those entry points.
 KERNEL_EVENTS = None
+KERNEL_EVENTS_ONLY = None
 
 
 def call(name: str, *args) -> None:
     ev = KERNEL_EVENTS
-    if ev is not None:
+    if ev is not None and (KERNEL_EVENTS_ONLY is None or name in KERNEL_EVENTS_ONLY):
         e0 = torch.cuda.Event(enable_timing=True)
         e1 = torch.cuda.Event(enable_timing=True)
         e0.record()

@@ -19,6 +19,8 @@
 // which lets one projected chapter serve every sequence that selected it.
 #include "moc_common.h"
 
+#include <type_traits>
+
 namespace moc {
 
 // Per-row statistics for the normalisation prologue: mean (layernorm only) and
@@ -90,8 +92,8 @@ template <typename T, typename TB>
 __global__ __launch_bounds__(kGemmThreads) void kv_project_kernel(
     const TB* __restrict__ bank, int64_t d, int Tc, const int32_t* __restrict__ uniq,
     const int32_t* __restrict__ n_uniq, int64_t max_u, const float* __restrict__ row_mean,
-    const float* __restrict__ row_rstd, const T* __restrict__ wkv, int HK, int Dh, T* __restrict__ kout,
-    T* __restrict__ vout, T* __restrict__ kout_t, T* __restrict__ vout_t) {
+    const float* __restrict__ row_rstd, const T* __restrict__ wkv, int HK, int Dh, int n_mblk, int n_nblk,
+    T* __restrict__ kout, T* __restrict__ vout, T* __restrict__ kout_t, T* __restrict__ vout_t) {
   constexpr int BK = 128 / (int)sizeof(T);  // elements per 128-byte row slice
   constexpr int EPC = 16 / (int)sizeof(T);  // elements per 16-byte chunk
   constexpr int KSTEPS = BK / 32;
@@ -99,10 +101,16 @@ __global__ __launch_bounds__(kGemmThreads) void kv_project_kernel(
   using Tile = SwzTile<T, BK>;
   __shared__ __attribute__((aligned(16))) char lds[2][2][TILE_BYTES];
 
+  // XCD-aware raster: workgroups are dealt round-robin to the 8 XCDs, so tile t =
+  // (w % 8) * per + w / 8 gives each XCD a contiguous range of tiles, and all N blocks
+  // of a row block (which share its gathered bank rows) run on one XCD's L2.
+  const int w = blockIdx.x, per = (int)(gridDim.x / 8);
+  const int t = (w % 8) * per + w / 8;
+  if (t >= n_mblk * n_nblk) return;
   const int64_t nrows = (int64_t)min((int64_t)n_uniq[0], max_u) * Tc;
-  const int64_t m0 = (int64_t)blockIdx.x * 128;
+  const int64_t m0 = (int64_t)(t / n_nblk) * 128;
   if (m0 >= nrows) return;
-  const int n0 = blockIdx.y * 128;
+  const int n0 = (t % n_nblk) * 128;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
   const int g = lane >> 4, c16 = lane & 15;
@@ -146,20 +154,26 @@ __global__ __launch_bounds__(kGemmThreads) void kv_project_kernel(
   auto stash = [&](int buf) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      float v[EPC];
-      ChunkLoad<T, TB>::run(reinterpret_cast<const TB*>(ra[i]), v);
-      if (row_rstd) {
+      V16 av;
+      if (std::is_same<T, TB>::value && !row_rstd) {
+        av = a_ok[i] ? ra[i][0] : V16{{0u, 0u, 0u, 0u}};
+      } else {
+        float v[EPC];
+        ChunkLoad<T, TB>::run(reinterpret_cast<const TB*>(ra[i]), v);
+        if (row_rstd) {
 #pragma unroll
-        for (int x = 0; x < EPC; ++x) v[x] = (v[x] - a_mu[i]) * a_rs[i];
+          for (int x = 0; x < EPC; ++x) v[x] = (v[x] - a_mu[i]) * a_rs[i];
+        }
+        if (!a_ok[i]) {
+#pragma unroll
+          for (int x = 0; x < EPC; ++x) v[x] = 0.f;
+        }
+        T tv[EPC];
+#pragma unroll
+        for (int x = 0; x < EPC; ++x) tv[x] = from_f<T>(v[x]);
+        av = *reinterpret_cast<V16*>(tv);
       }
-      if (!a_ok[i]) {
-#pragma unroll
-        for (int x = 0; x < EPC; ++x) v[x] = 0.f;
-      }
-      T t[EPC];
-#pragma unroll
-      for (int x = 0; x < EPC; ++x) t[x] = from_f<T>(v[x]);
-      st16(&lds[buf][0][Tile::off(a_row[i], a_cc[i] * EPC)], *reinterpret_cast<V16*>(t));
+      st16(&lds[buf][0][Tile::off(a_row[i], a_cc[i] * EPC)], av);
       st16(&lds[buf][1][Tile::off(a_row[i], a_cc[i] * EPC)], rb[i]);
     }
   };
@@ -232,6 +246,163 @@ __global__ __launch_bounds__(kGemmThreads) void kv_project_kernel(
   }
 }
 
+
+// Wide variant for bf16 compute with 64-row chapters and head_dim 64 (every caller
+// of the attention kernels): 256 x 256 output tile per workgroup, 8 waves in a
+// 2 (rows) x 4 (columns) grid of 128 x 64, so each wave owns two whole (chapter,
+// head) 64 x 64 output blocks.  The k-stage is 64 columns (128 bytes) of A and B,
+// double-buffered (128 KB of LDS).  The epilogue stages each block through the
+// wave's own 16 KB of LDS (row-major and transposed copies) and writes every
+// layout with 16-byte stores, one contiguous kilobyte per wave instruction.
+constexpr int kWideThreads = 512;
+
+template <typename TB, bool kNorm>
+__global__ __launch_bounds__(kWideThreads) void kv_project_wide_kernel(
+    const TB* __restrict__ bank, int64_t d, const int32_t* __restrict__ uniq, const int32_t* __restrict__ n_uniq,
+    int64_t max_u, const float* __restrict__ row_mean, const float* __restrict__ row_rstd,
+    const bf16* __restrict__ wkv, int HK, int n_mblk, int n_nblk, bf16* __restrict__ kout, bf16* __restrict__ vout,
+    bf16* __restrict__ kout_t, bf16* __restrict__ vout_t) {
+  using Tile = SwzTile<bf16, 64>;
+  constexpr int STAGE = 256 * 128;  // one operand stage: 256 rows x 128 bytes
+  constexpr bool kConv = kNorm || !std::is_same<TB, bf16>::value;
+  constexpr int NV = (8 * (int)sizeof(TB)) / 16;  // 16-byte loads per 8-element A chunk
+  __shared__ __attribute__((aligned(16))) char lds[2][2][STAGE];
+
+  // XCD-aware raster (see kv_project_kernel)
+  const int w = blockIdx.x, per = (int)(gridDim.x / 8);
+  const int t = (w % 8) * per + w / 8;
+  if (t >= n_mblk * n_nblk) return;
+  const int nu = (int)min((int64_t)n_uniq[0], max_u);
+  const int64_t nrows = (int64_t)nu * 64;
+  const int64_t m0 = (int64_t)(t / n_nblk) * 256;
+  if (m0 >= nrows) return;
+  const int n0 = (t % n_nblk) * 256;
+  const int KV = HK * 64;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 2, wn = wave & 3;
+  const int g = lane >> 4, c16 = lane & 15;
+
+  // staging: thread moves chunks q = tid + 512 i (i < 4) of A and of B (row q / 8, 16-byte column q % 8)
+  const TB* a_src[4];
+  float a_mu[4], a_rs[4];
+  bool a_ok[4];
+  int s_off[4];
+  uint32_t b_off[4];
+  // rows of W past 2 * HK * 64 read as zeros (buffer bound)
+  const Buf wb(wkv, (uint32_t)((size_t)2 * KV * d * sizeof(bf16)));
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int q = tid + kWideThreads * i;
+    const int row = q >> 3, cc = q & 7;
+    const int64_t r = m0 + row;
+    a_ok[i] = r < nrows;
+    const int64_t rr = a_ok[i] ? r : 0;
+    const int64_t src = (int64_t)uniq[rr >> 6] * 64 + (rr & 63);
+    a_src[i] = bank + src * d + cc * 8;
+    a_mu[i] = kNorm ? row_mean[rr] : 0.f;
+    a_rs[i] = kNorm ? row_rstd[rr] : 1.f;
+    s_off[i] = Tile::off(row, cc * 8);
+    b_off[i] = (uint32_t)(((int64_t)(n0 + row) * d + cc * 8) * (int64_t)sizeof(bf16));
+  }
+  V16 ra[4][NV], rb[4];
+  auto fetch = [&](int kt) {
+    const int64_t ko = (int64_t)kt * 64;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int x = 0; x < NV; ++x) ra[i][x] = ld16(a_src[i] + ko + x * (16 / (int)sizeof(TB)));
+      rb[i] = wb.load16(b_off[i], (uint32_t)(kt * 128));
+    }
+  };
+  auto stash = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      V16 av;
+      if constexpr (!kConv) {
+        av = a_ok[i] ? ra[i][0] : V16{{0u, 0u, 0u, 0u}};
+      } else {
+        float v[8];
+        ChunkLoad<bf16, TB>::run(reinterpret_cast<const TB*>(ra[i]), v);
+        bf16x8 o;
+#pragma unroll
+        for (int x = 0; x < 8; ++x) o[x] = (bf16)(a_ok[i] ? (v[x] - a_mu[i]) * a_rs[i] : 0.f);
+        av = __builtin_bit_cast(V16, o);
+      }
+      st16(&lds[buf][0][s_off[i]], av);
+      st16(&lds[buf][1][s_off[i]], rb[i]);
+    }
+  };
+
+  f32x4 acc[8][4];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int nk = (int)(d / 64);
+  fetch(0);
+  stash(0);
+  __syncthreads();
+  for (int kt = 0; kt < nk; ++kt) {
+    const int buf = kt & 1;
+    if (kt + 1 < nk) fetch(kt + 1);
+    const char* As = lds[buf][0];
+    const char* Bs = lds[buf][1];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      bf16x8 b[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) b[j] = Tile::frag(Bs, 64 * wn + 16 * j + c16, 32 * ks + 8 * g);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const bf16x8 a = Tile::frag(As, 128 * wm + 16 * i + c16, 32 * ks + 8 * g);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) mma(acc[i][j], a, b[j]);
+      }
+    }
+    if (kt + 1 < nk) stash(buf ^ 1);
+    __syncthreads();
+  }
+
+  // Epilogue: this wave's columns are one head of K or V
+  const int col0 = n0 + 64 * wn;
+  if (col0 >= 2 * KV) return;
+  const bool is_v = col0 >= KV;
+  const int hk = (is_v ? col0 - KV : col0) / 64;
+  bf16* dst = is_v ? vout : kout;
+  bf16* dst_t = is_v ? vout_t : kout_t;
+  char* R = &lds[0][0][0] + wave * 16384;  // [t][dh] block
+  char* Rt = R + 8192;                       // [dh][t] block
+#pragma unroll
+  for (int blk = 0; blk < 2; ++blk) {
+    const int64_t u = (m0 + 128 * wm + 64 * blk) >> 6;
+    if (u >= nu) break;
+#pragma unroll
+    for (int ii = 0; ii < 4; ++ii) {
+      const int i = 4 * blk + ii;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int tt = 16 * ii + 4 * g, dh = 16 * j + c16;
+        const bf16x4 v4 = bf16x4{(bf16)acc[i][j][0], (bf16)acc[i][j][1], (bf16)acc[i][j][2], (bf16)acc[i][j][3]};
+        if (dst) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) *reinterpret_cast<bf16*>(R + Tile::off(tt + e, dh)) = v4[e];
+        }
+        if (dst_t) *reinterpret_cast<bf16x4*>(Rt + Tile::off(dh, tt)) = v4;
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+    const size_t base = ((size_t)u * HK + hk) * 4096;
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+      const int ch = lane + 64 * m, row = ch >> 3, c8 = (ch & 7) * 8;
+      if (dst) st16(dst + base + row * 64 + c8, ld16(R + Tile::off(row, c8)));
+      if (dst_t) st16(dst_t + base + row * 64 + c8, ld16(Rt + Tile::off(row, c8)));
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+}
+
 }  // namespace moc
 
 using namespace moc;
@@ -274,16 +445,40 @@ int moc_kv_project(int dtype, const void* bank, int bank_dtype, int64_t d, int T
               2 * HK * Dh);
   if (max_u == 0) return MOC_OK;
   const int64_t rows = max_u * T;
-  dim3 grid((unsigned)((rows + 127) / 128), (unsigned)(2 * HK * Dh / 128));
+  if (dtype == MOC_BF16 && T == 64 && Dh == 64) {
+    const int64_t n_mblk = (rows + 255) / 256, n_nblk = (2 * HK * Dh + 255) / 256;
+    MOC_REQUIRE(n_mblk * n_nblk < ((int64_t)1 << 30) && 2 * HK * Dh * d * 2 < ((int64_t)1 << 32),
+                MOC_ERR_UNSUPPORTED, "moc_kv_project: problem too large");
+    const int64_t n_tiles = n_mblk * n_nblk;
+    dim3 grid((unsigned)((n_tiles + 7) / 8 * 8));  // a multiple of the 8 XCDs
+    const bool norm = row_rstd != nullptr;
+#define MOC_KVW(TB, NORM)                                                                                        \
+  hipLaunchKernelGGL((kv_project_wide_kernel<TB, NORM>), grid, dim3(kWideThreads), 0, stream, (const TB*)bank, d, \
+                     uniq, n_uniq, max_u, row_mean, row_rstd, (const bf16*)wkv, HK, (int)n_mblk, (int)n_nblk,     \
+                     (bf16*)k_tiles, (bf16*)v_tiles, (bf16*)kt_tiles, (bf16*)vt_tiles)
+    if (bank_dtype == MOC_BF16) {
+      if (norm) MOC_KVW(bf16, true); else MOC_KVW(bf16, false);
+    } else if (bank_dtype == MOC_F32) {
+      if (norm) MOC_KVW(float, true); else MOC_KVW(float, false);
+    } else {
+      return set_error(MOC_ERR_UNSUPPORTED, "moc_kv_project: bank dtype %d", bank_dtype);
+    }
+#undef MOC_KVW
+    return check_launch("kv_project_wide_kernel");
+  }
+  const int64_t n_mblk = (rows + 127) / 128, n_nblk = 2 * HK * Dh / 128;
+  MOC_REQUIRE(n_mblk * n_nblk < ((int64_t)1 << 30), MOC_ERR_UNSUPPORTED, "moc_kv_project: too many tiles");
+  const int64_t n_tiles = n_mblk * n_nblk;
+  dim3 grid((unsigned)((n_tiles + 7) / 8 * 8));  // a multiple of the 8 XCDs
   if (dtype == MOC_BF16 && bank_dtype == MOC_BF16)
     hipLaunchKernelGGL((kv_project_kernel<bf16, bf16>), grid, dim3(kGemmThreads), 0, stream, (const bf16*)bank, d, T, uniq,
-                       n_uniq, max_u, row_mean, row_rstd, (const bf16*)wkv, HK, Dh, (bf16*)k_tiles, (bf16*)v_tiles, (bf16*)kt_tiles, (bf16*)vt_tiles);
+                       n_uniq, max_u, row_mean, row_rstd, (const bf16*)wkv, HK, Dh, (int)n_mblk, (int)n_nblk, (bf16*)k_tiles, (bf16*)v_tiles, (bf16*)kt_tiles, (bf16*)vt_tiles);
   else if (dtype == MOC_BF16 && bank_dtype == MOC_F32)
     hipLaunchKernelGGL((kv_project_kernel<bf16, float>), grid, dim3(kGemmThreads), 0, stream, (const float*)bank, d, T, uniq,
-                       n_uniq, max_u, row_mean, row_rstd, (const bf16*)wkv, HK, Dh, (bf16*)k_tiles, (bf16*)v_tiles, (bf16*)kt_tiles, (bf16*)vt_tiles);
+                       n_uniq, max_u, row_mean, row_rstd, (const bf16*)wkv, HK, Dh, (int)n_mblk, (int)n_nblk, (bf16*)k_tiles, (bf16*)v_tiles, (bf16*)kt_tiles, (bf16*)vt_tiles);
   else if (dtype == MOC_F32 && bank_dtype == MOC_F32)
     hipLaunchKernelGGL((kv_project_kernel<float, float>), grid, dim3(kGemmThreads), 0, stream, (const float*)bank, d, T,
-                       uniq, n_uniq, max_u, row_mean, row_rstd, (const float*)wkv, HK, Dh, (float*)k_tiles,
+                       uniq, n_uniq, max_u, row_mean, row_rstd, (const float*)wkv, HK, Dh, (int)n_mblk, (int)n_nblk, (float*)k_tiles,
                        (float*)v_tiles, (float*)kt_tiles, (float*)vt_tiles);
   else
     return set_error(MOC_ERR_UNSUPPORTED, "moc_kv_project: dtype %d with bank dtype %d", dtype, bank_dtype);
