@@ -166,6 +166,17 @@ int moc_xattn_bwd_dkv(int dtype, const void* q, const void* qt, const void* dout
 int moc_dkv_reduce(int dtype, const void* dkv_edge, const int32_t* n_uniq, const int32_t* csr_off,
                    const int32_t* csr_edge, int64_t max_u, int64_t row_elems, void* dkv, hipStream_t stream);
 
+/* Weight gradient of the K/V projection with the chapter gather (and row norm) fused:
+ * dw [KV2][d] (out_dtype f32 or bf16) = dkv^T X, X[r] = norm(bank[uniq[r / 64] * 64 + r % 64]),
+ * over the plan's n_uniq * 64 rows; dkv [max_u * 64][KV2] bf16 from moc_dkv_reduce.  Replaces the
+ * autograd weight gradient of k_proj / v_proj (memory_transformer/memory_attention.py:241-243)
+ * over the gathered rows (memory_transformer/memory_bank.py:263-293).  T must be 64.  The rows
+ * are split over several workgroups per output tile; ws (moc_kv_wgrad_workspace bytes) holds
+ * their fp32 partials, summed in a fixed order. */
+size_t moc_kv_wgrad_workspace(int64_t KV2, int64_t d, int64_t max_u);
+int moc_kv_wgrad(const void* dkv, const void* bank, int bank_dtype, int64_t d, int T, const int32_t* uniq,
+                 const int32_t* n_uniq, int64_t max_u, const float* row_mean, const float* row_rstd, int64_t KV2,
+                 void* ws, size_t ws_bytes, int out_dtype, void* dw, hipStream_t stream);
 /* Gathered (and normalised) rows X [max_u * T][d] in dtype for the weight-gradient GEMM
  * dWkv = dkv^T X; rows of unused plan slots are zero. */
 int moc_gather_rows(int dtype, const void* bank, int bank_dtype, int64_t d, int T, const int32_t* uniq,

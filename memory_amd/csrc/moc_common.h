@@ -138,6 +138,23 @@ struct SwzTile {
   }
 };
 
+// 8 consecutive elements (16 bytes of bf16 / 32 bytes of fp32) as floats
+template <typename TB> struct ChunkLoadF;
+template <> struct ChunkLoadF<bf16> {
+  static __device__ __forceinline__ void run(const bf16* p, float* o) {
+    const bf16x8 v = *reinterpret_cast<const bf16x8*>(p);
+#pragma unroll
+    for (int x = 0; x < 8; ++x) o[x] = (float)v[x];
+  }
+};
+template <> struct ChunkLoadF<float> {
+  static __device__ __forceinline__ void run(const float* p, float* o) {
+    const f32x4 a = *reinterpret_cast<const f32x4*>(p), b = *reinterpret_cast<const f32x4*>(p + 4);
+#pragma unroll
+    for (int x = 0; x < 4; ++x) { o[x] = a[x]; o[4 + x] = b[x]; }
+  }
+};
+
 // s_waitcnt vmcnt(0) (expcnt / lgkmcnt left open), gfx9 encoding
 __device__ __forceinline__ void vm_wait_all() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 

@@ -306,10 +306,20 @@ class _RoutedAttention(torch.autograd.Function):
         need_bank, need_wk, need_wv = ctx.needs_input_grad[1:4]
         dbank = dwk = dwv = None
         if need_wk or need_wv:
-            X = torch.empty(max_u * T, d, device=dev, dtype=dtype)
-            call("moc_gather_rows", dt, ptr(bank), L.dtype_code(bank.dtype), d, T, ptr(uniq), ptr(n_uniq), max_u,
-                 ptr(mean), ptr(rstd), ptr(X), st)
-            dwkv = torch.matmul(dkv.t(), X)
+            if dtype == torch.bfloat16:
+                # split-row weight-gradient kernel with the gather fused in
+                ws = torch.empty(L.query("moc_kv_wgrad_workspace", 2 * KV, d, max_u) // 4, device=dev,
+                                 dtype=torch.float32)
+                out_dt = torch.float32 if torch.float32 in (wk_dtype, wv_dtype) else dtype
+                dwkv = torch.empty(2 * KV, d, device=dev, dtype=out_dt)
+                call("moc_kv_wgrad", ptr(dkv), ptr(bank), L.dtype_code(bank.dtype), d, T, ptr(uniq), ptr(n_uniq),
+                     max_u, ptr(mean), ptr(rstd), 2 * KV, ptr(ws), ws.numel() * 4, L.dtype_code(out_dt), ptr(dwkv),
+                     st)
+            else:
+                X = torch.empty(max_u * T, d, device=dev, dtype=dtype)
+                call("moc_gather_rows", dt, ptr(bank), L.dtype_code(bank.dtype), d, T, ptr(uniq), ptr(n_uniq),
+                     max_u, ptr(mean), ptr(rstd), ptr(X), st)
+                dwkv = torch.matmul(dkv.t(), X)
             dwk = dwkv[:KV].to(wk_dtype) if need_wk else None
             dwv = dwkv[KV:].to(wv_dtype) if need_wv else None
         if need_bank:

@@ -88,3 +88,47 @@ def test_routed_attention_backward(gpu_device, dtype, B, Lq, H, HK, C, k, norm, 
     sel[ci.reshape(-1)] = True
     unsel = (~sel).repeat_interleave(T)
     assert torch.count_nonzero(bg.grad.cpu()[unsel]) == 0
+
+
+@pytest.mark.parametrize("d,HK,C,nsel,bank_dtype,norm,out_dtype", [
+    (768, 12, 60, 41, torch.bfloat16, None, torch.bfloat16),
+    (128, 1, 20, 7, torch.bfloat16, "rms", torch.float32),
+    (200, 2, 30, 12, torch.float32, "layernorm", torch.float32),
+    (256, 4, 9, 9, torch.bfloat16, None, torch.float32),
+])
+def test_kv_weight_grad_kernel(gpu_device, d, HK, C, nsel, bank_dtype, norm, out_dtype):
+    """dW = dkv^T norm(gather(bank)) from the split-row kernel against float64 on the same
+    bf16-rounded operands (tolerance 2e-2 relative max error, fp32 accumulation)."""
+    print(f"kv_wgrad d={d} HK={HK} C={C} nsel={nsel} bank={bank_dtype} norm={norm} out={out_dtype}", flush=True)
+    from memory_amd import _lib as L
+    from memory_amd import ops
+    dev = gpu_device
+    T, KV2 = 64, 2 * HK * 64
+    g = gen(300 + d + HK)
+    bank = torch.randn(C * T, d, generator=g)
+    chap = torch.randperm(C, generator=g)[:nsel].to(torch.int32).view(1, -1)
+    plan = ops.chapter_plan(chap.to(dev), C)
+    bg = bank.to(dev, bank_dtype)
+    code = ops.norm_code(norm)
+    mean = rstd = None
+    if code:
+        mean, rstd = ops.row_stats(bg, plan, T, code, 1e-5)
+    max_u = plan.max_u
+    dkv = torch.randn(max_u * T, KV2, generator=g).to(torch.bfloat16)
+    n_u = int(plan.n_uniq[0])
+    dkv[n_u * T:] = 0
+    ws = torch.empty(L.query("moc_kv_wgrad_workspace", KV2, d, max_u) // 4, device=dev, dtype=torch.float32)
+    dw = torch.full((KV2, d), float("nan"), device=dev, dtype=out_dtype)
+    L.call("moc_kv_wgrad", L.ptr(dkv.to(dev)), L.ptr(bg), L.dtype_code(bank_dtype), d, T, L.ptr(plan.uniq),
+           L.ptr(plan.n_uniq), max_u, L.ptr(mean), L.ptr(rstd), KV2, L.ptr(ws), ws.numel() * 4,
+           L.dtype_code(out_dtype), L.ptr(dw), L.stream_ptr(dev))
+    uniq = plan.uniq[:n_u].cpu().long()
+    X, _ = O.gather_chapters(bg.cpu().double(), uniq.view(1, -1), T)
+    X = X[0]
+    if norm == "rms":
+        X = O.rms_norm(X, 1e-5)
+    elif norm == "layernorm":
+        X = torch.nn.functional.layer_norm(X, (d,), eps=1e-5)
+    X = X.to(torch.bfloat16).double()  # the kernel feeds bf16 operands to the MFMA
+    ref = dkv[:n_u * T].double().T @ X
+    assert_rel(dw, ref, 2e-2, "dW")
