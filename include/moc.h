@@ -177,6 +177,13 @@ size_t moc_kv_wgrad_workspace(int64_t KV2, int64_t d, int64_t max_u);
 int moc_kv_wgrad(const void* dkv, const void* bank, int bank_dtype, int64_t d, int T, const int32_t* uniq,
                  const int32_t* n_uniq, int64_t max_u, const float* row_mean, const float* row_rstd, int64_t KV2,
                  void* ws, size_t ws_bytes, int out_dtype, void* dw, hipStream_t stream);
+/* Same kernel over dense rows: dw [N][K] (out_dtype) = dy^T x with dy [R][N] bf16 and x [R][K]
+ * (x_dtype bf16 or f32, rounded to bf16 for the MFMA).  The weight gradient of the memory
+ * layer's bias-free q_proj / o_proj (memory_transformer/memory_attention.py:140-143, :241, :456),
+ * which the reference gets from autograd of nn.Linear; R is the token count. */
+size_t moc_linear_wgrad_workspace(int64_t R, int64_t N, int64_t K);
+int moc_linear_wgrad(const void* dy, const void* x, int x_dtype, int64_t R, int64_t N, int64_t K, void* ws,
+                     size_t ws_bytes, int out_dtype, void* dw, hipStream_t stream);
 /* Gathered (and normalised) rows X [max_u * T][d] in dtype for the weight-gradient GEMM
  * dWkv = dkv^T X; rows of unused plan slots are zero. */
 int moc_gather_rows(int dtype, const void* bank, int bank_dtype, int64_t d, int T, const int32_t* uniq,

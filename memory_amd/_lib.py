@@ -53,6 +53,8 @@ _SIGS = {
                                _P, _P, _P]),
     "moc_kv_wgrad_workspace": (_SZ, [_I64, _I64, _I64]),
     "moc_kv_wgrad": (_I, [_P, _P, _I, _I64, _I, _P, _P, _I64, _P, _P, _I64, _P, _SZ, _I, _P, _P]),
+    "moc_linear_wgrad_workspace": (_SZ, [_I64, _I64, _I64]),
+    "moc_linear_wgrad": (_I, [_P, _P, _I, _I64, _I64, _I64, _P, _SZ, _I, _P, _P]),
     "moc_dkv_reduce": (_I, [_I, _P, _P, _P, _P, _I64, _I64, _P, _P]),
     "moc_sparse_fwd": (_I, [_I, _P, _I64, _I, _P, _P, _I64, _I64, _I64, _I, _I, _P, _P, _P, _P, _I64, _I, _I, _I,
                             _I, _I, _F, _P, _P, _P]),

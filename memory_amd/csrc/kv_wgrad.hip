@@ -49,10 +49,12 @@ __device__ __forceinline__ bf16x8 tr_frag(const char* base, int rb, int cb, int 
   return __builtin_bit_cast(bf16x8, v);
 }
 
-template <typename TB, bool kNorm>
+// kGather: X rows are gathered chapter rows (stage st = distinct chapter st); otherwise X
+// is a dense [R][d] matrix and stage st covers rows 64 st .. 64 st + 63 (rows >= R read zero).
+template <typename TB, bool kNorm, bool kGather>
 __global__ __launch_bounds__(kWgThreads) void kv_wgrad_kernel(
     const bf16* __restrict__ dkv, int KV2, const TB* __restrict__ bank, int64_t d, const int32_t* __restrict__ uniq,
-    const int32_t* __restrict__ n_uniq, int64_t max_u, const float* __restrict__ row_mean,
+    const int32_t* __restrict__ n_uniq, int64_t max_u, int64_t R, const float* __restrict__ row_mean,
     const float* __restrict__ row_rstd, int n_ktile, float* __restrict__ ws) {
   constexpr int STAGE = 64 * 512;
   constexpr bool kConv = kNorm || !std::is_same<TB, bf16>::value;
@@ -65,7 +67,8 @@ __global__ __launch_bounds__(kWgThreads) void kv_wgrad_kernel(
   const int wn = wave >> 2, wk = wave & 3;  // wave tile: 128 (n) x 64 (k)
   const int g = lane >> 4, c16 = lane & 15;
 
-  const int64_t nstage = (int64_t)min((int64_t)n_uniq[0], max_u);  // one 64-row stage per chapter
+  // one 64-row stage per chapter (gather) or per 64 rows (dense)
+  const int64_t nstage = kGather ? (int64_t)min((int64_t)n_uniq[0], max_u) : (R + 63) / 64;
   const int64_t per = (nstage + splits - 1) / splits;
   const int64_t s0 = min(nstage, (int64_t)split * per), s1 = min(nstage, s0 + per);
 
@@ -85,19 +88,20 @@ __global__ __launch_bounds__(kWgThreads) void kv_wgrad_kernel(
   V16 ra[4], rb[4][NV];
   float mu[4], rs[4];
   auto fetch = [&](int64_t st) {
-    const int64_t u = st;  // stage st = distinct chapter st, rows st*64 .. +63
-    const int64_t chap = uniq[u];
+    const int64_t xbase = kGather ? (int64_t)uniq[st] * 64 : st * 64;  // first X row of the stage
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int q = tid + kWgThreads * i;
       const int row = q >> 5, cc = (q & 31) * 8;
-      ra[i] = a_ok[i] ? ld16(a_src[i] + u * 64 * KV2) : V16{{0u, 0u, 0u, 0u}};
-      const TB* xp = bank + (chap * 64 + row) * d + (b_ok[i] ? k0 + cc : 0);
+      const bool live = kGather || st * 64 + row < R;
+      ra[i] = a_ok[i] && live ? ld16(a_src[i] + st * 64 * KV2) : V16{{0u, 0u, 0u, 0u}};
+      const TB* xp = bank + (xbase + row) * d + (b_ok[i] ? k0 + cc : 0);
 #pragma unroll
-      for (int x = 0; x < NV; ++x) rb[i][x] = b_ok[i] ? ld16(xp + x * (16 / (int)sizeof(TB))) : V16{{0u, 0u, 0u, 0u}};
+      for (int x = 0; x < NV; ++x)
+        rb[i][x] = b_ok[i] && live ? ld16(xp + x * (16 / (int)sizeof(TB))) : V16{{0u, 0u, 0u, 0u}};
       if constexpr (kNorm) {
-        mu[i] = row_mean[u * 64 + row];
-        rs[i] = row_rstd[u * 64 + row];
+        mu[i] = row_mean[st * 64 + row];
+        rs[i] = row_rstd[st * 64 + row];
       }
     }
   };
@@ -188,11 +192,49 @@ int wgrad_tiles(int64_t KV2, int64_t d, int* n_ktile) {
   *n_ktile = (int)((d + 255) / 256);
   return (int)((KV2 + 255) / 256) * *n_ktile;
 }
-int wgrad_splits(int tiles, int64_t max_u) {
-  int s = 256 / tiles;
+// workgroups per output tile: fill the 256 CUs, but give each at least 8 stages
+int wgrad_splits(int tiles, int64_t max_stages) {
+  int64_t s = 256 / tiles;
+  const int64_t by_len = (max_stages + 7) / 8;
+  if (s > by_len) s = by_len;
   if (s < 1) s = 1;
-  if (s > max_u) s = (int)(max_u > 0 ? max_u : 1);
-  return s;
+  return (int)s;
+}
+
+template <bool kGather>
+int launch_wgrad(const void* dkv, const void* bank, int bank_dtype, int64_t d, const int32_t* uniq,
+                 const int32_t* n_uniq, int64_t max_u, int64_t R, const float* row_mean, const float* row_rstd,
+                 int64_t KV2, int64_t max_stages, void* ws, int out_dtype, void* dw, hipStream_t stream) {
+  int nk;
+  const int tiles = wgrad_tiles(KV2, d, &nk);
+  const int splits = wgrad_splits(tiles, max_stages);
+  MOC_REQUIRE(tiles < 65536 && splits < 65536, MOC_ERR_UNSUPPORTED, "weight gradient: problem too large");
+  dim3 grid((unsigned)tiles, (unsigned)splits);
+  const bool norm = row_rstd != nullptr;
+#define MOC_WG(TB, NORM)                                                                                        \
+  hipLaunchKernelGGL((kv_wgrad_kernel<TB, NORM, kGather>), grid, dim3(kWgThreads), 0, stream, (const bf16*)dkv, \
+                     (int)KV2, (const TB*)bank, d, uniq, n_uniq, max_u, R, row_mean, row_rstd, nk, (float*)ws)
+  if (bank_dtype == MOC_BF16) {
+    if (norm) MOC_WG(bf16, true); else MOC_WG(bf16, false);
+  } else if (bank_dtype == MOC_F32) {
+    if (norm) MOC_WG(float, true); else MOC_WG(float, false);
+  } else {
+    return set_error(MOC_ERR_UNSUPPORTED, "weight gradient: input dtype %d", bank_dtype);
+  }
+#undef MOC_WG
+  int rc = check_launch("kv_wgrad_kernel");
+  if (rc != MOC_OK) return rc;
+  const int64_t n4 = (int64_t)tiles * 8 * 32 * 64;
+  dim3 rgrid((unsigned)((n4 + 255) / 256));
+  if (out_dtype == MOC_F32)
+    hipLaunchKernelGGL(kv_wgrad_reduce_kernel<float>, rgrid, dim3(256), 0, stream, (const float*)ws, splits, tiles, nk,
+                       (int)KV2, d, (float*)dw);
+  else if (out_dtype == MOC_BF16)
+    hipLaunchKernelGGL(kv_wgrad_reduce_kernel<bf16>, rgrid, dim3(256), 0, stream, (const float*)ws, splits, tiles, nk,
+                       (int)KV2, d, (bf16*)dw);
+  else
+    return set_error(MOC_ERR_UNSUPPORTED, "weight gradient: out dtype %d", out_dtype);
+  return check_launch("kv_wgrad_reduce_kernel");
 }
 }  // namespace
 
@@ -214,36 +256,24 @@ int moc_kv_wgrad(const void* dkv, const void* bank, int bank_dtype, int64_t d, i
   MOC_REQUIRE(d > 0 && d % 8 == 0 && KV2 > 0 && KV2 % 8 == 0 && KV2 < (1 << 30) && max_u >= 0, MOC_ERR_UNSUPPORTED,
               "moc_kv_wgrad: d=%lld KV2=%lld must be multiples of 8", (long long)d, (long long)KV2);
   MOC_REQUIRE(ws_bytes >= moc_kv_wgrad_workspace(KV2, d, max_u), MOC_ERR_ARG, "moc_kv_wgrad: workspace too small");
+  return launch_wgrad<true>(dkv, bank, bank_dtype, d, uniq, n_uniq, max_u, 0, row_mean, row_rstd, KV2, max_u, ws,
+                            out_dtype, dw, stream);
+}
+
+size_t moc_linear_wgrad_workspace(int64_t R, int64_t N, int64_t K) {
   int nk;
-  const int tiles = wgrad_tiles(KV2, d, &nk);
-  const int splits = wgrad_splits(tiles, max_u);
-  MOC_REQUIRE(tiles < 65536 && splits < 65536, MOC_ERR_UNSUPPORTED, "moc_kv_wgrad: problem too large");
-  dim3 grid((unsigned)tiles, (unsigned)splits);
-  const bool norm = row_rstd != nullptr;
-#define MOC_WG(TB, NORM)                                                                                            \
-  hipLaunchKernelGGL((kv_wgrad_kernel<TB, NORM>), grid, dim3(kWgThreads), 0, stream, (const bf16*)dkv, (int)KV2, \
-                     (const TB*)bank, d, uniq, n_uniq, max_u, row_mean, row_rstd, nk, (float*)ws)
-  if (bank_dtype == MOC_BF16) {
-    if (norm) MOC_WG(bf16, true); else MOC_WG(bf16, false);
-  } else if (bank_dtype == MOC_F32) {
-    if (norm) MOC_WG(float, true); else MOC_WG(float, false);
-  } else {
-    return set_error(MOC_ERR_UNSUPPORTED, "moc_kv_wgrad: bank dtype %d", bank_dtype);
-  }
-#undef MOC_WG
-  int rc = check_launch("kv_wgrad_kernel");
-  if (rc != MOC_OK) return rc;
-  const int64_t n4 = (int64_t)tiles * 8 * 32 * 64;
-  dim3 rgrid((unsigned)((n4 + 255) / 256));
-  if (out_dtype == MOC_F32)
-    hipLaunchKernelGGL(kv_wgrad_reduce_kernel<float>, rgrid, dim3(256), 0, stream, (const float*)ws, splits, tiles, nk,
-                       (int)KV2, d, (float*)dw);
-  else if (out_dtype == MOC_BF16)
-    hipLaunchKernelGGL(kv_wgrad_reduce_kernel<bf16>, rgrid, dim3(256), 0, stream, (const float*)ws, splits, tiles, nk,
-                       (int)KV2, d, (bf16*)dw);
-  else
-    return set_error(MOC_ERR_UNSUPPORTED, "moc_kv_wgrad: out dtype %d", out_dtype);
-  return check_launch("kv_wgrad_reduce_kernel");
+  const int tiles = wgrad_tiles(N, K, &nk);
+  return (size_t)wgrad_splits(tiles, (R + 63) / 64) * tiles * 256 * 256 * sizeof(float);
+}
+
+int moc_linear_wgrad(const void* dy, const void* x, int x_dtype, int64_t R, int64_t N, int64_t K, void* ws,
+                     size_t ws_bytes, int out_dtype, void* dw, hipStream_t stream) {
+  MOC_REQUIRE(dy && x && ws && dw, MOC_ERR_ARG, "moc_linear_wgrad: null pointer");
+  MOC_REQUIRE(R >= 0 && N > 0 && N % 8 == 0 && N < (1 << 30) && K > 0 && K % 8 == 0, MOC_ERR_UNSUPPORTED,
+              "moc_linear_wgrad: N=%lld K=%lld must be multiples of 8", (long long)N, (long long)K);
+  MOC_REQUIRE(ws_bytes >= moc_linear_wgrad_workspace(R, N, K), MOC_ERR_ARG, "moc_linear_wgrad: workspace too small");
+  return launch_wgrad<false>(dy, x, x_dtype, K, nullptr, nullptr, 0, R, nullptr, nullptr, N, (R + 63) / 64, ws,
+                             out_dtype, dw, stream);
 }
 
 }  // extern "C"

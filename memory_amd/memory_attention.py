@@ -82,11 +82,11 @@ class MemoryCrossAttention(nn.Module):
 
     # ------------------------------------------------------------------ helpers
     def _project_output(self, attn_output: torch.Tensor) -> torch.Tensor:
-        return self.o_proj(attn_output)
+        return ops.linear(attn_output, self.o_proj.weight)
 
     def _queries(self, hidden_states: torch.Tensor) -> torch.Tensor:
         B, L, _ = hidden_states.shape
-        return self.q_proj(hidden_states).view(B, L, self.num_heads, self.head_dim)
+        return ops.linear(hidden_states, self.q_proj.weight).view(B, L, self.num_heads, self.head_dim)
 
     def _routed(self, hidden_states, bank, idx_star, omega, num_chapters, T, norm_type, eps):
         B, L, _ = hidden_states.shape

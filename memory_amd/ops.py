@@ -11,6 +11,7 @@ from dataclasses import dataclass
 from typing import Optional
 
 import torch
+import torch.nn.functional as F
 
 from . import _lib as L
 from ._lib import call, ptr, stream_ptr
@@ -163,8 +164,8 @@ class _PrependShared(torch.autograd.Function):
         if domega is None or k == 0:
             return None, None, None, None
         dw = torch.empty_like(w)
-        call("moc_prepend_shared_bwd", ptr(w), ptr(domega.float().contiguous()), R, k, ctx.S, ctx.scale, ptr(dw),
-             stream_ptr(w.device))
+        dom = domega.float().contiguous()  # held until the launch is enqueued
+        call("moc_prepend_shared_bwd", ptr(w), ptr(dom), R, k, ctx.S, ctx.scale, ptr(dw), stream_ptr(w.device))
         return None, dw, None, None
 
 
@@ -236,6 +237,45 @@ def kv_project(bank: torch.Tensor, plan: ChapterPlan, T: int, wkv: torch.Tensor,
          ptr(plan.n_uniq), plan.max_u, ptr(mean), ptr(rstd), ptr(wkv), HK, Dh, ptr(out.get("k")), ptr(out.get("v")),
          ptr(out.get("kt")), ptr(out.get("vt")), stream_ptr(bank.device))
     return tuple(out[n] for n in layouts)
+
+
+# ------------------------------------------------------------- dense projections
+
+class _Linear(torch.autograd.Function):
+    """y = x W^T (bias-free nn.Linear of the memory layer's q_proj / o_proj,
+    memory_transformer/memory_attention.py:140-143, :241 and :456).  The weight gradient
+    dW = dy^T x runs on the split-row MFMA kernel (the token dimension is long and
+    the output small); forward and dx stay on hipBLASLt."""
+
+    @staticmethod
+    def forward(ctx, x, w):
+        ctx.save_for_backward(x, w)
+        return F.linear(x, w)
+
+    @staticmethod
+    def backward(ctx, dy):
+        x, w = ctx.saved_tensors
+        dx = dw = None
+        if ctx.needs_input_grad[0]:
+            dx = torch.matmul(dy, w)
+        if ctx.needs_input_grad[1]:
+            n_out, n_in = w.shape
+            dy2 = dy.reshape(-1, n_out).contiguous()
+            x2 = x.reshape(-1, n_in).contiguous()
+            if dy2.dtype == torch.bfloat16 and x2.dtype in (torch.bfloat16, torch.float32) and dy2.is_cuda:
+                R = dy2.shape[0]
+                ws = torch.empty(L.query("moc_linear_wgrad_workspace", R, n_out, n_in) // 4, device=dy2.device,
+                                 dtype=torch.float32)
+                dw = torch.empty(n_out, n_in, device=dy2.device, dtype=w.dtype)
+                call("moc_linear_wgrad", ptr(dy2), ptr(x2), L.dtype_code(x2.dtype), R, n_out, n_in, ptr(ws),
+                     ws.numel() * 4, L.dtype_code(dw.dtype), ptr(dw), stream_ptr(dy2.device))
+            else:
+                dw = torch.matmul(dy2.t().to(x2.dtype), x2).to(w.dtype)
+        return dx, dw
+
+
+def linear(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    return _Linear.apply(x, w)
 
 
 # ------------------------------------------------------------- routed attention (A)

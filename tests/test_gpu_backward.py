@@ -119,7 +119,8 @@ def test_kv_weight_grad_kernel(gpu_device, d, HK, C, nsel, bank_dtype, norm, out
     dkv[n_u * T:] = 0
     ws = torch.empty(L.query("moc_kv_wgrad_workspace", KV2, d, max_u) // 4, device=dev, dtype=torch.float32)
     dw = torch.full((KV2, d), float("nan"), device=dev, dtype=out_dtype)
-    L.call("moc_kv_wgrad", L.ptr(dkv.to(dev)), L.ptr(bg), L.dtype_code(bank_dtype), d, T, L.ptr(plan.uniq),
+    dkv_d = dkv.to(dev)  # kept alive until the kernel has run
+    L.call("moc_kv_wgrad", L.ptr(dkv_d), L.ptr(bg), L.dtype_code(bank_dtype), d, T, L.ptr(plan.uniq),
            L.ptr(plan.n_uniq), max_u, L.ptr(mean), L.ptr(rstd), KV2, L.ptr(ws), ws.numel() * 4,
            L.dtype_code(out_dtype), L.ptr(dw), L.stream_ptr(dev))
     uniq = plan.uniq[:n_u].cpu().long()
@@ -132,3 +133,46 @@ def test_kv_weight_grad_kernel(gpu_device, d, HK, C, nsel, bank_dtype, norm, out
     X = X.to(torch.bfloat16).double()  # the kernel feeds bf16 operands to the MFMA
     ref = dkv[:n_u * T].double().T @ X
     assert_rel(dw, ref, 2e-2, "dW")
+
+
+@pytest.mark.parametrize("R,N,K,x_dtype,out_dtype", [
+    (8192, 768, 768, torch.bfloat16, torch.bfloat16),
+    (1000, 136, 200, torch.float32, torch.float32),
+    (64, 512, 128, torch.bfloat16, torch.float32),
+])
+def test_linear_weight_grad_kernel(gpu_device, R, N, K, x_dtype, out_dtype):
+    """dW = dy^T x of the dense projections (split-row kernel) against float64 on the same
+    bf16-rounded operands, including a ragged row count (2e-2 relative max error)."""
+    print(f"linear_wgrad R={R} N={N} K={K} x={x_dtype} out={out_dtype}", flush=True)
+    from memory_amd import _lib as L
+    dev = gpu_device
+    g = gen(400 + R + N)
+    dy = torch.randn(R, N, generator=g).to(torch.bfloat16)
+    x = torch.randn(R, K, generator=g).to(x_dtype)
+    ws = torch.empty(L.query("moc_linear_wgrad_workspace", R, N, K) // 4, device=dev, dtype=torch.float32)
+    dw = torch.full((N, K), float("nan"), device=dev, dtype=out_dtype)
+    dy_d, x_d = dy.to(dev), x.to(dev)  # kept alive until the kernel has run
+    L.call("moc_linear_wgrad", L.ptr(dy_d), L.ptr(x_d), L.dtype_code(x_dtype), R, N, K, L.ptr(ws),
+           ws.numel() * 4, L.dtype_code(out_dtype), L.ptr(dw), L.stream_ptr(dev))
+    ref = dy.double().T @ x.to(torch.bfloat16).double()
+    assert_rel(dw, ref, 2e-2, "dW")
+
+
+def test_linear_autograd_matches_reference(gpu_device):
+    """ops.linear (q_proj / o_proj) gradients against float64 autograd, bf16 operands."""
+    from memory_amd import ops
+    dev = gpu_device
+    g = gen(77)
+    x = torch.randn(3, 130, 256, generator=g).to(torch.bfloat16)
+    w = (torch.randn(384, 256, generator=g) / 16).to(torch.bfloat16)
+    dy = torch.randn(3, 130, 384, generator=g).to(torch.bfloat16)
+    xg = x.to(dev).requires_grad_(True)
+    wg = w.to(dev).requires_grad_(True)
+    y = ops.linear(xg, wg)
+    y.backward(dy.to(dev))
+    xd = x.double().requires_grad_(True)
+    wd = w.double().requires_grad_(True)
+    (xd @ wd.T).backward(dy.double())
+    assert_rel(y, (x.double() @ w.double().T), 2e-2, "y")
+    assert_rel(xg.grad, xd.grad, 2e-2, "dx")
+    assert_rel(wg.grad, wd.grad, 2e-2, "dW")
