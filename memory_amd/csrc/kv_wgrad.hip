@@ -55,13 +55,16 @@ template <typename TB, bool kNorm, bool kGather>
 __global__ __launch_bounds__(kWgThreads) void kv_wgrad_kernel(
     const bf16* __restrict__ dkv, int KV2, const TB* __restrict__ bank, int64_t d, const int32_t* __restrict__ uniq,
     const int32_t* __restrict__ n_uniq, int64_t max_u, int64_t R, const float* __restrict__ row_mean,
-    const float* __restrict__ row_rstd, int n_ktile, float* __restrict__ ws) {
+    const float* __restrict__ row_rstd, int n_ktile, int n_tiles, int splits, float* __restrict__ ws) {
   constexpr int STAGE = 64 * 512;
   constexpr bool kConv = kNorm || !std::is_same<TB, bf16>::value;
   constexpr int NV = (8 * (int)sizeof(TB)) / 16;
   __shared__ __attribute__((aligned(16))) char lds[2][2][STAGE];  // [buf][dkv | X]
 
-  const int tile = blockIdx.x, split = blockIdx.y, splits = gridDim.y;
+  // (split, tile) with split major, so the tiles that read the same rows share an XCD
+  const int64_t t = xcd_tile((int64_t)n_tiles * splits);
+  if (t < 0) return;
+  const int tile = (int)(t % n_tiles), split = (int)(t / n_tiles);
   const int n0 = (tile / n_ktile) * 256, k0 = (tile % n_ktile) * 256;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wn = wave >> 2, wk = wave & 3;  // wave tile: 128 (n) x 64 (k)
@@ -156,7 +159,7 @@ __global__ __launch_bounds__(kWgThreads) void kv_wgrad_kernel(
     }
   }
   // partial tile in accumulator order: [split][tile][wave][i][j][lane] f32x4
-  f32x4* out = reinterpret_cast<f32x4*>(ws) + (((size_t)split * gridDim.x + tile) * 8 + wave) * 32 * 64 + lane;
+  f32x4* out = reinterpret_cast<f32x4*>(ws) + (((size_t)split * n_tiles + tile) * 8 + wave) * 32 * 64 + lane;
 #pragma unroll
   for (int i = 0; i < 8; ++i)
 #pragma unroll
@@ -209,11 +212,12 @@ int launch_wgrad(const void* dkv, const void* bank, int bank_dtype, int64_t d, c
   const int tiles = wgrad_tiles(KV2, d, &nk);
   const int splits = wgrad_splits(tiles, max_stages);
   MOC_REQUIRE(tiles < 65536 && splits < 65536, MOC_ERR_UNSUPPORTED, "weight gradient: problem too large");
-  dim3 grid((unsigned)tiles, (unsigned)splits);
+  dim3 grid(xcd_grid((int64_t)tiles * splits));
   const bool norm = row_rstd != nullptr;
 #define MOC_WG(TB, NORM)                                                                                        \
   hipLaunchKernelGGL((kv_wgrad_kernel<TB, NORM, kGather>), grid, dim3(kWgThreads), 0, stream, (const bf16*)dkv, \
-                     (int)KV2, (const TB*)bank, d, uniq, n_uniq, max_u, R, row_mean, row_rstd, nk, (float*)ws)
+                     (int)KV2, (const TB*)bank, d, uniq, n_uniq, max_u, R, row_mean, row_rstd, nk, tiles, splits, \
+                     (float*)ws)
   if (bank_dtype == MOC_BF16) {
     if (norm) MOC_WG(bf16, true); else MOC_WG(bf16, false);
   } else if (bank_dtype == MOC_F32) {

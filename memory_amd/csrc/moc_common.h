@@ -155,6 +155,18 @@ template <> struct ChunkLoadF<float> {
   }
 };
 
+// XCD-aware tile order.  Workgroups of a launch are dealt round-robin to the 8 XCDs,
+// each with its own L2.  With a 1-D grid padded to a multiple of 8 (xcd_grid), tile
+// t = (w % 8) * (gridDim.x / 8) + w / 8 gives every XCD a contiguous range of tile ids,
+// so tiles that share inputs (numbered consecutively by the kernel) meet in one L2.
+// Returns -1 for the padding workgroups.
+__device__ __forceinline__ int64_t xcd_tile(int64_t n_tiles) {
+  const int64_t w = blockIdx.x, per = gridDim.x / 8;
+  const int64_t t = (w % 8) * per + w / 8;
+  return t < n_tiles ? t : -1;
+}
+inline unsigned xcd_grid(int64_t n_tiles) { return (unsigned)((n_tiles + 7) / 8 * 8); }
+
 // s_waitcnt vmcnt(0) (expcnt / lgkmcnt left open), gfx9 encoding
 __device__ __forceinline__ void vm_wait_all() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 

@@ -47,82 +47,104 @@ __device__ __forceinline__ float block_reduce_max(float v, float* red) {
   return t;
 }
 
-constexpr int kRouterThreads = 256;
 constexpr int kMaxTopK = 1024;
+constexpr int kMaxRouterC = 16384;  // the row lives in LDS (64 KB)
 
-// Softmax statistics of one row: max, sum of exp(z - max), and the masked sum
-// of probabilities over c >= S (probabilities formed as exp(z - max) / Z, the
-// same operation order as torch.softmax followed by a masked sum).
+// Workgroup size per row: rows are few for sequence-level routing (one per
+// sequence: latency-bound, so many threads per row) and many for token-level.
+inline int router_threads(int64_t R) { return R <= 64 ? 1024 : 256; }
+
+// Loads row z [C] into LDS with every load of a thread in flight before the stores.
+template <int NT>
+__device__ __forceinline__ void load_row(const float* __restrict__ z, int64_t C, float* zs) {
+  int64_t c = threadIdx.x;
+  for (; c + 3 * NT < C; c += 4 * NT) {
+    const float a = z[c], b = z[c + NT], e = z[c + 2 * NT], f = z[c + 3 * NT];
+    zs[c] = a;
+    zs[c + NT] = b;
+    zs[c + 2 * NT] = e;
+    zs[c + 3 * NT] = f;
+  }
+  for (; c < C; c += NT) zs[c] = z[c];
+  __syncthreads();
+}
+
+// Softmax statistics of one row (from LDS): max, sum of exp(z - max), and the
+// masked sum of probabilities over c >= S (probabilities formed as
+// exp(z - max) / Z, the same operation order as torch.softmax followed by a
+// masked sum).
 struct RowStats { float mx, Z, msum; };
 
-__device__ RowStats row_stats(const float* z, int64_t C, int S, float* red) {
+template <int NT>
+__device__ RowStats row_stats(const float* zs, int64_t C, int S, float* red) {
   float m = -INFINITY;
-  for (int64_t c = threadIdx.x; c < C; c += kRouterThreads) m = fmaxf(m, z[c]);
-  m = block_reduce_max<kRouterThreads>(m, red);
+  for (int64_t c = threadIdx.x; c < C; c += NT) m = fmaxf(m, zs[c]);
+  m = block_reduce_max<NT>(m, red);
   float s = 0.f;
-  for (int64_t c = threadIdx.x; c < C; c += kRouterThreads) s += __expf(z[c] - m);
-  const float Z = block_reduce_sum<kRouterThreads>(s, red);
+  for (int64_t c = threadIdx.x; c < C; c += NT) s += __expf(zs[c] - m);
+  const float Z = block_reduce_sum<NT>(s, red);
   float ms = 0.f;
-  if (S > 0)
-    for (int64_t c = S + threadIdx.x; c < C; c += kRouterThreads) ms += __expf(z[c] - m) / Z;
-  ms = block_reduce_sum<kRouterThreads>(ms, red);
+  if (S > 0) {
+    for (int64_t c = S + threadIdx.x; c < C; c += NT) ms += __expf(zs[c] - m) / Z;
+    ms = block_reduce_sum<NT>(ms, red);
+  }
   return RowStats{m, Z, ms};
 }
 
-// One workgroup per row of logits.
-__global__ __launch_bounds__(kRouterThreads) void router_topk_kernel(
+// One workgroup per row of logits; the row is read from HBM once into LDS.
+template <int NT>
+__global__ __launch_bounds__(NT) void router_topk_kernel(
     const float* __restrict__ logits, int64_t C, int S, int k,
     int32_t* __restrict__ idx_out, float* __restrict__ w_out, float* __restrict__ probs_out) {
-  __shared__ float red[kRouterThreads / 64];
+  extern __shared__ float zs[];  // the row, C floats
+  __shared__ float red[NT / 64];
   __shared__ int hist[256];
   __shared__ uint32_t sel_key[kMaxTopK];
   __shared__ int32_t sel_idx[kMaxTopK];
   __shared__ float sel_w[kMaxTopK];
-  __shared__ int s_state[4];  // prefix, remaining, n_gt counter, running eq
-  __shared__ int wave_cnt[kRouterThreads / 64];
+  __shared__ int s_state[5];  // chosen bin, remaining, n collected, running eq, ties at threshold
+  __shared__ int wave_cnt[NT / 64];
 
   const int64_t r = blockIdx.x;
-  const float* z = logits + r * C;
   const int tid = threadIdx.x;
-  const RowStats st = row_stats(z, C, S, red);
+  load_row<NT>(logits + r * C, C, zs);
+  const RowStats st = row_stats<NT>(zs, C, S, red);
   const float denom = fmaxf(st.msum, 1e-12f);
 
   if (probs_out) {
-    for (int64_t c = tid; c < C; c += kRouterThreads) probs_out[r * C + c] = __expf(z[c] - st.mx) / st.Z;
+    for (int64_t c = tid; c < C; c += NT) probs_out[r * C + c] = __expf(zs[c] - st.mx) / st.Z;
   }
 
   // ---- radix select: exact k-th largest key among c in [S, C)
   uint32_t prefix = 0, mask = 0;
   int remaining = k;
   for (int shift = 24; shift >= 0; shift -= 8) {
-    hist[tid] = 0;
+    if (tid < 256) hist[tid] = 0;
     __syncthreads();
-    for (int64_t c = S + tid; c < C; c += kRouterThreads) {
-      uint32_t u = fkey(z[c]);
+    for (int64_t c = S + tid; c < C; c += NT) {
+      const uint32_t u = fkey(zs[c]);
       if ((u & mask) == prefix) atomicAdd(&hist[(u >> shift) & 255], 1);
     }
     __syncthreads();
     if (tid < 64) {
       // lane owns bins 4*lane .. 4*lane+3; suffix sums over bins above.
-      int b0 = hist[4 * tid], b1 = hist[4 * tid + 1], b2 = hist[4 * tid + 2], b3 = hist[4 * tid + 3];
-      int mine = b0 + b1 + b2 + b3;
+      const int b0 = hist[4 * tid], b1 = hist[4 * tid + 1], b2 = hist[4 * tid + 2], b3 = hist[4 * tid + 3];
+      const int mine = b0 + b1 + b2 + b3;
       int incl = mine;  // inclusive suffix over lanes >= tid
 #pragma unroll
       for (int o = 1; o < 64; o <<= 1) {
-        int t = __shfl_down(incl, o, 64);
+        const int t = __shfl_down(incl, o, 64);
         if (tid + o < 64) incl += t;
       }
-      int above = incl - mine;  // count in bins of lanes > tid
-      // walk own bins high to low
-      int cnt[4] = {b0, b1, b2, b3};
+      const int cnt[4] = {b0, b1, b2, b3};
       int chosen = -1, chosen_above = 0;
-      int acc = above;
+      int acc = incl - mine;  // count in bins of lanes > tid
 #pragma unroll
       for (int j = 3; j >= 0; --j) {
         if (chosen < 0 && acc < remaining && acc + cnt[j] >= remaining) { chosen = 4 * tid + j; chosen_above = acc; }
         acc += cnt[j];
       }
-      if (chosen >= 0) { s_state[0] = chosen; s_state[1] = remaining - chosen_above; }
+      if (chosen >= 0) { s_state[0] = chosen; s_state[1] = remaining - chosen_above; s_state[4] = cnt[chosen & 3]; }
     }
     __syncthreads();
     prefix |= ((uint32_t)s_state[0]) << shift;
@@ -132,59 +154,64 @@ __global__ __launch_bounds__(kRouterThreads) void router_topk_kernel(
   }
   const uint32_t thr = prefix;
   const int n_gt = k - remaining;
+  // after the last pass every key of the chosen bin equals thr
+  const bool all_ties = s_state[4] == remaining;
   if (tid == 0) { s_state[2] = 0; s_state[3] = 0; }
   __syncthreads();
-  // ---- collect keys strictly above the threshold (slot order irrelevant: sorted below)
-  for (int64_t c = S + tid; c < C; c += kRouterThreads) {
-    uint32_t u = fkey(z[c]);
-    if (u > thr) {
-      int p = atomicAdd(&s_state[2], 1);
+  // ---- collect keys above the threshold (and every tie when all of them are taken);
+  // slot order is irrelevant: the rank sort below fixes it
+  for (int64_t c = S + tid; c < C; c += NT) {
+    const uint32_t u = fkey(zs[c]);
+    if (u > thr || (all_ties && u == thr)) {
+      const int p = atomicAdd(&s_state[2], 1);
       sel_key[p] = u;
       sel_idx[p] = (int32_t)c;
     }
   }
-  // ---- collect the `remaining` lowest-index keys equal to the threshold
-  const int w = tid >> 6, lane = tid & 63;
-  for (int64_t base = S; base < C; base += kRouterThreads) {
-    int64_t c = base + tid;
-    bool eq = (c < C) && fkey(z[c]) == thr;
-    unsigned long long bal = __ballot(eq);
-    int rank_in_wave = __popcll(bal & ((1ull << lane) - 1ull));
-    if (lane == 0) wave_cnt[w] = __popcll(bal);
-    __syncthreads();
-    int off = s_state[3];
-    for (int i = 0; i < w; ++i) off += wave_cnt[i];
-    int pos = off + rank_in_wave;
-    if (eq && pos < remaining) {
-      sel_key[n_gt + pos] = thr;
-      sel_idx[n_gt + pos] = (int32_t)c;
+  if (!all_ties) {
+    // ---- more ties than slots: the `remaining` lowest-index keys equal to the threshold
+    const int w = tid >> 6, lane = tid & 63;
+    for (int64_t base = S; base < C; base += NT) {
+      const int64_t c = base + tid;
+      const bool eq = (c < C) && fkey(zs[c]) == thr;
+      const unsigned long long bal = __ballot(eq);
+      const int rank_in_wave = __popcll(bal & ((1ull << lane) - 1ull));
+      if (lane == 0) wave_cnt[w] = __popcll(bal);
+      __syncthreads();
+      int off = s_state[3];
+      for (int i = 0; i < w; ++i) off += wave_cnt[i];
+      const int pos = off + rank_in_wave;
+      if (eq && pos < remaining) {
+        sel_key[n_gt + pos] = thr;
+        sel_idx[n_gt + pos] = (int32_t)c;
+      }
+      __syncthreads();
+      if (tid == 0) {
+        int t = 0;
+        for (int i = 0; i < NT / 64; ++i) t += wave_cnt[i];
+        s_state[3] += t;
+      }
+      __syncthreads();
+      if (s_state[3] >= remaining) break;
     }
-    __syncthreads();
-    if (tid == 0) {
-      int t = 0;
-      for (int i = 0; i < kRouterThreads / 64; ++i) t += wave_cnt[i];
-      s_state[3] += t;
-    }
-    __syncthreads();
-    if (s_state[3] >= remaining) break;
   }
   __syncthreads();
   // ---- probabilities of the selected chapters, sum, renormalise
   float part = 0.f;
-  for (int i = tid; i < k; i += kRouterThreads) {
-    float p = __expf(z[sel_idx[i]] - st.mx) / st.Z;
+  for (int i = tid; i < k; i += NT) {
+    float p = __expf(zs[sel_idx[i]] - st.mx) / st.Z;
     if (S > 0) p = p / denom;
     sel_w[i] = p;
     part += p;
   }
-  const float W = fmaxf(block_reduce_sum<kRouterThreads>(part, red), 1e-12f);
+  const float W = fmaxf(block_reduce_sum<NT>(part, red), 1e-12f);
   // ---- rank sort: (key desc, index asc)
-  for (int i = tid; i < k; i += kRouterThreads) {
+  for (int i = tid; i < k; i += NT) {
     const uint32_t ki = sel_key[i];
     const int32_t ii = sel_idx[i];
     int rank = 0;
     for (int j = 0; j < k; ++j) {
-      uint32_t kj = sel_key[j];
+      const uint32_t kj = sel_key[j];
       rank += (kj > ki) || (kj == ki && sel_idx[j] < ii);
     }
     idx_out[r * k + rank] = ii;
@@ -195,62 +222,56 @@ __global__ __launch_bounds__(kRouterThreads) void router_topk_kernel(
 // dlogits for the chain  p = softmax(z); q = p masked to c >= S; p' = q / clamp(sum q);
 // w = p'[idx]; w_hat = w / clamp(sum w).  dw_hat is the incoming gradient.  Mirrors
 // autograd of memory_transformer/router.py:114-149 including the clamp_min(1e-12) gates.
-__global__ __launch_bounds__(kRouterThreads) void router_topk_bwd_kernel(
+// The row and the dense dp vector live in LDS.
+template <int NT>
+__global__ __launch_bounds__(NT) void router_topk_bwd_kernel(
     const float* __restrict__ logits, const int32_t* __restrict__ idx, const float* __restrict__ dw_hat,
     int64_t C, int S, int k, float* __restrict__ dlogits) {
-  __shared__ float red[kRouterThreads / 64];
+  extern __shared__ float zs[];  // row [C] then dp [C]
+  float* dps = zs + C;
+  __shared__ float red[NT / 64];
   __shared__ float s_dwraw[kMaxTopK];
   const int64_t r = blockIdx.x;
-  const float* z = logits + r * C;
   float* dz = dlogits + r * C;
   const int tid = threadIdx.x;
-  const RowStats st = row_stats(z, C, S, red);
+  load_row<NT>(logits + r * C, C, zs);
+  const RowStats st = row_stats<NT>(zs, C, S, red);
   const float denom = fmaxf(st.msum, 1e-12f);
   const bool denom_live = st.msum >= 1e-12f;
 
   // w_raw and its sum
   float part = 0.f, gw = 0.f;
-  for (int i = tid; i < k; i += kRouterThreads) {
-    float p = __expf(z[idx[r * k + i]] - st.mx) / st.Z;
+  for (int i = tid; i < k; i += NT) {
+    float p = __expf(zs[idx[r * k + i]] - st.mx) / st.Z;
     if (S > 0) p = p / denom;
     part += p;
     gw += dw_hat[r * k + i] * p;
   }
-  const float Wsum = block_reduce_sum<kRouterThreads>(part, red);
-  const float GW = block_reduce_sum<kRouterThreads>(gw, red);  // sum_j g_j w_raw_j
+  const float Wsum = block_reduce_sum<NT>(part, red);
+  const float GW = block_reduce_sum<NT>(gw, red);  // sum_j g_j w_raw_j
   const float W = fmaxf(Wsum, 1e-12f);
   const bool W_live = Wsum >= 1e-12f;
   // dw_raw_i = g_i / W - [live] * GW / W^2 ; A = sum_i dw_raw_i * q_{idx_i}
   float a = 0.f;
-  for (int i = tid; i < k; i += kRouterThreads) {
-    float dwr = dw_hat[r * k + i] / W - (W_live ? GW / (W * W) : 0.f);
+  for (int i = tid; i < k; i += NT) {
+    const float dwr = dw_hat[r * k + i] / W - (W_live ? GW / (W * W) : 0.f);
     s_dwraw[i] = dwr;
-    float p = __expf(z[idx[r * k + i]] - st.mx) / st.Z;
+    const float p = __expf(zs[idx[r * k + i]] - st.mx) / st.Z;
     a += dwr * p;
   }
-  const float A = block_reduce_sum<kRouterThreads>(a, red);
+  const float A = block_reduce_sum<NT>(a, red);
+  // dp_c: the mask/renormalisation term for every c >= S, plus the selected entries
+  const float base = (S > 0 && denom_live) ? -A / (denom * denom) : 0.f;
+  for (int64_t c = tid; c < C; c += NT) dps[c] = (S > 0 && c >= S) ? base : 0.f;
   __syncthreads();
-  // dp_c: dense.  First pass writes dp into dz and accumulates sum_c dp_c p_c.
+  for (int i = tid; i < k; i += NT) dps[idx[r * k + i]] += (S > 0) ? s_dwraw[i] / denom : s_dwraw[i];
+  __syncthreads();
   float dpp = 0.f;
-  for (int64_t c = tid; c < C; c += kRouterThreads) {
-    float dp = 0.f;
-    if (S > 0) {
-      if (c >= S) dp = -(denom_live ? A / (denom * denom) : 0.f);
-    }
-    dz[c] = dp;
-  }
-  __syncthreads();
-  for (int i = tid; i < k; i += kRouterThreads) {
-    int c = idx[r * k + i];
-    dz[c] += (S > 0) ? s_dwraw[i] / denom : s_dwraw[i];
-  }
-  __threadfence_block();
-  __syncthreads();
-  for (int64_t c = tid; c < C; c += kRouterThreads) dpp += dz[c] * (__expf(z[c] - st.mx) / st.Z);
-  const float DPP = block_reduce_sum<kRouterThreads>(dpp, red);
-  for (int64_t c = tid; c < C; c += kRouterThreads) {
-    float p = __expf(z[c] - st.mx) / st.Z;
-    dz[c] = p * (dz[c] - DPP);
+  for (int64_t c = tid; c < C; c += NT) dpp += dps[c] * (__expf(zs[c] - st.mx) / st.Z);
+  const float DPP = block_reduce_sum<NT>(dpp, red);
+  for (int64_t c = tid; c < C; c += NT) {
+    const float p = __expf(zs[c] - st.mx) / st.Z;
+    dz[c] = p * (dps[c] - DPP);
   }
 }
 
@@ -292,100 +313,201 @@ __global__ void prepend_bwd_kernel(const float* __restrict__ w, const float* __r
 }
 
 // pooled[b, :] = sum_l coef[l] * h[b, l, :]   (coef == nullptr: mean over L).
-// grid (ceil(d/256), B, nsplit); partials [nsplit][B][d] reduced by pool_reduce.
+// grid (B, nsplit), 128 threads: thread t sums 8-column chunks t, t + 128, ... of
+// rows [l0, l1) with several 16/32-byte loads in flight; partials [nsplit][B][d]
+// are reduced by pool_reduce.  d % 8 == 0.
+constexpr int kPoolThreads = 128;
 template <typename T>
-__global__ __launch_bounds__(256) void pool_partial_kernel(const T* __restrict__ h, int64_t L, int64_t d,
-                                                           const float* __restrict__ coef, int rows_per_split,
-                                                           float* __restrict__ part) {
-  const int64_t col = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const int64_t b = blockIdx.y;
-  const int split = blockIdx.z;
-  if (col >= d) return;
+__global__ __launch_bounds__(kPoolThreads) void pool_partial_kernel(const T* __restrict__ h, int64_t L, int64_t d,
+                                                                    const float* __restrict__ coef,
+                                                                    int rows_per_split, float* __restrict__ part) {
+  const int64_t b = blockIdx.x;
+  const int split = blockIdx.y;
   const int64_t l0 = (int64_t)split * rows_per_split;
   const int64_t l1 = min((int64_t)L, l0 + rows_per_split);
-  const T* hb = h + b * L * d + col;
-  float acc = 0.f;
-  if (coef) {
-    for (int64_t l = l0; l < l1; ++l) acc += coef[l] * to_f(hb[l * d]);
-  } else {
-    for (int64_t l = l0; l < l1; ++l) acc += to_f(hb[l * d]);
+  for (int64_t c8 = (int64_t)threadIdx.x * 8; c8 < d; c8 += kPoolThreads * 8) {
+    const T* hb = h + b * L * d + c8;
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    int64_t l = l0;
+    for (; l + 4 <= l1; l += 4) {
+      float v[4][8];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) ChunkLoadF<T>::run(hb + (l + u) * d, v[u]);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const float cw = coef ? coef[l + u] : 1.f;
+#pragma unroll
+        for (int x = 0; x < 8; ++x) acc[x] += cw * v[u][x];
+      }
+    }
+    for (; l < l1; ++l) {
+      float v[8];
+      ChunkLoadF<T>::run(hb + l * d, v);
+      const float cw = coef ? coef[l] : 1.f;
+#pragma unroll
+      for (int x = 0; x < 8; ++x) acc[x] += cw * v[x];
+    }
+    float* dst = part + ((int64_t)split * gridDim.x + b) * d + c8;
+    *reinterpret_cast<f32x4*>(dst) = f32x4{acc[0], acc[1], acc[2], acc[3]};
+    *reinterpret_cast<f32x4*>(dst + 4) = f32x4{acc[4], acc[5], acc[6], acc[7]};
   }
-  part[((int64_t)split * gridDim.y + b) * d + col] = acc;
 }
 
-__global__ void pool_reduce_kernel(const float* __restrict__ part, int nsplit, int64_t B, int64_t d, float inv,
-                                   float* __restrict__ pooled) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= B * d) return;
+// out[i] = inv * sum_j part[j][i] for i < n, j < nsplit.  A workgroup owns 64
+// consecutive outputs; its 4 waves sum interleaved quarters of the partials with
+// 8 loads in flight, then wave 0 adds the 4 quarters in order (deterministic).
+__global__ __launch_bounds__(256) void pool_reduce_kernel(const float* __restrict__ part, int nsplit, int64_t B,
+                                                          int64_t d, float inv, float* __restrict__ out) {
+  __shared__ float q4[4][64];
+  const int64_t n = B * d;
+  const int o = threadIdx.x & 63, g = threadIdx.x >> 6;
+  const int64_t i = (int64_t)blockIdx.x * 64 + o;
   float s = 0.f;
-  for (int j = 0; j < nsplit; ++j) s += part[(int64_t)j * B * d + i];
-  pooled[i] = s * inv;
+  if (i < n) {
+    int j = g;
+    for (; j + 28 < nsplit; j += 32) {
+      float v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = part[(int64_t)(j + 4 * u) * n + i];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) s += v[u];
+    }
+    for (; j < nsplit; j += 4) s += part[(int64_t)j * n + i];
+  }
+  q4[g][o] = s;
+  __syncthreads();
+  if (g == 0 && i < n) out[i] = (q4[0][o] + q4[1][o] + q4[2][o] + q4[3][o]) * inv;
 }
 
-// logits[r, c] = x[r, :] . W[c, :] + b[c]; one wave per chapter row, all R rows.
+// Router linear for few rows (one per sequence).  A workgroup owns kLinChap
+// consecutive chapters (4 per wave) and stages up to kLinRows rows of x in LDS,
+// so W is streamed from HBM once and x is read from LDS.  Every loop keeps its
+// global loads in registers before the first use (4 floats per lane per load),
+// so a thread never waits on one load at a time.  d % 4 == 0.
+constexpr int kLinChap = 16;
+constexpr int kLinRows = 16;
+
+__device__ __forceinline__ f32x4 load4f(const float* p) { return *reinterpret_cast<const f32x4*>(p); }
+__device__ __forceinline__ f32x4 load4f(const bf16* p) {
+  const bf16x4 v = *reinterpret_cast<const bf16x4*>(p);
+  return f32x4{(float)v[0], (float)v[1], (float)v[2], (float)v[3]};
+}
+
+// xs[0 .. n) = x[0 .. n), n % 4 == 0, 16-byte loads, 4 in flight per thread
+__device__ __forceinline__ void stage_rows(const float* __restrict__ x, int64_t n, float* xs) {
+  int64_t i = (int64_t)threadIdx.x * 4;
+  for (; i + 3 * 1024 < n; i += 4 * 1024) {
+    const f32x4 a = load4f(x + i), b = load4f(x + i + 1024), c = load4f(x + i + 2048), e = load4f(x + i + 3072);
+    *reinterpret_cast<f32x4*>(xs + i) = a;
+    *reinterpret_cast<f32x4*>(xs + i + 1024) = b;
+    *reinterpret_cast<f32x4*>(xs + i + 2048) = c;
+    *reinterpret_cast<f32x4*>(xs + i + 3072) = e;
+  }
+  for (; i < n; i += 1024) *reinterpret_cast<f32x4*>(xs + i) = load4f(x + i);
+}
+
 template <typename TW>
 __global__ __launch_bounds__(256) void router_linear_kernel(const float* __restrict__ x, int64_t R, int64_t d,
                                                             const TW* __restrict__ W, const float* __restrict__ bias,
                                                             int64_t C, float* __restrict__ logits) {
-  const int64_t c = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  if (c >= C) return;
-  const TW* wr = W + c * d;
-  const float bc = bias ? bias[c] : 0.f;
-  for (int64_t r = 0; r < R; ++r) {
-    const float* xr = x + r * d;
-    float acc = 0.f;
-    for (int64_t j = lane; j < d; j += 64) acc += xr[j] * to_f(wr[j]);
-    acc = wave_sum(acc);
-    if (lane == 0) logits[r * C + c] = acc + bc;
+  extern __shared__ float xs[];  // [kLinRows][d]
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t c0 = (int64_t)blockIdx.x * kLinChap + 4 * wave;  // this wave's 4 chapters
+  for (int64_t r0 = 0; r0 < R; r0 += kLinRows) {
+    const int nr = (int)min((int64_t)kLinRows, R - r0);
+    __syncthreads();
+    stage_rows(x + r0 * d, (int64_t)nr * d, xs);
+    __syncthreads();
+    float acc[4][kLinRows];
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int r = 0; r < kLinRows; ++r) acc[q][r] = 0.f;
+    for (int64_t j = 4 * lane; j < d; j += 256) {
+      f32x4 wv[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) wv[q] = c0 + q < C ? load4f(W + (c0 + q) * d + j) : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int r = 0; r < kLinRows; ++r) {
+        if (r < nr) {  // (a guard, not a break: the loop must unroll fully to keep acc in registers)
+          const f32x4 xv = *reinterpret_cast<const f32x4*>(xs + r * d + j);
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            acc[q][r] += xv[0] * wv[q][0] + xv[1] * wv[q][1] + xv[2] * wv[q][2] + xv[3] * wv[q][3];
+        }
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int64_t c = c0 + q;
+      const float bc = (bias && c < C) ? bias[c] : 0.f;
+#pragma unroll
+      for (int r = 0; r < kLinRows; ++r) {
+        if (r < nr) {
+          const float v = wave_sum(acc[q][r]);
+          if (lane == 0 && c < C) logits[(r0 + r) * C + c] = v + bc;
+        }
+      }
+    }
   }
 }
 
-// Backward of the router linear for small R.
-//   dW[c, :] = sum_r dz[r, c] x[r, :]     db[c] = sum_r dz[r, c]
-//   dx partials over chapter splits, reduced by pool_reduce_kernel.
-__global__ __launch_bounds__(256) void router_linear_dw_kernel(const float* __restrict__ dz, const float* __restrict__ x,
-                                                               int64_t R, int64_t d, int64_t C,
-                                                               float* __restrict__ dW, float* __restrict__ db) {
-  const int64_t c = blockIdx.x;
-  for (int64_t j = threadIdx.x; j < d; j += 256) {
-    float acc = 0.f;
-    for (int64_t r = 0; r < R; ++r) acc += dz[r * C + c] * x[r * d + j];
-    dW[c * d + j] = acc;
-  }
-  if (threadIdx.x == 0 && db) {
-    float s = 0.f;
-    for (int64_t r = 0; r < R; ++r) s += dz[r * C + c];
-    db[c] = s;
-  }
-}
-
-// dx partials: each thread owns one column j and up to kDxRows rows; W is read
-// once per row-chunk.  grid (ceil(d/256), nsplit over C, ceil(R/kDxRows)).
-constexpr int kDxRows = 16;
+// Backward of the router linear for few rows, one pass over W:
+//   dW[c, :] = sum_r dz[r, c] x[r, :],  db[c] = sum_r dz[r, c]   (workgroup's chapters)
+//   part[wg][r][j] = sum_{c of wg} dz[r, c] W[c, j]               (dx partial, 4 columns per thread)
+// the dx partials are summed over workgroups by pool_reduce (fixed order).
 template <typename TW>
-__global__ __launch_bounds__(256) void router_linear_dx_partial_kernel(const float* __restrict__ dz, const TW* __restrict__ W,
-                                                                       int64_t R, int64_t d, int64_t C, int c_per_split,
-                                                                       float* __restrict__ part) {
-  const int64_t j = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const int split = blockIdx.y;
-  const int64_t r0 = (int64_t)blockIdx.z * kDxRows;
-  const int nr = (int)min((int64_t)kDxRows, R - r0);
-  if (j >= d) return;
-  const int64_t c0 = (int64_t)split * c_per_split;
-  const int64_t c1 = min(C, c0 + c_per_split);
-  float acc[kDxRows];
+__global__ __launch_bounds__(256) void router_linear_bwd_kernel(const float* __restrict__ dz,
+                                                                const float* __restrict__ x, int64_t R, int64_t d,
+                                                                const TW* __restrict__ W, int64_t C,
+                                                                float* __restrict__ dW, float* __restrict__ db,
+                                                                float* __restrict__ part) {
+  extern __shared__ float xs[];  // [kLinRows][d]
+  __shared__ float dzs[kLinRows][kLinChap];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t cbase = (int64_t)blockIdx.x * kLinChap;
+  const int nc = (int)min((int64_t)kLinChap, C - cbase);
+  for (int64_t r0 = 0; r0 < R; r0 += kLinRows) {
+    const int nr = (int)min((int64_t)kLinRows, R - r0);
+    __syncthreads();
+    if (dW) stage_rows(x + r0 * d, (int64_t)nr * d, xs);
+    {
+      const int r = threadIdx.x / kLinChap, cc = threadIdx.x % kLinChap;  // 256 = 16 x 16
+      dzs[r][cc] = (r < nr && cc < nc) ? dz[(r0 + r) * C + cbase + cc] : 0.f;
+    }
+    __syncthreads();
+    // dW rows of this wave's 4 chapters (x from LDS, no global loads in the loop)
+    if (dW) {
+      for (int q = 0; q < 4; ++q) {
+        const int cc = 4 * wave + q;
+        if (cc >= nc) break;
+        float* dst = dW + (cbase + cc) * d;
+        for (int64_t j = 4 * lane; j < d; j += 256) {
+          f32x4 a = r0 > 0 ? *reinterpret_cast<const f32x4*>(dst + j) : f32x4{0.f, 0.f, 0.f, 0.f};
+          for (int r = 0; r < nr; ++r) a += dzs[r][cc] * *reinterpret_cast<const f32x4*>(xs + r * d + j);
+          *reinterpret_cast<f32x4*>(dst + j) = a;
+        }
+      }
+    }
+    if (db && threadIdx.x < nc) {
+      float sacc = r0 > 0 ? db[cbase + threadIdx.x] : 0.f;
+      for (int r = 0; r < nr; ++r) sacc += dzs[r][threadIdx.x];
+      db[cbase + threadIdx.x] = sacc;
+    }
+    if (part) {
+      for (int64_t j = 4 * (int64_t)threadIdx.x; j < d; j += 1024) {
+        f32x4 wv[kLinChap];
 #pragma unroll
-  for (int r = 0; r < kDxRows; ++r) acc[r] = 0.f;
-  for (int64_t c = c0; c < c1; ++c) {
-    const float wv = to_f(W[c * d + j]);
+        for (int cc = 0; cc < kLinChap; ++cc) wv[cc] = cc < nc ? load4f(W + (cbase + cc) * d + j) : f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int r = 0; r < nr; ++r) {
+          f32x4 a = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int r = 0; r < kDxRows; ++r)
-      if (r < nr) acc[r] += dz[(r0 + r) * C + c] * wv;
+          for (int cc = 0; cc < kLinChap; ++cc) a += dzs[r][cc] * wv[cc];
+          *reinterpret_cast<f32x4*>(part + ((int64_t)blockIdx.x * R + r0 + r) * d + j) = a;
+        }
+      }
+    }
   }
-#pragma unroll
-  for (int r = 0; r < kDxRows; ++r)
-    if (r < nr) part[((int64_t)split * R + r0 + r) * d + j] = acc[r];
 }
 
 }  // namespace moc
@@ -401,8 +523,15 @@ int moc_router_topk(const float* logits, int64_t R, int64_t C, int S, int k, int
   MOC_REQUIRE(S >= 0 && S <= C, MOC_ERR_ARG, "exclude_prefix_chapters must be in [0, %lld], got %d", (long long)C, S);
   MOC_REQUIRE(k > 0 && k <= C - S, MOC_ERR_ARG, "moc_router_topk: k=%d must be in [1, C-S=%lld]", k, (long long)(C - S));
   MOC_REQUIRE(k <= kMaxTopK, MOC_ERR_UNSUPPORTED, "moc_router_topk: k=%d exceeds %d", k, kMaxTopK);
+  MOC_REQUIRE(C <= kMaxRouterC, MOC_ERR_UNSUPPORTED, "moc_router_topk: C=%lld exceeds %d", (long long)C, kMaxRouterC);
   if (R == 0) return MOC_OK;
-  hipLaunchKernelGGL(router_topk_kernel, dim3((unsigned)R), dim3(kRouterThreads), 0, stream, logits, C, S, k, idx, w, probs);
+  const size_t lds = (size_t)C * sizeof(float);
+  if (router_threads(R) == 1024)
+    hipLaunchKernelGGL(router_topk_kernel<1024>, dim3((unsigned)R), dim3(1024), lds, stream, logits, C, S, k, idx, w,
+                       probs);
+  else
+    hipLaunchKernelGGL(router_topk_kernel<256>, dim3((unsigned)R), dim3(256), lds, stream, logits, C, S, k, idx, w,
+                       probs);
   return check_launch("router_topk_kernel");
 }
 
@@ -411,8 +540,16 @@ int moc_router_topk_bwd(const float* logits, const int32_t* idx, const float* dw
   MOC_REQUIRE(logits && idx && dw && dlogits, MOC_ERR_ARG, "moc_router_topk_bwd: null pointer");
   MOC_REQUIRE(S >= 0 && S <= C && k > 0 && k <= C - S && k <= kMaxTopK, MOC_ERR_ARG,
               "moc_router_topk_bwd: bad S=%d k=%d C=%lld", S, k, (long long)C);
+  MOC_REQUIRE(C <= kMaxRouterC / 2, MOC_ERR_UNSUPPORTED, "moc_router_topk_bwd: C=%lld exceeds %d", (long long)C,
+              kMaxRouterC / 2);
   if (R == 0) return MOC_OK;
-  hipLaunchKernelGGL(router_topk_bwd_kernel, dim3((unsigned)R), dim3(kRouterThreads), 0, stream, logits, idx, dw, C, S, k, dlogits);
+  const size_t lds = 2 * (size_t)C * sizeof(float);
+  if (router_threads(R) == 1024)
+    hipLaunchKernelGGL(router_topk_bwd_kernel<1024>, dim3((unsigned)R), dim3(1024), lds, stream, logits, idx, dw, C, S,
+                       k, dlogits);
+  else
+    hipLaunchKernelGGL(router_topk_bwd_kernel<256>, dim3((unsigned)R), dim3(256), lds, stream, logits, idx, dw, C, S, k,
+                       dlogits);
   return check_launch("router_topk_bwd_kernel");
 }
 
@@ -436,10 +573,17 @@ int moc_prepend_shared_bwd(const float* w, const float* domega, int64_t R, int k
   return check_launch("prepend_bwd_kernel");
 }
 
+namespace {
+int pool_splits(int64_t B, int64_t L) {
+  // ~16 rows per workgroup, at most 256 splits, at least ~512 workgroups when L allows
+  int64_t n = (L + 15) / 16;
+  if (n > 256) n = 256;
+  return (int)(n < 1 ? 1 : n);
+}
+}  // namespace
+
 size_t moc_router_pool_workspace(int64_t B, int64_t L, int64_t d) {
-  int nsplit = (int)((L + 63) / 64);
-  if (nsplit > 64) nsplit = 64;
-  return (size_t)nsplit * B * d * sizeof(float);
+  return (size_t)pool_splits(B, L) * B * d * sizeof(float);
 }
 
 int moc_router_pool(const void* h, int dtype, int64_t B, int64_t L, int64_t d, const float* coef, float* pooled,
@@ -447,22 +591,26 @@ int moc_router_pool(const void* h, int dtype, int64_t B, int64_t L, int64_t d, c
   MOC_REQUIRE(h && pooled && workspace, MOC_ERR_ARG, "moc_router_pool: null pointer");
   MOC_REQUIRE(B >= 0 && L > 0 && d > 0, MOC_ERR_ARG, "moc_router_pool: bad shape");
   MOC_REQUIRE(workspace_bytes >= moc_router_pool_workspace(B, L, d), MOC_ERR_ARG, "moc_router_pool: workspace too small");
+  MOC_REQUIRE(d % 8 == 0, MOC_ERR_UNSUPPORTED, "moc_router_pool: d=%lld must be a multiple of 8", (long long)d);
+  MOC_REQUIRE(B < 65536, MOC_ERR_UNSUPPORTED, "moc_router_pool: B=%lld too large", (long long)B);
   if (B == 0) return MOC_OK;
-  int nsplit = (int)((L + 63) / 64);
-  if (nsplit > 64) nsplit = 64;
-  int rows = (int)((L + nsplit - 1) / nsplit);
-  dim3 grid((unsigned)((d + 255) / 256), (unsigned)B, (unsigned)nsplit);
+  const int nsplit = pool_splits(B, L);
+  const int rows = (int)((L + nsplit - 1) / nsplit);
+  dim3 grid((unsigned)B, (unsigned)nsplit);
   float* part = (float*)workspace;
   if (dtype == MOC_F32)
-    hipLaunchKernelGGL(pool_partial_kernel<float>, grid, dim3(256), 0, stream, (const float*)h, L, d, coef, rows, part);
+    hipLaunchKernelGGL(pool_partial_kernel<float>, grid, dim3(kPoolThreads), 0, stream, (const float*)h, L, d, coef,
+                       rows, part);
   else if (dtype == MOC_BF16)
-    hipLaunchKernelGGL(pool_partial_kernel<bf16>, grid, dim3(256), 0, stream, (const bf16*)h, L, d, coef, rows, part);
+    hipLaunchKernelGGL(pool_partial_kernel<bf16>, grid, dim3(kPoolThreads), 0, stream, (const bf16*)h, L, d, coef,
+                       rows, part);
   else
     return set_error(MOC_ERR_UNSUPPORTED, "moc_router_pool: dtype %d", dtype);
   int rc = check_launch("pool_partial_kernel");
   if (rc) return rc;
   const float inv = coef ? 1.f : 1.f / (float)L;
-  hipLaunchKernelGGL(pool_reduce_kernel, dim3((unsigned)((B * d + 255) / 256)), dim3(256), 0, stream, part, nsplit, B, d, inv, pooled);
+  hipLaunchKernelGGL(pool_reduce_kernel, dim3((unsigned)((B * d + 63) / 64)), dim3(256), 0, stream, part, nsplit, B, d,
+                     inv, pooled);
   return check_launch("pool_reduce_kernel");
 }
 
@@ -470,50 +618,54 @@ int moc_router_linear(const float* x, int64_t R, int64_t d, const void* W, int w
                       float* logits, hipStream_t stream) {
   MOC_REQUIRE(x && W && logits, MOC_ERR_ARG, "moc_router_linear: null pointer");
   MOC_REQUIRE(R >= 0 && d > 0 && C > 0, MOC_ERR_ARG, "moc_router_linear: bad shape");
+  MOC_REQUIRE(d <= 4096 && d % 4 == 0, MOC_ERR_UNSUPPORTED, "moc_router_linear: d=%lld must be a multiple of 4, <= 4096",
+              (long long)d);
   if (R == 0) return MOC_OK;
-  dim3 grid((unsigned)((C + 3) / 4));
+  dim3 grid((unsigned)((C + kLinChap - 1) / kLinChap));
+  const size_t lds = (size_t)kLinRows * d * sizeof(float);
   if (w_dtype == MOC_F32)
-    hipLaunchKernelGGL(router_linear_kernel<float>, grid, dim3(256), 0, stream, x, R, d, (const float*)W, bias, C, logits);
+    hipLaunchKernelGGL(router_linear_kernel<float>, grid, dim3(256), lds, stream, x, R, d, (const float*)W, bias, C,
+                       logits);
   else if (w_dtype == MOC_BF16)
-    hipLaunchKernelGGL(router_linear_kernel<bf16>, grid, dim3(256), 0, stream, x, R, d, (const bf16*)W, bias, C, logits);
+    hipLaunchKernelGGL(router_linear_kernel<bf16>, grid, dim3(256), lds, stream, x, R, d, (const bf16*)W, bias, C,
+                       logits);
   else
     return set_error(MOC_ERR_UNSUPPORTED, "moc_router_linear: dtype %d", w_dtype);
   return check_launch("router_linear_kernel");
 }
 
 size_t moc_router_linear_bwd_workspace(int64_t R, int64_t d, int64_t C) {
-  int nsplit = (int)((C + 127) / 128);
-  return (size_t)nsplit * R * d * sizeof(float);
+  return (size_t)((C + kLinChap - 1) / kLinChap) * R * d * sizeof(float);
 }
 
 int moc_router_linear_bwd(const float* dz, const float* x, int64_t R, int64_t d, const void* W, int w_dtype, int64_t C,
                           float* dx, float* dW, float* db, void* workspace, size_t workspace_bytes,
                           hipStream_t stream) {
   MOC_REQUIRE(dz && x && W, MOC_ERR_ARG, "moc_router_linear_bwd: null pointer");
-  if (R == 0) return MOC_OK;
-  if (dW) {
-    hipLaunchKernelGGL(router_linear_dw_kernel, dim3((unsigned)C), dim3(256), 0, stream, dz, x, R, d, C, dW, db);
-    int rc = check_launch("router_linear_dw_kernel");
-    if (rc) return rc;
-  }
+  MOC_REQUIRE(d <= 4096 && d % 4 == 0, MOC_ERR_UNSUPPORTED,
+              "moc_router_linear_bwd: d=%lld must be a multiple of 4, <= 4096", (long long)d);
+  if (R == 0 || (!dx && !dW && !db)) return MOC_OK;
+  const int64_t nwg = (C + kLinChap - 1) / kLinChap;
+  float* part = nullptr;
   if (dx) {
     MOC_REQUIRE(workspace && workspace_bytes >= moc_router_linear_bwd_workspace(R, d, C), MOC_ERR_ARG,
                 "moc_router_linear_bwd: workspace too small");
-    int nsplit = (int)((C + 127) / 128);
-    dim3 grid((unsigned)((d + 255) / 256), (unsigned)nsplit, (unsigned)((R + kDxRows - 1) / kDxRows));
-    float* part = (float*)workspace;
-    if (w_dtype == MOC_F32)
-      hipLaunchKernelGGL(router_linear_dx_partial_kernel<float>, grid, dim3(256), 0, stream, dz, (const float*)W, R, d, C, 128, part);
-    else if (w_dtype == MOC_BF16)
-      hipLaunchKernelGGL(router_linear_dx_partial_kernel<bf16>, grid, dim3(256), 0, stream, dz, (const bf16*)W, R, d, C, 128, part);
-    else
-      return set_error(MOC_ERR_UNSUPPORTED, "moc_router_linear_bwd: dtype %d", w_dtype);
-    int rc = check_launch("router_linear_dx_partial_kernel");
-    if (rc) return rc;
-    hipLaunchKernelGGL(pool_reduce_kernel, dim3((unsigned)((R * d + 255) / 256)), dim3(256), 0, stream, part, nsplit, R, d, 1.f, dx);
-    return check_launch("pool_reduce_kernel");
+    part = (float*)workspace;
   }
-  return MOC_OK;
+  const size_t lds = (size_t)kLinRows * d * sizeof(float);
+  if (w_dtype == MOC_F32)
+    hipLaunchKernelGGL(router_linear_bwd_kernel<float>, dim3((unsigned)nwg), dim3(256), lds, stream, dz, x, R, d,
+                       (const float*)W, C, dW, db, part);
+  else if (w_dtype == MOC_BF16)
+    hipLaunchKernelGGL(router_linear_bwd_kernel<bf16>, dim3((unsigned)nwg), dim3(256), lds, stream, dz, x, R, d,
+                       (const bf16*)W, C, dW, db, part);
+  else
+    return set_error(MOC_ERR_UNSUPPORTED, "moc_router_linear_bwd: dtype %d", w_dtype);
+  int rc = check_launch("router_linear_bwd_kernel");
+  if (rc || !dx) return rc;
+  hipLaunchKernelGGL(pool_reduce_kernel, dim3((unsigned)((R * d + 63) / 64)), dim3(256), 0, stream, part, (int)nwg, R,
+                     d, 1.f, dx);
+  return check_launch("pool_reduce_kernel");
 }
 
 }  // extern "C"

@@ -80,8 +80,8 @@ template <typename T>
 __global__ __launch_bounds__(kBThreads) void xattn_bwd_dq_kernel(
     const T* __restrict__ q, const T* __restrict__ ktiles, const T* __restrict__ kttiles,
     const T* __restrict__ vtiles, const int32_t* __restrict__ slot_u, const float* __restrict__ omega,
-    const T* __restrict__ dout, const float* __restrict__ lse, const float* __restrict__ delta, int L, int H, int HK,
-    int NS, int64_t n_tiles, float scale_log2, float scale, T* __restrict__ dq) {
+    const T* __restrict__ dout, const float* __restrict__ lse, const float* __restrict__ delta, int B, int L, int H,
+    int HK, int NS, int64_t n_tiles, float scale_log2, float scale, T* __restrict__ dq) {
   typedef typename Frag<T>::type F8;
   using Tile = SwzTile<T, 64>;
   constexpr int TB = kBT * kBDh * (int)sizeof(T);
@@ -90,10 +90,14 @@ __global__ __launch_bounds__(kBThreads) void xattn_bwd_dq_kernel(
   __shared__ __attribute__((aligned(16))) char sKt[2][TB];
   __shared__ __attribute__((aligned(16))) char sV[2][TB];
 
-  const int b = blockIdx.z, h = blockIdx.y;
+  // tiles: (sequence, head) major, 128-query block minor (XCD-local chapter tiles)
+  const int nqb = (L + 127) / 128;
+  const int64_t t = xcd_tile((int64_t)B * H * nqb);
+  if (t < 0) return;
+  const int b = (int)(t / ((int64_t)H * nqb)), h = (int)((t / nqb) % H);
   const int hk = h / (H / HK);
-  const int q0 = blockIdx.x * 128;
-  const int Lp = (int)gridDim.x * 128;
+  const int q0 = (int)(t % nqb) * 128;
+  const int Lp = nqb * 128;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 4, c16 = lane & 15;
 
@@ -243,8 +247,9 @@ template <typename T>
 __global__ __launch_bounds__(64 * DkvCfg<T>::SG, 1) void xattn_bwd_dkv_kernel(
     const T* __restrict__ q, const T* __restrict__ qt, const T* __restrict__ dout, const T* __restrict__ dot,
     const T* __restrict__ ktiles, const T* __restrict__ vtiles, const int32_t* __restrict__ slot_u,
-    const float* __restrict__ omega, const float* __restrict__ lse, const float* __restrict__ delta, int L, int Lp,
-    int H, int HK, int NS, float scale_log2, float scale, T* __restrict__ dkv_edge, float* __restrict__ domega_part) {
+    const float* __restrict__ omega, const float* __restrict__ lse, const float* __restrict__ delta, int B, int L,
+    int Lp, int H, int HK, int NS, float scale_log2, float scale, T* __restrict__ dkv_edge,
+    float* __restrict__ domega_part) {
   typedef typename Frag<T>::type F8;
   constexpr int SG = DkvCfg<T>::SG, QS = DkvCfg<T>::QS, NT = 64 * SG;
   constexpr bool kKVRegs = DkvCfg<T>::kKVRegs;
@@ -258,10 +263,15 @@ __global__ __launch_bounds__(64 * DkvCfg<T>::SG, 1) void xattn_bwd_dkv_kernel(
   __shared__ __attribute__((aligned(16))) char sStage[2][4][STB];  // [buf][Q, dO, Q^T, dO^T]
   __shared__ float sL[2][QS], sDl[2][QS];
 
-  const int b = blockIdx.z, hk = blockIdx.y;
+  // tiles: (sequence, kv head) major, slot group minor, so the slot groups that stage
+  // the same query tiles share one XCD's L2
+  const int nsg = (NS + SG - 1) / SG;
+  const int64_t t = xcd_tile((int64_t)B * HK * nsg);
+  if (t < 0) return;
+  const int b = (int)(t / ((int64_t)HK * nsg)), hk = (int)((t / nsg) % HK);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 4, c16 = lane & 15;
-  const int slot = SG * blockIdx.x + wave;
+  const int slot = SG * (int)(t % nsg) + wave;
   const int e = b * NS + slot;
   const int u = slot < NS ? slot_u[e] : -1;
   const bool active = u >= 0;
@@ -667,16 +677,17 @@ int moc_xattn_bwd_dq(int dtype, const void* q, const void* k_tiles, const void* 
   MOC_REQUIRE(n_tiles > 0 && n_tiles * 64 * 64 * (dtype == MOC_F32 ? 4 : 2) < ((int64_t)1 << 32), MOC_ERR_UNSUPPORTED,
               "moc_xattn_bwd_dq: tile buffers must be < 4 GiB (n_tiles=%lld)", (long long)n_tiles);
   if (B == 0 || L == 0) return MOC_OK;
-  dim3 grid((unsigned)((L + 127) / 128), (unsigned)H, (unsigned)B);
+  MOC_REQUIRE(B * H * ((L + 127) / 128) < ((int64_t)1 << 31), MOC_ERR_UNSUPPORTED, "moc_xattn_bwd_dq: grid too large");
+  dim3 grid(xcd_grid(B * H * ((L + 127) / 128)));
   const float sl2 = scale * 1.4426950408889634f;
   if (dtype == MOC_BF16)
     hipLaunchKernelGGL(xattn_bwd_dq_kernel<bf16>, grid, dim3(kBThreads), 0, stream, (const bf16*)q, (const bf16*)k_tiles,
-                       (const bf16*)kt_tiles, (const bf16*)v_tiles, slot_u, omega, (const bf16*)dout, lse, delta, (int)L, H, HK, NS, n_tiles, sl2,
-                       scale, (bf16*)dq);
+                       (const bf16*)kt_tiles, (const bf16*)v_tiles, slot_u, omega, (const bf16*)dout, lse, delta, (int)B, (int)L, H, HK, NS,
+                       n_tiles, sl2, scale, (bf16*)dq);
   else if (dtype == MOC_F32)
     hipLaunchKernelGGL(xattn_bwd_dq_kernel<float>, grid, dim3(kBThreads), 0, stream, (const float*)q,
                        (const float*)k_tiles, (const float*)kt_tiles, (const float*)v_tiles, slot_u, omega, (const float*)dout, lse, delta,
-                       (int)L, H, HK, NS, n_tiles, sl2, scale, (float*)dq);
+                       (int)B, (int)L, H, HK, NS, n_tiles, sl2, scale, (float*)dq);
   else
     return set_error(MOC_ERR_UNSUPPORTED, "moc_xattn_bwd_dq: dtype %d", dtype);
   return check_launch("xattn_bwd_dq_kernel");
@@ -699,16 +710,16 @@ int moc_xattn_bwd_dkv(int dtype, const void* q, const void* qt, const void* dout
   const float sl2 = scale * 1.4426950408889634f;
   if (dtype == MOC_BF16) {
     constexpr int SG = DkvCfg<bf16>::SG;
-    dim3 grid((unsigned)((NS + SG - 1) / SG), (unsigned)HK, (unsigned)B);
+    dim3 grid(xcd_grid(B * HK * ((NS + SG - 1) / SG)));
     hipLaunchKernelGGL(xattn_bwd_dkv_kernel<bf16>, grid, dim3(64 * SG), 0, stream, (const bf16*)q, (const bf16*)qt,
                        (const bf16*)dout, (const bf16*)dot, (const bf16*)k_tiles, (const bf16*)v_tiles, slot_u,
-                       omega, lse, delta, (int)L, Lp, H, HK, NS, sl2, scale, (bf16*)dkv_edge, domega_part);
+                       omega, lse, delta, (int)B, (int)L, Lp, H, HK, NS, sl2, scale, (bf16*)dkv_edge, domega_part);
   } else if (dtype == MOC_F32) {
     constexpr int SG = DkvCfg<float>::SG;
-    dim3 grid((unsigned)((NS + SG - 1) / SG), (unsigned)HK, (unsigned)B);
+    dim3 grid(xcd_grid(B * HK * ((NS + SG - 1) / SG)));
     hipLaunchKernelGGL(xattn_bwd_dkv_kernel<float>, grid, dim3(64 * SG), 0, stream, (const float*)q,
                        (const float*)qt, (const float*)dout, (const float*)dot, (const float*)k_tiles,
-                       (const float*)v_tiles, slot_u, omega, lse, delta, (int)L, Lp, H, HK, NS, sl2, scale,
+                       (const float*)v_tiles, slot_u, omega, lse, delta, (int)B, (int)L, Lp, H, HK, NS, sl2, scale,
                        (float*)dkv_edge, domega_part);
   } else {
     return set_error(MOC_ERR_UNSUPPORTED, "moc_xattn_bwd_dkv: dtype %d", dtype);

@@ -36,7 +36,7 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 template <typename T>
 __global__ __launch_bounds__(kFwdThreads) void xattn_fwd_kernel(
     const T* __restrict__ q, const T* __restrict__ ktiles, const T* __restrict__ vttiles,
-    const int32_t* __restrict__ slot_u, const float* __restrict__ omega, int L, int H, int HK, int NS,
+    const int32_t* __restrict__ slot_u, const float* __restrict__ omega, int B, int L, int H, int HK, int NS,
     int64_t n_tiles, float scale_log2, T* __restrict__ out, float* __restrict__ lse) {
   typedef typename Frag<T>::type F8;
   using Tile = SwzTile<T, 64>;
@@ -44,9 +44,14 @@ __global__ __launch_bounds__(kFwdThreads) void xattn_fwd_kernel(
   __shared__ __attribute__((aligned(16))) char sK[2][TB];
   __shared__ __attribute__((aligned(16))) char sV[2][TB];
 
-  const int b = blockIdx.z, h = blockIdx.y;
+  // tiles: (sequence, head) major, 128-query block minor, so the query blocks that read
+  // the same chapter tiles share one XCD's L2
+  const int nqb = (L + 127) / 128;
+  const int64_t t = xcd_tile((int64_t)B * H * nqb);
+  if (t < 0) return;
+  const int b = (int)(t / ((int64_t)H * nqb)), h = (int)((t / nqb) % H);
   const int hk = h / (H / HK);
-  const int q0 = blockIdx.x * 128;
+  const int q0 = (int)(t % nqb) * 128;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 4, c16 = lane & 15;
 
@@ -195,7 +200,7 @@ __global__ __launch_bounds__(kFwdThreads) void xattn_fwd_kernel(
   // lse rows have stride Lp = round_up(L, 128); padded entries hold +inf so
   // that the backward's exp2(s - lse) is exactly 0 there (also for a row
   // whose every slot was skipped).
-  const int Lp = (int)gridDim.x * 128;
+  const int Lp = nqb * 128;
 #pragma unroll
   for (int qb = 0; qb < 2; ++qb) {
     const float l = quad_sum(lpart[qb]);
@@ -229,14 +234,15 @@ int moc_xattn_fwd(int dtype, const void* q, const void* k_tiles, const void* vt_
   MOC_REQUIRE(n_tiles > 0 && n_tiles * 64 * 64 * (dtype == MOC_F32 ? 4 : 2) < ((int64_t)1 << 32), MOC_ERR_UNSUPPORTED,
               "moc_xattn_fwd: tile buffers must be < 4 GiB (n_tiles=%lld)", (long long)n_tiles);
   if (B == 0 || L == 0) return MOC_OK;
-  dim3 grid((unsigned)((L + 127) / 128), (unsigned)H, (unsigned)B);
+  MOC_REQUIRE(B * H * ((L + 127) / 128) < ((int64_t)1 << 31), MOC_ERR_UNSUPPORTED, "moc_xattn_fwd: grid too large");
+  dim3 grid(xcd_grid(B * H * ((L + 127) / 128)));
   const float sl2 = scale * 1.4426950408889634f;
   if (dtype == MOC_BF16)
     hipLaunchKernelGGL(xattn_fwd_kernel<bf16>, grid, dim3(kFwdThreads), 0, stream, (const bf16*)q, (const bf16*)k_tiles,
-                       (const bf16*)vt_tiles, slot_u, omega, (int)L, H, HK, NS, n_tiles, sl2, (bf16*)out, lse);
+                       (const bf16*)vt_tiles, slot_u, omega, (int)B, (int)L, H, HK, NS, n_tiles, sl2, (bf16*)out, lse);
   else if (dtype == MOC_F32)
     hipLaunchKernelGGL(xattn_fwd_kernel<float>, grid, dim3(kFwdThreads), 0, stream, (const float*)q,
-                       (const float*)k_tiles, (const float*)vt_tiles, slot_u, omega, (int)L, H, HK, NS, n_tiles, sl2,
+                       (const float*)k_tiles, (const float*)vt_tiles, slot_u, omega, (int)B, (int)L, H, HK, NS, n_tiles, sl2,
                        (float*)out,
                        lse);
   else

@@ -84,16 +84,13 @@ class _RouterLinear(torch.autograd.Function):
         dx = torch.empty(R, d, device=x.device, dtype=torch.float32) if need_x else None
         dW = torch.empty(C, d, device=x.device, dtype=torch.float32) if need_w else None
         db = torch.empty(C, device=x.device, dtype=torch.float32) if (need_b and ctx.has_b) else None
-        if dW is None and db is not None:
-            dW_tmp = torch.empty(C, d, device=x.device, dtype=torch.float32)
-        else:
-            dW_tmp = dW
-        if dW_tmp is not None or db is not None:
-            call("moc_router_linear_bwd", ptr(dz), ptr(x), R, d, ptr(Wc), L.dtype_code(Wc.dtype), C, None,
-                 ptr(dW_tmp), ptr(db), None, 0, stream_ptr(x.device))
+        ws = None
         if dx is not None:
-            # dx = dz W: a plain (R, C) x (C, d) GEMM (hipBLASLt)
-            torch.matmul(dz, Wc.float(), out=dx)
+            ws = torch.empty(L.query("moc_router_linear_bwd_workspace", R, d, C) // 4, device=x.device,
+                             dtype=torch.float32)
+        # one pass over W: dW, db and dx (partials over chapter blocks, summed in order)
+        call("moc_router_linear_bwd", ptr(dz), ptr(x), R, d, ptr(Wc), L.dtype_code(Wc.dtype), C, ptr(dx), ptr(dW),
+             ptr(db), ptr(ws), 0 if ws is None else ws.numel() * 4, stream_ptr(x.device))
         if dW is not None:
             dW = dW.to(Wc.dtype)
         if db is not None:

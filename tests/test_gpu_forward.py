@@ -30,7 +30,7 @@ def _ops():
 # ------------------------------------------------------------------ router top-k
 
 @pytest.mark.parametrize("R,C,S,k", [(8, 4097, 1, 64), (3, 33, 1, 4), (5, 33, 1, 32), (4, 50, 0, 7),
-                                     (2, 1500, 3, 1), (6, 300, 2, 298)])
+                                     (2, 1500, 3, 1), (6, 300, 2, 298), (100, 4097, 1, 16), (70, 257, 0, 40)])
 def test_router_topk_matches_oracle(dev, R, C, S, k):
     print(f"router_topk R={R} C={C} S={S} k={k}", flush=True)
     logits = torch.randn(R, C, generator=gen(R * 1000 + C))
@@ -50,8 +50,9 @@ def test_router_topk_ties_lower_index_first(dev):
     assert_rel(w.cpu(), rw, 1e-5, "tie weights")
 
 
-def test_router_topk_backward_matches_autograd(dev):
-    R, C, S, k = 4, 97, 1, 8
+@pytest.mark.parametrize("R,C,S,k", [(4, 97, 1, 8), (80, 130, 2, 5), (3, 4097, 1, 64)])
+def test_router_topk_backward_matches_autograd(dev, R, C, S, k):
+    print(f"router_topk_bwd R={R} C={C} S={S} k={k}", flush=True)
     logits = torch.randn(R, C, generator=gen(11), dtype=torch.float64)
     dw = torch.randn(R, k, generator=gen(12), dtype=torch.float64)
     z = logits.clone().requires_grad_(True)
@@ -81,8 +82,9 @@ def test_prepend_forward_backward(dev):
     assert_rel(wg.grad.cpu(), wr.grad, 1e-5, "dw")
 
 
-def test_router_pool_and_linear(dev):
-    B, Lq, d, C = 3, 37, 128, 65
+@pytest.mark.parametrize("B,Lq,d,C", [(3, 37, 128, 65), (20, 70, 64, 33), (8, 1024, 768, 4097)])
+def test_router_pool_and_linear(dev, B, Lq, d, C):
+    print(f"router pool+linear B={B} L={Lq} d={d} C={C}", flush=True)
     h = torch.randn(B, Lq, d, generator=gen(16))
     W = torch.randn(C, d, generator=gen(17)) * 0.05
     b = torch.randn(C, generator=gen(18)) * 0.1

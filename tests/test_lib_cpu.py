@@ -58,7 +58,8 @@ def test_host_validation_rejects_before_launch(libpath):
 
 def test_workspace_queries(libpath):
     assert _lib.query("moc_chapter_plan_workspace", 520, 4097) == (1 * 4097 + 3 * 4097) * 4
-    assert _lib.query("moc_router_pool_workspace", 8, 1024, 768) == 16 * 8 * 768 * 4
+    assert _lib.query("moc_router_pool_workspace", 8, 1024, 768) == 64 * 8 * 768 * 4  # 16 rows per split
+    assert _lib.query("moc_router_linear_bwd_workspace", 8, 768, 4097) == 257 * 8 * 768 * 4  # 16 chapters / wg
 
 
 def test_cpu_tensors_are_rejected():
