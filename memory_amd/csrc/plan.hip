@@ -118,6 +118,83 @@ __global__ __launch_bounds__(256) void plan_place_kernel(const int32_t* __restri
   }
 }
 
+// Whole plan in one workgroup for small batches (E <= 1024 edges, C <= 8192): the
+// histogram, both scans and the stable placement run out of LDS, so the plan
+// costs one launch instead of four (the sequence-level path has B * (S + k)
+// edges, 520 at the paper shape).  Same outputs as the general path.
+constexpr int kPlanSmallE = 1024;
+constexpr int kPlanSmallC = 8192;
+
+__device__ __forceinline__ int wave_incl_scan(int v) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int t = __shfl_up(v, o, 64);
+    if (lane >= o) v += t;
+  }
+  return v;
+}
+
+__global__ __launch_bounds__(1024) void plan_small_kernel(const int32_t* __restrict__ chap, int64_t E, int64_t C,
+                                                          int32_t* __restrict__ uniq, int32_t* __restrict__ n_uniq,
+                                                          int32_t* __restrict__ edge_u,
+                                                          int32_t* __restrict__ csr_off,
+                                                          int32_t* __restrict__ csr_edge) {
+  extern __shared__ int32_t lds[];
+  int32_t* cnt = lds;      // [C] counts, then first csr position of each chapter
+  int32_t* uid = lds + C;  // [C] unique index of each present chapter
+  __shared__ int32_t ids[kPlanSmallE];
+  __shared__ int32_t wsum[2][16];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  for (int64_t c = tid; c < C; c += 1024) cnt[c] = 0;
+  if (tid < E) ids[tid] = chap[tid];
+  __syncthreads();
+  if (tid < E) {
+    const int32_t c = ids[tid];
+    if (c >= 0 && c < C) atomicAdd(&cnt[c], 1);  // out-of-range ids are dropped (counted below)
+  }
+  __syncthreads();
+  // thread t owns bins [t * per, (t + 1) * per): local totals, block exclusive scan
+  const int per = (int)((C + 1023) / 1024);
+  const int64_t c0 = (int64_t)tid * per, c1 = min(C, c0 + per);
+  int lt = 0, lf = 0;
+  for (int64_t c = c0; c < c1; ++c) { lt += cnt[c]; lf += cnt[c] > 0; }
+  const int it = wave_incl_scan(lt), iff = wave_incl_scan(lf);
+  if (lane == 63) { wsum[0][wave] = it; wsum[1][wave] = iff; }
+  __syncthreads();
+  int ot = 0, of = 0, tot_t = 0, tot_f = 0;
+  for (int w = 0; w < 16; ++w) {
+    if (w < wave) { ot += wsum[0][w]; of += wsum[1][w]; }
+    tot_t += wsum[0][w];
+    tot_f += wsum[1][w];
+  }
+  int rt = ot + it - lt, rf = of + iff - lf;  // exclusive prefix of this thread's bins
+  for (int64_t c = c0; c < c1; ++c) {
+    const int t = cnt[c];
+    if (t > 0) {
+      uniq[rf] = (int32_t)c;
+      csr_off[rf] = rt;
+      uid[c] = rf;
+      ++rf;
+    }
+    cnt[c] = rt;
+    rt += t;
+  }
+  if (tid == 0) { n_uniq[0] = tot_f; n_uniq[1] = (int32_t)(E - tot_t); csr_off[tot_f] = tot_t; }
+  __syncthreads();
+  // stable placement: chapter start + edges of the same chapter earlier in the batch
+  if (tid < E) {
+    const int32_t c = ids[tid];
+    const bool ok = c >= 0 && c < C;
+    edge_u[tid] = ok ? uid[c] : -1;
+    if (ok) {
+      int before = 0;
+      for (int j = 0; j < tid; ++j) before += ids[j] == c;
+      csr_edge[cnt[c] + before] = tid;
+    }
+  }
+}
+
 }  // namespace moc
 
 using namespace moc;
@@ -139,6 +216,11 @@ int moc_chapter_plan(const int32_t* chap, int64_t E, int64_t C, void* workspace,
   MOC_REQUIRE(C > 0 && C <= kPlanMaxC, MOC_ERR_UNSUPPORTED, "moc_chapter_plan: C=%lld not in [1, %d]", (long long)C,
               kPlanMaxC);
   MOC_REQUIRE(workspace_bytes >= moc_chapter_plan_workspace(E, C), MOC_ERR_ARG, "moc_chapter_plan: workspace too small");
+  if (E <= kPlanSmallE && C <= kPlanSmallC) {
+    hipLaunchKernelGGL(plan_small_kernel, dim3(1), dim3(1024), 2 * (size_t)C * sizeof(int32_t), stream, chap, E, C,
+                       uniq, n_uniq, edge_u, csr_off, csr_edge);
+    return check_launch("plan_small_kernel");
+  }
   const int G = (int)((E + kPlanEdgesPerBlock - 1) / kPlanEdgesPerBlock);
   int32_t* counts = (int32_t*)workspace;
   int32_t* total = counts + (int64_t)G * C;

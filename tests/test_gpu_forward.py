@@ -113,7 +113,8 @@ def test_router_pool_and_linear(dev, B, Lq, d, C):
 
 # ------------------------------------------------------------------ chapter plan
 
-@pytest.mark.parametrize("B,NS,C", [(8, 65, 4097), (2, 5, 33), (64, 65, 4097), (3, 7, 5), (300, 16, 4096)])
+@pytest.mark.parametrize("B,NS,C", [(8, 65, 4097), (2, 5, 33), (64, 65, 4097), (3, 7, 5), (300, 16, 4096),
+                                    (16, 64, 300), (4, 20, 10000)])
 def test_chapter_plan_matches_numpy(dev, B, NS, C):
     g = np.random.default_rng(B * NS + C)
     chap = np.stack([g.choice(C, size=NS, replace=NS > C) for _ in range(B)]).astype(np.int32)
