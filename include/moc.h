@@ -168,15 +168,19 @@ int moc_dkv_reduce(int dtype, const void* dkv_edge, const int32_t* n_uniq, const
 
 /* Weight gradient of the K/V projection with the chapter gather (and row norm) fused:
  * dw [KV2][d] (out_dtype f32 or bf16) = dkv^T X, X[r] = norm(bank[uniq[r / 64] * 64 + r % 64]),
- * over the plan's n_uniq * 64 rows; dkv [max_u * 64][KV2] bf16 from moc_dkv_reduce.  Replaces the
+ * over the plan's n_uniq * 64 rows; dkv [max_u * 64][KV2] bf16 from moc_dkv_reduce.  With edge_u
+ * (the plan's edge -> distinct chapter map) dkv is instead the per-edge rows of moc_xattn_bwd_dkv
+ * ([E * 64][KV2], max_u = E): edge e's rows pair with the rows of chapter uniq[edge_u[e]], and
+ * skipped edges (edge_u < 0) contribute nothing, so no per-chapter reduction is needed.  Replaces the
  * autograd weight gradient of k_proj / v_proj (memory_transformer/memory_attention.py:241-243)
  * over the gathered rows (memory_transformer/memory_bank.py:263-293).  T must be 64.  The rows
  * are split over several workgroups per output tile; ws (moc_kv_wgrad_workspace bytes) holds
  * their fp32 partials, summed in a fixed order. */
 size_t moc_kv_wgrad_workspace(int64_t KV2, int64_t d, int64_t max_u);
 int moc_kv_wgrad(const void* dkv, const void* bank, int bank_dtype, int64_t d, int T, const int32_t* uniq,
-                 const int32_t* n_uniq, int64_t max_u, const float* row_mean, const float* row_rstd, int64_t KV2,
-                 void* ws, size_t ws_bytes, int out_dtype, void* dw, hipStream_t stream);
+                 const int32_t* n_uniq, const int32_t* edge_u, int64_t max_u, const float* row_mean,
+                 const float* row_rstd, int64_t KV2, void* ws, size_t ws_bytes, int out_dtype, void* dw,
+                 hipStream_t stream);
 /* Same kernel over dense rows: dw [N][K] (out_dtype) = dy^T x with dy [R][N] bf16 and x [R][K]
  * (x_dtype bf16 or f32, rounded to bf16 for the MFMA).  The weight gradient of the memory
  * layer's bias-free q_proj / o_proj (memory_transformer/memory_attention.py:140-143, :241, :456),
@@ -191,12 +195,15 @@ int moc_gather_rows(int dtype, const void* bank, int bank_dtype, int64_t d, int 
                     hipStream_t stream);
 
 /* Backward of the gather (memory_bank.py:287-291, a scatter-add into the bank gradient) through
- * the optional row normalisation: grad_bank[uniq[u]*T + t, :] = norm_bwd(dX[u*T + t, :]).
- * Distinct chapters own distinct rows, so the rows are stored, not added; grad_bank must be
- * zero elsewhere.  dX [max_u * T][d] of dx_dtype, grad_bank of bank_dtype. */
+ * the optional row normalisation: grad_bank[uniq[u]*T + t, :] = norm_bwd(g), g = dX[u*T + t, :]
+ * (dX [max_u * T][d], one row per distinct-chapter row) or, when the plan's csr_off / csr_edge are
+ * given, g = sum over the chapter's edges e (csr order) of dX[e*T + t, :] (dX [E * T][d], one row
+ * per edge row).  Distinct chapters own distinct rows, so the rows are stored, not added;
+ * grad_bank must be zero elsewhere.  dX of dx_dtype, grad_bank of bank_dtype. */
 int moc_bank_scatter(int dx_dtype, const void* dX, const void* bank, int bank_dtype, int64_t d, int T,
-                     const int32_t* uniq, const int32_t* n_uniq, int64_t max_u, const float* row_mean,
-                     const float* row_rstd, int norm, void* grad_bank, hipStream_t stream);
+                     const int32_t* uniq, const int32_t* n_uniq, int64_t max_u, const int32_t* csr_off,
+                     const int32_t* csr_edge, const float* row_mean, const float* row_rstd, int norm,
+                     void* grad_bank, hipStream_t stream);
 
 /* -------------------------------------------- token-routed sparse attention */
 

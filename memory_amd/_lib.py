@@ -52,7 +52,7 @@ _SIGS = {
     "moc_xattn_bwd_dkv": (_I, [_I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I, _I, _I, _I, _I, _F,
                                _P, _P, _P]),
     "moc_kv_wgrad_workspace": (_SZ, [_I64, _I64, _I64]),
-    "moc_kv_wgrad": (_I, [_P, _P, _I, _I64, _I, _P, _P, _I64, _P, _P, _I64, _P, _SZ, _I, _P, _P]),
+    "moc_kv_wgrad": (_I, [_P, _P, _I, _I64, _I, _P, _P, _P, _I64, _P, _P, _I64, _P, _SZ, _I, _P, _P]),
     "moc_linear_wgrad_workspace": (_SZ, [_I64, _I64, _I64]),
     "moc_linear_wgrad": (_I, [_P, _P, _I, _I64, _I64, _I64, _P, _SZ, _I, _P, _P]),
     "moc_dkv_reduce": (_I, [_I, _P, _P, _P, _P, _I64, _I64, _P, _P]),
@@ -66,7 +66,7 @@ _SIGS = {
     "moc_sparse_dw": (_I, [_P, _P, _P, _I, _I, _I64, _P, _P]),
     "moc_decode_partial": (_I, [_I, _P, _I64, _I, _P, _P, _I, _I, _I, _P, _P, _P, _P, _I64, _P, _I, _F, _P, _P, _P]),
     "moc_gather_rows": (_I, [_I, _P, _I, _I64, _I, _P, _P, _I64, _P, _P, _P, _P]),
-    "moc_bank_scatter": (_I, [_I, _P, _P, _I, _I64, _I, _P, _P, _I64, _P, _P, _I, _P, _P]),
+    "moc_bank_scatter": (_I, [_I, _P, _P, _I, _I64, _I, _P, _P, _I64, _P, _P, _P, _P, _I, _P, _P]),
 }
 
 _lib = None

@@ -54,7 +54,8 @@ __device__ __forceinline__ bf16x8 tr_frag(const char* base, int rb, int cb, int 
 template <typename TB, bool kNorm, bool kGather>
 __global__ __launch_bounds__(kWgThreads) void kv_wgrad_kernel(
     const bf16* __restrict__ dkv, int KV2, const TB* __restrict__ bank, int64_t d, const int32_t* __restrict__ uniq,
-    const int32_t* __restrict__ n_uniq, int64_t max_u, int64_t R, const float* __restrict__ row_mean,
+    const int32_t* __restrict__ n_uniq, const int32_t* __restrict__ edge_u, int64_t max_u, int64_t R,
+    const float* __restrict__ row_mean,
     const float* __restrict__ row_rstd, int n_ktile, int n_tiles, int splits, float* __restrict__ ws) {
   constexpr int STAGE = 64 * 512;
   constexpr bool kConv = kNorm || !std::is_same<TB, bf16>::value;
@@ -70,8 +71,9 @@ __global__ __launch_bounds__(kWgThreads) void kv_wgrad_kernel(
   const int wn = wave >> 2, wk = wave & 3;  // wave tile: 128 (n) x 64 (k)
   const int g = lane >> 4, c16 = lane & 15;
 
-  // one 64-row stage per chapter (gather) or per 64 rows (dense)
-  const int64_t nstage = kGather ? (int64_t)min((int64_t)n_uniq[0], max_u) : (R + 63) / 64;
+  // one 64-row stage per distinct chapter (gather), per edge (gather with edge_u: dkv rows are
+  // per edge, e -> distinct chapter edge_u[e], skipped edges read as zero) or per 64 rows (dense)
+  const int64_t nstage = !kGather ? (R + 63) / 64 : edge_u ? max_u : (int64_t)min((int64_t)n_uniq[0], max_u);
   const int64_t per = (nstage + splits - 1) / splits;
   const int64_t s0 = min(nstage, (int64_t)split * per), s1 = min(nstage, s0 + per);
 
@@ -91,20 +93,22 @@ __global__ __launch_bounds__(kWgThreads) void kv_wgrad_kernel(
   V16 ra[4], rb[4][NV];
   float mu[4], rs[4];
   auto fetch = [&](int64_t st) {
-    const int64_t xbase = kGather ? (int64_t)uniq[st] * 64 : st * 64;  // first X row of the stage
+    // distinct chapter of the stage (-1: a skipped edge) and its first X row
+    const int64_t u = !kGather ? 0 : edge_u ? (int64_t)edge_u[st] : st;
+    const int64_t xbase = !kGather ? st * 64 : u >= 0 ? (int64_t)uniq[u] * 64 : 0;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int q = tid + kWgThreads * i;
       const int row = q >> 5, cc = (q & 31) * 8;
-      const bool live = kGather || st * 64 + row < R;
+      const bool live = kGather ? u >= 0 : st * 64 + row < R;
       ra[i] = a_ok[i] && live ? ld16(a_src[i] + st * 64 * KV2) : V16{{0u, 0u, 0u, 0u}};
       const TB* xp = bank + (xbase + row) * d + (b_ok[i] ? k0 + cc : 0);
 #pragma unroll
       for (int x = 0; x < NV; ++x)
         rb[i][x] = b_ok[i] && live ? ld16(xp + x * (16 / (int)sizeof(TB))) : V16{{0u, 0u, 0u, 0u}};
       if constexpr (kNorm) {
-        mu[i] = row_mean[st * 64 + row];
-        rs[i] = row_rstd[st * 64 + row];
+        mu[i] = live ? row_mean[u * 64 + row] : 0.f;
+        rs[i] = live ? row_rstd[u * 64 + row] : 0.f;
       }
     }
   };
@@ -206,7 +210,8 @@ int wgrad_splits(int tiles, int64_t max_stages) {
 
 template <bool kGather>
 int launch_wgrad(const void* dkv, const void* bank, int bank_dtype, int64_t d, const int32_t* uniq,
-                 const int32_t* n_uniq, int64_t max_u, int64_t R, const float* row_mean, const float* row_rstd,
+                 const int32_t* n_uniq, const int32_t* edge_u, int64_t max_u, int64_t R, const float* row_mean,
+                 const float* row_rstd,
                  int64_t KV2, int64_t max_stages, void* ws, int out_dtype, void* dw, hipStream_t stream) {
   int nk;
   const int tiles = wgrad_tiles(KV2, d, &nk);
@@ -216,8 +221,8 @@ int launch_wgrad(const void* dkv, const void* bank, int bank_dtype, int64_t d, c
   const bool norm = row_rstd != nullptr;
 #define MOC_WG(TB, NORM)                                                                                        \
   hipLaunchKernelGGL((kv_wgrad_kernel<TB, NORM, kGather>), grid, dim3(kWgThreads), 0, stream, (const bf16*)dkv, \
-                     (int)KV2, (const TB*)bank, d, uniq, n_uniq, max_u, R, row_mean, row_rstd, nk, tiles, splits, \
-                     (float*)ws)
+                     (int)KV2, (const TB*)bank, d, uniq, n_uniq, edge_u, max_u, R, row_mean, row_rstd, nk, tiles,    \
+                     splits, (float*)ws)
   if (bank_dtype == MOC_BF16) {
     if (norm) MOC_WG(bf16, true); else MOC_WG(bf16, false);
   } else if (bank_dtype == MOC_F32) {
@@ -251,8 +256,9 @@ size_t moc_kv_wgrad_workspace(int64_t KV2, int64_t d, int64_t max_u) {
 }
 
 int moc_kv_wgrad(const void* dkv, const void* bank, int bank_dtype, int64_t d, int T, const int32_t* uniq,
-                 const int32_t* n_uniq, int64_t max_u, const float* row_mean, const float* row_rstd, int64_t KV2,
-                 void* ws, size_t ws_bytes, int out_dtype, void* dw, hipStream_t stream) {
+                 const int32_t* n_uniq, const int32_t* edge_u, int64_t max_u, const float* row_mean,
+                 const float* row_rstd, int64_t KV2, void* ws, size_t ws_bytes, int out_dtype, void* dw,
+                 hipStream_t stream) {
   MOC_REQUIRE(dkv && bank && uniq && n_uniq && ws && dw, MOC_ERR_ARG, "moc_kv_wgrad: null pointer");
   MOC_REQUIRE((row_mean == nullptr) == (row_rstd == nullptr), MOC_ERR_ARG,
               "moc_kv_wgrad: mean/rstd must be both set or both null");
@@ -260,8 +266,8 @@ int moc_kv_wgrad(const void* dkv, const void* bank, int bank_dtype, int64_t d, i
   MOC_REQUIRE(d > 0 && d % 8 == 0 && KV2 > 0 && KV2 % 8 == 0 && KV2 < (1 << 30) && max_u >= 0, MOC_ERR_UNSUPPORTED,
               "moc_kv_wgrad: d=%lld KV2=%lld must be multiples of 8", (long long)d, (long long)KV2);
   MOC_REQUIRE(ws_bytes >= moc_kv_wgrad_workspace(KV2, d, max_u), MOC_ERR_ARG, "moc_kv_wgrad: workspace too small");
-  return launch_wgrad<true>(dkv, bank, bank_dtype, d, uniq, n_uniq, max_u, 0, row_mean, row_rstd, KV2, max_u, ws,
-                            out_dtype, dw, stream);
+  return launch_wgrad<true>(dkv, bank, bank_dtype, d, uniq, n_uniq, edge_u, max_u, 0, row_mean, row_rstd, KV2, max_u,
+                            ws, out_dtype, dw, stream);
 }
 
 size_t moc_linear_wgrad_workspace(int64_t R, int64_t N, int64_t K) {
@@ -276,8 +282,8 @@ int moc_linear_wgrad(const void* dy, const void* x, int x_dtype, int64_t R, int6
   MOC_REQUIRE(R >= 0 && N > 0 && N % 8 == 0 && N < (1 << 30) && K > 0 && K % 8 == 0, MOC_ERR_UNSUPPORTED,
               "moc_linear_wgrad: N=%lld K=%lld must be multiples of 8", (long long)N, (long long)K);
   MOC_REQUIRE(ws_bytes >= moc_linear_wgrad_workspace(R, N, K), MOC_ERR_ARG, "moc_linear_wgrad: workspace too small");
-  return launch_wgrad<false>(dy, x, x_dtype, K, nullptr, nullptr, 0, R, nullptr, nullptr, N, (R + 63) / 64, ws,
-                             out_dtype, dw, stream);
+  return launch_wgrad<false>(dy, x, x_dtype, K, nullptr, nullptr, nullptr, 0, R, nullptr, nullptr, N, (R + 63) / 64,
+                             ws, out_dtype, dw, stream);
 }
 
 }  // extern "C"

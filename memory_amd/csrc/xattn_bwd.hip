@@ -594,26 +594,46 @@ __global__ __launch_bounds__(256) void gather_rows_kernel(const TB* __restrict__
   }
 }
 
-// grad_bank[src(r), :] = norm_bwd(dX[r, :]) for r < n_uniq * T.  Distinct
-// chapters own distinct bank rows, so plain stores suffice (grad_bank must be
-// zero-initialised by the caller for rows that are not selected).
+// grad_bank[src(r), :] = norm_bwd(g_r) for r < n_uniq * T, where g_r is dX[r, :] (one dX row
+// per distinct-chapter row) or, given the plan's inverted index, the sum over the chapter's
+// edges (csr order, deterministic) of the per-edge rows dX[e * T + t, :].  Distinct chapters
+// own distinct bank rows, so plain stores suffice (grad_bank must be zero-initialised by the
+// caller for rows that are not selected).
 template <typename TX, typename TB, typename TG>
 __global__ __launch_bounds__(256) void bank_scatter_kernel(const TX* __restrict__ dX, const TB* __restrict__ bank,
                                                            int64_t d, int Tc, const int32_t* __restrict__ uniq,
                                                            const int32_t* __restrict__ n_uniq, int64_t rows,
+                                                           const int32_t* __restrict__ csr_off,
+                                                           const int32_t* __restrict__ csr_edge,
                                                            const float* __restrict__ mean,
                                                            const float* __restrict__ rstd, int layernorm,
                                                            TG* __restrict__ grad) {
   const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (r >= rows || r >= (int64_t)n_uniq[0] * Tc) return;
-  const int64_t src = (int64_t)uniq[r / Tc] * Tc + r % Tc;
-  const TX* gr = dX + r * d;
+  const int64_t u = r / Tc, t = r % Tc;
+  const int64_t src = (int64_t)uniq[u] * Tc + t;
+  const int p0 = csr_off ? csr_off[u] : 0, p1 = csr_off ? csr_off[u + 1] : 0;
+  // gradient w.r.t. the gathered row, 8 columns starting at j
+  auto grow = [&](int64_t j, float* gv) {
+    if (!csr_off) {
+      load8f<TG, TX>(dX + r * d + j, gv);
+      return;
+    }
+#pragma unroll
+    for (int x = 0; x < 8; ++x) gv[x] = 0.f;
+    for (int p = p0; p < p1; ++p) {
+      float e8[8];
+      load8f<TG, TX>(dX + ((int64_t)csr_edge[p] * Tc + t) * d + j, e8);
+#pragma unroll
+      for (int x = 0; x < 8; ++x) gv[x] += e8[x];
+    }
+  };
   TG* o = grad + src * d;
   float gv[8];
   if (!rstd) {
     for (int64_t j = 8 * lane; j < d; j += 512) {
-      load8f<TG, TX>(gr + j, gv);
+      grow(j, gv);
       store8f<TG>(o + j, gv);
     }
     return;
@@ -622,7 +642,7 @@ __global__ __launch_bounds__(256) void bank_scatter_kernel(const TX* __restrict_
   const float mu = mean[r], rs = rstd[r];
   float sg = 0.f, sgx = 0.f, xv[8];
   for (int64_t j = 8 * lane; j < d; j += 512) {
-    load8f<TG, TX>(gr + j, gv);
+    grow(j, gv);
     load8f<TG, TB>(xr + j, xv);
 #pragma unroll
     for (int x = 0; x < 8; ++x) {
@@ -633,7 +653,7 @@ __global__ __launch_bounds__(256) void bank_scatter_kernel(const TX* __restrict_
   sg = wave_sum(sg) / (float)d;
   sgx = wave_sum(sgx) / (float)d;
   for (int64_t j = 8 * lane; j < d; j += 512) {
-    load8f<TG, TX>(gr + j, gv);
+    grow(j, gv);
     load8f<TG, TB>(xr + j, xv);
 #pragma unroll
     for (int x = 0; x < 8; ++x) gv[x] = rs * (gv[x] - (layernorm ? sg : 0.f) - (xv[x] - mu) * rs * sgx);
@@ -763,9 +783,12 @@ int moc_gather_rows(int dtype, const void* bank, int bank_dtype, int64_t d, int 
 }
 
 int moc_bank_scatter(int dx_dtype, const void* dX, const void* bank, int bank_dtype, int64_t d, int T,
-                     const int32_t* uniq, const int32_t* n_uniq, int64_t max_u, const float* row_mean,
-                     const float* row_rstd, int norm, void* grad_bank, hipStream_t stream) {
+                     const int32_t* uniq, const int32_t* n_uniq, int64_t max_u, const int32_t* csr_off,
+                     const int32_t* csr_edge, const float* row_mean, const float* row_rstd, int norm,
+                     void* grad_bank, hipStream_t stream) {
   MOC_REQUIRE(dX && bank && uniq && n_uniq && grad_bank, MOC_ERR_ARG, "moc_bank_scatter: null pointer");
+  MOC_REQUIRE((csr_off == nullptr) == (csr_edge == nullptr), MOC_ERR_ARG,
+              "moc_bank_scatter: csr_off / csr_edge must be both set or both null");
   MOC_REQUIRE(d % 8 == 0, MOC_ERR_UNSUPPORTED, "moc_bank_scatter: d=%lld must be a multiple of 8", (long long)d);
   MOC_REQUIRE((norm == MOC_NORM_NONE) == (row_rstd == nullptr), MOC_ERR_ARG, "moc_bank_scatter: norm/stats mismatch");
   const int64_t rows = max_u * T;
@@ -774,7 +797,7 @@ int moc_bank_scatter(int dx_dtype, const void* dX, const void* bank, int bank_dt
   const int ln = norm == MOC_NORM_LAYERNORM;
 #define BS(TX, BT)                                                                                                     \
   hipLaunchKernelGGL((bank_scatter_kernel<TX, BT, BT>), grid, dim3(256), 0, stream, (const TX*)dX, (const BT*)bank, d, \
-                     T, uniq, n_uniq, rows, row_mean, row_rstd, ln, (BT*)grad_bank)
+                     T, uniq, n_uniq, rows, csr_off, csr_edge, row_mean, row_rstd, ln, (BT*)grad_bank)
   if (dx_dtype == MOC_BF16 && bank_dtype == MOC_BF16) BS(bf16, bf16);
   else if (dx_dtype == MOC_BF16 && bank_dtype == MOC_F32) BS(bf16, float);
   else if (dx_dtype == MOC_F32 && bank_dtype == MOC_F32) BS(float, float);

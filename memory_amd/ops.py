@@ -336,34 +336,47 @@ class _RoutedAttention(torch.autograd.Function):
         dom_part = torch.zeros(B * NS, HK, device=dev, dtype=torch.float32)
         call("moc_xattn_bwd_dkv", dt, ptr(q), ptr(qt), ptr(dout), ptr(dot), ptr(kt), ptr(vt), ptr(edge_u), ptr(om),
              ptr(lse), ptr(delta), B, Lq, H, HK, Dh, T, NS, scale, ptr(dkv_edge), ptr(dom_part), st)
-        dkv = torch.empty(max_u * T, 2 * KV, device=dev, dtype=dtype)
-        call("moc_dkv_reduce", dt, ptr(dkv_edge), ptr(n_uniq), ptr(csr_off), ptr(csr_edge), max_u, 2 * KV, ptr(dkv),
-             st)
         domega = dom_part.sum(-1).view(B, NS)
         need_bank, need_wk, need_wv = ctx.needs_input_grad[1:4]
         dbank = dwk = dwv = None
-        if need_wk or need_wv:
-            if dtype == torch.bfloat16:
-                # split-row weight-gradient kernel with the gather fused in
-                ws = torch.empty(L.query("moc_kv_wgrad_workspace", 2 * KV, d, max_u) // 4, device=dev,
+        E = B * NS
+        if dtype == torch.bfloat16:
+            # per-edge dK/dV rows feed both products directly: the weight gradient pairs edge e's
+            # rows with its chapter's bank rows, and the bank scatter sums dX over each chapter's
+            # edges (csr order), so no per-chapter reduction pass is needed
+            if need_wk or need_wv:
+                ws = torch.empty(L.query("moc_kv_wgrad_workspace", 2 * KV, d, E) // 4, device=dev,
                                  dtype=torch.float32)
                 out_dt = torch.float32 if torch.float32 in (wk_dtype, wv_dtype) else dtype
                 dwkv = torch.empty(2 * KV, d, device=dev, dtype=out_dt)
-                call("moc_kv_wgrad", ptr(dkv), ptr(bank), L.dtype_code(bank.dtype), d, T, ptr(uniq), ptr(n_uniq),
-                     max_u, ptr(mean), ptr(rstd), 2 * KV, ptr(ws), ws.numel() * 4, L.dtype_code(out_dt), ptr(dwkv),
-                     st)
-            else:
-                X = torch.empty(max_u * T, d, device=dev, dtype=dtype)
-                call("moc_gather_rows", dt, ptr(bank), L.dtype_code(bank.dtype), d, T, ptr(uniq), ptr(n_uniq),
-                     max_u, ptr(mean), ptr(rstd), ptr(X), st)
-                dwkv = torch.matmul(dkv.t(), X)
+                call("moc_kv_wgrad", ptr(dkv_edge), ptr(bank), L.dtype_code(bank.dtype), d, T, ptr(uniq),
+                     ptr(n_uniq), ptr(edge_u), E, ptr(mean), ptr(rstd), 2 * KV, ptr(ws), ws.numel() * 4,
+                     L.dtype_code(out_dt), ptr(dwkv), st)
+                dwk = dwkv[:KV].to(wk_dtype) if need_wk else None
+                dwv = dwkv[KV:].to(wv_dtype) if need_wv else None
+            if need_bank:
+                dX = torch.matmul(dkv_edge, wkv)  # rows of skipped edges are never read
+                dbank = torch.zeros(bank.shape, device=dev, dtype=bank_dtype)
+                call("moc_bank_scatter", L.dtype_code(dX.dtype), ptr(dX), ptr(bank), L.dtype_code(bank.dtype), d,
+                     T, ptr(uniq), ptr(n_uniq), max_u, ptr(csr_off), ptr(csr_edge), ptr(mean), ptr(rstd), norm,
+                     ptr(dbank), st)
+            return dq, dbank, dwk, dwv, domega, None, None, None, None, None, None
+        # fp32: sum per distinct chapter first, then library GEMMs
+        dkv = torch.empty(max_u * T, 2 * KV, device=dev, dtype=dtype)
+        call("moc_dkv_reduce", dt, ptr(dkv_edge), ptr(n_uniq), ptr(csr_off), ptr(csr_edge), max_u, 2 * KV, ptr(dkv),
+             st)
+        if need_wk or need_wv:
+            X = torch.empty(max_u * T, d, device=dev, dtype=dtype)
+            call("moc_gather_rows", dt, ptr(bank), L.dtype_code(bank.dtype), d, T, ptr(uniq), ptr(n_uniq),
+                 max_u, ptr(mean), ptr(rstd), ptr(X), st)
+            dwkv = torch.matmul(dkv.t(), X)
             dwk = dwkv[:KV].to(wk_dtype) if need_wk else None
             dwv = dwkv[KV:].to(wv_dtype) if need_wv else None
         if need_bank:
             dX = torch.matmul(dkv, wkv)
             dbank = torch.zeros(bank.shape, device=dev, dtype=bank_dtype)
             call("moc_bank_scatter", L.dtype_code(dX.dtype), ptr(dX), ptr(bank), L.dtype_code(bank.dtype), d, T,
-                 ptr(uniq), ptr(n_uniq), max_u, ptr(mean), ptr(rstd), norm, ptr(dbank), st)
+                 ptr(uniq), ptr(n_uniq), max_u, None, None, ptr(mean), ptr(rstd), norm, ptr(dbank), st)
         return dq, dbank, dwk, dwv, domega, None, None, None, None, None, None
 
 

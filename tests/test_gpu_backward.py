@@ -121,7 +121,7 @@ def test_kv_weight_grad_kernel(gpu_device, d, HK, C, nsel, bank_dtype, norm, out
     dw = torch.full((KV2, d), float("nan"), device=dev, dtype=out_dtype)
     dkv_d = dkv.to(dev)  # kept alive until the kernel has run
     L.call("moc_kv_wgrad", L.ptr(dkv_d), L.ptr(bg), L.dtype_code(bank_dtype), d, T, L.ptr(plan.uniq),
-           L.ptr(plan.n_uniq), max_u, L.ptr(mean), L.ptr(rstd), KV2, L.ptr(ws), ws.numel() * 4,
+           L.ptr(plan.n_uniq), None, max_u, L.ptr(mean), L.ptr(rstd), KV2, L.ptr(ws), ws.numel() * 4,
            L.dtype_code(out_dtype), L.ptr(dw), L.stream_ptr(dev))
     uniq = plan.uniq[:n_u].cpu().long()
     X, _ = O.gather_chapters(bg.cpu().double(), uniq.view(1, -1), T)
@@ -176,3 +176,43 @@ def test_linear_autograd_matches_reference(gpu_device):
     assert_rel(y, (x.double() @ w.double().T), 2e-2, "y")
     assert_rel(xg.grad, xd.grad, 2e-2, "dx")
     assert_rel(wg.grad, wd.grad, 2e-2, "dW")
+
+
+@pytest.mark.parametrize("bank_dtype,norm", [(torch.bfloat16, None), (torch.bfloat16, "rms")])
+def test_kv_weight_grad_per_edge(gpu_device, bank_dtype, norm):
+    """Per-edge mode: dkv rows per (sequence, slot) edge, chapters repeated across sequences and one
+    skipped edge (out-of-range id) whose rows hold NaN and must not be read."""
+    from memory_amd import _lib as L
+    from memory_amd import ops
+    dev = gpu_device
+    T, d, HK, C = 64, 256, 2, 30
+    KV2 = 2 * HK * 64
+    g = gen(515)
+    bank = torch.randn(C * T, d, generator=g)
+    chap = torch.randint(0, 12, (3, 5), generator=g).to(torch.int32)  # duplicates across rows
+    chap[1, 2] = C + 7                                                 # skipped edge
+    E = chap.numel()
+    plan = ops.chapter_plan(chap.to(dev), C)
+    bg = bank.to(dev, bank_dtype)
+    code = ops.norm_code(norm)
+    mean = rstd = None
+    if code:
+        mean, rstd = ops.row_stats(bg, plan, T, code, 1e-5)
+    dkv = torch.randn(E * T, KV2, generator=g).to(torch.bfloat16)
+    dkv.view(E, T, KV2)[7] = float("nan")  # edge 7 = (1, 2), the skipped one
+    dkv_d = dkv.to(dev)
+    ws = torch.empty(L.query("moc_kv_wgrad_workspace", KV2, d, E) // 4, device=dev, dtype=torch.float32)
+    dw = torch.empty(KV2, d, device=dev, dtype=torch.float32)
+    L.call("moc_kv_wgrad", L.ptr(dkv_d), L.ptr(bg), L.dtype_code(bank_dtype), d, T, L.ptr(plan.uniq),
+           L.ptr(plan.n_uniq), L.ptr(plan.edge_u), E, L.ptr(mean), L.ptr(rstd), KV2, L.ptr(ws), ws.numel() * 4,
+           L.dtype_code(torch.float32), L.ptr(dw), L.stream_ptr(dev))
+    ref = torch.zeros(KV2, d, dtype=torch.float64)
+    for e, c in enumerate(chap.reshape(-1).tolist()):
+        if not 0 <= c < C:
+            continue
+        X = bg.cpu().double()[c * T:(c + 1) * T]
+        if norm == "rms":
+            X = O.rms_norm(X, 1e-5)
+        ref += dkv.view(E, T, KV2)[e].double().T @ X.to(torch.bfloat16).double()
+    assert torch.isfinite(dw).all()
+    assert_rel(dw, ref, 2e-2, "dW per edge")
