@@ -116,8 +116,10 @@ int moc_row_stats(const void* bank, int bank_dtype, int64_t d, int T, const int3
  * computed once per distinct chapter.  bank [N_m, d] (bf16 or f32), wkv [2*HK*Dh, d] of dtype
  * (= [Wk; Wv]); row_mean/row_rstd from moc_row_stats or both NULL.  Outputs (each may be NULL,
  * but K and V each need one form): chapter-head tiles k_tiles, v_tiles [max_u][HK][T][Dh] and
- * their transposes kt_tiles, vt_tiles [max_u][HK][Dh][T], of dtype.  d % 64 == 0,
- * (2*HK*Dh) % 128 == 0. */
+ * their transposes kt_tiles, vt_tiles [max_u][HK][Dh][T], of dtype.  The key axis of the
+ * transposed tiles is stored in MFMA key order: within each 32-key group, key 4g + e sits at
+ * position 8g + e and key 16 + 4g + e at 8g + 4 + e (g, e < 4).  d % 64 == 0,
+ * (2*HK*Dh) % 128 == 0, T % 32 == 0 when a transposed output is requested. */
 int moc_kv_project(int dtype, const void* bank, int bank_dtype, int64_t d, int T, const int32_t* uniq,
                    const int32_t* n_uniq, int64_t max_u, const float* row_mean, const float* row_rstd,
                    const void* wkv, int HK, int Dh, void* k_tiles, void* v_tiles, void* kt_tiles, void* vt_tiles,

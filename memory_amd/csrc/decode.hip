@@ -9,7 +9,8 @@
 // (sequence, slot) edges).
 //
 // decode_partial_kernel: one wave per (distinct chapter u, kv head hk).  Lane j
-// holds key row j of the K tile and lane d value column d (row d of the V^T tile).
+// holds key row j of the K tile and lane d value column d (row d of the V^T tile,
+// whose key axis is in MFMA key order).
 // For every edge (b, slot) of u and every query head hq of hk:
 //   s_j = omega * scale * q . k_j  ->  lse (log2), o_d = omega * sum_j p_j v_jd / sum_j p_j
 // written as partials; moc_sparse_combine (joint mode) merges the slots of a sequence.
@@ -75,7 +76,9 @@ __global__ __launch_bounds__(64 * kDecWaves) void decode_partial_kernel(
       const float l = wave_sum(pj);
       float o = 0.f;
 #pragma unroll
-      for (int j = 0; j < 64; ++j) o += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pj), j)) * vc[j];
+      // vc[j] is V^T at position j of the MFMA key order, i.e. key mfma_pos_key(j)
+      for (int j = 0; j < 64; ++j)
+        o += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pj), mfma_pos_key(j))) * vc[j];
       const size_t row = (size_t)e * H + hq;
       o_part[row * 64 + lane] = o * (w / l);
       if (lane == 0) lse_part[row] = m + log2f(l);

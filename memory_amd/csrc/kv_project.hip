@@ -233,9 +233,9 @@ __global__ __launch_bounds__(kGemmThreads) void kv_project_kernel(
           if (dst) dst[((u * HK + hk) * Tc + jj) * Dh + dh] = vals[e];
         }
       }
-      if (dst_t && r0 < nrows) {  // Tc % 4 == 0 and nrows % Tc == 0: the 4 rows share a chapter
+      if (dst_t && r0 < nrows) {  // Tc % 32 == 0: the 4 rows share a chapter and stay adjacent in key order
         const int64_t u = r0 / Tc, jj = r0 % Tc;
-        T* p = dst_t + ((u * HK + hk) * Dh + dh) * Tc + jj;
+        T* p = dst_t + ((u * HK + hk) * Dh + dh) * Tc + mfma_key_pos((int)jj);
         if constexpr (sizeof(T) == 2) {
           *reinterpret_cast<bf16x4*>(p) = bf16x4{vals[0], vals[1], vals[2], vals[3]};
         } else {
@@ -388,7 +388,7 @@ __global__ __launch_bounds__(kWideThreads) void kv_project_wide_kernel(
 #pragma unroll
           for (int e = 0; e < 4; ++e) *reinterpret_cast<bf16*>(R + Tile::off(tt + e, dh)) = v4[e];
         }
-        if (dst_t) *reinterpret_cast<bf16x4*>(Rt + Tile::off(dh, tt)) = v4;
+        if (dst_t) *reinterpret_cast<bf16x4*>(Rt + Tile::off(dh, mfma_key_pos(tt))) = v4;  // 4 keys stay adjacent
       }
     }
     __builtin_amdgcn_wave_barrier();
@@ -436,8 +436,8 @@ int moc_kv_project(int dtype, const void* bank, int bank_dtype, int64_t d, int T
               "moc_kv_project: null pointer");
   MOC_REQUIRE((row_mean == nullptr) == (row_rstd == nullptr), MOC_ERR_ARG, "moc_kv_project: mean/rstd must be both set or both null");
   MOC_REQUIRE(T > 0 && HK > 0 && Dh > 0 && max_u >= 0, MOC_ERR_ARG, "moc_kv_project: bad shape");
-  MOC_REQUIRE((kt_tiles == nullptr && vt_tiles == nullptr) || T % 4 == 0, MOC_ERR_ARG,
-              "moc_kv_project: transposed tiles need T %% 4 == 0");
+  MOC_REQUIRE((kt_tiles == nullptr && vt_tiles == nullptr) || T % 32 == 0, MOC_ERR_ARG,
+              "moc_kv_project: transposed tiles need T %% 32 == 0");
   const int BK = dtype == MOC_BF16 ? 64 : 32;
   MOC_REQUIRE(d % 64 == 0 && d >= BK, MOC_ERR_UNSUPPORTED, "moc_kv_project: memory_dim %lld must be a multiple of 64",
               (long long)d);

@@ -167,6 +167,18 @@ __device__ __forceinline__ int64_t xcd_tile(int64_t n_tiles) {
 }
 inline unsigned xcd_grid(int64_t n_tiles) { return (unsigned)((n_tiles + 7) / 8 * 8); }
 
+// MFMA key order of transposed tiles.  The P^T / dS^T fragments that feed the PV-type
+// products (16x16x32) hold, in lane group g, keys 4g..4g+3 and 16+4g..16+4g+3 of each
+// 32-key group.  Transposed tiles (K^T, V^T, Q^T, dO^T) store their key axis in that
+// order -- key 4g + e at position 8g + e, key 16 + 4g + e at 8g + 4 + e -- so every such
+// fragment is one contiguous 16-byte read (Tile::frag at column 32 c + 8 g).
+__host__ __device__ constexpr int mfma_key_pos(int k) {
+  return (k & ~31) | ((k & 31) < 16 ? 8 * ((k & 15) >> 2) + (k & 3) : 8 * ((k & 15) >> 2) + 4 + (k & 3));
+}
+__host__ __device__ constexpr int mfma_pos_key(int p) {
+  return (p & ~31) | (((p & 4) ? 16 : 0) + 4 * ((p & 31) >> 3) + (p & 3));
+}
+
 // s_waitcnt vmcnt(0) (expcnt / lgkmcnt left open), gfx9 encoding
 __device__ __forceinline__ void vm_wait_all() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
@@ -237,9 +249,13 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 // Reduce over the 4 lanes {l, l^16, l^32, l^48} that share a 16x16 column.
+// max without the operand canonicalisation fmaxf needs in IEEE mode (NaN-propagating;
+// three-input forms fuse into v_maximum3_f32)
+__device__ __forceinline__ float fmax_fast(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+
 __device__ __forceinline__ float quad_max(float v) {
-  v = fmaxf(v, __shfl_xor(v, 16, 64));
-  v = fmaxf(v, __shfl_xor(v, 32, 64));
+  v = fmax_fast(v, __shfl_xor(v, 16, 64));
+  v = fmax_fast(v, __shfl_xor(v, 32, 64));
   return v;
 }
 __device__ __forceinline__ float quad_sum(float v) {

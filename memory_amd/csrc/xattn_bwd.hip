@@ -70,8 +70,9 @@ __global__ __launch_bounds__(256) void xattn_bwd_prep_kernel(const T* __restrict
   const size_t base = ((size_t)b * H + h) * kBDh;
   for (int i = tid; i < 64 * 64; i += 256) {
     const int dd = i >> 6, qq = i & 63;
-    qt[(base + dd) * Lp + q0 + qq] = tq[qq][dd];
-    dot[(base + dd) * Lp + q0 + qq] = td[qq][dd];
+    // query axis in MFMA key order within each 32-query group (the dK/dV operands)
+    qt[(base + dd) * Lp + q0 + mfma_key_pos(qq)] = tq[qq][dd];
+    dot[(base + dd) * Lp + q0 + mfma_key_pos(qq)] = td[qq][dd];
   }
 }
 
@@ -191,7 +192,7 @@ __global__ __launch_bounds__(kBThreads) void xattn_bwd_dq_kernel(
       for (int ks2 = 0; ks2 < 2; ++ks2)
 #pragma unroll
         for (int db = 0; db < 4; ++db) {
-          F8 bk = Tile::frag44(sKtc, 16 * db + c16, 32 * ks2 + 4 * g, 32 * ks2 + 16 + 4 * g);
+          F8 bk = Tile::frag(sKtc, 16 * db + c16, 32 * ks2 + 8 * g);  // K^T tiles are in MFMA key order
 #pragma unroll
           for (int qb = 0; qb < 2; ++qb) mma(acc[qb][db], dsf[qb][ks2], bk);
         }
@@ -436,8 +437,9 @@ __global__ __launch_bounds__(64 * DkvCfg<T>::SG, 1) void xattn_bwd_dkv_kernel(
           }
 #pragma unroll
           for (int db = 0; db < 4; ++db) {
-            F8 bq = TileT::frag44(sQt, 16 * db + c16, qb0 + 4 * g, qb0 + 16 + 4 * g);
-            F8 bd = TileT::frag44(sDt, 16 * db + c16, qb0 + 4 * g, qb0 + 16 + 4 * g);
+            // Q^T / dO^T are stored with their query axis in MFMA key order
+            F8 bq = TileT::frag(sQt, 16 * db + c16, qb0 + 8 * g);
+            F8 bd = TileT::frag(sDt, 16 * db + c16, qb0 + 8 * g);
 #pragma unroll
             for (int kb = 0; kb < 4; ++kb) {
               mma(dv[kb][db], pa[kb], bd);

@@ -14,10 +14,11 @@
 // Work decomposition (Dh = T = 64): one workgroup = 128 queries of one
 // (sequence, head); 4 waves x 32 queries.  Every chapter is one 64-key tile,
 // so omega is a scalar per tile and folds into the exp2 argument.  Each wave
-// computes S^T = K Q^T (lane = one query, 16 keys), keeps the running max and
-// a lane-partial row sum, and accumulates O^T = V^T P^T, whose accumulator
-// layout is again "lane = one query", so the online-softmax rescale needs no
-// data movement.  K and V^T tiles are double-buffered in LDS.
+// computes S^T = K Q^T (lane = one query, 16 keys), keeps the running max,
+// accumulates O^T = V^T P^T, whose accumulator layout is again "lane = one
+// query", so the online-softmax rescale needs no data movement, and takes the
+// row sums from an MFMA of an all-ones operand with the same P^T fragments.
+// K and V^T tiles are double-buffered in LDS.
 #include "moc_common.h"
 
 namespace moc {
@@ -70,7 +71,12 @@ __global__ __launch_bounds__(kFwdThreads) void xattn_fwd_kernel(
   }
 
   float m[2] = {-INFINITY, -INFINITY};
-  float lpart[2] = {0.f, 0.f};
+  float lsum[2] = {0.f, 0.f};  // row sums of p (in units of exp2(m)), complete per lane
+  // all-ones A operand: the MFMA with it sums a P~^T fragment over its 32 keys, which
+  // takes the row sums off the VALU (the sums use the same rounded P~ as O)
+  F8 ones;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) ones[j] = from_f<T>(1.f);
   f32x4 o[4][2];
 #pragma unroll
   for (int db = 0; db < 4; ++db)
@@ -129,10 +135,11 @@ __global__ __launch_bounds__(kFwdThreads) void xattn_fwd_kernel(
       bool grow = false;
 #pragma unroll
       for (int qb = 0; qb < 2; ++qb) {
-        float mx = fmaxf(fmaxf(st[0][qb][0], st[0][qb][1]), fmaxf(st[0][qb][2], st[0][qb][3]));
+        float mx = fmax_fast(fmax_fast(st[0][qb][0], st[0][qb][1]), fmax_fast(st[0][qb][2], st[0][qb][3]));
 #pragma unroll
         for (int kb = 1; kb < 4; ++kb)
-          mx = fmaxf(mx, fmaxf(fmaxf(st[kb][qb][0], st[kb][qb][1]), fmaxf(st[kb][qb][2], st[kb][qb][3])));
+          mx = fmax_fast(mx, fmax_fast(fmax_fast(st[kb][qb][0], st[kb][qb][1]),
+                                       fmax_fast(st[kb][qb][2], st[kb][qb][3])));
         cm[qb] = quad_max(mx) * c;  // c >= 0 (router weights are non-negative)
         grow |= cm[qb] > m[qb] + kRescaleSlack;
       }
@@ -142,7 +149,7 @@ __global__ __launch_bounds__(kFwdThreads) void xattn_fwd_kernel(
           const float mn = cm[qb] > m[qb] + kRescaleSlack ? cm[qb] : m[qb];
           const float alpha = fast_exp2(m[qb] - mn);
           m[qb] = mn;
-          lpart[qb] *= alpha;
+          lsum[qb] *= alpha;
 #pragma unroll
           for (int db = 0; db < 4; ++db) o[db][qb] *= alpha;
         }
@@ -155,30 +162,24 @@ __global__ __launch_bounds__(kFwdThreads) void xattn_fwd_kernel(
 #pragma unroll
         for (int qb = 0; qb < 2; ++qb) {
           const float off = m[qb] - lw;
-          float ps = 0.f;
-#pragma unroll
-          for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              const float p = fast_exp2(st[kb][qb][e] * c - off);
-              ps += p;
-              st[kb][qb][e] = p;
-            }
-          lpart[qb] += ps * rw;
 #pragma unroll
           for (int ks2 = 0; ks2 < 2; ++ks2)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-              pf[qb][ks2][e] = from_f<T>(st[2 * ks2][qb][e]);
-              pf[qb][ks2][4 + e] = from_f<T>(st[2 * ks2 + 1][qb][e]);
+              pf[qb][ks2][e] = from_f<T>(fast_exp2(st[2 * ks2][qb][e] * c - off));
+              pf[qb][ks2][4 + e] = from_f<T>(fast_exp2(st[2 * ks2 + 1][qb][e] * c - off));
             }
+          f32x4 ls = f32x4{0.f, 0.f, 0.f, 0.f};
+          mma(ls, ones, pf[qb][0]);
+          mma(ls, ones, pf[qb][1]);
+          lsum[qb] += ls[0] * rw;
         }
         // O^T[db][qb] += V^T(dims 16*db + c16, keys) * P~^T
 #pragma unroll
         for (int ks2 = 0; ks2 < 2; ++ks2) {
 #pragma unroll
           for (int db = 0; db < 4; ++db) {
-            F8 a = Tile::frag44(Vs, 16 * db + c16, 32 * ks2 + 4 * g, 32 * ks2 + 16 + 4 * g);
+            F8 a = Tile::frag(Vs, 16 * db + c16, 32 * ks2 + 8 * g);  // V^T tiles are in MFMA key order
 #pragma unroll
             for (int qb = 0; qb < 2; ++qb) mma(o[db][qb], a, pf[qb][ks2]);
           }
@@ -186,7 +187,7 @@ __global__ __launch_bounds__(kFwdThreads) void xattn_fwd_kernel(
       } else {
         // zero weight: keys and values are zero, every logit is 0 -> only the denominator moves
 #pragma unroll
-        for (int qb = 0; qb < 2; ++qb) lpart[qb] += 16.f * fast_exp2(-m[qb]);
+        for (int qb = 0; qb < 2; ++qb) lsum[qb] += 64.f * fast_exp2(-m[qb]);
       }
     }
     if (u_next >= 0) {
@@ -203,7 +204,7 @@ __global__ __launch_bounds__(kFwdThreads) void xattn_fwd_kernel(
   const int Lp = nqb * 128;
 #pragma unroll
   for (int qb = 0; qb < 2; ++qb) {
-    const float l = quad_sum(lpart[qb]);
+    const float l = lsum[qb];
     const float inv = l > 0.f ? 1.f / l : 0.f;
     const int qi = q0 + 32 * wave + 16 * qb + c16;
     if (qi < L) {

@@ -179,9 +179,13 @@ def test_kv_project_matches_reference(dev, dtype, bank_dtype, norm):
     tol = 1e-4 if dtype == torch.float32 else 2e-2
     assert_rel(kt[:n_u].cpu(), Kr, tol, "K tiles")
     assert_rel(vt[:n_u].cpu(), Vr, tol, "V tiles")
-    # the transposed tiles are the same values, bit for bit
-    assert torch.equal(ktt[:n_u].transpose(-1, -2).cpu(), kt[:n_u].cpu())
-    assert torch.equal(vtt[:n_u].transpose(-1, -2).cpu(), vt[:n_u].cpu())
+    # the transposed tiles are the same values, bit for bit, with the key axis in MFMA order
+    # (within each 32-key group: key 4g + e at position 8g + e, key 16 + 4g + e at 8g + 4 + e)
+    pos = torch.tensor([32 * (k // 32) + (8 * ((k % 16) // 4) + (k % 4) + (4 if k % 32 >= 16 else 0))
+                        for k in range(T)])
+    assert sorted(pos.tolist()) == list(range(T))
+    assert torch.equal(ktt[:n_u][..., pos].transpose(-1, -2).cpu(), kt[:n_u].cpu())
+    assert torch.equal(vtt[:n_u][..., pos].transpose(-1, -2).cpu(), vt[:n_u].cpu())
 
 
 # --------------------------------------------------- routed attention forward
