@@ -218,17 +218,17 @@ __global__ __launch_bounds__(kBThreads) void xattn_bwd_dq_kernel(
     }
 }
 
-// dk/dv, slot-group decomposition.  One workgroup = one (sequence b, kv head
-// hk, group of SG consecutive slots); wave w owns slot SG*blockIdx.x + w, i.e.
-// the 64 keys of one selected chapter.  All slots of a sequence attend the same
-// queries, so the query-side tiles of a step (Q and dO row-major, Q^T and dO^T,
-// QS queries each) are staged in LDS once and shared by the SG waves; they are
-// double-buffered, the next step's global loads being issued before the math of
-// the current one, so a step costs one barrier.  In bf16 the wave's K and V
-// fragments live in registers for the whole kernel (loaded once from HBM); the
-// fp32 variant keeps them in LDS.  Output: per-edge dk / dv rows (edge e =
-// b*NS + slot), summed per distinct chapter by dkv_reduce_kernel, and
-// d omega per (edge, query head).
+// dk/dv, slot-group decomposition.  One workgroup = one (sequence b, kv head hk,
+// group of CPW consecutive slots); each slot's chapter (64 keys) is split over two
+// waves of 32 keys, so a wave's accumulators, K / V fragments and score tiles fit in
+// 256 registers and two waves share each SIMD (one wave's MFMAs run under the
+// other's softmax work and stalls).  All slots of a sequence attend the same
+// queries, so the query-side tiles of a step (Q and dO row-major, Q^T and dO^T, QS
+// queries each) are staged in LDS once and shared by all waves; they are
+// double-buffered, the next step's global loads being issued before the math of the
+// current one, so a step costs one barrier.  K and V fragments live in registers for
+// the whole kernel (loaded once from HBM).  Output: per-edge dk / dv rows (edge e =
+// b*NS + slot) and d omega per (edge, kv head).
 //
 // Per score element (key j, query i) with p = exp2(c s - lse_i) the softmax
 // probability (c = omega * scale * log2 e, s = q_i . k_j, dP = dO_i . v_j):
@@ -237,42 +237,45 @@ __global__ __launch_bounds__(kBThreads) void xattn_bwd_dq_kernel(
 //   ds~  = p~ t                                          (A operand of dK = dS~^T Q)
 // which is the gradient of softmax(omega s scale) against omega-scaled values.
 // d omega = sum_ij p~ (t s + dP) / omega is read off the accumulators at the end:
-// sum_j dk_j . k_j + dv_j . v_j.  omega == 0 runs the same loop with p~ = p (log2
-// omega taken as 0): d omega then needs no division, and the chapter's dK / dV
-// (which vanish) are zeroed.
+// sum_j dk_j . k_j + dv_j . v_j, the two key halves summed in a fixed order.
+// omega == 0 runs the same loop with p~ = p (log2 omega taken as 0): d omega then
+// needs no division, and the chapter's dK / dV (which vanish) are zeroed.
 template <typename T> struct DkvCfg;
-template <> struct DkvCfg<bf16> { static constexpr int SG = 4, QS = 64; static constexpr bool kKVRegs = true; };
-template <> struct DkvCfg<float> { static constexpr int SG = 2, QS = 32; static constexpr bool kKVRegs = false; };
+template <> struct DkvCfg<bf16> { static constexpr int CPW = 4, QS = 64; };
+template <> struct DkvCfg<float> { static constexpr int CPW = 2, QS = 32; };
+constexpr int kDkvWavesPerChapter = 2;
 
 template <typename T>
-__global__ __launch_bounds__(64 * DkvCfg<T>::SG, 1) void xattn_bwd_dkv_kernel(
+__global__ __launch_bounds__(64 * kDkvWavesPerChapter * DkvCfg<T>::CPW) void xattn_bwd_dkv_kernel(
     const T* __restrict__ q, const T* __restrict__ qt, const T* __restrict__ dout, const T* __restrict__ dot,
     const T* __restrict__ ktiles, const T* __restrict__ vtiles, const int32_t* __restrict__ slot_u,
     const float* __restrict__ omega, const float* __restrict__ lse, const float* __restrict__ delta, int B, int L,
     int Lp, int H, int HK, int NS, float scale_log2, float scale, T* __restrict__ dkv_edge,
     float* __restrict__ domega_part) {
   typedef typename Frag<T>::type F8;
-  constexpr int SG = DkvCfg<T>::SG, QS = DkvCfg<T>::QS, NT = 64 * SG;
-  constexpr bool kKVRegs = DkvCfg<T>::kKVRegs;
+  constexpr int CPW = DkvCfg<T>::CPW, QS = DkvCfg<T>::QS;
+  constexpr int WPC = kDkvWavesPerChapter, NW = CPW * WPC, NT = 64 * NW;
+  constexpr int NKB = 64 / WPC / 16;              // 16-key blocks per wave
   constexpr int EPC = 16 / (int)sizeof(T);
-  using TileK = SwzTile<T, 64>;   // [key][dim] and [query][dim]
+  using TileK = SwzTile<T, 64>;   // [query][dim]
   using TileT = SwzTile<T, QS>;   // [dim][query]
-  constexpr int KVB = 64 * 64 * (int)sizeof(T);
   constexpr int STB = 64 * QS * (int)sizeof(T);  // one staged tile (always 8 KB)
   constexpr int CPT = STB / 16 / NT;             // chunks per thread per staged tile
-  __shared__ __attribute__((aligned(16))) char sKV[kKVRegs ? 1 : SG][2][kKVRegs ? 16 : KVB];
+  static_assert(CPT >= 1, "staging needs at least one chunk per thread");
   __shared__ __attribute__((aligned(16))) char sStage[2][4][STB];  // [buf][Q, dO, Q^T, dO^T]
   __shared__ float sL[2][QS], sDl[2][QS];
+  __shared__ float sDom[NW];
 
   // tiles: (sequence, kv head) major, slot group minor, so the slot groups that stage
   // the same query tiles share one XCD's L2
-  const int nsg = (NS + SG - 1) / SG;
+  const int nsg = (NS + CPW - 1) / CPW;
   const int64_t t = xcd_tile((int64_t)B * HK * nsg);
   if (t < 0) return;
   const int b = (int)(t / ((int64_t)HK * nsg)), hk = (int)((t / nsg) % HK);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 4, c16 = lane & 15;
-  const int slot = SG * (int)(t % nsg) + wave;
+  const int slot = CPW * (int)(t % nsg) + wave / WPC;
+  const int k0 = 64 / WPC * (wave % WPC);  // this wave's first key of the chapter
   const int e = b * NS + slot;
   const int u = slot < NS ? slot_u[e] : -1;
   const bool active = u >= 0;
@@ -280,43 +283,27 @@ __global__ __launch_bounds__(64 * DkvCfg<T>::SG, 1) void xattn_bwd_dkv_kernel(
   const int KV = HK * 64;
   const size_t row_stride = 2 * (size_t)KV;
 
-  // K / V fragments of this wave's chapter: B operands of S = Q K^T and dP = dO V^T
-  // (key row 16 kb + c16, dims 32 ks + 8 g .. +7)
-  F8 kreg[4][2], vreg[4][2];
+  // K / V fragments of this wave's keys: B operands of S = Q K^T and dP = dO V^T
+  // (key row k0 + 16 kb + c16, dims 32 ks + 8 g .. +7)
+  F8 kreg[NKB][2], vreg[NKB][2];
   if (active) {
     const T* kp = ktiles + ((size_t)u * HK + hk) * 4096;
     const T* vp = vtiles + ((size_t)u * HK + hk) * 4096;
-    if constexpr (kKVRegs) {
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb)
+    for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-          kreg[kb][ks] = Load8<T, T>::run(kp + (16 * kb + c16) * 64 + 32 * ks + 8 * g);
-          vreg[kb][ks] = Load8<T, T>::run(vp + (16 * kb + c16) * 64 + 32 * ks + 8 * g);
-        }
-    } else {
-      for (int i = lane; i < 64 * (64 / EPC); i += 64) {
-        const int row = i / (64 / EPC), cc = (i % (64 / EPC)) * EPC;
-        st16(sKV[wave][0] + TileK::off(row, cc), ld16(kp + (size_t)i * EPC));
-        st16(sKV[wave][1] + TileK::off(row, cc), ld16(vp + (size_t)i * EPC));
+      for (int ks = 0; ks < 2; ++ks) {
+        kreg[kb][ks] = Load8<T, T>::run(kp + (k0 + 16 * kb + c16) * 64 + 32 * ks + 8 * g);
+        vreg[kb][ks] = Load8<T, T>::run(vp + (k0 + 16 * kb + c16) * 64 + 32 * ks + 8 * g);
       }
-    }
   }
-  auto kfrag = [&](int kb, int ks) -> F8 {
-    if constexpr (kKVRegs) return kreg[kb][ks];
-    else return TileK::frag(sKV[wave][0], 16 * kb + c16, 32 * ks + 8 * g);
-  };
-  auto vfrag = [&](int kb, int ks) -> F8 {
-    if constexpr (kKVRegs) return vreg[kb][ks];
-    else return TileK::frag(sKV[wave][1], 16 * kb + c16, 32 * ks + 8 * g);
-  };
   const float w = active ? omega[e] : 0.f;
   const float c = w * scale_log2, dsc = w * scale;
   const float lw = w > 0.f ? __log2f(w) : 0.f;
 
-  f32x4 dk[4][4], dv[4][4];
+  f32x4 dk[NKB][4], dv[NKB][4];
 #pragma unroll
-  for (int kb = 0; kb < 4; ++kb)
+  for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
       dk[kb][db] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -327,8 +314,9 @@ __global__ __launch_bounds__(64 * DkvCfg<T>::SG, 1) void xattn_bwd_dkv_kernel(
   for (int hq = hk * G; hq < hk * G + G; ++hq) {
     const size_t bh = (size_t)b * H + hq;
     // staged tiles of a step: 0 = Q rows, 1 = dO rows ([query][dim]), 2 = Q^T, 3 = dO^T
-    // ([dim][query]); every thread moves CPT 16-byte chunks of each.  Row tiles read
-    // through a buffer spanning this sequence only, so rows past L come back as zeros.
+    // ([dim][query], query axis in MFMA key order); every thread moves CPT 16-byte chunks
+    // of each.  Row tiles read through a buffer spanning this sequence only, so rows past
+    // L come back as zeros.
     const uint32_t seq_bytes = (uint32_t)((size_t)L * H * 64 * sizeof(T));
     const uint32_t head_bytes = (uint32_t)((size_t)64 * Lp * sizeof(T));
     const Buf bq(q + (size_t)b * L * H * 64, seq_bytes), bd(dout + (size_t)b * L * H * 64, seq_bytes);
@@ -390,11 +378,11 @@ __global__ __launch_bounds__(64 * DkvCfg<T>::SG, 1) void xattn_bwd_dkv_kernel(
 #pragma unroll
         for (int half = 0; half < QS / 32; ++half) {
           const int qb0 = 32 * half;
-          f32x4 sc[2][4], dp[2][4];
+          f32x4 sc[2][NKB], dp[2][NKB];
 #pragma unroll
           for (int qb = 0; qb < 2; ++qb)
 #pragma unroll
-            for (int kb = 0; kb < 4; ++kb) {
+            for (int kb = 0; kb < NKB; ++kb) {
               sc[qb][kb] = f32x4{0.f, 0.f, 0.f, 0.f};
               dp[qb][kb] = f32x4{0.f, 0.f, 0.f, 0.f};
             }
@@ -407,24 +395,21 @@ __global__ __launch_bounds__(64 * DkvCfg<T>::SG, 1) void xattn_bwd_dkv_kernel(
               da[qb] = TileK::frag(sD, qb0 + 16 * qb + c16, 32 * ks + 8 * g);
             }
 #pragma unroll
-            for (int kb = 0; kb < 4; ++kb) {
-              const F8 kf = kfrag(kb, ks);
-              const F8 vf = vfrag(kb, ks);
+            for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
               for (int qb = 0; qb < 2; ++qb) {
-                mma(sc[qb][kb], qa[qb], kf);
-                mma(dp[qb][kb], da[qb], vf);
+                mma(sc[qb][kb], qa[qb], kreg[kb][ks]);
+                mma(dp[qb][kb], da[qb], vreg[kb][ks]);
               }
-            }
           }
-          F8 pa[4], sa[4];
+          F8 pa[NKB], sa[NKB];
 #pragma unroll
           for (int qb = 0; qb < 2; ++qb) {
             // l2 - log2(omega): exp2(c s - l2) = omega p;  dl = scale * delta
             const f32x4 l2 = *reinterpret_cast<const f32x4*>(&sL[buf][qb0 + 16 * qb + 4 * g]) - lw;
             const f32x4 dl = *reinterpret_cast<const f32x4*>(&sDl[buf][qb0 + 16 * qb + 4 * g]);
 #pragma unroll
-            for (int kb = 0; kb < 4; ++kb)
+            for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
               for (int x = 0; x < 4; ++x) {
                 const float sraw = sc[qb][kb][x];
@@ -438,12 +423,12 @@ __global__ __launch_bounds__(64 * DkvCfg<T>::SG, 1) void xattn_bwd_dkv_kernel(
 #pragma unroll
           for (int db = 0; db < 4; ++db) {
             // Q^T / dO^T are stored with their query axis in MFMA key order
-            F8 bq = TileT::frag(sQt, 16 * db + c16, qb0 + 8 * g);
-            F8 bd = TileT::frag(sDt, 16 * db + c16, qb0 + 8 * g);
+            const F8 fq = TileT::frag(sQt, 16 * db + c16, qb0 + 8 * g);
+            const F8 fd = TileT::frag(sDt, 16 * db + c16, qb0 + 8 * g);
 #pragma unroll
-            for (int kb = 0; kb < 4; ++kb) {
-              mma(dv[kb][db], pa[kb], bd);
-              mma(dk[kb][db], sa[kb], bq);
+            for (int kb = 0; kb < NKB; ++kb) {
+              mma(dv[kb][db], pa[kb], fd);
+              mma(dk[kb][db], sa[kb], fq);
             }
           }
         }
@@ -452,31 +437,38 @@ __global__ __launch_bounds__(64 * DkvCfg<T>::SG, 1) void xattn_bwd_dkv_kernel(
       __syncthreads();
     }
   }
-  if (!active) return;
   // omega dL/domega = sum_ij p~ (t s + dP) = sum_j dk_j . k_j + dv_j . v_j (the accumulators
-  // are p~-weighted sums of dS~^T Q and P~^T dO), summed over the query heads of hk
-  {
+  // are p~-weighted sums of dS~^T Q and P~^T dO), summed over the query heads of hk and,
+  // in a fixed order, over the chapter's two key halves
+  float dom = 0.f;
+  if (active) {
     const T* kp = ktiles + ((size_t)u * HK + hk) * 4096;
     const T* vp = vtiles + ((size_t)u * HK + hk) * 4096;
-    float acc = 0.f;
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb)
+    for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
       for (int db = 0; db < 4; ++db)
 #pragma unroll
         for (int x = 0; x < 4; ++x) {
-          const int off = (16 * kb + 4 * g + x) * 64 + 16 * db + c16;
-          acc += dk[kb][db][x] * to_f(kp[off]) + dv[kb][db][x] * to_f(vp[off]);
+          const int off = (k0 + 16 * kb + 4 * g + x) * 64 + 16 * db + c16;
+          dom += dk[kb][db][x] * to_f(kp[off]) + dv[kb][db][x] * to_f(vp[off]);
         }
-    acc = wave_sum(acc);
-    if (w > 0.f) acc /= w;
-    if (lane == 0) domega_part[(size_t)e * HK + hk] = acc;
+    dom = wave_sum(dom);
+  }
+  if (lane == 0) sDom[wave] = dom;
+  __syncthreads();
+  if (!active) return;
+  if (wave % WPC == 0 && lane == 0) {
+    float s = 0.f;
+    for (int i = 0; i < WPC; ++i) s += sDom[wave + i];
+    if (w > 0.f) s /= w;
+    domega_part[(size_t)e * HK + hk] = s;
   }
   if (w == 0.f) {
     // the element loop ran with p in place of omega p: keys and values of a zero-weight
     // chapter carry no gradient
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb)
+    for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
       for (int db = 0; db < 4; ++db) {
         dk[kb][db] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -485,12 +477,12 @@ __global__ __launch_bounds__(64 * DkvCfg<T>::SG, 1) void xattn_bwd_dkv_kernel(
   }
   T* rows = dkv_edge + (size_t)e * 64 * row_stride;
 #pragma unroll
-  for (int kb = 0; kb < 4; ++kb)
+  for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
     for (int db = 0; db < 4; ++db)
 #pragma unroll
       for (int x = 0; x < 4; ++x) {
-        const int key = 16 * kb + 4 * g + x, dim = 16 * db + c16;
+        const int key = k0 + 16 * kb + 4 * g + x, dim = 16 * db + c16;
         rows[(size_t)key * row_stride + hk * 64 + dim] = from_f<T>(dk[kb][db][x]);
         rows[(size_t)key * row_stride + KV + hk * 64 + dim] = from_f<T>(dv[kb][db][x]);
       }
@@ -731,15 +723,15 @@ int moc_xattn_bwd_dkv(int dtype, const void* q, const void* qt, const void* dout
   const int Lp = (int)((L + 127) / 128 * 128);
   const float sl2 = scale * 1.4426950408889634f;
   if (dtype == MOC_BF16) {
-    constexpr int SG = DkvCfg<bf16>::SG;
-    dim3 grid(xcd_grid(B * HK * ((NS + SG - 1) / SG)));
-    hipLaunchKernelGGL(xattn_bwd_dkv_kernel<bf16>, grid, dim3(64 * SG), 0, stream, (const bf16*)q, (const bf16*)qt,
+    constexpr int CPW = DkvCfg<bf16>::CPW;
+    dim3 grid(xcd_grid(B * HK * ((NS + CPW - 1) / CPW)));
+    hipLaunchKernelGGL(xattn_bwd_dkv_kernel<bf16>, grid, dim3(64 * kDkvWavesPerChapter * CPW), 0, stream, (const bf16*)q, (const bf16*)qt,
                        (const bf16*)dout, (const bf16*)dot, (const bf16*)k_tiles, (const bf16*)v_tiles, slot_u,
                        omega, lse, delta, (int)B, (int)L, Lp, H, HK, NS, sl2, scale, (bf16*)dkv_edge, domega_part);
   } else if (dtype == MOC_F32) {
-    constexpr int SG = DkvCfg<float>::SG;
-    dim3 grid(xcd_grid(B * HK * ((NS + SG - 1) / SG)));
-    hipLaunchKernelGGL(xattn_bwd_dkv_kernel<float>, grid, dim3(64 * SG), 0, stream, (const float*)q,
+    constexpr int CPW = DkvCfg<float>::CPW;
+    dim3 grid(xcd_grid(B * HK * ((NS + CPW - 1) / CPW)));
+    hipLaunchKernelGGL(xattn_bwd_dkv_kernel<float>, grid, dim3(64 * kDkvWavesPerChapter * CPW), 0, stream, (const float*)q,
                        (const float*)qt, (const float*)dout, (const float*)dot, (const float*)k_tiles,
                        (const float*)v_tiles, slot_u, omega, lse, delta, (int)B, (int)L, Lp, H, HK, NS, sl2, scale,
                        (float*)dkv_edge, domega_part);
