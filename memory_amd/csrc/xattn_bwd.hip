@@ -155,47 +155,52 @@ __global__ __launch_bounds__(kBThreads) void xattn_bwd_dq_kernel(
       const float w = om[s];
       const float c = w * scale_log2;
       const float dsc = w * scale;
-      f32x4 st[4][2], dp[4][2];
+      // ds * dsc = p * (w dP - delta) * dsc = p * (dP * (w dsc) - delta * dsc)
+      const float wd = w * dsc;
+      const float dlc[2] = {dl[0] * dsc, dl[1] * dsc};
+      // the chapter's 64 keys in two halves of 32 (one dQ k-step each), which halves the
+      // score registers and lets three waves share a SIMD
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb)
+      for (int kh = 0; kh < 2; ++kh) {
+        f32x4 st[2][2], dp[2][2];
 #pragma unroll
-        for (int qb = 0; qb < 2; ++qb) {
-          st[kb][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
-          dp[kb][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
-        }
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-#pragma unroll
-        for (int kb = 0; kb < 4; ++kb) {
-          F8 ak = Tile::frag(sKc, 16 * kb + c16, 32 * ks + 8 * g);
-          F8 av = Tile::frag(sVc, 16 * kb + c16, 32 * ks + 8 * g);
+        for (int kbl = 0; kbl < 2; ++kbl)
 #pragma unroll
           for (int qb = 0; qb < 2; ++qb) {
-            mma(st[kb][qb], ak, qf[qb][ks]);
-            mma(dp[kb][qb], av, dof[qb][ks]);
+            st[kbl][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
+            dp[kbl][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
+          }
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+          for (int kbl = 0; kbl < 2; ++kbl) {
+            const int kb = 2 * kh + kbl;
+            F8 ak = Tile::frag(sKc, 16 * kb + c16, 32 * ks + 8 * g);
+            F8 av = Tile::frag(sVc, 16 * kb + c16, 32 * ks + 8 * g);
+#pragma unroll
+            for (int qb = 0; qb < 2; ++qb) {
+              mma(st[kbl][qb], ak, qf[qb][ks]);
+              mma(dp[kbl][qb], av, dof[qb][ks]);
+            }
           }
         }
-      }
-      F8 dsf[2][2];
+        F8 dsf[2];
 #pragma unroll
-      for (int qb = 0; qb < 2; ++qb)
+        for (int qb = 0; qb < 2; ++qb)
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb)
+          for (int kbl = 0; kbl < 2; ++kbl)
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const float p = __builtin_amdgcn_exp2f(st[kb][qb][e] * c - lse2[qb]);
-            const float ds = p * (w * dp[kb][qb][e] - dl[qb]) * dsc;
-            const int ks2 = kb >> 1, half = kb & 1;
-            dsf[qb][ks2][4 * half + e] = from_f<T>(ds);
-          }
-#pragma unroll
-      for (int ks2 = 0; ks2 < 2; ++ks2)
+            for (int e = 0; e < 4; ++e) {
+              const float p = __builtin_amdgcn_exp2f(st[kbl][qb][e] * c - lse2[qb]);
+              dsf[qb][4 * kbl + e] = from_f<T>(p * (dp[kbl][qb][e] * wd - dlc[qb]));
+            }
 #pragma unroll
         for (int db = 0; db < 4; ++db) {
-          F8 bk = Tile::frag(sKtc, 16 * db + c16, 32 * ks2 + 8 * g);  // K^T tiles are in MFMA key order
+          F8 bk = Tile::frag(sKtc, 16 * db + c16, 32 * kh + 8 * g);  // K^T tiles are in MFMA key order
 #pragma unroll
-          for (int qb = 0; qb < 2; ++qb) mma(acc[qb][db], dsf[qb][ks2], bk);
+          for (int qb = 0; qb < 2; ++qb) mma(acc[qb][db], dsf[qb], bk);
         }
+      }
     }
     if (u_next >= 0) {
       kio.store(sK[buf ^ 1], tid);
