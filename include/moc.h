@@ -217,7 +217,9 @@ int moc_bank_scatter(int dx_dtype, const void* dX, const void* bank, int bank_dt
  * chapter plan of the edges e = token * S + slot (token = b * Tq + t).
  * q [tokens][HQ][64]; K/V addressed by element strides (chapter cs, kv head hs, row rs).
  * Heads hk0 .. hk0+nhk-1 are processed; each edge serves rpe rows (query heads
- * hq_off .. hq_off+rpe-1).  Partials: o_part f32 [E * rpe][64], lse_part f32 [E * rpe]. */
+ * hq_off .. hq_off+rpe-1).  Partials: o_part f32 [E * rpe][64], lse_part f32 [E * rpe].
+ * bf16 runs one wave per (chapter, kv head) and needs 16-byte aligned q / k / v / o_part
+ * and cs / hs / rs multiples of 8. */
 int moc_sparse_fwd(int dtype, const void* q, int64_t ntok, int HQ, const void* k, const void* v, int64_t cs,
                    int64_t hs, int64_t rs, int HK, int Dh, const int32_t* uniq, const int32_t* n_uniq,
                    const int32_t* csr_off, const int32_t* csr_edge, int64_t max_u, int S, int hk0, int nhk,
@@ -228,16 +230,23 @@ int moc_sparse_fwd(int dtype, const void* q, int64_t ntok, int HQ, const void* k
 int moc_sparse_combine(int dtype, const float* o_part, const float* lse_part, const int32_t* edge_u, const float* w,
                        int mode, int S, int rpe, int64_t ntok, int HQ, int hq_off, void* out, float* lse_joint,
                        hipStream_t stream);
-/* Backward prep: mode 0 -> dst f32 [E * rpe] = dout . o_part; else dst f32 [tokens * rpe] = dout . out. */
+/* Backward prep: modes 1-3 -> dst f32 [tokens * rpe] = dout . out (the joint softmax delta that
+ * moc_sparse_bwd reads).  mode 0 -> dst f32 [E * rpe] = dout . o_part; moc_sparse_bwd computes
+ * these per-chapter deltas itself, so mode 0 callers do not need this call. */
 int moc_sparse_bwd_prep(int dtype, const void* dout, const void* out, const float* o_part, const int32_t* edge_u,
                         int mode, int S, int rpe, int64_t ntok, int HQ, int hq_off, float* dst, hipStream_t stream);
 /* Chapter-centric backward: dK/dV of every (chapter, kv head) stored with element strides
  * (ocs, ohs, ors) into dk / dv (rows of untouched chapters are left as they are); per-edge
- * dq parts f32 [E * rpe][64]; dlog f32 [E * rpe] (modes 2-3, d loss / d log weight). */
+ * dq parts f32 [E * rpe][64]; dlog f32 [E * rpe] (modes 2-3, d loss / d log weight).
+ * delta_row: modes 1-3 read the joint delta [tokens * rpe] of moc_sparse_bwd_prep; mode 0
+ * WRITES the per-chapter delta dout . o_s [E * rpe] (computed from P and dO V^T), the input
+ * of moc_sparse_dw.  bf16 runs one wave per (chapter, kv head) and needs 16-byte aligned
+ * q / dout / k / v / dq_part, 8-byte aligned dk / dv, cs / hs / rs multiples of 8 and
+ * ocs / ohs / ors multiples of 4. */
 int moc_sparse_bwd(int dtype, const void* q, const void* dout, int64_t ntok, int HQ, const void* k, const void* v,
                    int64_t cs, int64_t hs, int64_t rs, int HK, int Dh, const int32_t* uniq, const int32_t* n_uniq,
                    const int32_t* csr_off, const int32_t* csr_edge, int64_t max_u, int S, int hk0, int nhk,
-                   int hq_off, int rpe, int mode, const float* lse_row, const float* delta_row, const float* w,
+                   int hq_off, int rpe, int mode, const float* lse_row, float* delta_row, const float* w,
                    float scale, void* dk, void* dv, int64_t ocs, int64_t ohs, int64_t ors, float* dq_part,
                    float* dlog, hipStream_t stream);
 /* dq [tokens][HQ][64] rows hq_off .. hq_off+rpe-1 = sum over valid slots of dq_part. */

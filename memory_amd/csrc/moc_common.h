@@ -179,6 +179,33 @@ __host__ __device__ constexpr int mfma_pos_key(int p) {
   return (p & ~31) | (((p & 4) ? 16 : 0) + 4 * ((p & 31) >> 3) + (p & 3));
 }
 
+// Transposing fragment read (ds_read_b64_tr_b16) from a row-major bf16 LDS tile with
+// layout Tile::off(row, col): lane l receives column cb + l % 16 at rows rb + 4g + e
+// (elements e = 0..3) and rb + 16 + 4g + e (elements 4 + e), g = l / 16 -- the k order
+// of the MFMA key order above, so the result pairs with P / dS fragments held in
+// accumulator layout.  Each 16-lane group reads 4 rows x 16 columns per instruction;
+// lane q of the group supplies the address of row q / 4, columns 4 (q % 4) .. + 3.
+template <typename Tile>
+__device__ __forceinline__ bf16x8 tr_frag_mk(const char* base, int rb, int cb, int lane) {
+  typedef short v4s __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) v4s* lds_v4s;
+  const int q = lane & 15;
+  const int row = rb + 4 * (lane >> 4) + (q >> 2), col = cb + 4 * (q & 3);
+  const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(base + Tile::off(row, col)));
+  const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(base + Tile::off(row + 16, col)));
+  const v4s v[2] = {lo, hi};
+  return __builtin_bit_cast(bf16x8, v);
+}
+
+// Orders LDS accesses of one wave: everything before is visible to every lane of the
+// wave after (LDS executes one wave's instructions in order; this keeps the compiler
+// from moving accesses across).
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // s_waitcnt vmcnt(0) (expcnt / lgkmcnt left open), gfx9 encoding
 __device__ __forceinline__ void vm_wait_all() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 

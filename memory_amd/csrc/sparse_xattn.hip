@@ -270,7 +270,7 @@ __global__ __launch_bounds__(64 * SpCfg<T>::NW, 1) void sparse_bwd_kernel(
     const T* __restrict__ q, const T* __restrict__ dout, int HQ, const T* __restrict__ k, const T* __restrict__ v,
     int64_t cs, int64_t hs, int64_t rs, int HK, const int32_t* __restrict__ uniq, const int32_t* __restrict__ n_uniq,
     const int32_t* __restrict__ csr_off, const int32_t* __restrict__ csr_edge, int S, int hk0, int hq_off, int rpe,
-    int mode, const float* __restrict__ lse_row, const float* __restrict__ delta_row, const float* __restrict__ w,
+    int mode, const float* __restrict__ lse_row, float* __restrict__ delta_row, const float* __restrict__ w,
     float scale_log2, float scale, T* __restrict__ dk, T* __restrict__ dv, int64_t ocs, int64_t ohs, int64_t ors,
     float* __restrict__ dq_part, float* __restrict__ dlog) {
   typedef typename Frag<T>::type F8;
@@ -375,7 +375,6 @@ __global__ __launch_bounds__(64 * SpCfg<T>::NW, 1) void sparse_bwd_kernel(
           if (mode == 0) {
             lr[qb][x] = lse_row[erw];
             wr[qb][x] = w[e];
-            dr[qb][x] = delta_row[erw];
           } else {
             const int64_t trow = (int64_t)(e / S) * rpe + (hq - hq_off);
             lr[qb][x] = lse_row[trow];
@@ -405,6 +404,30 @@ __global__ __launch_bounds__(64 * SpCfg<T>::NW, 1) void sparse_bwd_kernel(
           mma(dp[qb][kb], da[qb][ks], vf);
         }
       }
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int x = 0; x < 4; ++x) sc[qb][kb][x] = exp2f(sc[qb][kb][x] * scale_log2 + lw[qb][x] - lr[qb][x]);
+    if (mode == 0) {
+      // per-chapter softmax delta of each row (sum over the 64 keys of P dPu), also the
+      // per edge-row dO . o_s that moc_sparse_dw sums into dw
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+        for (int x = 0; x < 4; ++x) {
+          float t = 0.f;
+#pragma unroll
+          for (int kb = 0; kb < 4; ++kb) t += sc[qb][kb][x] * dp[qb][kb][x];
+          t += __shfl_xor(t, 1, 16);
+          t += __shfl_xor(t, 2, 16);
+          t += __shfl_xor(t, 4, 16);
+          t += __shfl_xor(t, 8, 16);
+          dr[qb][x] = t;
+          if (c16 == 0 && er[qb][x] >= 0) delta_row[er[qb][x]] = t;
+        }
+    }
     F8 pa[4], sa[4];
     float rowsum[2][4];
 #pragma unroll
@@ -417,7 +440,7 @@ __global__ __launch_bounds__(64 * SpCfg<T>::NW, 1) void sparse_bwd_kernel(
       for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
         for (int x = 0; x < 4; ++x) {
-          const float p = exp2f(sc[qb][kb][x] * scale_log2 + lw[qb][x] - lr[qb][x]);
+          const float p = sc[qb][kb][x];
           float ds, pv;
           if (mode == 0) {
             ds = wr[qb][x] * p * (dp[qb][kb][x] - dr[qb][x]);
@@ -574,9 +597,419 @@ __global__ void sparse_dw_kernel(const float* __restrict__ src, const float* __r
   dw[e] = s;
 }
 
+// ----------------------------------------------------- bf16: one wave per unit
+// A unit is one (distinct chapter, kv head) pair; a chapter serves ~E / n_chapters
+// query rows (tens), so one wave holds the whole unit: no workgroup barriers, no
+// cross-wave reduction.  Workgroups carry kUnitWaves independent waves.
+// Operands that need the other orientation come from LDS through transposing reads
+// (tr_frag_mk): V^T in the forward, Q^T / dO^T / K^T / dS^T in the backward.
+constexpr int kUnitWaves = 4;
+
+// [64 keys][32 query rows] bf16 (64-byte rows), 16-byte chunks XOR-swizzled by key / 4
+struct DsTile {
+  __device__ static __forceinline__ int off(int row, int col) {
+    return row * 64 + ((((col >> 3) ^ (row >> 2)) & 3) << 4) + ((col & 7) << 1);
+  }
+};
+
+struct UnitRows {
+  int u, hk, gid, p0, nrows;
+};
+
+__device__ __forceinline__ bool unit_setup(UnitRows& ur, const int32_t* uniq, const int32_t* n_uniq,
+                                           const int32_t* csr_off, int hk0, int nhk, int G) {
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t unit = (int64_t)blockIdx.x * kUnitWaves + wave;
+  ur.u = (int)(unit / nhk);
+  if (ur.u >= n_uniq[0]) return false;
+  ur.hk = hk0 + (int)(unit % nhk);
+  ur.gid = uniq[ur.u];
+  ur.p0 = csr_off[ur.u];
+  ur.nrows = (csr_off[ur.u + 1] - ur.p0) * G;
+  return true;
+}
+
+__global__ __launch_bounds__(64 * kUnitWaves) void sparse_fwd_unit_kernel(
+    const bf16* __restrict__ q, int HQ, const bf16* __restrict__ k, const bf16* __restrict__ v, int64_t cs,
+    int64_t hs, int64_t rs, int HK, const int32_t* __restrict__ uniq, const int32_t* __restrict__ n_uniq,
+    const int32_t* __restrict__ csr_off, const int32_t* __restrict__ csr_edge, int S, int hk0, int nhk, int hq_off,
+    int rpe, float scale_log2, float* __restrict__ o_part, float* __restrict__ lse_part) {
+  using Tile = SwzTile<bf16, 64>;
+  __shared__ __attribute__((aligned(16))) char sVall[kUnitWaves][64 * 64 * 2];
+  const int G = HQ / HK;
+  UnitRows ur;
+  if (!unit_setup(ur, uniq, n_uniq, csr_off, hk0, nhk, G)) return;
+  const int lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
+  char* sV = sVall[threadIdx.x >> 6];
+  const int64_t kv0 = (int64_t)ur.gid * cs + (int64_t)ur.hk * hs;
+  // K as the A operand of S^T = K Q^T (lane = key), V staged row-major for V^T reads
+  bf16x8 kf[4][2];
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) kf[kb][ks] = Load8<bf16, bf16>::run(k + kv0 + (16 * kb + c16) * rs + 32 * ks + 8 * g);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int row = 8 * i + (lane >> 3), c0 = 8 * (lane & 7);
+    st16(sV + Tile::off(row, c0), ld16(v + kv0 + row * rs + c0));
+  }
+  wave_lds_sync();
+  for (int r0 = 0; r0 < ur.nrows; r0 += 32) {
+    const bool two = r0 + 16 < ur.nrows;
+    bf16x8 qf[2][2];
+    int erow[2];
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+      const int r = r0 + 16 * qb + c16;
+      erow[qb] = -1;
+      qf[qb][0] = qf[qb][1] = zero_frag<bf16>();
+      if (r < ur.nrows) {
+        const int e = csr_edge[ur.p0 + r / G];
+        const int hq = ur.hk * G + r % G;
+        erow[qb] = e * rpe + (hq - hq_off);
+        const bf16* qp = q + ((int64_t)(e / S) * HQ + hq) * kSpDh + 8 * g;
+        qf[qb][0] = Load8<bf16, bf16>::run(qp);
+        qf[qb][1] = Load8<bf16, bf16>::run(qp + 32);
+      }
+    }
+    // S^T: lane = query row 16 qb + c16, keys 16 kb + 4 g + x
+    f32x4 st[4][2];
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb) {
+        st[kb][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (qb == 0 || two) {
+          mma(st[kb][qb], kf[kb][0], qf[qb][0]);
+          mma(st[kb][qb], kf[kb][1], qf[qb][1]);
+        }
+      }
+    bf16x8 pf[2][2];
+    float m[2], l[2];
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+      float mx = st[0][qb][0];
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int x = 0; x < 4; ++x) mx = fmax_fast(mx, st[kb][qb][x]);
+      m[qb] = quad_max(mx) * scale_log2;
+      float ps = 0.f;
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int x = 0; x < 4; ++x) {
+          const float p = exp2f(st[kb][qb][x] * scale_log2 - m[qb]);
+          ps += p;
+          pf[qb][kb >> 1][4 * (kb & 1) + x] = (bf16)p;
+        }
+      l[qb] = quad_sum(ps);
+    }
+    // O^T = V^T P^T: lane = query row, dims 16 db + 4 g + x
+    f32x4 o[4][2];
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+      const bf16x8 a0 = tr_frag_mk<Tile>(sV, 0, 16 * db, lane);
+      const bf16x8 a1 = tr_frag_mk<Tile>(sV, 32, 16 * db, lane);
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb) {
+        o[db][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (qb == 0 || two) {
+          mma(o[db][qb], a0, pf[qb][0]);
+          mma(o[db][qb], a1, pf[qb][1]);
+        }
+      }
+    }
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+      if (erow[qb] < 0) continue;
+      const float inv = 1.f / l[qb];
+      float* op = o_part + (int64_t)erow[qb] * kSpDh;
+#pragma unroll
+      for (int db = 0; db < 4; ++db) *reinterpret_cast<f32x4*>(op + 16 * db + 4 * g) = o[db][qb] * inv;
+      if (g == 0) lse_part[erow[qb]] = m[qb] + log2f(l[qb]);
+    }
+  }
+}
+
+// Backward of one unit.  Per 32-row block: S = Q K^T and dPu = dO V^T with lane = key
+// (accumulator layout, rows 16 qb + 4 g + x), P and dS in registers, then
+//   dV^T += dO^T P,  dK^T += Q^T dS      (A = transposing reads of the staged rows)
+//   dQ^T  = K^T dS^T                      (dS staged key-major, both operands transposed)
+// mode 0 computes the per-chapter softmax delta sum_j P_j dPu_j itself and writes it
+// to delta_row (the per edge-row dO . o_s that moc_sparse_dw sums into dw).
+__global__ __launch_bounds__(64 * kUnitWaves, 1) void sparse_bwd_unit_kernel(
+    const bf16* __restrict__ q, const bf16* __restrict__ dout, int HQ, const bf16* __restrict__ k,
+    const bf16* __restrict__ v, int64_t cs, int64_t hs, int64_t rs, int HK, const int32_t* __restrict__ uniq,
+    const int32_t* __restrict__ n_uniq, const int32_t* __restrict__ csr_off, const int32_t* __restrict__ csr_edge,
+    int S, int hk0, int nhk, int hq_off, int rpe, int mode, const float* __restrict__ lse_row,
+    float* __restrict__ delta_row, const float* __restrict__ w, float scale_log2, float scale, bf16* __restrict__ dk,
+    bf16* __restrict__ dv, int64_t ocs, int64_t ohs, int64_t ors, float* __restrict__ dq_part,
+    float* __restrict__ dlog) {
+  using Tile = SwzTile<bf16, 64>;
+  constexpr int kKB = 64 * 64 * 2, kRB = 32 * 64 * 2;
+  struct WaveLds {
+    char k[kKB];     // K [key][dim]
+    char q[kRB];     // Q rows of the block [row][dim]
+    char d[kRB];     // dO rows
+    char ds[kRB];    // dS [key][row] (DsTile)
+    float lse[32], del[32], wr[32];
+    int er[32];
+  };
+  __shared__ __attribute__((aligned(16))) WaveLds sAll[kUnitWaves];
+  const int G = HQ / HK;
+  UnitRows ur;
+  if (!unit_setup(ur, uniq, n_uniq, csr_off, hk0, nhk, G)) return;
+  const int lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
+  WaveLds& L = sAll[threadIdx.x >> 6];
+  const int64_t kv0 = (int64_t)ur.gid * cs + (int64_t)ur.hk * hs;
+  // K, V as the B operands of S / dPu (lane = key); K also staged for K^T reads
+  bf16x8 kf[4][2], vf[4][2];
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const int64_t off = kv0 + (16 * kb + c16) * rs + 32 * ks + 8 * g;
+      kf[kb][ks] = Load8<bf16, bf16>::run(k + off);
+      vf[kb][ks] = Load8<bf16, bf16>::run(v + off);
+    }
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+      *reinterpret_cast<bf16x8*>(L.k + Tile::off(16 * kb + c16, 32 * ks + 8 * g)) = kf[kb][ks];
+  f32x4 dkt[4][4], dvt[4][4];   // [db][kb]: lane = key 16 kb + c16, dims 16 db + 4 g + x
+#pragma unroll
+  for (int db = 0; db < 4; ++db)
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      dkt[db][kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+      dvt[db][kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  for (int r0 = 0; r0 < ur.nrows; r0 += 32) {
+    const bool two = r0 + 16 < ur.nrows;
+    // ---- rows as A operands (lane = row 16 qb + c16), staged for the transposing reads
+    bf16x8 qa[2][2], da[2][2];
+    int erow_a[2];
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+      const int r = r0 + 16 * qb + c16;
+      erow_a[qb] = -1;
+      qa[qb][0] = qa[qb][1] = da[qb][0] = da[qb][1] = zero_frag<bf16>();
+      if (r < ur.nrows) {
+        const int e = csr_edge[ur.p0 + r / G];
+        const int hq = ur.hk * G + r % G;
+        erow_a[qb] = e * rpe + (hq - hq_off);
+        const int64_t off = ((int64_t)(e / S) * HQ + hq) * kSpDh + 8 * g;
+        qa[qb][0] = Load8<bf16, bf16>::run(q + off);
+        qa[qb][1] = Load8<bf16, bf16>::run(q + off + 32);
+        da[qb][0] = Load8<bf16, bf16>::run(dout + off);
+        da[qb][1] = Load8<bf16, bf16>::run(dout + off + 32);
+      }
+    }
+    // ---- per-row constants, one lane per row
+    if (lane < 32) {
+      const int r = r0 + lane;
+      float lse = INFINITY, del = 0.f, wv = 0.f;
+      int er = -1;
+      if (r < ur.nrows) {
+        const int e = csr_edge[ur.p0 + r / G];
+        const int hr = ur.hk * G + r % G - hq_off;
+        er = e * rpe + hr;
+        if (mode == 0) {
+          lse = lse_row[er];
+          wv = w[e];
+        } else {
+          const int64_t trow = (int64_t)(e / S) * rpe + hr;
+          lse = lse_row[trow];
+          del = delta_row[trow];
+          wv = sp_logw(mode, w ? w[e] : 1.f);
+        }
+      }
+      L.lse[lane] = lse;
+      L.del[lane] = del;
+      L.wr[lane] = wv;
+      L.er[lane] = er;
+    }
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        *reinterpret_cast<bf16x8*>(L.q + Tile::off(16 * qb + c16, 32 * ks + 8 * g)) = qa[qb][ks];
+        *reinterpret_cast<bf16x8*>(L.d + Tile::off(16 * qb + c16, 32 * ks + 8 * g)) = da[qb][ks];
+      }
+    // ---- S and dPu (lane = key 16 kb + c16, rows 16 qb + 4 g + x)
+    f32x4 sc[2][4], dp[2][4];
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) {
+        sc[qb][kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+        dp[qb][kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (qb == 0 || two) {
+#pragma unroll
+          for (int ks = 0; ks < 2; ++ks) {
+            mma(sc[qb][kb], qa[qb][ks], kf[kb][ks]);
+            mma(dp[qb][kb], da[qb][ks], vf[kb][ks]);
+          }
+        }
+      }
+    wave_lds_sync();
+    float lr[2][4], dr[2][4], wr[2][4];
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+      for (int x = 0; x < 4; ++x) {
+        const int rr = 16 * qb + 4 * g + x;
+        lr[qb][x] = L.lse[rr];
+        dr[qb][x] = L.del[rr];
+        wr[qb][x] = L.wr[rr];
+      }
+    // ---- P (in sc)
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int x = 0; x < 4; ++x)
+          sc[qb][kb][x] = exp2f(sc[qb][kb][x] * scale_log2 + (mode == 0 ? 0.f : wr[qb][x]) - lr[qb][x]);
+    if (mode == 0) {
+      // per-chapter softmax delta of each row: sum over the 64 keys of P dPu
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+        for (int x = 0; x < 4; ++x) {
+          float t = 0.f;
+#pragma unroll
+          for (int kb = 0; kb < 4; ++kb) t += sc[qb][kb][x] * dp[qb][kb][x];
+          t += __shfl_xor(t, 1, 16);
+          t += __shfl_xor(t, 2, 16);
+          t += __shfl_xor(t, 4, 16);
+          t += __shfl_xor(t, 8, 16);
+          dr[qb][x] = t;
+        }
+      if (c16 == 0) {
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+          for (int x = 0; x < 4; ++x) {
+            const int er = L.er[16 * qb + 4 * g + x];
+            if (er >= 0) delta_row[er] = dr[qb][x];
+          }
+      }
+    }
+    bf16x8 pa[4], sa[4];
+    float rsum[2][4];
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+      for (int x = 0; x < 4; ++x) rsum[qb][x] = 0.f;
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int x = 0; x < 4; ++x) {
+          const float p = sc[qb][kb][x];
+          const float pw = mode == 0 ? wr[qb][x] * p : p;
+          const float ds = pw * (dp[qb][kb][x] - dr[qb][x]);
+          rsum[qb][x] += ds;
+          pa[kb][4 * qb + x] = (bf16)pw;
+          sa[kb][4 * qb + x] = (bf16)ds;
+        }
+    // ---- dV^T += dO^T P, dK^T += Q^T dS
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+      const bf16x8 ad = tr_frag_mk<Tile>(L.d, 0, 16 * db, lane);
+      const bf16x8 aq = tr_frag_mk<Tile>(L.q, 0, 16 * db, lane);
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) {
+        mma(dvt[db][kb], ad, pa[kb]);
+        mma(dkt[db][kb], aq, sa[kb]);
+      }
+    }
+    // ---- dS key-major for dQ
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      const int key = 16 * kb + c16;
+      const bf16x4 lo = {sa[kb][0], sa[kb][1], sa[kb][2], sa[kb][3]};
+      const bf16x4 hi = {sa[kb][4], sa[kb][5], sa[kb][6], sa[kb][7]};
+      *reinterpret_cast<bf16x4*>(L.ds + DsTile::off(key, 4 * g)) = lo;
+      *reinterpret_cast<bf16x4*>(L.ds + DsTile::off(key, 16 + 4 * g)) = hi;
+    }
+    if (dlog) {
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+        for (int x = 0; x < 4; ++x) {
+          float t = rsum[qb][x];
+          t += __shfl_xor(t, 1, 16);
+          t += __shfl_xor(t, 2, 16);
+          t += __shfl_xor(t, 4, 16);
+          t += __shfl_xor(t, 8, 16);
+          const int er = L.er[16 * qb + 4 * g + x];
+          if (c16 == 0 && er >= 0) dlog[er] = t;
+        }
+    }
+    wave_lds_sync();
+    // ---- dQ^T = K^T dS^T: lane = row 16 qb + c16, dims 16 db + 4 g + x
+    f32x4 dq[4][2];
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb) dq[db][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      bf16x8 bs[2];
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb) bs[qb] = tr_frag_mk<DsTile>(L.ds, 32 * ks, 16 * qb, lane);
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+        const bf16x8 ak = tr_frag_mk<Tile>(L.k, 32 * ks, 16 * db, lane);
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb)
+          if (qb == 0 || two) mma(dq[db][qb], ak, bs[qb]);
+      }
+    }
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+      if (erow_a[qb] < 0) continue;
+      float* dst = dq_part + (int64_t)erow_a[qb] * kSpDh + 4 * g;
+#pragma unroll
+      for (int db = 0; db < 4; ++db) *reinterpret_cast<f32x4*>(dst + 16 * db) = dq[db][qb] * scale;
+    }
+    wave_lds_sync();
+  }
+  // ---- dK = scale dK^T^T, dV: lane = key, 4 consecutive dims per store
+  bf16* dkb = dk + (int64_t)ur.gid * ocs + (int64_t)ur.hk * ohs;
+  bf16* dvb = dv + (int64_t)ur.gid * ocs + (int64_t)ur.hk * ohs;
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+      const int64_t off = (int64_t)(16 * kb + c16) * ors + 16 * db + 4 * g;
+      bf16x4 a, b;
+#pragma unroll
+      for (int x = 0; x < 4; ++x) {
+        a[x] = (bf16)(dkt[db][kb][x] * scale);
+        b[x] = (bf16)dvt[db][kb][x];
+      }
+      *reinterpret_cast<bf16x4*>(dkb + off) = a;
+      *reinterpret_cast<bf16x4*>(dvb + off) = b;
+    }
+}
+
 }  // namespace moc
 
 using namespace moc;
+
+namespace {
+// 16-byte K/V/q fragment loads of the one-wave-per-unit kernels
+bool unit_kv_aligned(const void* q, const void* k, const void* v, int64_t cs, int64_t hs, int64_t rs) {
+  return ((uintptr_t)q & 15) == 0 && ((uintptr_t)k & 15) == 0 && ((uintptr_t)v & 15) == 0 && cs % 8 == 0 &&
+         hs % 8 == 0 && rs % 8 == 0;
+}
+}  // namespace
 
 extern "C" {
 
@@ -593,11 +1026,15 @@ int moc_sparse_fwd(int dtype, const void* q, int64_t ntok, int HQ, const void* k
   if (max_u == 0 || ntok == 0) return MOC_OK;
   dim3 grid((unsigned)max_u, (unsigned)nhk);
   const float sl2 = scale * 1.4426950408889634f;
-  if (dtype == MOC_BF16)
-    hipLaunchKernelGGL(sparse_fwd_kernel<bf16>, grid, dim3(sp_threads<bf16>()), 0, stream, (const bf16*)q, HQ,
-                       (const bf16*)k, (const bf16*)v, cs, hs, rs, HK, uniq, n_uniq, csr_off, csr_edge, S, hk0, hq_off,
-                       rpe, sl2, o_part, lse_part);
-  else if (dtype == MOC_F32)
+  if (dtype == MOC_BF16) {
+    MOC_REQUIRE(unit_kv_aligned(q, k, v, cs, hs, rs) && ((uintptr_t)o_part & 15) == 0, MOC_ERR_ARG,
+                "moc_sparse_fwd: bf16 needs 16-byte aligned q/k/v/o_part and strides that are multiples of 8");
+    const int64_t units = max_u * nhk;
+    hipLaunchKernelGGL(sparse_fwd_unit_kernel, dim3((unsigned)((units + kUnitWaves - 1) / kUnitWaves)),
+                       dim3(64 * kUnitWaves), 0, stream, (const bf16*)q, HQ, (const bf16*)k, (const bf16*)v, cs, hs,
+                       rs, HK, uniq, n_uniq, csr_off, csr_edge, S, hk0, nhk, hq_off, rpe, sl2, o_part, lse_part);
+    return check_launch("sparse_fwd_unit_kernel");
+  } else if (dtype == MOC_F32)
     hipLaunchKernelGGL(sparse_fwd_kernel<float>, grid, dim3(sp_threads<float>()), 0, stream, (const float*)q, HQ,
                        (const float*)k, (const float*)v, cs, hs, rs, HK, uniq, n_uniq, csr_off, csr_edge, S, hk0,
                        hq_off, rpe, sl2, o_part, lse_part);
@@ -647,7 +1084,7 @@ int moc_sparse_bwd_prep(int dtype, const void* dout, const void* out, const floa
 int moc_sparse_bwd(int dtype, const void* q, const void* dout, int64_t ntok, int HQ, const void* k, const void* v,
                    int64_t cs, int64_t hs, int64_t rs, int HK, int Dh, const int32_t* uniq, const int32_t* n_uniq,
                    const int32_t* csr_off, const int32_t* csr_edge, int64_t max_u, int S, int hk0, int nhk,
-                   int hq_off, int rpe, int mode, const float* lse_row, const float* delta_row, const float* w,
+                   int hq_off, int rpe, int mode, const float* lse_row, float* delta_row, const float* w,
                    float scale, void* dk, void* dv, int64_t ocs, int64_t ohs, int64_t ors, float* dq_part,
                    float* dlog, hipStream_t stream) {
   MOC_REQUIRE(q && dout && k && v && uniq && n_uniq && csr_off && csr_edge && lse_row && delta_row && dk && dv &&
@@ -660,12 +1097,20 @@ int moc_sparse_bwd(int dtype, const void* q, const void* dout, int64_t ntok, int
   if (max_u == 0 || ntok == 0) return MOC_OK;
   dim3 grid((unsigned)max_u, (unsigned)nhk);
   const float sl2 = scale * 1.4426950408889634f;
-  if (dtype == MOC_BF16)
-    hipLaunchKernelGGL(sparse_bwd_kernel<bf16>, grid, dim3(sp_threads<bf16>()), 0, stream, (const bf16*)q,
-                       (const bf16*)dout, HQ, (const bf16*)k, (const bf16*)v, cs, hs, rs, HK, uniq, n_uniq, csr_off,
-                       csr_edge, S, hk0, hq_off, rpe, mode, lse_row, delta_row, w, sl2, scale, (bf16*)dk, (bf16*)dv,
-                       ocs, ohs, ors, dq_part, dlog);
-  else if (dtype == MOC_F32)
+  if (dtype == MOC_BF16) {
+    MOC_REQUIRE(unit_kv_aligned(q, k, v, cs, hs, rs) && ((uintptr_t)dout & 15) == 0 && ((uintptr_t)dq_part & 15) == 0 &&
+                    ((uintptr_t)dk & 7) == 0 && ((uintptr_t)dv & 7) == 0 && ocs % 4 == 0 && ohs % 4 == 0 &&
+                    ors % 4 == 0,
+                MOC_ERR_ARG,
+                "moc_sparse_bwd: bf16 needs 16-byte aligned q/dout/k/v/dq_part, 8-byte aligned dk/dv, input strides "
+                "that are multiples of 8 and output strides that are multiples of 4");
+    const int64_t units = max_u * nhk;
+    hipLaunchKernelGGL(sparse_bwd_unit_kernel, dim3((unsigned)((units + kUnitWaves - 1) / kUnitWaves)),
+                       dim3(64 * kUnitWaves), 0, stream, (const bf16*)q, (const bf16*)dout, HQ, (const bf16*)k,
+                       (const bf16*)v, cs, hs, rs, HK, uniq, n_uniq, csr_off, csr_edge, S, hk0, nhk, hq_off, rpe,
+                       mode, lse_row, delta_row, w, sl2, scale, (bf16*)dk, (bf16*)dv, ocs, ohs, ors, dq_part, dlog);
+    return check_launch("sparse_bwd_unit_kernel");
+  } else if (dtype == MOC_F32)
     hipLaunchKernelGGL(sparse_bwd_kernel<float>, grid, dim3(sp_threads<float>()), 0, stream, (const float*)q,
                        (const float*)dout, HQ, (const float*)k, (const float*)v, cs, hs, rs, HK, uniq, n_uniq,
                        csr_off, csr_edge, S, hk0, hq_off, rpe, mode, lse_row, delta_row, w, sl2, scale, (float*)dk,

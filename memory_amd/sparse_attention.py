@@ -68,7 +68,9 @@ def _forward(q, k, v, layout, segments: List[_Segment], mode: int, S: int, scale
         lse_joint = None if mode == 0 else torch.empty(ntok * sg.rpe, device=q.device, dtype=torch.float32)
         call("moc_sparse_combine", dt, ptr(o_part), ptr(lse_part), ptr(sg.plan.edge_u), ptr(sg.w), mode, S, sg.rpe,
              ntok, HQ, sg.hq_off, ptr(out), ptr(lse_joint), st)
-        saved.append((o_part, lse_part, lse_joint))
+        # the backward needs the per-edge lse (mode 0) or the joint lse (modes 1-3), not o_part
+        saved.append((lse_part if mode == 0 else None, lse_joint))
+        del o_part
     return out, saved
 
 
@@ -84,15 +86,16 @@ def _backward(q, k, v, layout, out, dout, segments, saved, mode, S, scale, dk, d
     dws = []
     dout = dout.to(q.dtype).contiguous()
     ocs, ohs, ors, dv_off = dk_layout
-    for sg, (o_part, lse_part, lse_joint) in zip(segments, saved):
+    for sg, (lse_part, lse_joint) in zip(segments, saved):
         if mode == 0:
+            # per-chapter deltas dO . o_s, written by moc_sparse_bwd itself
             drow = torch.empty(sg.E * sg.rpe, device=q.device, dtype=torch.float32)
             lrow = lse_part
         else:
             drow = torch.empty(ntok * sg.rpe, device=q.device, dtype=torch.float32)
             lrow = lse_joint
-        call("moc_sparse_bwd_prep", dt, ptr(dout), ptr(out), ptr(o_part), ptr(sg.plan.edge_u), mode, S, sg.rpe, ntok,
-             HQ, sg.hq_off, ptr(drow), st)
+            call("moc_sparse_bwd_prep", dt, ptr(dout), ptr(out), None, ptr(sg.plan.edge_u), mode, S, sg.rpe,
+                 ntok, HQ, sg.hq_off, ptr(drow), st)
         dq_part = torch.empty(sg.E * sg.rpe, D, device=q.device, dtype=torch.float32)
         dlog = torch.empty(sg.E * sg.rpe, device=q.device, dtype=torch.float32) if mode in (2, 3) else None
         call("moc_sparse_bwd", dt, ptr(q), ptr(dout), ntok, HQ, ptr(k), ptr(v), cs, hs, rs, HK, D,
