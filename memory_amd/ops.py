@@ -387,14 +387,55 @@ def routed_attention(q, bank, wk, wv, omega, idx_star, *, num_chapters: int, tok
                                   norm_code(norm_type), float(eps), HK)
 
 
-def router_token_logits(h: torch.Tensor, W: torch.Tensor, b: Optional[torch.Tensor]) -> torch.Tensor:
-    """Per-token router logits (B*T, C) in fp32 (router.py:294, ``self.router(hidden_states)``).
+class _TokenRouterLinear(torch.autograd.Function):
+    """logits = x W^T + b for per-token routing (router.py:294, ``self.router(hidden_states)``).
 
-    A plain (B*T, d) x (d, C) fp32 GEMM (hipBLASLt through torch.matmul).  fp32, not the
-    reference's autocast bf16, so that the top-k selection sees distinct logits."""
+    The GEMM operands are in the activation dtype (bf16 activations round W to bf16, the
+    operand precision of the reference under autocast) and accumulate in fp32 on
+    hipBLASLt; the logits stay fp32 (not rounded to bf16 as under autocast) so that the
+    top-k selection sees distinct values.  Backward: dx = dlogits W in the activation
+    dtype, dW = dlogits^T x and db = sum dlogits in fp32."""
+
+    @staticmethod
+    def forward(ctx, x, W, b):
+        Wc = W.to(x.dtype).contiguous()
+        if x.dtype == torch.float32:
+            y = torch.mm(x, Wc.t())
+        else:
+            y = torch.mm(x, Wc.t(), out_dtype=torch.float32)
+        if b is not None:
+            y.add_(b.float())
+        ctx.save_for_backward(x, Wc)
+        ctx.meta = (W.dtype, None if b is None else b.dtype)
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        x, Wc = ctx.saved_tensors
+        w_dtype, b_dtype = ctx.meta
+        dy = dy.contiguous()
+        dyc = dy if x.dtype == torch.float32 else dy.to(x.dtype)
+        dx = dW = db = None
+        if ctx.needs_input_grad[0]:
+            dx = torch.mm(dyc, Wc)
+        if ctx.needs_input_grad[1]:
+            if x.dtype == torch.float32:
+                dW = torch.mm(dyc.t(), x)
+            else:
+                dW = torch.mm(dyc.t(), x, out_dtype=torch.float32)
+            dW = dW.to(w_dtype)
+        if b_dtype is not None and ctx.needs_input_grad[2]:
+            db = dy.sum(0).to(b_dtype)
+        return dx, dW, db
+
+
+def router_token_logits(h: torch.Tensor, W: torch.Tensor, b: Optional[torch.Tensor]) -> torch.Tensor:
+    """Per-token router logits (B*T, C) in fp32 (router.py:294); see _TokenRouterLinear."""
     L.require_gpu(h, W)
-    x = h.reshape(-1, h.shape[-1]).float()
-    return torch.nn.functional.linear(x, W.float(), None if b is None else b.float())
+    x = h.reshape(-1, h.shape[-1])
+    if x.dtype not in (torch.float32, torch.bfloat16):
+        x = x.float()
+    return _TokenRouterLinear.apply(x.contiguous(), W, b)
 
 
 def token_routed_attention(q, routed_memory, wk, wv, idx, chapter_weights, *, tokens_per_chapter: int,

@@ -1,10 +1,11 @@
 """ChapterRouter with the reference's module API, running on libmoc kernels.
 
 Mirrors memory_transformer/router.py (constructor :28-68, forward :70-156,
-route_token_level :262-340, compute_total_router_loss :490-527).  Logits are
-computed in fp32 (mean-pool + linear kernels) and the softmax / shared-prefix
-mask / top-k / renormalisation chain is one HIP kernel per row with a HIP
-backward.  Top-k order: logit descending, equal logits by ascending chapter id.
+route_token_level :262-340, compute_total_router_loss :490-527).  Sequence
+logits are computed in fp32 (mean-pool + linear kernels); per-token logits are
+fp32 results of a GEMM whose operands are in the activation dtype.  The softmax /
+shared-prefix mask / top-k / renormalisation chain is one HIP kernel per row with
+a HIP backward.  Top-k order: logit descending, equal logits by ascending chapter id.
 """
 
 from __future__ import annotations
