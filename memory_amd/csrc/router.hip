@@ -315,7 +315,7 @@ __global__ void prepend_bwd_kernel(const float* __restrict__ w, const float* __r
 // pooled[b, :] = sum_l coef[l] * h[b, l, :]   (coef == nullptr: mean over L).
 // grid (B, nsplit), 128 threads: thread t sums 8-column chunks t, t + 128, ... of
 // rows [l0, l1) with several 16/32-byte loads in flight; partials [nsplit][B][d]
-// are reduced by pool_reduce.  d % 8 == 0.
+// are reduced by pool_reduce.  d % 8 == 0 and 32-byte aligned rows (else pool_partial_cols).
 constexpr int kPoolThreads = 128;
 template <typename T>
 __global__ __launch_bounds__(kPoolThreads) void pool_partial_kernel(const T* __restrict__ h, int64_t L, int64_t d,
@@ -350,6 +350,32 @@ __global__ __launch_bounds__(kPoolThreads) void pool_partial_kernel(const T* __r
     float* dst = part + ((int64_t)split * gridDim.x + b) * d + c8;
     *reinterpret_cast<f32x4*>(dst) = f32x4{acc[0], acc[1], acc[2], acc[3]};
     *reinterpret_cast<f32x4*>(dst + 4) = f32x4{acc[4], acc[5], acc[6], acc[7]};
+  }
+}
+
+// pool_partial for any d (rows need not be 16-byte aligned): thread t sums single
+// columns t, t + 128, ... with coalesced 4-byte loads, 8 rows in flight.
+template <typename T>
+__global__ __launch_bounds__(kPoolThreads) void pool_partial_cols_kernel(const T* __restrict__ h, int64_t L,
+                                                                         int64_t d, const float* __restrict__ coef,
+                                                                         int rows_per_split, float* __restrict__ part) {
+  const int64_t b = blockIdx.x;
+  const int split = blockIdx.y;
+  const int64_t l0 = (int64_t)split * rows_per_split;
+  const int64_t l1 = min((int64_t)L, l0 + rows_per_split);
+  for (int64_t c = threadIdx.x; c < d; c += kPoolThreads) {
+    const T* hb = h + b * L * d + c;
+    float acc = 0.f;
+    int64_t l = l0;
+    for (; l + 8 <= l1; l += 8) {
+      float v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = to_f(hb[(l + u) * d]);
+#pragma unroll
+      for (int u = 0; u < 8; ++u) acc += (coef ? coef[l + u] : 1.f) * v[u];
+    }
+    for (; l < l1; ++l) acc += (coef ? coef[l] : 1.f) * to_f(hb[l * d]);
+    part[((int64_t)split * gridDim.x + b) * d + c] = acc;
   }
 }
 
@@ -591,14 +617,23 @@ int moc_router_pool(const void* h, int dtype, int64_t B, int64_t L, int64_t d, c
   MOC_REQUIRE(h && pooled && workspace, MOC_ERR_ARG, "moc_router_pool: null pointer");
   MOC_REQUIRE(B >= 0 && L > 0 && d > 0, MOC_ERR_ARG, "moc_router_pool: bad shape");
   MOC_REQUIRE(workspace_bytes >= moc_router_pool_workspace(B, L, d), MOC_ERR_ARG, "moc_router_pool: workspace too small");
-  MOC_REQUIRE(d % 8 == 0, MOC_ERR_UNSUPPORTED, "moc_router_pool: d=%lld must be a multiple of 8", (long long)d);
   MOC_REQUIRE(B < 65536, MOC_ERR_UNSUPPORTED, "moc_router_pool: B=%lld too large", (long long)B);
   if (B == 0) return MOC_OK;
   const int nsplit = pool_splits(B, L);
   const int rows = (int)((L + nsplit - 1) / nsplit);
   dim3 grid((unsigned)B, (unsigned)nsplit);
   float* part = (float*)workspace;
-  if (dtype == MOC_F32)
+  const bool vec = d % 8 == 0 && ((uintptr_t)h & 31) == 0;
+  if (!vec) {
+    if (dtype == MOC_F32)
+      hipLaunchKernelGGL(pool_partial_cols_kernel<float>, grid, dim3(kPoolThreads), 0, stream, (const float*)h, L, d,
+                         coef, rows, part);
+    else if (dtype == MOC_BF16)
+      hipLaunchKernelGGL(pool_partial_cols_kernel<bf16>, grid, dim3(kPoolThreads), 0, stream, (const bf16*)h, L, d,
+                         coef, rows, part);
+    else
+      return set_error(MOC_ERR_UNSUPPORTED, "moc_router_pool: dtype %d", dtype);
+  } else if (dtype == MOC_F32)
     hipLaunchKernelGGL(pool_partial_kernel<float>, grid, dim3(kPoolThreads), 0, stream, (const float*)h, L, d, coef,
                        rows, part);
   else if (dtype == MOC_BF16)

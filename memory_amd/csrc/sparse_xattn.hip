@@ -616,29 +616,32 @@ struct UnitRows {
   int u, hk, gid, p0, nrows;
 };
 
+// The grid never exceeds max_u * nhk units, so u < max_u and the plan reads below are in
+// bounds before the n_uniq check; issuing them together saves a dependent round trip.
 __device__ __forceinline__ bool unit_setup(UnitRows& ur, const int32_t* uniq, const int32_t* n_uniq,
-                                           const int32_t* csr_off, int hk0, int nhk, int G) {
+                                           const int32_t* csr_off, int hk0, int nhk, int G, int64_t max_u) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int64_t unit = (int64_t)blockIdx.x * kUnitWaves + wave;
   ur.u = (int)(unit / nhk);
-  if (ur.u >= n_uniq[0]) return false;
+  if (ur.u >= max_u) return false;
+  const int nu = n_uniq[0];
   ur.hk = hk0 + (int)(unit % nhk);
   ur.gid = uniq[ur.u];
   ur.p0 = csr_off[ur.u];
   ur.nrows = (csr_off[ur.u + 1] - ur.p0) * G;
-  return true;
+  return ur.u < nu;
 }
 
 __global__ __launch_bounds__(64 * kUnitWaves) void sparse_fwd_unit_kernel(
     const bf16* __restrict__ q, int HQ, const bf16* __restrict__ k, const bf16* __restrict__ v, int64_t cs,
     int64_t hs, int64_t rs, int HK, const int32_t* __restrict__ uniq, const int32_t* __restrict__ n_uniq,
-    const int32_t* __restrict__ csr_off, const int32_t* __restrict__ csr_edge, int S, int hk0, int nhk, int hq_off,
-    int rpe, float scale_log2, float* __restrict__ o_part, float* __restrict__ lse_part) {
+    const int32_t* __restrict__ csr_off, const int32_t* __restrict__ csr_edge, int64_t max_u, int S, int hk0,
+    int nhk, int hq_off, int rpe, float scale_log2, float* __restrict__ o_part, float* __restrict__ lse_part) {
   using Tile = SwzTile<bf16, 64>;
   __shared__ __attribute__((aligned(16))) char sVall[kUnitWaves][64 * 64 * 2];
   const int G = HQ / HK;
   UnitRows ur;
-  if (!unit_setup(ur, uniq, n_uniq, csr_off, hk0, nhk, G)) return;
+  if (!unit_setup(ur, uniq, n_uniq, csr_off, hk0, nhk, G, max_u)) return;
   const int lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
   char* sV = sVall[threadIdx.x >> 6];
   const int64_t kv0 = (int64_t)ur.gid * cs + (int64_t)ur.hk * hs;
@@ -732,74 +735,87 @@ __global__ __launch_bounds__(64 * kUnitWaves) void sparse_fwd_unit_kernel(
   }
 }
 
-// Backward of one unit.  Per 32-row block: S = Q K^T and dPu = dO V^T with lane = key
-// (accumulator layout, rows 16 qb + 4 g + x), P and dS in registers, then
+// Backward of one unit on a workgroup of two waves, wave w owning keys 32 w .. 32 w + 31
+// (K / V fragments and the dK / dV accumulators split in half, so two units fit per
+// SIMD).  Per 32-row block: S = Q K^T and dPu = dO V^T with lane = key (accumulator
+// layout, rows 16 qb + 4 g + x), P and dS in registers, then
 //   dV^T += dO^T P,  dK^T += Q^T dS      (A = transposing reads of the staged rows)
-//   dQ^T  = K^T dS^T                      (dS staged key-major, both operands transposed)
-// mode 0 computes the per-chapter softmax delta sum_j P_j dPu_j itself and writes it
-// to delta_row (the per edge-row dO . o_s that moc_sparse_dw sums into dw).
-__global__ __launch_bounds__(64 * kUnitWaves, 1) void sparse_bwd_unit_kernel(
+//   dQ^T  = K^T dS^T over all 64 keys     (wave w: dims 32 w .. 32 w + 31)
+// with the per-row sums over the chapter's 64 keys (mode 0 softmax delta sum_j P_j dPu_j,
+// the d log-weight row sums of modes 2-3) added from the two waves' halves in a fixed
+// order.  mode 0 writes the delta to delta_row (the per edge-row dO . o_s that
+// moc_sparse_dw sums into dw).
+constexpr int kBwdWaves = 2;
+
+__global__ __launch_bounds__(64 * kBwdWaves) void sparse_bwd_unit_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ dout, int HQ, const bf16* __restrict__ k,
     const bf16* __restrict__ v, int64_t cs, int64_t hs, int64_t rs, int HK, const int32_t* __restrict__ uniq,
     const int32_t* __restrict__ n_uniq, const int32_t* __restrict__ csr_off, const int32_t* __restrict__ csr_edge,
-    int S, int hk0, int nhk, int hq_off, int rpe, int mode, const float* __restrict__ lse_row,
+    int64_t max_u, int S, int hk0, int nhk, int hq_off, int rpe, int mode, const float* __restrict__ lse_row,
     float* __restrict__ delta_row, const float* __restrict__ w, float scale_log2, float scale, bf16* __restrict__ dk,
     bf16* __restrict__ dv, int64_t ocs, int64_t ohs, int64_t ors, float* __restrict__ dq_part,
     float* __restrict__ dlog) {
   using Tile = SwzTile<bf16, 64>;
   constexpr int kKB = 64 * 64 * 2, kRB = 32 * 64 * 2;
-  struct WaveLds {
-    char k[kKB];     // K [key][dim]
-    char q[kRB];     // Q rows of the block [row][dim]
-    char d[kRB];     // dO rows
-    char ds[kRB];    // dS [key][row] (DsTile)
-    float lse[32], del[32], wr[32];
-    int er[32];
-  };
-  __shared__ __attribute__((aligned(16))) WaveLds sAll[kUnitWaves];
+  __shared__ __attribute__((aligned(16))) char sK[kKB];    // K [key][dim]
+  __shared__ __attribute__((aligned(16))) char sQ[kRB];    // Q rows of the block [row][dim]
+  __shared__ __attribute__((aligned(16))) char sD[kRB];    // dO rows
+  __shared__ __attribute__((aligned(16))) char sDS[kRB];   // dS [key][row] (DsTile)
+  __shared__ float sLse[32], sDel[32], sWr[32], sPart[kBwdWaves][2][32];
+  __shared__ int sEr[32];
   const int G = HQ / HK;
-  UnitRows ur;
-  if (!unit_setup(ur, uniq, n_uniq, csr_off, hk0, nhk, G)) return;
+  const int64_t unit = blockIdx.x;
+  const int u = (int)(unit / nhk);
+  if (u >= max_u) return;                 // whole workgroup (before any barrier)
+  const int nu = n_uniq[0];
+  const int hk = hk0 + (int)(unit % nhk);
+  const int gid = uniq[u];
+  const int p0 = csr_off[u];
+  const int nrows = (csr_off[u + 1] - p0) * G;
+  if (u >= nu) return;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
-  WaveLds& L = sAll[threadIdx.x >> 6];
-  const int64_t kv0 = (int64_t)ur.gid * cs + (int64_t)ur.hk * hs;
-  // K, V as the B operands of S / dPu (lane = key); K also staged for K^T reads
-  bf16x8 kf[4][2], vf[4][2];
+  const int key0 = 32 * wave;
+  const int64_t kv0 = (int64_t)gid * cs + (int64_t)hk * hs;
+  // K, V of this wave's keys as the B operands of S / dPu (lane = key); K staged for K^T
+  bf16x8 kf[2][2], vf[2][2];
 #pragma unroll
-  for (int kb = 0; kb < 4; ++kb)
+  for (int j = 0; j < 2; ++j)
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
-      const int64_t off = kv0 + (16 * kb + c16) * rs + 32 * ks + 8 * g;
-      kf[kb][ks] = Load8<bf16, bf16>::run(k + off);
-      vf[kb][ks] = Load8<bf16, bf16>::run(v + off);
+      const int64_t off = kv0 + (key0 + 16 * j + c16) * rs + 32 * ks + 8 * g;
+      kf[j][ks] = Load8<bf16, bf16>::run(k + off);
+      vf[j][ks] = Load8<bf16, bf16>::run(v + off);
     }
 #pragma unroll
-  for (int kb = 0; kb < 4; ++kb)
+  for (int j = 0; j < 2; ++j)
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks)
-      *reinterpret_cast<bf16x8*>(L.k + Tile::off(16 * kb + c16, 32 * ks + 8 * g)) = kf[kb][ks];
-  f32x4 dkt[4][4], dvt[4][4];   // [db][kb]: lane = key 16 kb + c16, dims 16 db + 4 g + x
+      *reinterpret_cast<bf16x8*>(sK + Tile::off(key0 + 16 * j + c16, 32 * ks + 8 * g)) = kf[j][ks];
+  f32x4 dkt[4][2], dvt[4][2];   // [db][j]: lane = key key0 + 16 j + c16, dims 16 db + 4 g + x
 #pragma unroll
   for (int db = 0; db < 4; ++db)
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-      dkt[db][kb] = f32x4{0.f, 0.f, 0.f, 0.f};
-      dvt[db][kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < 2; ++j) {
+      dkt[db][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+      dvt[db][j] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
-  for (int r0 = 0; r0 < ur.nrows; r0 += 32) {
-    const bool two = r0 + 16 < ur.nrows;
-    // ---- rows as A operands (lane = row 16 qb + c16), staged for the transposing reads
-    bf16x8 qa[2][2], da[2][2];
-    int erow_a[2];
+  // rows of a block as A operands (lane = row 16 qb + c16, both waves) and the per-row
+  // constants (wave 0, one lane per row); block r0 + 32 is fetched while r0 computes
+  bf16x8 qa[2][2], da[2][2];
+  int erow_n[2];
+  float c_lse = INFINITY, c_del = 0.f, c_w = 0.f;
+  int c_er = -1;
+  auto fetch_rows = [&](int r0) {
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb) {
       const int r = r0 + 16 * qb + c16;
-      erow_a[qb] = -1;
+      erow_n[qb] = -1;
       qa[qb][0] = qa[qb][1] = da[qb][0] = da[qb][1] = zero_frag<bf16>();
-      if (r < ur.nrows) {
-        const int e = csr_edge[ur.p0 + r / G];
-        const int hq = ur.hk * G + r % G;
-        erow_a[qb] = e * rpe + (hq - hq_off);
+      if (r < nrows) {
+        const int e = csr_edge[p0 + r / G];
+        const int hq = hk * G + r % G;
+        erow_n[qb] = e * rpe + (hq - hq_off);
         const int64_t off = ((int64_t)(e / S) * HQ + hq) * kSpDh + 8 * g;
         qa[qb][0] = Load8<bf16, bf16>::run(q + off);
         qa[qb][1] = Load8<bf16, bf16>::run(q + off + 32);
@@ -807,98 +823,107 @@ __global__ __launch_bounds__(64 * kUnitWaves, 1) void sparse_bwd_unit_kernel(
         da[qb][1] = Load8<bf16, bf16>::run(dout + off + 32);
       }
     }
-    // ---- per-row constants, one lane per row
-    if (lane < 32) {
-      const int r = r0 + lane;
-      float lse = INFINITY, del = 0.f, wv = 0.f;
-      int er = -1;
-      if (r < ur.nrows) {
-        const int e = csr_edge[ur.p0 + r / G];
-        const int hr = ur.hk * G + r % G - hq_off;
-        er = e * rpe + hr;
-        if (mode == 0) {
-          lse = lse_row[er];
-          wv = w[e];
-        } else {
-          const int64_t trow = (int64_t)(e / S) * rpe + hr;
-          lse = lse_row[trow];
-          del = delta_row[trow];
-          wv = sp_logw(mode, w ? w[e] : 1.f);
+    c_lse = INFINITY;
+    c_del = c_w = 0.f;
+    c_er = -1;
+    const int r = r0 + (lane & 31);
+    if (wave == 0 && lane < 32 && r < nrows) {
+      const int e = csr_edge[p0 + r / G];
+      const int hr = hk * G + r % G - hq_off;
+      c_er = e * rpe + hr;
+      if (mode == 0) {
+        c_lse = lse_row[c_er];
+        c_w = w[e];
+      } else {
+        const int64_t trow = (int64_t)(e / S) * rpe + hr;
+        c_lse = lse_row[trow];
+        c_del = delta_row[trow];
+        c_w = sp_logw(mode, w ? w[e] : 1.f);
+      }
+    }
+  };
+  fetch_rows(0);
+  for (int r0 = 0; r0 < nrows; r0 += 32) {
+    const bool two = r0 + 16 < nrows;
+    const int erow_a[2] = {erow_n[0], erow_n[1]};
+    if (wave == 0 && lane < 32) {
+      sLse[lane] = c_lse;
+      sDel[lane] = c_del;
+      sWr[lane] = c_w;
+      sEr[lane] = c_er;
+    }
+    // wave w stages rows 16 w .. 16 w + 15
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb)
+      if (qb == wave) {
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+          *reinterpret_cast<bf16x8*>(sQ + Tile::off(16 * qb + c16, 32 * ks + 8 * g)) = qa[qb][ks];
+          *reinterpret_cast<bf16x8*>(sD + Tile::off(16 * qb + c16, 32 * ks + 8 * g)) = da[qb][ks];
         }
       }
-      L.lse[lane] = lse;
-      L.del[lane] = del;
-      L.wr[lane] = wv;
-      L.er[lane] = er;
-    }
+    // ---- S and dPu for this wave's keys (lane = key, rows 16 qb + 4 g + x)
+    f32x4 sc[2][2], dp[2][2];
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb)
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        *reinterpret_cast<bf16x8*>(L.q + Tile::off(16 * qb + c16, 32 * ks + 8 * g)) = qa[qb][ks];
-        *reinterpret_cast<bf16x8*>(L.d + Tile::off(16 * qb + c16, 32 * ks + 8 * g)) = da[qb][ks];
-      }
-    // ---- S and dPu (lane = key 16 kb + c16, rows 16 qb + 4 g + x)
-    f32x4 sc[2][4], dp[2][4];
-#pragma unroll
-    for (int qb = 0; qb < 2; ++qb)
-#pragma unroll
-      for (int kb = 0; kb < 4; ++kb) {
-        sc[qb][kb] = f32x4{0.f, 0.f, 0.f, 0.f};
-        dp[qb][kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int j = 0; j < 2; ++j) {
+        sc[qb][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+        dp[qb][j] = f32x4{0.f, 0.f, 0.f, 0.f};
         if (qb == 0 || two) {
 #pragma unroll
           for (int ks = 0; ks < 2; ++ks) {
-            mma(sc[qb][kb], qa[qb][ks], kf[kb][ks]);
-            mma(dp[qb][kb], da[qb][ks], vf[kb][ks]);
+            mma(sc[qb][j], qa[qb][ks], kf[j][ks]);
+            mma(dp[qb][j], da[qb][ks], vf[j][ks]);
           }
         }
       }
-    wave_lds_sync();
+    if (r0 + 32 < nrows) fetch_rows(r0 + 32);
+    __syncthreads();   // (1) staged rows, constants (and K) visible to both waves
     float lr[2][4], dr[2][4], wr[2][4];
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb)
 #pragma unroll
       for (int x = 0; x < 4; ++x) {
         const int rr = 16 * qb + 4 * g + x;
-        lr[qb][x] = L.lse[rr];
-        dr[qb][x] = L.del[rr];
-        wr[qb][x] = L.wr[rr];
+        lr[qb][x] = sLse[rr];
+        dr[qb][x] = sDel[rr];
+        wr[qb][x] = sWr[rr];
       }
-    // ---- P (in sc)
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb)
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb)
+      for (int j = 0; j < 2; ++j)
 #pragma unroll
         for (int x = 0; x < 4; ++x)
-          sc[qb][kb][x] = exp2f(sc[qb][kb][x] * scale_log2 + (mode == 0 ? 0.f : wr[qb][x]) - lr[qb][x]);
+          sc[qb][j][x] = exp2f(sc[qb][j][x] * scale_log2 + (mode == 0 ? 0.f : wr[qb][x]) - lr[qb][x]);
     if (mode == 0) {
-      // per-chapter softmax delta of each row: sum over the 64 keys of P dPu
+      // per-chapter softmax delta: this wave's 32 keys, then both halves in order
 #pragma unroll
       for (int qb = 0; qb < 2; ++qb)
 #pragma unroll
         for (int x = 0; x < 4; ++x) {
-          float t = 0.f;
-#pragma unroll
-          for (int kb = 0; kb < 4; ++kb) t += sc[qb][kb][x] * dp[qb][kb][x];
+          float t = sc[qb][0][x] * dp[qb][0][x] + sc[qb][1][x] * dp[qb][1][x];
           t += __shfl_xor(t, 1, 16);
           t += __shfl_xor(t, 2, 16);
           t += __shfl_xor(t, 4, 16);
           t += __shfl_xor(t, 8, 16);
-          dr[qb][x] = t;
+          if (c16 == 0) sPart[wave][0][16 * qb + 4 * g + x] = t;
         }
-      if (c16 == 0) {
+      __syncthreads();   // (2)
 #pragma unroll
-        for (int qb = 0; qb < 2; ++qb)
+      for (int qb = 0; qb < 2; ++qb)
 #pragma unroll
-          for (int x = 0; x < 4; ++x) {
-            const int er = L.er[16 * qb + 4 * g + x];
-            if (er >= 0) delta_row[er] = dr[qb][x];
-          }
+        for (int x = 0; x < 4; ++x) {
+          const int rr = 16 * qb + 4 * g + x;
+          dr[qb][x] = sPart[0][0][rr] + sPart[1][0][rr];
+        }
+      if (wave == 0 && lane < 32) {
+        const int er = sEr[lane];
+        if (er >= 0) delta_row[er] = sPart[0][0][lane] + sPart[1][0][lane];
       }
     }
-    bf16x8 pa[4], sa[4];
+    bf16x8 pa[2], sa[2];
     float rsum[2][4];
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb)
@@ -907,35 +932,35 @@ __global__ __launch_bounds__(64 * kUnitWaves, 1) void sparse_bwd_unit_kernel(
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb)
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb)
+      for (int j = 0; j < 2; ++j)
 #pragma unroll
         for (int x = 0; x < 4; ++x) {
-          const float p = sc[qb][kb][x];
+          const float p = sc[qb][j][x];
           const float pw = mode == 0 ? wr[qb][x] * p : p;
-          const float ds = pw * (dp[qb][kb][x] - dr[qb][x]);
+          const float ds = pw * (dp[qb][j][x] - dr[qb][x]);
           rsum[qb][x] += ds;
-          pa[kb][4 * qb + x] = (bf16)pw;
-          sa[kb][4 * qb + x] = (bf16)ds;
+          pa[j][4 * qb + x] = (bf16)pw;
+          sa[j][4 * qb + x] = (bf16)ds;
         }
     // ---- dV^T += dO^T P, dK^T += Q^T dS
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
-      const bf16x8 ad = tr_frag_mk<Tile>(L.d, 0, 16 * db, lane);
-      const bf16x8 aq = tr_frag_mk<Tile>(L.q, 0, 16 * db, lane);
+      const bf16x8 ad = tr_frag_mk<Tile>(sD, 0, 16 * db, lane);
+      const bf16x8 aq = tr_frag_mk<Tile>(sQ, 0, 16 * db, lane);
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb) {
-        mma(dvt[db][kb], ad, pa[kb]);
-        mma(dkt[db][kb], aq, sa[kb]);
+      for (int j = 0; j < 2; ++j) {
+        mma(dvt[db][j], ad, pa[j]);
+        mma(dkt[db][j], aq, sa[j]);
       }
     }
-    // ---- dS key-major for dQ
+    // ---- dS key-major for dQ, d log-weight row sums
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-      const int key = 16 * kb + c16;
-      const bf16x4 lo = {sa[kb][0], sa[kb][1], sa[kb][2], sa[kb][3]};
-      const bf16x4 hi = {sa[kb][4], sa[kb][5], sa[kb][6], sa[kb][7]};
-      *reinterpret_cast<bf16x4*>(L.ds + DsTile::off(key, 4 * g)) = lo;
-      *reinterpret_cast<bf16x4*>(L.ds + DsTile::off(key, 16 + 4 * g)) = hi;
+    for (int j = 0; j < 2; ++j) {
+      const int key = key0 + 16 * j + c16;
+      const bf16x4 lo = {sa[j][0], sa[j][1], sa[j][2], sa[j][3]};
+      const bf16x4 hi = {sa[j][4], sa[j][5], sa[j][6], sa[j][7]};
+      *reinterpret_cast<bf16x4*>(sDS + DsTile::off(key, 4 * g)) = lo;
+      *reinterpret_cast<bf16x4*>(sDS + DsTile::off(key, 16 + 4 * g)) = hi;
     }
     if (dlog) {
 #pragma unroll
@@ -947,52 +972,54 @@ __global__ __launch_bounds__(64 * kUnitWaves, 1) void sparse_bwd_unit_kernel(
           t += __shfl_xor(t, 2, 16);
           t += __shfl_xor(t, 4, 16);
           t += __shfl_xor(t, 8, 16);
-          const int er = L.er[16 * qb + 4 * g + x];
-          if (c16 == 0 && er >= 0) dlog[er] = t;
+          if (c16 == 0) sPart[wave][1][16 * qb + 4 * g + x] = t;
         }
     }
-    wave_lds_sync();
-    // ---- dQ^T = K^T dS^T: lane = row 16 qb + c16, dims 16 db + 4 g + x
-    f32x4 dq[4][2];
+    __syncthreads();   // (3) dS and the row-sum halves visible
+    if (dlog && wave == 0 && lane < 32) {
+      const int er = sEr[lane];
+      if (er >= 0) dlog[er] = sPart[0][1][lane] + sPart[1][1][lane];
+    }
+    // ---- dQ^T = K^T dS^T for dims 32 wave .. + 31: lane = row 16 qb + c16, dims 16 db + 4 g + x
+    f32x4 dq[2][2];
 #pragma unroll
-    for (int db = 0; db < 4; ++db)
+    for (int i = 0; i < 2; ++i)
 #pragma unroll
-      for (int qb = 0; qb < 2; ++qb) dq[db][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int qb = 0; qb < 2; ++qb) dq[i][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
       bf16x8 bs[2];
 #pragma unroll
-      for (int qb = 0; qb < 2; ++qb) bs[qb] = tr_frag_mk<DsTile>(L.ds, 32 * ks, 16 * qb, lane);
+      for (int qb = 0; qb < 2; ++qb) bs[qb] = tr_frag_mk<DsTile>(sDS, 32 * ks, 16 * qb, lane);
 #pragma unroll
-      for (int db = 0; db < 4; ++db) {
-        const bf16x8 ak = tr_frag_mk<Tile>(L.k, 32 * ks, 16 * db, lane);
+      for (int i = 0; i < 2; ++i) {
+        const bf16x8 ak = tr_frag_mk<Tile>(sK, 32 * ks, 32 * wave + 16 * i, lane);
 #pragma unroll
         for (int qb = 0; qb < 2; ++qb)
-          if (qb == 0 || two) mma(dq[db][qb], ak, bs[qb]);
+          if (qb == 0 || two) mma(dq[i][qb], ak, bs[qb]);
       }
     }
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb) {
       if (erow_a[qb] < 0) continue;
-      float* dst = dq_part + (int64_t)erow_a[qb] * kSpDh + 4 * g;
+      float* dst = dq_part + (int64_t)erow_a[qb] * kSpDh + 32 * wave + 4 * g;
 #pragma unroll
-      for (int db = 0; db < 4; ++db) *reinterpret_cast<f32x4*>(dst + 16 * db) = dq[db][qb] * scale;
+      for (int i = 0; i < 2; ++i) *reinterpret_cast<f32x4*>(dst + 16 * i) = dq[i][qb] * scale;
     }
-    wave_lds_sync();
   }
-  // ---- dK = scale dK^T^T, dV: lane = key, 4 consecutive dims per store
-  bf16* dkb = dk + (int64_t)ur.gid * ocs + (int64_t)ur.hk * ohs;
-  bf16* dvb = dv + (int64_t)ur.gid * ocs + (int64_t)ur.hk * ohs;
+  // ---- dK = scale (dK^T)^T, dV: lane = key, 4 consecutive dims per store
+  bf16* dkb = dk + (int64_t)gid * ocs + (int64_t)hk * ohs;
+  bf16* dvb = dv + (int64_t)gid * ocs + (int64_t)hk * ohs;
 #pragma unroll
-  for (int kb = 0; kb < 4; ++kb)
+  for (int j = 0; j < 2; ++j)
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
-      const int64_t off = (int64_t)(16 * kb + c16) * ors + 16 * db + 4 * g;
+      const int64_t off = (int64_t)(key0 + 16 * j + c16) * ors + 16 * db + 4 * g;
       bf16x4 a, b;
 #pragma unroll
       for (int x = 0; x < 4; ++x) {
-        a[x] = (bf16)(dkt[db][kb][x] * scale);
-        b[x] = (bf16)dvt[db][kb][x];
+        a[x] = (bf16)(dkt[db][j][x] * scale);
+        b[x] = (bf16)dvt[db][j][x];
       }
       *reinterpret_cast<bf16x4*>(dkb + off) = a;
       *reinterpret_cast<bf16x4*>(dvb + off) = b;
@@ -1032,7 +1059,8 @@ int moc_sparse_fwd(int dtype, const void* q, int64_t ntok, int HQ, const void* k
     const int64_t units = max_u * nhk;
     hipLaunchKernelGGL(sparse_fwd_unit_kernel, dim3((unsigned)((units + kUnitWaves - 1) / kUnitWaves)),
                        dim3(64 * kUnitWaves), 0, stream, (const bf16*)q, HQ, (const bf16*)k, (const bf16*)v, cs, hs,
-                       rs, HK, uniq, n_uniq, csr_off, csr_edge, S, hk0, nhk, hq_off, rpe, sl2, o_part, lse_part);
+                       rs, HK, uniq, n_uniq, csr_off, csr_edge, max_u, S, hk0, nhk, hq_off, rpe, sl2, o_part,
+                       lse_part);
     return check_launch("sparse_fwd_unit_kernel");
   } else if (dtype == MOC_F32)
     hipLaunchKernelGGL(sparse_fwd_kernel<float>, grid, dim3(sp_threads<float>()), 0, stream, (const float*)q, HQ,
@@ -1105,10 +1133,10 @@ int moc_sparse_bwd(int dtype, const void* q, const void* dout, int64_t ntok, int
                 "moc_sparse_bwd: bf16 needs 16-byte aligned q/dout/k/v/dq_part, 8-byte aligned dk/dv, input strides "
                 "that are multiples of 8 and output strides that are multiples of 4");
     const int64_t units = max_u * nhk;
-    hipLaunchKernelGGL(sparse_bwd_unit_kernel, dim3((unsigned)((units + kUnitWaves - 1) / kUnitWaves)),
-                       dim3(64 * kUnitWaves), 0, stream, (const bf16*)q, (const bf16*)dout, HQ, (const bf16*)k,
-                       (const bf16*)v, cs, hs, rs, HK, uniq, n_uniq, csr_off, csr_edge, S, hk0, nhk, hq_off, rpe,
-                       mode, lse_row, delta_row, w, sl2, scale, (bf16*)dk, (bf16*)dv, ocs, ohs, ors, dq_part, dlog);
+    hipLaunchKernelGGL(sparse_bwd_unit_kernel, dim3((unsigned)units), dim3(64 * kBwdWaves), 0, stream, (const bf16*)q, (const bf16*)dout, HQ, (const bf16*)k,
+                       (const bf16*)v, cs, hs, rs, HK, uniq, n_uniq, csr_off, csr_edge, max_u, S, hk0, nhk, hq_off,
+                       rpe, mode, lse_row, delta_row, w, sl2, scale, (bf16*)dk, (bf16*)dv, ocs, ohs, ors, dq_part,
+                       dlog);
     return check_launch("sparse_bwd_unit_kernel");
   } else if (dtype == MOC_F32)
     hipLaunchKernelGGL(sparse_bwd_kernel<float>, grid, dim3(sp_threads<float>()), 0, stream, (const float*)q,

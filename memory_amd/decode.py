@@ -31,7 +31,7 @@ class MemoryDecodeCache:
         C, T = int(num_chapters), int(tokens_per_chapter)
         self.num_chapters, self.T, self.HK, self.dtype = C, T, int(num_kv_heads), dtype
         with torch.no_grad():
-            plan = ops.chapter_plan(torch.arange(C, device=bank.device, dtype=torch.int32), C)
+            plan = ops.identity_plan(C, bank.device)
             code = ops.norm_code(norm_type)
             mean = rstd = None
             if code:

@@ -71,6 +71,33 @@ def normalize_shared_routed_memory_vectors(memory: torch.Tensor, *, num_shared_c
     raise ValueError(f"Unsupported norm_type: {norm_type}")
 
 
+class _SplitRows(torch.autograd.Function):
+    """(x[:n], x[n:]) whose backward writes both row-block gradients into one new tensor
+    with a single concatenation (autograd's slice backward zero-fills a full-size
+    gradient per slice, copies into it and sums the two)."""
+
+    @staticmethod
+    def forward(ctx, x, n):
+        ctx.n, ctx.shape = n, x.shape
+        return x[:n], x[n:]
+
+    @staticmethod
+    def backward(ctx, ga, gb):
+        n, shape = ctx.n, ctx.shape
+        ref = ga if ga is not None else gb
+        if ga is None:
+            ga = ref.new_zeros((n,) + tuple(shape[1:]))
+        if gb is None:
+            gb = ref.new_zeros((shape[0] - n,) + tuple(shape[1:]))
+        return torch.cat([ga, gb], 0), None
+
+
+def split_rows(x: torch.Tensor, n: int):
+    if not x.requires_grad:
+        return x[:n], x[n:]
+    return _SplitRows.apply(x, n)
+
+
 class RoutedMemoryLayer(nn.Module):
     """One sequence-routed memory sublayer (router + memory cross-attention).
 
@@ -151,14 +178,15 @@ class TokenRoutedMemoryLayer(nn.Module):
         S, T = self.num_shared_chapters, self.tokens_per_chapter
         idx, w, losses = self.router.route_token_level(hidden_states, return_losses=return_losses,
                                                        exclude_prefix_chapters=S)
-        st = S * T
-        shared = bank[:st] if st > 0 else None
-        routed = bank[st:] if st < bank.shape[0] else None
-        if self.normalize and shared is not None and routed is not None and shared.numel() and routed.numel():
-            merged = normalize_shared_routed_memory_vectors(bank.unsqueeze(0), num_shared_chapters=S,
-                                                            tokens_per_chapter=T, norm_type=self.norm_type,
-                                                            eps=self.norm_eps).squeeze(0)
-            shared, routed = merged[:st], merged[st:]
+        st = min(S * T, bank.shape[0])
+        src = bank
+        if self.normalize and 0 < st < bank.shape[0]:
+            src = normalize_shared_routed_memory_vectors(bank.unsqueeze(0), num_shared_chapters=S,
+                                                         tokens_per_chapter=T, norm_type=self.norm_type,
+                                                         eps=self.norm_eps).squeeze(0)
+        shared, routed = split_rows(src, st)
+        shared = shared if st > 0 else None
+        routed = routed if st < bank.shape[0] else None
         state = {"shared_memory": shared, "routed_memory": routed,
                  "token_chapter_indices": (idx - S).to(torch.int32), "tokens_per_chapter": T,
                  "routed_scale": self.routed_scaling_factor, "kernel_version": self.kernel_version,

@@ -203,6 +203,16 @@ def chapter_plan(chap: torch.Tensor, num_chapters: int) -> ChapterPlan:
     return ChapterPlan(uniq, n_uniq, edge_u, csr_off, csr_edge, max_u, C)
 
 
+def identity_plan(num_chapters: int, device) -> ChapterPlan:
+    """The plan of edges 0 .. C-1 selecting chapters 0 .. C-1 (every chapter once, in order),
+    written directly: what moc_chapter_plan returns for arange(C)."""
+    C = int(num_chapters)
+    ar = torch.arange(C + 1, device=device, dtype=torch.int32)
+    n_uniq = torch.full((2,), C, device=device, dtype=torch.int32)   # {C, 0} without a host copy
+    n_uniq[1:].zero_()
+    return ChapterPlan(ar[:C], n_uniq, ar[:C], ar, ar[:C], C, C)
+
+
 _NORM = {None: L.MOC_NORM_NONE, "none": L.MOC_NORM_NONE, "rms": L.MOC_NORM_RMS, "layernorm": L.MOC_NORM_LAYERNORM}
 
 
@@ -259,20 +269,27 @@ class _Linear(torch.autograd.Function):
             n_out, n_in = w.shape
             dy2 = dy.reshape(-1, n_out).contiguous()
             x2 = x.reshape(-1, n_in).contiguous()
-            if dy2.dtype == torch.bfloat16 and x2.dtype in (torch.bfloat16, torch.float32) and dy2.is_cuda:
-                R = dy2.shape[0]
-                ws = torch.empty(L.query("moc_linear_wgrad_workspace", R, n_out, n_in) // 4, device=dy2.device,
-                                 dtype=torch.float32)
-                dw = torch.empty(n_out, n_in, device=dy2.device, dtype=w.dtype)
-                call("moc_linear_wgrad", ptr(dy2), ptr(x2), L.dtype_code(x2.dtype), R, n_out, n_in, ptr(ws),
-                     ws.numel() * 4, L.dtype_code(dw.dtype), ptr(dw), stream_ptr(dy2.device))
-            else:
-                dw = torch.matmul(dy2.t().to(x2.dtype), x2).to(w.dtype)
+            dw = linear_wgrad(dy2, x2, w.dtype)
         return dx, dw
 
 
 def linear(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
     return _Linear.apply(x, w)
+
+
+def linear_wgrad(dy: torch.Tensor, x: torch.Tensor, out_dtype: torch.dtype) -> torch.Tensor:
+    """dW = dy^T x for dy [R][N], x [R][K] (row-major, contiguous): the split-row MFMA
+    kernel for bf16 dy (N, K multiples of 8), a plain GEMM otherwise."""
+    R, N = dy.shape
+    K = x.shape[1]
+    if (dy.dtype == torch.bfloat16 and x.dtype in (torch.bfloat16, torch.float32) and dy.is_cuda and N % 8 == 0
+            and K % 8 == 0 and out_dtype in (torch.float32, torch.bfloat16)):
+        ws = torch.empty(L.query("moc_linear_wgrad_workspace", R, N, K) // 4, device=dy.device, dtype=torch.float32)
+        dw = torch.empty(N, K, device=dy.device, dtype=out_dtype)
+        call("moc_linear_wgrad", ptr(dy), ptr(x), L.dtype_code(x.dtype), R, N, K, ptr(ws), ws.numel() * 4,
+             L.dtype_code(out_dtype), ptr(dw), stream_ptr(dy.device))
+        return dw
+    return torch.matmul(dy.t().to(x.dtype), x).to(out_dtype)
 
 
 # ------------------------------------------------------------- routed attention (A)
@@ -425,8 +442,24 @@ class _TokenRouterLinear(torch.autograd.Function):
                 dW = torch.mm(dyc.t(), x, out_dtype=torch.float32)
             dW = dW.to(w_dtype)
         if b_dtype is not None and ctx.needs_input_grad[2]:
-            db = dy.sum(0).to(b_dtype)
+            db = col_sum(dy).to(b_dtype)
         return dx, dW, db
+
+
+def col_sum(x: torch.Tensor) -> torch.Tensor:
+    """Column sums (fp32) of a 2-D fp32 / bf16 matrix on the router's pooling kernels
+    (fixed-order split-row partials, deterministic)."""
+    x = x.contiguous()
+    R, C = x.shape
+    out = torch.empty(C, device=x.device, dtype=torch.float32)
+    if R == 0:
+        return out.zero_()
+    ones = torch.ones(R, device=x.device, dtype=torch.float32)
+    ws_bytes = L.query("moc_router_pool_workspace", 1, R, C)
+    ws = torch.empty(max(1, ws_bytes // 4), device=x.device, dtype=torch.float32)
+    call("moc_router_pool", ptr(x), L.dtype_code(x.dtype), 1, R, C, ptr(ones), ptr(out), ptr(ws), ws_bytes,
+         stream_ptr(x.device))
+    return out
 
 
 def router_token_logits(h: torch.Tensor, W: torch.Tensor, b: Optional[torch.Tensor]) -> torch.Tensor:

@@ -267,7 +267,7 @@ class _TokenRouted(torch.autograd.Function):
         C = Nr // BLOCK
         q = q.contiguous()
         routed = routed.contiguous()
-        all_plan = ops.chapter_plan(torch.arange(C, device=q.device, dtype=torch.int32), C)
+        all_plan = ops.identity_plan(C, q.device)
         wkv = torch.cat([wk, wv], 0).to(dtype).contiguous()
         kt, vt = ops.kv_project(routed, all_plan, BLOCK, wkv, HK, D, None, None, dtype, ("k", "v"))
         S = idx.shape[-1]
@@ -294,7 +294,7 @@ class _TokenRouted(torch.autograd.Function):
         need_r, need_wk, need_wv = ctx.needs_input_grad[1:4]
         dr = dwk = dwv = None
         if need_wk or need_wv:
-            dwkv = torch.matmul(dkv.t(), routed.to(dtype))
+            dwkv = ops.linear_wgrad(dkv, routed, torch.float32 if torch.float32 in (wk_dtype, wv_dtype) else dtype)
             dwk = dwkv[:KV].to(wk_dtype) if need_wk else None
             dwv = dwkv[KV:].to(wv_dtype) if need_wv else None
         if need_r:

@@ -82,7 +82,7 @@ def test_prepend_forward_backward(dev):
     assert_rel(wg.grad.cpu(), wr.grad, 1e-5, "dw")
 
 
-@pytest.mark.parametrize("B,Lq,d,C", [(3, 37, 128, 65), (20, 70, 64, 33), (8, 1024, 768, 4097)])
+@pytest.mark.parametrize("B,Lq,d,C", [(3, 37, 128, 65), (20, 70, 64, 33), (8, 1024, 768, 4097), (2, 33, 100, 17)])
 def test_router_pool_and_linear(dev, B, Lq, d, C):
     print(f"router pool+linear B={B} L={Lq} d={d} C={C}", flush=True)
     h = torch.randn(B, Lq, d, generator=gen(16))
@@ -109,6 +109,15 @@ def test_router_pool_and_linear(dev, B, Lq, d, C):
         assert_rel(hg.grad.cpu(), hr.grad, 1e-5, "dh")
         assert_rel(Wg.grad.cpu(), Wr.grad, 1e-5, "dW")
         assert_rel(bg.grad.cpu(), br.grad, 1e-5, "db")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("R,C", [(8192, 4097), (5, 3), (1000, 64)])
+def test_col_sum(dev, dtype, R, C):
+    """Column sums on the pooling kernels (router bias gradient of the token path)."""
+    x = torch.randn(R, C, generator=gen(R + C)).to(dtype)
+    got = _ops().col_sum(x.to(dev))
+    assert_rel(got.cpu(), x.double().sum(0), 1e-5, "column sums")
 
 
 # ------------------------------------------------------------------ chapter plan
@@ -142,6 +151,16 @@ def test_chapter_plan_skips_out_of_range(dev):
     assert plan.edge_u.cpu().tolist() == [0, 2, 3, -1, 2, -1, 1, 3]
     assert plan.csr_off.cpu().tolist()[:5] == [0, 1, 2, 4, 6]
     assert plan.csr_edge.cpu().tolist()[:6] == [0, 6, 1, 4, 2, 7]
+
+
+@pytest.mark.parametrize("C", [1, 300, 4097])
+def test_identity_plan_equals_plan_of_arange(dev, C):
+    ops = _ops()
+    ref = ops.chapter_plan(torch.arange(C, dtype=torch.int32, device=dev), C)
+    got = ops.identity_plan(C, dev)
+    assert (got.max_u, got.num_chapters) == (ref.max_u, ref.num_chapters)
+    for name in ("uniq", "n_uniq", "edge_u", "csr_off", "csr_edge"):
+        assert torch.equal(getattr(got, name).cpu(), getattr(ref, name).cpu()), name
 
 
 # --------------------------------------------------- gather + K/V projection
