@@ -89,7 +89,10 @@ class _SplitRows(torch.autograd.Function):
             ga = ref.new_zeros((n,) + tuple(shape[1:]))
         if gb is None:
             gb = ref.new_zeros((shape[0] - n,) + tuple(shape[1:]))
-        return torch.cat([ga, gb], 0), None
+        out = torch.empty(shape, device=ref.device, dtype=ref.dtype)
+        out[:n].copy_(ga)       # two device copies (faster than torch.cat's kernel here)
+        out[n:].copy_(gb)
+        return out, None
 
 
 def split_rows(x: torch.Tensor, n: int):

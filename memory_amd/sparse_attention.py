@@ -21,6 +21,7 @@ from __future__ import annotations
 from typing import List, Optional
 
 import torch
+import torch.nn.functional as F
 
 from . import _lib as L
 from ._lib import call, ptr, stream_ptr
@@ -50,12 +51,26 @@ def _kv_strides(layout: str, HK: int):
     raise ValueError(layout)
 
 
+def _kv_geom(layout: str, k: torch.Tensor):
+    """(HK, (chapter, kv head, row) element strides) of a K or V operand.  "rows" is a
+    [chapters*64, HK*64] view with any row stride (K or V columns of a fused KV GEMM output)."""
+    if layout == "natural":
+        HK = k.shape[-2]
+    elif layout == "tiles":
+        HK = k.shape[1]
+    elif layout == "rows":
+        rs = k.stride(0)
+        return k.shape[1] // 64, (64 * rs, 64, rs)
+    else:
+        raise ValueError(layout)
+    return HK, _kv_strides(layout, HK)
+
+
 def _forward(q, k, v, layout, segments: List[_Segment], mode: int, S: int, scale: float):
     B, Tq, HQ, D = q.shape
-    HK = k.shape[-2] if layout == "natural" else k.shape[1]
+    HK, (cs, hs, rs) = _kv_geom(layout, k)
     dt = L.dtype_code(q.dtype)
     st = stream_ptr(q.device)
-    cs, hs, rs = _kv_strides(layout, HK)
     ntok = B * Tq
     out = torch.empty(B, Tq, HQ, D, device=q.device, dtype=q.dtype)
     saved = []
@@ -77,10 +92,9 @@ def _forward(q, k, v, layout, segments: List[_Segment], mode: int, S: int, scale
 def _backward(q, k, v, layout, out, dout, segments, saved, mode, S, scale, dk, dv, dk_layout):
     """Fills dk/dv (pre-zeroed, layout dk_layout), returns dq and the per-edge dw (or None)."""
     B, Tq, HQ, D = q.shape
-    HK = k.shape[-2] if layout == "natural" else k.shape[1]
+    HK, (cs, hs, rs) = _kv_geom(layout, k)
     dt = L.dtype_code(q.dtype)
     st = stream_ptr(q.device)
-    cs, hs, rs = _kv_strides(layout, HK)
     ntok = B * Tq
     dq = torch.empty_like(q)
     dws = []
@@ -251,7 +265,7 @@ def FSA_topk_sparse_attention_weighted_joint_bias_bthd(q_bthd, k_bthd, v_bthd, b
 
 class _TokenRouted(torch.autograd.Function):
     """Routed branch of the token-level memory layer: K/V of the routed bank are
-    projected once (kv_project over every routed chapter), then sparse attention.
+    projected once (one GEMM over every routed chapter), then sparse attention.
 
     q (B, L, H, 64); routed (N_r, d); wk/wv (HK*64, d); idx (B, L, k) local chapter
     ids; w (B, L, k) or None.  Returns (B, L, H, 64)."""
@@ -267,20 +281,22 @@ class _TokenRouted(torch.autograd.Function):
         C = Nr // BLOCK
         q = q.contiguous()
         routed = routed.contiguous()
-        all_plan = ops.identity_plan(C, q.device)
         wkv = torch.cat([wk, wv], 0).to(dtype).contiguous()
-        kt, vt = ops.kv_project(routed, all_plan, BLOCK, wkv, HK, D, None, None, dtype, ("k", "v"))
+        # every routed chapter is projected (no gather, no norm): one plain GEMM on hipBLASLt,
+        # K and V read by the sparse kernels as strided column blocks of kv [Nr][2 KV]
+        KV = HK * D
+        kv = F.linear(routed.to(dtype), wkv)
         S = idx.shape[-1]
         segs = _segments(idx, w, mode, C, False, HQ, HK, C)
-        out, saved = _forward(q, kt, vt, "tiles", segs, mode, S, D ** -0.5)
-        ctx.segs, ctx.saved_parts, ctx.all_plan = segs, saved, all_plan
-        ctx.save_for_backward(q, routed, wkv, kt, vt, out)
+        out, saved = _forward(q, kv[:, :KV], kv[:, KV:], "rows", segs, mode, S, D ** -0.5)
+        ctx.segs, ctx.saved_parts = segs, saved
+        ctx.save_for_backward(q, routed, wkv, kv, out)
         ctx.cfg = (mode, S, HK, wk.dtype, wv.dtype, None if w is None else w.shape)
         return out
 
     @staticmethod
     def backward(ctx, dout):
-        q, routed, wkv, kt, vt, out = ctx.saved_tensors
+        q, routed, wkv, kv, out = ctx.saved_tensors
         mode, S, HK, wk_dtype, wv_dtype, w_shape = ctx.cfg
         dtype = q.dtype
         D = q.shape[-1]
@@ -289,8 +305,8 @@ class _TokenRouted(torch.autograd.Function):
         dkv = torch.zeros(Nr, 2 * KV, device=q.device, dtype=dtype)
         # dk / dv written as rows [chapter*64 + key][hk*64 + dim] (dv at column offset KV)
         elem = dkv.element_size()
-        dq, dws = _backward(q, kt, vt, "tiles", out, dout, ctx.segs, ctx.saved_parts, mode, S, D ** -0.5, dkv, None,
-                            (64 * 2 * KV, 64, 2 * KV, KV * elem))
+        dq, dws = _backward(q, kv[:, :KV], kv[:, KV:], "rows", out, dout, ctx.segs, ctx.saved_parts, mode, S,
+                            D ** -0.5, dkv, None, (64 * 2 * KV, 64, 2 * KV, KV * elem))
         need_r, need_wk, need_wv = ctx.needs_input_grad[1:4]
         dr = dwk = dwv = None
         if need_wk or need_wv:
