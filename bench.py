@@ -138,7 +138,7 @@ PROBE_BYTES = 256 << 20
 # entry point -> device kernel whose HBM traffic the counter passes measured
 TRAFFIC_KERNELS = {"moc_xattn_bwd_dkv": "xattn_bwd_dkv_kernel", "moc_xattn_fwd": "xattn_fwd_kernel",
                    "moc_xattn_bwd_dq": "xattn_bwd_dq_kernel", "moc_kv_project": "kv_project_wide_kernel",
-                   "moc_decode_partial": "decode_partial_kernel", "moc_sparse_bwd": "sparse_bwd_kernel"}
+                   "moc_decode_partial": "sparse_fwd_unit_kernel", "moc_sparse_bwd": "sparse_bwd_unit_kernel"}
 
 
 def measured_traffic(workload, entry):

@@ -262,9 +262,11 @@ int moc_sparse_dw(const float* src, const float* w, const int32_t* edge_u, int m
  * chapter tiles of every chapter (kv_project over all chapters), i.e. the decode use of
  * memory_transformer/model.py:612-692 with the chapters and omega fixed for the generation.
  * Chapter-centric over the plan of the (sequence, slot) edges, so each selected tile is read
- * once per step.  q [B][H][64]; omega f32 [B * NS]; partials o_part f32 [B * NS * H][64] and
- * lse_part f32 [B * NS * H] are merged by moc_sparse_combine in joint mode (rpe = H). */
-int moc_decode_partial(int dtype, const void* q, int64_t B, int H, const void* k_tiles, const void* vt_tiles, int HK,
+ * once per step.  q [B][H][64]; k_tiles, v_tiles [C][HK][64 keys][64 dims] (kv_project's
+ * "k" / "v" layouts); omega f32 [B * NS], >= 0; partials o_part f32 [B * NS * H][64] and
+ * lse_part f32 [B * NS * H] are merged by moc_sparse_combine in joint mode (rpe = H).
+ * bf16 needs 16-byte aligned q / tiles / o_part. */
+int moc_decode_partial(int dtype, const void* q, int64_t B, int H, const void* k_tiles, const void* v_tiles, int HK,
                        int Dh, int T, const int32_t* uniq, const int32_t* n_uniq, const int32_t* csr_off,
                        const int32_t* csr_edge, int64_t max_u, const float* omega, int NS, float scale, float* o_part,
                        float* lse_part, hipStream_t stream);

@@ -62,7 +62,7 @@ __global__ __launch_bounds__(64 * SpCfg<T>::NW) void sparse_fwd_kernel(
     const T* __restrict__ q, int HQ, const T* __restrict__ k, const T* __restrict__ v, int64_t cs, int64_t hs,
     int64_t rs, int HK, const int32_t* __restrict__ uniq, const int32_t* __restrict__ n_uniq,
     const int32_t* __restrict__ csr_off, const int32_t* __restrict__ csr_edge, int S, int hk0, int hq_off, int rpe,
-    float scale_log2, float* __restrict__ o_part, float* __restrict__ lse_part) {
+    float scale_log2, float* __restrict__ o_part, float* __restrict__ lse_part, const float* __restrict__ omega) {
   typedef typename Frag<T>::type F8;
   constexpr int NW = SpCfg<T>::NW, NT = 64 * NW;
   using Tile = SwzTile<T, 64>;
@@ -83,6 +83,7 @@ __global__ __launch_bounds__(64 * SpCfg<T>::NW) void sparse_fwd_kernel(
   for (int r0 = 32 * wave; r0 < nrows; r0 += 32 * NW) {
     F8 qf[2][2];
     int erow[2];  // e * rpe + row, or -1
+    float wrow[2] = {1.f, 1.f};
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb) {
       const int r = r0 + 16 * qb + c16;
@@ -92,6 +93,7 @@ __global__ __launch_bounds__(64 * SpCfg<T>::NW) void sparse_fwd_kernel(
         const int hq = hk * G + r % G;
         const int64_t tok = e / S;
         erow[qb] = e * rpe + (hq - hq_off);
+        if (omega) wrow[qb] = omega[e];
         const T* qp = q + ((size_t)tok * HQ + hq) * kSpDh;
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) qf[qb][ks] = Load8<T, T>::run(qp + 32 * ks + 8 * g);
@@ -122,13 +124,14 @@ __global__ __launch_bounds__(64 * SpCfg<T>::NW) void sparse_fwd_kernel(
       for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
         for (int x = 0; x < 4; ++x) mx = fmaxf(mx, st[kb][qb][x]);
-      m[qb] = quad_max(mx) * scale_log2;
+      const float c = wrow[qb] * scale_log2;
+      m[qb] = quad_max(mx) * c;
       float ps = 0.f;
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
         for (int x = 0; x < 4; ++x) {
-          const float p = exp2f(st[kb][qb][x] * scale_log2 - m[qb]);
+          const float p = exp2f(st[kb][qb][x] * c - m[qb]);
           ps += p;
           st[kb][qb][x] = p;
         }
@@ -157,7 +160,7 @@ __global__ __launch_bounds__(64 * SpCfg<T>::NW) void sparse_fwd_kernel(
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb) {
       if (erow[qb] < 0) continue;
-      const float inv = 1.f / l[qb];
+      const float inv = wrow[qb] / l[qb];
       float* op = o_part + (size_t)erow[qb] * kSpDh;
 #pragma unroll
       for (int db = 0; db < 4; ++db)
@@ -167,57 +170,106 @@ __global__ __launch_bounds__(64 * SpCfg<T>::NW) void sparse_fwd_kernel(
   }
 }
 
-// Per (token, row): combine the slot partials.  16 lanes per row, 4 dims each.
+// Per (token, row): combine the slot partials.  One wave per row: the slot weights a_s
+// live one per lane (64-slot chunks), the 16-lane group g streams the o_part rows of
+// slots g, g + 4, ... (16 bytes per lane), and the 4 groups are added in a fixed order.
 __device__ __forceinline__ float sp_logw(int mode, float w) {
   if (mode == 2) return w > 0.f ? log2f(w) : -INFINITY;
   if (mode == 3) return log2f(fmaxf(w, 1e-20f));
   return 0.f;
 }
 
+// Weighted sum over the slots s0 .. s0 + 63 of one row (lane group g takes slots g, g + 4,
+// ...; lane s - s0 holds a_s); a_s = 0 marks a skipped slot, whose partial row is never read.
+__device__ __forceinline__ f32x4 sp_slot_sum(const float* __restrict__ part, int64_t tok, int S, int rpe, int r,
+                                             float a, int s0, int lane) {
+  const int g = lane >> 4, sub = lane & 15;
+  const int n = min(64, S - s0);
+  const int iters = (n + 3) >> 2;   // wave-uniform trip count; 4 rows in flight per lane
+  f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int k0 = 0; k0 < iters; k0 += 4) {
+    f32x4 v[4];
+    float av[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int j = 4 * (k0 + i) + g;
+      const float aj = __shfl(a, j & 63, 64);
+      av[i] = j < n ? aj : 0.f;
+      v[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+      if (av[i] != 0.f) {
+        const int64_t e = tok * S + s0 + j;
+        v[i] = *reinterpret_cast<const f32x4*>(part + (e * rpe + r) * kSpDh + 4 * sub);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc += av[i] * v[i];
+  }
+  return acc;
+}
+
+__device__ __forceinline__ f32x4 sp_groups_sum(f32x4 acc) {
+#pragma unroll
+  for (int x = 0; x < 4; ++x) {
+    acc[x] += __shfl_xor(acc[x], 16, 64);
+    acc[x] += __shfl_xor(acc[x], 32, 64);
+  }
+  return acc;
+}
+
+constexpr int kCombWaves = 4;
+
 template <typename T>
-__global__ __launch_bounds__(256) void sparse_combine_kernel(const float* __restrict__ o_part,
-                                                             const float* __restrict__ lse_part,
-                                                             const int32_t* __restrict__ edge_u,
-                                                             const float* __restrict__ w, int mode, int S, int rpe,
-                                                             int64_t ntok, int HQ, int hq_off, T* __restrict__ out,
-                                                             float* __restrict__ lse_joint) {
-  const int64_t row = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
-  const int sub = threadIdx.x & 15;
+__global__ __launch_bounds__(64 * kCombWaves) void sparse_combine_kernel(const float* __restrict__ o_part,
+                                                                         const float* __restrict__ lse_part,
+                                                                         const int32_t* __restrict__ edge_u,
+                                                                         const float* __restrict__ w, int mode, int S,
+                                                                         int rpe, int64_t ntok, int HQ, int hq_off,
+                                                                         T* __restrict__ out,
+                                                                         float* __restrict__ lse_joint) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * kCombWaves + (threadIdx.x >> 6);
   if (row >= ntok * rpe) return;
   const int64_t tok = row / rpe;
   const int r = (int)(row % rpe);
-  f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
-  if (mode == 0) {
-    for (int s = 0; s < S; ++s) {
-      const int64_t e = tok * S + s;
-      if (edge_u[e] < 0) continue;
-      const float ws = w[e];
-      acc += ws * *reinterpret_cast<const f32x4*>(o_part + ((size_t)e * rpe + r) * kSpDh + 4 * sub);
-    }
-  } else {
-    float M = -INFINITY;
-    for (int s = 0; s < S; ++s) {
-      const int64_t e = tok * S + s;
-      if (edge_u[e] < 0) continue;
-      M = fmaxf(M, lse_part[(size_t)e * rpe + r] + sp_logw(mode, w ? w[e] : 1.f));
-    }
-    float den = 0.f;
-    if (M > -INFINITY) {
-      for (int s = 0; s < S; ++s) {
+  // slot weights: mode 0 a_s = w_s; joint modes a_s = 2^(lse_s + log w_s - M)
+  float M = -INFINITY;
+  if (mode != 0) {
+    for (int s0 = 0; s0 < S; s0 += 64) {
+      const int s = s0 + lane;
+      if (s < S) {
         const int64_t e = tok * S + s;
-        if (edge_u[e] < 0) continue;
-        const float a = exp2f(lse_part[(size_t)e * rpe + r] + sp_logw(mode, w ? w[e] : 1.f) - M);
-        den += a;
-        acc += a * *reinterpret_cast<const f32x4*>(o_part + ((size_t)e * rpe + r) * kSpDh + 4 * sub);
+        if (edge_u[e] >= 0) M = fmaxf(M, lse_part[e * rpe + r] + sp_logw(mode, w ? w[e] : 1.f));
       }
     }
-    const float inv = den > 0.f ? 1.f / den : 0.f;
-    acc *= inv;
-    if (sub == 0) lse_joint[row] = den > 0.f ? M + log2f(den) : INFINITY;
+    M = wave_max(M);
   }
-  T* op = out + ((size_t)tok * HQ + hq_off + r) * kSpDh + 4 * sub;
+  float den = 0.f;
+  f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int s0 = 0; s0 < S; s0 += 64) {
+    const int s = s0 + lane;
+    float a = 0.f;
+    if (s < S) {
+      const int64_t e = tok * S + s;
+      if (edge_u[e] >= 0) {
+        if (mode == 0) a = w[e];
+        else if (M > -INFINITY) a = exp2f(lse_part[e * rpe + r] + sp_logw(mode, w ? w[e] : 1.f) - M);
+      }
+    }
+    den += a;
+    acc += sp_slot_sum(o_part, tok, S, rpe, r, a, s0, lane);
+  }
+  acc = sp_groups_sum(acc);
+  float inv = 1.f;
+  if (mode != 0) {
+    den = wave_sum(den);
+    inv = den > 0.f ? 1.f / den : 0.f;
+    if (lane == 0) lse_joint[row] = den > 0.f ? M + log2f(den) : INFINITY;
+  }
+  if (lane < 16) {
+    T* op = out + ((int64_t)tok * HQ + hq_off + r) * kSpDh + 4 * lane;
 #pragma unroll
-  for (int x = 0; x < 4; ++x) op[x] = from_f<T>(acc[x]);
+    for (int x = 0; x < 4; ++x) op[x] = from_f<T>(acc[x] * inv);
+  }
 }
 
 // ----------------------------------------------------------------- backward
@@ -560,26 +612,29 @@ __global__ __launch_bounds__(64 * SpCfg<T>::NW, 1) void sparse_bwd_kernel(
   reduce_store(dva, dvb);
 }
 
-// dq[token, hq_off + r] = sum over valid slots of dq_part[e, r]
+// dq[token, hq_off + r] = sum over valid slots of dq_part[e, r]  (one wave per row)
 template <typename T>
-__global__ __launch_bounds__(256) void sparse_dq_combine_kernel(const float* __restrict__ dq_part,
-                                                                const int32_t* __restrict__ edge_u, int S, int rpe,
-                                                                int64_t ntok, int HQ, int hq_off,
-                                                                T* __restrict__ dq) {
-  const int64_t row = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
-  const int sub = threadIdx.x & 15;
+__global__ __launch_bounds__(64 * kCombWaves) void sparse_dq_combine_kernel(const float* __restrict__ dq_part,
+                                                                            const int32_t* __restrict__ edge_u, int S,
+                                                                            int rpe, int64_t ntok, int HQ, int hq_off,
+                                                                            T* __restrict__ dq) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * kCombWaves + (threadIdx.x >> 6);
   if (row >= ntok * rpe) return;
   const int64_t tok = row / rpe;
   const int r = (int)(row % rpe);
   f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
-  for (int s = 0; s < S; ++s) {
-    const int64_t e = tok * S + s;
-    if (edge_u[e] < 0) continue;
-    acc += *reinterpret_cast<const f32x4*>(dq_part + ((size_t)e * rpe + r) * kSpDh + 4 * sub);
+  for (int s0 = 0; s0 < S; s0 += 64) {
+    const int s = s0 + lane;
+    const float a = (s < S && edge_u[tok * S + s] >= 0) ? 1.f : 0.f;
+    acc += sp_slot_sum(dq_part, tok, S, rpe, r, a, s0, lane);
   }
-  T* op = dq + ((size_t)tok * HQ + hq_off + r) * kSpDh + 4 * sub;
+  acc = sp_groups_sum(acc);
+  if (lane < 16) {
+    T* op = dq + ((int64_t)tok * HQ + hq_off + r) * kSpDh + 4 * lane;
 #pragma unroll
-  for (int x = 0; x < 4; ++x) op[x] = from_f<T>(acc[x]);
+    for (int x = 0; x < 4; ++x) op[x] = from_f<T>(acc[x]);
+  }
 }
 
 // dw[e] for an edge e = token * S + s, summed over its rpe rows:
@@ -636,7 +691,8 @@ __global__ __launch_bounds__(64 * kUnitWaves) void sparse_fwd_unit_kernel(
     const bf16* __restrict__ q, int HQ, const bf16* __restrict__ k, const bf16* __restrict__ v, int64_t cs,
     int64_t hs, int64_t rs, int HK, const int32_t* __restrict__ uniq, const int32_t* __restrict__ n_uniq,
     const int32_t* __restrict__ csr_off, const int32_t* __restrict__ csr_edge, int64_t max_u, int S, int hk0,
-    int nhk, int hq_off, int rpe, float scale_log2, float* __restrict__ o_part, float* __restrict__ lse_part) {
+    int nhk, int hq_off, int rpe, float scale_log2, float* __restrict__ o_part, float* __restrict__ lse_part,
+    const float* __restrict__ omega) {
   using Tile = SwzTile<bf16, 64>;
   __shared__ __attribute__((aligned(16))) char sVall[kUnitWaves][64 * 64 * 2];
   const int G = HQ / HK;
@@ -661,6 +717,7 @@ __global__ __launch_bounds__(64 * kUnitWaves) void sparse_fwd_unit_kernel(
     const bool two = r0 + 16 < ur.nrows;
     bf16x8 qf[2][2];
     int erow[2];
+    float wrow[2] = {1.f, 1.f};
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb) {
       const int r = r0 + 16 * qb + c16;
@@ -670,6 +727,7 @@ __global__ __launch_bounds__(64 * kUnitWaves) void sparse_fwd_unit_kernel(
         const int e = csr_edge[ur.p0 + r / G];
         const int hq = ur.hk * G + r % G;
         erow[qb] = e * rpe + (hq - hq_off);
+        if (omega) wrow[qb] = omega[e];
         const bf16* qp = q + ((int64_t)(e / S) * HQ + hq) * kSpDh + 8 * g;
         qf[qb][0] = Load8<bf16, bf16>::run(qp);
         qf[qb][1] = Load8<bf16, bf16>::run(qp + 32);
@@ -696,13 +754,14 @@ __global__ __launch_bounds__(64 * kUnitWaves) void sparse_fwd_unit_kernel(
       for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
         for (int x = 0; x < 4; ++x) mx = fmax_fast(mx, st[kb][qb][x]);
-      m[qb] = quad_max(mx) * scale_log2;
+      const float c = wrow[qb] * scale_log2;
+      m[qb] = quad_max(mx) * c;
       float ps = 0.f;
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
         for (int x = 0; x < 4; ++x) {
-          const float p = exp2f(st[kb][qb][x] * scale_log2 - m[qb]);
+          const float p = exp2f(st[kb][qb][x] * c - m[qb]);
           ps += p;
           pf[qb][kb >> 1][4 * (kb & 1) + x] = (bf16)p;
         }
@@ -726,7 +785,7 @@ __global__ __launch_bounds__(64 * kUnitWaves) void sparse_fwd_unit_kernel(
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb) {
       if (erow[qb] < 0) continue;
-      const float inv = 1.f / l[qb];
+      const float inv = wrow[qb] / l[qb];
       float* op = o_part + (int64_t)erow[qb] * kSpDh;
 #pragma unroll
       for (int db = 0; db < 4; ++db) *reinterpret_cast<f32x4*>(op + 16 * db + 4 * g) = o[db][qb] * inv;
@@ -1038,6 +1097,32 @@ bool unit_kv_aligned(const void* q, const void* k, const void* v, int64_t cs, in
 }
 }  // namespace
 
+int moc::sparse_fwd_launch(int dtype, const void* q, int HQ, const void* k, const void* v, int64_t cs, int64_t hs,
+                           int64_t rs, int HK, const int32_t* uniq, const int32_t* n_uniq, const int32_t* csr_off,
+                           const int32_t* csr_edge, int64_t max_u, int S, int hk0, int nhk, int hq_off, int rpe,
+                           float scale, const float* omega, float* o_part, float* lse_part, hipStream_t stream,
+                           const char* who) {
+  const float sl2 = scale * 1.4426950408889634f;
+  if (dtype == MOC_BF16) {
+    MOC_REQUIRE(unit_kv_aligned(q, k, v, cs, hs, rs) && ((uintptr_t)o_part & 15) == 0, MOC_ERR_ARG,
+                "%s: bf16 needs 16-byte aligned q/k/v/o_part and strides that are multiples of 8", who);
+    const int64_t units = max_u * nhk;
+    hipLaunchKernelGGL(sparse_fwd_unit_kernel, dim3((unsigned)((units + kUnitWaves - 1) / kUnitWaves)),
+                       dim3(64 * kUnitWaves), 0, stream, (const bf16*)q, HQ, (const bf16*)k, (const bf16*)v, cs, hs,
+                       rs, HK, uniq, n_uniq, csr_off, csr_edge, max_u, S, hk0, nhk, hq_off, rpe, sl2, o_part,
+                       lse_part, omega);
+    return check_launch("sparse_fwd_unit_kernel");
+  }
+  if (dtype == MOC_F32) {
+    dim3 grid((unsigned)max_u, (unsigned)nhk);
+    hipLaunchKernelGGL(sparse_fwd_kernel<float>, grid, dim3(sp_threads<float>()), 0, stream, (const float*)q, HQ,
+                       (const float*)k, (const float*)v, cs, hs, rs, HK, uniq, n_uniq, csr_off, csr_edge, S, hk0,
+                       hq_off, rpe, sl2, o_part, lse_part, omega);
+    return check_launch("sparse_fwd_kernel");
+  }
+  return set_error(MOC_ERR_UNSUPPORTED, "%s: dtype %d", who, dtype);
+}
+
 extern "C" {
 
 
@@ -1051,24 +1136,8 @@ int moc_sparse_fwd(int dtype, const void* q, int64_t ntok, int HQ, const void* k
   MOC_REQUIRE(HQ > 0 && HK > 0 && HQ % HK == 0 && nhk > 0 && hk0 >= 0 && hk0 + nhk <= HK && S > 0, MOC_ERR_ARG,
               "moc_sparse_fwd: bad heads HQ=%d HK=%d hk0=%d nhk=%d", HQ, HK, hk0, nhk);
   if (max_u == 0 || ntok == 0) return MOC_OK;
-  dim3 grid((unsigned)max_u, (unsigned)nhk);
-  const float sl2 = scale * 1.4426950408889634f;
-  if (dtype == MOC_BF16) {
-    MOC_REQUIRE(unit_kv_aligned(q, k, v, cs, hs, rs) && ((uintptr_t)o_part & 15) == 0, MOC_ERR_ARG,
-                "moc_sparse_fwd: bf16 needs 16-byte aligned q/k/v/o_part and strides that are multiples of 8");
-    const int64_t units = max_u * nhk;
-    hipLaunchKernelGGL(sparse_fwd_unit_kernel, dim3((unsigned)((units + kUnitWaves - 1) / kUnitWaves)),
-                       dim3(64 * kUnitWaves), 0, stream, (const bf16*)q, HQ, (const bf16*)k, (const bf16*)v, cs, hs,
-                       rs, HK, uniq, n_uniq, csr_off, csr_edge, max_u, S, hk0, nhk, hq_off, rpe, sl2, o_part,
-                       lse_part);
-    return check_launch("sparse_fwd_unit_kernel");
-  } else if (dtype == MOC_F32)
-    hipLaunchKernelGGL(sparse_fwd_kernel<float>, grid, dim3(sp_threads<float>()), 0, stream, (const float*)q, HQ,
-                       (const float*)k, (const float*)v, cs, hs, rs, HK, uniq, n_uniq, csr_off, csr_edge, S, hk0,
-                       hq_off, rpe, sl2, o_part, lse_part);
-  else
-    return set_error(MOC_ERR_UNSUPPORTED, "moc_sparse_fwd: dtype %d", dtype);
-  return check_launch("sparse_fwd_kernel");
+  return moc::sparse_fwd_launch(dtype, q, HQ, k, v, cs, hs, rs, HK, uniq, n_uniq, csr_off, csr_edge, max_u, S, hk0,
+                                nhk, hq_off, rpe, scale, nullptr, o_part, lse_part, stream, "moc_sparse_fwd");
 }
 
 int moc_sparse_combine(int dtype, const float* o_part, const float* lse_part, const int32_t* edge_u, const float* w,
@@ -1080,12 +1149,12 @@ int moc_sparse_combine(int dtype, const float* o_part, const float* lse_part, co
   MOC_REQUIRE(mode == 0 || lse_joint, MOC_ERR_ARG, "moc_sparse_combine: joint modes need lse_joint");
   const int64_t rows = ntok * rpe;
   if (rows == 0) return MOC_OK;
-  dim3 grid((unsigned)((rows + 15) / 16));
+  dim3 grid((unsigned)((rows + kCombWaves - 1) / kCombWaves));
   if (dtype == MOC_BF16)
-    hipLaunchKernelGGL(sparse_combine_kernel<bf16>, grid, dim3(256), 0, stream, o_part, lse_part, edge_u, w, mode, S,
+    hipLaunchKernelGGL(sparse_combine_kernel<bf16>, grid, dim3(64 * kCombWaves), 0, stream, o_part, lse_part, edge_u, w, mode, S,
                        rpe, ntok, HQ, hq_off, (bf16*)out, lse_joint);
   else if (dtype == MOC_F32)
-    hipLaunchKernelGGL(sparse_combine_kernel<float>, grid, dim3(256), 0, stream, o_part, lse_part, edge_u, w, mode, S,
+    hipLaunchKernelGGL(sparse_combine_kernel<float>, grid, dim3(64 * kCombWaves), 0, stream, o_part, lse_part, edge_u, w, mode, S,
                        rpe, ntok, HQ, hq_off, (float*)out, lse_joint);
   else
     return set_error(MOC_ERR_UNSUPPORTED, "moc_sparse_combine: dtype %d", dtype);
@@ -1153,12 +1222,12 @@ int moc_sparse_dq_combine(int dtype, const float* dq_part, const int32_t* edge_u
   MOC_REQUIRE(dq_part && edge_u && dq, MOC_ERR_ARG, "moc_sparse_dq_combine: null pointer");
   const int64_t rows = ntok * rpe;
   if (rows == 0) return MOC_OK;
-  dim3 grid((unsigned)((rows + 15) / 16));
+  dim3 grid((unsigned)((rows + kCombWaves - 1) / kCombWaves));
   if (dtype == MOC_BF16)
-    hipLaunchKernelGGL(sparse_dq_combine_kernel<bf16>, grid, dim3(256), 0, stream, dq_part, edge_u, S, rpe, ntok, HQ,
+    hipLaunchKernelGGL(sparse_dq_combine_kernel<bf16>, grid, dim3(64 * kCombWaves), 0, stream, dq_part, edge_u, S, rpe, ntok, HQ,
                        hq_off, (bf16*)dq);
   else if (dtype == MOC_F32)
-    hipLaunchKernelGGL(sparse_dq_combine_kernel<float>, grid, dim3(256), 0, stream, dq_part, edge_u, S, rpe, ntok, HQ,
+    hipLaunchKernelGGL(sparse_dq_combine_kernel<float>, grid, dim3(64 * kCombWaves), 0, stream, dq_part, edge_u, S, rpe, ntok, HQ,
                        hq_off, (float*)dq);
   else
     return set_error(MOC_ERR_UNSUPPORTED, "moc_sparse_dq_combine: dtype %d", dtype);

@@ -22,7 +22,7 @@ from ._lib import call, ptr, stream_ptr
 
 
 class MemoryDecodeCache:
-    """Per-layer K tiles and transposed V tiles [C][HK][64][64] of the whole bank (optionally row-normalised)."""
+    """Per-layer K and V tiles [C][HK][64 keys][64 dims] of the whole bank (optionally row-normalised)."""
 
     def __init__(self, bank: torch.Tensor, wk: torch.Tensor, wv: torch.Tensor, *, num_chapters: int,
                  tokens_per_chapter: int, num_kv_heads: int, norm_type: Optional[str] = None, eps: float = 1e-6,
@@ -37,8 +37,8 @@ class MemoryDecodeCache:
             if code:
                 mean, rstd = ops.row_stats(bank.contiguous(), plan, T, code, eps)
             wkv = torch.cat([wk, wv], 0).to(dtype).contiguous()
-            self.k_tiles, self.vt_tiles = ops.kv_project(bank.contiguous(), plan, T, wkv, self.HK, 64, mean, rstd,
-                                                         dtype, ("k", "vt"))
+            self.k_tiles, self.v_tiles = ops.kv_project(bank.contiguous(), plan, T, wkv, self.HK, 64, mean, rstd,
+                                                        dtype, ("k", "v"))
 
     @property
     def nbytes(self) -> int:
@@ -73,7 +73,7 @@ def decode_attention(q: torch.Tensor, cache: MemoryDecodeCache, routing: DecodeR
     o_part = torch.empty(E * H, D, device=q.device, dtype=torch.float32)
     lse_part = torch.empty(E * H, device=q.device, dtype=torch.float32)
     pl = routing.plan
-    call("moc_decode_partial", dt, ptr(q), B, H, ptr(cache.k_tiles), ptr(cache.vt_tiles), cache.HK, D, cache.T,
+    call("moc_decode_partial", dt, ptr(q), B, H, ptr(cache.k_tiles), ptr(cache.v_tiles), cache.HK, D, cache.T,
          ptr(pl.uniq), ptr(pl.n_uniq), ptr(pl.csr_off), ptr(pl.csr_edge), pl.max_u, ptr(routing.omega), NS,
          float(D) ** -0.5, ptr(o_part), ptr(lse_part), st)
     out = torch.empty(B, H, D, device=q.device, dtype=cache.dtype)
