@@ -1,0 +1,124 @@
+"""Parity at the full BASELINE sizes (the shapes bench.py measures), bf16 on the GPU against
+the oracle in fp32 on the CPU.
+
+config 3 (B=8, L=1024, d=768, 12 heads, bank 4,097 x 64, S=1 shared + k=64 routed, scale 2.5):
+  * routing: each sequence's 64 routed chapters are distinct and form a top-64 of the oracle's
+    fp64 router logits up to a tie band of 1e-5 (the GPU logits are fp32 sums, so chapters whose
+    logits differ by less than fp32 rounding may swap);
+  * output and every gradient (h, bank, q/k/v/o projections, router weight and bias): the
+    oracle's gather -> x omega -> cross-attention chain (model.py:677-692,
+    memory_attention.py:402-478) evaluated on the GPU's own chapter choice, with omega from the
+    oracle's renormalised router probabilities (router.py:114-149, model.py:356-391), so the
+    comparison cannot hinge on a near-tie.
+config 5 (decode, B=64, k=64, 12 heads over the 4,097-chapter bank): the decode step against
+  the oracle's decode_step on the same routing.
+
+bf16 tolerance 2e-2 relative max error (5e-2 for the router weight gradient, as in the other
+layer tests)."""
+
+import pytest
+import torch
+
+import oracle as O
+from helpers import assert_rel
+
+pytestmark = pytest.mark.gpu
+
+B, L, D, H, C, T, S, K, SCALE = 8, 1024, 768, 12, 4097, 64, 1, 64, 2.5
+
+
+def test_config3_full_size_forward_backward(gpu_device):
+    print("full-size config 3 forward + backward", flush=True)
+    from memory_amd.model import RoutedMemoryLayer
+    dev = gpu_device
+    bf = torch.bfloat16
+    g = torch.Generator().manual_seed(3)
+    h = torch.randn(B, L, D, generator=g).to(bf)
+    bank = (torch.randn(C * T, D, generator=g) * 0.5).to(bf)
+    Wr = torch.randn(C, D, generator=g) * 0.02
+    br = torch.randn(C, generator=g) * 0.01
+    Wq, Wk, Wv, Wo = ((torch.randn(D, D, generator=g) * D ** -0.5).to(bf) for _ in range(4))
+    dO = torch.randn(B, L, D, generator=g)
+
+    layer = RoutedMemoryLayer(D, H, C, T, K, num_shared_chapters=S, routed_scaling_factor=SCALE,
+                              wo_init_zero=False)
+    with torch.no_grad():
+        layer.router.router.weight.copy_(Wr)
+        layer.router.router.bias.copy_(br)
+        for lin, W in ((layer.memory_attn.q_proj, Wq), (layer.memory_attn.k_proj, Wk),
+                       (layer.memory_attn.v_proj, Wv), (layer.memory_attn.o_proj, Wo)):
+            lin.weight.copy_(W.float())
+    layer = layer.to(dev)
+    for m in (layer.memory_attn.q_proj, layer.memory_attn.k_proj, layer.memory_attn.v_proj,
+              layer.memory_attn.o_proj):
+        m.to(bf)
+    hg = h.to(dev).requires_grad_(True)
+    bg = bank.to(dev).requires_grad_(True)
+    out, _ = layer(hg, bg, return_losses=False)
+    (out.float() * dO.to(dev)).sum().backward()
+    idx_star, _, _ = layer.route(hg.detach(), return_losses=False)
+    sel = idx_star[:, S:].cpu().long()                       # global chapter ids of the routed slots
+
+    # routing: distinct, and a top-K of the fp64 logits up to the tie band
+    logits64 = O.linear(O.sequence_pool(h.double()), Wr.double(), br.double())
+    routed = logits64[:, S:]
+    assert all(torch.unique(sel[b]).numel() == K for b in range(B))
+    assert int(sel.min()) >= S
+    kth = torch.topk(routed, K, dim=-1).values[:, -1:]
+    assert bool((routed.gather(1, sel - S) >= kth - 1e-5).all()), "routed chapters are not a top-k of the logits"
+
+    # output and gradients: oracle chain on the GPU's chapter choice (fp32, CPU)
+    leaves = [t.float().clone().requires_grad_(True) for t in (h, bank, Wr, br, Wq, Wk, Wv, Wo)]
+    hf, bankf, Wrf, brf, Wqf, Wkf, Wvf, Wof = leaves
+    logits = O.linear(O.sequence_pool(hf), Wrf, brf)
+    probs = torch.softmax(logits, dim=-1)
+    p = torch.cat([torch.zeros_like(probs[:, :S]), probs[:, S:]], dim=-1)
+    p = p / p.sum(dim=-1, keepdim=True).clamp_min(1e-12)
+    w = p.gather(1, sel)
+    w = w / w.sum(dim=-1, keepdim=True).clamp_min(1e-12)
+    ci, cw = O.prepend_shared_chapters(sel, w, num_chapters=C, num_shared_chapters=S, routed_scaling_factor=SCALE)
+    assert torch.equal(ci, idx_star.cpu().long())
+    # the oracle's row indices; rows taken by plain indexing (the same rows as its batched
+    # gather, whose backward would materialise a (B, 262208, 768) gradient)
+    with torch.no_grad():
+        _, rows = O.gather_chapters(bankf, ci, T)
+    mem = bankf[rows]
+    ref = O.cross_attention(hf, O.weight_memory(mem, cw, T), Wqf, Wkf, Wvf, Wof, H, H)
+    (ref * dO).sum().backward()
+
+    assert_rel(out, ref.detach(), 2e-2, "out")
+    got = [hg.grad, bg.grad, layer.router.router.weight.grad, layer.router.router.bias.grad,
+           layer.memory_attn.q_proj.weight.grad, layer.memory_attn.k_proj.weight.grad,
+           layer.memory_attn.v_proj.weight.grad, layer.memory_attn.o_proj.weight.grad]
+    names = ["dh", "dbank", "dWr", "dbr", "dWq", "dWk", "dWv", "dWo"]
+    for n, gr, r in zip(names, got, leaves):
+        assert_rel(gr, r.grad, 5e-2 if n in ("dWr", "dbr") else 2e-2, n)
+
+
+def test_config5_full_size_decode(gpu_device):
+    print("full-size config 5 decode", flush=True)
+    from memory_amd.decode import DecodeRouting, MemoryDecodeCache, memory_decode_step
+    from memory_amd.memory_attention import MemoryCrossAttention
+    dev = gpu_device
+    bf = torch.bfloat16
+    Bd = 64
+    g = torch.Generator().manual_seed(5)
+    h = torch.randn(Bd, 1, D, generator=g).to(bf)
+    bank = (torch.randn(C * T, D, generator=g) * 0.5).to(bf)
+    Wq, Wk, Wv, Wo = ((torch.randn(D, D, generator=g) * D ** -0.5).to(bf) for _ in range(4))
+    logits = torch.randn(Bd, C, generator=g) * 2
+    idx, w, _ = O.route_sequence(logits, K, S)
+    ci, cw = O.prepend_shared_chapters(idx, w, num_chapters=C, num_shared_chapters=S, routed_scaling_factor=SCALE)
+
+    attn = MemoryCrossAttention(D, H, H, wo_init_zero=False)
+    with torch.no_grad():
+        for lin, W in ((attn.q_proj, Wq), (attn.k_proj, Wk), (attn.v_proj, Wv), (attn.o_proj, Wo)):
+            lin.weight.copy_(W.float())
+    attn = attn.to(dev, bf)
+    cache = MemoryDecodeCache(bank.to(dev), attn.k_proj.weight, attn.v_proj.weight, num_chapters=C,
+                              tokens_per_chapter=T, num_kv_heads=H, dtype=bf)
+    routing = DecodeRouting(ci.to(dev), cw.to(dev), C)
+    out = memory_decode_step(attn, h.to(dev), cache, routing)
+    ref = O.decode_step(h.float(), bank.float(), ci, cw.float(), Wq.float(), Wk.float(), Wv.float(), Wo.float(),
+                        H=H, HK=H, T=T, S=S)
+    assert_rel(out, ref, 2e-2, "decode output")
