@@ -122,3 +122,66 @@ def test_config5_full_size_decode(gpu_device):
     ref = O.decode_step(h.float(), bank.float(), ci, cw.float(), Wq.float(), Wk.float(), Wv.float(), Wo.float(),
                         H=H, HK=H, T=T, S=S)
     assert_rel(out, ref, 2e-2, "decode output")
+
+
+def test_config4_widths_token_layer(gpu_device):
+    """The token-level layer at config 4's widths (d=768, 12 heads, the 4,097-chapter bank,
+    S=1 + k=16, v4 MoE combine) on 256 tokens: every routed chapter's (chapter, head) unit holds
+    one or two rows.  Routing: a top-16 of the logits (GEMM operands rounded to bf16 as on the
+    GPU) up to a 1e-5 tie band; output and every gradient against the oracle's token layer
+    (token_routed_preproj) on the GPU's chapter choice."""
+    print("config-4 widths token layer", flush=True)
+    from memory_amd.model import TokenRoutedMemoryLayer
+    dev = gpu_device
+    bf = torch.bfloat16
+    Lq, K4 = 256, 16
+    g = torch.Generator().manual_seed(4)
+    h = torch.randn(1, Lq, D, generator=g).to(bf)
+    bank = (torch.randn(C * T, D, generator=g) * 0.5).to(bf)
+    Wr = (torch.randn(C, D, generator=g) * 0.02).to(bf).float()   # the router GEMM rounds W to bf16
+    br = torch.randn(C, generator=g) * 0.01
+    Wq, Wk, Wv, Wo = ((torch.randn(D, D, generator=g) * D ** -0.5).to(bf) for _ in range(4))
+    dO = torch.randn(1, Lq, D, generator=g)
+
+    layer = TokenRoutedMemoryLayer(D, H, C, T, K4, num_shared_chapters=S, routed_scaling_factor=SCALE,
+                                   weighted=True, kernel_version="v4", wo_init_zero=False)
+    with torch.no_grad():
+        layer.router.router.weight.copy_(Wr)
+        layer.router.router.bias.copy_(br)
+        for lin, W in ((layer.memory_attn.q_proj, Wq), (layer.memory_attn.k_proj, Wk),
+                       (layer.memory_attn.v_proj, Wv), (layer.memory_attn.o_proj, Wo)):
+            lin.weight.copy_(W.float())
+    layer = layer.to(dev)
+    for m in (layer.memory_attn.q_proj, layer.memory_attn.k_proj, layer.memory_attn.v_proj,
+              layer.memory_attn.o_proj):
+        m.to(bf)
+    hg = h.to(dev).requires_grad_(True)
+    bg = bank.to(dev).requires_grad_(True)
+    out, _ = layer(hg, bg, return_losses=False)
+    (out.float() * dO.to(dev)).sum().backward()
+    idx, _, _ = layer.router.route_token_level(hg.detach(), return_losses=False, exclude_prefix_chapters=S)
+    idx = idx.cpu().long()                                          # (1, Lq, K4) global ids
+
+    logits64 = O.linear(h.double(), Wr.double(), br.double())[..., S:]
+    assert int(idx.min()) >= S
+    assert all(torch.unique(idx[0, t]).numel() == K4 for t in range(Lq))
+    kth = torch.topk(logits64, K4, dim=-1).values[..., -1:]
+    assert bool((logits64.gather(-1, idx - S) >= kth - 1e-5).all()), "routed chapters are not a top-k"
+
+    leaves = [t.float().clone().requires_grad_(True) for t in (h, bank, Wr, br, Wq, Wk, Wv, Wo)]
+    hf, bankf, Wrf, brf, Wqf, Wkf, Wvf, Wof = leaves
+    probs = torch.softmax(O.linear(hf, Wrf, brf), dim=-1)
+    routed = probs[..., S:] / probs[..., S:].sum(dim=-1, keepdim=True).clamp_min(1e-12)
+    w = routed.gather(-1, idx - S)
+    w = w / w.sum(dim=-1, keepdim=True).clamp_min(1e-12)
+    pre = O.token_routed_preproj(hf, bankf[: S * T], bankf[S * T:], idx - S, w, T, SCALE, Wqf, Wkf, Wvf, H, H)
+    ref = O.linear(pre, Wof)
+    (ref * dO).sum().backward()
+
+    assert_rel(out, ref.detach(), 2e-2, "out")
+    got = [hg.grad, bg.grad, layer.router.router.weight.grad, layer.router.router.bias.grad,
+           layer.memory_attn.q_proj.weight.grad, layer.memory_attn.k_proj.weight.grad,
+           layer.memory_attn.v_proj.weight.grad, layer.memory_attn.o_proj.weight.grad]
+    names = ["dh", "dbank", "dWr", "dbr", "dWq", "dWk", "dWv", "dWo"]
+    for n, gr, r in zip(names, got, leaves):
+        assert_rel(gr, r.grad, 5e-2 if n in ("dWr", "dbr") else 2e-2, n)
