@@ -54,9 +54,13 @@ class DecodeRouting:
         self.omega = chapter_weights.float().contiguous()
         self.B, self.NS = self.idx.shape
         self.plan = ops.chapter_plan(self.idx, num_chapters)
+        # the routing is fixed for the whole generation: read the distinct-chapter count once
+        # (one synchronisation here, none per step) so each step launches exactly one wave per
+        # selected (chapter, kv head) tile instead of min(B * NS, C) chapters' worth
+        self.n_unique = int(self.plan.n_uniq[0].item())
 
     def unique_chapters(self) -> int:
-        return int(self.plan.n_uniq[0].item())
+        return self.n_unique
 
 
 def decode_attention(q: torch.Tensor, cache: MemoryDecodeCache, routing: DecodeRouting) -> torch.Tensor:
@@ -74,7 +78,7 @@ def decode_attention(q: torch.Tensor, cache: MemoryDecodeCache, routing: DecodeR
     lse_part = torch.empty(E * H, device=q.device, dtype=torch.float32)
     pl = routing.plan
     call("moc_decode_partial", dt, ptr(q), B, H, ptr(cache.k_tiles), ptr(cache.v_tiles), cache.HK, D, cache.T,
-         ptr(pl.uniq), ptr(pl.n_uniq), ptr(pl.csr_off), ptr(pl.csr_edge), pl.max_u, ptr(routing.omega), NS,
+         ptr(pl.uniq), ptr(pl.n_uniq), ptr(pl.csr_off), ptr(pl.csr_edge), routing.n_unique, ptr(routing.omega), NS,
          float(D) ** -0.5, ptr(o_part), ptr(lse_part), st)
     out = torch.empty(B, H, D, device=q.device, dtype=cache.dtype)
     lse = torch.empty(B * H, device=q.device, dtype=torch.float32)
