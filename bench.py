@@ -251,6 +251,7 @@ def run_c4(args):
         out.backward(dout)
 
     ms, per, _, _ = timed(step, args.steps, args.warmup)
+    losses = router_losses_timing(layer, h, cfg)
     fl = c4_flops(cfg)
     tflops = fl["step"] / (ms * 1e-3) / 1e12
     kernels = {n: {"avg_ms": round(v["avg_ms"], 4), "calls": v["calls_per_step"]}
@@ -263,7 +264,61 @@ def run_c4(args):
         "config": {"workload": "c4: token-level routed memory layer fwd+bwd (v4 MoE combine)", **cfg},
         "tflops": round(tflops, 2), "mfma_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
         "algorithmic_gflop_per_step": round(fl["step"] / 1e9, 1), "kernels": kernels,
+        "router_losses": losses,
     }
+
+
+def router_losses_timing(layer, h, cfg, iters=20):
+    """The router's auxiliary losses (router.py:197-260) at the token-level shape, forward +
+    backward of their sum: the fused kernels against the same formulas as unfused torch ops
+    (the reference's (rows, k, C) one-hot included), both on the GPU."""
+    import torch
+    import torch.nn.functional as F
+    from memory_amd import ops
+    C, k = cfg["C"], cfg["k"]
+    with torch.no_grad():
+        logits0 = ops.router_token_logits(h.detach(), layer.router.router.weight, layer.router.router.bias)
+        idx = torch.topk(logits0[:, 1:], k, dim=-1).indices + 1
+
+    def fused():
+        z = logits0.detach().requires_grad_(True)
+        v = ops.router_losses(z, idx, C)
+        sum(v.values()).backward()
+
+    def unfused():
+        z = logits0.detach().requires_grad_(True)
+        probs = torch.softmax(z, dim=-1)
+        f = F.one_hot(idx, num_classes=C).float().sum(dim=1).mean(dim=0)
+        lb = C * (f * probs.mean(dim=0)).sum()
+        aux = F.mse_loss(probs.pow(2).mean(dim=0), torch.full((C,), 1.0 / C, device=z.device))
+        zl = (torch.logsumexp(z, dim=-1) ** 2).mean()
+        ent = -(probs * torch.log(probs.clamp_min(1e-12))).sum(dim=-1).mean()
+        (lb + aux + zl + ent).backward()
+
+    out = {"rows": int(logits0.shape[0]), "chapters": C, "k": k}
+    for name, fn in (("fused_ms", fused), ("torch_ops_ms", unfused)):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(iters):
+            fn()
+        torch.cuda.synchronize()
+        out[name] = round((time.perf_counter() - t0) * 1e3 / iters, 4)
+    # the fused entry points' own GPU time (HIP events on the launch stream), outside the loop above
+    from memory_amd import _lib as L
+    L.KERNEL_EVENTS, L.KERNEL_EVENTS_ONLY = {}, {"moc_router_losses", "moc_router_losses_bwd"}
+    try:
+        for _ in range(iters):
+            fused()
+        torch.cuda.synchronize()
+        ev = L.KERNEL_EVENTS
+    finally:
+        L.KERNEL_EVENTS, L.KERNEL_EVENTS_ONLY = None, None
+    for n, key in (("moc_router_losses", "fused_fwd_kernels_ms"), ("moc_router_losses_bwd", "fused_bwd_kernels_ms")):
+        pairs = ev.get(n, [])
+        out[key] = round(sum(a.elapsed_time(b) for a, b in pairs) / max(1, len(pairs)), 4)
+    return out
 
 
 C5 = dict(B=64, d=768, H=12, HK=12, C=4097, T=64, S=1, k=64, scale=2.5, layers=4, prompt=512)

@@ -91,6 +91,25 @@ int moc_router_linear_bwd(const float* dz, const float* x, int64_t R, int64_t d,
                           int64_t C, float* dx, float* dW, float* db, void* workspace, size_t workspace_bytes,
                           hipStream_t stream);
 
+/* Replaces ChapterRouter._compute_losses (router.py:197-260) for rows of logits f32 [R, C] and
+ * the selected chapter ids idx i32 [R, k] (entries outside [0, C) are ignored):
+ * losses f32 [4] = {load_balance, auxiliary, z_loss, entropy} with p = softmax(logits) per row,
+ *   load_balance = C sum_c f_c P_c (f_c = selections of c / R, P_c = mean_r p_rc),
+ *   auxiliary = mean_c (mean_r p_rc^2 - 1/C)^2, z_loss = mean_r lse_r^2,
+ *   entropy = -mean_r sum_c p_rc log(max(p_rc, 1e-12)).
+ * Also writes counts i32 [C] (selections per chapter) and what the backward reads: row_lse
+ * f32 [R] and col_coef f32 [C][2] (8-byte aligned) = {C counts_c / R^2,
+ * 4 (mean_r p_rc^2 - 1/C) / (C R)}.  Deterministic (fixed-order sums, integer counts).
+ * C <= 16384. */
+size_t moc_router_losses_workspace(int64_t R, int64_t C);
+int moc_router_losses(const float* logits, int64_t R, int64_t C, const int32_t* idx, int k, float* row_lse,
+                      float* col_coef, int32_t* counts, float* losses, void* workspace, size_t workspace_bytes,
+                      hipStream_t stream);
+/* dlogits f32 [R, C] = d(sum_i dlosses[i] losses[i]) / d logits, dlosses f32 [4] on the device
+ * (the selection counts are constants, as the reference's one-hot is). */
+int moc_router_losses_bwd(const float* logits, int64_t R, int64_t C, const float* row_lse, const float* col_coef,
+                          const float* dlosses, float* dlogits, hipStream_t stream);
+
 /* ------------------------------------------------------------- chapter plan */
 
 /* De-duplicates the chapters of E edges and builds the chapter -> edges inverted index

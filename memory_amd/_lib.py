@@ -41,6 +41,9 @@ _SIGS = {
     "moc_router_linear": (_I, [_P, _I64, _I64, _P, _I, _P, _I64, _P, _P]),
     "moc_router_linear_bwd_workspace": (_SZ, [_I64, _I64, _I64]),
     "moc_router_linear_bwd": (_I, [_P, _P, _I64, _I64, _P, _I, _I64, _P, _P, _P, _P, _SZ, _P]),
+    "moc_router_losses_workspace": (_SZ, [_I64, _I64]),
+    "moc_router_losses": (_I, [_P, _I64, _I64, _P, _I, _P, _P, _P, _P, _P, _SZ, _P]),
+    "moc_router_losses_bwd": (_I, [_P, _I64, _I64, _P, _P, _P, _P, _P]),
     "moc_chapter_plan_workspace": (_SZ, [_I64, _I64]),
     "moc_chapter_plan": (_I, [_P, _I64, _I64, _P, _SZ, _P, _P, _P, _P, _P, _P]),
     "moc_row_stats": (_I, [_P, _I, _I64, _I, _P, _P, _I64, _I, _F, _P, _P, _P]),

@@ -536,6 +536,275 @@ __global__ __launch_bounds__(256) void router_linear_bwd_kernel(const float* __r
   }
 }
 
+// ------------------------------------------------------------ router auxiliary losses
+// ChapterRouter._compute_losses (router.py:197-260) on logits z [R][C] and the selected
+// chapter ids I [R][k], p = softmax(z) per row:
+//   load_balance = C sum_c f_c P_c,  f_c = counts_c / R (selections of c),  P_c = mean_r p_rc
+//   auxiliary    = mean_c (Q_c - 1/C)^2,  Q_c = mean_r p_rc^2   (F.mse_loss)
+//   z_loss       = mean_r lse_r^2,  lse_r = log sum_c exp z_rc
+//   entropy      = -mean_r sum_c p_rc log(max(p_rc, 1e-12))
+// Row statistics one wave per row (lse, entropy; the row's selections counted by exact
+// integer atomics), the column sums of p and p^2 one thread per column over a slice of rows
+// (coalesced; partials reduced in a fixed order by pool_reduce), then one workgroup for the
+// four scalars.  The backward is one wave per row.
+constexpr int kLossThreads = 256;
+constexpr int kLossColRows = 128;          // rows per column-sum workgroup
+constexpr int kLossFinalThreads = 1024;
+
+__global__ __launch_bounds__(kLossThreads) void router_loss_zero_kernel(int32_t* __restrict__ counts, int64_t C) {
+  const int64_t c = (int64_t)blockIdx.x * kLossThreads + threadIdx.x;
+  if (c < C) counts[c] = 0;
+}
+
+// log(1e-12): the floor the entropy term's clamp puts under log p
+constexpr float kLogPFloor = -27.631021115928547f;
+// Rows of up to kLossThreads * kLossRowCols chapters are held in registers by one workgroup
+// (one read of the logits, all loads in flight at once); longer rows are streamed by one
+// wave each.
+constexpr int kLossRowCols = 18;
+
+// Streamed: one wave per row, three passes over the row.
+__global__ __launch_bounds__(kLossThreads) void router_loss_rowstats_kernel(
+    const float* __restrict__ z, int64_t R, int64_t C, const int32_t* __restrict__ idx, int k,
+    float* __restrict__ row_lse, float* __restrict__ row_ent, int32_t* __restrict__ counts) {
+  const int64_t r = (int64_t)blockIdx.x * (kLossThreads / 64) + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (r >= R) return;
+  const float* zr = z + r * C;
+  float m = -INFINITY;
+  for (int64_t c = lane; c < C; c += 64) m = fmaxf(m, zr[c]);
+  m = wave_max(m);
+  float s = 0.f;
+  for (int64_t c = lane; c < C; c += 64) s += __expf(zr[c] - m);
+  const float lse = m + __logf(wave_sum(s));
+  float e = 0.f;
+  for (int64_t c = lane; c < C; c += 64) {
+    const float lz = zr[c] - lse;
+    e += __expf(lz) * fmaxf(lz, kLogPFloor);
+  }
+  e = wave_sum(e);
+  if (lane == 0) {
+    row_lse[r] = lse;
+    row_ent[r] = e;
+  }
+  for (int j = lane; j < k; j += 64) {
+    const int32_t c = idx[r * k + j];
+    if (c >= 0 && c < C) atomicAdd(&counts[c], 1);   // integer: exact in any order
+  }
+}
+
+// Register-resident: one workgroup per row (C <= kLossThreads * kLossRowCols).
+// p log max(p, 1e-12) is taken with log p = z - lse (no log per element); past the row
+// z = -inf, p = 0 and the term vanishes.
+__global__ __launch_bounds__(kLossThreads) void router_loss_rowstats_block_kernel(
+    const float* __restrict__ z, int64_t R, int64_t C, const int32_t* __restrict__ idx, int k,
+    float* __restrict__ row_lse, float* __restrict__ row_ent, int32_t* __restrict__ counts) {
+  __shared__ float red[kLossThreads / 64];
+  const int64_t r = blockIdx.x;
+  const int tid = threadIdx.x;
+  const float* zr = z + r * C;
+  float v[kLossRowCols];
+#pragma unroll
+  for (int i = 0; i < kLossRowCols; ++i) {
+    const int64_t c = tid + kLossThreads * i;
+    v[i] = c < C ? zr[c] : -INFINITY;
+  }
+  float m = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < kLossRowCols; ++i) m = fmaxf(m, v[i]);
+  m = block_reduce_max<kLossThreads>(m, red);
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < kLossRowCols; ++i) s += __expf(v[i] - m);
+  const float lse = m + __logf(block_reduce_sum<kLossThreads>(s, red));
+  float e = 0.f;
+#pragma unroll
+  for (int i = 0; i < kLossRowCols; ++i) {
+    const float lz = v[i] - lse;
+    e += __expf(lz) * fmaxf(lz, kLogPFloor);
+  }
+  e = block_reduce_sum<kLossThreads>(e, red);
+  if (tid == 0) {
+    row_lse[r] = lse;
+    row_ent[r] = e;
+  }
+  for (int j = tid; j < k; j += kLossThreads) {
+    const int32_t c = idx[r * k + j];
+    if (c >= 0 && c < C) atomicAdd(&counts[c], 1);
+  }
+}
+
+// part[split][0][c] = sum over the split's rows of p_rc, part[split][1][c] of p_rc^2
+__global__ __launch_bounds__(kLossThreads) void router_loss_colsum_kernel(const float* __restrict__ z, int64_t R,
+                                                                          int64_t C,
+                                                                          const float* __restrict__ row_lse,
+                                                                          float* __restrict__ part) {
+  const int64_t c = (int64_t)blockIdx.x * kLossThreads + threadIdx.x;
+  const int64_t r0 = (int64_t)blockIdx.y * kLossColRows, r1 = min(R, r0 + kLossColRows);
+  if (c >= C) return;
+  float sp = 0.f, sq = 0.f;
+  int64_t r = r0;
+  for (; r + 4 <= r1; r += 4) {
+    float p[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) p[u] = __expf(z[(r + u) * C + c] - row_lse[r + u]);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      sp += p[u];
+      sq += p[u] * p[u];
+    }
+  }
+  for (; r < r1; ++r) {
+    const float p = __expf(z[r * C + c] - row_lse[r]);
+    sp += p;
+    sq += p * p;
+  }
+  float* dst = part + (int64_t)blockIdx.y * 2 * C;
+  dst[c] = sp;
+  dst[C + c] = sq;
+}
+
+// losses[4] = {load_balance, auxiliary, z_loss, entropy}; coef[c] = the column's terms of the
+// backward's per-element gradient (before the incoming loss gradients scale them):
+//   coef[c].x = C counts_c / R^2          (load balance, d/dp_rc)
+//   coef[c].y = 4 (Q_c - 1/C) / (C R)     (auxiliary, d/dp_rc per unit p_rc; Q_c = mean_r p_rc^2)
+__global__ __launch_bounds__(kLossFinalThreads) void router_loss_final_kernel(
+    const float* __restrict__ col, const float* __restrict__ row_lse, const float* __restrict__ row_ent,
+    const int32_t* __restrict__ counts, int64_t R, int64_t C, float* __restrict__ losses,
+    float2* __restrict__ coef) {
+  __shared__ float red[kLossFinalThreads / 64];
+  const int tid = threadIdx.x;
+  const float invC = 1.f / (float)C, invR = 1.f / (float)R;
+  const float cLB = (float)C * invR * invR, cAux = 4.f * invC * invR;
+  // loads batched kUnroll at a time (one workgroup: latency, not bandwidth, bounds this kernel)
+  constexpr int kUnroll = 4;
+  float lb = 0.f, aux = 0.f;
+  for (int64_t c0 = tid; c0 < C; c0 += kUnroll * kLossFinalThreads) {
+    float n[kUnroll], pc[kUnroll], qc[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t c = c0 + u * kLossFinalThreads;
+      n[u] = c < C ? (float)counts[c] : 0.f;
+      pc[u] = c < C ? col[c] : 0.f;
+      qc[u] = c < C ? col[C + c] : 0.f;
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t c = c0 + u * kLossFinalThreads;
+      if (c < C) {
+        lb += n[u] * pc[u];
+        const float t = qc[u] * invR - invC;
+        aux += t * t;
+        coef[c] = make_float2(cLB * n[u], cAux * t);
+      }
+    }
+  }
+  lb = block_reduce_sum<kLossFinalThreads>(lb, red);
+  aux = block_reduce_sum<kLossFinalThreads>(aux, red);
+  float zl = 0.f, en = 0.f;
+  for (int64_t r0 = tid; r0 < R; r0 += kUnroll * kLossFinalThreads) {
+    float l[kUnroll], e[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t r = r0 + u * kLossFinalThreads;
+      l[u] = r < R ? row_lse[r] : 0.f;
+      e[u] = r < R ? row_ent[r] : 0.f;
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      zl += l[u] * l[u];
+      en += e[u];
+    }
+  }
+  zl = block_reduce_sum<kLossFinalThreads>(zl, red);
+  en = block_reduce_sum<kLossFinalThreads>(en, red);
+  if (tid == 0) {
+    losses[0] = (float)C * lb * invR * invR;
+    losses[1] = aux * invC;
+    losses[2] = zl * invR;
+    losses[3] = -en * invR;
+  }
+}
+
+// Backward: dz_rc = p_rc (g_rc - sum_c' p_rc' g_rc' + gz (2 / R) lse_r) with
+//   g_rc = gLB coef_c.x + gaux coef_c.y p_rc - gent (log max(p_rc, 1e-12) + [p_rc > 1e-12]) / R
+// (dlosses = {gLB, gaux, gz, gent} on the device; coef from router_loss_final_kernel;
+// log p_rc = z_rc - lse_r).
+struct LossGrad {
+  const float2* coef;
+  float gLB, gaux, cEnt, zc;
+  __device__ LossGrad(const float2* cf, const float* dlosses, int64_t R, float lse) : coef(cf) {
+    const float invR = 1.f / (float)R;
+    gLB = dlosses[0];
+    gaux = dlosses[1];
+    zc = dlosses[2] * 2.f * invR * lse;
+    cEnt = dlosses[3] * invR;
+  }
+  // g_rc from log p_rc and p_rc
+  __device__ float operator()(int64_t c, float lz, float p) const {
+    const float2 cf = coef[c];
+    return gLB * cf.x + gaux * cf.y * p - cEnt * (lz > kLogPFloor ? lz + 1.f : kLogPFloor);
+  }
+};
+
+// Streamed: one wave per row, two passes over the row.
+__global__ __launch_bounds__(kLossThreads) void router_loss_bwd_kernel(
+    const float* __restrict__ z, int64_t R, int64_t C, const float* __restrict__ row_lse,
+    const float2* __restrict__ coef, const float* __restrict__ dlosses, float* __restrict__ dz) {
+  const int64_t r = (int64_t)blockIdx.x * (kLossThreads / 64) + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (r >= R) return;
+  const float* zr = z + r * C;
+  const float lse = row_lse[r];
+  const LossGrad g(coef, dlosses, R, lse);
+  float s = 0.f;
+  for (int64_t c = lane; c < C; c += 64) {
+    const float lz = zr[c] - lse, p = __expf(lz);
+    s += p * g(c, lz, p);
+  }
+  s = wave_sum(s);
+  float* o = dz + r * C;
+  for (int64_t c = lane; c < C; c += 64) {
+    const float lz = zr[c] - lse, p = __expf(lz);
+    o[c] = p * (g(c, lz, p) - s + g.zc);
+  }
+}
+
+// Register-resident: one workgroup per row (C <= kLossThreads * kLossRowCols).
+__global__ __launch_bounds__(kLossThreads) void router_loss_bwd_block_kernel(
+    const float* __restrict__ z, int64_t R, int64_t C, const float* __restrict__ row_lse,
+    const float2* __restrict__ coef, const float* __restrict__ dlosses, float* __restrict__ dz) {
+  __shared__ float red[kLossThreads / 64];
+  const int64_t r = blockIdx.x;
+  const int tid = threadIdx.x;
+  const float* zr = z + r * C;
+  const float lse = row_lse[r];
+  const LossGrad g(coef, dlosses, R, lse);
+  // p[i] = p_rc, pg[i] = p_rc g_rc (0 past the row)
+  float p[kLossRowCols], pg[kLossRowCols];
+#pragma unroll
+  for (int i = 0; i < kLossRowCols; ++i) {
+    const int64_t c = tid + kLossThreads * i;
+    p[i] = c < C ? zr[c] - lse : -INFINITY;
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < kLossRowCols; ++i) {
+    const int64_t c = tid + kLossThreads * i;
+    const float lz = p[i];
+    p[i] = __expf(lz);
+    pg[i] = c < C ? p[i] * g(c, lz, p[i]) : 0.f;
+    s += pg[i];
+  }
+  s = block_reduce_sum<kLossThreads>(s, red) - g.zc;
+  float* o = dz + r * C;
+#pragma unroll
+  for (int i = 0; i < kLossRowCols; ++i) {
+    const int64_t c = tid + kLossThreads * i;
+    if (c < C) o[c] = pg[i] - p[i] * s;
+  }
+}
+
 }  // namespace moc
 
 using namespace moc;
@@ -701,6 +970,68 @@ int moc_router_linear_bwd(const float* dz, const float* x, int64_t R, int64_t d,
   hipLaunchKernelGGL(pool_reduce_kernel, dim3((unsigned)((R * d + 63) / 64)), dim3(256), 0, stream, part, (int)nwg, R,
                      d, 1.f, dx);
   return check_launch("pool_reduce_kernel");
+}
+
+size_t moc_router_losses_workspace(int64_t R, int64_t C) {
+  const int64_t nsplit = (R + kLossColRows - 1) / kLossColRows;
+  // column-sum partials [nsplit][2][C], column sums [2][C], row entropies [R]
+  return (size_t)(nsplit * 2 * C + 2 * C + R) * sizeof(float);
+}
+
+int moc_router_losses(const float* logits, int64_t R, int64_t C, const int32_t* idx, int k, float* row_lse,
+                      float* col_coef, int32_t* counts, float* losses, void* workspace, size_t workspace_bytes,
+                      hipStream_t stream) {
+  MOC_REQUIRE(logits && row_lse && col_coef && counts && losses && workspace && (idx || k == 0), MOC_ERR_ARG,
+              "moc_router_losses: null pointer");
+  MOC_REQUIRE(R > 0 && C > 0 && k >= 0, MOC_ERR_ARG, "moc_router_losses: bad shape R=%lld C=%lld k=%d", (long long)R,
+              (long long)C, k);
+  MOC_REQUIRE(C <= kMaxRouterC, MOC_ERR_UNSUPPORTED, "moc_router_losses: C=%lld exceeds %d", (long long)C, kMaxRouterC);
+  MOC_REQUIRE(R < ((int64_t)1 << 31) / 4, MOC_ERR_UNSUPPORTED, "moc_router_losses: too many rows");
+  MOC_REQUIRE(workspace_bytes >= moc_router_losses_workspace(R, C), MOC_ERR_ARG, "moc_router_losses: workspace too small");
+  MOC_REQUIRE(((uintptr_t)col_coef & 7) == 0 && ((uintptr_t)workspace & 3) == 0, MOC_ERR_ARG,
+              "moc_router_losses: col_coef must be 8-byte and workspace 4-byte aligned");
+  const int64_t nsplit = (R + kLossColRows - 1) / kLossColRows;
+  float* part = (float*)workspace;
+  float* col_sums = part + nsplit * 2 * C;
+  float* row_ent = col_sums + 2 * C;
+  const unsigned cblk = (unsigned)((C + kLossThreads - 1) / kLossThreads);
+  hipLaunchKernelGGL(router_loss_zero_kernel, dim3(cblk), dim3(kLossThreads), 0, stream, counts, C);
+  int rc = check_launch("router_loss_zero_kernel");
+  if (rc) return rc;
+  if (C <= kLossThreads * kLossRowCols)
+    hipLaunchKernelGGL(router_loss_rowstats_block_kernel, dim3((unsigned)R), dim3(kLossThreads), 0, stream, logits, R,
+                       C, idx, k, row_lse, row_ent, counts);
+  else
+    hipLaunchKernelGGL(router_loss_rowstats_kernel, dim3((unsigned)((R + 3) / 4)), dim3(kLossThreads), 0, stream,
+                       logits, R, C, idx, k, row_lse, row_ent, counts);
+  rc = check_launch("router_loss_rowstats_kernel");
+  if (rc) return rc;
+  hipLaunchKernelGGL(router_loss_colsum_kernel, dim3(cblk, (unsigned)nsplit), dim3(kLossThreads), 0, stream, logits,
+                     R, C, row_lse, part);
+  rc = check_launch("router_loss_colsum_kernel");
+  if (rc) return rc;
+  hipLaunchKernelGGL(pool_reduce_kernel, dim3((unsigned)((2 * C + 63) / 64)), dim3(256), 0, stream, part, (int)nsplit,
+                     (int64_t)1, 2 * C, 1.f, col_sums);
+  rc = check_launch("pool_reduce_kernel");
+  if (rc) return rc;
+  hipLaunchKernelGGL(router_loss_final_kernel, dim3(1), dim3(kLossFinalThreads), 0, stream, col_sums, row_lse, row_ent,
+                     counts, R, C, losses, (float2*)col_coef);
+  return check_launch("router_loss_final_kernel");
+}
+
+int moc_router_losses_bwd(const float* logits, int64_t R, int64_t C, const float* row_lse, const float* col_coef,
+                          const float* dlosses, float* dlogits, hipStream_t stream) {
+  MOC_REQUIRE(logits && row_lse && col_coef && dlosses && dlogits, MOC_ERR_ARG, "moc_router_losses_bwd: null pointer");
+  MOC_REQUIRE(R > 0 && C > 0 && R < ((int64_t)1 << 31), MOC_ERR_ARG, "moc_router_losses_bwd: bad shape");
+  MOC_REQUIRE(((uintptr_t)col_coef & 7) == 0, MOC_ERR_ARG, "moc_router_losses_bwd: col_coef must be 8-byte aligned");
+  const float2* cf = (const float2*)col_coef;
+  if (C <= kLossThreads * kLossRowCols)
+    hipLaunchKernelGGL(router_loss_bwd_block_kernel, dim3((unsigned)R), dim3(kLossThreads), 0, stream, logits, R, C,
+                       row_lse, cf, dlosses, dlogits);
+  else
+    hipLaunchKernelGGL(router_loss_bwd_kernel, dim3((unsigned)((R + 3) / 4)), dim3(kLossThreads), 0, stream, logits,
+                       R, C, row_lse, cf, dlosses, dlogits);
+  return check_launch("router_loss_bwd_kernel");
 }
 
 }  // extern "C"

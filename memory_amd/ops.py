@@ -446,6 +446,52 @@ class _TokenRouterLinear(torch.autograd.Function):
         return dx, dW, db
 
 
+class _RouterLosses(torch.autograd.Function):
+    """The router's auxiliary losses (router.py:197-260) in one pass over the logits:
+    returns f32 [4] = (load_balance, auxiliary, z_loss, entropy); the gradient flows to the
+    logits (the selection counts are constants, as the reference's one-hot is)."""
+
+    @staticmethod
+    def forward(ctx, logits: torch.Tensor, idx: torch.Tensor, num_chapters: int):
+        L.require_gpu(logits, idx)
+        z = logits.reshape(-1, logits.shape[-1]).float().contiguous()
+        R, C = z.shape
+        if C != int(num_chapters):
+            raise ValueError(f"logits have {C} chapters, expected {num_chapters}")
+        sel = idx.reshape(R, -1).to(torch.int32).contiguous()
+        k = sel.shape[1]
+        dev = z.device
+        row_lse = torch.empty(R, device=dev, dtype=torch.float32)
+        coef = torch.empty(C, 2, device=dev, dtype=torch.float32)
+        counts = torch.empty(C, device=dev, dtype=torch.int32)
+        losses = torch.empty(4, device=dev, dtype=torch.float32)
+        ws_bytes = L.query("moc_router_losses_workspace", R, C)
+        ws = torch.empty(ws_bytes // 4, device=dev, dtype=torch.float32)
+        call("moc_router_losses", ptr(z), R, C, ptr(sel) if k else None, k, ptr(row_lse), ptr(coef), ptr(counts),
+             ptr(losses), ptr(ws), ws_bytes, stream_ptr(dev))
+        ctx.save_for_backward(z, row_lse, coef)
+        ctx.shape, ctx.dtype = logits.shape, logits.dtype
+        return losses
+
+    @staticmethod
+    def backward(ctx, dlosses):
+        z, row_lse, coef = ctx.saved_tensors
+        R, C = z.shape
+        dz = torch.empty_like(z)
+        g = dlosses.float().contiguous()
+        call("moc_router_losses_bwd", ptr(z), R, C, ptr(row_lse), ptr(coef), ptr(g), ptr(dz), stream_ptr(z.device))
+        return dz.view(ctx.shape).to(ctx.dtype), None, None
+
+
+ROUTER_LOSS_NAMES = ("load_balance", "auxiliary", "z_loss", "entropy")
+
+
+def router_losses(logits: torch.Tensor, idx: torch.Tensor, num_chapters: int):
+    """Dict of the four router losses (scalar tensors) on the fused kernels."""
+    v = _RouterLosses.apply(logits, idx, int(num_chapters))
+    return {n: v[i] for i, n in enumerate(ROUTER_LOSS_NAMES)}
+
+
 def col_sum(x: torch.Tensor) -> torch.Tensor:
     """Column sums (fp32) of a 2-D fp32 / bf16 matrix on the router's pooling kernels
     (fixed-order split-row partials, deterministic)."""

@@ -247,3 +247,27 @@ def test_routed_attention_forward(dev, dtype, B, Lq, H, HK, norm):
     ref = O.attention(qr, kr, vr)
     tol = 1e-4 if dtype == torch.float32 else 2e-2
     assert_rel(out.cpu(), ref, tol, "attention output")
+
+
+@pytest.mark.parametrize("R,C,k,scale", [(8, 4097, 64, 1.0), (300, 257, 5, 3.0), (1, 33, 4, 1.0),
+                                         (1024, 4097, 16, 0.5), (5, 16000, 3, 1.0), (40, 65, 0, 1.0),
+                                         (7, 4608, 8, 1.0), (7, 4609, 8, 1.0)])
+def test_router_losses_fused_match_oracle(dev, R, C, k, scale):
+    """The fused router-loss kernels (router.py:197-260): the four losses and the gradient of a
+    random combination of them w.r.t. the logits, against the oracle in float64."""
+    print(f"router losses R={R} C={C} k={k}", flush=True)
+    g = gen(R + C + k)
+    logits = torch.randn(R, C, generator=g, dtype=torch.float64) * scale
+    logits[0, : min(5, C)] += 6.0          # a peaked row (entropy / z-loss away from uniform)
+    idx = torch.stack([torch.randperm(C, generator=g)[:k] for _ in range(R)]) if k else torch.empty(R, 0, dtype=torch.long)
+    coef = torch.rand(4, generator=g, dtype=torch.float64) + 0.5
+    lr = logits.clone().requires_grad_(True)
+    ref = O.router_losses(lr, torch.softmax(lr, dim=-1), idx, C)
+    names = ("load_balance", "auxiliary", "z_loss", "entropy")
+    sum(coef[i] * ref[n] for i, n in enumerate(names)).backward()
+    lg = logits.float().to(dev).requires_grad_(True)
+    got = _ops().router_losses(lg, idx.to(dev), C)
+    sum(float(coef[i]) * got[n] for i, n in enumerate(names)).backward()
+    for n in names:
+        assert_rel(got[n].reshape(1).cpu(), ref[n].reshape(1).detach(), 1e-5, n)
+    assert_rel(lg.grad.cpu(), lr.grad, 1e-4, "dlogits")
