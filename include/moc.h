@@ -226,6 +226,50 @@ int moc_bank_scatter(int dx_dtype, const void* dX, const void* bank, int bank_dt
                      const int32_t* csr_edge, const float* row_mean, const float* row_rstd, int norm,
                      void* grad_bank, hipStream_t stream);
 
+/* Row-sparse bank gradient (no counterpart in the reference, whose bank gradient is the dense
+ * autograd result of the gather, memory_bank.py:287-291): the same rows as moc_bank_scatter,
+ * accumulated in f32 grad_acc [N_m][d] for the chapters of the current `epoch`.  chap_epoch
+ * i32 [C] tags which chapters already hold rows for the epoch: a chapter's first contribution
+ * is stored, later ones (other layers sharing the bank, further micro-batches) are added, so
+ * the accumulator is never zero-filled.  fresh i32 [max_u] is scratch. */
+int moc_bank_grad_accumulate(int dx_dtype, const void* dX, const void* bank, int bank_dtype, int64_t d, int T,
+                             const int32_t* uniq, const int32_t* n_uniq, int64_t max_u, const int32_t* csr_off,
+                             const int32_t* csr_edge, const float* row_mean, const float* row_rstd, int norm,
+                             int epoch, int32_t* chap_epoch, int32_t* fresh, float* grad_acc, hipStream_t stream);
+
+/* ------------------------------------------------------------ bank optimizer */
+
+/* torch.optim.AdamW as the reference steps the bank (training/trainer.py:309-392, param group
+ * "memory_bank"; torch >= 2.0 foreach algorithm, amsgrad off) for an f32 bank of num_chapters
+ * chapter blocks of chunk_elems = T * d contiguous elements, optionally mirrored to a bf16 copy
+ * (mirror_dtype MOC_BF16) that the forward kernels read.  Per element and step j:
+ *   p = p (1 - lr_j wd); m = lerp(m, g, 1 - beta1); v = v beta2 + (1 - beta2) g g;
+ *   p = p + (-lr_j / bc1_j) m / (sqrt(v) / sqrt(bc2_j) + eps).
+ * Each chunk of a chapter block carries in tags i32 [num_chapters * moc_bank_chunk_count] the
+ * step it is current to; hist f32 [hist_capacity][4] holds per step j the scalars
+ * {1 - lr_j wd, -lr_j / bc1_j, sqrt(bc2_j), 0}.
+ * grad != NULL: optimizer step `step` (scalars decay / neg_step_size / bc2_sqrt, recorded into
+ *   hist[step]) with gradient grad * grad_scale[0] (grad_scale may be NULL) on the listed chapters
+ *   (list i32, n_list[0] of them, at most max_list; NULL list = every chapter, dense), each chunk
+ *   first brought to step-1 with zero-gradient steps.
+ * grad == NULL: bring the listed chapters to `step` (zero-gradient steps from hist) — run before
+ *   chapters are read.  Rows outside the list are left as they are (they are behind, exactly by
+ *   their zero-gradient steps). */
+int moc_bank_chunk_count(int64_t chunk_elems);
+int moc_bank_adamw(float* param, void* mirror, int mirror_dtype, float* exp_avg, float* exp_avg_sq, const float* grad,
+                   const float* grad_scale, const int32_t* list, const int32_t* n_list, int64_t max_list,
+                   int64_t num_chapters, int64_t chunk_elems, int32_t* tags, float* hist, int64_t hist_capacity,
+                   int step, float decay, float neg_step_size, float bc2_sqrt, float beta1, float beta2, float eps,
+                   hipStream_t stream);
+/* list = the chapters whose chap_epoch equals epoch, ascending; n_list[0] = their number. */
+int moc_bank_touched(const int32_t* chap_epoch, int64_t num_chapters, int epoch, int32_t* list, int32_t* n_list,
+                     hipStream_t stream);
+/* out[0] = sum of g^2 over the listed chapters' blocks (NULL list: the first max_list chapters),
+ * fixed order.  Feeds the global norm of clip_grad_norm_ (trainer.py:876-882). */
+size_t moc_bank_sqnorm_workspace(int64_t max_list, int64_t chunk_elems);
+int moc_bank_sqnorm(const float* grad, const int32_t* list, const int32_t* n_list, int64_t max_list,
+                    int64_t chunk_elems, void* workspace, size_t workspace_bytes, float* out, hipStream_t stream);
+
 /* -------------------------------------------- token-routed sparse attention */
 
 /* Token-level routing (every query token picks its own chapters): the per-chapter

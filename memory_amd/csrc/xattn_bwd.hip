@@ -597,7 +597,8 @@ __global__ __launch_bounds__(256) void gather_rows_kernel(const TB* __restrict__
 // per distinct-chapter row) or, given the plan's inverted index, the sum over the chapter's
 // edges (csr order, deterministic) of the per-edge rows dX[e * T + t, :].  Distinct chapters
 // own distinct bank rows, so plain stores suffice (grad_bank must be zero-initialised by the
-// caller for rows that are not selected).
+// caller for rows that are not selected).  With `fresh` (accumulator mode) chapter u's rows are
+// stored when fresh[u] is set and added to the rows already there otherwise.
 template <typename TX, typename TB, typename TG>
 __global__ __launch_bounds__(256) void bank_scatter_kernel(const TX* __restrict__ dX, const TB* __restrict__ bank,
                                                            int64_t d, int Tc, const int32_t* __restrict__ uniq,
@@ -606,6 +607,7 @@ __global__ __launch_bounds__(256) void bank_scatter_kernel(const TX* __restrict_
                                                            const int32_t* __restrict__ csr_edge,
                                                            const float* __restrict__ mean,
                                                            const float* __restrict__ rstd, int layernorm,
+                                                           const int32_t* __restrict__ fresh,
                                                            TG* __restrict__ grad) {
   const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
@@ -629,11 +631,21 @@ __global__ __launch_bounds__(256) void bank_scatter_kernel(const TX* __restrict_
     }
   };
   TG* o = grad + src * d;
+  const bool add = fresh != nullptr && fresh[u] == 0;
+  auto put = [&](int64_t j, float* gv) {
+    if (add) {
+      float old8[8];
+      load8f<TG, TG>(o + j, old8);
+#pragma unroll
+      for (int x = 0; x < 8; ++x) gv[x] += old8[x];
+    }
+    store8f<TG>(o + j, gv);
+  };
   float gv[8];
   if (!rstd) {
     for (int64_t j = 8 * lane; j < d; j += 512) {
       grow(j, gv);
-      store8f<TG>(o + j, gv);
+      put(j, gv);
     }
     return;
   }
@@ -656,8 +668,21 @@ __global__ __launch_bounds__(256) void bank_scatter_kernel(const TX* __restrict_
     load8f<TG, TB>(xr + j, xv);
 #pragma unroll
     for (int x = 0; x < 8; ++x) gv[x] = rs * (gv[x] - (layernorm ? sg : 0.f) - (xv[x] - mu) * rs * sgx);
-    store8f<TG>(o + j, gv);
+    put(j, gv);
   }
+}
+
+// fresh[u] = 1 when chapter uniq[u] has no rows in the accumulator for `epoch` yet (its tag
+// differs), 0 otherwise; the tag is then set.  The plan's chapters are distinct.
+__global__ __launch_bounds__(256) void bank_grad_mark_kernel(const int32_t* __restrict__ uniq,
+                                                             const int32_t* __restrict__ n_uniq, int64_t max_u,
+                                                             int epoch, int32_t* __restrict__ chap_epoch,
+                                                             int32_t* __restrict__ fresh) {
+  const int64_t u = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (u >= max_u || u >= (int64_t)n_uniq[0]) return;
+  const int32_t c = uniq[u];
+  fresh[u] = chap_epoch[c] != epoch ? 1 : 0;
+  chap_epoch[c] = epoch;
 }
 
 }  // namespace moc
@@ -796,13 +821,45 @@ int moc_bank_scatter(int dx_dtype, const void* dX, const void* bank, int bank_dt
   const int ln = norm == MOC_NORM_LAYERNORM;
 #define BS(TX, BT)                                                                                                     \
   hipLaunchKernelGGL((bank_scatter_kernel<TX, BT, BT>), grid, dim3(256), 0, stream, (const TX*)dX, (const BT*)bank, d, \
-                     T, uniq, n_uniq, rows, csr_off, csr_edge, row_mean, row_rstd, ln, (BT*)grad_bank)
+                     T, uniq, n_uniq, rows, csr_off, csr_edge, row_mean, row_rstd, ln, nullptr, (BT*)grad_bank)
   if (dx_dtype == MOC_BF16 && bank_dtype == MOC_BF16) BS(bf16, bf16);
   else if (dx_dtype == MOC_BF16 && bank_dtype == MOC_F32) BS(bf16, float);
   else if (dx_dtype == MOC_F32 && bank_dtype == MOC_F32) BS(float, float);
   else if (dx_dtype == MOC_F32 && bank_dtype == MOC_BF16) BS(float, bf16);
   else return set_error(MOC_ERR_UNSUPPORTED, "moc_bank_scatter: dtypes %d/%d", dx_dtype, bank_dtype);
 #undef BS
+  return check_launch("bank_scatter_kernel");
+}
+
+int moc_bank_grad_accumulate(int dx_dtype, const void* dX, const void* bank, int bank_dtype, int64_t d, int T,
+                             const int32_t* uniq, const int32_t* n_uniq, int64_t max_u, const int32_t* csr_off,
+                             const int32_t* csr_edge, const float* row_mean, const float* row_rstd, int norm,
+                             int epoch, int32_t* chap_epoch, int32_t* fresh, float* grad_acc, hipStream_t stream) {
+  MOC_REQUIRE(dX && bank && uniq && n_uniq && chap_epoch && fresh && grad_acc, MOC_ERR_ARG,
+              "moc_bank_grad_accumulate: null pointer");
+  MOC_REQUIRE((csr_off == nullptr) == (csr_edge == nullptr), MOC_ERR_ARG,
+              "moc_bank_grad_accumulate: csr_off / csr_edge must be both set or both null");
+  MOC_REQUIRE(d % 8 == 0, MOC_ERR_UNSUPPORTED, "moc_bank_grad_accumulate: d=%lld must be a multiple of 8",
+              (long long)d);
+  MOC_REQUIRE((norm == MOC_NORM_NONE) == (row_rstd == nullptr), MOC_ERR_ARG,
+              "moc_bank_grad_accumulate: norm/stats mismatch");
+  if (max_u == 0) return MOC_OK;
+  hipLaunchKernelGGL(bank_grad_mark_kernel, dim3((unsigned)((max_u + 255) / 256)), dim3(256), 0, stream, uniq, n_uniq,
+                     max_u, epoch, chap_epoch, fresh);
+  int rc = check_launch("bank_grad_mark_kernel");
+  if (rc) return rc;
+  const int64_t rows = max_u * T;
+  dim3 grid((unsigned)((rows + 3) / 4));
+  const int ln = norm == MOC_NORM_LAYERNORM;
+#define BA(TX, BT)                                                                                                     \
+  hipLaunchKernelGGL((bank_scatter_kernel<TX, BT, float>), grid, dim3(256), 0, stream, (const TX*)dX, (const BT*)bank, \
+                     d, T, uniq, n_uniq, rows, csr_off, csr_edge, row_mean, row_rstd, ln, fresh, grad_acc)
+  if (dx_dtype == MOC_BF16 && bank_dtype == MOC_BF16) BA(bf16, bf16);
+  else if (dx_dtype == MOC_BF16 && bank_dtype == MOC_F32) BA(bf16, float);
+  else if (dx_dtype == MOC_F32 && bank_dtype == MOC_F32) BA(float, float);
+  else if (dx_dtype == MOC_F32 && bank_dtype == MOC_BF16) BA(float, bf16);
+  else return set_error(MOC_ERR_UNSUPPORTED, "moc_bank_grad_accumulate: dtypes %d/%d", dx_dtype, bank_dtype);
+#undef BA
   return check_launch("bank_scatter_kernel");
 }
 

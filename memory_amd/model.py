@@ -181,6 +181,9 @@ class TokenRoutedMemoryLayer(nn.Module):
         S, T = self.num_shared_chapters, self.tokens_per_chapter
         idx, w, losses = self.router.route_token_level(hidden_states, return_losses=return_losses,
                                                        exclude_prefix_chapters=S)
+        opt = getattr(bank, "_moc_bank_opt", None)
+        if opt is not None:
+            opt.catch_up()   # every chapter is projected: bring the whole bank to the last step
         st = min(S * T, bank.shape[0])
         src = bank
         if self.normalize and 0 < st < bank.shape[0]:

@@ -305,11 +305,20 @@ class _RoutedAttention(torch.autograd.Function):
     def forward(ctx, q, bank, wk, wv, omega, idx_star, num_chapters, T, norm, eps, HK):
         L.require_gpu(q, bank, wk, wv, omega, idx_star)
         dtype = q.dtype
+        bank_dtype = bank.dtype
         B, Lq, H, Dh = q.shape
         NS = idx_star.shape[1]
         q = q.contiguous()
-        bank = bank.contiguous()
+        # a bank stepped by BankAdamW: its plan's chapters are brought to the last step before
+        # they are read, and the forward kernels read its mirror when it keeps one; a bank with
+        # a RowSparseBankGrad receives its gradient rows there instead of a dense gradient
+        opt = getattr(bank, "_moc_bank_opt", None)
+        ctx.row_grad = getattr(bank, "_moc_row_grad", None)
         plan = chapter_plan(idx_star, num_chapters)
+        if opt is not None:
+            opt.catch_up(plan.uniq, plan.n_uniq, plan.max_u)
+            bank = opt.read_view()
+        bank = bank.contiguous()
         mean = rstd = None
         if norm != L.MOC_NORM_NONE:
             mean, rstd = row_stats(bank, plan, T, norm, eps)
@@ -323,7 +332,7 @@ class _RoutedAttention(torch.autograd.Function):
              ptr(om), B, Lq, H, HK, Dh, T, NS, float(Dh) ** -0.5, ptr(out), ptr(lse), stream_ptr(q.device))
         ctx.save_for_backward(q, bank, wkv, om, out, lse, kt, vt, ktt, mean, rstd, plan.uniq, plan.n_uniq,
                               plan.edge_u, plan.csr_off, plan.csr_edge)
-        ctx.cfg = (num_chapters, T, norm, eps, HK, plan.max_u, wk.dtype, wv.dtype, bank.dtype)
+        ctx.cfg = (num_chapters, T, norm, eps, HK, plan.max_u, wk.dtype, wv.dtype, bank_dtype)
         return out
 
     @staticmethod
@@ -373,10 +382,14 @@ class _RoutedAttention(torch.autograd.Function):
                 dwv = dwkv[KV:].to(wv_dtype) if need_wv else None
             if need_bank:
                 dX = torch.matmul(dkv_edge, wkv)  # rows of skipped edges are never read
-                dbank = torch.zeros(bank.shape, device=dev, dtype=bank_dtype)
-                call("moc_bank_scatter", L.dtype_code(dX.dtype), ptr(dX), ptr(bank), L.dtype_code(bank.dtype), d,
-                     T, ptr(uniq), ptr(n_uniq), max_u, ptr(csr_off), ptr(csr_edge), ptr(mean), ptr(rstd), norm,
-                     ptr(dbank), st)
+                if ctx.row_grad is not None:
+                    ctx.row_grad.accumulate(dX, bank, uniq, n_uniq, max_u, csr_off, csr_edge, mean, rstd, norm)
+                else:
+                    dbank = torch.zeros(bank.shape, device=dev, dtype=bank.dtype)
+                    call("moc_bank_scatter", L.dtype_code(dX.dtype), ptr(dX), ptr(bank), L.dtype_code(bank.dtype),
+                         d, T, ptr(uniq), ptr(n_uniq), max_u, ptr(csr_off), ptr(csr_edge), ptr(mean), ptr(rstd),
+                         norm, ptr(dbank), st)
+                    dbank = dbank.to(bank_dtype)   # the bank read may be a mirror of another dtype
             return dq, dbank, dwk, dwv, domega, None, None, None, None, None, None
         # fp32: sum per distinct chapter first, then library GEMMs
         dkv = torch.empty(max_u * T, 2 * KV, device=dev, dtype=dtype)
@@ -391,9 +404,13 @@ class _RoutedAttention(torch.autograd.Function):
             dwv = dwkv[KV:].to(wv_dtype) if need_wv else None
         if need_bank:
             dX = torch.matmul(dkv, wkv)
-            dbank = torch.zeros(bank.shape, device=dev, dtype=bank_dtype)
-            call("moc_bank_scatter", L.dtype_code(dX.dtype), ptr(dX), ptr(bank), L.dtype_code(bank.dtype), d, T,
-                 ptr(uniq), ptr(n_uniq), max_u, None, None, ptr(mean), ptr(rstd), norm, ptr(dbank), st)
+            if ctx.row_grad is not None:
+                ctx.row_grad.accumulate(dX, bank, uniq, n_uniq, max_u, None, None, mean, rstd, norm)
+            else:
+                dbank = torch.zeros(bank.shape, device=dev, dtype=bank.dtype)
+                call("moc_bank_scatter", L.dtype_code(dX.dtype), ptr(dX), ptr(bank), L.dtype_code(bank.dtype), d,
+                     T, ptr(uniq), ptr(n_uniq), max_u, None, None, ptr(mean), ptr(rstd), norm, ptr(dbank), st)
+                dbank = dbank.to(bank_dtype)
         return dq, dbank, dwk, dwv, domega, None, None, None, None, None, None
 
 

@@ -37,7 +37,7 @@ __all__ = [
     "naive_reference_weighted_joint_bias", "naive_reference_block_weighted",
     "sparse_attention_unweighted", "sparse_attention_weighted",
     "sparse_attention_joint_bias", "sparse_attention_block_weighted",
-    "decode_step", "moe_with_routing", "rms_norm",
+    "decode_step", "moe_with_routing", "rms_norm", "adamw_step", "clip_grad_norm",
 ]
 
 
@@ -639,3 +639,37 @@ def moe_with_routing(h, memory, chapter_indices, chapter_weights, T, Wq, Wk, Wv,
             acc = acc + out * chapter_weights[:, i].view(B, 1, 1)
         return acc
     return cross_attention(h, sel, Wq, Wk, Wv, Wo, H, HK)
+
+
+# --------------------------------------------------------------------------
+# bank optimizer (training/trainer.py:309-392 builds it, :876-889 steps it)
+# --------------------------------------------------------------------------
+# The reference steps every parameter, the bank (memory_bank.py:62) included, with
+# torch.optim.AdamW (a third-party routine: torch >= 2.0, requirements.txt:14; uv.lock pins
+# nothing) after accelerator.clip_grad_norm_, i.e. torch.nn.utils.clip_grad_norm_ with the
+# default norm_type 2.  Restated from the published AdamW algorithm (decoupled weight decay,
+# bias-corrected moments, amsgrad off) in the operation order of torch's implementation.
+
+def adamw_step(p: torch.Tensor, g: torch.Tensor, m: torch.Tensor, v: torch.Tensor, step: int,
+               lr: float, betas=(0.9, 0.999), eps: float = 1e-8, weight_decay: float = 1e-2) -> None:
+    """One AdamW step in place on (p, m, v); ``step`` is the 1-based step number after this
+    step's increment (torch's ``state['step']``)."""
+    b1, b2 = betas
+    p.mul_(1 - lr * weight_decay)
+    m.lerp_(g, 1 - b1)
+    v.mul_(b2).addcmul_(g, g, value=1 - b2)
+    bc1 = 1 - b1 ** step
+    bc2 = 1 - b2 ** step
+    denom = (v.sqrt() / math.sqrt(bc2)).add_(eps)
+    p.addcdiv_(m, denom, value=-lr / bc1)
+
+
+def clip_grad_norm(grads, max_norm: float) -> torch.Tensor:
+    """torch.nn.utils.clip_grad_norm_ (norm_type 2) on a list of gradients, in place: the
+    total norm is the 2-norm of the per-tensor 2-norms; every gradient is multiplied by
+    min(1, max_norm / (total + 1e-6)).  Returns the total norm."""
+    total = torch.linalg.vector_norm(torch.stack([torch.linalg.vector_norm(g, 2) for g in grads]), 2)
+    coef = torch.clamp(max_norm / (total + 1e-6), max=1.0)
+    for g in grads:
+        g.mul_(coef)
+    return total

@@ -364,3 +364,53 @@ def test_moe_with_routing_single_chapter_equals_cross_attention():
     out = O.moe_with_routing(h, bank, idx, torch.ones(2, 1), 4, Wq, Wk, Wv, Wo, 2, 2)
     mem, _ = O.gather_chapters(bank, idx, 4)
     assert torch.allclose(out, O.cross_attention(h, mem, Wq, Wk, Wv, Wo, 2, 2), atol=1e-12)
+
+
+@pytest.mark.parametrize("foreach", [False, True])
+def test_adamw_step_matches_torch_adamw(foreach):
+    """The oracle's AdamW against torch.optim.AdamW itself (the reference's optimizer, a library
+    routine) over several steps with a changing lr, weight decay and rows whose gradient is zero."""
+    g0 = _rng(11)
+    p = torch.randn(7, 5, generator=g0)
+    ref = p.clone().requires_grad_(True)
+    opt = torch.optim.AdamW([ref], lr=1e-2, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, foreach=foreach)
+    m = torch.zeros_like(p)
+    v = torch.zeros_like(p)
+    for step in range(1, 7):
+        lr = 1e-2 * (0.5 + 0.1 * step)
+        for grp in opt.param_groups:
+            grp["lr"] = lr
+        g = torch.randn(7, 5, generator=g0)
+        g[step % 7] = 0.0                       # a row without gradient this step
+        ref.grad = g.clone()
+        opt.step()
+        O.adamw_step(p, g, m, v, step, lr, (0.9, 0.95), 1e-8, 0.1)
+        st = opt.state[ref]
+        assert torch.allclose(p, ref.detach(), rtol=0, atol=1e-13)
+        assert torch.allclose(m, st["exp_avg"], rtol=0, atol=1e-13)
+        assert torch.allclose(v, st["exp_avg_sq"], rtol=0, atol=1e-13)
+
+
+def test_adamw_first_step_closed_form():
+    """Step 1: m/bc1 = g and sqrt(v/bc2) = |g|, so p1 = p0 (1 - lr wd) - lr g / (|g| + eps)."""
+    g0 = _rng(12)
+    p0 = torch.randn(20, generator=g0)
+    g = torch.randn(20, generator=g0)
+    p, m, v = p0.clone(), torch.zeros(20), torch.zeros(20)
+    lr, wd, eps = 3e-3, 0.1, 1e-8
+    O.adamw_step(p, g, m, v, 1, lr, (0.9, 0.95), eps, wd)
+    assert torch.allclose(p, p0 * (1 - lr * wd) - lr * g / (g.abs() + eps), rtol=0, atol=1e-14)
+
+
+@pytest.mark.parametrize("max_norm", [0.5, 1e3])
+def test_clip_grad_norm_matches_torch(max_norm):
+    g0 = _rng(13)
+    ps = [torch.randn(s, generator=g0).requires_grad_(True) for s in ((4, 3), (5,), (2, 2, 2))]
+    grads = [torch.randn(pp.shape, generator=g0) for pp in ps]
+    for pp, gg in zip(ps, grads):
+        pp.grad = gg.clone()
+    total_ref = torch.nn.utils.clip_grad_norm_(ps, max_norm)
+    total = O.clip_grad_norm(grads, max_norm)
+    assert torch.allclose(total, total_ref, rtol=1e-14)
+    for pp, gg in zip(ps, grads):
+        assert torch.allclose(gg, pp.grad, rtol=1e-14, atol=0)
