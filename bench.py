@@ -138,7 +138,8 @@ PROBE_BYTES = 256 << 20
 # entry point -> device kernel whose HBM traffic the counter passes measured
 TRAFFIC_KERNELS = {"moc_xattn_bwd_dkv": "xattn_bwd_dkv_kernel", "moc_xattn_fwd": "xattn_fwd_kernel",
                    "moc_xattn_bwd_dq": "xattn_bwd_dq_kernel", "moc_kv_project": "kv_project_wide_kernel",
-                   "moc_decode_partial": "sparse_fwd_unit_kernel", "moc_sparse_bwd": "sparse_bwd_unit_kernel"}
+                   "moc_decode_partial": "sparse_fwd_unit_kernel", "moc_sparse_bwd": "sparse_bwd_unit_kernel",
+                   "moc_bank_adamw": "bank_adamw_kernel"}
 
 
 def measured_traffic(workload, entry):
@@ -386,13 +387,116 @@ def run_c5(args):
     }
 
 
+# training-run optimizer settings of the reference (configs/base_small_run2.yaml:111, :159-163)
+BANK_OPT = dict(lr=6e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1)
+MAX_GRAD_NORM = 1.0
+
+
+def run_c3opt(args):
+    """The config-3 memory layer's training step with the bank's optimizer: router + layer
+    forward, backward, clip_grad_norm_ over the bank and the layer's parameters, AdamW on the
+    fp32 bank (training/trainer.py:876-889).  Four batches are cycled so the routed chapters
+    change between steps.  Variants:
+      reference_style - the kernels read the fp32 bank, dense fp32 bank gradient,
+                        torch.nn.utils.clip_grad_norm_ and foreach torch.optim.AdamW;
+      bank_adamw      - BankAdamW: row-sparse bank gradient, exact lazy catch-up, bf16 mirror
+                        read by the kernels (the value of this line);
+      bank_adamw_dense - BankAdamW without row sparsity (dense gradient, one fused pass).
+    Only the bank is stepped (the layer's own parameters are clipped but not updated), so
+    every variant runs the same routing."""
+    import torch
+    from memory_amd.bank_optim import BankAdamW, clip_grad_norm_
+
+    dev = torch.device("cuda", 0)
+    dtype = torch.bfloat16
+    cfg = dict(CFG)
+    layer, h, _, dout = build_inputs(dev, dtype, cfg)
+    B, L, C, T, d = cfg["B"], cfg["L"], cfg["C"], cfg["T"], cfg["d"]
+    torch.manual_seed(2)
+    bank0 = torch.randn(C * T, d, device=dev, dtype=torch.float32) * 0.02
+    hs = [torch.randn(B, L, d, device=dev, dtype=dtype).requires_grad_(True) for _ in range(4)]
+    with torch.no_grad():
+        plans = [set(torch.unique(layer.route(x, return_losses=False)[0]).tolist()) for x in hs]
+    elems = T * d
+    step_bytes = [len(plans[i]) * elems * 30 + len(plans[i] - plans[i - 1]) * elems * 26 for i in range(4)]
+
+    def make(kind):
+        bank = torch.nn.Parameter(bank0.clone())
+        if kind == "reference_style":
+            opt = torch.optim.AdamW([bank], foreach=True, **BANK_OPT)
+        else:
+            opt = BankAdamW(bank, T, mirror_dtype=torch.bfloat16, row_sparse=(kind == "bank_adamw"), **BANK_OPT)
+        params = [bank, *layer.parameters()]
+        it = [0]
+
+        def step():
+            x = hs[it[0] % len(hs)]
+            it[0] += 1
+            x.grad = None
+            for p in layer.parameters():
+                p.grad = None
+            out, _ = layer(x, bank, return_losses=False)
+            out.backward(dout)
+            if kind == "reference_style":
+                torch.nn.utils.clip_grad_norm_(params, MAX_GRAD_NORM)
+            else:
+                clip_grad_norm_(params, MAX_GRAD_NORM)
+            opt.step()
+            opt.zero_grad()
+        return step
+
+    res = {}
+    kinds = [k for k in ("reference_style", "bank_adamw_dense", "bank_adamw") if k in args.variants.split(",")]
+    if "bank_adamw" not in kinds:
+        raise SystemExit("--variants must include bank_adamw (the value of the c3opt line)")
+    for kind in kinds:
+        step = make(kind)
+        entry = "moc_bank_adamw" if kind == "bank_adamw" else None
+        ms, per, _, live = timed(step, args.steps, args.warmup, roofline_entry=entry)
+        res[kind] = {"ms_per_step": round(ms, 4),
+                     "kernels": {n: {"avg_ms": round(v["avg_ms"], 4), "calls": v["calls_per_step"]}
+                                 for n, v in sorted(per.items(), key=lambda kv: -kv[1]["ms_per_step"])[:8]}}
+        if kind == "bank_adamw":
+            res[kind]["live"] = live
+        torch.cuda.synchronize()
+        del step
+        torch.cuda.empty_cache()
+
+    ms = res["bank_adamw"]["ms_per_step"]
+    live = res["bank_adamw"].pop("live")
+    roofline = None
+    if live:
+        # both launches of a step (catch-up of the plan's stale chapters, then the step of the
+        # touched ones): algorithmic bytes per launch = the cycle's mean bytes per step / 2
+        per_launch = sum(step_bytes) / len(step_bytes) / live["calls_per_step"]
+        ach = per_launch / (live["avg_ms"] * 1e-3) / 1e9
+        roofline = {"kernel": "moc_bank_adamw", "bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS,
+                    "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4),
+                    "traffic": measured_traffic("c3opt", "moc_bank_adamw"),
+                    "avg_ms": round(live["avg_ms"], 4), "algorithmic_bytes": int(per_launch)}
+    return {
+        "metric": "memory-layer training step tokens/s incl. clip + bank AdamW (L=1024,d=768,k=64,T=64)",
+        "value": round(B * L / (ms * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic (four seeded batches cycled; N(0,0.02) fp32 bank)",
+        "config": {"workload": "c3opt: config-3 memory layer fwd+bwd + clip_grad_norm_ + AdamW on the fp32 bank",
+                   **{k: cfg[k] for k in ("B", "L", "d", "H", "C", "T", "S", "k")}, **BANK_OPT,
+                   "max_grad_norm": MAX_GRAD_NORM,
+                   "chapters_per_step": [len(p) for p in plans]},
+        "variants": res,
+        "roofline": roofline,
+    }
+
+
 def main():
     ap = argparse.ArgumentParser()
-    ap.add_argument("--workload", choices=["c3", "c4", "c5"], default="c3")
+    ap.add_argument("--workload", choices=["c3", "c4", "c5", "c3opt"], default="c3")
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--variants", default="reference_style,bank_adamw_dense,bank_adamw",
+                    help="c3opt: which optimizer variants to run (comma-separated)")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
     ap.add_argument("--traffic-probe", action="store_true",
                     help="run one plain 256 MiB device copy before the warmup: the reference kernel "
@@ -412,8 +516,8 @@ def main():
         del src, dst
 
     if args.workload != "c3":
-        line = run_c4(args) if args.workload == "c4" else run_c5(args)
-        print(json.dumps(line), flush=True)
+        run = {"c4": run_c4, "c5": run_c5, "c3opt": run_c3opt}[args.workload]
+        print(json.dumps(run(args)), flush=True)
         return
 
     import torch
