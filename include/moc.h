@@ -237,6 +237,24 @@ int moc_bank_grad_accumulate(int dx_dtype, const void* dX, const void* bank, int
                              const int32_t* csr_edge, const float* row_mean, const float* row_rstd, int norm,
                              int epoch, int32_t* chap_epoch, int32_t* fresh, float* grad_acc, hipStream_t stream);
 
+/* ------------------------------------------------------- caller-side norm */
+
+/* The memory sublayer's `memory_layernorm` (memory_transformer/memory_block.py:549-558):
+ * norm MOC_NORM_RMS = RMSNorm (memory_block.py:18-28, y = x / sqrt(mean(x^2) + eps) * w) or
+ * MOC_NORM_LAYERNORM (nn.LayerNorm, y = (x - mu) / sqrt(var + eps) * w + b) over rows x [R][d]
+ * (d % 8 == 0, d <= 2048; x f32 or bf16, y f32 or bf16, not bf16 -> f32).  weight / bias f32 [d]
+ * (bias may be NULL).  Writes rstd f32 [R] and, for LayerNorm, mean f32 [R] for the backward. */
+int moc_row_norm_fwd(int norm, int x_dtype, const void* x, int64_t R, int64_t d, const float* weight,
+                     const float* bias, float eps, int y_dtype, void* y, float* mean, float* rstd,
+                     hipStream_t stream);
+/* dx [R][d] and dweight_dbias f32 [2][d] = {sum_rows dy xh, sum_rows dy} (fixed order) from x,
+ * the saved mean / rstd and dy.  dtypes (x, dy, dx): (f32, f32, f32), (f32, bf16, f32) or
+ * (bf16, bf16, bf16). */
+size_t moc_row_norm_bwd_workspace(int64_t R, int64_t d);
+int moc_row_norm_bwd(int norm, int x_dtype, const void* x, int64_t R, int64_t d, const float* weight,
+                     const float* mean, const float* rstd, int dy_dtype, const void* dy, int dx_dtype, void* dx,
+                     float* dweight_dbias, void* workspace, size_t workspace_bytes, hipStream_t stream);
+
 /* ------------------------------------------------------------ bank optimizer */
 
 /* torch.optim.AdamW as the reference steps the bank (training/trainer.py:309-392, param group

@@ -304,4 +304,8 @@ int sparse_fwd_launch(int dtype, const void* q, int HQ, const void* k, const voi
                       float scale, const float* omega, float* o_part, float* lse_part, hipStream_t stream,
                       const char* who);
 
+// out[i] = inv * sum_j part[j * n + i] for i < n, j < nsplit, summed in a fixed order
+// (router.hip's split-row reduction); returns a MOC_ status.
+int launch_split_reduce(const float* part, int nsplit, int64_t n, float inv, float* out, hipStream_t stream);
+
 }  // namespace moc

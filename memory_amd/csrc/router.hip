@@ -805,6 +805,13 @@ __global__ __launch_bounds__(kLossThreads) void router_loss_bwd_block_kernel(
   }
 }
 
+int launch_split_reduce(const float* part, int nsplit, int64_t n, float inv, float* out, hipStream_t stream) {
+  if (n <= 0) return MOC_OK;
+  hipLaunchKernelGGL(pool_reduce_kernel, dim3((unsigned)((n + 63) / 64)), dim3(256), 0, stream, part, nsplit,
+                     (int64_t)1, n, inv, out);
+  return check_launch("pool_reduce_kernel");
+}
+
 }  // namespace moc
 
 using namespace moc;

@@ -133,20 +133,26 @@ class MemoryCrossAttention(nn.Module):
                 routed_memory_state: Optional[Dict[str, Any]] = None) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
         if return_attn_weights:
             raise NotImplementedError("return_attn_weights is not supported by the fused HIP attention")
+        return self._project_output(self.attention_preproj(hidden_states, memory, token_routing_state,
+                                                           token_routing_kernel_version, routed_memory_state)), None
+
+    def attention_preproj(self, hidden_states: torch.Tensor, memory: Optional[torch.Tensor] = None,
+                          token_routing_state: Optional[Dict[str, Any]] = None,
+                          token_routing_kernel_version: str = "v2",
+                          routed_memory_state: Optional[Dict[str, Any]] = None) -> torch.Tensor:
+        """forward's attention output before o_proj, (B, L, hidden_dim)."""
         if token_routing_state is not None:
-            preproj = self._forward_token_routed_attention(hidden_states, token_routing_state,
-                                                           token_routing_kernel_version)
-            return self._project_output(preproj), None
+            return self._forward_token_routed_attention(hidden_states, token_routing_state,
+                                                        token_routing_kernel_version)
         if routed_memory_state is not None:
             st = routed_memory_state
             norm_type = st.get("norm_type") if st.get("normalize", False) else None
-            attn = self._routed(hidden_states, st["bank"], st["chapter_indices"], st["chapter_weights"],
+            return self._routed(hidden_states, st["bank"], st["chapter_indices"], st["chapter_weights"],
                                 int(st["num_chapters"]), int(st["tokens_per_chapter"]), norm_type,
                                 float(st.get("eps", 1e-6)))
-            return self._project_output(attn), None
         if memory is None:
             raise ValueError("memory must be provided when token_routing_state is None.")
-        return self._project_output(self._dense_as_chapters(hidden_states, memory)), None
+        return self._dense_as_chapters(hidden_states, memory)
 
     def _forward_token_routed_attention(self, hidden_states: torch.Tensor, token_routing_state: Dict[str, Any],
                                         token_routing_kernel_version: str = "v2") -> torch.Tensor:

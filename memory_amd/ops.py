@@ -277,6 +277,109 @@ def linear(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
     return _Linear.apply(x, w)
 
 
+class _LinearResidual(torch.autograd.Function):
+    """out = residual + x W^T: the memory sublayer's o_proj and its residual add
+    (memory_block.py:549-558, ``hidden_states = residual + mem_output``) as one GEMM with the
+    residual as the accumulator input (beta = 1) when both have the output dtype."""
+
+    @staticmethod
+    def forward(ctx, x, w, residual):
+        ctx.save_for_backward(x, w)
+        ctx.res_dtype = residual.dtype
+        n_out = w.shape[0]
+        x2 = x.reshape(-1, x.shape[-1])
+        r2 = residual.reshape(-1, n_out)
+        if residual.dtype == x.dtype == w.dtype:
+            out = torch.addmm(r2, x2, w.t())
+        else:
+            out = r2 + F.linear(x2, w)
+        return out.view(residual.shape)
+
+    @staticmethod
+    def backward(ctx, dy):
+        x, w = ctx.saved_tensors
+        dx = dw = dres = None
+        n_out, n_in = w.shape
+        dy2 = dy.reshape(-1, n_out)
+        if ctx.needs_input_grad[2]:
+            dres = dy
+        g = dy2.to(x.dtype).contiguous()
+        if ctx.needs_input_grad[0]:
+            dx = torch.matmul(g, w.to(x.dtype)).view(x.shape)
+        if ctx.needs_input_grad[1]:
+            dw = linear_wgrad(g, x.reshape(-1, n_in).contiguous(), w.dtype)
+        return dx, dw, dres
+
+
+def linear_residual(x: torch.Tensor, w: torch.Tensor, residual: torch.Tensor) -> torch.Tensor:
+    return _LinearResidual.apply(x, w, residual)
+
+
+class _RowNorm(torch.autograd.Function):
+    """The memory sublayer's ``memory_layernorm`` (RMSNorm of memory_block.py:18-28, or
+    nn.LayerNorm) on the HIP row kernels: y in ``out_dtype``; gradients for x, weight, bias."""
+
+    @staticmethod
+    def forward(ctx, x, weight, bias, norm, eps, out_dtype):
+        L.require_gpu(x, weight)
+        shape = x.shape
+        d = shape[-1]
+        x2 = x.reshape(-1, d)
+        if x2.dtype not in (torch.float32, torch.bfloat16):
+            x2 = x2.float()
+        x2 = x2.contiguous()
+        R = x2.shape[0]
+        if out_dtype == torch.float32 and x2.dtype == torch.bfloat16:
+            x2 = x2.float()
+        w = weight.float().contiguous()
+        b = bias.float().contiguous() if bias is not None else None
+        dev = x2.device
+        y = torch.empty(R, d, device=dev, dtype=out_dtype)
+        rstd = torch.empty(R, device=dev, dtype=torch.float32)
+        mean = torch.empty(R, device=dev, dtype=torch.float32) if norm == L.MOC_NORM_LAYERNORM else None
+        call("moc_row_norm_fwd", norm, L.dtype_code(x2.dtype), ptr(x2), R, d, ptr(w), ptr(b), float(eps),
+             L.dtype_code(out_dtype), ptr(y), ptr(mean), ptr(rstd), stream_ptr(dev))
+        ctx.save_for_backward(x2, w, mean, rstd)
+        ctx.cfg = (norm, shape, x.dtype, weight.dtype, None if bias is None else bias.dtype)
+        return y.view(*shape[:-1], d)
+
+    @staticmethod
+    def backward(ctx, dy):
+        x2, w, mean, rstd = ctx.saved_tensors
+        norm, shape, x_dtype, w_dtype, b_dtype = ctx.cfg
+        R, d = x2.shape
+        dev = x2.device
+        dy2 = dy.reshape(R, d)
+        if x2.dtype == torch.bfloat16:
+            dy2 = dy2.to(torch.bfloat16)
+        elif dy2.dtype not in (torch.float32, torch.bfloat16):
+            dy2 = dy2.float()
+        dy2 = dy2.contiguous()
+        dx = torch.empty(R, d, device=dev, dtype=x2.dtype)
+        dwb = torch.empty(2, d, device=dev, dtype=torch.float32)
+        ws_bytes = L.query("moc_row_norm_bwd_workspace", R, d)
+        ws = torch.empty(max(1, ws_bytes // 4), device=dev, dtype=torch.float32)
+        call("moc_row_norm_bwd", norm, L.dtype_code(x2.dtype), ptr(x2), R, d, ptr(w), ptr(mean), ptr(rstd),
+             L.dtype_code(dy2.dtype), ptr(dy2), L.dtype_code(dx.dtype), ptr(dx), ptr(dwb), ptr(ws), ws_bytes,
+             stream_ptr(dev))
+        dw = dwb[0].to(w_dtype) if ctx.needs_input_grad[1] else None
+        db = dwb[1].to(b_dtype) if (b_dtype is not None and ctx.needs_input_grad[2]) else None
+        return dx.view(shape).to(x_dtype), dw, db, None, None, None
+
+
+def row_norm(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor], eps: float, norm: str = "rms",
+             out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+    """RMSNorm (``norm="rms"``) or LayerNorm (``"layer"``) over the last dim, output in
+    ``out_dtype`` (default: x's dtype)."""
+    code = {"rms": L.MOC_NORM_RMS, "layer": L.MOC_NORM_LAYERNORM}.get(norm)
+    if code is None:
+        raise ValueError(f"norm must be 'rms' or 'layer', got {norm!r}")
+    od = x.dtype if out_dtype is None else out_dtype
+    if od not in (torch.float32, torch.bfloat16):
+        raise ValueError(f"row_norm outputs float32 or bfloat16, got {od}")
+    return _RowNorm.apply(x, weight, bias, code, float(eps), od)
+
+
 def linear_wgrad(dy: torch.Tensor, x: torch.Tensor, out_dtype: torch.dtype) -> torch.Tensor:
     """dW = dy^T x for dy [R][N], x [R][K] (row-major, contiguous): the split-row MFMA
     kernel for bf16 dy (N, K multiples of 8), a plain GEMM otherwise."""

@@ -38,6 +38,7 @@ __all__ = [
     "sparse_attention_unweighted", "sparse_attention_weighted",
     "sparse_attention_joint_bias", "sparse_attention_block_weighted",
     "decode_step", "moe_with_routing", "rms_norm", "adamw_step", "clip_grad_norm",
+    "block_rms_norm", "memory_sublayer",
 ]
 
 
@@ -673,3 +674,24 @@ def clip_grad_norm(grads, max_norm: float) -> torch.Tensor:
     for g in grads:
         g.mul_(coef)
     return total
+
+
+# --------------------------------------------------------------------------
+# caller side: the memory sublayer of MemoryTransformerBlock
+# --------------------------------------------------------------------------
+
+def block_rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    """RMSNorm.forward (memory_block.py:26-28): x / sqrt(mean(x^2) + eps) * weight."""
+    rms = torch.sqrt(x.pow(2).mean(-1, keepdim=True) + eps)
+    return x / rms * weight
+
+
+def memory_sublayer(h, norm_weight, norm_bias, eps, use_rms_norm, memory, Wq, Wk, Wv, Wo, H, HK):
+    """The memory lines of MemoryTransformerBlock.forward (memory_block.py:549-558):
+    residual + memory_attn(memory_layernorm(h)); memory (B, N, d) is the already gathered,
+    weighted memory (model.py:677-692).  LayerNorm is nn.LayerNorm (F.layer_norm)."""
+    if use_rms_norm:
+        x = block_rms_norm(h, norm_weight, eps)
+    else:
+        x = F.layer_norm(h, (h.shape[-1],), norm_weight, norm_bias, eps)
+    return h + cross_attention(x, memory, Wq, Wk, Wv, Wo, H, HK)

@@ -414,3 +414,31 @@ def test_clip_grad_norm_matches_torch(max_norm):
     assert torch.allclose(total, total_ref, rtol=1e-14)
     for pp, gg in zip(ps, grads):
         assert torch.allclose(gg, pp.grad, rtol=1e-14, atol=0)
+
+
+def test_block_rms_norm_matches_torch_rms_norm():
+    """The reference's RMSNorm module restated, against torch's own rms_norm (a library
+    routine with the same definition) and a closed form: a constant row c gives sign(c) * w."""
+    g0 = _rng(21)
+    x = torch.randn(5, 7, 24, generator=g0)
+    w = torch.randn(24, generator=g0)
+    ref = F.rms_norm(x, (24,), w, 1e-6)
+    assert torch.allclose(O.block_rms_norm(x, w, 1e-6), ref, rtol=1e-12, atol=1e-12)
+    c = torch.full((3, 24), -2.5)
+    assert torch.allclose(O.block_rms_norm(c, w, 0.0), -w.expand(3, 24), rtol=1e-14)
+
+
+def test_memory_sublayer_is_residual_plus_cross_attention():
+    """With a zero output projection the sublayer is the identity (the wo_init_zero start of
+    memory_attention.py:140-143), and with LayerNorm of unit weight / zero bias it equals the
+    residual plus attention over standardised rows."""
+    g0 = _rng(22)
+    B, L, N, d, H = 2, 5, 8, 16, 2
+    h = torch.randn(B, L, d, generator=g0)
+    mem = torch.randn(B, N, d, generator=g0)
+    Wq, Wk, Wv, Wo = (torch.randn(d, d, generator=g0) * 0.2 for _ in range(4))
+    out = O.memory_sublayer(h, torch.ones(d), None, 1e-6, True, mem, Wq, Wk, Wv, torch.zeros(d, d), H, H)
+    assert torch.equal(out, h)
+    out = O.memory_sublayer(h, torch.ones(d), torch.zeros(d), 1e-5, False, mem, Wq, Wk, Wv, Wo, H, H)
+    xs = (h - h.mean(-1, keepdim=True)) / torch.sqrt(h.var(-1, unbiased=False, keepdim=True) + 1e-5)
+    assert torch.allclose(out, h + O.cross_attention(xs, mem, Wq, Wk, Wv, Wo, H, H), rtol=1e-12, atol=1e-12)
