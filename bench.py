@@ -488,9 +488,75 @@ def run_c3opt(args):
     }
 
 
+def run_c3block(args):
+    """The memory sublayer of a transformer block at config 3 (memory_block.py:549-558):
+    routing on the block input, memory_layernorm (RMSNorm, eps 1e-5 as configs/base_small_run2.yaml:40),
+    memory cross-attention over the routed chapters, o_proj and the residual add; forward +
+    backward.  Variants:
+      reference_style - the reference's RMSNorm module as torch ops (memory_block.py:26-28), then
+                        o_proj and a separate residual add;
+      fused           - MemorySublayer: the norm as one HIP row kernel writing bf16, the residual as
+                        the o_proj GEMM's accumulator input (the value of this line)."""
+    import torch
+    from memory_amd import ops
+    from memory_amd.memory_block import MemorySublayer
+
+    dev = torch.device("cuda", 0)
+    dtype = torch.bfloat16
+    cfg = dict(CFG)
+    layer, h, bank, dout = build_inputs(dev, dtype, cfg)
+    B, L, d, C, T = cfg["B"], cfg["L"], cfg["d"], cfg["C"], cfg["T"]
+    sub = MemorySublayer(d, cfg["H"], cfg["HK"], use_rms_norm=True, norm_eps=1e-5, wo_init_zero=False).to(dev)
+    sub.memory_attn = layer.memory_attn            # the bf16 projections of the c3 layer
+    norm_w = sub.memory_layernorm.weight
+
+    def state(x):
+        idx_star, omega, _ = layer.route(x, return_losses=False)
+        return {"bank": bank, "chapter_indices": idx_star, "chapter_weights": omega, "num_chapters": C,
+                "tokens_per_chapter": T}
+
+    def ref_rms(x):
+        rms = torch.sqrt(x.pow(2).mean(-1, keepdim=True) + 1e-5)
+        return x / rms * norm_w
+
+    def step_ref():
+        h.grad = bank.grad = norm_w.grad = None
+        for p in layer.parameters():
+            p.grad = None
+        x = ref_rms(h).to(dtype)
+        pre = layer.memory_attn.attention_preproj(x, routed_memory_state=state(h))
+        out = h + ops.linear(pre, layer.memory_attn.o_proj.weight)
+        out.backward(dout)
+
+    def step_fused():
+        h.grad = bank.grad = norm_w.grad = None
+        for p in layer.parameters():
+            p.grad = None
+        out = sub(h, routed_memory_state=state(h))
+        out.backward(dout)
+
+    res = {}
+    for kind, fn in (("reference_style", step_ref), ("fused", step_fused)):
+        ms, per, _, _ = timed(fn, args.steps, args.warmup)
+        res[kind] = {"ms_per_step": round(ms, 4),
+                     "kernels": {n: {"avg_ms": round(v["avg_ms"], 4), "calls": v["calls_per_step"]}
+                                 for n, v in sorted(per.items(), key=lambda kv: -kv[1]["ms_per_step"])
+                                 if n in ("moc_row_norm_fwd", "moc_row_norm_bwd")}}
+    ms = res["fused"]["ms_per_step"]
+    return {
+        "metric": "memory sublayer fwd+bwd tokens/s incl. memory_layernorm + residual (L=1024,d=768,k=64,T=64)",
+        "value": round(B * L / (ms * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic (seeded N(0,1) hidden states, random-init)",
+        "config": {"workload": "c3block: memory_layernorm + routed memory cross-attention + residual, fwd+bwd",
+                   **{k: cfg[k] for k in ("B", "L", "d", "H", "C", "T", "S", "k")}, "norm": "rms", "norm_eps": 1e-5},
+        "variants": res,
+    }
+
+
 def main():
     ap = argparse.ArgumentParser()
-    ap.add_argument("--workload", choices=["c3", "c4", "c5", "c3opt"], default="c3")
+    ap.add_argument("--workload", choices=["c3", "c4", "c5", "c3opt", "c3block"], default="c3")
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
@@ -516,7 +582,7 @@ def main():
         del src, dst
 
     if args.workload != "c3":
-        run = {"c4": run_c4, "c5": run_c5, "c3opt": run_c3opt}[args.workload]
+        run = {"c4": run_c4, "c5": run_c5, "c3opt": run_c3opt, "c3block": run_c3block}[args.workload]
         print(json.dumps(run(args)), flush=True)
         return
 
