@@ -44,6 +44,49 @@ class MemoryDecodeCache:
     def nbytes(self) -> int:
         return self.k_tiles.numel() * self.k_tiles.element_size() * 2
 
+    # File format of a saved cache (safetensors): tensors ``k_tiles`` and ``v_tiles``, each
+    # [num_chapters][num_kv_heads][tokens_per_chapter keys][64 dims] in the cache dtype (the
+    # projected, optionally row-normalised bank, K = norm(M) Wk^T and V = norm(M) Wv^T per
+    # chapter), and string metadata: format, num_chapters, tokens_per_chapter, num_kv_heads,
+    # dtype.  The K/V of one memory layer; omega is applied at attention time.
+    FORMAT = "moc-decode-kv/1"
+
+    def save(self, path: str) -> None:
+        from safetensors.torch import save_file
+        meta = {"format": self.FORMAT, "num_chapters": str(self.num_chapters), "tokens_per_chapter": str(self.T),
+                "num_kv_heads": str(self.HK), "dtype": str(self.dtype).replace("torch.", "")}
+        save_file({"k_tiles": self.k_tiles.contiguous().cpu(), "v_tiles": self.v_tiles.contiguous().cpu()}, path,
+                  metadata=meta)
+
+    @classmethod
+    def load(cls, path: str, device: torch.device) -> "MemoryDecodeCache":
+        from safetensors import safe_open
+        with safe_open(path, framework="pt", device="cpu") as f:
+            meta = f.metadata() or {}
+            if meta.get("format") != cls.FORMAT:
+                raise ValueError(f"{path}: not a {cls.FORMAT} decode cache (format {meta.get('format')!r})")
+            k, v = f.get_tensor("k_tiles"), f.get_tensor("v_tiles")
+        C, T, HK = int(meta["num_chapters"]), int(meta["tokens_per_chapter"]), int(meta["num_kv_heads"])
+        if tuple(k.shape) != (C, HK, T, 64) or k.shape != v.shape:
+            raise ValueError(f"{path}: tile shape {tuple(k.shape)} does not match the metadata")
+        return cls.from_tiles(k.to(device), v.to(device), num_chapters=C, tokens_per_chapter=T, num_kv_heads=HK)
+
+    @classmethod
+    def from_tiles(cls, k_tiles: torch.Tensor, v_tiles: torch.Tensor, *, num_chapters: int, tokens_per_chapter: int,
+                   num_kv_heads: int) -> "MemoryDecodeCache":
+        """A cache over already projected tiles [num_chapters][num_kv_heads][T][64]."""
+        L.require_gpu(k_tiles, v_tiles)
+        if k_tiles.dtype not in (torch.float32, torch.bfloat16) or v_tiles.dtype != k_tiles.dtype:
+            raise ValueError("decode cache tiles must be float32 or bfloat16, both of one dtype")
+        if k_tiles.shape != (num_chapters, num_kv_heads, tokens_per_chapter, 64) or v_tiles.shape != k_tiles.shape:
+            raise ValueError(f"tiles of shape {tuple(k_tiles.shape)}, expected "
+                             f"{(num_chapters, num_kv_heads, tokens_per_chapter, 64)}")
+        self = cls.__new__(cls)
+        self.num_chapters, self.T, self.HK, self.dtype = int(num_chapters), int(tokens_per_chapter), \
+            int(num_kv_heads), k_tiles.dtype
+        self.k_tiles, self.v_tiles = k_tiles.contiguous(), v_tiles.contiguous()
+        return self
+
 
 class DecodeRouting:
     """Fixed (chapter ids incl. the shared prefix, omega) of a batch of sequences and their plan."""
