@@ -327,7 +327,7 @@ C5 = dict(B=64, d=768, H=12, HK=12, C=4097, T=64, S=1, k=64, scale=2.5, layers=4
 
 def run_c5(args):
     import torch
-    from memory_amd.decode import DecodeRouting, MemoryDecodeCache, decode_attention
+    from memory_amd.decode import DecodeRouting, DecodeStepGraph, MemoryDecodeCache, memory_decode_step
     from memory_amd.model import RoutedMemoryLayer
     cfg = dict(C5)
     dev = torch.device("cuda", 0)
@@ -357,13 +357,22 @@ def run_c5(args):
     per_seq_bytes = cfg["layers"] * B * (cfg["S"] + cfg["k"]) * tile_bytes
 
     def step():
-        with torch.no_grad():
-            for lay, cache, routing in layers:
-                q = lay.memory_attn.q_proj(h_t.reshape(B, d)).view(B, H, 64)
-                a = decode_attention(q, cache, routing)
-                lay.memory_attn.o_proj(a.reshape(B, 1, d))
+        for lay, cache, routing in layers:
+            memory_decode_step(lay.memory_attn, h_t, cache, routing)
 
     ms, per, _, dec = timed(step, args.steps, args.warmup, "moc_decode_partial")
+    # the same step replayed from one captured HIP graph (the serving path for a fixed batch)
+    graph = DecodeStepGraph([(lay.memory_attn, cache, routing) for lay, cache, routing in layers],
+                            [h_t] * len(layers))
+    for _ in range(args.warmup):
+        graph.run([h_t] * len(layers))
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        graph.run([h_t] * len(layers))
+    torch.cuda.synchronize()
+    graph_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    del graph
     roofline = None
     if dec:
         ach = (unique_bytes / cfg["layers"]) / (dec["avg_ms"] * 1e-3) / 1e9
@@ -384,6 +393,9 @@ def run_c5(args):
         "per_sequence_gbs": round(per_seq_bytes / (ms * 1e-3) / 1e9, 1),
         "tokens_per_s": round(B / (ms * 1e-3), 1),
         "roofline": roofline, "kernels": kernels,
+        "graph_replay": {"ms_per_step": round(graph_ms, 4),
+                         "gbs": round(unique_bytes / (graph_ms * 1e-3) / 1e9, 1),
+                         "tokens_per_s": round(B / (graph_ms * 1e-3), 1)},
     }
 
 

@@ -237,6 +237,14 @@ int moc_bank_grad_accumulate(int dx_dtype, const void* dX, const void* bank, int
                              const int32_t* csr_edge, const float* row_mean, const float* row_rstd, int norm,
                              int epoch, int32_t* chap_epoch, int32_t* fresh, float* grad_acc, hipStream_t stream);
 
+/* ------------------------------------------------------------ few-row linear */
+
+/* y [M][N] = x [M][K] W[N][K]^T for M <= 256 rows (bf16 x and W, fp32 accumulation, y bf16 or
+ * f32): the decode step's q_proj / o_proj (memory_attention.py:140-143, :241, :456) on one
+ * token per sequence.  K % 128 == 0, N % 16 == 0, 16-byte aligned x and W. */
+int moc_linear_rows(const void* x, int64_t M, int64_t K, const void* W, int64_t N, int out_dtype, void* y,
+                    hipStream_t stream);
+
 /* ------------------------------------------------------- caller-side norm */
 
 /* The memory sublayer's `memory_layernorm` (memory_transformer/memory_block.py:549-558):

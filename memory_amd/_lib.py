@@ -73,6 +73,7 @@ _SIGS = {
     "moc_bank_grad_accumulate": (_I, [_I, _P, _P, _I, _I64, _I, _P, _P, _I64, _P, _P, _P, _P, _I, _I, _P, _P, _P,
                                       _P]),
     "moc_bank_chunk_count": (_I, [_I64]),
+    "moc_linear_rows": (_I, [_P, _I64, _I64, _P, _I64, _I, _P, _P]),
     "moc_row_norm_fwd": (_I, [_I, _I, _P, _I64, _I64, _P, _P, _F, _I, _P, _P, _P, _P]),
     "moc_row_norm_bwd_workspace": (_SZ, [_I64, _I64]),
     "moc_row_norm_bwd": (_I, [_I, _I, _P, _I64, _I64, _P, _P, _P, _I, _P, _I, _P, _P, _P, _SZ, _P]),

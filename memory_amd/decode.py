@@ -136,6 +136,44 @@ def memory_decode_step(memory_attn, hidden: torch.Tensor, cache: MemoryDecodeCac
     B = hidden.shape[0]
     H = memory_attn.num_heads
     with torch.no_grad():
-        q = memory_attn.q_proj(hidden.reshape(B, -1)).view(B, H, memory_attn.head_dim)
+        wq, wo = memory_attn.q_proj.weight, memory_attn.o_proj.weight
+        q = ops.linear(hidden.reshape(B, -1).to(wq.dtype), wq).view(B, H, memory_attn.head_dim)
         a = decode_attention(q, cache, routing)
-        return memory_attn.o_proj(a.reshape(B, 1, -1).to(memory_attn.o_proj.weight.dtype))
+        return ops.linear(a.reshape(B, 1, -1).to(wo.dtype), wo)
+
+
+class DecodeStepGraph:
+    """The per-token decode of several memory sublayers captured once as a HIP graph
+    (torch.cuda.CUDAGraph) and replayed for every generated token: one graph launch replaces
+    the ~4 kernel launches per layer, and their inter-launch gaps.
+
+    ``layers`` is a list of (memory_attn, cache, routing); ``inputs`` the per-layer hidden
+    states (B, 1, d) used for the capture (their shapes and dtypes are fixed).  ``run(inputs)``
+    copies new hidden states into the captured input buffers, replays, and returns the
+    per-layer outputs (buffers owned by the graph, overwritten by the next replay).  The
+    routing and the caches must stay alive and unchanged while the graph is used."""
+
+    def __init__(self, layers, inputs, warmup: int = 2):
+        if len(layers) != len(inputs):
+            raise ValueError("one input per layer")
+        self.layers = list(layers)
+        self.static_in = [x.detach().clone() for x in inputs]
+        stream = torch.cuda.Stream(device=self.static_in[0].device)
+        stream.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(stream):
+            for _ in range(warmup):
+                self._body()
+        torch.cuda.current_stream().wait_stream(stream)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self.static_out = self._body()
+
+    def _body(self):
+        return [memory_decode_step(attn, x, cache, routing)
+                for (attn, cache, routing), x in zip(self.layers, self.static_in)]
+
+    def run(self, inputs):
+        for buf, x in zip(self.static_in, inputs):
+            buf.copy_(x)
+        self.graph.replay()
+        return self.static_out

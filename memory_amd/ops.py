@@ -257,7 +257,7 @@ class _Linear(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, w):
         ctx.save_for_backward(x, w)
-        return F.linear(x, w)
+        return linear_rows(x, w) if _few_rows(x, w) else F.linear(x, w)
 
     @staticmethod
     def backward(ctx, dy):
@@ -275,6 +275,23 @@ class _Linear(torch.autograd.Function):
 
 def linear(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
     return _Linear.apply(x, w)
+
+
+def _few_rows(x: torch.Tensor, w: torch.Tensor) -> bool:
+    K = x.shape[-1]
+    return (x.is_cuda and x.dtype == torch.bfloat16 and w.dtype == torch.bfloat16 and x.numel() // max(K, 1) <= 256
+            and K % 128 == 0 and w.shape[0] % 16 == 0)
+
+
+def linear_rows(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """x W^T for at most 256 rows on the few-row kernel (bf16, fp32 accumulation)."""
+    K = x.shape[-1]
+    N = w.shape[0]
+    x2 = x.reshape(-1, K).contiguous()
+    wc = w.contiguous()
+    y = torch.empty(x2.shape[0], N, device=x.device, dtype=x.dtype)
+    call("moc_linear_rows", ptr(x2), x2.shape[0], K, ptr(wc), N, L.dtype_code(y.dtype), ptr(y), stream_ptr(x.device))
+    return y.view(*x.shape[:-1], N)
 
 
 class _LinearResidual(torch.autograd.Function):

@@ -47,3 +47,35 @@ def test_decode_step_matches_oracle(gpu_device, dtype, B, H, HK, C, k, norm):
     ref = O.decode_step(rd(h), rd(bank), ci, cw.double(), rd(Wq), rd(Wk), rd(Wv), rd(Wo), H=H, HK=HK, T=T,
                         normalize=norm is not None, norm_type=norm or "rms", eps=1e-5, S=S)
     assert_rel(out, ref, 1e-4 if dtype == torch.float32 else 2e-2, "decode output")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_decode_step_graph_replays_match_eager(gpu_device, dtype):
+    """Two memory layers' decode captured as one HIP graph: every replay (with new inputs,
+    eager work and synchronisations between replays) equals the eager decode step bit for bit."""
+    print(f"decode graph replays dtype={dtype}", flush=True)
+    from memory_amd.decode import DecodeRouting, DecodeStepGraph, MemoryDecodeCache, memory_decode_step
+    from memory_amd.memory_attention import MemoryCrossAttention
+    dev = gpu_device
+    g = gen(321)
+    B, H, HK, C, k, d, T = 8, 2, 2, 17, 5, 128, 64
+    layers = []
+    for _ in range(2):
+        attn = MemoryCrossAttention(d, H, HK, wo_init_zero=False).to(dev, dtype)
+        bank = torch.randn(C * T, d, generator=g).to(dev, dtype)
+        cache = MemoryDecodeCache(bank, attn.k_proj.weight, attn.v_proj.weight, num_chapters=C, tokens_per_chapter=T,
+                                  num_kv_heads=HK, dtype=dtype)
+        idx, w, _ = O.route_sequence(torch.randn(B, C, generator=g), k, 1)
+        ci, cw = O.prepend_shared_chapters(idx, w, num_chapters=C, num_shared_chapters=1, routed_scaling_factor=2.5)
+        layers.append((attn, cache, DecodeRouting(ci.to(dev), cw.to(dev), C)))
+    xs = [torch.randn(B, 1, d, generator=g).to(dev, dtype) for _ in range(2)]
+    graph = DecodeStepGraph(layers, xs)
+    for rep in range(4):
+        inputs = [torch.randn(B, 1, d, generator=g).to(dev, dtype) for _ in range(2)]
+        outs = [o.clone() for o in graph.run(inputs)]
+        junk = torch.randn(1000, device=dev).sum()          # eager work between replays
+        torch.cuda.synchronize()
+        ref = [memory_decode_step(a, x, c, r) for (a, c, r), x in zip(layers, inputs)]
+        for i, (o, r) in enumerate(zip(outs, ref)):
+            assert torch.equal(o, r), f"replay {rep}, layer {i}"
+        del junk

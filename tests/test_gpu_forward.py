@@ -271,3 +271,24 @@ def test_router_losses_fused_match_oracle(dev, R, C, k, scale):
     for n in names:
         assert_rel(got[n].reshape(1).cpu(), ref[n].reshape(1).detach(), 1e-5, n)
     assert_rel(lg.grad.cpu(), lr.grad, 1e-4, "dlogits")
+
+
+@pytest.mark.parametrize("M,K,N,odt", [(1, 768, 768, torch.bfloat16), (64, 768, 768, torch.bfloat16),
+                                       (65, 640, 48, torch.float32), (7, 128, 16, torch.bfloat16),
+                                       (256, 2048, 1536, torch.float32), (200, 896, 256, torch.bfloat16)])
+def test_linear_rows_matches_fp64(dev, M, K, N, odt):
+    """The few-row x W^T kernel (decode q_proj / o_proj) against a float64 product of the same
+    bf16 operands."""
+    from memory_amd import ops
+    g = gen(M + K + N)
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    W = (torch.randn(N, K, generator=g) * K ** -0.5).to(torch.bfloat16)
+    y = torch.empty(M, N, device=dev, dtype=odt)
+    from memory_amd import _lib as L
+    xd, Wd = x.to(dev), W.to(dev)          # held: the kernel reads them after the call returns
+    L.call("moc_linear_rows", L.ptr(xd), M, K, L.ptr(Wd), N, L.dtype_code(odt), L.ptr(y), L.stream_ptr(dev))
+    torch.cuda.synchronize()
+    ref = x.double() @ W.double().t()
+    assert_rel(y.float().cpu(), ref, 1e-5 if odt == torch.float32 else 1e-2, "x W^T")
+    # the product path dispatches few-row bf16 inputs here
+    assert_rel(ops.linear(xd, Wd).float().cpu(), ref, 1e-2, "ops.linear")
