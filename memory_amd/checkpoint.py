@@ -24,7 +24,7 @@ import torch
 import torch.nn as nn
 
 from .memory_block import MemorySublayer
-from .model import prepend_shared_chapters, split_rows, normalize_shared_routed_memory_vectors
+from .model import prepend_shared_chapters32, split_rows, normalize_shared_routed_memory_vectors
 from .router import ChapterRouter
 
 WEIGHT_FILES = ("model.pt", "model.safetensors", "pytorch_model.bin")
@@ -265,10 +265,10 @@ class MemoryStack(nn.Module):
             return sub(hidden_states, token_routing_state=state,
                        token_routing_kernel_version=self.kernel_version), losses
         window = self.window if self.strategy in ("sequence-rolling", "sequence_rolling") else None
-        idx, w, losses = router(block_input, return_losses=return_losses, exclude_prefix_chapters=S,
-                                rolling_window_size=window)
-        idx_star, omega = prepend_shared_chapters(idx, w, num_chapters=self.num_chapters, num_shared_chapters=S,
-                                                  routed_scaling_factor=self.routed_scaling_factor)
+        idx, w, losses = router.route_ids32(block_input, return_losses=return_losses, exclude_prefix_chapters=S,
+                                            rolling_window_size=window)
+        idx_star, omega = prepend_shared_chapters32(idx, w, num_chapters=self.num_chapters, num_shared_chapters=S,
+                                                    routed_scaling_factor=self.routed_scaling_factor)
         normalize = self.normalize and 0 < S < idx_star.shape[1]
         state = {"bank": bank, "chapter_indices": idx_star, "chapter_weights": omega,
                  "num_chapters": self.num_chapters, "tokens_per_chapter": T, "normalize": normalize,

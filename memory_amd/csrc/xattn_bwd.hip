@@ -462,7 +462,11 @@ __global__ __launch_bounds__(64 * kDkvWavesPerChapter * DkvCfg<T>::CPW) void xat
   }
   if (lane == 0) sDom[wave] = dom;
   __syncthreads();
-  if (!active) return;
+  if (!active) {
+    // a skipped slot's d omega is 0 (written, so the caller needs no zero fill)
+    if (slot < NS && wave % WPC == 0 && lane == 0) domega_part[(size_t)e * HK + hk] = 0.f;
+    return;
+  }
   if (wave % WPC == 0 && lane == 0) {
     float s = 0.f;
     for (int i = 0; i < WPC; ++i) s += sDom[wave + i];

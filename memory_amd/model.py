@@ -44,11 +44,20 @@ def select_routed_chapters_from_probs(probs: torch.Tensor, top_k: int, num_share
 def prepend_shared_chapters(chapter_indices: torch.Tensor, chapter_weights: torch.Tensor, *, num_chapters: int,
                             num_shared_chapters: int, routed_scaling_factor: float):
     """model.py:356-391 (prepend kernel + its backward)."""
+    idx_star, omega = prepend_shared_chapters32(chapter_indices, chapter_weights, num_chapters=num_chapters,
+                                                num_shared_chapters=num_shared_chapters,
+                                                routed_scaling_factor=routed_scaling_factor)
+    return idx_star.long(), omega
+
+
+def prepend_shared_chapters32(chapter_indices: torch.Tensor, chapter_weights: torch.Tensor, *, num_chapters: int,
+                              num_shared_chapters: int, routed_scaling_factor: float):
+    """prepend_shared_chapters with int32 chapter ids (no conversion kernels on the layer's
+    own path)."""
     S = max(0, min(int(num_shared_chapters), int(num_chapters)))
     if S <= 0:
-        return chapter_indices, chapter_weights
-    idx_star, omega = ops.prepend_shared(chapter_indices, chapter_weights, S, routed_scaling_factor)
-    return idx_star.long(), omega
+        return chapter_indices.to(torch.int32), chapter_weights
+    return ops.prepend_shared(chapter_indices, chapter_weights, S, routed_scaling_factor)
 
 
 def normalize_shared_routed_memory_vectors(memory: torch.Tensor, *, num_shared_chapters: int,
@@ -129,17 +138,21 @@ class RoutedMemoryLayer(nn.Module):
                                                 gradient_checkpointing=gradient_checkpointing)
 
     def route(self, hidden_states: torch.Tensor, return_losses: bool = True):
-        idx, w, losses = self.router(hidden_states, return_losses=return_losses,
-                                     exclude_prefix_chapters=self.num_shared_chapters,
-                                     rolling_window_size=self.routing_window_size)
-        idx_star, omega = prepend_shared_chapters(idx, w, num_chapters=self.num_chapters,
-                                                  num_shared_chapters=self.num_shared_chapters,
-                                                  routed_scaling_factor=self.routed_scaling_factor)
+        idx_star, omega, losses = self._route32(hidden_states, return_losses)
+        return idx_star.long(), omega, losses
+
+    def _route32(self, hidden_states: torch.Tensor, return_losses: bool = True):
+        idx, w, losses = self.router.route_ids32(hidden_states, return_losses=return_losses,
+                                                 exclude_prefix_chapters=self.num_shared_chapters,
+                                                 rolling_window_size=self.routing_window_size)
+        idx_star, omega = prepend_shared_chapters32(idx, w, num_chapters=self.num_chapters,
+                                                    num_shared_chapters=self.num_shared_chapters,
+                                                    routed_scaling_factor=self.routed_scaling_factor)
         return idx_star, omega, losses
 
     def forward(self, hidden_states: torch.Tensor, bank: torch.Tensor,
                 return_losses: bool = True) -> Tuple[torch.Tensor, Dict[str, torch.Tensor]]:
-        idx_star, omega, losses = self.route(hidden_states, return_losses)
+        idx_star, omega, losses = self._route32(hidden_states, return_losses)
         NS = idx_star.shape[1]
         # model.py:402-405: normalisation only mixes when both the shared and routed slices are non-empty
         normalize = self.normalize and 0 < self.num_shared_chapters < NS

@@ -116,6 +116,7 @@ class _RouterTopK(torch.autograd.Function):
         ctx.save_for_backward(logits, idx)
         ctx.k, ctx.S = k, S
         ctx.mark_non_differentiable(idx)
+        ctx.set_materialize_grads(False)   # no zero-filled gradient for the int ids
         return idx, w
 
     @staticmethod
@@ -152,6 +153,7 @@ class _PrependShared(torch.autograd.Function):
         ctx.save_for_backward(w)
         ctx.S, ctx.scale = S, float(scale)
         ctx.mark_non_differentiable(idx_star)
+        ctx.set_materialize_grads(False)   # no zero-filled gradient for the int ids
         return idx_star, omega
 
     @staticmethod
@@ -479,7 +481,7 @@ class _RoutedAttention(torch.autograd.Function):
         call("moc_xattn_bwd_dq", dt, ptr(q), ptr(kt), ptr(ktt), ptr(vt), kt.shape[0] * HK, ptr(edge_u), ptr(om),
              ptr(dout), ptr(lse), ptr(delta), B, Lq, H, HK, Dh, T, NS, scale, ptr(dq), st)
         dkv_edge = torch.empty(B * NS * T, 2 * KV, device=dev, dtype=dtype)
-        dom_part = torch.zeros(B * NS, HK, device=dev, dtype=torch.float32)
+        dom_part = torch.empty(B * NS, HK, device=dev, dtype=torch.float32)   # every entry written
         call("moc_xattn_bwd_dkv", dt, ptr(q), ptr(qt), ptr(dout), ptr(dot), ptr(kt), ptr(vt), ptr(edge_u), ptr(om),
              ptr(lse), ptr(delta), B, Lq, H, HK, Dh, T, NS, scale, ptr(dkv_edge), ptr(dom_part), st)
         domega = dom_part.sum(-1).view(B, NS)

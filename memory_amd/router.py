@@ -86,6 +86,13 @@ class ChapterRouter(nn.Module):
     # -- forward --------------------------------------------------------------
     def forward(self, hidden_states: torch.Tensor, return_losses: bool = True, exclude_prefix_chapters: int = 0,
                 rolling_window_size: Optional[int] = None) -> Tuple[torch.Tensor, torch.Tensor, Dict[str, torch.Tensor]]:
+        idx, w, losses = self.route_ids32(hidden_states, return_losses, exclude_prefix_chapters, rolling_window_size)
+        return idx.long(), w, losses
+
+    def route_ids32(self, hidden_states: torch.Tensor, return_losses: bool = True, exclude_prefix_chapters: int = 0,
+                    rolling_window_size: Optional[int] = None):
+        """forward with the chapter ids left in int32 (the kernels' index type), for callers
+        that pass them straight on to the chapter plan."""
         B = hidden_states.shape[0]
         logits = self.sequence_logits(hidden_states, rolling_window_size)
         S = int(exclude_prefix_chapters)
@@ -93,11 +100,10 @@ class ChapterRouter(nn.Module):
             raise ValueError(f"exclude_prefix_chapters must be in [0, {self.num_chapters}], got {S}")
         k = min(int(self.top_k), self.num_chapters - S) if S > 0 else int(self.top_k)
         if k <= 0:
-            idx = torch.empty((B, 0), dtype=torch.long, device=hidden_states.device)
+            idx = torch.empty((B, 0), dtype=torch.int32, device=hidden_states.device)
             w = torch.empty((B, 0), dtype=torch.float32, device=hidden_states.device)
         else:
-            idx32, w = ops.router_topk(logits, k, S)
-            idx = idx32.long()
+            idx, w = ops.router_topk(logits, k, S)
         losses = {}
         if return_losses:
             losses = compute_router_losses(logits, None, idx, self.num_chapters)
