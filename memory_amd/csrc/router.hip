@@ -412,6 +412,10 @@ __global__ __launch_bounds__(256) void pool_reduce_kernel(const float* __restric
 // so a thread never waits on one load at a time.  d % 4 == 0.
 constexpr int kLinChap = 16;
 constexpr int kLinRows = 16;
+// The forward gives each wave one chapter (4 per workgroup): its cost is the per-(chapter, row)
+// wave reductions, so more, smaller workgroups keep more of them in flight.
+constexpr int kLinCpw = 1;
+constexpr int kLinChapFwd = 4 * kLinCpw;
 
 __device__ __forceinline__ f32x4 load4f(const float* p) { return *reinterpret_cast<const f32x4*>(p); }
 __device__ __forceinline__ f32x4 load4f(const bf16* p) {
@@ -438,33 +442,34 @@ __global__ __launch_bounds__(256) void router_linear_kernel(const float* __restr
                                                             int64_t C, float* __restrict__ logits) {
   extern __shared__ float xs[];  // [kLinRows][d]
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int64_t c0 = (int64_t)blockIdx.x * kLinChap + 4 * wave;  // this wave's 4 chapters
+  const int64_t c0 = (int64_t)blockIdx.x * kLinChapFwd + kLinCpw * wave;  // this wave's chapters
   for (int64_t r0 = 0; r0 < R; r0 += kLinRows) {
     const int nr = (int)min((int64_t)kLinRows, R - r0);
     __syncthreads();
     stage_rows(x + r0 * d, (int64_t)nr * d, xs);
     __syncthreads();
-    float acc[4][kLinRows];
+    float acc[kLinCpw][kLinRows];
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
+    for (int q = 0; q < kLinCpw; ++q)
 #pragma unroll
       for (int r = 0; r < kLinRows; ++r) acc[q][r] = 0.f;
     for (int64_t j = 4 * lane; j < d; j += 256) {
-      f32x4 wv[4];
+      f32x4 wv[kLinCpw];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) wv[q] = c0 + q < C ? load4f(W + (c0 + q) * d + j) : f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int q = 0; q < kLinCpw; ++q)
+        wv[q] = c0 + q < C ? load4f(W + (c0 + q) * d + j) : f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int r = 0; r < kLinRows; ++r) {
         if (r < nr) {  // (a guard, not a break: the loop must unroll fully to keep acc in registers)
           const f32x4 xv = *reinterpret_cast<const f32x4*>(xs + r * d + j);
 #pragma unroll
-          for (int q = 0; q < 4; ++q)
+          for (int q = 0; q < kLinCpw; ++q)
             acc[q][r] += xv[0] * wv[q][0] + xv[1] * wv[q][1] + xv[2] * wv[q][2] + xv[3] * wv[q][3];
         }
       }
     }
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
+    for (int q = 0; q < kLinCpw; ++q) {
       const int64_t c = c0 + q;
       const float bc = (bias && c < C) ? bias[c] : 0.f;
 #pragma unroll
@@ -932,7 +937,7 @@ int moc_router_linear(const float* x, int64_t R, int64_t d, const void* W, int w
   MOC_REQUIRE(d <= 4096 && d % 4 == 0, MOC_ERR_UNSUPPORTED, "moc_router_linear: d=%lld must be a multiple of 4, <= 4096",
               (long long)d);
   if (R == 0) return MOC_OK;
-  dim3 grid((unsigned)((C + kLinChap - 1) / kLinChap));
+  dim3 grid((unsigned)((C + kLinChapFwd - 1) / kLinChapFwd));
   const size_t lds = (size_t)kLinRows * d * sizeof(float);
   if (w_dtype == MOC_F32)
     hipLaunchKernelGGL(router_linear_kernel<float>, grid, dim3(256), lds, stream, x, R, d, (const float*)W, bias, C,

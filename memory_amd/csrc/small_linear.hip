@@ -3,42 +3,44 @@
 //
 // A library GEMM tiles such a product into a handful of output tiles, each walking the whole
 // K dimension on its own, so the launch is one long chain of dependent loads.  Here a
-// workgroup owns 16 output columns and 64 rows, and its 4 waves split K: each wave issues
-// all of its x and W fragment loads before its first MFMA (v_mfma_f32_16x16x32_bf16), and the
-// four partial tiles are added through LDS in a fixed order.  Bound: the latency of one
-// round of loads (W is read once: N * K * 2 bytes).
+// workgroup owns one 16 x 16 output tile (64 rows x 768 columns make 192 workgroups), and its
+// 4 waves split K: each wave issues all of its x and W fragment loads before its first MFMA
+// (v_mfma_f32_16x16x32_bf16), and the four partial tiles are added through LDS in a fixed
+// order.  Bound: the latency of one round of loads (each W slice is re-read by the M / 16 row
+// tiles, mostly from L2).
 
 #include "moc_common.h"
 
 namespace moc {
 
 constexpr int kSlWaves = 4;
-constexpr int kSlRows = 64;       // rows per workgroup (4 MFMA row tiles)
+constexpr int kSlTiles = 1;       // 16-row MFMA tiles per workgroup
+constexpr int kSlRows = 16 * kSlTiles;
 constexpr int kSlChunks = 6;      // 32-wide K chunks a wave holds in registers at once
 
 template <typename TO>
 __global__ __launch_bounds__(64 * kSlWaves) void small_linear_kernel(const bf16* __restrict__ x, int M, int K,
                                                                     const bf16* __restrict__ W, int N,
                                                                     TO* __restrict__ y) {
-  __shared__ f32x4 red[kSlWaves][4][64];
+  __shared__ f32x4 red[kSlWaves][kSlTiles][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g = lane >> 4, c16 = lane & 15;
   const int n0 = blockIdx.x * 16, m0 = blockIdx.y * kSlRows;
   const int kw = K / kSlWaves;                 // this wave's K range: [wave * kw, wave * kw + kw)
   const int nch = kw / 32;
-  f32x4 acc[4];
+  f32x4 acc[kSlTiles];
 #pragma unroll
-  for (int mt = 0; mt < 4; ++mt) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int mt = 0; mt < kSlTiles; ++mt) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
   const bf16* wrow = W + (size_t)(n0 + c16) * K + wave * kw + 8 * g;
   for (int c0 = 0; c0 < nch; c0 += kSlChunks) {
-    bf16x8 a[kSlChunks][4], b[kSlChunks];
+    bf16x8 a[kSlChunks][kSlTiles], b[kSlChunks];
 #pragma unroll
     for (int j = 0; j < kSlChunks; ++j) {
       const bool live = c0 + j < nch;
       const int k = 32 * (c0 + j);
       b[j] = live ? *reinterpret_cast<const bf16x8*>(wrow + k) : bf16x8{};
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt) {
+      for (int mt = 0; mt < kSlTiles; ++mt) {
         const int m = m0 + 16 * mt + c16;
         a[j][mt] = (live && m < M) ? *reinterpret_cast<const bf16x8*>(x + (size_t)m * K + wave * kw + k + 8 * g)
                                    : bf16x8{};
@@ -47,13 +49,14 @@ __global__ __launch_bounds__(64 * kSlWaves) void small_linear_kernel(const bf16*
 #pragma unroll
     for (int j = 0; j < kSlChunks; ++j)
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt) mma(acc[mt], a[j][mt], b[j]);
+      for (int mt = 0; mt < kSlTiles; ++mt) mma(acc[mt], a[j][mt], b[j]);
   }
 #pragma unroll
-  for (int mt = 0; mt < 4; ++mt) red[wave][mt][lane] = acc[mt];
+  for (int mt = 0; mt < kSlTiles; ++mt) red[wave][mt][lane] = acc[mt];
   __syncthreads();
-  // thread t sums tile (t / 64) of lane (t % 64) over the waves, in wave order
+  // wave t (< kSlTiles) sums tile t of its lane over the waves, in wave order
   const int mt = threadIdx.x >> 6;
+  if (mt >= kSlTiles) return;
   f32x4 s = red[0][mt][lane];
 #pragma unroll
   for (int w = 1; w < kSlWaves; ++w) {

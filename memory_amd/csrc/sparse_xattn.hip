@@ -272,6 +272,75 @@ __global__ __launch_bounds__(64 * kCombWaves) void sparse_combine_kernel(const f
   }
 }
 
+// The same combine for few rows of at most 4 * kCombSmallPerGroup slots (decode: the shared
+// chapter + 64 routed), with every load of a row in one round: each lane reads the
+// slot values of slots lane and lane + 64, and lane group g reads the partial rows of slots
+// g, g + 4, ... before any of them is weighted.  The rows of skipped slots lie inside o_part
+// but were never written: their values are dropped by a select (never multiplied by a zero
+// weight, which would keep a NaN).
+constexpr int kCombSmallPerGroup = 17;
+
+template <typename T>
+__global__ __launch_bounds__(64 * kCombWaves) void sparse_combine_small_kernel(
+    const float* __restrict__ o_part, const float* __restrict__ lse_part, const int32_t* __restrict__ edge_u,
+    const float* __restrict__ w, int mode, int S, int rpe, int64_t ntok, int HQ, int hq_off, T* __restrict__ out,
+    float* __restrict__ lse_joint) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * kCombWaves + (threadIdx.x >> 6);
+  if (row >= ntok * rpe) return;
+  const int64_t tok = row / rpe;
+  const int r = (int)(row % rpe);
+  const int g = lane >> 4, sub = lane & 15;
+  // slot values (lane s holds slot s and s + 64)
+  float lg[2];
+  bool ok[2];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int sl = lane + 64 * q;
+    const int64_t e = tok * S + sl;
+    ok[q] = sl < S && edge_u[e] >= 0;
+    lg[q] = 0.f;
+    if (ok[q]) lg[q] = mode == 0 ? w[e] : lse_part[e * rpe + r] + sp_logw(mode, w ? w[e] : 1.f);
+  }
+  // partial rows of this lane group's slots, all in flight
+  f32x4 v[kCombSmallPerGroup];
+#pragma unroll
+  for (int i = 0; i < kCombSmallPerGroup; ++i) {
+    const int j = 4 * i + g;
+    v[i] = j < S ? *reinterpret_cast<const f32x4*>(o_part + ((tok * S + j) * rpe + r) * kSpDh + 4 * sub)
+                 : f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  float M = -INFINITY;
+  if (mode != 0) {
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+      if (ok[q]) M = fmaxf(M, lg[q]);
+    M = wave_max(M);
+  }
+  float a[2];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) a[q] = !ok[q] ? 0.f : mode == 0 ? lg[q] : (M > -INFINITY ? exp2f(lg[q] - M) : 0.f);
+  f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < kCombSmallPerGroup; ++i) {
+    const int j = 4 * i + g;
+    const float aj = __shfl(j < 64 ? a[0] : a[1], j & 63, 64);
+    if (j < S && aj != 0.f) acc += aj * v[i];
+  }
+  acc = sp_groups_sum(acc);
+  float inv = 1.f;
+  if (mode != 0) {
+    const float den = wave_sum(a[0] + a[1]);
+    inv = den > 0.f ? 1.f / den : 0.f;
+    if (lane == 0) lse_joint[row] = den > 0.f ? M + log2f(den) : INFINITY;
+  }
+  if (lane < 16) {
+    T* op = out + ((int64_t)tok * HQ + hq_off + r) * kSpDh + 4 * lane;
+#pragma unroll
+    for (int x = 0; x < 4; ++x) op[x] = from_f<T>(acc[x] * inv);
+  }
+}
+
 // ----------------------------------------------------------------- backward
 // mode 0: dwe[e*rpe + r] = dO_row . o_part[e, r]      (dL/dw_s partial per head)
 // else:   delta[row]     = dO_row . out_row
@@ -1150,14 +1219,20 @@ int moc_sparse_combine(int dtype, const float* o_part, const float* lse_part, co
   const int64_t rows = ntok * rpe;
   if (rows == 0) return MOC_OK;
   dim3 grid((unsigned)((rows + kCombWaves - 1) / kCombWaves));
-  if (dtype == MOC_BF16)
-    hipLaunchKernelGGL(sparse_combine_kernel<bf16>, grid, dim3(64 * kCombWaves), 0, stream, o_part, lse_part, edge_u, w, mode, S,
-                       rpe, ntok, HQ, hq_off, (bf16*)out, lse_joint);
-  else if (dtype == MOC_F32)
-    hipLaunchKernelGGL(sparse_combine_kernel<float>, grid, dim3(64 * kCombWaves), 0, stream, o_part, lse_part, edge_u, w, mode, S,
-                       rpe, ntok, HQ, hq_off, (float*)out, lse_joint);
-  else
+  // few rows (decode): latency-bound, every load of a row in one round; many rows (token
+  // routing over a batch): throughput-bound, the lighter streaming kernel keeps more rows resident
+  const bool small = S <= 4 * kCombSmallPerGroup && rows <= 16384;
+#define SC(KERN, TT)                                                                                                  \
+  hipLaunchKernelGGL(KERN<TT>, grid, dim3(64 * kCombWaves), 0, stream, o_part, lse_part, edge_u, w, mode, S, rpe, ntok, \
+                     HQ, hq_off, (TT*)out, lse_joint)
+  if (dtype == MOC_BF16) {
+    if (small) SC(sparse_combine_small_kernel, bf16); else SC(sparse_combine_kernel, bf16);
+  } else if (dtype == MOC_F32) {
+    if (small) SC(sparse_combine_small_kernel, float); else SC(sparse_combine_kernel, float);
+  } else {
     return set_error(MOC_ERR_UNSUPPORTED, "moc_sparse_combine: dtype %d", dtype);
+  }
+#undef SC
   return check_launch("sparse_combine_kernel");
 }
 
