@@ -50,9 +50,12 @@ def _ref(mode, q, k, v, idx, w, scale):
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("mode", [0, 1, 2, 3])
-# the third case gives every (chapter, kv head) ~130 rows: several 32-row blocks and a ragged last one
+# the third case gives every (chapter, kv head) ~130 rows: several 32-row blocks and a ragged last one;
+# the last two take the streaming slot combine (more than 68 slots per token; more than 16,384 rows),
+# the others the single-round one
 @pytest.mark.parametrize("B,Tq,HQ,HK,M,S,per_head", [(2, 40, 2, 2, 6, 3, False), (1, 70, 4, 2, 5, 2, True),
-                                                     (1, 200, 2, 2, 3, 2, False)])
+                                                     (1, 200, 2, 2, 3, 2, False), (1, 30, 2, 2, 80, 70, False),
+                                                     (1, 2100, 8, 2, 4, 2, False)])
 def test_fsa_modes_forward_backward(gpu_device, dtype, mode, B, Tq, HQ, HK, M, S, per_head):
     print(f"fsa mode={mode} dtype={dtype} B={B} Tq={Tq} HQ={HQ} HK={HK} M={M} S={S} per_head={per_head}", flush=True)
     from memory_amd import sparse_attention as SA
