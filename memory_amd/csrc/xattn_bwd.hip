@@ -226,10 +226,13 @@ __global__ __launch_bounds__(kBThreads) void xattn_bwd_dq_kernel(
 // dk/dv, slot-group decomposition.  One workgroup = one (sequence b, kv head hk,
 // group of CPW consecutive slots); each slot's chapter (64 keys) is split over two
 // waves of 32 keys, so a wave's accumulators, K / V fragments and score tiles fit in
-// 256 registers and two waves share each SIMD (one wave's MFMAs run under the
-// other's softmax work and stalls).  All slots of a sequence attend the same
-// queries, so the query-side tiles of a step (Q and dO row-major, Q^T and dO^T, QS
-// queries each) are staged in LDS once and shared by all waves; they are
+// 256 registers and two waves share each SIMD.  A bf16 workgroup is 4 waves (2 slots),
+// one per SIMD, so the two waves on a SIMD belong to different workgroups: their steps
+// are not aligned by a common barrier, and one wave's MFMAs run under the other's
+// softmax work (8-wave workgroups, in lockstep, measured 5% slower).  All slots of a
+// sequence attend the same queries, so the query-side tiles of a step (Q and dO
+// row-major, Q^T and dO^T, QS queries each) are staged in LDS once per workgroup and
+// shared by its waves; they are
 // double-buffered, the next step's global loads being issued before the math of the
 // current one, so a step costs one barrier.  K and V fragments live in registers for
 // the whole kernel (loaded once from HBM).  Output: per-edge dk / dv rows (edge e =
@@ -237,16 +240,14 @@ __global__ __launch_bounds__(kBThreads) void xattn_bwd_dq_kernel(
 //
 // Per score element (key j, query i) with p = exp2(c s - lse_i) the softmax
 // probability (c = omega * scale * log2 e, s = q_i . k_j, dP = dO_i . v_j):
-//   p~   = omega p = exp2(c s - (lse_i - log2 omega))   (A operand of dV = P~^T dO)
 //   t    = scale (omega dP - delta_i)
-//   ds~  = p~ t                                          (A operand of dK = dS~^T Q)
-// which is the gradient of softmax(omega s scale) against omega-scaled values.
-// d omega = sum_ij p~ (t s + dP) / omega is read off the accumulators at the end:
-// sum_j dk_j . k_j + dv_j . v_j, the two key halves summed in a fixed order.
-// omega == 0 runs the same loop with p~ = p (log2 omega taken as 0): d omega then
-// needs no division, and the chapter's dK / dV (which vanish) are zeroed.
+//   dk'_j = sum_i p t q_i      dv'_j = sum_i p dO_i     (A operands p t and p)
+// dk = omega dk' and dv = omega dv' (the keys enter the logits and the values the output
+// scaled by omega), applied once at the store; d omega = sum_ij (p t s + p dP) =
+// sum_j dk'_j . k_j + dv'_j . v_j, read off the accumulators, the two key halves summed in
+// a fixed order.  The same loop serves omega == 0 (all logits of the chapter 0, dk = dv = 0).
 template <typename T> struct DkvCfg;
-template <> struct DkvCfg<bf16> { static constexpr int CPW = 4, QS = 64; };
+template <> struct DkvCfg<bf16> { static constexpr int CPW = 2, QS = 64; };
 template <> struct DkvCfg<float> { static constexpr int CPW = 2, QS = 32; };
 constexpr int kDkvWavesPerChapter = 2;
 
@@ -304,7 +305,6 @@ __global__ __launch_bounds__(64 * kDkvWavesPerChapter * DkvCfg<T>::CPW) void xat
   }
   const float w = active ? omega[e] : 0.f;
   const float c = w * scale_log2, dsc = w * scale;
-  const float lw = w > 0.f ? __log2f(w) : 0.f;
 
   f32x4 dk[NKB][4], dv[NKB][4];
 #pragma unroll
@@ -410,8 +410,8 @@ __global__ __launch_bounds__(64 * kDkvWavesPerChapter * DkvCfg<T>::CPW) void xat
           F8 pa[NKB], sa[NKB];
 #pragma unroll
           for (int qb = 0; qb < 2; ++qb) {
-            // l2 - log2(omega): exp2(c s - l2) = omega p;  dl = scale * delta
-            const f32x4 l2 = *reinterpret_cast<const f32x4*>(&sL[buf][qb0 + 16 * qb + 4 * g]) - lw;
+            // exp2(c s - l2) = p;  dl = scale * delta
+            const f32x4 l2 = *reinterpret_cast<const f32x4*>(&sL[buf][qb0 + 16 * qb + 4 * g]);
             const f32x4 dl = *reinterpret_cast<const f32x4*>(&sDl[buf][qb0 + 16 * qb + 4 * g]);
 #pragma unroll
             for (int kb = 0; kb < NKB; ++kb)
@@ -419,7 +419,7 @@ __global__ __launch_bounds__(64 * kDkvWavesPerChapter * DkvCfg<T>::CPW) void xat
               for (int x = 0; x < 4; ++x) {
                 const float sraw = sc[qb][kb][x];
                 const float dpu = dp[qb][kb][x];
-                const float pt = __builtin_amdgcn_exp2f(sraw * c - l2[x]);  // omega p (p if omega = 0)
+                const float pt = __builtin_amdgcn_exp2f(sraw * c - l2[x]);  // p
                 const float tq = dpu * dsc - dl[x];                           // scale (omega dP - delta)
                 pa[kb][4 * qb + x] = from_f<T>(pt);
                 sa[kb][4 * qb + x] = from_f<T>(pt * tq);
@@ -442,9 +442,8 @@ __global__ __launch_bounds__(64 * kDkvWavesPerChapter * DkvCfg<T>::CPW) void xat
       __syncthreads();
     }
   }
-  // omega dL/domega = sum_ij p~ (t s + dP) = sum_j dk_j . k_j + dv_j . v_j (the accumulators
-  // are p~-weighted sums of dS~^T Q and P~^T dO), summed over the query heads of hk and,
-  // in a fixed order, over the chapter's two key halves
+  // dL/domega = sum_ij p (t s + dP) = sum_j dk'_j . k_j + dv'_j . v_j, summed over the query
+  // heads of hk and, in a fixed order, over the chapter's two key halves
   float dom = 0.f;
   if (active) {
     const T* kp = ktiles + ((size_t)u * HK + hk) * 4096;
@@ -470,19 +469,7 @@ __global__ __launch_bounds__(64 * kDkvWavesPerChapter * DkvCfg<T>::CPW) void xat
   if (wave % WPC == 0 && lane == 0) {
     float s = 0.f;
     for (int i = 0; i < WPC; ++i) s += sDom[wave + i];
-    if (w > 0.f) s /= w;
     domega_part[(size_t)e * HK + hk] = s;
-  }
-  if (w == 0.f) {
-    // the element loop ran with p in place of omega p: keys and values of a zero-weight
-    // chapter carry no gradient
-#pragma unroll
-    for (int kb = 0; kb < NKB; ++kb)
-#pragma unroll
-      for (int db = 0; db < 4; ++db) {
-        dk[kb][db] = f32x4{0.f, 0.f, 0.f, 0.f};
-        dv[kb][db] = f32x4{0.f, 0.f, 0.f, 0.f};
-      }
   }
   T* rows = dkv_edge + (size_t)e * 64 * row_stride;
 #pragma unroll
@@ -492,8 +479,8 @@ __global__ __launch_bounds__(64 * kDkvWavesPerChapter * DkvCfg<T>::CPW) void xat
 #pragma unroll
       for (int x = 0; x < 4; ++x) {
         const int key = k0 + 16 * kb + 4 * g + x, dim = 16 * db + c16;
-        rows[(size_t)key * row_stride + hk * 64 + dim] = from_f<T>(dk[kb][db][x]);
-        rows[(size_t)key * row_stride + KV + hk * 64 + dim] = from_f<T>(dv[kb][db][x]);
+        rows[(size_t)key * row_stride + hk * 64 + dim] = from_f<T>(w * dk[kb][db][x]);
+        rows[(size_t)key * row_stride + KV + hk * 64 + dim] = from_f<T>(w * dv[kb][db][x]);
       }
 }
 
