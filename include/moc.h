@@ -134,8 +134,9 @@ int moc_row_stats(const void* bank, int bank_dtype, int64_t d, int T, const int3
  * followed by k_proj/v_proj of MemoryCrossAttention._compute_qkv (memory_attention.py:241-243),
  * computed once per distinct chapter.  bank [N_m, d] (bf16 or f32), wkv [2*HK*Dh, d] of dtype
  * (= [Wk; Wv]); row_mean/row_rstd from moc_row_stats or both NULL.  Outputs (each may be NULL,
- * but K and V each need one form): chapter-head tiles k_tiles, v_tiles [max_u][HK][T][Dh] and
- * their transposes kt_tiles, vt_tiles [max_u][HK][Dh][T], of dtype.  The key axis of the
+ * but K and V each need one form): chapter-head tiles k_tiles, v_tiles [max_u][HK][T][Dh] (the
+ * form every attention entry point here reads) and, optionally, their transposes kt_tiles,
+ * vt_tiles [max_u][HK][Dh][T], of dtype.  The key axis of the
  * transposed tiles is stored in MFMA key order: within each 32-key group, key 4g + e sits at
  * position 8g + e and key 16 + 4g + e at 8g + 4 + e (g, e < 4).  d % 64 == 0,
  * (2*HK*Dh) % 128 == 0, T % 32 == 0 when a transposed output is requested. */
@@ -149,11 +150,11 @@ int moc_kv_project(int dtype, const void* bank, int bank_dtype, int64_t d, int T
 /* Replaces MemoryCrossAttention._attention on omega-weighted gathered memory
  * (memory_transformer/model.py:689-692 + memory_attention.py:458-478, :269-318) for the
  * sequence-level path: one joint softmax over the NS selected chapters of each sequence,
- * with omega scaling both logits and values.  q [B, L, H, Dh]; k_tiles and vt_tiles (V transposed)
+ * with omega scaling both logits and values.  q [B, L, H, Dh]; k_tiles and v_tiles [n_tiles][T][Dh]
  * from moc_kv_project, n_tiles = max_u * HK tiles each (< 4 GiB per buffer); slot_u i32 [B, NS] (the plan's edge_u); omega f32 [B, NS]; out [B, L, H, Dh];
  * lse f32 [B, H, round_up(L, 128)] (log2 domain, +inf in the padding; consumed by the backward).
  * Dh == 64, T == 64. */
-int moc_xattn_fwd(int dtype, const void* q, const void* k_tiles, const void* vt_tiles, int64_t n_tiles,
+int moc_xattn_fwd(int dtype, const void* q, const void* k_tiles, const void* v_tiles, int64_t n_tiles,
                   const int32_t* slot_u, const float* omega, int64_t B, int64_t L, int H, int HK, int Dh, int T,
                   int NS, float scale, void* out, float* lse, hipStream_t stream);
 
@@ -166,8 +167,8 @@ int moc_xattn_fwd(int dtype, const void* q, const void* k_tiles, const void* vt_
  * transposed per (sequence, head), zero-padded. */
 int moc_xattn_bwd_prep(int dtype, const void* q, const void* out, const void* dout, int64_t B, int64_t L, int H,
                        int Dh, float* delta, void* qt, void* dot, hipStream_t stream);
-/* dq [B, L, H, Dh] (dtype); needs K, K^T and V tiles. */
-int moc_xattn_bwd_dq(int dtype, const void* q, const void* k_tiles, const void* kt_tiles, const void* v_tiles,
+/* dq [B, L, H, Dh] (dtype) from the K and V tiles of moc_xattn_fwd. */
+int moc_xattn_bwd_dq(int dtype, const void* q, const void* k_tiles, const void* v_tiles,
                      int64_t n_tiles, const int32_t* slot_u, const float* omega, const void* dout, const float* lse,
                      const float* delta, int64_t B, int64_t L, int H, int HK, int Dh, int T, int NS, float scale,
                      void* dq, hipStream_t stream);
@@ -175,7 +176,7 @@ int moc_xattn_bwd_dq(int dtype, const void* q, const void* k_tiles, const void* 
  * the chapter in slot `slot` of sequence b the rows [dL/dk (all kv heads) | dL/dv], where
  * dL/dk, dL/dv are gradients w.r.t. the unweighted projected keys/values (omega folded in).
  * Rows of skipped slots are not written.  domega_part f32 [B * NS][HK]: per (edge, kv head)
- * parts of dL/domega (caller sums over HK; skipped edges are not written). */
+ * parts of dL/domega (caller sums over HK; skipped edges get 0). */
 int moc_xattn_bwd_dkv(int dtype, const void* q, const void* qt, const void* dout, const void* dot,
                       const void* k_tiles, const void* v_tiles, const int32_t* slot_u, const float* omega,
                       const float* lse, const float* delta, int64_t B, int64_t L, int H, int HK, int Dh, int T,

@@ -197,6 +197,24 @@ __device__ __forceinline__ bf16x8 tr_frag_mk(const char* base, int rb, int cb, i
   return __builtin_bit_cast(bf16x8, v);
 }
 
+// The same MFMA-key-order fragment for either element type: bf16 through the transposing
+// read above, fp32 (no transposing read for 32-bit elements) element by element.
+template <typename Tile, typename T>
+__device__ __forceinline__ typename Frag<T>::type mk_frag(const char* base, int rb, int cb, int lane) {
+  if constexpr (sizeof(T) == 2) {
+    return tr_frag_mk<Tile>(base, rb, cb, lane);
+  } else {
+    f32x8 r;
+    const int row = rb + 4 * (lane >> 4), col = cb + (lane & 15);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      r[e] = *reinterpret_cast<const float*>(base + Tile::off(row + e, col));
+      r[4 + e] = *reinterpret_cast<const float*>(base + Tile::off(row + 16 + e, col));
+    }
+    return r;
+  }
+}
+
 // Orders LDS accesses of one wave: everything before is visible to every lane of the
 // wave after (LDS executes one wave's instructions in order; this keeps the compiler
 // from moving accesses across).

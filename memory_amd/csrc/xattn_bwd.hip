@@ -79,16 +79,16 @@ __global__ __launch_bounds__(256) void xattn_bwd_prep_kernel(const T* __restrict
 // dq: one workgroup = 128 queries of one (sequence, head), loop over its slots.
 template <typename T>
 __global__ __launch_bounds__(kBThreads) void xattn_bwd_dq_kernel(
-    const T* __restrict__ q, const T* __restrict__ ktiles, const T* __restrict__ kttiles,
-    const T* __restrict__ vtiles, const int32_t* __restrict__ slot_u, const float* __restrict__ omega,
+    const T* __restrict__ q, const T* __restrict__ ktiles, const T* __restrict__ vtiles,
+    const int32_t* __restrict__ slot_u, const float* __restrict__ omega,
     const T* __restrict__ dout, const float* __restrict__ lse, const float* __restrict__ delta, int B, int L, int H,
     int HK, int NS, int64_t n_tiles, float scale_log2, float scale, T* __restrict__ dq) {
   typedef typename Frag<T>::type F8;
   using Tile = SwzTile<T, 64>;
   constexpr int TB = kBT * kBDh * (int)sizeof(T);
-  // double-buffered K, K^T and V tiles (48 KB bf16, 96 KB fp32)
+  // double-buffered K and V tiles (32 KB bf16, 64 KB fp32); the K^T operand of dQ = dS K
+  // is read from the K tile with the transposing LDS read
   __shared__ __attribute__((aligned(16))) char sK[2][TB];
-  __shared__ __attribute__((aligned(16))) char sKt[2][TB];
   __shared__ __attribute__((aligned(16))) char sV[2][TB];
 
   // tiles: (sequence, head) major, 128-query block minor (XCD-local chapter tiles)
@@ -125,17 +125,15 @@ __global__ __launch_bounds__(kBThreads) void xattn_bwd_dq_kernel(
 
   const int32_t* su = slot_u + (size_t)b * NS;
   const float* om = omega + (size_t)b * NS;
-  TileIO<T, kBThreads> kio, ktio, vio;
+  TileIO<T, kBThreads> kio, vio;
   const uint32_t nbytes = (uint32_t)(n_tiles * TB);
-  const Buf kb(ktiles, nbytes), ktb(kttiles, nbytes), vb(vtiles, nbytes);
+  const Buf kb(ktiles, nbytes), vb(vtiles, nbytes);
   auto tile_off = [&](int u) { return (uint32_t)(((size_t)u * HK + hk) * TB); };
   int u_cur = su[0];
   if (u_cur >= 0) {
     kio.load(kb, tile_off(u_cur), tid);
-    ktio.load(ktb, tile_off(u_cur), tid);
     vio.load(vb, tile_off(u_cur), tid);
     kio.store(sK[0], tid);
-    ktio.store(sKt[0], tid);
     vio.store(sV[0], tid);
   }
   vm_wait_all();  // Q / dO fragments have landed on every path into the loop
@@ -145,12 +143,10 @@ __global__ __launch_bounds__(kBThreads) void xattn_bwd_dq_kernel(
     const int u_next = (s + 1 < NS) ? su[s + 1] : -1;
     if (u_next >= 0) {
       kio.load(kb, tile_off(u_next), tid);
-      ktio.load(ktb, tile_off(u_next), tid);
       vio.load(vb, tile_off(u_next), tid);
     }
     if (u_cur >= 0) {
       const char* sKc = sK[buf];
-      const char* sKtc = sKt[buf];
       const char* sVc = sV[buf];
       const float w = om[s];
       const float c = w * scale_log2;
@@ -196,7 +192,7 @@ __global__ __launch_bounds__(kBThreads) void xattn_bwd_dq_kernel(
             }
 #pragma unroll
         for (int db = 0; db < 4; ++db) {
-          F8 bk = Tile::frag(sKtc, 16 * db + c16, 32 * kh + 8 * g);  // K^T tiles are in MFMA key order
+          const F8 bk = mk_frag<Tile, T>(sKc, 32 * kh, 16 * db, lane);  // K^T, keys in MFMA key order
 #pragma unroll
           for (int qb = 0; qb < 2; ++qb) mma(acc[qb][db], dsf[qb], bk);
         }
@@ -204,7 +200,6 @@ __global__ __launch_bounds__(kBThreads) void xattn_bwd_dq_kernel(
     }
     if (u_next >= 0) {
       kio.store(sK[buf ^ 1], tid);
-      ktio.store(sKt[buf ^ 1], tid);
       vio.store(sV[buf ^ 1], tid);
     }
     u_cur = u_next;
@@ -701,11 +696,11 @@ int moc_xattn_bwd_prep(int dtype, const void* q, const void* out, const void* do
   return check_launch("xattn_bwd_prep_kernel");
 }
 
-int moc_xattn_bwd_dq(int dtype, const void* q, const void* k_tiles, const void* kt_tiles, const void* v_tiles,
+int moc_xattn_bwd_dq(int dtype, const void* q, const void* k_tiles, const void* v_tiles,
                      int64_t n_tiles, const int32_t* slot_u, const float* omega, const void* dout, const float* lse,
                      const float* delta, int64_t B, int64_t L, int H, int HK, int Dh, int T, int NS, float scale,
                      void* dq, hipStream_t stream) {
-  MOC_REQUIRE(q && k_tiles && kt_tiles && v_tiles && slot_u && omega && dout && lse && delta && dq, MOC_ERR_ARG,
+  MOC_REQUIRE(q && k_tiles && v_tiles && slot_u && omega && dout && lse && delta && dq, MOC_ERR_ARG,
               "moc_xattn_bwd_dq: null pointer");
   MOC_REQUIRE(Dh == kBDh && T == kBT, MOC_ERR_UNSUPPORTED, "moc_xattn_bwd_dq: needs head_dim 64 and T 64");
   MOC_REQUIRE(H > 0 && HK > 0 && H % HK == 0 && NS > 0, MOC_ERR_ARG, "moc_xattn_bwd_dq: bad shape");
@@ -717,11 +712,11 @@ int moc_xattn_bwd_dq(int dtype, const void* q, const void* k_tiles, const void* 
   const float sl2 = scale * 1.4426950408889634f;
   if (dtype == MOC_BF16)
     hipLaunchKernelGGL(xattn_bwd_dq_kernel<bf16>, grid, dim3(kBThreads), 0, stream, (const bf16*)q, (const bf16*)k_tiles,
-                       (const bf16*)kt_tiles, (const bf16*)v_tiles, slot_u, omega, (const bf16*)dout, lse, delta, (int)B, (int)L, H, HK, NS,
+                       (const bf16*)v_tiles, slot_u, omega, (const bf16*)dout, lse, delta, (int)B, (int)L, H, HK, NS,
                        n_tiles, sl2, scale, (bf16*)dq);
   else if (dtype == MOC_F32)
     hipLaunchKernelGGL(xattn_bwd_dq_kernel<float>, grid, dim3(kBThreads), 0, stream, (const float*)q,
-                       (const float*)k_tiles, (const float*)kt_tiles, (const float*)v_tiles, slot_u, omega, (const float*)dout, lse, delta,
+                       (const float*)k_tiles, (const float*)v_tiles, slot_u, omega, (const float*)dout, lse, delta,
                        (int)B, (int)L, H, HK, NS, n_tiles, sl2, scale, (float*)dq);
   else
     return set_error(MOC_ERR_UNSUPPORTED, "moc_xattn_bwd_dq: dtype %d", dtype);

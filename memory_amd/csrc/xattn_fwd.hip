@@ -18,7 +18,9 @@
 // accumulates O^T = V^T P^T, whose accumulator layout is again "lane = one
 // query", so the online-softmax rescale needs no data movement, and takes the
 // row sums from an MFMA of an all-ones operand with the same P^T fragments.
-// K and V^T tiles are double-buffered in LDS.
+// K and V tiles (both [key][dim], as kv_project.hip writes them) are double-buffered in
+// LDS; the V^T operand is read from the V tile with the transposing LDS read, whose lane
+// order is the key order of the P~^T fragments.
 #include "moc_common.h"
 
 namespace moc {
@@ -36,7 +38,7 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 
 template <typename T>
 __global__ __launch_bounds__(kFwdThreads) void xattn_fwd_kernel(
-    const T* __restrict__ q, const T* __restrict__ ktiles, const T* __restrict__ vttiles,
+    const T* __restrict__ q, const T* __restrict__ ktiles, const T* __restrict__ vtiles,
     const int32_t* __restrict__ slot_u, const float* __restrict__ omega, int B, int L, int H, int HK, int NS,
     int64_t n_tiles, float scale_log2, T* __restrict__ out, float* __restrict__ lse) {
   typedef typename Frag<T>::type F8;
@@ -87,7 +89,7 @@ __global__ __launch_bounds__(kFwdThreads) void xattn_fwd_kernel(
   const float* om = omega + (size_t)b * NS;
   TileIO<T, kFwdThreads> kio, vio;
   // tiles are addressed as byte offsets into two buffers (n_tiles * TB bytes each)
-  const Buf kb(ktiles, (uint32_t)(n_tiles * TB)), vb(vttiles, (uint32_t)(n_tiles * TB));
+  const Buf kb(ktiles, (uint32_t)(n_tiles * TB)), vb(vtiles, (uint32_t)(n_tiles * TB));
   auto tile_off = [&](int u) { return (uint32_t)(((size_t)u * HK + hk) * TB); };
 
   int u_cur = su[0];
@@ -179,7 +181,7 @@ __global__ __launch_bounds__(kFwdThreads) void xattn_fwd_kernel(
         for (int ks2 = 0; ks2 < 2; ++ks2) {
 #pragma unroll
           for (int db = 0; db < 4; ++db) {
-            F8 a = Tile::frag(Vs, 16 * db + c16, 32 * ks2 + 8 * g);  // V^T tiles are in MFMA key order
+            const F8 a = mk_frag<Tile, T>(Vs, 32 * ks2, 16 * db, lane);  // V^T, keys in MFMA key order
 #pragma unroll
             for (int qb = 0; qb < 2; ++qb) mma(o[db][qb], a, pf[qb][ks2]);
           }
@@ -224,10 +226,10 @@ using namespace moc;
 
 extern "C" {
 
-int moc_xattn_fwd(int dtype, const void* q, const void* k_tiles, const void* vt_tiles, int64_t n_tiles,
+int moc_xattn_fwd(int dtype, const void* q, const void* k_tiles, const void* v_tiles, int64_t n_tiles,
                   const int32_t* slot_u, const float* omega, int64_t B, int64_t L, int H, int HK, int Dh, int T,
                   int NS, float scale, void* out, float* lse, hipStream_t stream) {
-  MOC_REQUIRE(q && k_tiles && vt_tiles && slot_u && omega && out && lse, MOC_ERR_ARG, "moc_xattn_fwd: null pointer");
+  MOC_REQUIRE(q && k_tiles && v_tiles && slot_u && omega && out && lse, MOC_ERR_ARG, "moc_xattn_fwd: null pointer");
   MOC_REQUIRE(Dh == kDh && T == kTch, MOC_ERR_UNSUPPORTED, "moc_xattn_fwd: needs head_dim 64 and 64 tokens per chapter (got %d, %d)", Dh, T);
   MOC_REQUIRE(H > 0 && HK > 0 && H % HK == 0, MOC_ERR_ARG, "moc_xattn_fwd: H=%d HK=%d", H, HK);
   MOC_REQUIRE(NS > 0 && B >= 0 && L >= 0, MOC_ERR_ARG, "moc_xattn_fwd: bad shape");
@@ -240,10 +242,10 @@ int moc_xattn_fwd(int dtype, const void* q, const void* k_tiles, const void* vt_
   const float sl2 = scale * 1.4426950408889634f;
   if (dtype == MOC_BF16)
     hipLaunchKernelGGL(xattn_fwd_kernel<bf16>, grid, dim3(kFwdThreads), 0, stream, (const bf16*)q, (const bf16*)k_tiles,
-                       (const bf16*)vt_tiles, slot_u, omega, (int)B, (int)L, H, HK, NS, n_tiles, sl2, (bf16*)out, lse);
+                       (const bf16*)v_tiles, slot_u, omega, (int)B, (int)L, H, HK, NS, n_tiles, sl2, (bf16*)out, lse);
   else if (dtype == MOC_F32)
     hipLaunchKernelGGL(xattn_fwd_kernel<float>, grid, dim3(kFwdThreads), 0, stream, (const float*)q,
-                       (const float*)k_tiles, (const float*)vt_tiles, slot_u, omega, (int)B, (int)L, H, HK, NS, n_tiles, sl2,
+                       (const float*)k_tiles, (const float*)v_tiles, slot_u, omega, (int)B, (int)L, H, HK, NS, n_tiles, sl2,
                        (float*)out,
                        lse);
   else

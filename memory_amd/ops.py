@@ -445,21 +445,21 @@ class _RoutedAttention(torch.autograd.Function):
         if norm != L.MOC_NORM_NONE:
             mean, rstd = row_stats(bank, plan, T, norm, eps)
         wkv = torch.cat([wk, wv], 0).to(dtype).contiguous()
-        kt, vt, ktt, vtt = kv_project(bank, plan, T, wkv, HK, Dh, mean, rstd, dtype, ("k", "v", "kt", "vt"))
+        kt, vt = kv_project(bank, plan, T, wkv, HK, Dh, mean, rstd, dtype, ("k", "v"))
         om = omega.float().contiguous()
         out = torch.empty(B, Lq, H, Dh, device=q.device, dtype=dtype)
         Lp = (Lq + 127) // 128 * 128
         lse = torch.empty(B, H, Lp, device=q.device, dtype=torch.float32)
-        call("moc_xattn_fwd", L.dtype_code(dtype), ptr(q), ptr(kt), ptr(vtt), plan.max_u * HK, ptr(plan.edge_u),
+        call("moc_xattn_fwd", L.dtype_code(dtype), ptr(q), ptr(kt), ptr(vt), plan.max_u * HK, ptr(plan.edge_u),
              ptr(om), B, Lq, H, HK, Dh, T, NS, float(Dh) ** -0.5, ptr(out), ptr(lse), stream_ptr(q.device))
-        ctx.save_for_backward(q, bank, wkv, om, out, lse, kt, vt, ktt, mean, rstd, plan.uniq, plan.n_uniq,
+        ctx.save_for_backward(q, bank, wkv, om, out, lse, kt, vt, mean, rstd, plan.uniq, plan.n_uniq,
                               plan.edge_u, plan.csr_off, plan.csr_edge)
         ctx.cfg = (num_chapters, T, norm, eps, HK, plan.max_u, wk.dtype, wv.dtype, bank_dtype)
         return out
 
     @staticmethod
     def backward(ctx, dout):
-        (q, bank, wkv, om, out, lse, kt, vt, ktt, mean, rstd, uniq, n_uniq, edge_u, csr_off,
+        (q, bank, wkv, om, out, lse, kt, vt, mean, rstd, uniq, n_uniq, edge_u, csr_off,
          csr_edge) = ctx.saved_tensors
         C, T, norm, eps, HK, max_u, wk_dtype, wv_dtype, bank_dtype = ctx.cfg
         dtype = q.dtype
@@ -478,7 +478,7 @@ class _RoutedAttention(torch.autograd.Function):
         dot = torch.empty_like(qt)
         call("moc_xattn_bwd_prep", dt, ptr(q), ptr(out), ptr(dout), B, Lq, H, Dh, ptr(delta), ptr(qt), ptr(dot), st)
         dq = torch.empty_like(q)
-        call("moc_xattn_bwd_dq", dt, ptr(q), ptr(kt), ptr(ktt), ptr(vt), kt.shape[0] * HK, ptr(edge_u), ptr(om),
+        call("moc_xattn_bwd_dq", dt, ptr(q), ptr(kt), ptr(vt), kt.shape[0] * HK, ptr(edge_u), ptr(om),
              ptr(dout), ptr(lse), ptr(delta), B, Lq, H, HK, Dh, T, NS, scale, ptr(dq), st)
         dkv_edge = torch.empty(B * NS * T, 2 * KV, device=dev, dtype=dtype)
         dom_part = torch.empty(B * NS, HK, device=dev, dtype=torch.float32)   # every entry written
