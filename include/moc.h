@@ -227,6 +227,12 @@ int moc_bank_scatter(int dx_dtype, const void* dX, const void* bank, int bank_dt
                      const int32_t* csr_edge, const float* row_mean, const float* row_rstd, int norm,
                      void* grad_bank, hipStream_t stream);
 
+/* Zero fill of `bytes` (multiple of 16, 16-byte aligned address) by `workgroups` one-wave
+ * workgroups: the zeros of the dense bank gradient (autograd's zero-initialised result of the
+ * gather, memory_bank.py:287-291, before moc_bank_scatter stores the selected rows), sized to
+ * run beside the attention backward on a second stream rather than as a full-chip fill. */
+int moc_fill_zero(void* dst, int64_t bytes, int workgroups, hipStream_t stream);
+
 /* Row-sparse bank gradient (no counterpart in the reference, whose bank gradient is the dense
  * autograd result of the gather, memory_bank.py:287-291): the same rows as moc_bank_scatter,
  * accumulated in f32 grad_acc [N_m][d] for the chapters of the current `epoch`.  chap_epoch

@@ -70,6 +70,7 @@ _SIGS = {
     "moc_decode_partial": (_I, [_I, _P, _I64, _I, _P, _P, _I, _I, _I, _P, _P, _P, _P, _I64, _P, _I, _F, _P, _P, _P]),
     "moc_gather_rows": (_I, [_I, _P, _I, _I64, _I, _P, _P, _I64, _P, _P, _P, _P]),
     "moc_bank_scatter": (_I, [_I, _P, _P, _I, _I64, _I, _P, _P, _I64, _P, _P, _P, _P, _I, _P, _P]),
+    "moc_fill_zero": (_I, [_P, _I64, _I, _P]),
     "moc_bank_grad_accumulate": (_I, [_I, _P, _P, _I, _I64, _I, _P, _P, _I64, _P, _P, _P, _P, _I, _I, _P, _P, _P,
                                       _P]),
     "moc_bank_chunk_count": (_I, [_I64]),

@@ -671,6 +671,23 @@ __global__ __launch_bounds__(256) void bank_grad_mark_kernel(const int32_t* __re
   chap_epoch[c] = epoch;
 }
 
+// Zero fill of the dense bank gradient by a few single-wave workgroups (one per CU by
+// default), 4 x 16 bytes per lane per iteration.  Launched on a second stream at the start
+// of the backward, its waves sit beside the attention-backward waves (16 VGPRs, no LDS)
+// and use HBM bandwidth those MFMA / VALU-bound kernels leave idle.
+__global__ __launch_bounds__(64) void fill_zero_kernel(V16* __restrict__ dst, int64_t n16) {
+  const V16 z{{0u, 0u, 0u, 0u}};
+  const int64_t stride = (int64_t)gridDim.x * 64;
+  int64_t i = (int64_t)blockIdx.x * 64 + threadIdx.x;
+  for (; i + 3 * stride < n16; i += 4 * stride) {
+    dst[i] = z;
+    dst[i + stride] = z;
+    dst[i + 2 * stride] = z;
+    dst[i + 3 * stride] = z;
+  }
+  for (; i < n16; i += stride) dst[i] = z;
+}
+
 }  // namespace moc
 
 using namespace moc;
@@ -815,6 +832,16 @@ int moc_bank_scatter(int dx_dtype, const void* dX, const void* bank, int bank_dt
   else return set_error(MOC_ERR_UNSUPPORTED, "moc_bank_scatter: dtypes %d/%d", dx_dtype, bank_dtype);
 #undef BS
   return check_launch("bank_scatter_kernel");
+}
+
+int moc_fill_zero(void* dst, int64_t bytes, int workgroups, hipStream_t stream) {
+  MOC_REQUIRE(dst || bytes == 0, MOC_ERR_ARG, "moc_fill_zero: null pointer");
+  MOC_REQUIRE(bytes >= 0 && bytes % 16 == 0 && ((uintptr_t)dst & 15) == 0, MOC_ERR_ARG,
+              "moc_fill_zero: bytes=%lld and the address must be multiples of 16", (long long)bytes);
+  MOC_REQUIRE(workgroups > 0 && workgroups <= 65536, MOC_ERR_ARG, "moc_fill_zero: workgroups=%d", workgroups);
+  if (bytes == 0) return MOC_OK;
+  hipLaunchKernelGGL(fill_zero_kernel, dim3((unsigned)workgroups), dim3(64), 0, stream, (V16*)dst, bytes / 16);
+  return check_launch("fill_zero_kernel");
 }
 
 int moc_bank_grad_accumulate(int dx_dtype, const void* dX, const void* bank, int bank_dtype, int64_t d, int T,

@@ -477,6 +477,10 @@ class _RoutedAttention(torch.autograd.Function):
         qt = torch.empty(B, H, Dh, Lp, device=dev, dtype=dtype)
         dot = torch.empty_like(qt)
         call("moc_xattn_bwd_prep", dt, ptr(q), ptr(out), ptr(dout), B, Lq, H, Dh, ptr(delta), ptr(qt), ptr(dot), st)
+        # the dense bank gradient's zeros are written beside the dQ and dK/dV kernels
+        dbank_zero = None
+        if dtype == torch.bfloat16 and ctx.needs_input_grad[1] and ctx.row_grad is None:
+            dbank_zero = zeros_beside(bank.shape, bank.dtype, dev)
         dq = torch.empty_like(q)
         call("moc_xattn_bwd_dq", dt, ptr(q), ptr(kt), ptr(vt), kt.shape[0] * HK, ptr(edge_u), ptr(om),
              ptr(dout), ptr(lse), ptr(delta), B, Lq, H, HK, Dh, T, NS, scale, ptr(dq), st)
@@ -507,7 +511,9 @@ class _RoutedAttention(torch.autograd.Function):
                 if ctx.row_grad is not None:
                     ctx.row_grad.accumulate(dX, bank, uniq, n_uniq, max_u, csr_off, csr_edge, mean, rstd, norm)
                 else:
-                    dbank = torch.zeros(bank.shape, device=dev, dtype=bank.dtype)
+                    dbank, filled = dbank_zero
+                    if filled is not None:
+                        torch.cuda.current_stream(dev).wait_event(filled)
                     call("moc_bank_scatter", L.dtype_code(dX.dtype), ptr(dX), ptr(bank), L.dtype_code(bank.dtype),
                          d, T, ptr(uniq), ptr(n_uniq), max_u, ptr(csr_off), ptr(csr_edge), ptr(mean), ptr(rstd),
                          norm, ptr(dbank), st)
@@ -534,6 +540,41 @@ class _RoutedAttention(torch.autograd.Function):
                      T, ptr(uniq), ptr(n_uniq), max_u, None, None, ptr(mean), ptr(rstd), norm, ptr(dbank), st)
                 dbank = dbank.to(bank_dtype)
         return dq, dbank, dwk, dwv, domega, None, None, None, None, None, None
+
+
+_SIDE_STREAMS: dict = {}
+
+
+def _side_stream(dev: torch.device) -> torch.cuda.Stream:
+    """A second stream (default priority) per device for work that runs beside the main
+    sequence of kernels."""
+    key = (dev.type, dev.index)
+    s = _SIDE_STREAMS.get(key)
+    if s is None:
+        s = _SIDE_STREAMS[key] = torch.cuda.Stream(device=dev)
+    return s
+
+
+def zeros_beside(shape, dtype: torch.dtype, dev: torch.device, workgroups: Optional[int] = None):
+    """A zero-filled tensor whose fill (moc_fill_zero, one single-wave workgroup per CU) runs
+    on a side stream, so that it overlaps the compute-bound kernels queued next on the
+    current stream.  Returns (tensor, event); the current stream must wait on the event
+    before it touches the tensor (event None: filled in order on the current stream)."""
+    t = torch.empty(shape, device=dev, dtype=dtype)
+    nbytes = t.numel() * t.element_size()
+    if nbytes % 16 or t.data_ptr() % 16:
+        t.zero_()
+        return t, None
+    main = torch.cuda.current_stream(dev)
+    side = _side_stream(dev)
+    side.wait_stream(main)
+    if workgroups is None:
+        workgroups = torch.cuda.get_device_properties(dev).multi_processor_count
+    call("moc_fill_zero", ptr(t), nbytes, int(workgroups), side.cuda_stream)
+    t.record_stream(side)
+    ev = torch.cuda.Event()
+    ev.record(side)
+    return t, ev
 
 
 def routed_attention(q, bank, wk, wv, omega, idx_star, *, num_chapters: int, tokens_per_chapter: int,

@@ -216,3 +216,20 @@ def test_kv_weight_grad_per_edge(gpu_device, bank_dtype, norm):
         ref += dkv.view(E, T, KV2)[e].double().T @ X.to(torch.bfloat16).double()
     assert torch.isfinite(dw).all()
     assert_rel(dw, ref, 2e-2, "dW per edge")
+
+
+@pytest.mark.parametrize("shape,dtype", [((4097, 768), torch.bfloat16), ((3, 5), torch.bfloat16),
+                                         ((1000, 24), torch.float32), ((0, 8), torch.bfloat16)])
+def test_zeros_beside(gpu_device, shape, dtype):
+    """The side-stream zero fill of the dense bank gradient: every element zero once the
+    current stream has waited on the returned event (sizes that are not a multiple of 16
+    bytes take the in-order fill)."""
+    print(f"zeros_beside {shape} {dtype}", flush=True)
+    from memory_amd import ops
+    junk = torch.full(shape, 7.0, device=gpu_device, dtype=dtype)
+    del junk   # the caching allocator hands the same block out again
+    t, ev = ops.zeros_beside(shape, dtype, gpu_device)
+    if ev is not None:
+        torch.cuda.current_stream(gpu_device).wait_event(ev)
+    assert t.shape == shape and t.dtype == dtype
+    assert torch.count_nonzero(t).item() == 0
