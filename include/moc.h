@@ -150,12 +150,16 @@ int moc_kv_project(int dtype, const void* bank, int bank_dtype, int64_t d, int T
 /* Replaces MemoryCrossAttention._attention on omega-weighted gathered memory
  * (memory_transformer/model.py:689-692 + memory_attention.py:458-478, :269-318) for the
  * sequence-level path: one joint softmax over the NS selected chapters of each sequence,
- * with omega scaling both logits and values.  q [B, L, H, Dh]; k_tiles and v_tiles [n_tiles][T][Dh]
- * from moc_kv_project, n_tiles = max_u * HK tiles each (< 4 GiB per buffer); slot_u i32 [B, NS] (the plan's edge_u); omega f32 [B, NS]; out [B, L, H, Dh];
+ * with omega scaling both logits and values.  q [B, L, H, Dh].  K / V of the plan's chapters:
+ * element (t, dh) of (chapter slot u, kv head hk) at k + u*su + hk*sh + t*st + dh (and the same
+ * offsets from v), each base readable for kv_span elements (< 4 GiB; strides in elements,
+ * 16-byte multiples, st >= 64): the chapter-head tiles of moc_kv_project are (HK*T*Dh, T*Dh, Dh);
+ * projection rows [max_u*T][2*HK*Dh] (K columns, then V) are (T*2*HK*Dh, Dh, 2*HK*Dh) with
+ * v = k + HK*Dh.  slot_u i32 [B, NS] (the plan's edge_u); omega f32 [B, NS]; out [B, L, H, Dh];
  * lse f32 [B, H, round_up(L, 128)] (log2 domain, +inf in the padding; consumed by the backward).
  * Dh == 64, T == 64. */
-int moc_xattn_fwd(int dtype, const void* q, const void* k_tiles, const void* v_tiles, int64_t n_tiles,
-                  const int32_t* slot_u, const float* omega, int64_t B, int64_t L, int H, int HK, int Dh, int T,
+int moc_xattn_fwd(int dtype, const void* q, const void* k_tiles, const void* v_tiles, int64_t kv_span, int64_t su,
+                  int sh, int st, const int32_t* slot_u, const float* omega, int64_t B, int64_t L, int H, int HK, int Dh, int T,
                   int NS, float scale, void* out, float* lse, hipStream_t stream);
 
 /* ------------------------------------------------ routed attention backward */
@@ -167,9 +171,9 @@ int moc_xattn_fwd(int dtype, const void* q, const void* k_tiles, const void* v_t
  * transposed per (sequence, head), zero-padded. */
 int moc_xattn_bwd_prep(int dtype, const void* q, const void* out, const void* dout, int64_t B, int64_t L, int H,
                        int Dh, float* delta, void* qt, void* dot, hipStream_t stream);
-/* dq [B, L, H, Dh] (dtype) from the K and V tiles of moc_xattn_fwd. */
-int moc_xattn_bwd_dq(int dtype, const void* q, const void* k_tiles, const void* v_tiles,
-                     int64_t n_tiles, const int32_t* slot_u, const float* omega, const void* dout, const float* lse,
+/* dq [B, L, H, Dh] (dtype); K / V as for moc_xattn_fwd. */
+int moc_xattn_bwd_dq(int dtype, const void* q, const void* k_tiles, const void* v_tiles, int64_t kv_span,
+                     int64_t su, int sh, int st, const int32_t* slot_u, const float* omega, const void* dout, const float* lse,
                      const float* delta, int64_t B, int64_t L, int H, int HK, int Dh, int T, int NS, float scale,
                      void* dq, hipStream_t stream);
 /* dK/dV per edge (edge e = b * NS + slot): dkv_edge [B * NS * T][2 * HK * Dh] (dtype) holds for
@@ -178,7 +182,8 @@ int moc_xattn_bwd_dq(int dtype, const void* q, const void* k_tiles, const void* 
  * Rows of skipped slots are not written.  domega_part f32 [B * NS][HK]: per (edge, kv head)
  * parts of dL/domega (caller sums over HK; skipped edges get 0). */
 int moc_xattn_bwd_dkv(int dtype, const void* q, const void* qt, const void* dout, const void* dot,
-                      const void* k_tiles, const void* v_tiles, const int32_t* slot_u, const float* omega,
+                      const void* k_tiles, const void* v_tiles, int64_t kv_span, int64_t su, int sh, int st,
+                      const int32_t* slot_u, const float* omega,
                       const float* lse, const float* delta, int64_t B, int64_t L, int H, int HK, int Dh, int T,
                       int NS, float scale, void* dkv_edge, float* domega_part, hipStream_t stream);
 /* Sums the per-edge rows per distinct chapter following the plan's inverted index (the

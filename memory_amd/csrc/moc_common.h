@@ -45,6 +45,19 @@ int check_launch(const char* what);
                               hipGetErrorString(_e));                  \
   } while (0)
 
+// Host check of a K / V block layout of the attention entry points: element (t, dh) of
+// block (chapter slot u, kv head hk) at base + u * su + hk * sh + t * st + dh, each base
+// readable for kv_span elements (bounded buffer loads).
+inline int check_kv_layout(const char* who, int dtype, int64_t kv_span, int64_t su, int64_t sh, int64_t st) {
+  const int64_t es = dtype == MOC_F32 ? 4 : 2;
+  MOC_REQUIRE(kv_span > 0 && kv_span * es < ((int64_t)1 << 32), MOC_ERR_UNSUPPORTED,
+              "%s: K / V buffers must be < 4 GiB (kv_span=%lld)", who, (long long)kv_span);
+  MOC_REQUIRE(st >= 64 && sh >= 0 && su >= 0 && (st * es) % 16 == 0 && (sh * es) % 16 == 0 && (su * es) % 16 == 0,
+              MOC_ERR_ARG, "%s: K / V strides (%lld, %lld, %lld) must be 16-byte multiples, row stride >= 64", who,
+              (long long)su, (long long)sh, (long long)st);
+  return MOC_OK;
+}
+
 // ------------------------------------------------------------ element helpers
 template <typename T> struct Frag;
 template <> struct Frag<bf16> { typedef bf16x8 type; };
@@ -262,6 +275,14 @@ struct TileIO {
   __device__ __forceinline__ void load(const Buf& b, uint32_t tile_off, int tid) {
 #pragma unroll
     for (int i = 0; i < NCHUNK; ++i) r[i] = b.load16((uint32_t)(tid + NT * i) * 16u, tile_off);
+  }
+  // 64 rows of 64 elements, row r at byte offset blk_off + r * row_bytes of buffer `b`
+  __device__ __forceinline__ void load_rows(const Buf& b, uint32_t blk_off, uint32_t row_bytes, int tid) {
+#pragma unroll
+    for (int i = 0; i < NCHUNK; ++i) {
+      const uint32_t q = (uint32_t)(tid + NT * i);
+      r[i] = b.load16((q / CPR) * row_bytes + (q % CPR) * 16u, blk_off);
+    }
   }
   __device__ __forceinline__ void store(char* dst, int tid) const {
 #pragma unroll

@@ -82,7 +82,8 @@ __global__ __launch_bounds__(kBThreads) void xattn_bwd_dq_kernel(
     const T* __restrict__ q, const T* __restrict__ ktiles, const T* __restrict__ vtiles,
     const int32_t* __restrict__ slot_u, const float* __restrict__ omega,
     const T* __restrict__ dout, const float* __restrict__ lse, const float* __restrict__ delta, int B, int L, int H,
-    int HK, int NS, int64_t n_tiles, float scale_log2, float scale, T* __restrict__ dq) {
+    int HK, int NS, int64_t kv_span, int64_t kv_su, int kv_sh, int kv_st, float scale_log2, float scale,
+    T* __restrict__ dq) {
   typedef typename Frag<T>::type F8;
   using Tile = SwzTile<T, 64>;
   constexpr int TB = kBT * kBDh * (int)sizeof(T);
@@ -126,13 +127,14 @@ __global__ __launch_bounds__(kBThreads) void xattn_bwd_dq_kernel(
   const int32_t* su = slot_u + (size_t)b * NS;
   const float* om = omega + (size_t)b * NS;
   TileIO<T, kBThreads> kio, vio;
-  const uint32_t nbytes = (uint32_t)(n_tiles * TB);
+  const uint32_t nbytes = (uint32_t)(kv_span * (int64_t)sizeof(T));
+  const uint32_t row_bytes = (uint32_t)(kv_st * (int)sizeof(T));
   const Buf kb(ktiles, nbytes), vb(vtiles, nbytes);
-  auto tile_off = [&](int u) { return (uint32_t)(((size_t)u * HK + hk) * TB); };
+  auto tile_off = [&](int u) { return (uint32_t)(((size_t)u * kv_su + (size_t)hk * kv_sh) * sizeof(T)); };
   int u_cur = su[0];
   if (u_cur >= 0) {
-    kio.load(kb, tile_off(u_cur), tid);
-    vio.load(vb, tile_off(u_cur), tid);
+    kio.load_rows(kb, tile_off(u_cur), row_bytes, tid);
+    vio.load_rows(vb, tile_off(u_cur), row_bytes, tid);
     kio.store(sK[0], tid);
     vio.store(sV[0], tid);
   }
@@ -142,8 +144,8 @@ __global__ __launch_bounds__(kBThreads) void xattn_bwd_dq_kernel(
     const int buf = s & 1;
     const int u_next = (s + 1 < NS) ? su[s + 1] : -1;
     if (u_next >= 0) {
-      kio.load(kb, tile_off(u_next), tid);
-      vio.load(vb, tile_off(u_next), tid);
+      kio.load_rows(kb, tile_off(u_next), row_bytes, tid);
+      vio.load_rows(vb, tile_off(u_next), row_bytes, tid);
     }
     if (u_cur >= 0) {
       const char* sKc = sK[buf];
@@ -251,8 +253,8 @@ __global__ __launch_bounds__(64 * kDkvWavesPerChapter * DkvCfg<T>::CPW) void xat
     const T* __restrict__ q, const T* __restrict__ qt, const T* __restrict__ dout, const T* __restrict__ dot,
     const T* __restrict__ ktiles, const T* __restrict__ vtiles, const int32_t* __restrict__ slot_u,
     const float* __restrict__ omega, const float* __restrict__ lse, const float* __restrict__ delta, int B, int L,
-    int Lp, int H, int HK, int NS, float scale_log2, float scale, T* __restrict__ dkv_edge,
-    float* __restrict__ domega_part) {
+    int Lp, int H, int HK, int NS, int64_t kv_su, int kv_sh, int kv_st, float scale_log2, float scale,
+    T* __restrict__ dkv_edge, float* __restrict__ domega_part) {
   typedef typename Frag<T>::type F8;
   constexpr int CPW = DkvCfg<T>::CPW, QS = DkvCfg<T>::QS;
   constexpr int WPC = kDkvWavesPerChapter, NW = CPW * WPC, NT = 64 * NW;
@@ -288,14 +290,14 @@ __global__ __launch_bounds__(64 * kDkvWavesPerChapter * DkvCfg<T>::CPW) void xat
   // (key row k0 + 16 kb + c16, dims 32 ks + 8 g .. +7)
   F8 kreg[NKB][2], vreg[NKB][2];
   if (active) {
-    const T* kp = ktiles + ((size_t)u * HK + hk) * 4096;
-    const T* vp = vtiles + ((size_t)u * HK + hk) * 4096;
+    const T* kp = ktiles + (size_t)u * kv_su + (size_t)hk * kv_sh;
+    const T* vp = vtiles + (size_t)u * kv_su + (size_t)hk * kv_sh;
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
-        kreg[kb][ks] = Load8<T, T>::run(kp + (k0 + 16 * kb + c16) * 64 + 32 * ks + 8 * g);
-        vreg[kb][ks] = Load8<T, T>::run(vp + (k0 + 16 * kb + c16) * 64 + 32 * ks + 8 * g);
+        kreg[kb][ks] = Load8<T, T>::run(kp + (size_t)(k0 + 16 * kb + c16) * kv_st + 32 * ks + 8 * g);
+        vreg[kb][ks] = Load8<T, T>::run(vp + (size_t)(k0 + 16 * kb + c16) * kv_st + 32 * ks + 8 * g);
       }
   }
   const float w = active ? omega[e] : 0.f;
@@ -441,15 +443,15 @@ __global__ __launch_bounds__(64 * kDkvWavesPerChapter * DkvCfg<T>::CPW) void xat
   // heads of hk and, in a fixed order, over the chapter's two key halves
   float dom = 0.f;
   if (active) {
-    const T* kp = ktiles + ((size_t)u * HK + hk) * 4096;
-    const T* vp = vtiles + ((size_t)u * HK + hk) * 4096;
+    const T* kp = ktiles + (size_t)u * kv_su + (size_t)hk * kv_sh;
+    const T* vp = vtiles + (size_t)u * kv_su + (size_t)hk * kv_sh;
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
       for (int db = 0; db < 4; ++db)
 #pragma unroll
         for (int x = 0; x < 4; ++x) {
-          const int off = (k0 + 16 * kb + 4 * g + x) * 64 + 16 * db + c16;
+          const size_t off = (size_t)(k0 + 16 * kb + 4 * g + x) * kv_st + 16 * db + c16;
           dom += dk[kb][db][x] * to_f(kp[off]) + dv[kb][db][x] * to_f(vp[off]);
         }
     dom = wave_sum(dom);
@@ -713,16 +715,15 @@ int moc_xattn_bwd_prep(int dtype, const void* q, const void* out, const void* do
   return check_launch("xattn_bwd_prep_kernel");
 }
 
-int moc_xattn_bwd_dq(int dtype, const void* q, const void* k_tiles, const void* v_tiles,
-                     int64_t n_tiles, const int32_t* slot_u, const float* omega, const void* dout, const float* lse,
+int moc_xattn_bwd_dq(int dtype, const void* q, const void* k_tiles, const void* v_tiles, int64_t kv_span,
+                     int64_t su, int sh, int st, const int32_t* slot_u, const float* omega, const void* dout, const float* lse,
                      const float* delta, int64_t B, int64_t L, int H, int HK, int Dh, int T, int NS, float scale,
                      void* dq, hipStream_t stream) {
   MOC_REQUIRE(q && k_tiles && v_tiles && slot_u && omega && dout && lse && delta && dq, MOC_ERR_ARG,
               "moc_xattn_bwd_dq: null pointer");
   MOC_REQUIRE(Dh == kBDh && T == kBT, MOC_ERR_UNSUPPORTED, "moc_xattn_bwd_dq: needs head_dim 64 and T 64");
   MOC_REQUIRE(H > 0 && HK > 0 && H % HK == 0 && NS > 0, MOC_ERR_ARG, "moc_xattn_bwd_dq: bad shape");
-  MOC_REQUIRE(n_tiles > 0 && n_tiles * 64 * 64 * (dtype == MOC_F32 ? 4 : 2) < ((int64_t)1 << 32), MOC_ERR_UNSUPPORTED,
-              "moc_xattn_bwd_dq: tile buffers must be < 4 GiB (n_tiles=%lld)", (long long)n_tiles);
+  if (int rc = check_kv_layout("moc_xattn_bwd_dq", dtype, kv_span, su, sh, st)) return rc;
   if (B == 0 || L == 0) return MOC_OK;
   MOC_REQUIRE(B * H * ((L + 127) / 128) < ((int64_t)1 << 31), MOC_ERR_UNSUPPORTED, "moc_xattn_bwd_dq: grid too large");
   dim3 grid(xcd_grid(B * H * ((L + 127) / 128)));
@@ -730,18 +731,19 @@ int moc_xattn_bwd_dq(int dtype, const void* q, const void* k_tiles, const void* 
   if (dtype == MOC_BF16)
     hipLaunchKernelGGL(xattn_bwd_dq_kernel<bf16>, grid, dim3(kBThreads), 0, stream, (const bf16*)q, (const bf16*)k_tiles,
                        (const bf16*)v_tiles, slot_u, omega, (const bf16*)dout, lse, delta, (int)B, (int)L, H, HK, NS,
-                       n_tiles, sl2, scale, (bf16*)dq);
+                       kv_span, su, sh, st, sl2, scale, (bf16*)dq);
   else if (dtype == MOC_F32)
     hipLaunchKernelGGL(xattn_bwd_dq_kernel<float>, grid, dim3(kBThreads), 0, stream, (const float*)q,
                        (const float*)k_tiles, (const float*)v_tiles, slot_u, omega, (const float*)dout, lse, delta,
-                       (int)B, (int)L, H, HK, NS, n_tiles, sl2, scale, (float*)dq);
+                       (int)B, (int)L, H, HK, NS, kv_span, su, sh, st, sl2, scale, (float*)dq);
   else
     return set_error(MOC_ERR_UNSUPPORTED, "moc_xattn_bwd_dq: dtype %d", dtype);
   return check_launch("xattn_bwd_dq_kernel");
 }
 
 int moc_xattn_bwd_dkv(int dtype, const void* q, const void* qt, const void* dout, const void* dot,
-                      const void* k_tiles, const void* v_tiles, const int32_t* slot_u, const float* omega,
+                      const void* k_tiles, const void* v_tiles, int64_t kv_span, int64_t su, int sh, int st,
+                      const int32_t* slot_u, const float* omega,
                       const float* lse, const float* delta, int64_t B, int64_t L, int H, int HK, int Dh, int T,
                       int NS, float scale, void* dkv_edge, float* domega_part, hipStream_t stream) {
   MOC_REQUIRE(q && qt && dout && dot && k_tiles && v_tiles && slot_u && omega && lse && delta && dkv_edge &&
@@ -752,6 +754,7 @@ int moc_xattn_bwd_dkv(int dtype, const void* q, const void* qt, const void* dout
               "moc_xattn_bwd_dkv: bad shape");
   MOC_REQUIRE(L * H * 64 * (dtype == MOC_F32 ? 4 : 2) < ((int64_t)1 << 32), MOC_ERR_UNSUPPORTED,
               "moc_xattn_bwd_dkv: one sequence's q / dout must be < 4 GiB (L=%lld, H=%d)", (long long)L, H);
+  if (int rc = check_kv_layout("moc_xattn_bwd_dkv", dtype, kv_span, su, sh, st)) return rc;
   if (B == 0 || L == 0) return MOC_OK;
   const int Lp = (int)((L + 127) / 128 * 128);
   const float sl2 = scale * 1.4426950408889634f;
@@ -760,14 +763,15 @@ int moc_xattn_bwd_dkv(int dtype, const void* q, const void* qt, const void* dout
     dim3 grid(xcd_grid(B * HK * ((NS + CPW - 1) / CPW)));
     hipLaunchKernelGGL(xattn_bwd_dkv_kernel<bf16>, grid, dim3(64 * kDkvWavesPerChapter * CPW), 0, stream, (const bf16*)q, (const bf16*)qt,
                        (const bf16*)dout, (const bf16*)dot, (const bf16*)k_tiles, (const bf16*)v_tiles, slot_u,
-                       omega, lse, delta, (int)B, (int)L, Lp, H, HK, NS, sl2, scale, (bf16*)dkv_edge, domega_part);
+                       omega, lse, delta, (int)B, (int)L, Lp, H, HK, NS, su, sh, st, sl2, scale, (bf16*)dkv_edge,
+                       domega_part);
   } else if (dtype == MOC_F32) {
     constexpr int CPW = DkvCfg<float>::CPW;
     dim3 grid(xcd_grid(B * HK * ((NS + CPW - 1) / CPW)));
     hipLaunchKernelGGL(xattn_bwd_dkv_kernel<float>, grid, dim3(64 * kDkvWavesPerChapter * CPW), 0, stream, (const float*)q,
                        (const float*)qt, (const float*)dout, (const float*)dot, (const float*)k_tiles,
-                       (const float*)v_tiles, slot_u, omega, lse, delta, (int)B, (int)L, Lp, H, HK, NS, sl2, scale,
-                       (float*)dkv_edge, domega_part);
+                       (const float*)v_tiles, slot_u, omega, lse, delta, (int)B, (int)L, Lp, H, HK, NS, su, sh, st, sl2,
+                       scale, (float*)dkv_edge, domega_part);
   } else {
     return set_error(MOC_ERR_UNSUPPORTED, "moc_xattn_bwd_dkv: dtype %d", dtype);
   }

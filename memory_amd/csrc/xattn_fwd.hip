@@ -40,7 +40,7 @@ template <typename T>
 __global__ __launch_bounds__(kFwdThreads) void xattn_fwd_kernel(
     const T* __restrict__ q, const T* __restrict__ ktiles, const T* __restrict__ vtiles,
     const int32_t* __restrict__ slot_u, const float* __restrict__ omega, int B, int L, int H, int HK, int NS,
-    int64_t n_tiles, float scale_log2, T* __restrict__ out, float* __restrict__ lse) {
+    int64_t kv_span, int64_t kv_su, int kv_sh, int kv_st, float scale_log2, T* __restrict__ out, float* __restrict__ lse) {
   typedef typename Frag<T>::type F8;
   using Tile = SwzTile<T, 64>;
   constexpr int TB = kTch * kDh * (int)sizeof(T);
@@ -88,14 +88,16 @@ __global__ __launch_bounds__(kFwdThreads) void xattn_fwd_kernel(
   const int32_t* su = slot_u + (size_t)b * NS;
   const float* om = omega + (size_t)b * NS;
   TileIO<T, kFwdThreads> kio, vio;
-  // tiles are addressed as byte offsets into two buffers (n_tiles * TB bytes each)
-  const Buf kb(ktiles, (uint32_t)(n_tiles * TB)), vb(vtiles, (uint32_t)(n_tiles * TB));
-  auto tile_off = [&](int u) { return (uint32_t)(((size_t)u * HK + hk) * TB); };
+  // block (u, hk) of K / V: element (t, dh) at u kv_su + hk kv_sh + t kv_st + dh of two buffers of
+  // kv_span elements each
+  const Buf kb(ktiles, (uint32_t)(kv_span * (int64_t)sizeof(T))), vb(vtiles, (uint32_t)(kv_span * (int64_t)sizeof(T)));
+  auto tile_off = [&](int u) { return (uint32_t)(((size_t)u * kv_su + (size_t)hk * kv_sh) * sizeof(T)); };
+  const uint32_t row_bytes = (uint32_t)(kv_st * (int)sizeof(T));
 
   int u_cur = su[0];
   if (u_cur >= 0) {
-    kio.load(kb, tile_off(u_cur), tid);
-    vio.load(vb, tile_off(u_cur), tid);
+    kio.load_rows(kb, tile_off(u_cur), row_bytes, tid);
+    vio.load_rows(vb, tile_off(u_cur), row_bytes, tid);
     kio.store(sK[0], tid);
     vio.store(sV[0], tid);
   }
@@ -109,8 +111,8 @@ __global__ __launch_bounds__(kFwdThreads) void xattn_fwd_kernel(
     const int buf = s & 1;
     const int u_next = (s + 1 < NS) ? su[s + 1] : -1;
     if (u_next >= 0) {
-      kio.load(kb, tile_off(u_next), tid);
-      vio.load(vb, tile_off(u_next), tid);
+      kio.load_rows(kb, tile_off(u_next), row_bytes, tid);
+      vio.load_rows(vb, tile_off(u_next), row_bytes, tid);
     }
     if (u_cur >= 0) {
       const float w = om[s];
@@ -226,28 +228,26 @@ using namespace moc;
 
 extern "C" {
 
-int moc_xattn_fwd(int dtype, const void* q, const void* k_tiles, const void* v_tiles, int64_t n_tiles,
-                  const int32_t* slot_u, const float* omega, int64_t B, int64_t L, int H, int HK, int Dh, int T,
+int moc_xattn_fwd(int dtype, const void* q, const void* k_tiles, const void* v_tiles, int64_t kv_span, int64_t su,
+                  int sh, int st, const int32_t* slot_u, const float* omega, int64_t B, int64_t L, int H, int HK, int Dh, int T,
                   int NS, float scale, void* out, float* lse, hipStream_t stream) {
   MOC_REQUIRE(q && k_tiles && v_tiles && slot_u && omega && out && lse, MOC_ERR_ARG, "moc_xattn_fwd: null pointer");
   MOC_REQUIRE(Dh == kDh && T == kTch, MOC_ERR_UNSUPPORTED, "moc_xattn_fwd: needs head_dim 64 and 64 tokens per chapter (got %d, %d)", Dh, T);
   MOC_REQUIRE(H > 0 && HK > 0 && H % HK == 0, MOC_ERR_ARG, "moc_xattn_fwd: H=%d HK=%d", H, HK);
   MOC_REQUIRE(NS > 0 && B >= 0 && L >= 0, MOC_ERR_ARG, "moc_xattn_fwd: bad shape");
   MOC_REQUIRE(B < 65536 && H < 65536, MOC_ERR_UNSUPPORTED, "moc_xattn_fwd: grid too large");
-  MOC_REQUIRE(n_tiles > 0 && n_tiles * 64 * 64 * (dtype == MOC_F32 ? 4 : 2) < ((int64_t)1 << 32), MOC_ERR_UNSUPPORTED,
-              "moc_xattn_fwd: tile buffers must be < 4 GiB (n_tiles=%lld)", (long long)n_tiles);
+  if (int rc = check_kv_layout("moc_xattn_fwd", dtype, kv_span, su, sh, st)) return rc;
   if (B == 0 || L == 0) return MOC_OK;
   MOC_REQUIRE(B * H * ((L + 127) / 128) < ((int64_t)1 << 31), MOC_ERR_UNSUPPORTED, "moc_xattn_fwd: grid too large");
   dim3 grid(xcd_grid(B * H * ((L + 127) / 128)));
   const float sl2 = scale * 1.4426950408889634f;
   if (dtype == MOC_BF16)
     hipLaunchKernelGGL(xattn_fwd_kernel<bf16>, grid, dim3(kFwdThreads), 0, stream, (const bf16*)q, (const bf16*)k_tiles,
-                       (const bf16*)v_tiles, slot_u, omega, (int)B, (int)L, H, HK, NS, n_tiles, sl2, (bf16*)out, lse);
+                       (const bf16*)v_tiles, slot_u, omega, (int)B, (int)L, H, HK, NS, kv_span, su, sh, st, sl2, (bf16*)out, lse);
   else if (dtype == MOC_F32)
     hipLaunchKernelGGL(xattn_fwd_kernel<float>, grid, dim3(kFwdThreads), 0, stream, (const float*)q,
-                       (const float*)k_tiles, (const float*)v_tiles, slot_u, omega, (int)B, (int)L, H, HK, NS, n_tiles, sl2,
-                       (float*)out,
-                       lse);
+                       (const float*)k_tiles, (const float*)v_tiles, slot_u, omega, (int)B, (int)L, H, HK, NS, kv_span, su, sh, st,
+                       sl2, (float*)out, lse);
   else
     return set_error(MOC_ERR_UNSUPPORTED, "moc_xattn_fwd: dtype %d", dtype);
   return check_launch("xattn_fwd_kernel");

@@ -248,6 +248,14 @@ def kv_project(bank: torch.Tensor, plan: ChapterPlan, T: int, wkv: torch.Tensor,
     return tuple(out[n] for n in layouts)
 
 
+def kv_rows_layout(kv: torch.Tensor, T: int, HK: int, Dh: int):
+    """(kv_span, su, sh, st) of projection rows kv [max_u * T][2 * HK * Dh] (K columns, then V)
+    for the attention entry points: block (u, hk) row t at u*T*2KV + hk*Dh + t*2KV; the span
+    is what the V base (kv + HK*Dh) can still read."""
+    row = 2 * HK * Dh
+    return kv.numel() - HK * Dh, T * row, Dh, row
+
+
 # ------------------------------------------------------------- dense projections
 
 class _Linear(torch.autograd.Function):
@@ -445,21 +453,32 @@ class _RoutedAttention(torch.autograd.Function):
         if norm != L.MOC_NORM_NONE:
             mean, rstd = row_stats(bank, plan, T, norm, eps)
         wkv = torch.cat([wk, wv], 0).to(dtype).contiguous()
-        kt, vt = kv_project(bank, plan, T, wkv, HK, Dh, mean, rstd, dtype, ("k", "v"))
+        # K / V of the plan's chapters as projection rows [max_u * T][K | V]: the (normalised)
+        # bank rows gathered once, then one library GEMM (faster at these shapes than the fused
+        # gather-projection kernel, which writes chapter-head tiles); the attention kernels
+        # read (chapter, kv head) blocks of it through strides
+        KV = HK * Dh
+        X = torch.empty(plan.max_u * T, bank.shape[1], device=q.device, dtype=dtype)
+        call("moc_gather_rows", L.dtype_code(dtype), ptr(bank), L.dtype_code(bank.dtype), bank.shape[1], T,
+             ptr(plan.uniq), ptr(plan.n_uniq), plan.max_u, ptr(mean), ptr(rstd), ptr(X), stream_ptr(q.device))
+        kv = F.linear(X, wkv)
+        del X
+        kvl = kv_rows_layout(kv, T, HK, Dh)
         om = omega.float().contiguous()
         out = torch.empty(B, Lq, H, Dh, device=q.device, dtype=dtype)
         Lp = (Lq + 127) // 128 * 128
         lse = torch.empty(B, H, Lp, device=q.device, dtype=torch.float32)
-        call("moc_xattn_fwd", L.dtype_code(dtype), ptr(q), ptr(kt), ptr(vt), plan.max_u * HK, ptr(plan.edge_u),
-             ptr(om), B, Lq, H, HK, Dh, T, NS, float(Dh) ** -0.5, ptr(out), ptr(lse), stream_ptr(q.device))
-        ctx.save_for_backward(q, bank, wkv, om, out, lse, kt, vt, mean, rstd, plan.uniq, plan.n_uniq,
+        call("moc_xattn_fwd", L.dtype_code(dtype), ptr(q), ptr(kv), ptr(kv) + KV * kv.element_size(), *kvl,
+             ptr(plan.edge_u), ptr(om), B, Lq, H, HK, Dh, T, NS, float(Dh) ** -0.5, ptr(out), ptr(lse),
+             stream_ptr(q.device))
+        ctx.save_for_backward(q, bank, wkv, om, out, lse, kv, mean, rstd, plan.uniq, plan.n_uniq,
                               plan.edge_u, plan.csr_off, plan.csr_edge)
         ctx.cfg = (num_chapters, T, norm, eps, HK, plan.max_u, wk.dtype, wv.dtype, bank_dtype)
         return out
 
     @staticmethod
     def backward(ctx, dout):
-        (q, bank, wkv, om, out, lse, kt, vt, mean, rstd, uniq, n_uniq, edge_u, csr_off,
+        (q, bank, wkv, om, out, lse, kv, mean, rstd, uniq, n_uniq, edge_u, csr_off,
          csr_edge) = ctx.saved_tensors
         C, T, norm, eps, HK, max_u, wk_dtype, wv_dtype, bank_dtype = ctx.cfg
         dtype = q.dtype
@@ -482,11 +501,13 @@ class _RoutedAttention(torch.autograd.Function):
         if dtype == torch.bfloat16 and ctx.needs_input_grad[1] and ctx.row_grad is None:
             dbank_zero = zeros_beside(bank.shape, bank.dtype, dev)
         dq = torch.empty_like(q)
-        call("moc_xattn_bwd_dq", dt, ptr(q), ptr(kt), ptr(vt), kt.shape[0] * HK, ptr(edge_u), ptr(om),
+        kvl = kv_rows_layout(kv, T, HK, Dh)
+        vptr = ptr(kv) + KV * kv.element_size()
+        call("moc_xattn_bwd_dq", dt, ptr(q), ptr(kv), vptr, *kvl, ptr(edge_u), ptr(om),
              ptr(dout), ptr(lse), ptr(delta), B, Lq, H, HK, Dh, T, NS, scale, ptr(dq), st)
         dkv_edge = torch.empty(B * NS * T, 2 * KV, device=dev, dtype=dtype)
         dom_part = torch.empty(B * NS, HK, device=dev, dtype=torch.float32)   # every entry written
-        call("moc_xattn_bwd_dkv", dt, ptr(q), ptr(qt), ptr(dout), ptr(dot), ptr(kt), ptr(vt), ptr(edge_u), ptr(om),
+        call("moc_xattn_bwd_dkv", dt, ptr(q), ptr(qt), ptr(dout), ptr(dot), ptr(kv), vptr, *kvl, ptr(edge_u), ptr(om),
              ptr(lse), ptr(delta), B, Lq, H, HK, Dh, T, NS, scale, ptr(dkv_edge), ptr(dom_part), st)
         domega = dom_part.sum(-1).view(B, NS)
         need_bank, need_wk, need_wv = ctx.needs_input_grad[1:4]

@@ -47,7 +47,11 @@ def test_host_validation_rejects_before_launch(libpath):
     with pytest.raises(ValueError, match="k=20"):
         _lib.call("moc_router_topk", 1, 4, 10, 1, 20, 1, 1, None, None)
     with pytest.raises(ValueError, match="head_dim 64"):
-        _lib.call("moc_xattn_fwd", _lib.MOC_BF16, 1, 1, 1, 4, 1, 1, 2, 8, 4, 4, 32, 64, 5, 0.1, 1, 1, None)
+        _lib.call("moc_xattn_fwd", _lib.MOC_BF16, 1, 1, 1, 4096, 4096, 4096, 64, 1, 1, 2, 8, 4, 4, 32, 64, 5, 0.1, 1,
+                  1, None)
+    with pytest.raises(ValueError, match="row stride >= 64"):
+        _lib.call("moc_xattn_fwd", _lib.MOC_BF16, 1, 1, 1, 4096, 4096, 4096, 32, 1, 1, 2, 8, 4, 4, 64, 64, 5, 0.1, 1,
+                  1, None)
     with pytest.raises(ValueError, match="multiple of 64"):
         _lib.call("moc_kv_project", _lib.MOC_BF16, 1, _lib.MOC_BF16, 100, 64, 1, 1, 4, None, None, 1, 4, 64, 1, 1,
                   None, None, None)
