@@ -440,9 +440,20 @@ template <typename TW>
 __global__ __launch_bounds__(256) void router_linear_kernel(const float* __restrict__ x, int64_t R, int64_t d,
                                                             const TW* __restrict__ W, const float* __restrict__ bias,
                                                             int64_t C, float* __restrict__ logits) {
-  extern __shared__ float xs[];  // [kLinRows][d]
+  extern __shared__ float xs[];  // [min(R, kLinRows)][d]
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int64_t c0 = (int64_t)blockIdx.x * kLinChapFwd + kLinCpw * wave;  // this wave's chapters
+  // the first kLinPre 256-column chunks of the wave's W rows are loaded before x is staged (the
+  // two load latencies overlap) and kept for every chunk of rows; wider rows stream the rest
+  constexpr int kLinPre = 4;
+  f32x4 wpre[kLinPre][kLinCpw];
+#pragma unroll
+  for (int i = 0; i < kLinPre; ++i)
+#pragma unroll
+    for (int q = 0; q < kLinCpw; ++q) {
+      const int64_t j = 4 * lane + 256 * i;
+      wpre[i][q] = (c0 + q < C && j < d) ? load4f(W + (c0 + q) * d + j) : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
   for (int64_t r0 = 0; r0 < R; r0 += kLinRows) {
     const int nr = (int)min((int64_t)kLinRows, R - r0);
     __syncthreads();
@@ -453,7 +464,23 @@ __global__ __launch_bounds__(256) void router_linear_kernel(const float* __restr
     for (int q = 0; q < kLinCpw; ++q)
 #pragma unroll
       for (int r = 0; r < kLinRows; ++r) acc[q][r] = 0.f;
-    for (int64_t j = 4 * lane; j < d; j += 256) {
+#pragma unroll
+    for (int i = 0; i < kLinPre; ++i) {
+      const int64_t j = 4 * lane + 256 * i;
+      if (j < d) {
+#pragma unroll
+        for (int r = 0; r < kLinRows; ++r) {
+          if (r < nr) {
+            const f32x4 xv = *reinterpret_cast<const f32x4*>(xs + r * d + j);
+#pragma unroll
+            for (int q = 0; q < kLinCpw; ++q)
+              acc[q][r] += xv[0] * wpre[i][q][0] + xv[1] * wpre[i][q][1] + xv[2] * wpre[i][q][2] +
+                           xv[3] * wpre[i][q][3];
+          }
+        }
+      }
+    }
+    for (int64_t j = 4 * lane + 256 * kLinPre; j < d; j += 256) {
       f32x4 wv[kLinCpw];
 #pragma unroll
       for (int q = 0; q < kLinCpw; ++q)
@@ -938,7 +965,8 @@ int moc_router_linear(const float* x, int64_t R, int64_t d, const void* W, int w
               (long long)d);
   if (R == 0) return MOC_OK;
   dim3 grid((unsigned)((C + kLinChapFwd - 1) / kLinChapFwd));
-  const size_t lds = (size_t)kLinRows * d * sizeof(float);
+  // only the rows of one chunk: small batches leave room for more resident workgroups
+  const size_t lds = (size_t)std::min<int64_t>(R, kLinRows) * d * sizeof(float);
   if (w_dtype == MOC_F32)
     hipLaunchKernelGGL(router_linear_kernel<float>, grid, dim3(256), lds, stream, x, R, d, (const float*)W, bias, C,
                        logits);
