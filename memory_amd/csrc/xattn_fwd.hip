@@ -7,8 +7,9 @@
 // which is exactly MemoryCrossAttention over the omega-weighted gathered rows
 // (memory_transformer/model.py:689-692 then memory_attention.py:458-478 /
 // :269-318): (omega x) W^T = omega (x W^T), so the key and the value of every
-// row of chapter c carry the factor omega_c.  k_j / v_j come from the
-// chapter-head tiles written by kv_project.hip; slot_u[b, c] says which
+// row of chapter c carry the factor omega_c.  k_j / v_j are read as (chapter, kv head)
+// blocks of 64 rows through strides (projection rows [u*64 + t][K | V] on the training
+// path, kv_project.hip's chapter-head tiles for the decode cache); slot_u[b, c] says which
 // de-duplicated chapter holds slot c of sequence b (negative = skip the slot).
 //
 // Work decomposition (Dh = T = 64): one workgroup = 128 queries of one
@@ -18,7 +19,7 @@
 // accumulates O^T = V^T P^T, whose accumulator layout is again "lane = one
 // query", so the online-softmax rescale needs no data movement, and takes the
 // row sums from an MFMA of an all-ones operand with the same P^T fragments.
-// K and V tiles (both [key][dim], as kv_project.hip writes them) are double-buffered in
+// K and V blocks (both [key][dim]) are double-buffered in
 // LDS; the V^T operand is read from the V tile with the transposing LDS read, whose lane
 // order is the key order of the P~^T fragments.
 #include "moc_common.h"
