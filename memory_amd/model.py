@@ -16,6 +16,8 @@ from __future__ import annotations
 
 from typing import Dict, Optional, Tuple
 
+import math
+
 import torch
 import torch.nn as nn
 import torch.nn.functional as F
@@ -94,6 +96,16 @@ class _SplitRows(torch.autograd.Function):
     def backward(ctx, ga, gb):
         n, shape = ctx.n, ctx.shape
         ref = ga if ga is not None else gb
+        # the token path writes its gradient into the tail of a whole-shape buffer
+        # (sparse_attention._rows_grad): fill the head rows of that buffer and return it
+        base = None if gb is None else gb._base
+        if base is not None and base.shape == shape and base.dtype == gb.dtype and base.is_contiguous() \
+                and gb.storage_offset() - base.storage_offset() == n * math.prod(shape[1:]):
+            if ga is None:
+                base[:n].zero_()
+            else:
+                base[:n].copy_(ga)
+            return base, None
         if ga is None:
             ga = ref.new_zeros((n,) + tuple(shape[1:]))
         if gb is None:

@@ -314,11 +314,29 @@ class _TokenRouted(torch.autograd.Function):
             dwk = dwkv[:KV].to(wk_dtype) if need_wk else None
             dwv = dwkv[KV:].to(wv_dtype) if need_wv else None
         if need_r:
-            dr = torch.matmul(dkv, wkv).to(routed.dtype)
+            dr = _rows_grad(routed, dkv, wkv)
         dw = None
         if w_shape is not None and dws:
             dw = dws[0].view(w_shape) if len(dws) == 1 else torch.stack(dws, 0).sum(0).view(w_shape)
         return dq, dr, dwk, dwv, dw, None, None, None
+
+
+def _rows_grad(routed: torch.Tensor, dkv: torch.Tensor, wkv: torch.Tensor) -> torch.Tensor:
+    """d routed = dkv [Wk; Wv].  When `routed` is the tail rows of a larger tensor (the routed
+    part of a bank whose first rows are the shared chapters, split off by model.split_rows),
+    the product is written into the tail of a buffer of the whole bank's shape, so the split's
+    backward can hand that buffer on after filling the head rows instead of copying the tail."""
+    base = routed._base
+    if base is not None and base.dim() == 2 and base.is_contiguous() and routed.is_contiguous() \
+            and base.shape[1] == routed.shape[1] and routed.dtype == dkv.dtype and base.dtype == routed.dtype:
+        off = routed.storage_offset() - base.storage_offset()
+        d = routed.shape[1]
+        if off % d == 0 and off // d + routed.shape[0] == base.shape[0]:
+            full = torch.empty(base.shape, device=dkv.device, dtype=dkv.dtype)
+            tail = full[off // d:]
+            torch.mm(dkv, wkv, out=tail)
+            return tail
+    return torch.matmul(dkv, wkv).to(routed.dtype)
 
 
 def token_routed_attention(q, routed_memory, wk, wv, idx, chapter_weights, *, tokens_per_chapter: int,
