@@ -167,8 +167,9 @@ int moc_xattn_fwd(int dtype, const void* q, const void* k_tiles, const void* v_t
 /* Backward of moc_xattn_fwd (autograd of memory_transformer/memory_attention.py:301-316 through
  * the omega weighting of model.py:689-692).  Rows of lse / delta / qt / dot have stride
  * Lp = round_up(L, 128) (moc_xattn_fwd writes lse that way, padded with +inf).
- * prep: delta f32 [B, H, Lp] = rowsum(dout * out); qt, dot [B, H, Dh, Lp] (dtype) = q and dout
- * transposed per (sequence, head), zero-padded. */
+ * prep: delta f32 [B, H, Lp] = rowsum(dout * out); optionally (both non-NULL) qt, dot
+ * [B, H, Dh, Lp] (dtype) = q and dout transposed per (sequence, head), zero-padded, query axis
+ * in MFMA key order (no entry point here needs them: moc_xattn_bwd_dkv reads q / dout). */
 int moc_xattn_bwd_prep(int dtype, const void* q, const void* out, const void* dout, int64_t B, int64_t L, int H,
                        int Dh, float* delta, void* qt, void* dot, hipStream_t stream);
 /* dq [B, L, H, Dh] (dtype); K / V as for moc_xattn_fwd. */
@@ -181,7 +182,7 @@ int moc_xattn_bwd_dq(int dtype, const void* q, const void* k_tiles, const void* 
  * dL/dk, dL/dv are gradients w.r.t. the unweighted projected keys/values (omega folded in).
  * Rows of skipped slots are not written.  domega_part f32 [B * NS][HK]: per (edge, kv head)
  * parts of dL/domega (caller sums over HK; skipped edges get 0). */
-int moc_xattn_bwd_dkv(int dtype, const void* q, const void* qt, const void* dout, const void* dot,
+int moc_xattn_bwd_dkv(int dtype, const void* q, const void* dout,
                       const void* k_tiles, const void* v_tiles, int64_t kv_span, int64_t su, int sh, int st,
                       const int32_t* slot_u, const float* omega,
                       const float* lse, const float* delta, int64_t B, int64_t L, int H, int HK, int Dh, int T,

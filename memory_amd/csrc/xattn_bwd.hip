@@ -28,8 +28,8 @@ constexpr int kBT = 64;
 //   delta[b, h, i] = dO_i . O_i
 //   qt[b, h, :, i] = Q[b, i, h, :]     dot[b, h, :, i] = dO[b, i, h, :]
 // Rows of delta / qt / dot have stride Lp = round_up(L, 128); padded entries are 0.
-// The transposed copies give the dK/dV kernel its query-major MFMA operands as
-// plain 8-byte loads.
+// qt / dot are optional (null: delta only); the dK/dV kernel reads its query-major
+// operands transposed from the staged Q / dO tiles instead.
 template <typename T>
 __global__ __launch_bounds__(256) void xattn_bwd_prep_kernel(const T* __restrict__ q, const T* __restrict__ out,
                                                              const T* __restrict__ dout, int L, int Lp, int H,
@@ -39,7 +39,8 @@ __global__ __launch_bounds__(256) void xattn_bwd_prep_kernel(const T* __restrict
   __shared__ T td[64][66];
   const int q0 = blockIdx.x * 64, h = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x;
-  for (int i = tid; i < 64 * 64; i += 256) {
+  const bool tr = qt != nullptr;
+  for (int i = tid; tr && i < 64 * 64; i += 256) {
     const int qq = i >> 6, dd = i & 63;
     const int qi = q0 + qq;
     T vq = from_f<T>(0.f), vd = from_f<T>(0.f);
@@ -66,6 +67,7 @@ __global__ __launch_bounds__(256) void xattn_bwd_prep_kernel(const T* __restrict
     acc += __shfl_xor(acc, 2, 4);
     if (part == 0) delta[((size_t)b * H + h) * Lp + qi] = acc;
   }
+  if (!tr) return;
   __syncthreads();
   const size_t base = ((size_t)b * H + h) * kBDh;
   for (int i = tid; i < 64 * 64; i += 256) {
@@ -250,7 +252,7 @@ constexpr int kDkvWavesPerChapter = 2;
 
 template <typename T>
 __global__ __launch_bounds__(64 * kDkvWavesPerChapter * DkvCfg<T>::CPW) void xattn_bwd_dkv_kernel(
-    const T* __restrict__ q, const T* __restrict__ qt, const T* __restrict__ dout, const T* __restrict__ dot,
+    const T* __restrict__ q, const T* __restrict__ dout,
     const T* __restrict__ ktiles, const T* __restrict__ vtiles, const int32_t* __restrict__ slot_u,
     const float* __restrict__ omega, const float* __restrict__ lse, const float* __restrict__ delta, int B, int L,
     int Lp, int H, int HK, int NS, int64_t kv_su, int kv_sh, int kv_st, float scale_log2, float scale,
@@ -261,11 +263,10 @@ __global__ __launch_bounds__(64 * kDkvWavesPerChapter * DkvCfg<T>::CPW) void xat
   constexpr int NKB = 64 / WPC / 16;              // 16-key blocks per wave
   constexpr int EPC = 16 / (int)sizeof(T);
   using TileK = SwzTile<T, 64>;   // [query][dim]
-  using TileT = SwzTile<T, QS>;   // [dim][query]
   constexpr int STB = 64 * QS * (int)sizeof(T);  // one staged tile (always 8 KB)
   constexpr int CPT = STB / 16 / NT;             // chunks per thread per staged tile
   static_assert(CPT >= 1, "staging needs at least one chunk per thread");
-  __shared__ __attribute__((aligned(16))) char sStage[2][4][STB];  // [buf][Q, dO, Q^T, dO^T]
+  __shared__ __attribute__((aligned(16))) char sStage[2][2][STB];  // [buf][Q, dO]
   __shared__ float sL[2][QS], sDl[2][QS];
   __shared__ float sDom[NW];
 
@@ -315,34 +316,28 @@ __global__ __launch_bounds__(64 * kDkvWavesPerChapter * DkvCfg<T>::CPW) void xat
   const int nstep = (L + QS - 1) / QS;
   for (int hq = hk * G; hq < hk * G + G; ++hq) {
     const size_t bh = (size_t)b * H + hq;
-    // staged tiles of a step: 0 = Q rows, 1 = dO rows ([query][dim]), 2 = Q^T, 3 = dO^T
-    // ([dim][query], query axis in MFMA key order); every thread moves CPT 16-byte chunks
-    // of each.  Row tiles read through a buffer spanning this sequence only, so rows past
-    // L come back as zeros.
+    // staged tiles of a step: 0 = Q rows, 1 = dO rows ([query][dim]; the query-major operands
+    // Q^T, dO^T of dK, dV are read from them with the transposing LDS read); every thread
+    // moves CPT 16-byte chunks of each.  Rows are read through a buffer spanning this
+    // sequence only, so rows past L come back as zeros.
     const uint32_t seq_bytes = (uint32_t)((size_t)L * H * 64 * sizeof(T));
-    const uint32_t head_bytes = (uint32_t)((size_t)64 * Lp * sizeof(T));
     const Buf bq(q + (size_t)b * L * H * 64, seq_bytes), bd(dout + (size_t)b * L * H * 64, seq_bytes);
-    const Buf bqt(qt + bh * 64 * Lp, head_bytes), bdt(dot + bh * 64 * Lp, head_bytes);
-    uint32_t voff_r[CPT], voff_t[CPT];
+    uint32_t voff_r[CPT];
 #pragma unroll
     for (int j = 0; j < CPT; ++j) {
       const int r = tid + NT * j;
       const int qq = r / (64 / EPC), cc = (r % (64 / EPC)) * EPC;
-      const int dd = r / (QS / EPC), ct = (r % (QS / EPC)) * EPC;
       voff_r[j] = (uint32_t)(((qq * H + hq) * 64 + cc) * (int)sizeof(T));
-      voff_t[j] = (uint32_t)((dd * Lp + ct) * (int)sizeof(T));
     }
-    V16 pre[4 * CPT];
+    V16 pre[2 * CPT];
     float preL = 0.f, preD = 0.f;
     auto fetch = [&](int st) {
       const int q0 = st * QS;
-      const uint32_t so_r = (uint32_t)((size_t)q0 * H * 64 * sizeof(T)), so_t = (uint32_t)(q0 * sizeof(T));
+      const uint32_t so_r = (uint32_t)((size_t)q0 * H * 64 * sizeof(T));
 #pragma unroll
       for (int j = 0; j < CPT; ++j) {
         pre[j] = bq.load16(voff_r[j], so_r);
         pre[CPT + j] = bd.load16(voff_r[j], so_r);
-        pre[2 * CPT + j] = bqt.load16(voff_t[j], so_t);
-        pre[3 * CPT + j] = bdt.load16(voff_t[j], so_t);
       }
       if (tid < QS) {
         preL = lse[bh * Lp + q0 + tid];
@@ -354,11 +349,8 @@ __global__ __launch_bounds__(64 * kDkvWavesPerChapter * DkvCfg<T>::CPW) void xat
       for (int j = 0; j < CPT; ++j) {
         const int r = tid + NT * j;
         const int qq = r / (64 / EPC), cc = (r % (64 / EPC)) * EPC;
-        const int dd = r / (QS / EPC), ct = (r % (QS / EPC)) * EPC;
         st16(sStage[buf][0] + TileK::off(qq, cc), pre[j]);
         st16(sStage[buf][1] + TileK::off(qq, cc), pre[CPT + j]);
-        st16(sStage[buf][2] + TileT::off(dd, ct), pre[2 * CPT + j]);
-        st16(sStage[buf][3] + TileT::off(dd, ct), pre[3 * CPT + j]);
       }
       if (tid < QS) {
         // scaled here, not in fetch, so the loads stay in flight across a step's math
@@ -375,8 +367,6 @@ __global__ __launch_bounds__(64 * kDkvWavesPerChapter * DkvCfg<T>::CPW) void xat
       if (active) {
         const char* sQ = sStage[buf][0];
         const char* sD = sStage[buf][1];
-        const char* sQt = sStage[buf][2];
-        const char* sDt = sStage[buf][3];
 #pragma unroll
         for (int half = 0; half < QS / 32; ++half) {
           const int qb0 = 32 * half;
@@ -424,9 +414,10 @@ __global__ __launch_bounds__(64 * kDkvWavesPerChapter * DkvCfg<T>::CPW) void xat
           }
 #pragma unroll
           for (int db = 0; db < 4; ++db) {
-            // Q^T / dO^T are stored with their query axis in MFMA key order
-            const F8 fq = TileT::frag(sQt, 16 * db + c16, qb0 + 8 * g);
-            const F8 fd = TileT::frag(sDt, 16 * db + c16, qb0 + 8 * g);
+            // Q^T / dO^T fragments (dims 16 db + c16, queries in MFMA key order) read
+            // transposed from the row tiles
+            const F8 fq = mk_frag<TileK, T>(sQ, qb0, 16 * db, lane);
+            const F8 fd = mk_frag<TileK, T>(sD, qb0, 16 * db, lane);
 #pragma unroll
             for (int kb = 0; kb < NKB; ++kb) {
               mma(dv[kb][db], pa[kb], fd);
@@ -698,7 +689,8 @@ extern "C" {
 
 int moc_xattn_bwd_prep(int dtype, const void* q, const void* out, const void* dout, int64_t B, int64_t L, int H,
                        int Dh, float* delta, void* qt, void* dot, hipStream_t stream) {
-  MOC_REQUIRE(q && out && dout && delta && qt && dot, MOC_ERR_ARG, "moc_xattn_bwd_prep: null pointer");
+  MOC_REQUIRE(q && out && dout && delta && (qt != nullptr) == (dot != nullptr), MOC_ERR_ARG,
+              "moc_xattn_bwd_prep: null pointer (qt and dot are both set or both null)");
   MOC_REQUIRE(Dh == kBDh, MOC_ERR_UNSUPPORTED, "moc_xattn_bwd_prep: head_dim %d (needs 64)", Dh);
   MOC_REQUIRE(B >= 0 && L >= 0 && H > 0 && B < 65536, MOC_ERR_ARG, "moc_xattn_bwd_prep: bad shape");
   if (B == 0 || L == 0) return MOC_OK;
@@ -741,12 +733,12 @@ int moc_xattn_bwd_dq(int dtype, const void* q, const void* k_tiles, const void* 
   return check_launch("xattn_bwd_dq_kernel");
 }
 
-int moc_xattn_bwd_dkv(int dtype, const void* q, const void* qt, const void* dout, const void* dot,
+int moc_xattn_bwd_dkv(int dtype, const void* q, const void* dout,
                       const void* k_tiles, const void* v_tiles, int64_t kv_span, int64_t su, int sh, int st,
                       const int32_t* slot_u, const float* omega,
                       const float* lse, const float* delta, int64_t B, int64_t L, int H, int HK, int Dh, int T,
                       int NS, float scale, void* dkv_edge, float* domega_part, hipStream_t stream) {
-  MOC_REQUIRE(q && qt && dout && dot && k_tiles && v_tiles && slot_u && omega && lse && delta && dkv_edge &&
+  MOC_REQUIRE(q && dout && k_tiles && v_tiles && slot_u && omega && lse && delta && dkv_edge &&
                   domega_part,
               MOC_ERR_ARG, "moc_xattn_bwd_dkv: null pointer");
   MOC_REQUIRE(Dh == kBDh && T == kBT, MOC_ERR_UNSUPPORTED, "moc_xattn_bwd_dkv: needs head_dim 64 and T 64");
@@ -761,15 +753,15 @@ int moc_xattn_bwd_dkv(int dtype, const void* q, const void* qt, const void* dout
   if (dtype == MOC_BF16) {
     constexpr int CPW = DkvCfg<bf16>::CPW;
     dim3 grid(xcd_grid(B * HK * ((NS + CPW - 1) / CPW)));
-    hipLaunchKernelGGL(xattn_bwd_dkv_kernel<bf16>, grid, dim3(64 * kDkvWavesPerChapter * CPW), 0, stream, (const bf16*)q, (const bf16*)qt,
-                       (const bf16*)dout, (const bf16*)dot, (const bf16*)k_tiles, (const bf16*)v_tiles, slot_u,
+    hipLaunchKernelGGL(xattn_bwd_dkv_kernel<bf16>, grid, dim3(64 * kDkvWavesPerChapter * CPW), 0, stream, (const bf16*)q,
+                       (const bf16*)dout, (const bf16*)k_tiles, (const bf16*)v_tiles, slot_u,
                        omega, lse, delta, (int)B, (int)L, Lp, H, HK, NS, su, sh, st, sl2, scale, (bf16*)dkv_edge,
                        domega_part);
   } else if (dtype == MOC_F32) {
     constexpr int CPW = DkvCfg<float>::CPW;
     dim3 grid(xcd_grid(B * HK * ((NS + CPW - 1) / CPW)));
     hipLaunchKernelGGL(xattn_bwd_dkv_kernel<float>, grid, dim3(64 * kDkvWavesPerChapter * CPW), 0, stream, (const float*)q,
-                       (const float*)qt, (const float*)dout, (const float*)dot, (const float*)k_tiles,
+                       (const float*)dout, (const float*)k_tiles,
                        (const float*)v_tiles, slot_u, omega, lse, delta, (int)B, (int)L, Lp, H, HK, NS, su, sh, st, sl2,
                        scale, (float*)dkv_edge, domega_part);
   } else {

@@ -493,9 +493,7 @@ class _RoutedAttention(torch.autograd.Function):
         dout = dout.to(dtype).contiguous()
         Lp = lse.shape[2]
         delta = torch.empty(B, H, Lp, device=dev, dtype=torch.float32)
-        qt = torch.empty(B, H, Dh, Lp, device=dev, dtype=dtype)
-        dot = torch.empty_like(qt)
-        call("moc_xattn_bwd_prep", dt, ptr(q), ptr(out), ptr(dout), B, Lq, H, Dh, ptr(delta), ptr(qt), ptr(dot), st)
+        call("moc_xattn_bwd_prep", dt, ptr(q), ptr(out), ptr(dout), B, Lq, H, Dh, ptr(delta), None, None, st)
         # the dense bank gradient's zeros are written beside the dQ and dK/dV kernels
         dbank_zero = None
         if dtype == torch.bfloat16 and ctx.needs_input_grad[1] and ctx.row_grad is None:
@@ -507,7 +505,7 @@ class _RoutedAttention(torch.autograd.Function):
              ptr(dout), ptr(lse), ptr(delta), B, Lq, H, HK, Dh, T, NS, scale, ptr(dq), st)
         dkv_edge = torch.empty(B * NS * T, 2 * KV, device=dev, dtype=dtype)
         dom_part = torch.empty(B * NS, HK, device=dev, dtype=torch.float32)   # every entry written
-        call("moc_xattn_bwd_dkv", dt, ptr(q), ptr(qt), ptr(dout), ptr(dot), ptr(kv), vptr, *kvl, ptr(edge_u), ptr(om),
+        call("moc_xattn_bwd_dkv", dt, ptr(q), ptr(dout), ptr(kv), vptr, *kvl, ptr(edge_u), ptr(om),
              ptr(lse), ptr(delta), B, Lq, H, HK, Dh, T, NS, scale, ptr(dkv_edge), ptr(dom_part), st)
         domega = dom_part.sum(-1).view(B, NS)
         need_bank, need_wk, need_wv = ctx.needs_input_grad[1:4]
