@@ -357,6 +357,14 @@ int moc_sparse_dq_combine(int dtype, const float* dq_part, const int32_t* edge_u
 /* dw f32 [E]: mode 0 sum of dst rows; modes 2/3 sum of dlog rows / w (0 where the clamp is active). */
 int moc_sparse_dw(const float* src, const float* w, const int32_t* edge_u, int mode, int rpe, int64_t E, float* dw,
                   hipStream_t stream);
+/* Zeros the (chapter, kv head) blocks of dK / dV (element (t, dh) at c*cs + hk*hs + t*rs + dh,
+ * heads hk0 .. hk0+nhk-1, C chapters) whose chapter is not among the plan's uniq[0 .. n_uniq):
+ * moc_sparse_bwd writes every block it touches whole, so this replaces zero-initialising the
+ * gradient (autograd's zeros for the unselected chapters of the reference's gather,
+ * memory_bank.py:287-291).  mark i32 [C] is scratch. */
+int moc_sparse_zero_untouched(int dtype, void* dk, void* dv, int64_t cs, int64_t hs, int64_t rs, int64_t C, int hk0,
+                              int nhk, const int32_t* uniq, const int32_t* n_uniq, int64_t max_u, int32_t* mark,
+                              hipStream_t stream);
 
 /* ------------------------------------------------------------------ decode */
 

@@ -1154,6 +1154,40 @@ __global__ __launch_bounds__(64 * kBwdWaves) void sparse_bwd_unit_kernel(
     }
 }
 
+// dK / dV blocks (chapter, kv head) that no edge of a plan touched: the sparse backward
+// writes every touched block whole, so zeroing only the others replaces a zero fill of the
+// whole gradient.  mark[c] = 1 for the plan's chapters; one workgroup per (chapter, head).
+__global__ __launch_bounds__(256) void untouched_mark_kernel(const int32_t* __restrict__ uniq,
+                                                             const int32_t* __restrict__ n_uniq, int64_t max_u,
+                                                             int64_t C, int32_t* __restrict__ mark) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < min((int64_t)n_uniq[0], max_u)) {
+    const int c = uniq[i];
+    if (c >= 0 && c < C) mark[c] = 1;
+  }
+}
+
+__global__ __launch_bounds__(256) void mark_clear_kernel(int32_t* __restrict__ mark, int64_t C) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < C) mark[i] = 0;
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void zero_untouched_kernel(T* __restrict__ dk, T* __restrict__ dv, int64_t cs,
+                                                             int64_t hs, int64_t rs, int hk0, int nhk,
+                                                             const int32_t* __restrict__ mark) {
+  const int64_t c = blockIdx.x / nhk;
+  const int hk = hk0 + (int)(blockIdx.x % nhk);
+  if (mark[c]) return;
+  constexpr int EPC = 16 / (int)sizeof(T), CPR = 64 / EPC;  // 16-byte chunks per 64-element row
+  const V16 z{{0u, 0u, 0u, 0u}};
+  for (int i = threadIdx.x; i < 64 * CPR; i += 256) {
+    const int64_t off = c * cs + hk * hs + (int64_t)(i / CPR) * rs + (i % CPR) * EPC;
+    st16(dk + off, z);
+    st16(dv + off, z);
+  }
+}
+
 }  // namespace moc
 
 using namespace moc;
@@ -1317,6 +1351,35 @@ int moc_sparse_dw(const float* src, const float* w, const int32_t* edge_u, int m
   hipLaunchKernelGGL(sparse_dw_kernel, dim3((unsigned)((E + 255) / 256)), dim3(256), 0, stream, src, w, edge_u, mode,
                      rpe, E, dw);
   return check_launch("sparse_dw_kernel");
+}
+
+int moc_sparse_zero_untouched(int dtype, void* dk, void* dv, int64_t cs, int64_t hs, int64_t rs, int64_t C, int hk0,
+                              int nhk, const int32_t* uniq, const int32_t* n_uniq, int64_t max_u, int32_t* mark,
+                              hipStream_t stream) {
+  MOC_REQUIRE(dk && dv && uniq && n_uniq && mark, MOC_ERR_ARG, "moc_sparse_zero_untouched: null pointer");
+  MOC_REQUIRE(C > 0 && C * nhk < ((int64_t)1 << 31) && hk0 >= 0 && nhk > 0 && max_u >= 0, MOC_ERR_ARG,
+              "moc_sparse_zero_untouched: C=%lld hk0=%d nhk=%d", (long long)C, hk0, nhk);
+  const int64_t es = dtype == MOC_F32 ? 4 : 2;
+  MOC_REQUIRE(rs >= 64 && (cs * es) % 16 == 0 && (hs * es) % 16 == 0 && (rs * es) % 16 == 0 &&
+                  ((uintptr_t)dk & 15) == 0 && ((uintptr_t)dv & 15) == 0,
+              MOC_ERR_ARG, "moc_sparse_zero_untouched: strides and pointers must be 16-byte multiples");
+  hipLaunchKernelGGL(mark_clear_kernel, dim3((unsigned)((C + 255) / 256)), dim3(256), 0, stream, mark, C);
+  if (int rc = check_launch("mark_clear_kernel")) return rc;
+  if (max_u > 0) {
+    hipLaunchKernelGGL(untouched_mark_kernel, dim3((unsigned)((max_u + 255) / 256)), dim3(256), 0, stream, uniq, n_uniq,
+                       max_u, C, mark);
+    if (int rc = check_launch("untouched_mark_kernel")) return rc;
+  }
+  const dim3 grid((unsigned)(C * nhk));
+  if (dtype == MOC_BF16)
+    hipLaunchKernelGGL(zero_untouched_kernel<bf16>, grid, dim3(256), 0, stream, (bf16*)dk, (bf16*)dv, cs, hs, rs, hk0,
+                       nhk, (const int32_t*)mark);
+  else if (dtype == MOC_F32)
+    hipLaunchKernelGGL(zero_untouched_kernel<float>, grid, dim3(256), 0, stream, (float*)dk, (float*)dv, cs, hs, rs,
+                       hk0, nhk, (const int32_t*)mark);
+  else
+    return set_error(MOC_ERR_UNSUPPORTED, "moc_sparse_zero_untouched: dtype %d", dtype);
+  return check_launch("zero_untouched_kernel");
 }
 
 }  // extern "C"

@@ -89,8 +89,11 @@ def _forward(q, k, v, layout, segments: List[_Segment], mode: int, S: int, scale
     return out, saved
 
 
-def _backward(q, k, v, layout, out, dout, segments, saved, mode, S, scale, dk, dv, dk_layout):
-    """Fills dk/dv (pre-zeroed, layout dk_layout), returns dq and the per-edge dw (or None)."""
+def _backward(q, k, v, layout, out, dout, segments, saved, mode, S, scale, dk, dv, dk_layout,
+              zero_chapters: int = 0):
+    """Fills dk/dv (layout dk_layout), returns dq and the per-edge dw (or None).  dk/dv are
+    pre-zeroed, or, with zero_chapters = C > 0, uninitialised: the blocks of the C chapters
+    that a segment's plan does not touch are zeroed here (the touched ones are written whole)."""
     B, Tq, HQ, D = q.shape
     HK, (cs, hs, rs) = _kv_geom(layout, k)
     dt = L.dtype_code(q.dtype)
@@ -110,12 +113,17 @@ def _backward(q, k, v, layout, out, dout, segments, saved, mode, S, scale, dk, d
             lrow = lse_joint
             call("moc_sparse_bwd_prep", dt, ptr(dout), ptr(out), None, ptr(sg.plan.edge_u), mode, S, sg.rpe,
                  ntok, HQ, sg.hq_off, ptr(drow), st)
+        dv_ptr = dv.data_ptr() if dv is not None else dk.data_ptr() + dv_off
+        if zero_chapters:
+            mark = torch.empty(zero_chapters, device=q.device, dtype=torch.int32)
+            call("moc_sparse_zero_untouched", dt, ptr(dk), dv_ptr, ocs, ohs, ors, zero_chapters, sg.hk0, sg.nhk,
+                 ptr(sg.plan.uniq), ptr(sg.plan.n_uniq), sg.plan.max_u, ptr(mark), st)
         dq_part = torch.empty(sg.E * sg.rpe, D, device=q.device, dtype=torch.float32)
         dlog = torch.empty(sg.E * sg.rpe, device=q.device, dtype=torch.float32) if mode in (2, 3) else None
         call("moc_sparse_bwd", dt, ptr(q), ptr(dout), ntok, HQ, ptr(k), ptr(v), cs, hs, rs, HK, D,
              ptr(sg.plan.uniq), ptr(sg.plan.n_uniq), ptr(sg.plan.csr_off), ptr(sg.plan.csr_edge), sg.plan.max_u, S,
              sg.hk0, sg.nhk, sg.hq_off, sg.rpe, mode, ptr(lrow), ptr(drow), ptr(sg.w), float(scale), ptr(dk),
-             dv.data_ptr() if dv is not None else dk.data_ptr() + dv_off, ocs, ohs, ors, ptr(dq_part), ptr(dlog), st)
+             dv_ptr, ocs, ohs, ors, ptr(dq_part), ptr(dlog), st)
         call("moc_sparse_dq_combine", dt, ptr(dq_part), ptr(sg.plan.edge_u), S, sg.rpe, ntok, HQ, sg.hq_off, ptr(dq),
              st)
         if mode != 1:
@@ -302,11 +310,12 @@ class _TokenRouted(torch.autograd.Function):
         D = q.shape[-1]
         KV = HK * D
         Nr, d = routed.shape
-        dkv = torch.zeros(Nr, 2 * KV, device=q.device, dtype=dtype)
-        # dk / dv written as rows [chapter*64 + key][hk*64 + dim] (dv at column offset KV)
+        # dk / dv written as rows [chapter*64 + key][hk*64 + dim] (dv at column offset KV); blocks
+        # of chapters no token selected are zeroed by the backward instead of a 2 KV x Nr fill
+        dkv = torch.empty(Nr, 2 * KV, device=q.device, dtype=dtype)
         elem = dkv.element_size()
         dq, dws = _backward(q, kv[:, :KV], kv[:, KV:], "rows", out, dout, ctx.segs, ctx.saved_parts, mode, S,
-                            D ** -0.5, dkv, None, (64 * 2 * KV, 64, 2 * KV, KV * elem))
+                            D ** -0.5, dkv, None, (64 * 2 * KV, 64, 2 * KV, KV * elem), zero_chapters=Nr // BLOCK)
         need_r, need_wk, need_wv = ctx.needs_input_grad[1:4]
         dr = dwk = dwv = None
         if need_wk or need_wv:
