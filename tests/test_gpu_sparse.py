@@ -184,3 +184,29 @@ def _token_layer_v5(h, bank, Wr, br, Wq, Wk, Wv, Wo, *, H, C, T, S, top_k):
     idx4 = (idx - S).unsqueeze(2).expand(B, Lq, H, top_k)
     r = O.sparse_attention_joint_bias(q, k, v, idx4, w, T, q.shape[-1] ** -0.5)
     return O.linear(shared + r.reshape(B, Lq, -1) * 2.5, Wo)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("hk0,nhk", [(0, 3), (1, 1)])
+def test_zero_untouched_blocks(gpu_device, dtype, hk0, nhk):
+    """moc_sparse_zero_untouched: the (chapter, kv head) blocks of dK / dV (rows layout) whose
+    chapter the plan does not hold are zeroed, every other element is left as it was."""
+    print(f"zero untouched {dtype} hk0={hk0} nhk={nhk}", flush=True)
+    from memory_amd import _lib, ops
+    C, HK, KV = 9, 3, 3 * 64
+    chap = torch.tensor([4, 0, 4, 7, -1, 2], dtype=torch.int32, device=gpu_device)   # -1: skipped edge
+    plan = ops.chapter_plan(chap, C)
+    g = torch.Generator().manual_seed(3)
+    dkv = (torch.randn(C * 64, 2 * KV, generator=g) + 5).to(dtype).to(gpu_device)
+    before = dkv.clone()
+    mark = torch.empty(C, dtype=torch.int32, device=gpu_device)
+    es = dkv.element_size()
+    _lib.call("moc_sparse_zero_untouched", _lib.dtype_code(dtype), dkv.data_ptr(), dkv.data_ptr() + KV * es,
+              64 * 2 * KV, 64, 2 * KV, C, hk0, nhk, plan.uniq.data_ptr(), plan.n_uniq.data_ptr(), plan.max_u,
+              mark.data_ptr(), _lib.stream_ptr(gpu_device))
+    torch.cuda.synchronize()
+    got, ref = dkv.cpu().view(C, 64, 2, HK, 64), before.cpu().view(C, 64, 2, HK, 64).clone()
+    for c in range(C):
+        if c not in (0, 2, 4, 7):
+            ref[c, :, :, hk0:hk0 + nhk, :] = 0
+    assert torch.equal(got, ref)
