@@ -615,12 +615,14 @@ class _TokenRouterLinear(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, W, b):
         Wc = W.to(x.dtype).contiguous()
-        if x.dtype == torch.float32:
-            y = torch.mm(x, Wc.t())
+        # the bias rides in the GEMM's epilogue (a separate broadcast add re-reads and rewrites
+        # the fp32 logits: 0.27 GB at 8,192 tokens x 4,097 chapters)
+        if b is None:
+            y = torch.mm(x, Wc.t()) if x.dtype == torch.float32 else torch.mm(x, Wc.t(), out_dtype=torch.float32)
+        elif x.dtype == torch.float32:
+            y = torch.addmm(b.float(), x, Wc.t())
         else:
-            y = torch.mm(x, Wc.t(), out_dtype=torch.float32)
-        if b is not None:
-            y.add_(b.float())
+            y = torch.addmm(b.float(), x, Wc.t(), out_dtype=torch.float32)
         ctx.save_for_backward(x, Wc)
         ctx.meta = (W.dtype, None if b is None else b.dtype)
         return y
