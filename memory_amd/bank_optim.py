@@ -182,9 +182,12 @@ class BankAdamW(torch.optim.Optimizer):
         bank._moc_bank_opt = self
 
     # ------------------------------------------------------------------ reads
-    def read_view(self) -> torch.Tensor:
-        """The tensor the forward kernels read (the mirror if there is one)."""
-        return self.mirror if self.mirror is not None else self.bank
+    def read_view(self, compute_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+        """The tensor the forward kernels read: the bf16 mirror if there is one and the
+        layer computes in bf16 (None: any dtype), else the fp32 bank."""
+        if self.mirror is not None and compute_dtype != torch.float32:
+            return self.mirror
+        return self.bank
 
     def _run(self, grad, list_, n_list, max_list, step, scalars, grad_scale=None):
         g = self.param_groups[0]
@@ -208,6 +211,13 @@ class BankAdamW(torch.optim.Optimizer):
     def flush(self) -> None:
         """Bring every chapter to the last completed step."""
         self.catch_up(None)
+
+    def sync_mirror(self) -> None:
+        """After the bank's values were written outside the optimizer (a checkpoint load, after
+        ``flush()``): the bf16 mirror the kernels read is refreshed from the bank."""
+        if self.mirror is not None:
+            with torch.no_grad():
+                self.mirror.copy_(self.bank.detach())
 
     # ------------------------------------------------------------------ step
     def _step_scalars(self, t: int):

@@ -152,6 +152,7 @@ class MemoryStack(nn.Module):
         self.norm_type = _cfg(memory, "shared_routed_norm_type", "rms")
         self.norm_eps = float(_cfg(memory, "shared_routed_norm_eps", 1e-6))
         self.strategy = _cfg(memory, "routing_strategy_train", "sequence")
+        self.strategy_inference = _cfg(memory, "routing_strategy_inference", "sequence")
         self.window = _cfg(memory, "routing_window_size", 128)
         self.kernel_version = _cfg(memory, "token_routing_kernel_version", "v2")
         heads = _cfg(memory, "memory_num_heads") or num_heads
@@ -223,12 +224,33 @@ class MemoryStack(nn.Module):
         if strict and (missing or unknown):
             raise KeyError(f"reference state dict does not match the memory stack: missing {missing[:8]}, "
                            f"unexpected {unknown[:8]}")
+        for k, v in mem.items():
+            if tuple(v.shape) != tuple(own[k].shape):
+                raise ValueError(f"{k}: shape {tuple(v.shape)} in the checkpoint, {tuple(own[k].shape)} here")
         with torch.no_grad():
             for k, v in mem.items():
-                if tuple(v.shape) != tuple(own[k].shape):
-                    raise ValueError(f"{k}: shape {tuple(v.shape)} in the checkpoint, {tuple(own[k].shape)} here")
                 own[k].copy_(v.to(own[k].dtype))
+            # a bank stepped by BankAdamW: its chapters were all brought to the last step before
+            # the copy (state_dict above flushes), so the loaded values are current; the bf16
+            # mirror the kernels read is refreshed from them
+            for opt in self._bank_optimizers():
+                opt.sync_mirror()
         return unused
+
+    def _bank_optimizers(self):
+        out = []
+        for b in self.memory_banks.values():
+            opt = getattr(b.memory, "_moc_bank_opt", None)
+            if opt is not None:
+                out.append(opt)
+        return out
+
+    def state_dict(self, *args, **kwargs):
+        """nn.Module.state_dict after every BankAdamW-stepped bank is brought to its last step
+        (chapters not read since then still owe their lazy zero-gradient steps)."""
+        for opt in self._bank_optimizers():
+            opt.flush()
+        return super().state_dict(*args, **kwargs)
 
     def reference_state_dict(self) -> Dict[str, torch.Tensor]:
         """This stack's parameters under the reference's keys (a subset of its model.pt)."""
@@ -238,13 +260,25 @@ class MemoryStack(nn.Module):
     def bank_for(self, layer_idx: int) -> nn.Parameter:
         return self.memory_banks[str(self.bank_of[layer_idx])].memory
 
+    def routing_strategy(self) -> str:
+        """model.py:538 and :612-625: the training strategy while training; otherwise the
+        inference strategy, where "rolling" / "hybrid" (which need the decode-time routing cache)
+        fall back to "sequence" as they do without use_cache."""
+        if self.training:
+            return self.strategy
+        s = self.strategy_inference
+        return "sequence" if s in ("rolling", "hybrid") else s
+
     def forward(self, layer_idx: int, block_input: torch.Tensor, hidden_states: torch.Tensor,
-                return_losses: bool = True):
+                return_losses: Optional[bool] = None):
         key = str(layer_idx)
         router, sub = self.routers[key], self.layers[key]
         bank = self.bank_for(layer_idx)
         S, T = self.num_shared_chapters, self.tokens_per_chapter
-        if self.strategy == "token":
+        if return_losses is None:
+            return_losses = self.training             # model.py:623, return_losses=self.training
+        strategy = self.routing_strategy()
+        if strategy == "token":
             idx, w, losses = router.route_token_level(block_input, return_losses=return_losses,
                                                       exclude_prefix_chapters=S)
             opt = getattr(bank, "_moc_bank_opt", None)
@@ -264,7 +298,8 @@ class MemoryStack(nn.Module):
                      "chapter_weights": w}
             return sub(hidden_states, token_routing_state=state,
                        token_routing_kernel_version=self.kernel_version), losses
-        window = self.window if self.strategy in ("sequence-rolling", "sequence_rolling") else None
+        window = self.window if strategy in ("sequence-rolling", "sequence_rolling") else None
+        router.routing_strategy = strategy            # model.py:620, as the reference sets it per call
         idx, w, losses = router.route_ids32(block_input, return_losses=return_losses, exclude_prefix_chapters=S,
                                             rolling_window_size=window)
         idx_star, omega = prepend_shared_chapters32(idx, w, num_chapters=self.num_chapters, num_shared_chapters=S,

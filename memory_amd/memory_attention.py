@@ -187,3 +187,68 @@ class MemoryCrossAttention(nn.Module):
         if combined is None:
             combined = hidden_states.new_zeros((B, L, self.hidden_dim))
         return combined
+
+
+class MemoryCrossAttentionWithRouting(nn.Module):
+    """Cross-attention over sequence-level routed chapters (memory_attention.py:901-1054).
+
+    ``forward(hidden_states, memory, chapter_indices, chapter_weights=None)``:
+      * ``memory`` (N, d) is the bank, chapter i of sequence b = rows
+        chapter_indices[b, i] * T ... + T (:1011-1054); a (B, k*T, d) memory is already routed
+        (chapter i = rows i*T ... + T of its sequence);
+      * with ``chapter_weights`` (B, k): sum_i w_i * o_proj(softmax over chapter i's keys),
+        one softmax per chapter (:982-1001).  o_proj is linear and bias-free, so this is
+        o_proj of the weighted per-chapter combine, which runs on the token-routed kernels'
+        exact MoE mode (v4 semantics) with every token of a sequence selecting its sequence's
+        chapters;
+      * without weights: one joint softmax over all selected keys (:1003-1009), the dense
+        path of MemoryCrossAttention over the selected rows.
+    Returns ``(output (B, L, hidden_dim), None)``."""
+
+    def __init__(self, hidden_dim: int, num_heads: int, num_chapters: int, tokens_per_chapter: int, top_k: int,
+                 num_kv_heads: Optional[int] = None, memory_dim: Optional[int] = None,
+                 use_low_rank_projections: bool = False, projection_rank: Optional[int] = None,
+                 reduced_dim_mode: bool = False, reduced_dim: Optional[int] = None, wo_init_zero: bool = True,
+                 dropout: float = 0.0, use_flash_attention: bool = True):
+        super().__init__()
+        self.num_chapters = num_chapters
+        self.tokens_per_chapter = tokens_per_chapter
+        self.top_k = top_k
+        self.attention = MemoryCrossAttention(
+            hidden_dim=hidden_dim, num_heads=num_heads, num_kv_heads=num_kv_heads, memory_dim=memory_dim,
+            use_low_rank_projections=use_low_rank_projections, projection_rank=projection_rank,
+            reduced_dim_mode=reduced_dim_mode, reduced_dim=reduced_dim, wo_init_zero=wo_init_zero,
+            dropout=dropout, use_flash_attention=use_flash_attention)
+
+    def _select_chapters(self, memory: torch.Tensor, chapter_indices: torch.Tensor) -> torch.Tensor:
+        """(B, k*T, d) rows of the selected chapters (memory_attention.py:1011-1054)."""
+        T = int(self.tokens_per_chapter)
+        B, k = chapter_indices.shape
+        rows = (chapter_indices.long().unsqueeze(-1) * T
+                + torch.arange(T, device=chapter_indices.device).view(1, 1, T)).reshape(B, k * T)
+        return memory[rows]
+
+    def forward(self, hidden_states: torch.Tensor, memory: torch.Tensor, chapter_indices: torch.Tensor,
+                chapter_weights: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
+        attn = self.attention
+        T = int(self.tokens_per_chapter)
+        if T != CHAPTER_TOKENS:
+            raise ValueError(f"tokens_per_chapter must be {CHAPTER_TOKENS} for the HIP kernels, got {T}")
+        selected = self._select_chapters(memory, chapter_indices) if memory.dim() == 2 else memory
+        if chapter_weights is None:
+            return attn(hidden_states, selected)
+        from .sparse_attention import FSA_topk_sparse_attention_weighted_bthd
+        B, L, _ = hidden_states.shape
+        k = chapter_indices.shape[1]
+        if selected.shape[1] < k * T:
+            raise ValueError(f"routed memory has {selected.shape[1]} rows, needs {k} chapters of {T}")
+        N = selected.shape[1]
+        q = attn._queries(hidden_states)
+        dt = q.dtype
+        kk = ops.linear(selected.to(dt), attn.k_proj.weight.to(dt)).view(B, N, attn.num_kv_heads, attn.head_dim)
+        vv = ops.linear(selected.to(dt), attn.v_proj.weight.to(dt)).view(B, N, attn.num_kv_heads, attn.head_dim)
+        idx = torch.arange(k, device=q.device, dtype=torch.int32).view(1, 1, k).expand(B, L, k)
+        w = chapter_weights.float().view(B, 1, k).expand(B, L, k)
+        o = FSA_topk_sparse_attention_weighted_bthd(q, kk, vv, idx, w, T, softmax_scale=attn.scale,
+                                                    disable_causal_mask=True)
+        return attn._project_output(o.reshape(B, L, attn.hidden_dim)), None

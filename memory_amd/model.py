@@ -30,17 +30,26 @@ from .router import ChapterRouter
 def select_routed_chapters_from_probs(probs: torch.Tensor, top_k: int, num_shared_chapters: int):
     """model.py:331-354: mask the shared prefix, renormalise, top-k, renormalise.
 
-    Selection runs the router top-k kernel on log(probs) (same order as probs;
-    the kernel's softmax of log(probs) is probs / sum(probs))."""
+    The masked, renormalised probabilities are formed in the probabilities' dtype as the
+    reference does; the router top-k kernel selects on those values directly (its selection is
+    a radix select on the raw fp32 keys; ties: lower chapter id first), and the weights are
+    the selected values renormalised, so gradients flow to ``probs`` as in the reference."""
     B, C = probs.shape
     S = max(0, min(int(num_shared_chapters), C))
     k = min(int(top_k), C - S)
     if k <= 0:
         return (torch.empty((B, 0), dtype=torch.long, device=probs.device),
                 torch.empty((B, 0), dtype=probs.dtype, device=probs.device))
-    logits = torch.log(probs.float().clamp_min(torch.finfo(torch.float32).tiny))
-    idx, w = ops.router_topk(logits, k, S)
-    return idx.long(), w
+    masked = probs.clone()
+    if S > 0:
+        masked[:, :S] = 0.0
+    masked = masked / masked.sum(dim=-1, keepdim=True).clamp_min(1e-12)
+    with torch.no_grad():
+        idx, _ = ops.router_topk(masked.detach().float(), k, S)
+    idx = idx.long()
+    w = masked.gather(-1, idx)
+    w = w / w.sum(dim=-1, keepdim=True).clamp_min(1e-12)
+    return idx, w
 
 
 def prepend_shared_chapters(chapter_indices: torch.Tensor, chapter_weights: torch.Tensor, *, num_chapters: int,
@@ -96,10 +105,12 @@ class _SplitRows(torch.autograd.Function):
     def backward(ctx, ga, gb):
         n, shape = ctx.n, ctx.shape
         ref = ga if ga is not None else gb
-        # the token path writes its gradient into the tail of a whole-shape buffer
-        # (sparse_attention._rows_grad): fill the head rows of that buffer and return it
+        # the token path writes its gradient into the tail of a whole-shape buffer that it marks
+        # (sparse_attention._rows_grad sets ``_moc_rows_tail`` on it): fill the head rows of that
+        # buffer and return it.  Any other view (e.g. from cat's backward) takes the copy below.
         base = None if gb is None else gb._base
-        if base is not None and base.shape == shape and base.dtype == gb.dtype and base.is_contiguous() \
+        if base is not None and getattr(base, "_moc_rows_tail", None) == n and base.shape == shape \
+                and base.dtype == gb.dtype and base.is_contiguous() \
                 and gb.storage_offset() - base.storage_offset() == n * math.prod(shape[1:]):
             if ga is None:
                 base[:n].zero_()

@@ -447,7 +447,7 @@ class _RoutedAttention(torch.autograd.Function):
         plan = chapter_plan(idx_star, num_chapters)
         if opt is not None:
             opt.catch_up(plan.uniq, plan.n_uniq, plan.max_u)
-            bank = opt.read_view()
+            bank = opt.read_view(dtype)
         bank = bank.contiguous()
         mean = rstd = None
         if norm != L.MOC_NORM_NONE:

@@ -342,6 +342,7 @@ def _rows_grad(routed: torch.Tensor, dkv: torch.Tensor, wkv: torch.Tensor) -> to
         d = routed.shape[1]
         if off % d == 0 and off // d + routed.shape[0] == base.shape[0]:
             full = torch.empty(base.shape, device=dkv.device, dtype=dkv.dtype)
+            full._moc_rows_tail = off // d        # read by model._SplitRows.backward
             tail = full[off // d:]
             torch.mm(dkv, wkv, out=tail)
             return tail

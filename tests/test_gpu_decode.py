@@ -7,7 +7,7 @@ import pytest
 import torch
 
 import oracle as O
-from helpers import assert_rel, gen
+from helpers import assert_parity, gen
 
 pytestmark = pytest.mark.gpu
 
@@ -46,7 +46,7 @@ def test_decode_step_matches_oracle(gpu_device, dtype, B, H, HK, C, k, norm):
     rd = lambda t: t.to(dtype).double()
     ref = O.decode_step(rd(h), rd(bank), ci, cw.double(), rd(Wq), rd(Wk), rd(Wv), rd(Wo), H=H, HK=HK, T=T,
                         normalize=norm is not None, norm_type=norm or "rms", eps=1e-5, S=S)
-    assert_rel(out, ref, 1e-4 if dtype == torch.float32 else 2e-2, "decode output")
+    assert_parity(out, ref, dtype, "decode output")
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])

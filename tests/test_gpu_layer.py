@@ -12,7 +12,7 @@ import pytest
 import torch
 
 import oracle as O
-from helpers import assert_rel
+from helpers import assert_parity, assert_rel
 
 pytestmark = pytest.mark.gpu
 
@@ -78,16 +78,13 @@ def test_config1_layer_forward_backward(gpu_device, dtype, normalize, strategy, 
     (ref * dO.double()).sum().backward()
     idx_star, _, _ = layer.route(hg.detach(), return_losses=False)
     assert torch.equal(idx_star.cpu(), det["idx_star"])
-    tol = 1e-4 if dtype == torch.float32 else 2e-2
-    assert_rel(out, ref, tol, "out")
+    assert_parity(out, ref, dtype, "out")
     names = ["dh", "dbank", "dWr", "dbr", "dWq", "dWk", "dWv", "dWo"]
     got = [hg.grad, bg.grad, layer.router.router.weight.grad, layer.router.router.bias.grad,
            layer.memory_attn.q_proj.weight.grad, layer.memory_attn.k_proj.weight.grad,
            layer.memory_attn.v_proj.weight.grad, layer.memory_attn.o_proj.weight.grad]
     for n, g, r in zip(names, got, leaves):
-        # router grads are computed in fp32 end to end (logits, omega chain), also for bf16 runs
-        t = 1e-4 if (dtype == torch.float32) else (5e-2 if n in ("dWr", "dbr") else tol)
-        assert_rel(g, r.grad, t, n)
+        assert_parity(g, r.grad, dtype, n)
 
 
 def test_config1_recipe_scale_router_losses(gpu_device):

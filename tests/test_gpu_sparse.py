@@ -10,7 +10,7 @@ import pytest
 import torch
 
 import oracle as O
-from helpers import assert_rel, gen
+from helpers import assert_parity, assert_rel, gen
 
 pytestmark = pytest.mark.gpu
 
@@ -78,13 +78,12 @@ def test_fsa_modes_forward_backward(gpu_device, dtype, mode, B, Tq, HQ, HK, M, S
     else:
         out = SA.FSA_topk_sparse_attention_bthd(gq, gk, gv, idx_d, 64, block_weights_bths=gw, **kw)
     (out.float() * dO.to(dev)).sum().backward()
-    tol = 1e-4 if dtype == torch.float32 else 2e-2
-    assert_rel(out, ref, tol, "out")
-    assert_rel(gq.grad, rq.grad, tol, "dq")
-    assert_rel(gk.grad, rk.grad, tol, "dk")
-    assert_rel(gv.grad, rv.grad, tol, "dv")
+    assert_parity(out, ref, dtype, "out")
+    assert_parity(gq.grad, rq.grad, dtype, "dq")
+    assert_parity(gk.grad, rk.grad, dtype, "dk")
+    assert_parity(gv.grad, rv.grad, dtype, "dv")
     if w is not None:
-        assert_rel(gw.grad, rw.grad, 1e-4 if dtype == torch.float32 else 3e-2, "dw")
+        assert_parity(gw.grad, rw.grad, dtype, "dw")
 
 
 def test_fsa_out_of_range_chapters_are_skipped(gpu_device):
@@ -102,7 +101,7 @@ def test_fsa_out_of_range_chapters_are_skipped(gpu_device):
     ref = O.sparse_attention_weighted(q.double(), k.double(), v.double(), ref_idx, ref_w.double(), 64, 0.125)
     out = SA.FSA_topk_sparse_attention_weighted_bthd(q.to(dev), k.to(dev), v.to(dev), bad.to(dev, torch.int32),
                                                      w.to(dev), 64, softmax_scale=0.125, disable_causal_mask=True)
-    assert_rel(out, ref, 1e-4, "out with skipped slots")
+    assert_parity(out, ref, torch.float32, "out with skipped slots")
 
 
 def test_fsa_rejects_unsupported(gpu_device):
@@ -118,16 +117,20 @@ def test_fsa_rejects_unsupported(gpu_device):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("weighted,version", [(True, "v4"), (False, "v2"), (True, "v5")])
-def test_token_layer_matches_oracle(gpu_device, dtype, weighted, version):
+@pytest.mark.parametrize("weighted,version,shape", [(True, "v4", "dense"), (False, "v2", "dense"),
+                                                    (True, "v5", "dense"), (True, "v4", "sparse")])
+def test_token_layer_matches_oracle(gpu_device, dtype, weighted, version, shape):
     """MemoryCrossAttention's token-routing path (shared dense + routed MoE) vs the oracle's
-    token_memory_layer, including gradients of h, the bank and every projection."""
-    print(f"token layer dtype={dtype} weighted={weighted} version={version}", flush=True)
+    token_memory_layer, including gradients of h, the bank and every projection.  "sparse":
+    65 chapters, 4 tokens, k=2, so most routed chapters go unselected and their bank-gradient
+    rows must come out exactly zero (the dK / dV rows are not pre-zeroed: the blocks no token
+    selected are zeroed by moc_sparse_zero_untouched)."""
+    print(f"token layer dtype={dtype} weighted={weighted} version={version} shape={shape}", flush=True)
     from memory_amd.memory_attention import MemoryCrossAttention
     from memory_amd.model import TokenRoutedMemoryLayer
     dev = gpu_device
     g = gen(55)
-    B, Lq, d, H, C, T, S, k = 2, 48, 128, 2, 9, 64, 1, 3
+    B, Lq, d, H, C, T, S, k = (2, 48, 128, 2, 9, 64, 1, 3) if shape == "dense" else (1, 4, 128, 2, 65, 64, 1, 2)
     h = torch.randn(B, Lq, d, generator=g)
     bank = torch.randn(C * T, d, generator=g)
     Wr = torch.randn(C, d, generator=g) * 0.3
@@ -160,8 +163,7 @@ def test_token_layer_matches_oracle(gpu_device, dtype, weighted, version):
     else:
         ref = O.token_memory_layer(*leaves, H=H, HK=H, C=C, T=T, S=S, top_k=k, routed_scale=2.5, weighted=weighted)
     (ref * dO.double()).sum().backward()
-    tol = 1e-4 if dtype == torch.float32 else 2e-2
-    assert_rel(out, ref, tol, "out")
+    assert_parity(out, ref, dtype, "out")
     names = ["dh", "dbank", "dWr", "dbr", "dWq", "dWk", "dWv", "dWo"]
     got = [hg.grad, bg.grad, layer.router.router.weight.grad, layer.router.router.bias.grad,
            layer.memory_attn.q_proj.weight.grad, layer.memory_attn.k_proj.weight.grad,
@@ -169,8 +171,15 @@ def test_token_layer_matches_oracle(gpu_device, dtype, weighted, version):
     for n, gr, r in zip(names, got, leaves):
         if r.grad is None or (not weighted and n in ("dWr", "dbr")):
             continue
-        t = tol if n not in ("dWr", "dbr") else (1e-4 if dtype == torch.float32 else 5e-2)
-        assert_rel(gr, r.grad, t, n)
+        assert_parity(gr, r.grad, dtype, n)
+    if shape == "sparse":
+        idx, _, _ = layer.router.route_token_level(hg.detach(), return_losses=False, exclude_prefix_chapters=S)
+        sel = torch.zeros(C, dtype=torch.bool)
+        sel[:S] = True
+        sel[idx.reshape(-1).cpu().long()] = True
+        assert int((~sel).sum()) >= C // 2
+        unsel = (~sel).repeat_interleave(T)
+        assert int(torch.count_nonzero(bg.grad.cpu()[unsel])) == 0, "unselected chapters' bank rows must be zero"
 
 
 def _token_layer_v5(h, bank, Wr, br, Wq, Wk, Wv, Wo, *, H, C, T, S, top_k):
