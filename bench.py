@@ -98,7 +98,7 @@ def cpu_baseline(cfg, budget_s=20.0):
     import torch
     import oracle as O
 
-    ncores = min(16, len(os.sched_getaffinity(0)))
+    ncores = len(os.sched_getaffinity(0))
     torch.set_num_threads(ncores)
     g = torch.Generator().manual_seed(0)
     Bs = 1
@@ -129,9 +129,22 @@ def cpu_baseline(cfg, budget_s=20.0):
         times.append(time.perf_counter() - t0)
     med = statistics.median(times)
     return {"value": Bs * L / med, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+            "affinity_cores": ncores, "torch_threads": torch.get_num_threads(), "cpu_model": cpu_model(),
             "sample": f"oracle sequence_memory_layer fwd+bwd fp32, 1 sequence x {L} tokens at the full paper shape "
-                      f"(d={d}, H={H}, bank {C * T} rows, k={k}); median of {iters} iterations "
-                      f"({med * 1e3:.0f} ms each)"}
+                      f"(d={d}, H={H}, bank {C * T} rows, k={k}); 1 warm-up, median of {iters} iterations "
+                      f"({med * 1e3:.0f} ms each); tokens/s of that sequence"}
+
+
+def cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo, as lscpu reports it)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.lower().startswith("model name"):
+                    return ln.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 PROBE_BYTES = 256 << 20
@@ -140,21 +153,131 @@ TRAFFIC_KERNELS = {"moc_xattn_bwd_dkv": "xattn_bwd_dkv_kernel", "moc_xattn_fwd":
                    "moc_xattn_bwd_dq": "xattn_bwd_dq_kernel", "moc_kv_project": "kv_project_wide_kernel",
                    "moc_decode_partial": "sparse_fwd_unit_kernel", "moc_sparse_bwd": "sparse_bwd_unit_kernel",
                    "moc_bank_adamw": "bank_adamw_kernel"}
+# device kernel -> the HIP source it is built from (counter figures are tied to that file's hash)
+KERNEL_SOURCES = {"xattn_fwd_kernel": "xattn_fwd.hip", "xattn_bwd_dq_kernel": "xattn_bwd.hip",
+                  "xattn_bwd_dkv_kernel": "xattn_bwd.hip", "xattn_bwd_kernel": "xattn_bwd.hip",
+                  "gather_rows_kernel": "xattn_bwd.hip", "kv_project_wide_kernel": "kv_project.hip",
+                  "kv_wgrad_kernel": "kv_wgrad.hip", "kv_wgrad_kernel_dense": "kv_wgrad.hip",
+                  "kv_wgrad_kernel_gather": "kv_wgrad.hip", "sparse_fwd_unit_kernel": "sparse_xattn.hip",
+                  "sparse_bwd_unit_kernel": "sparse_xattn.hip", "sparse_combine_kernel": "sparse_xattn.hip",
+                  "sparse_dq_combine_kernel": "sparse_xattn.hip", "bank_adamw_kernel": "bank_optim.hip"}
+
+
+def source_sha(kernel: str):
+    """First 16 hex digits of the SHA-256 of the HIP source ``kernel`` is built from."""
+    import hashlib
+    src = KERNEL_SOURCES.get(kernel)
+    if src is None:
+        return None
+    path = os.path.join(ROOT, "memory_amd", "csrc", src)
+    if not os.path.exists(path):
+        return None
+    with open(path, "rb") as f:
+        return hashlib.sha256(f.read()).hexdigest()[:16]
+
+
+def profile_value(workload: str, key: str, kern: str, kind: str = "traffic"):
+    """A per-kernel figure from a committed counter summary (profiles/<kind>_<workload>.md, lines
+    `<key> <kernel> <value> <source sha16>`), returned only while the kernel's HIP source still
+    hashes to the recorded value: (value or None, note)."""
+    path = os.path.join(ROOT, "profiles", f"{kind}_{workload}.md")
+    if kern is None or not os.path.exists(path):
+        return None, "no profile"
+    with open(path) as f:
+        for ln in f:
+            parts = ln.strip().strip("`").split()
+            if len(parts) >= 3 and parts[0] == key and parts[1] == kern:
+                sha = parts[3] if len(parts) > 3 else None
+                cur = source_sha(kern)
+                if sha is None or sha != cur:
+                    return None, f"stale: {os.path.basename(path)} measured source {sha}, current {cur}"
+                return float(parts[2]), f"profiles/{kind}_{workload}.md (source {sha})"
+    return None, "kernel not in profile"
 
 
 def measured_traffic(workload, entry):
     """HBM bytes per launch of `entry`'s kernel from the committed counter summary
-    (profiles/traffic_<workload>.md, lines `traffic_bytes <kernel> <bytes>`), or None."""
+    (profiles/traffic_<workload>.md), or None when absent or measured on another source."""
+    v, note = profile_value(workload, "traffic_bytes", TRAFFIC_KERNELS.get(entry))
+    return (None if v is None else int(v)), note
+
+
+XCDS, SIMDS, CUS = 8, 1024, 256   # MI355X: GRBM_GUI_ACTIVE sums the 8 XCDs' counts
+
+
+def _short_kernel(name: str) -> str:
+    import re
+    m = re.match(r"_ZN3moc(\d+)", name)
+    if m:
+        return name[len(m.group(0)):len(m.group(0)) + int(m.group(1))]
+    m = re.search(r"moc::(\w+)", name)
+    return m.group(1) if m else name[:48]
+
+
+def pmc_summary(paths):
+    """Per-kernel means of rocprofv3 --pmc counter_collection.csv files (several passes with
+    different counters may be given): MFMA-busy, VALU-busy and co-issue fractions of the
+    SIMD-cycles of a launch, LDS activity and conflicts, instructions per wave.  Prints a
+    markdown table and the machine-readable lines bench.py reads back (tied to the kernel
+    source's hash)."""
+    import csv
+    from collections import defaultdict
+    per = defaultdict(lambda: defaultdict(dict))
+    grid = {}
+    for p in paths:
+        with open(p) as f:
+            for r in csv.DictReader(f):
+                k = _short_kernel(r["Kernel_Name"])
+                per[k][(p, r["Dispatch_Id"])][r["Counter_Name"]] = float(r["Counter_Value"])
+                grid[k] = int(r["Grid_Size"])
+    rows, lines = [], []
+    for k in sorted(per):
+        acc = defaultdict(list)
+        for c in per[k].values():
+            for n, v in c.items():
+                acc[n].append(v)
+        a = {n: sum(v) / len(v) for n, v in acc.items()}
+        cyc = a.get("GRBM_GUI_ACTIVE", 0.0) / XCDS
+        if cyc <= 0:
+            continue
+        waves = max(1, grid[k] // 64)
+        f = lambda n, scale=1.0, den=SIMDS: (scale * a[n] / (den * cyc)) if n in a else None
+        mb, vb = f("SQ_VALU_MFMA_BUSY_CYCLES"), f("SQ_ACTIVE_INST_VALU", 4.0)
+        co, lds = f("SQ_VALU_MFMA_COEXEC_CYCLES"), f("SQ_LDS_IDX_ACTIVE", den=CUS)
+        conf = (a["SQ_LDS_BANK_CONFLICT"] / a["SQ_LDS_IDX_ACTIVE"]) if a.get("SQ_LDS_IDX_ACTIVE") else None
+        ipw = {n: a[n] / waves for n in ("SQ_INSTS_VALU", "SQ_INSTS_MFMA", "SQ_INSTS_VALU_TRANS_F32", "SQ_INSTS_LDS",
+                                          "SQ_INSTS_SALU") if n in a}
+        fmt = lambda v: "-" if v is None else f"{v:.3f}"
+        rows.append(f"| `{k}` | {len(per[k])} | {cyc / 2400:.1f} | {fmt(mb)} | {fmt(vb)} | {fmt(co)} | {fmt(lds)} | "
+                    f"{fmt(conf)} | " + " / ".join(f"{ipw.get(n, 0):.0f}" for n in
+                                                     ("SQ_INSTS_VALU", "SQ_INSTS_MFMA", "SQ_INSTS_VALU_TRANS_F32",
+                                                      "SQ_INSTS_LDS", "SQ_INSTS_SALU")) + " |")
+        sha = source_sha(k)
+        if sha is None:
+            continue
+        if mb is not None:
+            lines.append(f"    mfma_busy {k} {mb:.4f} {sha}")
+        if vb is not None:
+            lines.append(f"    valu_busy {k} {vb:.4f} {sha}")
+    head = ("| kernel | dispatches | us at 2.4 GHz (GRBM_GUI_ACTIVE / 8) | MFMA busy | VALU busy | MFMA+VALU co-issue | "
+            "LDS active (per CU) | LDS conflicts / access | per wave: VALU (incl. MFMA) / MFMA / TRANS_F32 / LDS / SALU |\n"
+            "|---|---:|---:|---:|---:|---:|---:|---:|---|")
+    return head + "\n" + "\n".join(rows) + "\n\nMachine-readable (read by bench.py):\n\n" + "\n".join(lines)
+
+
+def traffic_fields(workload, entry):
+    v, note = measured_traffic(workload, entry)
+    return {"traffic": v, "traffic_source": note}
+
+
+def counter_fields(workload, entry):
+    """The roofline kernel's MFMA-busy fraction (SQ_VALU_MFMA_BUSY_CYCLES over the SIMD-cycles of
+    the launch) and VALU-busy fraction from the committed SQ counter summary
+    (profiles/counters_<workload>.md), tied to the kernel's source like the traffic."""
     kern = TRAFFIC_KERNELS.get(entry)
-    path = os.path.join(ROOT, "profiles", f"traffic_{workload}.md")
-    if kern is None or not os.path.exists(path):
-        return None
-    with open(path) as f:
-        for ln in f:
-            parts = ln.strip().strip("`").split()
-            if len(parts) == 3 and parts[0] == "traffic_bytes" and parts[1] == kern:
-                return int(parts[2])
-    return None
+    mb, note = profile_value(workload, "mfma_busy", kern, "counters")
+    vb, _ = profile_value(workload, "valu_busy", kern, "counters")
+    return {"mfma_busy": mb, "valu_busy": vb, "counters_source": note}
 
 
 def kernel_table(events, steps):
@@ -221,7 +344,7 @@ def c4_flops(cfg):
     return dict(router=router, q=q, o=o, attn=attn, kv=kv, fwd=fwd, step=3.0 * fwd)
 
 
-def run_c4(args):
+def run_c4(args, losses_timing=True):
     import torch
     from memory_amd.model import TokenRoutedMemoryLayer
     cfg = dict(C4)
@@ -251,12 +374,29 @@ def run_c4(args):
         out, _ = layer(h, bank, return_losses=False)
         out.backward(dout)
 
-    ms, per, _, _ = timed(step, args.steps, args.warmup)
-    losses = router_losses_timing(layer, h, cfg)
+    # distinct chapters of this batch's routing (per-launch bytes of the sparse backward)
+    with torch.no_grad():
+        idx, _, _ = layer.router.route_token_level(h.detach(), return_losses=False,
+                                                   exclude_prefix_chapters=cfg["S"])
+        n_chap = int(torch.unique(idx).numel())
+    ms, per, _, live = timed(step, args.steps, args.warmup, "moc_sparse_bwd")
+    losses = router_losses_timing(layer, h, cfg) if losses_timing else None
     fl = c4_flops(cfg)
     tflops = fl["step"] / (ms * 1e-3) / 1e12
     kernels = {n: {"avg_ms": round(v["avg_ms"], 4), "calls": v["calls_per_step"]}
                for n, v in sorted(per.items(), key=lambda kv: -kv[1]["ms_per_step"])}
+    roofline = None
+    if live:
+        # sparse backward: K and V tiles of the selected (chapter, kv head) units read, their dK and
+        # dV written, q and dO read and dq written once per (token, head)
+        tile = 64 * 64 * 2
+        unit_bytes = n_chap * cfg["HK"] * tile * 2 * 2
+        row_bytes = B * L * H * 64 * 2 * 3
+        alg = unit_bytes + row_bytes
+        ach = alg / (live["avg_ms"] * 1e-3) / 1e9
+        roofline = {"kernel": "moc_sparse_bwd", "bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS,
+                    "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4), **traffic_fields("c4", "moc_sparse_bwd"),
+                    "avg_ms": round(live["avg_ms"], 4), "algorithmic_bytes": alg, "selected_chapters": n_chap}
     return {
         "metric": "token-level memory-xattn fwd+bwd tokens/s (B=4,L=2048,d=768,k=16,T=64)",
         "value": round(B * L / (ms * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
@@ -264,8 +404,8 @@ def run_c4(args):
         "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
         "config": {"workload": "c4: token-level routed memory layer fwd+bwd (v4 MoE combine)", **cfg},
         "tflops": round(tflops, 2), "mfma_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
-        "algorithmic_gflop_per_step": round(fl["step"] / 1e9, 1), "kernels": kernels,
-        "router_losses": losses,
+        "algorithmic_gflop_per_step": round(fl["step"] / 1e9, 1), "roofline": roofline, "kernels": kernels,
+        **({"router_losses": losses} if losses is not None else {}),
     }
 
 
@@ -378,7 +518,7 @@ def run_c5(args):
         ach = (unique_bytes / cfg["layers"]) / (dec["avg_ms"] * 1e-3) / 1e9
         roofline = {"kernel": "moc_decode_partial", "bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS,
                     "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4),
-                    "traffic": measured_traffic("c5", "moc_decode_partial"),
+                    **traffic_fields("c5", "moc_decode_partial"),
                     "avg_ms": round(dec["avg_ms"], 4), "algorithmic_bytes": unique_bytes / cfg["layers"]}
     kernels = {n: {"avg_ms": round(v["avg_ms"], 4), "calls": v["calls_per_step"]}
                for n, v in sorted(per.items(), key=lambda kv: -kv[1]["ms_per_step"])}
@@ -484,7 +624,7 @@ def run_c3opt(args):
         ach = per_launch / (live["avg_ms"] * 1e-3) / 1e9
         roofline = {"kernel": "moc_bank_adamw", "bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS,
                     "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4),
-                    "traffic": measured_traffic("c3opt", "moc_bank_adamw"),
+                    **traffic_fields("c3opt", "moc_bank_adamw"),
                     "avg_ms": round(live["avg_ms"], 4), "algorithmic_bytes": int(per_launch)}
     return {
         "metric": "memory-layer training step tokens/s incl. clip + bank AdamW (L=1024,d=768,k=64,T=64)",
@@ -576,10 +716,17 @@ def main():
     ap.add_argument("--variants", default="reference_style,bank_adamw_dense,bank_adamw",
                     help="c3opt: which optimizer variants to run (comma-separated)")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
+    ap.add_argument("--headline-only", action="store_true",
+                    help="c3: skip the c5 decode and c4 token-level lines that ride along the headline")
+    ap.add_argument("--pmc-summary", nargs="+", metavar="CSV",
+                    help="print the per-kernel summary of rocprofv3 --pmc counter_collection.csv files and exit")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="run one plain 256 MiB device copy before the warmup: the reference kernel "
                          "that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes")
     args = ap.parse_args()
+    if args.pmc_summary:
+        print(pmc_summary(args.pmc_summary))
+        return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); "
               "the path shards by sequence with no exchange in the forward, see DESIGN.md", file=sys.stderr)
@@ -625,7 +772,7 @@ def main():
         ach = fl[flop_key[dom]] / (live["avg_ms"] * 1e-3) / 1e12
         roofline = {"kernel": dom, "bound": "mfma", "achieved": round(ach, 2), "peak": MFMA_BF16_PEAK_TFLOPS,
                     "unit": "TFLOP/s", "frac": round(ach / MFMA_BF16_PEAK_TFLOPS, 4),
-                    "traffic": measured_traffic("c3", dom),
+                    **traffic_fields("c3", dom), **counter_fields("c3", dom),
                     "avg_ms": round(live["avg_ms"], 4), "algorithmic_flop": fl[flop_key[dom]]}
     kernels = {}
     for n, v in sorted(per_kernel.items(), key=lambda kv: -kv[1]["ms_per_step"]):
@@ -637,6 +784,20 @@ def main():
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(cfg, args.cpu_budget)
+
+    # the other GPU workloads of BASELINE, timed in the same run (their own lines via --workload)
+    others = {}
+    if not args.headline_only:
+        del layer, h, bank, dout
+        torch.cuda.empty_cache()
+        for name, fn in (("c5", run_c5), ("c4", lambda a: run_c4(a, losses_timing=False))):
+            sub = fn(args)
+            others[name] = {k: sub[k] for k in ("metric", "value", "unit", "ms_per_step", "config", "roofline")
+                            if k in sub}
+            for k in ("graph_replay", "hbm_frac", "tflops", "mfma_frac"):
+                if k in sub:
+                    others[name][k] = sub[k]
+            torch.cuda.empty_cache()
 
     line = {
         "metric": "memory-xattn fwd+bwd tokens/s & %MFMA peak (L=1024,d=768,k=64,T=64)",
@@ -662,6 +823,7 @@ def main():
         "roofline": roofline,
         "kernels": kernels,
         "cpu_baseline": cpu,
+        **others,
     }
     print(json.dumps(line), flush=True)
 

@@ -148,6 +148,31 @@ def call(name: str, *args) -> None:
         raise MocError(f"{name} failed ({rc}): {msg}")
 
 
+class region:
+    """``with region(name): ...`` records a pair of events around work that is not a libmoc
+    entry point (a library GEMM, a torch op) under the same rules as ``call``, so that the
+    per-kernel table accounts for the whole step."""
+
+    def __init__(self, name: str):
+        self.name = name
+        self.ev = None
+
+    def __enter__(self):
+        ev = KERNEL_EVENTS
+        if ev is not None and (KERNEL_EVENTS_ONLY is None or self.name in KERNEL_EVENTS_ONLY):
+            self.ev = ev
+            self.e0 = torch.cuda.Event(enable_timing=True)
+            self.e0.record()
+        return self
+
+    def __exit__(self, *exc):
+        if self.ev is not None:
+            e1 = torch.cuda.Event(enable_timing=True)
+            e1.record()
+            self.ev.setdefault(self.name, []).append((self.e0, e1))
+        return False
+
+
 def query(name: str, *args):
     return getattr(lib(), name)(*args)
 

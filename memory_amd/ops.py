@@ -267,14 +267,18 @@ class _Linear(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, w):
         ctx.save_for_backward(x, w)
-        return linear_rows(x, w) if _few_rows(x, w) else F.linear(x, w)
+        if _few_rows(x, w):
+            return linear_rows(x, w)
+        with L.region("lib_linear_fwd"):
+            return F.linear(x, w)
 
     @staticmethod
     def backward(ctx, dy):
         x, w = ctx.saved_tensors
         dx = dw = None
         if ctx.needs_input_grad[0]:
-            dx = torch.matmul(dy, w)
+            with L.region("lib_linear_dx"):
+                dx = torch.matmul(dy, w)
         if ctx.needs_input_grad[1]:
             n_out, n_in = w.shape
             dy2 = dy.reshape(-1, n_out).contiguous()
@@ -316,10 +320,11 @@ class _LinearResidual(torch.autograd.Function):
         n_out = w.shape[0]
         x2 = x.reshape(-1, x.shape[-1])
         r2 = residual.reshape(-1, n_out)
-        if residual.dtype == x.dtype == w.dtype:
-            out = torch.addmm(r2, x2, w.t())
-        else:
-            out = r2 + F.linear(x2, w)
+        with L.region("lib_linear_fwd"):
+            if residual.dtype == x.dtype == w.dtype:
+                out = torch.addmm(r2, x2, w.t())
+            else:
+                out = r2 + F.linear(x2, w)
         return out.view(residual.shape)
 
     @staticmethod
@@ -332,7 +337,8 @@ class _LinearResidual(torch.autograd.Function):
             dres = dy
         g = dy2.to(x.dtype).contiguous()
         if ctx.needs_input_grad[0]:
-            dx = torch.matmul(g, w.to(x.dtype)).view(x.shape)
+            with L.region("lib_linear_dx"):
+                dx = torch.matmul(g, w.to(x.dtype)).view(x.shape)
         if ctx.needs_input_grad[1]:
             dw = linear_wgrad(g, x.reshape(-1, n_in).contiguous(), w.dtype)
         return dx, dw, dres
@@ -461,7 +467,8 @@ class _RoutedAttention(torch.autograd.Function):
         X = torch.empty(plan.max_u * T, bank.shape[1], device=q.device, dtype=dtype)
         call("moc_gather_rows", L.dtype_code(dtype), ptr(bank), L.dtype_code(bank.dtype), bank.shape[1], T,
              ptr(plan.uniq), ptr(plan.n_uniq), plan.max_u, ptr(mean), ptr(rstd), ptr(X), stream_ptr(q.device))
-        kv = F.linear(X, wkv)
+        with L.region("lib_kv_project_gemm"):
+            kv = F.linear(X, wkv)
         del X
         kvl = kv_rows_layout(kv, T, HK, Dh)
         om = omega.float().contiguous()
@@ -526,7 +533,8 @@ class _RoutedAttention(torch.autograd.Function):
                 dwk = dwkv[:KV].to(wk_dtype) if need_wk else None
                 dwv = dwkv[KV:].to(wv_dtype) if need_wv else None
             if need_bank:
-                dX = torch.matmul(dkv_edge, wkv)  # rows of skipped edges are never read
+                with L.region("lib_kv_dx_gemm"):
+                    dX = torch.matmul(dkv_edge, wkv)  # rows of skipped edges are never read
                 if ctx.row_grad is not None:
                     ctx.row_grad.accumulate(dX, bank, uniq, n_uniq, max_u, csr_off, csr_edge, mean, rstd, norm)
                 else:

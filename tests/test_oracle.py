@@ -118,6 +118,50 @@ def test_router_losses_closed_forms():
     assert abs(float(tot) - (0.01 * k + 0.001 * math.log(C) ** 2)) < 1e-12
 
 
+def test_router_losses_one_hot_peaked_closed_form():
+    """Rows whose probabilities are one-hot up to e^-60 at column c_r: mean_r p^2 per column is
+    n_c / R (n_c = rows peaked at c), so auxiliary = mean_c (n_c / R - 1 / C)^2 -- a swap of the
+    square and the row mean, (mean_r p)^2 = (n_c / R)^2, fails it; load balance =
+    C sum_c f_c n_c / R with f_c = selections of c per row averaged over rows; entropy -> 0;
+    z_loss = mean_r (60 + log(1 + (C - 1) e^-60))^2."""
+    C, R = 7, 10
+    peaks = torch.tensor([0, 0, 0, 1, 1, 2, 3, 3, 3, 3])
+    logits = torch.zeros(R, C)
+    logits[torch.arange(R), peaks] = 60.0
+    probs = F.softmax(logits, -1)
+    idx = torch.stack([peaks, (peaks + 2) % C], dim=1)          # each row selects its peak and one more
+    L = O.router_losses(logits, probs, idx, C)
+    n = torch.bincount(peaks, minlength=C).double()
+    aux = float(((n / R - 1.0 / C) ** 2).mean())
+    assert abs(float(L["auxiliary"]) - aux) < 1e-12
+    swapped = float(((n / R) ** 2 - 1.0 / C).pow(2).mean())
+    assert abs(swapped - aux) > 1e-3                           # the pin tells the two apart
+    f = (torch.bincount(idx[:, 0], minlength=C) + torch.bincount(idx[:, 1], minlength=C)).double() / R
+    assert abs(float(L["load_balance"]) - C * float((f * n / R).sum())) < 1e-12
+    assert float(L["entropy"]) < 1e-20
+    lse = 60.0 + math.log1p((C - 1) * math.exp(-60.0))
+    assert abs(float(L["z_loss"]) - lse ** 2) < 1e-9
+
+
+def test_sparse_unweighted_same_chapters_is_dense_attention():
+    """Every token selecting the same chapters: the joint softmax over their keys is plain
+    (textbook) attention over those rows, here torch's scaled_dot_product_attention."""
+    g = _rng(17)
+    B, Tq, HQ, HK, D, BS, M = 2, 9, 4, 2, 8, 4, 6
+    q = torch.randn(B, Tq, HQ, D, generator=g)
+    k = torch.randn(B, M * BS, HK, D, generator=g)
+    v = torch.randn(B, M * BS, HK, D, generator=g)
+    chosen = torch.tensor([4, 1, 3])
+    idx = chosen.view(1, 1, 1, -1).expand(B, Tq, HK, 3)
+    sc = 0.37
+    got = O.sparse_attention_unweighted(q, k, v, idx, BS, sc)
+    rows = (chosen.view(-1, 1) * BS + torch.arange(BS)).reshape(-1)
+    kk = k[:, rows].repeat_interleave(HQ // HK, dim=2).transpose(1, 2)     # (B, HQ, keys, D)
+    vv = v[:, rows].repeat_interleave(HQ // HK, dim=2).transpose(1, 2)
+    want = F.scaled_dot_product_attention(q.transpose(1, 2), kk, vv, scale=sc).transpose(1, 2)
+    assert torch.allclose(got, want, atol=1e-12)
+
+
 def test_select_from_probs_equals_route():
     g = _rng(5)
     logits = torch.randn(4, 21, generator=g)
