@@ -36,6 +36,18 @@ constexpr int kTch = 64;
 constexpr float kRescaleSlack = 8.f;
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ __forceinline__ float max3f(float a, float b, float c) { return fmax_fast(fmax_fast(a, b), c); }
+// max over the lanes {l, l^16, l^32, l^48} (the four row groups of a 16x16 accumulator column)
+// with the gfx950 row-swap permutes.  v_permlane16_swap_b32 a, b swaps the odd 16-lane rows of
+// a with the even rows of b (v_permlane32_swap_b32: the upper 32 lanes of a with the lower 32 of
+// b); from two copies of v it leaves v's partner-row values in one of the copies.
+__device__ __forceinline__ float quad_max_pl(float v) {
+  float a = v, b = v;
+  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+  float c = fmax_fast(a, b), d = c;
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(c), "+v"(d));
+  return fmax_fast(c, d);
+}
 
 template <typename T>
 __global__ __launch_bounds__(kFwdThreads) void xattn_fwd_kernel(
@@ -75,6 +87,7 @@ __global__ __launch_bounds__(kFwdThreads) void xattn_fwd_kernel(
 
   float m[2] = {-INFINITY, -INFINITY};
   float lsum[2] = {0.f, 0.f};  // row sums of p (in units of exp2(m)), complete per lane
+  float pend_ls[2] = {0.f, 0.f}, pend_rw = 0.f;   // last chapter's row sums, not yet folded in
   // all-ones A operand: the MFMA with it sums a P~^T fragment over its 32 keys, which
   // takes the row sums off the VALU (the sums use the same rounded P~ as O)
   F8 ones;
@@ -135,17 +148,25 @@ __global__ __launch_bounds__(kFwdThreads) void xattn_fwd_kernel(
           for (int qb = 0; qb < 2; ++qb) mma(st[kb][qb], a, qf[qb][ks]);
         }
       }
-      // chapter max per row, lazy update of the reference max
+      // the previous chapter's row sums (their MFMA has long completed): folded in before any
+      // rescale, in units of the reference max they were taken against
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb) lsum[qb] += pend_ls[qb] * pend_rw;
+      pend_rw = 0.f;
+      // chapter max per row (three-input max chains), lazy update of the reference max
       float cm[2];
       bool grow = false;
 #pragma unroll
       for (int qb = 0; qb < 2; ++qb) {
-        float mx = fmax_fast(fmax_fast(st[0][qb][0], st[0][qb][1]), fmax_fast(st[0][qb][2], st[0][qb][3]));
-#pragma unroll
-        for (int kb = 1; kb < 4; ++kb)
-          mx = fmax_fast(mx, fmax_fast(fmax_fast(st[kb][qb][0], st[kb][qb][1]),
-                                       fmax_fast(st[kb][qb][2], st[kb][qb][3])));
-        cm[qb] = quad_max(mx) * c;  // c >= 0 (router weights are non-negative)
+        float mx = max3f(st[0][qb][0], st[0][qb][1], st[0][qb][2]);
+        mx = max3f(mx, st[0][qb][3], st[1][qb][0]);
+        mx = max3f(mx, st[1][qb][1], st[1][qb][2]);
+        mx = max3f(mx, st[1][qb][3], st[2][qb][0]);
+        mx = max3f(mx, st[2][qb][1], st[2][qb][2]);
+        mx = max3f(mx, st[2][qb][3], st[3][qb][0]);
+        mx = max3f(mx, st[3][qb][1], st[3][qb][2]);
+        mx = fmax_fast(mx, st[3][qb][3]);
+        cm[qb] = quad_max_pl(mx) * c;  // c >= 0 (router weights are non-negative)
         grow |= cm[qb] > m[qb] + kRescaleSlack;
       }
       if (__any(grow)) {
@@ -162,8 +183,8 @@ __global__ __launch_bounds__(kFwdThreads) void xattn_fwd_kernel(
       F8 pf[2][2];
       if (w > 0.f) {
         // p~ = w * exp2(s*c - m): w folded into the exponent; the row sum needs sum(p~) / w
-        const float lw = __log2f(w);
-        const float rw = 1.f / w;
+        const float lw = __builtin_amdgcn_logf(w);
+        const float rw = __builtin_amdgcn_rcpf(w);
 #pragma unroll
         for (int qb = 0; qb < 2; ++qb) {
           const float off = m[qb] - lw;
@@ -177,8 +198,9 @@ __global__ __launch_bounds__(kFwdThreads) void xattn_fwd_kernel(
           f32x4 ls = f32x4{0.f, 0.f, 0.f, 0.f};
           mma(ls, ones, pf[qb][0]);
           mma(ls, ones, pf[qb][1]);
-          lsum[qb] += ls[0] * rw;
+          pend_ls[qb] = ls[0];   // folded in at the next chapter (no wait on this MFMA here)
         }
+        pend_rw = rw;
         // O^T[db][qb] += V^T(dims 16*db + c16, keys) * P~^T
 #pragma unroll
         for (int ks2 = 0; ks2 < 2; ++ks2) {
@@ -203,6 +225,8 @@ __global__ __launch_bounds__(kFwdThreads) void xattn_fwd_kernel(
     __syncthreads();
   }
 
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb) lsum[qb] += pend_ls[qb] * pend_rw;
   // lse rows have stride Lp = round_up(L, 128); padded entries hold +inf so
   // that the backward's exp2(s - lse) is exactly 0 there (also for a row
   // whose every slot was skipped).
