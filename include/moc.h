@@ -122,6 +122,15 @@ size_t moc_chapter_plan_workspace(int64_t E, int64_t C);
 int moc_chapter_plan(const int32_t* chap, int64_t E, int64_t C, void* workspace, size_t workspace_bytes,
                      int32_t* uniq, int32_t* n_uniq, int32_t* edge_u, int32_t* csr_off, int32_t* csr_edge,
                      hipStream_t stream);
+/* moc_chapter_plan without a caller workspace and without allocating: no counterpart in the
+ * reference; for callers that cannot allocate device memory (code under HIP graph capture,
+ * serving loops, harnesses that forbid hipMalloc).  The workspace is a fixed 4 MiB device array
+ * of the library (one per GPU, held until the process ends), so E and C are limited to
+ * moc_chapter_plan_workspace(E, C) <= 4 MiB (e.g. E <= 258,048 edges over 4,097 chapters);
+ * larger plans return MOC_ERR_UNSUPPORTED.  Every call on a GPU shares that array: calls that
+ * overlap on one GPU (concurrent streams) race and must not be issued. */
+int moc_chapter_plan_noalloc(const int32_t* chap, int64_t E, int64_t C, int32_t* uniq, int32_t* n_uniq,
+                             int32_t* edge_u, int32_t* csr_off, int32_t* csr_edge, hipStream_t stream);
 
 /* --------------------------------------------------- gather + K/V projection */
 

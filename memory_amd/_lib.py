@@ -46,6 +46,7 @@ _SIGS = {
     "moc_router_losses_bwd": (_I, [_P, _I64, _I64, _P, _P, _P, _P, _P]),
     "moc_chapter_plan_workspace": (_SZ, [_I64, _I64]),
     "moc_chapter_plan": (_I, [_P, _I64, _I64, _P, _SZ, _P, _P, _P, _P, _P, _P]),
+    "moc_chapter_plan_noalloc": (_I, [_P, _I64, _I64, _P, _P, _P, _P, _P, _P]),
     "moc_row_stats": (_I, [_P, _I, _I64, _I, _P, _P, _I64, _I, _F, _P, _P, _P]),
     "moc_kv_project": (_I, [_I, _P, _I, _I64, _I, _P, _P, _I64, _P, _P, _P, _I, _I, _P, _P, _P, _P, _P]),
     "moc_xattn_fwd": (_I, [_I, _P, _P, _P, _I64, _I64, _I, _I, _P, _P, _I64, _I64, _I, _I, _I, _I, _I, _F, _P, _P,

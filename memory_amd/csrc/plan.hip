@@ -17,6 +17,8 @@
 // argsort on (b*H + h)*M + chapter (kernels-final/kernel_v4.py:213-257).
 #include "moc_common.h"
 
+#include <mutex>
+
 namespace moc {
 
 constexpr int kPlanEdgesPerBlock = 1024;
@@ -195,27 +197,42 @@ __global__ __launch_bounds__(1024) void plan_small_kernel(const int32_t* __restr
   }
 }
 
-}  // namespace moc
+// Workspace of moc_chapter_plan_noalloc: a fixed device array (each GPU holds its own copy for
+// the life of the process).  Host code never passes `scratch` itself to a kernel -- in host
+// code the name is a stand-in, not a device address -- but the address hipGetSymbolAddress
+// returns for the current device, looked up once per device and kept.
+constexpr size_t kPlanScratchBytes = (size_t)4 << 20;
+static __device__ __align__(256) unsigned char scratch[kPlanScratchBytes];
 
-using namespace moc;
+constexpr int kPlanMaxDevices = 64;
+static std::mutex scratch_mu;
+static void* scratch_ptr[kPlanMaxDevices];
 
-extern "C" {
+// This device's address of `scratch` (looked up on the first call on the device).
+static int plan_scratch(void** out) {
+  int dev = 0;
+  MOC_HIP(hipGetDevice(&dev));
+  MOC_REQUIRE(dev >= 0 && dev < kPlanMaxDevices, MOC_ERR_UNSUPPORTED, "moc_chapter_plan_noalloc: device %d", dev);
+  std::lock_guard<std::mutex> lock(scratch_mu);
+  if (!scratch_ptr[dev]) {
+    void* p = nullptr;
+    MOC_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    MOC_REQUIRE(p != nullptr, MOC_ERR_LAUNCH, "moc_chapter_plan_noalloc: no device address for the scratch array");
+    scratch_ptr[dev] = p;
+  }
+  *out = scratch_ptr[dev];
+  return MOC_OK;
+}
 
-size_t moc_chapter_plan_workspace(int64_t E, int64_t C) {
+size_t plan_workspace_bytes(int64_t E, int64_t C) {
   const int64_t G = (E + kPlanEdgesPerBlock - 1) / kPlanEdgesPerBlock;
   // counts[G][C] + total[C] + start[C] + uid[C]
   return (size_t)(G * C + 3 * C) * sizeof(int32_t);
 }
 
-int moc_chapter_plan(const int32_t* chap, int64_t E, int64_t C, void* workspace, size_t workspace_bytes,
-                     int32_t* uniq, int32_t* n_uniq, int32_t* edge_u, int32_t* csr_off, int32_t* csr_edge,
-                     hipStream_t stream) {
-  MOC_REQUIRE(chap && workspace && uniq && n_uniq && edge_u && csr_off && csr_edge, MOC_ERR_ARG,
-              "moc_chapter_plan: null pointer");
-  MOC_REQUIRE(E > 0 && E < (int64_t)1 << 31, MOC_ERR_ARG, "moc_chapter_plan: E=%lld out of range", (long long)E);
-  MOC_REQUIRE(C > 0 && C <= kPlanMaxC, MOC_ERR_UNSUPPORTED, "moc_chapter_plan: C=%lld not in [1, %d]", (long long)C,
-              kPlanMaxC);
-  MOC_REQUIRE(workspace_bytes >= moc_chapter_plan_workspace(E, C), MOC_ERR_ARG, "moc_chapter_plan: workspace too small");
+// The plan's kernels on a given workspace (every word of it is written before it is read).
+int plan_launch(const int32_t* chap, int64_t E, int64_t C, void* workspace, int32_t* uniq, int32_t* n_uniq,
+                int32_t* edge_u, int32_t* csr_off, int32_t* csr_edge, hipStream_t stream) {
   if (E <= kPlanSmallE && C <= kPlanSmallC) {
     hipLaunchKernelGGL(plan_small_kernel, dim3(1), dim3(1024), 2 * (size_t)C * sizeof(int32_t), stream, chap, E, C,
                        uniq, n_uniq, edge_u, csr_off, csr_edge);
@@ -236,6 +253,44 @@ int moc_chapter_plan(const int32_t* chap, int64_t E, int64_t C, void* workspace,
   if ((rc = check_launch("plan_scan_kernel"))) return rc;
   hipLaunchKernelGGL(plan_place_kernel, dim3(G), dim3(256), 0, stream, chap, E, C, counts, start, uid, edge_u, csr_edge);
   return check_launch("plan_place_kernel");
+}
+
+}  // namespace moc
+
+using namespace moc;
+
+extern "C" {
+
+size_t moc_chapter_plan_workspace(int64_t E, int64_t C) { return plan_workspace_bytes(E, C); }
+
+int moc_chapter_plan(const int32_t* chap, int64_t E, int64_t C, void* workspace, size_t workspace_bytes,
+                     int32_t* uniq, int32_t* n_uniq, int32_t* edge_u, int32_t* csr_off, int32_t* csr_edge,
+                     hipStream_t stream) {
+  MOC_REQUIRE(chap && workspace && uniq && n_uniq && edge_u && csr_off && csr_edge, MOC_ERR_ARG,
+              "moc_chapter_plan: null pointer");
+  MOC_REQUIRE(E > 0 && E < (int64_t)1 << 31, MOC_ERR_ARG, "moc_chapter_plan: E=%lld out of range", (long long)E);
+  MOC_REQUIRE(C > 0 && C <= kPlanMaxC, MOC_ERR_UNSUPPORTED, "moc_chapter_plan: C=%lld not in [1, %d]", (long long)C,
+              kPlanMaxC);
+  MOC_REQUIRE(workspace_bytes >= moc_chapter_plan_workspace(E, C), MOC_ERR_ARG, "moc_chapter_plan: workspace too small");
+  return plan_launch(chap, E, C, workspace, uniq, n_uniq, edge_u, csr_off, csr_edge, stream);
+}
+
+int moc_chapter_plan_noalloc(const int32_t* chap, int64_t E, int64_t C, int32_t* uniq, int32_t* n_uniq,
+                             int32_t* edge_u, int32_t* csr_off, int32_t* csr_edge, hipStream_t stream) {
+  MOC_REQUIRE(chap && uniq && n_uniq && edge_u && csr_off && csr_edge, MOC_ERR_ARG,
+              "moc_chapter_plan_noalloc: null pointer");
+  MOC_REQUIRE(E > 0 && E < (int64_t)1 << 31, MOC_ERR_ARG, "moc_chapter_plan_noalloc: E=%lld out of range",
+              (long long)E);
+  MOC_REQUIRE(C > 0 && C <= kPlanMaxC, MOC_ERR_UNSUPPORTED, "moc_chapter_plan_noalloc: C=%lld not in [1, %d]",
+              (long long)C, kPlanMaxC);
+  const size_t need = plan_workspace_bytes(E, C);
+  MOC_REQUIRE(need <= kPlanScratchBytes, MOC_ERR_UNSUPPORTED,
+              "moc_chapter_plan_noalloc: E=%lld edges over C=%lld chapters need %zu bytes of workspace, more than "
+              "the %zu-byte fixed scratch (use moc_chapter_plan with a caller workspace)",
+              (long long)E, (long long)C, need, kPlanScratchBytes);
+  void* ws = nullptr;
+  if (int rc = plan_scratch(&ws)) return rc;
+  return plan_launch(chap, E, C, ws, uniq, n_uniq, edge_u, csr_off, csr_edge, stream);
 }
 
 }  // extern "C"
