@@ -154,6 +154,40 @@ int moc_kv_project(int dtype, const void* bank, int bank_dtype, int64_t d, int T
                    const void* wkv, int HK, int Dh, void* k_tiles, void* v_tiles, void* kt_tiles, void* vt_tiles,
                    hipStream_t stream);
 
+/* K/V projection of the plan's distinct chapters on the matrix cores, the gather fused into the
+ * operand loads: y[c*64 + j][n] = sum_k X_c[j][k] * w[n][k] for c < n_uniq, j < 64, where
+ * X_c is bank rows uniq[c]*64 .. +63 (gather != 0; rows = the bank) or rows c*64 .. +63 of a
+ * contiguous block (gather == 0; e.g. moc_gather_rows output).  rows bf16 with row stride ld
+ * elements, w [N][K] bf16 (= [Wk; Wv], N = 2*HK*Dh), y [max_u*64][ldy] bf16; rows of plan slots
+ * >= n_uniq are not written.  Replaces ChapteredMemoryBank.get_chapters_batched
+ * (memory_transformer/memory_bank.py:263-293) followed by k_proj / v_proj of
+ * MemoryCrossAttention._compute_qkv (memory_attention.py:241-243), once per distinct chapter;
+ * the result is the "projection rows" K / V layout of moc_xattn_fwd.  N % 256 == 0,
+ * K % 64 == 0, T == 64. */
+int moc_chapter_project(const void* rows, int64_t ld, int gather, const int32_t* uniq, const int32_t* n_uniq,
+                        int64_t max_u, const void* w, int N, int K, void* y, int64_t ldy, hipStream_t stream);
+/* Input gradient of that projection summed over each chapter's edges and stored per chapter:
+ * out_c = (sum over the chapter's edges e, csr order, of dkv_edge rows e*64 .. +63) w_t^T, i.e.
+ * out_c[j][n] = sum_k dK|dV_c[j][k] * w_t[n][k] with w_t [N = d][K = 2*HK*Dh] = [Wk; Wv]^T
+ * (moc_weight_pack).  dkv_edge [E*64][ld] bf16 from moc_xattn_bwd_dkv; chapters with several
+ * edges are summed first (fp32, rounded to bf16) into red [max_u*64][ld] bf16 (workspace).
+ * out_bank_rows != 0: out is the dense bank gradient [N_m][ldo] and chapter c's rows are stored
+ * at uniq[c]*64 .. +63 (the scatter-add of the gather's backward, memory_bank.py:287-291:
+ * distinct chapters own distinct rows, so they are stored; the rest must be zero already);
+ * out_bank_rows == 0: out [max_u*64][ldo], chapter c at rows c*64 .. (for a normalised bank or
+ * a row-sparse gradient, finished by moc_bank_scatter / moc_bank_grad_accumulate without csr).
+ * out_dtype MOC_BF16 or MOC_F32.  Replaces the autograd input gradient of k_proj / v_proj
+ * (memory_attention.py:241-243) through get_chapters_batched (memory_bank.py:263-293). */
+int moc_chapter_dx(const void* dkv_edge, int64_t ld, const int32_t* uniq, const int32_t* n_uniq, int64_t max_u,
+                   const int32_t* csr_off, const int32_t* csr_edge, void* red, const void* w_t, int N, int K,
+                   int out_dtype, void* out, int64_t ldo, int out_bank_rows, hipStream_t stream);
+/* wkv [2*kv][d] bf16 = [wk; wv] and / or wkv_t [d][2*kv] bf16 = its transpose (either may be
+ * NULL), from wk, wv [kv][d] of MOC_F32 / MOC_BF16: the concatenated K/V weight that the
+ * chapter GEMMs read (the reference keeps k_proj and v_proj as two nn.Linear,
+ * memory_transformer/memory_attention.py:140-143). */
+int moc_weight_pack(const void* wk, int wk_dtype, const void* wv, int wv_dtype, int64_t kv, int64_t d, void* wkv,
+                    void* wkv_t, hipStream_t stream);
+
 /* ------------------------------------------------- routed attention forward */
 
 /* Replaces MemoryCrossAttention._attention on omega-weighted gathered memory

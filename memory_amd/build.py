@@ -68,6 +68,15 @@ def build(verbose: bool = False, jobs: int | None = None) -> str:
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stdout}\n{res.stderr}")
+    # a kernel template whose host-side stub was not emitted links fine but cannot launch;
+    # refuse such a library here rather than at the first launch on a GPU
+    nm = shutil.which("nm")
+    if nm:
+        res = subprocess.run([nm, "-u", tmp], capture_output=True, text=True)
+        missing = [ln.split()[-1] for ln in res.stdout.splitlines() if "__device_stub__" in ln]
+        if missing:
+            os.remove(tmp)
+            raise RuntimeError("kernel launch stubs missing from the host code: " + ", ".join(missing))
     os.replace(tmp, LIB)
     if verbose:
         print(f"built {LIB}")

@@ -1,0 +1,393 @@
+// Chapter-block GEMMs of the K/V path on the matrix cores.
+//
+//   Y_c[j, n] = sum_k X_c[j, k] * W[n, k]      for every distinct chapter c < n_uniq, j < 64
+//
+// X_c is a block of 64 rows chosen per chapter (the chapter's bank rows, a contiguous block, or
+// the chapter's per-edge dK/dV rows), W is [N][K] bf16, and Y_c is stored to a block chosen per
+// chapter (contiguous projection rows, or the chapter's rows of the bank gradient).  Two uses:
+//
+//  * moc_chapter_project: K/V projection of the distinct chapters, gather fused into the operand
+//    loads (memory_transformer/memory_bank.py:263-293 get_chapters_batched, then k_proj / v_proj
+//    of memory_attention.py:241-243 with W = [Wk; Wv]).  The router weight omega is applied
+//    inside attention ((omega x) W^T = omega (x W^T)), so one projected chapter serves every
+//    sequence that selected it.
+//  * moc_chapter_dx: the input gradient of that projection summed over a chapter's edges and
+//    stored into the chapter's bank rows (the autograd of k_proj / v_proj followed by the
+//    scatter-add of the gather's backward, memory_bank.py:287-291): W = [Wk; Wv]^T, X_c = the
+//    chapter's dK|dV rows (one edge) or their sum (several edges, summed beforehand by
+//    dkv_multi_reduce_kernel), stores straight into the dense bank gradient (distinct chapters
+//    own distinct rows, so no atomics).
+//
+// Kernel design (gfx950): a persistent grid of one 512-thread workgroup per CU walks a list of
+// 256 (features) x BM (rows) output tiles.  Each XCD (workgroups are dealt round-robin to the 8
+// XCDs) takes a contiguous range of tiles, feature blocks fastest, so the feature tiles of one
+// row block share its X rows in that XCD's L2.  Operands move global -> LDS with
+// buffer_load ... lds (no VGPR staging), 64 k-columns per stage, two stages in flight; the
+// 16-byte chunks of every LDS row are XOR-swizzled by (row & 7) so fragment reads are
+// conflict-free.  8 waves in a 4 (features) x 2 (rows) grid; each wave owns 64 features x BM/2
+// rows (v_mfma_f32_16x16x32_bf16, fp32 accumulators in VGPRs).  The W tile's rows sit in LDS in a
+// permuted order (row 32b + 16h + 4g + e holds feature 32b + 8g + 4h + e) so that a lane's
+// accumulators of two adjacent MFMA tiles are 8 consecutive features of one row: the epilogue
+// writes every output row piece with one 16-byte store (bf16) straight from registers.
+#include "moc_common.h"
+
+namespace moc {
+namespace {
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+constexpr int kCgThreads = 512;
+constexpr int kCgStageW = 256 * 128;  // LDS bytes of one W stage (256 rows x 64 bf16)
+constexpr int kCgDxRows = 128;        // row tile of the dX GEMM (N = d is 3 feature tiles at d = 768)
+
+enum { CG_SRC_GATHER = 0, CG_SRC_CONTIG = 1, CG_SRC_EDGE = 2 };
+enum { CG_DST_CONTIG = 0, CG_DST_BANK = 1 };
+
+__device__ __forceinline__ int cg_perm(int r) {
+  return (r & ~31) | (((r >> 2) & 3) << 3) | (((r >> 4) & 1) << 2) | (r & 3);
+}
+
+__device__ __forceinline__ int rfl(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+// buffer resource over `bytes` bytes at p (raw buffer, bounds-checked; a macro, since the
+// host pass of the kernel templates cannot take the resource type through a function)
+#define CG_RSRC(p, bytes) \
+  __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>((const void*)(p)), (short)0, (int)(bytes), 0x00020000)
+
+// s_waitcnt vmcnt(0) (gfx9 encoding: vmcnt[3:0], expcnt[6:4], lgkmcnt[11:8], vmcnt_hi[15:14])
+__device__ __forceinline__ void cg_wait_vm0() { __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8)); }
+
+template <int SRC>
+__device__ __forceinline__ const bf16* cg_src_rows(int c, const bf16* __restrict__ x, const bf16* __restrict__ xred,
+                                                   int64_t ldx, const int32_t* __restrict__ uniq,
+                                                   const int32_t* __restrict__ csr_off,
+                                                   const int32_t* __restrict__ csr_edge) {
+  if constexpr (SRC == CG_SRC_GATHER) {
+    return x + (int64_t)rfl(uniq[c]) * 64 * ldx;
+  } else if constexpr (SRC == CG_SRC_CONTIG) {
+    return x + (int64_t)c * 64 * ldx;
+  } else {
+    const int p0 = rfl(csr_off[c]), cnt = rfl(csr_off[c + 1]) - p0;
+    return cnt == 1 ? x + (int64_t)rfl(csr_edge[p0]) * 64 * ldx : xred + (int64_t)c * 64 * ldx;
+  }
+}
+
+template <int SRC, int DST, typename TO, int BM>
+__global__ __launch_bounds__(kCgThreads) void chapter_gemm_kernel(
+    const bf16* __restrict__ x, const bf16* __restrict__ xred, int64_t ldx, const int32_t* __restrict__ uniq,
+    const int32_t* __restrict__ n_uniq, const int32_t* __restrict__ csr_off, const int32_t* __restrict__ csr_edge,
+    int64_t max_u, const bf16* __restrict__ w, int N, int K, TO* __restrict__ y, int64_t ldy) {
+  constexpr int CPT = BM / 64;              // chapters per tile
+  constexpr int IPX = BM / 64;              // X DMA instructions per thread per stage
+  constexpr int JB = BM / 32;               // 16-row MFMA tiles per wave
+  constexpr int STX = BM * 128;             // LDS bytes of one X stage
+  __shared__ __attribute__((aligned(1024))) char smem[2 * kCgStageW + 2 * STX];
+  char* const sW = smem;
+  char* const sX = smem + 2 * kCgStageW;
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = rfl(tid >> 6);
+  const int nu = rfl((int)min((int64_t)n_uniq[0], max_u));
+  const int NB = N >> 8;
+  const int V = ((nu + CPT - 1) / CPT) * NB;  // tiles: row blocks x feature blocks
+  const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3, nslot = gridDim.x >> 3;
+  const int lo = (int)(((int64_t)xcd * V) >> 3), hi = (int)(((int64_t)(xcd + 1) * V) >> 3);
+  const int nmine = hi - lo > slot ? (hi - lo - slot + nslot - 1) / nslot : 0;
+  if (nmine == 0) return;
+  const int nk = K >> 6;
+  const int S = nmine * nk;  // stages of this workgroup
+
+  // DMA geometry: instruction i of wave w fills LDS rows 64 i + 8 w + lane / 8 (1 KB per
+  // instruction), physical chunk lane % 8 holding logical chunk (lane % 8) ^ (row & 7).
+  const int srow = 8 * wave + (lane >> 3);
+  const int lchunk = (lane & 7) ^ (srow & 7);
+  // cg_perm keeps bits >= 5, so W-tile row 64 i + srow holds feature 64 i + cg_perm(srow)
+  const uint32_t woff = (uint32_t)(cg_perm(srow) * K * 2 + lchunk * 16);
+  const uint32_t xoff = (uint32_t)(srow * ldx * 2 + lchunk * 16);
+  const uint32_t xbytes = (uint32_t)(64 * ldx * 2);
+
+  __amdgpu_buffer_rsrc_t wres;
+  const bf16* xbase[IPX];
+  auto set_tile = [&](int t) {
+    const int rb = t / NB, nb = t - rb * NB;
+    wres = CG_RSRC(w + (int64_t)nb * 256 * K, (uint32_t)(256 * K * 2));
+#pragma unroll
+    for (int i = 0; i < IPX; ++i) {
+      const int c = min(rb * CPT + i, nu - 1);  // rows of chapters past n_uniq: computed, not stored
+      xbase[i] = cg_src_rows<SRC>(c, x, xred, ldx, uniq, csr_off, csr_edge);
+    }
+  };
+  auto issue = [&](int buf, int kt) {
+    __builtin_amdgcn_sched_barrier(0);
+    const uint32_t ko = (uint32_t)kt * 128;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(wres, (lds_ptr_t)(sW + buf * kCgStageW + (8 * i + wave) * 1024), 16,
+                                               woff, ko + (uint32_t)(64 * i * K * 2), 0, 0);
+#pragma unroll
+    for (int i = 0; i < IPX; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(CG_RSRC(xbase[i], xbytes),
+                                               (lds_ptr_t)(sX + buf * STX + (8 * i + wave) * 1024), 16, xoff, ko, 0,
+                                               0);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  const int wf = wave & 3, wr = wave >> 2;
+  const int g = lane >> 4, m = lane & 15;
+  // fragment reads: row base + 16 i + m (so row & 7 == m & 7), logical chunk 4 ks + g
+  const int aoff0 = (64 * wf + m) * 128 + ((g ^ (m & 7)) << 4);
+  const int aoff1 = (64 * wf + m) * 128 + (((4 + g) ^ (m & 7)) << 4);
+  const int boff0 = ((BM / 2) * wr + m) * 128 + ((g ^ (m & 7)) << 4);
+  const int boff1 = ((BM / 2) * wr + m) * 128 + (((4 + g) ^ (m & 7)) << 4);
+
+  f32x4 acc[4][JB];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < JB; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  auto compute = [&](int buf) {
+    const char* sw = sW + buf * kCgStageW;
+    const char* sx = sX + buf * STX;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const int ao = ks ? aoff1 : aoff0, bo = ks ? boff1 : boff0;
+      bf16x8 a[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) a[i] = *reinterpret_cast<const bf16x8*>(sw + ao + 2048 * i);
+#pragma unroll
+      for (int jh = 0; jh < JB / 4; ++jh) {
+        bf16x8 b[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) b[j] = *reinterpret_cast<const bf16x8*>(sx + bo + 2048 * (4 * jh + j));
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) mma(acc[i][4 * jh + j], a[i], b[j]);
+      }
+    }
+  };
+
+  // Epilogue: lane (g, m) of wave (wf, wr) holds, for row (BM/2) wr + 16 j + m of the tile,
+  // features nb*256 + 64 wf + 32 p + 8 g .. + 7 in acc[2p][j] (4) and acc[2p+1][j] (4).
+  // Rows of chapters >= n_uniq fall outside their chapter's buffer range and are dropped.
+  auto epilogue = [&](int t) {
+    const int rb = t / NB, nb = t - rb * NB;
+#pragma unroll
+    for (int j = 0; j < JB; ++j) {
+      const int rt = (BM / 2) * wr + 16 * j;     // tile row of this 16-row group (wave-uniform)
+      const int c = rb * CPT + rt / 64;
+      const bool live = c < nu;
+      const int cc = live ? c : 0;
+      TO* dst = DST == CG_DST_BANK ? y + (int64_t)rfl(uniq[cc]) * 64 * ldy : y + (int64_t)cc * 64 * ldy;
+      const __amdgpu_buffer_rsrc_t yres = CG_RSRC(dst, live ? (uint32_t)(64 * ldy * sizeof(TO)) : 0u);
+      const uint32_t vrow = (uint32_t)((((rt & 63) + m) * ldy + nb * 256 + 64 * wf + 8 * g) * sizeof(TO));
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        typedef int i32x4 __attribute__((ext_vector_type(4)));
+        if constexpr (sizeof(TO) == 2) {
+          bf16x8 v;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            v[e] = (bf16)acc[2 * p][j][e];
+            v[4 + e] = (bf16)acc[2 * p + 1][j][e];
+          }
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, v), yres, vrow + 64 * p, 0, 0);
+        } else {
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, acc[2 * p][j]), yres, vrow + 128 * p, 0, 0);
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, acc[2 * p + 1][j]), yres,
+                                                 vrow + 128 * p + 16, 0, 0);
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < JB; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  };
+
+  // issue cursor: tile tis, stage kis; one stage in flight ahead of the one being computed
+  int tis = lo + slot, kis = 0, s_issue = 0;
+  set_tile(tis);
+  auto issue_next = [&]() {
+    if (s_issue < S) {
+      issue(s_issue & 1, kis);
+      ++s_issue;
+      if (++kis == nk) {
+        kis = 0;
+        tis += nslot;
+        if (s_issue < S) set_tile(tis);
+      }
+    }
+  };
+  issue_next();
+
+  int tcur = lo + slot, kt = 0;
+  for (int s = 0; s < S; s += 2) {
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      if (s + b < S) {
+        cg_wait_vm0();     // this wave's loads of stage s + b have landed
+        __syncthreads();   // ... and every wave's; every wave is done with the other buffer
+        issue_next();
+        compute(b);
+        if (++kt == nk) {
+          epilogue(tcur);
+          tcur += nslot;
+          kt = 0;
+        }
+      }
+    }
+  }
+}
+
+// Per-chapter sums of the dK|dV rows of chapters selected by several edges (csr order, fp32
+// accumulation, rounded to bf16); chapters with one edge are read in place by the GEMM.
+constexpr int kMultiSplit = 8;
+__global__ __launch_bounds__(256) void dkv_multi_reduce_kernel(const bf16* __restrict__ dkv_edge,
+                                                               const int32_t* __restrict__ n_uniq,
+                                                               const int32_t* __restrict__ csr_off,
+                                                               const int32_t* __restrict__ csr_edge, int64_t row_elems,
+                                                               bf16* __restrict__ red) {
+  const int u = blockIdx.x;
+  if (u >= n_uniq[0]) return;
+  const int p0 = csr_off[u], p1 = csr_off[u + 1];
+  if (p1 - p0 == 1) return;
+  const int64_t nch = 64 * row_elems / 8;  // 16-byte chunks of the chapter block
+  const int64_t per = (nch + kMultiSplit - 1) / kMultiSplit;
+  const int64_t c0 = (int64_t)blockIdx.y * per, c1 = min(nch, c0 + per);
+  bf16* dst = red + (size_t)u * 64 * row_elems;
+  for (int64_t i = c0 + threadIdx.x; i < c1; i += 256) {
+    float acc[8];
+#pragma unroll
+    for (int x = 0; x < 8; ++x) acc[x] = 0.f;
+    for (int p = p0; p < p1; ++p) {
+      const bf16x8 v = *reinterpret_cast<const bf16x8*>(dkv_edge + ((size_t)csr_edge[p] * 64 * row_elems + i * 8));
+#pragma unroll
+      for (int x = 0; x < 8; ++x) acc[x] += (float)v[x];
+    }
+    bf16x8 o;
+#pragma unroll
+    for (int x = 0; x < 8; ++x) o[x] = (bf16)acc[x];
+    *reinterpret_cast<bf16x8*>(dst + i * 8) = o;
+  }
+}
+
+// [Wk; Wv] (rows kv of each, any of f32 / bf16) -> wkv [2 kv][d] bf16 and / or its transpose
+// wkv_t [d][2 kv] (either may be null): 64 x 64 tiles through LDS.
+template <typename TK, typename TV>
+__global__ __launch_bounds__(256) void weight_pack_kernel(const TK* __restrict__ wk, const TV* __restrict__ wv,
+                                                          int64_t kv, int64_t d, bf16* __restrict__ wkv,
+                                                          bf16* __restrict__ wkv_t) {
+  __shared__ float tile[64][65];
+  const int64_t r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  for (int rr = ty; rr < 64; rr += 4) {
+    const int64_t r = r0 + rr, c = c0 + tx;
+    float v = 0.f;
+    if (r < 2 * kv && c < d) v = r < kv ? to_f(wk[r * d + c]) : to_f(wv[(r - kv) * d + c]);
+    if (wkv && r < 2 * kv && c < d) wkv[r * d + c] = (bf16)v;
+    tile[rr][tx] = v;
+  }
+  if (!wkv_t) return;
+  __syncthreads();
+  for (int cc = ty; cc < 64; cc += 4) {
+    const int64_t c = c0 + cc, r = r0 + tx;
+    if (c < d && r < 2 * kv) wkv_t[c * 2 * kv + r] = (bf16)tile[tx][cc];
+  }
+}
+
+int cg_grid() {
+  static int cus = 0;
+  if (cus == 0) {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
+      cus = n;
+    else
+      cus = 256;
+  }
+  return (cus + 7) / 8 * 8;
+}
+
+int cg_check(const char* who, int64_t ldx, int N, int K, int64_t max_u, int64_t ldy) {
+  MOC_REQUIRE(N > 0 && N % 256 == 0, MOC_ERR_UNSUPPORTED, "%s: N=%d must be a positive multiple of 256", who, N);
+  MOC_REQUIRE(K > 0 && K % 64 == 0, MOC_ERR_UNSUPPORTED, "%s: K=%d must be a positive multiple of 64", who, K);
+  MOC_REQUIRE(ldx >= K && ldx % 8 == 0, MOC_ERR_ARG, "%s: row stride %lld (K=%d)", who, (long long)ldx, K);
+  MOC_REQUIRE(ldy >= N && ldy % 8 == 0, MOC_ERR_ARG, "%s: output row stride %lld (N=%d)", who, (long long)ldy, N);
+  MOC_REQUIRE(64 * ldx * 2 < ((int64_t)1 << 31) && 64 * ldy * 4 < ((int64_t)1 << 31) &&
+                  (int64_t)256 * K * 2 < ((int64_t)1 << 31) && max_u < ((int64_t)1 << 30),
+              MOC_ERR_UNSUPPORTED, "%s: problem too large", who);
+  return MOC_OK;
+}
+
+}  // namespace
+}  // namespace moc
+
+using namespace moc;
+
+extern "C" {
+
+int moc_chapter_project(const void* rows, int64_t ld, int gather, const int32_t* uniq, const int32_t* n_uniq,
+                        int64_t max_u, const void* w, int N, int K, void* y, int64_t ldy, hipStream_t stream) {
+  MOC_REQUIRE(rows && n_uniq && w && y && (uniq || !gather), MOC_ERR_ARG, "moc_chapter_project: null pointer");
+  MOC_REQUIRE(max_u >= 0, MOC_ERR_ARG, "moc_chapter_project: max_u %lld", (long long)max_u);
+  if (int rc = cg_check("moc_chapter_project", ld, N, K, max_u, ldy)) return rc;
+  if (max_u == 0) return MOC_OK;
+  const dim3 grid((unsigned)cg_grid());
+  if (gather)
+    hipLaunchKernelGGL((chapter_gemm_kernel<CG_SRC_GATHER, CG_DST_CONTIG, bf16, 256>), grid, dim3(kCgThreads), 0,
+                       stream, (const bf16*)rows, nullptr, ld, uniq, n_uniq, nullptr, nullptr, max_u, (const bf16*)w,
+                       N, K, (bf16*)y, ldy);
+  else
+    hipLaunchKernelGGL((chapter_gemm_kernel<CG_SRC_CONTIG, CG_DST_CONTIG, bf16, 256>), grid, dim3(kCgThreads), 0,
+                       stream, (const bf16*)rows, nullptr, ld, uniq, n_uniq, nullptr, nullptr, max_u, (const bf16*)w,
+                       N, K, (bf16*)y, ldy);
+  return check_launch("chapter_gemm_kernel(project)");
+}
+
+int moc_chapter_dx(const void* dkv_edge, int64_t ld, const int32_t* uniq, const int32_t* n_uniq, int64_t max_u,
+                   const int32_t* csr_off, const int32_t* csr_edge, void* red, const void* w_t, int N, int K,
+                   int out_dtype, void* out, int64_t ldo, int out_bank_rows, hipStream_t stream) {
+  MOC_REQUIRE(dkv_edge && uniq && n_uniq && csr_off && csr_edge && red && w_t && out, MOC_ERR_ARG,
+              "moc_chapter_dx: null pointer");
+  MOC_REQUIRE(max_u >= 0, MOC_ERR_ARG, "moc_chapter_dx: max_u %lld", (long long)max_u);
+  MOC_REQUIRE(out_dtype == MOC_BF16 || out_dtype == MOC_F32, MOC_ERR_UNSUPPORTED, "moc_chapter_dx: out dtype %d",
+              out_dtype);
+  if (int rc = cg_check("moc_chapter_dx", ld, N, K, max_u, ldo)) return rc;
+  if (max_u == 0) return MOC_OK;
+  hipLaunchKernelGGL(dkv_multi_reduce_kernel, dim3((unsigned)max_u, kMultiSplit), dim3(256), 0, stream,
+                     (const bf16*)dkv_edge, n_uniq, csr_off, csr_edge, ld, (bf16*)red);
+  if (int rc = check_launch("dkv_multi_reduce_kernel")) return rc;
+  const dim3 grid((unsigned)cg_grid());
+#define MOC_CGDX(DST, TO)                                                                                           \
+  hipLaunchKernelGGL((chapter_gemm_kernel<CG_SRC_EDGE, DST, TO, kCgDxRows>), grid, dim3(kCgThreads), 0, stream,          \
+                     (const bf16*)dkv_edge, (const bf16*)red, ld, uniq, n_uniq, csr_off, csr_edge, max_u,           \
+                     (const bf16*)w_t, N, K, (TO*)out, ldo)
+  if (out_bank_rows) {
+    if (out_dtype == MOC_BF16) MOC_CGDX(CG_DST_BANK, bf16); else MOC_CGDX(CG_DST_BANK, float);
+  } else {
+    if (out_dtype == MOC_BF16) MOC_CGDX(CG_DST_CONTIG, bf16); else MOC_CGDX(CG_DST_CONTIG, float);
+  }
+#undef MOC_CGDX
+  return check_launch("chapter_gemm_kernel(dx)");
+}
+
+int moc_weight_pack(const void* wk, int wk_dtype, const void* wv, int wv_dtype, int64_t kv, int64_t d, void* wkv,
+                    void* wkv_t, hipStream_t stream) {
+  MOC_REQUIRE(wk && wv && (wkv || wkv_t), MOC_ERR_ARG, "moc_weight_pack: null pointer");
+  MOC_REQUIRE(kv > 0 && d > 0 && 2 * kv * d < ((int64_t)1 << 40), MOC_ERR_ARG, "moc_weight_pack: bad shape");
+  const dim3 grid((unsigned)((d + 63) / 64), (unsigned)((2 * kv + 63) / 64));
+#define MOC_WP(TK, TV)                                                                                           \
+  hipLaunchKernelGGL((weight_pack_kernel<TK, TV>), grid, dim3(256), 0, stream, (const TK*)wk, (const TV*)wv, kv, \
+                     d, (bf16*)wkv, (bf16*)wkv_t)
+  if (wk_dtype == MOC_BF16 && wv_dtype == MOC_BF16) MOC_WP(bf16, bf16);
+  else if (wk_dtype == MOC_F32 && wv_dtype == MOC_F32) MOC_WP(float, float);
+  else if (wk_dtype == MOC_BF16 && wv_dtype == MOC_F32) MOC_WP(bf16, float);
+  else if (wk_dtype == MOC_F32 && wv_dtype == MOC_BF16) MOC_WP(float, bf16);
+  else return set_error(MOC_ERR_UNSUPPORTED, "moc_weight_pack: dtypes %d, %d", wk_dtype, wv_dtype);
+#undef MOC_WP
+  return check_launch("weight_pack_kernel");
+}
+
+}  // extern "C"

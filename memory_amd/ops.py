@@ -248,6 +248,43 @@ def kv_project(bank: torch.Tensor, plan: ChapterPlan, T: int, wkv: torch.Tensor,
     return tuple(out[n] for n in layouts)
 
 
+def weight_pack(wk: torch.Tensor, wv: torch.Tensor, rows: bool = True, transposed: bool = False):
+    """[Wk; Wv] in bf16 ([2*KV][d]) and / or its transpose ([d][2*KV]) in one kernel (the
+    concatenated K/V weight of the chapter GEMMs).  Returns (wkv or None, wkv_t or None)."""
+    wk = wk.contiguous()
+    wv = wv.contiguous()
+    KV, d = wk.shape
+    dev = wk.device
+    wkv = torch.empty(2 * KV, d, device=dev, dtype=torch.bfloat16) if rows else None
+    wkv_t = torch.empty(d, 2 * KV, device=dev, dtype=torch.bfloat16) if transposed else None
+    call("moc_weight_pack", ptr(wk), L.dtype_code(wk.dtype), ptr(wv), L.dtype_code(wv.dtype), KV, d, ptr(wkv),
+         ptr(wkv_t), stream_ptr(dev))
+    return wkv, wkv_t
+
+
+def chapter_project(rows: torch.Tensor, plan: ChapterPlan, wkv: torch.Tensor, gather: bool) -> torch.Tensor:
+    """Projection rows [max_u * 64][2*KV] (bf16) of the plan's distinct chapters: rows are the
+    bank (gather) or a contiguous [max_u * 64][d] block; wkv [2*KV][d] bf16."""
+    N, K = wkv.shape
+    y = torch.empty(plan.max_u * 64, N, device=rows.device, dtype=torch.bfloat16)
+    call("moc_chapter_project", ptr(rows), rows.stride(0), 1 if gather else 0, ptr(plan.uniq), ptr(plan.n_uniq),
+         plan.max_u, ptr(wkv), N, K, ptr(y), N, stream_ptr(rows.device))
+    return y
+
+
+def chapter_dx(dkv_edge: torch.Tensor, uniq, n_uniq, max_u: int, csr_off, csr_edge, wkv_t: torch.Tensor,
+               out: torch.Tensor, bank_rows: bool) -> torch.Tensor:
+    """Per-chapter input gradient of the K/V projection, summed over each chapter's edges:
+    stored at the chapter's bank rows of ``out`` (bank_rows) or at rows c*64.. of ``out``
+    ([max_u * 64][d]).  dkv_edge [E*64][2*KV] bf16, wkv_t [d][2*KV] bf16."""
+    N, K = wkv_t.shape
+    red = torch.empty(max_u * 64, K, device=dkv_edge.device, dtype=torch.bfloat16)
+    call("moc_chapter_dx", ptr(dkv_edge), dkv_edge.stride(0), ptr(uniq), ptr(n_uniq), max_u, ptr(csr_off),
+         ptr(csr_edge), ptr(red), ptr(wkv_t), N, K, L.dtype_code(out.dtype), ptr(out), out.stride(0),
+         1 if bank_rows else 0, stream_ptr(dkv_edge.device))
+    return out
+
+
 def kv_rows_layout(kv: torch.Tensor, T: int, HK: int, Dh: int):
     """(kv_span, su, sh, st) of projection rows kv [max_u * T][2 * HK * Dh] (K columns, then V)
     for the attention entry points: block (u, hk) row t at u*T*2KV + hk*Dh + t*2KV; the span
@@ -458,18 +495,30 @@ class _RoutedAttention(torch.autograd.Function):
         mean = rstd = None
         if norm != L.MOC_NORM_NONE:
             mean, rstd = row_stats(bank, plan, T, norm, eps)
-        wkv = torch.cat([wk, wv], 0).to(dtype).contiguous()
-        # K / V of the plan's chapters as projection rows [max_u * T][K | V]: the (normalised)
-        # bank rows gathered once, then one library GEMM (faster at these shapes than the fused
-        # gather-projection kernel, which writes chapter-head tiles); the attention kernels
-        # read (chapter, kv head) blocks of it through strides
+        # K / V of the plan's chapters as projection rows [max_u * T][K | V]; the attention
+        # kernels read (chapter, kv head) blocks of it through strides
         KV = HK * Dh
-        X = torch.empty(plan.max_u * T, bank.shape[1], device=q.device, dtype=dtype)
-        call("moc_gather_rows", L.dtype_code(dtype), ptr(bank), L.dtype_code(bank.dtype), bank.shape[1], T,
-             ptr(plan.uniq), ptr(plan.n_uniq), plan.max_u, ptr(mean), ptr(rstd), ptr(X), stream_ptr(q.device))
-        with L.region("lib_kv_project_gemm"):
-            kv = F.linear(X, wkv)
-        del X
+        d = bank.shape[1]
+        if dtype == torch.bfloat16 and T == 64 and (2 * KV) % 256 == 0 and d % 64 == 0:
+            # bf16: the chapter GEMM, gathering bank rows straight into its operand tiles (a
+            # normalised or f32 bank is gathered into bf16 rows first)
+            wkv, _ = weight_pack(wk, wv)
+            if norm == L.MOC_NORM_NONE and bank.dtype == torch.bfloat16:
+                kv = chapter_project(bank, plan, wkv, gather=True)
+            else:
+                X = torch.empty(plan.max_u * T, d, device=q.device, dtype=dtype)
+                call("moc_gather_rows", L.dtype_code(dtype), ptr(bank), L.dtype_code(bank.dtype), d, T,
+                     ptr(plan.uniq), ptr(plan.n_uniq), plan.max_u, ptr(mean), ptr(rstd), ptr(X), stream_ptr(q.device))
+                kv = chapter_project(X, plan, wkv, gather=False)
+                del X
+        else:
+            wkv = torch.cat([wk, wv], 0).to(dtype).contiguous()
+            X = torch.empty(plan.max_u * T, d, device=q.device, dtype=dtype)
+            call("moc_gather_rows", L.dtype_code(dtype), ptr(bank), L.dtype_code(bank.dtype), d, T,
+                 ptr(plan.uniq), ptr(plan.n_uniq), plan.max_u, ptr(mean), ptr(rstd), ptr(X), stream_ptr(q.device))
+            with L.region("lib_kv_project_gemm"):
+                kv = F.linear(X, wkv)
+            del X
         kvl = kv_rows_layout(kv, T, HK, Dh)
         om = omega.float().contiguous()
         out = torch.empty(B, Lq, H, Dh, device=q.device, dtype=dtype)
@@ -532,9 +581,10 @@ class _RoutedAttention(torch.autograd.Function):
                      L.dtype_code(out_dt), ptr(dwkv), st)
                 dwk = dwkv[:KV].to(wk_dtype) if need_wk else None
                 dwv = dwkv[KV:].to(wv_dtype) if need_wv else None
-            if need_bank:
-                with L.region("lib_kv_dx_gemm"):
-                    dX = torch.matmul(dkv_edge, wkv)  # rows of skipped edges are never read
+            if need_bank and not (T == 64 and d % 256 == 0 and (2 * KV) % 64 == 0):
+                # shapes outside the chapter GEMM's tiling: per-edge dX on the library GEMM,
+                # summed per chapter by the scatter
+                dX = torch.matmul(dkv_edge, wkv)  # rows of skipped edges are never read
                 if ctx.row_grad is not None:
                     ctx.row_grad.accumulate(dX, bank, uniq, n_uniq, max_u, csr_off, csr_edge, mean, rstd, norm)
                 else:
@@ -544,7 +594,30 @@ class _RoutedAttention(torch.autograd.Function):
                     call("moc_bank_scatter", L.dtype_code(dX.dtype), ptr(dX), ptr(bank), L.dtype_code(bank.dtype),
                          d, T, ptr(uniq), ptr(n_uniq), max_u, ptr(csr_off), ptr(csr_edge), ptr(mean), ptr(rstd),
                          norm, ptr(dbank), st)
+                    dbank = dbank.to(bank_dtype)
+            elif need_bank:
+                # dX per distinct chapter (edges summed) on the chapter GEMM; with a plain bank it
+                # is stored straight into the chapter's rows of the dense gradient
+                _, wkv_t = weight_pack(wkv[:KV], wkv[KV:], rows=False, transposed=True)
+                if ctx.row_grad is None and norm == L.MOC_NORM_NONE:
+                    dbank, filled = dbank_zero
+                    if filled is not None:
+                        torch.cuda.current_stream(dev).wait_event(filled)
+                    chapter_dx(dkv_edge, uniq, n_uniq, max_u, csr_off, csr_edge, wkv_t, dbank, bank_rows=True)
                     dbank = dbank.to(bank_dtype)   # the bank read may be a mirror of another dtype
+                else:
+                    dXc = torch.empty(max_u * T, d, device=dev, dtype=torch.float32)
+                    chapter_dx(dkv_edge, uniq, n_uniq, max_u, csr_off, csr_edge, wkv_t, dXc, bank_rows=False)
+                    if ctx.row_grad is not None:
+                        ctx.row_grad.accumulate(dXc, bank, uniq, n_uniq, max_u, None, None, mean, rstd, norm)
+                    else:
+                        dbank, filled = dbank_zero
+                        if filled is not None:
+                            torch.cuda.current_stream(dev).wait_event(filled)
+                        call("moc_bank_scatter", L.dtype_code(dXc.dtype), ptr(dXc), ptr(bank),
+                             L.dtype_code(bank.dtype), d, T, ptr(uniq), ptr(n_uniq), max_u, None, None, ptr(mean),
+                             ptr(rstd), norm, ptr(dbank), st)
+                        dbank = dbank.to(bank_dtype)
             return dq, dbank, dwk, dwv, domega, None, None, None, None, None, None
         # fp32: sum per distinct chapter first, then library GEMMs
         dkv = torch.empty(max_u * T, 2 * KV, device=dev, dtype=dtype)

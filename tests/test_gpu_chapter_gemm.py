@@ -1,0 +1,131 @@
+"""Chapter GEMMs of the K/V path (moc_chapter_project, moc_chapter_dx, moc_weight_pack) against
+float64 references of the reference's math: the gather + k_proj/v_proj of
+memory_transformer/memory_bank.py:263-293 and memory_attention.py:241-243, and its input gradient
+scattered into the bank (memory_bank.py:287-291)."""
+
+import pytest
+import torch
+
+from helpers import assert_parity, gen
+
+pytestmark = pytest.mark.gpu
+
+
+def _ops():
+    from memory_amd import ops
+    return ops
+
+
+@pytest.fixture(scope="module")
+def dev():
+    if not torch.cuda.is_available():
+        pytest.skip("needs a ROCm GPU")
+    return torch.device("cuda", 0)
+
+
+@pytest.mark.parametrize("wdt", [(torch.bfloat16, torch.bfloat16), (torch.float32, torch.float32),
+                                 (torch.float32, torch.bfloat16)])
+def test_weight_pack_exact(dev, wdt):
+    ops = _ops()
+    wk = torch.randn(192, 320, generator=gen(1)).to(wdt[0])
+    wv = torch.randn(192, 320, generator=gen(2)).to(wdt[1])
+    wkv, wkv_t = ops.weight_pack(wk.to(dev), wv.to(dev), rows=True, transposed=True)
+    ref = torch.cat([wk.to(torch.bfloat16), wv.to(torch.bfloat16)])
+    assert torch.equal(wkv.cpu(), ref)
+    assert torch.equal(wkv_t.cpu(), ref.t().contiguous())
+    _, only_t = ops.weight_pack(wk.to(dev), wv.to(dev), rows=False, transposed=True)
+    assert torch.equal(only_t.cpu(), ref.t().contiguous())
+
+
+def _plan(ops, dev, chap, C):
+    return ops.chapter_plan(torch.as_tensor(chap, dtype=torch.int32).to(dev), C)
+
+
+# (C, d, N, chap) -- N = 2*HK*Dh; the second case spans many tiles, every XCD range, a
+# row block with fewer than 4 chapters and unused plan slots
+_PROJ_CASES = [
+    (40, 256, 256, [[0, 7, 3, 39], [0, 3, 11, 25], [0, 39, 38, 1]]),
+    (700, 768, 1536, "random"),
+]
+
+
+@pytest.mark.parametrize("case", range(len(_PROJ_CASES)))
+@pytest.mark.parametrize("gather", [True, False])
+def test_chapter_project(dev, case, gather):
+    ops = _ops()
+    C, d, N, chap = _PROJ_CASES[case]
+    T = 64
+    if chap == "random":
+        g = gen(5)
+        chap = torch.cat([torch.zeros(8, 1, dtype=torch.int64),
+                          torch.stack([torch.randperm(C - 1, generator=g)[:40] + 1 for _ in range(8)])], 1)
+    bank = (torch.randn(C * T, d, generator=gen(6)) * 0.5).to(torch.bfloat16)
+    w = (torch.randn(N, d, generator=gen(7)) / d ** 0.5).to(torch.bfloat16)
+    plan = _plan(ops, dev, chap, C)
+    n_u = int(plan.n_uniq[0])
+    uniq = plan.uniq[:n_u].cpu().long()
+    X = bank.view(C, T, d)[uniq].reshape(-1, d)
+    bg = bank.to(dev)
+    if gather:
+        rows = bg
+    else:
+        rows = torch.zeros(plan.max_u * T, d, dtype=torch.bfloat16)
+        rows[: n_u * T] = X
+        rows = rows.to(dev)
+    y = ops.chapter_project(rows, plan, w.to(dev), gather=gather)
+    ref = X.double() @ w.double().t()
+    print(f"C={C} d={d} N={N} n_uniq={n_u} max_u={plan.max_u} gather={gather}")
+    assert_parity(y[: n_u * T].cpu(), ref, torch.bfloat16, "projection rows")
+    # bf16 rounding of fp32 sums: no element further than one bf16 ulp of the result
+    err = (y[: n_u * T].cpu().double() - ref).abs()
+    assert (err <= ref.abs() * 2 ** -8 + 1e-3).all(), err.max().item()
+
+
+def _dx_case(C, NSEQ, NS, seed):
+    g = gen(seed)
+    rows = [torch.cat([torch.zeros(1, dtype=torch.int64), torch.randint(1, C, (NS - 1,), generator=g)])
+            for _ in range(NSEQ)]
+    return torch.stack(rows)   # chapter 0 in every sequence, random collisions elsewhere
+
+
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("bank_rows", [True, False])
+@pytest.mark.parametrize("shape", [(60, 4, 9, 256, 512), (600, 8, 65, 768, 1536)])
+def test_chapter_dx(dev, out_dtype, bank_rows, shape):
+    ops = _ops()
+    C, NSEQ, NS, d, K = shape
+    T = 64
+    chap = _dx_case(C, NSEQ, NS, 11)
+    E = chap.numel()
+    plan = _plan(ops, dev, chap, C)
+    n_u = int(plan.n_uniq[0])
+    uniq = plan.uniq[:n_u].cpu().long()
+    dkv = torch.randn(E * T, K, generator=gen(12)).to(torch.bfloat16)
+    wkv = (torch.randn(K, d, generator=gen(13)) / K ** 0.5).to(torch.bfloat16)
+    _, wkv_t = ops.weight_pack(wkv[: K // 2].to(dev), wkv[K // 2:].to(dev), rows=False, transposed=True)
+    flat = chap.reshape(-1)
+    ref_c = torch.zeros(n_u, T, d, dtype=torch.float64)
+    for u in range(n_u):
+        edges = (flat == uniq[u]).nonzero().view(-1)
+        s = sum(dkv[e * T:(e + 1) * T].double() for e in edges.tolist())
+        ref_c[u] = s @ wkv.double()
+    counts = torch.bincount(flat, minlength=C)
+    assert counts.max() > 1 and (counts == 1).any()   # both code paths (summed and in-place)
+    if bank_rows:
+        out = torch.zeros(C * T, d, device=dev, dtype=out_dtype)
+    else:
+        out = torch.full((plan.max_u * T, d), float("nan"), device=dev, dtype=out_dtype)
+    ops.chapter_dx(dkv.to(dev), plan.uniq, plan.n_uniq, plan.max_u, plan.csr_off, plan.csr_edge, wkv_t, out,
+                   bank_rows=bank_rows)
+    o = out.cpu()
+    print(f"C={C} E={E} n_uniq={n_u} d={d} K={K} out={out_dtype} bank_rows={bank_rows}")
+    if bank_rows:
+        got = o.view(C, T, d)[uniq]
+        mask = torch.ones(C, dtype=torch.bool)
+        mask[uniq] = False
+        assert (o.view(C, T, d)[mask] == 0).all(), "rows of unselected chapters must stay zero"
+    else:
+        got = o[: n_u * T].view(n_u, T, d)
+        if plan.max_u > n_u:
+            assert torch.isnan(o[n_u * T:].float()).all(), "unused plan slots must not be written"
+    assert_parity(got, ref_c, torch.bfloat16, "dX per chapter")
