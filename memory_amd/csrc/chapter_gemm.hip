@@ -39,6 +39,7 @@ typedef __attribute__((address_space(3))) void* lds_ptr_t;
 constexpr int kCgThreads = 512;
 constexpr int kCgStageW = 256 * 128;  // LDS bytes of one W stage (256 rows x 64 bf16)
 constexpr int kCgDxRows = 128;        // row tile of the dX GEMM (N = d is 3 feature tiles at d = 768)
+constexpr int kCgXpd = 1;             // stages the X operand is loaded ahead (W: one)
 
 enum { CG_SRC_GATHER = 0, CG_SRC_CONTIG = 1, CG_SRC_EDGE = 2 };
 enum { CG_DST_CONTIG = 0, CG_DST_BANK = 1 };
@@ -49,13 +50,28 @@ __device__ __forceinline__ int cg_perm(int r) {
 
 __device__ __forceinline__ int rfl(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
+// 8 consecutive elements as floats (one 16-byte load for bf16, two for f32)
+template <typename T> struct ChunkLoad8;
+template <> struct ChunkLoad8<bf16> {
+  static __device__ __forceinline__ void run(const bf16* p, float* o) {
+    const bf16x8 v = *reinterpret_cast<const bf16x8*>(p);
+#pragma unroll
+    for (int x = 0; x < 8; ++x) o[x] = (float)v[x];
+  }
+};
+template <> struct ChunkLoad8<float> {
+  static __device__ __forceinline__ void run(const float* p, float* o) {
+    const f32x4 a = *reinterpret_cast<const f32x4*>(p), b = *reinterpret_cast<const f32x4*>(p + 4);
+#pragma unroll
+    for (int x = 0; x < 4; ++x) { o[x] = a[x]; o[4 + x] = b[x]; }
+  }
+};
+
 // buffer resource over `bytes` bytes at p (raw buffer, bounds-checked; a macro, since the
 // host pass of the kernel templates cannot take the resource type through a function)
 #define CG_RSRC(p, bytes) \
   __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>((const void*)(p)), (short)0, (int)(bytes), 0x00020000)
 
-// s_waitcnt vmcnt(0) (gfx9 encoding: vmcnt[3:0], expcnt[6:4], lgkmcnt[11:8], vmcnt_hi[15:14])
-__device__ __forceinline__ void cg_wait_vm0() { __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8)); }
 
 template <int SRC>
 __device__ __forceinline__ const bf16* cg_src_rows(int c, const bf16* __restrict__ x, const bf16* __restrict__ xred,
@@ -72,7 +88,24 @@ __device__ __forceinline__ const bf16* cg_src_rows(int c, const bf16* __restrict
   }
 }
 
-template <int SRC, int DST, typename TO, int BM>
+// One 16-byte-per-lane LDS DMA (buffer_load_dwordx4 ... lds): lane l's 16 bytes at voff (+ soff)
+// of the buffer land at LDS address m0 + 16 l.  Written as inline assembly so that the waits
+// on these loads stay explicit (cg_wait_vm): the compiler's own accounting waits for every
+// outstanding load and store before each barrier, which would also wait for the loads issued
+// ahead for later stages and for the epilogue's stores.
+__device__ __forceinline__ void cg_dma16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, const char* lds) {
+  const uint32_t m0 = (uint32_t)(uintptr_t)(lds_ptr_t)lds;
+  asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(r), "s"(soff), "{m0}"(m0) : "memory");
+}
+// s_waitcnt vmcnt(n), n in {0, 2, 4}: all but this wave's newest n vector memory operations done
+// (loads complete in issue order)
+__device__ __forceinline__ void cg_wait_vm(int n) {
+  if (n == 4) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+  else if (n == 2) asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
+  else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
+
+template <int SRC, int DST, typename TO, int BM, int XPD>
 __global__ __launch_bounds__(kCgThreads) void chapter_gemm_kernel(
     const bf16* __restrict__ x, const bf16* __restrict__ xred, int64_t ldx, const int32_t* __restrict__ uniq,
     const int32_t* __restrict__ n_uniq, const int32_t* __restrict__ csr_off, const int32_t* __restrict__ csr_edge,
@@ -81,7 +114,9 @@ __global__ __launch_bounds__(kCgThreads) void chapter_gemm_kernel(
   constexpr int IPX = BM / 64;              // X DMA instructions per thread per stage
   constexpr int JB = BM / 32;               // 16-row MFMA tiles per wave
   constexpr int STX = BM * 128;             // LDS bytes of one X stage
-  __shared__ __attribute__((aligned(1024))) char smem[2 * kCgStageW + 2 * STX];
+  constexpr int NXB = XPD + 1;              // X stages in LDS (X runs XPD stages ahead, W one)
+  static_assert(2 * kCgStageW + NXB * STX <= 163840, "LDS");
+  __shared__ __attribute__((aligned(1024))) char smem[2 * kCgStageW + NXB * STX];
   char* const sW = smem;
   char* const sX = smem + 2 * kCgStageW;
 
@@ -106,30 +141,25 @@ __global__ __launch_bounds__(kCgThreads) void chapter_gemm_kernel(
   const uint32_t xoff = (uint32_t)(srow * ldx * 2 + lchunk * 16);
   const uint32_t xbytes = (uint32_t)(64 * ldx * 2);
 
-  __amdgpu_buffer_rsrc_t wres;
-  const bf16* xbase[IPX];
-  auto set_tile = [&](int t) {
-    const int rb = t / NB, nb = t - rb * NB;
-    wres = CG_RSRC(w + (int64_t)nb * 256 * K, (uint32_t)(256 * K * 2));
+  // W and X stage streams, each with its own cursor (tile, k-stage): X runs ahead of W
+  auto issue_w = [&](int s) {  // W of stage s (tile lo + slot + nslot * (s / nk), k-stage s % nk)
+    const int t = lo + slot + nslot * (s / nk), kt = s % nk;
+    const int nb = t % NB;
+    const __amdgpu_buffer_rsrc_t wres = CG_RSRC(w + (int64_t)nb * 256 * K, (uint32_t)(256 * K * 2));
+    const char* dst = sW + (s & 1) * kCgStageW + wave * 1024;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) cg_dma16(wres, woff, (uint32_t)(kt * 128 + 64 * i * K * 2), dst + 8192 * i);
+  };
+  auto issue_x = [&](int s) {
+    const int t = lo + slot + nslot * (s / nk), kt = s % nk;
+    const int rb = t / NB;
+    const char* dst = sX + (s % NXB) * STX + wave * 1024;
 #pragma unroll
     for (int i = 0; i < IPX; ++i) {
       const int c = min(rb * CPT + i, nu - 1);  // rows of chapters past n_uniq: computed, not stored
-      xbase[i] = cg_src_rows<SRC>(c, x, xred, ldx, uniq, csr_off, csr_edge);
+      const bf16* xb = cg_src_rows<SRC>(c, x, xred, ldx, uniq, csr_off, csr_edge);
+      cg_dma16(CG_RSRC(xb, xbytes), xoff, (uint32_t)(kt * 128), dst + 8192 * i);
     }
-  };
-  auto issue = [&](int buf, int kt) {
-    __builtin_amdgcn_sched_barrier(0);
-    const uint32_t ko = (uint32_t)kt * 128;
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(wres, (lds_ptr_t)(sW + buf * kCgStageW + (8 * i + wave) * 1024), 16,
-                                               woff, ko + (uint32_t)(64 * i * K * 2), 0, 0);
-#pragma unroll
-    for (int i = 0; i < IPX; ++i)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(CG_RSRC(xbase[i], xbytes),
-                                               (lds_ptr_t)(sX + buf * STX + (8 * i + wave) * 1024), 16, xoff, ko, 0,
-                                               0);
-    __builtin_amdgcn_sched_barrier(0);
   };
 
   const int wf = wave & 3, wr = wave >> 2;
@@ -146,9 +176,7 @@ __global__ __launch_bounds__(kCgThreads) void chapter_gemm_kernel(
 #pragma unroll
     for (int j = 0; j < JB; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  auto compute = [&](int buf) {
-    const char* sw = sW + buf * kCgStageW;
-    const char* sx = sX + buf * STX;
+  auto compute = [&](const char* sw, const char* sx) {
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
       const int ao = ks ? aoff1 : aoff0, bo = ks ? boff1 : boff0;
@@ -206,94 +234,132 @@ __global__ __launch_bounds__(kCgThreads) void chapter_gemm_kernel(
       for (int j = 0; j < JB; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
   };
 
-  // issue cursor: tile tis, stage kis; one stage in flight ahead of the one being computed
-  int tis = lo + slot, kis = 0, s_issue = 0;
-  set_tile(tis);
-  auto issue_next = [&]() {
-    if (s_issue < S) {
-      issue(s_issue & 1, kis);
-      ++s_issue;
-      if (++kis == nk) {
-        kis = 0;
-        tis += nslot;
-        if (s_issue < S) set_tile(tis);
-      }
-    }
-  };
-  issue_next();
-
-  int tcur = lo + slot, kt = 0;
-  for (int s = 0; s < S; s += 2) {
+  // Stage s computes from W(s) and X(s).  Per wave the loads go out as W(0), X(0 .. XPD-1), then
+  // at each stage W(s+1) and X(s+XPD); a wave's loads complete in issue order, so when the
+  // newest batch's X stage is allowed to stay in flight, "vmcnt <= IPX" means W(s+1) and
+  // X(s+1) have landed.  At a tile's last stage the X load goes out after the epilogue's stores,
+  // so no store ever sits between a needed load and the loads allowed in flight (with XPD == 1
+  // nothing stays in flight: every stage waits for all of the wave's loads and stores).
+  issue_w(0);
 #pragma unroll
-    for (int b = 0; b < 2; ++b) {
-      if (s + b < S) {
-        cg_wait_vm0();     // this wave's loads of stage s + b have landed
-        __syncthreads();   // ... and every wave's; every wave is done with the other buffer
-        issue_next();
-        compute(b);
-        if (++kt == nk) {
-          epilogue(tcur);
-          tcur += nslot;
-          kt = 0;
-        }
-      }
+  for (int p = 0; p < XPD; ++p)
+    if (p < S) issue_x(p);
+  int in_flight = XPD > 1 && 1 < S ? IPX : 0;
+  for (int s = 0, kt = 0, t = lo + slot; s < S; ++s) {
+    cg_wait_vm(in_flight);
+    __syncthreads();  // every wave's loads of stage s landed; every wave is done with stage s-1
+    __builtin_amdgcn_sched_barrier(0);
+    const bool tile_end = kt + 1 == nk;
+    const bool has_w = s + 1 < S, has_x = s + XPD < S;
+    if (has_w) issue_w(s + 1);
+    if (has_x && (XPD == 1 || !tile_end)) issue_x(s + XPD);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(sW + (s & 1) * kCgStageW, sX + (s % NXB) * STX);
+    if (tile_end) {
+      epilogue(t);
+      t += nslot;
+      kt = 0;
+      if (XPD > 1 && has_x) issue_x(s + XPD);
+    } else {
+      ++kt;
     }
+    in_flight = XPD > 1 && has_x ? IPX : 0;
   }
 }
 
 // Per-chapter sums of the dK|dV rows of chapters selected by several edges (csr order, fp32
-// accumulation, rounded to bf16); chapters with one edge are read in place by the GEMM.
-constexpr int kMultiSplit = 8;
+// accumulation, rounded to bf16); chapters with one edge are read in place by the GEMM.  Every
+// workgroup owns one 4 KB slice (256 threads x 16 bytes) of the 64-row chapter block and one of
+// kMultiGroups shares of the chapters (u % kMultiGroups): it lists its share's chapters with
+// several edges (the shared chapter, collisions) in LDS from one coalesced pass over csr_off, then
+// sums its slice of each.
+constexpr int kMultiGroups = 16;
 __global__ __launch_bounds__(256) void dkv_multi_reduce_kernel(const bf16* __restrict__ dkv_edge,
                                                                const int32_t* __restrict__ n_uniq,
                                                                const int32_t* __restrict__ csr_off,
                                                                const int32_t* __restrict__ csr_edge, int64_t row_elems,
                                                                bf16* __restrict__ red) {
-  const int u = blockIdx.x;
-  if (u >= n_uniq[0]) return;
-  const int p0 = csr_off[u], p1 = csr_off[u + 1];
-  if (p1 - p0 == 1) return;
-  const int64_t nch = 64 * row_elems / 8;  // 16-byte chunks of the chapter block
-  const int64_t per = (nch + kMultiSplit - 1) / kMultiSplit;
-  const int64_t c0 = (int64_t)blockIdx.y * per, c1 = min(nch, c0 + per);
-  bf16* dst = red + (size_t)u * 64 * row_elems;
-  for (int64_t i = c0 + threadIdx.x; i < c1; i += 256) {
-    float acc[8];
+  __shared__ int list[1024];
+  __shared__ int count;
+  const int64_t nch = 64 * row_elems / 8;  // 16-byte chunks of one chapter block
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int nu = n_uniq[0];
+  for (int base = 0; base < nu; base += 1024) {
+    if (threadIdx.x == 0) count = 0;
+    __syncthreads();
+    // this workgroup's share: chapters u with u % gridDim.y == blockIdx.y (the same set for every
+    // slice, whatever order the list is built in)
+    for (int u = base + threadIdx.x; u < min(nu, base + 1024); u += 256)
+      if ((int)(u % gridDim.y) == (int)blockIdx.y && csr_off[u + 1] - csr_off[u] != 1) list[atomicAdd(&count, 1)] = u;
+    __syncthreads();
+    const int n = count;
+    for (int k = 0; k < n && i < nch; ++k) {
+      const int u = list[k];
+      const int p0 = csr_off[u], p1 = csr_off[u + 1];
+      float acc[8];
 #pragma unroll
-    for (int x = 0; x < 8; ++x) acc[x] = 0.f;
-    for (int p = p0; p < p1; ++p) {
-      const bf16x8 v = *reinterpret_cast<const bf16x8*>(dkv_edge + ((size_t)csr_edge[p] * 64 * row_elems + i * 8));
+      for (int x = 0; x < 8; ++x) acc[x] = 0.f;
+      for (int p = p0; p < p1; p += 4) {
+        bf16x8 v[4];
 #pragma unroll
-      for (int x = 0; x < 8; ++x) acc[x] += (float)v[x];
+        for (int q = 0; q < 4; ++q)
+          if (p + q < p1)
+            v[q] = *reinterpret_cast<const bf16x8*>(dkv_edge + ((size_t)csr_edge[p + q] * 64 * row_elems + i * 8));
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          if (p + q < p1) {
+#pragma unroll
+            for (int x = 0; x < 8; ++x) acc[x] += (float)v[q][x];
+          }
+      }
+      bf16x8 o;
+#pragma unroll
+      for (int x = 0; x < 8; ++x) o[x] = (bf16)acc[x];
+      *reinterpret_cast<bf16x8*>(red + (size_t)u * 64 * row_elems + i * 8) = o;
     }
-    bf16x8 o;
-#pragma unroll
-    for (int x = 0; x < 8; ++x) o[x] = (bf16)acc[x];
-    *reinterpret_cast<bf16x8*>(dst + i * 8) = o;
+    __syncthreads();
   }
 }
 
 // [Wk; Wv] (rows kv of each, any of f32 / bf16) -> wkv [2 kv][d] bf16 and / or its transpose
-// wkv_t [d][2 kv] (either may be null): 64 x 64 tiles through LDS.
+// wkv_t [d][2 kv] (either may be null).  One workgroup per 64 x 64 tile: 16-byte loads, the tile
+// kept in LDS as bf16 (rows padded to 72 elements), 16-byte stores of both layouts.  d and kv
+// are multiples of 8 (host check).
 template <typename TK, typename TV>
 __global__ __launch_bounds__(256) void weight_pack_kernel(const TK* __restrict__ wk, const TV* __restrict__ wv,
                                                           int64_t kv, int64_t d, bf16* __restrict__ wkv,
                                                           bf16* __restrict__ wkv_t) {
-  __shared__ float tile[64][65];
+  __shared__ __attribute__((aligned(16))) bf16 tile[64][72];
   const int64_t r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;
-  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
-  for (int rr = ty; rr < 64; rr += 4) {
-    const int64_t r = r0 + rr, c = c0 + tx;
-    float v = 0.f;
-    if (r < 2 * kv && c < d) v = r < kv ? to_f(wk[r * d + c]) : to_f(wv[(r - kv) * d + c]);
-    if (wkv && r < 2 * kv && c < d) wkv[r * d + c] = (bf16)v;
-    tile[rr][tx] = v;
+#pragma unroll
+  for (int it = 0; it < 2; ++it) {
+    const int q = threadIdx.x + 256 * it, rr = q >> 3, cc = (q & 7) * 8;
+    const int64_t r = r0 + rr, c = c0 + cc;
+    bf16x8 v;
+    if (r < 2 * kv && c < d) {
+      float f[8];
+      if (r < kv) ChunkLoad8<TK>::run(wk + r * d + c, f);
+      else ChunkLoad8<TV>::run(wv + (r - kv) * d + c, f);
+#pragma unroll
+      for (int x = 0; x < 8; ++x) v[x] = (bf16)f[x];
+      if (wkv) *reinterpret_cast<bf16x8*>(wkv + r * d + c) = v;
+    } else {
+#pragma unroll
+      for (int x = 0; x < 8; ++x) v[x] = (bf16)0.f;
+    }
+    *reinterpret_cast<bf16x8*>(&tile[rr][cc]) = v;
   }
   if (!wkv_t) return;
   __syncthreads();
-  for (int cc = ty; cc < 64; cc += 4) {
-    const int64_t c = c0 + cc, r = r0 + tx;
-    if (c < d && r < 2 * kv) wkv_t[c * 2 * kv + r] = (bf16)tile[tx][cc];
+#pragma unroll
+  for (int it = 0; it < 2; ++it) {
+    const int q = threadIdx.x + 256 * it, cc = q >> 3, rr = (q & 7) * 8;
+    const int64_t c = c0 + cc, r = r0 + rr;
+    if (c >= d || r >= 2 * kv) continue;
+    bf16x8 v;
+#pragma unroll
+    for (int x = 0; x < 8; ++x) v[x] = tile[rr + x][cc];
+    *reinterpret_cast<bf16x8*>(wkv_t + c * 2 * kv + r) = v;
   }
 }
 
@@ -336,11 +402,11 @@ int moc_chapter_project(const void* rows, int64_t ld, int gather, const int32_t*
   if (max_u == 0) return MOC_OK;
   const dim3 grid((unsigned)cg_grid());
   if (gather)
-    hipLaunchKernelGGL((chapter_gemm_kernel<CG_SRC_GATHER, CG_DST_CONTIG, bf16, 256>), grid, dim3(kCgThreads), 0,
+    hipLaunchKernelGGL((chapter_gemm_kernel<CG_SRC_GATHER, CG_DST_CONTIG, bf16, 256, kCgXpd>), grid, dim3(kCgThreads), 0,
                        stream, (const bf16*)rows, nullptr, ld, uniq, n_uniq, nullptr, nullptr, max_u, (const bf16*)w,
                        N, K, (bf16*)y, ldy);
   else
-    hipLaunchKernelGGL((chapter_gemm_kernel<CG_SRC_CONTIG, CG_DST_CONTIG, bf16, 256>), grid, dim3(kCgThreads), 0,
+    hipLaunchKernelGGL((chapter_gemm_kernel<CG_SRC_CONTIG, CG_DST_CONTIG, bf16, 256, kCgXpd>), grid, dim3(kCgThreads), 0,
                        stream, (const bf16*)rows, nullptr, ld, uniq, n_uniq, nullptr, nullptr, max_u, (const bf16*)w,
                        N, K, (bf16*)y, ldy);
   return check_launch("chapter_gemm_kernel(project)");
@@ -356,12 +422,12 @@ int moc_chapter_dx(const void* dkv_edge, int64_t ld, const int32_t* uniq, const 
               out_dtype);
   if (int rc = cg_check("moc_chapter_dx", ld, N, K, max_u, ldo)) return rc;
   if (max_u == 0) return MOC_OK;
-  hipLaunchKernelGGL(dkv_multi_reduce_kernel, dim3((unsigned)max_u, kMultiSplit), dim3(256), 0, stream,
+  hipLaunchKernelGGL(dkv_multi_reduce_kernel, dim3((unsigned)((64 * ld / 8 + 255) / 256), kMultiGroups), dim3(256), 0, stream,
                      (const bf16*)dkv_edge, n_uniq, csr_off, csr_edge, ld, (bf16*)red);
   if (int rc = check_launch("dkv_multi_reduce_kernel")) return rc;
   const dim3 grid((unsigned)cg_grid());
 #define MOC_CGDX(DST, TO)                                                                                           \
-  hipLaunchKernelGGL((chapter_gemm_kernel<CG_SRC_EDGE, DST, TO, kCgDxRows>), grid, dim3(kCgThreads), 0, stream,          \
+  hipLaunchKernelGGL((chapter_gemm_kernel<CG_SRC_EDGE, DST, TO, kCgDxRows, kCgXpd>), grid, dim3(kCgThreads), 0, stream,          \
                      (const bf16*)dkv_edge, (const bf16*)red, ld, uniq, n_uniq, csr_off, csr_edge, max_u,           \
                      (const bf16*)w_t, N, K, (TO*)out, ldo)
   if (out_bank_rows) {
@@ -376,7 +442,8 @@ int moc_chapter_dx(const void* dkv_edge, int64_t ld, const int32_t* uniq, const 
 int moc_weight_pack(const void* wk, int wk_dtype, const void* wv, int wv_dtype, int64_t kv, int64_t d, void* wkv,
                     void* wkv_t, hipStream_t stream) {
   MOC_REQUIRE(wk && wv && (wkv || wkv_t), MOC_ERR_ARG, "moc_weight_pack: null pointer");
-  MOC_REQUIRE(kv > 0 && d > 0 && 2 * kv * d < ((int64_t)1 << 40), MOC_ERR_ARG, "moc_weight_pack: bad shape");
+  MOC_REQUIRE(kv > 0 && d > 0 && kv % 8 == 0 && d % 8 == 0 && 2 * kv * d < ((int64_t)1 << 40), MOC_ERR_ARG,
+              "moc_weight_pack: kv=%lld, d=%lld must be positive multiples of 8", (long long)kv, (long long)d);
   const dim3 grid((unsigned)((d + 63) / 64), (unsigned)((2 * kv + 63) / 64));
 #define MOC_WP(TK, TV)                                                                                           \
   hipLaunchKernelGGL((weight_pack_kernel<TK, TV>), grid, dim3(256), 0, stream, (const TK*)wk, (const TV*)wv, kv, \
