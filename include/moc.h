@@ -170,7 +170,7 @@ int moc_chapter_project(const void* rows, int64_t ld, int gather, const int32_t*
  * out_c = (sum over the chapter's edges e, csr order, of dkv_edge rows e*64 .. +63) w_t^T, i.e.
  * out_c[j][n] = sum_k dK|dV_c[j][k] * w_t[n][k] with w_t [N = d][K = 2*HK*Dh] = [Wk; Wv]^T
  * (moc_weight_pack).  dkv_edge [E*64][ld] bf16 from moc_xattn_bwd_dkv; chapters with several
- * edges are summed first (fp32, rounded to bf16) into red [max_u*64][ld] bf16 (workspace).
+ * edges are read from red [max_u*64][ld] bf16, their sums from moc_dkv_multi_reduce.
  * out_bank_rows != 0: out is the dense bank gradient [N_m][ldo] and chapter c's rows are stored
  * at uniq[c]*64 .. +63 (the scatter-add of the gather's backward, memory_bank.py:287-291:
  * distinct chapters own distinct rows, so they are stored; the rest must be zero already);
@@ -181,6 +181,27 @@ int moc_chapter_project(const void* rows, int64_t ld, int gather, const int32_t*
 int moc_chapter_dx(const void* dkv_edge, int64_t ld, const int32_t* uniq, const int32_t* n_uniq, int64_t max_u,
                    const int32_t* csr_off, const int32_t* csr_edge, void* red, const void* w_t, int N, int K,
                    int out_dtype, void* out, int64_t ldo, int out_bank_rows, hipStream_t stream);
+/* Sums of the per-edge dK|dV rows of the chapters selected by more than one edge (csr order,
+ * fp32 accumulation, rounded to bf16): red [max_u*64][ld] (rows of other chapters untouched).
+ * Feeds moc_chapter_dx and moc_chapter_wgrad, which read a single-edge chapter's rows in place
+ * (the reference accumulates per chapter with its inverted-index kernel,
+ * kernels-final/kernel_v4.py:534-671). */
+int moc_dkv_multi_reduce(const void* dkv_edge, int64_t ld, const int32_t* n_uniq, int64_t max_u,
+                         const int32_t* csr_off, const int32_t* csr_edge, void* red, hipStream_t stream);
+/* Weight gradient of the K/V projection from the per-chapter rows: dw [N][K] (out_dtype f32 or
+ * bf16) = sum over chapters c < n_uniq of dK|dV_c^T X_c, with dK|dV_c read like moc_chapter_dx
+ * (one edge in place, several from red) and X_c the chapter's bank rows uniq[c]*64 .. (gather
+ * != 0, x = the bf16 bank, row stride ldx) or rows c*64 .. of a contiguous bf16 block (gather
+ * == 0, e.g. moc_gather_rows output for a normalised bank).  Replaces the autograd weight
+ * gradient of k_proj / v_proj (memory_transformer/memory_attention.py:241-243) over the gathered
+ * rows (memory_bank.py:263-293).  The chapters are split over several workgroups per 256 x 256
+ * output tile; ws (moc_chapter_wgrad_workspace bytes) holds their fp32 partials, summed in a
+ * fixed order.  N, K multiples of 256. */
+size_t moc_chapter_wgrad_workspace(int N, int K, int64_t max_u);
+int moc_chapter_wgrad(const void* dkv_edge, int64_t lda, const void* red, const void* x, int64_t ldx, int gather,
+                      const int32_t* uniq, const int32_t* n_uniq, int64_t max_u, const int32_t* csr_off,
+                      const int32_t* csr_edge, int N, int K, void* ws, size_t ws_bytes, int out_dtype, void* dw,
+                      hipStream_t stream);
 /* wkv [2*kv][d] bf16 = [wk; wv] and / or wkv_t [d][2*kv] bf16 = its transpose (either may be
  * NULL), from wk, wv [kv][d] of MOC_F32 / MOC_BF16: the concatenated K/V weight that the
  * chapter GEMMs read (the reference keeps k_proj and v_proj as two nn.Linear,

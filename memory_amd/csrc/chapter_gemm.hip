@@ -363,6 +363,141 @@ __global__ __launch_bounds__(256) void weight_pack_kernel(const TK* __restrict__
   }
 }
 
+// ------------------------------------------------------------ weight gradients
+//   dW[n][k] = sum over 64-row blocks c < nblk and rows j < 64 of A_c[j][n] * B_c[j][k]
+// A_c / B_c: the same per-block row sources as the GEMM above (a chapter's dK|dV rows, its bank
+// rows, or rows 64c .. of a dense matrix, rows past the matrix end reading zero).  The output is
+// small (N x K) and the reduction long, so the blocks are split over `splits` workgroups per
+// 256 x 256 output tile, each writing an fp32 partial tile that cg_wgrad_reduce_kernel sums in a
+// fixed order (deterministic).  Both operands keep the reduction index (rows) outermost, so the
+// MFMA fragments (8 consecutive rows of one column per lane) come from gfx950's transposing LDS
+// load ds_read_b64_tr_b16; the stage tiles are [64 rows][256 bf16] with 16-byte chunk c of row r
+// at c ^ ((r & 3) | ((r >> 3) & 3) << 2), which spreads the 16 rows of one transposing load over
+// 16 bank groups.  Operands move global -> LDS by LDS DMA, one block ahead.
+__device__ __forceinline__ int cg_tr_swz(int r) { return (r & 3) | (((r >> 3) & 3) << 2); }
+__device__ __forceinline__ int cg_tr_off(int row, int col) {
+  return row * 512 + ((((col >> 3) ^ cg_tr_swz(row)) & 31) << 4) + ((col & 7) << 1);
+}
+typedef short cg_v4s __attribute__((ext_vector_type(4)));
+// fragment: rows rb + 8 g + 0..7 (g = lane / 16) of column cb + lane % 16; within each 16-lane
+// group, lane q supplies the address of row q / 4, columns 4 (q % 4) .. + 3
+__device__ __forceinline__ bf16x8 cg_tr_frag(const char* base, int rb, int cb, int lane) {
+  const int q = lane & 15;
+  const int row = rb + 8 * (lane >> 4) + (q >> 2), col = cb + 4 * (q & 3);
+  typedef __attribute__((address_space(3))) cg_v4s* lds_v4s;
+  const cg_v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(base + cg_tr_off(row, col)));
+  const cg_v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(base + cg_tr_off(row + 4, col)));
+  const cg_v4s v[2] = {lo, hi};
+  return __builtin_bit_cast(bf16x8, v);
+}
+
+template <int SRC>
+__device__ __forceinline__ uint32_t cg_block_bytes(int c, int64_t ld, int64_t rows) {
+  if constexpr (SRC == CG_SRC_CONTIG) {
+    const int64_t left = rows - (int64_t)c * 64;
+    return (uint32_t)((left < 64 ? (left > 0 ? left : 0) : 64) * ld * 2);
+  } else {
+    return (uint32_t)(64 * ld * 2);
+  }
+}
+
+template <int SRCA, int SRCB>
+__global__ __launch_bounds__(kCgThreads) void chapter_wgrad_kernel(
+    const bf16* __restrict__ a, const bf16* __restrict__ ared, int64_t lda, int64_t arows, const bf16* __restrict__ b,
+    int64_t ldb, int64_t brows, const int32_t* __restrict__ uniq, const int32_t* __restrict__ n_uniq,
+    const int32_t* __restrict__ csr_off, const int32_t* __restrict__ csr_edge, int64_t nblk_max, int N, int K,
+    int splits, float* __restrict__ ws) {
+  constexpr int STG = 64 * 512;  // one operand stage: 64 rows x 256 bf16
+  __shared__ __attribute__((aligned(1024))) char smem[4 * STG];  // [buf][A | B]
+  const int nkb = K >> 8, tiles = (N >> 8) * nkb;
+  const int64_t t = xcd_tile((int64_t)tiles * splits);  // split major: a split's tiles share an XCD
+  if (t < 0) return;
+  const int tile = (int)(t % tiles), split = (int)(t / tiles);
+  const int n0 = (tile / nkb) * 256, k0 = (tile % nkb) * 256;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = rfl(tid >> 6);
+  const int wn = wave >> 2, wk = wave & 3;  // wave tile: 128 (n) x 64 (k)
+  const int nblk = n_uniq ? rfl((int)min((int64_t)n_uniq[0], nblk_max)) : (int)nblk_max;
+  const int per = (nblk + splits - 1) / splits;
+  const int s0 = min(nblk, split * per), s1 = min(nblk, s0 + per);
+
+  // DMA: instruction i of wave w fills LDS rows 16 i + 2 w + lane / 32, physical chunk lane % 32
+  const int r0 = 2 * wave + (lane >> 5);
+  uint32_t aoff[4], boff[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int c = (lane & 31) ^ cg_tr_swz(16 * i + r0);
+    aoff[i] = (uint32_t)(((int64_t)(16 * i + r0) * lda + n0 + 8 * c) * 2);
+    boff[i] = (uint32_t)(((int64_t)(16 * i + r0) * ldb + k0 + 8 * c) * 2);
+  }
+  auto issue = [&](int blk, int buf) {
+    const bf16* ab = cg_src_rows<SRCA>(blk, a, ared, lda, uniq, csr_off, csr_edge);
+    const bf16* bb = cg_src_rows<SRCB>(blk, b, nullptr, ldb, uniq, csr_off, csr_edge);
+    const __amdgpu_buffer_rsrc_t ar = CG_RSRC(ab, cg_block_bytes<SRCA>(blk, lda, arows));
+    const __amdgpu_buffer_rsrc_t br = CG_RSRC(bb, cg_block_bytes<SRCB>(blk, ldb, brows));
+    const char* da = smem + buf * 2 * STG + wave * 1024;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      cg_dma16(ar, aoff[i], 0u, da + 8192 * i);
+      cg_dma16(br, boff[i], 0u, da + STG + 8192 * i);
+    }
+  };
+
+  f32x4 acc[8][4];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  if (s0 < s1) issue(s0, 0);
+  for (int st = s0; st < s1; ++st) {
+    const int buf = (st - s0) & 1;
+    cg_wait_vm(0);
+    __syncthreads();  // block st landed for every wave; every wave is done with block st-1
+    __builtin_amdgcn_sched_barrier(0);
+    if (st + 1 < s1) issue(st + 1, buf ^ 1);
+    __builtin_amdgcn_sched_barrier(0);
+    const char* As = smem + buf * 2 * STG;
+    const char* Bs = As + STG;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      bf16x8 bfr[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) bfr[j] = cg_tr_frag(Bs, 32 * ks, 64 * wk + 16 * j, lane);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const bf16x8 afr = cg_tr_frag(As, 32 * ks, 128 * wn + 16 * i, lane);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) mma(acc[i][j], afr, bfr[j]);
+      }
+    }
+  }
+  // partial tile in accumulator order: [split][tile][wave][i][j][lane] f32x4
+  f32x4* out = reinterpret_cast<f32x4*>(ws) + (((size_t)split * tiles + tile) * 8 + wave) * 32 * 64 + lane;
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) out[(i * 4 + j) * 64] = acc[i][j];
+}
+
+// dW[n, k] = sum over splits (in order) of the partial tiles; one thread per f32x4.
+template <typename TO>
+__global__ __launch_bounds__(256) void cg_wgrad_reduce_kernel(const float* __restrict__ ws, int splits, int tiles,
+                                                              int nkb, int K, TO* __restrict__ dw) {
+  const int64_t p = (int64_t)blockIdx.x * 256 + threadIdx.x;  // f32x4 index within one split
+  const int64_t per_split = (int64_t)tiles * 8 * 32 * 64;
+  if (p >= per_split) return;
+  f32x4 s = reinterpret_cast<const f32x4*>(ws)[p];
+  for (int sp = 1; sp < splits; ++sp) s += reinterpret_cast<const f32x4*>(ws)[sp * per_split + p];
+  const int lane = (int)(p & 63), ij = (int)((p >> 6) & 31), wave = (int)((p >> 11) & 7);
+  const int tile = (int)(p >> 14);
+  const int i = ij >> 2, j = ij & 3, wn = wave >> 2, wk = wave & 3;
+  const int n = (tile / nkb) * 256 + 128 * wn + 16 * i + 4 * (lane >> 4);
+  const int64_t k = (int64_t)(tile % nkb) * 256 + 64 * wk + 16 * j + (lane & 15);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) dw[(int64_t)(n + e) * K + k] = from_f<TO>(s[e]);
+}
+
 int cg_grid() {
   static int cus = 0;
   if (cus == 0) {
@@ -387,7 +522,47 @@ int cg_check(const char* who, int64_t ldx, int N, int K, int64_t max_u, int64_t 
   return MOC_OK;
 }
 
+// workgroups per output tile of the weight gradients: fill the 256 CUs, but give each at least
+// 8 row blocks
+int cg_wgrad_splits(int tiles, int64_t blocks) {
+  int64_t s = 256 / tiles;
+  const int64_t by_len = (blocks + 7) / 8;
+  if (s > by_len) s = by_len;
+  if (s < 1) s = 1;
+  return (int)s;
+}
+
+int cg_wgrad_reduce(void* ws, int splits, int tiles, int K, int out_dtype, void* dw, hipStream_t stream) {
+  const int64_t n4 = (int64_t)tiles * 8 * 32 * 64;
+  const dim3 rgrid((unsigned)((n4 + 255) / 256));
+  if (out_dtype == MOC_F32)
+    hipLaunchKernelGGL(cg_wgrad_reduce_kernel<float>, rgrid, dim3(256), 0, stream, (const float*)ws, splits, tiles,
+                       K / 256, K, (float*)dw);
+  else
+    hipLaunchKernelGGL(cg_wgrad_reduce_kernel<bf16>, rgrid, dim3(256), 0, stream, (const float*)ws, splits, tiles,
+                       K / 256, K, (bf16*)dw);
+  return check_launch("cg_wgrad_reduce_kernel");
+}
+
 }  // namespace
+
+// Dense weight gradient dw [N][K] = dy^T x over R rows (dy [R][N], x [R][K], both bf16, row
+// strides N and K) on the chapter weight-gradient kernel; used by moc_linear_wgrad for the
+// shapes it tiles (N, K multiples of 256).  The split count (and so the workspace) follows the
+// same rule as moc_linear_wgrad_workspace.
+int chapter_wgrad_dense(const void* dy, const void* x, int64_t R, int64_t N, int64_t K, void* ws, int out_dtype,
+                        void* dw, hipStream_t stream) {
+  const int tiles = (int)((N / 256) * (K / 256));
+  const int64_t blocks = (R + 63) / 64;
+  const int splits = cg_wgrad_splits(tiles, blocks);
+  const dim3 grid(xcd_grid((int64_t)tiles * splits));
+  hipLaunchKernelGGL((chapter_wgrad_kernel<CG_SRC_CONTIG, CG_SRC_CONTIG>), grid, dim3(kCgThreads), 0, stream,
+                     (const bf16*)dy, (const bf16*)nullptr, (int64_t)N, R, (const bf16*)x, (int64_t)K, R, nullptr,
+                     nullptr, nullptr, nullptr, blocks, (int)N, (int)K, splits, (float*)ws);
+  if (int rc = check_launch("chapter_wgrad_kernel(dense)")) return rc;
+  return cg_wgrad_reduce(ws, splits, tiles, (int)K, out_dtype, dw, stream);
+}
+
 }  // namespace moc
 
 using namespace moc;
@@ -422,9 +597,6 @@ int moc_chapter_dx(const void* dkv_edge, int64_t ld, const int32_t* uniq, const 
               out_dtype);
   if (int rc = cg_check("moc_chapter_dx", ld, N, K, max_u, ldo)) return rc;
   if (max_u == 0) return MOC_OK;
-  hipLaunchKernelGGL(dkv_multi_reduce_kernel, dim3((unsigned)((64 * ld / 8 + 255) / 256), kMultiGroups), dim3(256), 0, stream,
-                     (const bf16*)dkv_edge, n_uniq, csr_off, csr_edge, ld, (bf16*)red);
-  if (int rc = check_launch("dkv_multi_reduce_kernel")) return rc;
   const dim3 grid((unsigned)cg_grid());
 #define MOC_CGDX(DST, TO)                                                                                           \
   hipLaunchKernelGGL((chapter_gemm_kernel<CG_SRC_EDGE, DST, TO, kCgDxRows, kCgXpd>), grid, dim3(kCgThreads), 0, stream,          \
@@ -437,6 +609,50 @@ int moc_chapter_dx(const void* dkv_edge, int64_t ld, const int32_t* uniq, const 
   }
 #undef MOC_CGDX
   return check_launch("chapter_gemm_kernel(dx)");
+}
+
+int moc_dkv_multi_reduce(const void* dkv_edge, int64_t ld, const int32_t* n_uniq, int64_t max_u,
+                         const int32_t* csr_off, const int32_t* csr_edge, void* red, hipStream_t stream) {
+  MOC_REQUIRE(dkv_edge && n_uniq && csr_off && csr_edge && red, MOC_ERR_ARG, "moc_dkv_multi_reduce: null pointer");
+  MOC_REQUIRE(ld > 0 && ld % 8 == 0 && max_u >= 0, MOC_ERR_ARG, "moc_dkv_multi_reduce: ld=%lld", (long long)ld);
+  if (max_u == 0) return MOC_OK;
+  hipLaunchKernelGGL(dkv_multi_reduce_kernel, dim3((unsigned)((64 * ld / 8 + 255) / 256), kMultiGroups), dim3(256), 0,
+                     stream, (const bf16*)dkv_edge, n_uniq, csr_off, csr_edge, ld, (bf16*)red);
+  return check_launch("dkv_multi_reduce_kernel");
+}
+
+size_t moc_chapter_wgrad_workspace(int N, int K, int64_t max_u) {
+  if (N <= 0 || K <= 0 || N % 256 || K % 256) return 0;
+  const int tiles = (N / 256) * (K / 256);
+  return (size_t)cg_wgrad_splits(tiles, max_u) * tiles * 256 * 256 * sizeof(float);
+}
+
+int moc_chapter_wgrad(const void* dkv_edge, int64_t lda, const void* red, const void* x, int64_t ldx, int gather,
+                      const int32_t* uniq, const int32_t* n_uniq, int64_t max_u, const int32_t* csr_off,
+                      const int32_t* csr_edge, int N, int K, void* ws, size_t ws_bytes, int out_dtype, void* dw,
+                      hipStream_t stream) {
+  MOC_REQUIRE(dkv_edge && red && x && uniq && n_uniq && csr_off && csr_edge && ws && dw, MOC_ERR_ARG,
+              "moc_chapter_wgrad: null pointer");
+  MOC_REQUIRE(N > 0 && N % 256 == 0 && K > 0 && K % 256 == 0, MOC_ERR_UNSUPPORTED,
+              "moc_chapter_wgrad: N=%d, K=%d must be positive multiples of 256", N, K);
+  MOC_REQUIRE(lda >= N && lda % 8 == 0 && ldx >= K && ldx % 8 == 0 && 64 * lda * 2 < ((int64_t)1 << 31) &&
+                  64 * ldx * 2 < ((int64_t)1 << 31) && max_u >= 0 && max_u < ((int64_t)1 << 30),
+              MOC_ERR_ARG, "moc_chapter_wgrad: bad strides");
+  MOC_REQUIRE(ws_bytes >= moc_chapter_wgrad_workspace(N, K, max_u), MOC_ERR_ARG, "moc_chapter_wgrad: workspace too small");
+  MOC_REQUIRE(out_dtype == MOC_F32 || out_dtype == MOC_BF16, MOC_ERR_UNSUPPORTED, "moc_chapter_wgrad: out dtype %d",
+              out_dtype);
+  const int tiles = (N / 256) * (K / 256), splits = cg_wgrad_splits(tiles, max_u);
+  const dim3 grid(xcd_grid((int64_t)tiles * splits));
+  if (gather)
+    hipLaunchKernelGGL((chapter_wgrad_kernel<CG_SRC_EDGE, CG_SRC_GATHER>), grid, dim3(kCgThreads), 0, stream,
+                       (const bf16*)dkv_edge, (const bf16*)red, lda, (int64_t)0, (const bf16*)x, ldx, (int64_t)0, uniq,
+                       n_uniq, csr_off, csr_edge, max_u, N, K, splits, (float*)ws);
+  else
+    hipLaunchKernelGGL((chapter_wgrad_kernel<CG_SRC_EDGE, CG_SRC_CONTIG>), grid, dim3(kCgThreads), 0, stream,
+                       (const bf16*)dkv_edge, (const bf16*)red, lda, (int64_t)0, (const bf16*)x, ldx, max_u * 64, uniq,
+                       n_uniq, csr_off, csr_edge, max_u, N, K, splits, (float*)ws);
+  if (int rc = check_launch("chapter_wgrad_kernel")) return rc;
+  return cg_wgrad_reduce(ws, splits, tiles, K, out_dtype, dw, stream);
 }
 
 int moc_weight_pack(const void* wk, int wk_dtype, const void* wv, int wv_dtype, int64_t kv, int64_t d, void* wkv,

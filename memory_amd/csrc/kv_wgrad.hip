@@ -192,6 +192,11 @@ __global__ __launch_bounds__(256) void kv_wgrad_reduce_kernel(const float* __res
 
 }  // namespace moc
 
+namespace moc {
+int chapter_wgrad_dense(const void* dy, const void* x, int64_t R, int64_t N, int64_t K, void* ws, int out_dtype,
+                        void* dw, hipStream_t stream);
+}
+
 using namespace moc;
 
 namespace {
@@ -282,6 +287,11 @@ int moc_linear_wgrad(const void* dy, const void* x, int x_dtype, int64_t R, int6
   MOC_REQUIRE(R >= 0 && N > 0 && N % 8 == 0 && N < (1 << 30) && K > 0 && K % 8 == 0, MOC_ERR_UNSUPPORTED,
               "moc_linear_wgrad: N=%lld K=%lld must be multiples of 8", (long long)N, (long long)K);
   MOC_REQUIRE(ws_bytes >= moc_linear_wgrad_workspace(R, N, K), MOC_ERR_ARG, "moc_linear_wgrad: workspace too small");
+  MOC_REQUIRE(out_dtype == MOC_F32 || out_dtype == MOC_BF16, MOC_ERR_UNSUPPORTED, "moc_linear_wgrad: out dtype %d",
+              out_dtype);
+  // bf16 operands on 256-multiples: the LDS-DMA chapter weight-gradient kernel (same splits)
+  if (x_dtype == MOC_BF16 && N % 256 == 0 && K % 256 == 0 && R > 0 && R * (N > K ? N : K) * 2 < ((int64_t)1 << 40))
+    return chapter_wgrad_dense(dy, x, R, N, K, ws, out_dtype, dw, stream);
   return launch_wgrad<false>(dy, x, x_dtype, K, nullptr, nullptr, nullptr, 0, R, nullptr, nullptr, N, (R + 63) / 64,
                              ws, out_dtype, dw, stream);
 }

@@ -272,13 +272,23 @@ def chapter_project(rows: torch.Tensor, plan: ChapterPlan, wkv: torch.Tensor, ga
     return y
 
 
-def chapter_dx(dkv_edge: torch.Tensor, uniq, n_uniq, max_u: int, csr_off, csr_edge, wkv_t: torch.Tensor,
-               out: torch.Tensor, bank_rows: bool) -> torch.Tensor:
+def dkv_multi_reduce(dkv_edge: torch.Tensor, n_uniq, max_u: int, csr_off, csr_edge) -> torch.Tensor:
+    """Sums of the dK|dV rows of the chapters selected by several edges ([max_u * 64][2*KV]
+    bf16; rows of single-edge chapters are not written)."""
+    K = dkv_edge.shape[1]
+    red = torch.empty(max_u * 64, K, device=dkv_edge.device, dtype=torch.bfloat16)
+    call("moc_dkv_multi_reduce", ptr(dkv_edge), dkv_edge.stride(0), ptr(n_uniq), max_u, ptr(csr_off), ptr(csr_edge),
+         ptr(red), stream_ptr(dkv_edge.device))
+    return red
+
+
+def chapter_dx(dkv_edge: torch.Tensor, red: torch.Tensor, uniq, n_uniq, max_u: int, csr_off, csr_edge,
+               wkv_t: torch.Tensor, out: torch.Tensor, bank_rows: bool) -> torch.Tensor:
     """Per-chapter input gradient of the K/V projection, summed over each chapter's edges:
     stored at the chapter's bank rows of ``out`` (bank_rows) or at rows c*64.. of ``out``
-    ([max_u * 64][d]).  dkv_edge [E*64][2*KV] bf16, wkv_t [d][2*KV] bf16."""
+    ([max_u * 64][d]).  dkv_edge [E*64][2*KV] bf16, red from dkv_multi_reduce, wkv_t [d][2*KV]
+    bf16."""
     N, K = wkv_t.shape
-    red = torch.empty(max_u * 64, K, device=dkv_edge.device, dtype=torch.bfloat16)
     call("moc_chapter_dx", ptr(dkv_edge), dkv_edge.stride(0), ptr(uniq), ptr(n_uniq), max_u, ptr(csr_off),
          ptr(csr_edge), ptr(red), ptr(wkv_t), N, K, L.dtype_code(out.dtype), ptr(out), out.stride(0),
          1 if bank_rows else 0, stream_ptr(dkv_edge.device))
@@ -568,20 +578,42 @@ class _RoutedAttention(torch.autograd.Function):
         dbank = dwk = dwv = None
         E = B * NS
         if dtype == torch.bfloat16:
-            # per-edge dK/dV rows feed both products directly: the weight gradient pairs edge e's
-            # rows with its chapter's bank rows, and the bank scatter sums dX over each chapter's
-            # edges (csr order), so no per-chapter reduction pass is needed
+            # the chapter GEMMs read a chapter's dK|dV rows in place when one edge selected it and
+            # from `red` (the edges' sum, written once here) when several did
+            tiled = T == 64 and d % 256 == 0 and (2 * KV) % 256 == 0
+            red = None
+            if tiled and (need_bank or need_wk or need_wv):
+                red = torch.empty(max_u * T, 2 * KV, device=dev, dtype=torch.bfloat16)
+                call("moc_dkv_multi_reduce", ptr(dkv_edge), 2 * KV, ptr(n_uniq), max_u, ptr(csr_off), ptr(csr_edge),
+                     ptr(red), st)
             if need_wk or need_wv:
-                ws = torch.empty(L.query("moc_kv_wgrad_workspace", 2 * KV, d, E) // 4, device=dev,
-                                 dtype=torch.float32)
                 out_dt = torch.float32 if torch.float32 in (wk_dtype, wv_dtype) else dtype
                 dwkv = torch.empty(2 * KV, d, device=dev, dtype=out_dt)
-                call("moc_kv_wgrad", ptr(dkv_edge), ptr(bank), L.dtype_code(bank.dtype), d, T, ptr(uniq),
-                     ptr(n_uniq), ptr(edge_u), E, ptr(mean), ptr(rstd), 2 * KV, ptr(ws), ws.numel() * 4,
-                     L.dtype_code(out_dt), ptr(dwkv), st)
+                if tiled:
+                    # dW = sum over distinct chapters of dK|dV_c^T X_c (bank rows gathered by the
+                    # kernel; a normalised or f32 bank is gathered into bf16 rows first)
+                    ws_bytes = L.query("moc_chapter_wgrad_workspace", 2 * KV, d, max_u)
+                    ws = torch.empty(ws_bytes // 4, device=dev, dtype=torch.float32)
+                    if norm == L.MOC_NORM_NONE and bank.dtype == torch.bfloat16:
+                        xs, gather = bank, 1
+                    else:
+                        xs = torch.empty(max_u * T, d, device=dev, dtype=torch.bfloat16)
+                        call("moc_gather_rows", L.MOC_BF16, ptr(bank), L.dtype_code(bank.dtype), d, T, ptr(uniq),
+                             ptr(n_uniq), max_u, ptr(mean), ptr(rstd), ptr(xs), st)
+                        gather = 0
+                    call("moc_chapter_wgrad", ptr(dkv_edge), 2 * KV, ptr(red), ptr(xs), xs.stride(0), gather,
+                         ptr(uniq), ptr(n_uniq), max_u, ptr(csr_off), ptr(csr_edge), 2 * KV, d, ptr(ws), ws_bytes,
+                         L.dtype_code(out_dt), ptr(dwkv), st)
+                else:
+                    # per-edge rows paired with their chapter's bank rows (no per-chapter sums needed)
+                    ws = torch.empty(L.query("moc_kv_wgrad_workspace", 2 * KV, d, E) // 4, device=dev,
+                                     dtype=torch.float32)
+                    call("moc_kv_wgrad", ptr(dkv_edge), ptr(bank), L.dtype_code(bank.dtype), d, T, ptr(uniq),
+                         ptr(n_uniq), ptr(edge_u), E, ptr(mean), ptr(rstd), 2 * KV, ptr(ws), ws.numel() * 4,
+                         L.dtype_code(out_dt), ptr(dwkv), st)
                 dwk = dwkv[:KV].to(wk_dtype) if need_wk else None
                 dwv = dwkv[KV:].to(wv_dtype) if need_wv else None
-            if need_bank and not (T == 64 and d % 256 == 0 and (2 * KV) % 64 == 0):
+            if need_bank and not tiled:
                 # shapes outside the chapter GEMM's tiling: per-edge dX on the library GEMM,
                 # summed per chapter by the scatter
                 dX = torch.matmul(dkv_edge, wkv)  # rows of skipped edges are never read
@@ -603,11 +635,11 @@ class _RoutedAttention(torch.autograd.Function):
                     dbank, filled = dbank_zero
                     if filled is not None:
                         torch.cuda.current_stream(dev).wait_event(filled)
-                    chapter_dx(dkv_edge, uniq, n_uniq, max_u, csr_off, csr_edge, wkv_t, dbank, bank_rows=True)
+                    chapter_dx(dkv_edge, red, uniq, n_uniq, max_u, csr_off, csr_edge, wkv_t, dbank, bank_rows=True)
                     dbank = dbank.to(bank_dtype)   # the bank read may be a mirror of another dtype
                 else:
                     dXc = torch.empty(max_u * T, d, device=dev, dtype=torch.float32)
-                    chapter_dx(dkv_edge, uniq, n_uniq, max_u, csr_off, csr_edge, wkv_t, dXc, bank_rows=False)
+                    chapter_dx(dkv_edge, red, uniq, n_uniq, max_u, csr_off, csr_edge, wkv_t, dXc, bank_rows=False)
                     if ctx.row_grad is not None:
                         ctx.row_grad.accumulate(dXc, bank, uniq, n_uniq, max_u, None, None, mean, rstd, norm)
                     else:

@@ -115,7 +115,9 @@ def test_chapter_dx(dev, out_dtype, bank_rows, shape):
         out = torch.zeros(C * T, d, device=dev, dtype=out_dtype)
     else:
         out = torch.full((plan.max_u * T, d), float("nan"), device=dev, dtype=out_dtype)
-    ops.chapter_dx(dkv.to(dev), plan.uniq, plan.n_uniq, plan.max_u, plan.csr_off, plan.csr_edge, wkv_t, out,
+    dkv_d = dkv.to(dev)
+    red = ops.dkv_multi_reduce(dkv_d, plan.n_uniq, plan.max_u, plan.csr_off, plan.csr_edge)
+    ops.chapter_dx(dkv_d, red, plan.uniq, plan.n_uniq, plan.max_u, plan.csr_off, plan.csr_edge, wkv_t, out,
                    bank_rows=bank_rows)
     o = out.cpu()
     print(f"C={C} E={E} n_uniq={n_u} d={d} K={K} out={out_dtype} bank_rows={bank_rows}")
@@ -129,3 +131,59 @@ def test_chapter_dx(dev, out_dtype, bank_rows, shape):
         if plan.max_u > n_u:
             assert torch.isnan(o[n_u * T:].float()).all(), "unused plan slots must not be written"
     assert_parity(got, ref_c, torch.bfloat16, "dX per chapter")
+
+
+@pytest.mark.parametrize("gather", [True, False])
+@pytest.mark.parametrize("shape", [(60, 4, 9, 256, 512), (600, 8, 65, 768, 1536)])
+def test_chapter_wgrad(dev, gather, shape):
+    """dW = sum over distinct chapters of (sum of the chapter's edge rows)^T X_c: the weight
+    gradient of k_proj / v_proj over the gathered rows (memory_attention.py:241-243)."""
+    ops = _ops()
+    from memory_amd import _lib as L
+    C, NSEQ, NS, d, K = shape
+    T = 64
+    chap = _dx_case(C, NSEQ, NS, 21)
+    E = chap.numel()
+    plan = _plan(ops, dev, chap, C)
+    n_u = int(plan.n_uniq[0])
+    uniq = plan.uniq[:n_u].cpu().long()
+    dkv = torch.randn(E * T, K, generator=gen(22)).to(torch.bfloat16)
+    bank = torch.randn(C * T, d, generator=gen(23)).to(torch.bfloat16)
+    flat = chap.reshape(-1)
+    ref = torch.zeros(K, d, dtype=torch.float64)
+    for u in range(n_u):
+        edges = (flat == uniq[u]).nonzero().view(-1)
+        s = sum(dkv[e * T:(e + 1) * T].double() for e in edges.tolist())
+        ref += s.t() @ bank.view(C, T, d)[uniq[u]].double()
+    dkv_d = dkv.to(dev)
+    red = ops.dkv_multi_reduce(dkv_d, plan.n_uniq, plan.max_u, plan.csr_off, plan.csr_edge)
+    if gather:
+        xs = bank.to(dev)
+    else:
+        xs = torch.zeros(plan.max_u * T, d, dtype=torch.bfloat16)
+        xs[: n_u * T] = bank.view(C, T, d)[uniq].reshape(-1, d)
+        xs = xs.to(dev)
+    ws_bytes = L.query("moc_chapter_wgrad_workspace", K, d, plan.max_u)
+    ws = torch.empty(ws_bytes // 4, device=dev)
+    for out_dtype in (torch.float32, torch.bfloat16):
+        dw = torch.empty(K, d, device=dev, dtype=out_dtype)
+        L.call("moc_chapter_wgrad", dkv_d.data_ptr(), K, red.data_ptr(), xs.data_ptr(), xs.stride(0), int(gather),
+               plan.uniq.data_ptr(), plan.n_uniq.data_ptr(), plan.max_u, plan.csr_off.data_ptr(),
+               plan.csr_edge.data_ptr(), K, d, ws.data_ptr(), ws_bytes, L.dtype_code(out_dtype), dw.data_ptr(),
+               torch.cuda.current_stream().cuda_stream)
+        print(f"C={C} E={E} n_uniq={n_u} d={d} K={K} gather={gather} out={out_dtype}")
+        assert_parity(dw.cpu(), ref, torch.bfloat16, "dW")
+
+
+@pytest.mark.parametrize("shape", [(8192, 768, 768), (1000, 512, 256)])
+def test_dense_wgrad_lds_dma_path(dev, shape):
+    """moc_linear_wgrad on bf16 operands with N, K multiples of 256 (the chapter weight-gradient
+    kernel, rows past R reading zero) against a float64 product."""
+    ops = _ops()
+    R, N, K = shape
+    dy = torch.randn(R, N, generator=gen(31)).to(torch.bfloat16)
+    x = torch.randn(R, K, generator=gen(32)).to(torch.bfloat16)
+    dw = ops.linear_wgrad(dy.to(dev), x.to(dev), torch.float32)
+    ref = dy.double().t() @ x.double()
+    print(f"R={R} N={N} K={K}")
+    assert_parity(dw.cpu(), ref, torch.bfloat16, "dW dense")
