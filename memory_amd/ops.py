@@ -586,33 +586,32 @@ class _RoutedAttention(torch.autograd.Function):
                 red = torch.empty(max_u * T, 2 * KV, device=dev, dtype=torch.bfloat16)
                 call("moc_dkv_multi_reduce", ptr(dkv_edge), 2 * KV, ptr(n_uniq), max_u, ptr(csr_off), ptr(csr_edge),
                      ptr(red), st)
+            dwkv = None
             if need_wk or need_wv:
                 out_dt = torch.float32 if torch.float32 in (wk_dtype, wv_dtype) else dtype
                 dwkv = torch.empty(2 * KV, d, device=dev, dtype=out_dt)
                 if tiled:
-                    # dW = sum over distinct chapters of dK|dV_c^T X_c (bank rows gathered by the
-                    # kernel; a normalised or f32 bank is gathered into bf16 rows first)
+                    # dW = sum over distinct chapters of dK|dV_c^T X_c (bank rows gathered by
+                    # the kernel; a normalised or f32 bank is gathered into bf16 rows first)
                     ws_bytes = L.query("moc_chapter_wgrad_workspace", 2 * KV, d, max_u)
                     ws = torch.empty(ws_bytes // 4, device=dev, dtype=torch.float32)
                     if norm == L.MOC_NORM_NONE and bank.dtype == torch.bfloat16:
                         xs, gather = bank, 1
                     else:
                         xs = torch.empty(max_u * T, d, device=dev, dtype=torch.bfloat16)
-                        call("moc_gather_rows", L.MOC_BF16, ptr(bank), L.dtype_code(bank.dtype), d, T, ptr(uniq),
-                             ptr(n_uniq), max_u, ptr(mean), ptr(rstd), ptr(xs), st)
+                        call("moc_gather_rows", L.MOC_BF16, ptr(bank), L.dtype_code(bank.dtype), d, T,
+                             ptr(uniq), ptr(n_uniq), max_u, ptr(mean), ptr(rstd), ptr(xs), st)
                         gather = 0
                     call("moc_chapter_wgrad", ptr(dkv_edge), 2 * KV, ptr(red), ptr(xs), xs.stride(0), gather,
-                         ptr(uniq), ptr(n_uniq), max_u, ptr(csr_off), ptr(csr_edge), 2 * KV, d, ptr(ws), ws_bytes,
-                         L.dtype_code(out_dt), ptr(dwkv), st)
+                         ptr(uniq), ptr(n_uniq), max_u, ptr(csr_off), ptr(csr_edge), 2 * KV, d, ptr(ws),
+                         ws_bytes, L.dtype_code(out_dt), ptr(dwkv), st)
                 else:
-                    # per-edge rows paired with their chapter's bank rows (no per-chapter sums needed)
+                    # per-edge rows paired with their chapter's bank rows (no per-chapter sums)
                     ws = torch.empty(L.query("moc_kv_wgrad_workspace", 2 * KV, d, E) // 4, device=dev,
                                      dtype=torch.float32)
-                    call("moc_kv_wgrad", ptr(dkv_edge), ptr(bank), L.dtype_code(bank.dtype), d, T, ptr(uniq),
-                         ptr(n_uniq), ptr(edge_u), E, ptr(mean), ptr(rstd), 2 * KV, ptr(ws), ws.numel() * 4,
-                         L.dtype_code(out_dt), ptr(dwkv), st)
-                dwk = dwkv[:KV].to(wk_dtype) if need_wk else None
-                dwv = dwkv[KV:].to(wv_dtype) if need_wv else None
+                    call("moc_kv_wgrad", ptr(dkv_edge), ptr(bank), L.dtype_code(bank.dtype), d, T,
+                         ptr(uniq), ptr(n_uniq), ptr(edge_u), E, ptr(mean), ptr(rstd), 2 * KV, ptr(ws),
+                         ws.numel() * 4, L.dtype_code(out_dt), ptr(dwkv), st)
             if need_bank and not tiled:
                 # shapes outside the chapter GEMM's tiling: per-edge dX on the library GEMM,
                 # summed per chapter by the scatter
@@ -650,6 +649,9 @@ class _RoutedAttention(torch.autograd.Function):
                              L.dtype_code(bank.dtype), d, T, ptr(uniq), ptr(n_uniq), max_u, None, None, ptr(mean),
                              ptr(rstd), norm, ptr(dbank), st)
                         dbank = dbank.to(bank_dtype)
+            if dwkv is not None:
+                dwk = dwkv[:KV].to(wk_dtype) if need_wk else None
+                dwv = dwkv[KV:].to(wv_dtype) if need_wv else None
             return dq, dbank, dwk, dwv, domega, None, None, None, None, None, None
         # fp32: sum per distinct chapter first, then library GEMMs
         dkv = torch.empty(max_u * T, 2 * KV, device=dev, dtype=dtype)
@@ -677,10 +679,10 @@ class _RoutedAttention(torch.autograd.Function):
 _SIDE_STREAMS: dict = {}
 
 
-def _side_stream(dev: torch.device) -> torch.cuda.Stream:
-    """A second stream (default priority) per device for work that runs beside the main
-    sequence of kernels."""
-    key = (dev.type, dev.index)
+def _side_stream(dev: torch.device, name: str = "fill") -> torch.cuda.Stream:
+    """A second stream (default priority) per device and purpose for work that runs beside
+    the main sequence of kernels."""
+    key = (dev.type, dev.index, name)
     s = _SIDE_STREAMS.get(key)
     if s is None:
         s = _SIDE_STREAMS[key] = torch.cuda.Stream(device=dev)
