@@ -181,6 +181,12 @@ int moc_chapter_project(const void* rows, int64_t ld, int gather, const int32_t*
 int moc_chapter_dx(const void* dkv_edge, int64_t ld, const int32_t* uniq, const int32_t* n_uniq, int64_t max_u,
                    const int32_t* csr_off, const int32_t* csr_edge, void* red, const void* w_t, int N, int K,
                    int out_dtype, void* out, int64_t ldo, int out_bank_rows, hipStream_t stream);
+/* y [R][N] = x [R][K] w^T on the chapter GEMM (bf16 in and out, fp32 accumulation), x and y row
+ * strides ldx, ldy: the bias-free nn.Linear of the memory layer's q_proj / o_proj
+ * (memory_transformer/memory_attention.py:140-143, :241, :456) and its input gradient (w = the
+ * transposed weight).  N % 256 == 0, K % 64 == 0. */
+int moc_rows_linear(const void* x, int64_t ldx, int64_t R, const void* w, int N, int K, void* y, int64_t ldy,
+                    hipStream_t stream);
 /* Sums of the per-edge dK|dV rows of the chapters selected by more than one edge (csr order,
  * fp32 accumulation, rounded to bf16): red [max_u*64][ld] (rows of other chapters untouched).
  * Feeds moc_chapter_dx and moc_chapter_wgrad, which read a single-edge chapter's rows in place

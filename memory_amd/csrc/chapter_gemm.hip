@@ -109,7 +109,8 @@ template <int SRC, int DST, typename TO, int BM, int XPD>
 __global__ __launch_bounds__(kCgThreads) void chapter_gemm_kernel(
     const bf16* __restrict__ x, const bf16* __restrict__ xred, int64_t ldx, const int32_t* __restrict__ uniq,
     const int32_t* __restrict__ n_uniq, const int32_t* __restrict__ csr_off, const int32_t* __restrict__ csr_edge,
-    int64_t max_u, const bf16* __restrict__ w, int N, int K, TO* __restrict__ y, int64_t ldy) {
+    int64_t max_u, const bf16* __restrict__ w, int N, int K, TO* __restrict__ y, int64_t ldy, int64_t xrows,
+    int64_t yrows) {
   constexpr int CPT = BM / 64;              // chapters per tile
   constexpr int IPX = BM / 64;              // X DMA instructions per thread per stage
   constexpr int JB = BM / 32;               // 16-row MFMA tiles per wave
@@ -122,7 +123,7 @@ __global__ __launch_bounds__(kCgThreads) void chapter_gemm_kernel(
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = rfl(tid >> 6);
-  const int nu = rfl((int)min((int64_t)n_uniq[0], max_u));
+  const int nu = n_uniq ? rfl((int)min((int64_t)n_uniq[0], max_u)) : (int)max_u;
   const int NB = N >> 8;
   const int V = ((nu + CPT - 1) / CPT) * NB;  // tiles: row blocks x feature blocks
   const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3, nslot = gridDim.x >> 3;
@@ -158,7 +159,9 @@ __global__ __launch_bounds__(kCgThreads) void chapter_gemm_kernel(
     for (int i = 0; i < IPX; ++i) {
       const int c = min(rb * CPT + i, nu - 1);  // rows of chapters past n_uniq: computed, not stored
       const bf16* xb = cg_src_rows<SRC>(c, x, xred, ldx, uniq, csr_off, csr_edge);
-      cg_dma16(CG_RSRC(xb, xbytes), xoff, (uint32_t)(kt * 128), dst + 8192 * i);
+      // a contiguous source ends at row xrows: rows past it read zero
+      const uint32_t nb = SRC == CG_SRC_CONTIG ? (uint32_t)(min((int64_t)64, xrows - (int64_t)c * 64) * ldx * 2) : xbytes;
+      cg_dma16(CG_RSRC(xb, nb), xoff, (uint32_t)(kt * 128), dst + 8192 * i);
     }
   };
 
@@ -208,7 +211,9 @@ __global__ __launch_bounds__(kCgThreads) void chapter_gemm_kernel(
       const bool live = c < nu;
       const int cc = live ? c : 0;
       TO* dst = DST == CG_DST_BANK ? y + (int64_t)rfl(uniq[cc]) * 64 * ldy : y + (int64_t)cc * 64 * ldy;
-      const __amdgpu_buffer_rsrc_t yres = CG_RSRC(dst, live ? (uint32_t)(64 * ldy * sizeof(TO)) : 0u);
+      // a contiguous destination ends at row yrows: stores past it are dropped
+      const int64_t yr = DST == CG_DST_CONTIG ? min((int64_t)64, yrows - (int64_t)cc * 64) : 64;
+      const __amdgpu_buffer_rsrc_t yres = CG_RSRC(dst, live ? (uint32_t)(yr * ldy * sizeof(TO)) : 0u);
       const uint32_t vrow = (uint32_t)((((rt & 63) + m) * ldy + nb * 256 + 64 * wf + 8 * g) * sizeof(TO));
 #pragma unroll
       for (int p = 0; p < 2; ++p) {
@@ -579,11 +584,11 @@ int moc_chapter_project(const void* rows, int64_t ld, int gather, const int32_t*
   if (gather)
     hipLaunchKernelGGL((chapter_gemm_kernel<CG_SRC_GATHER, CG_DST_CONTIG, bf16, 256, kCgXpd>), grid, dim3(kCgThreads), 0,
                        stream, (const bf16*)rows, nullptr, ld, uniq, n_uniq, nullptr, nullptr, max_u, (const bf16*)w,
-                       N, K, (bf16*)y, ldy);
+                       N, K, (bf16*)y, ldy, max_u * 64, max_u * 64);
   else
     hipLaunchKernelGGL((chapter_gemm_kernel<CG_SRC_CONTIG, CG_DST_CONTIG, bf16, 256, kCgXpd>), grid, dim3(kCgThreads), 0,
                        stream, (const bf16*)rows, nullptr, ld, uniq, n_uniq, nullptr, nullptr, max_u, (const bf16*)w,
-                       N, K, (bf16*)y, ldy);
+                       N, K, (bf16*)y, ldy, max_u * 64, max_u * 64);
   return check_launch("chapter_gemm_kernel(project)");
 }
 
@@ -601,7 +606,7 @@ int moc_chapter_dx(const void* dkv_edge, int64_t ld, const int32_t* uniq, const 
 #define MOC_CGDX(DST, TO)                                                                                           \
   hipLaunchKernelGGL((chapter_gemm_kernel<CG_SRC_EDGE, DST, TO, kCgDxRows, kCgXpd>), grid, dim3(kCgThreads), 0, stream,          \
                      (const bf16*)dkv_edge, (const bf16*)red, ld, uniq, n_uniq, csr_off, csr_edge, max_u,           \
-                     (const bf16*)w_t, N, K, (TO*)out, ldo)
+                     (const bf16*)w_t, N, K, (TO*)out, ldo, max_u * 64, max_u * 64)
   if (out_bank_rows) {
     if (out_dtype == MOC_BF16) MOC_CGDX(CG_DST_BANK, bf16); else MOC_CGDX(CG_DST_BANK, float);
   } else {
@@ -609,6 +614,19 @@ int moc_chapter_dx(const void* dkv_edge, int64_t ld, const int32_t* uniq, const 
   }
 #undef MOC_CGDX
   return check_launch("chapter_gemm_kernel(dx)");
+}
+
+int moc_rows_linear(const void* x, int64_t ldx, int64_t R, const void* w, int N, int K, void* y, int64_t ldy,
+                    hipStream_t stream) {
+  MOC_REQUIRE(x && w && y, MOC_ERR_ARG, "moc_rows_linear: null pointer");
+  MOC_REQUIRE(R >= 0 && R < ((int64_t)1 << 36), MOC_ERR_ARG, "moc_rows_linear: R=%lld", (long long)R);
+  const int64_t blocks = (R + 63) / 64;
+  if (int rc = cg_check("moc_rows_linear", ldx, N, K, blocks, ldy)) return rc;
+  if (R == 0) return MOC_OK;
+  hipLaunchKernelGGL((chapter_gemm_kernel<CG_SRC_CONTIG, CG_DST_CONTIG, bf16, 128, kCgXpd>), dim3((unsigned)cg_grid()),
+                     dim3(kCgThreads), 0, stream, (const bf16*)x, nullptr, ldx, nullptr, nullptr, nullptr, nullptr,
+                     blocks, (const bf16*)w, N, K, (bf16*)y, ldy, R, R);
+  return check_launch("chapter_gemm_kernel(rows)");
 }
 
 int moc_dkv_multi_reduce(const void* dkv_edge, int64_t ld, const int32_t* n_uniq, int64_t max_u,

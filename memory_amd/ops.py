@@ -305,11 +305,22 @@ def kv_rows_layout(kv: torch.Tensor, T: int, HK: int, Dh: int):
 
 # ------------------------------------------------------------- dense projections
 
+def rows_linear(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """x W^T on the chapter GEMM over 64-row blocks of x (bf16, fp32 accumulation); w [N][K]."""
+    N, K = w.shape
+    x2 = x.reshape(-1, K).contiguous()
+    wc = w.contiguous()
+    y = torch.empty(x2.shape[0], N, device=x.device, dtype=x.dtype)
+    call("moc_rows_linear", ptr(x2), K, x2.shape[0], ptr(wc), N, K, ptr(y), N, stream_ptr(x.device))
+    return y.view(*x.shape[:-1], N)
+
+
 class _Linear(torch.autograd.Function):
     """y = x W^T (bias-free nn.Linear of the memory layer's q_proj / o_proj,
     memory_transformer/memory_attention.py:140-143, :241 and :456).  The weight gradient
-    dW = dy^T x runs on the split-row MFMA kernel (the token dimension is long and
-    the output small); forward and dx stay on hipBLASLt."""
+    dW = dy^T x runs on the split-row MFMA kernel (the token dimension is long and the output
+    small); forward and dx stay on hipBLASLt (at 8,192 x 768 x 768 it beats the chapter GEMM,
+    whose 192 tiles fill one round of the chip), few rows on the few-row kernel."""
 
     @staticmethod
     def forward(ctx, x, w):

@@ -157,14 +157,18 @@ def test_linear_weight_grad_kernel(gpu_device, R, N, K, x_dtype, out_dtype):
     assert_parity(dw, ref, out_dtype, "dW")
 
 
-def test_linear_autograd_matches_reference(gpu_device):
-    """ops.linear (q_proj / o_proj) gradients against float64 autograd, bf16 operands."""
+@pytest.mark.parametrize("shape", [(3, 130, 256, 384), (3, 130, 256, 512), (8, 1024, 768, 768)])
+def test_linear_autograd_matches_reference(gpu_device, shape):
+    """ops.linear (q_proj / o_proj) gradients against float64 autograd, bf16 operands, with the
+    weight gradient on the split-row kernel (384 outputs) and on the LDS-DMA kernel
+    (256-multiples, over a row count that leaves a partial 64-row block, and at the c3 shape)."""
     from memory_amd import ops
     dev = gpu_device
+    B, Lq, K, N = shape
     g = gen(77)
-    x = torch.randn(3, 130, 256, generator=g).to(torch.bfloat16)
-    w = (torch.randn(384, 256, generator=g) / 16).to(torch.bfloat16)
-    dy = torch.randn(3, 130, 384, generator=g).to(torch.bfloat16)
+    x = torch.randn(B, Lq, K, generator=g).to(torch.bfloat16)
+    w = (torch.randn(N, K, generator=g) / 16).to(torch.bfloat16)
+    dy = torch.randn(B, Lq, N, generator=g).to(torch.bfloat16)
     xg = x.to(dev).requires_grad_(True)
     wg = w.to(dev).requires_grad_(True)
     y = ops.linear(xg, wg)
@@ -232,3 +236,19 @@ def test_zeros_beside(gpu_device, shape, dtype):
         torch.cuda.current_stream(gpu_device).wait_event(ev)
     assert t.shape == shape and t.dtype == dtype
     assert torch.count_nonzero(t).item() == 0
+
+
+@pytest.mark.parametrize("shape", [(390, 256, 512), (8192, 768, 768)])
+def test_rows_linear_matches_fp64(gpu_device, shape):
+    """moc_rows_linear (y = x W^T on the chapter GEMM over 64-row blocks) against a float64
+    product; rows past R are neither read nor written (the output buffer's tail stays NaN)."""
+    from memory_amd import _lib as L
+    R, K, N = shape
+    g = gen(91)
+    x = torch.randn(R, K, generator=g).to(torch.bfloat16)
+    w = (torch.randn(N, K, generator=g) / 16).to(torch.bfloat16)
+    xd, wd = x.to(gpu_device), w.to(gpu_device)
+    y = torch.full((R + 64, N), float("nan"), device=gpu_device, dtype=torch.bfloat16)
+    L.call("moc_rows_linear", L.ptr(xd), K, R, L.ptr(wd), N, K, L.ptr(y), N, L.stream_ptr(gpu_device))
+    assert_parity(y[:R], x.double() @ w.double().T, torch.bfloat16, "y")
+    assert torch.isnan(y[R:].float()).all()
