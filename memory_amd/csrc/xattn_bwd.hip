@@ -241,10 +241,17 @@ __global__ __launch_bounds__(kBThreads) void xattn_bwd_dq_kernel(
 // probability (c = omega * scale * log2 e, s = q_i . k_j, dP = dO_i . v_j):
 //   t    = scale (omega dP - delta_i)
 //   dk'_j = sum_i p t q_i      dv'_j = sum_i p dO_i     (A operands p t and p)
+// The per-wave constants are folded into the register-resident operands once per kernel:
+// k~ = c k and v~ = omega scale v, so the logit product Q k~^T started from the accumulator
+// -lse is the exp2 argument itself and dO v~^T started from -scale delta is t; each element
+// then costs one exp2, one multiply (p t) and half of two conversions (the bf16 operands
+// k~, v~ carry one rounding of the scaled values, as the reference's omega-weighted memory
+// does before its projection).
 // dk = omega dk' and dv = omega dv' (the keys enter the logits and the values the output
 // scaled by omega), applied once at the store; d omega = sum_ij (p t s + p dP) =
-// sum_j dk'_j . k_j + dv'_j . v_j, read off the accumulators, the two key halves summed in
-// a fixed order.  The same loop serves omega == 0 (all logits of the chapter 0, dk = dv = 0).
+// sum_j dk'_j . k_j + dv'_j . v_j with the unscaled k, v, read off the accumulators, the two
+// key halves summed in a fixed order.  The same loop serves omega == 0 (k~ = v~ = 0: every
+// logit of the chapter 0, t = -scale delta, dk = dv = 0).
 template <typename T> struct DkvCfg;
 template <> struct DkvCfg<bf16> { static constexpr int CPW = 2, QS = 64; };
 template <> struct DkvCfg<float> { static constexpr int CPW = 2, QS = 32; };
@@ -303,6 +310,16 @@ __global__ __launch_bounds__(64 * kDkvWavesPerChapter * DkvCfg<T>::CPW) void xat
   }
   const float w = active ? omega[e] : 0.f;
   const float c = w * scale_log2, dsc = w * scale;
+  // k~ = c k, v~ = omega scale v (see above)
+#pragma unroll
+  for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int x = 0; x < 8; ++x) {
+        kreg[kb][ks][x] = from_f<T>(c * to_f(kreg[kb][ks][x]));
+        vreg[kb][ks][x] = from_f<T>(dsc * to_f(vreg[kb][ks][x]));
+      }
 
   f32x4 dk[NKB][4], dv[NKB][4];
 #pragma unroll
@@ -353,9 +370,10 @@ __global__ __launch_bounds__(64 * kDkvWavesPerChapter * DkvCfg<T>::CPW) void xat
         st16(sStage[buf][1] + TileK::off(qq, cc), pre[CPT + j]);
       }
       if (tid < QS) {
-        // scaled here, not in fetch, so the loads stay in flight across a step's math
-        sL[buf][tid] = preL;
-        sDl[buf][tid] = preD * scale;
+        // the accumulator starts -lse and -scale delta; negated and scaled here, not in fetch,
+        // so the loads stay in flight across a step's math
+        sL[buf][tid] = -preL;
+        sDl[buf][tid] = -preD * scale;
       }
     };
     fetch(0);
@@ -372,12 +390,16 @@ __global__ __launch_bounds__(64 * kDkvWavesPerChapter * DkvCfg<T>::CPW) void xat
           const int qb0 = 32 * half;
           f32x4 sc[2][NKB], dp[2][NKB];
 #pragma unroll
-          for (int qb = 0; qb < 2; ++qb)
+          for (int qb = 0; qb < 2; ++qb) {
+            // -lse and -scale delta of the tile's queries (rows 4 g + x of the accumulator)
+            const f32x4 nl2 = *reinterpret_cast<const f32x4*>(&sL[buf][qb0 + 16 * qb + 4 * g]);
+            const f32x4 ndl = *reinterpret_cast<const f32x4*>(&sDl[buf][qb0 + 16 * qb + 4 * g]);
 #pragma unroll
             for (int kb = 0; kb < NKB; ++kb) {
-              sc[qb][kb] = f32x4{0.f, 0.f, 0.f, 0.f};
-              dp[qb][kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+              sc[qb][kb] = nl2;
+              dp[qb][kb] = ndl;
             }
+          }
 #pragma unroll
           for (int ks = 0; ks < 2; ++ks) {
             F8 qa[2], da[2];
@@ -396,22 +418,15 @@ __global__ __launch_bounds__(64 * kDkvWavesPerChapter * DkvCfg<T>::CPW) void xat
           }
           F8 pa[NKB], sa[NKB];
 #pragma unroll
-          for (int qb = 0; qb < 2; ++qb) {
-            // exp2(c s - l2) = p;  dl = scale * delta
-            const f32x4 l2 = *reinterpret_cast<const f32x4*>(&sL[buf][qb0 + 16 * qb + 4 * g]);
-            const f32x4 dl = *reinterpret_cast<const f32x4*>(&sDl[buf][qb0 + 16 * qb + 4 * g]);
+          for (int qb = 0; qb < 2; ++qb)
 #pragma unroll
             for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
               for (int x = 0; x < 4; ++x) {
-                const float sraw = sc[qb][kb][x];
-                const float dpu = dp[qb][kb][x];
-                const float pt = __builtin_amdgcn_exp2f(sraw * c - l2[x]);  // p
-                const float tq = dpu * dsc - dl[x];                           // scale (omega dP - delta)
+                const float pt = __builtin_amdgcn_exp2f(sc[qb][kb][x]);  // p = exp2(c s - lse)
                 pa[kb][4 * qb + x] = from_f<T>(pt);
-                sa[kb][4 * qb + x] = from_f<T>(pt * tq);
+                sa[kb][4 * qb + x] = from_f<T>(pt * dp[qb][kb][x]);    // p scale (omega dP - delta)
               }
-          }
 #pragma unroll
           for (int db = 0; db < 4; ++db) {
             // Q^T / dO^T fragments (dims 16 db + c16, queries in MFMA key order) read
