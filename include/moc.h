@@ -74,12 +74,34 @@ int moc_prepend_shared(const int32_t* idx, const float* w, int64_t R, int k, int
 int moc_prepend_shared_bwd(const float* w, const float* domega, int64_t R, int k, int S, float scale, float* dw,
                            hipStream_t stream);
 
+/* The sequence router's top-k followed by the shared-chapter prepend in one launch
+ * (router.py:114-149 then model.py:356-391): idx / w as moc_router_topk, idx_star / omega as
+ * moc_prepend_shared on them (bit-identical to the two separate calls).  S > 0. */
+int moc_router_topk_prepend(const float* logits, int64_t R, int64_t C, int S, int k, float scale, int32_t* idx,
+                            float* w, int32_t* idx_star, float* omega, hipStream_t stream);
+/* Backward of that chain from the attention's d omega partials to the logits, one launch:
+ * d omega[r, j] = sum_hk dom_part[(r (S+k) + j) HK + hk] (dom_part f32 [R (S+k), HK], as
+ * moc_xattn_bwd_dkv writes it), then moc_prepend_shared_bwd and moc_router_topk_bwd (w = the
+ * top-k's weights); dlogits f32 [R, C] also receives dz_in f32 [R, C] when non-NULL (a
+ * gradient arriving at the logits from the router losses).  S <= 1024, C <= 8192. */
+int moc_router_seq_bwd(const float* logits, const int32_t* idx, const float* w, const float* dom_part, int HK,
+                       int64_t R, int64_t C, int S, int k, float scale, const float* dz_in, float* dlogits,
+                       hipStream_t stream);
+
 /* Replaces the pooling of ChapterRouter.forward (router.py:96-107 mean; :158-195 rolling
  * mean given as per-position coefficients coef f32 [L], NULL = mean).
  * h [B, L, d] of dtype; pooled f32 [B, d]; workspace from moc_router_pool_workspace. */
 size_t moc_router_pool_workspace(int64_t B, int64_t L, int64_t d);
 int moc_router_pool(const void* h, int dtype, int64_t B, int64_t L, int64_t d, const float* coef, float* pooled,
                     void* workspace, size_t workspace_bytes, hipStream_t stream);
+/* The same pooling in one launch, without a workspace, for d % 8 == 0 and 16-byte aligned h. */
+int moc_router_pool1(const void* h, int dtype, int64_t B, int64_t L, int64_t d, const float* coef, float* pooled,
+                     hipStream_t stream);
+/* Backward of the pooling added into an existing gradient (autograd's accumulation of the two
+ * uses of hidden_states, router.py:96-107 and the q projection): x [B, L, d] of dtype +=
+ * v f32 [B, d] * (coef ? coef[l] : scale), in place.  d % 8 == 0, 16-byte aligned. */
+int moc_rows_add_bcast(void* x, int dtype, int64_t B, int64_t L, int64_t d, const float* v, const float* coef,
+                       float scale, hipStream_t stream);
 
 /* Replaces ChapterRouter.router (nn.Linear(d, C, bias=True), router.py:64) for few rows:
  * logits f32 [R, C] = x f32 [R, d] . W[C, d]^T + bias f32 [C] (bias may be NULL). */
@@ -214,6 +236,41 @@ int moc_chapter_wgrad(const void* dkv_edge, int64_t lda, const void* red, const 
  * memory_transformer/memory_attention.py:140-143). */
 int moc_weight_pack(const void* wk, int wk_dtype, const void* wv, int wv_dtype, int64_t kv, int64_t d, void* wkv,
                     void* wkv_t, hipStream_t stream);
+
+/* ------------------------------------------- the whole sequence-routed layer */
+
+/* One memory layer of MemoryTransformer.forward with sequence-level routing and its sublayer
+ * call (memory_transformer/model.py:609-692, memory_block.py:549-558 without the caller's norm
+ * and residual; router.py:96-149, model.py:356-391, memory_attention.py:241-243, :269-478) as
+ * one host call per direction: the library's router, chapter-plan, chapter-GEMM, attention and
+ * weight-gradient entry points ordered over the caller's stream `main` and the side streams
+ * `aux` (and `fill` in the backward), joined back into `main` by events before returning.
+ * Shapes: h [B, L, d] bf16, d = 64 H (head_dim 64), d and 2*HK*64 multiples of 256, T = 64,
+ * bank [N_m, d] bf16 (plain rows: no row norm), wr [C, d] f32 or bf16 (wr_dtype), br f32 [C] or
+ * NULL, wq / wo [d, d], wk / wv [HK*64, d] bf16, coef f32 [L] (rolling-mean pooling) or NULL
+ * (mean), 1 <= S <= 1024 shared chapters, 1 <= k <= min(1024, C - S), C <= 8192, B <= 64.
+ * forward outputs: out [B, L, d] bf16 (after o_proj), logits f32 [B, C], idx i32 [B, k] (routed
+ * global ids), idx_star i32 [B, S+k] and omega f32 [B, S+k] (after the prepend); `saved`
+ * (moc_seq_layer_saved_bytes) holds what the backward reads and must reach it unchanged.
+ * backward: dout [B, L, d] bf16, dlogits f32 [B, C] or NULL (a gradient at the logits from the
+ * router losses); outputs, each NULL when not wanted: dh [B, L, d] bf16, dbank [bank_rows, d]
+ * bf16 (dense: zeros except the selected chapters' rows), dwr f32 [C, d], dbr f32 [C], dwq and
+ * dwo [d, d] bf16, dwkv [2*HK*64, d] (= [dWk; dWv], dwkv_dtype f32 or bf16); `scratch`
+ * (moc_seq_layer_scratch_bytes) is working memory.  Both return 0 sizes for unsupported shapes.
+ * Calls on one device must be issued from one host thread at a time. */
+size_t moc_seq_layer_saved_bytes(int64_t B, int64_t L, int64_t d, int H, int HK, int64_t C, int S, int k);
+size_t moc_seq_layer_scratch_bytes(int64_t B, int64_t L, int64_t d, int H, int HK, int64_t C, int S, int k);
+int moc_seq_layer_fwd(const void* h, const void* bank, const void* wr, int wr_dtype, const float* br, const void* wq,
+                      const void* wk, const void* wv, const void* wo, const float* coef, int64_t B, int64_t L,
+                      int64_t d, int H, int HK, int64_t C, int S, int k, float routed_scale, void* out,
+                      float* logits, int32_t* idx, int32_t* idx_star, float* omega, void* saved, size_t saved_bytes,
+                      hipStream_t main, hipStream_t aux);
+int moc_seq_layer_bwd(const void* h, const void* bank, const void* wr, int wr_dtype, const float* coef, int64_t B,
+                      int64_t L, int64_t d, int H, int HK, int64_t C, int S, int k, float routed_scale,
+                      const float* logits, const int32_t* idx, const float* omega, const void* saved,
+                      size_t saved_bytes, const void* dout, const float* dlogits, void* dh, void* dbank,
+                      int64_t bank_rows, float* dwr, float* dbr, void* dwq, void* dwkv, int dwkv_dtype, void* dwo,
+                      void* scratch, size_t scratch_bytes, hipStream_t main, hipStream_t aux, hipStream_t fill);
 
 /* ------------------------------------------------- routed attention forward */
 

@@ -36,6 +36,16 @@ _SIGS = {
     "moc_router_topk_bwd": (_I, [_P, _P, _P, _I64, _I64, _I, _I, _P, _P]),
     "moc_prepend_shared": (_I, [_P, _P, _I64, _I, _I, _F, _P, _P, _P]),
     "moc_prepend_shared_bwd": (_I, [_P, _P, _I64, _I, _I, _F, _P, _P]),
+    "moc_router_topk_prepend": (_I, [_P, _I64, _I64, _I, _I, _F, _P, _P, _P, _P, _P]),
+    "moc_router_seq_bwd": (_I, [_P, _P, _P, _P, _I, _I64, _I64, _I, _I, _F, _P, _P, _P]),
+    "moc_router_pool1": (_I, [_P, _I, _I64, _I64, _I64, _P, _P, _P]),
+    "moc_seq_layer_saved_bytes": (_SZ, [_I64, _I64, _I64, _I, _I, _I64, _I, _I]),
+    "moc_seq_layer_scratch_bytes": (_SZ, [_I64, _I64, _I64, _I, _I, _I64, _I, _I]),
+    "moc_seq_layer_fwd": (_I, [_P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I, _I, _I64, _I, _I, _F,
+                               _P, _P, _P, _P, _P, _P, _SZ, _P, _P]),
+    "moc_seq_layer_bwd": (_I, [_P, _P, _P, _I, _P, _I64, _I64, _I64, _I, _I, _I64, _I, _I, _F, _P, _P, _P, _P, _SZ,
+                               _P, _P, _P, _P, _I64, _P, _P, _P, _P, _I, _P, _P, _SZ, _P, _P, _P]),
+    "moc_rows_add_bcast": (_I, [_P, _I, _I64, _I64, _I64, _P, _P, _F, _P]),
     "moc_router_pool_workspace": (_SZ, [_I64, _I64, _I64]),
     "moc_router_pool": (_I, [_P, _I, _I64, _I64, _I64, _P, _P, _P, _SZ, _P]),
     "moc_router_linear": (_I, [_P, _I64, _I64, _P, _I, _P, _I64, _P, _P]),

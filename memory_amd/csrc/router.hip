@@ -48,6 +48,7 @@ __device__ __forceinline__ float block_reduce_max(float v, float* red) {
 }
 
 constexpr int kMaxTopK = 1024;
+constexpr int kMaxSeqShared = 1024;  // shared chapters of the fused sequence-router backward
 constexpr int kMaxRouterC = 16384;  // the row lives in LDS (64 KB)
 
 // Workgroup size per row: rows are few for sequence-level routing (one per
@@ -91,17 +92,55 @@ __device__ RowStats row_stats(const float* zs, int64_t C, int S, float* red) {
   return RowStats{m, Z, ms};
 }
 
+// omega = [1..1 (S), scale * w] / clamp(sum); idx_star = [0..S-1, idx] for one row, by one
+// wave (lane = threadIdx.x % 64): the sum is formed lane-strided and wave-reduced, the order
+// prepend_kernel and prepend_row_bwd use.
+__device__ __forceinline__ void prepend_row(const int32_t* idx, const float* w, int k, int S, float scale,
+                                            int32_t* idx_star, float* omega, int lane) {
+  const int NS = S + k;
+  float s = 0.f;
+  for (int j = lane; j < NS; j += 64) s += (j < S) ? 1.f : scale * w[j - S];
+  s = fmaxf(wave_sum(s), 1e-12f);
+  for (int j = lane; j < NS; j += 64) {
+    const float a = (j < S) ? 1.f : scale * w[j - S];
+    omega[j] = a / s;
+    idx_star[j] = (j < S) ? j : idx[j - S];
+  }
+}
+
+// Gradient of prepend_row w.r.t. w for one row (one wave): dw[i] = scale (domega[S+i] / D - corr).
+__device__ __forceinline__ void prepend_row_bwd(const float* w, const float* domega, int k, int S, float scale,
+                                                float* dw, int lane) {
+  const int NS = S + k;
+  float s = 0.f, g = 0.f;
+  for (int j = lane; j < NS; j += 64) {
+    const float a = (j < S) ? 1.f : scale * w[j - S];
+    s += a;
+    g += domega[j] * a;
+  }
+  s = wave_sum(s);
+  g = wave_sum(g);
+  const float D = fmaxf(s, 1e-12f);
+  const float corr = (s >= 1e-12f) ? g / (D * D) : 0.f;
+  for (int j = S + lane; j < NS; j += 64) dw[j - S] = scale * (domega[j] / D - corr);
+}
+
 // One workgroup per row of logits; the row is read from HBM once into LDS.
+// With idx_star / omega (non-null, S > 0) the kernel also writes the shared-chapter prepend of
+// its row (prepend_kernel's values, summed in the same order), so the sequence router's chain
+// top-k -> prepend is one launch.
 template <int NT>
 __global__ __launch_bounds__(NT) void router_topk_kernel(
     const float* __restrict__ logits, int64_t C, int S, int k,
-    int32_t* __restrict__ idx_out, float* __restrict__ w_out, float* __restrict__ probs_out) {
+    int32_t* __restrict__ idx_out, float* __restrict__ w_out, float* __restrict__ probs_out,
+    float scale, int32_t* __restrict__ idx_star, float* __restrict__ omega) {
   extern __shared__ float zs[];  // the row, C floats
   __shared__ float red[NT / 64];
   __shared__ int hist[256];
   __shared__ uint32_t sel_key[kMaxTopK];
   __shared__ int32_t sel_idx[kMaxTopK];
-  __shared__ float sel_w[kMaxTopK];
+  __shared__ float sorted_w[kMaxTopK];
+  __shared__ int32_t sorted_i[kMaxTopK];
   __shared__ int s_state[5];  // chosen bin, remaining, n collected, running eq, ties at threshold
   __shared__ int wave_cnt[NT / 64];
 
@@ -196,16 +235,9 @@ __global__ __launch_bounds__(NT) void router_topk_kernel(
     }
   }
   __syncthreads();
-  // ---- probabilities of the selected chapters, sum, renormalise
-  float part = 0.f;
-  for (int i = tid; i < k; i += NT) {
-    float p = __expf(zs[sel_idx[i]] - st.mx) / st.Z;
-    if (S > 0) p = p / denom;
-    sel_w[i] = p;
-    part += p;
-  }
-  const float W = fmaxf(block_reduce_sum<NT>(part, red), 1e-12f);
-  // ---- rank sort: (key desc, index asc)
+  // ---- rank sort (key desc, index asc) of the selected chapters with their probabilities;
+  // the slots above were filled in atomic order, so everything after this works in rank order
+  // (the sum below is then formed the same way on every run)
   for (int i = tid; i < k; i += NT) {
     const uint32_t ki = sel_key[i];
     const int32_t ii = sel_idx[i];
@@ -214,27 +246,37 @@ __global__ __launch_bounds__(NT) void router_topk_kernel(
       const uint32_t kj = sel_key[j];
       rank += (kj > ki) || (kj == ki && sel_idx[j] < ii);
     }
-    idx_out[r * k + rank] = ii;
-    w_out[r * k + rank] = sel_w[i] / W;
+    float p = __expf(zs[ii] - st.mx) / st.Z;
+    if (S > 0) p = p / denom;
+    sorted_w[rank] = p;
+    sorted_i[rank] = ii;
   }
+  __syncthreads();
+  // ---- renormalise
+  float part = 0.f;
+  for (int i = tid; i < k; i += NT) part += sorted_w[i];
+  const float W = fmaxf(block_reduce_sum<NT>(part, red), 1e-12f);
+  for (int i = tid; i < k; i += NT) {
+    const float v = sorted_w[i] / W;
+    idx_out[r * k + i] = sorted_i[i];
+    w_out[r * k + i] = v;
+    sorted_w[i] = v;
+  }
+  if (!idx_star) return;
+  __syncthreads();
+  if (tid < 64) prepend_row(sorted_i, sorted_w, k, S, scale, idx_star + r * (S + k), omega + r * (S + k), tid);
 }
 
 // dlogits for the chain  p = softmax(z); q = p masked to c >= S; p' = q / clamp(sum q);
-// w = p'[idx]; w_hat = w / clamp(sum w).  dw_hat is the incoming gradient.  Mirrors
-// autograd of memory_transformer/router.py:114-149 including the clamp_min(1e-12) gates.
-// The row and the dense dp vector live in LDS.
+// w = p'[idx]; w_hat = w / clamp(sum w).  dw_hat is the incoming gradient (global or LDS).
+// Mirrors autograd of memory_transformer/router.py:114-149 including the clamp_min(1e-12)
+// gates.  The row (zs) and the dense dp vector (dps) live in LDS; dz_in (optional) is a
+// gradient arriving at the logits from elsewhere (the router losses), added at the end.
 template <int NT>
-__global__ __launch_bounds__(NT) void router_topk_bwd_kernel(
-    const float* __restrict__ logits, const int32_t* __restrict__ idx, const float* __restrict__ dw_hat,
-    int64_t C, int S, int k, float* __restrict__ dlogits) {
-  extern __shared__ float zs[];  // row [C] then dp [C]
-  float* dps = zs + C;
-  __shared__ float red[NT / 64];
-  __shared__ float s_dwraw[kMaxTopK];
-  const int64_t r = blockIdx.x;
-  float* dz = dlogits + r * C;
+__device__ void topk_bwd_row(const float* zs, float* dps, int64_t C, int S, int k, const int32_t* __restrict__ idx,
+                             const float* dw_hat, const float* __restrict__ dz_in, float* __restrict__ dz,
+                             float* red, float* s_dwraw) {
   const int tid = threadIdx.x;
-  load_row<NT>(logits + r * C, C, zs);
   const RowStats st = row_stats<NT>(zs, C, S, red);
   const float denom = fmaxf(st.msum, 1e-12f);
   const bool denom_live = st.msum >= 1e-12f;
@@ -242,10 +284,10 @@ __global__ __launch_bounds__(NT) void router_topk_bwd_kernel(
   // w_raw and its sum
   float part = 0.f, gw = 0.f;
   for (int i = tid; i < k; i += NT) {
-    float p = __expf(zs[idx[r * k + i]] - st.mx) / st.Z;
+    float p = __expf(zs[idx[i]] - st.mx) / st.Z;
     if (S > 0) p = p / denom;
     part += p;
-    gw += dw_hat[r * k + i] * p;
+    gw += dw_hat[i] * p;
   }
   const float Wsum = block_reduce_sum<NT>(part, red);
   const float GW = block_reduce_sum<NT>(gw, red);  // sum_j g_j w_raw_j
@@ -254,9 +296,9 @@ __global__ __launch_bounds__(NT) void router_topk_bwd_kernel(
   // dw_raw_i = g_i / W - [live] * GW / W^2 ; A = sum_i dw_raw_i * q_{idx_i}
   float a = 0.f;
   for (int i = tid; i < k; i += NT) {
-    const float dwr = dw_hat[r * k + i] / W - (W_live ? GW / (W * W) : 0.f);
+    const float dwr = dw_hat[i] / W - (W_live ? GW / (W * W) : 0.f);
     s_dwraw[i] = dwr;
-    const float p = __expf(zs[idx[r * k + i]] - st.mx) / st.Z;
+    const float p = __expf(zs[idx[i]] - st.mx) / st.Z;
     a += dwr * p;
   }
   const float A = block_reduce_sum<NT>(a, red);
@@ -264,52 +306,73 @@ __global__ __launch_bounds__(NT) void router_topk_bwd_kernel(
   const float base = (S > 0 && denom_live) ? -A / (denom * denom) : 0.f;
   for (int64_t c = tid; c < C; c += NT) dps[c] = (S > 0 && c >= S) ? base : 0.f;
   __syncthreads();
-  for (int i = tid; i < k; i += NT) dps[idx[r * k + i]] += (S > 0) ? s_dwraw[i] / denom : s_dwraw[i];
+  for (int i = tid; i < k; i += NT) dps[idx[i]] += (S > 0) ? s_dwraw[i] / denom : s_dwraw[i];
   __syncthreads();
   float dpp = 0.f;
   for (int64_t c = tid; c < C; c += NT) dpp += dps[c] * (__expf(zs[c] - st.mx) / st.Z);
   const float DPP = block_reduce_sum<NT>(dpp, red);
   for (int64_t c = tid; c < C; c += NT) {
     const float p = __expf(zs[c] - st.mx) / st.Z;
-    dz[c] = p * (dps[c] - DPP);
+    dz[c] = p * (dps[c] - DPP) + (dz_in ? dz_in[c] : 0.f);
   }
 }
 
-// omega = [1..1 (S), scale * w] / clamp(sum); idx_star = [0..S-1, idx].
+template <int NT>
+__global__ __launch_bounds__(NT) void router_topk_bwd_kernel(
+    const float* __restrict__ logits, const int32_t* __restrict__ idx, const float* __restrict__ dw_hat,
+    int64_t C, int S, int k, float* __restrict__ dlogits) {
+  extern __shared__ float zs[];  // row [C] then dp [C]
+  __shared__ float red[NT / 64];
+  __shared__ float s_dwraw[kMaxTopK];
+  const int64_t r = blockIdx.x;
+  load_row<NT>(logits + r * C, C, zs);
+  topk_bwd_row<NT>(zs, zs + C, C, S, k, idx + r * k, dw_hat + r * k, nullptr, dlogits + r * C, red, s_dwraw);
+}
+
+// The sequence router's backward from the attention's d omega to the logits, one workgroup
+// per row: d omega_j = sum over kv heads of dom_part[(r NS + j) HK + hk] (NS = S + k slots),
+// the prepend's backward (prepend_row_bwd) to dw, the top-k chain's backward (topk_bwd_row),
+// plus dz_in.  w is the top-k's output weights (the prepend's input).
+template <int NT>
+__global__ __launch_bounds__(NT) void router_seq_bwd_kernel(
+    const float* __restrict__ logits, const int32_t* __restrict__ idx, const float* __restrict__ w,
+    const float* __restrict__ dom_part, int HK, int64_t C, int S, int k, float scale,
+    const float* __restrict__ dz_in, float* __restrict__ dlogits) {
+  extern __shared__ float zs[];  // row [C] then dp [C]
+  __shared__ float red[NT / 64];
+  __shared__ float s_dwraw[kMaxTopK];
+  __shared__ float s_dom[kMaxTopK + kMaxSeqShared];
+  __shared__ float s_dw[kMaxTopK];
+  const int64_t r = blockIdx.x;
+  const int NS = S + k;
+  const int tid = threadIdx.x;
+  for (int j = tid; j < NS; j += NT) {
+    const float* p = dom_part + ((int64_t)r * NS + j) * HK;
+    float t = 0.f;
+    for (int h = 0; h < HK; ++h) t += p[h];
+    s_dom[j] = t;
+  }
+  load_row<NT>(logits + r * C, C, zs);  // (ends with a barrier)
+  if (tid < 64) prepend_row_bwd(w + r * k, s_dom, k, S, scale, s_dw, tid);
+  __syncthreads();
+  topk_bwd_row<NT>(zs, zs + C, C, S, k, idx + r * k, s_dw, dz_in ? dz_in + r * C : nullptr, dlogits + r * C, red,
+                   s_dwraw);
+}
+
+// omega = [1..1 (S), scale * w] / clamp(sum); idx_star = [0..S-1, idx]; one wave per row.
 __global__ void prepend_kernel(const int32_t* __restrict__ idx, const float* __restrict__ w, int64_t R,
                                int k, int S, float scale, int32_t* __restrict__ idx_star,
                                float* __restrict__ omega) {
   const int64_t r = (int64_t)blockIdx.x * blockDim.y + threadIdx.y;
   if (r >= R) return;
-  const int lane = threadIdx.x;  // 64 lanes per row
-  const int NS = S + k;
-  float s = 0.f;
-  for (int j = lane; j < NS; j += 64) s += (j < S) ? 1.f : scale * w[r * k + (j - S)];
-  s = fmaxf(wave_sum(s), 1e-12f);
-  for (int j = lane; j < NS; j += 64) {
-    float a = (j < S) ? 1.f : scale * w[r * k + (j - S)];
-    omega[r * NS + j] = a / s;
-    idx_star[r * NS + j] = (j < S) ? j : idx[r * k + (j - S)];
-  }
+  prepend_row(idx + r * k, w + r * k, k, S, scale, idx_star + r * (S + k), omega + r * (S + k), threadIdx.x);
 }
 
 __global__ void prepend_bwd_kernel(const float* __restrict__ w, const float* __restrict__ domega, int64_t R,
                                    int k, int S, float scale, float* __restrict__ dw) {
   const int64_t r = (int64_t)blockIdx.x * blockDim.y + threadIdx.y;
   if (r >= R) return;
-  const int lane = threadIdx.x;
-  const int NS = S + k;
-  float s = 0.f, g = 0.f;
-  for (int j = lane; j < NS; j += 64) {
-    float a = (j < S) ? 1.f : scale * w[r * k + (j - S)];
-    s += a;
-    g += domega[r * NS + j] * a;
-  }
-  s = wave_sum(s);
-  g = wave_sum(g);
-  const float D = fmaxf(s, 1e-12f);
-  const float corr = (s >= 1e-12f) ? g / (D * D) : 0.f;
-  for (int j = S + lane; j < NS; j += 64) dw[r * k + (j - S)] = scale * (domega[r * NS + j] / D - corr);
+  prepend_row_bwd(w + r * k, domega + r * (S + k), k, S, scale, dw + r * k, threadIdx.x);
 }
 
 // pooled[b, :] = sum_l coef[l] * h[b, l, :]   (coef == nullptr: mean over L).
@@ -376,6 +439,87 @@ __global__ __launch_bounds__(kPoolThreads) void pool_partial_cols_kernel(const T
     }
     for (; l < l1; ++l) acc += (coef ? coef[l] : 1.f) * to_f(hb[l * d]);
     part[((int64_t)split * gridDim.x + b) * d + c] = acc;
+  }
+}
+
+// One-launch pooling for 16-byte rows: pooled[b, c] = scale * sum_l coef[l] h[b, l, c]
+// (coef == nullptr: scale = 1 / L).  Workgroup (b, 64-column block): thread t sums 8 columns
+// (chunk t % 8) over the rows l = t / 8 (mod 32) with four 16-byte loads in flight; the 32 row
+// groups are added in a fixed order through LDS.  d % 8 == 0, rows 16-byte aligned.
+constexpr int kPool1Groups = 32;
+template <typename T>
+__global__ __launch_bounds__(256) void pool_single_kernel(const T* __restrict__ h, int64_t L, int64_t d,
+                                                          const float* __restrict__ coef, float scale,
+                                                          float* __restrict__ pooled) {
+  __shared__ float part[kPool1Groups][65];
+  const int64_t b = blockIdx.y;
+  const int chunk = threadIdx.x & 7, grp = threadIdx.x >> 3;
+  const int64_t c8 = (int64_t)blockIdx.x * 64 + 8 * chunk;
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  if (c8 < d) {
+    const T* hb = h + b * L * d + c8;
+    int64_t l = grp;
+    for (; l + 3 * kPool1Groups < L; l += 4 * kPool1Groups) {
+      float v[4][8];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) ChunkLoadF<T>::run(hb + (l + u * kPool1Groups) * d, v[u]);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const float cw = coef ? coef[l + u * kPool1Groups] : 1.f;
+#pragma unroll
+        for (int x = 0; x < 8; ++x) acc[x] += cw * v[u][x];
+      }
+    }
+    for (; l < L; l += kPool1Groups) {
+      float v[8];
+      ChunkLoadF<T>::run(hb + l * d, v);
+      const float cw = coef ? coef[l] : 1.f;
+#pragma unroll
+      for (int x = 0; x < 8; ++x) acc[x] += cw * v[x];
+    }
+  }
+#pragma unroll
+  for (int x = 0; x < 8; ++x) part[grp][8 * chunk + x] = acc[x];
+  __syncthreads();
+  if (threadIdx.x < 64) {
+    const int64_t c = (int64_t)blockIdx.x * 64 + threadIdx.x;
+    float t = 0.f;
+#pragma unroll 8
+    for (int g = 0; g < kPool1Groups; ++g) t += part[g][threadIdx.x];
+    if (c < d) pooled[b * d + c] = t * scale;
+  }
+}
+
+// x[b, l, :] += v[b, :] * (coef ? coef[l] : scale), in place (the pooling's backward added into
+// a gradient that already holds another contribution).  One thread per 8 columns of a row.
+template <typename T>
+__global__ __launch_bounds__(256) void rows_add_bcast_kernel(T* __restrict__ x, int64_t B, int64_t L, int64_t d,
+                                                             const float* __restrict__ v,
+                                                             const float* __restrict__ coef, float scale) {
+  const int64_t n8 = d / 8;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= B * L * n8) return;
+  const int64_t row = i / n8, c8 = (i - row * n8) * 8;
+  const int64_t b = row / L, l = row - b * L;
+  const float cw = coef ? coef[l] : scale;
+  T* p = x + row * d + c8;
+  float a[8];
+  ChunkLoadF<T>::run(p, a);
+  const f32x4 v0 = *reinterpret_cast<const f32x4*>(v + b * d + c8);
+  const f32x4 v1 = *reinterpret_cast<const f32x4*>(v + b * d + c8 + 4);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    a[e] += cw * v0[e];
+    a[4 + e] += cw * v1[e];
+  }
+  if constexpr (sizeof(T) == 2) {
+    bf16x8 o;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = (bf16)a[e];
+    *reinterpret_cast<bf16x8*>(p) = o;
+  } else {
+    *reinterpret_cast<f32x4*>(p) = f32x4{a[0], a[1], a[2], a[3]};
+    *reinterpret_cast<f32x4*>(p + 4) = f32x4{a[4], a[5], a[6], a[7]};
   }
 }
 
@@ -862,11 +1006,33 @@ int moc_router_topk(const float* logits, int64_t R, int64_t C, int S, int k, int
   const size_t lds = (size_t)C * sizeof(float);
   if (router_threads(R) == 1024)
     hipLaunchKernelGGL(router_topk_kernel<1024>, dim3((unsigned)R), dim3(1024), lds, stream, logits, C, S, k, idx, w,
-                       probs);
+                       probs, 0.f, nullptr, nullptr);
   else
     hipLaunchKernelGGL(router_topk_kernel<256>, dim3((unsigned)R), dim3(256), lds, stream, logits, C, S, k, idx, w,
-                       probs);
+                       probs, 0.f, nullptr, nullptr);
   return check_launch("router_topk_kernel");
+}
+
+int moc_router_topk_prepend(const float* logits, int64_t R, int64_t C, int S, int k, float scale, int32_t* idx,
+                            float* w, int32_t* idx_star, float* omega, hipStream_t stream) {
+  MOC_REQUIRE(logits && idx && w && idx_star && omega, MOC_ERR_ARG, "moc_router_topk_prepend: null pointer");
+  MOC_REQUIRE(R >= 0 && C > 0, MOC_ERR_ARG, "moc_router_topk_prepend: bad shape R=%lld C=%lld", (long long)R,
+              (long long)C);
+  MOC_REQUIRE(S > 0 && S <= C, MOC_ERR_ARG, "moc_router_topk_prepend: needs 0 < S <= C, got S=%d", S);
+  MOC_REQUIRE(k > 0 && k <= C - S, MOC_ERR_ARG, "moc_router_topk_prepend: k=%d must be in [1, C-S=%lld]", k,
+              (long long)(C - S));
+  MOC_REQUIRE(k <= kMaxTopK, MOC_ERR_UNSUPPORTED, "moc_router_topk_prepend: k=%d exceeds %d", k, kMaxTopK);
+  MOC_REQUIRE(C <= kMaxRouterC, MOC_ERR_UNSUPPORTED, "moc_router_topk_prepend: C=%lld exceeds %d", (long long)C,
+              kMaxRouterC);
+  if (R == 0) return MOC_OK;
+  const size_t lds = (size_t)C * sizeof(float);
+  if (router_threads(R) == 1024)
+    hipLaunchKernelGGL(router_topk_kernel<1024>, dim3((unsigned)R), dim3(1024), lds, stream, logits, C, S, k, idx, w,
+                       nullptr, scale, idx_star, omega);
+  else
+    hipLaunchKernelGGL(router_topk_kernel<256>, dim3((unsigned)R), dim3(256), lds, stream, logits, C, S, k, idx, w,
+                       nullptr, scale, idx_star, omega);
+  return check_launch("router_topk_kernel(prepend)");
 }
 
 int moc_router_topk_bwd(const float* logits, const int32_t* idx, const float* dw, int64_t R, int64_t C, int S, int k,
@@ -885,6 +1051,26 @@ int moc_router_topk_bwd(const float* logits, const int32_t* idx, const float* dw
     hipLaunchKernelGGL(router_topk_bwd_kernel<256>, dim3((unsigned)R), dim3(256), lds, stream, logits, idx, dw, C, S, k,
                        dlogits);
   return check_launch("router_topk_bwd_kernel");
+}
+
+int moc_router_seq_bwd(const float* logits, const int32_t* idx, const float* w, const float* dom_part, int HK,
+                       int64_t R, int64_t C, int S, int k, float scale, const float* dz_in, float* dlogits,
+                       hipStream_t stream) {
+  MOC_REQUIRE(logits && idx && w && dom_part && dlogits, MOC_ERR_ARG, "moc_router_seq_bwd: null pointer");
+  MOC_REQUIRE(HK > 0 && S > 0 && S <= C && k > 0 && k <= C - S, MOC_ERR_ARG,
+              "moc_router_seq_bwd: bad HK=%d S=%d k=%d C=%lld", HK, S, k, (long long)C);
+  MOC_REQUIRE(k <= kMaxTopK && S <= kMaxSeqShared && C <= kMaxRouterC / 2, MOC_ERR_UNSUPPORTED,
+              "moc_router_seq_bwd: k=%d, S=%d or C=%lld beyond %d / %d / %d", k, S, (long long)C, kMaxTopK,
+              kMaxSeqShared, kMaxRouterC / 2);
+  if (R == 0) return MOC_OK;
+  const size_t lds = 2 * (size_t)C * sizeof(float);
+  if (router_threads(R) == 1024)
+    hipLaunchKernelGGL(router_seq_bwd_kernel<1024>, dim3((unsigned)R), dim3(1024), lds, stream, logits, idx, w,
+                       dom_part, HK, C, S, k, scale, dz_in, dlogits);
+  else
+    hipLaunchKernelGGL(router_seq_bwd_kernel<256>, dim3((unsigned)R), dim3(256), lds, stream, logits, idx, w, dom_part,
+                       HK, C, S, k, scale, dz_in, dlogits);
+  return check_launch("router_seq_bwd_kernel");
 }
 
 int moc_prepend_shared(const int32_t* idx, const float* w, int64_t R, int k, int S, float scale, int32_t* idx_star,
@@ -955,6 +1141,44 @@ int moc_router_pool(const void* h, int dtype, int64_t B, int64_t L, int64_t d, c
   hipLaunchKernelGGL(pool_reduce_kernel, dim3((unsigned)((B * d + 63) / 64)), dim3(256), 0, stream, part, nsplit, B, d,
                      inv, pooled);
   return check_launch("pool_reduce_kernel");
+}
+
+int moc_router_pool1(const void* h, int dtype, int64_t B, int64_t L, int64_t d, const float* coef, float* pooled,
+                     hipStream_t stream) {
+  MOC_REQUIRE(h && pooled, MOC_ERR_ARG, "moc_router_pool1: null pointer");
+  MOC_REQUIRE(B >= 0 && L > 0 && d > 0 && B < 65536, MOC_ERR_ARG, "moc_router_pool1: bad shape");
+  MOC_REQUIRE(d % 8 == 0 && ((uintptr_t)h & 15) == 0, MOC_ERR_UNSUPPORTED,
+              "moc_router_pool1: d=%lld must be a multiple of 8 with 16-byte aligned rows", (long long)d);
+  if (B == 0) return MOC_OK;
+  const dim3 grid((unsigned)((d + 63) / 64), (unsigned)B);
+  const float scale = coef ? 1.f : 1.f / (float)L;
+  if (dtype == MOC_BF16)
+    hipLaunchKernelGGL(pool_single_kernel<bf16>, grid, dim3(256), 0, stream, (const bf16*)h, L, d, coef, scale, pooled);
+  else if (dtype == MOC_F32)
+    hipLaunchKernelGGL(pool_single_kernel<float>, grid, dim3(256), 0, stream, (const float*)h, L, d, coef, scale,
+                       pooled);
+  else
+    return set_error(MOC_ERR_UNSUPPORTED, "moc_router_pool1: dtype %d", dtype);
+  return check_launch("pool_single_kernel");
+}
+
+int moc_rows_add_bcast(void* x, int dtype, int64_t B, int64_t L, int64_t d, const float* v, const float* coef,
+                       float scale, hipStream_t stream) {
+  MOC_REQUIRE(x && v, MOC_ERR_ARG, "moc_rows_add_bcast: null pointer");
+  MOC_REQUIRE(B >= 0 && L >= 0 && d > 0 && d % 8 == 0 && ((uintptr_t)x & 15) == 0 && ((uintptr_t)v & 15) == 0,
+              MOC_ERR_UNSUPPORTED, "moc_rows_add_bcast: d=%lld must be a multiple of 8, pointers 16-byte aligned",
+              (long long)d);
+  const int64_t n = B * L * (d / 8);
+  if (n == 0) return MOC_OK;
+  MOC_REQUIRE(n < ((int64_t)1 << 39), MOC_ERR_UNSUPPORTED, "moc_rows_add_bcast: too large");
+  const dim3 grid((unsigned)((n + 255) / 256));
+  if (dtype == MOC_BF16)
+    hipLaunchKernelGGL(rows_add_bcast_kernel<bf16>, grid, dim3(256), 0, stream, (bf16*)x, B, L, d, v, coef, scale);
+  else if (dtype == MOC_F32)
+    hipLaunchKernelGGL(rows_add_bcast_kernel<float>, grid, dim3(256), 0, stream, (float*)x, B, L, d, v, coef, scale);
+  else
+    return set_error(MOC_ERR_UNSUPPORTED, "moc_rows_add_bcast: dtype %d", dtype);
+  return check_launch("rows_add_bcast_kernel");
 }
 
 int moc_router_linear(const float* x, int64_t R, int64_t d, const void* W, int w_dtype, const float* bias, int64_t C,

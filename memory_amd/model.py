@@ -22,9 +22,9 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from . import ops
+from . import ops, seq_layer
 from .memory_attention import MemoryCrossAttention
-from .router import ChapterRouter
+from .router import ChapterRouter, compute_router_losses, rolling_coefficients
 
 
 def select_routed_chapters_from_probs(probs: torch.Tensor, top_k: int, num_shared_chapters: int):
@@ -159,6 +159,9 @@ class RoutedMemoryLayer(nn.Module):
         self.router = ChapterRouter(hidden_dim, num_chapters, top_k, routing_strategy)
         self.memory_attn = MemoryCrossAttention(hidden_dim, num_heads, num_kv_heads, wo_init_zero=wo_init_zero,
                                                 gradient_checkpointing=gradient_checkpointing)
+        # run the whole layer as one autograd function (memory_amd.seq_layer) where it applies;
+        # False keeps the per-op autograd functions (router, q_proj, attention, o_proj)
+        self.fused = True
 
     def route(self, hidden_states: torch.Tensor, return_losses: bool = True):
         idx_star, omega, losses = self._route32(hidden_states, return_losses)
@@ -173,8 +176,40 @@ class RoutedMemoryLayer(nn.Module):
                                                     routed_scaling_factor=self.routed_scaling_factor)
         return idx_star, omega, losses
 
+    def _fused(self, hidden_states: torch.Tensor, bank: torch.Tensor):
+        """The whole layer as one autograd function (memory_amd.seq_layer) when it applies."""
+        if not self.fused:
+            return None
+        attn = self.memory_attn
+        strategy = self.router.routing_strategy
+        S = self.num_shared_chapters
+        C = self.num_chapters
+        if strategy not in ("sequence", "token", "sequence-rolling", "sequence_rolling"):
+            return None
+        if attn.gradient_checkpointing and self.training:
+            return None
+        k = min(int(self.router.top_k), C - S)
+        if not seq_layer.supported(hidden_states, bank, attn.q_proj.weight, attn.o_proj.weight,
+                                   self.router.router.weight, S, k, C, self.tokens_per_chapter):
+            return None
+        coef = None
+        if strategy in ("sequence-rolling", "sequence_rolling"):
+            coef = rolling_coefficients(hidden_states.shape[1], self.routing_window_size, hidden_states.device)
+        normalize = self.normalize and 0 < S < S + k
+        return seq_layer.seq_routed_layer(
+            hidden_states, bank, self.router.router.weight, self.router.router.bias, attn.q_proj.weight,
+            attn.k_proj.weight, attn.v_proj.weight, attn.o_proj.weight, num_chapters=C,
+            tokens_per_chapter=self.tokens_per_chapter, num_shared=S, top_k=k,
+            routed_scale=self.routed_scaling_factor, num_heads=attn.num_heads, num_kv_heads=attn.num_kv_heads,
+            norm_type=self.norm_type if normalize else None, eps=self.norm_eps, coef=coef)
+
     def forward(self, hidden_states: torch.Tensor, bank: torch.Tensor,
                 return_losses: bool = True) -> Tuple[torch.Tensor, Dict[str, torch.Tensor]]:
+        fused = self._fused(hidden_states, bank)
+        if fused is not None:
+            out, logits, idx, _, _ = fused
+            losses = compute_router_losses(logits, None, idx, self.num_chapters) if return_losses else {}
+            return out, losses
         idx_star, omega, losses = self._route32(hidden_states, return_losses)
         NS = idx_star.shape[1]
         # model.py:402-405: normalisation only mixes when both the shared and routed slices are non-empty

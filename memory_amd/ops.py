@@ -471,22 +471,231 @@ def row_norm(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor]
     return _RowNorm.apply(x, weight, bias, code, float(eps), od)
 
 
-def linear_wgrad(dy: torch.Tensor, x: torch.Tensor, out_dtype: torch.dtype) -> torch.Tensor:
+def linear_wgrad(dy: torch.Tensor, x: torch.Tensor, out_dtype: torch.dtype,
+                 out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """dW = dy^T x for dy [R][N], x [R][K] (row-major, contiguous): the split-row MFMA
-    kernel for bf16 dy (N, K multiples of 8), a plain GEMM otherwise."""
+    kernel for bf16 dy (N, K multiples of 8), a plain GEMM otherwise.  ``out``: a [N][K]
+    tensor of out_dtype to write (allocated here when None)."""
     R, N = dy.shape
     K = x.shape[1]
+    dw = torch.empty(N, K, device=dy.device, dtype=out_dtype) if out is None else out
     if (dy.dtype == torch.bfloat16 and x.dtype in (torch.bfloat16, torch.float32) and dy.is_cuda and N % 8 == 0
             and K % 8 == 0 and out_dtype in (torch.float32, torch.bfloat16)):
         ws = torch.empty(L.query("moc_linear_wgrad_workspace", R, N, K) // 4, device=dy.device, dtype=torch.float32)
-        dw = torch.empty(N, K, device=dy.device, dtype=out_dtype)
         call("moc_linear_wgrad", ptr(dy), ptr(x), L.dtype_code(x.dtype), R, N, K, ptr(ws), ws.numel() * 4,
              L.dtype_code(out_dtype), ptr(dw), stream_ptr(dy.device))
         return dw
-    return torch.matmul(dy.t().to(x.dtype), x).to(out_dtype)
+    dw.copy_(torch.matmul(dy.t().to(x.dtype), x))
+    return dw
 
 
 # ------------------------------------------------------------- routed attention (A)
+
+_ATTN_SAVED = ("q", "bank", "wkv", "om", "out", "lse", "kv", "mean", "rstd", "uniq", "n_uniq", "edge_u", "csr_off",
+               "csr_edge")
+
+
+def routed_attn_forward(q, bank, wk, wv, omega, idx_star, num_chapters, T, norm, eps, HK, wkv=None):
+    """Forward body of the sequence-routed attention (plan, gather + K/V projection, joint
+    attention): returns (out, saved tensors in _ATTN_SAVED order, cfg).  ``wkv``: the packed
+    bf16 [Wk; Wv] when the caller already has it (its pack then stays off this stream)."""
+    L.require_gpu(q, bank, wk, wv, omega, idx_star)
+    dtype = q.dtype
+    bank_dtype = bank.dtype
+    B, Lq, H, Dh = q.shape
+    NS = idx_star.shape[1]
+    q = q.contiguous()
+    # a bank stepped by BankAdamW: its plan's chapters are brought to the last step before
+    # they are read, and the forward kernels read its mirror when it keeps one
+    opt = getattr(bank, "_moc_bank_opt", None)
+    plan = chapter_plan(idx_star, num_chapters)
+    if opt is not None:
+        opt.catch_up(plan.uniq, plan.n_uniq, plan.max_u)
+        bank = opt.read_view(dtype)
+    bank = bank.contiguous()
+    mean = rstd = None
+    if norm != L.MOC_NORM_NONE:
+        mean, rstd = row_stats(bank, plan, T, norm, eps)
+    # K / V of the plan's chapters as projection rows [max_u * T][K | V]; the attention
+    # kernels read (chapter, kv head) blocks of it through strides
+    KV = HK * Dh
+    d = bank.shape[1]
+    if dtype == torch.bfloat16 and T == 64 and (2 * KV) % 256 == 0 and d % 64 == 0:
+        # bf16: the chapter GEMM, gathering bank rows straight into its operand tiles (a
+        # normalised or f32 bank is gathered into bf16 rows first)
+        if wkv is None:
+            wkv, _ = weight_pack(wk, wv)
+        if norm == L.MOC_NORM_NONE and bank.dtype == torch.bfloat16:
+            kv = chapter_project(bank, plan, wkv, gather=True)
+        else:
+            X = torch.empty(plan.max_u * T, d, device=q.device, dtype=dtype)
+            call("moc_gather_rows", L.dtype_code(dtype), ptr(bank), L.dtype_code(bank.dtype), d, T,
+                 ptr(plan.uniq), ptr(plan.n_uniq), plan.max_u, ptr(mean), ptr(rstd), ptr(X), stream_ptr(q.device))
+            kv = chapter_project(X, plan, wkv, gather=False)
+            del X
+    else:
+        wkv = torch.cat([wk, wv], 0).to(dtype).contiguous()
+        X = torch.empty(plan.max_u * T, d, device=q.device, dtype=dtype)
+        call("moc_gather_rows", L.dtype_code(dtype), ptr(bank), L.dtype_code(bank.dtype), d, T,
+             ptr(plan.uniq), ptr(plan.n_uniq), plan.max_u, ptr(mean), ptr(rstd), ptr(X), stream_ptr(q.device))
+        with L.region("lib_kv_project_gemm"):
+            kv = F.linear(X, wkv)
+        del X
+    kvl = kv_rows_layout(kv, T, HK, Dh)
+    om = omega.float().contiguous()
+    out = torch.empty(B, Lq, H, Dh, device=q.device, dtype=dtype)
+    Lp = (Lq + 127) // 128 * 128
+    lse = torch.empty(B, H, Lp, device=q.device, dtype=torch.float32)
+    call("moc_xattn_fwd", L.dtype_code(dtype), ptr(q), ptr(kv), ptr(kv) + KV * kv.element_size(), *kvl,
+         ptr(plan.edge_u), ptr(om), B, Lq, H, HK, Dh, T, NS, float(Dh) ** -0.5, ptr(out), ptr(lse),
+         stream_ptr(q.device))
+    saved = (q, bank, wkv, om, out, lse, kv, mean, rstd, plan.uniq, plan.n_uniq, plan.edge_u, plan.csr_off,
+             plan.csr_edge)
+    cfg = (num_chapters, T, norm, eps, HK, plan.max_u, wk.dtype, wv.dtype, bank_dtype)
+    return out, saved, cfg
+
+
+def routed_attn_backward(saved, cfg, dout, needs, row_grad=None, after_dq=None, after_dkv=None):
+    """Backward body of the sequence-routed attention.  ``needs`` = (q, bank, wk, wv, omega)
+    input-gradient flags.  Returns (dq, dbank, dwk, dwv, dom_part) with dom_part f32
+    [B * NS, HK] (d omega per (edge, kv head); d omega = its sum over kv heads).  The hooks run
+    on the host right after the dQ launch (``after_dq(dq)``) and after the dK/dV launch
+    (``after_dkv(dom_part)``): callers fork work that needs only those onto other streams."""
+    (q, bank, wkv, om, out, lse, kv, mean, rstd, uniq, n_uniq, edge_u, csr_off, csr_edge) = saved
+    C, T, norm, eps, HK, max_u, wk_dtype, wv_dtype, bank_dtype = cfg
+    dtype = q.dtype
+    dt = L.dtype_code(dtype)
+    B, Lq, H, Dh = q.shape
+    NS = om.shape[1]
+    KV = HK * Dh
+    d = bank.shape[1]
+    dev = q.device
+    st = stream_ptr(dev)
+    scale = float(Dh) ** -0.5
+    _need_q, need_bank, need_wk, need_wv, _need_om = needs
+    dout = dout.to(dtype).contiguous()
+    Lp = lse.shape[2]
+    delta = torch.empty(B, H, Lp, device=dev, dtype=torch.float32)
+    call("moc_xattn_bwd_prep", dt, ptr(q), ptr(out), ptr(dout), B, Lq, H, Dh, ptr(delta), None, None, st)
+    # the dense bank gradient's zeros are written beside the dQ and dK/dV kernels
+    dbank_zero = None
+    if dtype == torch.bfloat16 and need_bank and row_grad is None:
+        dbank_zero = zeros_beside(bank.shape, bank.dtype, dev)
+    dq = torch.empty_like(q)
+    kvl = kv_rows_layout(kv, T, HK, Dh)
+    vptr = ptr(kv) + KV * kv.element_size()
+    call("moc_xattn_bwd_dq", dt, ptr(q), ptr(kv), vptr, *kvl, ptr(edge_u), ptr(om),
+         ptr(dout), ptr(lse), ptr(delta), B, Lq, H, HK, Dh, T, NS, scale, ptr(dq), st)
+    if after_dq is not None:
+        after_dq(dq)
+    dkv_edge = torch.empty(B * NS * T, 2 * KV, device=dev, dtype=dtype)
+    dom_part = torch.empty(B * NS, HK, device=dev, dtype=torch.float32)   # every entry written
+    call("moc_xattn_bwd_dkv", dt, ptr(q), ptr(dout), ptr(kv), vptr, *kvl, ptr(edge_u), ptr(om),
+         ptr(lse), ptr(delta), B, Lq, H, HK, Dh, T, NS, scale, ptr(dkv_edge), ptr(dom_part), st)
+    if after_dkv is not None:
+        after_dkv(dom_part)
+    dbank = dwk = dwv = None
+    E = B * NS
+    if dtype == torch.bfloat16:
+        # the chapter GEMMs read a chapter's dK|dV rows in place when one edge selected it and
+        # from `red` (the edges' sum, written once here) when several did
+        tiled = T == 64 and d % 256 == 0 and (2 * KV) % 256 == 0
+        red = None
+        if tiled and (need_bank or need_wk or need_wv):
+            red = torch.empty(max_u * T, 2 * KV, device=dev, dtype=torch.bfloat16)
+            call("moc_dkv_multi_reduce", ptr(dkv_edge), 2 * KV, ptr(n_uniq), max_u, ptr(csr_off), ptr(csr_edge),
+                 ptr(red), st)
+        dwkv = None
+        if need_wk or need_wv:
+            out_dt = torch.float32 if torch.float32 in (wk_dtype, wv_dtype) else dtype
+            dwkv = torch.empty(2 * KV, d, device=dev, dtype=out_dt)
+            if tiled:
+                # dW = sum over distinct chapters of dK|dV_c^T X_c (bank rows gathered by
+                # the kernel; a normalised or f32 bank is gathered into bf16 rows first)
+                ws_bytes = L.query("moc_chapter_wgrad_workspace", 2 * KV, d, max_u)
+                ws = torch.empty(ws_bytes // 4, device=dev, dtype=torch.float32)
+                if norm == L.MOC_NORM_NONE and bank.dtype == torch.bfloat16:
+                    xs, gather = bank, 1
+                else:
+                    xs = torch.empty(max_u * T, d, device=dev, dtype=torch.bfloat16)
+                    call("moc_gather_rows", L.MOC_BF16, ptr(bank), L.dtype_code(bank.dtype), d, T,
+                         ptr(uniq), ptr(n_uniq), max_u, ptr(mean), ptr(rstd), ptr(xs), st)
+                    gather = 0
+                call("moc_chapter_wgrad", ptr(dkv_edge), 2 * KV, ptr(red), ptr(xs), xs.stride(0), gather,
+                     ptr(uniq), ptr(n_uniq), max_u, ptr(csr_off), ptr(csr_edge), 2 * KV, d, ptr(ws),
+                     ws_bytes, L.dtype_code(out_dt), ptr(dwkv), st)
+            else:
+                # per-edge rows paired with their chapter's bank rows (no per-chapter sums)
+                ws = torch.empty(L.query("moc_kv_wgrad_workspace", 2 * KV, d, E) // 4, device=dev,
+                                 dtype=torch.float32)
+                call("moc_kv_wgrad", ptr(dkv_edge), ptr(bank), L.dtype_code(bank.dtype), d, T,
+                     ptr(uniq), ptr(n_uniq), ptr(edge_u), E, ptr(mean), ptr(rstd), 2 * KV, ptr(ws),
+                     ws.numel() * 4, L.dtype_code(out_dt), ptr(dwkv), st)
+        if need_bank and not tiled:
+            # shapes outside the chapter GEMM's tiling: per-edge dX on the library GEMM,
+            # summed per chapter by the scatter
+            dX = torch.matmul(dkv_edge, wkv)  # rows of skipped edges are never read
+            if row_grad is not None:
+                row_grad.accumulate(dX, bank, uniq, n_uniq, max_u, csr_off, csr_edge, mean, rstd, norm)
+            else:
+                dbank, filled = dbank_zero
+                if filled is not None:
+                    torch.cuda.current_stream(dev).wait_event(filled)
+                call("moc_bank_scatter", L.dtype_code(dX.dtype), ptr(dX), ptr(bank), L.dtype_code(bank.dtype),
+                     d, T, ptr(uniq), ptr(n_uniq), max_u, ptr(csr_off), ptr(csr_edge), ptr(mean), ptr(rstd),
+                     norm, ptr(dbank), st)
+                dbank = dbank.to(bank_dtype)
+        elif need_bank:
+            # dX per distinct chapter (edges summed) on the chapter GEMM; with a plain bank it
+            # is stored straight into the chapter's rows of the dense gradient
+            _, wkv_t = weight_pack(wkv[:KV], wkv[KV:], rows=False, transposed=True)
+            if row_grad is None and norm == L.MOC_NORM_NONE:
+                dbank, filled = dbank_zero
+                if filled is not None:
+                    torch.cuda.current_stream(dev).wait_event(filled)
+                chapter_dx(dkv_edge, red, uniq, n_uniq, max_u, csr_off, csr_edge, wkv_t, dbank, bank_rows=True)
+                dbank = dbank.to(bank_dtype)   # the bank read may be a mirror of another dtype
+            else:
+                dXc = torch.empty(max_u * T, d, device=dev, dtype=torch.float32)
+                chapter_dx(dkv_edge, red, uniq, n_uniq, max_u, csr_off, csr_edge, wkv_t, dXc, bank_rows=False)
+                if row_grad is not None:
+                    row_grad.accumulate(dXc, bank, uniq, n_uniq, max_u, None, None, mean, rstd, norm)
+                else:
+                    dbank, filled = dbank_zero
+                    if filled is not None:
+                        torch.cuda.current_stream(dev).wait_event(filled)
+                    call("moc_bank_scatter", L.dtype_code(dXc.dtype), ptr(dXc), ptr(bank),
+                         L.dtype_code(bank.dtype), d, T, ptr(uniq), ptr(n_uniq), max_u, None, None, ptr(mean),
+                         ptr(rstd), norm, ptr(dbank), st)
+                    dbank = dbank.to(bank_dtype)
+        if dwkv is not None:
+            dwk = dwkv[:KV].to(wk_dtype) if need_wk else None
+            dwv = dwkv[KV:].to(wv_dtype) if need_wv else None
+        return dq, dbank, dwk, dwv, dom_part
+    # fp32: sum per distinct chapter first, then library GEMMs
+    dkv = torch.empty(max_u * T, 2 * KV, device=dev, dtype=dtype)
+    call("moc_dkv_reduce", dt, ptr(dkv_edge), ptr(n_uniq), ptr(csr_off), ptr(csr_edge), max_u, 2 * KV, ptr(dkv),
+         st)
+    if need_wk or need_wv:
+        X = torch.empty(max_u * T, d, device=dev, dtype=dtype)
+        call("moc_gather_rows", dt, ptr(bank), L.dtype_code(bank.dtype), d, T, ptr(uniq), ptr(n_uniq),
+             max_u, ptr(mean), ptr(rstd), ptr(X), st)
+        dwkv = torch.matmul(dkv.t(), X)
+        dwk = dwkv[:KV].to(wk_dtype) if need_wk else None
+        dwv = dwkv[KV:].to(wv_dtype) if need_wv else None
+    if need_bank:
+        dX = torch.matmul(dkv, wkv)
+        if row_grad is not None:
+            row_grad.accumulate(dX, bank, uniq, n_uniq, max_u, None, None, mean, rstd, norm)
+        else:
+            dbank = torch.zeros(bank.shape, device=dev, dtype=bank.dtype)
+            call("moc_bank_scatter", L.dtype_code(dX.dtype), ptr(dX), ptr(bank), L.dtype_code(bank.dtype), d,
+                 T, ptr(uniq), ptr(n_uniq), max_u, None, None, ptr(mean), ptr(rstd), norm, ptr(dbank), st)
+            dbank = dbank.to(bank_dtype)
+    return dq, dbank, dwk, dwv, dom_part
+
+
+
 
 class _RoutedAttention(torch.autograd.Function):
     """Gather + K/V projection + joint routed attention (sequence level).
@@ -497,193 +706,20 @@ class _RoutedAttention(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, q, bank, wk, wv, omega, idx_star, num_chapters, T, norm, eps, HK):
-        L.require_gpu(q, bank, wk, wv, omega, idx_star)
-        dtype = q.dtype
-        bank_dtype = bank.dtype
-        B, Lq, H, Dh = q.shape
-        NS = idx_star.shape[1]
-        q = q.contiguous()
-        # a bank stepped by BankAdamW: its plan's chapters are brought to the last step before
-        # they are read, and the forward kernels read its mirror when it keeps one; a bank with
-        # a RowSparseBankGrad receives its gradient rows there instead of a dense gradient
-        opt = getattr(bank, "_moc_bank_opt", None)
+        # a bank with a RowSparseBankGrad receives its gradient rows there instead of a dense gradient
         ctx.row_grad = getattr(bank, "_moc_row_grad", None)
-        plan = chapter_plan(idx_star, num_chapters)
-        if opt is not None:
-            opt.catch_up(plan.uniq, plan.n_uniq, plan.max_u)
-            bank = opt.read_view(dtype)
-        bank = bank.contiguous()
-        mean = rstd = None
-        if norm != L.MOC_NORM_NONE:
-            mean, rstd = row_stats(bank, plan, T, norm, eps)
-        # K / V of the plan's chapters as projection rows [max_u * T][K | V]; the attention
-        # kernels read (chapter, kv head) blocks of it through strides
-        KV = HK * Dh
-        d = bank.shape[1]
-        if dtype == torch.bfloat16 and T == 64 and (2 * KV) % 256 == 0 and d % 64 == 0:
-            # bf16: the chapter GEMM, gathering bank rows straight into its operand tiles (a
-            # normalised or f32 bank is gathered into bf16 rows first)
-            wkv, _ = weight_pack(wk, wv)
-            if norm == L.MOC_NORM_NONE and bank.dtype == torch.bfloat16:
-                kv = chapter_project(bank, plan, wkv, gather=True)
-            else:
-                X = torch.empty(plan.max_u * T, d, device=q.device, dtype=dtype)
-                call("moc_gather_rows", L.dtype_code(dtype), ptr(bank), L.dtype_code(bank.dtype), d, T,
-                     ptr(plan.uniq), ptr(plan.n_uniq), plan.max_u, ptr(mean), ptr(rstd), ptr(X), stream_ptr(q.device))
-                kv = chapter_project(X, plan, wkv, gather=False)
-                del X
-        else:
-            wkv = torch.cat([wk, wv], 0).to(dtype).contiguous()
-            X = torch.empty(plan.max_u * T, d, device=q.device, dtype=dtype)
-            call("moc_gather_rows", L.dtype_code(dtype), ptr(bank), L.dtype_code(bank.dtype), d, T,
-                 ptr(plan.uniq), ptr(plan.n_uniq), plan.max_u, ptr(mean), ptr(rstd), ptr(X), stream_ptr(q.device))
-            with L.region("lib_kv_project_gemm"):
-                kv = F.linear(X, wkv)
-            del X
-        kvl = kv_rows_layout(kv, T, HK, Dh)
-        om = omega.float().contiguous()
-        out = torch.empty(B, Lq, H, Dh, device=q.device, dtype=dtype)
-        Lp = (Lq + 127) // 128 * 128
-        lse = torch.empty(B, H, Lp, device=q.device, dtype=torch.float32)
-        call("moc_xattn_fwd", L.dtype_code(dtype), ptr(q), ptr(kv), ptr(kv) + KV * kv.element_size(), *kvl,
-             ptr(plan.edge_u), ptr(om), B, Lq, H, HK, Dh, T, NS, float(Dh) ** -0.5, ptr(out), ptr(lse),
-             stream_ptr(q.device))
-        ctx.save_for_backward(q, bank, wkv, om, out, lse, kv, mean, rstd, plan.uniq, plan.n_uniq,
-                              plan.edge_u, plan.csr_off, plan.csr_edge)
-        ctx.cfg = (num_chapters, T, norm, eps, HK, plan.max_u, wk.dtype, wv.dtype, bank_dtype)
+        out, saved, cfg = routed_attn_forward(q, bank, wk, wv, omega, idx_star, num_chapters, T, norm, eps, HK)
+        ctx.save_for_backward(*saved)
+        ctx.cfg = cfg
         return out
 
     @staticmethod
     def backward(ctx, dout):
-        (q, bank, wkv, om, out, lse, kv, mean, rstd, uniq, n_uniq, edge_u, csr_off,
-         csr_edge) = ctx.saved_tensors
-        C, T, norm, eps, HK, max_u, wk_dtype, wv_dtype, bank_dtype = ctx.cfg
-        dtype = q.dtype
-        dt = L.dtype_code(dtype)
-        B, Lq, H, Dh = q.shape
-        NS = om.shape[1]
-        KV = HK * Dh
-        d = bank.shape[1]
-        dev = q.device
-        st = stream_ptr(dev)
-        scale = float(Dh) ** -0.5
-        dout = dout.to(dtype).contiguous()
-        Lp = lse.shape[2]
-        delta = torch.empty(B, H, Lp, device=dev, dtype=torch.float32)
-        call("moc_xattn_bwd_prep", dt, ptr(q), ptr(out), ptr(dout), B, Lq, H, Dh, ptr(delta), None, None, st)
-        # the dense bank gradient's zeros are written beside the dQ and dK/dV kernels
-        dbank_zero = None
-        if dtype == torch.bfloat16 and ctx.needs_input_grad[1] and ctx.row_grad is None:
-            dbank_zero = zeros_beside(bank.shape, bank.dtype, dev)
-        dq = torch.empty_like(q)
-        kvl = kv_rows_layout(kv, T, HK, Dh)
-        vptr = ptr(kv) + KV * kv.element_size()
-        call("moc_xattn_bwd_dq", dt, ptr(q), ptr(kv), vptr, *kvl, ptr(edge_u), ptr(om),
-             ptr(dout), ptr(lse), ptr(delta), B, Lq, H, HK, Dh, T, NS, scale, ptr(dq), st)
-        dkv_edge = torch.empty(B * NS * T, 2 * KV, device=dev, dtype=dtype)
-        dom_part = torch.empty(B * NS, HK, device=dev, dtype=torch.float32)   # every entry written
-        call("moc_xattn_bwd_dkv", dt, ptr(q), ptr(dout), ptr(kv), vptr, *kvl, ptr(edge_u), ptr(om),
-             ptr(lse), ptr(delta), B, Lq, H, HK, Dh, T, NS, scale, ptr(dkv_edge), ptr(dom_part), st)
+        needs = tuple(ctx.needs_input_grad[:5])
+        dq, dbank, dwk, dwv, dom_part = routed_attn_backward(ctx.saved_tensors, ctx.cfg, dout, needs,
+                                                              row_grad=ctx.row_grad)
+        B, NS = ctx.saved_tensors[3].shape
         domega = dom_part.sum(-1).view(B, NS)
-        need_bank, need_wk, need_wv = ctx.needs_input_grad[1:4]
-        dbank = dwk = dwv = None
-        E = B * NS
-        if dtype == torch.bfloat16:
-            # the chapter GEMMs read a chapter's dK|dV rows in place when one edge selected it and
-            # from `red` (the edges' sum, written once here) when several did
-            tiled = T == 64 and d % 256 == 0 and (2 * KV) % 256 == 0
-            red = None
-            if tiled and (need_bank or need_wk or need_wv):
-                red = torch.empty(max_u * T, 2 * KV, device=dev, dtype=torch.bfloat16)
-                call("moc_dkv_multi_reduce", ptr(dkv_edge), 2 * KV, ptr(n_uniq), max_u, ptr(csr_off), ptr(csr_edge),
-                     ptr(red), st)
-            dwkv = None
-            if need_wk or need_wv:
-                out_dt = torch.float32 if torch.float32 in (wk_dtype, wv_dtype) else dtype
-                dwkv = torch.empty(2 * KV, d, device=dev, dtype=out_dt)
-                if tiled:
-                    # dW = sum over distinct chapters of dK|dV_c^T X_c (bank rows gathered by
-                    # the kernel; a normalised or f32 bank is gathered into bf16 rows first)
-                    ws_bytes = L.query("moc_chapter_wgrad_workspace", 2 * KV, d, max_u)
-                    ws = torch.empty(ws_bytes // 4, device=dev, dtype=torch.float32)
-                    if norm == L.MOC_NORM_NONE and bank.dtype == torch.bfloat16:
-                        xs, gather = bank, 1
-                    else:
-                        xs = torch.empty(max_u * T, d, device=dev, dtype=torch.bfloat16)
-                        call("moc_gather_rows", L.MOC_BF16, ptr(bank), L.dtype_code(bank.dtype), d, T,
-                             ptr(uniq), ptr(n_uniq), max_u, ptr(mean), ptr(rstd), ptr(xs), st)
-                        gather = 0
-                    call("moc_chapter_wgrad", ptr(dkv_edge), 2 * KV, ptr(red), ptr(xs), xs.stride(0), gather,
-                         ptr(uniq), ptr(n_uniq), max_u, ptr(csr_off), ptr(csr_edge), 2 * KV, d, ptr(ws),
-                         ws_bytes, L.dtype_code(out_dt), ptr(dwkv), st)
-                else:
-                    # per-edge rows paired with their chapter's bank rows (no per-chapter sums)
-                    ws = torch.empty(L.query("moc_kv_wgrad_workspace", 2 * KV, d, E) // 4, device=dev,
-                                     dtype=torch.float32)
-                    call("moc_kv_wgrad", ptr(dkv_edge), ptr(bank), L.dtype_code(bank.dtype), d, T,
-                         ptr(uniq), ptr(n_uniq), ptr(edge_u), E, ptr(mean), ptr(rstd), 2 * KV, ptr(ws),
-                         ws.numel() * 4, L.dtype_code(out_dt), ptr(dwkv), st)
-            if need_bank and not tiled:
-                # shapes outside the chapter GEMM's tiling: per-edge dX on the library GEMM,
-                # summed per chapter by the scatter
-                dX = torch.matmul(dkv_edge, wkv)  # rows of skipped edges are never read
-                if ctx.row_grad is not None:
-                    ctx.row_grad.accumulate(dX, bank, uniq, n_uniq, max_u, csr_off, csr_edge, mean, rstd, norm)
-                else:
-                    dbank, filled = dbank_zero
-                    if filled is not None:
-                        torch.cuda.current_stream(dev).wait_event(filled)
-                    call("moc_bank_scatter", L.dtype_code(dX.dtype), ptr(dX), ptr(bank), L.dtype_code(bank.dtype),
-                         d, T, ptr(uniq), ptr(n_uniq), max_u, ptr(csr_off), ptr(csr_edge), ptr(mean), ptr(rstd),
-                         norm, ptr(dbank), st)
-                    dbank = dbank.to(bank_dtype)
-            elif need_bank:
-                # dX per distinct chapter (edges summed) on the chapter GEMM; with a plain bank it
-                # is stored straight into the chapter's rows of the dense gradient
-                _, wkv_t = weight_pack(wkv[:KV], wkv[KV:], rows=False, transposed=True)
-                if ctx.row_grad is None and norm == L.MOC_NORM_NONE:
-                    dbank, filled = dbank_zero
-                    if filled is not None:
-                        torch.cuda.current_stream(dev).wait_event(filled)
-                    chapter_dx(dkv_edge, red, uniq, n_uniq, max_u, csr_off, csr_edge, wkv_t, dbank, bank_rows=True)
-                    dbank = dbank.to(bank_dtype)   # the bank read may be a mirror of another dtype
-                else:
-                    dXc = torch.empty(max_u * T, d, device=dev, dtype=torch.float32)
-                    chapter_dx(dkv_edge, red, uniq, n_uniq, max_u, csr_off, csr_edge, wkv_t, dXc, bank_rows=False)
-                    if ctx.row_grad is not None:
-                        ctx.row_grad.accumulate(dXc, bank, uniq, n_uniq, max_u, None, None, mean, rstd, norm)
-                    else:
-                        dbank, filled = dbank_zero
-                        if filled is not None:
-                            torch.cuda.current_stream(dev).wait_event(filled)
-                        call("moc_bank_scatter", L.dtype_code(dXc.dtype), ptr(dXc), ptr(bank),
-                             L.dtype_code(bank.dtype), d, T, ptr(uniq), ptr(n_uniq), max_u, None, None, ptr(mean),
-                             ptr(rstd), norm, ptr(dbank), st)
-                        dbank = dbank.to(bank_dtype)
-            if dwkv is not None:
-                dwk = dwkv[:KV].to(wk_dtype) if need_wk else None
-                dwv = dwkv[KV:].to(wv_dtype) if need_wv else None
-            return dq, dbank, dwk, dwv, domega, None, None, None, None, None, None
-        # fp32: sum per distinct chapter first, then library GEMMs
-        dkv = torch.empty(max_u * T, 2 * KV, device=dev, dtype=dtype)
-        call("moc_dkv_reduce", dt, ptr(dkv_edge), ptr(n_uniq), ptr(csr_off), ptr(csr_edge), max_u, 2 * KV, ptr(dkv),
-             st)
-        if need_wk or need_wv:
-            X = torch.empty(max_u * T, d, device=dev, dtype=dtype)
-            call("moc_gather_rows", dt, ptr(bank), L.dtype_code(bank.dtype), d, T, ptr(uniq), ptr(n_uniq),
-                 max_u, ptr(mean), ptr(rstd), ptr(X), st)
-            dwkv = torch.matmul(dkv.t(), X)
-            dwk = dwkv[:KV].to(wk_dtype) if need_wk else None
-            dwv = dwkv[KV:].to(wv_dtype) if need_wv else None
-        if need_bank:
-            dX = torch.matmul(dkv, wkv)
-            if ctx.row_grad is not None:
-                ctx.row_grad.accumulate(dX, bank, uniq, n_uniq, max_u, None, None, mean, rstd, norm)
-            else:
-                dbank = torch.zeros(bank.shape, device=dev, dtype=bank.dtype)
-                call("moc_bank_scatter", L.dtype_code(dX.dtype), ptr(dX), ptr(bank), L.dtype_code(bank.dtype), d,
-                     T, ptr(uniq), ptr(n_uniq), max_u, None, None, ptr(mean), ptr(rstd), norm, ptr(dbank), st)
-                dbank = dbank.to(bank_dtype)
         return dq, dbank, dwk, dwv, domega, None, None, None, None, None, None
 
 

@@ -50,11 +50,17 @@ def _layer(dev, dtype, Wr, br, Wq, Wk, Wv, Wo, normalize, strategy="sequence", w
     return layer
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dtype,fused", [(torch.float32, "per-op"), (torch.bfloat16, "native"),
+                                         (torch.bfloat16, "python"), (torch.bfloat16, "per-op")])
 @pytest.mark.parametrize("normalize,strategy,window", [(False, "sequence", None), (True, "sequence", None),
                                                        (False, "sequence-rolling", 16)])
-def test_config1_layer_forward_backward(gpu_device, dtype, normalize, strategy, window):
-    print(f"config1 layer dtype={dtype} normalize={normalize} strategy={strategy}", flush=True)
+def test_config1_layer_forward_backward(gpu_device, monkeypatch, dtype, fused, normalize, strategy, window):
+    """bf16 runs the whole-layer autograd function (memory_amd.seq_layer) with its native
+    schedule (moc_seq_layer_fwd / _bwd; a normalised bank takes the Python-scheduled one) and
+    with the Python-scheduled one, and the per-op functions; fp32 always takes the per-op path."""
+    from memory_amd import seq_layer
+    print(f"config1 layer dtype={dtype} fused={fused} normalize={normalize} strategy={strategy}", flush=True)
+    monkeypatch.setattr(seq_layer, "NATIVE", fused == "native")
     dev = gpu_device
     c = C1
     # larger router / projection weights than the 0.02 recipe so that every gradient is well
@@ -62,6 +68,7 @@ def test_config1_layer_forward_backward(gpu_device, dtype, normalize, strategy, 
     h, bank, Wr, br, Wq, Wk, Wv, Wo = _config1_inputs(scale_w=0.08)
     bank = bank * 25.0
     layer = _layer(dev, dtype, Wr, br, Wq, Wk, Wv, Wo, normalize, strategy, window)
+    layer.fused = fused != "per-op"
     hg = h.to(dev, dtype).requires_grad_(True)
     bg = bank.to(dev, dtype).requires_grad_(True)
     out, _ = layer(hg, bg, return_losses=False)
