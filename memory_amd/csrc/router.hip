@@ -443,15 +443,17 @@ __global__ __launch_bounds__(kPoolThreads) void pool_partial_cols_kernel(const T
 }
 
 // One-launch pooling for 16-byte rows: pooled[b, c] = scale * sum_l coef[l] h[b, l, c]
-// (coef == nullptr: scale = 1 / L).  Workgroup (b, 64-column block): thread t sums 8 columns
-// (chunk t % 8) over the rows l = t / 8 (mod 32) with four 16-byte loads in flight; the 32 row
-// groups are added in a fixed order through LDS.  d % 8 == 0, rows 16-byte aligned.
-constexpr int kPool1Groups = 32;
+// (coef == nullptr: scale = 1 / L).  Workgroup (b, 64-column block), 1,024 threads: thread t sums
+// 8 columns (chunk t % 8) over the rows l = t / 8 (mod 128) with up to eight 16-byte loads in
+// flight, so L <= 1,024 rows are read in one round; the 128 row groups are added in a fixed
+// order through LDS (16 groups per thread, then 8 sums).  d % 8 == 0, rows 16-byte aligned.
+constexpr int kPool1Groups = 128;
 template <typename T>
-__global__ __launch_bounds__(256) void pool_single_kernel(const T* __restrict__ h, int64_t L, int64_t d,
-                                                          const float* __restrict__ coef, float scale,
-                                                          float* __restrict__ pooled) {
+__global__ __launch_bounds__(1024) void pool_single_kernel(const T* __restrict__ h, int64_t L, int64_t d,
+                                                           const float* __restrict__ coef, float scale,
+                                                           float* __restrict__ pooled) {
   __shared__ float part[kPool1Groups][65];
+  __shared__ float part2[8][65];
   const int64_t b = blockIdx.y;
   const int chunk = threadIdx.x & 7, grp = threadIdx.x >> 3;
   const int64_t c8 = (int64_t)blockIdx.x * 64 + 8 * chunk;
@@ -459,12 +461,12 @@ __global__ __launch_bounds__(256) void pool_single_kernel(const T* __restrict__ 
   if (c8 < d) {
     const T* hb = h + b * L * d + c8;
     int64_t l = grp;
-    for (; l + 3 * kPool1Groups < L; l += 4 * kPool1Groups) {
-      float v[4][8];
+    for (; l + 7 * kPool1Groups < L; l += 8 * kPool1Groups) {
+      float v[8][8];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) ChunkLoadF<T>::run(hb + (l + u * kPool1Groups) * d, v[u]);
+      for (int u = 0; u < 8; ++u) ChunkLoadF<T>::run(hb + (l + u * kPool1Groups) * d, v[u]);
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
+      for (int u = 0; u < 8; ++u) {
         const float cw = coef ? coef[l + u * kPool1Groups] : 1.f;
 #pragma unroll
         for (int x = 0; x < 8; ++x) acc[x] += cw * v[u][x];
@@ -481,11 +483,19 @@ __global__ __launch_bounds__(256) void pool_single_kernel(const T* __restrict__ 
 #pragma unroll
   for (int x = 0; x < 8; ++x) part[grp][8 * chunk + x] = acc[x];
   __syncthreads();
+  if (threadIdx.x < 512) {
+    const int col = threadIdx.x & 63, q = threadIdx.x >> 6;
+    float t = 0.f;
+#pragma unroll
+    for (int g = 0; g < 16; ++g) t += part[16 * q + g][col];
+    part2[q][col] = t;
+  }
+  __syncthreads();
   if (threadIdx.x < 64) {
     const int64_t c = (int64_t)blockIdx.x * 64 + threadIdx.x;
     float t = 0.f;
-#pragma unroll 8
-    for (int g = 0; g < kPool1Groups; ++g) t += part[g][threadIdx.x];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) t += part2[q][threadIdx.x];
     if (c < d) pooled[b * d + c] = t * scale;
   }
 }
@@ -651,6 +661,64 @@ __global__ __launch_bounds__(256) void router_linear_kernel(const float* __restr
         }
       }
     }
+  }
+}
+
+// Router linear for few rows on the fp32 matrix cores (v_mfma_f32_16x16x4_f32): a workgroup owns
+// 16 chapters; its 4 waves split d into quarters (d % 64 == 0) and hold every W and x chunk of
+// their quarter in registers before the first product (one round of loads); the 4 partial
+// 16 x 16 tiles (chapters x rows) are added in wave order through LDS.  Lane (m, g) of an MFMA
+// k-block of 16 columns supplies W[c0 + m][kb + 4g + j] and x[r0 + m][kb + 4g + j] for step j,
+// so both operands are 16-byte loads.  Rows are taken 16 at a time.
+template <typename TW, int KB>
+__global__ __launch_bounds__(256) void router_linear_mfma_kernel(const float* __restrict__ x, int64_t R, int64_t d,
+                                                                 const TW* __restrict__ W,
+                                                                 const float* __restrict__ bias, int64_t C,
+                                                                 float* __restrict__ logits) {
+  __shared__ f32x4 red[4][64];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int m = lane & 15, g = lane >> 4;
+  const int64_t c0 = (int64_t)blockIdx.x * 16;
+  const int64_t kq = d / 4, k0 = wave * kq;  // this wave's quarter of d
+  const int nkb = (int)(kq / 16);
+  // W chunks of this wave's quarter (KB blocks kept in registers; wider rows stream the rest)
+  f32x4 wreg[KB];
+  const bool crow = c0 + m < C;
+#pragma unroll
+  for (int i = 0; i < KB; ++i)
+    wreg[i] = (crow && i < nkb) ? load4f(W + (c0 + m) * d + k0 + 16 * i + 4 * g) : f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int64_t r0 = 0; r0 < R; r0 += 16) {
+    const bool rrow = r0 + m < R;
+    f32x4 xreg[KB];
+#pragma unroll
+    for (int i = 0; i < KB; ++i)
+      xreg[i] = (rrow && i < nkb) ? load4f(x + (r0 + m) * d + k0 + 16 * i + 4 * g) : f32x4{0.f, 0.f, 0.f, 0.f};
+    f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < KB; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(wreg[i][j], xreg[i][j], acc, 0, 0, 0);
+    for (int i = KB; i < nkb; ++i) {
+      const f32x4 wv = crow ? load4f(W + (c0 + m) * d + k0 + 16 * i + 4 * g) : f32x4{0.f, 0.f, 0.f, 0.f};
+      const f32x4 xv = rrow ? load4f(x + (r0 + m) * d + k0 + 16 * i + 4 * g) : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(wv[j], xv[j], acc, 0, 0, 0);
+    }
+    red[wave][lane] = acc;
+    __syncthreads();
+    if (wave == 0) {
+      // lane (n = row, g) holds chapters 4g + e of row n
+      const f32x4 t = ((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane];
+      const int64_t r = r0 + m;
+      if (r < R) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int64_t c = c0 + 4 * g + e;
+          if (c < C) logits[r * C + c] = t[e] + (bias ? bias[c] : 0.f);
+        }
+      }
+    }
+    __syncthreads();
   }
 }
 
@@ -1153,9 +1221,10 @@ int moc_router_pool1(const void* h, int dtype, int64_t B, int64_t L, int64_t d, 
   const dim3 grid((unsigned)((d + 63) / 64), (unsigned)B);
   const float scale = coef ? 1.f : 1.f / (float)L;
   if (dtype == MOC_BF16)
-    hipLaunchKernelGGL(pool_single_kernel<bf16>, grid, dim3(256), 0, stream, (const bf16*)h, L, d, coef, scale, pooled);
+    hipLaunchKernelGGL(pool_single_kernel<bf16>, grid, dim3(1024), 0, stream, (const bf16*)h, L, d, coef, scale,
+                       pooled);
   else if (dtype == MOC_F32)
-    hipLaunchKernelGGL(pool_single_kernel<float>, grid, dim3(256), 0, stream, (const float*)h, L, d, coef, scale,
+    hipLaunchKernelGGL(pool_single_kernel<float>, grid, dim3(1024), 0, stream, (const float*)h, L, d, coef, scale,
                        pooled);
   else
     return set_error(MOC_ERR_UNSUPPORTED, "moc_router_pool1: dtype %d", dtype);
@@ -1188,6 +1257,19 @@ int moc_router_linear(const float* x, int64_t R, int64_t d, const void* W, int w
   MOC_REQUIRE(d <= 4096 && d % 4 == 0, MOC_ERR_UNSUPPORTED, "moc_router_linear: d=%lld must be a multiple of 4, <= 4096",
               (long long)d);
   if (R == 0) return MOC_OK;
+  if (d % 64 == 0 && d <= 64 * 16 * 4) {
+    // matrix-core version: W chunks for d <= 1,024 fully in registers (12 blocks at d = 768)
+    const dim3 g16((unsigned)((C + 15) / 16));
+    if (w_dtype == MOC_F32)
+      hipLaunchKernelGGL((router_linear_mfma_kernel<float, 16>), g16, dim3(256), 0, stream, x, R, d, (const float*)W,
+                         bias, C, logits);
+    else if (w_dtype == MOC_BF16)
+      hipLaunchKernelGGL((router_linear_mfma_kernel<bf16, 16>), g16, dim3(256), 0, stream, x, R, d, (const bf16*)W,
+                         bias, C, logits);
+    else
+      return set_error(MOC_ERR_UNSUPPORTED, "moc_router_linear: dtype %d", w_dtype);
+    return check_launch("router_linear_mfma_kernel");
+  }
   dim3 grid((unsigned)((C + kLinChapFwd - 1) / kLinChapFwd));
   // only the rows of one chunk: small batches leave room for more resident workgroups
   const size_t lds = (size_t)std::min<int64_t>(R, kLinRows) * d * sizeof(float);

@@ -185,14 +185,17 @@ int moc_seq_layer_fwd(const void* h, const void* bank, const void* wr, int wr_dt
   const int64_t tok = B * L;
   const int KV2 = 2 * y.KV;
 
-  // aux: q projection and the weight packs, beside the router
+  // aux: the [Wk; Wv] pack and the q projection beside the router (the projection's wait is on
+  // them), then the transposed weights the backward reads, beside the projection and attention
   MOC_HIP(hipEventRecord(ev[0], main));
   MOC_HIP(hipStreamWaitEvent(aux, ev[0], 0));
+  SEQ_TRY(moc_weight_pack(wk, MOC_BF16, wv, MOC_BF16, y.KV, d, wkv, nullptr, aux));
   SEQ_TRY(moc_rows_linear(h, d, tok, wq, (int)d, (int)d, q, d, aux));
-  SEQ_TRY(moc_weight_pack(wk, MOC_BF16, wv, MOC_BF16, y.KV, d, wkv, sv + y.wkv_t, aux));
+  MOC_HIP(hipEventRecord(ev[1], aux));
+  SEQ_TRY(moc_weight_pack(wk, MOC_BF16, wv, MOC_BF16, y.KV, d, nullptr, sv + y.wkv_t, aux));
   SEQ_TRY(moc_weight_pack(wq, MOC_BF16, (const bf16*)wq + (d / 2) * d, MOC_BF16, d / 2, d, nullptr, sv + y.wq_t, aux));
   SEQ_TRY(moc_weight_pack(wo, MOC_BF16, (const bf16*)wo + (d / 2) * d, MOC_BF16, d / 2, d, nullptr, sv + y.wo_t, aux));
-  MOC_HIP(hipEventRecord(ev[1], aux));
+  MOC_HIP(hipEventRecord(ev[2], aux));
 
   // main: router, plan
   SEQ_TRY(moc_router_pool1(h, MOC_BF16, B, L, d, coef, pooled, main));
@@ -207,6 +210,7 @@ int moc_seq_layer_fwd(const void* h, const void* bank, const void* wr, int wr_dt
   SEQ_TRY(moc_xattn_fwd(MOC_BF16, q, kv, kv + y.KV, span, (int64_t)64 * KV2, 64, KV2, edge_u, omega, B, L, H, HK, 64,
                         64, y.NS, 0.125f, attn, lse, main));
   SEQ_TRY(moc_rows_linear(attn, d, tok, wo, (int)d, (int)d, out, d, main));
+  MOC_HIP(hipStreamWaitEvent(main, ev[2], 0));
   return MOC_OK;
 }
 
