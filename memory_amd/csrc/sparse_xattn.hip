@@ -770,30 +770,30 @@ __global__ __launch_bounds__(64 * kUnitWaves) void sparse_fwd_unit_kernel(
   const int lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
   char* sV = sVall[threadIdx.x >> 6];
   const int64_t kv0 = (int64_t)ur.gid * cs + (int64_t)ur.hk * hs;
-  // K as the A operand of S^T = K Q^T (lane = key), V staged row-major for V^T reads
-  bf16x8 kf[4][2];
-#pragma unroll
-  for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) kf[kb][ks] = Load8<bf16, bf16>::run(k + kv0 + (16 * kb + c16) * rs + 32 * ks + 8 * g);
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int row = 8 * i + (lane >> 3), c0 = 8 * (lane & 7);
-    st16(sV + Tile::off(row, c0), ld16(v + kv0 + row * rs + c0));
-  }
-  wave_lds_sync();
-  for (int r0 = 0; r0 < ur.nrows; r0 += 32) {
-    const bool two = r0 + 16 < ur.nrows;
-    bf16x8 qf[2][2];
-    int erow[2];
-    float wrow[2] = {1.f, 1.f};
+  // Row operands of a 32-row block: the edge of each row (csr order), its omega and its q
+  // fragments.  The first block's edge ids are requested before the K / V tiles, so their
+  // q loads go out while the tiles are still in flight (one memory round trip, not two,
+  // after the tiles).
+  int eid[2];
+  auto row_edges = [&](int r0) {
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb) {
       const int r = r0 + 16 * qb + c16;
+      eid[qb] = r < ur.nrows ? csr_edge[ur.p0 + r / G] : -1;
+    }
+  };
+  bf16x8 qf[2][2];
+  int erow[2];
+  float wrow[2];
+  auto row_operands = [&](int r0) {
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+      const int r = r0 + 16 * qb + c16;
+      const int e = eid[qb];
       erow[qb] = -1;
+      wrow[qb] = 1.f;
       qf[qb][0] = qf[qb][1] = zero_frag<bf16>();
-      if (r < ur.nrows) {
-        const int e = csr_edge[ur.p0 + r / G];
+      if (e >= 0) {
         const int hq = ur.hk * G + r % G;
         erow[qb] = e * rpe + (hq - hq_off);
         if (omega) wrow[qb] = omega[e];
@@ -801,6 +801,33 @@ __global__ __launch_bounds__(64 * kUnitWaves) void sparse_fwd_unit_kernel(
         qf[qb][0] = Load8<bf16, bf16>::run(qp);
         qf[qb][1] = Load8<bf16, bf16>::run(qp + 32);
       }
+    }
+  };
+  row_edges(0);
+  // K as the A operand of S^T = K Q^T (lane = key), V staged row-major for V^T reads
+  bf16x8 kf[4][2];
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) kf[kb][ks] = Load8<bf16, bf16>::run(k + kv0 + (16 * kb + c16) * rs + 32 * ks + 8 * g);
+  V16 vrow[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int row = 8 * i + (lane >> 3), c0 = 8 * (lane & 7);
+    vrow[i] = ld16(v + kv0 + row * rs + c0);
+  }
+  row_operands(0);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int row = 8 * i + (lane >> 3), c0 = 8 * (lane & 7);
+    st16(sV + Tile::off(row, c0), vrow[i]);
+  }
+  wave_lds_sync();
+  for (int r0 = 0; r0 < ur.nrows; r0 += 32) {
+    const bool two = r0 + 16 < ur.nrows;
+    if (r0 > 0) {
+      row_edges(r0);
+      row_operands(r0);
     }
     // S^T: lane = query row 16 qb + c16, keys 16 kb + 4 g + x
     f32x4 st[4][2];
