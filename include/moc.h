@@ -506,7 +506,13 @@ int moc_sparse_zero_untouched(int dtype, void* dk, void* dv, int64_t cs, int64_t
 int moc_decode_partial(int dtype, const void* q, int64_t B, int H, const void* k_tiles, const void* v_tiles, int HK,
                        int Dh, int T, const int32_t* uniq, const int32_t* n_uniq, const int32_t* csr_off,
                        const int32_t* csr_edge, int64_t max_u, const float* omega, int NS, float scale, float* o_part,
-                       float* lse_part, hipStream_t stream);
+                       float* lse_part, const int32_t* row_tab, hipStream_t stream);
+/* The decode step's row table, built once per routing: row_tab i32 [max_u][16] = the first 16
+ * edges (csr order) of each distinct chapter of the plan, -1 padded (no reference counterpart: a
+ * precomputed index of the same plan).  moc_decode_partial reads it (when non-NULL) instead of
+ * csr_edge for a unit's first 16 rows. */
+int moc_decode_row_table(const int32_t* n_uniq, const int32_t* csr_off, const int32_t* csr_edge, int64_t max_u,
+                         int32_t* row_tab, hipStream_t stream);
 
 #ifdef __cplusplus
 }

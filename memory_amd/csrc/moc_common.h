@@ -336,12 +336,14 @@ inline int dtype_size(int dt) { return dt == MOC_F32 ? 4 : (dt == MOC_BF16 ? 2 :
 // with the decode step: per (distinct chapter, kv head) unit, every row of every edge of
 // the chapter gets o_part (normalised, times omega[e]) and lse_part (log2 domain) over
 // the chapter's 64 keys, with logits scaled by omega[e] * scale (omega == nullptr: 1;
-// omega >= 0).  Arguments as moc_sparse_fwd; `who` names the caller in errors.
+// omega >= 0).  Arguments as moc_sparse_fwd; `who` names the caller in errors.  row_tab
+// (optional, i32 [max_u][16]): the first 16 edges of each distinct chapter (-1 padded,
+// moc_decode_row_table), read instead of csr_edge for a unit's first 16 rows.
 int sparse_fwd_launch(int dtype, const void* q, int HQ, const void* k, const void* v, int64_t cs, int64_t hs,
                       int64_t rs, int HK, const int32_t* uniq, const int32_t* n_uniq, const int32_t* csr_off,
                       const int32_t* csr_edge, int64_t max_u, int S, int hk0, int nhk, int hq_off, int rpe,
                       float scale, const float* omega, float* o_part, float* lse_part, hipStream_t stream,
-                      const char* who);
+                      const char* who, const int32_t* row_tab = nullptr);
 
 // out[i] = inv * sum_j part[j * n + i] for i < n, j < nsplit, summed in a fixed order
 // (router.hip's split-row reduction); returns a MOC_ status.

@@ -756,136 +756,133 @@ __device__ __forceinline__ bool unit_setup(UnitRows& ur, const int32_t* uniq, co
   return ur.u < nu;
 }
 
+// One 16-byte-per-lane LDS DMA (buffer_load_dwordx4 ... lds): lane l's 16 bytes at voff of the
+// buffer land at LDS address m0 + 16 l.  Inline assembly, so the wait on these loads is the
+// explicit vmcnt(0) below (the compiler's own waits cover only its loads; they stay correct since
+// waiting for an older load with newer DMAs outstanding only waits longer).
+typedef __attribute__((address_space(3))) void* unit_lds_ptr_t;
+__device__ __forceinline__ void unit_dma16(__amdgpu_buffer_rsrc_t r, uint32_t voff, const char* lds) {
+  const uint32_t m0 = (uint32_t)(uintptr_t)(unit_lds_ptr_t)lds;
+  asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(r), "{m0}"(m0) : "memory");
+}
+
+// Forward of one unit: S^T = K Q^T (lane = query row), per-row softmax over the chapter's 64 keys,
+// O^T = V^T P^T, normalised partial rows and their lse.  The V tile goes global -> LDS by DMA (no
+// registers held while it is in flight; the source addresses carry the tile's chunk swizzle), K
+// fragments straight into registers, and the first 16-row block's edge ids before both, so its
+// q loads go out while the tiles are in flight.  Rows are taken 16 at a time (a decode unit has
+// one or two).
 __global__ __launch_bounds__(64 * kUnitWaves) void sparse_fwd_unit_kernel(
     const bf16* __restrict__ q, int HQ, const bf16* __restrict__ k, const bf16* __restrict__ v, int64_t cs,
     int64_t hs, int64_t rs, int HK, const int32_t* __restrict__ uniq, const int32_t* __restrict__ n_uniq,
     const int32_t* __restrict__ csr_off, const int32_t* __restrict__ csr_edge, int64_t max_u, int S, int hk0,
     int nhk, int hq_off, int rpe, float scale_log2, float* __restrict__ o_part, float* __restrict__ lse_part,
-    const float* __restrict__ omega) {
+    const float* __restrict__ omega, const int32_t* __restrict__ row_tab) {
   using Tile = SwzTile<bf16, 64>;
-  __shared__ __attribute__((aligned(16))) char sVall[kUnitWaves][64 * 64 * 2];
+  __shared__ __attribute__((aligned(1024))) char sVall[kUnitWaves][64 * 64 * 2];
   const int G = HQ / HK;
   UnitRows ur;
-  if (!unit_setup(ur, uniq, n_uniq, csr_off, hk0, nhk, G, max_u)) return;
   const int lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
+  // with a row table (first 16 edges of every distinct chapter, -1 padded: the decode path,
+  // whose plan is fixed for a whole generation) the first block's edge ids do not wait for
+  // csr_off: they are requested together with the plan entries
+  int eid_tab = -1;
+  if (row_tab) {
+    const int64_t u0 = ((int64_t)blockIdx.x * kUnitWaves + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6)) / nhk;
+    if (u0 < max_u) eid_tab = row_tab[u0 * 16 + c16 / G];
+  }
+  if (!unit_setup(ur, uniq, n_uniq, csr_off, hk0, nhk, G, max_u)) return;
   char* sV = sVall[threadIdx.x >> 6];
   const int64_t kv0 = (int64_t)ur.gid * cs + (int64_t)ur.hk * hs;
-  // Row operands of a 32-row block: the edge of each row (csr order), its omega and its q
-  // fragments.  The first block's edge ids are requested before the K / V tiles, so their
-  // q loads go out while the tiles are still in flight (one memory round trip, not two,
-  // after the tiles).
-  int eid[2];
-  auto row_edges = [&](int r0) {
+  {
+    // DMA instruction i fills LDS rows 8 i .. 8 i + 7: lane l -> row 8 i + l / 8, physical chunk
+    // l % 8 = logical chunk (l % 8) ^ (row & 7) of Tile::off
+    const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<bf16*>(v + kv0), (short)0, (int)((63 * rs + 64) * 2), 0x00020000);
 #pragma unroll
-    for (int qb = 0; qb < 2; ++qb) {
-      const int r = r0 + 16 * qb + c16;
-      eid[qb] = r < ur.nrows ? csr_edge[ur.p0 + r / G] : -1;
+    for (int i = 0; i < 8; ++i) {
+      const int row = 8 * i + (lane >> 3), lch = (lane & 7) ^ (row & 7);
+      unit_dma16(vr, (uint32_t)((row * rs + 8 * lch) * 2), sV + 1024 * i);
     }
+  }
+  int eid = -1;
+  auto row_edge = [&](int r0) {
+    const int r = r0 + c16;
+    eid = r < ur.nrows ? (row_tab && r0 == 0 ? eid_tab : csr_edge[ur.p0 + r / G]) : -1;
   };
-  bf16x8 qf[2][2];
-  int erow[2];
-  float wrow[2];
+  bf16x8 qf[2];
+  int erow;
+  float wrow;
   auto row_operands = [&](int r0) {
-#pragma unroll
-    for (int qb = 0; qb < 2; ++qb) {
-      const int r = r0 + 16 * qb + c16;
-      const int e = eid[qb];
-      erow[qb] = -1;
-      wrow[qb] = 1.f;
-      qf[qb][0] = qf[qb][1] = zero_frag<bf16>();
-      if (e >= 0) {
-        const int hq = ur.hk * G + r % G;
-        erow[qb] = e * rpe + (hq - hq_off);
-        if (omega) wrow[qb] = omega[e];
-        const bf16* qp = q + ((int64_t)(e / S) * HQ + hq) * kSpDh + 8 * g;
-        qf[qb][0] = Load8<bf16, bf16>::run(qp);
-        qf[qb][1] = Load8<bf16, bf16>::run(qp + 32);
-      }
+    const int r = r0 + c16;
+    erow = -1;
+    wrow = 1.f;
+    qf[0] = qf[1] = zero_frag<bf16>();
+    if (eid >= 0) {
+      const int hq = ur.hk * G + r % G;
+      erow = eid * rpe + (hq - hq_off);
+      if (omega) wrow = omega[eid];
+      const bf16* qp = q + ((int64_t)(eid / S) * HQ + hq) * kSpDh + 8 * g;
+      qf[0] = Load8<bf16, bf16>::run(qp);
+      qf[1] = Load8<bf16, bf16>::run(qp + 32);
     }
   };
-  row_edges(0);
-  // K as the A operand of S^T = K Q^T (lane = key), V staged row-major for V^T reads
+  row_edge(0);
+  // K as the A operand of S^T = K Q^T (lane = key)
   bf16x8 kf[4][2];
 #pragma unroll
   for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) kf[kb][ks] = Load8<bf16, bf16>::run(k + kv0 + (16 * kb + c16) * rs + 32 * ks + 8 * g);
-  V16 vrow[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int row = 8 * i + (lane >> 3), c0 = 8 * (lane & 7);
-    vrow[i] = ld16(v + kv0 + row * rs + c0);
-  }
   row_operands(0);
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int row = 8 * i + (lane >> 3), c0 = 8 * (lane & 7);
-    st16(sV + Tile::off(row, c0), vrow[i]);
-  }
-  wave_lds_sync();
-  for (int r0 = 0; r0 < ur.nrows; r0 += 32) {
-    const bool two = r0 + 16 < ur.nrows;
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the V tile (and everything before) has landed
+  for (int r0 = 0; r0 < ur.nrows; r0 += 16) {
     if (r0 > 0) {
-      row_edges(r0);
+      row_edge(r0);
       row_operands(r0);
     }
-    // S^T: lane = query row 16 qb + c16, keys 16 kb + 4 g + x
-    f32x4 st[4][2];
+    // S^T: lane = query row r0 + c16, keys 16 kb + 4 g + x
+    f32x4 st[4];
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      st[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+      mma(st[kb], kf[kb][0], qf[0]);
+      mma(st[kb], kf[kb][1], qf[1]);
+    }
+    bf16x8 pf[2];
+    float mx = st[0][0];
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-      for (int qb = 0; qb < 2; ++qb) {
-        st[kb][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
-        if (qb == 0 || two) {
-          mma(st[kb][qb], kf[kb][0], qf[qb][0]);
-          mma(st[kb][qb], kf[kb][1], qf[qb][1]);
-        }
+      for (int x = 0; x < 4; ++x) mx = fmax_fast(mx, st[kb][x]);
+    const float c = wrow * scale_log2;
+    const float m = quad_max(mx) * c;
+    float ps = 0.f;
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+      for (int x = 0; x < 4; ++x) {
+        const float p = exp2f(st[kb][x] * c - m);
+        ps += p;
+        pf[kb >> 1][4 * (kb & 1) + x] = (bf16)p;
       }
-    bf16x8 pf[2][2];
-    float m[2], l[2];
-#pragma unroll
-    for (int qb = 0; qb < 2; ++qb) {
-      float mx = st[0][qb][0];
-#pragma unroll
-      for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-        for (int x = 0; x < 4; ++x) mx = fmax_fast(mx, st[kb][qb][x]);
-      const float c = wrow[qb] * scale_log2;
-      m[qb] = quad_max(mx) * c;
-      float ps = 0.f;
-#pragma unroll
-      for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-        for (int x = 0; x < 4; ++x) {
-          const float p = exp2f(st[kb][qb][x] * c - m[qb]);
-          ps += p;
-          pf[qb][kb >> 1][4 * (kb & 1) + x] = (bf16)p;
-        }
-      l[qb] = quad_sum(ps);
-    }
+    const float l = quad_sum(ps);
     // O^T = V^T P^T: lane = query row, dims 16 db + 4 g + x
-    f32x4 o[4][2];
+    f32x4 o[4];
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
       const bf16x8 a0 = tr_frag_mk<Tile>(sV, 0, 16 * db, lane);
       const bf16x8 a1 = tr_frag_mk<Tile>(sV, 32, 16 * db, lane);
-#pragma unroll
-      for (int qb = 0; qb < 2; ++qb) {
-        o[db][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
-        if (qb == 0 || two) {
-          mma(o[db][qb], a0, pf[qb][0]);
-          mma(o[db][qb], a1, pf[qb][1]);
-        }
-      }
+      o[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+      mma(o[db], a0, pf[0]);
+      mma(o[db], a1, pf[1]);
     }
+    if (erow >= 0) {
+      const float inv = wrow / l;
+      float* op = o_part + (int64_t)erow * kSpDh;
 #pragma unroll
-    for (int qb = 0; qb < 2; ++qb) {
-      if (erow[qb] < 0) continue;
-      const float inv = wrow[qb] / l[qb];
-      float* op = o_part + (int64_t)erow[qb] * kSpDh;
-#pragma unroll
-      for (int db = 0; db < 4; ++db) *reinterpret_cast<f32x4*>(op + 16 * db + 4 * g) = o[db][qb] * inv;
-      if (g == 0) lse_part[erow[qb]] = m[qb] + log2f(l[qb]);
+      for (int db = 0; db < 4; ++db) *reinterpret_cast<f32x4*>(op + 16 * db + 4 * g) = o[db] * inv;
+      if (g == 0) lse_part[erow] = m + log2f(l);
     }
   }
 }
@@ -1231,7 +1228,7 @@ int moc::sparse_fwd_launch(int dtype, const void* q, int HQ, const void* k, cons
                            int64_t rs, int HK, const int32_t* uniq, const int32_t* n_uniq, const int32_t* csr_off,
                            const int32_t* csr_edge, int64_t max_u, int S, int hk0, int nhk, int hq_off, int rpe,
                            float scale, const float* omega, float* o_part, float* lse_part, hipStream_t stream,
-                           const char* who) {
+                           const char* who, const int32_t* row_tab) {
   const float sl2 = scale * 1.4426950408889634f;
   if (dtype == MOC_BF16) {
     MOC_REQUIRE(unit_kv_aligned(q, k, v, cs, hs, rs) && ((uintptr_t)o_part & 15) == 0, MOC_ERR_ARG,
@@ -1240,7 +1237,7 @@ int moc::sparse_fwd_launch(int dtype, const void* q, int HQ, const void* k, cons
     hipLaunchKernelGGL(sparse_fwd_unit_kernel, dim3((unsigned)((units + kUnitWaves - 1) / kUnitWaves)),
                        dim3(64 * kUnitWaves), 0, stream, (const bf16*)q, HQ, (const bf16*)k, (const bf16*)v, cs, hs,
                        rs, HK, uniq, n_uniq, csr_off, csr_edge, max_u, S, hk0, nhk, hq_off, rpe, sl2, o_part,
-                       lse_part, omega);
+                       lse_part, omega, row_tab);
     return check_launch("sparse_fwd_unit_kernel");
   }
   if (dtype == MOC_F32) {

@@ -101,6 +101,11 @@ class DecodeRouting:
         # (one synchronisation here, none per step) so each step launches exactly one wave per
         # selected (chapter, kv head) tile instead of min(B * NS, C) chapters' worth
         self.n_unique = int(self.plan.n_uniq[0].item())
+        # the first 16 edges of every distinct chapter, read by the decode kernel with its plan
+        # entries (instead of after them, through csr_off)
+        self.row_tab = torch.empty(self.n_unique * 16, device=self.idx.device, dtype=torch.int32)
+        call("moc_decode_row_table", ptr(self.plan.n_uniq), ptr(self.plan.csr_off), ptr(self.plan.csr_edge),
+             self.n_unique, ptr(self.row_tab), stream_ptr(self.idx.device))
 
     def unique_chapters(self) -> int:
         return self.n_unique
@@ -122,7 +127,7 @@ def decode_attention(q: torch.Tensor, cache: MemoryDecodeCache, routing: DecodeR
     pl = routing.plan
     call("moc_decode_partial", dt, ptr(q), B, H, ptr(cache.k_tiles), ptr(cache.v_tiles), cache.HK, D, cache.T,
          ptr(pl.uniq), ptr(pl.n_uniq), ptr(pl.csr_off), ptr(pl.csr_edge), routing.n_unique, ptr(routing.omega), NS,
-         float(D) ** -0.5, ptr(o_part), ptr(lse_part), st)
+         float(D) ** -0.5, ptr(o_part), ptr(lse_part), ptr(routing.row_tab), st)
     out = torch.empty(B, H, D, device=q.device, dtype=cache.dtype)
     lse = torch.empty(B * H, device=q.device, dtype=torch.float32)
     call("moc_sparse_combine", dt, ptr(o_part), ptr(lse_part), ptr(pl.edge_u), None, 1, NS, H, B, H, 0, ptr(out),
