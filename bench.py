@@ -149,24 +149,31 @@ def cpu_model() -> str:
 
 PROBE_BYTES = 256 << 20
 # entry point -> device kernel whose HBM traffic the counter passes measured
-TRAFFIC_KERNELS = {"moc_xattn_bwd_dkv": "xattn_bwd_dkv_kernel", "moc_xattn_fwd": "xattn_fwd_kernel",
-                   "moc_xattn_bwd_dq": "xattn_bwd_dq_kernel", "moc_kv_project": "kv_project_wide_kernel",
+# entry point / native-layer stage -> the device kernel its roofline figures are about
+TRAFFIC_KERNELS = {"moc_xattn_bwd_dkv": "xattn_bwd_dkv_kernel<bf16>", "moc_xattn_fwd": "xattn_fwd_kernel<bf16>",
+                   "moc_xattn_bwd_dq": "xattn_bwd_dq_kernel<bf16>", "moc_kv_project": "kv_project_wide_kernel",
                    "moc_decode_partial": "sparse_fwd_unit_kernel", "moc_sparse_bwd": "sparse_bwd_unit_kernel",
                    "moc_bank_adamw": "bank_adamw_kernel"}
-# device kernel -> the HIP source it is built from (counter figures are tied to that file's hash)
-KERNEL_SOURCES = {"xattn_fwd_kernel": "xattn_fwd.hip", "xattn_bwd_dq_kernel": "xattn_bwd.hip",
-                  "xattn_bwd_dkv_kernel": "xattn_bwd.hip", "xattn_bwd_kernel": "xattn_bwd.hip",
-                  "gather_rows_kernel": "xattn_bwd.hip", "kv_project_wide_kernel": "kv_project.hip",
-                  "kv_wgrad_kernel": "kv_wgrad.hip", "kv_wgrad_kernel_dense": "kv_wgrad.hip",
-                  "kv_wgrad_kernel_gather": "kv_wgrad.hip", "sparse_fwd_unit_kernel": "sparse_xattn.hip",
-                  "sparse_bwd_unit_kernel": "sparse_xattn.hip", "sparse_combine_kernel": "sparse_xattn.hip",
-                  "sparse_dq_combine_kernel": "sparse_xattn.hip", "bank_adamw_kernel": "bank_optim.hip"}
+
+
+def kernel_sources():
+    """Device kernel name (without template arguments) -> the HIP source that defines it, read
+    from the `__global__` declarations under memory_amd/csrc."""
+    import glob
+    import re
+    out = {}
+    for path in sorted(glob.glob(os.path.join(ROOT, "memory_amd", "csrc", "*.hip"))):
+        with open(path) as f:
+            text = f.read()
+        for n in re.findall(r"__global__(?:\s+__launch_bounds__\([^)]*\))?\s+void\s+(\w+)\s*\(", text):
+            out.setdefault(n, os.path.basename(path))
+    return out
 
 
 def source_sha(kernel: str):
     """First 16 hex digits of the SHA-256 of the HIP source ``kernel`` is built from."""
     import hashlib
-    src = KERNEL_SOURCES.get(kernel)
+    src = kernel_sources().get(kernel.split("<")[0])
     if src is None:
         return None
     path = os.path.join(ROOT, "memory_amd", "csrc", src)
@@ -205,13 +212,101 @@ def measured_traffic(workload, entry):
 XCDS, SIMDS, CUS = 8, 1024, 256   # MI355X: GRBM_GUI_ACTIVE sums the 8 XCDs' counts
 
 
+_MANGLED_TYPES = {"DF16b": "bf16", "f": "f32", "d": "f64", "i": "i32", "l": "i64", "b": "bool"}
+
+
 def _short_kernel(name: str) -> str:
+    """`kernel<template args>` from a rocprofv3 kernel name, mangled (`_ZN3moc...`) or demangled
+    (`void moc::...::name<2, 0>(...)`); the arguments tell instantiations apart."""
     import re
-    m = re.match(r"_ZN3moc(\d+)", name)
-    if m:
-        return name[len(m.group(0)):len(m.group(0)) + int(m.group(1))]
-    m = re.search(r"moc::(\w+)", name)
-    return m.group(1) if m else name[:48]
+    if name.startswith("_ZN"):
+        i, parts = 3, []
+        while i < len(name) and name[i].isdigit():
+            m = re.match(r"\d+", name[i:])
+            n = int(m.group(0))
+            i += len(m.group(0))
+            parts.append(name[i:i + n])
+            i += n
+        base, args = parts[-1] if parts else name[:48], []
+        if i < len(name) and name[i] == "I":
+            i += 1
+            while i < len(name) and name[i] != "E":
+                lit = re.match(r"L(DF16b|[a-z])(-?\d+)E", name[i:])
+                if lit:
+                    args.append(lit.group(2))
+                    i += len(lit.group(0))
+                    continue
+                for code, t in _MANGLED_TYPES.items():
+                    if name.startswith(code, i):
+                        args.append(t)
+                        i += len(code)
+                        break
+                else:
+                    break
+        return base + (f"<{','.join(args)}>" if args else "")
+    m = re.search(r"(\w+)(<[^()]*>)?\(", name)
+    if not m:
+        return name[:48]
+    args = (m.group(2) or "").replace(" ", "").replace("float", "f32")
+    return m.group(1) + args
+
+
+def traffic_summary(fetch_csv, write_csv):
+    """HBM bytes per launch and kernel from two rocprofv3 --pmc runs (FETCH_SIZE, then
+    WRITE_SIZE; counter_collection.csv, KiB per dispatch), each scaled by what the same counter
+    reads for the plain PROBE_BYTES device copy (`--traffic-probe`, `__amd_rocclr_copyBuffer`)
+    of the same run.  Prints a markdown table and the machine-readable lines bench.py reads back
+    (tied to the kernel source's hash)."""
+    import csv
+    from collections import defaultdict
+
+    def read(path, counter):
+        per = defaultdict(list)
+        with open(path) as f:
+            for r in csv.DictReader(f):
+                if r["Counter_Name"] == counter:
+                    per[_short_kernel(r["Kernel_Name"])].append(float(r["Counter_Value"]))
+        return per
+
+    fe, wr = read(fetch_csv, "FETCH_SIZE"), read(write_csv, "WRITE_SIZE")
+    probe = "__amd_rocclr_copyBuffer"
+    if probe not in fe or probe not in wr:
+        raise SystemExit(f"traffic summary: no {probe} dispatch (run with --traffic-probe)")
+    kib = PROBE_BYTES / 1024.0
+    f_scale, w_scale = kib / max(fe[probe]), kib / max(wr[probe])
+    rows, lines = [], []
+    for k in sorted(set(fe) & set(wr)):
+        if source_sha(k) is None:   # runtime copies, torch and rocprim kernels
+            continue
+        f, w = sum(fe[k]) / len(fe[k]), sum(wr[k]) / len(wr[k])
+        nbytes = (f * f_scale + w * w_scale) * 1024.0
+        rows.append(f"| `{k}` | {len(fe[k])} | {f:.1f} | {w:.1f} | {nbytes / 1e6:.1f} MB |")
+        sha = source_sha(k)
+        if sha is not None:
+            lines.append(f"    traffic_bytes {k} {nbytes:.0f} {sha}")
+    head = (f"Probe copy ({PROBE_BYTES} bytes read and written): FETCH_SIZE {max(fe[probe]):.1f} KiB, "
+            f"WRITE_SIZE {max(wr[probe]):.1f} KiB, so bytes = FETCH_SIZE x {f_scale:.4f} x 1024 + "
+            f"WRITE_SIZE x {w_scale:.4f} x 1024.\n\n"
+            "| kernel | launches | FETCH_SIZE (KiB) | WRITE_SIZE (KiB) | HBM bytes / launch (scaled) |\n"
+            "|---|---:|---:|---:|---:|")
+    return head + "\n" + "\n".join(rows) + "\n\nMachine-readable (read by bench.py):\n\n" + "\n".join(lines)
+
+
+def stats_summary(path):
+    """Markdown table of a rocprofv3 --kernel-trace --stats kernel_stats.csv with the kernels named
+    as `kernel<template args>` and the HIP source each one is built from."""
+    import csv
+    src = kernel_sources()
+    rows = ["| kernel | source | calls | avg (us) | total (ms) | % |", "|---|---|---:|---:|---:|---:|"]
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            k = _short_kernel(r["Name"])
+            if len(k) > 72:
+                k = k[:69] + "..."
+            rows.append(f"| `{k}` | {src.get(k.split('<')[0], '-')} | {r['Calls']} | "
+                        f"{float(r['AverageNs']) / 1e3:.1f} | {float(r['TotalDurationNs']) / 1e6:.3f} | "
+                        f"{float(r['Percentage']):.1f} |")
+    return "\n".join(rows)
 
 
 def pmc_summary(paths):
@@ -232,6 +327,8 @@ def pmc_summary(paths):
                 grid[k] = int(r["Grid_Size"])
     rows, lines = [], []
     for k in sorted(per):
+        if source_sha(k) is None:   # runtime copies, torch and rocprim kernels
+            continue
         acc = defaultdict(list)
         for c in per[k].values():
             for n, v in c.items():
@@ -289,17 +386,27 @@ def kernel_table(events, steps):
     return per
 
 
+def stage_table(stages, steps):
+    """Per-kernel table entries from the native layer's stage timing (moc_seq_layer_timing)."""
+    return {n: {"calls_per_step": c / steps, "avg_ms": t / c, "ms_per_step": t / steps}
+            for n, (t, c, _) in stages.items() if c}
+
+
 def profile_pass(fn, steps):
-    """Untimed pass with events around every entry point: the per-kernel table."""
+    """Untimed pass with events around every entry point and every stage of the native layer
+    (its kernels are launched from inside moc_seq_layer_fwd / _bwd): the per-kernel table."""
     import torch
     from memory_amd import _lib
     torch.cuda.synchronize()
+    _lib.seq_stage_timing(None, steps)
     _lib.KERNEL_EVENTS, _lib.KERNEL_EVENTS_ONLY = {}, None
     for _ in range(steps):
         fn()
     torch.cuda.synchronize()
     ev, _lib.KERNEL_EVENTS = _lib.KERNEL_EVENTS, None
-    return kernel_table(ev, steps)
+    stages = stage_table(_lib.seq_stage_read(), steps)
+    _lib.seq_stage_timing(None, 0)
+    return {**kernel_table(ev, steps), **stages}, set(stages)
 
 
 def timed(fn, steps, warmup, roofline_entry=None):
@@ -313,20 +420,30 @@ def timed(fn, steps, warmup, roofline_entry=None):
     from memory_amd import _lib
     for _ in range(warmup):
         fn()
-    per = profile_pass(fn, min(steps, 10))
+    per, stage_names = profile_pass(fn, min(steps, 10))
     if roofline_entry is None and per:
-        roofline_entry = max(per, key=lambda n: per[n]["ms_per_step"])
+        # the host calls of the native layer span many kernels: the roofline kernel is one of its stages
+        kern = [n for n in per if not n.startswith("moc_seq_layer_")]
+        roofline_entry = max(kern or per, key=lambda n: per[n]["ms_per_step"])
+    is_stage = roofline_entry in stage_names
     torch.cuda.synchronize()
-    _lib.KERNEL_EVENTS, _lib.KERNEL_EVENTS_ONLY = {}, {roofline_entry}
+    if is_stage:
+        _lib.seq_stage_timing([roofline_entry], steps)
+    else:
+        _lib.KERNEL_EVENTS, _lib.KERNEL_EVENTS_ONLY = {}, {roofline_entry}
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(steps):
         fn()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    ev = _lib.KERNEL_EVENTS
-    _lib.KERNEL_EVENTS, _lib.KERNEL_EVENTS_ONLY = None, None
-    live = kernel_table(ev, steps).get(roofline_entry)
+    if is_stage:
+        live = stage_table(_lib.seq_stage_read(), steps).get(roofline_entry)
+        _lib.seq_stage_timing(None, 0)
+    else:
+        ev = _lib.KERNEL_EVENTS
+        _lib.KERNEL_EVENTS, _lib.KERNEL_EVENTS_ONLY = None, None
+        live = kernel_table(ev, steps).get(roofline_entry)
     return wall * 1e3 / steps, per, roofline_entry, live
 
 
@@ -720,12 +837,23 @@ def main():
                     help="c3: skip the c5 decode and c4 token-level lines that ride along the headline")
     ap.add_argument("--pmc-summary", nargs="+", metavar="CSV",
                     help="print the per-kernel summary of rocprofv3 --pmc counter_collection.csv files and exit")
+    ap.add_argument("--stats-summary", metavar="STATS_CSV",
+                    help="print a rocprofv3 --stats kernel_stats.csv as a markdown table and exit")
+    ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="print the per-kernel HBM bytes of a FETCH_SIZE and a WRITE_SIZE "
+                         "counter_collection.csv (runs made with --traffic-probe) and exit")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="run one plain 256 MiB device copy before the warmup: the reference kernel "
                          "that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes")
     args = ap.parse_args()
     if args.pmc_summary:
         print(pmc_summary(args.pmc_summary))
+        return
+    if args.stats_summary:
+        print(stats_summary(args.stats_summary))
+        return
+    if args.traffic_summary:
+        print(traffic_summary(*args.traffic_summary))
         return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); "
@@ -760,13 +888,20 @@ def main():
         idx_star, _, _ = layer.route(h, return_losses=False)
         n_unique = int(torch.unique(idx_star).numel())
 
-    ms, per_kernel, dom, live = timed(lambda: run_step(layer, h, bank, dout), args.steps, args.warmup)
+    # the roofline kernel is the attention backward's dK/dV kernel (the largest main-stream stage;
+    # stages on the side streams overlap it, so their event spans include time shared with it)
+    ms, per_kernel, dom, live = timed(lambda: run_step(layer, h, bank, dout), args.steps, args.warmup,
+                                      roofline_entry="moc_xattn_bwd_dkv")
     ntok = cfg["B"] * cfg["L"]
     fl = algorithmic_flops(cfg, n_unique)
     tflops = fl["step"] / (ms * 1e-3) / 1e12
 
     flop_key = {"moc_kv_project": "kv_project_launch", "moc_xattn_fwd": "xattn_fwd_launch",
-                "moc_xattn_bwd_dq": "xattn_bwd_dq_launch", "moc_xattn_bwd_dkv": "xattn_bwd_dkv_launch"}
+                "moc_xattn_bwd_dq": "xattn_bwd_dq_launch", "moc_xattn_bwd_dkv": "xattn_bwd_dkv_launch",
+                "moc_chapter_project": "kv_project_launch", "moc_chapter_wgrad": "kv_project_launch",
+                "moc_chapter_dx": "kv_project_launch", "moc_rows_linear:q_proj": "q", "moc_rows_linear:o_proj": "o",
+                "moc_rows_linear:o_proj_dx": "o", "moc_rows_linear:q_proj_dx": "q", "moc_linear_wgrad:o_proj": "o",
+                "moc_linear_wgrad:q_proj": "q"}
     roofline = None
     if dom in flop_key and live:
         ach = fl[flop_key[dom]] / (live["avg_ms"] * 1e-3) / 1e12

@@ -271,6 +271,19 @@ int moc_seq_layer_bwd(const void* h, const void* bank, const void* wr, int wr_dt
                       size_t saved_bytes, const void* dout, const float* dlogits, void* dh, void* dbank,
                       int64_t bank_rows, float* dwr, float* dbr, void* dwq, void* dwkv, int dwkv_dtype, void* dwo,
                       void* scratch, size_t scratch_bytes, hipStream_t main, hipStream_t aux, hipStream_t fill);
+/* Stage timing of the two calls above (no counterpart in the reference, which times whole steps
+ * with torch.cuda.Event in its benchmarks, kernels-final/benchmark_kernels_final.py): stage s is
+ * one or a few launches on one stream, named by moc_seq_layer_stage_name(s) (the entry point
+ * and, where it is called more than once, its role).  moc_seq_layer_timing(mask, capacity) arms
+ * the stages whose bit is set in `mask` on the current device (timing events around each of
+ * their next `capacity` launches, on the stage's own stream; mask 0 disarms) and clears the
+ * counts; moc_seq_layer_timing_read waits for the recorded events and returns, per stage, the
+ * summed milliseconds, the timed launches and the launches past `capacity` (dropped may be
+ * NULL), then clears the counts.  Not for use under graph capture. */
+int moc_seq_layer_stage_count(void);
+const char* moc_seq_layer_stage_name(int stage);
+int moc_seq_layer_timing(uint64_t stage_mask, int capacity);
+int moc_seq_layer_timing_read(double* total_ms, int32_t* launches, int32_t* dropped, int n);
 
 /* ------------------------------------------------- routed attention forward */
 

@@ -45,6 +45,10 @@ _SIGS = {
                                _P, _P, _P, _P, _P, _P, _SZ, _P, _P]),
     "moc_seq_layer_bwd": (_I, [_P, _P, _P, _I, _P, _I64, _I64, _I64, _I, _I, _I64, _I, _I, _F, _P, _P, _P, _P, _SZ,
                                _P, _P, _P, _P, _I64, _P, _P, _P, _P, _I, _P, _P, _SZ, _P, _P, _P]),
+    "moc_seq_layer_stage_count": (_I, []),
+    "moc_seq_layer_stage_name": (ctypes.c_char_p, [_I]),
+    "moc_seq_layer_timing": (_I, [ctypes.c_uint64, _I]),
+    "moc_seq_layer_timing_read": (_I, [_P, _P, _P, _I]),
     "moc_rows_add_bcast": (_I, [_P, _I, _I64, _I64, _I64, _P, _P, _F, _P]),
     "moc_router_pool_workspace": (_SZ, [_I64, _I64, _I64]),
     "moc_router_pool": (_I, [_P, _I, _I64, _I64, _I64, _P, _P, _P, _SZ, _P]),
@@ -166,6 +170,36 @@ def call(name: str, *args) -> None:
         if rc in (MOC_ERR_ARG, MOC_ERR_UNSUPPORTED):
             raise ValueError(f"{name}: {msg}")
         raise MocError(f"{name} failed ({rc}): {msg}")
+
+
+def seq_stage_names():
+    """Names of the timed stages of moc_seq_layer_fwd / _bwd, in stage order."""
+    l = lib()
+    return [l.moc_seq_layer_stage_name(i).decode() for i in range(l.moc_seq_layer_stage_count())]
+
+
+def seq_stage_timing(names=None, capacity: int = 0) -> None:
+    """Arm timing events around the next ``capacity`` launches of the named stages of the
+    native layer (all stages when ``names`` is None; ``capacity`` 0 disarms)."""
+    all_names = seq_stage_names()
+    want = set(all_names) if names is None else set(names)
+    unknown = want - set(all_names)
+    if unknown:
+        raise ValueError(f"unknown moc_seq_layer stages: {sorted(unknown)}")
+    mask = sum(1 << i for i, n in enumerate(all_names) if n in want) if capacity else 0
+    call("moc_seq_layer_timing", ctypes.c_uint64(mask), int(capacity))
+
+
+def seq_stage_read():
+    """{stage name: (summed ms, timed launches, launches past capacity)} for the stages that ran
+    since arming; clears the counts (the stages stay armed)."""
+    names = seq_stage_names()
+    n = len(names)
+    tot = (ctypes.c_double * n)()
+    cnt = (ctypes.c_int32 * n)()
+    drop = (ctypes.c_int32 * n)()
+    call("moc_seq_layer_timing_read", ctypes.cast(tot, _P), ctypes.cast(cnt, _P), ctypes.cast(drop, _P), n)
+    return {names[i]: (tot[i], cnt[i], drop[i]) for i in range(n) if cnt[i] or drop[i]}
 
 
 class region:

@@ -22,7 +22,9 @@
 // 256 (features) x BM (rows) output tiles.  Each XCD (workgroups are dealt round-robin to the 8
 // XCDs) takes a contiguous range of tiles, feature blocks fastest, so the feature tiles of one
 // row block share its X rows in that XCD's L2.  Operands move global -> LDS with
-// buffer_load ... lds (no VGPR staging), 64 k-columns per stage, two stages in flight; the
+// buffer_load ... lds (no VGPR staging), 64 k-columns per stage, DEPTH stages loaded ahead of the
+// one being computed (DEPTH + 1 LDS buffers per operand: 2 for 256-row tiles, 3 for 128-row
+// tiles, whose few tiles per workgroup leave nothing else to hide the load latency); the
 // 16-byte chunks of every LDS row are XOR-swizzled by (row & 7) so fragment reads are
 // conflict-free.  8 waves in a 4 (features) x 2 (rows) grid; each wave owns 64 features x BM/2
 // rows (v_mfma_f32_16x16x32_bf16, fp32 accumulators in VGPRs).  The W tile's rows sit in LDS in a
@@ -39,7 +41,8 @@ typedef __attribute__((address_space(3))) void* lds_ptr_t;
 constexpr int kCgThreads = 512;
 constexpr int kCgStageW = 256 * 128;  // LDS bytes of one W stage (256 rows x 64 bf16)
 constexpr int kCgDxRows = 128;        // row tile of the dX GEMM (N = d is 3 feature tiles at d = 768)
-constexpr int kCgXpd = 1;             // stages the X operand is loaded ahead (W: one)
+constexpr int kCgDepth256 = 1;        // k-stages loaded ahead with 256-row tiles (LDS: 2 x 96 KB)
+constexpr int kCgDepth128 = 2;        // ... with 128-row tiles (LDS: 3 x 48 KB)
 
 enum { CG_SRC_GATHER = 0, CG_SRC_CONTIG = 1, CG_SRC_EDGE = 2 };
 enum { CG_DST_CONTIG = 0, CG_DST_BANK = 1 };
@@ -97,15 +100,16 @@ __device__ __forceinline__ void cg_dma16(__amdgpu_buffer_rsrc_t r, uint32_t voff
   const uint32_t m0 = (uint32_t)(uintptr_t)(lds_ptr_t)lds;
   asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(r), "s"(soff), "{m0}"(m0) : "memory");
 }
-// s_waitcnt vmcnt(n), n in {0, 2, 4}: all but this wave's newest n vector memory operations done
-// (loads complete in issue order)
+// s_waitcnt vmcnt(n), n in {0, 5, 6, 8}: all but this wave's newest n vector memory operations
+// done (loads complete in issue order); any other n waits for everything
 __device__ __forceinline__ void cg_wait_vm(int n) {
-  if (n == 4) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
-  else if (n == 2) asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
+  if (n == 8) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+  else if (n == 6) asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
+  else if (n == 5) asm volatile("s_waitcnt vmcnt(5)" ::: "memory");
   else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
-template <int SRC, int DST, typename TO, int BM, int XPD>
+template <int SRC, int DST, typename TO, int BM, int DEPTH>
 __global__ __launch_bounds__(kCgThreads) void chapter_gemm_kernel(
     const bf16* __restrict__ x, const bf16* __restrict__ xred, int64_t ldx, const int32_t* __restrict__ uniq,
     const int32_t* __restrict__ n_uniq, const int32_t* __restrict__ csr_off, const int32_t* __restrict__ csr_edge,
@@ -115,11 +119,14 @@ __global__ __launch_bounds__(kCgThreads) void chapter_gemm_kernel(
   constexpr int IPX = BM / 64;              // X DMA instructions per thread per stage
   constexpr int JB = BM / 32;               // 16-row MFMA tiles per wave
   constexpr int STX = BM * 128;             // LDS bytes of one X stage
-  constexpr int NXB = XPD + 1;              // X stages in LDS (X runs XPD stages ahead, W one)
-  static_assert(2 * kCgStageW + NXB * STX <= 163840, "LDS");
-  __shared__ __attribute__((aligned(1024))) char smem[2 * kCgStageW + NXB * STX];
+  constexpr int NBUF = DEPTH + 1;           // LDS buffers per operand
+  constexpr int kBatch = 4 + IPX;           // DMA instructions per wave and stage (W, then X)
+  static_assert(NBUF * (kCgStageW + STX) <= 163840, "LDS");
+  static_assert(DEPTH >= 1 && (DEPTH == 1 || (DEPTH - 1) * kBatch == 5 || (DEPTH - 1) * kBatch == 6 ||
+                               (DEPTH - 1) * kBatch == 8), "cg_wait_vm count");
+  __shared__ __attribute__((aligned(1024))) char smem[NBUF * (kCgStageW + STX)];
   char* const sW = smem;
-  char* const sX = smem + 2 * kCgStageW;
+  char* const sX = smem + NBUF * kCgStageW;
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = rfl(tid >> 6);
@@ -142,19 +149,19 @@ __global__ __launch_bounds__(kCgThreads) void chapter_gemm_kernel(
   const uint32_t xoff = (uint32_t)(srow * ldx * 2 + lchunk * 16);
   const uint32_t xbytes = (uint32_t)(64 * ldx * 2);
 
-  // W and X stage streams, each with its own cursor (tile, k-stage): X runs ahead of W
-  auto issue_w = [&](int s) {  // W of stage s (tile lo + slot + nslot * (s / nk), k-stage s % nk)
+  // the loads of stage s: tile lo + slot + nslot * (s / nk), k-stage s % nk, into buffer s % NBUF
+  auto issue_w = [&](int s) {
     const int t = lo + slot + nslot * (s / nk), kt = s % nk;
     const int nb = t % NB;
     const __amdgpu_buffer_rsrc_t wres = CG_RSRC(w + (int64_t)nb * 256 * K, (uint32_t)(256 * K * 2));
-    const char* dst = sW + (s & 1) * kCgStageW + wave * 1024;
+    const char* dst = sW + (s % NBUF) * kCgStageW + wave * 1024;
 #pragma unroll
     for (int i = 0; i < 4; ++i) cg_dma16(wres, woff, (uint32_t)(kt * 128 + 64 * i * K * 2), dst + 8192 * i);
   };
   auto issue_x = [&](int s) {
     const int t = lo + slot + nslot * (s / nk), kt = s % nk;
     const int rb = t / NB;
-    const char* dst = sX + (s % NXB) * STX + wave * 1024;
+    const char* dst = sX + (s % NBUF) * STX + wave * 1024;
 #pragma unroll
     for (int i = 0; i < IPX; ++i) {
       const int c = min(rb * CPT + i, nu - 1);  // rows of chapters past n_uniq: computed, not stored
@@ -239,36 +246,38 @@ __global__ __launch_bounds__(kCgThreads) void chapter_gemm_kernel(
       for (int j = 0; j < JB; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
   };
 
-  // Stage s computes from W(s) and X(s).  Per wave the loads go out as W(0), X(0 .. XPD-1), then
-  // at each stage W(s+1) and X(s+XPD); a wave's loads complete in issue order, so when the
-  // newest batch's X stage is allowed to stay in flight, "vmcnt <= IPX" means W(s+1) and
-  // X(s+1) have landed.  At a tile's last stage the X load goes out after the epilogue's stores,
-  // so no store ever sits between a needed load and the loads allowed in flight (with XPD == 1
-  // nothing stays in flight: every stage waits for all of the wave's loads and stores).
-  issue_w(0);
+  // Stage s computes from W(s) and X(s).  Per wave the loads go out as the batches W(p), X(p) of
+  // stages 0 .. DEPTH-1, then one batch (of stage s + DEPTH, into the buffer stage s-1 used) at
+  // each stage after its barrier.  A wave's loads complete in issue order, so with the batches
+  // of stages s+1 .. s+DEPTH-1 allowed to stay in flight, "vmcnt <= (those batches) x kBatch"
+  // means stage s's batch has landed.  After a tile's epilogue its stores are the newest
+  // operations, so the next stage waits for everything instead.
 #pragma unroll
-  for (int p = 0; p < XPD; ++p)
-    if (p < S) issue_x(p);
-  int in_flight = XPD > 1 && 1 < S ? IPX : 0;
+  for (int p = 0; p < DEPTH; ++p)
+    if (p < S) {
+      issue_w(p);
+      issue_x(p);
+    }
+  bool stored = false;
   for (int s = 0, kt = 0, t = lo + slot; s < S; ++s) {
-    cg_wait_vm(in_flight);
+    const int newer = min(DEPTH - 1, S - 1 - s);  // batches issued after stage s's
+    cg_wait_vm(stored ? 0 : newer * kBatch);
     __syncthreads();  // every wave's loads of stage s landed; every wave is done with stage s-1
     __builtin_amdgcn_sched_barrier(0);
-    const bool tile_end = kt + 1 == nk;
-    const bool has_w = s + 1 < S, has_x = s + XPD < S;
-    if (has_w) issue_w(s + 1);
-    if (has_x && (XPD == 1 || !tile_end)) issue_x(s + XPD);
+    if (s + DEPTH < S) {
+      issue_w(s + DEPTH);
+      issue_x(s + DEPTH);
+    }
     __builtin_amdgcn_sched_barrier(0);
-    compute(sW + (s & 1) * kCgStageW, sX + (s % NXB) * STX);
-    if (tile_end) {
+    compute(sW + (s % NBUF) * kCgStageW, sX + (s % NBUF) * STX);
+    stored = kt + 1 == nk;
+    if (stored) {
       epilogue(t);
       t += nslot;
       kt = 0;
-      if (XPD > 1 && has_x) issue_x(s + XPD);
     } else {
       ++kt;
     }
-    in_flight = XPD > 1 && has_x ? IPX : 0;
   }
 }
 
@@ -582,11 +591,11 @@ int moc_chapter_project(const void* rows, int64_t ld, int gather, const int32_t*
   if (max_u == 0) return MOC_OK;
   const dim3 grid((unsigned)cg_grid());
   if (gather)
-    hipLaunchKernelGGL((chapter_gemm_kernel<CG_SRC_GATHER, CG_DST_CONTIG, bf16, 256, kCgXpd>), grid, dim3(kCgThreads), 0,
+    hipLaunchKernelGGL((chapter_gemm_kernel<CG_SRC_GATHER, CG_DST_CONTIG, bf16, 256, kCgDepth256>), grid, dim3(kCgThreads), 0,
                        stream, (const bf16*)rows, nullptr, ld, uniq, n_uniq, nullptr, nullptr, max_u, (const bf16*)w,
                        N, K, (bf16*)y, ldy, max_u * 64, max_u * 64);
   else
-    hipLaunchKernelGGL((chapter_gemm_kernel<CG_SRC_CONTIG, CG_DST_CONTIG, bf16, 256, kCgXpd>), grid, dim3(kCgThreads), 0,
+    hipLaunchKernelGGL((chapter_gemm_kernel<CG_SRC_CONTIG, CG_DST_CONTIG, bf16, 256, kCgDepth256>), grid, dim3(kCgThreads), 0,
                        stream, (const bf16*)rows, nullptr, ld, uniq, n_uniq, nullptr, nullptr, max_u, (const bf16*)w,
                        N, K, (bf16*)y, ldy, max_u * 64, max_u * 64);
   return check_launch("chapter_gemm_kernel(project)");
@@ -604,7 +613,7 @@ int moc_chapter_dx(const void* dkv_edge, int64_t ld, const int32_t* uniq, const 
   if (max_u == 0) return MOC_OK;
   const dim3 grid((unsigned)cg_grid());
 #define MOC_CGDX(DST, TO)                                                                                           \
-  hipLaunchKernelGGL((chapter_gemm_kernel<CG_SRC_EDGE, DST, TO, kCgDxRows, kCgXpd>), grid, dim3(kCgThreads), 0, stream,          \
+  hipLaunchKernelGGL((chapter_gemm_kernel<CG_SRC_EDGE, DST, TO, kCgDxRows, kCgDepth128>), grid, dim3(kCgThreads), 0, stream,          \
                      (const bf16*)dkv_edge, (const bf16*)red, ld, uniq, n_uniq, csr_off, csr_edge, max_u,           \
                      (const bf16*)w_t, N, K, (TO*)out, ldo, max_u * 64, max_u * 64)
   if (out_bank_rows) {
@@ -623,7 +632,7 @@ int moc_rows_linear(const void* x, int64_t ldx, int64_t R, const void* w, int N,
   const int64_t blocks = (R + 63) / 64;
   if (int rc = cg_check("moc_rows_linear", ldx, N, K, blocks, ldy)) return rc;
   if (R == 0) return MOC_OK;
-  hipLaunchKernelGGL((chapter_gemm_kernel<CG_SRC_CONTIG, CG_DST_CONTIG, bf16, 128, kCgXpd>), dim3((unsigned)cg_grid()),
+  hipLaunchKernelGGL((chapter_gemm_kernel<CG_SRC_CONTIG, CG_DST_CONTIG, bf16, 128, kCgDepth128>), dim3((unsigned)cg_grid()),
                      dim3(kCgThreads), 0, stream, (const bf16*)x, nullptr, ldx, nullptr, nullptr, nullptr, nullptr,
                      blocks, (const bf16*)w, N, K, (bf16*)y, ldy, R, R);
   return check_launch("chapter_gemm_kernel(rows)");

@@ -53,6 +53,47 @@ int seq_events(hipEvent_t** out) {
 
 inline size_t al256(size_t x) { return (x + 255) & ~(size_t)255; }
 
+// Optional per-stage timing (off unless armed by moc_seq_layer_timing): a timing event pair
+// recorded around a stage's launches on the stream that stage runs on, so the elapsed time is
+// that stage's own kernels.  One set for the process, armed on one device; used by the
+// benchmark, never under graph capture.
+const char* const kStageNames[] = {
+    "moc_router_pool1", "moc_router_linear", "moc_router_topk_prepend", "moc_chapter_plan",
+    "moc_weight_pack:wkv", "moc_rows_linear:q_proj", "moc_weight_pack:transposed", "moc_chapter_project",
+    "moc_xattn_fwd", "moc_rows_linear:o_proj", "moc_linear_wgrad:o_proj", "moc_rows_linear:o_proj_dx",
+    "moc_xattn_bwd_prep", "moc_fill_zero:dbank", "moc_xattn_bwd_dq", "moc_rows_linear:q_proj_dx",
+    "moc_linear_wgrad:q_proj", "moc_xattn_bwd_dkv", "moc_router_seq_bwd+linear_bwd+pool_bwd",
+    "moc_dkv_multi_reduce", "moc_chapter_wgrad", "moc_chapter_dx"};
+enum Stage {
+  kStPool, kStRouterLinear, kStTopk, kStPlan, kStPackWkv, kStQProj, kStPackT, kStKVProj, kStAttnFwd, kStOProj,
+  kStOWgrad, kStODx, kStPrep, kStFill, kStDq, kStQDx, kStQWgrad, kStDkv, kStRouterBwd, kStMultiReduce, kStKVWgrad,
+  kStBankDx, kNumStages
+};
+static_assert(sizeof(kStageNames) / sizeof(kStageNames[0]) == kNumStages, "stage names");
+
+struct StageTimer {
+  uint64_t mask = 0;
+  int cap = 0, dev = -1;
+  hipEvent_t* ev = nullptr;  // [kNumStages][cap][2]
+  int count[kNumStages] = {};
+  int dropped[kNumStages] = {};
+};
+StageTimer g_timer;
+
+// Records the start event of stage s on `st` and returns its pair, or nullptr when s is not armed.
+hipEvent_t* stage_begin(int s, hipStream_t st) {
+  StageTimer& t = g_timer;
+  if (!(t.mask >> s & 1)) return nullptr;
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev != t.dev) return nullptr;
+  if (t.count[s] >= t.cap) {
+    ++t.dropped[s];
+    return nullptr;
+  }
+  hipEvent_t* p = t.ev + ((size_t)s * t.cap + t.count[s]++) * 2;
+  return hipEventRecord(p[0], st) == hipSuccess ? p : nullptr;
+}
+
 // Layout of the saved buffer (forward -> backward) and of the backward's scratch buffer.
 struct SeqLayout {
   int64_t B, L, d, C;
@@ -125,6 +166,14 @@ struct SeqLayout {
     if (int _rc = (call)) return _rc;  \
   } while (0)
 
+// `call` (which may be several launches) on stream `st`, timed as stage `s` when armed
+#define SEQ_STAGE(s, st, call)                                       \
+  do {                                                               \
+    hipEvent_t* _pair = stage_begin((s), (st));                      \
+    call;                                                            \
+    if (_pair) MOC_HIP(hipEventRecord(_pair[1], (st)));              \
+  } while (0)
+
 int fill_cus() {
   static int cus = 0;
   if (cus == 0) {
@@ -189,27 +238,35 @@ int moc_seq_layer_fwd(const void* h, const void* bank, const void* wr, int wr_dt
   // them), then the transposed weights the backward reads, beside the projection and attention
   MOC_HIP(hipEventRecord(ev[0], main));
   MOC_HIP(hipStreamWaitEvent(aux, ev[0], 0));
-  SEQ_TRY(moc_weight_pack(wk, MOC_BF16, wv, MOC_BF16, y.KV, d, wkv, nullptr, aux));
-  SEQ_TRY(moc_rows_linear(h, d, tok, wq, (int)d, (int)d, q, d, aux));
+  SEQ_STAGE(kStPackWkv, aux, SEQ_TRY(moc_weight_pack(wk, MOC_BF16, wv, MOC_BF16, y.KV, d, wkv, nullptr, aux)));
+  SEQ_STAGE(kStQProj, aux, SEQ_TRY(moc_rows_linear(h, d, tok, wq, (int)d, (int)d, q, d, aux)));
   MOC_HIP(hipEventRecord(ev[1], aux));
-  SEQ_TRY(moc_weight_pack(wk, MOC_BF16, wv, MOC_BF16, y.KV, d, nullptr, sv + y.wkv_t, aux));
-  SEQ_TRY(moc_weight_pack(wq, MOC_BF16, (const bf16*)wq + (d / 2) * d, MOC_BF16, d / 2, d, nullptr, sv + y.wq_t, aux));
-  SEQ_TRY(moc_weight_pack(wo, MOC_BF16, (const bf16*)wo + (d / 2) * d, MOC_BF16, d / 2, d, nullptr, sv + y.wo_t, aux));
+  SEQ_STAGE(kStPackT, aux, {
+    SEQ_TRY(moc_weight_pack(wk, MOC_BF16, wv, MOC_BF16, y.KV, d, nullptr, sv + y.wkv_t, aux));
+    SEQ_TRY(moc_weight_pack(wq, MOC_BF16, (const bf16*)wq + (d / 2) * d, MOC_BF16, d / 2, d, nullptr, sv + y.wq_t,
+                            aux));
+    SEQ_TRY(moc_weight_pack(wo, MOC_BF16, (const bf16*)wo + (d / 2) * d, MOC_BF16, d / 2, d, nullptr, sv + y.wo_t,
+                            aux));
+  });
   MOC_HIP(hipEventRecord(ev[2], aux));
 
   // main: router, plan
-  SEQ_TRY(moc_router_pool1(h, MOC_BF16, B, L, d, coef, pooled, main));
-  SEQ_TRY(moc_router_linear(pooled, B, d, wr, wr_dtype, br, C, logits, main));
-  SEQ_TRY(moc_router_topk_prepend(logits, B, C, S, k, routed_scale, idx, w, idx_star, omega, main));
-  SEQ_TRY(moc_chapter_plan(idx_star, y.E, C, sv + y.plan_ws, y.plan_ws_bytes, uniq, n_uniq, edge_u, csr_off, csr_edge,
-                           main));
+  SEQ_STAGE(kStPool, main, SEQ_TRY(moc_router_pool1(h, MOC_BF16, B, L, d, coef, pooled, main)));
+  SEQ_STAGE(kStRouterLinear, main, SEQ_TRY(moc_router_linear(pooled, B, d, wr, wr_dtype, br, C, logits, main)));
+  SEQ_STAGE(kStTopk, main,
+            SEQ_TRY(moc_router_topk_prepend(logits, B, C, S, k, routed_scale, idx, w, idx_star, omega, main)));
+  SEQ_STAGE(kStPlan, main,
+            SEQ_TRY(moc_chapter_plan(idx_star, y.E, C, sv + y.plan_ws, y.plan_ws_bytes, uniq, n_uniq, edge_u, csr_off,
+                                     csr_edge, main)));
   // main: K/V projection (gather fused), attention, o_proj
   MOC_HIP(hipStreamWaitEvent(main, ev[1], 0));
-  SEQ_TRY(moc_chapter_project(bank, d, 1, uniq, n_uniq, y.max_u, wkv, KV2, (int)d, kv, KV2, main));
+  SEQ_STAGE(kStKVProj, main,
+            SEQ_TRY(moc_chapter_project(bank, d, 1, uniq, n_uniq, y.max_u, wkv, KV2, (int)d, kv, KV2, main)));
   const int64_t span = y.max_u * 64 * KV2 - y.KV;
-  SEQ_TRY(moc_xattn_fwd(MOC_BF16, q, kv, kv + y.KV, span, (int64_t)64 * KV2, 64, KV2, edge_u, omega, B, L, H, HK, 64,
-                        64, y.NS, 0.125f, attn, lse, main));
-  SEQ_TRY(moc_rows_linear(attn, d, tok, wo, (int)d, (int)d, out, d, main));
+  SEQ_STAGE(kStAttnFwd, main,
+            SEQ_TRY(moc_xattn_fwd(MOC_BF16, q, kv, kv + y.KV, span, (int64_t)64 * KV2, 64, KV2, edge_u, omega, B, L,
+                                  H, HK, 64, 64, y.NS, 0.125f, attn, lse, main)));
+  SEQ_STAGE(kStOProj, main, SEQ_TRY(moc_rows_linear(attn, d, tok, wo, (int)d, (int)d, out, d, main)));
   MOC_HIP(hipStreamWaitEvent(main, ev[2], 0));
   return MOC_OK;
 }
@@ -260,50 +317,115 @@ int moc_seq_layer_bwd(const void* h, const void* bank, const void* wr, int wr_dt
   // aux: o_proj dW beside o_proj dX and the attention backward
   MOC_HIP(hipEventRecord(ev[0], main));
   MOC_HIP(hipStreamWaitEvent(aux, ev[0], 0));
-  if (dwo) SEQ_TRY(moc_linear_wgrad(dout, attn, MOC_BF16, tok, d, d, sc + y.lw_ws, y.lw_ws_bytes, MOC_BF16, dwo, aux));
+  if (dwo)
+    SEQ_STAGE(kStOWgrad, aux,
+              SEQ_TRY(moc_linear_wgrad(dout, attn, MOC_BF16, tok, d, d, sc + y.lw_ws, y.lw_ws_bytes, MOC_BF16, dwo,
+                                       aux)));
   // main: o_proj dX, backward prep
-  SEQ_TRY(moc_rows_linear(dout, d, tok, sv + y.wo_t, (int)d, (int)d, d_attn, d, main));
-  SEQ_TRY(moc_xattn_bwd_prep(MOC_BF16, q, attn, d_attn, B, L, H, 64, delta, nullptr, nullptr, main));
+  SEQ_STAGE(kStODx, main, SEQ_TRY(moc_rows_linear(dout, d, tok, sv + y.wo_t, (int)d, (int)d, d_attn, d, main)));
+  SEQ_STAGE(kStPrep, main,
+            SEQ_TRY(moc_xattn_bwd_prep(MOC_BF16, q, attn, d_attn, B, L, H, 64, delta, nullptr, nullptr, main)));
   // fill: the dense bank gradient's zeros beside dQ
   if (dbank) {
     MOC_HIP(hipEventRecord(ev[1], main));
     MOC_HIP(hipStreamWaitEvent(fill, ev[1], 0));
-    SEQ_TRY(moc_fill_zero(dbank, bank_rows * d * 2, fill_cus(), fill));
+    SEQ_STAGE(kStFill, fill, SEQ_TRY(moc_fill_zero(dbank, bank_rows * d * 2, fill_cus(), fill)));
     MOC_HIP(hipEventRecord(ev[2], fill));
   }
-  SEQ_TRY(moc_xattn_bwd_dq(MOC_BF16, q, kv, kv + y.KV, span, (int64_t)64 * KV2, 64, KV2, edge_u, omega, d_attn, lse,
-                           delta, B, L, H, HK, 64, 64, y.NS, 0.125f, dq, main));
+  SEQ_STAGE(kStDq, main,
+            SEQ_TRY(moc_xattn_bwd_dq(MOC_BF16, q, kv, kv + y.KV, span, (int64_t)64 * KV2, 64, KV2, edge_u, omega,
+                                     d_attn, lse, delta, B, L, H, HK, 64, 64, y.NS, 0.125f, dq, main)));
   // aux: q_proj dX into dh and dW beside dK/dV
   MOC_HIP(hipEventRecord(ev[3], main));
   MOC_HIP(hipStreamWaitEvent(aux, ev[3], 0));
-  if (dh) SEQ_TRY(moc_rows_linear(dq, d, tok, sv + y.wq_t, (int)d, (int)d, dh, d, aux));
-  if (dwq) SEQ_TRY(moc_linear_wgrad(dq, h, MOC_BF16, tok, d, d, sc + y.lw_ws, y.lw_ws_bytes, MOC_BF16, dwq, aux));
-  SEQ_TRY(moc_xattn_bwd_dkv(MOC_BF16, q, d_attn, kv, kv + y.KV, span, (int64_t)64 * KV2, 64, KV2, edge_u, omega, lse,
-                            delta, B, L, H, HK, 64, 64, y.NS, 0.125f, dkv_edge, dom_part, main));
+  if (dh) SEQ_STAGE(kStQDx, aux, SEQ_TRY(moc_rows_linear(dq, d, tok, sv + y.wq_t, (int)d, (int)d, dh, d, aux)));
+  if (dwq)
+    SEQ_STAGE(kStQWgrad, aux,
+              SEQ_TRY(moc_linear_wgrad(dq, h, MOC_BF16, tok, d, d, sc + y.lw_ws, y.lw_ws_bytes, MOC_BF16, dwq, aux)));
+  SEQ_STAGE(kStDkv, main,
+            SEQ_TRY(moc_xattn_bwd_dkv(MOC_BF16, q, d_attn, kv, kv + y.KV, span, (int64_t)64 * KV2, 64, KV2, edge_u,
+                                      omega, lse, delta, B, L, H, HK, 64, 64, y.NS, 0.125f, dkv_edge, dom_part,
+                                      main)));
   // aux: router backward and the pooling's gradient, beside the K/V chapter GEMMs
   MOC_HIP(hipEventRecord(ev[4], main));
   MOC_HIP(hipStreamWaitEvent(aux, ev[4], 0));
   if (router_grads) {
     float* dz = (float*)(sc + y.dz);
     float* dpooled = dh ? (float*)(sc + y.dpooled) : nullptr;
-    SEQ_TRY(moc_router_seq_bwd(logits, idx, w, dom_part, HK, B, C, S, k, routed_scale, dlogits, dz, aux));
-    SEQ_TRY(moc_router_linear_bwd(dz, pooled, B, d, wr, wr_dtype, C, dpooled, dwr, dbr, sc + y.rl_ws, y.rl_ws_bytes,
-                                  aux));
-    if (dh) SEQ_TRY(moc_rows_add_bcast(dh, MOC_BF16, B, L, d, dpooled, coef, 1.f / (float)L, aux));
+    SEQ_STAGE(kStRouterBwd, aux, {
+      SEQ_TRY(moc_router_seq_bwd(logits, idx, w, dom_part, HK, B, C, S, k, routed_scale, dlogits, dz, aux));
+      SEQ_TRY(moc_router_linear_bwd(dz, pooled, B, d, wr, wr_dtype, C, dpooled, dwr, dbr, sc + y.rl_ws,
+                                    y.rl_ws_bytes, aux));
+      if (dh) SEQ_TRY(moc_rows_add_bcast(dh, MOC_BF16, B, L, d, dpooled, coef, 1.f / (float)L, aux));
+    });
   }
   MOC_HIP(hipEventRecord(ev[5], aux));
   // main: K/V weight gradient and the projection's dX into the bank rows
   if (dbank || dwkv)
-    SEQ_TRY(moc_dkv_multi_reduce(dkv_edge, KV2, n_uniq, y.max_u, csr_off, csr_edge, red, main));
+    SEQ_STAGE(kStMultiReduce, main,
+              SEQ_TRY(moc_dkv_multi_reduce(dkv_edge, KV2, n_uniq, y.max_u, csr_off, csr_edge, red, main)));
   if (dwkv)
-    SEQ_TRY(moc_chapter_wgrad(dkv_edge, KV2, red, bank, d, 1, uniq, n_uniq, y.max_u, csr_off, csr_edge, KV2, (int)d,
-                              sc + y.cw_ws, y.cw_ws_bytes, dwkv_dtype, dwkv, main));
+    SEQ_STAGE(kStKVWgrad, main,
+              SEQ_TRY(moc_chapter_wgrad(dkv_edge, KV2, red, bank, d, 1, uniq, n_uniq, y.max_u, csr_off, csr_edge, KV2,
+                                        (int)d, sc + y.cw_ws, y.cw_ws_bytes, dwkv_dtype, dwkv, main)));
   if (dbank) {
     MOC_HIP(hipStreamWaitEvent(main, ev[2], 0));
-    SEQ_TRY(moc_chapter_dx(dkv_edge, KV2, uniq, n_uniq, y.max_u, csr_off, csr_edge, red, sv + y.wkv_t, (int)d, KV2,
-                           MOC_BF16, dbank, d, 1, main));
+    SEQ_STAGE(kStBankDx, main,
+              SEQ_TRY(moc_chapter_dx(dkv_edge, KV2, uniq, n_uniq, y.max_u, csr_off, csr_edge, red, sv + y.wkv_t,
+                                     (int)d, KV2, MOC_BF16, dbank, d, 1, main)));
   }
   MOC_HIP(hipStreamWaitEvent(main, ev[5], 0));
+  return MOC_OK;
+}
+
+int moc_seq_layer_stage_count(void) { return kNumStages; }
+
+const char* moc_seq_layer_stage_name(int stage) {
+  return stage >= 0 && stage < kNumStages ? kStageNames[stage] : nullptr;
+}
+
+int moc_seq_layer_timing(uint64_t stage_mask, int capacity) {
+  StageTimer& t = g_timer;
+  MOC_REQUIRE(capacity >= 0 && capacity <= 4096, MOC_ERR_ARG, "moc_seq_layer_timing: capacity %d (0..4096)",
+              capacity);
+  t.mask = 0;
+  int dev = 0;
+  MOC_HIP(hipGetDevice(&dev));
+  if (t.ev && (t.dev != dev || (stage_mask && capacity != t.cap))) {
+    for (size_t i = 0; i < (size_t)kNumStages * t.cap * 2; ++i) (void)hipEventDestroy(t.ev[i]);
+    delete[] t.ev;
+    t.ev = nullptr;
+  }
+  for (int s = 0; s < kNumStages; ++s) t.count[s] = t.dropped[s] = 0;
+  if (!stage_mask || capacity == 0) return MOC_OK;
+  if (!t.ev) {
+    t.ev = new hipEvent_t[(size_t)kNumStages * capacity * 2];
+    for (size_t i = 0; i < (size_t)kNumStages * capacity * 2; ++i) MOC_HIP(hipEventCreate(&t.ev[i]));
+    t.cap = capacity;
+    t.dev = dev;
+  }
+  t.mask = stage_mask;
+  return MOC_OK;
+}
+
+int moc_seq_layer_timing_read(double* total_ms, int32_t* launches, int32_t* dropped, int n) {
+  StageTimer& t = g_timer;
+  MOC_REQUIRE(total_ms && launches && n >= kNumStages, MOC_ERR_ARG, "moc_seq_layer_timing_read: n=%d < %d", n,
+              kNumStages);
+  for (int s = 0; s < kNumStages; ++s) {
+    double sum = 0.0;
+    for (int i = 0; i < t.count[s]; ++i) {
+      hipEvent_t* p = t.ev + ((size_t)s * t.cap + i) * 2;
+      MOC_HIP(hipEventSynchronize(p[1]));
+      float ms = 0.f;
+      MOC_HIP(hipEventElapsedTime(&ms, p[0], p[1]));
+      sum += ms;
+    }
+    total_ms[s] = sum;
+    launches[s] = t.count[s];
+    if (dropped) dropped[s] = t.dropped[s];
+    t.count[s] = t.dropped[s] = 0;
+  }
   return MOC_OK;
 }
 

@@ -111,3 +111,35 @@ def test_config1_recipe_scale_router_losses(gpu_device):
     tot = compute_total_router_loss(losses, 0.01, 0.0, 0.001)
     rtot = O.compute_total_router_loss(det["losses"], 0.01, 0.0, 0.001)
     assert_rel(tot.reshape(1), rtot.reshape(1), 1e-5, "total router loss")
+
+
+def test_native_stage_timing(gpu_device, monkeypatch):
+    """The native layer's stage timing (moc_seq_layer_timing) times every stage of one forward +
+    backward once, and is inert once disarmed."""
+    from memory_amd import _lib, seq_layer
+    monkeypatch.setattr(seq_layer, "NATIVE", True)
+    dev = gpu_device
+    h, bank, Wr, br, Wq, Wk, Wv, Wo = _config1_inputs(scale_w=0.08)
+    layer = _layer(dev, torch.bfloat16, Wr, br, Wq, Wk, Wv, Wo, False)
+    hg = h.to(dev, torch.bfloat16).requires_grad_(True)
+    bg = bank.to(dev, torch.bfloat16).requires_grad_(True)
+
+    def step():
+        out, _ = layer(hg, bg, return_losses=False)
+        out.float().sum().backward()
+
+    step()
+    torch.cuda.synchronize()
+    _lib.seq_stage_timing(None, 2)
+    try:
+        step()
+        torch.cuda.synchronize()
+        st = _lib.seq_stage_read()
+    finally:
+        _lib.seq_stage_timing(None, 0)
+    assert set(st) == set(_lib.seq_stage_names())
+    for name, (ms, launches, dropped) in st.items():
+        assert launches == 1 and dropped == 0 and 0.0 < ms < 100.0, (name, ms, launches, dropped)
+    step()
+    torch.cuda.synchronize()
+    assert _lib.seq_stage_read() == {}

@@ -71,3 +71,16 @@ def test_cpu_tensors_are_rejected():
     from memory_amd import ops
     with pytest.raises(RuntimeError, match="no CPU fallback"):
         ops.router_topk(torch.randn(2, 10), 3, 1)
+
+
+def test_seq_layer_stage_names(libpath):
+    """The native layer's timed stages carry distinct names, and the stages the benchmark maps to
+    algorithmic work (the attention kernels, the chapter GEMMs) are among them."""
+    names = _lib.seq_stage_names()
+    assert len(names) == len(set(names)) >= 20
+    for n in ("moc_xattn_fwd", "moc_xattn_bwd_dq", "moc_xattn_bwd_dkv", "moc_chapter_project", "moc_chapter_wgrad",
+              "moc_chapter_dx", "moc_rows_linear:q_proj", "moc_rows_linear:o_proj"):
+        assert n in names
+    assert _lib.lib().moc_seq_layer_stage_name(len(names)) is None
+    with pytest.raises(ValueError):
+        _lib.seq_stage_timing(["no_such_stage"], 4)
