@@ -143,12 +143,17 @@ __global__ __launch_bounds__(1024) void plan_small_kernel(const int32_t* __restr
                                                           int32_t* __restrict__ csr_off,
                                                           int32_t* __restrict__ csr_edge) {
   extern __shared__ int32_t lds[];
-  int32_t* cnt = lds;      // [C] counts, then first csr position of each chapter
-  int32_t* uid = lds + C;  // [C] unique index of each present chapter
+  int32_t* cnt = lds;          // [C] counts, then first csr position of each chapter
+  int32_t* uid = lds + C;      // [C] unique index of each present chapter
+  int32_t* fill = lds + 2 * C;  // [C] edges placed so far
   __shared__ int32_t ids[kPlanSmallE];
+  __shared__ int32_t tmp[kPlanSmallE];
   __shared__ int32_t wsum[2][16];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  for (int64_t c = tid; c < C; c += 1024) cnt[c] = 0;
+  for (int64_t c = tid; c < C; c += 1024) {
+    cnt[c] = 0;
+    fill[c] = 0;
+  }
   if (tid < E) ids[tid] = chap[tid];
   __syncthreads();
   if (tid < E) {
@@ -184,15 +189,19 @@ __global__ __launch_bounds__(1024) void plan_small_kernel(const int32_t* __restr
   }
   if (tid == 0) { n_uniq[0] = tot_f; n_uniq[1] = (int32_t)(E - tot_t); csr_off[tot_f] = tot_t; }
   __syncthreads();
-  // stable placement: chapter start + edges of the same chapter earlier in the batch
+  // placement into the chapter's segment in arrival order, then the stable order: an edge's
+  // slot is the segment start plus the number of the segment's edges with a smaller id
+  const int32_t c = tid < E ? ids[tid] : -1;
+  const bool ok = c >= 0 && c < C;
+  if (ok) tmp[cnt[c] + atomicAdd(&fill[c], 1)] = tid;
+  __syncthreads();
   if (tid < E) {
-    const int32_t c = ids[tid];
-    const bool ok = c >= 0 && c < C;
     edge_u[tid] = ok ? uid[c] : -1;
     if (ok) {
+      const int s0 = cnt[c], n = fill[c];
       int before = 0;
-      for (int j = 0; j < tid; ++j) before += ids[j] == c;
-      csr_edge[cnt[c] + before] = tid;
+      for (int j = 0; j < n; ++j) before += tmp[s0 + j] < tid;
+      csr_edge[s0 + before] = tid;
     }
   }
 }
@@ -234,7 +243,7 @@ size_t plan_workspace_bytes(int64_t E, int64_t C) {
 int plan_launch(const int32_t* chap, int64_t E, int64_t C, void* workspace, int32_t* uniq, int32_t* n_uniq,
                 int32_t* edge_u, int32_t* csr_off, int32_t* csr_edge, hipStream_t stream) {
   if (E <= kPlanSmallE && C <= kPlanSmallC) {
-    hipLaunchKernelGGL(plan_small_kernel, dim3(1), dim3(1024), 2 * (size_t)C * sizeof(int32_t), stream, chap, E, C,
+    hipLaunchKernelGGL(plan_small_kernel, dim3(1), dim3(1024), 3 * (size_t)C * sizeof(int32_t), stream, chap, E, C,
                        uniq, n_uniq, edge_u, csr_off, csr_edge);
     return check_launch("plan_small_kernel");
   }

@@ -125,36 +125,14 @@ __device__ __forceinline__ void prepend_row_bwd(const float* w, const float* dom
   for (int j = S + lane; j < NS; j += 64) dw[j - S] = scale * (domega[j] / D - corr);
 }
 
-// One workgroup per row of logits; the row is read from HBM once into LDS.
-// With idx_star / omega (non-null, S > 0) the kernel also writes the shared-chapter prepend of
-// its row (prepend_kernel's values, summed in the same order), so the sequence router's chain
-// top-k -> prepend is one launch.
+// Exact k-th largest key among c in [S, C) by an 8-bit radix select over the order-preserving
+// keys, then the keys above it and the lowest-id ties at it, into sel_key / sel_idx (any order).
+// The top-k kernel's path for rows whose boundary value bin holds too many logits.
 template <int NT>
-__global__ __launch_bounds__(NT) void router_topk_kernel(
-    const float* __restrict__ logits, int64_t C, int S, int k,
-    int32_t* __restrict__ idx_out, float* __restrict__ w_out, float* __restrict__ probs_out,
-    float scale, int32_t* __restrict__ idx_star, float* __restrict__ omega) {
-  extern __shared__ float zs[];  // the row, C floats
-  __shared__ float red[NT / 64];
+__device__ void radix_select(const float* zs, int64_t C, int S, int k, uint32_t* sel_key, int32_t* sel_idx,
+                             int* s_state, int* wave_cnt) {
   __shared__ int hist[256];
-  __shared__ uint32_t sel_key[kMaxTopK];
-  __shared__ int32_t sel_idx[kMaxTopK];
-  __shared__ float sorted_w[kMaxTopK];
-  __shared__ int32_t sorted_i[kMaxTopK];
-  __shared__ int s_state[5];  // chosen bin, remaining, n collected, running eq, ties at threshold
-  __shared__ int wave_cnt[NT / 64];
-
-  const int64_t r = blockIdx.x;
   const int tid = threadIdx.x;
-  load_row<NT>(logits + r * C, C, zs);
-  const RowStats st = row_stats<NT>(zs, C, S, red);
-  const float denom = fmaxf(st.msum, 1e-12f);
-
-  if (probs_out) {
-    for (int64_t c = tid; c < C; c += NT) probs_out[r * C + c] = __expf(zs[c] - st.mx) / st.Z;
-  }
-
-  // ---- radix select: exact k-th largest key among c in [S, C)
   uint32_t prefix = 0, mask = 0;
   int remaining = k;
   for (int shift = 24; shift >= 0; shift -= 8) {
@@ -195,6 +173,7 @@ __global__ __launch_bounds__(NT) void router_topk_kernel(
   const int n_gt = k - remaining;
   // after the last pass every key of the chosen bin equals thr
   const bool all_ties = s_state[4] == remaining;
+  __syncthreads();
   if (tid == 0) { s_state[2] = 0; s_state[3] = 0; }
   __syncthreads();
   // ---- collect keys above the threshold (and every tie when all of them are taken);
@@ -234,28 +213,226 @@ __global__ __launch_bounds__(NT) void router_topk_kernel(
       if (s_state[3] >= remaining) break;
     }
   }
+}
+
+// Ranks of n keys (key descending, chapter id ascending): G lanes of one wave (G a power of two,
+// as many as NT threads allow up to 64) share one element's count over j, then emit(i, rank,
+// key, id) runs on the group's first lane.
+template <int NT, typename Emit>
+__device__ __forceinline__ void rank_keys(const uint32_t* key, const int32_t* id, int n, Emit emit) {
+  int G = 64;
+  while (G > 1 && G * n > NT) G >>= 1;
+  const int tid = threadIdx.x, part = tid & (G - 1);
+  for (int i0 = 0; i0 < n; i0 += NT / G) {
+    const int i = i0 + tid / G;  // the same for the G lanes of a group
+    int rank = 0;
+    uint32_t ki = 0;
+    int32_t ii = 0;
+    if (i < n) {
+      ki = key[i];
+      ii = id[i];
+      for (int j = part; j < n; j += G) {
+        const uint32_t kj = key[j];
+        rank += (kj > ki) || (kj == ki && id[j] < ii);
+      }
+    }
+    for (int o = 1; o < G; o <<= 1) rank += __shfl_xor(rank, o, 64);
+    if (i < n && part == 0) emit(i, rank, ki, ii);
+  }
+}
+
+// Selection by value bins: the selectable logits (c >= S) span [lo, hi]; bin(z) =
+// min(kTopkBins - 1, (z - lo) * kTopkBins / (hi - lo)) is non-decreasing in z, so every logit
+// in a bin above the bin holding the k-th largest is selected and only that boundary bin's
+// logits (a handful for any spread of values) are ranked exactly.
+constexpr int kTopkBins = 2048;
+constexpr int kTopkCand = 512;  // boundary-bin logits ranked directly; more go to the radix path
+
+__device__ __forceinline__ int topk_bin(float z, float lo, float inv) {
+  return min(kTopkBins - 1, (int)((z - lo) * inv));
+}
+
+// One workgroup per row of logits; the row is read from HBM once into LDS.
+// With idx_star / omega (non-null, S > 0) the kernel also writes the shared-chapter prepend of
+// its row (prepend_kernel's values, summed in the same order), so the sequence router's chain
+// top-k -> prepend is one launch.
+template <int NT>
+__global__ __launch_bounds__(NT) void router_topk_kernel(
+    const float* __restrict__ logits, int64_t C, int S, int k,
+    int32_t* __restrict__ idx_out, float* __restrict__ w_out, float* __restrict__ probs_out,
+    float scale, int32_t* __restrict__ idx_star, float* __restrict__ omega) {
+  static_assert(kTopkBins % NT == 0, "bins per thread");
+  constexpr int BPT = kTopkBins / NT;
+  constexpr int NW = NT / 64;
+  extern __shared__ float zs[];  // the row, C floats
+  __shared__ float red[3][NW];
+  __shared__ int hist[kTopkBins];
+  __shared__ int wsum[NW];
+  __shared__ uint32_t sel_key[kMaxTopK];
+  __shared__ int32_t sel_idx[kMaxTopK];
+  __shared__ float sorted_w[kMaxTopK];
+  __shared__ int32_t sorted_i[kMaxTopK];
+  __shared__ uint32_t cand_key[kTopkCand];
+  __shared__ int32_t cand_idx[kTopkCand];
+  // boundary bin, remaining, logits in it, selected appended, candidates appended, running eq,
+  // ties at threshold (radix path)
+  __shared__ int s_state[8];
+  __shared__ int wave_cnt[NW];
+
+  const int64_t r = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  load_row<NT>(logits + r * C, C, zs);
+
+  // ---- max of the row (softmax) and the selectable range [lo, hi]; the histogram is cleared
+  // before the reduction's barriers
+#pragma unroll
+  for (int i = 0; i < BPT; ++i) hist[tid * BPT + i] = 0;
+  if (tid < 8) s_state[tid] = 0;
+  float mxa = -INFINITY, hi = -INFINITY, lo = INFINITY;
+  for (int64_t c = tid; c < C; c += NT) {
+    const float z = zs[c];
+    mxa = fmaxf(mxa, z);
+    if (c >= S) {
+      hi = fmaxf(hi, z);
+      lo = fminf(lo, z);
+    }
+  }
+  mxa = wave_max(mxa);
+  hi = wave_max(hi);
+  lo = -wave_max(-lo);
+  if (lane == 0) {
+    red[0][wv] = mxa;
+    red[1][wv] = hi;
+    red[2][wv] = lo;
+  }
+  __syncthreads();
+  mxa = red[0][0], hi = red[1][0], lo = red[2][0];
+#pragma unroll
+  for (int i = 1; i < NW; ++i) {
+    mxa = fmaxf(mxa, red[0][i]);
+    hi = fmaxf(hi, red[1][i]);
+    lo = fminf(lo, red[2][i]);
+  }
+  const float inv = (float)kTopkBins / (hi - lo);
+  const bool binned = hi > lo && inv > 0.f && inv < INFINITY;
+  __syncthreads();  // red is reused below
+
+  // ---- softmax sums (all chapters; the selectable ones) and the histogram of the selectable
+  float s_all = 0.f, s_sel = 0.f;
+  for (int64_t c = tid; c < C; c += NT) {
+    const float z = zs[c];
+    const float e = __expf(z - mxa);
+    s_all += e;
+    if (c >= S) {
+      s_sel += e;
+      if (binned) atomicAdd(&hist[topk_bin(z, lo, inv)], 1);
+    }
+  }
+  s_all = wave_sum(s_all);
+  s_sel = wave_sum(s_sel);
+  if (lane == 0) {
+    red[0][wv] = s_all;
+    red[1][wv] = s_sel;
+  }
+  __syncthreads();
+  float Z = 0.f, Zs = 0.f;
+#pragma unroll
+  for (int i = 0; i < NW; ++i) {
+    Z += red[0][i];
+    Zs += red[1][i];
+  }
+  // masked probability mass over c >= S (router.py:126-129 renormalisation)
+  const RowStats st{mxa, Z, S > 0 ? Zs / Z : 1.f};
+  const float denom = fmaxf(st.msum, 1e-12f);
+
+  if (probs_out) {
+    for (int64_t c = tid; c < C; c += NT) probs_out[r * C + c] = __expf(zs[c] - st.mx) / st.Z;
+  }
+
+  bool exact = false;  // sel_key / sel_idx hold the k selected (any order)
+  if (!binned && hi == lo) {
+    // every selectable logit is equal: the k lowest chapter ids
+    for (int i = tid; i < k; i += NT) {
+      sel_key[i] = fkey(hi);
+      sel_idx[i] = S + i;
+    }
+    exact = true;
+  } else if (binned) {
+    // boundary bin: suffix sums over bins from the top; thread tid owns bins tid*BPT .. +BPT-1
+    int cnt[BPT];
+    int mine = 0;
+#pragma unroll
+    for (int i = 0; i < BPT; ++i) {
+      cnt[i] = hist[tid * BPT + i];
+      mine += cnt[i];
+    }
+    // inclusive suffix sum over the wave's lanes >= lane, then over the waves above
+    int incl = mine;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int t = __shfl_down(incl, o, 64);
+      if (lane + o < 64) incl += t;
+    }
+    if (lane == 0) wsum[wv] = incl;
+    __syncthreads();
+    int above = incl - mine;  // bins of higher threads
+    for (int i = wv + 1; i < NW; ++i) above += wsum[i];
+#pragma unroll
+    for (int i = BPT - 1; i >= 0; --i) {
+      if (above < k && above + cnt[i] >= k) {
+        s_state[0] = tid * BPT + i;
+        s_state[1] = k - above;
+        s_state[2] = cnt[i];
+      }
+      above += cnt[i];
+    }
+    __syncthreads();
+    const int bstar = s_state[0], remaining = s_state[1], nb = s_state[2];
+    const int n_above = k - remaining;
+    if (nb <= kTopkCand) {
+      // collect: bins above the boundary are selected, the boundary bin's logits are candidates
+      for (int64_t c = S + tid; c < C; c += NT) {
+        const float z = zs[c];
+        const int b = topk_bin(z, lo, inv);
+        if (b > bstar) {
+          const int p = atomicAdd(&s_state[3], 1);
+          sel_key[p] = fkey(z);
+          sel_idx[p] = (int32_t)c;
+        } else if (b == bstar) {
+          const int p = atomicAdd(&s_state[4], 1);
+          cand_key[p] = fkey(z);
+          cand_idx[p] = (int32_t)c;
+        }
+      }
+      __syncthreads();
+      // the `remaining` best candidates (key descending, chapter id ascending)
+      rank_keys<NT>(cand_key, cand_idx, nb, [&](int, int rank, uint32_t ki, int32_t ii) {
+        if (rank < remaining) {
+          sel_key[n_above + rank] = ki;
+          sel_idx[n_above + rank] = ii;
+        }
+      });
+      exact = true;
+    }
+  }
+  if (!exact) {
+    radix_select<NT>(zs, C, S, k, sel_key, sel_idx, s_state, wave_cnt);
+  }
   __syncthreads();
   // ---- rank sort (key desc, index asc) of the selected chapters with their probabilities;
   // the slots above were filled in atomic order, so everything after this works in rank order
   // (the sum below is then formed the same way on every run)
-  for (int i = tid; i < k; i += NT) {
-    const uint32_t ki = sel_key[i];
-    const int32_t ii = sel_idx[i];
-    int rank = 0;
-    for (int j = 0; j < k; ++j) {
-      const uint32_t kj = sel_key[j];
-      rank += (kj > ki) || (kj == ki && sel_idx[j] < ii);
-    }
+  rank_keys<NT>(sel_key, sel_idx, k, [&](int, int rank, uint32_t, int32_t ii) {
     float p = __expf(zs[ii] - st.mx) / st.Z;
     if (S > 0) p = p / denom;
     sorted_w[rank] = p;
     sorted_i[rank] = ii;
-  }
+  });
   __syncthreads();
   // ---- renormalise
   float part = 0.f;
   for (int i = tid; i < k; i += NT) part += sorted_w[i];
-  const float W = fmaxf(block_reduce_sum<NT>(part, red), 1e-12f);
+  const float W = fmaxf(block_reduce_sum<NT>(part, red[2]), 1e-12f);
   for (int i = tid; i < k; i += NT) {
     const float v = sorted_w[i] / W;
     idx_out[r * k + i] = sorted_i[i];

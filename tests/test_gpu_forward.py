@@ -50,6 +50,31 @@ def test_router_topk_ties_lower_index_first(dev):
     assert_rel(w.cpu(), rw, 1e-5, "tie weights")
 
 
+@pytest.mark.parametrize("R", [2, 70])   # 1024- and 256-thread workgroups
+@pytest.mark.parametrize("pattern", ["all_equal", "plateau", "plateau_low", "two_values"])
+def test_router_topk_degenerate_rows(dev, R, pattern):
+    """Rows the value-bin selection does not resolve by itself: every selectable logit equal
+    (the k lowest ids), and a plateau of thousands of equal logits at the boundary (more than
+    the boundary bin's direct ranking takes: the radix path), with ties to the lower id."""
+    C, S, k = 4097, 1, 64
+    g = gen(31)
+    z = torch.zeros(R, C)
+    if pattern == "plateau":          # 20 larger logits, one smaller, ~4,000 tied at the boundary
+        z[:, torch.randperm(C, generator=g)[:20]] = 1.0
+        z[:, 7] = -1.0
+    elif pattern == "plateau_low":    # the plateau is the top: ties decide every slot
+        z[:, torch.randperm(C, generator=g)[:30]] = -2.0
+    elif pattern == "two_values":     # half the row at each of two values, k inside the upper half
+        z[:, ::2] = 0.5
+    z[:, 0] = 3.0                     # the shared prefix is excluded whatever its value
+    print(f"router_topk degenerate R={R} pattern={pattern}", flush=True)
+    idx, w = _ops().router_topk(z.to(dev), k, S)
+    ri = O.topk_desc_numpy(np.where(np.arange(C)[None, :] < S, -np.inf, z.numpy()), k)
+    assert np.array_equal(idx.cpu().numpy(), ri)
+    _, rw, _ = O.route_sequence(z, k, S)
+    assert_rel(w.cpu(), rw, 1e-5, "weights")
+
+
 @pytest.mark.parametrize("R,C,S,k", [(4, 97, 1, 8), (80, 130, 2, 5), (3, 4097, 1, 64)])
 def test_router_topk_backward_matches_autograd(dev, R, C, S, k):
     print(f"router_topk_bwd R={R} C={C} S={S} k={k}", flush=True)
