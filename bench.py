@@ -764,8 +764,10 @@ def run_c3block(args):
     backward.  Variants:
       reference_style - the reference's RMSNorm module as torch ops (memory_block.py:26-28), then
                         o_proj and a separate residual add;
-      fused           - MemorySublayer: the norm as one HIP row kernel writing bf16, the residual as
-                        the o_proj GEMM's accumulator input (the value of this line)."""
+      norm_kernel     - MemorySublayer with the norm as one HIP row kernel writing bf16 ahead of the
+                        q projection, the residual as the o_proj GEMM's accumulator input;
+      fused           - MemorySublayer with the norm folded into the q projection's GEMM
+                        (ops.norm_linear) and the residual as above (the value of this line)."""
     import torch
     from memory_amd import ops
     from memory_amd.memory_block import MemorySublayer
@@ -797,20 +799,24 @@ def run_c3block(args):
         out = h + ops.linear(pre, layer.memory_attn.o_proj.weight)
         out.backward(dout)
 
-    def step_fused():
-        h.grad = bank.grad = norm_w.grad = None
-        for p in layer.parameters():
-            p.grad = None
-        out = sub(h, routed_memory_state=state(h))
-        out.backward(dout)
+    def step_sub(fuse):
+        def step():
+            h.grad = bank.grad = norm_w.grad = None
+            for p in layer.parameters():
+                p.grad = None
+            sub.fuse_norm = fuse
+            out = sub(h, routed_memory_state=state(h))
+            out.backward(dout)
+        return step
 
     res = {}
-    for kind, fn in (("reference_style", step_ref), ("fused", step_fused)):
+    for kind, fn in (("reference_style", step_ref), ("norm_kernel", step_sub(False)), ("fused", step_sub(True))):
         ms, per, _, _ = timed(fn, args.steps, args.warmup)
         res[kind] = {"ms_per_step": round(ms, 4),
                      "kernels": {n: {"avg_ms": round(v["avg_ms"], 4), "calls": v["calls_per_step"]}
                                  for n, v in sorted(per.items(), key=lambda kv: -kv[1]["ms_per_step"])
-                                 if n in ("moc_row_norm_fwd", "moc_row_norm_bwd")}}
+                                 if n in ("moc_row_norm_fwd", "moc_row_norm_bwd", "moc_rows_linear_norm",
+                                          "moc_norm_fold_weight")}}
     ms = res["fused"]["ms_per_step"]
     return {
         "metric": "memory sublayer fwd+bwd tokens/s incl. memory_layernorm + residual (L=1024,d=768,k=64,T=64)",

@@ -209,6 +209,21 @@ int moc_chapter_dx(const void* dkv_edge, int64_t ld, const int32_t* uniq, const 
  * transposed weight).  N % 256 == 0, K % 64 == 0. */
 int moc_rows_linear(const void* x, int64_t ldx, int64_t R, const void* w, int N, int K, void* y, int64_t ldy,
                     hipStream_t stream);
+/* The memory sublayer's memory_layernorm folded into its q projection (memory_block.py:549-558:
+ * q_proj(memory_layernorm(hidden)); RMSNorm memory_block.py:18-28 or nn.LayerNorm): y = norm(x) W^T
+ * for x [R, K] bf16 (row stride ldx) without writing the normalised rows.  moc_norm_fold_weight
+ * takes W [N, K] bf16, gamma f32 [K] and (LayerNorm) beta f32 [K] or NULL and writes
+ * w_out = W diag(gamma) bf16 [N, K], u f32 [N] = row sums of w_out and v f32 [N] = W beta (u and v
+ * for LayerNorm only; NULL for RMSNorm; beta NULL = no bias, v = 0).  moc_rows_linear_norm (norm
+ * MOC_NORM_RMS or MOC_NORM_LAYERNORM) then computes y [R, N] bf16 = rstd (x w_out^T) (RMSNorm) or
+ * rstd (x w_out^T - mean u) + v (LayerNorm), the row statistics over the K columns of x (fp32
+ * sums; rstd = 1 / sqrt(mean(x^2) or var + eps)) taken inside the GEMM and written to rstd_out /
+ * mean_out [R] f32 when non-NULL (what moc_row_norm_bwd reads).  N a multiple of 256, K of 64. */
+int moc_norm_fold_weight(const void* w, int N, int K, const float* gamma, const float* beta, void* w_out, float* u,
+                         float* v, hipStream_t stream);
+int moc_rows_linear_norm(const void* x, int64_t ldx, int64_t R, const void* w_folded, int N, int K, int norm,
+                         float eps, const float* u, const float* v, void* y, int64_t ldy, float* mean_out,
+                         float* rstd_out, hipStream_t stream);
 /* Sums of the per-edge dK|dV rows of the chapters selected by more than one edge (csr order,
  * fp32 accumulation, rounded to bf16): red [max_u*64][ld] (rows of other chapters untouched).
  * Feeds moc_chapter_dx and moc_chapter_wgrad, which read a single-edge chapter's rows in place

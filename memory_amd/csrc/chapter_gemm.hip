@@ -109,12 +109,29 @@ __device__ __forceinline__ void cg_wait_vm(int n) {
   else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
-template <int SRC, int DST, typename TO, int BM, int DEPTH>
+// Row normalisation folded into the rows GEMM (NORM = MOC_NORM_RMS or MOC_NORM_LAYERNORM): y =
+// norm(x) W^T with W already scaled by the norm weight (moc_norm_fold_weight) is
+// rstd (x W~^T) for RMSNorm and rstd (x W~^T - mean u) + v for LayerNorm (u = W~ 1, v = W beta),
+// so the GEMM reads the raw rows; each row's sums of x and x^2 are taken from the X tiles the
+// stages bring into LDS anyway (4 threads per row, 16 columns each, by bf16 dot2) and applied
+// in the epilogue.
+struct CgNorm {
+  float eps;
+  const float* u;   // LayerNorm: [N]
+  const float* v;   // LayerNorm: [N]
+  float* mean_out;  // LayerNorm: [rows] or null
+  float* rstd_out;  // [rows] or null
+};
+
+template <int SRC, int DST, typename TO, int BM, int DEPTH, int NORM = MOC_NORM_NONE>
 __global__ __launch_bounds__(kCgThreads) void chapter_gemm_kernel(
     const bf16* __restrict__ x, const bf16* __restrict__ xred, int64_t ldx, const int32_t* __restrict__ uniq,
     const int32_t* __restrict__ n_uniq, const int32_t* __restrict__ csr_off, const int32_t* __restrict__ csr_edge,
     int64_t max_u, const bf16* __restrict__ w, int N, int K, TO* __restrict__ y, int64_t ldy, int64_t xrows,
-    int64_t yrows) {
+    int64_t yrows, CgNorm nrm = CgNorm{}) {
+  static_assert(NORM == MOC_NORM_NONE || (SRC == CG_SRC_CONTIG && DST == CG_DST_CONTIG && BM == 128 &&
+                                          sizeof(TO) == 2),
+                "row normalisation: contiguous rows, 128-row tiles, bf16 output");
   constexpr int CPT = BM / 64;              // chapters per tile
   constexpr int IPX = BM / 64;              // X DMA instructions per thread per stage
   constexpr int JB = BM / 32;               // 16-row MFMA tiles per wave
@@ -186,6 +203,54 @@ __global__ __launch_bounds__(kCgThreads) void chapter_gemm_kernel(
 #pragma unroll
     for (int j = 0; j < JB; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+  // row statistics (NORM): thread t sums columns 16 (t % 4) .. +15 of tile row t / 4 of each
+  // X stage; the four partial sums of a row are combined at the tile's end into sStat
+  __shared__ float2 sStat[NORM != MOC_NORM_NONE ? BM : 1];
+  float st_x = 0.f, st_xx = 0.f;
+  const int st_row = tid >> 2, st_part = tid & 3;
+  auto stats_stage = [&](const char* sx) {
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int pc = (2 * st_part + h) ^ (st_row & 7);
+      const bf16x8_t v8 = *reinterpret_cast<const bf16x8_t*>(sx + st_row * 128 + (pc << 4));
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const bf16x2_t p2 = bf16x2_t{v8[2 * e], v8[2 * e + 1]};
+        st_xx = __builtin_amdgcn_fdot2_f32_bf16(p2, p2, st_xx, false);
+        if constexpr (NORM == MOC_NORM_LAYERNORM)
+          st_x = __builtin_amdgcn_fdot2_f32_bf16(p2, bf16x2_t{(__bf16)1.f, (__bf16)1.f}, st_x, false);
+      }
+    }
+  };
+  // at a tile's last stage: per-row (mean, rstd) into sStat (and, for the tile's first feature
+  // block, to mean_out / rstd_out); every wave then reads its rows' statistics in the epilogue
+  auto stats_finish = [&](int t) {
+    st_xx += __shfl_xor(st_xx, 1, 64);
+    st_xx += __shfl_xor(st_xx, 2, 64);
+    if constexpr (NORM == MOC_NORM_LAYERNORM) {
+      st_x += __shfl_xor(st_x, 1, 64);
+      st_x += __shfl_xor(st_x, 2, 64);
+    }
+    if (st_part == 0) {
+      const float inv_k = 1.f / (float)K;
+      const float mean = NORM == MOC_NORM_LAYERNORM ? st_x * inv_k : 0.f;
+      const float var = NORM == MOC_NORM_LAYERNORM ? fmaxf(st_xx * inv_k - mean * mean, 0.f) : st_xx * inv_k;
+      const float rstd = rsqrtf(var + nrm.eps);
+      sStat[st_row] = float2{mean, rstd};
+      const int rb = t / NB, nb = t - rb * NB;
+      const int64_t row = (int64_t)rb * BM + st_row;
+      if (nb == 0 && row < yrows) {
+        if (nrm.rstd_out) nrm.rstd_out[row] = rstd;
+        if (NORM == MOC_NORM_LAYERNORM && nrm.mean_out) nrm.mean_out[row] = mean;
+      }
+    }
+    st_x = 0.f;
+    st_xx = 0.f;
+    __syncthreads();
+  };
+
   auto compute = [&](const char* sw, const char* sx) {
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
@@ -227,10 +292,33 @@ __global__ __launch_bounds__(kCgThreads) void chapter_gemm_kernel(
         typedef int i32x4 __attribute__((ext_vector_type(4)));
         if constexpr (sizeof(TO) == 2) {
           bf16x8 v;
+          if constexpr (NORM != MOC_NORM_NONE) {
+            // features nb*256 + 64 wf + 32 p + 8 g + e (acc[2p]) and + 4 + e (acc[2p+1])
+            const float2 sr = sStat[rt + m];
+            if constexpr (NORM == MOC_NORM_LAYERNORM) {
+              const int f0 = nb * 256 + 64 * wf + 32 * p + 8 * g;
+              const f32x4 u0 = *reinterpret_cast<const f32x4*>(nrm.u + f0);
+              const f32x4 u1 = *reinterpret_cast<const f32x4*>(nrm.u + f0 + 4);
+              const f32x4 v0 = *reinterpret_cast<const f32x4*>(nrm.v + f0);
+              const f32x4 v1 = *reinterpret_cast<const f32x4*>(nrm.v + f0 + 4);
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            v[e] = (bf16)acc[2 * p][j][e];
-            v[4 + e] = (bf16)acc[2 * p + 1][j][e];
+              for (int e = 0; e < 4; ++e) {
+                v[e] = (bf16)(sr.y * (acc[2 * p][j][e] - sr.x * u0[e]) + v0[e]);
+                v[4 + e] = (bf16)(sr.y * (acc[2 * p + 1][j][e] - sr.x * u1[e]) + v1[e]);
+              }
+            } else {
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                v[e] = (bf16)(sr.y * acc[2 * p][j][e]);
+                v[4 + e] = (bf16)(sr.y * acc[2 * p + 1][j][e]);
+              }
+            }
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              v[e] = (bf16)acc[2 * p][j][e];
+              v[4 + e] = (bf16)acc[2 * p + 1][j][e];
+            }
           }
           __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, v), yres, vrow + 64 * p, 0, 0);
         } else {
@@ -270,8 +358,10 @@ __global__ __launch_bounds__(kCgThreads) void chapter_gemm_kernel(
     }
     __builtin_amdgcn_sched_barrier(0);
     compute(sW + (s % NBUF) * kCgStageW, sX + (s % NBUF) * STX);
+    if constexpr (NORM != MOC_NORM_NONE) stats_stage(sX + (s % NBUF) * STX);
     stored = kt + 1 == nk;
     if (stored) {
+      if constexpr (NORM != MOC_NORM_NONE) stats_finish(t);
       epilogue(t);
       t += nslot;
       kt = 0;
@@ -512,6 +602,46 @@ __global__ __launch_bounds__(256) void cg_wgrad_reduce_kernel(const float* __res
   for (int e = 0; e < 4; ++e) dw[(int64_t)(n + e) * K + k] = from_f<TO>(s[e]);
 }
 
+// W~ = W diag(gamma) (bf16, rounded once), u[n] = sum_k W~[n][k] (over the rounded values the GEMM
+// multiplies), v[n] = sum_k W[n][k] beta[k]; one wave per output row, lane-strided sums reduced
+// in a fixed order
+__global__ __launch_bounds__(256) void norm_fold_kernel(const bf16* __restrict__ w, int N, int K,
+                                                        const float* __restrict__ gamma,
+                                                        const float* __restrict__ beta, bf16* __restrict__ w_out,
+                                                        float* __restrict__ u, float* __restrict__ v) {
+  const int n = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (n >= N) return;
+  const bf16* wr = w + (int64_t)n * K;
+  bf16* wo = w_out + (int64_t)n * K;
+  float su = 0.f, sv = 0.f;
+  for (int k0 = 8 * lane; k0 < K; k0 += 512) {
+    const bf16x8 a = *reinterpret_cast<const bf16x8*>(wr + k0);
+    const f32x4 g0 = *reinterpret_cast<const f32x4*>(gamma + k0), g1 = *reinterpret_cast<const f32x4*>(gamma + k0 + 4);
+    f32x4 b0 = f32x4{0.f, 0.f, 0.f, 0.f}, b1 = b0;
+    if (beta) {
+      b0 = *reinterpret_cast<const f32x4*>(beta + k0);
+      b1 = *reinterpret_cast<const f32x4*>(beta + k0 + 4);
+    }
+    bf16x8 o;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float wf = (float)a[e];
+      o[e] = (bf16)(wf * (e < 4 ? g0[e] : g1[e - 4]));
+      su += (float)o[e];
+      sv += wf * (e < 4 ? b0[e] : b1[e - 4]);
+    }
+    *reinterpret_cast<bf16x8*>(wo + k0) = o;
+  }
+  if (u) {
+    su = wave_sum(su);
+    sv = wave_sum(sv);
+    if (lane == 0) {
+      u[n] = su;
+      if (v) v[n] = sv;
+    }
+  }
+}
+
 int cg_grid() {
   static int cus = 0;
   if (cus == 0) {
@@ -593,11 +723,11 @@ int moc_chapter_project(const void* rows, int64_t ld, int gather, const int32_t*
   if (gather)
     hipLaunchKernelGGL((chapter_gemm_kernel<CG_SRC_GATHER, CG_DST_CONTIG, bf16, 256, kCgDepth256>), grid, dim3(kCgThreads), 0,
                        stream, (const bf16*)rows, nullptr, ld, uniq, n_uniq, nullptr, nullptr, max_u, (const bf16*)w,
-                       N, K, (bf16*)y, ldy, max_u * 64, max_u * 64);
+                       N, K, (bf16*)y, ldy, max_u * 64, max_u * 64, CgNorm{});
   else
     hipLaunchKernelGGL((chapter_gemm_kernel<CG_SRC_CONTIG, CG_DST_CONTIG, bf16, 256, kCgDepth256>), grid, dim3(kCgThreads), 0,
                        stream, (const bf16*)rows, nullptr, ld, uniq, n_uniq, nullptr, nullptr, max_u, (const bf16*)w,
-                       N, K, (bf16*)y, ldy, max_u * 64, max_u * 64);
+                       N, K, (bf16*)y, ldy, max_u * 64, max_u * 64, CgNorm{});
   return check_launch("chapter_gemm_kernel(project)");
 }
 
@@ -615,7 +745,7 @@ int moc_chapter_dx(const void* dkv_edge, int64_t ld, const int32_t* uniq, const 
 #define MOC_CGDX(DST, TO)                                                                                           \
   hipLaunchKernelGGL((chapter_gemm_kernel<CG_SRC_EDGE, DST, TO, kCgDxRows, kCgDepth128>), grid, dim3(kCgThreads), 0, stream,          \
                      (const bf16*)dkv_edge, (const bf16*)red, ld, uniq, n_uniq, csr_off, csr_edge, max_u,           \
-                     (const bf16*)w_t, N, K, (TO*)out, ldo, max_u * 64, max_u * 64)
+                     (const bf16*)w_t, N, K, (TO*)out, ldo, max_u * 64, max_u * 64, CgNorm{})
   if (out_bank_rows) {
     if (out_dtype == MOC_BF16) MOC_CGDX(CG_DST_BANK, bf16); else MOC_CGDX(CG_DST_BANK, float);
   } else {
@@ -634,8 +764,47 @@ int moc_rows_linear(const void* x, int64_t ldx, int64_t R, const void* w, int N,
   if (R == 0) return MOC_OK;
   hipLaunchKernelGGL((chapter_gemm_kernel<CG_SRC_CONTIG, CG_DST_CONTIG, bf16, 128, kCgDepth128>), dim3((unsigned)cg_grid()),
                      dim3(kCgThreads), 0, stream, (const bf16*)x, nullptr, ldx, nullptr, nullptr, nullptr, nullptr,
-                     blocks, (const bf16*)w, N, K, (bf16*)y, ldy, R, R);
+                     blocks, (const bf16*)w, N, K, (bf16*)y, ldy, R, R, CgNorm{});
   return check_launch("chapter_gemm_kernel(rows)");
+}
+
+int moc_norm_fold_weight(const void* w, int N, int K, const float* gamma, const float* beta, void* w_out, float* u,
+                         float* v, hipStream_t stream) {
+  MOC_REQUIRE(w && gamma && w_out, MOC_ERR_ARG, "moc_norm_fold_weight: null pointer");
+  MOC_REQUIRE(N > 0 && K > 0 && K % 8 == 0, MOC_ERR_ARG, "moc_norm_fold_weight: N=%d K=%d (K a multiple of 8)", N, K);
+  MOC_REQUIRE(((uintptr_t)w & 15) == 0 && ((uintptr_t)w_out & 15) == 0 && ((uintptr_t)gamma & 15) == 0 &&
+                  ((uintptr_t)beta & 15) == 0,
+              MOC_ERR_ARG, "moc_norm_fold_weight: w, w_out, gamma and beta must be 16-byte aligned");
+  MOC_REQUIRE(!beta || (u && v), MOC_ERR_ARG, "moc_norm_fold_weight: a bias needs u and v");
+  MOC_REQUIRE(!v || u, MOC_ERR_ARG, "moc_norm_fold_weight: v needs u");
+  hipLaunchKernelGGL(norm_fold_kernel, dim3((unsigned)((N + 3) / 4)), dim3(256), 0, stream, (const bf16*)w, N, K,
+                     gamma, beta, (bf16*)w_out, u, v);
+  return check_launch("norm_fold_kernel");
+}
+
+int moc_rows_linear_norm(const void* x, int64_t ldx, int64_t R, const void* w_folded, int N, int K, int norm,
+                         float eps, const float* u, const float* v, void* y, int64_t ldy, float* mean_out,
+                         float* rstd_out, hipStream_t stream) {
+  MOC_REQUIRE(x && w_folded && y, MOC_ERR_ARG, "moc_rows_linear_norm: null pointer");
+  MOC_REQUIRE(norm == MOC_NORM_RMS || norm == MOC_NORM_LAYERNORM, MOC_ERR_ARG, "moc_rows_linear_norm: norm %d",
+              norm);
+  MOC_REQUIRE(norm == MOC_NORM_RMS || (u && v && ((uintptr_t)u & 15) == 0 && ((uintptr_t)v & 15) == 0), MOC_ERR_ARG,
+              "moc_rows_linear_norm: LayerNorm needs 16-byte aligned u and v");
+  MOC_REQUIRE(R >= 0 && R < ((int64_t)1 << 36) && eps >= 0.f, MOC_ERR_ARG, "moc_rows_linear_norm: R=%lld eps=%g",
+              (long long)R, (double)eps);
+  const int64_t blocks = (R + 63) / 64;
+  if (int rc = cg_check("moc_rows_linear_norm", ldx, N, K, blocks, ldy)) return rc;
+  if (R == 0) return MOC_OK;
+  const CgNorm nrm{eps, u, v, mean_out, rstd_out};
+  if (norm == MOC_NORM_RMS)
+    hipLaunchKernelGGL((chapter_gemm_kernel<CG_SRC_CONTIG, CG_DST_CONTIG, bf16, 128, kCgDepth128, MOC_NORM_RMS>),
+                       dim3((unsigned)cg_grid()), dim3(kCgThreads), 0, stream, (const bf16*)x, nullptr, ldx, nullptr,
+                       nullptr, nullptr, nullptr, blocks, (const bf16*)w_folded, N, K, (bf16*)y, ldy, R, R, nrm);
+  else
+    hipLaunchKernelGGL((chapter_gemm_kernel<CG_SRC_CONTIG, CG_DST_CONTIG, bf16, 128, kCgDepth128, MOC_NORM_LAYERNORM>),
+                       dim3((unsigned)cg_grid()), dim3(kCgThreads), 0, stream, (const bf16*)x, nullptr, ldx, nullptr,
+                       nullptr, nullptr, nullptr, blocks, (const bf16*)w_folded, N, K, (bf16*)y, ldy, R, R, nrm);
+  return check_launch("chapter_gemm_kernel(rows, norm)");
 }
 
 int moc_dkv_multi_reduce(const void* dkv_edge, int64_t ld, const int32_t* n_uniq, int64_t max_u,

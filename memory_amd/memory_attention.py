@@ -79,20 +79,30 @@ class MemoryCrossAttention(nn.Module):
         self.o_proj = nn.Linear(self.hidden_dim, self.hidden_dim, bias=False)
         if wo_init_zero:
             nn.init.zeros_(self.o_proj.weight)
+        self._qnorm = None  # a caller's norm folded into q_proj for the duration of one call
 
     # ------------------------------------------------------------------ helpers
     def _project_output(self, attn_output: torch.Tensor) -> torch.Tensor:
         return ops.linear(attn_output, self.o_proj.weight)
 
-    def _queries(self, hidden_states: torch.Tensor) -> torch.Tensor:
+    def _queries(self, hidden_states: torch.Tensor, qnorm=None) -> torch.Tensor:
+        """q_proj(hidden_states), or q_proj(norm(hidden_states)) as one fused GEMM when the caller
+        hands its memory_layernorm over (``qnorm`` = (weight, bias, eps, "rms" | "layer"))."""
         B, L, _ = hidden_states.shape
-        return ops.linear(hidden_states, self.q_proj.weight).view(B, L, self.num_heads, self.head_dim)
+        qnorm = self._qnorm if qnorm is None else qnorm
+        if qnorm is not None:
+            weight, bias, eps, kind = qnorm
+            q = ops.norm_linear(hidden_states, weight, bias, eps, kind, self.q_proj.weight)
+        else:
+            q = ops.linear(hidden_states, self.q_proj.weight)
+        return q.view(B, L, self.num_heads, self.head_dim)
 
     def _routed(self, hidden_states, bank, idx_star, omega, num_chapters, T, norm_type, eps):
         B, L, _ = hidden_states.shape
+        qnorm = self._qnorm  # captured: a checkpointed recompute runs after the forward returned
 
         def run(h):
-            q = self._queries(h)
+            q = self._queries(h, qnorm)
             a = ops.routed_attention(q, bank, self.k_proj.weight, self.v_proj.weight, omega, idx_star,
                                      num_chapters=num_chapters, tokens_per_chapter=T, norm_type=norm_type, eps=eps,
                                      num_kv_heads=self.num_kv_heads)
@@ -139,8 +149,20 @@ class MemoryCrossAttention(nn.Module):
     def attention_preproj(self, hidden_states: torch.Tensor, memory: Optional[torch.Tensor] = None,
                           token_routing_state: Optional[Dict[str, Any]] = None,
                           token_routing_kernel_version: str = "v2",
-                          routed_memory_state: Optional[Dict[str, Any]] = None) -> torch.Tensor:
-        """forward's attention output before o_proj, (B, L, hidden_dim)."""
+                          routed_memory_state: Optional[Dict[str, Any]] = None,
+                          query_norm=None) -> torch.Tensor:
+        """forward's attention output before o_proj, (B, L, hidden_dim).  ``query_norm`` =
+        (weight, bias, eps, "rms" | "layer"): hidden_states are the un-normalised rows and the norm
+        is applied inside the q projection (only the queries read the normalised rows)."""
+        if query_norm is not None:
+            # the caller's norm, folded into the q projection (MemorySublayer): every path's
+            # _queries picks it up for the duration of this call
+            prev, self._qnorm = self._qnorm, query_norm
+            try:
+                return self.attention_preproj(hidden_states, memory, token_routing_state, token_routing_kernel_version,
+                                              routed_memory_state)
+            finally:
+                self._qnorm = prev
         if token_routing_state is not None:
             return self._forward_token_routed_attention(hidden_states, token_routing_state,
                                                         token_routing_kernel_version)

@@ -54,6 +54,9 @@ class MemorySublayer(nn.Module):
         self.memory_attn = MemoryCrossAttention(hidden_dim, num_heads, num_kv_heads, memory_dim=memory_dim,
                                                 wo_init_zero=wo_init_zero,
                                                 gradient_checkpointing=gradient_checkpointing)
+        # memory_layernorm folded into the q projection's GEMM where the shapes allow it
+        # (ops.norm_linear_supported); False runs the norm kernel ahead of the projection
+        self.fuse_norm = True
 
     def forward(self, hidden_states: torch.Tensor, memory: Optional[torch.Tensor] = None,
                 token_routing_state: Optional[Dict[str, Any]] = None, token_routing_kernel_version: str = "v2",
@@ -63,10 +66,14 @@ class MemorySublayer(nn.Module):
         if cdt not in (torch.float32, torch.bfloat16):
             raise ValueError(f"memory projections in {cdt}: the HIP kernels take float32 or bfloat16")
         ln = self.memory_layernorm
-        if self.use_rms_norm:
-            x = ops.row_norm(hidden_states, ln.weight, None, ln.eps, "rms", cdt)
+        kind = "rms" if self.use_rms_norm else "layer"
+        bias = None if self.use_rms_norm else ln.bias
+        if self.fuse_norm and ops.norm_linear_supported(hidden_states, attn.q_proj.weight):
+            # only the q projection reads the normalised rows: the norm runs inside its GEMM
+            pre = attn.attention_preproj(hidden_states, memory, token_routing_state, token_routing_kernel_version,
+                                         routed_memory_state, query_norm=(ln.weight, bias, ln.eps, kind))
         else:
-            x = ops.row_norm(hidden_states, ln.weight, ln.bias, ln.eps, "layer", cdt)
-        pre = attn.attention_preproj(x, memory, token_routing_state, token_routing_kernel_version,
-                                     routed_memory_state)
+            x = ops.row_norm(hidden_states, ln.weight, bias, ln.eps, kind, cdt)
+            pre = attn.attention_preproj(x, memory, token_routing_state, token_routing_kernel_version,
+                                         routed_memory_state)
         return ops.linear_residual(pre, attn.o_proj.weight, hidden_states)

@@ -471,6 +471,90 @@ def row_norm(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor]
     return _RowNorm.apply(x, weight, bias, code, float(eps), od)
 
 
+class _NormLinear(torch.autograd.Function):
+    """q_proj(memory_layernorm(x)) of the memory sublayer (memory_block.py:549-558 with
+    memory_attention.py:241) as one GEMM: the norm weight folded into the projection weight
+    (``moc_norm_fold_weight``) and the row statistics taken inside the GEMM
+    (``moc_rows_linear_norm``), so the normalised rows are never written in the forward.
+    Backward: d(normalised rows) = dy W on the chapter GEMM, the norm's backward
+    (``moc_row_norm_bwd``) from x and the statistics the GEMM wrote, and dW = dy^T norm(x) with
+    the normalised rows recomputed here (the only place they are materialised)."""
+
+    @staticmethod
+    def forward(ctx, x, weight, bias, w, norm, eps):
+        N, K = w.shape
+        x2 = x.reshape(-1, K).contiguous()
+        R = x2.shape[0]
+        dev = x.device
+        st = stream_ptr(dev)
+        g = weight.float().contiguous()
+        b = bias.float().contiguous() if bias is not None else None
+        wc = w.contiguous()
+        wf = torch.empty_like(wc)
+        ln = norm == L.MOC_NORM_LAYERNORM
+        u = torch.empty(N, device=dev, dtype=torch.float32) if ln else None
+        v = torch.empty(N, device=dev, dtype=torch.float32) if ln else None
+        call("moc_norm_fold_weight", ptr(wc), N, K, ptr(g), ptr(b), ptr(wf), ptr(u), ptr(v), st)
+        y = torch.empty(R, N, device=dev, dtype=torch.bfloat16)
+        rstd = torch.empty(R, device=dev, dtype=torch.float32)
+        mean = torch.empty(R, device=dev, dtype=torch.float32) if ln else None
+        call("moc_rows_linear_norm", ptr(x2), K, R, ptr(wf), N, K, norm, float(eps), ptr(u), ptr(v), ptr(y), N,
+             ptr(mean), ptr(rstd), st)
+        ctx.save_for_backward(x2, g, b, wc, mean, rstd)
+        ctx.cfg = (norm, float(eps), x.shape, weight.dtype, None if bias is None else bias.dtype)
+        return y.view(*x.shape[:-1], N)
+
+    @staticmethod
+    def backward(ctx, dy):
+        x2, g, b, w, mean, rstd = ctx.saved_tensors
+        norm, eps, shape, w_dtype, b_dtype = ctx.cfg
+        R, K = x2.shape
+        N = w.shape[0]
+        dev = x2.device
+        st = stream_ptr(dev)
+        dy2 = dy.reshape(R, N).to(torch.bfloat16).contiguous()
+        dx = dg = db = dw = None
+        if ctx.needs_input_grad[0] or ctx.needs_input_grad[1] or ctx.needs_input_grad[2]:
+            dxn = rows_linear(dy2, w.t().contiguous()) if K % 256 == 0 and N % 64 == 0 else torch.matmul(dy2, w)
+            dxr = torch.empty(R, K, device=dev, dtype=torch.bfloat16)
+            dwb = torch.empty(2, K, device=dev, dtype=torch.float32)
+            ws_bytes = L.query("moc_row_norm_bwd_workspace", R, K)
+            ws = torch.empty(max(1, ws_bytes // 4), device=dev, dtype=torch.float32)
+            call("moc_row_norm_bwd", norm, L.MOC_BF16, ptr(x2), R, K, ptr(g), ptr(mean), ptr(rstd), L.MOC_BF16,
+                 ptr(dxn), L.MOC_BF16, ptr(dxr), ptr(dwb), ptr(ws), ws_bytes, st)
+            dx = dxr.view(shape)
+            dg = dwb[0].to(w_dtype) if ctx.needs_input_grad[1] else None
+            db = dwb[1].to(b_dtype) if (b_dtype is not None and ctx.needs_input_grad[2]) else None
+        if ctx.needs_input_grad[3]:
+            xn = torch.empty(R, K, device=dev, dtype=torch.bfloat16)
+            m2 = torch.empty(R, device=dev, dtype=torch.float32) if norm == L.MOC_NORM_LAYERNORM else None
+            r2 = torch.empty(R, device=dev, dtype=torch.float32)
+            call("moc_row_norm_fwd", norm, L.MOC_BF16, ptr(x2), R, K, ptr(g), ptr(b), eps, L.MOC_BF16, ptr(xn),
+                 ptr(m2), ptr(r2), st)
+            dw = linear_wgrad(dy2, xn, w.dtype)
+        return dx, dg, db, dw, None, None
+
+
+def norm_linear_supported(x: torch.Tensor, w: torch.Tensor) -> bool:
+    """Shapes and dtypes the fused norm + projection takes (bf16 rows and weight, N a multiple
+    of 256, K of 64, on a ROCm device)."""
+    N, K = w.shape
+    return (x.is_cuda and x.dtype == torch.bfloat16 and w.dtype == torch.bfloat16 and x.shape[-1] == K
+            and N % 256 == 0 and K % 64 == 0)
+
+
+def norm_linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor], eps: float, norm: str,
+                w: torch.Tensor) -> torch.Tensor:
+    """``norm(x) W^T`` with norm = RMSNorm (``"rms"``) or LayerNorm (``"layer"``) over the last
+    dim: one fused GEMM where ``norm_linear_supported``, else the norm kernel then the projection."""
+    code = {"rms": L.MOC_NORM_RMS, "layer": L.MOC_NORM_LAYERNORM}.get(norm)
+    if code is None:
+        raise ValueError(f"norm must be 'rms' or 'layer', got {norm!r}")
+    if norm_linear_supported(x, w):
+        return _NormLinear.apply(x, weight, bias if code == L.MOC_NORM_LAYERNORM else None, w, code, float(eps))
+    return linear(row_norm(x, weight, bias, eps, norm, w.dtype), w)
+
+
 def linear_wgrad(dy: torch.Tensor, x: torch.Tensor, out_dtype: torch.dtype,
                  out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """dW = dy^T x for dy [R][N], x [R][K] (row-major, contiguous): the split-row MFMA

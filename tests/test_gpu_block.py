@@ -59,6 +59,71 @@ def test_row_norm_matches_oracle(dev, norm, xdt, ydt, R, d):
     assert_parity(wg.grad, w64.grad, gate, "dweight")
 
 
+@pytest.mark.parametrize("norm", ["rms", "layer"])
+@pytest.mark.parametrize("R,K,N", [(300, 768, 768), (8192, 768, 768), (1000, 512, 256), (129, 256, 768)])
+def test_norm_linear_matches_oracle(dev, norm, R, K, N):
+    """q_proj(memory_layernorm(x)) as one GEMM (ops.norm_linear: the norm weight folded into the
+    projection weight, row statistics inside the GEMM) against float64: output, dx, dweight,
+    dbias and dW; rows with a non-zero mean so LayerNorm's centring matters; ragged R."""
+    print(f"norm_linear {norm} R={R} K={K} N={N}", flush=True)
+    from memory_amd import ops
+    g0 = gen(R + K + N)
+    x = (torch.randn(R, K, generator=g0) * 2 + 0.5).to(torch.bfloat16)
+    w = torch.randn(K, generator=g0) * 0.5 + 1
+    b = torch.randn(K, generator=g0) * 0.1 if norm == "layer" else None
+    W = (torch.randn(N, K, generator=g0) * K ** -0.5).to(torch.bfloat16)
+    dy = torch.randn(R, N, generator=g0)
+    eps = 1e-5
+    assert ops.norm_linear_supported(x.to(dev), W.to(dev))
+    xg, wg, Wg = x.to(dev).requires_grad_(True), w.to(dev).requires_grad_(True), W.to(dev).requires_grad_(True)
+    bg = b.to(dev).requires_grad_(True) if b is not None else None
+    y = ops.norm_linear(xg, wg, bg, eps, norm, Wg)
+    assert y.dtype == torch.bfloat16 and y.shape == (R, N)
+    (y.float() * dy.to(dev)).sum().backward()
+    x64, w64, W64 = (t.double().requires_grad_(True) for t in (x, w, W))
+    b64 = b.double().requires_grad_(True) if b is not None else None
+    xn = O.block_rms_norm(x64, w64, eps) if norm == "rms" else F.layer_norm(x64, (K,), w64, b64, eps)
+    ref = xn @ W64.t()
+    (ref * dy.double()).sum().backward()
+    assert_parity(y.float(), ref.detach(), torch.bfloat16, "y")
+    assert_parity(xg.grad.float(), x64.grad, torch.bfloat16, "dx")
+    assert_parity(wg.grad.float(), w64.grad, torch.bfloat16, "dweight")
+    assert_parity(Wg.grad.float(), W64.grad, torch.bfloat16, "dW")
+    if b is not None:
+        assert_parity(bg.grad.float(), b64.grad, torch.bfloat16, "dbias")
+
+
+def test_rows_linear_norm_statistics(dev):
+    """The row statistics the fused GEMM writes for the norm's backward equal the norm
+    kernel's (fp32, same eps), for RMSNorm and LayerNorm."""
+    from memory_amd import _lib as L
+    g0 = gen(3)
+    R, K, N = 333, 768, 256
+    x = (torch.randn(R, K, generator=g0) * 3 - 1).to(torch.bfloat16).to(dev)
+    W = (torch.randn(N, K, generator=g0) * 0.05).to(torch.bfloat16).to(dev)
+    gamma = torch.ones(K, device=dev)
+    beta = torch.zeros(K, device=dev)
+    st = L.stream_ptr(dev)
+    for norm in (L.MOC_NORM_RMS, L.MOC_NORM_LAYERNORM):
+        ln = norm == L.MOC_NORM_LAYERNORM
+        wf = torch.empty_like(W)
+        u = torch.empty(N, device=dev) if ln else None
+        v = torch.empty(N, device=dev) if ln else None
+        L.call("moc_norm_fold_weight", L.ptr(W), N, K, L.ptr(gamma), L.ptr(beta if ln else None), L.ptr(wf),
+               L.ptr(u), L.ptr(v), st)
+        assert torch.equal(wf, W)   # unit gamma: the folded weight is the weight
+        y = torch.empty(R, N, device=dev, dtype=torch.bfloat16)
+        mean, rstd = torch.empty(R, device=dev), torch.empty(R, device=dev)
+        L.call("moc_rows_linear_norm", L.ptr(x), K, R, L.ptr(wf), N, K, norm, 1e-5, L.ptr(u), L.ptr(v), L.ptr(y), N,
+               L.ptr(mean), L.ptr(rstd), st)
+        x64 = x.double()
+        m64 = x64.mean(-1) if ln else torch.zeros(R, dtype=torch.float64, device=dev)
+        var = ((x64 - m64[:, None]) ** 2).mean(-1) if ln else (x64 ** 2).mean(-1)
+        assert_rel(rstd.double(), 1 / torch.sqrt(var + 1e-5), 1e-5, "rstd")
+        if ln:
+            assert_rel(mean.double(), m64, 1e-5, "mean")
+
+
 @pytest.mark.parametrize("rdt", [torch.bfloat16, torch.float32])
 def test_linear_residual(dev, rdt):
     from memory_amd import ops
@@ -80,15 +145,18 @@ def test_linear_residual(dev, rdt):
     assert_rel(rg.grad.float(), r64.grad, 1e-6 if rdt == torch.float32 else 1e-2, "dresidual")
 
 
-@pytest.mark.parametrize("dtype,use_rms", [(torch.float32, True), (torch.float32, False), (torch.bfloat16, True),
-                                           (torch.bfloat16, False)])
-def test_memory_sublayer_matches_oracle(dev, dtype, use_rms):
+@pytest.mark.parametrize("dtype,use_rms,d", [(torch.float32, True, 128), (torch.float32, False, 128),
+                                             (torch.bfloat16, True, 128), (torch.bfloat16, False, 128),
+                                             (torch.bfloat16, True, 256), (torch.bfloat16, False, 256)])
+def test_memory_sublayer_matches_oracle(dev, dtype, use_rms, d):
     """residual + memory_attn(memory_layernorm(h)) over routed chapters of a bank (the fused
     routed_memory_state path): output and every gradient (h, norm weight / bias, q/k/v/o
-    weights, bank) against the oracle's sublayer on the gathered, omega-weighted memory."""
-    print(f"memory sublayer {dtype} rms={use_rms}", flush=True)
+    weights, bank) against the oracle's sublayer on the gathered, omega-weighted memory.  At
+    d = 256 in bf16 the norm runs inside the q projection's GEMM (ops.norm_linear)."""
+    print(f"memory sublayer {dtype} rms={use_rms} d={d}", flush=True)
+    from memory_amd import ops
     from memory_amd.memory_block import MemorySublayer
-    B, L, d, H, C, T, k, S = 2, 70, 128, 2, 9, 64, 3, 1
+    B, L, H, C, T, k, S = 2, 70, d // 64, 9, 64, 3, 1
     g0 = gen(77 + int(use_rms))
     h = torch.randn(B, L, d, generator=g0).to(dtype)
     bank = (torch.randn(C * T, d, generator=g0) * 0.5).to(dtype)
@@ -113,6 +181,7 @@ def test_memory_sublayer_matches_oracle(dev, dtype, use_rms):
         lin.to(dtype)
     hg = h.to(dev).requires_grad_(True)
     bg = bank.to(dev).requires_grad_(True)
+    assert ops.norm_linear_supported(hg, sub.memory_attn.q_proj.weight) == (dtype == torch.bfloat16 and d == 256)
     state = {"bank": bg, "chapter_indices": ci.to(dev), "chapter_weights": cw.to(dev), "num_chapters": C,
              "tokens_per_chapter": T}
     out = sub(hg, routed_memory_state=state)
