@@ -444,6 +444,395 @@ __global__ __launch_bounds__(NT) void router_topk_kernel(
   if (tid < 64) prepend_row(sorted_i, sorted_w, k, S, scale, idx_star + r * (S + k), omega + r * (S + k), tid);
 }
 
+// --------------------------------------------------- many rows: one wave per row
+// Rows of at most 64 * kWaveMaxE logits with k <= 64 (the token-level router: R = B * L rows):
+// the row lives in the wave's registers (lane l holds c = l + 64 j), every reduction is across
+// lanes, and nothing waits on a workgroup barrier; a workgroup carries kWaveRows independent rows.
+constexpr int kWaveMaxE = 72;  // C <= 4,608
+constexpr int kWaveRows = 4;
+constexpr int kWaveBins = 1024;
+constexpr int kWaveCand = 128;
+constexpr int kWaveMaxK = 64;
+
+struct WaveTopkLds {
+  int hist[kWaveBins];
+  uint32_t sel_key[kWaveMaxK];
+  int32_t sel_idx[kWaveMaxK];
+  uint32_t cand_key[kWaveCand];
+  int32_t cand_idx[kWaveCand];
+  float sorted_w[kWaveMaxK];
+  int32_t sorted_i[kWaveMaxK];
+  int count[2];
+};
+
+__device__ __forceinline__ int lanes_below(uint64_t m) {
+  return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+__device__ __forceinline__ float fkey_inv(uint32_t u) {
+  return __uint_as_float((u & 0x80000000u) ? (u & 0x7fffffffu) : ~u);
+}
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    const uint32_t lo = __shfl_xor((uint32_t)v, o, 64), hi = __shfl_xor((uint32_t)(v >> 32), o, 64);
+    const uint64_t w = ((uint64_t)hi << 32) | lo;
+    v = w > v ? w : v;
+  }
+  return v;
+}
+// inclusive sum over lanes >= lane
+__device__ __forceinline__ int wave_suffix_sum(int v, int lane) {
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int t = __shfl_down(v, o, 64);
+    if (lane + o < 64) v += t;
+  }
+  return v;
+}
+
+// the lane id through an empty asm: the per-element predicates derived from it are then formed
+// inside each loop instead of once for the whole kernel (72 lane masks would stay live in SGPRs)
+__device__ __forceinline__ int wave_opaque(int v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+
+// z[j] = row[lane + 64 j] for j < kWaveMaxE (-inf past C): buffer loads from a per-row resource,
+// one lane offset and constant column offsets (no 64-bit address per load)
+__device__ __forceinline__ void wave_load_row(const float* row, int C, int lane, float (&z)[kWaveMaxE]) {
+  const __amdgpu_buffer_rsrc_t rs =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(row), (short)0, C * 4, 0x00020000);
+#pragma unroll
+  for (int j = 0; j < kWaveMaxE; ++j) {
+    const float v = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, lane * 4, 256 * j, 0));
+    z[j] = lane + 64 * j < C ? v : -INFINITY;
+  }
+}
+
+// Forward: the selection of router_topk_kernel (value bins over the selectable range, the
+// boundary bin's logits ranked exactly; key descending, chapter id ascending) within one wave.
+// A boundary bin with more than kWaveCand logits (plateaus of equal or near-equal values) is
+// resolved by repeated wave-wide maxima of (key, -id) over its logits, one selection each.
+__global__ __launch_bounds__(64 * kWaveRows) void router_topk_wave_kernel(
+    const float* __restrict__ logits, int64_t R, int64_t C, int S, int k, int32_t* __restrict__ idx_out,
+    float* __restrict__ w_out, float* __restrict__ probs_out, float scale, int32_t* __restrict__ idx_star,
+    float* __restrict__ omega) {
+  __shared__ WaveTopkLds lds_all[kWaveRows];
+  const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t r = (int64_t)blockIdx.x * kWaveRows + wv;  // wave-uniform: the row's buffer resources stay scalar
+  if (r >= R) return;
+  WaveTopkLds& sm = lds_all[wv];
+  const int Ci = (int)C;
+  float z[kWaveMaxE];
+  wave_load_row(logits + r * C, Ci, lane, z);
+#pragma unroll
+  for (int i = 0; i < kWaveBins / 64; ++i) sm.hist[lane * (kWaveBins / 64) + i] = 0;
+  if (lane < 2) sm.count[lane] = 0;
+  // padding holds -inf: it takes part in no maximum and adds exp(-inf) = 0 to the sums
+  float mxa = -INFINITY, hi = -INFINITY, lo = INFINITY;
+  int ln = wave_opaque(lane);
+#pragma unroll
+  for (int j = 0; j < kWaveMaxE; ++j) {
+    const int c = ln + 64 * j;
+    const bool sel = c < Ci && c >= S;
+    mxa = fmaxf(mxa, z[j]);
+    hi = fmaxf(hi, sel ? z[j] : -INFINITY);
+    lo = fminf(lo, sel ? z[j] : INFINITY);
+  }
+  const float lane_hi = hi;
+  mxa = wave_max(mxa);
+  hi = wave_max(hi);
+  lo = -wave_max(-lo);
+  float s_all = 0.f, s_sel = 0.f;
+  ln = wave_opaque(lane);
+#pragma unroll
+  for (int j = 0; j < kWaveMaxE; ++j) {
+    const float e = __expf(z[j] - mxa);
+    s_all += e;
+    s_sel += ln + 64 * j >= S ? e : 0.f;
+  }
+  const float Z = wave_sum(s_all), Zs = wave_sum(s_sel);
+  const float msum = S > 0 ? Zs / Z : 1.f;
+  const float denom = fmaxf(msum, 1e-12f);
+  if (probs_out) {
+    const __amdgpu_buffer_rsrc_t ps = __builtin_amdgcn_make_buffer_rsrc(probs_out + r * C, (short)0, Ci * 4, 0x00020000);
+#pragma unroll
+    for (int j = 0; j < kWaveMaxE; ++j)
+      __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(int, __expf(z[j] - mxa) / Z), ps, lane * 4, 256 * j, 0);
+  }
+
+  // ---- fast selection: t0 = the k-th largest of the 64 lanes' maxima; at least k selectable
+  // logits are >= t0, so the top k are among them.  Those candidates (a few dozen for any spread
+  // of values) are ranked exactly, which is also the final order.
+  {
+    int lrank = 0;
+    for (int i = 0; i < 64; ++i) {
+      const float m = __shfl(lane_hi, i, 64);
+      lrank += (m > lane_hi) || (m == lane_hi && i < lane);
+    }
+    const uint64_t at = __ballot(lrank == k - 1);
+    const float t0 = __shfl(lane_hi, __builtin_ctzll(at), 64);
+    int ncand = 0;
+    {
+      const int ln0 = wave_opaque(lane);
+#pragma unroll
+      for (int j = 0; j < kWaveMaxE; ++j) {
+        const int c = ln0 + 64 * j;
+        const bool cand = c < Ci && c >= S && z[j] >= t0;
+        const uint64_t mc = __ballot(cand);
+        if (cand) {
+          const int p = ncand + lanes_below(mc);
+          if (p < kWaveCand) {
+            sm.cand_key[p] = fkey(z[j]);
+            sm.cand_idx[p] = c;
+          }
+        }
+        ncand += __popcll(mc);
+      }
+    }
+    if (ncand <= kWaveCand && t0 > -INFINITY) {
+      wave_lds_sync();
+      for (int i = lane; i < ncand; i += 64) {
+        const uint32_t ki = sm.cand_key[i];
+        const int32_t ii = sm.cand_idx[i];
+        int rank = 0;
+        for (int j = 0; j < ncand; ++j) {
+          const uint32_t kj = sm.cand_key[j];
+          rank += (kj > ki) || (kj == ki && sm.cand_idx[j] < ii);
+        }
+        if (rank < k) {
+          float p = __expf(fkey_inv(ki) - mxa) / Z;
+          if (S > 0) p = p / denom;
+          sm.sorted_w[rank] = p;
+          sm.sorted_i[rank] = ii;
+        }
+      }
+      wave_lds_sync();
+      const float ps = lane < k ? sm.sorted_w[lane] : 0.f;
+      const float W = fmaxf(wave_sum(ps), 1e-12f);
+      if (lane < k) {
+        const float wn = ps / W;
+        idx_out[r * k + lane] = sm.sorted_i[lane];
+        w_out[r * k + lane] = wn;
+        sm.sorted_w[lane] = wn;
+      }
+      if (!idx_star) return;
+      wave_lds_sync();
+      prepend_row(sm.sorted_i, sm.sorted_w, k, S, scale, idx_star + r * (S + k), omega + r * (S + k), lane);
+      return;
+    }
+    wave_lds_sync();
+  }
+
+  // ---- selection into sm.sel_key / sm.sel_idx (any order)
+  const float inv = (float)kWaveBins / (hi - lo);
+  const bool binned = hi > lo && inv > 0.f && inv < INFINITY;
+  auto bin_of = [&](float v) { return binned ? min(kWaveBins - 1, (int)((v - lo) * inv)) : 0; };
+  wave_lds_sync();
+  // boundary bin (every selectable logit in bin 0 when the range does not split)
+  int bstar = 0, remaining = k, nb = Ci - S;
+  if (binned) {
+    ln = wave_opaque(lane);
+#pragma unroll
+    for (int j = 0; j < kWaveMaxE; ++j) {
+      const int c = ln + 64 * j;
+      const bool sel = c < Ci && c >= S;
+      atomicAdd(&sm.hist[sel ? bin_of(z[j]) : 0], sel ? 1 : 0);
+    }
+    wave_lds_sync();
+    constexpr int BPL = kWaveBins / 64;
+    int cnt[BPL], mine = 0;
+#pragma unroll
+    for (int i = 0; i < BPL; ++i) {
+      cnt[i] = sm.hist[lane * BPL + i];
+      mine += cnt[i];
+    }
+    int above = wave_suffix_sum(mine, lane) - mine;
+    int my_b = -1, my_rem = 0, my_nb = 0;
+#pragma unroll
+    for (int i = BPL - 1; i >= 0; --i) {
+      if (above < k && above + cnt[i] >= k) {
+        my_b = lane * BPL + i;
+        my_rem = k - above;
+        my_nb = cnt[i];
+      }
+      above += cnt[i];
+    }
+    const int src = __builtin_ctzll(__ballot(my_b >= 0));
+    bstar = __shfl(my_b, src, 64);
+    remaining = __shfl(my_rem, src, 64);
+    nb = __shfl(my_nb, src, 64);
+  }
+  const int n_above = k - remaining;
+  const bool direct = nb <= kWaveCand;
+  // logits above the boundary bin are selected, the boundary bin's are candidates (slots taken
+  // from per-wave LDS counters; the order is fixed by the ranks below).  The bins are formed
+  // again here rather than kept from the histogram pass (72 more live registers).
+  ln = wave_opaque(lane);
+  float lo2 = lo, inv2 = inv;
+  asm volatile("" : "+v"(lo2), "+v"(inv2));
+#pragma unroll
+  for (int j = 0; j < kWaveMaxE; ++j) {
+    const int c = ln + 64 * j;
+    const int b = binned ? min(kWaveBins - 1, (int)((z[j] - lo2) * inv2)) : 0;
+    if (c < Ci && c >= S && b >= bstar) {
+      if (b > bstar) {
+        const int p = atomicAdd(&sm.count[0], 1);
+        sm.sel_key[p] = fkey(z[j]);
+        sm.sel_idx[p] = c;
+      } else if (direct) {
+        const int p = atomicAdd(&sm.count[1], 1);
+        sm.cand_key[p] = fkey(z[j]);
+        sm.cand_idx[p] = c;
+      }
+    }
+  }
+  wave_lds_sync();
+  if (direct) {
+    // the `remaining` best of the boundary bin
+    for (int i = lane; i < nb; i += 64) {
+      const uint32_t ki = sm.cand_key[i];
+      const int32_t ii = sm.cand_idx[i];
+      int rank = 0;
+      for (int j = 0; j < nb; ++j) {
+        const uint32_t kj = sm.cand_key[j];
+        rank += (kj > ki) || (kj == ki && sm.cand_idx[j] < ii);
+      }
+      if (rank < remaining) {
+        sm.sel_key[n_above + rank] = ki;
+        sm.sel_idx[n_above + rank] = ii;
+      }
+    }
+  } else {
+    // crowded boundary bin: one wave-wide maximum of (key, -id) per remaining slot; the pairs
+    // taken are exactly those at or above the last one taken
+    uint64_t last = ~0ull;
+    for (int t = 0; t < remaining; ++t) {
+      uint64_t best = 0;
+      ln = wave_opaque(lane);
+#pragma unroll
+      for (int j = 0; j < kWaveMaxE; ++j) {
+        const int c = ln + 64 * j;
+        const uint64_t v = ((uint64_t)fkey(z[j]) << 32) | (uint32_t)~(uint32_t)c;
+        const bool cand = c < Ci && c >= S && bin_of(z[j]) == bstar && v < last;
+        best = cand && v > best ? v : best;
+      }
+      best = wave_max_u64(best);
+      if (lane == 0) {
+        sm.sel_key[n_above + t] = (uint32_t)(best >> 32);
+        sm.sel_idx[n_above + t] = (int32_t)~(uint32_t)best;
+      }
+      last = best;
+    }
+  }
+  wave_lds_sync();
+  // ---- rank order (key descending, id ascending), probabilities, renormalisation in rank order
+  if (lane < k) {
+    const uint32_t ki = sm.sel_key[lane];
+    const int32_t ii = sm.sel_idx[lane];
+    int rank = 0;
+    for (int j = 0; j < k; ++j) {
+      const uint32_t kj = sm.sel_key[j];
+      rank += (kj > ki) || (kj == ki && sm.sel_idx[j] < ii);
+    }
+    float p = __expf(fkey_inv(ki) - mxa) / Z;
+    if (S > 0) p = p / denom;
+    sm.sorted_w[rank] = p;
+    sm.sorted_i[rank] = ii;
+  }
+  wave_lds_sync();
+  const float ps = lane < k ? sm.sorted_w[lane] : 0.f;
+  const float W = fmaxf(wave_sum(ps), 1e-12f);
+  if (lane < k) {
+    const float wn = ps / W;
+    idx_out[r * k + lane] = sm.sorted_i[lane];
+    w_out[r * k + lane] = wn;
+    sm.sorted_w[lane] = wn;
+  }
+  if (!idx_star) return;
+  wave_lds_sync();
+  prepend_row(sm.sorted_i, sm.sorted_w, k, S, scale, idx_star + r * (S + k), omega + r * (S + k), lane);
+}
+
+// Backward of the top-k chain (router.py:114-149 autograd, as topk_bwd_row) within one wave per
+// row.  With q = softmax(z), the masked renormalisation p' = q / D (D = clamp(sum_{c>=S} q)), the
+// selected w_raw = p'[idx] and w = w_raw / clamp(sum w_raw): dq_c = base for every c >= S plus
+// dw_raw_i / D at c = idx_i, base = -A / D^2 (A = sum_i dw_raw_i q[idx_i]), and
+// sum_c dq_c q_c = base * msum + A / D (msum = sum_{c>=S} q), so dz = q (dq - that) needs no dense
+// dq: the row is stored with dq = base, then the k selected entries are rewritten.
+__global__ __launch_bounds__(64 * kWaveRows) void router_topk_bwd_wave_kernel(
+    const float* __restrict__ logits, const int32_t* __restrict__ idx, const float* __restrict__ dw_hat, int64_t R,
+    int64_t C, int S, int k, const float* __restrict__ dz_in, float* __restrict__ dlogits) {
+  const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t r = (int64_t)blockIdx.x * kWaveRows + wv;  // wave-uniform: the row's buffer resources stay scalar
+  if (r >= R) return;
+  const float* row = logits + r * C;
+  int32_t ci = 0;
+  float g = 0.f, zi = 0.f;
+  if (lane < k) {
+    ci = idx[r * k + lane];
+    g = dw_hat[r * k + lane];
+    zi = row[ci];
+  }
+  const int Ci = (int)C;
+  float z[kWaveMaxE];
+  wave_load_row(row, Ci, lane, z);
+  float mxa = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < kWaveMaxE; ++j) mxa = fmaxf(mxa, z[j]);
+  mxa = wave_max(mxa);
+  float s_all = 0.f, s_sel = 0.f;
+  int ln = wave_opaque(lane);
+#pragma unroll
+  for (int j = 0; j < kWaveMaxE; ++j) {
+    const float e = __expf(z[j] - mxa);  // 0 for the -inf padding
+    s_all += e;
+    s_sel += ln + 64 * j >= S ? e : 0.f;
+  }
+  const float Z = wave_sum(s_all), Zs = wave_sum(s_sel);
+  const float msum = S > 0 ? Zs / Z : 1.f;
+  const float denom = fmaxf(msum, 1e-12f);
+  const bool denom_live = msum >= 1e-12f;
+  const float qi = lane < k ? __expf(zi - mxa) / Z : 0.f;
+  const float pi = S > 0 ? qi / denom : qi;
+  const float Wsum = wave_sum(pi), GW = wave_sum(g * pi);
+  const float W = fmaxf(Wsum, 1e-12f);
+  const bool W_live = Wsum >= 1e-12f;
+  const float dwr = lane < k ? g / W - (W_live ? GW / (W * W) : 0.f) : 0.f;
+  const float A = wave_sum(dwr * qi);
+  const float base = (S > 0 && denom_live) ? -A / (denom * denom) : 0.f;
+  const float dsel = S > 0 ? dwr / denom : dwr;
+  const float DPP = (S > 0 ? base * msum : 0.f) + wave_sum(dsel * qi);
+  float* out = dlogits + r * C;
+  // buffer stores: the row's resource bound drops the padding's stores
+  const __amdgpu_buffer_rsrc_t os = __builtin_amdgcn_make_buffer_rsrc(out, (short)0, Ci * 4, 0x00020000);
+  const __amdgpu_buffer_rsrc_t is =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(dz_in ? dz_in + r * C : out), (short)0,
+                                        dz_in ? Ci * 4 : 0, 0x00020000);
+  const float iz = 1.f / Z;
+  ln = wave_opaque(lane);
+#pragma unroll
+  for (int j = 0; j < kWaveMaxE; ++j) {
+    const int c = ln + 64 * j;
+    const float q = __expf(z[j] - mxa) * iz;
+    const float dq = (S > 0 && c >= S) ? base : 0.f;
+    const float din = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(is, lane * 4, 256 * j, 0));
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(int, q * (dq - DPP) + din), os, lane * 4, 256 * j, 0);
+  }
+  // the selected entries, after the dense stores have completed
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  if (lane < k) {
+    const float dq = (S > 0 && ci >= S ? base : 0.f) + dsel;
+    out[ci] = qi * (dq - DPP) + (dz_in ? dz_in[r * C + ci] : 0.f);
+  }
+}
+
+// Whether the one-wave-per-row kernels take these rows: many rows (the workgroup-per-row
+// kernels suit a few long-latency rows better), short enough for registers, k <= 64.
+inline bool router_wave_rows(int64_t R, int64_t C, int k) {
+  return R > 64 && C <= 64 * kWaveMaxE && k <= kWaveMaxK;
+}
+
 // dlogits for the chain  p = softmax(z); q = p masked to c >= S; p' = q / clamp(sum q);
 // w = p'[idx]; w_hat = w / clamp(sum w).  dw_hat is the incoming gradient (global or LDS).
 // Mirrors autograd of memory_transformer/router.py:114-149 including the clamp_min(1e-12)
@@ -1248,6 +1637,11 @@ int moc_router_topk(const float* logits, int64_t R, int64_t C, int S, int k, int
   MOC_REQUIRE(k <= kMaxTopK, MOC_ERR_UNSUPPORTED, "moc_router_topk: k=%d exceeds %d", k, kMaxTopK);
   MOC_REQUIRE(C <= kMaxRouterC, MOC_ERR_UNSUPPORTED, "moc_router_topk: C=%lld exceeds %d", (long long)C, kMaxRouterC);
   if (R == 0) return MOC_OK;
+  if (router_wave_rows(R, C, k)) {
+    hipLaunchKernelGGL(router_topk_wave_kernel, dim3((unsigned)((R + kWaveRows - 1) / kWaveRows)),
+                       dim3(64 * kWaveRows), 0, stream, logits, R, C, S, k, idx, w, probs, 0.f, nullptr, nullptr);
+    return check_launch("router_topk_wave_kernel");
+  }
   const size_t lds = (size_t)C * sizeof(float);
   if (router_threads(R) == 1024)
     hipLaunchKernelGGL(router_topk_kernel<1024>, dim3((unsigned)R), dim3(1024), lds, stream, logits, C, S, k, idx, w,
@@ -1270,6 +1664,11 @@ int moc_router_topk_prepend(const float* logits, int64_t R, int64_t C, int S, in
   MOC_REQUIRE(C <= kMaxRouterC, MOC_ERR_UNSUPPORTED, "moc_router_topk_prepend: C=%lld exceeds %d", (long long)C,
               kMaxRouterC);
   if (R == 0) return MOC_OK;
+  if (router_wave_rows(R, C, k)) {
+    hipLaunchKernelGGL(router_topk_wave_kernel, dim3((unsigned)((R + kWaveRows - 1) / kWaveRows)),
+                       dim3(64 * kWaveRows), 0, stream, logits, R, C, S, k, idx, w, nullptr, scale, idx_star, omega);
+    return check_launch("router_topk_wave_kernel(prepend)");
+  }
   const size_t lds = (size_t)C * sizeof(float);
   if (router_threads(R) == 1024)
     hipLaunchKernelGGL(router_topk_kernel<1024>, dim3((unsigned)R), dim3(1024), lds, stream, logits, C, S, k, idx, w,
@@ -1288,6 +1687,11 @@ int moc_router_topk_bwd(const float* logits, const int32_t* idx, const float* dw
   MOC_REQUIRE(C <= kMaxRouterC / 2, MOC_ERR_UNSUPPORTED, "moc_router_topk_bwd: C=%lld exceeds %d", (long long)C,
               kMaxRouterC / 2);
   if (R == 0) return MOC_OK;
+  if (router_wave_rows(R, C, k)) {
+    hipLaunchKernelGGL(router_topk_bwd_wave_kernel, dim3((unsigned)((R + kWaveRows - 1) / kWaveRows)),
+                       dim3(64 * kWaveRows), 0, stream, logits, idx, dw, R, C, S, k, nullptr, dlogits);
+    return check_launch("router_topk_bwd_wave_kernel");
+  }
   const size_t lds = 2 * (size_t)C * sizeof(float);
   if (router_threads(R) == 1024)
     hipLaunchKernelGGL(router_topk_bwd_kernel<1024>, dim3((unsigned)R), dim3(1024), lds, stream, logits, idx, dw, C, S,
