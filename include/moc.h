@@ -474,27 +474,29 @@ int moc_bank_sqnorm(const float* grad, const int32_t* list, const int32_t* n_lis
  * chapter plan of the edges e = token * S + slot (token = b * Tq + t).
  * q [tokens][HQ][64]; K/V addressed by element strides (chapter cs, kv head hs, row rs).
  * Heads hk0 .. hk0+nhk-1 are processed; each edge serves rpe rows (query heads
- * hq_off .. hq_off+rpe-1).  Partials: o_part f32 [E * rpe][64], lse_part f32 [E * rpe].
- * bf16 runs one wave per (chapter, kv head) and needs 16-byte aligned q / k / v / o_part
- * and cs / hs / rs multiples of 8. */
+ * hq_off .. hq_off+rpe-1).  Partials: o_part [E * rpe][64] in the call's dtype (bf16 or f32:
+ * the per-edge rows are normalised, so bf16 keeps their round trip through HBM at half the
+ * bytes), lse_part f32 [E * rpe].  bf16 runs one wave per (chapter, kv head) and needs 16-byte
+ * aligned q / k / v / o_part and cs / hs / rs multiples of 8. */
 int moc_sparse_fwd(int dtype, const void* q, int64_t ntok, int HQ, const void* k, const void* v, int64_t cs,
                    int64_t hs, int64_t rs, int HK, int Dh, const int32_t* uniq, const int32_t* n_uniq,
                    const int32_t* csr_off, const int32_t* csr_edge, int64_t max_u, int S, int hk0, int nhk,
-                   int hq_off, int rpe, float scale, float* o_part, float* lse_part, hipStream_t stream);
+                   int hq_off, int rpe, float scale, void* o_part, float* lse_part, hipStream_t stream);
 /* Combine of the slot partials: mode 0 MoE sum_s w_s o_s; 1 joint; 2 joint with block weights
  * max(w, 0); 3 joint with log(max(w, 1e-20)) bias.  w f32 [E] (per edge), edge_u from the plan
- * (negative = skipped slot).  out [tokens][HQ][64]; lse_joint f32 [tokens * rpe] (modes 1-3). */
-int moc_sparse_combine(int dtype, const float* o_part, const float* lse_part, const int32_t* edge_u, const float* w,
+ * (negative = skipped slot), o_part in the call's dtype.  out [tokens][HQ][64]; lse_joint f32
+ * [tokens * rpe] (modes 1-3). */
+int moc_sparse_combine(int dtype, const void* o_part, const float* lse_part, const int32_t* edge_u, const float* w,
                        int mode, int S, int rpe, int64_t ntok, int HQ, int hq_off, void* out, float* lse_joint,
                        hipStream_t stream);
 /* Backward prep: modes 1-3 -> dst f32 [tokens * rpe] = dout . out (the joint softmax delta that
  * moc_sparse_bwd reads).  mode 0 -> dst f32 [E * rpe] = dout . o_part; moc_sparse_bwd computes
  * these per-chapter deltas itself, so mode 0 callers do not need this call. */
-int moc_sparse_bwd_prep(int dtype, const void* dout, const void* out, const float* o_part, const int32_t* edge_u,
+int moc_sparse_bwd_prep(int dtype, const void* dout, const void* out, const void* o_part, const int32_t* edge_u,
                         int mode, int S, int rpe, int64_t ntok, int HQ, int hq_off, float* dst, hipStream_t stream);
 /* Chapter-centric backward: dK/dV of every (chapter, kv head) stored with element strides
  * (ocs, ohs, ors) into dk / dv (rows of untouched chapters are left as they are); per-edge
- * dq parts f32 [E * rpe][64]; dlog f32 [E * rpe] (modes 2-3, d loss / d log weight).
+ * dq parts [E * rpe][64] in the call's dtype; dlog f32 [E * rpe] (modes 2-3, d loss / d log weight).
  * delta_row: modes 1-3 read the joint delta [tokens * rpe] of moc_sparse_bwd_prep; mode 0
  * WRITES the per-chapter delta dout . o_s [E * rpe] (computed from P and dO V^T), the input
  * of moc_sparse_dw.  bf16 runs one wave per (chapter, kv head) and needs 16-byte aligned
@@ -504,10 +506,10 @@ int moc_sparse_bwd(int dtype, const void* q, const void* dout, int64_t ntok, int
                    int64_t cs, int64_t hs, int64_t rs, int HK, int Dh, const int32_t* uniq, const int32_t* n_uniq,
                    const int32_t* csr_off, const int32_t* csr_edge, int64_t max_u, int S, int hk0, int nhk,
                    int hq_off, int rpe, int mode, const float* lse_row, float* delta_row, const float* w,
-                   float scale, void* dk, void* dv, int64_t ocs, int64_t ohs, int64_t ors, float* dq_part,
+                   float scale, void* dk, void* dv, int64_t ocs, int64_t ohs, int64_t ors, void* dq_part,
                    float* dlog, hipStream_t stream);
 /* dq [tokens][HQ][64] rows hq_off .. hq_off+rpe-1 = sum over valid slots of dq_part. */
-int moc_sparse_dq_combine(int dtype, const float* dq_part, const int32_t* edge_u, int S, int rpe, int64_t ntok,
+int moc_sparse_dq_combine(int dtype, const void* dq_part, const int32_t* edge_u, int S, int rpe, int64_t ntok,
                           int HQ, int hq_off, void* dq, hipStream_t stream);
 /* dw f32 [E]: mode 0 sum of dst rows; modes 2/3 sum of dlog rows / w (0 where the clamp is active). */
 int moc_sparse_dw(const float* src, const float* w, const int32_t* edge_u, int mode, int rpe, int64_t E, float* dw,
@@ -528,12 +530,12 @@ int moc_sparse_zero_untouched(int dtype, void* dk, void* dv, int64_t cs, int64_t
  * memory_transformer/model.py:612-692 with the chapters and omega fixed for the generation.
  * Chapter-centric over the plan of the (sequence, slot) edges, so each selected tile is read
  * once per step.  q [B][H][64]; k_tiles, v_tiles [C][HK][64 keys][64 dims] (kv_project's
- * "k" / "v" layouts); omega f32 [B * NS], >= 0; partials o_part f32 [B * NS * H][64] and
+ * "k" / "v" layouts); omega f32 [B * NS], >= 0; partials o_part [B * NS * H][64] (call dtype) and
  * lse_part f32 [B * NS * H] are merged by moc_sparse_combine in joint mode (rpe = H).
  * bf16 needs 16-byte aligned q / tiles / o_part. */
 int moc_decode_partial(int dtype, const void* q, int64_t B, int H, const void* k_tiles, const void* v_tiles, int HK,
                        int Dh, int T, const int32_t* uniq, const int32_t* n_uniq, const int32_t* csr_off,
-                       const int32_t* csr_edge, int64_t max_u, const float* omega, int NS, float scale, float* o_part,
+                       const int32_t* csr_edge, int64_t max_u, const float* omega, int NS, float scale, void* o_part,
                        float* lse_part, const int32_t* row_tab, hipStream_t stream);
 /* The decode step's row table, built once per routing: row_tab i32 [max_u][16] = the first 16
  * edges (csr order) of each distinct chapter of the plan, -1 padded (no reference counterpart: a

@@ -59,7 +59,7 @@ int moc_decode_row_table(const int32_t* n_uniq, const int32_t* csr_off, const in
 
 int moc_decode_partial(int dtype, const void* q, int64_t B, int H, const void* k_tiles, const void* v_tiles, int HK,
                        int Dh, int T, const int32_t* uniq, const int32_t* n_uniq, const int32_t* csr_off,
-                       const int32_t* csr_edge, int64_t max_u, const float* omega, int NS, float scale, float* o_part,
+                       const int32_t* csr_edge, int64_t max_u, const float* omega, int NS, float scale, void* o_part,
                        float* lse_part, const int32_t* row_tab, hipStream_t stream) {
   MOC_REQUIRE(q && k_tiles && v_tiles && uniq && n_uniq && csr_off && csr_edge && omega && o_part && lse_part,
               MOC_ERR_ARG, "moc_decode_partial: null pointer");

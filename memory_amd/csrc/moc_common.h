@@ -342,7 +342,7 @@ inline int dtype_size(int dt) { return dt == MOC_F32 ? 4 : (dt == MOC_BF16 ? 2 :
 int sparse_fwd_launch(int dtype, const void* q, int HQ, const void* k, const void* v, int64_t cs, int64_t hs,
                       int64_t rs, int HK, const int32_t* uniq, const int32_t* n_uniq, const int32_t* csr_off,
                       const int32_t* csr_edge, int64_t max_u, int S, int hk0, int nhk, int hq_off, int rpe,
-                      float scale, const float* omega, float* o_part, float* lse_part, hipStream_t stream,
+                      float scale, const float* omega, void* o_part, float* lse_part, hipStream_t stream,
                       const char* who, const int32_t* row_tab = nullptr);
 
 // out[i] = inv * sum_j part[j * n + i] for i < n, j < nsplit, summed in a fixed order

@@ -57,12 +57,27 @@ __device__ __forceinline__ void sp_load_tile(char* dst, const T* base, int64_t r
 }
 
 // ------------------------------------------------------------------ forward
+// Partial rows (per (edge, row) outputs and dQ contributions) are kept in the data type of the
+// call: bf16 for bf16 inputs (half the bytes of the round trip through HBM), f32 for f32.
+__device__ __forceinline__ f32x4 part_load4(const float* p) { return *reinterpret_cast<const f32x4*>(p); }
+__device__ __forceinline__ f32x4 part_load4(const bf16* p) {
+  const bf16x4 v = *reinterpret_cast<const bf16x4*>(p);
+  return f32x4{(float)v[0], (float)v[1], (float)v[2], (float)v[3]};
+}
+__device__ __forceinline__ void part_store4(float* p, f32x4 v) { *reinterpret_cast<f32x4*>(p) = v; }
+__device__ __forceinline__ void part_store4(bf16* p, f32x4 v) {
+  bf16x4 o;
+#pragma unroll
+  for (int x = 0; x < 4; ++x) o[x] = (bf16)v[x];
+  *reinterpret_cast<bf16x4*>(p) = o;
+}
+
 template <typename T>
 __global__ __launch_bounds__(64 * SpCfg<T>::NW) void sparse_fwd_kernel(
     const T* __restrict__ q, int HQ, const T* __restrict__ k, const T* __restrict__ v, int64_t cs, int64_t hs,
     int64_t rs, int HK, const int32_t* __restrict__ uniq, const int32_t* __restrict__ n_uniq,
     const int32_t* __restrict__ csr_off, const int32_t* __restrict__ csr_edge, int S, int hk0, int hq_off, int rpe,
-    float scale_log2, float* __restrict__ o_part, float* __restrict__ lse_part, const float* __restrict__ omega) {
+    float scale_log2, T* __restrict__ o_part, float* __restrict__ lse_part, const float* __restrict__ omega) {
   typedef typename Frag<T>::type F8;
   constexpr int NW = SpCfg<T>::NW, NT = 64 * NW;
   using Tile = SwzTile<T, 64>;
@@ -161,10 +176,9 @@ __global__ __launch_bounds__(64 * SpCfg<T>::NW) void sparse_fwd_kernel(
     for (int qb = 0; qb < 2; ++qb) {
       if (erow[qb] < 0) continue;
       const float inv = wrow[qb] / l[qb];
-      float* op = o_part + (size_t)erow[qb] * kSpDh;
+      T* op = o_part + (size_t)erow[qb] * kSpDh;
 #pragma unroll
-      for (int db = 0; db < 4; ++db)
-        *reinterpret_cast<f32x4*>(op + 16 * db + 4 * g) = o[db][qb] * inv;
+      for (int db = 0; db < 4; ++db) part_store4(op + 16 * db + 4 * g, o[db][qb] * inv);
       if (g == 0) lse_part[erow[qb]] = m[qb] + log2f(l[qb]);
     }
   }
@@ -181,7 +195,8 @@ __device__ __forceinline__ float sp_logw(int mode, float w) {
 
 // Weighted sum over the slots s0 .. s0 + 63 of one row (lane group g takes slots g, g + 4,
 // ...; lane s - s0 holds a_s); a_s = 0 marks a skipped slot, whose partial row is never read.
-__device__ __forceinline__ f32x4 sp_slot_sum(const float* __restrict__ part, int64_t tok, int S, int rpe, int r,
+template <typename P>
+__device__ __forceinline__ f32x4 sp_slot_sum(const P* __restrict__ part, int64_t tok, int S, int rpe, int r,
                                              float a, int s0, int lane) {
   const int g = lane >> 4, sub = lane & 15;
   const int n = min(64, S - s0);
@@ -198,7 +213,7 @@ __device__ __forceinline__ f32x4 sp_slot_sum(const float* __restrict__ part, int
       v[i] = f32x4{0.f, 0.f, 0.f, 0.f};
       if (av[i] != 0.f) {
         const int64_t e = tok * S + s0 + j;
-        v[i] = *reinterpret_cast<const f32x4*>(part + (e * rpe + r) * kSpDh + 4 * sub);
+        v[i] = part_load4(part + (e * rpe + r) * kSpDh + 4 * sub);
       }
     }
 #pragma unroll
@@ -219,7 +234,7 @@ __device__ __forceinline__ f32x4 sp_groups_sum(f32x4 acc) {
 constexpr int kCombWaves = 4;
 
 template <typename T>
-__global__ __launch_bounds__(64 * kCombWaves) void sparse_combine_kernel(const float* __restrict__ o_part,
+__global__ __launch_bounds__(64 * kCombWaves) void sparse_combine_kernel(const T* __restrict__ o_part,
                                                                          const float* __restrict__ lse_part,
                                                                          const int32_t* __restrict__ edge_u,
                                                                          const float* __restrict__ w, int mode, int S,
@@ -282,7 +297,7 @@ constexpr int kCombSmallPerGroup = 17;
 
 template <typename T>
 __global__ __launch_bounds__(64 * kCombWaves) void sparse_combine_small_kernel(
-    const float* __restrict__ o_part, const float* __restrict__ lse_part, const int32_t* __restrict__ edge_u,
+    const T* __restrict__ o_part, const float* __restrict__ lse_part, const int32_t* __restrict__ edge_u,
     const float* __restrict__ w, int mode, int S, int rpe, int64_t ntok, int HQ, int hq_off, T* __restrict__ out,
     float* __restrict__ lse_joint) {
   const int lane = threadIdx.x & 63;
@@ -307,8 +322,7 @@ __global__ __launch_bounds__(64 * kCombWaves) void sparse_combine_small_kernel(
 #pragma unroll
   for (int i = 0; i < kCombSmallPerGroup; ++i) {
     const int j = 4 * i + g;
-    v[i] = j < S ? *reinterpret_cast<const f32x4*>(o_part + ((tok * S + j) * rpe + r) * kSpDh + 4 * sub)
-                 : f32x4{0.f, 0.f, 0.f, 0.f};
+    v[i] = j < S ? part_load4(o_part + ((tok * S + j) * rpe + r) * kSpDh + 4 * sub) : f32x4{0.f, 0.f, 0.f, 0.f};
   }
   float M = -INFINITY;
   if (mode != 0) {
@@ -346,7 +360,7 @@ __global__ __launch_bounds__(64 * kCombWaves) void sparse_combine_small_kernel(
 // else:   delta[row]     = dO_row . out_row
 template <typename T>
 __global__ __launch_bounds__(256) void sparse_bwd_prep_kernel(const T* __restrict__ dout, const T* __restrict__ out,
-                                                              const float* __restrict__ o_part,
+                                                              const T* __restrict__ o_part,
                                                               const int32_t* __restrict__ edge_u, int mode, int S,
                                                               int rpe, int64_t ntok, int HQ, int hq_off,
                                                               float* __restrict__ dst) {
@@ -364,7 +378,7 @@ __global__ __launch_bounds__(256) void sparse_bwd_prep_kernel(const T* __restric
       const int64_t e = tok * S + s;
       float acc = 0.f;
       if (edge_u[e] >= 0) {
-        const f32x4 o = *reinterpret_cast<const f32x4*>(o_part + ((size_t)e * rpe + r) * kSpDh + 4 * sub);
+        const f32x4 o = part_load4(o_part + ((size_t)e * rpe + r) * kSpDh + 4 * sub);
         acc = d[0] * o[0] + d[1] * o[1] + d[2] * o[2] + d[3] * o[3];
       }
 #pragma unroll
@@ -393,7 +407,7 @@ __global__ __launch_bounds__(64 * SpCfg<T>::NW, 1) void sparse_bwd_kernel(
     const int32_t* __restrict__ csr_off, const int32_t* __restrict__ csr_edge, int S, int hk0, int hq_off, int rpe,
     int mode, const float* __restrict__ lse_row, float* __restrict__ delta_row, const float* __restrict__ w,
     float scale_log2, float scale, T* __restrict__ dk, T* __restrict__ dv, int64_t ocs, int64_t ohs, int64_t ors,
-    float* __restrict__ dq_part, float* __restrict__ dlog) {
+    T* __restrict__ dq_part, float* __restrict__ dlog) {
   typedef typename Frag<T>::type F8;
   constexpr int NW = SpCfg<T>::NW, NT = 64 * NW;
   using Tile = SwzTile<T, 64>;   // [key][dim] and [dim][key] tiles
@@ -621,9 +635,9 @@ __global__ __launch_bounds__(64 * SpCfg<T>::NW, 1) void sparse_bwd_kernel(
 #pragma unroll
       for (int x = 0; x < 4; ++x) {
         if (er[qb][x] < 0) continue;
-        float* dst = dq_part + (size_t)er[qb][x] * kSpDh;
+        T* dst = dq_part + (size_t)er[qb][x] * kSpDh;
 #pragma unroll
-        for (int db = 0; db < 4; ++db) dst[16 * db + c16] = dqa[qb][db][x] * scale;
+        for (int db = 0; db < 4; ++db) dst[16 * db + c16] = from_f<T>(dqa[qb][db][x] * scale);
       }
     if (dlog) {
 #pragma unroll
@@ -683,7 +697,7 @@ __global__ __launch_bounds__(64 * SpCfg<T>::NW, 1) void sparse_bwd_kernel(
 
 // dq[token, hq_off + r] = sum over valid slots of dq_part[e, r]  (one wave per row)
 template <typename T>
-__global__ __launch_bounds__(64 * kCombWaves) void sparse_dq_combine_kernel(const float* __restrict__ dq_part,
+__global__ __launch_bounds__(64 * kCombWaves) void sparse_dq_combine_kernel(const T* __restrict__ dq_part,
                                                                             const int32_t* __restrict__ edge_u, int S,
                                                                             int rpe, int64_t ntok, int HQ, int hq_off,
                                                                             T* __restrict__ dq) {
@@ -776,7 +790,7 @@ __global__ __launch_bounds__(64 * kUnitWaves) void sparse_fwd_unit_kernel(
     const bf16* __restrict__ q, int HQ, const bf16* __restrict__ k, const bf16* __restrict__ v, int64_t cs,
     int64_t hs, int64_t rs, int HK, const int32_t* __restrict__ uniq, const int32_t* __restrict__ n_uniq,
     const int32_t* __restrict__ csr_off, const int32_t* __restrict__ csr_edge, int64_t max_u, int S, int hk0,
-    int nhk, int hq_off, int rpe, float scale_log2, float* __restrict__ o_part, float* __restrict__ lse_part,
+    int nhk, int hq_off, int rpe, float scale_log2, bf16* __restrict__ o_part, float* __restrict__ lse_part,
     const float* __restrict__ omega, const int32_t* __restrict__ row_tab) {
   using Tile = SwzTile<bf16, 64>;
   __shared__ __attribute__((aligned(1024))) char sVall[kUnitWaves][64 * 64 * 2];
@@ -879,9 +893,9 @@ __global__ __launch_bounds__(64 * kUnitWaves) void sparse_fwd_unit_kernel(
     }
     if (erow >= 0) {
       const float inv = wrow / l;
-      float* op = o_part + (int64_t)erow * kSpDh;
+      bf16* op = o_part + (int64_t)erow * kSpDh;
 #pragma unroll
-      for (int db = 0; db < 4; ++db) *reinterpret_cast<f32x4*>(op + 16 * db + 4 * g) = o[db] * inv;
+      for (int db = 0; db < 4; ++db) part_store4(op + 16 * db + 4 * g, o[db] * inv);
       if (g == 0) lse_part[erow] = m + log2f(l);
     }
   }
@@ -905,7 +919,7 @@ __global__ __launch_bounds__(64 * kBwdWaves) void sparse_bwd_unit_kernel(
     const int32_t* __restrict__ n_uniq, const int32_t* __restrict__ csr_off, const int32_t* __restrict__ csr_edge,
     int64_t max_u, int S, int hk0, int nhk, int hq_off, int rpe, int mode, const float* __restrict__ lse_row,
     float* __restrict__ delta_row, const float* __restrict__ w, float scale_log2, float scale, bf16* __restrict__ dk,
-    bf16* __restrict__ dv, int64_t ocs, int64_t ohs, int64_t ors, float* __restrict__ dq_part,
+    bf16* __restrict__ dv, int64_t ocs, int64_t ohs, int64_t ors, bf16* __restrict__ dq_part,
     float* __restrict__ dlog) {
   using Tile = SwzTile<bf16, 64>;
   constexpr int kKB = 64 * 64 * 2, kRB = 32 * 64 * 2;
@@ -1154,9 +1168,9 @@ __global__ __launch_bounds__(64 * kBwdWaves) void sparse_bwd_unit_kernel(
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb) {
       if (erow_a[qb] < 0) continue;
-      float* dst = dq_part + (int64_t)erow_a[qb] * kSpDh + 32 * wave + 4 * g;
+      bf16* dst = dq_part + (int64_t)erow_a[qb] * kSpDh + 32 * wave + 4 * g;
 #pragma unroll
-      for (int i = 0; i < 2; ++i) *reinterpret_cast<f32x4*>(dst + 16 * i) = dq[i][qb] * scale;
+      for (int i = 0; i < 2; ++i) part_store4(dst + 16 * i, dq[i][qb] * scale);
     }
   }
   // ---- dK = scale (dK^T)^T, dV: lane = key, 4 consecutive dims per store
@@ -1227,7 +1241,7 @@ bool unit_kv_aligned(const void* q, const void* k, const void* v, int64_t cs, in
 int moc::sparse_fwd_launch(int dtype, const void* q, int HQ, const void* k, const void* v, int64_t cs, int64_t hs,
                            int64_t rs, int HK, const int32_t* uniq, const int32_t* n_uniq, const int32_t* csr_off,
                            const int32_t* csr_edge, int64_t max_u, int S, int hk0, int nhk, int hq_off, int rpe,
-                           float scale, const float* omega, float* o_part, float* lse_part, hipStream_t stream,
+                           float scale, const float* omega, void* o_part, float* lse_part, hipStream_t stream,
                            const char* who, const int32_t* row_tab) {
   const float sl2 = scale * 1.4426950408889634f;
   if (dtype == MOC_BF16) {
@@ -1236,7 +1250,7 @@ int moc::sparse_fwd_launch(int dtype, const void* q, int HQ, const void* k, cons
     const int64_t units = max_u * nhk;
     hipLaunchKernelGGL(sparse_fwd_unit_kernel, dim3((unsigned)((units + kUnitWaves - 1) / kUnitWaves)),
                        dim3(64 * kUnitWaves), 0, stream, (const bf16*)q, HQ, (const bf16*)k, (const bf16*)v, cs, hs,
-                       rs, HK, uniq, n_uniq, csr_off, csr_edge, max_u, S, hk0, nhk, hq_off, rpe, sl2, o_part,
+                       rs, HK, uniq, n_uniq, csr_off, csr_edge, max_u, S, hk0, nhk, hq_off, rpe, sl2, (bf16*)o_part,
                        lse_part, omega, row_tab);
     return check_launch("sparse_fwd_unit_kernel");
   }
@@ -1244,7 +1258,7 @@ int moc::sparse_fwd_launch(int dtype, const void* q, int HQ, const void* k, cons
     dim3 grid((unsigned)max_u, (unsigned)nhk);
     hipLaunchKernelGGL(sparse_fwd_kernel<float>, grid, dim3(sp_threads<float>()), 0, stream, (const float*)q, HQ,
                        (const float*)k, (const float*)v, cs, hs, rs, HK, uniq, n_uniq, csr_off, csr_edge, S, hk0,
-                       hq_off, rpe, sl2, o_part, lse_part, omega);
+                       hq_off, rpe, sl2, (float*)o_part, lse_part, omega);
     return check_launch("sparse_fwd_kernel");
   }
   return set_error(MOC_ERR_UNSUPPORTED, "%s: dtype %d", who, dtype);
@@ -1256,7 +1270,7 @@ extern "C" {
 int moc_sparse_fwd(int dtype, const void* q, int64_t ntok, int HQ, const void* k, const void* v, int64_t cs,
                    int64_t hs, int64_t rs, int HK, int Dh, const int32_t* uniq, const int32_t* n_uniq,
                    const int32_t* csr_off, const int32_t* csr_edge, int64_t max_u, int S, int hk0, int nhk,
-                   int hq_off, int rpe, float scale, float* o_part, float* lse_part, hipStream_t stream) {
+                   int hq_off, int rpe, float scale, void* o_part, float* lse_part, hipStream_t stream) {
   MOC_REQUIRE(q && k && v && uniq && n_uniq && csr_off && csr_edge && o_part && lse_part, MOC_ERR_ARG,
               "moc_sparse_fwd: null pointer");
   MOC_REQUIRE(Dh == kSpDh, MOC_ERR_UNSUPPORTED, "moc_sparse_fwd: head_dim %d (needs 64)", Dh);
@@ -1267,7 +1281,7 @@ int moc_sparse_fwd(int dtype, const void* q, int64_t ntok, int HQ, const void* k
                                 nhk, hq_off, rpe, scale, nullptr, o_part, lse_part, stream, "moc_sparse_fwd");
 }
 
-int moc_sparse_combine(int dtype, const float* o_part, const float* lse_part, const int32_t* edge_u, const float* w,
+int moc_sparse_combine(int dtype, const void* o_part, const float* lse_part, const int32_t* edge_u, const float* w,
                        int mode, int S, int rpe, int64_t ntok, int HQ, int hq_off, void* out, float* lse_joint,
                        hipStream_t stream) {
   MOC_REQUIRE(o_part && lse_part && edge_u && out, MOC_ERR_ARG, "moc_sparse_combine: null pointer");
@@ -1281,8 +1295,8 @@ int moc_sparse_combine(int dtype, const float* o_part, const float* lse_part, co
   // routing over a batch): throughput-bound, the lighter streaming kernel keeps more rows resident
   const bool small = S <= 4 * kCombSmallPerGroup && rows <= 16384;
 #define SC(KERN, TT)                                                                                                  \
-  hipLaunchKernelGGL(KERN<TT>, grid, dim3(64 * kCombWaves), 0, stream, o_part, lse_part, edge_u, w, mode, S, rpe, ntok, \
-                     HQ, hq_off, (TT*)out, lse_joint)
+  hipLaunchKernelGGL(KERN<TT>, grid, dim3(64 * kCombWaves), 0, stream, (const TT*)o_part, lse_part, edge_u, w, mode, S, \
+                     rpe, ntok, HQ, hq_off, (TT*)out, lse_joint)
   if (dtype == MOC_BF16) {
     if (small) SC(sparse_combine_small_kernel, bf16); else SC(sparse_combine_kernel, bf16);
   } else if (dtype == MOC_F32) {
@@ -1294,7 +1308,7 @@ int moc_sparse_combine(int dtype, const float* o_part, const float* lse_part, co
   return check_launch("sparse_combine_kernel");
 }
 
-int moc_sparse_bwd_prep(int dtype, const void* dout, const void* out, const float* o_part, const int32_t* edge_u,
+int moc_sparse_bwd_prep(int dtype, const void* dout, const void* out, const void* o_part, const int32_t* edge_u,
                         int mode, int S, int rpe, int64_t ntok, int HQ, int hq_off, float* dst, hipStream_t stream) {
   MOC_REQUIRE(dout && out && edge_u && dst && (mode != 0 || o_part), MOC_ERR_ARG, "moc_sparse_bwd_prep: null pointer");
   const int64_t rows = ntok * rpe;
@@ -1302,10 +1316,10 @@ int moc_sparse_bwd_prep(int dtype, const void* dout, const void* out, const floa
   dim3 grid((unsigned)((rows + 15) / 16));
   if (dtype == MOC_BF16)
     hipLaunchKernelGGL(sparse_bwd_prep_kernel<bf16>, grid, dim3(256), 0, stream, (const bf16*)dout, (const bf16*)out,
-                       o_part, edge_u, mode, S, rpe, ntok, HQ, hq_off, dst);
+                       (const bf16*)o_part, edge_u, mode, S, rpe, ntok, HQ, hq_off, dst);
   else if (dtype == MOC_F32)
     hipLaunchKernelGGL(sparse_bwd_prep_kernel<float>, grid, dim3(256), 0, stream, (const float*)dout,
-                       (const float*)out, o_part, edge_u, mode, S, rpe, ntok, HQ, hq_off, dst);
+                       (const float*)out, (const float*)o_part, edge_u, mode, S, rpe, ntok, HQ, hq_off, dst);
   else
     return set_error(MOC_ERR_UNSUPPORTED, "moc_sparse_bwd_prep: dtype %d", dtype);
   return check_launch("sparse_bwd_prep_kernel");
@@ -1315,7 +1329,7 @@ int moc_sparse_bwd(int dtype, const void* q, const void* dout, int64_t ntok, int
                    int64_t cs, int64_t hs, int64_t rs, int HK, int Dh, const int32_t* uniq, const int32_t* n_uniq,
                    const int32_t* csr_off, const int32_t* csr_edge, int64_t max_u, int S, int hk0, int nhk,
                    int hq_off, int rpe, int mode, const float* lse_row, float* delta_row, const float* w,
-                   float scale, void* dk, void* dv, int64_t ocs, int64_t ohs, int64_t ors, float* dq_part,
+                   float scale, void* dk, void* dv, int64_t ocs, int64_t ohs, int64_t ors, void* dq_part,
                    float* dlog, hipStream_t stream) {
   MOC_REQUIRE(q && dout && k && v && uniq && n_uniq && csr_off && csr_edge && lse_row && delta_row && dk && dv &&
                   dq_part,
@@ -1337,30 +1351,30 @@ int moc_sparse_bwd(int dtype, const void* q, const void* dout, int64_t ntok, int
     const int64_t units = max_u * nhk;
     hipLaunchKernelGGL(sparse_bwd_unit_kernel, dim3((unsigned)units), dim3(64 * kBwdWaves), 0, stream, (const bf16*)q, (const bf16*)dout, HQ, (const bf16*)k,
                        (const bf16*)v, cs, hs, rs, HK, uniq, n_uniq, csr_off, csr_edge, max_u, S, hk0, nhk, hq_off,
-                       rpe, mode, lse_row, delta_row, w, sl2, scale, (bf16*)dk, (bf16*)dv, ocs, ohs, ors, dq_part,
-                       dlog);
+                       rpe, mode, lse_row, delta_row, w, sl2, scale, (bf16*)dk, (bf16*)dv, ocs, ohs, ors,
+                       (bf16*)dq_part, dlog);
     return check_launch("sparse_bwd_unit_kernel");
   } else if (dtype == MOC_F32)
     hipLaunchKernelGGL(sparse_bwd_kernel<float>, grid, dim3(sp_threads<float>()), 0, stream, (const float*)q,
                        (const float*)dout, HQ, (const float*)k, (const float*)v, cs, hs, rs, HK, uniq, n_uniq,
                        csr_off, csr_edge, S, hk0, hq_off, rpe, mode, lse_row, delta_row, w, sl2, scale, (float*)dk,
-                       (float*)dv, ocs, ohs, ors, dq_part, dlog);
+                       (float*)dv, ocs, ohs, ors, (float*)dq_part, dlog);
   else
     return set_error(MOC_ERR_UNSUPPORTED, "moc_sparse_bwd: dtype %d", dtype);
   return check_launch("sparse_bwd_kernel");
 }
 
-int moc_sparse_dq_combine(int dtype, const float* dq_part, const int32_t* edge_u, int S, int rpe, int64_t ntok,
+int moc_sparse_dq_combine(int dtype, const void* dq_part, const int32_t* edge_u, int S, int rpe, int64_t ntok,
                           int HQ, int hq_off, void* dq, hipStream_t stream) {
   MOC_REQUIRE(dq_part && edge_u && dq, MOC_ERR_ARG, "moc_sparse_dq_combine: null pointer");
   const int64_t rows = ntok * rpe;
   if (rows == 0) return MOC_OK;
   dim3 grid((unsigned)((rows + kCombWaves - 1) / kCombWaves));
   if (dtype == MOC_BF16)
-    hipLaunchKernelGGL(sparse_dq_combine_kernel<bf16>, grid, dim3(64 * kCombWaves), 0, stream, dq_part, edge_u, S, rpe, ntok, HQ,
+    hipLaunchKernelGGL(sparse_dq_combine_kernel<bf16>, grid, dim3(64 * kCombWaves), 0, stream, (const bf16*)dq_part, edge_u, S, rpe, ntok, HQ,
                        hq_off, (bf16*)dq);
   else if (dtype == MOC_F32)
-    hipLaunchKernelGGL(sparse_dq_combine_kernel<float>, grid, dim3(64 * kCombWaves), 0, stream, dq_part, edge_u, S, rpe, ntok, HQ,
+    hipLaunchKernelGGL(sparse_dq_combine_kernel<float>, grid, dim3(64 * kCombWaves), 0, stream, (const float*)dq_part, edge_u, S, rpe, ntok, HQ,
                        hq_off, (float*)dq);
   else
     return set_error(MOC_ERR_UNSUPPORTED, "moc_sparse_dq_combine: dtype %d", dtype);

@@ -122,7 +122,7 @@ def decode_attention(q: torch.Tensor, cache: MemoryDecodeCache, routing: DecodeR
     st = stream_ptr(q.device)
     NS = routing.NS
     E = B * NS
-    o_part = torch.empty(E * H, D, device=q.device, dtype=torch.float32)
+    o_part = torch.empty(E * H, D, device=q.device, dtype=cache.dtype)
     lse_part = torch.empty(E * H, device=q.device, dtype=torch.float32)
     pl = routing.plan
     call("moc_decode_partial", dt, ptr(q), B, H, ptr(cache.k_tiles), ptr(cache.v_tiles), cache.HK, D, cache.T,

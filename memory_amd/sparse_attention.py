@@ -75,7 +75,7 @@ def _forward(q, k, v, layout, segments: List[_Segment], mode: int, S: int, scale
     out = torch.empty(B, Tq, HQ, D, device=q.device, dtype=q.dtype)
     saved = []
     for sg in segments:
-        o_part = torch.empty(sg.E * sg.rpe, D, device=q.device, dtype=torch.float32)
+        o_part = torch.empty(sg.E * sg.rpe, D, device=q.device, dtype=q.dtype)   # partials in the data dtype
         lse_part = torch.empty(sg.E * sg.rpe, device=q.device, dtype=torch.float32)
         call("moc_sparse_fwd", dt, ptr(q), ntok, HQ, ptr(k), ptr(v), cs, hs, rs, HK, D, ptr(sg.plan.uniq),
              ptr(sg.plan.n_uniq), ptr(sg.plan.csr_off), ptr(sg.plan.csr_edge), sg.plan.max_u, S, sg.hk0, sg.nhk,
@@ -118,7 +118,7 @@ def _backward(q, k, v, layout, out, dout, segments, saved, mode, S, scale, dk, d
             mark = torch.empty(zero_chapters, device=q.device, dtype=torch.int32)
             call("moc_sparse_zero_untouched", dt, ptr(dk), dv_ptr, ocs, ohs, ors, zero_chapters, sg.hk0, sg.nhk,
                  ptr(sg.plan.uniq), ptr(sg.plan.n_uniq), sg.plan.max_u, ptr(mark), st)
-        dq_part = torch.empty(sg.E * sg.rpe, D, device=q.device, dtype=torch.float32)
+        dq_part = torch.empty(sg.E * sg.rpe, D, device=q.device, dtype=q.dtype)
         dlog = torch.empty(sg.E * sg.rpe, device=q.device, dtype=torch.float32) if mode in (2, 3) else None
         call("moc_sparse_bwd", dt, ptr(q), ptr(dout), ntok, HQ, ptr(k), ptr(v), cs, hs, rs, HK, D,
              ptr(sg.plan.uniq), ptr(sg.plan.n_uniq), ptr(sg.plan.csr_off), ptr(sg.plan.csr_edge), sg.plan.max_u, S,
@@ -293,7 +293,8 @@ class _TokenRouted(torch.autograd.Function):
         # every routed chapter is projected (no gather, no norm): one plain GEMM on hipBLASLt,
         # K and V read by the sparse kernels as strided column blocks of kv [Nr][2 KV]
         KV = HK * D
-        kv = F.linear(routed.to(dtype), wkv)
+        with L.region("lib_token_kv_project"):
+            kv = F.linear(routed.to(dtype), wkv)
         S = idx.shape[-1]
         segs = _segments(idx, w, mode, C, False, HQ, HK, C)
         out, saved = _forward(q, kv[:, :KV], kv[:, KV:], "rows", segs, mode, S, D ** -0.5)
@@ -323,7 +324,8 @@ class _TokenRouted(torch.autograd.Function):
             dwk = dwkv[:KV].to(wk_dtype) if need_wk else None
             dwv = dwkv[KV:].to(wv_dtype) if need_wv else None
         if need_r:
-            dr = _rows_grad(routed, dkv, wkv)
+            with L.region("lib_token_kv_dx"):
+                dr = _rows_grad(routed, dkv, wkv)
         dw = None
         if w_shape is not None and dws:
             dw = dws[0].view(w_shape) if len(dws) == 1 else torch.stack(dws, 0).sum(0).view(w_shape)
