@@ -175,7 +175,7 @@ def test_chapter_wgrad(dev, gather, shape):
         assert_parity(dw.cpu(), ref, torch.bfloat16, "dW")
 
 
-@pytest.mark.parametrize("shape", [(8192, 768, 768), (1000, 512, 256)])
+@pytest.mark.parametrize("shape", [(8192, 768, 768), (1000, 512, 256), (980, 256, 512)])
 def test_dense_wgrad_lds_dma_path(dev, shape):
     """moc_linear_wgrad on bf16 operands with N, K multiples of 256 (the chapter weight-gradient
     kernel, rows past R reading zero) against a float64 product."""
