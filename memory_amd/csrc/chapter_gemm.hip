@@ -676,10 +676,10 @@ int cg_check(const char* who, int64_t ldx, int N, int K, int64_t max_u, int64_t 
   return MOC_OK;
 }
 
-// workgroups per output tile of the weight gradients: fill the 256 CUs, but give each at least
-// 8 row blocks
-int cg_wgrad_splits(int tiles, int64_t blocks) {
-  int64_t s = 256 / tiles;
+// workgroups per output tile of the weight gradients: fill `budget` CUs (256: the chip), but give
+// each at least 8 row blocks
+int cg_wgrad_splits(int tiles, int64_t blocks, int budget = 256) {
+  int64_t s = budget / tiles;
   const int64_t by_len = (blocks + 7) / 8;
   if (s > by_len) s = by_len;
   if (s < 1) s = 1;
@@ -848,6 +848,18 @@ int moc_chapter_wgrad(const void* dkv_edge, int64_t lda, const void* red, const 
                       const int32_t* uniq, const int32_t* n_uniq, int64_t max_u, const int32_t* csr_off,
                       const int32_t* csr_edge, int N, int K, void* ws, size_t ws_bytes, int out_dtype, void* dw,
                       hipStream_t stream) {
+  return chapter_wgrad_budget(dkv_edge, lda, red, x, ldx, gather, uniq, n_uniq, max_u, csr_off, csr_edge, N, K, ws,
+                              ws_bytes, out_dtype, dw, 256, stream);
+}
+
+}  // extern "C"
+
+namespace moc {
+
+int chapter_wgrad_budget(const void* dkv_edge, int64_t lda, const void* red, const void* x, int64_t ldx, int gather,
+                         const int32_t* uniq, const int32_t* n_uniq, int64_t max_u, const int32_t* csr_off,
+                         const int32_t* csr_edge, int N, int K, void* ws, size_t ws_bytes, int out_dtype, void* dw,
+                         int budget, hipStream_t stream) {
   MOC_REQUIRE(dkv_edge && red && x && uniq && n_uniq && csr_off && csr_edge && ws && dw, MOC_ERR_ARG,
               "moc_chapter_wgrad: null pointer");
   MOC_REQUIRE(N > 0 && N % 256 == 0 && K > 0 && K % 256 == 0, MOC_ERR_UNSUPPORTED,
@@ -858,7 +870,8 @@ int moc_chapter_wgrad(const void* dkv_edge, int64_t lda, const void* red, const 
   MOC_REQUIRE(ws_bytes >= moc_chapter_wgrad_workspace(N, K, max_u), MOC_ERR_ARG, "moc_chapter_wgrad: workspace too small");
   MOC_REQUIRE(out_dtype == MOC_F32 || out_dtype == MOC_BF16, MOC_ERR_UNSUPPORTED, "moc_chapter_wgrad: out dtype %d",
               out_dtype);
-  const int tiles = (N / 256) * (K / 256), splits = cg_wgrad_splits(tiles, max_u);
+  MOC_REQUIRE(budget > 0 && budget <= 256, MOC_ERR_ARG, "chapter weight gradient: workgroup budget %d", budget);
+  const int tiles = (N / 256) * (K / 256), splits = cg_wgrad_splits(tiles, max_u, budget);
   const dim3 grid(xcd_grid((int64_t)tiles * splits));
   if (gather)
     hipLaunchKernelGGL((chapter_wgrad_kernel<CG_SRC_EDGE, CG_SRC_GATHER>), grid, dim3(kCgThreads), 0, stream,
@@ -871,6 +884,10 @@ int moc_chapter_wgrad(const void* dkv_edge, int64_t lda, const void* red, const 
   if (int rc = check_launch("chapter_wgrad_kernel")) return rc;
   return cg_wgrad_reduce(ws, splits, tiles, K, out_dtype, dw, stream);
 }
+
+}  // namespace moc
+
+extern "C" {
 
 int moc_weight_pack(const void* wk, int wk_dtype, const void* wv, int wv_dtype, int64_t kv, int64_t d, void* wkv,
                     void* wkv_t, hipStream_t stream) {

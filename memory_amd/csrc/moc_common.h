@@ -349,4 +349,11 @@ int sparse_fwd_launch(int dtype, const void* q, int HQ, const void* k, const voi
 // (router.hip's split-row reduction); returns a MOC_ status.
 int launch_split_reduce(const float* part, int nsplit, int64_t n, float inv, float* out, hipStream_t stream);
 
+// moc_chapter_wgrad with its grid held to `budget` workgroups (1..256), leaving the rest of the
+// chip to work on other streams (the layer's router backward beside the K/V weight gradient)
+int chapter_wgrad_budget(const void* dkv_edge, int64_t lda, const void* red, const void* x, int64_t ldx, int gather,
+                         const int32_t* uniq, const int32_t* n_uniq, int64_t max_u, const int32_t* csr_off,
+                         const int32_t* csr_edge, int N, int K, void* ws, size_t ws_bytes, int out_dtype, void* dw,
+                         int budget, hipStream_t stream);
+
 }  // namespace moc

@@ -1110,15 +1110,24 @@ __global__ __launch_bounds__(256) void pool_reduce_kernel(const float* __restric
   const int64_t i = (int64_t)blockIdx.x * 64 + o;
   float s = 0.f;
   if (i < n) {
+    // 32 loads in flight per thread before the first add (a reduction over a few hundred splits
+    // is then two or three rounds of memory latency, not one per eight loads: it often runs on
+    // the few CUs other kernels leave free)
     int j = g;
-    for (; j + 28 < nsplit; j += 32) {
-      float v[8];
+    for (; j + 124 < nsplit; j += 128) {
+      float v[32];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) v[u] = part[(int64_t)(j + 4 * u) * n + i];
+      for (int u = 0; u < 32; ++u) v[u] = part[(int64_t)(j + 4 * u) * n + i];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) s += v[u];
+      for (int u = 0; u < 32; ++u) s += v[u];
     }
-    for (; j < nsplit; j += 4) s += part[(int64_t)j * n + i];
+    if (j < nsplit) {
+      float v[32];
+#pragma unroll
+      for (int u = 0; u < 32; ++u) v[u] = j + 4 * u < nsplit ? part[(int64_t)(j + 4 * u) * n + i] : 0.f;
+#pragma unroll
+      for (int u = 0; u < 32; ++u) s += v[u];
+    }
   }
   q4[g][o] = s;
   __syncthreads();

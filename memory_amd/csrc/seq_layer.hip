@@ -15,9 +15,9 @@
 //                 not depend on the routing, beside the latency-bound router launches
 // backward  main: o_proj dX -> bwd prep -> dQ -> dK/dV -> multi-edge sums -> K/V weight gradient
 //                 -> dX of the projection into the chapters' bank rows
-//           aux:  o_proj dW (beside dX / dQ); after dQ: q_proj dX (into dh) and dW (beside
-//                 dK/dV); after dK/dV: the router backward and the pooling's gradient added into dh
-//           fill: the dense bank gradient's zeros (beside dQ)
+//           aux:  o_proj dW (beside dX / dQ); after dQ: q_proj dX (into dh, beside dK/dV); after
+//                 dK/dV: the router backward and the pooling's gradient added into dh
+//           fill: the dense bank gradient's zeros (beside dQ); after dQ: q_proj dW (beside dK/dV)
 // Every wait is an event: the caller's stream (main) waits for aux and fill before each call
 // returns, so to the caller both calls are ordinary stream-ordered work (also under graph capture).
 // A wait on an event that has already completed costs nothing; one the stream reaches before the
@@ -36,6 +36,10 @@ namespace {
 // stream ~3 us instead of ~4.7 us (measured with back-to-back kernels on the box).
 constexpr unsigned kSeqEventFlags = hipEventDisableTiming | hipEventDisableSystemFence;
 constexpr unsigned kTimerEventFlags = hipEventDisableSystemFence;
+// The K/V weight gradient runs on 192 of the 256 CUs (10 row splits per 256 x 256 tile instead of
+// 14): the router backward on the aux stream then runs beside it instead of after the main
+// stream's last kernel (c3: 0.936 -> 0.921 ms per step; it is ~25 us slower on its own).
+constexpr int kSeqWgradBudget = 192;
 constexpr int kSeqEvents = 8;
 
 struct DevEvents {
@@ -329,6 +333,7 @@ int moc_seq_layer_bwd(const void* h, const void* bank, const void* wr, int wr_dt
     SEQ_STAGE(kStOWgrad, aux,
               SEQ_TRY(moc_linear_wgrad(dout, attn, MOC_BF16, tok, d, d, sc + y.lw_ws, y.lw_ws_bytes, MOC_BF16, dwo,
                                        aux)));
+  MOC_HIP(hipEventRecord(ev[6], aux));  // the weight-gradient workspace is free again
   // main: o_proj dX, backward prep, dQ
   SEQ_STAGE(kStODx, main, SEQ_TRY(moc_rows_linear(dout, d, tok, sv + y.wo_t, (int)d, (int)d, d_attn, d, main)));
   SEQ_STAGE(kStPrep, main,
@@ -344,15 +349,25 @@ int moc_seq_layer_bwd(const void* h, const void* bank, const void* wr, int wr_dt
   SEQ_STAGE(kStDq, main,
             SEQ_TRY(moc_xattn_bwd_dq(MOC_BF16, q, kv, kv + y.KV, span, (int64_t)64 * KV2, 64, KV2, edge_u, omega,
                                      d_attn, lse, delta, B, L, H, HK, 64, 64, y.NS, 0.125f, dq, main)));
-  // aux: q_proj dX into dh and dW beside dK/dV.  When dK/dV is timed, its start event is the one
-  // the aux stream waits on (one record instead of two).
+  // the zeros are in place before dX stores into the bank rows (the fill ends during dQ; waited
+  // for here, before the fill stream takes more work, the wait is free -- before dX it cost ~6 us)
+  if (dbank) MOC_HIP(hipStreamWaitEvent(main, ev[2], 0));
+  // aux: q_proj dX into dh beside dK/dV; fill (done with the zeros by then): q_proj dW beside
+  // dK/dV, so that the aux stream reaches the router backward when dK/dV ends (both on aux, they
+  // ran past dK/dV's end and the router backward past the main stream's last kernel).  When
+  // dK/dV is timed, its start event is the one the side streams wait on (one record, not two).
   hipEvent_t* dkv_pair = stage_begin(kStDkv, main);
   if (!dkv_pair) MOC_HIP(hipEventRecord(ev[3], main));
-  MOC_HIP(hipStreamWaitEvent(aux, dkv_pair ? dkv_pair[0] : ev[3], 0));
+  const hipEvent_t after_dq = dkv_pair ? dkv_pair[0] : ev[3];
+  MOC_HIP(hipStreamWaitEvent(aux, after_dq, 0));
   if (dh) SEQ_STAGE(kStQDx, aux, SEQ_TRY(moc_rows_linear(dq, d, tok, sv + y.wq_t, (int)d, (int)d, dh, d, aux)));
-  if (dwq)
-    SEQ_STAGE(kStQWgrad, aux,
-              SEQ_TRY(moc_linear_wgrad(dq, h, MOC_BF16, tok, d, d, sc + y.lw_ws, y.lw_ws_bytes, MOC_BF16, dwq, aux)));
+  if (dwq) {
+    MOC_HIP(hipStreamWaitEvent(fill, after_dq, 0));
+    MOC_HIP(hipStreamWaitEvent(fill, ev[6], 0));
+    SEQ_STAGE(kStQWgrad, fill,
+              SEQ_TRY(moc_linear_wgrad(dq, h, MOC_BF16, tok, d, d, sc + y.lw_ws, y.lw_ws_bytes, MOC_BF16, dwq, fill)));
+    MOC_HIP(hipEventRecord(ev[7], fill));
+  }
   SEQ_TRY(moc_xattn_bwd_dkv(MOC_BF16, q, d_attn, kv, kv + y.KV, span, (int64_t)64 * KV2, 64, KV2, edge_u, omega, lse,
                             delta, B, L, H, HK, 64, 64, y.NS, 0.125f, dkv_edge, dom_part, main));
   // aux: the router backward from the attention's d omega and the pooling's gradient added into
@@ -377,15 +392,16 @@ int moc_seq_layer_bwd(const void* h, const void* bank, const void* wr, int wr_dt
               SEQ_TRY(moc_dkv_multi_reduce(dkv_edge, KV2, n_uniq, y.max_u, csr_off, csr_edge, red, main)));
   if (dwkv)
     SEQ_STAGE(kStKVWgrad, main,
-              SEQ_TRY(moc_chapter_wgrad(dkv_edge, KV2, red, bank, d, 1, uniq, n_uniq, y.max_u, csr_off, csr_edge, KV2,
-                                        (int)d, sc + y.cw_ws, y.cw_ws_bytes, dwkv_dtype, dwkv, main)));
+              SEQ_TRY(chapter_wgrad_budget(dkv_edge, KV2, red, bank, d, 1, uniq, n_uniq, y.max_u, csr_off, csr_edge,
+                                           KV2, (int)d, sc + y.cw_ws, y.cw_ws_bytes, dwkv_dtype, dwkv,
+                                           kSeqWgradBudget, main)));
   if (dbank) {
-    MOC_HIP(hipStreamWaitEvent(main, ev[2], 0));
     SEQ_STAGE(kStBankDx, main,
               SEQ_TRY(moc_chapter_dx(dkv_edge, KV2, uniq, n_uniq, y.max_u, csr_off, csr_edge, red, sv + y.wkv_t,
                                      (int)d, KV2, MOC_BF16, dbank, d, 1, main)));
   }
   MOC_HIP(hipStreamWaitEvent(main, ev[5], 0));
+  if (dwq) MOC_HIP(hipStreamWaitEvent(main, ev[7], 0));
   return MOC_OK;
 }
 
