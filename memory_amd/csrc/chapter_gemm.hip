@@ -486,9 +486,12 @@ __global__ __launch_bounds__(256) void weight_pack_kernel(const TK* __restrict__
 // fixed order (deterministic).  Both operands keep the reduction index (rows) outermost, so the
 // MFMA fragments (8 consecutive rows of one column per lane) come from gfx950's transposing LDS
 // load ds_read_b64_tr_b16; the stage tiles are [64 rows][256 bf16] with 16-byte chunk c of row r
-// at c ^ ((r & 3) | ((r >> 3) & 3) << 2), which spreads the 16 rows of one transposing load over
-// 16 bank groups.  Operands move global -> LDS by LDS DMA, one block ahead.
-__device__ __forceinline__ int cg_tr_swz(int r) { return (r & 3) | (((r >> 3) & 3) << 2); }
+// at c ^ (2 (r & 3) | 8 ((r >> 3) & 3)).  A 16-lane group of one transposing load reads 4 rows x 2
+// adjacent chunks and the two groups of a half-wave are 8 rows apart: the XOR puts those 16 chunks
+// on 16 distinct 4-bank groups (XOR-ing by r & 3 instead had rows r and r ^ 1 share their chunk
+// pair: 0.5 bank conflicts per access by the SQ counters, the kernel 2% slower).  Operands move
+// global -> LDS by LDS DMA, one block ahead.
+__device__ __forceinline__ int cg_tr_swz(int r) { return ((r & 3) << 1) | (((r >> 3) & 3) << 3); }
 __device__ __forceinline__ int cg_tr_off(int row, int col) {
   return row * 512 + ((((col >> 3) ^ cg_tr_swz(row)) & 31) << 4) + ((col & 7) << 1);
 }

@@ -251,6 +251,7 @@ int moc_seq_layer_fwd(const void* h, const void* bank, const void* wr, int wr_dt
   MOC_HIP(hipEventRecord(ev[0], main));
   MOC_HIP(hipStreamWaitEvent(aux, ev[0], 0));
   SEQ_STAGE(kStPackWkv, aux, SEQ_TRY(moc_weight_pack(wk, MOC_BF16, wv, MOC_BF16, y.KV, d, wkv, nullptr, aux)));
+  MOC_HIP(hipEventRecord(ev[3], aux));
   SEQ_STAGE(kStQProj, aux, SEQ_TRY(moc_rows_linear(h, d, tok, wq, (int)d, (int)d, q, d, aux)));
   MOC_HIP(hipEventRecord(ev[1], aux));
   SEQ_STAGE(kStPackT, aux, {
@@ -270,10 +271,14 @@ int moc_seq_layer_fwd(const void* h, const void* bank, const void* wr, int wr_dt
   SEQ_STAGE(kStPlan, main,
             SEQ_TRY(moc_chapter_plan(idx_star, y.E, C, sv + y.plan_ws, y.plan_ws_bytes, uniq, n_uniq, edge_u, csr_off,
                                      csr_edge, main)));
-  // main: K/V projection (gather fused), attention, o_proj
-  MOC_HIP(hipStreamWaitEvent(main, ev[1], 0));
+  // main: K/V projection (gather fused), attention, o_proj.  The projection waits for the [Wk; Wv]
+  // pack only and the attention for the q projection: both events have completed when the main
+  // stream reaches them, so the waits cost nothing (the q projection ends about when the router
+  // does, and waiting for it before the projection cost ~6 us of wake-up).
+  MOC_HIP(hipStreamWaitEvent(main, ev[3], 0));
   SEQ_STAGE(kStKVProj, main,
             SEQ_TRY(moc_chapter_project(bank, d, 1, uniq, n_uniq, y.max_u, wkv, KV2, (int)d, kv, KV2, main)));
+  MOC_HIP(hipStreamWaitEvent(main, ev[1], 0));
   const int64_t span = y.max_u * 64 * KV2 - y.KV;
   SEQ_STAGE(kStAttnFwd, main,
             SEQ_TRY(moc_xattn_fwd(MOC_BF16, q, kv, kv + y.KV, span, (int64_t)64 * KV2, 64, KV2, edge_u, omega, B, L,
