@@ -19,10 +19,10 @@ pytestmark = pytest.mark.gpu
 C1 = dict(B=2, L=128, d=256, H=4, C=33, T=64, S=1, k=4, s=2.5)
 
 
-def _config1_inputs(scale_w=0.02):
+def _config1_inputs(scale_w=0.02, L=None):
     torch.manual_seed(0)
     c = C1
-    h = torch.randn(c["B"], c["L"], c["d"])
+    h = torch.randn(c["B"], L or c["L"], c["d"])
     bank = torch.randn(c["C"] * c["T"], c["d"]) * 0.02
     Wr = torch.randn(c["C"], c["d"]) * scale_w
     Wq, Wk, Wv, Wo = (torch.randn(c["d"], c["d"]) * scale_w for _ in range(4))
@@ -54,18 +54,20 @@ def _layer(dev, dtype, Wr, br, Wq, Wk, Wv, Wo, normalize, strategy="sequence", w
                                          (torch.bfloat16, "python"), (torch.bfloat16, "per-op")])
 @pytest.mark.parametrize("normalize,strategy,window", [(False, "sequence", None), (True, "sequence", None),
                                                        (False, "sequence-rolling", 16)])
-def test_config1_layer_forward_backward(gpu_device, monkeypatch, dtype, fused, normalize, strategy, window):
+@pytest.mark.parametrize("Lq", [128, 96])
+def test_config1_layer_forward_backward(gpu_device, monkeypatch, dtype, fused, normalize, strategy, window, Lq):
     """bf16 runs the whole-layer autograd function (memory_amd.seq_layer) with its native
     schedule (moc_seq_layer_fwd / _bwd; a normalised bank takes the Python-scheduled one) and
     with the Python-scheduled one, and the per-op functions; fp32 always takes the per-op path."""
     from memory_amd import seq_layer
-    print(f"config1 layer dtype={dtype} fused={fused} normalize={normalize} strategy={strategy}", flush=True)
+    print(f"config1 layer dtype={dtype} fused={fused} normalize={normalize} strategy={strategy} L={Lq}", flush=True)
     monkeypatch.setattr(seq_layer, "NATIVE", fused == "native")
     dev = gpu_device
     c = C1
     # larger router / projection weights than the 0.02 recipe so that every gradient is well
     # above rounding noise (the recipe's o_proj of std 0.02 makes outputs ~1e-4)
-    h, bank, Wr, br, Wq, Wk, Wv, Wo = _config1_inputs(scale_w=0.08)
+    # (L = 96: rows of delta / lse padded to 128 in the native backward)
+    h, bank, Wr, br, Wq, Wk, Wv, Wo = _config1_inputs(scale_w=0.08, L=Lq)
     bank = bank * 25.0
     layer = _layer(dev, dtype, Wr, br, Wq, Wk, Wv, Wo, normalize, strategy, window)
     layer.fused = fused != "per-op"
