@@ -306,16 +306,21 @@ __global__ __launch_bounds__(64 * kCombWaves) void sparse_combine_small_kernel(
   const int64_t tok = row / rpe;
   const int r = (int)(row % rpe);
   const int g = lane >> 4, sub = lane & 15;
-  // slot values (lane s holds slot s and s + 64)
+  // slot values (lane s holds slot s and s + 64); the slot's id, lse and weight are loaded
+  // together for every slot in range (the buffers hold every (token, slot, row) entry) and the
+  // skipped slots masked afterwards, so they take one round of memory latency, not two
   float lg[2];
   bool ok[2];
 #pragma unroll
   for (int q = 0; q < 2; ++q) {
     const int sl = lane + 64 * q;
     const int64_t e = tok * S + sl;
-    ok[q] = sl < S && edge_u[e] >= 0;
-    lg[q] = 0.f;
-    if (ok[q]) lg[q] = mode == 0 ? w[e] : lse_part[e * rpe + r] + sp_logw(mode, w ? w[e] : 1.f);
+    const bool in = sl < S;
+    const int eu = in ? edge_u[e] : -1;
+    const float lp = in && mode != 0 ? lse_part[e * rpe + r] : 0.f;
+    const float we = in && w ? w[e] : 1.f;
+    ok[q] = in && eu >= 0;
+    lg[q] = !ok[q] ? 0.f : mode == 0 ? we : lp + sp_logw(mode, we);
   }
   // partial rows of this lane group's slots, all in flight
   f32x4 v[kCombSmallPerGroup];

@@ -178,7 +178,11 @@ class DecodeStepGraph:
                 for (attn, cache, routing), x in zip(self.layers, self.static_in)]
 
     def run(self, inputs):
+        """Replay with ``inputs`` (copied into the captured input buffers unless they are those
+        buffers: a serving loop that writes each token's hidden states into ``static_in``
+        directly replays with no copies)."""
         for buf, x in zip(self.static_in, inputs):
-            buf.copy_(x)
+            if x.data_ptr() != buf.data_ptr():
+                buf.copy_(x)
         self.graph.replay()
         return self.static_out

@@ -79,3 +79,12 @@ def test_decode_step_graph_replays_match_eager(gpu_device, dtype):
         for i, (o, r) in enumerate(zip(outs, ref)):
             assert torch.equal(o, r), f"replay {rep}, layer {i}"
         del junk
+    # hidden states written straight into the captured input buffers: replayed without copies
+    for rep in range(2):
+        for buf in graph.static_in:
+            buf.copy_(torch.randn(B, 1, d, generator=g).to(dev, dtype))
+        outs = [o.clone() for o in graph.run(graph.static_in)]
+        torch.cuda.synchronize()
+        ref = [memory_decode_step(a, x.clone(), c, r) for (a, c, r), x in zip(layers, graph.static_in)]
+        for i, (o, r) in enumerate(zip(outs, ref)):
+            assert torch.equal(o, r), f"in-place replay {rep}, layer {i}"
