@@ -680,11 +680,12 @@ __global__ __launch_bounds__(256) void bank_grad_mark_kernel(const int32_t* __re
 }
 
 // Zero fill of the dense bank gradient by a few single-wave workgroups (one per CU by
-// default), 4 x 16 bytes per lane per iteration.  Launched on a second stream beside the dQ
-// kernel, its waves sit beside the attention-backward waves (16 VGPRs, no LDS) and use HBM
-// bandwidth those MFMA / VALU-bound kernels leave idle.  The stores are non-temporal
-// (global_store ... nt), so the zeros stream past the L2s instead of evicting the K/V tiles
-// the attention kernels re-read there (c3: the fill beside dQ 155 -> ~110 us, dQ 221 -> 193 us).
+// default), 4 x 16 bytes per lane per iteration.  Launched on a side stream beside the
+// attention backward (the layer's dK/dV kernel), its waves sit beside the attention-backward
+// waves (16 VGPRs, no LDS) and use HBM bandwidth those MFMA / VALU-bound kernels leave idle.  The
+// stores are non-temporal (global_store ... nt), so the zeros stream past the L2s instead of
+// evicting the tiles the attention kernels re-read there (c3, beside dQ: the fill 155 -> ~110 us,
+// dQ 221 -> 193 us).
 __global__ __launch_bounds__(64) void fill_zero_kernel(V16* __restrict__ dst, int64_t n16) {
   const int64_t stride = (int64_t)gridDim.x * 64;
   int64_t i = (int64_t)blockIdx.x * 64 + threadIdx.x;
