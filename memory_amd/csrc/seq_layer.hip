@@ -17,7 +17,7 @@
 //                 -> dX of the projection into the chapters' bank rows
 //           aux:  o_proj dW (beside dX / dQ); after dQ: q_proj dX (into dh, beside dK/dV); after
 //                 dK/dV: the router backward and the pooling's gradient added into dh
-//           fill: after dQ: the dense bank gradient's zeros, then q_proj dW (beside dK/dV)
+//           fill: the dense bank gradient's zeros (beside dQ); after dQ: q_proj dW (beside dK/dV)
 // Every wait is an event: the caller's stream (main) waits for aux and fill before each call
 // returns, so to the caller both calls are ordinary stream-ordered work (also under graph capture).
 // A wait on an event that has already completed costs nothing; one the stream reaches before the
@@ -343,9 +343,20 @@ int moc_seq_layer_bwd(const void* h, const void* bank, const void* wr, int wr_dt
   SEQ_STAGE(kStODx, main, SEQ_TRY(moc_rows_linear(dout, d, tok, sv + y.wo_t, (int)d, (int)d, d_attn, d, main)));
   SEQ_STAGE(kStPrep, main,
             SEQ_TRY(moc_xattn_bwd_prep(MOC_BF16, q, attn, d_attn, B, L, H, 64, delta, nullptr, nullptr, main)));
+  // fill: the dense bank gradient's zeros beside dQ (started with the backward, beside o_proj's
+  // dX and dW, it slowed o_proj's dW 55 -> 116 us and the step by 25 us)
+  if (dbank) {
+    MOC_HIP(hipEventRecord(ev[1], main));
+    MOC_HIP(hipStreamWaitEvent(fill, ev[1], 0));
+    SEQ_STAGE(kStFill, fill, SEQ_TRY(moc_fill_zero(dbank, bank_rows * d * 2, fill_cus(), fill)));
+    MOC_HIP(hipEventRecord(ev[2], fill));
+  }
   SEQ_STAGE(kStDq, main,
             SEQ_TRY(moc_xattn_bwd_dq(MOC_BF16, q, kv, kv + y.KV, span, (int64_t)64 * KV2, 64, KV2, edge_u, omega,
                                      d_attn, lse, delta, B, L, H, HK, 64, 64, y.NS, 0.125f, dq, main)));
+  // the zeros are in place before dX stores into the bank rows (the fill ends during dQ; waited
+  // for here, before the fill stream takes more work, the wait is free -- before dX it cost ~6 us)
+  if (dbank) MOC_HIP(hipStreamWaitEvent(main, ev[2], 0));
   // aux: q_proj dX into dh beside dK/dV; fill (done with the zeros by then): q_proj dW beside
   // dK/dV, so that the aux stream reaches the router backward when dK/dV ends (both on aux, they
   // ran past dK/dV's end and the router backward past the main stream's last kernel).  When
@@ -355,14 +366,6 @@ int moc_seq_layer_bwd(const void* h, const void* bank, const void* wr, int wr_dt
   const hipEvent_t after_dq = dkv_pair ? dkv_pair[0] : ev[3];
   MOC_HIP(hipStreamWaitEvent(aux, after_dq, 0));
   if (dh) SEQ_STAGE(kStQDx, aux, SEQ_TRY(moc_rows_linear(dq, d, tok, sv + y.wq_t, (int)d, (int)d, dh, d, aux)));
-  // fill: the dense bank gradient's zeros beside dK/dV (beside dQ they slowed it 175 -> ~190 us and
-  // cost a record on the main stream; started with the backward, beside o_proj's dX and dW, they
-  // slowed o_proj's dW 55 -> 116 us), then q_proj's dW
-  if (dbank) {
-    MOC_HIP(hipStreamWaitEvent(fill, after_dq, 0));
-    SEQ_STAGE(kStFill, fill, SEQ_TRY(moc_fill_zero(dbank, bank_rows * d * 2, fill_cus(), fill)));
-    MOC_HIP(hipEventRecord(ev[2], fill));
-  }
   if (dwq) {
     MOC_HIP(hipStreamWaitEvent(fill, after_dq, 0));
     MOC_HIP(hipStreamWaitEvent(fill, ev[6], 0));
@@ -398,7 +401,6 @@ int moc_seq_layer_bwd(const void* h, const void* bank, const void* wr, int wr_dt
                                            KV2, (int)d, sc + y.cw_ws, y.cw_ws_bytes, dwkv_dtype, dwkv,
                                            kSeqWgradBudget, main)));
   if (dbank) {
-    MOC_HIP(hipStreamWaitEvent(main, ev[2], 0));  // the zeros are in place (they end during dK/dV)
     SEQ_STAGE(kStBankDx, main,
               SEQ_TRY(moc_chapter_dx(dkv_edge, KV2, uniq, n_uniq, y.max_u, csr_off, csr_edge, red, sv + y.wkv_t,
                                      (int)d, KV2, MOC_BF16, dbank, d, 1, main)));

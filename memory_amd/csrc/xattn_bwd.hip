@@ -681,7 +681,7 @@ __global__ __launch_bounds__(256) void bank_grad_mark_kernel(const int32_t* __re
 
 // Zero fill of the dense bank gradient by a few single-wave workgroups (one per CU by
 // default), 4 x 16 bytes per lane per iteration.  Launched on a side stream beside the
-// attention backward (the layer's dK/dV kernel), its waves sit beside the attention-backward
+// attention backward (the layer's dQ kernel), its waves sit beside the attention-backward
 // waves (16 VGPRs, no LDS) and use HBM bandwidth those MFMA / VALU-bound kernels leave idle.  The
 // stores are non-temporal (global_store ... nt), so the zeros stream past the L2s instead of
 // evicting the tiles the attention kernels re-read there (c3, beside dQ: the fill 155 -> ~110 us,
