@@ -149,15 +149,20 @@ __global__ __launch_bounds__(kBThreads) void xattn_bwd_dq_kernel(
       kio.load_rows(kb, tile_off(u_next), row_bytes, tid);
       vio.load_rows(vb, tile_off(u_next), row_bytes, tid);
     }
-    if (u_cur >= 0) {
+    // a slot of zero router weight has dS = 0 (its keys and values are zero): no dQ contribution
+    const float w = u_cur >= 0 ? om[s] : 0.f;
+    if (w > 0.f) {
       const char* sKc = sK[buf];
       const char* sVc = sV[buf];
-      const float w = om[s];
       const float c = w * scale_log2;
-      const float dsc = w * scale;
-      // ds * dsc = p * (w dP - delta) * dsc = p * (dP * (w dsc) - delta * dsc)
-      const float wd = w * dsc;
-      const float dlc[2] = {dl[0] * dsc, dl[1] * dsc};
+      // ds * dsc = p (w dP - delta) dsc = (p wd) (dP - delta / w) with wd = w dsc = w^2 scale:
+      // p wd = exp2(c s - lse + log2 wd) takes the factor in the exponent's constant, and the dP
+      // accumulators start at -delta / w (the MFMA's C operand), so dS is one multiply
+      const float lwd = __builtin_amdgcn_logf(w * w * scale);
+      const float offc[2] = {lse2[0] - lwd, lse2[1] - lwd};
+      const float iw = __builtin_amdgcn_rcpf(w);
+      const f32x4 dinit[2] = {f32x4{-dl[0] * iw, -dl[0] * iw, -dl[0] * iw, -dl[0] * iw},
+                              f32x4{-dl[1] * iw, -dl[1] * iw, -dl[1] * iw, -dl[1] * iw}};
       // the chapter's 64 keys in two halves of 32 (one dQ k-step each), which halves the
       // score registers and lets three waves share a SIMD
 #pragma unroll
@@ -168,7 +173,7 @@ __global__ __launch_bounds__(kBThreads) void xattn_bwd_dq_kernel(
 #pragma unroll
           for (int qb = 0; qb < 2; ++qb) {
             st[kbl][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
-            dp[kbl][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
+            dp[kbl][qb] = dinit[qb];
           }
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
@@ -191,8 +196,8 @@ __global__ __launch_bounds__(kBThreads) void xattn_bwd_dq_kernel(
           for (int kbl = 0; kbl < 2; ++kbl)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-              const float p = __builtin_amdgcn_exp2f(st[kbl][qb][e] * c - lse2[qb]);
-              dsf[qb][4 * kbl + e] = from_f<T>(p * (dp[kbl][qb][e] * wd - dlc[qb]));
+              const float pw = __builtin_amdgcn_exp2f(st[kbl][qb][e] * c - offc[qb]);
+              dsf[qb][4 * kbl + e] = from_f<T>(pw * dp[kbl][qb][e]);
             }
 #pragma unroll
         for (int db = 0; db < 4; ++db) {
