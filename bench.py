@@ -841,6 +841,9 @@ def main():
     ap.add_argument("--variants", default="reference_style,bank_adamw_dense,bank_adamw",
                     help="c3opt: which optimizer variants to run (comma-separated)")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
+    ap.add_argument("--no-losses-timing", action="store_true",
+                    help="c4: skip the router-loss comparison (fused kernels vs unfused torch ops) that "
+                         "follows the timed steps, so that a kernel trace holds the step's kernels only")
     ap.add_argument("--headline-only", action="store_true",
                     help="c3: skip the c5 decode and c4 token-level lines that ride along the headline")
     ap.add_argument("--pmc-summary", nargs="+", metavar="CSV",
@@ -877,7 +880,8 @@ def main():
         del src, dst
 
     if args.workload != "c3":
-        run = {"c4": run_c4, "c5": run_c5, "c3opt": run_c3opt, "c3block": run_c3block}[args.workload]
+        run = {"c4": lambda a: run_c4(a, losses_timing=not a.no_losses_timing), "c5": run_c5, "c3opt": run_c3opt,
+               "c3block": run_c3block}[args.workload]
         print(json.dumps(run(args)), flush=True)
         return
 

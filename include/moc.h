@@ -113,6 +113,15 @@ int moc_router_linear_bwd(const float* dz, const float* x, int64_t R, int64_t d,
                           int64_t C, float* dx, float* dW, float* db, void* workspace, size_t workspace_bytes,
                           hipStream_t stream);
 
+/* The per-token router's logit gradient dz f32 [R, C] as the bf16 operand of its backward
+ * products (the input and weight gradients of ``self.router(hidden_states)``, router.py:294):
+ * dzp bf16 [R, Cp] (row stride Cp, even, >= C; columns C .. Cp-1 zero), and when db != NULL the
+ * bias gradient db f32 [C] = sum over rows of dz (fp32, fixed order; workspace from
+ * moc_logit_grad_pack_workspace).  One read of dz. */
+size_t moc_logit_grad_pack_workspace(int64_t R, int64_t C);
+int moc_logit_grad_pack(const float* dz, int64_t R, int64_t C, int64_t Cp, void* dzp, float* db, void* workspace,
+                        size_t workspace_bytes, hipStream_t stream);
+
 /* Replaces ChapterRouter._compute_losses (router.py:197-260) for rows of logits f32 [R, C] and
  * the selected chapter ids idx i32 [R, k] (entries outside [0, C) are ignored):
  * losses f32 [4] = {load_balance, auxiliary, z_loss, entropy} with p = softmax(logits) per row,
@@ -150,7 +159,10 @@ int moc_chapter_plan(const int32_t* chap, int64_t E, int64_t C, void* workspace,
  * of the library (one per GPU, held until the process ends), so E and C are limited to
  * moc_chapter_plan_workspace(E, C) <= 4 MiB (e.g. E <= 258,048 edges over 4,097 chapters);
  * larger plans return MOC_ERR_UNSUPPORTED.  Every call on a GPU shares that array: calls that
- * overlap on one GPU (concurrent streams) race and must not be issued. */
+ * overlap on one GPU (concurrent streams) race and must not be issued.  The first call on each
+ * device looks the array's device address up (hipGetSymbolAddress): make it outside stream
+ * capture; later calls only launch kernels (no memset, no allocation) and may be captured into a
+ * HIP graph and replayed. */
 int moc_chapter_plan_noalloc(const int32_t* chap, int64_t E, int64_t C, int32_t* uniq, int32_t* n_uniq,
                              int32_t* edge_u, int32_t* csr_off, int32_t* csr_edge, hipStream_t stream);
 
@@ -209,6 +221,20 @@ int moc_chapter_dx(const void* dkv_edge, int64_t ld, const int32_t* uniq, const 
  * transposed weight).  N % 256 == 0, K % 64 == 0. */
 int moc_rows_linear(const void* x, int64_t ldx, int64_t R, const void* w, int N, int K, void* y, int64_t ldy,
                     hipStream_t stream);
+/* y [R][N] = res [R][N] + x [R][K] w^T in one GEMM (bf16 in and out, the residual added to the
+ * fp32 product before the one rounding): the memory sublayer's o_proj with its residual add,
+ * memory_transformer/memory_block.py:549-558 (``hidden_states = residual + mem_output`` after
+ * memory_attention.py:456 ``self.o_proj(attn_output)``).  res row stride ldr (a multiple of 8,
+ * 16-byte aligned); res may equal y (each element is read before it is written, by the same
+ * lane).  N % 256 == 0, K % 64 == 0. */
+int moc_rows_linear_residual(const void* x, int64_t ldx, int64_t R, const void* w, int N, int K, const void* res,
+                             int64_t ldr, void* y, int64_t ldy, hipStream_t stream);
+/* y [R][N] f32 = x [R][K] w^T (+ bias [N] f32 when bias != NULL) for any N (w [N][K] bf16, K % 64
+ * == 0; y row stride ldy >= N, any value): the per-token router logits, ``self.router(hidden)``
+ * of ChapterRouter.route_token_level (memory_transformer/router.py:294), with operands in bf16
+ * and the logits accumulated and kept in fp32. */
+int moc_rows_linear_f32(const void* x, int64_t ldx, int64_t R, const void* w, int N, int K, const float* bias,
+                        float* y, int64_t ldy, hipStream_t stream);
 /* The memory sublayer's memory_layernorm folded into its q projection (memory_block.py:549-558:
  * q_proj(memory_layernorm(hidden)); RMSNorm memory_block.py:18-28 or nn.LayerNorm): y = norm(x) W^T
  * for x [R, K] bf16 (row stride ldx) without writing the normalised rows.  moc_norm_fold_weight

@@ -68,6 +68,10 @@ _SIGS = {
     "moc_weight_pack": (_I, [_P, _I, _P, _I, _I64, _I64, _P, _P, _P]),
     "moc_dkv_multi_reduce": (_I, [_P, _I64, _P, _I64, _P, _P, _P, _P]),
     "moc_rows_linear": (_I, [_P, _I64, _I64, _P, _I, _I, _P, _I64, _P]),
+    "moc_logit_grad_pack_workspace": (_SZ, [_I64, _I64]),
+    "moc_logit_grad_pack": (_I, [_P, _I64, _I64, _I64, _P, _P, _P, _SZ, _P]),
+    "moc_rows_linear_residual": (_I, [_P, _I64, _I64, _P, _I, _I, _P, _I64, _P, _I64, _P]),
+    "moc_rows_linear_f32": (_I, [_P, _I64, _I64, _P, _I, _I, _P, _P, _I64, _P]),
     "moc_norm_fold_weight": (_I, [_P, _I, _I, _P, _P, _P, _P, _P, _P]),
     "moc_rows_linear_norm": (_I, [_P, _I64, _I64, _P, _I, _I, _I, _F, _P, _P, _P, _I64, _P, _P, _P]),
     "moc_chapter_wgrad_workspace": (_SZ, [_I, _I, _I64]),

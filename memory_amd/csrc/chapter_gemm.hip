@@ -125,16 +125,32 @@ struct CgNorm {
   float* rstd_out;  // [rows] or null
 };
 
-template <int SRC, int DST, typename TO, int BM, int DEPTH, int NORM = MOC_NORM_NONE, int BN = 256>
+// Epilogue options of the contiguous rows GEMM (bit flags): EPI_RES adds residual rows (bf16, the
+// output's row indexing, row stride ldr) to the fp32 product before the one rounding to bf16;
+// EPI_BIAS adds a per-feature f32 bias; EPI_MASKN allows any N (the W rows past N read zero, the
+// output columns past N are not stored; fp32 output by element stores, so any row stride).
+enum { CG_EPI_RES = 1, CG_EPI_BIAS = 2, CG_EPI_MASKN = 4 };
+struct CgEpi {
+  const bf16* res;
+  int64_t ldr;
+  const float* bias;
+};
+
+template <int SRC, int DST, typename TO, int BM, int DEPTH, int NORM = MOC_NORM_NONE, int BN = 256, int EPI = 0>
 __global__ __launch_bounds__(kCgThreads) void chapter_gemm_kernel(
     const bf16* __restrict__ x, const bf16* __restrict__ xred, int64_t ldx, const int32_t* __restrict__ uniq,
     const int32_t* __restrict__ n_uniq, const int32_t* __restrict__ csr_off, const int32_t* __restrict__ csr_edge,
     int64_t max_u, const bf16* __restrict__ w, int N, int K, TO* __restrict__ y, int64_t ldy, int64_t xrows,
-    int64_t yrows, CgNorm nrm = CgNorm{}) {
+    int64_t yrows, CgNorm nrm = CgNorm{}, CgEpi ep = CgEpi{}) {
   static_assert(NORM == MOC_NORM_NONE || (SRC == CG_SRC_CONTIG && DST == CG_DST_CONTIG && BM == 128 &&
                                           sizeof(TO) == 2),
                 "row normalisation: contiguous rows, 128-row tiles, bf16 output");
   static_assert(BN == 256 || BN == 384, "feature tile");
+  static_assert(EPI == 0 || (SRC == CG_SRC_CONTIG && DST == CG_DST_CONTIG && NORM == MOC_NORM_NONE),
+                "epilogue options: contiguous rows GEMM");
+  static_assert(!(EPI & CG_EPI_RES) || sizeof(TO) == 2, "residual rows: bf16 output");
+  static_assert(!(EPI & (CG_EPI_BIAS | CG_EPI_MASKN)) || sizeof(TO) == 4, "bias / any N: fp32 output");
+  static_assert(!(EPI & CG_EPI_MASKN) || BN == 256, "any N: 256-feature tiles");
   constexpr int CPT = BM / 64;              // chapters per tile
   constexpr int IPX = BM / 64;              // X DMA instructions per thread per stage
   constexpr int FT = BN / 64;               // 16-feature MFMA tiles per wave (= W DMA instructions per thread)
@@ -143,17 +159,20 @@ __global__ __launch_bounds__(kCgThreads) void chapter_gemm_kernel(
   constexpr int STX = BM * 128;             // LDS bytes of one X stage
   constexpr int NBUF = DEPTH + 1;           // LDS buffers per operand
   constexpr int kBatch = FT + IPX;          // DMA instructions per wave and stage (W, then X)
-  static_assert(NBUF * (STW + STX) <= 163840, "LDS");
+  // any N: each wave's 16-row x 64-feature fp32 output block is staged in 4 KB of LDS so that the
+  // stores go out as whole row pieces (element stores: any row stride)
+  constexpr int EPI_LDS = (EPI & CG_EPI_MASKN) ? 8 * 4096 : 0;
+  static_assert(NBUF * (STW + STX) + EPI_LDS <= 163840, "LDS");
   static_assert(DEPTH >= 1 && (DEPTH == 1 || (DEPTH - 1) * kBatch == 5 || (DEPTH - 1) * kBatch == 6 ||
                                (DEPTH - 1) * kBatch == 8), "cg_wait_vm count");
-  __shared__ __attribute__((aligned(1024))) char smem[NBUF * (STW + STX)];
+  __shared__ __attribute__((aligned(1024))) char smem[NBUF * (STW + STX) + EPI_LDS];
   char* const sW = smem;
   char* const sX = smem + NBUF * STW;
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = rfl(tid >> 6);
   const int nu = n_uniq ? rfl((int)min((int64_t)n_uniq[0], max_u)) : (int)max_u;
-  const int NB = N / BN;
+  const int NB = (EPI & CG_EPI_MASKN) ? (N + BN - 1) / BN : N / BN;
   const int V = ((nu + CPT - 1) / CPT) * NB;  // tiles: row blocks x feature blocks
   const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3, nslot = gridDim.x >> 3;
   const int lo = (int)(((int64_t)xcd * V) >> 3), hi = (int)(((int64_t)(xcd + 1) * V) >> 3);
@@ -175,10 +194,12 @@ __global__ __launch_bounds__(kCgThreads) void chapter_gemm_kernel(
   auto issue_w = [&](int s) {
     const int t = lo + slot + nslot * (s / nk), kt = s % nk;
     const int nb = t % NB;
-    const __amdgpu_buffer_rsrc_t wres = CG_RSRC(w + (int64_t)nb * BN * K, (uint32_t)(BN * K * 2));
+    // (any N: the rows of the last feature block past N read zero)
+    const __amdgpu_buffer_rsrc_t wres = CG_RSRC(w + (int64_t)nb * BN * K, (uint32_t)(min(BN, N - nb * BN) * K * 2));
     const char* dst = sW + (s % NBUF) * STW + wave * 1024;
+    // the row offset of instruction i rides in the per-lane offset, which the buffer bound checks
 #pragma unroll
-    for (int i = 0; i < FT; ++i) cg_dma16(wres, woff, (uint32_t)(kt * 128 + 64 * i * K * 2), dst + 8192 * i);
+    for (int i = 0; i < FT; ++i) cg_dma16(wres, woff + (uint32_t)(64 * i * K * 2), (uint32_t)(kt * 128), dst + 8192 * i);
   };
   auto issue_x = [&](int s) {
     const int t = lo + slot + nslot * (s / nk), kt = s % nk;
@@ -212,20 +233,34 @@ __global__ __launch_bounds__(kCgThreads) void chapter_gemm_kernel(
   // X stage; the four partial sums of a row are combined at the tile's end into sStat
   __shared__ float2 sStat[NORM != MOC_NORM_NONE ? BM : 1];
   float st_x = 0.f, st_xx = 0.f;
+  // LayerNorm: the sums are taken around a pivot, the row's first element (read at the tile's
+  // first stage), so var = E[(x - p)^2] - (E[x - p])^2 does not cancel for rows whose mean is
+  // large against their spread; RMSNorm needs sum x^2 only (no cancellation)
+  float st_p = 0.f;
   const int st_row = tid >> 2, st_part = tid & 3;
-  auto stats_stage = [&](const char* sx) {
+  auto stats_stage = [&](const char* sx, bool first) {
     typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
     typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+    if constexpr (NORM == MOC_NORM_LAYERNORM) {
+      if (first) st_p = (float)*reinterpret_cast<const __bf16*>(sx + st_row * 128 + ((st_row & 7) << 4));
+    }
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int pc = (2 * st_part + h) ^ (st_row & 7);
       const bf16x8_t v8 = *reinterpret_cast<const bf16x8_t*>(sx + st_row * 128 + (pc << 4));
+      if constexpr (NORM == MOC_NORM_LAYERNORM) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const bf16x2_t p2 = bf16x2_t{v8[2 * e], v8[2 * e + 1]};
-        st_xx = __builtin_amdgcn_fdot2_f32_bf16(p2, p2, st_xx, false);
-        if constexpr (NORM == MOC_NORM_LAYERNORM)
-          st_x = __builtin_amdgcn_fdot2_f32_bf16(p2, bf16x2_t{(__bf16)1.f, (__bf16)1.f}, st_x, false);
+        for (int e = 0; e < 8; ++e) {
+          const float dx = (float)v8[e] - st_p;
+          st_x += dx;
+          st_xx = fmaf(dx, dx, st_xx);
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const bf16x2_t p2 = bf16x2_t{v8[2 * e], v8[2 * e + 1]};
+          st_xx = __builtin_amdgcn_fdot2_f32_bf16(p2, p2, st_xx, false);
+        }
       }
     }
   };
@@ -240,8 +275,9 @@ __global__ __launch_bounds__(kCgThreads) void chapter_gemm_kernel(
     }
     if (st_part == 0) {
       const float inv_k = 1.f / (float)K;
-      const float mean = NORM == MOC_NORM_LAYERNORM ? st_x * inv_k : 0.f;
-      const float var = NORM == MOC_NORM_LAYERNORM ? fmaxf(st_xx * inv_k - mean * mean, 0.f) : st_xx * inv_k;
+      const float dmean = NORM == MOC_NORM_LAYERNORM ? st_x * inv_k : 0.f;  // mean - pivot
+      const float mean = st_p + dmean;
+      const float var = NORM == MOC_NORM_LAYERNORM ? fmaxf(st_xx * inv_k - dmean * dmean, 0.f) : st_xx * inv_k;
       const float rstd = rsqrtf(var + nrm.eps);
       sStat[st_row] = float2{mean, rstd};
       const int rb = t / NB, nb = t - rb * NB;
@@ -292,12 +328,52 @@ __global__ __launch_bounds__(kCgThreads) void chapter_gemm_kernel(
       const int64_t yr = DST == CG_DST_CONTIG ? min((int64_t)64, yrows - (int64_t)cc * 64) : 64;
       const __amdgpu_buffer_rsrc_t yres = CG_RSRC(dst, live ? (uint32_t)(yr * ldy * sizeof(TO)) : 0u);
       const uint32_t vrow = (uint32_t)((((rt & 63) + m) * ldy + nb * BN + 16 * FT * wf + 8 * g) * sizeof(TO));
+      __amdgpu_buffer_rsrc_t rres = yres;
+      uint32_t rrow = 0;
+      if constexpr ((EPI & CG_EPI_RES) != 0) {
+        rres = CG_RSRC(ep.res + (int64_t)cc * 64 * ep.ldr, live ? (uint32_t)(yr * ep.ldr * 2) : 0u);
+        rrow = (uint32_t)((((rt & 63) + m) * ep.ldr + nb * BN + 16 * FT * wf + 8 * g) * 2);
+      }
 #pragma unroll
       for (int p = 0; p < FT / 2; ++p) {
         typedef int i32x4 __attribute__((ext_vector_type(4)));
-        if constexpr (sizeof(TO) == 2) {
+        if constexpr ((EPI & CG_EPI_MASKN) != 0) {
+          // 16-byte chunk (8p + 2g + h) of row m (acc[2p + h]: features 32p + 8g + 4h .. + 3 of the
+          // wave's 64) at chunk position (8p + 2g + h) ^ m of the row's 256 bytes: the 16 rows a
+          // chunk column spans sit on distinct banks
+          float* sE = reinterpret_cast<float*>(smem + NBUF * (STW + STX)) + wave * 1024;
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+            *reinterpret_cast<f32x4*>(sE + m * 64 + (((8 * p + 2 * g + h) ^ m) << 2)) = acc[2 * p + h][j];
+          if (p + 1 == FT / 2) {
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            // lane l: feature l of each of the 16 rows, one 256-byte row piece per store
+            const int f = nb * BN + 16 * FT * wf + lane;
+            float bl = 0.f;
+            if constexpr ((EPI & CG_EPI_BIAS) != 0) bl = f < N ? ep.bias[f] : 0.f;
+            const uint32_t ecol = (uint32_t)(((rt & 63) * ldy + f) * 4);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const float val = sE[r * 64 + (((lane >> 2) ^ r) << 2) + (lane & 3)] + bl;
+              if (f < N)
+                __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(int, val), yres,
+                                                      ecol + (uint32_t)(r * ldy * 4), 0, 0);
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+          }
+        } else if constexpr (sizeof(TO) == 2) {
           bf16x8 v;
-          if constexpr (NORM != MOC_NORM_NONE) {
+          if constexpr ((EPI & CG_EPI_RES) != 0) {
+            const bf16x8 r8 = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rres, rrow + 64 * p, 0, 0));
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              v[e] = (bf16)(acc[2 * p][j][e] + (float)r8[e]);
+              v[4 + e] = (bf16)(acc[2 * p + 1][j][e] + (float)r8[4 + e]);
+            }
+          } else if constexpr (NORM != MOC_NORM_NONE) {
             // features nb*BN + (BN/4) wf + 32 p + 8 g + e (acc[2p]) and + 4 + e (acc[2p+1])
             const float2 sr = sStat[rt + m];
             if constexpr (NORM == MOC_NORM_LAYERNORM) {
@@ -367,7 +443,7 @@ __global__ __launch_bounds__(kCgThreads) void chapter_gemm_kernel(
     }
     __builtin_amdgcn_sched_barrier(0);
     compute(sW + (s % NBUF) * STW, sX + (s % NBUF) * STX);
-    if constexpr (NORM != MOC_NORM_NONE) stats_stage(sX + (s % NBUF) * STX);
+    if constexpr (NORM != MOC_NORM_NONE) stats_stage(sX + (s % NBUF) * STX, kt == 0);
     stored = kt + 1 == nk;
     if (stored) {
       if constexpr (DEPTH == 1) cg_wait_vm(0);  // stage s + 1's loads (no stores outstanding)
@@ -779,17 +855,82 @@ int moc_chapter_dx(const void* dkv_edge, int64_t ld, const int32_t* uniq, const 
   return check_launch("chapter_gemm_kernel(dx)");
 }
 
+}  // extern "C"
+
+namespace moc {
+namespace {
+
+// y [R][N] = x [R][K] w^T (+ epilogue options) over contiguous rows.  Tiles: 128 x 256 two
+// k-stages ahead while the 256 x 384 (or 256 x 256) tiles would not fill two rounds of the
+// persistent grid (the c3 q / o projections: 192 tiles against 64), else the wide tiles one
+// stage ahead (the bank-sized products of the token path: thousands of tiles, a sixth to a third
+// less operand traffic per product).
+template <typename TO, int EPI>
+int rows_gemm(const char* who, const void* x, int64_t ldx, int64_t R, const void* w, int N, int K, void* y,
+              int64_t ldy, CgEpi ep, hipStream_t stream) {
+  const int64_t blocks = (R + 63) / 64;
+  if (R == 0) return MOC_OK;
+  const int grid = cg_grid();
+  const bool n384 = (EPI & CG_EPI_MASKN) == 0 && N % 384 == 0;
+  const int64_t wide_tiles = (R + 255) / 256 * ((N + (n384 ? 383 : 255)) / (n384 ? 384 : 256));
+  // (the any-N epilogue's LDS staging leaves room for one k-stage ahead only)
+  constexpr int kNarrowDepth = (EPI & CG_EPI_MASKN) ? 1 : kCgDepth128;
+#define MOC_RG(BM, DEPTH, BN)                                                                                     \
+  hipLaunchKernelGGL((chapter_gemm_kernel<CG_SRC_CONTIG, CG_DST_CONTIG, TO, BM, DEPTH, MOC_NORM_NONE, BN, EPI>),  \
+                     dim3((unsigned)grid), dim3(kCgThreads), 0, stream, (const bf16*)x, nullptr, ldx, nullptr,    \
+                     nullptr, nullptr, nullptr, blocks, (const bf16*)w, N, K, (TO*)y, ldy, R, R, CgNorm{}, ep)
+  if (wide_tiles < 2 * (int64_t)grid) {
+    MOC_RG(128, kNarrowDepth, 256);
+  } else if constexpr ((EPI & CG_EPI_MASKN) == 0) {
+    if (n384) MOC_RG(256, kCgDepth256, 384);
+    else MOC_RG(256, kCgDepth256, 256);
+  } else {
+    MOC_RG(256, kCgDepth256, 256);
+  }
+#undef MOC_RG
+  return check_launch(who);
+}
+
+}  // namespace
+}  // namespace moc
+
+extern "C" {
+
 int moc_rows_linear(const void* x, int64_t ldx, int64_t R, const void* w, int N, int K, void* y, int64_t ldy,
                     hipStream_t stream) {
   MOC_REQUIRE(x && w && y, MOC_ERR_ARG, "moc_rows_linear: null pointer");
   MOC_REQUIRE(R >= 0 && R < ((int64_t)1 << 36), MOC_ERR_ARG, "moc_rows_linear: R=%lld", (long long)R);
-  const int64_t blocks = (R + 63) / 64;
-  if (int rc = cg_check("moc_rows_linear", ldx, N, K, blocks, ldy)) return rc;
-  if (R == 0) return MOC_OK;
-  hipLaunchKernelGGL((chapter_gemm_kernel<CG_SRC_CONTIG, CG_DST_CONTIG, bf16, 128, kCgDepth128>), dim3((unsigned)cg_grid()),
-                     dim3(kCgThreads), 0, stream, (const bf16*)x, nullptr, ldx, nullptr, nullptr, nullptr, nullptr,
-                     blocks, (const bf16*)w, N, K, (bf16*)y, ldy, R, R, CgNorm{});
-  return check_launch("chapter_gemm_kernel(rows)");
+  if (int rc = cg_check("moc_rows_linear", ldx, N, K, (R + 63) / 64, ldy)) return rc;
+  return rows_gemm<bf16, 0>("chapter_gemm_kernel(rows)", x, ldx, R, w, N, K, y, ldy, CgEpi{}, stream);
+}
+
+int moc_rows_linear_residual(const void* x, int64_t ldx, int64_t R, const void* w, int N, int K, const void* res,
+                             int64_t ldr, void* y, int64_t ldy, hipStream_t stream) {
+  MOC_REQUIRE(x && w && res && y, MOC_ERR_ARG, "moc_rows_linear_residual: null pointer");
+  MOC_REQUIRE(R >= 0 && R < ((int64_t)1 << 36), MOC_ERR_ARG, "moc_rows_linear_residual: R=%lld", (long long)R);
+  MOC_REQUIRE(ldr >= N && ldr % 8 == 0 && 64 * ldr * 2 < ((int64_t)1 << 31) && ((uintptr_t)res & 15) == 0,
+              MOC_ERR_ARG, "moc_rows_linear_residual: residual row stride %lld (N=%d), 16-byte aligned rows",
+              (long long)ldr, N);
+  if (int rc = cg_check("moc_rows_linear_residual", ldx, N, K, (R + 63) / 64, ldy)) return rc;
+  return rows_gemm<bf16, CG_EPI_RES>("chapter_gemm_kernel(rows, residual)", x, ldx, R, w, N, K, y, ldy,
+                                     CgEpi{(const bf16*)res, ldr, nullptr}, stream);
+}
+
+int moc_rows_linear_f32(const void* x, int64_t ldx, int64_t R, const void* w, int N, int K, const float* bias,
+                        float* y, int64_t ldy, hipStream_t stream) {
+  MOC_REQUIRE(x && w && y, MOC_ERR_ARG, "moc_rows_linear_f32: null pointer");
+  MOC_REQUIRE(R >= 0 && R < ((int64_t)1 << 36), MOC_ERR_ARG, "moc_rows_linear_f32: R=%lld", (long long)R);
+  MOC_REQUIRE(N > 0 && K > 0 && K % 64 == 0, MOC_ERR_UNSUPPORTED, "moc_rows_linear_f32: N=%d, K=%d (K a multiple of 64)",
+              N, K);
+  MOC_REQUIRE(ldx >= K && ldx % 8 == 0 && ldy >= N && 64 * ldx * 2 < ((int64_t)1 << 31) &&
+                  64 * ldy * 4 < ((int64_t)1 << 31) && (int64_t)256 * K * 2 < ((int64_t)1 << 31),
+              MOC_ERR_ARG, "moc_rows_linear_f32: row strides %lld, %lld (N=%d, K=%d)", (long long)ldx, (long long)ldy,
+              N, K);
+  const CgEpi ep{nullptr, 0, bias};
+  if (bias)
+    return rows_gemm<float, CG_EPI_MASKN | CG_EPI_BIAS>("chapter_gemm_kernel(rows, f32, bias)", x, ldx, R, w, N, K,
+                                                        y, ldy, ep, stream);
+  return rows_gemm<float, CG_EPI_MASKN>("chapter_gemm_kernel(rows, f32)", x, ldx, R, w, N, K, y, ldy, ep, stream);
 }
 
 int moc_norm_fold_weight(const void* w, int N, int K, const float* gamma, const float* beta, void* w_out, float* u,

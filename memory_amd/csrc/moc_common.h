@@ -58,6 +58,13 @@ inline int check_kv_layout(const char* who, int dtype, int64_t kv_span, int64_t 
   return MOC_OK;
 }
 
+// Router weights below this floor are taken as zero by the sequence-routed attention kernels,
+// which fold omega into the exp2 argument through log2(omega) and 1 / omega: for a denormal
+// omega those are -inf / inf (NaN once multiplied by a zero).  Below the floor the slot's keys
+// k~ = omega k make every logit 0 to fp32 precision and its values and dQ terms are O(omega), so
+// the zero-weight limit (the denominator gains exp2(-m) per key, nothing else) is exact in fp32.
+constexpr float kTinyOmega = 0x1p-64f;
+
 // ------------------------------------------------------------ element helpers
 template <typename T> struct Frag;
 template <> struct Frag<bf16> { typedef bf16x8 type; };

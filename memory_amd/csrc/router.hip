@@ -1631,6 +1631,48 @@ int launch_split_reduce(const float* part, int nsplit, int64_t n, float inv, flo
   return check_launch("pool_reduce_kernel");
 }
 
+
+// ------------------------------------------------------- per-token router: logit gradient pack
+// The bf16 operand of the token router's two backward products (dx = dz W, dW = dz^T x) and the
+// bias gradient (db = column sums of dz, router.py:294's nn.Linear bias) from one read of the fp32
+// logit gradient: dzp [R][Cp] bf16 (columns C .. Cp-1 zero, so that both products run over a
+// multiple of 256 chapters) and per-row-block column partials, summed in a fixed order.
+constexpr int kPackRows = 64;  // rows per workgroup (one partial row of column sums)
+
+__global__ __launch_bounds__(256) void logit_grad_pack_kernel(const float* __restrict__ dz, int64_t R, int64_t C,
+                                                              int64_t Cp, bf16* __restrict__ dzp,
+                                                              float* __restrict__ part) {
+  const int64_t c = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 2;  // columns c, c + 1
+  const int64_t r0 = (int64_t)blockIdx.y * kPackRows;
+  if (c >= Cp) return;
+  const int64_t r1 = min(R, r0 + kPackRows);
+  const bool in0 = c < C, in1 = c + 1 < C;
+  float s0 = 0.f, s1 = 0.f;
+#pragma unroll 8
+  for (int64_t r = r0; r < r1; ++r) {
+    const float* row = dz + r * C;
+    const float a = in0 ? row[c] : 0.f;
+    const float b = in1 ? row[c + 1] : 0.f;
+    s0 += a;
+    s1 += b;
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    *reinterpret_cast<bf16x2_t*>(dzp + r * Cp + c) = bf16x2_t{(bf16)a, (bf16)b};
+  }
+  if (part) {
+    if (in0) part[(int64_t)blockIdx.y * C + c] = s0;
+    if (in1) part[(int64_t)blockIdx.y * C + c + 1] = s1;
+  }
+}
+
+__global__ __launch_bounds__(256) void logit_grad_colsum_kernel(const float* __restrict__ part, int nblk, int64_t C,
+                                                                float* __restrict__ db) {
+  const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (c >= C) return;
+  float s = 0.f;
+  for (int i = 0; i < nblk; ++i) s += part[(int64_t)i * C + c];
+  db[c] = s;
+}
+
 }  // namespace moc
 
 using namespace moc;
@@ -1968,6 +2010,33 @@ int moc_router_losses_bwd(const float* logits, int64_t R, int64_t C, const float
     hipLaunchKernelGGL(router_loss_bwd_kernel, dim3((unsigned)((R + 3) / 4)), dim3(kLossThreads), 0, stream, logits,
                        R, C, row_lse, cf, dlosses, dlogits);
   return check_launch("router_loss_bwd_kernel");
+}
+
+
+size_t moc_logit_grad_pack_workspace(int64_t R, int64_t C) {
+  if (R <= 0 || C <= 0) return 0;
+  return (size_t)((R + kPackRows - 1) / kPackRows) * (size_t)C * sizeof(float);
+}
+
+int moc_logit_grad_pack(const float* dz, int64_t R, int64_t C, int64_t Cp, void* dzp, float* db, void* workspace,
+                        size_t workspace_bytes, hipStream_t stream) {
+  MOC_REQUIRE(dz && dzp, MOC_ERR_ARG, "moc_logit_grad_pack: null pointer");
+  MOC_REQUIRE(R > 0 && C > 0 && Cp >= C && Cp % 2 == 0 && R * Cp < ((int64_t)1 << 40), MOC_ERR_ARG,
+              "moc_logit_grad_pack: R=%lld C=%lld Cp=%lld (Cp >= C, even)", (long long)R, (long long)C,
+              (long long)Cp);
+  MOC_REQUIRE(((uintptr_t)dzp & 3) == 0, MOC_ERR_ARG, "moc_logit_grad_pack: dzp must be 4-byte aligned");
+  MOC_REQUIRE(!db || (workspace && workspace_bytes >= moc_logit_grad_pack_workspace(R, C)), MOC_ERR_ARG,
+              "moc_logit_grad_pack: workspace too small");
+  const int nblk = (int)((R + kPackRows - 1) / kPackRows);
+  MOC_REQUIRE(nblk < 65536, MOC_ERR_UNSUPPORTED, "moc_logit_grad_pack: R=%lld too large", (long long)R);
+  const dim3 grid((unsigned)((Cp / 2 + 255) / 256), (unsigned)nblk);
+  hipLaunchKernelGGL(logit_grad_pack_kernel, grid, dim3(256), 0, stream, dz, R, C, Cp, (bf16*)dzp,
+                     db ? (float*)workspace : nullptr);
+  if (int rc = check_launch("logit_grad_pack_kernel")) return rc;
+  if (!db) return MOC_OK;
+  hipLaunchKernelGGL(logit_grad_colsum_kernel, dim3((unsigned)((C + 255) / 256)), dim3(256), 0, stream,
+                     (const float*)workspace, nblk, C, db);
+  return check_launch("logit_grad_colsum_kernel");
 }
 
 }  // extern "C"

@@ -40,7 +40,7 @@ constexpr unsigned kTimerEventFlags = hipEventDisableSystemFence;
 // 14): the router backward on the aux stream then runs beside it instead of after the main
 // stream's last kernel (c3: 0.936 -> 0.921 ms per step; it is ~25 us slower on its own).
 constexpr int kSeqWgradBudget = 192;
-constexpr int kSeqEvents = 8;
+constexpr int kSeqEvents = 10;  // 0..7 the schedule's, 8..9 the error-path joins (SideJoin)
 
 struct DevEvents {
   hipEvent_t e[kSeqEvents];
@@ -64,6 +64,28 @@ int seq_events(hipEvent_t** out) {
 }
 
 inline size_t al256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+// Joins the side streams a layer call has forked into the main stream on every early return (an
+// error after the fork): the caller frees the layer's buffers in main-stream order once the call
+// fails, so main must not run ahead of side-stream kernels that still read or write them.  The
+// success path joins by the schedule's own events and disarms the guard.
+struct SideJoin {
+  hipStream_t main;
+  hipEvent_t* ev;  // the device's event set; 8 + i joins side stream i
+  hipStream_t side[2];
+  int n = 0;
+  void fork(hipStream_t s) { side[n++] = s; }
+  void disarm() { n = 0; }
+  ~SideJoin() {
+    for (int i = 0; i < n; ++i) {
+      if (hipEventRecord(ev[8 + i], side[i]) == hipSuccess) {
+        if (hipStreamWaitEvent(main, ev[8 + i], 0) != hipSuccess) (void)hipStreamSynchronize(side[i]);
+      } else {
+        (void)hipStreamSynchronize(side[i]);
+      }
+    }
+  }
+};
 
 // Optional per-stage timing (off unless armed by moc_seq_layer_timing): a timing event pair
 // recorded around a stage's launches on the stream that stage runs on, so the elapsed time is
@@ -250,6 +272,8 @@ int moc_seq_layer_fwd(const void* h, const void* bank, const void* wr, int wr_dt
   // them), then the transposed weights the backward reads, beside the projection and attention
   MOC_HIP(hipEventRecord(ev[0], main));
   MOC_HIP(hipStreamWaitEvent(aux, ev[0], 0));
+  SideJoin join{main, ev};
+  join.fork(aux);
   SEQ_STAGE(kStPackWkv, aux, SEQ_TRY(moc_weight_pack(wk, MOC_BF16, wv, MOC_BF16, y.KV, d, wkv, nullptr, aux)));
   MOC_HIP(hipEventRecord(ev[3], aux));
   SEQ_STAGE(kStQProj, aux, SEQ_TRY(moc_rows_linear(h, d, tok, wq, (int)d, (int)d, q, d, aux)));
@@ -285,6 +309,7 @@ int moc_seq_layer_fwd(const void* h, const void* bank, const void* wr, int wr_dt
                                   H, HK, 64, 64, y.NS, 0.125f, attn, lse, main)));
   SEQ_STAGE(kStOProj, main, SEQ_TRY(moc_rows_linear(attn, d, tok, wo, (int)d, (int)d, out, d, main)));
   MOC_HIP(hipStreamWaitEvent(main, ev[2], 0));
+  join.disarm();
   return MOC_OK;
 }
 
@@ -334,6 +359,8 @@ int moc_seq_layer_bwd(const void* h, const void* bank, const void* wr, int wr_dt
   // aux: o_proj dW beside o_proj dX and the attention backward
   MOC_HIP(hipEventRecord(ev[0], main));
   MOC_HIP(hipStreamWaitEvent(aux, ev[0], 0));
+  SideJoin join{main, ev};
+  join.fork(aux);
   if (dwo)
     SEQ_STAGE(kStOWgrad, aux,
               SEQ_TRY(moc_linear_wgrad(dout, attn, MOC_BF16, tok, d, d, sc + y.lw_ws, y.lw_ws_bytes, MOC_BF16, dwo,
@@ -348,6 +375,7 @@ int moc_seq_layer_bwd(const void* h, const void* bank, const void* wr, int wr_dt
   if (dbank) {
     MOC_HIP(hipEventRecord(ev[1], main));
     MOC_HIP(hipStreamWaitEvent(fill, ev[1], 0));
+    join.fork(fill);
     SEQ_STAGE(kStFill, fill, SEQ_TRY(moc_fill_zero(dbank, bank_rows * d * 2, fill_cus(), fill)));
     MOC_HIP(hipEventRecord(ev[2], fill));
   }
@@ -369,6 +397,7 @@ int moc_seq_layer_bwd(const void* h, const void* bank, const void* wr, int wr_dt
   if (dwq) {
     MOC_HIP(hipStreamWaitEvent(fill, after_dq, 0));
     MOC_HIP(hipStreamWaitEvent(fill, ev[6], 0));
+    if (!dbank) join.fork(fill);
     SEQ_STAGE(kStQWgrad, fill,
               SEQ_TRY(moc_linear_wgrad(dq, h, MOC_BF16, tok, d, d, sc + y.lw_ws, y.lw_ws_bytes, MOC_BF16, dwq, fill)));
     MOC_HIP(hipEventRecord(ev[7], fill));
@@ -407,6 +436,7 @@ int moc_seq_layer_bwd(const void* h, const void* bank, const void* wr, int wr_dt
   }
   MOC_HIP(hipStreamWaitEvent(main, ev[5], 0));
   if (dwq) MOC_HIP(hipStreamWaitEvent(main, ev[7], 0));
+  join.disarm();
   return MOC_OK;
 }
 

@@ -149,9 +149,10 @@ __global__ __launch_bounds__(kBThreads) void xattn_bwd_dq_kernel(
       kio.load_rows(kb, tile_off(u_next), row_bytes, tid);
       vio.load_rows(vb, tile_off(u_next), row_bytes, tid);
     }
-    // a slot of zero router weight has dS = 0 (its keys and values are zero): no dQ contribution
+    // a slot of zero router weight has dS = 0 (its keys and values are zero): no dQ contribution;
+    // below the floor kTinyOmega its contribution is O(omega), below fp32 resolution
     const float w = u_cur >= 0 ? om[s] : 0.f;
-    if (w > 0.f) {
+    if (w > kTinyOmega) {
       const char* sKc = sK[buf];
       const char* sVc = sV[buf];
       const float c = w * scale_log2;

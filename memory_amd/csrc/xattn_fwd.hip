@@ -181,7 +181,7 @@ __global__ __launch_bounds__(kFwdThreads) void xattn_fwd_kernel(
         }
       }
       F8 pf[2][2];
-      if (w > 0.f) {
+      if (w > kTinyOmega) {
         // p~ = w * exp2(s*c - m): w folded into the exponent; the row sum needs sum(p~) / w
         const float lw = __builtin_amdgcn_logf(w);
         const float rw = __builtin_amdgcn_rcpf(w);
@@ -212,7 +212,8 @@ __global__ __launch_bounds__(kFwdThreads) void xattn_fwd_kernel(
           }
         }
       } else {
-        // zero weight: keys and values are zero, every logit is 0 -> only the denominator moves
+        // zero (or below-floor) weight: keys and values vanish, every logit is 0 -> only the
+        // denominator moves
 #pragma unroll
         for (int qb = 0; qb < 2; ++qb) lsum[qb] += 64.f * fast_exp2(-m[qb]);
       }

@@ -305,14 +305,27 @@ def kv_rows_layout(kv: torch.Tensor, T: int, HK: int, Dh: int):
 
 # ------------------------------------------------------------- dense projections
 
-def rows_linear(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
-    """x W^T on the chapter GEMM over 64-row blocks of x (bf16, fp32 accumulation); w [N][K]."""
+def rows_linear(x: torch.Tensor, w: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """x W^T on the chapter GEMM over 64-row blocks of x (bf16, fp32 accumulation); w [N][K].
+    ``out``: a contiguous bf16 tensor of the result's shape to write into."""
     N, K = w.shape
     x2 = x.reshape(-1, K).contiguous()
     wc = w.contiguous()
-    y = torch.empty(x2.shape[0], N, device=x.device, dtype=x.dtype)
+    if out is None:
+        y = torch.empty(x2.shape[0], N, device=x.device, dtype=x.dtype)
+    else:
+        if not (out.is_contiguous() and out.dtype == x.dtype and out.numel() == x2.shape[0] * N):
+            raise ValueError("rows_linear: out must be contiguous with the result's dtype and size")
+        y = out.view(x2.shape[0], N)
     call("moc_rows_linear", ptr(x2), K, x2.shape[0], ptr(wc), N, K, ptr(y), N, stream_ptr(x.device))
     return y.view(*x.shape[:-1], N)
+
+
+def rows_gemm_ok(x: torch.Tensor, w: torch.Tensor) -> bool:
+    """Whether x W^T runs on the chapter GEMM: bf16 operands, N % 256 == 0, K % 64 == 0."""
+    N, K = w.shape
+    return (x.is_cuda and x.dtype == torch.bfloat16 and w.dtype == torch.bfloat16 and N % 256 == 0
+            and K % 64 == 0)
 
 
 class _Linear(torch.autograd.Function):
@@ -375,14 +388,18 @@ class _LinearResidual(torch.autograd.Function):
     def forward(ctx, x, w, residual):
         ctx.save_for_backward(x, w)
         ctx.res_dtype = residual.dtype
-        n_out = w.shape[0]
-        x2 = x.reshape(-1, x.shape[-1])
-        r2 = residual.reshape(-1, n_out)
+        n_out, n_in = w.shape
+        x2 = x.reshape(-1, n_in).contiguous()
+        if residual.dtype == x.dtype == w.dtype and rows_gemm_ok(x, w):
+            # bf16: the residual is the GEMM's accumulator input (moc_rows_linear_residual)
+            r2 = residual.reshape(-1, n_out).contiguous()
+            out = torch.empty_like(r2)
+            wc = w.contiguous()
+            call("moc_rows_linear_residual", ptr(x2), n_in, x2.shape[0], ptr(wc), n_out, n_in, ptr(r2),
+                 n_out, ptr(out), n_out, stream_ptr(x.device))
+            return out.view(residual.shape)
         with L.region("lib_linear_fwd"):
-            if residual.dtype == x.dtype == w.dtype:
-                out = torch.addmm(r2, x2, w.t())
-            else:
-                out = r2 + F.linear(x2, w)
+            out = residual.reshape(-1, n_out) + F.linear(x2, w)
         return out.view(residual.shape)
 
     @staticmethod
@@ -395,8 +412,12 @@ class _LinearResidual(torch.autograd.Function):
             dres = dy
         g = dy2.to(x.dtype).contiguous()
         if ctx.needs_input_grad[0]:
-            with L.region("lib_linear_dx"):
-                dx = torch.matmul(g, w.to(x.dtype)).view(x.shape)
+            wt = w.to(x.dtype).t().contiguous()
+            if rows_gemm_ok(g, wt):
+                dx = rows_linear(g, wt).view(x.shape)
+            else:
+                with L.region("lib_linear_dx"):
+                    dx = torch.matmul(g, w.to(x.dtype)).view(x.shape)
         if ctx.needs_input_grad[1]:
             dw = linear_wgrad(g, x.reshape(-1, n_in).contiguous(), w.dtype)
         return dx, dw, dres
@@ -853,17 +874,26 @@ class _TokenRouterLinear(torch.autograd.Function):
     """logits = x W^T + b for per-token routing (router.py:294, ``self.router(hidden_states)``).
 
     The GEMM operands are in the activation dtype (bf16 activations round W to bf16, the
-    operand precision of the reference under autocast) and accumulate in fp32 on
-    hipBLASLt; the logits stay fp32 (not rounded to bf16 as under autocast) so that the
-    top-k selection sees distinct values.  Backward: dx = dlogits W in the activation
-    dtype, dW = dlogits^T x and db = sum dlogits in fp32."""
+    operand precision of the reference under autocast) and accumulate in fp32; the logits stay
+    fp32 (not rounded to bf16 as under autocast) so that the top-k selection sees distinct
+    values.  bf16: the chapter GEMM with the bias in its epilogue (moc_rows_linear_f32, any
+    number of chapters).  Backward: dx = dlogits W in the activation dtype, dW = dlogits^T x and
+    db = sum dlogits in fp32; for bf16 the logit gradient is rounded once into a bf16 copy whose
+    rows are padded with zeros to a multiple of 256 chapters, so that both products run on the
+    chapter kernels (dx on the rows GEMM with the zero-padded W^T, dW on the split-row weight
+    gradient, its padded rows dropped).  fp32 activations stay on library GEMMs."""
 
     @staticmethod
     def forward(ctx, x, W, b):
         Wc = W.to(x.dtype).contiguous()
-        # the bias rides in the GEMM's epilogue (a separate broadcast add re-reads and rewrites
-        # the fp32 logits: 0.27 GB at 8,192 tokens x 4,097 chapters)
-        if b is None:
+        R, K = x.shape
+        C = Wc.shape[0]
+        if x.dtype == torch.bfloat16 and K % 64 == 0:
+            y = torch.empty(R, C, device=x.device, dtype=torch.float32)
+            bias = None if b is None else b.float().contiguous()
+            call("moc_rows_linear_f32", ptr(x), K, R, ptr(Wc), C, K, None if bias is None else ptr(bias), ptr(y), C,
+                 stream_ptr(x.device))
+        elif b is None:
             y = torch.mm(x, Wc.t()) if x.dtype == torch.float32 else torch.mm(x, Wc.t(), out_dtype=torch.float32)
         elif x.dtype == torch.float32:
             y = torch.addmm(b.float(), x, Wc.t())
@@ -878,17 +908,39 @@ class _TokenRouterLinear(torch.autograd.Function):
         x, Wc = ctx.saved_tensors
         w_dtype, b_dtype = ctx.meta
         dy = dy.contiguous()
-        dyc = dy if x.dtype == torch.float32 else dy.to(x.dtype)
+        R, K = x.shape
+        C = Wc.shape[0]
         dx = dW = db = None
-        if ctx.needs_input_grad[0]:
-            dx = torch.mm(dyc, Wc)
-        if ctx.needs_input_grad[1]:
-            if x.dtype == torch.float32:
-                dW = torch.mm(dyc.t(), x)
-            else:
-                dW = torch.mm(dyc.t(), x, out_dtype=torch.float32)
-            dW = dW.to(w_dtype)
-        if b_dtype is not None and ctx.needs_input_grad[2]:
+        need_db = b_dtype is not None and ctx.needs_input_grad[2]
+        if x.dtype == torch.bfloat16 and K % 256 == 0:
+            # one pass over the fp32 logit gradient: the zero-padded bf16 operand and the bias
+            # gradient's column sums (moc_logit_grad_pack)
+            Cp = (C + 255) // 256 * 256
+            dyp = torch.empty(R, Cp, device=dy.device, dtype=torch.bfloat16)
+            db32 = torch.empty(C, device=dy.device, dtype=torch.float32) if need_db else None
+            ws_bytes = L.query("moc_logit_grad_pack_workspace", R, C) if need_db else 0
+            ws = torch.empty(max(1, ws_bytes // 4), device=dy.device, dtype=torch.float32) if need_db else None
+            call("moc_logit_grad_pack", ptr(dy), R, C, Cp, ptr(dyp), ptr(db32), ptr(ws), ws_bytes,
+                 stream_ptr(dy.device))
+            if need_db:
+                db = db32.to(b_dtype)
+            if ctx.needs_input_grad[0]:
+                wt = torch.zeros(K, Cp, device=dy.device, dtype=torch.bfloat16)
+                wt[:, :C].copy_(Wc.t())
+                dx = rows_linear(dyp, wt)
+            if ctx.needs_input_grad[1]:
+                dW = linear_wgrad(dyp, x, torch.float32)[:C].to(w_dtype)
+        else:
+            dyc = dy if x.dtype == torch.float32 else dy.to(x.dtype)
+            if ctx.needs_input_grad[0]:
+                dx = torch.mm(dyc, Wc)
+            if ctx.needs_input_grad[1]:
+                if x.dtype == torch.float32:
+                    dW = torch.mm(dyc.t(), x)
+                else:
+                    dW = torch.mm(dyc.t(), x, out_dtype=torch.float32)
+                dW = dW.to(w_dtype)
+        if need_db and db is None:
             db = col_sum(dy).to(b_dtype)
         return dx, dW, db
 

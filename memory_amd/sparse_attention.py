@@ -290,11 +290,16 @@ class _TokenRouted(torch.autograd.Function):
         q = q.contiguous()
         routed = routed.contiguous()
         wkv = torch.cat([wk, wv], 0).to(dtype).contiguous()
-        # every routed chapter is projected (no gather, no norm): one plain GEMM on hipBLASLt,
-        # K and V read by the sparse kernels as strided column blocks of kv [Nr][2 KV]
+        # every routed chapter is projected (no gather, no norm): one rows GEMM over the routed
+        # bank (the chapter GEMM's wide tiles for bf16), K and V read by the sparse kernels as
+        # strided column blocks of kv [Nr][2 KV]
         KV = HK * D
-        with L.region("lib_token_kv_project"):
-            kv = F.linear(routed.to(dtype), wkv)
+        rows = routed.to(dtype)
+        if ops.rows_gemm_ok(rows, wkv):
+            kv = ops.rows_linear(rows, wkv)
+        else:
+            with L.region("lib_token_kv_project"):
+                kv = F.linear(rows, wkv)
         S = idx.shape[-1]
         segs = _segments(idx, w, mode, C, False, HQ, HK, C)
         out, saved = _forward(q, kv[:, :KV], kv[:, KV:], "rows", segs, mode, S, D ** -0.5)
@@ -324,8 +329,7 @@ class _TokenRouted(torch.autograd.Function):
             dwk = dwkv[:KV].to(wk_dtype) if need_wk else None
             dwv = dwkv[KV:].to(wv_dtype) if need_wv else None
         if need_r:
-            with L.region("lib_token_kv_dx"):
-                dr = _rows_grad(routed, dkv, wkv)
+            dr = _rows_grad(routed, dkv, wkv)
         dw = None
         if w_shape is not None and dws:
             dw = dws[0].view(w_shape) if len(dws) == 1 else torch.stack(dws, 0).sum(0).view(w_shape)
@@ -333,10 +337,20 @@ class _TokenRouted(torch.autograd.Function):
 
 
 def _rows_grad(routed: torch.Tensor, dkv: torch.Tensor, wkv: torch.Tensor) -> torch.Tensor:
-    """d routed = dkv [Wk; Wv].  When `routed` is the tail rows of a larger tensor (the routed
-    part of a bank whose first rows are the shared chapters, split off by model.split_rows),
-    the product is written into the tail of a buffer of the whole bank's shape, so the split's
-    backward can hand that buffer on after filling the head rows instead of copying the tail."""
+    """d routed = dkv [Wk; Wv] (bf16: the chapter GEMM's rows mode with W = [Wk; Wv]^T).  When
+    `routed` is the tail rows of a larger tensor (the routed part of a bank whose first rows are
+    the shared chapters, split off by model.split_rows), the product is written into the tail of
+    a buffer of the whole bank's shape, so the split's backward can hand that buffer on after
+    filling the head rows instead of copying the tail."""
+    wkv_t = wkv.t().contiguous()
+    native = ops.rows_gemm_ok(dkv, wkv_t)
+
+    def product(out=None):
+        if native:
+            return ops.rows_linear(dkv, wkv_t, out=out)
+        with L.region("lib_token_kv_dx"):
+            return torch.mm(dkv, wkv, out=out) if out is not None else torch.matmul(dkv, wkv)
+
     base = routed._base
     if base is not None and base.dim() == 2 and base.is_contiguous() and routed.is_contiguous() \
             and base.shape[1] == routed.shape[1] and routed.dtype == dkv.dtype and base.dtype == routed.dtype:
@@ -346,9 +360,9 @@ def _rows_grad(routed: torch.Tensor, dkv: torch.Tensor, wkv: torch.Tensor) -> to
             full = torch.empty(base.shape, device=dkv.device, dtype=dkv.dtype)
             full._moc_rows_tail = off // d        # read by model._SplitRows.backward
             tail = full[off // d:]
-            torch.mm(dkv, wkv, out=tail)
+            product(tail)
             return tail
-    return torch.matmul(dkv, wkv).to(routed.dtype)
+    return product().to(routed.dtype)
 
 
 def token_routed_attention(q, routed_memory, wk, wv, idx, chapter_weights, *, tokens_per_chapter: int,

@@ -37,6 +37,7 @@ def _ref_grads(q, bank, Wk, Wv, ci, cw, dO, T, S, norm, HK):
     (2, 130, 2, 1, 20, 3, "layernorm", True, False),
     (4, 64, 4, 4, 9, 8, None, True, False),
     (3, 96, 4, 2, 16, 6, None, True, True),
+    (3, 96, 4, 2, 16, 6, None, True, "tiny"),
 ])
 def test_routed_attention_backward(gpu_device, dtype, B, Lq, H, HK, C, k, norm, dup, zero_w):
     print(f"routed_attention bwd dtype={dtype} B={B} L={Lq} H={H} HK={HK} C={C} k={k} norm={norm} "
@@ -56,7 +57,14 @@ def test_routed_attention_backward(gpu_device, dtype, B, Lq, H, HK, C, k, norm, 
         logits = logits[:1].expand(B, C) + 0.01 * torch.randn(B, C, generator=g)
     idx, w, _ = O.route_sequence(logits, k, S)
     ci, cw = O.prepend_shared_chapters(idx, w, num_chapters=C, num_shared_chapters=S, routed_scaling_factor=2.5)
-    if zero_w:
+    if zero_w == "tiny":
+        # positive weights far below fp32 resolution (a denormal, and one whose square underflows):
+        # outputs and gradients finite and equal to the oracle's
+        cw = cw.clone()
+        cw[:, 2] = 1e-39
+        cw[0, 4] = 1e-30
+        cw[1, 3] = 1e-20
+    elif zero_w:
         # exact-zero chapter weights: keys / values vanish, d omega does not
         cw = cw.clone()
         cw[:, 2] = 0.0
@@ -82,6 +90,8 @@ def test_routed_attention_backward(gpu_device, dtype, B, Lq, H, HK, C, k, norm, 
     assert_parity(wvg.grad, gv, dtype, "dWv")
     assert_parity(bg.grad, gb, dtype, "dbank")
     assert_parity(cwg.grad, gw, dtype, "domega")
+    for t, name in ((out, "out"), (qg.grad, "dq"), (bg.grad, "dbank"), (cwg.grad, "domega")):
+        assert torch.isfinite(t.float()).all(), f"{name} not finite"
     # rows of chapters nobody selected get exactly zero gradient
     sel = torch.zeros(C, dtype=torch.bool)
     sel[ci.reshape(-1)] = True

@@ -93,13 +93,15 @@ def test_norm_linear_matches_oracle(dev, norm, R, K, N):
         assert_parity(bg.grad.float(), b64.grad, torch.bfloat16, "dbias")
 
 
-def test_rows_linear_norm_statistics(dev):
-    """The row statistics the fused GEMM writes for the norm's backward equal the norm
-    kernel's (fp32, same eps), for RMSNorm and LayerNorm."""
+@pytest.mark.parametrize("spread,offset", [(3.0, -1.0), (1.0, 200.0)])
+def test_rows_linear_norm_statistics(dev, spread, offset):
+    """The row statistics the fused GEMM writes for the norm's backward equal float64's
+    (fp32, same eps), for RMSNorm and LayerNorm; the second case has rows whose mean is 200 times
+    their spread, where a variance taken as E[x^2] - mean^2 in fp32 loses ~15 bits."""
     from memory_amd import _lib as L
     g0 = gen(3)
     R, K, N = 333, 768, 256
-    x = (torch.randn(R, K, generator=g0) * 3 - 1).to(torch.bfloat16).to(dev)
+    x = (torch.randn(R, K, generator=g0) * spread + offset).to(torch.bfloat16).to(dev)
     W = (torch.randn(N, K, generator=g0) * 0.05).to(torch.bfloat16).to(dev)
     gamma = torch.ones(K, device=dev)
     beta = torch.zeros(K, device=dev)
@@ -125,13 +127,17 @@ def test_rows_linear_norm_statistics(dev):
 
 
 @pytest.mark.parametrize("rdt", [torch.bfloat16, torch.float32])
-def test_linear_residual(dev, rdt):
+@pytest.mark.parametrize("shape", [(3, 40, 64), (2, 520, 768)])
+def test_linear_residual(dev, rdt, shape):
+    """residual + o_proj(x) (memory_block.py:549-558); at d = 768 in bf16 the residual rides in
+    the chapter GEMM's epilogue (moc_rows_linear_residual) and dx runs on the rows GEMM."""
     from memory_amd import ops
     g0 = gen(5)
-    x = torch.randn(3, 40, 64, generator=g0).to(torch.bfloat16)
-    W = (torch.randn(64, 64, generator=g0) * 0.125).to(torch.bfloat16)
-    r = torch.randn(3, 40, 64, generator=g0).to(rdt)
-    dy = torch.randn(3, 40, 64, generator=g0)
+    B, T, d = shape
+    x = torch.randn(B, T, d, generator=g0).to(torch.bfloat16)
+    W = (torch.randn(d, d, generator=g0) * d ** -0.5).to(torch.bfloat16)
+    r = torch.randn(B, T, d, generator=g0).to(rdt)
+    dy = torch.randn(B, T, d, generator=g0)
     xg, Wg, rg = (t.to(dev).requires_grad_(True) for t in (x, W, r))
     out = ops.linear_residual(xg, Wg, rg)
     assert out.dtype == rdt

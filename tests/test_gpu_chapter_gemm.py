@@ -187,3 +187,71 @@ def test_dense_wgrad_lds_dma_path(dev, shape):
     ref = dy.double().t() @ x.double()
     print(f"R={R} N={N} K={K}")
     assert_parity(dw.cpu(), ref, torch.bfloat16, "dW dense")
+
+
+# rows GEMM (moc_rows_linear): (R, N, K) -- the first two take the wide 256-row tiles (>= 2 rounds
+# of the persistent grid: the token path's K/V projection and its dX at reduced R, ragged last
+# block), the third the 128-row tiles
+@pytest.mark.parametrize("shape", [(70000, 1536, 768), (65600, 768, 1536), (1000, 768, 768)])
+def test_rows_linear(dev, shape):
+    """y = x W^T over contiguous rows (the token path's whole-bank K/V projection and its input
+    gradient, memory_attention.py:241-243) against a float64 product; rows past R untouched."""
+    ops = _ops()
+    R, N, K = shape
+    x = torch.randn(R, K, generator=gen(41)).to(torch.bfloat16)
+    w = (torch.randn(N, K, generator=gen(42)) / K ** 0.5).to(torch.bfloat16)
+    out = torch.full((R + 64, N), float("nan"), device=dev, dtype=torch.bfloat16)
+    ops.rows_linear(x.to(dev), w.to(dev), out=out[:R])
+    ref = x.double() @ w.double().t()
+    got = out[:R].cpu()
+    print(f"R={R} N={N} K={K}")
+    assert_parity(got, ref, torch.bfloat16, "rows linear")
+    err = (got.double() - ref).abs()
+    assert (err <= ref.abs() * 2 ** -8 + 1e-3).all(), err.max().item()
+    assert torch.isnan(out[R:].float().cpu()).all(), "rows past R must not be written"
+
+
+@pytest.mark.parametrize("shape", [(8192, 768, 768), (1000, 256, 512), (40000, 768, 768)])
+def test_rows_linear_residual(dev, shape):
+    """out = residual + x W^T in one GEMM (memory_block.py:549-558 with the o_proj of
+    memory_attention.py:456): one rounding of the fp32 sum, checked against float64; also in
+    place (residual buffer = output)."""
+    from memory_amd import _lib as L
+    R, N, K = shape
+    x = torch.randn(R, K, generator=gen(51)).to(torch.bfloat16)
+    w = (torch.randn(N, K, generator=gen(52)) / K ** 0.5).to(torch.bfloat16)
+    res = (torch.randn(R, N, generator=gen(53)) * 4).to(torch.bfloat16)
+    ref = res.double() + x.double() @ w.double().t()
+    xd, wd, rd = x.to(dev), w.to(dev), res.to(dev)
+    st = torch.cuda.current_stream().cuda_stream
+    y = torch.empty(R, N, device=dev, dtype=torch.bfloat16)
+    L.call("moc_rows_linear_residual", xd.data_ptr(), K, R, wd.data_ptr(), N, K, rd.data_ptr(), N, y.data_ptr(), N, st)
+    print(f"R={R} N={N} K={K}")
+    assert_parity(y.cpu(), ref, torch.bfloat16, "rows linear + residual")
+    err = (y.cpu().double() - ref).abs()
+    assert (err <= ref.abs() * 2 ** -8 + 1e-3).all(), err.max().item()
+    L.call("moc_rows_linear_residual", xd.data_ptr(), K, R, wd.data_ptr(), N, K, rd.data_ptr(), N, rd.data_ptr(), N,
+           st)
+    assert torch.equal(rd.cpu(), y.cpu()), "in place must equal out of place"
+
+
+@pytest.mark.parametrize("shape", [(8192, 4097, 768), (300, 4097, 768), (700, 100, 128), (8192, 4096, 768)])
+@pytest.mark.parametrize("bias", [True, False])
+def test_rows_linear_f32_any_n(dev, shape, bias):
+    """fp32 logits x W^T + b for any number of chapters (router.py:294 ``self.router(h)`` with bf16
+    operands): columns past N and rows past R untouched, within fp32 rounding of float64."""
+    from memory_amd import _lib as L
+    R, N, K = shape
+    x = torch.randn(R, K, generator=gen(61)).to(torch.bfloat16)
+    w = (torch.randn(N, K, generator=gen(62)) * 0.02).to(torch.bfloat16)
+    b = torch.randn(N, generator=gen(63))
+    ldy = N + 3
+    y = torch.full((R + 1, ldy), float("nan"), device=dev)
+    xd, wd, bd = x.to(dev), w.to(dev), b.to(dev)
+    L.call("moc_rows_linear_f32", xd.data_ptr(), K, R, wd.data_ptr(), N, K,
+           bd.data_ptr() if bias else None, y.data_ptr(), ldy, torch.cuda.current_stream().cuda_stream)
+    ref = x.double() @ w.double().t() + (b.double() if bias else 0.0)
+    yc = y.cpu()
+    print(f"R={R} N={N} K={K} bias={bias}")
+    assert_parity(yc[:R, :N], ref, torch.float32, "logits")
+    assert torch.isnan(yc[:R, N:]).all() and torch.isnan(yc[R:]).all(), "outside [R, N] must stay untouched"

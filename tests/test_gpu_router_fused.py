@@ -136,3 +136,28 @@ def test_rows_add_bcast(gpu_device, dtype, with_coef):
            L.stream_ptr(dev))
     tol = 1e-2 if dtype == torch.bfloat16 else 1e-6
     assert_rel(xd, ref, tol, "x + v")
+
+
+@pytest.mark.parametrize("R,C", [(8192, 4097), (100, 33), (65, 512)])
+def test_logit_grad_pack(gpu_device, R, C):
+    """moc_logit_grad_pack: the bf16 copy of the per-token router's logit gradient, padded with
+    zero columns to a multiple of 256 (exactly torch's round-to-nearest conversion), and the bias
+    gradient db = sum over rows (router.py:294's nn.Linear bias) against float64."""
+    dev = gpu_device
+    g = torch.Generator().manual_seed(R + C)
+    dz = torch.randn(R, C, generator=g) * torch.rand(R, 1, generator=g) * 3
+    Cp = (C + 255) // 256 * 256
+    dzd = dz.to(dev)
+    dzp = torch.full((R, Cp), float("nan"), device=dev, dtype=torch.bfloat16)
+    db = torch.empty(C, device=dev)
+    ws_bytes = L.query("moc_logit_grad_pack_workspace", R, C)
+    ws = torch.empty(ws_bytes // 4, device=dev)
+    L.call("moc_logit_grad_pack", L.ptr(dzd), R, C, Cp, L.ptr(dzp), L.ptr(db), L.ptr(ws), ws_bytes, L.stream_ptr(dev))
+    got = dzp.cpu()
+    assert torch.equal(got[:, :C], dz.to(torch.bfloat16)), "bf16 copy"
+    assert (got[:, C:] == 0).all(), "padding columns must be zero"
+    assert_rel(db.cpu(), dz.double().sum(0), 1e-5, "db")
+    # without the bias gradient: only the copy
+    dzp2 = torch.full((R, Cp), float("nan"), device=dev, dtype=torch.bfloat16)
+    L.call("moc_logit_grad_pack", L.ptr(dzd), R, C, Cp, L.ptr(dzp2), None, None, 0, L.stream_ptr(dev))
+    assert torch.equal(dzp2.cpu(), got)

@@ -57,3 +57,49 @@ def test_noalloc_plan_refuses_plans_beyond_the_scratch(gpu_device):
     with pytest.raises(ValueError, match="scratch"):
         L.call("moc_chapter_plan_noalloc", L.ptr(chap), E, C, L.ptr(dummy), L.ptr(dummy), L.ptr(dummy), L.ptr(dummy),
                L.ptr(dummy), L.stream_ptr(gpu_device))
+
+
+def test_noalloc_plan_graph_replay(gpu_device):
+    """The entry point captured into a HIP graph after one uncaptured call: every replay, on new
+    chapter ids written into the captured input, with eager work and synchronisation between the
+    replays, equals moc_chapter_plan on the same ids."""
+    from memory_amd import _lib as L
+    L.lib()
+    g = torch.Generator().manual_seed(1)
+    E, C = 150_000, 4097
+    chap_d = torch.randint(0, C, (E,), generator=g, dtype=torch.int32).to(gpu_device)
+    mu = min(E, C)
+    outs = [torch.full((mu,), -7, device=gpu_device, dtype=torch.int32),
+            torch.full((2,), -7, device=gpu_device, dtype=torch.int32),
+            torch.full((E,), -7, device=gpu_device, dtype=torch.int32),
+            torch.full((mu + 1,), -7, device=gpu_device, dtype=torch.int32),
+            torch.full((E,), -7, device=gpu_device, dtype=torch.int32)]
+    L.call("moc_chapter_plan_noalloc", L.ptr(chap_d), E, C, *(L.ptr(t) for t in outs), L.stream_ptr(gpu_device))
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            L.call("moc_chapter_plan_noalloc", L.ptr(chap_d), E, C, *(L.ptr(t) for t in outs),
+                   L.stream_ptr(gpu_device))
+    torch.cuda.current_stream().wait_stream(side)
+    for rep in range(3):
+        lo = -2 if rep == 1 else 0
+        chap = torch.randint(lo, C // (rep + 1), (E,), generator=g, dtype=torch.int32)
+        chap_d.copy_(chap.to(gpu_device))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        got = [t.clone() for t in outs]
+        want = _plan(L, chap_d, C, False)   # eager plan with its own workspace between the replays
+        n_u = int(want[1][0])
+        print(f"replay {rep}: E={E} C={C} n_uniq={n_u}", flush=True)
+        assert int(got[1][0]) == n_u and int(got[1][1]) == int(want[1][1])
+        assert torch.equal(got[0][:n_u].cpu(), want[0][:n_u].cpu())
+        assert torch.equal(got[2].cpu(), want[2].cpu())
+        assert torch.equal(got[3][:n_u + 1].cpu(), want[3][:n_u + 1].cpu())
+        # csr_edge is defined for the valid edges only (csr_off[n_uniq] of them); the captured
+        # buffer keeps an earlier replay's entries past them
+        tot = int(want[3][n_u])
+        assert torch.equal(got[4][:tot].cpu(), want[4][:tot].cpu())
