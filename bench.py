@@ -447,6 +447,13 @@ def timed(fn, steps, warmup, roofline_entry=None):
     return wall * 1e3 / steps, per, roofline_entry, live
 
 
+# stages of the native layer launched on its side streams (moc_seq_layer_fwd's aux stream,
+# moc_seq_layer_bwd's aux and fill streams)
+SIDE_STREAM_STAGES = {"moc_weight_pack:wkv", "moc_rows_linear:q_proj", "moc_weight_pack:transposed",
+                      "moc_linear_wgrad:o_proj", "moc_fill_zero:dbank", "moc_rows_linear:q_proj_dx",
+                      "moc_linear_wgrad:q_proj", "moc_router_seq_bwd+linear_bwd+pool_bwd"}
+
+
 C4 = dict(B=4, L=2048, d=768, H=12, HK=12, C=4097, T=64, S=1, k=16, scale=2.5)
 
 
@@ -924,7 +931,11 @@ def main():
     kernels = {}
     for n, v in sorted(per_kernel.items(), key=lambda kv: -kv[1]["ms_per_step"]):
         e = {"avg_ms": round(v["avg_ms"], 4), "calls": v["calls_per_step"]}
-        if n in flop_key:
+        if n in SIDE_STREAM_STAGES:
+            # runs beside the main stream's kernels: its event span includes time shared with
+            # them, so it is no kernel duration and gets no rate
+            e["stream"] = "side (overlapped)"
+        elif n in flop_key:
             e["tflops"] = round(fl[flop_key[n]] / (v["avg_ms"] * 1e-3) / 1e12, 1)
         kernels[n] = e
 

@@ -382,9 +382,6 @@ int moc_seq_layer_bwd(const void* h, const void* bank, const void* wr, int wr_dt
   SEQ_STAGE(kStDq, main,
             SEQ_TRY(moc_xattn_bwd_dq(MOC_BF16, q, kv, kv + y.KV, span, (int64_t)64 * KV2, 64, KV2, edge_u, omega,
                                      d_attn, lse, delta, B, L, H, HK, 64, 64, y.NS, 0.125f, dq, main)));
-  // the zeros are in place before dX stores into the bank rows (the fill ends during dQ; waited
-  // for here, before the fill stream takes more work, the wait is free -- before dX it cost ~6 us)
-  if (dbank) MOC_HIP(hipStreamWaitEvent(main, ev[2], 0));
   // aux: q_proj dX into dh beside dK/dV; fill (done with the zeros by then): q_proj dW beside
   // dK/dV, so that the aux stream reaches the router backward when dK/dV ends (both on aux, they
   // ran past dK/dV's end and the router backward past the main stream's last kernel).  When
@@ -430,6 +427,10 @@ int moc_seq_layer_bwd(const void* h, const void* bank, const void* wr, int wr_dt
                                            KV2, (int)d, sc + y.cw_ws, y.cw_ws_bytes, dwkv_dtype, dwkv,
                                            kSeqWgradBudget, main)));
   if (dbank) {
+    // the zeros are in place before dX stores into the bank rows: the fill runs beside dQ and
+    // dK/dV and has ended long before (waited for right after dQ, the step waited ~20 us for
+    // it once dQ took its tiles by LDS DMA)
+    MOC_HIP(hipStreamWaitEvent(main, ev[2], 0));
     SEQ_STAGE(kStBankDx, main,
               SEQ_TRY(moc_chapter_dx(dkv_edge, KV2, uniq, n_uniq, y.max_u, csr_off, csr_edge, red, sv + y.wkv_t,
                                      (int)d, KV2, MOC_BF16, dbank, d, 1, main)));

@@ -78,6 +78,15 @@ __global__ __launch_bounds__(256) void xattn_bwd_prep_kernel(const T* __restrict
   }
 }
 
+// One 16-byte-per-lane LDS DMA (buffer_load_dwordx4 ... lds): lane l's 16 bytes at voff (+ soff)
+// of the buffer land at LDS address m0 + 16 l.  The wait on these loads is an explicit vmcnt(0).
+typedef __attribute__((address_space(3))) void* bwd_lds_ptr_t;
+__device__ __forceinline__ void bq_dma16(__amdgpu_buffer_rsrc_t r, uint32_t voff, const char* lds,
+                                         uint32_t soff = 0) {
+  const uint32_t m0 = (uint32_t)(uintptr_t)(bwd_lds_ptr_t)lds;
+  asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(r), "s"(soff), "{m0}"(m0) : "memory");
+}
+
 // dq: one workgroup = 128 queries of one (sequence, head), loop over its slots.
 template <typename T>
 __global__ __launch_bounds__(kBThreads) void xattn_bwd_dq_kernel(
@@ -128,27 +137,44 @@ __global__ __launch_bounds__(kBThreads) void xattn_bwd_dq_kernel(
 
   const int32_t* su = slot_u + (size_t)b * NS;
   const float* om = omega + (size_t)b * NS;
+  // bf16: a slot's K and V tiles go global -> LDS by DMA (no registers held while in flight):
+  // 8 instructions of 1 KB (8 rows of 128 B) per tile, wave w issuing 2w and 2w + 1; lane l fills
+  // row 8 j + l / 8, physical chunk l % 8 = logical chunk (l % 8) ^ (row & 7) of Tile::off.
+  // fp32: through registers.
+  constexpr bool kDma = sizeof(T) == 2;
   TileIO<T, kBThreads> kio, vio;
   const uint32_t nbytes = (uint32_t)(kv_span * (int64_t)sizeof(T));
   const uint32_t row_bytes = (uint32_t)(kv_st * (int)sizeof(T));
   const Buf kb(ktiles, nbytes), vb(vtiles, nbytes);
   auto tile_off = [&](int u) { return (uint32_t)(((size_t)u * kv_su + (size_t)hk * kv_sh) * sizeof(T)); };
+  const uint32_t dma_v0 = (uint32_t)((16 * wave + (lane >> 3)) * row_bytes + 16 * ((lane & 7) ^ (lane >> 3)));
+  auto fetch = [&](int u, int buf) {
+    if constexpr (kDma) {
+      const uint32_t so = tile_off(u);
+      bq_dma16(kb.r, dma_v0, sK[buf] + 2048 * wave, so);
+      bq_dma16(kb.r, dma_v0 + 8 * row_bytes, sK[buf] + 2048 * wave + 1024, so);
+      bq_dma16(vb.r, dma_v0, sV[buf] + 2048 * wave, so);
+      bq_dma16(vb.r, dma_v0 + 8 * row_bytes, sV[buf] + 2048 * wave + 1024, so);
+    } else {
+      kio.load_rows(kb, tile_off(u), row_bytes, tid);
+      vio.load_rows(vb, tile_off(u), row_bytes, tid);
+    }
+  };
   int u_cur = su[0];
   if (u_cur >= 0) {
-    kio.load_rows(kb, tile_off(u_cur), row_bytes, tid);
-    vio.load_rows(vb, tile_off(u_cur), row_bytes, tid);
-    kio.store(sK[0], tid);
-    vio.store(sV[0], tid);
+    fetch(u_cur, 0);
+    if constexpr (!kDma) {
+      kio.store(sK[0], tid);
+      vio.store(sV[0], tid);
+    }
   }
-  vm_wait_all();  // Q / dO fragments have landed on every path into the loop
+  vm_wait_all();  // Q / dO fragments (and the first tiles) have landed on every path into the loop
   __syncthreads();
   for (int s = 0; s < NS; ++s) {
     const int buf = s & 1;
     const int u_next = (s + 1 < NS) ? su[s + 1] : -1;
-    if (u_next >= 0) {
-      kio.load_rows(kb, tile_off(u_next), row_bytes, tid);
-      vio.load_rows(vb, tile_off(u_next), row_bytes, tid);
-    }
+    // (buffer buf ^ 1 was last read in slot s - 1, which every wave has finished)
+    if (u_next >= 0) fetch(u_next, buf ^ 1);
     // a slot of zero router weight has dS = 0 (its keys and values are zero): no dQ contribution;
     // below the floor kTinyOmega its contribution is O(omega), below fp32 resolution
     const float w = u_cur >= 0 ? om[s] : 0.f;
@@ -209,8 +235,12 @@ __global__ __launch_bounds__(kBThreads) void xattn_bwd_dq_kernel(
       }
     }
     if (u_next >= 0) {
-      kio.store(sK[buf ^ 1], tid);
-      vio.store(sV[buf ^ 1], tid);
+      if constexpr (kDma) {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the next slot's tiles landed
+      } else {
+        kio.store(sK[buf ^ 1], tid);
+        vio.store(sV[buf ^ 1], tid);
+      }
     }
     u_cur = u_next;
     __syncthreads();
@@ -259,7 +289,7 @@ __global__ __launch_bounds__(kBThreads) void xattn_bwd_dq_kernel(
 // key halves summed in a fixed order.  The same loop serves omega == 0 (k~ = v~ = 0: every
 // logit of the chapter 0, t = -scale delta, dk = dv = 0).
 template <typename T> struct DkvCfg;
-template <> struct DkvCfg<bf16> { static constexpr int CPW = 2, QS = 64; };
+template <> struct DkvCfg<bf16> { static constexpr int CPW = 2, QS = 128; };
 template <> struct DkvCfg<float> { static constexpr int CPW = 2, QS = 32; };
 constexpr int kDkvWavesPerChapter = 2;
 
@@ -352,15 +382,39 @@ __global__ __launch_bounds__(64 * kDkvWavesPerChapter * DkvCfg<T>::CPW) void xat
       const int qq = r / (64 / EPC), cc = (r % (64 / EPC)) * EPC;
       voff_r[j] = (uint32_t)(((qq * H + hq) * 64 + cc) * (int)sizeof(T));
     }
-    V16 pre[2 * CPT];
+    // bf16: the Q and dO tiles go global -> LDS by DMA (buffer_load ... lds, no registers held
+    // while they are in flight): a tile is STB / 1 KB instructions of 8 rows of 128 B, wave w
+    // issues the IPW consecutive instructions IPW w .. of each tile; lane l fills row
+    // 8 j + l / 8, physical chunk l % 8, which holds logical chunk (l % 8) ^ (row & 7) of
+    // TileK::off.  fp32: through registers.
+    constexpr bool kDma = sizeof(T) == 2;
+    constexpr int IPW = STB / 1024 / NW;
+    static_assert(!kDma || (IPW * NW * 1024 == STB && IPW >= 1), "DMA staging geometry");
+    const int dlc = (lane & 7) ^ (lane >> 3);
+    const uint32_t dvo0 =
+        (uint32_t)((((8 * IPW * (tid >> 6) + (lane >> 3)) * H + hq) * 64 + 8 * dlc) * (int)sizeof(T));
+    constexpr uint32_t kDvoRows8 = 8u * 64u * (uint32_t)sizeof(T);  // x H: 8 rows further
+    V16 pre[kDma ? 1 : 2 * CPT];
     float preL = 0.f, preD = 0.f;
-    auto fetch = [&](int st) {
+    auto fetch = [&](int st, int buf) {
       const int q0 = st * QS;
       const uint32_t so_r = (uint32_t)((size_t)q0 * H * 64 * sizeof(T));
+      if constexpr (kDma) {
+        // rows past L: the row offset rides in the per-lane offset, which the bound checks
+        const char* l0 = sStage[buf][0] + 1024 * IPW * (tid >> 6);
+        const char* l1 = sStage[buf][1] + 1024 * IPW * (tid >> 6);
 #pragma unroll
-      for (int j = 0; j < CPT; ++j) {
-        pre[j] = bq.load16(voff_r[j], so_r);
-        pre[CPT + j] = bd.load16(voff_r[j], so_r);
+        for (int i = 0; i < IPW; ++i) {
+          const uint32_t vo = dvo0 + so_r + (uint32_t)i * kDvoRows8 * (uint32_t)H;
+          bq_dma16(bq.r, vo, l0 + 1024 * i);
+          bq_dma16(bd.r, vo, l1 + 1024 * i);
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < CPT; ++j) {
+          pre[j] = bq.load16(voff_r[j], so_r);
+          pre[CPT + j] = bd.load16(voff_r[j], so_r);
+        }
       }
       if (tid < QS) {
         preL = lse[bh * Lp + q0 + tid];
@@ -368,12 +422,14 @@ __global__ __launch_bounds__(64 * kDkvWavesPerChapter * DkvCfg<T>::CPW) void xat
       }
     };
     auto stash = [&](int buf) {
+      if constexpr (!kDma) {
 #pragma unroll
-      for (int j = 0; j < CPT; ++j) {
-        const int r = tid + NT * j;
-        const int qq = r / (64 / EPC), cc = (r % (64 / EPC)) * EPC;
-        st16(sStage[buf][0] + TileK::off(qq, cc), pre[j]);
-        st16(sStage[buf][1] + TileK::off(qq, cc), pre[CPT + j]);
+        for (int j = 0; j < CPT; ++j) {
+          const int r = tid + NT * j;
+          const int qq = r / (64 / EPC), cc = (r % (64 / EPC)) * EPC;
+          st16(sStage[buf][0] + TileK::off(qq, cc), pre[j]);
+          st16(sStage[buf][1] + TileK::off(qq, cc), pre[CPT + j]);
+        }
       }
       if (tid < QS) {
         // the accumulator starts -lse and -scale delta; negated and scaled here, not in fetch,
@@ -382,12 +438,14 @@ __global__ __launch_bounds__(64 * kDkvWavesPerChapter * DkvCfg<T>::CPW) void xat
         sDl[buf][tid] = -preD * scale;
       }
     };
-    fetch(0);
+    fetch(0, 0);
     stash(0);
+    if constexpr (kDma) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     for (int st = 0; st < nstep; ++st) {
       const int buf = st & 1;
-      if (st + 1 < nstep) fetch(st + 1);
+      // (buffer buf ^ 1 was last read in step st - 1, which every wave has finished)
+      if (st + 1 < nstep) fetch(st + 1, buf ^ 1);
       if (active) {
         const char* sQ = sStage[buf][0];
         const char* sD = sStage[buf][1];
@@ -448,6 +506,7 @@ __global__ __launch_bounds__(64 * kDkvWavesPerChapter * DkvCfg<T>::CPW) void xat
         }
       }
       if (st + 1 < nstep) stash(buf ^ 1);
+      if constexpr (kDma) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the next step's tiles landed
       __syncthreads();
     }
   }

@@ -49,6 +49,14 @@ __device__ __forceinline__ float quad_max_pl(float v) {
   return fmax_fast(c, d);
 }
 
+// One 16-byte-per-lane LDS DMA (buffer_load_dwordx4 ... lds): lane l's 16 bytes at voff + soff
+// of the buffer land at LDS address m0 + 16 l.  The wait on these loads is an explicit vmcnt(0).
+typedef __attribute__((address_space(3))) void* fwd_lds_ptr_t;
+__device__ __forceinline__ void fwd_dma16(__amdgpu_buffer_rsrc_t r, uint32_t voff, const char* lds, uint32_t soff) {
+  const uint32_t m0 = (uint32_t)(uintptr_t)(fwd_lds_ptr_t)lds;
+  asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(r), "s"(soff), "{m0}"(m0) : "memory");
+}
+
 template <typename T>
 __global__ __launch_bounds__(kFwdThreads) void xattn_fwd_kernel(
     const T* __restrict__ q, const T* __restrict__ ktiles, const T* __restrict__ vtiles,
@@ -107,13 +115,33 @@ __global__ __launch_bounds__(kFwdThreads) void xattn_fwd_kernel(
   const Buf kb(ktiles, (uint32_t)(kv_span * (int64_t)sizeof(T))), vb(vtiles, (uint32_t)(kv_span * (int64_t)sizeof(T)));
   auto tile_off = [&](int u) { return (uint32_t)(((size_t)u * kv_su + (size_t)hk * kv_sh) * sizeof(T)); };
   const uint32_t row_bytes = (uint32_t)(kv_st * (int)sizeof(T));
+  // bf16: a slot's K and V tiles go global -> LDS by DMA (no registers held while in flight):
+  // 8 instructions of 1 KB (8 rows of 128 B) per tile, wave w issuing 2w and 2w + 1; lane l fills
+  // row 8 j + l / 8, physical chunk l % 8 = logical chunk (l % 8) ^ (row & 7) of Tile::off.
+  // fp32: through registers.
+  constexpr bool kDma = sizeof(T) == 2;
+  static_assert(!kDma || (kFwdThreads == 256 && TB == 8192), "DMA staging geometry");
+  const uint32_t dma_v0 = (uint32_t)((16 * wave + (lane >> 3)) * row_bytes + 16 * ((lane & 7) ^ (lane >> 3)));
+  auto fetch = [&](int u, int buf) {
+    if constexpr (kDma) {
+      const uint32_t so = tile_off(u);
+      fwd_dma16(kb.r, dma_v0, sK[buf] + 2048 * wave, so);
+      fwd_dma16(kb.r, dma_v0 + 8 * row_bytes, sK[buf] + 2048 * wave + 1024, so);
+      fwd_dma16(vb.r, dma_v0, sV[buf] + 2048 * wave, so);
+      fwd_dma16(vb.r, dma_v0 + 8 * row_bytes, sV[buf] + 2048 * wave + 1024, so);
+    } else {
+      kio.load_rows(kb, tile_off(u), row_bytes, tid);
+      vio.load_rows(vb, tile_off(u), row_bytes, tid);
+    }
+  };
 
   int u_cur = su[0];
   if (u_cur >= 0) {
-    kio.load_rows(kb, tile_off(u_cur), row_bytes, tid);
-    vio.load_rows(vb, tile_off(u_cur), row_bytes, tid);
-    kio.store(sK[0], tid);
-    vio.store(sV[0], tid);
+    fetch(u_cur, 0);
+    if constexpr (!kDma) {
+      kio.store(sK[0], tid);
+      vio.store(sV[0], tid);
+    }
   }
   // Q fragments must have landed before the loop on every path (also when slot 0
   // is skipped); otherwise the wait for them inside the loop can't be told apart
@@ -124,10 +152,8 @@ __global__ __launch_bounds__(kFwdThreads) void xattn_fwd_kernel(
   for (int s = 0; s < NS; ++s) {
     const int buf = s & 1;
     const int u_next = (s + 1 < NS) ? su[s + 1] : -1;
-    if (u_next >= 0) {
-      kio.load_rows(kb, tile_off(u_next), row_bytes, tid);
-      vio.load_rows(vb, tile_off(u_next), row_bytes, tid);
-    }
+    // (buffer buf ^ 1 was last read in slot s - 1, which every wave has finished)
+    if (u_next >= 0) fetch(u_next, buf ^ 1);
     if (u_cur >= 0) {
       const float w = om[s];
       const float c = w * scale_log2;
@@ -219,8 +245,12 @@ __global__ __launch_bounds__(kFwdThreads) void xattn_fwd_kernel(
       }
     }
     if (u_next >= 0) {
-      kio.store(sK[buf ^ 1], tid);
-      vio.store(sV[buf ^ 1], tid);
+      if constexpr (kDma) {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the next slot's tiles landed
+      } else {
+        kio.store(sK[buf ^ 1], tid);
+        vio.store(sV[buf ^ 1], tid);
+      }
     }
     u_cur = u_next;
     __syncthreads();

@@ -69,8 +69,8 @@ def assert_parity(got, ref, dtype, what="", bf16_atol=BF16_ATOL, fp32_rtol=FP32_
                f"max|ref| {amax:.3e} -> {'PASS' if ok else 'FAIL'}")
     else:
         ok = mabs <= bf16_atol and relmax <= bf16_atol
-        tag = "" if s == 1.0 else f" x{s:g}"
-        msg = (f"{what}: bf16 max-abs{tag} {mabs:.3e}, rel-max {relmax:.3e} (gate {bf16_atol:.0e}) "
+        tag = f" {mabs:.3e}" if s == 1.0 else f" x{s:g} {mabs:.3e} (unscaled {mabs / s:.3e})"
+        msg = (f"{what}: bf16 max-abs{tag}, rel-max {relmax:.3e} (gate {bf16_atol:.0e}) "
                f"max|ref| {amax:.3e} -> {'PASS' if ok else 'FAIL'}")
     print(msg, flush=True)
     assert ok, msg

@@ -107,6 +107,9 @@ def test_config1_recipe_scale_router_losses(gpu_device):
     ref, det = O.sequence_memory_layer(h.double(), bank.double(), Wr.double(), br.double(), Wq.double(),
                                        Wk.double(), Wv.double(), Wo.double(), H=c["H"], HK=c["H"], C=c["C"],
                                        T=c["T"], S=c["S"], top_k=c["k"], routed_scale=c["s"], return_details=True)
+    idx_star, _, _ = layer.route(h.to(dev), return_losses=False)
+    assert torch.equal(idx_star.cpu(), det["idx_star"]), "chapter selection differs from the oracle's"
+    assert_parity(out, ref, torch.float32, "out")
     assert_rel(out, ref, 1e-4, "out")
     for k in ("load_balance", "auxiliary", "z_loss", "entropy"):
         assert_rel(losses[k].reshape(1), det["losses"][k].reshape(1), 1e-5, k)
