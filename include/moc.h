@@ -525,15 +525,16 @@ int moc_sparse_bwd_prep(int dtype, const void* dout, const void* out, const void
  * dq parts [E * rpe][64] in the call's dtype; dlog f32 [E * rpe] (modes 2-3, d loss / d log weight).
  * delta_row: modes 1-3 read the joint delta [tokens * rpe] of moc_sparse_bwd_prep; mode 0
  * WRITES the per-chapter delta dout . o_s [E * rpe] (computed from P and dO V^T), the input
- * of moc_sparse_dw.  bf16 runs one wave per (chapter, kv head) and needs 16-byte aligned
- * q / dout / k / v / dq_part, 8-byte aligned dk / dv, cs / hs / rs multiples of 8 and
- * ocs / ohs / ors multiples of 4. */
+ * of moc_sparse_dw.  bf16 runs two waves per (chapter, kv head) and needs 16-byte aligned
+ * q / dout / k / v / dq_part / dk / dv and cs / hs / rs / ocs / ohs / ors multiples of 8.  row_tab (bf16 only, may be NULL): moc_plan_row_table of width
+ * 32 over this plan; a unit then reads its first block's edges from it together with its plan
+ * entries instead of after them. */
 int moc_sparse_bwd(int dtype, const void* q, const void* dout, int64_t ntok, int HQ, const void* k, const void* v,
                    int64_t cs, int64_t hs, int64_t rs, int HK, int Dh, const int32_t* uniq, const int32_t* n_uniq,
                    const int32_t* csr_off, const int32_t* csr_edge, int64_t max_u, int S, int hk0, int nhk,
                    int hq_off, int rpe, int mode, const float* lse_row, float* delta_row, const float* w,
                    float scale, void* dk, void* dv, int64_t ocs, int64_t ohs, int64_t ors, void* dq_part,
-                   float* dlog, hipStream_t stream);
+                   float* dlog, const int32_t* row_tab, hipStream_t stream);
 /* dq [tokens][HQ][64] rows hq_off .. hq_off+rpe-1 = sum over valid slots of dq_part. */
 int moc_sparse_dq_combine(int dtype, const void* dq_part, const int32_t* edge_u, int S, int rpe, int64_t ntok,
                           int HQ, int hq_off, void* dq, hipStream_t stream);
@@ -567,6 +568,10 @@ int moc_decode_partial(int dtype, const void* q, int64_t B, int H, const void* k
  * edges (csr order) of each distinct chapter of the plan, -1 padded (no reference counterpart: a
  * precomputed index of the same plan).  moc_decode_partial reads it (when non-NULL) instead of
  * csr_edge for a unit's first 16 rows. */
+/* The same index of any width: row_tab i32 [max_u][width] = the first `width` edges (csr order) of
+ * each distinct chapter, -1 padded; width 16 (moc_decode_partial) or 32 (moc_sparse_bwd). */
+int moc_plan_row_table(const int32_t* n_uniq, const int32_t* csr_off, const int32_t* csr_edge, int64_t max_u,
+                       int width, int32_t* row_tab, hipStream_t stream);
 int moc_decode_row_table(const int32_t* n_uniq, const int32_t* csr_off, const int32_t* csr_edge, int64_t max_u,
                          int32_t* row_tab, hipStream_t stream);
 

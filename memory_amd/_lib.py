@@ -93,12 +93,13 @@ _SIGS = {
     "moc_sparse_combine": (_I, [_I, _P, _P, _P, _P, _I, _I, _I, _I64, _I, _I, _P, _P, _P]),
     "moc_sparse_bwd_prep": (_I, [_I, _P, _P, _P, _P, _I, _I, _I, _I64, _I, _I, _P, _P]),
     "moc_sparse_bwd": (_I, [_I, _P, _P, _I64, _I, _P, _P, _I64, _I64, _I64, _I, _I, _P, _P, _P, _P, _I64, _I, _I,
-                            _I, _I, _I, _I, _P, _P, _P, _F, _P, _P, _I64, _I64, _I64, _P, _P, _P]),
+                            _I, _I, _I, _I, _P, _P, _P, _F, _P, _P, _I64, _I64, _I64, _P, _P, _P, _P]),
     "moc_sparse_dq_combine": (_I, [_I, _P, _P, _I, _I, _I64, _I, _I, _P, _P]),
     "moc_sparse_dw": (_I, [_P, _P, _P, _I, _I, _I64, _P, _P]),
     "moc_sparse_zero_untouched": (_I, [_I, _P, _P, _I64, _I64, _I64, _I64, _I, _I, _P, _P, _I64, _P, _P]),
     "moc_decode_partial": (_I, [_I, _P, _I64, _I, _P, _P, _I, _I, _I, _P, _P, _P, _P, _I64, _P, _I, _F, _P, _P, _P,
                                 _P]),
+    "moc_plan_row_table": (_I, [_P, _P, _P, _I64, _I, _P, _P]),
     "moc_decode_row_table": (_I, [_P, _P, _P, _I64, _P, _P]),
     "moc_gather_rows": (_I, [_I, _P, _I, _I64, _I, _P, _P, _I64, _P, _P, _P, _P]),
     "moc_bank_scatter": (_I, [_I, _P, _P, _I, _I64, _I, _P, _P, _I64, _P, _P, _P, _P, _I, _P, _P]),

@@ -24,15 +24,15 @@ using namespace moc;
 
 namespace {
 
-// row_tab[u * 16 + j] = the j-th edge (csr order) of distinct chapter u, -1 past its edges or past
+// row_tab[u * W + j] = the j-th edge (csr order) of distinct chapter u, -1 past its edges or past
 // n_uniq; one thread per entry.
 __global__ __launch_bounds__(256) void decode_row_table_kernel(const int32_t* __restrict__ n_uniq,
                                                                const int32_t* __restrict__ csr_off,
                                                                const int32_t* __restrict__ csr_edge, int64_t max_u,
-                                                               int32_t* __restrict__ row_tab) {
+                                                               int W, int32_t* __restrict__ row_tab) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const int64_t u = i / 16;
-  const int j = (int)(i % 16);
+  const int64_t u = i / W;
+  const int j = (int)(i % W);
   if (u >= max_u) return;
   int32_t e = -1;
   if (u < n_uniq[0]) {
@@ -46,15 +46,21 @@ __global__ __launch_bounds__(256) void decode_row_table_kernel(const int32_t* __
 
 extern "C" {
 
-int moc_decode_row_table(const int32_t* n_uniq, const int32_t* csr_off, const int32_t* csr_edge, int64_t max_u,
-                         int32_t* row_tab, hipStream_t stream) {
-  MOC_REQUIRE(n_uniq && csr_off && csr_edge && row_tab, MOC_ERR_ARG, "moc_decode_row_table: null pointer");
-  MOC_REQUIRE(max_u >= 0 && max_u < ((int64_t)1 << 30), MOC_ERR_ARG, "moc_decode_row_table: max_u %lld",
+int moc_plan_row_table(const int32_t* n_uniq, const int32_t* csr_off, const int32_t* csr_edge, int64_t max_u,
+                       int width, int32_t* row_tab, hipStream_t stream) {
+  MOC_REQUIRE(n_uniq && csr_off && csr_edge && row_tab, MOC_ERR_ARG, "moc_plan_row_table: null pointer");
+  MOC_REQUIRE(width == 16 || width == 32, MOC_ERR_ARG, "moc_plan_row_table: width %d (16 or 32)", width);
+  MOC_REQUIRE(max_u >= 0 && max_u < ((int64_t)1 << 25), MOC_ERR_ARG, "moc_plan_row_table: max_u %lld",
               (long long)max_u);
   if (max_u == 0) return MOC_OK;
-  hipLaunchKernelGGL(decode_row_table_kernel, dim3((unsigned)((max_u * 16 + 255) / 256)), dim3(256), 0, stream,
-                     n_uniq, csr_off, csr_edge, max_u, row_tab);
+  hipLaunchKernelGGL(decode_row_table_kernel, dim3((unsigned)((max_u * width + 255) / 256)), dim3(256), 0, stream,
+                     n_uniq, csr_off, csr_edge, max_u, width, row_tab);
   return check_launch("decode_row_table_kernel");
+}
+
+int moc_decode_row_table(const int32_t* n_uniq, const int32_t* csr_off, const int32_t* csr_edge, int64_t max_u,
+                         int32_t* row_tab, hipStream_t stream) {
+  return moc_plan_row_table(n_uniq, csr_off, csr_edge, max_u, 16, row_tab, stream);
 }
 
 int moc_decode_partial(int dtype, const void* q, int64_t B, int H, const void* k_tiles, const void* v_tiles, int HK,

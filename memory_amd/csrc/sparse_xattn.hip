@@ -925,44 +925,58 @@ __global__ __launch_bounds__(64 * kBwdWaves) void sparse_bwd_unit_kernel(
     int64_t max_u, int S, int hk0, int nhk, int hq_off, int rpe, int mode, const float* __restrict__ lse_row,
     float* __restrict__ delta_row, const float* __restrict__ w, float scale_log2, float scale, bf16* __restrict__ dk,
     bf16* __restrict__ dv, int64_t ocs, int64_t ohs, int64_t ors, bf16* __restrict__ dq_part,
-    float* __restrict__ dlog) {
+    float* __restrict__ dlog, const int32_t* __restrict__ row_tab, uint32_t qbytes) {
   using Tile = SwzTile<bf16, 64>;
   constexpr int kKB = 64 * 64 * 2, kRB = 32 * 64 * 2;
-  __shared__ __attribute__((aligned(16))) char sK[kKB];    // K [key][dim]
-  __shared__ __attribute__((aligned(16))) char sQ[kRB];    // Q rows of the block [row][dim]
-  __shared__ __attribute__((aligned(16))) char sD[kRB];    // dO rows
-  __shared__ __attribute__((aligned(16))) char sDS[kRB];   // dS [key][row] (DsTile)
+  __shared__ __attribute__((aligned(1024))) char sK[kKB];   // K [key][dim]
+  __shared__ __attribute__((aligned(1024))) char sV[kKB];   // V [key][dim]
+  __shared__ __attribute__((aligned(1024))) char sQ[kRB];   // Q rows of the block [row][dim]
+  __shared__ __attribute__((aligned(1024))) char sD[kRB];   // dO rows
+  __shared__ __attribute__((aligned(16))) char sDS[kRB];    // dS [key][row] (DsTile)
+  __shared__ __attribute__((aligned(1024))) char sDQ[kRB];  // the block's dQ rows [row][dim]
   __shared__ float sLse[32], sDel[32], sWr[32], sPart[kBwdWaves][2][32];
   __shared__ int sEr[32];
   const int G = HQ / HK;
   const int64_t unit = blockIdx.x;
   const int u = (int)(unit / nhk);
   if (u >= max_u) return;                 // whole workgroup (before any barrier)
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
+  // with a row table (the first 32 edges of every distinct chapter) the first block's edge ids
+  // are requested together with the plan entries: they depend on the unit only.  Per lane: the
+  // two rows its DMA instructions move (16 wave + 8 i + lane / 8) and the constants' row lane & 31
+  int tab_d[2] = {-1, -1}, tab_c = -1;
+  if (row_tab) {
+    const int32_t* tb = row_tab + (int64_t)u * 32;
+    tab_d[0] = tb[(16 * wave + (lane >> 3)) / G];
+    tab_d[1] = tb[(16 * wave + 8 + (lane >> 3)) / G];
+    tab_c = tb[(lane & 31) / G];
+  }
   const int nu = n_uniq[0];
   const int hk = hk0 + (int)(unit % nhk);
   const int gid = uniq[u];
   const int p0 = csr_off[u];
   const int nrows = (csr_off[u + 1] - p0) * G;
   if (u >= nu) return;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
   const int key0 = 32 * wave;
   const int64_t kv0 = (int64_t)gid * cs + (int64_t)hk * hs;
-  // K, V of this wave's keys as the B operands of S / dPu (lane = key); K staged for K^T
-  bf16x8 kf[2][2], vf[2][2];
+  // 16-byte LDS DMA geometry: an instruction fills 8 rows of 128 B; lane l -> row 8 i + l / 8,
+  // physical chunk l % 8, which holds logical chunk (l % 8) ^ (row & 7) of Tile::off
+  const int dlc = (lane & 7) ^ (lane >> 3);
+  {
+    // K and V tiles -> LDS (K the B operand of S and, transposed, of dQ; V the B operand of dPu):
+    // wave w moves keys 32 w .. 32 w + 31 of each
+    const __amdgpu_buffer_rsrc_t kr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<bf16*>(k + kv0), (short)0, (int)((63 * rs + 64) * 2), 0x00020000);
+    const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<bf16*>(v + kv0), (short)0, (int)((63 * rs + 64) * 2), 0x00020000);
 #pragma unroll
-  for (int j = 0; j < 2; ++j)
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      const int64_t off = kv0 + (key0 + 16 * j + c16) * rs + 32 * ks + 8 * g;
-      kf[j][ks] = Load8<bf16, bf16>::run(k + off);
-      vf[j][ks] = Load8<bf16, bf16>::run(v + off);
+    for (int i = 0; i < 4; ++i) {
+      const int key = 8 * (4 * wave + i) + (lane >> 3);
+      unit_dma16(kr, (uint32_t)((key * rs + 8 * dlc) * 2), sK + 1024 * (4 * wave + i));
+      unit_dma16(vr, (uint32_t)((key * rs + 8 * dlc) * 2), sV + 1024 * (4 * wave + i));
     }
-#pragma unroll
-  for (int j = 0; j < 2; ++j)
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
-      *reinterpret_cast<bf16x8*>(sK + Tile::off(key0 + 16 * j + c16, 32 * ks + 8 * g)) = kf[j][ks];
+  }
   f32x4 dkt[4][2], dvt[4][2];   // [db][j]: lane = key key0 + 16 j + c16, dims 16 db + 4 g + x
 #pragma unroll
   for (int db = 0; db < 4; ++db)
@@ -971,35 +985,34 @@ __global__ __launch_bounds__(64 * kBwdWaves) void sparse_bwd_unit_kernel(
       dkt[db][j] = f32x4{0.f, 0.f, 0.f, 0.f};
       dvt[db][j] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
-  // rows of a block as A operands (lane = row 16 qb + c16, both waves) and the per-row
-  // constants (wave 0, one lane per row); block r0 + 32 is fetched while r0 computes
-  bf16x8 qa[2][2], da[2][2];
-  int erow_n[2];
+  // the rows of a block (q, dO) go to LDS by DMA, wave w moving rows 16 w .. 16 w + 15; rows past
+  // the unit's read from an offset past the buffer, i.e. zeros.  The per-row constants (wave 0,
+  // one lane per row) are loaded into registers and staged at the block's start.
+  const __amdgpu_buffer_rsrc_t qr = __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16*>(q), (short)0, (int)qbytes,
+                                                                      0x00020000);
+  const __amdgpu_buffer_rsrc_t dr = __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16*>(dout), (short)0,
+                                                                      (int)qbytes, 0x00020000);
   float c_lse = INFINITY, c_del = 0.f, c_w = 0.f;
   int c_er = -1;
   auto fetch_rows = [&](int r0) {
 #pragma unroll
-    for (int qb = 0; qb < 2; ++qb) {
-      const int r = r0 + 16 * qb + c16;
-      erow_n[qb] = -1;
-      qa[qb][0] = qa[qb][1] = da[qb][0] = da[qb][1] = zero_frag<bf16>();
+    for (int i = 0; i < 2; ++i) {
+      const int r = r0 + 16 * wave + 8 * i + (lane >> 3);
+      uint32_t off = 0xFFFFFFF0u;   // >= qbytes (host check): the load returns zeros
       if (r < nrows) {
-        const int e = csr_edge[p0 + r / G];
+        const int e = row_tab && r0 == 0 ? tab_d[i] : csr_edge[p0 + r / G];
         const int hq = hk * G + r % G;
-        erow_n[qb] = e * rpe + (hq - hq_off);
-        const int64_t off = ((int64_t)(e / S) * HQ + hq) * kSpDh + 8 * g;
-        qa[qb][0] = Load8<bf16, bf16>::run(q + off);
-        qa[qb][1] = Load8<bf16, bf16>::run(q + off + 32);
-        da[qb][0] = Load8<bf16, bf16>::run(dout + off);
-        da[qb][1] = Load8<bf16, bf16>::run(dout + off + 32);
+        off = (uint32_t)((((int64_t)(e / S) * HQ + hq) * kSpDh + 8 * dlc) * 2);
       }
+      unit_dma16(qr, off, sQ + 1024 * (2 * wave + i));
+      unit_dma16(dr, off, sD + 1024 * (2 * wave + i));
     }
     c_lse = INFINITY;
     c_del = c_w = 0.f;
     c_er = -1;
     const int r = r0 + (lane & 31);
     if (wave == 0 && lane < 32 && r < nrows) {
-      const int e = csr_edge[p0 + r / G];
+      const int e = row_tab && r0 == 0 ? tab_c : csr_edge[p0 + r / G];
       const int hr = hk * G + r % G - hq_off;
       c_er = e * rpe + hr;
       if (mode == 0) {
@@ -1016,23 +1029,14 @@ __global__ __launch_bounds__(64 * kBwdWaves) void sparse_bwd_unit_kernel(
   fetch_rows(0);
   for (int r0 = 0; r0 < nrows; r0 += 32) {
     const bool two = r0 + 16 < nrows;
-    const int erow_a[2] = {erow_n[0], erow_n[1]};
     if (wave == 0 && lane < 32) {
       sLse[lane] = c_lse;
       sDel[lane] = c_del;
       sWr[lane] = c_w;
       sEr[lane] = c_er;
     }
-    // wave w stages rows 16 w .. 16 w + 15
-#pragma unroll
-    for (int qb = 0; qb < 2; ++qb)
-      if (qb == wave) {
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-          *reinterpret_cast<bf16x8*>(sQ + Tile::off(16 * qb + c16, 32 * ks + 8 * g)) = qa[qb][ks];
-          *reinterpret_cast<bf16x8*>(sD + Tile::off(16 * qb + c16, 32 * ks + 8 * g)) = da[qb][ks];
-        }
-      }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // this wave's DMA (K at the first block, the rows)
+    __syncthreads();   // (1) rows, K and the constants visible to both waves
     // ---- S and dPu for this wave's keys (lane = key, rows 16 qb + 4 g + x)
     f32x4 sc[2][2], dp[2][2];
 #pragma unroll
@@ -1041,33 +1045,38 @@ __global__ __launch_bounds__(64 * kBwdWaves) void sparse_bwd_unit_kernel(
       for (int j = 0; j < 2; ++j) {
         sc[qb][j] = f32x4{0.f, 0.f, 0.f, 0.f};
         dp[qb][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-        if (qb == 0 || two) {
+      }
 #pragma unroll
-          for (int ks = 0; ks < 2; ++ks) {
-            mma(sc[qb][j], qa[qb][ks], kf[j][ks]);
-            mma(dp[qb][j], da[qb][ks], vf[j][ks]);
+    for (int ks = 0; ks < 2; ++ks) {
+      bf16x8 kf[2], vf[2];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        kf[j] = Tile::frag(sK, key0 + 16 * j + c16, 32 * ks + 8 * g);
+        vf[j] = Tile::frag(sV, key0 + 16 * j + c16, 32 * ks + 8 * g);
+      }
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb)
+        if (qb == 0 || two) {
+          const bf16x8 qa = Tile::frag(sQ, 16 * qb + c16, 32 * ks + 8 * g);
+          const bf16x8 da = Tile::frag(sD, 16 * qb + c16, 32 * ks + 8 * g);
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            mma(sc[qb][j], qa, kf[j]);
+            mma(dp[qb][j], da, vf[j]);
           }
         }
-      }
-    if (r0 + 32 < nrows) fetch_rows(r0 + 32);
-    __syncthreads();   // (1) staged rows, constants (and K) visible to both waves
-    float lr[2][4], dr[2][4], wr[2][4];
+    }
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb)
 #pragma unroll
       for (int x = 0; x < 4; ++x) {
         const int rr = 16 * qb + 4 * g + x;
-        lr[qb][x] = sLse[rr];
-        dr[qb][x] = sDel[rr];
-        wr[qb][x] = sWr[rr];
+        const float lr = sLse[rr], wr = sWr[rr];
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          sc[qb][j][x] = exp2f(sc[qb][j][x] * scale_log2 + (mode == 0 ? 0.f : wr) - lr);
       }
-#pragma unroll
-    for (int qb = 0; qb < 2; ++qb)
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int x = 0; x < 4; ++x)
-          sc[qb][j][x] = exp2f(sc[qb][j][x] * scale_log2 + (mode == 0 ? 0.f : wr[qb][x]) - lr[qb][x]);
+    float dr[2][4];
     if (mode == 0) {
       // per-chapter softmax delta: this wave's 32 keys, then both halves in order
 #pragma unroll
@@ -1093,6 +1102,11 @@ __global__ __launch_bounds__(64 * kBwdWaves) void sparse_bwd_unit_kernel(
         const int er = sEr[lane];
         if (er >= 0) delta_row[er] = sPart[0][0][lane] + sPart[1][0][lane];
       }
+    } else {
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+        for (int x = 0; x < 4; ++x) dr[qb][x] = sDel[16 * qb + 4 * g + x];
     }
     bf16x8 pa[2], sa[2];
     float rsum[2][4];
@@ -1103,16 +1117,17 @@ __global__ __launch_bounds__(64 * kBwdWaves) void sparse_bwd_unit_kernel(
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb)
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
+      for (int x = 0; x < 4; ++x) {
+        const float wr = mode == 0 ? sWr[16 * qb + 4 * g + x] : 1.f;
 #pragma unroll
-        for (int x = 0; x < 4; ++x) {
-          const float p = sc[qb][j][x];
-          const float pw = mode == 0 ? wr[qb][x] * p : p;
+        for (int j = 0; j < 2; ++j) {
+          const float pw = wr * sc[qb][j][x];
           const float ds = pw * (dp[qb][j][x] - dr[qb][x]);
           rsum[qb][x] += ds;
           pa[j][4 * qb + x] = (bf16)pw;
           sa[j][4 * qb + x] = (bf16)ds;
         }
+      }
     // ---- dV^T += dO^T P, dK^T += Q^T dS
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
@@ -1146,11 +1161,14 @@ __global__ __launch_bounds__(64 * kBwdWaves) void sparse_bwd_unit_kernel(
           if (c16 == 0) sPart[wave][1][16 * qb + 4 * g + x] = t;
         }
     }
-    __syncthreads();   // (3) dS and the row-sum halves visible
+    __syncthreads();   // (3) dS and the row-sum halves visible; the rows and constants are read
     if (dlog && wave == 0 && lane < 32) {
       const int er = sEr[lane];
       if (er >= 0) dlog[er] = sPart[0][1][lane] + sPart[1][1][lane];
     }
+    // the next block's rows go out now (sQ / sD are no longer read in this block) and land
+    // during the dQ product
+    if (r0 + 32 < nrows) fetch_rows(r0 + 32);
     // ---- dQ^T = K^T dS^T for dims 32 wave .. + 31: lane = row 16 qb + c16, dims 16 db + 4 g + x
     f32x4 dq[2][2];
 #pragma unroll
@@ -1170,31 +1188,60 @@ __global__ __launch_bounds__(64 * kBwdWaves) void sparse_bwd_unit_kernel(
           if (qb == 0 || two) mma(dq[i][qb], ak, bs[qb]);
       }
     }
+    // dQ rows staged as [row][dim] in LDS, then stored as whole 128-byte rows (16 bytes per lane,
+    // chunks threadIdx + 128 t: row chunk / 8, 16-byte chunk chunk % 8); the rows' edge slots are
+    // read before the barrier (the next block's constants replace them after it)
 #pragma unroll
-    for (int qb = 0; qb < 2; ++qb) {
-      if (erow_a[qb] < 0) continue;
-      bf16* dst = dq_part + (int64_t)erow_a[qb] * kSpDh + 32 * wave + 4 * g;
+    for (int qb = 0; qb < 2; ++qb)
 #pragma unroll
-      for (int i = 0; i < 2; ++i) part_store4(dst + 16 * i, dq[i][qb] * scale);
+      for (int i = 0; i < 2; ++i) {
+        const f32x4 t = dq[i][qb] * scale;
+        const bf16x4 b = {(bf16)t[0], (bf16)t[1], (bf16)t[2], (bf16)t[3]};
+        *reinterpret_cast<bf16x4*>(sDQ + Tile::off(16 * qb + c16, 32 * wave + 16 * i + 4 * g)) = b;
+      }
+    int er_st[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) er_st[t] = sEr[(threadIdx.x + 128 * t) >> 3];
+    __syncthreads();   // (4) the block's dQ rows staged
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int cid = threadIdx.x + 128 * t, row = cid >> 3, ch = cid & 7;
+      if (er_st[t] >= 0)
+        *reinterpret_cast<bf16x8*>(dq_part + (int64_t)er_st[t] * kSpDh + 8 * ch) =
+            *reinterpret_cast<const bf16x8*>(sDQ + Tile::off(row, 8 * ch));
     }
   }
-  // ---- dK = scale (dK^T)^T, dV: lane = key, 4 consecutive dims per store
-  bf16* dkb = dk + (int64_t)gid * ocs + (int64_t)hk * ohs;
-  bf16* dvb = dv + (int64_t)gid * ocs + (int64_t)hk * ohs;
+  // ---- dK = scale (dK^T)^T, dV: the accumulators (lane = key, 4 consecutive dims each) are
+  // staged as [key][dim] rows in the K / V tiles' LDS (free once both waves have finished the
+  // last dQ product), then stored as whole 128-byte rows, 16 bytes per lane
+  __syncthreads();
 #pragma unroll
   for (int j = 0; j < 2; ++j)
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
-      const int64_t off = (int64_t)(key0 + 16 * j + c16) * ors + 16 * db + 4 * g;
+      const int key = key0 + 16 * j + c16;
       bf16x4 a, b;
 #pragma unroll
       for (int x = 0; x < 4; ++x) {
         a[x] = (bf16)(dkt[db][j][x] * scale);
         b[x] = (bf16)dvt[db][j][x];
       }
-      *reinterpret_cast<bf16x4*>(dkb + off) = a;
-      *reinterpret_cast<bf16x4*>(dvb + off) = b;
+      *reinterpret_cast<bf16x4*>(sK + Tile::off(key, 16 * db + 4 * g)) = a;
+      *reinterpret_cast<bf16x4*>(sV + Tile::off(key, 16 * db + 4 * g)) = b;
     }
+  // each wave reads back its own keys' rows (LDS operations of a wave complete in order)
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  bf16* dkb = dk + (int64_t)gid * ocs + (int64_t)hk * ohs;
+  bf16* dvb = dv + (int64_t)gid * ocs + (int64_t)hk * ohs;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int key = key0 + 8 * i + (lane >> 3), ch = lane & 7;
+    const int64_t off = (int64_t)key * ors + 8 * ch;
+    *reinterpret_cast<bf16x8*>(dkb + off) = *reinterpret_cast<const bf16x8*>(sK + Tile::off(key, 8 * ch));
+    *reinterpret_cast<bf16x8*>(dvb + off) = *reinterpret_cast<const bf16x8*>(sV + Tile::off(key, 8 * ch));
+  }
 }
 
 // dK / dV blocks (chapter, kv head) that no edge of a plan touched: the sparse backward
@@ -1335,7 +1382,7 @@ int moc_sparse_bwd(int dtype, const void* q, const void* dout, int64_t ntok, int
                    const int32_t* csr_off, const int32_t* csr_edge, int64_t max_u, int S, int hk0, int nhk,
                    int hq_off, int rpe, int mode, const float* lse_row, float* delta_row, const float* w,
                    float scale, void* dk, void* dv, int64_t ocs, int64_t ohs, int64_t ors, void* dq_part,
-                   float* dlog, hipStream_t stream) {
+                   float* dlog, const int32_t* row_tab, hipStream_t stream) {
   MOC_REQUIRE(q && dout && k && v && uniq && n_uniq && csr_off && csr_edge && lse_row && delta_row && dk && dv &&
                   dq_part,
               MOC_ERR_ARG, "moc_sparse_bwd: null pointer");
@@ -1348,16 +1395,21 @@ int moc_sparse_bwd(int dtype, const void* q, const void* dout, int64_t ntok, int
   const float sl2 = scale * 1.4426950408889634f;
   if (dtype == MOC_BF16) {
     MOC_REQUIRE(unit_kv_aligned(q, k, v, cs, hs, rs) && ((uintptr_t)dout & 15) == 0 && ((uintptr_t)dq_part & 15) == 0 &&
-                    ((uintptr_t)dk & 7) == 0 && ((uintptr_t)dv & 7) == 0 && ocs % 4 == 0 && ohs % 4 == 0 &&
-                    ors % 4 == 0,
+                    ((uintptr_t)dk & 15) == 0 && ((uintptr_t)dv & 15) == 0 && ocs % 8 == 0 && ohs % 8 == 0 &&
+                    ors % 8 == 0,
                 MOC_ERR_ARG,
-                "moc_sparse_bwd: bf16 needs 16-byte aligned q/dout/k/v/dq_part, 8-byte aligned dk/dv, input strides "
-                "that are multiples of 8 and output strides that are multiples of 4");
+                "moc_sparse_bwd: bf16 needs 16-byte aligned q/dout/k/v/dq_part/dk/dv and strides that are "
+                "multiples of 8");
+    // q / dout rows are moved by bounded buffer loads (rows past a unit read zeros from offsets
+    // past the buffer)
+    const int64_t qbytes = ntok * HQ * kSpDh * 2;
+    MOC_REQUIRE(qbytes < ((int64_t)1 << 32) - 16, MOC_ERR_UNSUPPORTED,
+                "moc_sparse_bwd: q / dout of %lld bytes (bf16 needs < 4 GiB)", (long long)qbytes);
     const int64_t units = max_u * nhk;
     hipLaunchKernelGGL(sparse_bwd_unit_kernel, dim3((unsigned)units), dim3(64 * kBwdWaves), 0, stream, (const bf16*)q, (const bf16*)dout, HQ, (const bf16*)k,
                        (const bf16*)v, cs, hs, rs, HK, uniq, n_uniq, csr_off, csr_edge, max_u, S, hk0, nhk, hq_off,
                        rpe, mode, lse_row, delta_row, w, sl2, scale, (bf16*)dk, (bf16*)dv, ocs, ohs, ors,
-                       (bf16*)dq_part, dlog);
+                       (bf16*)dq_part, dlog, row_tab, (uint32_t)qbytes);
     return check_launch("sparse_bwd_unit_kernel");
   } else if (dtype == MOC_F32)
     hipLaunchKernelGGL(sparse_bwd_kernel<float>, grid, dim3(sp_threads<float>()), 0, stream, (const float*)q,

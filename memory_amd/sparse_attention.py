@@ -120,10 +120,17 @@ def _backward(q, k, v, layout, out, dout, segments, saved, mode, S, scale, dk, d
                  ptr(sg.plan.uniq), ptr(sg.plan.n_uniq), sg.plan.max_u, ptr(mark), st)
         dq_part = torch.empty(sg.E * sg.rpe, D, device=q.device, dtype=q.dtype)
         dlog = torch.empty(sg.E * sg.rpe, device=q.device, dtype=torch.float32) if mode in (2, 3) else None
+        row_tab = None
+        if q.dtype == torch.bfloat16:
+            # the first 32 edges of every distinct chapter: a unit's first row block is requested
+            # together with its plan entries
+            row_tab = torch.empty(sg.plan.max_u * 32, device=q.device, dtype=torch.int32)
+            call("moc_plan_row_table", ptr(sg.plan.n_uniq), ptr(sg.plan.csr_off), ptr(sg.plan.csr_edge),
+                 sg.plan.max_u, 32, ptr(row_tab), st)
         call("moc_sparse_bwd", dt, ptr(q), ptr(dout), ntok, HQ, ptr(k), ptr(v), cs, hs, rs, HK, D,
              ptr(sg.plan.uniq), ptr(sg.plan.n_uniq), ptr(sg.plan.csr_off), ptr(sg.plan.csr_edge), sg.plan.max_u, S,
              sg.hk0, sg.nhk, sg.hq_off, sg.rpe, mode, ptr(lrow), ptr(drow), ptr(sg.w), float(scale), ptr(dk),
-             dv_ptr, ocs, ohs, ors, ptr(dq_part), ptr(dlog), st)
+             dv_ptr, ocs, ohs, ors, ptr(dq_part), ptr(dlog), ptr(row_tab), st)
         call("moc_sparse_dq_combine", dt, ptr(dq_part), ptr(sg.plan.edge_u), S, sg.rpe, ntok, HQ, sg.hq_off, ptr(dq),
              st)
         if mode != 1:
