@@ -288,24 +288,35 @@ __global__ __launch_bounds__(64 * kCombWaves) void sparse_combine_kernel(const T
 }
 
 // The same combine for few rows of at most 4 * kCombSmallPerGroup slots (decode: the shared
-// chapter + 64 routed), with every load of a row in one round: each lane reads the
-// slot values of slots lane and lane + 64, and lane group g reads the partial rows of slots
-// g, g + 4, ... before any of them is weighted.  The rows of skipped slots lie inside o_part
-// but were never written: their values are dropped by a select (never multiplied by a zero
-// weight, which would keep a NaN).
+// chapter + 64 routed), with every load of a row in one round: each lane reads the slot values
+// of slots lane and lane + 64, and the partial rows go out as 16-byte loads (a row of 64 dims is
+// LPR lanes: 8 for bf16, 16 for f32; lane group sg = lane / LPR reads slots sg, sg + NG, ...),
+// all of them issued before any is weighted.  Right after the decode kernel has written them,
+// 16-byte loads take half the time of 8-byte ones (6 against 12 us at 64 x 12 rows of 65 slots).
+// The rows of skipped slots lie inside o_part but were never written: their values are dropped
+// by a select (never multiplied by a zero weight, which would keep a NaN).
 constexpr int kCombSmallPerGroup = 17;
+
+template <typename T> struct Vec16;
+template <> struct Vec16<bf16> { typedef bf16x8 type; };
+template <> struct Vec16<float> { typedef f32x4 type; };
 
 template <typename T>
 __global__ __launch_bounds__(64 * kCombWaves) void sparse_combine_small_kernel(
     const T* __restrict__ o_part, const float* __restrict__ lse_part, const int32_t* __restrict__ edge_u,
     const float* __restrict__ w, int mode, int S, int rpe, int64_t ntok, int HQ, int hq_off, T* __restrict__ out,
     float* __restrict__ lse_joint) {
+  constexpr int EPL = 16 / (int)sizeof(T);    // elements per lane and load
+  constexpr int LPR = kSpDh / EPL;            // lanes per partial row
+  constexpr int NG = 64 / LPR;                // rows per load instruction
+  constexpr int NL = (4 * kCombSmallPerGroup + NG - 1) / NG;
+  typedef typename Vec16<T>::type V;
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * kCombWaves + (threadIdx.x >> 6);
   if (row >= ntok * rpe) return;
   const int64_t tok = row / rpe;
   const int r = (int)(row % rpe);
-  const int g = lane >> 4, sub = lane & 15;
+  const int sg = lane / LPR, ch = lane % LPR;
   // slot values (lane s holds slot s and s + 64); the slot's id, lse and weight are loaded
   // together for every slot in range (the buffers hold every (token, slot, row) entry) and the
   // skipped slots masked afterwards, so they take one round of memory latency, not two
@@ -323,11 +334,11 @@ __global__ __launch_bounds__(64 * kCombWaves) void sparse_combine_small_kernel(
     lg[q] = !ok[q] ? 0.f : mode == 0 ? we : lp + sp_logw(mode, we);
   }
   // partial rows of this lane group's slots, all in flight
-  f32x4 v[kCombSmallPerGroup];
+  V v[NL];
 #pragma unroll
-  for (int i = 0; i < kCombSmallPerGroup; ++i) {
-    const int j = 4 * i + g;
-    v[i] = j < S ? part_load4(o_part + ((tok * S + j) * rpe + r) * kSpDh + 4 * sub) : f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int i = 0; i < NL; ++i) {
+    const int j = NG * i + sg;
+    v[i] = j < S ? *reinterpret_cast<const V*>(o_part + ((tok * S + j) * rpe + r) * kSpDh + EPL * ch) : V{};
   }
   float M = -INFINITY;
   if (mode != 0) {
@@ -339,24 +350,34 @@ __global__ __launch_bounds__(64 * kCombWaves) void sparse_combine_small_kernel(
   float a[2];
 #pragma unroll
   for (int q = 0; q < 2; ++q) a[q] = !ok[q] ? 0.f : mode == 0 ? lg[q] : (M > -INFINITY ? exp2f(lg[q] - M) : 0.f);
-  f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+  float acc[EPL];
 #pragma unroll
-  for (int i = 0; i < kCombSmallPerGroup; ++i) {
-    const int j = 4 * i + g;
-    const float aj = __shfl(j < 64 ? a[0] : a[1], j & 63, 64);
-    if (j < S && aj != 0.f) acc += aj * v[i];
+  for (int x = 0; x < EPL; ++x) acc[x] = 0.f;
+#pragma unroll
+  for (int i = 0; i < NL; ++i) {
+    const int j = NG * i + sg;                 // j < 64 exactly when NG * i < 64: uniform over the wave
+    const float aj = __shfl(NG * i < 64 ? a[0] : a[1], j & 63, 64);
+    if (j < S && aj != 0.f) {
+#pragma unroll
+      for (int x = 0; x < EPL; ++x) acc[x] += aj * (float)v[i][x];
+    }
   }
-  acc = sp_groups_sum(acc);
+  // sum over the NG lane groups (lane bits LPR .. 32), in a fixed order
+#pragma unroll
+  for (int o = LPR; o < 64; o <<= 1)
+#pragma unroll
+    for (int x = 0; x < EPL; ++x) acc[x] += __shfl_xor(acc[x], o, 64);
   float inv = 1.f;
   if (mode != 0) {
     const float den = wave_sum(a[0] + a[1]);
     inv = den > 0.f ? 1.f / den : 0.f;
     if (lane == 0) lse_joint[row] = den > 0.f ? M + log2f(den) : INFINITY;
   }
-  if (lane < 16) {
-    T* op = out + ((int64_t)tok * HQ + hq_off + r) * kSpDh + 4 * lane;
+  if (lane < LPR) {
+    V o;
 #pragma unroll
-    for (int x = 0; x < 4; ++x) op[x] = from_f<T>(acc[x] * inv);
+    for (int x = 0; x < EPL; ++x) o[x] = from_f<T>(acc[x] * inv);
+    *reinterpret_cast<V*>(out + ((int64_t)tok * HQ + hq_off + r) * kSpDh + EPL * lane) = o;
   }
 }
 
@@ -1345,7 +1366,8 @@ int moc_sparse_combine(int dtype, const void* o_part, const float* lse_part, con
   dim3 grid((unsigned)((rows + kCombWaves - 1) / kCombWaves));
   // few rows (decode): latency-bound, every load of a row in one round; many rows (token
   // routing over a batch): throughput-bound, the lighter streaming kernel keeps more rows resident
-  const bool small = S <= 4 * kCombSmallPerGroup && rows <= 16384;
+  const bool small = S <= 4 * kCombSmallPerGroup && rows <= 16384 && ((uintptr_t)o_part & 15) == 0 &&
+                     ((uintptr_t)out & 15) == 0;
 #define SC(KERN, TT)                                                                                                  \
   hipLaunchKernelGGL(KERN<TT>, grid, dim3(64 * kCombWaves), 0, stream, (const TT*)o_part, lse_part, edge_u, w, mode, S, \
                      rpe, ntok, HQ, hq_off, (TT*)out, lse_joint)
