@@ -639,6 +639,28 @@ def run_c5(args):
     torch.cuda.synchronize()
     graph_ms = (time.perf_counter() - t0) * 1e3 / args.steps
     del graph
+    # the same step when every layer re-routes at every token ("rolling" inference strategy,
+    # window 128: window pooling, router logits, top-k + prepend, chapter plan, then the decode)
+    from memory_amd.decode import DecodeRouter
+    routers = [DecodeRouter(lay.router, num_chapters=C, num_shared_chapters=cfg["S"],
+                            routed_scaling_factor=cfg["scale"], strategy="rolling", window_size=128)
+               for lay, _, _ in layers]
+    with torch.no_grad():
+        for dr in routers:
+            dr.prefill(prompt)
+
+    def rerouted_step():
+        for (lay, cache, _), dr in zip(layers, routers):
+            memory_decode_step(lay.memory_attn, h_t, cache, dr.step(h_t))
+
+    for _ in range(args.warmup):
+        rerouted_step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        rerouted_step()
+    torch.cuda.synchronize()
+    rerouted_ms = (time.perf_counter() - t0) * 1e3 / args.steps
     roofline = None
     if dec:
         ach = (unique_bytes / cfg["layers"]) / (dec["avg_ms"] * 1e-3) / 1e9
@@ -662,6 +684,8 @@ def run_c5(args):
         "graph_replay": {"ms_per_step": round(graph_ms, 4),
                          "gbs": round(unique_bytes / (graph_ms * 1e-3) / 1e9, 1),
                          "tokens_per_s": round(B / (graph_ms * 1e-3), 1)},
+        "rerouted_rolling": {"ms_per_step": round(rerouted_ms, 4),
+                             "tokens_per_s": round(B / (rerouted_ms * 1e-3), 1)},
     }
 
 

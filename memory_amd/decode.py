@@ -89,26 +89,139 @@ class MemoryDecodeCache:
 
 
 class DecodeRouting:
-    """Fixed (chapter ids incl. the shared prefix, omega) of a batch of sequences and their plan."""
+    """(chapter ids incl. the shared prefix, omega) of a batch of sequences and their plan.
 
-    def __init__(self, chapter_indices: torch.Tensor, chapter_weights: torch.Tensor, num_chapters: int):
+    ``sync=True`` (routing fixed for a whole generation): the distinct-chapter count is read
+    once (one synchronisation here, none per step), so each step launches exactly one wave per
+    selected (chapter, kv head) tile.  ``sync=False`` (routing that changes every step,
+    ``DecodeRouter``): no host read; the launches are sized for min(B * NS, C) chapters and the
+    kernels read the count on the device (waves past it exit at once)."""
+
+    def __init__(self, chapter_indices: torch.Tensor, chapter_weights: torch.Tensor, num_chapters: int,
+                 sync: bool = True):
         L.require_gpu(chapter_indices, chapter_weights)
         self.idx = chapter_indices.to(torch.int32).contiguous()
         self.omega = chapter_weights.float().contiguous()
         self.B, self.NS = self.idx.shape
         self.plan = ops.chapter_plan(self.idx, num_chapters)
-        # the routing is fixed for the whole generation: read the distinct-chapter count once
-        # (one synchronisation here, none per step) so each step launches exactly one wave per
-        # selected (chapter, kv head) tile instead of min(B * NS, C) chapters' worth
-        self.n_unique = int(self.plan.n_uniq[0].item())
+        self._n_unique = int(self.plan.n_uniq[0].item()) if sync else None
+        self.max_units = self._n_unique if sync else min(self.B * self.NS, int(num_chapters))
         # the first 16 edges of every distinct chapter, read by the decode kernel with its plan
-        # entries (instead of after them, through csr_off)
-        self.row_tab = torch.empty(self.n_unique * 16, device=self.idx.device, dtype=torch.int32)
+        # entries (instead of after them, through csr_off); -1 rows past the count
+        self.row_tab = torch.empty(max(self.max_units, 1) * 16, device=self.idx.device, dtype=torch.int32)
         call("moc_decode_row_table", ptr(self.plan.n_uniq), ptr(self.plan.csr_off), ptr(self.plan.csr_edge),
-             self.n_unique, ptr(self.row_tab), stream_ptr(self.idx.device))
+             self.max_units, ptr(self.row_tab), stream_ptr(self.idx.device))
 
     def unique_chapters(self) -> int:
-        return self.n_unique
+        if self._n_unique is None:
+            self._n_unique = int(self.plan.n_uniq[0].item())
+        return self._n_unique
+
+
+def _masked_mean(states: torch.Tensor, mask: Optional[torch.Tensor]) -> torch.Tensor:
+    """Mean over the sequence ignoring padding (mask == 0), the mask's rightmost positions
+    aligned with the states (memory_transformer/model.py:468-493); fp32 result."""
+    if mask is None:
+        return ops.router_pool(states)
+    if mask.dim() != 2:
+        raise ValueError(f"attention_mask must be 2D (got shape {tuple(mask.shape)})")
+    if mask.shape[0] != states.shape[0]:
+        raise ValueError(f"attention_mask batch ({mask.shape[0]}) must match states batch ({states.shape[0]})")
+    if mask.shape[1] < states.shape[1]:
+        raise ValueError(f"attention_mask length ({mask.shape[1]}) must be >= states length ({states.shape[1]})")
+    if mask.shape[1] != states.shape[1]:
+        mask = mask[:, -states.shape[1]:]
+    m = mask.to(device=states.device, dtype=torch.float32).unsqueeze(-1)
+    return (states.float() * m).sum(dim=1) / m.sum(dim=1).clamp(min=1.0)
+
+
+class DecodeRouter:
+    """Chapter routing of one memory layer during generation, re-decided at every step
+    (MemoryTransformer.forward's inference strategies, memory_transformer/model.py:609-661):
+
+      * "sequence" / "sequence-rolling": the router on the call's own hidden states (the prompt at
+        prefill, the new token at each step), pooled as ChapterRouter pools them (mean, or the
+        rolling-window mean of router.py:158-195);
+      * "rolling": a window of the last ``window_size`` hidden states (prompt included), mean-pooled
+        (padding masked) at prefill and at every step;
+      * "hybrid": the prompt's full mean at prefill (its last ``window_size`` states start the
+        window), then the rolling window at every step.
+
+    Each call returns a ``DecodeRouting`` (shared chapters prepended, routed weights scaled and
+    renormalised as model.py:356-391) built without a host synchronisation, for
+    ``memory_decode_step``.  ``last_logits`` keeps the router logits of the last decision (fp32)."""
+
+    STRATEGIES = ("sequence", "sequence-rolling", "sequence_rolling", "rolling", "hybrid")
+
+    def __init__(self, router, *, num_chapters: int, num_shared_chapters: int = 1,
+                 routed_scaling_factor: float = 2.5, strategy: str = "sequence", window_size: int = 128):
+        if strategy not in self.STRATEGIES:
+            raise ValueError(f"Unknown routing_strategy_inference: {strategy}")
+        if int(window_size) <= 0:
+            raise ValueError(f"routing_window_size must be > 0, got {window_size}")
+        self.router = router
+        self.num_chapters = int(num_chapters)
+        self.num_shared = max(0, min(int(num_shared_chapters), self.num_chapters))
+        self.routed_scale = float(routed_scaling_factor)
+        self.strategy = strategy
+        self.window = int(window_size)
+        self.cache: Optional[torch.Tensor] = None   # (B, <= window, d): the rolling window
+        self.last_logits: Optional[torch.Tensor] = None
+
+    def reset(self) -> None:
+        self.cache = None
+        self.last_logits = None
+
+    def _decide(self, pooled: torch.Tensor) -> DecodeRouting:
+        from .model import prepend_shared_chapters32
+        r = self.router.router
+        logits = ops.router_linear(pooled, r.weight, r.bias)
+        self.last_logits = logits
+        C, S = self.num_chapters, self.num_shared
+        k = min(int(self.router.top_k), C - S)
+        if k > 0:
+            idx, w = ops.router_topk(logits, k, S)
+        else:
+            idx = torch.empty((pooled.shape[0], 0), dtype=torch.int32, device=pooled.device)
+            w = torch.empty((pooled.shape[0], 0), dtype=torch.float32, device=pooled.device)
+        idx_star, omega = prepend_shared_chapters32(idx, w, num_chapters=C, num_shared_chapters=S,
+                                                    routed_scaling_factor=self.routed_scale)
+        return DecodeRouting(idx_star, omega, C, sync=False)
+
+    def _own_states(self, hidden_states: torch.Tensor) -> torch.Tensor:
+        if self.strategy == "sequence":
+            return ops.router_pool(hidden_states)
+        from .router import rolling_coefficients
+        coef = rolling_coefficients(hidden_states.shape[1], self.window, hidden_states.device)
+        return ops.router_pool(hidden_states, coef)
+
+    def _window(self, hidden_states: torch.Tensor, attention_mask: Optional[torch.Tensor]) -> torch.Tensor:
+        combined = hidden_states if self.cache is None else torch.cat([self.cache, hidden_states], dim=1)
+        if combined.shape[1] > self.window:
+            combined = combined[:, -self.window:]
+        self.cache = combined.detach()
+        return _masked_mean(combined, attention_mask)
+
+    @torch.no_grad()
+    def prefill(self, hidden_states: torch.Tensor, attention_mask: Optional[torch.Tensor] = None) -> DecodeRouting:
+        """Routing of the prompt (B, P, d); starts a new window."""
+        L.require_gpu(hidden_states)
+        self.reset()
+        if self.strategy == "hybrid":
+            pooled = _masked_mean(hidden_states, attention_mask)
+            self.cache = hidden_states[:, -self.window:].detach()
+            return self._decide(pooled)
+        if self.strategy == "rolling":
+            return self._decide(self._window(hidden_states, attention_mask))
+        return self._decide(self._own_states(hidden_states))
+
+    @torch.no_grad()
+    def step(self, hidden_states: torch.Tensor, attention_mask: Optional[torch.Tensor] = None) -> DecodeRouting:
+        """Routing of one generated token's hidden states (B, 1, d)."""
+        L.require_gpu(hidden_states)
+        if self.strategy in ("rolling", "hybrid"):
+            return self._decide(self._window(hidden_states, attention_mask))
+        return self._decide(self._own_states(hidden_states))
 
 
 def decode_attention(q: torch.Tensor, cache: MemoryDecodeCache, routing: DecodeRouting) -> torch.Tensor:
@@ -126,7 +239,7 @@ def decode_attention(q: torch.Tensor, cache: MemoryDecodeCache, routing: DecodeR
     lse_part = torch.empty(E * H, device=q.device, dtype=torch.float32)
     pl = routing.plan
     call("moc_decode_partial", dt, ptr(q), B, H, ptr(cache.k_tiles), ptr(cache.v_tiles), cache.HK, D, cache.T,
-         ptr(pl.uniq), ptr(pl.n_uniq), ptr(pl.csr_off), ptr(pl.csr_edge), routing.n_unique, ptr(routing.omega), NS,
+         ptr(pl.uniq), ptr(pl.n_uniq), ptr(pl.csr_off), ptr(pl.csr_edge), routing.max_units, ptr(routing.omega), NS,
          float(D) ** -0.5, ptr(o_part), ptr(lse_part), ptr(routing.row_tab), st)
     out = torch.empty(B, H, D, device=q.device, dtype=cache.dtype)
     lse = torch.empty(B * H, device=q.device, dtype=torch.float32)

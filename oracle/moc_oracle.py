@@ -38,7 +38,7 @@ __all__ = [
     "sparse_attention_unweighted", "sparse_attention_weighted",
     "sparse_attention_joint_bias", "sparse_attention_block_weighted",
     "decode_step", "moe_with_routing", "rms_norm", "adamw_step", "clip_grad_norm",
-    "block_rms_norm", "memory_sublayer",
+    "block_rms_norm", "memory_sublayer", "masked_mean", "inference_route",
 ]
 
 
@@ -624,6 +624,64 @@ def decode_step(h_t, bank, idx_star, omega, Wq, Wk, Wv, Wo, *, H, HK, T,
                                       norm_type=norm_type, eps=eps)
     mem = weight_memory(mem, omega, T)
     return cross_attention(h_t, mem, Wq, Wk, Wv, Wo, H, HK)
+
+
+def masked_mean(states: torch.Tensor, mask: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """model.py:468-493: mean over dim 1 ignoring mask == 0 positions; a longer mask is aligned
+    on its rightmost states.shape[1] columns; the count is clamped to >= 1."""
+    if mask is None:
+        return states.mean(dim=1)
+    if mask.shape[1] != states.shape[1]:
+        mask = mask[:, -states.shape[1]:]
+    m = mask.to(states.dtype).unsqueeze(-1)
+    return (states * m).sum(dim=1) / m.sum(dim=1).clamp(min=1.0)
+
+
+def inference_route(strategy: str, hidden: torch.Tensor, cache: Optional[torch.Tensor], Wr, br, *, top_k: int,
+                    num_shared: int, num_chapters: int, routed_scale: float, window: int,
+                    mask: Optional[torch.Tensor] = None, prefill: bool = False,
+                    select_by_logits: Optional[torch.Tensor] = None):
+    """One routing decision of MemoryTransformer.forward at inference with a decode cache
+    (model.py:609-661, then the prepend of :663-670).  ``hidden`` is the call's hidden states
+    (the prompt at prefill, (B, 1, d) at a step), ``cache`` the rolling window kept between
+    calls.  Returns (pooled, logits, chapter ids, omega, new cache).
+
+      sequence / sequence-rolling: the router on ``hidden`` (router.py:96-107, :158-195);
+      hybrid at prefill: the masked mean of the prompt, whose last ``window`` states start the
+        window (:635-642);
+      rolling, and hybrid after prefill: cat(window, hidden)[-window:], masked mean (:643-654);
+      then softmax -> shared-prefix mask -> renorm -> top-k -> renorm (router.py:114-149 and
+      _select_routed_chapters_from_probs, model.py:331-354, the same chain).
+    ``select_by_logits``: logits to select on (the tie rule of ``route_sequence``); default the
+    logits computed here."""
+    if strategy in ("sequence", "sequence-rolling", "sequence_rolling"):
+        pooled = sequence_pool(hidden, "sequence" if strategy == "sequence" else strategy, window)
+        new_cache = cache
+    elif strategy == "hybrid" and prefill:
+        pooled = masked_mean(hidden, mask)
+        new_cache = hidden[:, -window:]
+    elif strategy in ("rolling", "hybrid"):
+        combined = hidden if (cache is None or prefill) else torch.cat([cache, hidden], dim=1)
+        if combined.shape[1] > window:
+            combined = combined[:, -window:]
+        pooled = masked_mean(combined, mask)
+        new_cache = combined
+    else:
+        raise ValueError(f"Unknown routing_strategy_inference: {strategy}")
+    logits = linear(pooled, Wr, br)
+    z = logits if select_by_logits is None else select_by_logits
+    idx, _, _ = route_sequence(z, top_k, num_shared)
+    probs = F.softmax(logits, dim=-1)
+    p = probs.clone()
+    S = max(0, min(int(num_shared), num_chapters))
+    if S > 0:
+        p[:, :S] = 0.0
+    p = p / p.sum(dim=-1, keepdim=True).clamp_min(1e-12)
+    w = torch.gather(p, -1, idx)
+    w = w / w.sum(dim=-1, keepdim=True).clamp_min(1e-12)
+    ci, cw = prepend_shared_chapters(idx, w, num_chapters=num_chapters, num_shared_chapters=num_shared,
+                                     routed_scaling_factor=routed_scale)
+    return pooled, logits, ci, cw, new_cache
 
 
 def moe_with_routing(h, memory, chapter_indices, chapter_weights, T, Wq, Wk, Wv, Wo, H, HK):

@@ -486,3 +486,55 @@ def test_memory_sublayer_is_residual_plus_cross_attention():
     out = O.memory_sublayer(h, torch.ones(d), torch.zeros(d), 1e-5, False, mem, Wq, Wk, Wv, Wo, H, H)
     xs = (h - h.mean(-1, keepdim=True)) / torch.sqrt(h.var(-1, unbiased=False, keepdim=True) + 1e-5)
     assert torch.allclose(out, h + O.cross_attention(xs, mem, Wq, Wk, Wv, Wo, H, H), rtol=1e-12, atol=1e-12)
+
+
+# ------------------------------------------------------------------ inference routing (decode)
+
+def test_masked_mean_special_cases():
+    """model.py:468-493: no mask = mean; a one-hot mask picks that position; an all-zero row is
+    0 (count clamped to 1); a longer mask is aligned on its rightmost columns."""
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(3, 5, 4, generator=g, dtype=torch.float64)
+    torch.testing.assert_close(O.masked_mean(x, None), x.mean(1))
+    torch.testing.assert_close(O.masked_mean(x, torch.ones(3, 5)), x.mean(1))
+    oh = torch.zeros(3, 5)
+    oh[0, 2] = oh[1, 4] = 1
+    got = O.masked_mean(x, oh)
+    torch.testing.assert_close(got[0], x[0, 2])
+    torch.testing.assert_close(got[1], x[1, 4])
+    assert torch.equal(got[2], torch.zeros(4, dtype=torch.float64))
+    long = torch.cat([torch.zeros(3, 7), torch.ones(3, 5)], dim=1)
+    torch.testing.assert_close(O.masked_mean(x, long), x.mean(1))
+
+
+def test_inference_route_windows_brute_force():
+    """The pooled router input of every strategy over a prefill and 5 steps, against brute force:
+    rolling = mean of the last W states of (prompt + generated so far); hybrid = the prompt's mean
+    at prefill, then the rolling window; sequence / sequence-rolling at a step = the token itself."""
+    g = torch.Generator().manual_seed(4)
+    B, P, d, C, W = 2, 7, 8, 10, 4
+    Wr = torch.randn(C, d, generator=g, dtype=torch.float64)
+    br = torch.randn(C, generator=g, dtype=torch.float64)
+    prompt = torch.randn(B, P, d, generator=g, dtype=torch.float64)
+    toks = [torch.randn(B, 1, d, generator=g, dtype=torch.float64) for _ in range(5)]
+    kw = dict(top_k=3, num_shared=1, num_chapters=C, routed_scale=2.5, window=W)
+    for strat in ("sequence", "sequence-rolling", "rolling", "hybrid"):
+        hist = [prompt[:, i:i + 1] for i in range(P)]
+        pooled, logits, ci, cw, cache = O.inference_route(strat, prompt, None, Wr, br, prefill=True, **kw)
+        if strat in ("sequence", "hybrid"):
+            torch.testing.assert_close(pooled, prompt.mean(1))
+        elif strat == "rolling":
+            torch.testing.assert_close(pooled, prompt[:, -W:].mean(1))
+        else:
+            torch.testing.assert_close(pooled, O.sequence_pool(prompt, "sequence-rolling", W))
+        torch.testing.assert_close(logits, pooled @ Wr.T + br)
+        assert ci.shape == (B, 4) and torch.equal(ci[:, 0], torch.zeros(B, dtype=torch.long))
+        torch.testing.assert_close(cw.sum(-1), torch.ones(B, dtype=torch.float64))
+        for t in toks:
+            hist.append(t)
+            pooled, _, ci, cw, cache = O.inference_route(strat, t, cache, Wr, br, **kw)
+            if strat in ("rolling", "hybrid"):
+                torch.testing.assert_close(pooled, torch.cat(hist[-W:], dim=1).mean(1))
+                assert cache.shape[1] == W
+            else:
+                torch.testing.assert_close(pooled, t[:, 0])
