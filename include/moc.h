@@ -342,6 +342,14 @@ int moc_seq_layer_timing_read(double* total_ms, int32_t* launches, int32_t* drop
 int moc_xattn_fwd(int dtype, const void* q, const void* k_tiles, const void* v_tiles, int64_t kv_span, int64_t su,
                   int sh, int st, const int32_t* slot_u, const float* omega, int64_t B, int64_t L, int H, int HK, int Dh, int T,
                   int NS, float scale, void* out, float* lse, hipStream_t stream);
+/* The attention weights of that forward (MemoryCrossAttention.forward with return_attn_weights,
+ * memory_transformer/memory_attention.py:437-447: softmax(q k^T * scale) over each sequence's
+ * NS * T selected, omega-weighted keys): weights [B, H, L, NS * T] (dtype), column c * T + j for
+ * key j of slot c, from q, the K of moc_xattn_fwd's layout and the lse it wrote; skipped slots
+ * (slot_u < 0) get 0.  q, k_tiles and weights 16-byte aligned. */
+int moc_xattn_weights(int dtype, const void* q, const void* k_tiles, int64_t kv_span, int64_t su, int sh, int st,
+                      const int32_t* slot_u, const float* omega, int64_t B, int64_t L, int H, int HK, int Dh, int T,
+                      int NS, float scale, const float* lse, void* weights, hipStream_t stream);
 
 /* ------------------------------------------------ routed attention backward */
 

@@ -78,6 +78,8 @@ _SIGS = {
     "moc_chapter_wgrad": (_I, [_P, _I64, _P, _P, _I64, _I, _P, _P, _I64, _P, _P, _I, _I, _P, _SZ, _I, _P, _P]),
     "moc_xattn_fwd": (_I, [_I, _P, _P, _P, _I64, _I64, _I, _I, _P, _P, _I64, _I64, _I, _I, _I, _I, _I, _F, _P, _P,
                            _P]),
+    "moc_xattn_weights": (_I, [_I, _P, _P, _I64, _I64, _I, _I, _P, _P, _I64, _I64, _I, _I, _I, _I, _I, _F, _P, _P,
+                                _P]),
     "moc_xattn_bwd_prep": (_I, [_I, _P, _P, _P, _I64, _I64, _I, _I, _P, _P, _P, _P]),
     "moc_xattn_bwd_dq": (_I, [_I, _P, _P, _P, _I64, _I64, _I, _I, _P, _P, _P, _P, _P, _I64, _I64, _I, _I, _I, _I,
                               _I, _F, _P, _P]),

@@ -278,6 +278,77 @@ __global__ __launch_bounds__(kFwdThreads) void xattn_fwd_kernel(
   }
 }
 
+// Attention weights of the forward above, materialised (MemoryCrossAttention.forward with
+// return_attn_weights, memory_attention.py:437-447: softmax(q k^T * scale) over the sequence's
+// selected keys, which carry omega): p_ij = exp2(omega_c scale log2(e) q_i . k_j - lse_i) with the
+// forward's row log-sum-exp.  One workgroup = 64 queries x one slot of one (sequence, head), wave w
+// owning queries 16 w .. 16 w + 15: S^T = K Q^T from global fragments (lane = query, 16 keys per
+// lane), then 4 consecutive keys per store.  A skipped slot's keys get weight 0; a slot below the
+// omega floor gets every logit 0 (its keys vanish), as in the forward.
+template <typename T>
+__global__ __launch_bounds__(256) void xattn_weights_kernel(
+    const T* __restrict__ q, const T* __restrict__ ktiles, const int32_t* __restrict__ slot_u,
+    const float* __restrict__ omega, int B, int L, int H, int HK, int NS, int64_t kv_span, int64_t kv_su, int kv_sh,
+    int kv_st, float scale_log2, const float* __restrict__ lse, T* __restrict__ P) {
+  typedef typename Frag<T>::type F8;
+  const int nqb = (L + 63) / 64;
+  const int64_t t = blockIdx.x;
+  const int s = (int)(t % NS);
+  const int64_t r = t / NS;
+  const int qb = (int)(r % nqb);
+  const int h = (int)((r / nqb) % H), b = (int)(r / ((int64_t)nqb * H));
+  const int hk = h / (H / HK);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int g = lane >> 4, c16 = lane & 15;
+  const int qi = qb * 64 + 16 * wave + c16;
+  const int Lp = (L + 127) / 128 * 128;
+  const int u = slot_u[(size_t)b * NS + s];
+  const float w = omega[(size_t)b * NS + s];
+  const float lq = qi < L ? lse[((size_t)b * H + h) * Lp + qi] : 0.f;
+  f32x4 st[4];
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb) st[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  if (u >= 0 && w > kTinyOmega) {
+    F8 qf[2];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+      qf[ks] = qi < L ? Load8<T, T>::run(q + ((size_t)(b * (size_t)L + qi) * H + h) * kDh + 32 * ks + 8 * g)
+                      : zero_frag<T>();
+    // K block (u, hk) through a bounded buffer resource (reads past kv_span return zero)
+    const Buf kbuf(ktiles, (uint32_t)(kv_span * (int64_t)sizeof(T)));
+    const uint32_t soff = (uint32_t)(((size_t)u * kv_su + (size_t)hk * kv_sh) * sizeof(T));
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const uint32_t voff = (uint32_t)(((16 * kb + c16) * kv_st + 32 * ks + 8 * g) * (int)sizeof(T));
+        F8 a;
+        if constexpr (sizeof(T) == 2) {
+          a = __builtin_bit_cast(F8, kbuf.load16(voff, soff));
+        } else {
+          const V16 lo = kbuf.load16(voff, soff), hi = kbuf.load16(voff + 16, soff);
+          a = F8{__uint_as_float(lo.w[0]), __uint_as_float(lo.w[1]), __uint_as_float(lo.w[2]), __uint_as_float(lo.w[3]),
+                 __uint_as_float(hi.w[0]), __uint_as_float(hi.w[1]), __uint_as_float(hi.w[2]), __uint_as_float(hi.w[3])};
+        }
+        mma(st[kb], a, qf[ks]);
+      }
+  }
+  if (qi >= L) return;
+  const float c = w * scale_log2;
+  T* row = P + (((size_t)b * H + h) * L + qi) * ((size_t)NS * kTch) + (size_t)s * kTch;
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb) {
+    T v[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = from_f<T>(u < 0 ? 0.f : fast_exp2(st[kb][e] * c - lq));
+    if constexpr (sizeof(T) == 2) {
+      *reinterpret_cast<bf16x4*>(row + 16 * kb + 4 * g) = bf16x4{v[0], v[1], v[2], v[3]};
+    } else {
+      *reinterpret_cast<f32x4*>(row + 16 * kb + 4 * g) = f32x4{v[0], v[1], v[2], v[3]};
+    }
+  }
+}
+
 }  // namespace moc
 
 using namespace moc;
@@ -307,6 +378,33 @@ int moc_xattn_fwd(int dtype, const void* q, const void* k_tiles, const void* v_t
   else
     return set_error(MOC_ERR_UNSUPPORTED, "moc_xattn_fwd: dtype %d", dtype);
   return check_launch("xattn_fwd_kernel");
+}
+
+int moc_xattn_weights(int dtype, const void* q, const void* k_tiles, int64_t kv_span, int64_t su, int sh, int st,
+                      const int32_t* slot_u, const float* omega, int64_t B, int64_t L, int H, int HK, int Dh, int T,
+                      int NS, float scale, const float* lse, void* weights, hipStream_t stream) {
+  MOC_REQUIRE(q && k_tiles && slot_u && omega && lse && weights, MOC_ERR_ARG, "moc_xattn_weights: null pointer");
+  MOC_REQUIRE(Dh == kDh && T == kTch, MOC_ERR_UNSUPPORTED,
+              "moc_xattn_weights: needs head_dim 64 and 64 tokens per chapter (got %d, %d)", Dh, T);
+  MOC_REQUIRE(H > 0 && HK > 0 && H % HK == 0 && NS > 0 && B >= 0 && L >= 0, MOC_ERR_ARG, "moc_xattn_weights: bad shape");
+  if (int rc = check_kv_layout("moc_xattn_weights", dtype, kv_span, su, sh, st)) return rc;
+  MOC_REQUIRE(((uintptr_t)q & 15) == 0 && ((uintptr_t)k_tiles & 15) == 0 && ((uintptr_t)weights & 15) == 0,
+              MOC_ERR_ARG, "moc_xattn_weights: q, K and the weights must be 16-byte aligned");
+  if (B == 0 || L == 0) return MOC_OK;
+  const int64_t blocks = B * H * ((L + 63) / 64) * NS;
+  MOC_REQUIRE(blocks < ((int64_t)1 << 31), MOC_ERR_UNSUPPORTED, "moc_xattn_weights: grid too large");
+  const float sl2 = scale * 1.4426950408889634f;
+  if (dtype == MOC_BF16)
+    hipLaunchKernelGGL(xattn_weights_kernel<bf16>, dim3((unsigned)blocks), dim3(256), 0, stream, (const bf16*)q,
+                       (const bf16*)k_tiles, slot_u, omega, (int)B, (int)L, H, HK, NS, kv_span, su, sh, st, sl2, lse,
+                       (bf16*)weights);
+  else if (dtype == MOC_F32)
+    hipLaunchKernelGGL(xattn_weights_kernel<float>, dim3((unsigned)blocks), dim3(256), 0, stream, (const float*)q,
+                       (const float*)k_tiles, slot_u, omega, (int)B, (int)L, H, HK, NS, kv_span, su, sh, st, sl2, lse,
+                       (float*)weights);
+  else
+    return set_error(MOC_ERR_UNSUPPORTED, "moc_xattn_weights: dtype %d", dtype);
+  return check_launch("xattn_weights_kernel");
 }
 
 }  // extern "C"

@@ -114,6 +114,12 @@ class MemoryCrossAttention(nn.Module):
 
     def _dense_as_chapters(self, hidden_states: torch.Tensor, memory: torch.Tensor) -> torch.Tensor:
         """Dense attention over `memory` via the routed kernels (64-row chapters, weight 1)."""
+        bank, idx, omega, C = self._dense_routing(hidden_states, memory)
+        return self._routed(hidden_states, bank, idx, omega, C, CHAPTER_TOKENS, None, 0.0)
+
+    def _dense_routing(self, hidden_states: torch.Tensor, memory: torch.Tensor):
+        """`memory` as a bank of 64-row chapters, every sequence selecting all of its own with
+        weight 1: (bank, chapter ids (B, N / 64), omega, number of chapters)."""
         B = hidden_states.shape[0]
         if memory.dim() not in (2, 3):
             raise ValueError(f"memory must be (N, d) or (B, N, d), got {tuple(memory.shape)}")
@@ -134,17 +140,43 @@ class MemoryCrossAttention(nn.Module):
                    + torch.arange(per, device=dev, dtype=torch.int32).view(1, per))
             C = B * per
         omega = torch.ones(B, per, device=dev, dtype=torch.float32)
-        return self._routed(hidden_states, bank, idx, omega, C, CHAPTER_TOKENS, None, 0.0)
+        return bank, idx, omega, C
+
+    @torch.no_grad()
+    def attention_weights(self, hidden_states: torch.Tensor, memory: Optional[torch.Tensor] = None,
+                          routed_memory_state: Optional[Dict[str, Any]] = None) -> torch.Tensor:
+        """The attention probabilities (B, H, L, N) that forward(return_attn_weights=True) returns
+        (memory_attention.py:437-447: softmax(q k^T * scale) over the memory keys, recomputed after
+        the forward): N = the memory rows, or the selected chapters' rows (slot-major, omega-weighted
+        keys) for ``routed_memory_state``.  Computed by moc_xattn_weights from the forward's row
+        log-sum-exp; no autograd."""
+        if routed_memory_state is not None:
+            st = routed_memory_state
+            norm_type = st.get("norm_type") if st.get("normalize", False) else None
+            bank, idx, omega = st["bank"], st["chapter_indices"], st["chapter_weights"]
+            C, T, eps = int(st["num_chapters"]), int(st["tokens_per_chapter"]), float(st.get("eps", 1e-6))
+        elif memory is not None:
+            bank, idx, omega, C = self._dense_routing(hidden_states, memory)
+            norm_type, T, eps = None, CHAPTER_TOKENS, 0.0
+        else:
+            raise ValueError("memory must be provided when token_routing_state is None.")
+        q = self._queries(hidden_states)
+        return ops.routed_attention_weights(q, bank, self.k_proj.weight, self.v_proj.weight, omega, idx,
+                                            num_chapters=C, tokens_per_chapter=T, norm_type=norm_type, eps=eps,
+                                            num_kv_heads=self.num_kv_heads)
 
     # ------------------------------------------------------------------ forward
     def forward(self, hidden_states: torch.Tensor, memory: Optional[torch.Tensor] = None,
                 token_routing_state: Optional[Dict[str, Any]] = None, token_routing_kernel_version: str = "v2",
                 return_attn_weights: bool = False,
                 routed_memory_state: Optional[Dict[str, Any]] = None) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
+        if return_attn_weights and token_routing_state is not None:
+            raise ValueError("return_attn_weights=True is not supported for token_routing_state path.")
+        out = self._project_output(self.attention_preproj(hidden_states, memory, token_routing_state,
+                                                          token_routing_kernel_version, routed_memory_state))
         if return_attn_weights:
-            raise NotImplementedError("return_attn_weights is not supported by the fused HIP attention")
-        return self._project_output(self.attention_preproj(hidden_states, memory, token_routing_state,
-                                                           token_routing_kernel_version, routed_memory_state)), None
+            return out, self.attention_weights(hidden_states, memory, routed_memory_state)
+        return out, None
 
     def attention_preproj(self, hidden_states: torch.Tensor, memory: Optional[torch.Tensor] = None,
                           token_routing_state: Optional[Dict[str, Any]] = None,

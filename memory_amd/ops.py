@@ -870,6 +870,27 @@ def routed_attention(q, bank, wk, wv, omega, idx_star, *, num_chapters: int, tok
                                   norm_code(norm_type), float(eps), HK)
 
 
+@torch.no_grad()
+def routed_attention_weights(q, bank, wk, wv, omega, idx_star, *, num_chapters: int, tokens_per_chapter: int,
+                             norm_type: Optional[str] = None, eps: float = 1e-6,
+                             num_kv_heads: Optional[int] = None) -> torch.Tensor:
+    """softmax(q k^T * scale) of the sequence-routed attention, (B, H, L, NS * T) in q's dtype
+    (memory_attention.py:437-447 on the omega-weighted gathered memory): the forward's K and row
+    log-sum-exp, then moc_xattn_weights."""
+    HK = q.shape[2] if num_kv_heads is None else int(num_kv_heads)
+    T = int(tokens_per_chapter)
+    _, saved, _ = routed_attn_forward(q, bank, wk, wv, omega, idx_star, int(num_chapters), T, norm_code(norm_type),
+                                      float(eps), HK)
+    qc, _, _, om, _, lse, kv, *_rest = saved
+    edge_u = saved[11]
+    B, Lq, H, Dh = qc.shape
+    NS = om.shape[1]
+    P = torch.empty(B, H, Lq, NS * T, device=q.device, dtype=qc.dtype)
+    call("moc_xattn_weights", L.dtype_code(qc.dtype), ptr(qc), ptr(kv), *kv_rows_layout(kv, T, HK, Dh), ptr(edge_u),
+         ptr(om), B, Lq, H, HK, Dh, T, NS, float(Dh) ** -0.5, ptr(lse), ptr(P), stream_ptr(q.device))
+    return P
+
+
 class _TokenRouterLinear(torch.autograd.Function):
     """logits = x W^T + b for per-token routing (router.py:294, ``self.router(hidden_states)``).
 

@@ -38,7 +38,7 @@ __all__ = [
     "sparse_attention_unweighted", "sparse_attention_weighted",
     "sparse_attention_joint_bias", "sparse_attention_block_weighted",
     "decode_step", "moe_with_routing", "rms_norm", "adamw_step", "clip_grad_norm",
-    "block_rms_norm", "memory_sublayer", "masked_mean", "inference_route",
+    "block_rms_norm", "memory_sublayer", "masked_mean", "inference_route", "attention_weights",
 ]
 
 
@@ -331,6 +331,17 @@ def attention(q, k, v, scale=None):
     qt, kt, vt = q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2)
     p = F.softmax(torch.matmul(qt, kt.transpose(-2, -1)) * scale, dim=-1)
     return torch.matmul(p, vt).transpose(1, 2)
+
+
+def attention_weights(h, memory, Wq, Wk, H, HK, scale=None):
+    """The weights forward(return_attn_weights=True) returns (memory_attention.py:437-447):
+    softmax(q k^T * scale) of the recomputed q, k (GQA expanded), (B, H, L, N)."""
+    q, k, _ = compute_qkv(h, memory, Wq, Wk, Wk, H, HK)
+    if HK != H:
+        k = k.repeat_interleave(H // HK, dim=2)
+    if scale is None:
+        scale = q.shape[-1] ** -0.5
+    return F.softmax(torch.matmul(q.transpose(1, 2), k.transpose(1, 2).transpose(-2, -1)) * scale, dim=-1)
 
 
 def cross_attention(h, memory, Wq, Wk, Wv, Wo, H, HK, return_preproj=False):

@@ -538,3 +538,22 @@ def test_inference_route_windows_brute_force():
                 assert cache.shape[1] == W
             else:
                 torch.testing.assert_close(pooled, t[:, 0])
+
+
+def test_attention_weights_consistent_with_attention():
+    """The returned weights are the probabilities ``attention`` mixes the values with (pinned
+    there against SDPA): weights @ v (GQA expanded) == attention(q, k, v), rows sum to 1."""
+    g = torch.Generator().manual_seed(5)
+    B, L, N, H, HK, Dh = 2, 5, 128, 4, 2, 8
+    d = H * Dh
+    h = torch.randn(B, L, d, generator=g, dtype=torch.float64)
+    mem = torch.randn(B, N, d, generator=g, dtype=torch.float64)
+    Wq = torch.randn(d, d, generator=g, dtype=torch.float64)
+    Wk = torch.randn(HK * Dh, d, generator=g, dtype=torch.float64)
+    Wv = torch.randn(HK * Dh, d, generator=g, dtype=torch.float64)
+    P = O.attention_weights(h, mem, Wq, Wk, H, HK)
+    assert P.shape == (B, H, L, N)
+    torch.testing.assert_close(P.sum(-1), torch.ones(B, H, L, dtype=torch.float64))
+    q, k, v = O.compute_qkv(h, mem, Wq, Wk, Wv, H, HK)
+    ve = v.repeat_interleave(H // HK, dim=2).transpose(1, 2)
+    torch.testing.assert_close(torch.matmul(P, ve).transpose(1, 2), O.attention(q, k, v))
