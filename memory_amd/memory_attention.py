@@ -97,25 +97,31 @@ class MemoryCrossAttention(nn.Module):
             q = ops.linear(hidden_states, self.q_proj.weight)
         return q.view(B, L, self.num_heads, self.head_dim)
 
-    def _routed(self, hidden_states, bank, idx_star, omega, num_chapters, T, norm_type, eps):
+    def _checkpointing(self) -> bool:
+        return bool(self.gradient_checkpointing and self.training and torch.is_grad_enabled() and torch_checkpoint)
+
+    def _routed(self, hidden_states, bank, idx_star, omega, num_chapters, T, norm_type, eps, q=None):
+        """``q``: the queries (B, L, H, Dh) when the caller already projected them (not with
+        gradient checkpointing, whose recompute projects them again)."""
         B, L, _ = hidden_states.shape
         qnorm = self._qnorm  # captured: a checkpointed recompute runs after the forward returned
 
-        def run(h):
-            q = self._queries(h, qnorm)
-            a = ops.routed_attention(q, bank, self.k_proj.weight, self.v_proj.weight, omega, idx_star,
+        def attend(qq):
+            a = ops.routed_attention(qq, bank, self.k_proj.weight, self.v_proj.weight, omega, idx_star,
                                      num_chapters=num_chapters, tokens_per_chapter=T, norm_type=norm_type, eps=eps,
                                      num_kv_heads=self.num_kv_heads)
             return a.reshape(B, L, self.hidden_dim)
 
-        if self.gradient_checkpointing and self.training and torch.is_grad_enabled() and torch_checkpoint:
-            return torch_checkpoint(run, hidden_states, use_reentrant=False)
-        return run(hidden_states)
+        if q is not None:
+            return attend(q)
+        if self._checkpointing():
+            return torch_checkpoint(lambda h: attend(self._queries(h, qnorm)), hidden_states, use_reentrant=False)
+        return attend(self._queries(hidden_states, qnorm))
 
-    def _dense_as_chapters(self, hidden_states: torch.Tensor, memory: torch.Tensor) -> torch.Tensor:
+    def _dense_as_chapters(self, hidden_states: torch.Tensor, memory: torch.Tensor, q=None) -> torch.Tensor:
         """Dense attention over `memory` via the routed kernels (64-row chapters, weight 1)."""
         bank, idx, omega, C = self._dense_routing(hidden_states, memory)
-        return self._routed(hidden_states, bank, idx, omega, C, CHAPTER_TOKENS, None, 0.0)
+        return self._routed(hidden_states, bank, idx, omega, C, CHAPTER_TOKENS, None, 0.0, q=q)
 
     def _dense_routing(self, hidden_states: torch.Tensor, memory: torch.Tensor):
         """`memory` as a bank of 64-row chapters, every sequence selecting all of its own with
@@ -229,10 +235,17 @@ class MemoryCrossAttention(nn.Module):
                 f"got hidden_states={tuple(hidden_states.shape)}, token_chapter_indices={tuple(idx.shape)}")
         B, L, _ = hidden_states.shape
         combined = None
-        if shared_memory is not None and shared_memory.numel() > 0:
-            combined = self._dense_as_chapters(hidden_states, shared_memory)
-        if routed_memory is not None and routed_memory.numel() > 0 and idx.shape[-1] > 0 and T > 0:
-            q = self._queries(hidden_states)
+        has_shared = shared_memory is not None and shared_memory.numel() > 0
+        has_routed = routed_memory is not None and routed_memory.numel() > 0 and idx.shape[-1] > 0 and T > 0
+        # the shared and the routed branches attend with the same queries: projected once (the
+        # reference's _forward_attention and _compute_qkv each project them; the gradients of the
+        # two uses add up in one tensor instead of two products)
+        q = self._queries(hidden_states) if has_routed and not (has_shared and self._checkpointing()) else None
+        if has_shared:
+            combined = self._dense_as_chapters(hidden_states, shared_memory, q=q)
+        if has_routed:
+            if q is None:
+                q = self._queries(hidden_states)
             routed = ops.token_routed_attention(q, routed_memory, self.k_proj.weight, self.v_proj.weight, idx,
                                                 chapter_weights, tokens_per_chapter=T, version=version,
                                                 num_kv_heads=self.num_kv_heads)
