@@ -277,6 +277,12 @@ int moc_chapter_wgrad(const void* dkv_edge, int64_t lda, const void* red, const 
  * memory_transformer/memory_attention.py:140-143). */
 int moc_weight_pack(const void* wk, int wk_dtype, const void* wv, int wv_dtype, int64_t kv, int64_t d, void* wkv,
                     void* wkv_t, hipStream_t stream);
+/* wt [K][ldt] bf16 = w^T for w [N][K] of MOC_F32 / MOC_BF16, columns N .. ldt-1 zero: the
+ * transposed (and zero-padded) weight operand of an input-gradient product on the rows GEMM,
+ * e.g. dx = dlogits W of the per-token router (router.py:294) with its chapter count padded to a
+ * multiple of 256.  K and ldt multiples of 8, ldt >= N; 16-byte aligned w and wt. */
+int moc_weight_transpose(const void* w, int w_dtype, int64_t N, int64_t K, void* wt, int64_t ldt,
+                         hipStream_t stream);
 
 /* ------------------------------------------- the whole sequence-routed layer */
 

@@ -66,6 +66,7 @@ _SIGS = {
     "moc_chapter_project": (_I, [_P, _I64, _I, _P, _P, _I64, _P, _I, _I, _P, _I64, _P]),
     "moc_chapter_dx": (_I, [_P, _I64, _P, _P, _I64, _P, _P, _P, _P, _I, _I, _I, _P, _I64, _I, _P]),
     "moc_weight_pack": (_I, [_P, _I, _P, _I, _I64, _I64, _P, _P, _P]),
+    "moc_weight_transpose": (_I, [_P, _I, _I64, _I64, _P, _I64, _P]),
     "moc_dkv_multi_reduce": (_I, [_P, _I64, _P, _I64, _P, _P, _P, _P]),
     "moc_rows_linear": (_I, [_P, _I64, _I64, _P, _I, _I, _P, _I64, _P]),
     "moc_logit_grad_pack_workspace": (_SZ, [_I64, _I64]),

@@ -517,8 +517,9 @@ __global__ __launch_bounds__(256) void dkv_multi_reduce_kernel(const bf16* __res
 // are multiples of 8 (host check).
 template <typename TK, typename TV>
 __global__ __launch_bounds__(256) void weight_pack_kernel(const TK* __restrict__ wk, const TV* __restrict__ wv,
-                                                          int64_t kv, int64_t d, bf16* __restrict__ wkv,
-                                                          bf16* __restrict__ wkv_t) {
+                                                          int64_t nk, int64_t R, int64_t d, bf16* __restrict__ wkv,
+                                                          bf16* __restrict__ wkv_t, int64_t ldt) {
+  // rows r < nk from wk, nk <= r < R from wv; wkv [R][d], wkv_t [d][ldt] (columns R .. ldt-1 zero)
   __shared__ __attribute__((aligned(16))) bf16 tile[64][72];
   const int64_t r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;
 #pragma unroll
@@ -526,10 +527,10 @@ __global__ __launch_bounds__(256) void weight_pack_kernel(const TK* __restrict__
     const int q = threadIdx.x + 256 * it, rr = q >> 3, cc = (q & 7) * 8;
     const int64_t r = r0 + rr, c = c0 + cc;
     bf16x8 v;
-    if (r < 2 * kv && c < d) {
+    if (r < R && c < d) {
       float f[8];
-      if (r < kv) ChunkLoad8<TK>::run(wk + r * d + c, f);
-      else ChunkLoad8<TV>::run(wv + (r - kv) * d + c, f);
+      if (r < nk) ChunkLoad8<TK>::run(wk + r * d + c, f);
+      else ChunkLoad8<TV>::run(wv + (r - nk) * d + c, f);
 #pragma unroll
       for (int x = 0; x < 8; ++x) v[x] = (bf16)f[x];
       if (wkv) *reinterpret_cast<bf16x8*>(wkv + r * d + c) = v;
@@ -545,11 +546,11 @@ __global__ __launch_bounds__(256) void weight_pack_kernel(const TK* __restrict__
   for (int it = 0; it < 2; ++it) {
     const int q = threadIdx.x + 256 * it, cc = q >> 3, rr = (q & 7) * 8;
     const int64_t c = c0 + cc, r = r0 + rr;
-    if (c >= d || r >= 2 * kv) continue;
+    if (c >= d || r >= ldt) continue;
     bf16x8 v;
 #pragma unroll
     for (int x = 0; x < 8; ++x) v[x] = tile[rr + x][cc];
-    *reinterpret_cast<bf16x8*>(wkv_t + c * 2 * kv + r) = v;
+    *reinterpret_cast<bf16x8*>(wkv_t + c * ldt + r) = v;
   }
 }
 
@@ -1041,13 +1042,33 @@ int moc_weight_pack(const void* wk, int wk_dtype, const void* wv, int wv_dtype, 
   const dim3 grid((unsigned)((d + 63) / 64), (unsigned)((2 * kv + 63) / 64));
 #define MOC_WP(TK, TV)                                                                                           \
   hipLaunchKernelGGL((weight_pack_kernel<TK, TV>), grid, dim3(256), 0, stream, (const TK*)wk, (const TV*)wv, kv, \
-                     d, (bf16*)wkv, (bf16*)wkv_t)
+                     2 * kv, d, (bf16*)wkv, (bf16*)wkv_t, 2 * kv)
   if (wk_dtype == MOC_BF16 && wv_dtype == MOC_BF16) MOC_WP(bf16, bf16);
   else if (wk_dtype == MOC_F32 && wv_dtype == MOC_F32) MOC_WP(float, float);
   else if (wk_dtype == MOC_BF16 && wv_dtype == MOC_F32) MOC_WP(bf16, float);
   else if (wk_dtype == MOC_F32 && wv_dtype == MOC_BF16) MOC_WP(float, bf16);
   else return set_error(MOC_ERR_UNSUPPORTED, "moc_weight_pack: dtypes %d, %d", wk_dtype, wv_dtype);
 #undef MOC_WP
+  return check_launch("weight_pack_kernel");
+}
+
+int moc_weight_transpose(const void* w, int w_dtype, int64_t N, int64_t K, void* wt, int64_t ldt,
+                         hipStream_t stream) {
+  MOC_REQUIRE(w && wt, MOC_ERR_ARG, "moc_weight_transpose: null pointer");
+  MOC_REQUIRE(N > 0 && K > 0 && K % 8 == 0 && ldt >= N && ldt % 8 == 0 && ldt * K < ((int64_t)1 << 40), MOC_ERR_ARG,
+              "moc_weight_transpose: N=%lld, K=%lld (a multiple of 8), ldt=%lld (>= N, a multiple of 8)",
+              (long long)N, (long long)K, (long long)ldt);
+  MOC_REQUIRE(((uintptr_t)w & 15) == 0 && ((uintptr_t)wt & 15) == 0, MOC_ERR_ARG,
+              "moc_weight_transpose: w and wt must be 16-byte aligned");
+  const dim3 grid((unsigned)((K + 63) / 64), (unsigned)((ldt + 63) / 64));
+  if (w_dtype == MOC_BF16)
+    hipLaunchKernelGGL((weight_pack_kernel<bf16, bf16>), grid, dim3(256), 0, stream, (const bf16*)w, (const bf16*)w, N,
+                       N, K, (bf16*)nullptr, (bf16*)wt, ldt);
+  else if (w_dtype == MOC_F32)
+    hipLaunchKernelGGL((weight_pack_kernel<float, float>), grid, dim3(256), 0, stream, (const float*)w,
+                       (const float*)w, N, N, K, (bf16*)nullptr, (bf16*)wt, ldt);
+  else
+    return set_error(MOC_ERR_UNSUPPORTED, "moc_weight_transpose: dtype %d", w_dtype);
   return check_launch("weight_pack_kernel");
 }
 

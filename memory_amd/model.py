@@ -251,7 +251,7 @@ class TokenRoutedMemoryLayer(nn.Module):
                 return_losses: bool = True) -> Tuple[torch.Tensor, Dict[str, torch.Tensor]]:
         S, T = self.num_shared_chapters, self.tokens_per_chapter
         idx, w, losses = self.router.route_token_level(hidden_states, return_losses=return_losses,
-                                                       exclude_prefix_chapters=S)
+                                                       exclude_prefix_chapters=S, ids32=True)
         opt = getattr(bank, "_moc_bank_opt", None)
         if opt is not None:
             opt.catch_up()   # every chapter is projected: bring the whole bank to the last step
@@ -265,7 +265,7 @@ class TokenRoutedMemoryLayer(nn.Module):
         shared = shared if st > 0 else None
         routed = routed if st < bank.shape[0] else None
         state = {"shared_memory": shared, "routed_memory": routed,
-                 "token_chapter_indices": (idx - S).to(torch.int32), "tokens_per_chapter": T,
+                 "token_chapter_indices": idx - S if S else idx, "tokens_per_chapter": T,
                  "routed_scale": self.routed_scaling_factor, "kernel_version": self.kernel_version,
                  "chapter_weights": w if self.weighted else None}
         out, _ = self.memory_attn(hidden_states, token_routing_state=state)

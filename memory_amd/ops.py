@@ -946,8 +946,10 @@ class _TokenRouterLinear(torch.autograd.Function):
             if need_db:
                 db = db32.to(b_dtype)
             if ctx.needs_input_grad[0]:
-                wt = torch.zeros(K, Cp, device=dy.device, dtype=torch.bfloat16)
-                wt[:, :C].copy_(Wc.t())
+                # W^T with its chapter columns zero-padded to Cp, in one transposing pass
+                wt = torch.empty(K, Cp, device=dy.device, dtype=torch.bfloat16)
+                call("moc_weight_transpose", ptr(Wc), L.dtype_code(Wc.dtype), C, K, ptr(wt), Cp,
+                     stream_ptr(dy.device))
                 dx = rows_linear(dyp, wt)
             if ctx.needs_input_grad[1]:
                 dW = linear_wgrad(dyp, x, torch.float32)[:C].to(w_dtype)

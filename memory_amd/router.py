@@ -110,8 +110,9 @@ class ChapterRouter(nn.Module):
         return idx, w, losses
 
     def route_token_level(self, hidden_states: torch.Tensor, return_losses: bool = True,
-                          exclude_prefix_chapters: int = 0):
-        """Per-token routing (router.py:262-340): indices (B, T, k) are global chapter ids."""
+                          exclude_prefix_chapters: int = 0, *, ids32: bool = False):
+        """Per-token routing (router.py:262-340): indices (B, T, k) are global chapter ids
+        (int64 as the reference returns them; ``ids32``: the kernels' int32)."""
         if hidden_states.dim() != 3:
             raise ValueError(f"hidden_states must be 3D (B, T, D), got shape {tuple(hidden_states.shape)}")
         S = int(exclude_prefix_chapters)
@@ -122,14 +123,14 @@ class ChapterRouter(nn.Module):
         logits = ops.router_token_logits(hidden_states, self.router.weight, self.router.bias)   # (B*T, C) fp32
         k = min(int(self.top_k), C - S)
         if k <= 0:
-            idx = torch.empty((B, T, 0), dtype=torch.long, device=hidden_states.device)
+            idx = torch.empty((B, T, 0), dtype=torch.int32 if ids32 else torch.long, device=hidden_states.device)
             w = torch.empty((B, T, 0), dtype=torch.float32, device=hidden_states.device)
             losses = {}
             if return_losses:
                 losses = compute_router_losses(logits, None, idx.reshape(B * T, 0), C)
             return idx, w, losses
         idx32, w = ops.router_topk(logits, k, S)
-        idx = idx32.long().view(B, T, k)
+        idx = (idx32 if ids32 else idx32.long()).view(B, T, k)
         losses = {}
         if return_losses:
             losses = compute_router_losses(logits, None, idx32, C)

@@ -142,9 +142,12 @@ def _backward(q, k, v, layout, out, dout, segments, saved, mode, S, scale, dk, d
 
 
 def _global_chapters(idx: torch.Tensor, M: int, per_batch: bool) -> torch.Tensor:
-    """Chapter ids in the plan's id space: b * M + c for per-batch K/V; -1 when c is out of range."""
+    """Chapter ids in the plan's id space: b * M + c for per-batch K/V; -1 when c is out of range.
+    int32 ids of a shared K/V pass through: the plan itself drops ids outside [0, M)."""
+    if idx.dtype == torch.int32 and not per_batch:
+        return idx
+    bad = (idx < 0) | (idx >= M)     # on the caller's ids (64-bit ids are not wrapped first)
     c = idx.to(torch.int32)
-    bad = (c < 0) | (c >= M)
     if per_batch:
         B = c.shape[0]
         shape = (B,) + (1,) * (c.dim() - 1)
@@ -296,7 +299,12 @@ class _TokenRouted(torch.autograd.Function):
         C = Nr // BLOCK
         q = q.contiguous()
         routed = routed.contiguous()
-        wkv = torch.cat([wk, wv], 0).to(dtype).contiguous()
+        wkv_t = None
+        if dtype == torch.bfloat16 and wk.shape[0] % 8 == 0 and wk.shape[1] % 8 == 0:
+            # [Wk; Wv] and its transpose (the input gradient's operand) in one kernel
+            wkv, wkv_t = ops.weight_pack(wk, wv, transposed=True)
+        else:
+            wkv = torch.cat([wk, wv], 0).to(dtype).contiguous()
         # every routed chapter is projected (no gather, no norm): one rows GEMM over the routed
         # bank (the chapter GEMM's wide tiles for bf16), K and V read by the sparse kernels as
         # strided column blocks of kv [Nr][2 KV]
@@ -311,13 +319,13 @@ class _TokenRouted(torch.autograd.Function):
         segs = _segments(idx, w, mode, C, False, HQ, HK, C)
         out, saved = _forward(q, kv[:, :KV], kv[:, KV:], "rows", segs, mode, S, D ** -0.5)
         ctx.segs, ctx.saved_parts = segs, saved
-        ctx.save_for_backward(q, routed, wkv, kv, out)
+        ctx.save_for_backward(q, routed, wkv, wkv_t, kv, out)
         ctx.cfg = (mode, S, HK, wk.dtype, wv.dtype, None if w is None else w.shape)
         return out
 
     @staticmethod
     def backward(ctx, dout):
-        q, routed, wkv, kv, out = ctx.saved_tensors
+        q, routed, wkv, wkv_t, kv, out = ctx.saved_tensors
         mode, S, HK, wk_dtype, wv_dtype, w_shape = ctx.cfg
         dtype = q.dtype
         D = q.shape[-1]
@@ -336,20 +344,22 @@ class _TokenRouted(torch.autograd.Function):
             dwk = dwkv[:KV].to(wk_dtype) if need_wk else None
             dwv = dwkv[KV:].to(wv_dtype) if need_wv else None
         if need_r:
-            dr = _rows_grad(routed, dkv, wkv)
+            dr = _rows_grad(routed, dkv, wkv, wkv_t)
         dw = None
         if w_shape is not None and dws:
             dw = dws[0].view(w_shape) if len(dws) == 1 else torch.stack(dws, 0).sum(0).view(w_shape)
         return dq, dr, dwk, dwv, dw, None, None, None
 
 
-def _rows_grad(routed: torch.Tensor, dkv: torch.Tensor, wkv: torch.Tensor) -> torch.Tensor:
+def _rows_grad(routed: torch.Tensor, dkv: torch.Tensor, wkv: torch.Tensor,
+               wkv_t: Optional[torch.Tensor] = None) -> torch.Tensor:
     """d routed = dkv [Wk; Wv] (bf16: the chapter GEMM's rows mode with W = [Wk; Wv]^T).  When
     `routed` is the tail rows of a larger tensor (the routed part of a bank whose first rows are
     the shared chapters, split off by model.split_rows), the product is written into the tail of
     a buffer of the whole bank's shape, so the split's backward can hand that buffer on after
     filling the head rows instead of copying the tail."""
-    wkv_t = wkv.t().contiguous()
+    if wkv_t is None:
+        wkv_t = wkv.t().contiguous()
     native = ops.rows_gemm_ok(dkv, wkv_t)
 
     def product(out=None):

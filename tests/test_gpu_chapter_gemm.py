@@ -37,6 +37,22 @@ def test_weight_pack_exact(dev, wdt):
     assert torch.equal(only_t.cpu(), ref.t().contiguous())
 
 
+@pytest.mark.parametrize("wdt", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("N,K,ldt", [(4097, 768, 4352), (200, 64, 200), (37, 136, 48)])
+def test_weight_transpose_exact(dev, wdt, N, K, ldt):
+    """moc_weight_transpose: wt [K][ldt] = bf16(w)^T with zero columns N .. ldt-1, bit for bit
+    (the per-token router's padded W^T)."""
+    from memory_amd import _lib as L
+    from memory_amd._lib import call, ptr, stream_ptr
+    w = torch.randn(N, K, generator=gen(N + K)).to(wdt)
+    wd = w.to(dev)
+    wt = torch.full((K, ldt), 7.0, device=dev, dtype=torch.bfloat16)
+    call("moc_weight_transpose", ptr(wd), L.dtype_code(wdt), N, K, ptr(wt), ldt, stream_ptr(dev))
+    ref = torch.zeros(K, ldt, dtype=torch.bfloat16)
+    ref[:, :N] = w.to(torch.bfloat16).t()
+    assert torch.equal(wt.cpu(), ref)
+
+
 def _plan(ops, dev, chap, C):
     return ops.chapter_plan(torch.as_tensor(chap, dtype=torch.int32).to(dev), C)
 
