@@ -201,14 +201,41 @@ __global__ __launch_bounds__(kCgThreads) void chapter_gemm_kernel(
 #pragma unroll
     for (int i = 0; i < FT; ++i) cg_dma16(wres, woff + (uint32_t)(64 * i * K * 2), (uint32_t)(kt * 128), dst + 8192 * i);
   };
+  // gathered / per-edge X sources: looked up once per row block, and the workgroup's next tile's
+  // a tile ahead of its first stage (plan lookups are dependent scalar loads: kept off the path
+  // from a barrier to the DMAs that follow it)
+  int cur_rb = -1, nxt_rb = -1;
+  const bf16* cur_src[IPX];
+  const bf16* nxt_src[IPX];
+  auto lookup = [&](int rb, const bf16** out) {
+#pragma unroll
+    for (int i = 0; i < IPX; ++i)
+      out[i] = cg_src_rows<SRC>(min(rb * CPT + i, nu - 1), x, xred, ldx, uniq, csr_off, csr_edge);
+  };
   auto issue_x = [&](int s) {
     const int t = lo + slot + nslot * (s / nk), kt = s % nk;
     const int rb = t / NB;
     const char* dst = sX + (s % NBUF) * STX + wave * 1024;
+    if constexpr (SRC != CG_SRC_CONTIG) {
+      if (rb != cur_rb) {
+        if (rb == nxt_rb) {
+#pragma unroll
+          for (int i = 0; i < IPX; ++i) cur_src[i] = nxt_src[i];
+        } else {
+          lookup(rb, cur_src);
+        }
+        cur_rb = rb;
+        const int tn = t + nslot;
+        if (tn < hi && tn / NB != rb) {
+          nxt_rb = tn / NB;
+          lookup(nxt_rb, nxt_src);
+        }
+      }
+    }
 #pragma unroll
     for (int i = 0; i < IPX; ++i) {
       const int c = min(rb * CPT + i, nu - 1);  // rows of chapters past n_uniq: computed, not stored
-      const bf16* xb = cg_src_rows<SRC>(c, x, xred, ldx, uniq, csr_off, csr_edge);
+      const bf16* xb = SRC == CG_SRC_CONTIG ? cg_src_rows<SRC>(c, x, xred, ldx, uniq, csr_off, csr_edge) : cur_src[i];
       // a contiguous source ends at row xrows: rows past it read zero
       const uint32_t nb = SRC == CG_SRC_CONTIG ? (uint32_t)(min((int64_t)64, xrows - (int64_t)c * 64) * ldx * 2) : xbytes;
       cg_dma16(CG_RSRC(xb, nb), xoff, (uint32_t)(kt * 128), dst + 8192 * i);
