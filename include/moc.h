@@ -525,8 +525,8 @@ int moc_sparse_fwd(int dtype, const void* q, int64_t ntok, int HQ, const void* k
 /* Combine of the slot partials: mode 0 MoE sum_s w_s o_s; 1 joint; 2 joint with block weights
  * max(w, 0); 3 joint with log(max(w, 1e-20)) bias.  w f32 [E] (per edge), edge_u from the plan
  * (negative = skipped slot), o_part in the call's dtype.  out [tokens][HQ][64]; lse_joint f32
- * [tokens * rpe] (modes 1-3).  Up to 16384 rows of at most 68 slots with 16-byte aligned o_part
- * and out (decode) take a kernel that issues every load of a row in one round. */
+ * [tokens * rpe] (modes 1-3).  o_part and out 16-byte aligned.  Up to 16384 rows of at most 68
+ * slots (decode) take a kernel that issues every load of a row in one round. */
 int moc_sparse_combine(int dtype, const void* o_part, const float* lse_part, const int32_t* edge_u, const float* w,
                        int mode, int S, int rpe, int64_t ntok, int HQ, int hq_off, void* out, float* lse_joint,
                        hipStream_t stream);
@@ -550,7 +550,8 @@ int moc_sparse_bwd(int dtype, const void* q, const void* dout, int64_t ntok, int
                    int hq_off, int rpe, int mode, const float* lse_row, float* delta_row, const float* w,
                    float scale, void* dk, void* dv, int64_t ocs, int64_t ohs, int64_t ors, void* dq_part,
                    float* dlog, const int32_t* row_tab, hipStream_t stream);
-/* dq [tokens][HQ][64] rows hq_off .. hq_off+rpe-1 = sum over valid slots of dq_part. */
+/* dq [tokens][HQ][64] rows hq_off .. hq_off+rpe-1 = sum over valid slots of dq_part (both 16-byte
+ * aligned). */
 int moc_sparse_dq_combine(int dtype, const void* dq_part, const int32_t* edge_u, int S, int rpe, int64_t ntok,
                           int HQ, int hq_off, void* dq, hipStream_t stream);
 /* dw f32 [E]: mode 0 sum of dst rows; modes 2/3 sum of dlog rows / w (0 where the clamp is active). */

@@ -184,51 +184,76 @@ __global__ __launch_bounds__(64 * SpCfg<T>::NW) void sparse_fwd_kernel(
   }
 }
 
-// Per (token, row): combine the slot partials.  One wave per row: the slot weights a_s
-// live one per lane (64-slot chunks), the 16-lane group g streams the o_part rows of
-// slots g, g + 4, ... (16 bytes per lane), and the 4 groups are added in a fixed order.
+// Per (token, row): combine the slot partials.  One wave per row: the slot weights a_s live one
+// per lane (64-slot chunks); the partial rows are read as 16-byte pieces, a row of 64 dims being
+// LPR lanes (8 for bf16, 16 for f32) and lane group sg = lane / LPR streaming the rows of slots
+// sg, sg + NG, ... (four loads in flight per lane); the NG groups are added in a fixed order.
+// (Right after the kernels that wrote them, 16-byte loads of these rows take about half the time
+// of 8-byte ones.)
 __device__ __forceinline__ float sp_logw(int mode, float w) {
   if (mode == 2) return w > 0.f ? log2f(w) : -INFINITY;
   if (mode == 3) return log2f(fmaxf(w, 1e-20f));
   return 0.f;
 }
 
-// Weighted sum over the slots s0 .. s0 + 63 of one row (lane group g takes slots g, g + 4,
-// ...; lane s - s0 holds a_s); a_s = 0 marks a skipped slot, whose partial row is never read.
+template <typename P> struct SpRow16 {
+  static constexpr int EPL = 16 / (int)sizeof(P);   // elements per lane and load
+  static constexpr int LPR = 64 / EPL;              // lanes per 64-dim row
+  static constexpr int NG = 64 / LPR;               // rows per load instruction
+  typedef typename std::conditional<sizeof(P) == 2, bf16x8, f32x4>::type V;
+};
+
+// acc += sum over the slots s0 .. s0 + 63 of one row of a_s * part row (lane s - s0 holds a_s);
+// a_s = 0 marks a skipped slot, whose partial row is never read.
 template <typename P>
-__device__ __forceinline__ f32x4 sp_slot_sum(const P* __restrict__ part, int64_t tok, int S, int rpe, int r,
-                                             float a, int s0, int lane) {
-  const int g = lane >> 4, sub = lane & 15;
+__device__ __forceinline__ void sp_slot_sum(const P* __restrict__ part, int64_t tok, int S, int rpe, int r, float a,
+                                            int s0, int lane, float (&acc)[SpRow16<P>::EPL]) {
+  using R = SpRow16<P>;
+  const int sg = lane / R::LPR, ch = lane % R::LPR;
   const int n = min(64, S - s0);
-  const int iters = (n + 3) >> 2;   // wave-uniform trip count; 4 rows in flight per lane
-  f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int iters = (n + R::NG - 1) / R::NG;   // wave-uniform trip count
   for (int k0 = 0; k0 < iters; k0 += 4) {
-    f32x4 v[4];
+    typename R::V v[4];
     float av[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int j = 4 * (k0 + i) + g;
+      const int j = R::NG * (k0 + i) + sg;
       const float aj = __shfl(a, j & 63, 64);
       av[i] = j < n ? aj : 0.f;
-      v[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+      v[i] = typename R::V{};
       if (av[i] != 0.f) {
         const int64_t e = tok * S + s0 + j;
-        v[i] = part_load4(part + (e * rpe + r) * kSpDh + 4 * sub);
+        v[i] = *reinterpret_cast<const typename R::V*>(part + (e * rpe + r) * kSpDh + R::EPL * ch);
       }
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) acc += av[i] * v[i];
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int x = 0; x < R::EPL; ++x) acc[x] += av[i] * (float)v[i][x];
   }
-  return acc;
 }
 
-__device__ __forceinline__ f32x4 sp_groups_sum(f32x4 acc) {
+// sum over the NG lane groups (lane bits LPR .. 32), in a fixed order
+template <typename P>
+__device__ __forceinline__ void sp_groups_sum(float (&acc)[SpRow16<P>::EPL]) {
+  using R = SpRow16<P>;
 #pragma unroll
-  for (int x = 0; x < 4; ++x) {
-    acc[x] += __shfl_xor(acc[x], 16, 64);
-    acc[x] += __shfl_xor(acc[x], 32, 64);
+  for (int o = R::LPR; o < 64; o <<= 1)
+#pragma unroll
+    for (int x = 0; x < R::EPL; ++x) acc[x] += __shfl_xor(acc[x], o, 64);
+}
+
+// lanes < LPR store the row's 64 values (16 bytes each)
+template <typename T>
+__device__ __forceinline__ void sp_row_store(T* __restrict__ row, const float (&acc)[SpRow16<T>::EPL], float scale,
+                                             int lane) {
+  using R = SpRow16<T>;
+  if (lane < R::LPR) {
+    typename R::V o;
+#pragma unroll
+    for (int x = 0; x < R::EPL; ++x) o[x] = from_f<T>(acc[x] * scale);
+    *reinterpret_cast<typename R::V*>(row + R::EPL * lane) = o;
   }
-  return acc;
 }
 
 constexpr int kCombWaves = 4;
@@ -259,7 +284,9 @@ __global__ __launch_bounds__(64 * kCombWaves) void sparse_combine_kernel(const T
     M = wave_max(M);
   }
   float den = 0.f;
-  f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+  float acc[SpRow16<T>::EPL];
+#pragma unroll
+  for (int x = 0; x < SpRow16<T>::EPL; ++x) acc[x] = 0.f;
   for (int s0 = 0; s0 < S; s0 += 64) {
     const int s = s0 + lane;
     float a = 0.f;
@@ -271,20 +298,16 @@ __global__ __launch_bounds__(64 * kCombWaves) void sparse_combine_kernel(const T
       }
     }
     den += a;
-    acc += sp_slot_sum(o_part, tok, S, rpe, r, a, s0, lane);
+    sp_slot_sum(o_part, tok, S, rpe, r, a, s0, lane, acc);
   }
-  acc = sp_groups_sum(acc);
+  sp_groups_sum<T>(acc);
   float inv = 1.f;
   if (mode != 0) {
     den = wave_sum(den);
     inv = den > 0.f ? 1.f / den : 0.f;
     if (lane == 0) lse_joint[row] = den > 0.f ? M + log2f(den) : INFINITY;
   }
-  if (lane < 16) {
-    T* op = out + ((int64_t)tok * HQ + hq_off + r) * kSpDh + 4 * lane;
-#pragma unroll
-    for (int x = 0; x < 4; ++x) op[x] = from_f<T>(acc[x] * inv);
-  }
+  sp_row_store(out + ((int64_t)tok * HQ + hq_off + r) * kSpDh, acc, inv, lane);
 }
 
 // The same combine for few rows of at most 4 * kCombSmallPerGroup slots (decode: the shared
@@ -297,20 +320,14 @@ __global__ __launch_bounds__(64 * kCombWaves) void sparse_combine_kernel(const T
 // by a select (never multiplied by a zero weight, which would keep a NaN).
 constexpr int kCombSmallPerGroup = 17;
 
-template <typename T> struct Vec16;
-template <> struct Vec16<bf16> { typedef bf16x8 type; };
-template <> struct Vec16<float> { typedef f32x4 type; };
-
 template <typename T>
 __global__ __launch_bounds__(64 * kCombWaves) void sparse_combine_small_kernel(
     const T* __restrict__ o_part, const float* __restrict__ lse_part, const int32_t* __restrict__ edge_u,
     const float* __restrict__ w, int mode, int S, int rpe, int64_t ntok, int HQ, int hq_off, T* __restrict__ out,
     float* __restrict__ lse_joint) {
-  constexpr int EPL = 16 / (int)sizeof(T);    // elements per lane and load
-  constexpr int LPR = kSpDh / EPL;            // lanes per partial row
-  constexpr int NG = 64 / LPR;                // rows per load instruction
+  constexpr int EPL = SpRow16<T>::EPL, LPR = SpRow16<T>::LPR, NG = SpRow16<T>::NG;
   constexpr int NL = (4 * kCombSmallPerGroup + NG - 1) / NG;
-  typedef typename Vec16<T>::type V;
+  typedef typename SpRow16<T>::V V;
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * kCombWaves + (threadIdx.x >> 6);
   if (row >= ntok * rpe) return;
@@ -362,23 +379,14 @@ __global__ __launch_bounds__(64 * kCombWaves) void sparse_combine_small_kernel(
       for (int x = 0; x < EPL; ++x) acc[x] += aj * (float)v[i][x];
     }
   }
-  // sum over the NG lane groups (lane bits LPR .. 32), in a fixed order
-#pragma unroll
-  for (int o = LPR; o < 64; o <<= 1)
-#pragma unroll
-    for (int x = 0; x < EPL; ++x) acc[x] += __shfl_xor(acc[x], o, 64);
+  sp_groups_sum<T>(acc);
   float inv = 1.f;
   if (mode != 0) {
     const float den = wave_sum(a[0] + a[1]);
     inv = den > 0.f ? 1.f / den : 0.f;
     if (lane == 0) lse_joint[row] = den > 0.f ? M + log2f(den) : INFINITY;
   }
-  if (lane < LPR) {
-    V o;
-#pragma unroll
-    for (int x = 0; x < EPL; ++x) o[x] = from_f<T>(acc[x] * inv);
-    *reinterpret_cast<V*>(out + ((int64_t)tok * HQ + hq_off + r) * kSpDh + EPL * lane) = o;
-  }
+  sp_row_store(out + ((int64_t)tok * HQ + hq_off + r) * kSpDh, acc, inv, lane);
 }
 
 // ----------------------------------------------------------------- backward
@@ -732,18 +740,16 @@ __global__ __launch_bounds__(64 * kCombWaves) void sparse_dq_combine_kernel(cons
   if (row >= ntok * rpe) return;
   const int64_t tok = row / rpe;
   const int r = (int)(row % rpe);
-  f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+  float acc[SpRow16<T>::EPL];
+#pragma unroll
+  for (int x = 0; x < SpRow16<T>::EPL; ++x) acc[x] = 0.f;
   for (int s0 = 0; s0 < S; s0 += 64) {
     const int s = s0 + lane;
     const float a = (s < S && edge_u[tok * S + s] >= 0) ? 1.f : 0.f;
-    acc += sp_slot_sum(dq_part, tok, S, rpe, r, a, s0, lane);
+    sp_slot_sum(dq_part, tok, S, rpe, r, a, s0, lane, acc);
   }
-  acc = sp_groups_sum(acc);
-  if (lane < 16) {
-    T* op = dq + ((int64_t)tok * HQ + hq_off + r) * kSpDh + 4 * lane;
-#pragma unroll
-    for (int x = 0; x < 4; ++x) op[x] = from_f<T>(acc[x]);
-  }
+  sp_groups_sum<T>(acc);
+  sp_row_store(dq + ((int64_t)tok * HQ + hq_off + r) * kSpDh, acc, 1.f, lane);
 }
 
 // dw[e] for an edge e = token * S + s, summed over its rpe rows:
@@ -1361,13 +1367,14 @@ int moc_sparse_combine(int dtype, const void* o_part, const float* lse_part, con
   MOC_REQUIRE(mode >= 0 && mode <= 3, MOC_ERR_ARG, "moc_sparse_combine: mode %d", mode);
   MOC_REQUIRE((mode == 0 || mode >= 2) ? w != nullptr : true, MOC_ERR_ARG, "moc_sparse_combine: mode %d needs weights", mode);
   MOC_REQUIRE(mode == 0 || lse_joint, MOC_ERR_ARG, "moc_sparse_combine: joint modes need lse_joint");
+  MOC_REQUIRE(((uintptr_t)o_part & 15) == 0 && ((uintptr_t)out & 15) == 0, MOC_ERR_ARG,
+              "moc_sparse_combine: o_part and out must be 16-byte aligned");
   const int64_t rows = ntok * rpe;
   if (rows == 0) return MOC_OK;
   dim3 grid((unsigned)((rows + kCombWaves - 1) / kCombWaves));
   // few rows (decode): latency-bound, every load of a row in one round; many rows (token
   // routing over a batch): throughput-bound, the lighter streaming kernel keeps more rows resident
-  const bool small = S <= 4 * kCombSmallPerGroup && rows <= 16384 && ((uintptr_t)o_part & 15) == 0 &&
-                     ((uintptr_t)out & 15) == 0;
+  const bool small = S <= 4 * kCombSmallPerGroup && rows <= 16384;
 #define SC(KERN, TT)                                                                                                  \
   hipLaunchKernelGGL(KERN<TT>, grid, dim3(64 * kCombWaves), 0, stream, (const TT*)o_part, lse_part, edge_u, w, mode, S, \
                      rpe, ntok, HQ, hq_off, (TT*)out, lse_joint)
@@ -1446,6 +1453,8 @@ int moc_sparse_bwd(int dtype, const void* q, const void* dout, int64_t ntok, int
 int moc_sparse_dq_combine(int dtype, const void* dq_part, const int32_t* edge_u, int S, int rpe, int64_t ntok,
                           int HQ, int hq_off, void* dq, hipStream_t stream) {
   MOC_REQUIRE(dq_part && edge_u && dq, MOC_ERR_ARG, "moc_sparse_dq_combine: null pointer");
+  MOC_REQUIRE(((uintptr_t)dq_part & 15) == 0 && ((uintptr_t)dq & 15) == 0, MOC_ERR_ARG,
+              "moc_sparse_dq_combine: dq_part and dq must be 16-byte aligned");
   const int64_t rows = ntok * rpe;
   if (rows == 0) return MOC_OK;
   dim3 grid((unsigned)((rows + kCombWaves - 1) / kCombWaves));
