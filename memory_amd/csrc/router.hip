@@ -1664,13 +1664,32 @@ __global__ __launch_bounds__(256) void logit_grad_pack_kernel(const float* __res
   }
 }
 
+// db[c] = sum over the partial rows: a workgroup per 64 columns, wave w summing partial rows
+// [w nq, (w + 1) nq) with eight loads in flight (eight running sums, added in order), the four
+// waves' sums added in wave order through LDS: a fixed order, so the result is deterministic.
 __global__ __launch_bounds__(256) void logit_grad_colsum_kernel(const float* __restrict__ part, int nblk, int64_t C,
                                                                 float* __restrict__ db) {
-  const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (c >= C) return;
-  float s = 0.f;
-  for (int i = 0; i < nblk; ++i) s += part[(int64_t)i * C + c];
-  db[c] = s;
+  __shared__ float red[4][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t c = (int64_t)blockIdx.x * 64 + lane;
+  const int nq = (nblk + 3) / 4;
+  const int i0 = wave * nq, i1 = min(nblk, i0 + nq);
+  float acc[8];
+#pragma unroll
+  for (int u = 0; u < 8; ++u) acc[u] = 0.f;
+  if (c < C) {
+    for (int i = i0; i < i1; i += 8) {
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (i + u < i1) acc[u] += part[(int64_t)(i + u) * C + c];
+    }
+  }
+  float s = acc[0];
+#pragma unroll
+  for (int u = 1; u < 8; ++u) s += acc[u];
+  red[wave][lane] = s;
+  __syncthreads();
+  if (wave == 0 && c < C) db[c] = ((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane];
 }
 
 }  // namespace moc
@@ -2034,7 +2053,7 @@ int moc_logit_grad_pack(const float* dz, int64_t R, int64_t C, int64_t Cp, void*
                      db ? (float*)workspace : nullptr);
   if (int rc = check_launch("logit_grad_pack_kernel")) return rc;
   if (!db) return MOC_OK;
-  hipLaunchKernelGGL(logit_grad_colsum_kernel, dim3((unsigned)((C + 255) / 256)), dim3(256), 0, stream,
+  hipLaunchKernelGGL(logit_grad_colsum_kernel, dim3((unsigned)((C + 63) / 64)), dim3(256), 0, stream,
                      (const float*)workspace, nblk, C, db);
   return check_launch("logit_grad_colsum_kernel");
 }

@@ -823,8 +823,10 @@ class _RoutedAttention(torch.autograd.Function):
         needs = tuple(ctx.needs_input_grad[:5])
         dq, dbank, dwk, dwv, dom_part = routed_attn_backward(ctx.saved_tensors, ctx.cfg, dout, needs,
                                                               row_grad=ctx.row_grad)
-        B, NS = ctx.saved_tensors[3].shape
-        domega = dom_part.sum(-1).view(B, NS)
+        domega = None
+        if ctx.needs_input_grad[4]:
+            B, NS = ctx.saved_tensors[3].shape
+            domega = dom_part.sum(-1).view(B, NS)
         return dq, dbank, dwk, dwv, domega, None, None, None, None, None, None
 
 
