@@ -64,6 +64,17 @@ int moc_router_topk(const float* logits, int64_t R, int64_t C, int S, int k, int
  * Writes every element of dlogits f32 [R, C].  Same clamp_min(1e-12) gating as autograd. */
 int moc_router_topk_bwd(const float* logits, const int32_t* idx, const float* dw, int64_t R, int64_t C, int S,
                         int k, float* dlogits, hipStream_t stream);
+/* The per-token router's backward in one pass (router.py:294 + :114-149 autograd): the logit
+ * gradient of moc_router_topk_bwd (plus dz_in f32 [R, C], the logits' own gradient from the
+ * router losses, or NULL) is not stored; instead dzp bf16 [R, Cp] = its bf16 copy (columns
+ * C .. Cp-1 zero; the operand of dx = dz W and dW = dz^T x on the chapter kernels) and the bias
+ * gradient db f32 [C] = its column sums (fp32, fixed order; workspace from
+ * moc_router_topk_bwd_pack_workspace).  R > 64, C <= Cp <= 4608, Cp even, k <= 64;
+ * MOC_ERR_UNSUPPORTED outside that range (moc_router_topk_bwd + moc_logit_grad_pack then). */
+size_t moc_router_topk_bwd_pack_workspace(int64_t R, int64_t C);
+int moc_router_topk_bwd_pack(const float* logits, const int32_t* idx, const float* dw, int64_t R, int64_t C, int S,
+                             int k, const float* dz_in, int64_t Cp, void* dzp, float* db, void* workspace,
+                             size_t workspace_bytes, hipStream_t stream);
 
 /* Replaces MemoryTransformer._prepend_shared_chapters (memory_transformer/model.py:356-391):
  * idx_star = [0..S-1, idx], omega = [1 (S times), scale * w] / sum.  S > 0.

@@ -34,6 +34,8 @@ _SIGS = {
     "moc_abi_version": (_I, []),
     "moc_router_topk": (_I, [_P, _I64, _I64, _I, _I, _P, _P, _P, _P]),
     "moc_router_topk_bwd": (_I, [_P, _P, _P, _I64, _I64, _I, _I, _P, _P]),
+    "moc_router_topk_bwd_pack_workspace": (_SZ, [_I64, _I64]),
+    "moc_router_topk_bwd_pack": (_I, [_P, _P, _P, _I64, _I64, _I, _I, _P, _I64, _P, _P, _P, _SZ, _P]),
     "moc_prepend_shared": (_I, [_P, _P, _I64, _I, _I, _F, _P, _P, _P]),
     "moc_prepend_shared_bwd": (_I, [_P, _P, _I64, _I, _I, _F, _P, _P]),
     "moc_router_topk_prepend": (_I, [_P, _I64, _I64, _I, _I, _F, _P, _P, _P, _P, _P]),

@@ -502,10 +502,11 @@ __device__ __forceinline__ int wave_opaque(int v) {
 __device__ __forceinline__ void wave_load_row(const float* row, int C, int lane, float (&z)[kWaveMaxE]) {
   const __amdgpu_buffer_rsrc_t rs =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(row), (short)0, C * 4, 0x00020000);
+  const int ln = wave_opaque(lane);   // keeps the 72 column predicates out of loops around the call
 #pragma unroll
   for (int j = 0; j < kWaveMaxE; ++j) {
     const float v = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, lane * 4, 256 * j, 0));
-    z[j] = lane + 64 * j < C ? v : -INFINITY;
+    z[j] = ln + 64 * j < C ? v : -INFINITY;
   }
 }
 
@@ -824,6 +825,126 @@ __global__ __launch_bounds__(64 * kWaveRows) void router_topk_bwd_wave_kernel(
   if (lane < k) {
     const float dq = (S > 0 && ci >= S ? base : 0.f) + dsel;
     out[ci] = qi * (dq - DPP) + (dz_in ? dz_in[r * C + ci] : 0.f);
+  }
+}
+
+// The same backward with the logit gradient consumed on the spot by the per-token router's
+// backward products (router.py:294): instead of dlogits f32 [R, C] the kernel writes its bf16
+// copy dzp [R, Cp] (columns C .. Cp-1 zero: the operand of dx = dz W and dW = dz^T x on the
+// chapter kernels) and per-workgroup column sums of the fp32 values for the bias gradient.  A
+// wave takes kPackWaveRows consecutive rows; its column sums stay in registers (lane l: columns
+// l + 64 j) and the k selected entries' corrections go to the wave's LDS row; the workgroup's
+// waves are added in wave order into one partial row.  The values are those of
+// router_topk_bwd_wave_kernel (same expressions, same order).
+constexpr int kPackWaveRows = 8;
+
+template <bool DIN>
+__global__ __launch_bounds__(64 * kWaveRows) void router_topk_bwd_pack_kernel(
+    const float* __restrict__ logits, const int32_t* __restrict__ idx, const float* __restrict__ dw_hat, int64_t R,
+    int64_t C, int S, int k, const float* __restrict__ dz_in, int64_t Cp, bf16* __restrict__ dzp,
+    float* __restrict__ part) {
+  __shared__ float fix_all[kWaveRows][64 * kWaveMaxE];
+  const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  float* fix = fix_all[wv];
+  const int Ci = (int)C, Cpi = (int)Cp;
+  float col[kWaveMaxE];
+#pragma unroll
+  for (int j = 0; j < kWaveMaxE; ++j) {
+    col[j] = 0.f;
+    fix[lane + 64 * j] = 0.f;
+  }
+  const int64_t r0 = ((int64_t)blockIdx.x * kWaveRows + wv) * kPackWaveRows;
+  for (int rr = 0; rr < kPackWaveRows; ++rr) {
+    const int64_t r = r0 + rr;   // wave-uniform
+    if (r >= R) break;
+    const float* row = logits + r * C;
+    int32_t ci = 0;
+    float g = 0.f, zi = 0.f;
+    if (lane < k) {
+      ci = idx[r * k + lane];
+      g = dw_hat[r * k + lane];
+      zi = row[ci];
+    }
+    float z[kWaveMaxE];
+    wave_load_row(row, Ci, lane, z);
+    float mxa = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < kWaveMaxE; ++j) mxa = fmaxf(mxa, z[j]);
+    mxa = wave_max(mxa);
+    float s_all = 0.f, s_sel = 0.f;
+    int ln = wave_opaque(lane);
+#pragma unroll
+    for (int j = 0; j < kWaveMaxE; ++j) {
+      const float e = __expf(z[j] - mxa);
+      s_all += e;
+      s_sel += ln + 64 * j >= S ? e : 0.f;
+    }
+    const float Z = wave_sum(s_all), Zs = wave_sum(s_sel);
+    const float msum = S > 0 ? Zs / Z : 1.f;
+    const float denom = fmaxf(msum, 1e-12f);
+    const bool denom_live = msum >= 1e-12f;
+    const float qi = lane < k ? __expf(zi - mxa) / Z : 0.f;
+    const float pi = S > 0 ? qi / denom : qi;
+    const float Wsum = wave_sum(pi), GW = wave_sum(g * pi);
+    const float W = fmaxf(Wsum, 1e-12f);
+    const bool W_live = Wsum >= 1e-12f;
+    const float dwr = lane < k ? g / W - (W_live ? GW / (W * W) : 0.f) : 0.f;
+    const float A = wave_sum(dwr * qi);
+    const float base = (S > 0 && denom_live) ? -A / (denom * denom) : 0.f;
+    const float dsel = S > 0 ? dwr / denom : dwr;
+    const float DPP = (S > 0 ? base * msum : 0.f) + wave_sum(dsel * qi);
+    // bf16 row, the padding columns C .. Cp-1 included (their stores hold zeros)
+    const __amdgpu_buffer_rsrc_t os = __builtin_amdgcn_make_buffer_rsrc(dzp + r * Cp, (short)0, Cpi * 2, 0x00020000);
+    const float iz = 1.f / Z;
+    ln = wave_opaque(lane);
+    // with an incoming gradient, its row is read eight columns at a time ahead of their stores
+    constexpr int kChunk = DIN ? 8 : kWaveMaxE;
+#pragma unroll
+    for (int j0 = 0; j0 < kWaveMaxE; j0 += kChunk) {
+      float din[kChunk];
+#pragma unroll
+      for (int jj = 0; jj < kChunk; ++jj) {
+        din[jj] = 0.f;
+        if constexpr (DIN) {
+          const __amdgpu_buffer_rsrc_t is =
+              __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(dz_in + r * C), (short)0, Ci * 4, 0x00020000);
+          din[jj] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(is, lane * 4, 256 * (j0 + jj), 0));
+        }
+      }
+#pragma unroll
+      for (int jj = 0; jj < kChunk; ++jj) {
+        const int j = j0 + jj;
+        const int c = ln + 64 * j;
+        const float q = __expf(z[j] - mxa) * iz;
+        const float dq = (S > 0 && c >= S) ? base : 0.f;
+        const float v = q * (dq - DPP) + din[jj];   // 0 past C (q = 0 there, din reads zero)
+        col[j] += v;
+        const bf16 h = (bf16)v;
+        __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, h), os, lane * 2, 128 * j, 0);
+      }
+    }
+    // the selected entries, after the dense stores have completed: their exact values, and the
+    // difference to the dense value (q (dsel) ... ) into the wave's correction row
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    if (lane < k) {
+      const float dq = (S > 0 && ci >= S ? base : 0.f) + dsel;
+      const float din = DIN ? dz_in[r * C + ci] : 0.f;
+      const float v = qi * (dq - DPP) + din;
+      const float vd = qi * ((S > 0 && ci >= S ? base : 0.f) - DPP) + din;
+      dzp[r * Cp + ci] = (bf16)v;
+      fix[ci] += v - vd;   // distinct columns within a row: no two lanes touch one entry
+    }
+  }
+  // this wave's column sums into its LDS row, then the workgroup's rows in wave order
+#pragma unroll
+  for (int j = 0; j < kWaveMaxE; ++j) fix[lane + 64 * j] += col[j];
+  __syncthreads();
+  float* out = part + (int64_t)blockIdx.x * C;
+  for (int c = threadIdx.x; c < Ci; c += 64 * kWaveRows) {
+    float t = fix_all[0][c];
+#pragma unroll
+    for (int w = 1; w < kWaveRows; ++w) t += fix_all[w][c];
+    out[c] = t;
   }
 }
 
@@ -2031,6 +2152,40 @@ int moc_router_losses_bwd(const float* logits, int64_t R, int64_t C, const float
   return check_launch("router_loss_bwd_kernel");
 }
 
+
+size_t moc_router_topk_bwd_pack_workspace(int64_t R, int64_t C) {
+  if (R <= 0 || C <= 0) return 0;
+  const int64_t per = (int64_t)kWaveRows * kPackWaveRows;
+  return (size_t)((R + per - 1) / per) * (size_t)C * sizeof(float);
+}
+
+int moc_router_topk_bwd_pack(const float* logits, const int32_t* idx, const float* dw, int64_t R, int64_t C, int S,
+                             int k, const float* dz_in, int64_t Cp, void* dzp, float* db, void* workspace,
+                             size_t workspace_bytes, hipStream_t stream) {
+  MOC_REQUIRE(logits && idx && dw && dzp && db && workspace, MOC_ERR_ARG, "moc_router_topk_bwd_pack: null pointer");
+  MOC_REQUIRE(S >= 0 && S <= C && k > 0 && k <= C - S, MOC_ERR_ARG, "moc_router_topk_bwd_pack: bad S=%d k=%d C=%lld",
+              S, k, (long long)C);
+  MOC_REQUIRE(R > 64 && C <= 64 * kWaveMaxE && k <= kWaveMaxK, MOC_ERR_UNSUPPORTED,
+              "moc_router_topk_bwd_pack: needs R > 64, C <= %d, k <= %d (R=%lld C=%lld k=%d)", 64 * kWaveMaxE,
+              kWaveMaxK, (long long)R, (long long)C, k);
+  MOC_REQUIRE(Cp >= C && Cp <= 64 * kWaveMaxE && Cp % 2 == 0 && R * Cp < ((int64_t)1 << 40), MOC_ERR_ARG,
+              "moc_router_topk_bwd_pack: Cp=%lld (>= C, even, <= %d)", (long long)Cp, 64 * kWaveMaxE);
+  MOC_REQUIRE(((uintptr_t)dzp & 3) == 0, MOC_ERR_ARG, "moc_router_topk_bwd_pack: dzp must be 4-byte aligned");
+  MOC_REQUIRE(workspace_bytes >= moc_router_topk_bwd_pack_workspace(R, C), MOC_ERR_ARG,
+              "moc_router_topk_bwd_pack: workspace too small");
+  const int64_t per = (int64_t)kWaveRows * kPackWaveRows;
+  const int nblk = (int)((R + per - 1) / per);
+  if (dz_in)
+    hipLaunchKernelGGL(router_topk_bwd_pack_kernel<true>, dim3((unsigned)nblk), dim3(64 * kWaveRows), 0, stream,
+                       logits, idx, dw, R, C, S, k, dz_in, Cp, (bf16*)dzp, (float*)workspace);
+  else
+    hipLaunchKernelGGL(router_topk_bwd_pack_kernel<false>, dim3((unsigned)nblk), dim3(64 * kWaveRows), 0, stream,
+                       logits, idx, dw, R, C, S, k, dz_in, Cp, (bf16*)dzp, (float*)workspace);
+  if (int rc = check_launch("router_topk_bwd_pack_kernel")) return rc;
+  hipLaunchKernelGGL(logit_grad_colsum_kernel, dim3((unsigned)((C + 63) / 64)), dim3(256), 0, stream,
+                     (const float*)workspace, nblk, C, db);
+  return check_launch("logit_grad_colsum_kernel");
+}
 
 size_t moc_logit_grad_pack_workspace(int64_t R, int64_t C) {
   if (R <= 0 || C <= 0) return 0;

@@ -1032,6 +1032,85 @@ def col_sum(x: torch.Tensor) -> torch.Tensor:
     return out
 
 
+class _TokenRouter(torch.autograd.Function):
+    """The per-token router in one function: logits = x W^T + b (router.py:294, fp32 logits from
+    bf16 operands) and the top-k chain (router.py:114-149 over every token).  Returns (logits,
+    idx, w); the logits are an output for the router losses.  Backward: moc_router_topk_bwd_pack
+    turns dw (plus the logits' own gradient, when the losses took one) straight into the bf16
+    operand of the two products and the bias gradient, so the fp32 logit gradient is never
+    written; then dx on the rows GEMM (zero-padded W^T) and dW on the split-row weight gradient,
+    as _TokenRouterLinear does from a materialised logit gradient."""
+
+    @staticmethod
+    def forward(ctx, x, W, b, k, S):
+        Wc = W.to(x.dtype).contiguous()
+        R, K = x.shape
+        C = Wc.shape[0]
+        dev = x.device
+        logits = torch.empty(R, C, device=dev, dtype=torch.float32)
+        bias = None if b is None else b.float().contiguous()
+        st = stream_ptr(dev)
+        call("moc_rows_linear_f32", ptr(x), K, R, ptr(Wc), C, K, None if bias is None else ptr(bias), ptr(logits), C, st)
+        idx = torch.empty(R, k, device=dev, dtype=torch.int32)
+        w = torch.empty(R, k, device=dev, dtype=torch.float32)
+        call("moc_router_topk", ptr(logits), R, C, S, k, ptr(idx), ptr(w), None, st)
+        ctx.save_for_backward(x, Wc, logits, idx)
+        ctx.meta = (W.dtype, None if b is None else b.dtype, int(k), int(S))
+        ctx.mark_non_differentiable(idx)
+        ctx.set_materialize_grads(False)
+        return logits, idx, w
+
+    @staticmethod
+    def backward(ctx, dlogits, _didx, dw):
+        x, Wc, logits, idx = ctx.saved_tensors
+        w_dtype, b_dtype, k, S = ctx.meta
+        if dw is None and dlogits is None:
+            return None, None, None, None, None
+        R, K = x.shape
+        C = Wc.shape[0]
+        dev = x.device
+        st = stream_ptr(dev)
+        dwc = torch.zeros(R, k, device=dev, dtype=torch.float32) if dw is None else dw.float().contiguous()
+        dzin = None if dlogits is None else dlogits.float().contiguous()
+        Cp = (C + 255) // 256 * 256
+        dzp = torch.empty(R, Cp, device=dev, dtype=torch.bfloat16)
+        db32 = torch.empty(C, device=dev, dtype=torch.float32)
+        ws_bytes = L.query("moc_router_topk_bwd_pack_workspace", R, C)
+        ws = torch.empty(max(1, ws_bytes // 4), device=dev, dtype=torch.float32)
+        call("moc_router_topk_bwd_pack", ptr(logits), ptr(idx), ptr(dwc), R, C, S, k, ptr(dzin), Cp, ptr(dzp),
+             ptr(db32), ptr(ws), ws_bytes, st)
+        dx = dW = db = None
+        if ctx.needs_input_grad[0]:
+            wt = torch.empty(K, Cp, device=dev, dtype=torch.bfloat16)
+            call("moc_weight_transpose", ptr(Wc), L.dtype_code(Wc.dtype), C, K, ptr(wt), Cp, st)
+            dx = rows_linear(dzp, wt)
+        if ctx.needs_input_grad[1]:
+            dW = linear_wgrad(dzp, x, torch.float32)[:C].to(w_dtype)
+        if ctx.needs_input_grad[2] and b_dtype is not None:
+            db = db32.to(b_dtype)
+        return dx, dW, db, None, None
+
+
+def token_router_fused_ok(x: torch.Tensor, C: int, k: int) -> bool:
+    """Whether _TokenRouter takes these rows (bf16 tokens, d % 256 == 0, the one-wave-per-row
+    top-k kernels: more than 64 rows, C <= 4,608, k <= 64)."""
+    R, K = x.shape
+    return x.dtype == torch.bfloat16 and K % 256 == 0 and R > 64 and C <= 4608 and 0 < k <= 64
+
+
+def token_router(h: torch.Tensor, W: torch.Tensor, b: Optional[torch.Tensor], k: int, S: int):
+    """(logits (B*T, C) fp32, idx int32 (B*T, k), w fp32 (B*T, k)) of the per-token router
+    (router.py:262-340): fused when token_router_fused_ok, else the logits GEMM and the top-k
+    chain as two functions."""
+    L.require_gpu(h, W)
+    x = h.reshape(-1, h.shape[-1])
+    if token_router_fused_ok(x, W.shape[0], k):
+        return _TokenRouter.apply(x.contiguous(), W, b, int(k), int(S))
+    logits = router_token_logits(h, W, b)
+    idx, w = router_topk(logits, k, S)
+    return logits, idx, w
+
+
 def router_token_logits(h: torch.Tensor, W: torch.Tensor, b: Optional[torch.Tensor]) -> torch.Tensor:
     """Per-token router logits (B*T, C) in fp32 (router.py:294); see _TokenRouterLinear."""
     L.require_gpu(h, W)

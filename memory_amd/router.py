@@ -120,16 +120,16 @@ class ChapterRouter(nn.Module):
             raise ValueError(f"exclude_prefix_chapters must be in [0, {self.num_chapters}], got {S}")
         B, T, _ = hidden_states.shape
         C = self.num_chapters
-        logits = ops.router_token_logits(hidden_states, self.router.weight, self.router.bias)   # (B*T, C) fp32
         k = min(int(self.top_k), C - S)
         if k <= 0:
+            logits = ops.router_token_logits(hidden_states, self.router.weight, self.router.bias)   # (B*T, C) fp32
             idx = torch.empty((B, T, 0), dtype=torch.int32 if ids32 else torch.long, device=hidden_states.device)
             w = torch.empty((B, T, 0), dtype=torch.float32, device=hidden_states.device)
             losses = {}
             if return_losses:
                 losses = compute_router_losses(logits, None, idx.reshape(B * T, 0), C)
             return idx, w, losses
-        idx32, w = ops.router_topk(logits, k, S)
+        logits, idx32, w = ops.token_router(hidden_states, self.router.weight, self.router.bias, k, S)
         idx = (idx32 if ids32 else idx32.long()).view(B, T, k)
         losses = {}
         if return_losses:

@@ -161,3 +161,73 @@ def test_logit_grad_pack(gpu_device, R, C):
     dzp2 = torch.full((R, Cp), float("nan"), device=dev, dtype=torch.bfloat16)
     L.call("moc_logit_grad_pack", L.ptr(dzd), R, C, Cp, L.ptr(dzp2), None, None, 0, L.stream_ptr(dev))
     assert torch.equal(dzp2.cpu(), got)
+
+
+@pytest.mark.parametrize("R,C,S,k,with_in", [(8192, 4097, 1, 16, False), (8192, 4097, 1, 16, True),
+                                             (200, 300, 0, 5, True), (97, 4600, 3, 64, False)])
+def test_topk_bwd_pack_matches_chain(gpu_device, R, C, S, k, with_in):
+    """moc_router_topk_bwd_pack == moc_router_topk_bwd (+ the incoming logit gradient) then the
+    bf16 copy: the padded bf16 rows bit for bit, the bias gradient (column sums) against float64
+    sums of the chain's fp32 gradient; row counts that are not a multiple of the 32-row groups."""
+    dev = gpu_device
+    g = torch.Generator().manual_seed(R + C + k)
+    logits = (torch.randn(R, C, generator=g) * 2).to(dev)
+    idx = torch.empty(R, k, device=dev, dtype=torch.int32)
+    w = torch.empty(R, k, device=dev, dtype=torch.float32)
+    L.call("moc_router_topk", L.ptr(logits), R, C, S, k, L.ptr(idx), L.ptr(w), None, L.stream_ptr(dev))
+    dw = torch.randn(R, k, generator=g).to(dev)
+    dz_in = torch.randn(R, C, generator=g).to(dev) * 1e-3 if with_in else None
+    ref = torch.empty(R, C, device=dev)
+    L.call("moc_router_topk_bwd", L.ptr(logits), L.ptr(idx), L.ptr(dw), R, C, S, k, L.ptr(ref), L.stream_ptr(dev))
+    if with_in:
+        ref = ref + dz_in
+    Cp = min((C + 255) // 256 * 256, 4608)
+    dzp = torch.full((R, Cp), float("nan"), device=dev, dtype=torch.bfloat16)
+    db = torch.empty(C, device=dev)
+    ws_bytes = L.query("moc_router_topk_bwd_pack_workspace", R, C)
+    ws = torch.empty(ws_bytes // 4, device=dev)
+    L.call("moc_router_topk_bwd_pack", L.ptr(logits), L.ptr(idx), L.ptr(dw), R, C, S, k, L.ptr(dz_in), Cp, L.ptr(dzp),
+           L.ptr(db), L.ptr(ws), ws_bytes, L.stream_ptr(dev))
+    got = dzp.cpu()
+    assert torch.equal(got[:, :C], ref.cpu().to(torch.bfloat16)), "bf16 logit gradient"
+    assert (got[:, C:] == 0).all(), "padding columns must be zero"
+    assert_rel(db.cpu(), ref.cpu().double().sum(0), 1e-5, "db")
+
+
+@pytest.mark.parametrize("with_losses", [False, True])
+def test_token_router_fused_gradients(gpu_device, with_losses):
+    """The fused per-token router (ops.token_router: logits GEMM + top-k in one function, its
+    backward through moc_router_topk_bwd_pack) against the two-function composition on the same
+    inputs: logits, ids and weights equal; dx, dW and db within the bf16 / fp32 gates."""
+    from memory_amd import ops
+    from memory_amd.router import compute_router_losses
+    from helpers import assert_parity
+    dev = gpu_device
+    g = torch.Generator().manual_seed(11 + with_losses)
+    R, d, C, k, S = 1024, 256, 1025, 8, 1
+    x0 = (torch.randn(R, d, generator=g)).to(dev, torch.bfloat16)
+    W0 = (torch.randn(C, d, generator=g) * 0.05).to(dev)
+    b0 = (torch.randn(C, generator=g) * 0.1).to(dev)
+    dw = torch.randn(R, k, generator=g).to(dev)
+    outs = []
+    for fused in (True, False):
+        x = x0.clone().requires_grad_(True)
+        W = W0.clone().requires_grad_(True)
+        b = b0.clone().requires_grad_(True)
+        if fused:
+            assert ops.token_router_fused_ok(x, C, k)
+            logits, idx, w = ops._TokenRouter.apply(x, W, b, k, S)
+        else:
+            logits = ops.router_token_logits(x, W, b)
+            idx, w = ops.router_topk(logits, k, S)
+        loss = (w * dw).sum()
+        if with_losses:
+            losses = compute_router_losses(logits, None, idx, C)
+            loss = loss + 0.3 * losses["load_balance"] + 0.01 * losses["z_loss"]
+        loss.backward()
+        outs.append((logits.detach(), idx, w.detach(), x.grad, W.grad, b.grad))
+    (l1, i1, w1, dx1, dW1, db1), (l2, i2, w2, dx2, dW2, db2) = outs
+    assert torch.equal(l1, l2) and torch.equal(i1, i2) and torch.equal(w1, w2)
+    assert_parity(dx1, dx2.float(), torch.bfloat16, "dx")
+    assert_parity(dW1, dW2, torch.float32, "dW")
+    assert_parity(db1, db2, torch.float32, "db")
