@@ -836,7 +836,7 @@ __global__ __launch_bounds__(64 * kWaveRows) void router_topk_bwd_wave_kernel(
 // l + 64 j) and the k selected entries' corrections go to the wave's LDS row; the workgroup's
 // waves are added in wave order into one partial row.  The values are those of
 // router_topk_bwd_wave_kernel (same expressions, same order).
-constexpr int kPackWaveRows = 8;
+constexpr int kPackWaveRows = 4;
 
 template <bool DIN>
 __global__ __launch_bounds__(64 * kWaveRows) void router_topk_bwd_pack_kernel(
@@ -1785,15 +1785,19 @@ __global__ __launch_bounds__(256) void logit_grad_pack_kernel(const float* __res
   }
 }
 
-// db[c] = sum over the partial rows: a workgroup per 64 columns, wave w summing partial rows
-// [w nq, (w + 1) nq) with eight loads in flight (eight running sums, added in order), the four
-// waves' sums added in wave order through LDS: a fixed order, so the result is deterministic.
-__global__ __launch_bounds__(256) void logit_grad_colsum_kernel(const float* __restrict__ part, int nblk, int64_t C,
-                                                                float* __restrict__ db) {
-  __shared__ float red[4][64];
+// db[c] = sum over the partial rows: a workgroup per 64 columns, wave w of kColsumWaves summing
+// partial rows [w nq, (w + 1) nq) with eight loads in flight (eight running sums, added in
+// order), the waves' sums added in wave order through LDS: a fixed order, so the result is
+// deterministic.
+constexpr int kColsumWaves = 16;
+
+__global__ __launch_bounds__(64 * kColsumWaves) void logit_grad_colsum_kernel(const float* __restrict__ part,
+                                                                              int nblk, int64_t C,
+                                                                              float* __restrict__ db) {
+  __shared__ float red[kColsumWaves][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t c = (int64_t)blockIdx.x * 64 + lane;
-  const int nq = (nblk + 3) / 4;
+  const int nq = (nblk + kColsumWaves - 1) / kColsumWaves;
   const int i0 = wave * nq, i1 = min(nblk, i0 + nq);
   float acc[8];
 #pragma unroll
@@ -1810,7 +1814,12 @@ __global__ __launch_bounds__(256) void logit_grad_colsum_kernel(const float* __r
   for (int u = 1; u < 8; ++u) s += acc[u];
   red[wave][lane] = s;
   __syncthreads();
-  if (wave == 0 && c < C) db[c] = ((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane];
+  if (wave == 0 && c < C) {
+    float t = red[0][lane];
+#pragma unroll
+    for (int w = 1; w < kColsumWaves; ++w) t += red[w][lane];
+    db[c] = t;
+  }
 }
 
 }  // namespace moc
@@ -2182,7 +2191,7 @@ int moc_router_topk_bwd_pack(const float* logits, const int32_t* idx, const floa
     hipLaunchKernelGGL(router_topk_bwd_pack_kernel<false>, dim3((unsigned)nblk), dim3(64 * kWaveRows), 0, stream,
                        logits, idx, dw, R, C, S, k, dz_in, Cp, (bf16*)dzp, (float*)workspace);
   if (int rc = check_launch("router_topk_bwd_pack_kernel")) return rc;
-  hipLaunchKernelGGL(logit_grad_colsum_kernel, dim3((unsigned)((C + 63) / 64)), dim3(256), 0, stream,
+  hipLaunchKernelGGL(logit_grad_colsum_kernel, dim3((unsigned)((C + 63) / 64)), dim3(64 * kColsumWaves), 0, stream,
                      (const float*)workspace, nblk, C, db);
   return check_launch("logit_grad_colsum_kernel");
 }
@@ -2208,7 +2217,7 @@ int moc_logit_grad_pack(const float* dz, int64_t R, int64_t C, int64_t Cp, void*
                      db ? (float*)workspace : nullptr);
   if (int rc = check_launch("logit_grad_pack_kernel")) return rc;
   if (!db) return MOC_OK;
-  hipLaunchKernelGGL(logit_grad_colsum_kernel, dim3((unsigned)((C + 63) / 64)), dim3(256), 0, stream,
+  hipLaunchKernelGGL(logit_grad_colsum_kernel, dim3((unsigned)((C + 63) / 64)), dim3(64 * kColsumWaves), 0, stream,
                      (const float*)workspace, nblk, C, db);
   return check_launch("logit_grad_colsum_kernel");
 }
