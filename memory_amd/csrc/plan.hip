@@ -41,17 +41,50 @@ __global__ __launch_bounds__(256) void plan_hist_kernel(const int32_t* __restric
   for (int64_t c = threadIdx.x; c < C; c += 256) counts[(int64_t)g * C + c] = h[c];
 }
 
-// Column prefix over blocks: counts[g][c] <- sum_{g' < g} counts[g'][c]; total[c] = sum.
-__global__ void plan_colscan_kernel(int32_t* __restrict__ counts, int G, int64_t C, int32_t* __restrict__ total) {
-  const int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (c >= C) return;
-  int32_t run = 0;
-  for (int g = 0; g < G; ++g) {
-    int32_t v = counts[(int64_t)g * C + c];
-    counts[(int64_t)g * C + c] = run;
-    run += v;
+// Column prefix over blocks: counts[g][c] <- sum_{g' < g} counts[g'][c]; total[c] = sum.  A
+// workgroup per 64 columns (lane = column), wave w of kScanWaves owning blocks [w gq, (w + 1) gq):
+// its counts are read at once, the waves' sums scanned through LDS, then each wave writes its
+// blocks' prefixes.
+constexpr int kScanWaves = 16;
+constexpr int kScanPer = 16;   // blocks a wave holds in registers per pass
+
+__global__ __launch_bounds__(64 * kScanWaves) void plan_colscan_kernel(int32_t* __restrict__ counts, int G, int64_t C,
+                                                                       int32_t* __restrict__ total) {
+  __shared__ int32_t wsum[kScanWaves][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t c = (int64_t)blockIdx.x * 64 + lane;
+  const int gq = (G + kScanWaves - 1) / kScanWaves;
+  const int g0 = wave * gq, g1 = min(G, g0 + gq);
+  int32_t s = 0;
+  if (c < C)
+    for (int g = g0; g < g1; g += kScanPer) {
+      int32_t v[kScanPer];
+#pragma unroll
+      for (int u = 0; u < kScanPer; ++u) v[u] = g + u < g1 ? counts[(int64_t)(g + u) * C + c] : 0;
+#pragma unroll
+      for (int u = 0; u < kScanPer; ++u) s += v[u];
+    }
+  wsum[wave][lane] = s;
+  __syncthreads();
+  int32_t run = 0, all = 0;
+#pragma unroll
+  for (int w = 0; w < kScanWaves; ++w) {
+    const int32_t t = wsum[w][lane];
+    run += w < wave ? t : 0;
+    all += t;
   }
-  total[c] = run;
+  if (c >= C) return;
+  if (wave == 0) total[c] = all;
+  for (int g = g0; g < g1; g += kScanPer) {
+    int32_t v[kScanPer];
+#pragma unroll
+    for (int u = 0; u < kScanPer; ++u) v[u] = g + u < g1 ? counts[(int64_t)(g + u) * C + c] : 0;
+#pragma unroll
+    for (int u = 0; u < kScanPer; ++u) {
+      if (g + u < g1) counts[(int64_t)(g + u) * C + c] = run;
+      run += v[u];
+    }
+  }
 }
 
 // Single workgroup: exclusive scans of total[c] and of (total[c] > 0).
@@ -95,27 +128,68 @@ __global__ __launch_bounds__(1024) void plan_scan_kernel(const int32_t* __restri
   if (tid == 0) { n_uniq[0] = carry[1]; n_uniq[1] = (int32_t)(E - carry[0]); csr_off[carry[1]] = carry[0]; }
 }
 
-// Stable placement: an edge's position is its chapter's start, plus the
-// edges of that chapter in earlier blocks, plus the edges of that chapter
-// earlier in this block (counted from an LDS copy of the block's ids).
+// Stable placement: an edge's position is its chapter's start, plus the edges of that chapter in
+// earlier blocks, plus the edges of that chapter earlier in this block.  The last term from LDS:
+// the block's edges are counted per chapter (arrival order, atomics), the counts scanned into
+// per-chapter segments of a block-local list filled in arrival order, and an edge's rank is the
+// number of its segment's entries with a smaller index (segments hold ~E / (G C) edges).
+__device__ __forceinline__ int plan_wave_incl_scan(int v) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int t = __shfl_up(v, o, 64);
+    if (lane >= o) v += t;
+  }
+  return v;
+}
+
 __global__ __launch_bounds__(256) void plan_place_kernel(const int32_t* __restrict__ chap, int64_t E, int64_t C,
                                                          const int32_t* __restrict__ counts,
                                                          const int32_t* __restrict__ start,
                                                          const int32_t* __restrict__ uid,
                                                          int32_t* __restrict__ edge_u, int32_t* __restrict__ csr_edge) {
-  __shared__ int32_t ids[kPlanEdgesPerBlock];
-  const int g = blockIdx.x;
+  extern __shared__ int32_t boff[];   // [C]: this block's count, then segment offset, per chapter
+  __shared__ int32_t ids[kPlanEdgesPerBlock], slot[kPlanEdgesPerBlock], lst[kPlanEdgesPerBlock];
+  __shared__ int32_t wtot[4];
+  const int g = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t e0 = (int64_t)g * kPlanEdgesPerBlock;
   const int n = (int)min((int64_t)kPlanEdgesPerBlock, E - e0);
-  for (int i = threadIdx.x; i < n; i += 256) ids[i] = chap[e0 + i];
+  for (int64_t c = tid; c < C; c += 256) boff[c] = 0;
+  for (int i = tid; i < n; i += 256) ids[i] = chap[e0 + i];
   __syncthreads();
-  for (int i = threadIdx.x; i < n; i += 256) {
+  for (int i = tid; i < n; i += 256) {
+    const int32_t c = ids[i];
+    slot[i] = (c >= 0 && c < C) ? atomicAdd(&boff[c], 1) : -1;
+  }
+  __syncthreads();
+  // exclusive scan of the per-chapter counts: thread t owns chapters [t per, (t + 1) per)
+  const int per = (int)((C + 255) / 256);
+  const int64_t c0 = (int64_t)tid * per, c1 = min(C, c0 + per);
+  int lt = 0;
+  for (int64_t c = c0; c < c1; ++c) lt += boff[c];
+  const int it = plan_wave_incl_scan(lt);
+  if (lane == 63) wtot[wave] = it;
+  __syncthreads();
+  int run = it - lt;
+  for (int w = 0; w < wave; ++w) run += wtot[w];
+  for (int64_t c = c0; c < c1; ++c) {
+    const int t = boff[c];
+    boff[c] = run;
+    run += t;
+  }
+  __syncthreads();
+  for (int i = tid; i < n; i += 256)
+    if (slot[i] >= 0) lst[boff[ids[i]] + slot[i]] = i;
+  __syncthreads();
+  const int placed = wtot[0] + wtot[1] + wtot[2] + wtot[3];
+  for (int i = tid; i < n; i += 256) {
     const int32_t c = ids[i];
     const bool ok = c >= 0 && c < C;
     edge_u[e0 + i] = ok ? uid[c] : -1;
     if (!ok) continue;
+    const int s0 = boff[c], s1 = c + 1 < C ? boff[c + 1] : placed;
     int before = 0;
-    for (int j = 0; j < i; ++j) before += ids[j] == c;
+    for (int j = s0; j < s1; ++j) before += lst[j] < i;
     csr_edge[start[c] + counts[(int64_t)g * C + c] + before] = (int32_t)(e0 + i);
   }
 }
@@ -256,11 +330,13 @@ int plan_launch(const int32_t* chap, int64_t E, int64_t C, void* workspace, int3
   hipLaunchKernelGGL(plan_hist_kernel, dim3(G), dim3(256), lds, stream, chap, E, C, counts);
   int rc = check_launch("plan_hist_kernel");
   if (rc) return rc;
-  hipLaunchKernelGGL(plan_colscan_kernel, dim3((unsigned)((C + 255) / 256)), dim3(256), 0, stream, counts, G, C, total);
+  hipLaunchKernelGGL(plan_colscan_kernel, dim3((unsigned)((C + 63) / 64)), dim3(64 * kScanWaves), 0, stream, counts, G,
+                     C, total);
   if ((rc = check_launch("plan_colscan_kernel"))) return rc;
   hipLaunchKernelGGL(plan_scan_kernel, dim3(1), dim3(1024), 0, stream, total, C, E, start, uid, uniq, csr_off, n_uniq);
   if ((rc = check_launch("plan_scan_kernel"))) return rc;
-  hipLaunchKernelGGL(plan_place_kernel, dim3(G), dim3(256), 0, stream, chap, E, C, counts, start, uid, edge_u, csr_edge);
+  hipLaunchKernelGGL(plan_place_kernel, dim3(G), dim3(256), lds, stream, chap, E, C, counts, start, uid, edge_u,
+                     csr_edge);
   return check_launch("plan_place_kernel");
 }
 

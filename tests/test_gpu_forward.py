@@ -151,7 +151,7 @@ def test_col_sum(dev, dtype, R, C):
 # ------------------------------------------------------------------ chapter plan
 
 @pytest.mark.parametrize("B,NS,C", [(8, 65, 4097), (2, 5, 33), (64, 65, 4097), (3, 7, 5), (300, 16, 4096),
-                                    (16, 64, 300), (4, 20, 10000)])
+                                    (16, 64, 300), (4, 20, 10000), (2048, 16, 33), (8192, 16, 4096)])
 def test_chapter_plan_matches_numpy(dev, B, NS, C):
     g = np.random.default_rng(B * NS + C)
     chap = np.stack([g.choice(C, size=NS, replace=NS > C) for _ in range(B)]).astype(np.int32)
@@ -179,6 +179,26 @@ def test_chapter_plan_skips_out_of_range(dev):
     assert plan.edge_u.cpu().tolist() == [0, 2, 3, -1, 2, -1, 1, 3]
     assert plan.csr_off.cpu().tolist()[:5] == [0, 1, 2, 4, 6]
     assert plan.csr_edge.cpu().tolist()[:6] == [0, 6, 1, 4, 2, 7]
+
+
+def test_chapter_plan_general_path_skips_out_of_range(dev):
+    """More than 1,024 edges (the multi-block path): ids outside [0, C) are skipped, the rest
+    planned as the stable (chapter, edge) order."""
+    g = np.random.default_rng(7)
+    C = 50
+    chap = g.integers(-3, C + 3, size=(100, 30)).astype(np.int32)
+    plan = _ops().chapter_plan(torch.from_numpy(chap).to(dev), C)
+    flat = chap.reshape(-1)
+    ok = (flat >= 0) & (flat < C)
+    n_u, n_bad = plan.n_uniq.cpu().tolist()
+    uniq = np.unique(flat[ok])
+    assert (n_u, n_bad) == (len(uniq), int((~ok).sum()))
+    assert np.array_equal(plan.uniq.cpu().numpy()[:n_u], uniq)
+    eu = plan.edge_u.cpu().numpy()
+    assert np.array_equal(eu[ok], np.searchsorted(uniq, flat[ok])) and (eu[~ok] == -1).all()
+    idx = np.arange(flat.size)[ok]
+    order = idx[np.lexsort((idx, flat[ok]))]
+    assert np.array_equal(plan.csr_edge.cpu().numpy()[:ok.sum()], order)
 
 
 @pytest.mark.parametrize("C", [1, 300, 4097])
