@@ -600,6 +600,12 @@ _ATTN_SAVED = ("q", "bank", "wkv", "om", "out", "lse", "kv", "mean", "rstd", "un
                "csr_edge")
 
 
+def _tiny_chapters(max_u: int, T: int, d: int, KV: int) -> bool:
+    """At most 256 rows of distinct chapters with the few-row kernel's shapes (d, 2 KV multiples
+    of 128): the K/V projection and its input gradient run on moc_linear_rows."""
+    return max_u * T <= 256 and d % 128 == 0 and (2 * KV) % 128 == 0
+
+
 def routed_attn_forward(q, bank, wk, wv, omega, idx_star, num_chapters, T, norm, eps, HK, wkv=None):
     """Forward body of the sequence-routed attention (plan, gather + K/V projection, joint
     attention): returns (out, saved tensors in _ATTN_SAVED order, cfg).  ``wkv``: the packed
@@ -630,7 +636,16 @@ def routed_attn_forward(q, bank, wk, wv, omega, idx_star, num_chapters, T, norm,
         # normalised or f32 bank is gathered into bf16 rows first)
         if wkv is None:
             wkv, _ = weight_pack(wk, wv)
-        if norm == L.MOC_NORM_NONE and bank.dtype == torch.bfloat16:
+        if _tiny_chapters(plan.max_u, T, d, KV):
+            # a few chapters (the token path's shared chapters): their rows gathered, then the
+            # few-row kernel, whose loads go out in one round (a persistent GEMM would walk the
+            # whole K dimension on one tile)
+            X = torch.empty(plan.max_u * T, d, device=q.device, dtype=dtype)
+            call("moc_gather_rows", L.dtype_code(dtype), ptr(bank), L.dtype_code(bank.dtype), d, T,
+                 ptr(plan.uniq), ptr(plan.n_uniq), plan.max_u, ptr(mean), ptr(rstd), ptr(X), stream_ptr(q.device))
+            kv = linear_rows(X, wkv)
+            del X
+        elif norm == L.MOC_NORM_NONE and bank.dtype == torch.bfloat16:
             kv = chapter_project(bank, plan, wkv, gather=True)
         else:
             X = torch.empty(plan.max_u * T, d, device=q.device, dtype=dtype)
@@ -754,7 +769,24 @@ def routed_attn_backward(saved, cfg, dout, needs, row_grad=None, after_dq=None, 
             # dX per distinct chapter (edges summed) on the chapter GEMM; with a plain bank it
             # is stored straight into the chapter's rows of the dense gradient
             _, wkv_t = weight_pack(wkv[:KV], wkv[KV:], rows=False, transposed=True)
-            if row_grad is None and norm == L.MOC_NORM_NONE:
+            if _tiny_chapters(max_u, T, d, KV):
+                # a few chapters: the edges' rows summed per chapter, dX on the few-row kernel
+                # (fp32 out), then the scatter into the bank gradient
+                dkv_c = torch.empty(max_u * T, 2 * KV, device=dev, dtype=torch.bfloat16)
+                call("moc_dkv_reduce", L.MOC_BF16, ptr(dkv_edge), ptr(n_uniq), ptr(csr_off), ptr(csr_edge), max_u,
+                     2 * KV, ptr(dkv_c), st)
+                dXc = torch.empty(max_u * T, d, device=dev, dtype=torch.float32)
+                call("moc_linear_rows", ptr(dkv_c), max_u * T, 2 * KV, ptr(wkv_t), d, L.MOC_F32, ptr(dXc), st)
+                if row_grad is not None:
+                    row_grad.accumulate(dXc, bank, uniq, n_uniq, max_u, None, None, mean, rstd, norm)
+                else:
+                    dbank, filled = dbank_zero
+                    if filled is not None:
+                        torch.cuda.current_stream(dev).wait_event(filled)
+                    call("moc_bank_scatter", L.MOC_F32, ptr(dXc), ptr(bank), L.dtype_code(bank.dtype), d, T,
+                         ptr(uniq), ptr(n_uniq), max_u, None, None, ptr(mean), ptr(rstd), norm, ptr(dbank), st)
+                    dbank = dbank.to(bank_dtype)
+            elif row_grad is None and norm == L.MOC_NORM_NONE:
                 dbank, filled = dbank_zero
                 if filled is not None:
                     torch.cuda.current_stream(dev).wait_event(filled)
