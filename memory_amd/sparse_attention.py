@@ -13,7 +13,8 @@ Combine modes (see csrc/sparse_xattn.hip): 0 = exact per-chapter MoE
 (sum_s w_s softmax_s V_s); 1 = joint softmax over all selected keys;
 2 = joint softmax with block weights p ~ max(w, 0) e^s (v1-v3 block_weights_bths);
 3 = joint softmax with a log(max(w, 1e-20)) logit bias (v5).
-Chapters are 64 tokens (block_size 64); head_dim 64.
+The kernels work on 64-key blocks (head_dim 64): block_size 64 for every mode, any multiple of
+64 for the joint modes; fp32, bf16, and fp16 through the fp32 kernels.
 """
 
 from __future__ import annotations
@@ -223,15 +224,42 @@ class _FSAFunction(torch.autograd.Function):
         return dq, dk, dv, dw, None, None, None
 
 
-def _check_common(cu_seqlens_q, cu_seqlens_k, disable_causal_mask, block_size):
+def _check_common(cu_seqlens_q, cu_seqlens_k, disable_causal_mask, block_size, joint: bool = True):
+    """``joint``: the combine is one softmax over every selected key (modes 1-3), so a block of
+    64 m keys may be taken as m consecutive 64-key blocks; the per-chapter MoE combine (mode 0)
+    needs block_size 64."""
     if cu_seqlens_q is not None or cu_seqlens_k is not None:
         raise NotImplementedError("variable-length (cu_seqlens) inputs are not supported by the HIP kernels")
     if not disable_causal_mask:
         raise NotImplementedError(
             "causal memory masking is not implemented; memory cross-attention is non-causal "
             "(MemoryCrossAttention passes disable_causal_mask=True, memory_attention.py:816)")
-    if int(block_size) != BLOCK:
-        raise ValueError(f"block_size must be {BLOCK} (the chapter tile of the HIP kernels), got {block_size}")
+    bs = int(block_size)
+    if joint and (bs < BLOCK or bs % BLOCK != 0):
+        raise ValueError(f"block_size must be a multiple of {BLOCK} (the chapter tile of the HIP kernels), got "
+                         f"{block_size}")
+    if not joint and bs != BLOCK:
+        raise ValueError(f"block_size must be {BLOCK} for the per-chapter (MoE) combine, got {block_size}")
+
+
+def _fsa(q, k, v, w, idx, mode: int, scale: float, block_size: int):
+    """The FSA function over 64-key blocks.  A block of 64 m keys (joint modes) is m consecutive
+    64-key blocks carrying the block's weight: the joint softmax over them is the joint softmax
+    over the blocks, the block weight's gradient the sum of its sub-blocks' (autograd of the
+    repeat), and a block reaching past the keys has its missing sub-blocks skipped as out of range
+    (the reference masks those keys).  fp16 inputs run the fp32 kernels (exact widening), the
+    output rounded back to fp16."""
+    m = int(block_size) // BLOCK
+    if m > 1:
+        sub = torch.arange(m, device=idx.device, dtype=idx.dtype)
+        idx = (idx.unsqueeze(-1) * m + sub).flatten(-2)    # negative ids stay negative
+        if w is not None:
+            w = w.repeat_interleave(m, dim=-1)
+    half = q.dtype == torch.float16
+    if half:
+        q, k, v = q.float(), k.float(), v.float()
+    out = _FSAFunction.apply(q, k, v, w, idx, mode, scale)
+    return out.to(torch.float16) if half else out
 
 
 def _indices(block_indices_bths, topk_idx_hns, q):
@@ -255,17 +283,17 @@ def FSA_topk_sparse_attention_bthd(q_bthd, k_bthd, v_bthd, block_indices_bths, b
         H, N, S = topk_w_hns.shape
         w = topk_w_hns.permute(1, 0, 2).reshape(q_bthd.shape[0], q_bthd.shape[1], H, S)
     scale = float(softmax_scale) if softmax_scale is not None else q_bthd.shape[-1] ** -0.5
-    return _FSAFunction.apply(q_bthd, k_bthd, v_bthd, w, idx, 1 if w is None else 2, scale)
+    return _fsa(q_bthd, k_bthd, v_bthd, w, idx, 1 if w is None else 2, scale, block_size)
 
 
 def FSA_topk_sparse_attention_weighted_bthd(q_bthd, k_bthd, v_bthd, block_indices_bths, chapter_weights_bts,
                                             block_size, softmax_scale=None, cu_seqlens_q=None, cu_seqlens_k=None,
                                             topk_idx_hns=None, assume_sorted_topk=False, disable_causal_mask=False):
     """Exact per-chapter MoE combine: sum_s w_s softmax(q K_s^T) V_s (kernel_v4 semantics)."""
-    _check_common(cu_seqlens_q, cu_seqlens_k, disable_causal_mask, block_size)
+    _check_common(cu_seqlens_q, cu_seqlens_k, disable_causal_mask, block_size, joint=False)
     idx = _indices(block_indices_bths, topk_idx_hns, q_bthd)
     scale = float(softmax_scale) if softmax_scale is not None else q_bthd.shape[-1] ** -0.5
-    return _FSAFunction.apply(q_bthd, k_bthd, v_bthd, chapter_weights_bts, idx, 0, scale)
+    return _fsa(q_bthd, k_bthd, v_bthd, chapter_weights_bts, idx, 0, scale, block_size)
 
 
 def FSA_topk_sparse_attention_weighted_joint_bias_bthd(q_bthd, k_bthd, v_bthd, block_indices_bths,
@@ -276,7 +304,7 @@ def FSA_topk_sparse_attention_weighted_joint_bias_bthd(q_bthd, k_bthd, v_bthd, b
     _check_common(cu_seqlens_q, cu_seqlens_k, disable_causal_mask, block_size)
     idx = _indices(block_indices_bths, topk_idx_hns, q_bthd)
     scale = float(softmax_scale) if softmax_scale is not None else q_bthd.shape[-1] ** -0.5
-    return _FSAFunction.apply(q_bthd, k_bthd, v_bthd, chapter_weights_bts, idx, 3, scale)
+    return _fsa(q_bthd, k_bthd, v_bthd, chapter_weights_bts, idx, 3, scale, block_size)
 
 
 # ------------------------------------------------------------------ model path

@@ -114,6 +114,77 @@ def test_fsa_rejects_unsupported(gpu_device):
         SA.FSA_topk_sparse_attention_bthd(q, k, k, idx, 64)
     with pytest.raises(ValueError, match="block_size"):
         SA.FSA_topk_sparse_attention_bthd(q, k, k, idx, 32, disable_causal_mask=True)
+    with pytest.raises(ValueError, match="block_size"):
+        SA.FSA_topk_sparse_attention_weighted_bthd(q, k, k, idx, torch.ones(1, 4, 1, device=dev), 128,
+                                                   disable_causal_mask=True)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("mode,BS", [(1, 128), (2, 128), (3, 256), (1, 64), (0, 64), (3, 64)])
+def test_fsa_block_sizes_and_fp16(gpu_device, dtype, mode, BS):
+    """The FSA entry points at block_size 64 m (the joint modes: a block as m consecutive 64-key
+    blocks with the block's weight; a last block reaching past the keys) and with fp16 inputs
+    (the fp32 kernels, output rounded to fp16), against the naive references at that block size
+    (benchmark_kernels_final.py:206-337 restated in the oracle), gradients included."""
+    print(f"fsa block sizes mode={mode} BS={BS} dtype={dtype}", flush=True)
+    from memory_amd import sparse_attention as SA
+    dev = gpu_device
+    g = gen(91 + mode + BS)
+    B, Tq, HQ, HK, S = 1, 48, 4, 2, 3
+    M = 5
+    Tk = M * BS - (64 if BS > 64 else 0)      # the last block is partial when BS > 64
+    q = torch.randn(B, Tq, HQ, 64, generator=g)
+    k = torch.randn(B, Tk, HK, 64, generator=g)
+    v = torch.randn(B, Tk, HK, 64, generator=g)
+    idx = torch.stack([torch.stack([torch.randperm(M, generator=g)[:S] for _ in range(HK)]) for _ in range(Tq)])
+    idx = idx.unsqueeze(0)                    # (B, Tq, HK, S)
+    w = None
+    if mode == 2:
+        w = torch.rand(B, Tq, HK, S, generator=g) + 0.05
+    elif mode in (0, 3):
+        w = torch.softmax(torch.randn(B, Tq, S, generator=g), -1)
+    dO = torch.randn(B, Tq, HQ, 64, generator=g)
+    scale = 0.125
+    # the reference over keys padded to M * BS with masked keys: zero keys would still take
+    # weight, so the padded rows get a large negative logit through -1e9 keys along one query dim
+    rq, rk, rv = (t.to(dtype).double().requires_grad_(True) for t in (q, k, v))
+    pad = M * BS - Tk
+    kp = torch.cat([rk, torch.zeros(B, pad, HK, 64, dtype=torch.float64)], 1) if pad else rk
+    vp = torch.cat([rv, torch.zeros(B, pad, HK, 64, dtype=torch.float64)], 1) if pad else rv
+    rw = None if w is None else w.double().requires_grad_(True)
+    if pad:
+        # a query that selects the partial block sees only its Tk - (M - 1) BS real keys: give the
+        # padding keys a logit of -inf by an extra query dimension (q . k_pad = -1e30)
+        qx = torch.cat([rq, torch.ones(B, Tq, HQ, 1, dtype=torch.float64)], -1)
+        kx = torch.cat([kp, torch.zeros(B, M * BS, HK, 1, dtype=torch.float64)], -1)
+        kx = kx.clone()
+        kx[:, Tk:, :, 64] = -1e30
+        vx = torch.cat([vp, torch.zeros(B, M * BS, HK, 1, dtype=torch.float64)], -1)
+    else:
+        qx, kx, vx = rq, kp, vp
+    f = REF[mode]
+    ref = f(qx, kx, vx, idx, BS, scale) if mode == 1 else f(qx, kx, vx, idx, rw, BS, scale)
+    ref = ref[..., :64]
+    (ref * dO.to(dtype).double()).sum().backward()
+    gq, gk, gv = (t.to(dev, dtype).requires_grad_(True) for t in (q, k, v))
+    gw = None if w is None else w.to(dev).requires_grad_(True)
+    kw = dict(softmax_scale=scale, disable_causal_mask=True)
+    idx_d = idx.to(dev, torch.int32)
+    if mode == 0:
+        out = SA.FSA_topk_sparse_attention_weighted_bthd(gq, gk, gv, idx_d, gw, BS, **kw)
+    elif mode == 3:
+        out = SA.FSA_topk_sparse_attention_weighted_joint_bias_bthd(gq, gk, gv, idx_d, gw, BS, **kw)
+    else:
+        out = SA.FSA_topk_sparse_attention_bthd(gq, gk, gv, idx_d, BS, block_weights_bths=gw, **kw)
+    assert out.dtype == dtype
+    (out.float() * dO.to(dev)).sum().backward()
+    chk = torch.bfloat16 if dtype == torch.float16 else dtype
+    assert_parity(out, ref, chk, "out")
+    assert_parity(gq.grad, rq.grad, chk, "dq")
+    assert_parity(gk.grad, rk.grad, chk, "dk")
+    assert_parity(gv.grad, rv.grad, chk, "dv")
+    if w is not None:
+        assert_parity(gw.grad, rw.grad, chk, "dw")
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
