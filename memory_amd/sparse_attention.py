@@ -13,8 +13,9 @@ Combine modes (see csrc/sparse_xattn.hip): 0 = exact per-chapter MoE
 (sum_s w_s softmax_s V_s); 1 = joint softmax over all selected keys;
 2 = joint softmax with block weights p ~ max(w, 0) e^s (v1-v3 block_weights_bths);
 3 = joint softmax with a log(max(w, 1e-20)) logit bias (v5).
-The kernels work on 64-key blocks (head_dim 64): block_size 64 for every mode, any multiple of
-64 for the joint modes; fp32, bf16, and fp16 through the fp32 kernels.
+The kernels work on 64-key blocks (head_dim 64); block sizes that are multiples of 64 are taken
+as consecutive 64-key blocks (the per-chapter MoE combine then one joint call per slot); fp32,
+bf16, and fp16 through the fp32 kernels.
 """
 
 from __future__ import annotations
@@ -224,10 +225,7 @@ class _FSAFunction(torch.autograd.Function):
         return dq, dk, dv, dw, None, None, None
 
 
-def _check_common(cu_seqlens_q, cu_seqlens_k, disable_causal_mask, block_size, joint: bool = True):
-    """``joint``: the combine is one softmax over every selected key (modes 1-3), so a block of
-    64 m keys may be taken as m consecutive 64-key blocks; the per-chapter MoE combine (mode 0)
-    needs block_size 64."""
+def _check_common(cu_seqlens_q, cu_seqlens_k, disable_causal_mask, block_size):
     if cu_seqlens_q is not None or cu_seqlens_k is not None:
         raise NotImplementedError("variable-length (cu_seqlens) inputs are not supported by the HIP kernels")
     if not disable_causal_mask:
@@ -235,11 +233,9 @@ def _check_common(cu_seqlens_q, cu_seqlens_k, disable_causal_mask, block_size, j
             "causal memory masking is not implemented; memory cross-attention is non-causal "
             "(MemoryCrossAttention passes disable_causal_mask=True, memory_attention.py:816)")
     bs = int(block_size)
-    if joint and (bs < BLOCK or bs % BLOCK != 0):
+    if bs < BLOCK or bs % BLOCK != 0:
         raise ValueError(f"block_size must be a multiple of {BLOCK} (the chapter tile of the HIP kernels), got "
                          f"{block_size}")
-    if not joint and bs != BLOCK:
-        raise ValueError(f"block_size must be {BLOCK} for the per-chapter (MoE) combine, got {block_size}")
 
 
 def _fsa(q, k, v, w, idx, mode: int, scale: float, block_size: int):
@@ -289,11 +285,24 @@ def FSA_topk_sparse_attention_bthd(q_bthd, k_bthd, v_bthd, block_indices_bths, b
 def FSA_topk_sparse_attention_weighted_bthd(q_bthd, k_bthd, v_bthd, block_indices_bths, chapter_weights_bts,
                                             block_size, softmax_scale=None, cu_seqlens_q=None, cu_seqlens_k=None,
                                             topk_idx_hns=None, assume_sorted_topk=False, disable_causal_mask=False):
-    """Exact per-chapter MoE combine: sum_s w_s softmax(q K_s^T) V_s (kernel_v4 semantics)."""
-    _check_common(cu_seqlens_q, cu_seqlens_k, disable_causal_mask, block_size, joint=False)
+    """Exact per-chapter MoE combine: sum_s w_s softmax(q K_s^T) V_s (kernel_v4 semantics).  At
+    block_size 64 m > 64 a block's softmax spans m 64-key blocks: each slot is then its own joint
+    softmax over its m sub-blocks (one call per slot, the reference's per-chapter calls of
+    memory_attention.py:640-707) and the slots are mixed by the weights."""
+    _check_common(cu_seqlens_q, cu_seqlens_k, disable_causal_mask, block_size)
     idx = _indices(block_indices_bths, topk_idx_hns, q_bthd)
     scale = float(softmax_scale) if softmax_scale is not None else q_bthd.shape[-1] ** -0.5
-    return _fsa(q_bthd, k_bthd, v_bthd, chapter_weights_bts, idx, 0, scale, block_size)
+    if int(block_size) == BLOCK:
+        return _fsa(q_bthd, k_bthd, v_bthd, chapter_weights_bts, idx, 0, scale, block_size)
+    w = chapter_weights_bts
+    out = None
+    for sl in range(idx.shape[-1]):
+        o = _fsa(q_bthd, k_bthd, v_bthd, None, idx[..., sl:sl + 1], 1, scale, block_size)
+        ws = w[..., sl]
+        ws = ws.unsqueeze(-1).unsqueeze(-1) if ws.dim() == 2 else ws.unsqueeze(-1)   # (B, T[, H]) -> broadcast
+        term = o.float() * ws.float()
+        out = term if out is None else out + term
+    return out.to(q_bthd.dtype)
 
 
 def FSA_topk_sparse_attention_weighted_joint_bias_bthd(q_bthd, k_bthd, v_bthd, block_indices_bths,

@@ -115,15 +115,16 @@ def test_fsa_rejects_unsupported(gpu_device):
     with pytest.raises(ValueError, match="block_size"):
         SA.FSA_topk_sparse_attention_bthd(q, k, k, idx, 32, disable_causal_mask=True)
     with pytest.raises(ValueError, match="block_size"):
-        SA.FSA_topk_sparse_attention_weighted_bthd(q, k, k, idx, torch.ones(1, 4, 1, device=dev), 128,
+        SA.FSA_topk_sparse_attention_weighted_bthd(q, k, k, idx, torch.ones(1, 4, 1, device=dev), 96,
                                                    disable_causal_mask=True)
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("mode,BS", [(1, 128), (2, 128), (3, 256), (1, 64), (0, 64), (3, 64)])
+@pytest.mark.parametrize("mode,BS", [(1, 128), (2, 128), (3, 256), (0, 128), (1, 64), (0, 64), (3, 64)])
 def test_fsa_block_sizes_and_fp16(gpu_device, dtype, mode, BS):
-    """The FSA entry points at block_size 64 m (the joint modes: a block as m consecutive 64-key
-    blocks with the block's weight; a last block reaching past the keys) and with fp16 inputs
+    """The FSA entry points at block_size 64 m (a block as m consecutive 64-key blocks with the
+    block's weight, the MoE combine one joint call per slot; a last block reaching past the
+    keys) and with fp16 inputs
     (the fp32 kernels, output rounded to fp16), against the naive references at that block size
     (benchmark_kernels_final.py:206-337 restated in the oracle), gradients included."""
     print(f"fsa block sizes mode={mode} BS={BS} dtype={dtype}", flush=True)
