@@ -299,8 +299,9 @@ class MemoryCrossAttentionWithRouting(nn.Module):
                 chapter_weights: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
         attn = self.attention
         T = int(self.tokens_per_chapter)
-        if T != CHAPTER_TOKENS:
-            raise ValueError(f"tokens_per_chapter must be {CHAPTER_TOKENS} for the HIP kernels, got {T}")
+        if T <= 0 or T % CHAPTER_TOKENS:
+            raise ValueError(f"tokens_per_chapter must be a positive multiple of {CHAPTER_TOKENS} for the HIP "
+                             f"kernels, got {T}")
         selected = self._select_chapters(memory, chapter_indices) if memory.dim() == 2 else memory
         if chapter_weights is None:
             return attn(hidden_states, selected)

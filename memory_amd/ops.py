@@ -897,10 +897,32 @@ def zeros_beside(shape, dtype: torch.dtype, dev: torch.device, workgroups: Optio
     return t, ev
 
 
+def sub_chapters(bank, omega, idx_star, num_chapters: int, tokens_per_chapter: int):
+    """Chapters of T = 64 m bank rows as m consecutive 64-row chapters (the kernels' chapter
+    tile): chapter c becomes sub-chapters m c .. m c + m - 1 with c's weight.  The joint softmax
+    over a sequence's selected keys, the keys' order and the gradients are unchanged (the
+    weight's gradient is the sum of its sub-chapters', by autograd of the repeat); ids outside
+    [0, C) stay outside [0, m C).  Returns (omega, idx_star, num_chapters) for T = 64."""
+    T = int(tokens_per_chapter)
+    if T <= 0 or T % 64:
+        raise ValueError(f"tokens_per_chapter must be a positive multiple of 64 for the HIP kernels, got {T}")
+    m = T // 64
+    if m == 1:
+        return omega, idx_star, int(num_chapters)
+    for attr in ("_moc_bank_opt", "_moc_row_grad"):
+        if getattr(bank, attr, None) is not None:
+            raise NotImplementedError(f"tokens_per_chapter {T}: a bank with row-sparse gradients or BankAdamW "
+                                      "needs 64-row chapters")
+    sub = torch.arange(m, device=idx_star.device, dtype=torch.int64)
+    idx = (idx_star.long().unsqueeze(-1) * m + sub).flatten(-2).to(idx_star.dtype)
+    return omega.repeat_interleave(m, dim=-1), idx, int(num_chapters) * m
+
+
 def routed_attention(q, bank, wk, wv, omega, idx_star, *, num_chapters: int, tokens_per_chapter: int,
                      norm_type: Optional[str] = None, eps: float = 1e-6, num_kv_heads: Optional[int] = None):
     HK = q.shape[2] if num_kv_heads is None else int(num_kv_heads)
-    return _RoutedAttention.apply(q, bank, wk, wv, omega, idx_star, int(num_chapters), int(tokens_per_chapter),
+    omega, idx_star, num_chapters = sub_chapters(bank, omega, idx_star, num_chapters, tokens_per_chapter)
+    return _RoutedAttention.apply(q, bank, wk, wv, omega, idx_star, int(num_chapters), 64,
                                   norm_code(norm_type), float(eps), HK)
 
 
@@ -912,7 +934,8 @@ def routed_attention_weights(q, bank, wk, wv, omega, idx_star, *, num_chapters: 
     (memory_attention.py:437-447 on the omega-weighted gathered memory): the forward's K and row
     log-sum-exp, then moc_xattn_weights."""
     HK = q.shape[2] if num_kv_heads is None else int(num_kv_heads)
-    T = int(tokens_per_chapter)
+    omega, idx_star, num_chapters = sub_chapters(bank, omega, idx_star, num_chapters, tokens_per_chapter)
+    T = 64
     _, saved, _ = routed_attn_forward(q, bank, wk, wv, omega, idx_star, int(num_chapters), T, norm_code(norm_type),
                                       float(eps), HK)
     qc, _, _, om, _, lse, kv, *_rest = saved

@@ -427,12 +427,26 @@ def token_routed_attention(q, routed_memory, wk, wv, idx, chapter_weights, *, to
     Dispatch mirrors the reference: weights given -> exact MoE combine (v1-v4),
     or the joint log-bias approximation when the version is v5; no weights ->
     joint softmax over the selected chapters."""
-    if int(tokens_per_chapter) != BLOCK:
-        raise ValueError(f"tokens_per_chapter must be {BLOCK} for the HIP kernels, got {tokens_per_chapter}")
+    T = int(tokens_per_chapter)
+    if T <= 0 or T % BLOCK:
+        raise ValueError(f"tokens_per_chapter must be a positive multiple of {BLOCK} for the HIP kernels, got {T}")
     HK = q.shape[2] if num_kv_heads is None else int(num_kv_heads)
     if chapter_weights is None:
         mode = 1
     else:
         mode = 3 if version == "v5" else 0
     w = None if chapter_weights is None else chapter_weights.float()
+    m = T // BLOCK
+    if m > 1:
+        # the joint combines (no weights, v5's log-bias) see a chapter of 64 m rows as m
+        # consecutive 64-row chapters with its weight; the per-chapter MoE combine would split
+        # its softmax, so it keeps 64-row chapters
+        if mode == 0:
+            raise NotImplementedError(f"tokens_per_chapter {T}: the per-chapter MoE combine (kernel versions "
+                                      "v1-v4 with chapter weights) needs 64-row chapters; v5 or no weights take "
+                                      "any multiple of 64")
+        sub = torch.arange(m, device=idx.device, dtype=torch.int64)
+        idx = (idx.long().unsqueeze(-1) * m + sub).flatten(-2).to(idx.dtype)
+        if w is not None:
+            w = w.repeat_interleave(m, dim=-1)
     return _TokenRouted.apply(q, routed_memory, wk, wv, w, idx, mode, HK)

@@ -157,10 +157,12 @@ def test_select_routed_chapters_from_probs_ties(dev):
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("weighted", [True, False])
 @pytest.mark.parametrize("routed_memory", [False, True])
-def test_memory_cross_attention_with_routing(dev, dtype, weighted, routed_memory):
+@pytest.mark.parametrize("T", [64, 128])
+def test_memory_cross_attention_with_routing(dev, dtype, weighted, routed_memory, T):
+    """T = 128: a chapter is two 64-row blocks (the weighted form one joint softmax per slot)."""
     from memory_amd.memory_attention import MemoryCrossAttentionWithRouting
-    print(f"with-routing dtype={dtype} weighted={weighted} routed_memory={routed_memory}", flush=True)
-    B, Lq, d, H, C, T, k = 2, 100, 256, 4, 17, 64, 3
+    print(f"with-routing dtype={dtype} weighted={weighted} routed_memory={routed_memory} T={T}", flush=True)
+    B, Lq, d, H, C, k = 2, 100, 256, 4, 17 if T == 64 else 9, 3
     g = gen(31)
     h = torch.randn(B, Lq, d, generator=g)
     bank = torch.randn(C * T, d, generator=g) * 0.5

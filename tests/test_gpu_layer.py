@@ -148,3 +148,54 @@ def test_native_stage_timing(gpu_device, monkeypatch):
     step()
     torch.cuda.synchronize()
     assert _lib.seq_stage_read() == {}
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("normalize", [False, True])
+def test_layer_128_token_chapters(gpu_device, dtype, normalize):
+    """tokens_per_chapter = 128: each chapter runs as two 64-row chapters carrying its weight
+    (ops.sub_chapters); selection, output and every gradient against the oracle's layer at
+    T = 128 (the router's omega gradient is the sum over the two halves)."""
+    from memory_amd.model import RoutedMemoryLayer
+    print(f"layer T=128 dtype={dtype} normalize={normalize}", flush=True)
+    dev = gpu_device
+    B, Lq, d, H, C, T, S, k, s = 2, 96, 256, 4, 17, 128, 1, 4, 2.5
+    g = torch.Generator().manual_seed(7)
+    h = torch.randn(B, Lq, d, generator=g)
+    bank = torch.randn(C * T, d, generator=g) * 0.5
+    Wr = torch.randn(C, d, generator=g) * 0.08
+    br = torch.zeros(C)
+    Wq, Wk, Wv, Wo = (torch.randn(d, d, generator=g) * 0.08 for _ in range(4))
+    layer = RoutedMemoryLayer(d, H, C, T, k, num_shared_chapters=S, routed_scaling_factor=s,
+                              normalize_shared_routed_before_mixing=normalize, shared_routed_norm_eps=1e-6,
+                              wo_init_zero=False)
+    with torch.no_grad():
+        layer.router.router.weight.copy_(Wr)
+        layer.router.router.bias.copy_(br)
+        for lin, W in zip((layer.memory_attn.q_proj, layer.memory_attn.k_proj, layer.memory_attn.v_proj,
+                           layer.memory_attn.o_proj), (Wq, Wk, Wv, Wo)):
+            lin.weight.copy_(W)
+    layer = layer.to(dev)
+    for m in (layer.memory_attn.q_proj, layer.memory_attn.k_proj, layer.memory_attn.v_proj, layer.memory_attn.o_proj):
+        m.to(dtype)
+    hg = h.to(dev, dtype).requires_grad_(True)
+    bg = bank.to(dev, dtype).requires_grad_(True)
+    out, _ = layer(hg, bg, return_losses=False)
+    dO = torch.randn(out.shape, generator=torch.Generator().manual_seed(8))
+    (out.float() * dO.to(dev)).sum().backward()
+
+    leaves = [t.double().clone().requires_grad_(True) for t in (h, bank, Wr, br, Wq, Wk, Wv, Wo)]
+    if dtype != torch.float32:
+        for i in (0, 1, 4, 5, 6, 7):
+            leaves[i] = leaves[i].detach().to(dtype).double().requires_grad_(True)
+    ref, det = O.sequence_memory_layer(*leaves, H=H, HK=H, C=C, T=T, S=S, top_k=k, routed_scale=s,
+                                       normalize=normalize, eps=1e-6, return_details=True)
+    (ref * dO.double()).sum().backward()
+    idx_star, _, _ = layer.route(hg.detach(), return_losses=False)
+    assert torch.equal(idx_star.cpu(), det["idx_star"])
+    assert_parity(out, ref, dtype, "out")
+    got = [hg.grad, bg.grad, layer.router.router.weight.grad, layer.router.router.bias.grad,
+           layer.memory_attn.q_proj.weight.grad, layer.memory_attn.k_proj.weight.grad,
+           layer.memory_attn.v_proj.weight.grad, layer.memory_attn.o_proj.weight.grad]
+    for n, gr, r in zip(["dh", "dbank", "dWr", "dbr", "dWq", "dWk", "dWv", "dWo"], got, leaves):
+        assert_parity(gr, r.grad, dtype, n)

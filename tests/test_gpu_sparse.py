@@ -190,7 +190,8 @@ def test_fsa_block_sizes_and_fp16(gpu_device, dtype, mode, BS):
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("weighted,version,shape", [(True, "v4", "dense"), (False, "v2", "dense"),
-                                                    (True, "v5", "dense"), (True, "v4", "sparse")])
+                                                    (True, "v5", "dense"), (True, "v4", "sparse"),
+                                                    (False, "v2", "dense128"), (True, "v5", "dense128")])
 def test_token_layer_matches_oracle(gpu_device, dtype, weighted, version, shape):
     """MemoryCrossAttention's token-routing path (shared dense + routed MoE) vs the oracle's
     token_memory_layer, including gradients of h, the bank and every projection.  "sparse":
@@ -202,7 +203,8 @@ def test_token_layer_matches_oracle(gpu_device, dtype, weighted, version, shape)
     from memory_amd.model import TokenRoutedMemoryLayer
     dev = gpu_device
     g = gen(55)
-    B, Lq, d, H, C, T, S, k = (2, 48, 128, 2, 9, 64, 1, 3) if shape == "dense" else (1, 4, 128, 2, 65, 64, 1, 2)
+    B, Lq, d, H, C, T, S, k = {"dense": (2, 48, 128, 2, 9, 64, 1, 3), "sparse": (1, 4, 128, 2, 65, 64, 1, 2),
+                               "dense128": (2, 48, 128, 2, 7, 128, 1, 3)}[shape]
     h = torch.randn(B, Lq, d, generator=g)
     bank = torch.randn(C * T, d, generator=g)
     Wr = torch.randn(C, d, generator=g) * 0.3
@@ -291,3 +293,20 @@ def test_zero_untouched_blocks(gpu_device, dtype, hk0, nhk):
         if c not in (0, 2, 4, 7):
             ref[c, :, :, hk0:hk0 + nhk, :] = 0
     assert torch.equal(got, ref)
+
+
+def test_token_path_moe_combine_needs_64_row_chapters(gpu_device):
+    """The per-chapter MoE combine (v1-v4 with weights) keeps 64-row chapters: a longer chapter
+    would split its softmax over sub-blocks, so it raises before any launch; the joint combines
+    take any multiple of 64, and other lengths raise."""
+    from memory_amd import sparse_attention as SA
+    dev = gpu_device
+    q = torch.zeros(1, 4, 2, 64, device=dev, dtype=torch.bfloat16)
+    mem = torch.zeros(256, 128, device=dev, dtype=torch.bfloat16)
+    w = torch.zeros(128, 128, device=dev, dtype=torch.bfloat16)
+    idx = torch.zeros(1, 4, 1, device=dev, dtype=torch.int32)
+    cw = torch.ones(1, 4, 1, device=dev)
+    with pytest.raises(NotImplementedError, match="64-row chapters"):
+        SA.token_routed_attention(q, mem, w, w, idx, cw, tokens_per_chapter=128, version="v4")
+    with pytest.raises(ValueError, match="multiple of 64"):
+        SA.token_routed_attention(q, mem, w, w, idx, None, tokens_per_chapter=96)
