@@ -15,7 +15,9 @@ Combine modes (see csrc/sparse_xattn.hip): 0 = exact per-chapter MoE
 3 = joint softmax with a log(max(w, 1e-20)) logit bias (v5).
 The kernels work on 64-key blocks (head_dim 64); block sizes that are multiples of 64 are taken
 as consecutive 64-key blocks (the per-chapter MoE combine then one joint call per slot); fp32,
-bf16, and fp16 through the fp32 kernels.
+bf16, and fp16 through the fp32 kernels.  Packed variable-length inputs (cu_seqlens_q /
+cu_seqlens_k) run as one batch row with global block ids when every sequence's keys start and
+end on a 64-key boundary.
 """
 
 from __future__ import annotations
@@ -226,8 +228,8 @@ class _FSAFunction(torch.autograd.Function):
 
 
 def _check_common(cu_seqlens_q, cu_seqlens_k, disable_causal_mask, block_size):
-    if cu_seqlens_q is not None or cu_seqlens_k is not None:
-        raise NotImplementedError("variable-length (cu_seqlens) inputs are not supported by the HIP kernels")
+    if (cu_seqlens_q is None) != (cu_seqlens_k is None):
+        raise ValueError("cu_seqlens_q and cu_seqlens_k are given together")
     if not disable_causal_mask:
         raise NotImplementedError(
             "causal memory masking is not implemented; memory cross-attention is non-causal "
@@ -258,6 +260,44 @@ def _fsa(q, k, v, w, idx, mode: int, scale: float, block_size: int):
     return out.to(torch.float16) if half else out
 
 
+def _varlen(q, k, v, idx, w, cu_q, cu_k, block_size):
+    """Packed variable-length inputs (kernel_v2.py:3181-3330): the B * Tq query rows and B * Tk
+    key rows hold sequences s = 0 .. n-1 at rows cu_q[s] .. cu_q[s+1] and cu_k[s] .. cu_k[s+1];
+    a query's block b is keys b BS .. b BS + BS - 1 of its own sequence, blocks past the
+    sequence skipped (a partial last block keeps the keys inside it).  When every sequence's
+    keys start on a 64-key boundary and count a multiple of 64, block b of sequence s is the
+    64-key blocks cu_k[s] / 64 + m b + j (j < m = BS / 64) of the packed keys that lie inside
+    the sequence: the packed tensors run as one batch row with those ids (-1: skipped).
+    Returns (q, k, v, ids (1, Nq, H, S m), weights repeated per sub-block or None)."""
+    B, Tq = q.shape[0], q.shape[1]
+    Nq, Nk = B * Tq, k.shape[0] * k.shape[1]
+    cq = cu_q.detach().to("cpu", torch.int64)
+    ck = cu_k.detach().to("cpu", torch.int64)
+    if cq.dim() != 1 or ck.shape != cq.shape or cq.numel() < 2:
+        raise ValueError("cu_seqlens_q / cu_seqlens_k must be 1-D of equal length n + 1")
+    if int(cq[0]) != 0 or int(ck[0]) != 0 or int(cq[-1]) != Nq or int(ck[-1]) != Nk:
+        raise ValueError(f"cu_seqlens must run from 0 to the packed lengths ({Nq} queries, {Nk} keys)")
+    if bool((cq[1:] < cq[:-1]).any()) or bool((ck[1:] < ck[:-1]).any()):
+        raise ValueError("cu_seqlens must be non-decreasing")
+    if bool((ck % BLOCK != 0).any()):
+        raise NotImplementedError(f"variable-length keys: every sequence's key rows must start and end on a "
+                                  f"{BLOCK}-row boundary (the chapter tile of the HIP kernels)")
+    m = int(block_size) // BLOCK
+    dev = idx.device
+    rows = torch.arange(Nq, device=dev)
+    seq = torch.bucketize(rows, cq[1:].to(dev), right=True)
+    kb0 = (ck.to(dev) // BLOCK)[seq]                                  # first 64-key block of the row's sequence
+    nkb = ((ck[1:] - ck[:-1]).to(dev) // BLOCK)[seq]                  # its 64-key blocks
+    ids = idx.reshape(Nq, idx.shape[2], idx.shape[3]).long()
+    sub = (ids.unsqueeze(-1) * m + torch.arange(m, device=dev)).flatten(-2)
+    ok = (ids.unsqueeze(-1) >= 0).expand(*ids.shape, m).flatten(-2) & (sub < nkb.view(Nq, 1, 1))
+    gid = torch.where(ok, sub + kb0.view(Nq, 1, 1), torch.full_like(sub, -1)).to(torch.int32)
+    if w is not None:
+        w = w.reshape(1, Nq, *w.shape[2:]).repeat_interleave(m, dim=-1)
+    return (q.reshape(1, Nq, *q.shape[2:]), k.reshape(1, Nk, *k.shape[2:]), v.reshape(1, Nk, *v.shape[2:]),
+            gid.unsqueeze(0), w)
+
+
 def _indices(block_indices_bths, topk_idx_hns, q):
     if block_indices_bths is not None:
         return block_indices_bths
@@ -279,7 +319,11 @@ def FSA_topk_sparse_attention_bthd(q_bthd, k_bthd, v_bthd, block_indices_bths, b
         H, N, S = topk_w_hns.shape
         w = topk_w_hns.permute(1, 0, 2).reshape(q_bthd.shape[0], q_bthd.shape[1], H, S)
     scale = float(softmax_scale) if softmax_scale is not None else q_bthd.shape[-1] ** -0.5
-    return _fsa(q_bthd, k_bthd, v_bthd, w, idx, 1 if w is None else 2, scale, block_size)
+    mode = 1 if w is None else 2
+    if cu_seqlens_q is not None:
+        q1, k1, v1, gid, w1 = _varlen(q_bthd, k_bthd, v_bthd, idx, w, cu_seqlens_q, cu_seqlens_k, block_size)
+        return _fsa(q1, k1, v1, w1, gid, mode, scale, BLOCK).reshape(q_bthd.shape)
+    return _fsa(q_bthd, k_bthd, v_bthd, w, idx, mode, scale, block_size)
 
 
 def FSA_topk_sparse_attention_weighted_bthd(q_bthd, k_bthd, v_bthd, block_indices_bths, chapter_weights_bts,
@@ -292,9 +336,23 @@ def FSA_topk_sparse_attention_weighted_bthd(q_bthd, k_bthd, v_bthd, block_indice
     _check_common(cu_seqlens_q, cu_seqlens_k, disable_causal_mask, block_size)
     idx = _indices(block_indices_bths, topk_idx_hns, q_bthd)
     scale = float(softmax_scale) if softmax_scale is not None else q_bthd.shape[-1] ** -0.5
-    if int(block_size) == BLOCK:
-        return _fsa(q_bthd, k_bthd, v_bthd, chapter_weights_bts, idx, 0, scale, block_size)
     w = chapter_weights_bts
+    m = int(block_size) // BLOCK
+    if cu_seqlens_q is not None:
+        q1, k1, v1, gid, _ = _varlen(q_bthd, k_bthd, v_bthd, idx, None, cu_seqlens_q, cu_seqlens_k, block_size)
+        w1 = w.reshape(1, q1.shape[1], *w.shape[2:])
+        if m == 1:
+            return _fsa(q1, k1, v1, w1, gid, 0, scale, BLOCK).reshape(q_bthd.shape)
+        out = None
+        for sl in range(idx.shape[-1]):
+            o = _fsa(q1, k1, v1, None, gid[..., sl * m:(sl + 1) * m], 1, scale, BLOCK)
+            ws = w1[..., sl]
+            ws = ws.unsqueeze(-1).unsqueeze(-1) if ws.dim() == 2 else ws.unsqueeze(-1)
+            term = o.float() * ws.float()
+            out = term if out is None else out + term
+        return out.to(q_bthd.dtype).reshape(q_bthd.shape)
+    if m == 1:
+        return _fsa(q_bthd, k_bthd, v_bthd, w, idx, 0, scale, block_size)
     out = None
     for sl in range(idx.shape[-1]):
         o = _fsa(q_bthd, k_bthd, v_bthd, None, idx[..., sl:sl + 1], 1, scale, block_size)
@@ -313,6 +371,10 @@ def FSA_topk_sparse_attention_weighted_joint_bias_bthd(q_bthd, k_bthd, v_bthd, b
     _check_common(cu_seqlens_q, cu_seqlens_k, disable_causal_mask, block_size)
     idx = _indices(block_indices_bths, topk_idx_hns, q_bthd)
     scale = float(softmax_scale) if softmax_scale is not None else q_bthd.shape[-1] ** -0.5
+    if cu_seqlens_q is not None:
+        q1, k1, v1, gid, w1 = _varlen(q_bthd, k_bthd, v_bthd, idx, chapter_weights_bts, cu_seqlens_q, cu_seqlens_k,
+                                      block_size)
+        return _fsa(q1, k1, v1, w1, gid, 3, scale, BLOCK).reshape(q_bthd.shape)
     return _fsa(q_bthd, k_bthd, v_bthd, chapter_weights_bts, idx, 3, scale, block_size)
 
 

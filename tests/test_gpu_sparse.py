@@ -310,3 +310,117 @@ def test_token_path_moe_combine_needs_64_row_chapters(gpu_device):
         SA.token_routed_attention(q, mem, w, w, idx, cw, tokens_per_chapter=128, version="v4")
     with pytest.raises(ValueError, match="multiple of 64"):
         SA.token_routed_attention(q, mem, w, w, idx, None, tokens_per_chapter=96)
+
+
+def _varlen_row_ref(mode, q, k, v, blocks, w, nb, BS, scale, HK):
+    """One query row of the FSA modes over its own sequence's keys, straight from the
+    definitions (float64): q (HQ, D); k, v (Nk_seq, HK, D); blocks (HK, S) local block ids, ids
+    outside [0, nb) skipped; w: (HK, S) block weights (mode 2), (S,) chapter weights (0, 3)."""
+    HQ = q.shape[0]
+    G = HQ // HK
+    outs = []
+    for h in range(HQ):
+        hk = h // G
+        ids = [int(b) for b in blocks[hk]]
+        if mode == 0:
+            o = torch.zeros_like(q[h])
+            for s_, b in enumerate(ids):
+                if 0 <= b < nb:
+                    kb, vb = k[b * BS:(b + 1) * BS, hk], v[b * BS:(b + 1) * BS, hk]
+                    o = o + w[s_] * torch.softmax(scale * kb @ q[h], 0) @ vb
+            outs.append(o)
+            continue
+        ks, vs, bias = [], [], []
+        for s_, b in enumerate(ids):
+            if 0 <= b < nb:
+                ks.append(k[b * BS:(b + 1) * BS, hk])
+                vs.append(v[b * BS:(b + 1) * BS, hk])
+                if mode == 2:
+                    bias.append(torch.log(w[hk, s_]).expand(BS))
+                elif mode == 3:
+                    bias.append(torch.log(torch.clamp(w[s_], min=1e-20)).expand(BS))
+        kk, vv = torch.cat(ks), torch.cat(vs)
+        z = scale * kk @ q[h]
+        if bias:
+            z = z + torch.cat(bias)
+        outs.append(torch.softmax(z, 0) @ vv)
+    return torch.stack(outs)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("mode,BS", [(1, 64), (2, 64), (0, 64), (3, 64), (1, 128), (0, 128), (3, 128)])
+def test_fsa_varlen(gpu_device, dtype, mode, BS):
+    """Packed variable-length inputs (cu_seqlens_q / cu_seqlens_k, kernel_v2.py:3181-3330): three
+    sequences of 5, 17 and 9 queries over 128, 384 and 256 keys in one batch row, block ids local
+    to each query's sequence; the first sequence names one block id past its keys in every row
+    (skipped: out of the joint softmax, no contribution to the MoE combine).  Against the
+    definitions evaluated row by row on each sequence alone (float64), gradients included."""
+    print(f"fsa varlen mode={mode} BS={BS} dtype={dtype}", flush=True)
+    from memory_amd import sparse_attention as SA
+    dev = gpu_device
+    g = gen(301 + mode + BS)
+    HQ, HK, S, D = 4, 2, 2, 64
+    lq, lk = [5, 17, 9], [128, 384, 256]
+    cq = torch.tensor([0, 5, 22, 31], dtype=torch.int32)
+    ck = torch.tensor([0, 128, 512, 768], dtype=torch.int32)
+    Nq, Nk = 31, 768
+    q = torch.randn(1, Nq, HQ, D, generator=g)
+    k = torch.randn(1, Nk, HK, D, generator=g)
+    v = torch.randn(1, Nk, HK, D, generator=g)
+    idx = torch.zeros(1, Nq, HK, S, dtype=torch.long)
+    for s_, (a, n, nk) in enumerate(zip(cq[:-1].tolist(), lq, lk)):
+        nb = nk // BS
+        for r in range(a, a + n):
+            for h in range(HK):
+                if s_ == 0:      # one valid block (< nb) and one id past the sequence
+                    idx[0, r, h] = torch.tensor([int(torch.randint(nb, (1,), generator=g)), nb + r % 2])
+                else:
+                    idx[0, r, h] = torch.randperm(nb, generator=g)[:S]
+    w = None
+    if mode == 2:
+        w = torch.rand(1, Nq, HK, S, generator=g) + 0.05
+    elif mode in (0, 3):
+        w = torch.softmax(torch.randn(1, Nq, S, generator=g), -1)
+    dO = torch.randn(1, Nq, HQ, D, generator=g)
+    scale = 0.125
+    rq, rk, rv = (t.to(dtype).double().requires_grad_(True) for t in (q, k, v))
+    rw = None if w is None else w.double().requires_grad_(True)
+    rows = []
+    for a, n, b0, nk in zip(cq[:-1].tolist(), lq, ck[:-1].tolist(), lk):
+        for r in range(a, a + n):
+            rows.append(_varlen_row_ref(mode, rq[0, r], rk[0, b0:b0 + nk], rv[0, b0:b0 + nk], idx[0, r],
+                                        None if rw is None else rw[0, r], nk // BS, BS, scale, HK))
+    ref = torch.stack(rows).unsqueeze(0)
+    (ref * dO.to(dtype).double()).sum().backward()
+    gq, gk, gv = (t.to(dev, dtype).requires_grad_(True) for t in (q, k, v))
+    gw = None if w is None else w.to(dev).requires_grad_(True)
+    kw = dict(softmax_scale=scale, disable_causal_mask=True, cu_seqlens_q=cq.to(dev), cu_seqlens_k=ck.to(dev))
+    idx_d = idx.to(dev, torch.int32)
+    if mode == 0:
+        out = SA.FSA_topk_sparse_attention_weighted_bthd(gq, gk, gv, idx_d, gw, BS, **kw)
+    elif mode == 3:
+        out = SA.FSA_topk_sparse_attention_weighted_joint_bias_bthd(gq, gk, gv, idx_d, gw, BS, **kw)
+    else:
+        out = SA.FSA_topk_sparse_attention_bthd(gq, gk, gv, idx_d, BS, block_weights_bths=gw, **kw)
+    (out.float() * dO.to(dev)).sum().backward()
+    assert_parity(out, ref, dtype, "out")
+    assert_parity(gq.grad, rq.grad, dtype, "dq")
+    assert_parity(gk.grad, rk.grad, dtype, "dk")
+    assert_parity(gv.grad, rv.grad, dtype, "dv")
+    if w is not None:
+        assert_parity(gw.grad, rw.grad, dtype, "dw")
+
+
+def test_fsa_varlen_rejects_unaligned_keys(gpu_device):
+    from memory_amd import sparse_attention as SA
+    dev = gpu_device
+    q = torch.randn(1, 4, 2, 64, device=dev)
+    k = torch.randn(1, 192, 2, 64, device=dev)
+    idx = torch.zeros(1, 4, 2, 1, dtype=torch.int32, device=dev)
+    cq = torch.tensor([0, 2, 4], dtype=torch.int32, device=dev)
+    with pytest.raises(NotImplementedError, match="boundary"):
+        SA.FSA_topk_sparse_attention_bthd(q, k, k, idx, 64, cu_seqlens_q=cq,
+                                          cu_seqlens_k=torch.tensor([0, 96, 192], dtype=torch.int32, device=dev),
+                                          disable_causal_mask=True)
+    with pytest.raises(ValueError, match="together"):
+        SA.FSA_topk_sparse_attention_bthd(q, k, k, idx, 64, cu_seqlens_q=cq, disable_causal_mask=True)

@@ -46,13 +46,14 @@ def test_loader_rejects_bad_version():
 
 
 def test_entry_points_reject_unsupported_arguments_before_any_launch():
-    """block sizes that are not a multiple of the 64-token chapter, cu_seqlens and a causal
-    memory mask raise on the host (no tensor is touched)."""
+    """block sizes that are not a multiple of the 64-token chapter, one of cu_seqlens_q /
+    cu_seqlens_k without the other and a causal memory mask raise on the host (no tensor is
+    touched)."""
     with pytest.raises(ValueError, match="block_size"):
         SA.FSA_topk_sparse_attention_weighted_bthd(None, None, None, None, None, 96, disable_causal_mask=True)
     with pytest.raises(ValueError, match="block_size"):
         SA.FSA_topk_sparse_attention_bthd(None, None, None, None, 32, disable_causal_mask=True)
-    with pytest.raises(NotImplementedError):
+    with pytest.raises(ValueError, match="together"):
         SA.FSA_topk_sparse_attention_bthd(None, None, None, None, 64, cu_seqlens_q=object(),
                                           disable_causal_mask=True)
     with pytest.raises(NotImplementedError):
