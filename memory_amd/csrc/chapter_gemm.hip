@@ -190,17 +190,14 @@ __global__ __launch_bounds__(kCgThreads) void chapter_gemm_kernel(
   const uint32_t xoff = (uint32_t)(srow * ldx * 2 + lchunk * 16);
   const uint32_t xbytes = (uint32_t)(64 * ldx * 2);
 
-  // the loads of stage s: tile lo + slot + nslot * (s / nk), k-stage s % nk, into buffer s % NBUF
-  auto issue_w = [&](int s) {
-    const int t = lo + slot + nslot * (s / nk), kt = s % nk;
-    const int nb = t % NB;
-    // (any N: the rows of the last feature block past N read zero)
-    const __amdgpu_buffer_rsrc_t wres = CG_RSRC(w + (int64_t)nb * BN * K, (uint32_t)(min(BN, N - nb * BN) * K * 2));
-    const char* dst = sW + (s % NBUF) * STW + wave * 1024;
-    // the row offset of instruction i rides in the per-lane offset, which the buffer bound checks
-#pragma unroll
-    for (int i = 0; i < FT; ++i) cg_dma16(wres, woff + (uint32_t)(64 * i * K * 2), (uint32_t)(kt * 128), dst + 8192 * i);
-  };
+  // Load cursor: the tile, k-stage and LDS buffer of the next stage whose loads go out, advanced
+  // one stage per issue.  The per-tile operands of the loads (the W block's buffer resource, the
+  // X rows' resources) are formed once per tile, so the instructions between a barrier and its
+  // DMAs are only the DMAs and their LDS addresses (the divisions and 64-bit address arithmetic
+  // per stage had cost ~180 scalar instructions there, with the matrix cores idle).
+  int ld_t = lo + slot, ld_kt = 0, ld_buf = 0;
+  __amdgpu_buffer_rsrc_t ld_w;
+  __amdgpu_buffer_rsrc_t ld_x[IPX];
   // gathered / per-edge X sources: looked up once per row block, and the workgroup's next tile's
   // a tile ahead of its first stage (plan lookups are dependent scalar loads: kept off the path
   // from a barrier to the DMAs that follow it)
@@ -212,10 +209,10 @@ __global__ __launch_bounds__(kCgThreads) void chapter_gemm_kernel(
     for (int i = 0; i < IPX; ++i)
       out[i] = cg_src_rows<SRC>(min(rb * CPT + i, nu - 1), x, xred, ldx, uniq, csr_off, csr_edge);
   };
-  auto issue_x = [&](int s) {
-    const int t = lo + slot + nslot * (s / nk), kt = s % nk;
-    const int rb = t / NB;
-    const char* dst = sX + (s % NBUF) * STX + wave * 1024;
+  auto ld_tile = [&]() {
+    const int t = ld_t, rb = t / NB, nb = t - rb * NB;
+    // (any N: the rows of the last feature block past N read zero)
+    ld_w = CG_RSRC(w + (int64_t)nb * BN * K, (uint32_t)(min(BN, N - nb * BN) * K * 2));
     if constexpr (SRC != CG_SRC_CONTIG) {
       if (rb != cur_rb) {
         if (rb == nxt_rb) {
@@ -237,8 +234,27 @@ __global__ __launch_bounds__(kCgThreads) void chapter_gemm_kernel(
       const int c = min(rb * CPT + i, nu - 1);  // rows of chapters past n_uniq: computed, not stored
       const bf16* xb = SRC == CG_SRC_CONTIG ? cg_src_rows<SRC>(c, x, xred, ldx, uniq, csr_off, csr_edge) : cur_src[i];
       // a contiguous source ends at row xrows: rows past it read zero
-      const uint32_t nb = SRC == CG_SRC_CONTIG ? (uint32_t)(min((int64_t)64, xrows - (int64_t)c * 64) * ldx * 2) : xbytes;
-      cg_dma16(CG_RSRC(xb, nb), xoff, (uint32_t)(kt * 128), dst + 8192 * i);
+      const uint32_t bytes = SRC == CG_SRC_CONTIG ? (uint32_t)(min((int64_t)64, xrows - (int64_t)c * 64) * ldx * 2) : xbytes;
+      ld_x[i] = CG_RSRC(xb, bytes);
+    }
+  };
+  ld_tile();
+  // the loads of the stage at the cursor (W rows, then X rows, into buffer ld_buf), then the
+  // cursor moves on; the row offset of instruction i rides in the per-lane offset, which the
+  // buffer bound checks
+  auto issue = [&]() {
+    const uint32_t so = (uint32_t)(ld_kt * 128);
+    const char* dw = sW + ld_buf * STW + wave * 1024;
+#pragma unroll
+    for (int i = 0; i < FT; ++i) cg_dma16(ld_w, woff + (uint32_t)(64 * i * K * 2), so, dw + 8192 * i);
+    const char* dx = sX + ld_buf * STX + wave * 1024;
+#pragma unroll
+    for (int i = 0; i < IPX; ++i) cg_dma16(ld_x[i], xoff, so, dx + 8192 * i);
+    ld_buf = ld_buf + 1 == NBUF ? 0 : ld_buf + 1;
+    if (++ld_kt == nk) {
+      ld_kt = 0;
+      ld_t += nslot;
+      if (ld_t < hi) ld_tile();
     }
   };
 
@@ -450,10 +466,7 @@ __global__ __launch_bounds__(kCgThreads) void chapter_gemm_kernel(
   // operations, so the next stage waits for everything instead.
 #pragma unroll
   for (int p = 0; p < DEPTH; ++p)
-    if (p < S) {
-      issue_w(p);
-      issue_x(p);
-    }
+    if (p < S) issue();
   // With one stage ahead, the wait for the next stage's loads is taken before a tile's epilogue
   // instead: the stage after it then needs no wait, and the stores are waited for one stage
   // later, when they have long completed.
@@ -464,10 +477,7 @@ __global__ __launch_bounds__(kCgThreads) void chapter_gemm_kernel(
     else if (!stored) cg_wait_vm(0);
     __syncthreads();  // every wave's loads of stage s landed; every wave is done with stage s-1
     __builtin_amdgcn_sched_barrier(0);
-    if (s + DEPTH < S) {
-      issue_w(s + DEPTH);
-      issue_x(s + DEPTH);
-    }
+    if (s + DEPTH < S) issue();
     __builtin_amdgcn_sched_barrier(0);
     compute(sW + (s % NBUF) * STW, sX + (s % NBUF) * STX);
     if constexpr (NORM != MOC_NORM_NONE) stats_stage(sX + (s % NBUF) * STX, kt == 0);
