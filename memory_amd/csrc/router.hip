@@ -449,6 +449,10 @@ __global__ __launch_bounds__(NT) void router_topk_kernel(
 // the row lives in the wave's registers (lane l holds c = l + 64 j), every reduction is across
 // lanes, and nothing waits on a workgroup barrier; a workgroup carries kWaveRows independent rows.
 constexpr int kWaveMaxE = 72;  // C <= 4,608
+// the kernels take E = ceil(C / 64) rounded up to one of these register-row lengths: rows of up
+// to 4,160 logits (4,097 chapters) in 65 registers per lane keep the top-k kernel at 157 VGPRs,
+// three waves per SIMD instead of two at 72
+constexpr int kWaveShortE = 65;
 constexpr int kWaveRows = 4;
 constexpr int kWaveBins = 1024;
 constexpr int kWaveCand = 128;
@@ -499,12 +503,13 @@ __device__ __forceinline__ int wave_opaque(int v) {
 
 // z[j] = row[lane + 64 j] for j < kWaveMaxE (-inf past C): buffer loads from a per-row resource,
 // one lane offset and constant column offsets (no 64-bit address per load)
-__device__ __forceinline__ void wave_load_row(const float* row, int C, int lane, float (&z)[kWaveMaxE]) {
+template <int E>
+__device__ __forceinline__ void wave_load_row(const float* row, int C, int lane, float (&z)[E]) {
   const __amdgpu_buffer_rsrc_t rs =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(row), (short)0, C * 4, 0x00020000);
   const int ln = wave_opaque(lane);   // keeps the 72 column predicates out of loops around the call
 #pragma unroll
-  for (int j = 0; j < kWaveMaxE; ++j) {
+  for (int j = 0; j < E; ++j) {
     const float v = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, lane * 4, 256 * j, 0));
     z[j] = ln + 64 * j < C ? v : -INFINITY;
   }
@@ -514,6 +519,7 @@ __device__ __forceinline__ void wave_load_row(const float* row, int C, int lane,
 // boundary bin's logits ranked exactly; key descending, chapter id ascending) within one wave.
 // A boundary bin with more than kWaveCand logits (plateaus of equal or near-equal values) is
 // resolved by repeated wave-wide maxima of (key, -id) over its logits, one selection each.
+template <int E>
 __global__ __launch_bounds__(64 * kWaveRows) void router_topk_wave_kernel(
     const float* __restrict__ logits, int64_t R, int64_t C, int S, int k, int32_t* __restrict__ idx_out,
     float* __restrict__ w_out, float* __restrict__ probs_out, float scale, int32_t* __restrict__ idx_star,
@@ -524,7 +530,7 @@ __global__ __launch_bounds__(64 * kWaveRows) void router_topk_wave_kernel(
   if (r >= R) return;
   WaveTopkLds& sm = lds_all[wv];
   const int Ci = (int)C;
-  float z[kWaveMaxE];
+  float z[E];
   wave_load_row(logits + r * C, Ci, lane, z);
 #pragma unroll
   for (int i = 0; i < kWaveBins / 64; ++i) sm.hist[lane * (kWaveBins / 64) + i] = 0;
@@ -533,7 +539,7 @@ __global__ __launch_bounds__(64 * kWaveRows) void router_topk_wave_kernel(
   float mxa = -INFINITY, hi = -INFINITY, lo = INFINITY;
   int ln = wave_opaque(lane);
 #pragma unroll
-  for (int j = 0; j < kWaveMaxE; ++j) {
+  for (int j = 0; j < E; ++j) {
     const int c = ln + 64 * j;
     const bool sel = c < Ci && c >= S;
     mxa = fmaxf(mxa, z[j]);
@@ -547,7 +553,7 @@ __global__ __launch_bounds__(64 * kWaveRows) void router_topk_wave_kernel(
   float s_all = 0.f, s_sel = 0.f;
   ln = wave_opaque(lane);
 #pragma unroll
-  for (int j = 0; j < kWaveMaxE; ++j) {
+  for (int j = 0; j < E; ++j) {
     const float e = __expf(z[j] - mxa);
     s_all += e;
     s_sel += ln + 64 * j >= S ? e : 0.f;
@@ -558,7 +564,7 @@ __global__ __launch_bounds__(64 * kWaveRows) void router_topk_wave_kernel(
   if (probs_out) {
     const __amdgpu_buffer_rsrc_t ps = __builtin_amdgcn_make_buffer_rsrc(probs_out + r * C, (short)0, Ci * 4, 0x00020000);
 #pragma unroll
-    for (int j = 0; j < kWaveMaxE; ++j)
+    for (int j = 0; j < E; ++j)
       __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(int, __expf(z[j] - mxa) / Z), ps, lane * 4, 256 * j, 0);
   }
 
@@ -577,7 +583,7 @@ __global__ __launch_bounds__(64 * kWaveRows) void router_topk_wave_kernel(
     {
       const int ln0 = wave_opaque(lane);
 #pragma unroll
-      for (int j = 0; j < kWaveMaxE; ++j) {
+      for (int j = 0; j < E; ++j) {
         const int c = ln0 + 64 * j;
         const bool cand = c < Ci && c >= S && z[j] >= t0;
         const uint64_t mc = __ballot(cand);
@@ -635,7 +641,7 @@ __global__ __launch_bounds__(64 * kWaveRows) void router_topk_wave_kernel(
   if (binned) {
     ln = wave_opaque(lane);
 #pragma unroll
-    for (int j = 0; j < kWaveMaxE; ++j) {
+    for (int j = 0; j < E; ++j) {
       const int c = ln + 64 * j;
       const bool sel = c < Ci && c >= S;
       atomicAdd(&sm.hist[sel ? bin_of(z[j]) : 0], sel ? 1 : 0);
@@ -673,7 +679,7 @@ __global__ __launch_bounds__(64 * kWaveRows) void router_topk_wave_kernel(
   float lo2 = lo, inv2 = inv;
   asm volatile("" : "+v"(lo2), "+v"(inv2));
 #pragma unroll
-  for (int j = 0; j < kWaveMaxE; ++j) {
+  for (int j = 0; j < E; ++j) {
     const int c = ln + 64 * j;
     const int b = binned ? min(kWaveBins - 1, (int)((z[j] - lo2) * inv2)) : 0;
     if (c < Ci && c >= S && b >= bstar) {
@@ -712,7 +718,7 @@ __global__ __launch_bounds__(64 * kWaveRows) void router_topk_wave_kernel(
       uint64_t best = 0;
       ln = wave_opaque(lane);
 #pragma unroll
-      for (int j = 0; j < kWaveMaxE; ++j) {
+      for (int j = 0; j < E; ++j) {
         const int c = ln + 64 * j;
         const uint64_t v = ((uint64_t)fkey(z[j]) << 32) | (uint32_t)~(uint32_t)c;
         const bool cand = c < Ci && c >= S && bin_of(z[j]) == bstar && v < last;
@@ -761,6 +767,7 @@ __global__ __launch_bounds__(64 * kWaveRows) void router_topk_wave_kernel(
 // dw_raw_i / D at c = idx_i, base = -A / D^2 (A = sum_i dw_raw_i q[idx_i]), and
 // sum_c dq_c q_c = base * msum + A / D (msum = sum_{c>=S} q), so dz = q (dq - that) needs no dense
 // dq: the row is stored with dq = base, then the k selected entries are rewritten.
+template <int E>
 __global__ __launch_bounds__(64 * kWaveRows) void router_topk_bwd_wave_kernel(
     const float* __restrict__ logits, const int32_t* __restrict__ idx, const float* __restrict__ dw_hat, int64_t R,
     int64_t C, int S, int k, const float* __restrict__ dz_in, float* __restrict__ dlogits) {
@@ -776,16 +783,16 @@ __global__ __launch_bounds__(64 * kWaveRows) void router_topk_bwd_wave_kernel(
     zi = row[ci];
   }
   const int Ci = (int)C;
-  float z[kWaveMaxE];
+  float z[E];
   wave_load_row(row, Ci, lane, z);
   float mxa = -INFINITY;
 #pragma unroll
-  for (int j = 0; j < kWaveMaxE; ++j) mxa = fmaxf(mxa, z[j]);
+  for (int j = 0; j < E; ++j) mxa = fmaxf(mxa, z[j]);
   mxa = wave_max(mxa);
   float s_all = 0.f, s_sel = 0.f;
   int ln = wave_opaque(lane);
 #pragma unroll
-  for (int j = 0; j < kWaveMaxE; ++j) {
+  for (int j = 0; j < E; ++j) {
     const float e = __expf(z[j] - mxa);  // 0 for the -inf padding
     s_all += e;
     s_sel += ln + 64 * j >= S ? e : 0.f;
@@ -813,7 +820,7 @@ __global__ __launch_bounds__(64 * kWaveRows) void router_topk_bwd_wave_kernel(
   const float iz = 1.f / Z;
   ln = wave_opaque(lane);
 #pragma unroll
-  for (int j = 0; j < kWaveMaxE; ++j) {
+  for (int j = 0; j < E; ++j) {
     const int c = ln + 64 * j;
     const float q = __expf(z[j] - mxa) * iz;
     const float dq = (S > 0 && c >= S) ? base : 0.f;
@@ -838,18 +845,18 @@ __global__ __launch_bounds__(64 * kWaveRows) void router_topk_bwd_wave_kernel(
 // router_topk_bwd_wave_kernel (same expressions, same order).
 constexpr int kPackWaveRows = 4;
 
-template <bool DIN>
+template <bool DIN, int E>
 __global__ __launch_bounds__(64 * kWaveRows) void router_topk_bwd_pack_kernel(
     const float* __restrict__ logits, const int32_t* __restrict__ idx, const float* __restrict__ dw_hat, int64_t R,
     int64_t C, int S, int k, const float* __restrict__ dz_in, int64_t Cp, bf16* __restrict__ dzp,
     float* __restrict__ part) {
-  __shared__ float fix_all[kWaveRows][64 * kWaveMaxE];
+  __shared__ float fix_all[kWaveRows][64 * E];
   const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   float* fix = fix_all[wv];
   const int Ci = (int)C, Cpi = (int)Cp;
-  float col[kWaveMaxE];
+  float col[E];
 #pragma unroll
-  for (int j = 0; j < kWaveMaxE; ++j) {
+  for (int j = 0; j < E; ++j) {
     col[j] = 0.f;
     fix[lane + 64 * j] = 0.f;
   }
@@ -865,16 +872,16 @@ __global__ __launch_bounds__(64 * kWaveRows) void router_topk_bwd_pack_kernel(
       g = dw_hat[r * k + lane];
       zi = row[ci];
     }
-    float z[kWaveMaxE];
+    float z[E];
     wave_load_row(row, Ci, lane, z);
     float mxa = -INFINITY;
 #pragma unroll
-    for (int j = 0; j < kWaveMaxE; ++j) mxa = fmaxf(mxa, z[j]);
+    for (int j = 0; j < E; ++j) mxa = fmaxf(mxa, z[j]);
     mxa = wave_max(mxa);
     float s_all = 0.f, s_sel = 0.f;
     int ln = wave_opaque(lane);
 #pragma unroll
-    for (int j = 0; j < kWaveMaxE; ++j) {
+    for (int j = 0; j < E; ++j) {
       const float e = __expf(z[j] - mxa);
       s_all += e;
       s_sel += ln + 64 * j >= S ? e : 0.f;
@@ -898,9 +905,9 @@ __global__ __launch_bounds__(64 * kWaveRows) void router_topk_bwd_pack_kernel(
     const float iz = 1.f / Z;
     ln = wave_opaque(lane);
     // with an incoming gradient, its row is read eight columns at a time ahead of their stores
-    constexpr int kChunk = DIN ? 8 : kWaveMaxE;
+    constexpr int kChunk = DIN ? 8 : E;
 #pragma unroll
-    for (int j0 = 0; j0 < kWaveMaxE; j0 += kChunk) {
+    for (int j0 = 0; j0 < E; j0 += kChunk) {
       float din[kChunk];
 #pragma unroll
       for (int jj = 0; jj < kChunk; ++jj) {
@@ -937,7 +944,7 @@ __global__ __launch_bounds__(64 * kWaveRows) void router_topk_bwd_pack_kernel(
   }
   // this wave's column sums into its LDS row, then the workgroup's rows in wave order
 #pragma unroll
-  for (int j = 0; j < kWaveMaxE; ++j) fix[lane + 64 * j] += col[j];
+  for (int j = 0; j < E; ++j) fix[lane + 64 * j] += col[j];
   __syncthreads();
   float* out = part + (int64_t)blockIdx.x * C;
   for (int c = threadIdx.x; c < Ci; c += 64 * kWaveRows) {
@@ -1838,8 +1845,12 @@ int moc_router_topk(const float* logits, int64_t R, int64_t C, int S, int k, int
   MOC_REQUIRE(C <= kMaxRouterC, MOC_ERR_UNSUPPORTED, "moc_router_topk: C=%lld exceeds %d", (long long)C, kMaxRouterC);
   if (R == 0) return MOC_OK;
   if (router_wave_rows(R, C, k)) {
-    hipLaunchKernelGGL(router_topk_wave_kernel, dim3((unsigned)((R + kWaveRows - 1) / kWaveRows)),
-                       dim3(64 * kWaveRows), 0, stream, logits, R, C, S, k, idx, w, probs, 0.f, nullptr, nullptr);
+    if (C <= 64 * kWaveShortE)
+      hipLaunchKernelGGL(router_topk_wave_kernel<kWaveShortE>, dim3((unsigned)((R + kWaveRows - 1) / kWaveRows)),
+                         dim3(64 * kWaveRows), 0, stream, logits, R, C, S, k, idx, w, probs, 0.f, nullptr, nullptr);
+    else
+      hipLaunchKernelGGL(router_topk_wave_kernel<kWaveMaxE>, dim3((unsigned)((R + kWaveRows - 1) / kWaveRows)),
+                         dim3(64 * kWaveRows), 0, stream, logits, R, C, S, k, idx, w, probs, 0.f, nullptr, nullptr);
     return check_launch("router_topk_wave_kernel");
   }
   const size_t lds = (size_t)C * sizeof(float);
@@ -1865,8 +1876,12 @@ int moc_router_topk_prepend(const float* logits, int64_t R, int64_t C, int S, in
               kMaxRouterC);
   if (R == 0) return MOC_OK;
   if (router_wave_rows(R, C, k)) {
-    hipLaunchKernelGGL(router_topk_wave_kernel, dim3((unsigned)((R + kWaveRows - 1) / kWaveRows)),
-                       dim3(64 * kWaveRows), 0, stream, logits, R, C, S, k, idx, w, nullptr, scale, idx_star, omega);
+    if (C <= 64 * kWaveShortE)
+      hipLaunchKernelGGL(router_topk_wave_kernel<kWaveShortE>, dim3((unsigned)((R + kWaveRows - 1) / kWaveRows)),
+                         dim3(64 * kWaveRows), 0, stream, logits, R, C, S, k, idx, w, nullptr, scale, idx_star, omega);
+    else
+      hipLaunchKernelGGL(router_topk_wave_kernel<kWaveMaxE>, dim3((unsigned)((R + kWaveRows - 1) / kWaveRows)),
+                         dim3(64 * kWaveRows), 0, stream, logits, R, C, S, k, idx, w, nullptr, scale, idx_star, omega);
     return check_launch("router_topk_wave_kernel(prepend)");
   }
   const size_t lds = (size_t)C * sizeof(float);
@@ -1888,8 +1903,12 @@ int moc_router_topk_bwd(const float* logits, const int32_t* idx, const float* dw
               kMaxRouterC / 2);
   if (R == 0) return MOC_OK;
   if (router_wave_rows(R, C, k)) {
-    hipLaunchKernelGGL(router_topk_bwd_wave_kernel, dim3((unsigned)((R + kWaveRows - 1) / kWaveRows)),
-                       dim3(64 * kWaveRows), 0, stream, logits, idx, dw, R, C, S, k, nullptr, dlogits);
+    if (C <= 64 * kWaveShortE)
+      hipLaunchKernelGGL(router_topk_bwd_wave_kernel<kWaveShortE>, dim3((unsigned)((R + kWaveRows - 1) / kWaveRows)),
+                         dim3(64 * kWaveRows), 0, stream, logits, idx, dw, R, C, S, k, nullptr, dlogits);
+    else
+      hipLaunchKernelGGL(router_topk_bwd_wave_kernel<kWaveMaxE>, dim3((unsigned)((R + kWaveRows - 1) / kWaveRows)),
+                         dim3(64 * kWaveRows), 0, stream, logits, idx, dw, R, C, S, k, nullptr, dlogits);
     return check_launch("router_topk_bwd_wave_kernel");
   }
   const size_t lds = 2 * (size_t)C * sizeof(float);
@@ -2185,10 +2204,10 @@ int moc_router_topk_bwd_pack(const float* logits, const int32_t* idx, const floa
   const int64_t per = (int64_t)kWaveRows * kPackWaveRows;
   const int nblk = (int)((R + per - 1) / per);
   if (dz_in)
-    hipLaunchKernelGGL(router_topk_bwd_pack_kernel<true>, dim3((unsigned)nblk), dim3(64 * kWaveRows), 0, stream,
+    hipLaunchKernelGGL((router_topk_bwd_pack_kernel<true, kWaveMaxE>), dim3((unsigned)nblk), dim3(64 * kWaveRows), 0, stream,
                        logits, idx, dw, R, C, S, k, dz_in, Cp, (bf16*)dzp, (float*)workspace);
   else
-    hipLaunchKernelGGL(router_topk_bwd_pack_kernel<false>, dim3((unsigned)nblk), dim3(64 * kWaveRows), 0, stream,
+    hipLaunchKernelGGL((router_topk_bwd_pack_kernel<false, kWaveMaxE>), dim3((unsigned)nblk), dim3(64 * kWaveRows), 0, stream,
                        logits, idx, dw, R, C, S, k, dz_in, Cp, (bf16*)dzp, (float*)workspace);
   if (int rc = check_launch("router_topk_bwd_pack_kernel")) return rc;
   hipLaunchKernelGGL(logit_grad_colsum_kernel, dim3((unsigned)((C + 63) / 64)), dim3(64 * kColsumWaves), 0, stream,
