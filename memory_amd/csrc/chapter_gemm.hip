@@ -548,6 +548,76 @@ __global__ __launch_bounds__(256) void dkv_multi_reduce_kernel(const bf16* __res
   }
 }
 
+// The multi-edge chapters of a plan as a list (moc_common.h): one 1,024-thread workgroup, slots
+// taken by an LDS counter, the count stored last.
+__global__ __launch_bounds__(1024) void dkv_multi_list_kernel(const int32_t* __restrict__ n_uniq,
+                                                              const int32_t* __restrict__ csr_off,
+                                                              const int32_t* __restrict__ csr_edge, int64_t max_u,
+                                                              int32_t* __restrict__ list) {
+  __shared__ int count;
+  if (threadIdx.x == 0) count = 0;
+  __syncthreads();
+  const int nu = (int)min((int64_t)n_uniq[0], max_u);
+  for (int u = threadIdx.x; u < nu; u += 1024) {
+    const int p0 = csr_off[u], cnt = csr_off[u + 1] - p0;
+    if (cnt != 1) {
+      int32_t* ent = list + 4 + kMultiEntry * atomicAdd(&count, 1);
+      ent[0] = u;
+      ent[1] = cnt;
+      ent[2] = p0;
+      ent[3] = 0;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) ent[4 + i] = i < cnt ? csr_edge[p0 + i] : -1;
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) list[0] = count;
+}
+
+// red[u] for the listed chapters: grid (16-byte slices of a chapter block / 256, groups); the
+// workgroup of group y sums its slice of entries y, y + groups, ...  The count and the first
+// entry are read together (one dependent load fewer than the scan of csr_off), each entry's rows
+// in flight together, fp32 sums in edge order, one rounding.
+__global__ __launch_bounds__(256) void dkv_multi_reduce_list_kernel(const bf16* __restrict__ dkv_edge,
+                                                                    const int32_t* __restrict__ list, int64_t max_u,
+                                                                    const int32_t* __restrict__ csr_edge,
+                                                                    int64_t row_elems, bf16* __restrict__ red) {
+  const int64_t nch = 64 * row_elems / 8;  // 16-byte chunks of one chapter block
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  typedef int i32x4 __attribute__((ext_vector_type(4)));
+  for (int k = blockIdx.y; k < max_u; k += gridDim.y) {
+    const i32x4* ent = reinterpret_cast<const i32x4*>(list + 4 + kMultiEntry * k);
+    const i32x4 h = ent[0], e0 = ent[1], e1 = ent[2];
+    if (k >= list[0]) break;
+    if (i >= nch) continue;
+    const int u = h[0], cnt = h[1], p0 = h[2];
+    float acc[8];
+#pragma unroll
+    for (int x = 0; x < 8; ++x) acc[x] = 0.f;
+    bf16x8 v[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int e = q < 4 ? e0[q] : e1[q - 4];
+      if (q < cnt) v[q] = *reinterpret_cast<const bf16x8*>(dkv_edge + ((size_t)e * 64 * row_elems + i * 8));
+    }
+#pragma unroll
+    for (int q = 0; q < 8; ++q)
+      if (q < cnt) {
+#pragma unroll
+        for (int x = 0; x < 8; ++x) acc[x] += (float)v[q][x];
+      }
+    for (int p = 8; p < cnt; ++p) {
+      const bf16x8 w = *reinterpret_cast<const bf16x8*>(dkv_edge + ((size_t)csr_edge[p0 + p] * 64 * row_elems + i * 8));
+#pragma unroll
+      for (int x = 0; x < 8; ++x) acc[x] += (float)w[x];
+    }
+    bf16x8 o;
+#pragma unroll
+    for (int x = 0; x < 8; ++x) o[x] = (bf16)acc[x];
+    *reinterpret_cast<bf16x8*>(red + (size_t)u * 64 * row_elems + i * 8) = o;
+  }
+}
+
 // [Wk; Wv] (rows kv of each, any of f32 / bf16) -> wkv [2 kv][d] bf16 and / or its transpose
 // wkv_t [d][2 kv] (either may be null).  One workgroup per 64 x 64 tile: 16-byte loads, the tile
 // kept in LDS as bf16 (rows padded to 72 elements), 16-byte stores of both layouts.  d and kv
@@ -1037,6 +1107,25 @@ int moc_chapter_wgrad(const void* dkv_edge, int64_t lda, const void* red, const 
 }  // extern "C"
 
 namespace moc {
+
+int dkv_multi_list(const int32_t* n_uniq, const int32_t* csr_off, const int32_t* csr_edge, int64_t max_u,
+                   int32_t* list, hipStream_t stream) {
+  MOC_REQUIRE(n_uniq && csr_off && csr_edge && list && ((uintptr_t)list & 15) == 0 && max_u >= 0, MOC_ERR_ARG,
+              "dkv_multi_list: null or unaligned pointer");
+  hipLaunchKernelGGL(dkv_multi_list_kernel, dim3(1), dim3(1024), 0, stream, n_uniq, csr_off, csr_edge, max_u, list);
+  return check_launch("dkv_multi_list_kernel");
+}
+
+int dkv_multi_reduce_list(const void* dkv_edge, int64_t ld, const int32_t* list, int64_t max_u,
+                          const int32_t* csr_edge, void* red, hipStream_t stream) {
+  MOC_REQUIRE(dkv_edge && list && csr_edge && red && ((uintptr_t)list & 15) == 0, MOC_ERR_ARG,
+              "dkv_multi_reduce_list: null or unaligned pointer");
+  MOC_REQUIRE(ld > 0 && ld % 8 == 0 && max_u >= 0, MOC_ERR_ARG, "dkv_multi_reduce_list: ld=%lld", (long long)ld);
+  if (max_u == 0) return MOC_OK;
+  hipLaunchKernelGGL(dkv_multi_reduce_list_kernel, dim3((unsigned)((64 * ld / 8 + 255) / 256), kMultiGroups), dim3(256),
+                     0, stream, (const bf16*)dkv_edge, list, max_u, csr_edge, ld, (bf16*)red);
+  return check_launch("dkv_multi_reduce_list_kernel");
+}
 
 int chapter_wgrad_budget(const void* dkv_edge, int64_t lda, const void* red, const void* x, int64_t ldx, int gather,
                          const int32_t* uniq, const int32_t* n_uniq, int64_t max_u, const int32_t* csr_off,

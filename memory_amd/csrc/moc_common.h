@@ -363,4 +363,17 @@ int chapter_wgrad_budget(const void* dkv_edge, int64_t lda, const void* red, con
                          const int32_t* csr_edge, int N, int K, void* ws, size_t ws_bytes, int out_dtype, void* dw,
                          int budget, hipStream_t stream);
 
+// The chapters of a plan with several edges (the shared chapter, collisions), listed once per
+// plan so that the per-chapter sums of their dK|dV rows need no scan of the inverted index:
+// list[0] = count, entry i at list + 4 + kMultiEntry i: (u, cnt, p0, 0, first 8 edge ids (-1
+// padded)).  dkv_multi_list: one workgroup (entries in any order; every sum below is fixed
+// order).  dkv_multi_reduce_list: red[u] = sum of the listed chapters' edge rows, as
+// moc_dkv_multi_reduce computes them (edges past the first 8 read from csr_edge + p0).
+constexpr int kMultiEntry = 12;
+inline size_t dkv_multi_list_bytes(int64_t max_u) { return (size_t)(4 + kMultiEntry * max_u) * 4; }
+int dkv_multi_list(const int32_t* n_uniq, const int32_t* csr_off, const int32_t* csr_edge, int64_t max_u,
+                   int32_t* list, hipStream_t stream);
+int dkv_multi_reduce_list(const void* dkv_edge, int64_t ld, const int32_t* list, int64_t max_u,
+                          const int32_t* csr_edge, void* red, hipStream_t stream);
+
 }  // namespace moc

@@ -137,6 +137,7 @@ struct SeqLayout {
   size_t q, attn, pooled, w, uniq, n_uniq, edge_u, csr_off, csr_edge, plan_ws, wkv, wkv_t, wq_t, wo_t, kv, lse;
   size_t plan_ws_bytes, saved_bytes;
   // scratch
+  size_t mlist;
   size_t d_attn, delta, dq, dkv_edge, dom_part, red, cw_ws, lw_ws, dz, dpooled, rl_ws;
   size_t cw_ws_bytes, lw_ws_bytes, rl_ws_bytes, scratch_bytes;
 
@@ -174,6 +175,7 @@ struct SeqLayout {
     wo_t = take((size_t)d * d * 2);
     kv = take((size_t)max_u * 64 * 2 * KV * 2);
     lse = take((size_t)B * H * Lp * 4);
+    mlist = take(dkv_multi_list_bytes(max_u));
     saved_bytes = o;
     o = 0;
     d_attn = take(tok * d * 2);
@@ -285,7 +287,6 @@ int moc_seq_layer_fwd(const void* h, const void* bank, const void* wr, int wr_dt
     SEQ_TRY(moc_weight_pack(wo, MOC_BF16, (const bf16*)wo + (d / 2) * d, MOC_BF16, d / 2, d, nullptr, sv + y.wo_t,
                             aux));
   });
-  MOC_HIP(hipEventRecord(ev[2], aux));
 
   // main: router, plan
   SEQ_STAGE(kStPool, main, SEQ_TRY(moc_router_pool1(h, MOC_BF16, B, L, d, coef, pooled, main)));
@@ -295,6 +296,12 @@ int moc_seq_layer_fwd(const void* h, const void* bank, const void* wr, int wr_dt
   SEQ_STAGE(kStPlan, main,
             SEQ_TRY(moc_chapter_plan(idx_star, y.E, C, sv + y.plan_ws, y.plan_ws_bytes, uniq, n_uniq, edge_u, csr_off,
                                      csr_edge, main)));
+  // aux: the plan's multi-edge chapters listed for the backward's per-chapter dK|dV sums (beside
+  // the projection; the list lives in the saved buffer)
+  MOC_HIP(hipEventRecord(ev[4], main));
+  MOC_HIP(hipStreamWaitEvent(aux, ev[4], 0));
+  SEQ_TRY(dkv_multi_list(n_uniq, csr_off, csr_edge, y.max_u, (int32_t*)(sv + y.mlist), aux));
+  MOC_HIP(hipEventRecord(ev[2], aux));
   // main: K/V projection (gather fused), attention, o_proj.  The projection waits for the [Wk; Wv]
   // pack only and the attention for the q projection: both events have completed when the main
   // stream reaches them, so the waits cost nothing (the q projection ends about when the router
@@ -420,7 +427,8 @@ int moc_seq_layer_bwd(const void* h, const void* bank, const void* wr, int wr_dt
   // main: K/V weight gradient and the projection's dX into the bank rows
   if (dbank || dwkv)
     SEQ_STAGE(kStMultiReduce, main,
-              SEQ_TRY(moc_dkv_multi_reduce(dkv_edge, KV2, n_uniq, y.max_u, csr_off, csr_edge, red, main)));
+              SEQ_TRY(dkv_multi_reduce_list(dkv_edge, KV2, (const int32_t*)(sv + y.mlist), y.max_u, csr_edge, red,
+                                            main)));
   if (dwkv)
     SEQ_STAGE(kStKVWgrad, main,
               SEQ_TRY(chapter_wgrad_budget(dkv_edge, KV2, red, bank, d, 1, uniq, n_uniq, y.max_u, csr_off, csr_edge,
