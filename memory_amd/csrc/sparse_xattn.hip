@@ -807,6 +807,15 @@ __device__ __forceinline__ bool unit_setup(UnitRows& ur, const int32_t* uniq, co
 // explicit vmcnt(0) below (the compiler's own waits cover only its loads; they stay correct since
 // waiting for an older load with newer DMAs outstanding only waits longer).
 typedef __attribute__((address_space(3))) void* unit_lds_ptr_t;
+// a value the compiler cannot see through, kept in a VGPR (a buffer load's offset, so that a
+// load of a uniform value still goes out as a vector load)
+__device__ __forceinline__ int wave_opaque_i(int v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t sp_rsrc(const void* p, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, bytes, 0x00020000);
+}
 __device__ __forceinline__ void unit_dma16(__amdgpu_buffer_rsrc_t r, uint32_t voff, const char* lds) {
   const uint32_t m0 = (uint32_t)(uintptr_t)(unit_lds_ptr_t)lds;
   asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(r), "{m0}"(m0) : "memory");
@@ -964,32 +973,56 @@ __global__ __launch_bounds__(64 * kBwdWaves) void sparse_bwd_unit_kernel(
   __shared__ float sLse[32], sDel[32], sWr[32], sPart[kBwdWaves][2][32];
   __shared__ int sEr[32];
   const int G = HQ / HK;
-  const int64_t unit = blockIdx.x;
-  const int u = (int)(unit / nhk);
-  if (u >= max_u) return;                 // whole workgroup (before any barrier)
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
-  // with a row table (the first 32 edges of every distinct chapter) the first block's edge ids
-  // are requested together with the plan entries: they depend on the unit only.  Per lane: the
-  // two rows its DMA instructions move (16 wave + 8 i + lane / 8) and the constants' row lane & 31
-  int tab_d[2] = {-1, -1}, tab_c = -1;
-  if (row_tab) {
-    const int32_t* tb = row_tab + (int64_t)u * 32;
-    tab_d[0] = tb[(16 * wave + (lane >> 3)) / G];
-    tab_d[1] = tb[(16 * wave + 8 + (lane >> 3)) / G];
-    tab_c = tb[(lane & 31) / G];
-  }
-  const int nu = n_uniq[0];
-  const int hk = hk0 + (int)(unit % nhk);
-  const int gid = uniq[u];
-  const int p0 = csr_off[u];
-  const int nrows = (csr_off[u + 1] - p0) * G;
-  if (u >= nu) return;
   const int key0 = 32 * wave;
-  const int64_t kv0 = (int64_t)gid * cs + (int64_t)hk * hs;
   // 16-byte LDS DMA geometry: an instruction fills 8 rows of 128 B; lane l -> row 8 i + l / 8,
   // physical chunk l % 8, which holds logical chunk (l % 8) ^ (row & 7) of Tile::off
   const int dlc = (lane & 7) ^ (lane >> 3);
+  // units of the plan's distinct chapters; the workgroups walk them persistently (unit, + grid, ...)
+  const int64_t lim = min((int64_t)n_uniq[0], max_u) * nhk;
+  // A unit's plan entries and, with a row table (the first 32 edges of every distinct chapter),
+  // its first block's edge ids, requested one unit ahead -- right after the current unit's first
+  // wait -- so that a unit's first loads depend on nothing still in flight.  They go out as
+  // vector loads (counted in vmcnt, which the unit's DMA wait covers anyway) rather than scalar
+  // loads, whose lgkmcnt the waits on LDS reads share.  Per lane: the two rows its DMA
+  // instructions move (16 wave + 8 i + lane / 8) and the constants' row lane & 31.
+  struct Ahead {
+    int gid, p0, p1, d0, d1, c;
+  };
+  auto request = [&](int64_t unit) {
+    Ahead a{0, 0, 0, -1, -1, -1};
+    if (unit < lim) {
+      const int u = (int)(unit / nhk);
+      const int z = wave_opaque_i(0);
+      a.gid = __builtin_amdgcn_raw_buffer_load_b32(sp_rsrc(uniq + u, 4), z, 0, 0);
+      a.p0 = __builtin_amdgcn_raw_buffer_load_b32(sp_rsrc(csr_off + u, 8), z, 0, 0);
+      a.p1 = __builtin_amdgcn_raw_buffer_load_b32(sp_rsrc(csr_off + u, 8), z, 4, 0);
+      if (row_tab) {
+        const int32_t* tb = row_tab + (int64_t)u * 32;
+        a.d0 = tb[(16 * wave + (lane >> 3)) / G];
+        a.d1 = tb[(16 * wave + 8 + (lane >> 3)) / G];
+        a.c = tb[(lane & 31) / G];
+      }
+    }
+    return a;
+  };
+  // the rows of a block (q, dO) go to LDS by DMA, wave w moving rows 16 w .. 16 w + 15; rows past
+  // the unit's read from an offset past the buffer, i.e. zeros.  The per-row constants (wave 0,
+  // one lane per row) are loaded into registers and staged at the block's start.
+  const __amdgpu_buffer_rsrc_t qr = __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16*>(q), (short)0, (int)qbytes,
+                                                                      0x00020000);
+  const __amdgpu_buffer_rsrc_t dr = __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16*>(dout), (short)0,
+                                                                      (int)qbytes, 0x00020000);
+  Ahead cur = request(blockIdx.x), nxt = cur;
+  for (int64_t unit = blockIdx.x; unit < lim; unit += gridDim.x) {
+  const int hk = hk0 + (int)(unit % nhk);
+  const int gid = __builtin_amdgcn_readfirstlane(cur.gid);
+  const int p0 = __builtin_amdgcn_readfirstlane(cur.p0);
+  const int nrows = (__builtin_amdgcn_readfirstlane(cur.p1) - p0) * G;
+  const int tab_d[2] = {cur.d0, cur.d1}, tab_c = cur.c;
+  const int64_t kv0 = (int64_t)gid * cs + (int64_t)hk * hs;
+  __syncthreads();   // the previous unit's dK / dV rows (staged in sK / sV) have been read back
   {
     // K and V tiles -> LDS (K the B operand of S and, transposed, of dQ; V the B operand of dPu):
     // wave w moves keys 32 w .. 32 w + 31 of each
@@ -1012,13 +1045,6 @@ __global__ __launch_bounds__(64 * kBwdWaves) void sparse_bwd_unit_kernel(
       dkt[db][j] = f32x4{0.f, 0.f, 0.f, 0.f};
       dvt[db][j] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
-  // the rows of a block (q, dO) go to LDS by DMA, wave w moving rows 16 w .. 16 w + 15; rows past
-  // the unit's read from an offset past the buffer, i.e. zeros.  The per-row constants (wave 0,
-  // one lane per row) are loaded into registers and staged at the block's start.
-  const __amdgpu_buffer_rsrc_t qr = __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16*>(q), (short)0, (int)qbytes,
-                                                                      0x00020000);
-  const __amdgpu_buffer_rsrc_t dr = __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16*>(dout), (short)0,
-                                                                      (int)qbytes, 0x00020000);
   float c_lse = INFINITY, c_del = 0.f, c_w = 0.f;
   int c_er = -1;
   auto fetch_rows = [&](int r0) {
@@ -1064,6 +1090,7 @@ __global__ __launch_bounds__(64 * kBwdWaves) void sparse_bwd_unit_kernel(
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // this wave's DMA (K at the first block, the rows)
     __syncthreads();   // (1) rows, K and the constants visible to both waves
+    if (r0 == 0) nxt = request(unit + gridDim.x);
     // ---- S and dPu for this wave's keys (lane = key, rows 16 qb + 4 g + x)
     f32x4 sc[2][2], dp[2][2];
 #pragma unroll
@@ -1269,6 +1296,8 @@ __global__ __launch_bounds__(64 * kBwdWaves) void sparse_bwd_unit_kernel(
     *reinterpret_cast<bf16x8*>(dkb + off) = *reinterpret_cast<const bf16x8*>(sK + Tile::off(key, 8 * ch));
     *reinterpret_cast<bf16x8*>(dvb + off) = *reinterpret_cast<const bf16x8*>(sV + Tile::off(key, 8 * ch));
   }
+  cur = nxt;
+  }
 }
 
 // dK / dV blocks (chapter, kv head) that no edge of a plan touched: the sparse backward
@@ -1310,6 +1339,21 @@ __global__ __launch_bounds__(256) void zero_untouched_kernel(T* __restrict__ dk,
 using namespace moc;
 
 namespace {
+// compute units of the current device (cached)
+int sp_cus() {
+  static int cus = 0;
+  if (cus == 0) {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
+      cus = n;
+    else
+      cus = 256;
+  }
+  return cus;
+}
+// workgroups per CU of the persistent sparse backward (its LDS and registers hold four)
+constexpr int kBwdPerCU = 4;
 // 16-byte K/V/q fragment loads of the one-wave-per-unit kernels
 bool unit_kv_aligned(const void* q, const void* k, const void* v, int64_t cs, int64_t hs, int64_t rs) {
   return ((uintptr_t)q & 15) == 0 && ((uintptr_t)k & 15) == 0 && ((uintptr_t)v & 15) == 0 && cs % 8 == 0 &&
@@ -1435,7 +1479,8 @@ int moc_sparse_bwd(int dtype, const void* q, const void* dout, int64_t ntok, int
     MOC_REQUIRE(qbytes < ((int64_t)1 << 32) - 16, MOC_ERR_UNSUPPORTED,
                 "moc_sparse_bwd: q / dout of %lld bytes (bf16 needs < 4 GiB)", (long long)qbytes);
     const int64_t units = max_u * nhk;
-    hipLaunchKernelGGL(sparse_bwd_unit_kernel, dim3((unsigned)units), dim3(64 * kBwdWaves), 0, stream, (const bf16*)q, (const bf16*)dout, HQ, (const bf16*)k,
+    const int64_t wgs = min(units, (int64_t)kBwdPerCU * sp_cus());
+    hipLaunchKernelGGL(sparse_bwd_unit_kernel, dim3((unsigned)wgs), dim3(64 * kBwdWaves), 0, stream, (const bf16*)q, (const bf16*)dout, HQ, (const bf16*)k,
                        (const bf16*)v, cs, hs, rs, HK, uniq, n_uniq, csr_off, csr_edge, max_u, S, hk0, nhk, hq_off,
                        rpe, mode, lse_row, delta_row, w, sl2, scale, (bf16*)dk, (bf16*)dv, ocs, ohs, ors,
                        (bf16*)dq_part, dlog, row_tab, (uint32_t)qbytes);
