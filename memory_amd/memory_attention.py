@@ -30,6 +30,7 @@ import torch.nn as nn
 
 from . import ops
 from .token_routing_kernel import normalize_kernel_version
+from ._half import float16_via_float32
 
 try:
     from torch.utils.checkpoint import checkpoint as torch_checkpoint
@@ -172,6 +173,7 @@ class MemoryCrossAttention(nn.Module):
                                             num_kv_heads=self.num_kv_heads)
 
     # ------------------------------------------------------------------ forward
+    @float16_via_float32
     def forward(self, hidden_states: torch.Tensor, memory: Optional[torch.Tensor] = None,
                 token_routing_state: Optional[Dict[str, Any]] = None, token_routing_kernel_version: str = "v2",
                 return_attn_weights: bool = False,
@@ -295,6 +297,7 @@ class MemoryCrossAttentionWithRouting(nn.Module):
                 + torch.arange(T, device=chapter_indices.device).view(1, 1, T)).reshape(B, k * T)
         return memory[rows]
 
+    @float16_via_float32
     def forward(self, hidden_states: torch.Tensor, memory: torch.Tensor, chapter_indices: torch.Tensor,
                 chapter_weights: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
         attn = self.attention

@@ -21,6 +21,7 @@ import torch.nn as nn
 
 from . import ops
 from .memory_attention import MemoryCrossAttention
+from ._half import float16_via_float32
 
 
 class RMSNorm(nn.Module):
@@ -58,6 +59,7 @@ class MemorySublayer(nn.Module):
         # (ops.norm_linear_supported); False runs the norm kernel ahead of the projection
         self.fuse_norm = True
 
+    @float16_via_float32
     def forward(self, hidden_states: torch.Tensor, memory: Optional[torch.Tensor] = None,
                 token_routing_state: Optional[Dict[str, Any]] = None, token_routing_kernel_version: str = "v2",
                 routed_memory_state: Optional[Dict[str, Any]] = None) -> torch.Tensor:

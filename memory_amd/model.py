@@ -25,6 +25,7 @@ import torch.nn.functional as F
 from . import ops, seq_layer
 from .memory_attention import MemoryCrossAttention
 from .router import ChapterRouter, compute_router_losses, rolling_coefficients
+from ._half import float16_via_float32
 
 
 def select_routed_chapters_from_probs(probs: torch.Tensor, top_k: int, num_shared_chapters: int):
@@ -203,6 +204,7 @@ class RoutedMemoryLayer(nn.Module):
             routed_scale=self.routed_scaling_factor, num_heads=attn.num_heads, num_kv_heads=attn.num_kv_heads,
             norm_type=self.norm_type if normalize else None, eps=self.norm_eps, coef=coef)
 
+    @float16_via_float32
     def forward(self, hidden_states: torch.Tensor, bank: torch.Tensor,
                 return_losses: bool = True) -> Tuple[torch.Tensor, Dict[str, torch.Tensor]]:
         fused = self._fused(hidden_states, bank)
@@ -247,6 +249,7 @@ class TokenRoutedMemoryLayer(nn.Module):
         self.router = ChapterRouter(hidden_dim, num_chapters, top_k, "token")
         self.memory_attn = MemoryCrossAttention(hidden_dim, num_heads, num_kv_heads, wo_init_zero=wo_init_zero)
 
+    @float16_via_float32
     def forward(self, hidden_states: torch.Tensor, bank: torch.Tensor,
                 return_losses: bool = True) -> Tuple[torch.Tensor, Dict[str, torch.Tensor]]:
         S, T = self.num_shared_chapters, self.tokens_per_chapter

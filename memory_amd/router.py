@@ -18,6 +18,7 @@ import torch
 import torch.nn as nn
 
 from . import ops
+from ._half import float16_via_float32
 
 
 @functools.lru_cache(maxsize=64)
@@ -84,6 +85,7 @@ class ChapterRouter(nn.Module):
         return ops.router_linear(pooled, self.router.weight, self.router.bias)
 
     # -- forward --------------------------------------------------------------
+    @float16_via_float32
     def forward(self, hidden_states: torch.Tensor, return_losses: bool = True, exclude_prefix_chapters: int = 0,
                 rolling_window_size: Optional[int] = None) -> Tuple[torch.Tensor, torch.Tensor, Dict[str, torch.Tensor]]:
         idx, w, losses = self.route_ids32(hidden_states, return_losses, exclude_prefix_chapters, rolling_window_size)
