@@ -1,7 +1,7 @@
 """float16 modules on the float32 kernels.
 
-The kernels compute in float32 or bfloat16.  A module whose forward gets float16 tensors, or
-whose parameters are float16, runs that forward on float32 copies of them (an exact widening,
+The kernels compute in float32 or bfloat16.  A module whose forward gets float16 tensors runs
+that forward on float32 copies of them and of its float16 parameters (an exact widening,
 differentiable, so the gradients reach the float16 tensors) and rounds its float32 tensor
 results back to float16 -- the float16 path of the reference's torch modules, computed at
 float32 precision in between.
@@ -45,9 +45,10 @@ def float16_via_float32(forward):
 
     @functools.wraps(forward)
     def run(self, *args, **kwargs):
-        if getattr(self, "_moc_widened", False):
-            return forward(self, *args, **kwargs)
-        if not (_any_half((args, kwargs)) or any(p.dtype == torch.float16 for p in self.parameters())):
+        # float16 is recognised by the inputs (a float16 module called with float32 or bfloat16
+        # tensors fails on their dtypes, as the torch modules do), which keeps the check off the
+        # parameters on every call
+        if getattr(self, "_moc_widened", False) or not _any_half((args, kwargs)):
             return forward(self, *args, **kwargs)
         wide = {n: (p.float() if p.dtype == torch.float16 else p) for n, p in self.named_parameters()}
         self._moc_widened = True
