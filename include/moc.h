@@ -383,6 +383,15 @@ int moc_xattn_bwd_dq(int dtype, const void* q, const void* k_tiles, const void* 
                      int64_t su, int sh, int st, const int32_t* slot_u, const float* omega, const void* dout, const float* lse,
                      const float* delta, int64_t B, int64_t L, int H, int HK, int Dh, int T, int NS, float scale,
                      void* dq, hipStream_t stream);
+/* moc_xattn_bwd_dq with the prep's delta fused in: out [B, L, H, Dh] (dtype) is the forward's
+ * output; delta f32 [B, H, Lp] = rowsum(dout * out) is written (padded rows 0) for
+ * moc_xattn_bwd_dkv, from the dout rows the dq kernel reads anyway, so moc_xattn_bwd_prep is not
+ * needed.  Same reference interface as prep + dq (the FlashAttention-style backward pre-pass and dQ
+ * of memory_transformer/memory_attention.py:301-316's autograd). */
+int moc_xattn_bwd_dq_delta(int dtype, const void* q, const void* k_tiles, const void* v_tiles, int64_t kv_span,
+                           int64_t su, int sh, int st, const int32_t* slot_u, const float* omega, const void* out,
+                           const void* dout, const float* lse, float* delta, int64_t B, int64_t L, int H, int HK, int Dh,
+                           int T, int NS, float scale, void* dq, hipStream_t stream);
 /* dK/dV per edge (edge e = b * NS + slot): dkv_edge [B * NS * T][2 * HK * Dh] (dtype) holds for
  * the chapter in slot `slot` of sequence b the rows [dL/dk (all kv heads) | dL/dv], where
  * dL/dk, dL/dv are gradients w.r.t. the unweighted projected keys/values (omega folded in).

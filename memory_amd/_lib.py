@@ -86,6 +86,8 @@ _SIGS = {
     "moc_xattn_bwd_prep": (_I, [_I, _P, _P, _P, _I64, _I64, _I, _I, _P, _P, _P, _P]),
     "moc_xattn_bwd_dq": (_I, [_I, _P, _P, _P, _I64, _I64, _I, _I, _P, _P, _P, _P, _P, _I64, _I64, _I, _I, _I, _I,
                               _I, _F, _P, _P]),
+    "moc_xattn_bwd_dq_delta": (_I, [_I, _P, _P, _P, _I64, _I64, _I, _I, _P, _P, _P, _P, _P, _P, _I64, _I64, _I, _I,
+                                    _I, _I, _I, _F, _P, _P]),
     "moc_xattn_bwd_dkv": (_I, [_I, _P, _P, _P, _P, _I64, _I64, _I, _I, _P, _P, _P, _P, _I64, _I64, _I, _I, _I, _I,
                                _I, _F, _P, _P, _P]),
     "moc_kv_wgrad_workspace": (_SZ, [_I64, _I64, _I64]),

@@ -13,7 +13,7 @@
 //                 attention -> o_proj
 //           aux:  q projection and the weight packs ([Wk; Wv], [Wk; Wv]^T, Wq^T, Wo^T), which do
 //                 not depend on the routing, beside the latency-bound router launches
-// backward  main: o_proj dX -> bwd prep -> dQ -> dK/dV -> multi-edge sums -> K/V weight gradient
+// backward  main: o_proj dX -> dQ (+ delta) -> dK/dV -> multi-edge sums -> K/V weight gradient
 //                 -> dX of the projection into the chapters' bank rows
 //           aux:  o_proj dW (beside dX / dQ); after dQ: q_proj dX (into dh, beside dK/dV); after
 //                 dK/dV: the router backward and the pooling's gradient added into dh
@@ -95,12 +95,12 @@ const char* const kStageNames[] = {
     "moc_router_pool1", "moc_router_linear", "moc_router_topk_prepend", "moc_chapter_plan",
     "moc_weight_pack:wkv", "moc_rows_linear:q_proj", "moc_weight_pack:transposed", "moc_chapter_project",
     "moc_xattn_fwd", "moc_rows_linear:o_proj", "moc_linear_wgrad:o_proj", "moc_rows_linear:o_proj_dx",
-    "moc_xattn_bwd_prep", "moc_fill_zero:dbank", "moc_xattn_bwd_dq", "moc_rows_linear:q_proj_dx",
+    "moc_fill_zero:dbank", "moc_xattn_bwd_dq", "moc_rows_linear:q_proj_dx",
     "moc_linear_wgrad:q_proj", "moc_xattn_bwd_dkv", "moc_router_seq_bwd+linear_bwd+pool_bwd",
     "moc_dkv_multi_reduce", "moc_chapter_wgrad", "moc_chapter_dx"};
 enum Stage {
   kStPool, kStRouterLinear, kStTopk, kStPlan, kStPackWkv, kStQProj, kStPackT, kStKVProj, kStAttnFwd, kStOProj,
-  kStOWgrad, kStODx, kStPrep, kStFill, kStDq, kStQDx, kStQWgrad, kStDkv, kStRouterBwd, kStMultiReduce, kStKVWgrad,
+  kStOWgrad, kStODx, kStFill, kStDq, kStQDx, kStQWgrad, kStDkv, kStRouterBwd, kStMultiReduce, kStKVWgrad,
   kStBankDx, kNumStages
 };
 static_assert(sizeof(kStageNames) / sizeof(kStageNames[0]) == kNumStages, "stage names");
@@ -373,22 +373,22 @@ int moc_seq_layer_bwd(const void* h, const void* bank, const void* wr, int wr_dt
               SEQ_TRY(moc_linear_wgrad(dout, attn, MOC_BF16, tok, d, d, sc + y.lw_ws, y.lw_ws_bytes, MOC_BF16, dwo,
                                        aux)));
   MOC_HIP(hipEventRecord(ev[6], aux));  // the weight-gradient workspace is free again
-  // main: o_proj dX, backward prep, dQ
+  // main: o_proj dX, dQ (with the backward pre-pass's row sums delta, which dK/dV reads)
   SEQ_STAGE(kStODx, main, SEQ_TRY(moc_rows_linear(dout, d, tok, sv + y.wo_t, (int)d, (int)d, d_attn, d, main)));
-  SEQ_STAGE(kStPrep, main,
-            SEQ_TRY(moc_xattn_bwd_prep(MOC_BF16, q, attn, d_attn, B, L, H, 64, delta, nullptr, nullptr, main)));
-  // fill: the dense bank gradient's zeros beside dQ (started with the backward, beside o_proj's
-  // dX and dW, it slowed o_proj's dW 55 -> 116 us and the step by 25 us)
+  // fill: the dense bank gradient's zeros beside dQ, after o_proj's dW on the aux stream (which is
+  // ordered after the caller's work, so the main stream records no event for it); started with
+  // the backward, beside o_proj's dX and dW, the fill slowed o_proj's dW 55 -> 116 us and the step
+  // by 25 us
   if (dbank) {
-    MOC_HIP(hipEventRecord(ev[1], main));
-    MOC_HIP(hipStreamWaitEvent(fill, ev[1], 0));
+    MOC_HIP(hipStreamWaitEvent(fill, ev[6], 0));
     join.fork(fill);
     SEQ_STAGE(kStFill, fill, SEQ_TRY(moc_fill_zero(dbank, bank_rows * d * 2, fill_cus(), fill)));
     MOC_HIP(hipEventRecord(ev[2], fill));
   }
   SEQ_STAGE(kStDq, main,
-            SEQ_TRY(moc_xattn_bwd_dq(MOC_BF16, q, kv, kv + y.KV, span, (int64_t)64 * KV2, 64, KV2, edge_u, omega,
-                                     d_attn, lse, delta, B, L, H, HK, 64, 64, y.NS, 0.125f, dq, main)));
+            SEQ_TRY(moc_xattn_bwd_dq_delta(MOC_BF16, q, kv, kv + y.KV, span, (int64_t)64 * KV2, 64, KV2, edge_u,
+                                           omega, attn, d_attn, lse, delta, B, L, H, HK, 64, 64, y.NS, 0.125f, dq,
+                                           main)));
   // aux: q_proj dX into dh beside dK/dV; fill (done with the zeros by then): q_proj dW beside
   // dK/dV, so that the aux stream reaches the router backward when dK/dV ends (both on aux, they
   // ran past dK/dV's end and the router backward past the main stream's last kernel).  When

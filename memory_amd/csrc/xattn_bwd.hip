@@ -87,14 +87,17 @@ __device__ __forceinline__ void bq_dma16(__amdgpu_buffer_rsrc_t r, uint32_t voff
   asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(r), "s"(soff), "{m0}"(m0) : "memory");
 }
 
-// dq: one workgroup = 128 queries of one (sequence, head), loop over its slots.
+// dq: one workgroup = 128 queries of one (sequence, head), loop over its slots.  With `out` (the
+// forward's output) the pre-pass is fused: the workgroup forms delta = rowsum(dout * out) of its
+// queries from the dO fragments it loads anyway and writes it (padded rows 0) for the dK/dV
+// kernel; without it delta is read.
 template <typename T>
 __global__ __launch_bounds__(kBThreads) void xattn_bwd_dq_kernel(
     const T* __restrict__ q, const T* __restrict__ ktiles, const T* __restrict__ vtiles,
     const int32_t* __restrict__ slot_u, const float* __restrict__ omega,
-    const T* __restrict__ dout, const float* __restrict__ lse, const float* __restrict__ delta, int B, int L, int H,
-    int HK, int NS, int64_t kv_span, int64_t kv_su, int kv_sh, int kv_st, float scale_log2, float scale,
-    T* __restrict__ dq) {
+    const T* __restrict__ dout, const T* __restrict__ out, const float* __restrict__ lse, float* __restrict__ delta,
+    int B, int L, int H, int HK, int NS, int64_t kv_span, int64_t kv_su, int kv_sh, int kv_st, float scale_log2,
+    float scale, T* __restrict__ dq) {
   typedef typename Frag<T>::type F8;
   using Tile = SwzTile<T, 64>;
   constexpr int TB = kBT * kBDh * (int)sizeof(T);
@@ -127,7 +130,25 @@ __global__ __launch_bounds__(kBThreads) void xattn_bwd_dq_kernel(
       dof[qb][ks] = ok ? Load8<T, T>::run(dout + row + 32 * ks + 8 * g) : zero_frag<T>();
     }
     lse2[qb] = ok ? lse[((size_t)b * H + h) * Lp + qi] : INFINITY;
-    dl[qb] = ok ? delta[((size_t)b * H + h) * Lp + qi] : 0.f;
+    if (out) {
+      // lane (g, c16) holds dims 32 ks + 8 g .. + 7 of query c16: 16 products, then the 4 lanes
+      // of the query
+      float sacc = 0.f;
+      if (ok) {
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+          const F8 of = Load8<T, T>::run(out + row + 32 * ks + 8 * g);
+#pragma unroll
+          for (int x = 0; x < 8; ++x) sacc += to_f(dof[qb][ks][x]) * to_f(of[x]);
+        }
+      }
+      sacc += __shfl_xor(sacc, 16);
+      sacc += __shfl_xor(sacc, 32);
+      dl[qb] = sacc;
+      if (g == 0) delta[((size_t)b * H + h) * Lp + qi] = sacc;
+    } else {
+      dl[qb] = ok ? delta[((size_t)b * H + h) * Lp + qi] : 0.f;
+    }
   }
   f32x4 acc[2][4];
 #pragma unroll
@@ -792,30 +813,56 @@ int moc_xattn_bwd_prep(int dtype, const void* q, const void* out, const void* do
   return check_launch("xattn_bwd_prep_kernel");
 }
 
-int moc_xattn_bwd_dq(int dtype, const void* q, const void* k_tiles, const void* v_tiles, int64_t kv_span,
-                     int64_t su, int sh, int st, const int32_t* slot_u, const float* omega, const void* dout, const float* lse,
-                     const float* delta, int64_t B, int64_t L, int H, int HK, int Dh, int T, int NS, float scale,
-                     void* dq, hipStream_t stream) {
+}  // extern "C"
+
+namespace moc {
+namespace {
+int bwd_dq(const char* who, int dtype, const void* q, const void* k_tiles, const void* v_tiles, int64_t kv_span,
+           int64_t su, int sh, int st, const int32_t* slot_u, const float* omega, const void* out, const void* dout,
+           const float* lse, float* delta, int64_t B, int64_t L, int H, int HK, int Dh, int T, int NS, float scale,
+           void* dq, hipStream_t stream) {
   MOC_REQUIRE(q && k_tiles && v_tiles && slot_u && omega && dout && lse && delta && dq, MOC_ERR_ARG,
-              "moc_xattn_bwd_dq: null pointer");
-  MOC_REQUIRE(Dh == kBDh && T == kBT, MOC_ERR_UNSUPPORTED, "moc_xattn_bwd_dq: needs head_dim 64 and T 64");
-  MOC_REQUIRE(H > 0 && HK > 0 && H % HK == 0 && NS > 0, MOC_ERR_ARG, "moc_xattn_bwd_dq: bad shape");
-  if (int rc = check_kv_layout("moc_xattn_bwd_dq", dtype, kv_span, su, sh, st)) return rc;
+              "%s: null pointer", who);
+  MOC_REQUIRE(Dh == kBDh && T == kBT, MOC_ERR_UNSUPPORTED, "%s: needs head_dim 64 and T 64", who);
+  MOC_REQUIRE(H > 0 && HK > 0 && H % HK == 0 && NS > 0, MOC_ERR_ARG, "%s: bad shape", who);
+  if (int rc = check_kv_layout(who, dtype, kv_span, su, sh, st)) return rc;
   if (B == 0 || L == 0) return MOC_OK;
-  MOC_REQUIRE(B * H * ((L + 127) / 128) < ((int64_t)1 << 31), MOC_ERR_UNSUPPORTED, "moc_xattn_bwd_dq: grid too large");
+  MOC_REQUIRE(B * H * ((L + 127) / 128) < ((int64_t)1 << 31), MOC_ERR_UNSUPPORTED, "%s: grid too large", who);
   dim3 grid(xcd_grid(B * H * ((L + 127) / 128)));
   const float sl2 = scale * 1.4426950408889634f;
   if (dtype == MOC_BF16)
     hipLaunchKernelGGL(xattn_bwd_dq_kernel<bf16>, grid, dim3(kBThreads), 0, stream, (const bf16*)q, (const bf16*)k_tiles,
-                       (const bf16*)v_tiles, slot_u, omega, (const bf16*)dout, lse, delta, (int)B, (int)L, H, HK, NS,
-                       kv_span, su, sh, st, sl2, scale, (bf16*)dq);
+                       (const bf16*)v_tiles, slot_u, omega, (const bf16*)dout, (const bf16*)out, lse, delta, (int)B,
+                       (int)L, H, HK, NS, kv_span, su, sh, st, sl2, scale, (bf16*)dq);
   else if (dtype == MOC_F32)
     hipLaunchKernelGGL(xattn_bwd_dq_kernel<float>, grid, dim3(kBThreads), 0, stream, (const float*)q,
-                       (const float*)k_tiles, (const float*)v_tiles, slot_u, omega, (const float*)dout, lse, delta,
-                       (int)B, (int)L, H, HK, NS, kv_span, su, sh, st, sl2, scale, (float*)dq);
+                       (const float*)k_tiles, (const float*)v_tiles, slot_u, omega, (const float*)dout,
+                       (const float*)out, lse, delta, (int)B, (int)L, H, HK, NS, kv_span, su, sh, st, sl2, scale,
+                       (float*)dq);
   else
-    return set_error(MOC_ERR_UNSUPPORTED, "moc_xattn_bwd_dq: dtype %d", dtype);
+    return set_error(MOC_ERR_UNSUPPORTED, "%s: dtype %d", who, dtype);
   return check_launch("xattn_bwd_dq_kernel");
+}
+}  // namespace
+}  // namespace moc
+
+extern "C" {
+
+int moc_xattn_bwd_dq(int dtype, const void* q, const void* k_tiles, const void* v_tiles, int64_t kv_span,
+                     int64_t su, int sh, int st, const int32_t* slot_u, const float* omega, const void* dout, const float* lse,
+                     const float* delta, int64_t B, int64_t L, int H, int HK, int Dh, int T, int NS, float scale,
+                     void* dq, hipStream_t stream) {
+  return bwd_dq("moc_xattn_bwd_dq", dtype, q, k_tiles, v_tiles, kv_span, su, sh, st, slot_u, omega, nullptr, dout, lse,
+                const_cast<float*>(delta), B, L, H, HK, Dh, T, NS, scale, dq, stream);
+}
+
+int moc_xattn_bwd_dq_delta(int dtype, const void* q, const void* k_tiles, const void* v_tiles, int64_t kv_span,
+                           int64_t su, int sh, int st, const int32_t* slot_u, const float* omega, const void* out,
+                           const void* dout, const float* lse, float* delta, int64_t B, int64_t L, int H, int HK, int Dh,
+                           int T, int NS, float scale, void* dq, hipStream_t stream) {
+  MOC_REQUIRE(out, MOC_ERR_ARG, "moc_xattn_bwd_dq_delta: null pointer");
+  return bwd_dq("moc_xattn_bwd_dq_delta", dtype, q, k_tiles, v_tiles, kv_span, su, sh, st, slot_u, omega, out, dout,
+                lse, delta, B, L, H, HK, Dh, T, NS, scale, dq, stream);
 }
 
 int moc_xattn_bwd_dkv(int dtype, const void* q, const void* dout,

@@ -695,8 +695,7 @@ def routed_attn_backward(saved, cfg, dout, needs, row_grad=None, after_dq=None, 
     _need_q, need_bank, need_wk, need_wv, _need_om = needs
     dout = dout.to(dtype).contiguous()
     Lp = lse.shape[2]
-    delta = torch.empty(B, H, Lp, device=dev, dtype=torch.float32)
-    call("moc_xattn_bwd_prep", dt, ptr(q), ptr(out), ptr(dout), B, Lq, H, Dh, ptr(delta), None, None, st)
+    delta = torch.empty(B, H, Lp, device=dev, dtype=torch.float32)   # written by the dQ kernel
     # the dense bank gradient's zeros are written beside the dQ and dK/dV kernels
     dbank_zero = None
     if dtype == torch.bfloat16 and need_bank and row_grad is None:
@@ -704,7 +703,7 @@ def routed_attn_backward(saved, cfg, dout, needs, row_grad=None, after_dq=None, 
     dq = torch.empty_like(q)
     kvl = kv_rows_layout(kv, T, HK, Dh)
     vptr = ptr(kv) + KV * kv.element_size()
-    call("moc_xattn_bwd_dq", dt, ptr(q), ptr(kv), vptr, *kvl, ptr(edge_u), ptr(om),
+    call("moc_xattn_bwd_dq_delta", dt, ptr(q), ptr(kv), vptr, *kvl, ptr(edge_u), ptr(om), ptr(out),
          ptr(dout), ptr(lse), ptr(delta), B, Lq, H, HK, Dh, T, NS, scale, ptr(dq), st)
     if after_dq is not None:
         after_dq(dq)

@@ -262,3 +262,53 @@ def test_rows_linear_matches_fp64(gpu_device, shape):
     L.call("moc_rows_linear", L.ptr(xd), K, R, L.ptr(wd), N, K, L.ptr(y), N, L.stream_ptr(gpu_device))
     assert_parity(y[:R], x.double() @ w.double().T, torch.bfloat16, "y")
     assert torch.isnan(y[R:].float()).all()
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("B,Lq,H,HK", [(2, 100, 4, 2), (3, 256, 4, 4), (1, 130, 2, 1)])
+def test_dq_with_fused_delta_matches_prep(gpu_device, dtype, B, Lq, H, HK):
+    """moc_xattn_bwd_dq_delta (the pre-pass's delta formed inside the dQ kernel) against
+    moc_xattn_bwd_prep + moc_xattn_bwd_dq: delta within fp32 rounding of the pre-pass's (the
+    summation order differs), padded rows exactly 0, dq within a few units of its last place."""
+    print(f"dq_delta dtype={dtype} B={B} L={Lq} H={H} HK={HK}", flush=True)
+    from memory_amd import ops, _lib as L
+    dev = gpu_device
+    g = gen(7 + B + Lq)
+    T, S, Dh, C, k, d = 64, 1, 64, 24, 5, 128
+    q = torch.randn(B, Lq, H, Dh, generator=g).to(dev, dtype)
+    bank = torch.randn(C * T, d, generator=g).to(dev, dtype)
+    Wk = (torch.randn(HK * Dh, d, generator=g) / d ** 0.5).to(dev, dtype)
+    Wv = (torch.randn(HK * Dh, d, generator=g) / d ** 0.5).to(dev, dtype)
+    idx, w, _ = O.route_sequence(torch.randn(B, C, generator=g) * 2, k, S)
+    ci, cw = O.prepend_shared_chapters(idx, w, num_chapters=C, num_shared_chapters=S, routed_scaling_factor=2.5)
+    out, saved, cfg = ops.routed_attn_forward(q, bank, Wk, Wv, cw.float().to(dev), ci.to(torch.int32).to(dev), C, T,
+                                              0, 0.0, HK)
+    (qs, _, _, om, outs, lse, kv, _, _, _, _, edge_u, _, _) = saved
+    dout = torch.randn(B, Lq, H, Dh, generator=g).to(dev, dtype)
+    Lp = lse.shape[2]
+    NS = om.shape[1]
+    dt = L.dtype_code(dtype)
+    st = L.stream_ptr(dev)
+    kvl = ops.kv_rows_layout(kv, T, HK, Dh)
+    vptr = L.ptr(kv) + HK * Dh * kv.element_size()
+    delta_ref = torch.full((B, H, Lp), float("nan"), device=dev)
+    L.call("moc_xattn_bwd_prep", dt, L.ptr(qs), L.ptr(outs), L.ptr(dout), B, Lq, H, Dh, L.ptr(delta_ref), None, None, st)
+    dq_ref = torch.empty_like(qs)
+    L.call("moc_xattn_bwd_dq", dt, L.ptr(qs), L.ptr(kv), vptr, *kvl, L.ptr(edge_u), L.ptr(om), L.ptr(dout),
+           L.ptr(lse), L.ptr(delta_ref), B, Lq, H, HK, Dh, T, NS, Dh ** -0.5, L.ptr(dq_ref), st)
+    delta = torch.full((B, H, Lp), float("nan"), device=dev)
+    dq = torch.empty_like(qs)
+    L.call("moc_xattn_bwd_dq_delta", dt, L.ptr(qs), L.ptr(kv), vptr, *kvl, L.ptr(edge_u), L.ptr(om), L.ptr(outs),
+           L.ptr(dout), L.ptr(lse), L.ptr(delta), B, Lq, H, HK, Dh, T, NS, Dh ** -0.5, L.ptr(dq), st)
+    torch.cuda.synchronize()
+    # delta from the rows in double: the fused value and the pre-pass's within fp32 rounding of it
+    exact = (dout.double() * outs.double()).sum(-1).permute(0, 2, 1)
+    scale = exact.abs().amax().item() + 1e-30
+    assert (delta[:, :, :Lq].double() - exact).abs().max().item() <= 1e-5 * scale
+    assert (delta_ref[:, :, :Lq].double() - exact).abs().max().item() <= 1e-5 * scale
+    assert torch.all(delta[:, :, Lq:] == 0)
+    tol = 1e-4 if dtype == torch.float32 else 2e-2
+    err = (dq.float() - dq_ref.float()).abs().max().item() / (dq_ref.float().abs().max().item() + 1e-30)
+    print(f"  delta max |fused - exact| / max|exact| "
+          f"{(delta[:, :, :Lq].double() - exact).abs().max().item() / scale:.2e}, dq rel diff {err:.2e}", flush=True)
+    assert err <= tol
